@@ -1,0 +1,172 @@
+/*
+ * qkv.h -- C ABI of libqkv, the MI355X (gfx950) kernels of the Qwen3
+ * sparse-attention KV-retrieval path.
+ *
+ * Every entry point takes plain device pointers, sizes and strides, launches
+ * asynchronously on the caller's HIP stream (`stream` is a hipStream_t, NULL
+ * for the default stream), never allocates and never synchronises.  Outputs
+ * and workspaces are owned by the caller.  Each returns QKV_OK or a negative
+ * status; qkv_last_error() then holds this thread's message.
+ *
+ * Reference citations are to littlexi001/kv_cache:
+ *   QK = ymluo/projects/qwen3_top2_head_limit3_ppl/src/qabs_cuda_kernels.py
+ *   EV = ymluo/projects/qwen3_top2_head_limit3_ppl/src/evaluate_qwen3_top2_head_limit3_ppl.py
+ *
+ * Strides are in elements of the tensor's own type.  The innermost (channel)
+ * axis is always contiguous unless a stride argument for it is given.
+ */
+#ifndef QKV_H_
+#define QKV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QKV_OK 0
+#define QKV_ERR_INVALID (-1)     /* bad shape, pointer, alignment or value  */
+#define QKV_ERR_LAUNCH (-2)      /* HIP reported an error at launch         */
+#define QKV_ERR_UNSUPPORTED (-3) /* valid request outside what is built     */
+
+#define QKV_DTYPE_BF16 0
+#define QKV_DTYPE_FP16 1
+#define QKV_DTYPE_FP32 2
+
+#define QKV_ABI_VERSION 1
+
+/* ABI version of the loaded library (QKV_ABI_VERSION it was built with). */
+int qkv_abi_version(void);
+
+/* Message of this thread's most recent failed call ("" if none).  Replaces
+ * the TORCH_CHECK messages the reference raises (QK:425-430, 576-593). */
+const char* qkv_last_error(void);
+
+/* ======================================================================
+ * Reference-signature family: the four kernels behind the reference's
+ * Python module, fp32 results, inputs in bf16 / fp16 / fp32 (dtype).
+ * ====================================================================== */
+
+/* Replaces qabs_partial_scores_forward (QK:421-459, kernel QK:98-158,
+ * Python partial_scores QK:654-656).
+ * query [B,H,D] contiguous; key [B,H,T,D] with k_strides = {b,h,t,d};
+ * out f32 [B,H,T] contiguous.  Per (b,h): the min(max(dim_count,1),D,128)
+ * dims of largest |q| (ties to the lower dim), then out = sum_s q*k in
+ * selection order, fp32. */
+int qkv_partial_scores(const void* query, const void* key, float* out, int dtype,
+                       int64_t batch, int64_t heads, int64_t keys, int64_t head_dim,
+                       const int64_t* k_strides, int64_t dim_count, void* stream);
+
+/* Replaces qabs_partial_scores_dim_major_forward (QK:461-504, kernel
+ * QK:63-96, Python partial_scores_dim_major QK:659-665).
+ * query [B,H,D] contiguous; key_dim_major [B,H,D,T] with kdm_strides =
+ * {b,h,d,t}; dim_indices int64 [B,H,S] contiguous; out f32 [B,H,T]. */
+int qkv_partial_scores_dim_major(const void* query, const void* key_dim_major,
+                                 const int64_t* dim_indices, float* out, int dtype,
+                                 int64_t batch, int64_t heads, int64_t keys, int64_t head_dim,
+                                 int64_t selected, const int64_t* kdm_strides, void* stream);
+
+/* Replaces qabs_candidate_full_scores_forward (QK:506-567, kernel
+ * QK:160-216, Python candidate_full_scores QK:668-691).
+ * Masks are uint8 [B,H,T] contiguous; previous / previous_final may be NULL.
+ * out f32 [B,H,T]: full-D dot * scaling where selected, else -inf. */
+int qkv_candidate_full_scores(const void* query, const void* key, const uint8_t* current,
+                              const uint8_t* previous, const uint8_t* previous_final,
+                              float* out, int dtype, int64_t batch, int64_t heads,
+                              int64_t keys, int64_t head_dim, const int64_t* k_strides,
+                              int64_t protect_sink, int64_t protect_recent, float scaling,
+                              void* stream);
+
+/* Replaces qabs_final_attention_forward (QK:569-638, kernel QK:335-419,
+ * Python final_attention QK:694-705).
+ * query [B,H,D], key/value [B,H,T,D], indices int64 [B,H,N], valid uint8
+ * [B,H,N], out [B,H,D] in dtype; all contiguous.  N <= 16384. */
+int qkv_final_attention(const void* query, const void* key, const void* value,
+                        const int64_t* indices, const uint8_t* valid, void* out, int dtype,
+                        int64_t batch, int64_t heads, int64_t keys, int64_t selected,
+                        int64_t head_dim, float scaling, void* stream);
+
+/* ======================================================================
+ * int4 family (no reference counterpart: the reference scores fp32 over
+ * GQA-expanded bf16 K).  K/V/q are bf16.  A "row" r = b * Hkv + j is one
+ * (sequence, KV head).  Packed K, scales and the subset slab are laid out
+ * [rows, capacity, ...] with capacity a multiple of 64 tokens.
+ * ====================================================================== */
+
+/* Quantize tokens [t_begin, t_end) of K [B,Hkv,*,D] (k_strides = {b,h,t},
+ * channels contiguous, rows 16-byte aligned) to symmetric int4 in groups of
+ * `group` channels (32, 64 or 128): packed uint8 [rows,capacity,D/2],
+ * scales fp16 bits [rows,capacity,D/group].  Nearest reference layout: the
+ * dim-major K copy kept per layer (EV:2018-2042). */
+int qkv_int4_pack_k(const void* key, const int64_t* k_strides, int64_t batch, int64_t kv_heads,
+                    int64_t t_begin, int64_t t_end, int64_t head_dim, int64_t group,
+                    uint8_t* packed, uint16_t* scales, int64_t capacity, void* stream);
+
+/* Static channel subset per row: stats[r,c] = sum_t |code| * scale * 2^24
+ * (exact uint64, T <= 2^20), then the `selected` channels of largest stat,
+ * ties to the lower channel, written ascending to chan_idx int32
+ * [rows,selected].  stats uint64 [rows,D] is an output the call overwrites.
+ * Replaces the per-step top-|q| dims of EV:4428 / QK:123-145 with a
+ * per-KV-head choice made once per prefill. */
+int qkv_int4_select_channels(const uint8_t* packed, const uint16_t* scales, int64_t rows,
+                             int64_t tokens, int64_t capacity, int64_t head_dim, int64_t group,
+                             int64_t selected, uint64_t* stats, int32_t* chan_idx, void* stream);
+
+/* Subset slab of tokens [t_begin, t_end): the `selected` channels chan_idx
+ * of each K row re-quantized as one int4 group: slab uint8
+ * [rows,capacity,selected/2], slab_scales fp16 bits [rows,capacity].
+ * selected in {16,32,64,128}.  int4 analogue of EV:2018-2042. */
+int qkv_int4_build_slab(const void* key, const int64_t* k_strides, int64_t batch,
+                        int64_t kv_heads, int64_t t_begin, int64_t t_end, int64_t head_dim,
+                        const int32_t* chan_idx, int64_t selected, uint8_t* slab,
+                        uint16_t* slab_scales, int64_t capacity, void* stream);
+
+/* Decode scoring over tokens [0, tokens) of every row, fused with block
+ * max-pooling.  Replaces qabs_partial_scores_dim_major_forward (QK:63-96)
+ * plus the block pool of EV:5038-5044.
+ * query bf16 [B,Hq,D] contiguous, Hq = G * Hkv.  Per row the G query heads
+ * are summed over the row's channels (fp32, head order), quantized to int8
+ * (scale amax/127), and I[t] = sum_s q8[s]*code[t,s] (int32); the ranking
+ * key is fp32(slab_scale[t]) * fp32(I[t]).
+ * bmax f32 [rows, ceil(tokens/block)] (block a power of two, 1..64*128/S).
+ * isum int32 [rows,tokens] and keys f32 [rows,tokens] are optional (NULL to
+ * skip); bmax may be NULL when either is given.  qscale f32 [rows] optional. */
+int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                           int64_t head_dim, const int32_t* chan_idx, int64_t selected,
+                           const uint8_t* slab, const uint16_t* slab_scales, int64_t capacity,
+                           int64_t tokens, int64_t block, float* bmax, int32_t* isum,
+                           float* keys, float* qscale, void* stream);
+
+/* Top-k per row with the lowest-index tie-break: out int32 [rows,k] holds the
+ * k indices first in (value descending, index ascending) order, written in
+ * ascending index order.  values f32 [rows, n] with row stride ld; 1 <= k <= n.
+ * -0 equals +0; NaN is outside the contract.  Replaces torch.topk at EV:4448
+ * and EV:5046. */
+int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
+             int32_t* out, void* stream);
+
+/* Bytes of f32 workspace qkv_sparse_attention needs for these sizes. */
+int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                             int64_t head_dim, int64_t n_sel, int64_t block);
+
+/* GQA-native sparse gather attention.  Replaces the reference's
+ * gather/matmul/softmax fallback (EV:4490-4502) and final-attention kernel
+ * (QK:335-419) without expanding K/V to the query heads (EV:6248-6251).
+ * query bf16 [B,Hq,D] contiguous; key/value bf16 [B,Hkv,*,D] with
+ * kv_strides = {b,h,t} (rows 16-byte aligned); block_ids int32 [rows,n_sel]
+ * (ids outside [0, ceil(tokens/block)) are skipped); each block covers
+ * tokens [id*block, min(tokens,(id+1)*block)).  Every query head of a row
+ * attends, with softmax(scaling * q.k), over the union of the row's blocks.
+ * out bf16 [B,Hq,D]; a head with no valid token gets zeros (QK:388, 404).
+ * D must be 128. */
+int qkv_sparse_attention(const void* query, const void* key, const void* value,
+                         const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                         int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                         const int32_t* block_ids, int64_t n_sel, int64_t block, float scaling,
+                         float* workspace, int64_t workspace_bytes, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QKV_H_ */

@@ -1,0 +1,103 @@
+"""ctypes binding of libqkv.so, the gfx950 C-ABI library.
+
+``load()`` is the singleton that replaces the reference's lazily JIT-built
+extension (``_load_extension``, qabs_cuda_kernels.py:642-651).  There is no
+fallback: if the library is missing or does not load, calls raise
+``RuntimeError``.  torch is imported first so that the library binds to the
+HIP runtime torch already loaded (both carry the soname libamdhip64.so.7),
+which makes torch's device pointers and streams valid in it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL so the HIP runtime is shared)
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libqkv.so"
+HEADER = PKG.parent / "include" / "qkv.h"
+ABI_VERSION = 1
+
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+_c = ctypes
+_vp, _i64, _i32, _f32 = _c.c_void_p, _c.c_int64, _c.c_int, _c.c_float
+_P = _c.POINTER
+
+# name -> (restype, argtypes); mirrors include/qkv.h.
+_PROTOTYPES = {
+    "qkv_abi_version": (_i32, []),
+    "qkv_last_error": (_c.c_char_p, []),
+    "qkv_partial_scores": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _P(_i64), _i64, _vp]),
+    "qkv_partial_scores_dim_major": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
+                                            _P(_i64), _vp]),
+    "qkv_candidate_full_scores": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64,
+                                         _P(_i64), _i64, _i64, _f32, _vp]),
+    "qkv_final_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
+                                   _f32, _vp]),
+    "qkv_int4_pack_k": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "qkv_int4_select_channels": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "qkv_int4_build_slab": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
+                                   _i64, _vp]),
+    "qkv_int4_decode_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64,
+                                      _i64, _vp, _vp, _vp, _vp, _vp]),
+    "qkv_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "qkv_sparse_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "qkv_sparse_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                                    _i64, _f32, _vp, _i64, _vp, _vp]),
+}
+
+_LIB = None
+
+
+def header_functions() -> list[str]:
+    """Function names declared in include/qkv.h."""
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(qkv_\w+)\s*\(", text, re.M)))
+
+
+def load() -> ctypes.CDLL:
+    """Load libqkv.so once; raises RuntimeError if it is absent or stale."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = Path(os.environ.get("QKV_LIBRARY", LIB_PATH))
+    if not path.exists():
+        raise RuntimeError(f"{path} is not built: run `python -m kv_cache_amd.build` "
+                           "(or __graft_entry__.build()) first")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in _PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.qkv_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI {lib.qkv_abi_version()}, expected {ABI_VERSION}: rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(load().qkv_last_error().decode())
+
+
+def strides(*vals: int):
+    arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+    return arr
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_cuda(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be CUDA")

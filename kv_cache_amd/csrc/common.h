@@ -1,0 +1,109 @@
+// Shared device helpers and C-ABI error plumbing for libqkv (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "../../include/qkv.h"
+
+#define QKV_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace qkv {
+
+// Records a printf-style message as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Checks hipGetLastError() after a launch; returns QKV_OK or QKV_ERR_LAUNCH.
+int check_launch(const char* what);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+__device__ __forceinline__ float f16bits_to_f32(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16));
+  return static_cast<float>(h);
+}
+
+// fp32 -> fp16 round-to-nearest-even (v_cvt_f16_f32 in the default mode), with
+// +inf saturated to 65504.  The argument is a non-negative magnitude.
+__device__ __forceinline__ uint32_t f32_to_f16bits_sat(float x) {
+  _Float16 h = static_cast<_Float16>(x);
+  uint32_t bits = __builtin_bit_cast(uint16_t, h);
+  return bits == 0x7C00u ? 0x7BFFu : bits;
+}
+
+// Symmetric int4 code of x for an fp16-representable scale s (s > 0):
+// clamp(rint_even(x / s), -8, 7).  The division is the IEEE-correct one
+// (hipcc's default for fp32 '/').
+__device__ __forceinline__ int int4_code(float x, float s) {
+  float r = __builtin_rintf(x / s);
+  r = fminf(fmaxf(r, -8.0f), 7.0f);
+  return static_cast<int>(r);
+}
+
+// Order-preserving map of an fp32 key onto uint32 (larger float -> larger
+// integer), with -0 folded onto +0.  NaN inputs are outside the contract.
+__device__ __forceinline__ uint32_t f32_sortable(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float sortable_f32(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+// ds_swizzle in bit-mask mode: lane i reads lane (i ^ m) within groups of 32.
+template <int M>
+__device__ __forceinline__ float swz_xor(float v) {
+  static_assert(M > 0 && M < 32, "xor mask must stay inside 32 lanes");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (M << 10)));
+}
+template <int M>
+__device__ __forceinline__ int swz_xor_i(int v) {
+  static_assert(M > 0 && M < 32, "xor mask must stay inside 32 lanes");
+  return __builtin_amdgcn_ds_swizzle(v, 0x1F | (M << 10));
+}
+
+// Lane i reads lane i ^ m for any m < 64 (ds_bpermute).
+__device__ __forceinline__ float shfl_xor(float v, int m) {
+  int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(v)));
+}
+__device__ __forceinline__ int shfl_xor_i(int v, int m) {
+  int lane = __lane_id();
+  return __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_i(v, m);
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  int lane = __lane_id();
+  for (int d = 1; d < 64; d <<= 1) {
+    int o = __builtin_amdgcn_ds_bpermute(((lane - d) & 63) << 2, v);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+}  // namespace qkv

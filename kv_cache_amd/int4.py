@@ -1,0 +1,256 @@
+"""Host API of the int4 sparse-attention KV-retrieval path on MI355X.
+
+The path (no int4 counterpart in the reference; its fp32 equivalent is the
+``qabs{S}cand{pct}attn`` / ``qboracle`` decode of evaluate_qwen3_top2_head_
+limit3_ppl.py:4400-4502 and 5008-5097):
+
+1. ``int4_pack_k``      -- K bf16 -> symmetric int4, fp16 scale per group.
+2. ``select_channels``  -- per KV head, the S channels of largest mean |K|.
+3. ``build_slab``       -- those S channels re-quantized as one int4 group:
+                           the S/2 + 2 bytes per token that decode scoring streams.
+4. ``decode_scores``    -- GQA-summed int8 query . int4 slab -> int32, ranking
+                           key fp32(scale) * I, max-pooled per block.
+5. ``block_topk``       -- top-k blocks, lowest index wins ties, ascending.
+6. ``sparse_attention`` -- every query head of a KV head attends over the
+                           selected blocks of bf16 K/V.
+
+All tensors live on the GPU; every function launches on the current stream
+and raises ``RuntimeError`` on bad input or a missing library (there is no
+CPU fallback).  Layouts: K/V [B, Hkv, T, D] bf16 with contiguous channels;
+packed/slab tensors [B, Hkv, capacity, ...] with capacity a multiple of 64.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+CAPACITY_MULTIPLE = 64
+
+
+def round_capacity(tokens: int) -> int:
+    return max(CAPACITY_MULTIPLE, -(-int(tokens) // CAPACITY_MULTIPLE) * CAPACITY_MULTIPLE)
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_kv(name: str, t: torch.Tensor) -> None:
+    _require(t.is_cuda, f"{name} must be CUDA")
+    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16")
+    _require(t.dim() == 4, f"{name} must have shape [batch, kv_heads, tokens, dim]")
+    _require(t.stride(3) == 1, f"{name} channels must be contiguous")
+
+
+def int4_pack_k(key: torch.Tensor, group: int, *, capacity: int | None = None,
+                packed: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                t_begin: int = 0, t_end: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize tokens [t_begin, t_end) of K into (packed uint8 [B,Hkv,cap,D/2],
+    scales fp16 [B,Hkv,cap,D/group]); existing outputs are written in place."""
+    lib = _lib.load()
+    _check_kv("key", key)
+    b, h, t, d = key.shape
+    t_end = t if t_end is None else int(t_end)
+    if packed is None or scales is None:
+        cap = round_capacity(t) if capacity is None else int(capacity)
+        packed = torch.empty((b, h, cap, d // 2), dtype=torch.uint8, device=key.device)
+        scales = torch.empty((b, h, cap, d // group), dtype=torch.float16, device=key.device)
+    cap = packed.size(2)
+    _require(packed.is_contiguous() and scales.is_contiguous(), "packed/scales must be contiguous")
+    _require(tuple(packed.shape) == (b, h, cap, d // 2), "packed shape mismatch")
+    _require(tuple(scales.shape) == (b, h, cap, d // group), "scales shape mismatch")
+    with torch.cuda.device(key.device):
+        _lib.check(lib.qkv_int4_pack_k(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
+                                       t_end, d, int(group), packed.data_ptr(), scales.data_ptr(), cap,
+                                       _lib.stream_of(key)))
+    return packed, scales
+
+
+def select_channels(packed: torch.Tensor, scales: torch.Tensor, tokens: int, group: int,
+                    count: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per (b, kv head): the ``count`` channels of largest exact mean
+    |dequantized K| over tokens [0, tokens), ties to the lower channel, in
+    ascending order.  Returns (chan_idx int32 [B,Hkv,count], stats int64
+    [B,Hkv,D] holding the uint64 statistic)."""
+    lib = _lib.load()
+    _require(packed.is_cuda and packed.dtype == torch.uint8 and packed.is_contiguous(), "bad packed K")
+    b, h, cap, half = packed.shape
+    d = half * 2
+    stats = torch.empty((b, h, d), dtype=torch.int64, device=packed.device)
+    chan = torch.empty((b, h, int(count)), dtype=torch.int32, device=packed.device)
+    with torch.cuda.device(packed.device):
+        _lib.check(lib.qkv_int4_select_channels(packed.data_ptr(), scales.data_ptr(), b * h, int(tokens), cap,
+                                                d, int(group), int(count), stats.data_ptr(), chan.data_ptr(),
+                                                _lib.stream_of(packed)))
+    return chan, stats
+
+
+def build_slab(key: torch.Tensor, chan_idx: torch.Tensor, *, capacity: int | None = None,
+               slab: torch.Tensor | None = None, slab_scales: torch.Tensor | None = None,
+               t_begin: int = 0, t_end: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Subset slab of tokens [t_begin, t_end): (slab uint8 [B,Hkv,cap,S/2],
+    slab_scales fp16 [B,Hkv,cap])."""
+    lib = _lib.load()
+    _check_kv("key", key)
+    b, h, t, d = key.shape
+    _require(chan_idx.dtype == torch.int32 and chan_idx.is_contiguous(), "chan_idx must be contiguous int32")
+    s = chan_idx.size(-1)
+    t_end = t if t_end is None else int(t_end)
+    if slab is None or slab_scales is None:
+        cap = round_capacity(t) if capacity is None else int(capacity)
+        slab = torch.empty((b, h, cap, s // 2), dtype=torch.uint8, device=key.device)
+        slab_scales = torch.empty((b, h, cap), dtype=torch.float16, device=key.device)
+    cap = slab.size(2)
+    with torch.cuda.device(key.device):
+        _lib.check(lib.qkv_int4_build_slab(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
+                                           t_end, d, chan_idx.data_ptr(), s, slab.data_ptr(),
+                                           slab_scales.data_ptr(), cap, _lib.stream_of(key)))
+    return slab, slab_scales
+
+
+def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tensor,
+                  slab_scales: torch.Tensor, tokens: int, block: int, *,
+                  bmax: torch.Tensor | None = None, debug: bool = False):
+    """Fused int4 scoring + block max over tokens [0, tokens).
+
+    query bf16 [B, Hq, D].  Returns bmax f32 [B, Hkv, ceil(tokens/block)];
+    with ``debug=True`` returns (bmax, isum int32 [B,Hkv,T], keys f32
+    [B,Hkv,T], qscale f32 [B,Hkv])."""
+    lib = _lib.load()
+    _require(query.is_cuda and query.dtype == torch.bfloat16 and query.dim() == 3, "query must be CUDA bf16 [B,Hq,D]")
+    q = query.contiguous()
+    b, hq, d = q.shape
+    _, hkv, cap, half = slab.shape
+    s = half * 2
+    _require(tuple(chan_idx.shape) == (b, hkv, s), "chan_idx shape mismatch")
+    nb = -(-int(tokens) // int(block))
+    if bmax is None:
+        bmax = torch.empty((b, hkv, nb), dtype=torch.float32, device=q.device)
+    isum = keys = qscale = None
+    if debug:
+        isum = torch.empty((b, hkv, int(tokens)), dtype=torch.int32, device=q.device)
+        keys = torch.empty((b, hkv, int(tokens)), dtype=torch.float32, device=q.device)
+        qscale = torch.empty((b, hkv), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_int4_decode_scores(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s, slab.data_ptr(),
+                                              slab_scales.data_ptr(), cap, int(tokens), int(block),
+                                              bmax.data_ptr(), _lib.ptr(isum), _lib.ptr(keys),
+                                              _lib.ptr(qscale), _lib.stream_of(q)))
+    if debug:
+        return bmax, isum, keys, qscale
+    return bmax
+
+
+def block_topk(values: torch.Tensor, k: int, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-k indices along the last axis, lowest index wins ties, ascending order (int32)."""
+    lib = _lib.load()
+    _require(values.is_cuda and values.dtype == torch.float32, "values must be CUDA float32")
+    n = values.size(-1)
+    v2 = values.reshape(-1, n)
+    _require(v2.stride(1) == 1, "values must be contiguous along the last axis")
+    rows = v2.size(0)
+    if out is None:
+        out = torch.empty((*values.shape[:-1], int(k)), dtype=torch.int32, device=values.device)
+    with torch.cuda.device(values.device):
+        _lib.check(lib.qkv_topk(v2.data_ptr(), rows, n, v2.stride(0), int(k), out.data_ptr(),
+                                _lib.stream_of(values)))
+    return out
+
+
+def attention_workspace_bytes(batch: int, q_heads: int, kv_heads: int, head_dim: int, n_sel: int,
+                              block: int) -> int:
+    n = _lib.load().qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block)
+    _require(n >= 0, "unsupported sparse-attention configuration")
+    return int(n)
+
+
+def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                     block_ids: torch.Tensor, block: int, tokens: int, scaling: float, *,
+                     workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """GQA-native attention of query bf16 [B,Hq,D] over the selected blocks
+    (int32 [B,Hkv,n]) of K/V bf16 [B,Hkv,*,D]; returns bf16 [B,Hq,D]."""
+    lib = _lib.load()
+    _check_kv("key", key)
+    _check_kv("value", value)
+    _require(key.stride() == value.stride() and key.shape == value.shape, "key/value layout mismatch")
+    q = query.contiguous()
+    b, hq, d = q.shape
+    hkv = key.size(1)
+    _require(block_ids.dtype == torch.int32 and block_ids.is_contiguous(), "block_ids must be contiguous int32")
+    n = block_ids.size(-1)
+    need = attention_workspace_bytes(b, hq, hkv, d, n, block)
+    if workspace is None:
+        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_sparse_attention(q.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                            _lib.strides(*key.stride()[:3]), b, hq, hkv, int(tokens), d,
+                                            block_ids.data_ptr(), n, int(block), float(scaling),
+                                            workspace.data_ptr(), workspace.numel() * 4, out.data_ptr(),
+                                            _lib.stream_of(q)))
+    return out
+
+
+class Int4KCache:
+    """int4 view of one layer's K cache: packed K, the static channel subset
+    of every KV head, and the subset slab decode scoring streams.
+
+    Built once from the prefill K (``from_prefill``); the reference keeps the
+    analogous per-layer state in ``SparQMeanState.key_dim_major``
+    (evaluate_qwen3_top2_head_limit3_ppl.py:2018-2042)."""
+
+    def __init__(self, packed, scales, chan_idx, slab, slab_scales, tokens, group):
+        self.packed, self.scales = packed, scales
+        self.chan_idx = chan_idx
+        self.slab, self.slab_scales = slab, slab_scales
+        self.tokens = int(tokens)
+        self.group = int(group)
+
+    @property
+    def capacity(self) -> int:
+        return self.slab.size(2)
+
+    @property
+    def selected(self) -> int:
+        return self.chan_idx.size(-1)
+
+    @classmethod
+    def from_prefill(cls, key: torch.Tensor, group: int, selected: int,
+                     capacity: int | None = None) -> "Int4KCache":
+        t = key.size(2)
+        cap = round_capacity(t) if capacity is None else int(capacity)
+        packed, scales = int4_pack_k(key, group, capacity=cap)
+        chan, _ = select_channels(packed, scales, t, group, selected)
+        slab, slab_scales = build_slab(key, chan, capacity=cap)
+        return cls(packed, scales, chan, slab, slab_scales, t, group)
+
+
+class SparseDecodeStep:
+    """One layer's decode step with every buffer allocated up front:
+    scoring + block max -> top-k blocks -> GQA sparse attention."""
+
+    def __init__(self, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
+                 block: int, topk: int, device: torch.device | str = "cuda"):
+        self.batch, self.q_heads, self.kv_heads = batch, q_heads, kv_heads
+        self.head_dim, self.tokens, self.block, self.topk = head_dim, tokens, block, topk
+        nb = math.ceil(tokens / block)
+        _require(1 <= topk <= nb, f"topk {topk} must be in [1, {nb}]")
+        self.bmax = torch.empty((batch, kv_heads, nb), dtype=torch.float32, device=device)
+        self.sel = torch.empty((batch, kv_heads, topk), dtype=torch.int32, device=device)
+        need = attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, topk, block)
+        self.workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+
+    def __call__(self, query: torch.Tensor, cache: Int4KCache, key: torch.Tensor, value: torch.Tensor,
+                 scaling: float) -> torch.Tensor:
+        decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.tokens, self.block,
+                      bmax=self.bmax)
+        block_topk(self.bmax, self.topk, out=self.sel)
+        return sparse_attention(query, key, value, self.sel, self.block, self.tokens, scaling,
+                                workspace=self.workspace, out=self.out)

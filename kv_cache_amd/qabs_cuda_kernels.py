@@ -1,0 +1,166 @@
+"""Drop-in for the reference's ``qabs_cuda_kernels`` module on MI355X.
+
+Same four functions, argument meaning, output shapes and error behaviour as
+ymluo/projects/qwen3_top2_head_limit3_ppl/src/qabs_cuda_kernels.py:654-705,
+backed by libqkv's gfx950 kernels instead of a JIT-built CUDA extension.
+Shape/dtype violations raise ``RuntimeError`` with the reference's
+``TORCH_CHECK`` messages; inputs are made contiguous exactly where the
+reference does so; outputs are allocated here (fp32 scores, query-dtype
+attention) and the kernels run on the current stream.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _load_extension():
+    """The reference's loader name (QK:642-651); returns the C-ABI library."""
+    return _lib.load()
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    code = _lib.DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise RuntimeError(f"unsupported dtype {t.dtype}")
+    return code
+
+
+def partial_scores(query: torch.Tensor, key_history: torch.Tensor, dim_count: int) -> torch.Tensor:
+    """QK:654-656 (host QK:421-459): fp32 [B,H,T] partial QK over the
+    ``dim_count`` largest-|q| dims of each query row, token-major K."""
+    lib = _lib.load()
+    _check(query.is_cuda, "query must be CUDA")
+    _check(key_history.is_cuda, "key must be CUDA")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key_history.dim() == 4, "key must have shape [batch, heads, key, dim]")
+    _check(query.dtype == key_history.dtype, "query/key dtype mismatch")
+    _check(query.size(0) == key_history.size(0) and query.size(1) == key_history.size(1)
+           and query.size(2) == key_history.size(3), "query/key shape mismatch")
+    q = query.contiguous()
+    b, h, d = q.shape
+    t = key_history.size(2)
+    out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_partial_scores(
+            q.data_ptr(), key_history.data_ptr(), out.data_ptr(), _dtype_code(q), b, h, t, d,
+            _lib.strides(*key_history.stride()), int(dim_count), _lib.stream_of(q)))
+    return out
+
+
+def partial_scores_dim_major(query: torch.Tensor, key_dim_major: torch.Tensor,
+                             dim_indices: torch.Tensor) -> torch.Tensor:
+    """QK:659-665 (host QK:461-504): fp32 [B,H,T] over dim-major K [B,H,D,T]
+    and int64 dim indices [B,H,S], accumulated in the given index order."""
+    lib = _lib.load()
+    _check(query.is_cuda, "query must be CUDA")
+    _check(key_dim_major.is_cuda, "key_dim_major must be CUDA")
+    _check(dim_indices.is_cuda, "dim_indices must be CUDA")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key_dim_major.dim() == 4, "key_dim_major must have shape [batch, heads, dim, key]")
+    _check(dim_indices.dim() == 3, "dim_indices must have shape [batch, heads, selected_dim]")
+    _check(query.dtype == key_dim_major.dtype, "query/key dtype mismatch")
+    _check(dim_indices.dtype == torch.int64, "dim_indices must be int64")
+    _check(query.size(0) == key_dim_major.size(0) and query.size(1) == key_dim_major.size(1)
+           and query.size(2) == key_dim_major.size(2), "query/key shape mismatch")
+    _check(dim_indices.size(0) == query.size(0) and dim_indices.size(1) == query.size(1),
+           "dim_indices shape mismatch")
+    q = query.contiguous()
+    idx = dim_indices.contiguous()
+    b, h, d = q.shape
+    t = key_dim_major.size(3)
+    out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_partial_scores_dim_major(
+            q.data_ptr(), key_dim_major.data_ptr(), idx.data_ptr(), out.data_ptr(), _dtype_code(q),
+            b, h, t, d, idx.size(2), _lib.strides(*key_dim_major.stride()), _lib.stream_of(q)))
+    return out
+
+
+def candidate_full_scores(query: torch.Tensor, key_history: torch.Tensor,
+                          current_candidate: torch.Tensor, previous_candidate: torch.Tensor | None,
+                          previous_final: torch.Tensor | None, protect_sink_tokens: int,
+                          protect_recent_tokens: int, scaling: float) -> torch.Tensor:
+    """QK:668-691 (host QK:506-567): full-D scores * scaling on candidate,
+    previous, sink and recent tokens, -inf elsewhere; fp32 [B,H,T]."""
+    lib = _lib.load()
+    _check(query.is_cuda, "query must be CUDA")
+    _check(key_history.is_cuda, "key must be CUDA")
+    _check(current_candidate.is_cuda, "current_candidate must be CUDA")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key_history.dim() == 4, "key must have shape [batch, heads, key, dim]")
+    _check(current_candidate.dim() == 3, "current_candidate must have shape [batch, heads, key]")
+    _check(query.dtype == key_history.dtype, "query/key dtype mismatch")
+    _check(current_candidate.dtype == torch.bool, "current_candidate must be bool")
+    _check(previous_candidate is None or previous_candidate.dtype == torch.bool,
+           "previous_candidate must be bool")
+    _check(previous_final is None or previous_final.dtype == torch.bool, "previous_final must be bool")
+    _check(query.size(0) == key_history.size(0) and query.size(1) == key_history.size(1)
+           and query.size(2) == key_history.size(3), "query/key shape mismatch")
+    _check(current_candidate.size(0) == key_history.size(0)
+           and current_candidate.size(1) == key_history.size(1)
+           and current_candidate.size(2) == key_history.size(2), "candidate shape mismatch")
+    q = query.contiguous()
+    cur = current_candidate.contiguous()
+    prev = previous_candidate.contiguous() if previous_candidate is not None else None
+    fin = previous_final.contiguous() if previous_final is not None else None
+    for name, m in (("previous_candidate", prev), ("previous_final", fin)):
+        _check(m is None or m.shape == cur.shape, f"{name} shape mismatch")
+    b, h, d = q.shape
+    t = key_history.size(2)
+    out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_candidate_full_scores(
+            q.data_ptr(), key_history.data_ptr(), cur.data_ptr(), _lib.ptr(prev), _lib.ptr(fin),
+            out.data_ptr(), _dtype_code(q), b, h, t, d, _lib.strides(*key_history.stride()),
+            int(protect_sink_tokens), int(protect_recent_tokens), float(scaling), _lib.stream_of(q)))
+    return out
+
+
+def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                    indices: torch.Tensor, valid: torch.Tensor, scaling: float) -> torch.Tensor:
+    """QK:694-705 (host QK:569-638): softmax attention over the valid
+    ``indices`` of each (b, h); returns [B, 1, H, D] in the query dtype."""
+    lib = _lib.load()
+    valid_u8 = valid.to(dtype=torch.uint8)
+    _check(query.is_cuda, "query must be CUDA")
+    _check(key.is_cuda, "key must be CUDA")
+    _check(value.is_cuda, "value must be CUDA")
+    _check(indices.is_cuda, "indices must be CUDA")
+    _check(valid_u8.is_cuda, "valid must be CUDA")
+    _check(query.device == key.device, "query/key device mismatch")
+    _check(query.device == value.device, "query/value device mismatch")
+    _check(query.device == indices.device, "query/indices device mismatch")
+    _check(query.device == valid_u8.device, "query/valid device mismatch")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key.dim() == 4, "key must have shape [batch, heads, key, dim]")
+    _check(value.shape == key.shape, "value must match key shape")
+    _check(indices.dim() == 3, "indices must have shape [batch, heads, selected]")
+    _check(valid_u8.shape == indices.shape, "valid must match indices shape")
+    _check(query.dtype == key.dtype, "query/key dtype mismatch")
+    _check(query.dtype == value.dtype, "query/value dtype mismatch")
+    _check(indices.dtype == torch.int64, "indices must be int64")
+    q = query.contiguous()
+    k = key.contiguous()
+    v = value.contiguous()
+    idx = indices.contiguous()
+    val = valid_u8.contiguous()
+    b, h, d = q.shape
+    t = k.size(2)
+    n = idx.size(2)
+    _check(k.size(0) == b and k.size(1) == h and k.size(3) == d, "key shape mismatch")
+    _check(idx.size(0) == b and idx.size(1) == h, "indices shape mismatch")
+    _check(n > 0, "select_count must be positive")
+    out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_final_attention(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(),
+            _dtype_code(q), b, h, t, n, d, float(scaling), _lib.stream_of(q)))
+    return out[:, None, :, :].contiguous()

@@ -1,0 +1,88 @@
+"""The C-ABI library loads on a CPU-only host, exports every entry point the
+header declares, and rejects bad arguments on the host side before any GPU
+call (no kernel is launched here)."""
+
+import ctypes
+
+import pytest
+
+from kv_cache_amd import _lib
+
+lib = _lib.load()
+
+
+def test_abi_version():
+    assert lib.qkv_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_header_symbol_is_exported_and_bound():
+    names = _lib.header_functions()
+    assert len(names) >= 13
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib._PROTOTYPES, f"{name} has no ctypes prototype"
+    assert set(_lib._PROTOTYPES) == set(names)
+
+
+def _err():
+    return lib.qkv_last_error().decode()
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda: lib.qkv_topk(None, 1, 10, 10, 3, None, None), "null pointer"),
+    (lambda: lib.qkv_topk(ctypes.c_void_p(16), 1, 10, 10, 11, ctypes.c_void_p(16), None), "1 <= k <= n"),
+    (lambda: lib.qkv_topk(ctypes.c_void_p(16), 1, 10, 5, 3, ctypes.c_void_p(16), None), "bad sizes"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 24,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
+                                        ctypes.c_void_p(16), None, None, None, None), "selected must be"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4000, 4000, 16,
+                                        ctypes.c_void_p(16), None, None, None, None), "multiple of 64"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 12,
+                                        ctypes.c_void_p(16), None, None, None, None), "power of two"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 15, 8, 128, ctypes.c_void_p(16), 32,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
+                                        ctypes.c_void_p(16), None, None, None, None), "multiple of kv_heads"),
+    (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 48,
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "group"),
+    (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 100, 128, 32,
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "token range"),
+    (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(18), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 32,
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "16-byte aligned"),
+    (lambda: lib.qkv_sparse_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                      _lib.strides(8, 8, 8), 1, 16, 8, 100, 64, ctypes.c_void_p(16), 4, 16,
+                                      1.0, ctypes.c_void_p(16), 1 << 20, ctypes.c_void_p(16), None), "128"),
+    (lambda: lib.qkv_sparse_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                      _lib.strides(8, 8, 8), 1, 16, 8, 100, 128, ctypes.c_void_p(16), 4, 16,
+                                      1.0, ctypes.c_void_p(16), 16, ctypes.c_void_p(16), None), "workspace"),
+    (lambda: lib.qkv_final_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                     ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
+                                     1, 1, 10, 0, 128, 1.0, None), "select_count must be positive"),
+    (lambda: lib.qkv_partial_scores(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 7,
+                                    1, 1, 10, 128, _lib.strides(1, 1, 1, 1), 8, None), "dtype"),
+])
+def test_host_side_validation(call, msg):
+    rc = call()
+    assert rc == -1 or rc == -3
+    assert msg in _err()
+
+
+def test_workspace_size_formula():
+    # rows * splits * G * (D + 2) floats; splits = ceil(n_sel / (256 // block))
+    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * 64 * 8 * 2 * 130
+    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * 8 * 1 * 2 * 130
+    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 64, 256, 1) == -1
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    import torch
+
+    from kv_cache_amd import qabs_cuda_kernels as Q
+
+    q = torch.zeros(1, 2, 8)
+    with pytest.raises(RuntimeError, match="query must be CUDA"):
+        Q.partial_scores(q, torch.zeros(1, 2, 4, 8), 2)
+    with pytest.raises(RuntimeError, match="query must be CUDA"):
+        Q.final_attention(q, torch.zeros(1, 2, 4, 8), torch.zeros(1, 2, 4, 8),
+                          torch.zeros(1, 2, 3, dtype=torch.long), torch.ones(1, 2, 3, dtype=torch.bool), 1.0)

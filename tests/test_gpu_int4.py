@@ -1,0 +1,253 @@
+"""GPU parity of the int4 path against the CPU oracle: bit-exact packing,
+channel choice, slab, int32 scores, fp32 keys, block maxima and top-k
+indices; attention within 1e-2 relative / 2e-2 absolute of fp64."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import int4 as K
+from kv_cache_amd.workloads import CONFIGS, make_layer
+from oracle import qkv_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2   # attention tolerance stated by the north star
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def bits16(t):
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def u64(t):
+    return t.cpu().numpy().view(np.uint64)
+
+
+def rand_k(b, h, t, d, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn((b, h, t, d), generator=g) * scale
+    k[..., 3] *= 8.0
+    return k.to(torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# pack
+# ---------------------------------------------------------------------------
+
+def test_pack_known_answers():
+    rows = torch.zeros((1, 1, 8, 128), dtype=torch.float32)
+    kat = [[0, 0, 0, 0], [7, -7, 3.5, 0.5], [14, 1, -1, 2.5], [7, 2.5, -2.5, 1.5],
+           [1.0e6, -1.0e6, 0, 1], [7 * 2.0 ** -20, 0, 0, 0], [2.0 ** -30, 0, 0, 0], [1, -0.5, 0.25, 0]]
+    for t, vals in enumerate(kat):
+        rows[0, 0, t, :4] = torch.tensor(vals)
+    key = rows.to(torch.bfloat16).to(DEV)
+    packed, scales = K.int4_pack_k(key, 32)
+    torch.cuda.synchronize()
+    want_p, want_s = O.int4_pack_k(f32(key), 32)
+    assert np.array_equal(packed[..., :8, :].cpu().numpy(), want_p)
+    assert np.array_equal(bits16(scales[..., :8, :]), want_s)
+    assert bits16(scales)[0, 0, :8, 0].tolist() == [0, 0x3C00, 0x4000, 0x3C00, 0x7BFF, 0x0010, 0, 0x3092]
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_pack_matches_oracle(group):
+    key = rand_k(2, 3, 300, 128, seed=group).to(DEV)
+    packed, scales = K.int4_pack_k(key, group)
+    want_p, want_s = O.int4_pack_k(f32(key), group)
+    assert np.array_equal(packed[:, :, :300].cpu().numpy(), want_p)
+    assert np.array_equal(bits16(scales[:, :, :300]), want_s)
+
+
+def test_pack_strided_and_appended_range():
+    # K as a slice of a larger-capacity buffer (non-contiguous token stride),
+    # packed in two calls: tokens [0, 100) then the decode-style append [100, 101).
+    big = rand_k(1, 2, 160, 128, seed=7).to(DEV)
+    key = big[:, :, :101]
+    packed = torch.zeros((1, 2, 128, 64), dtype=torch.uint8, device=DEV)
+    scales = torch.zeros((1, 2, 128, 4), dtype=torch.float16, device=DEV)
+    K.int4_pack_k(key, 32, packed=packed, scales=scales, t_end=100)
+    K.int4_pack_k(key, 32, packed=packed, scales=scales, t_begin=100, t_end=101)
+    want_p, want_s = O.int4_pack_k(f32(key), 32)
+    assert np.array_equal(packed[:, :, :101].cpu().numpy(), want_p)
+    assert np.array_equal(bits16(scales[:, :, :101]), want_s)
+    assert int(packed[:, :, 101:].abs().sum()) == 0
+
+
+# ---------------------------------------------------------------------------
+# channel subset and slab
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("group,count", [(32, 32), (128, 64), (64, 16), (32, 128)])
+def test_select_channels_matches_oracle(group, count):
+    key = rand_k(2, 4, 777, 128, seed=count).to(DEV)
+    packed, scales = K.int4_pack_k(key, group)
+    chan, stats = K.select_channels(packed, scales, 777, group, count)
+    want_p, want_s = O.int4_pack_k(f32(key), group)
+    want_stats = O.channel_stats(want_p, want_s, group)
+    assert np.array_equal(u64(stats).reshape(8, 128), want_stats.reshape(8, 128))
+    assert np.array_equal(chan.cpu().numpy().reshape(8, count), O.select_channels(want_stats.reshape(8, 128), count))
+    assert 3 in chan.cpu().numpy()[0, 0].tolist()   # the x8 outlier channel is always chosen
+
+
+def test_select_channels_all_ties():
+    key = torch.ones((1, 1, 64, 128), dtype=torch.bfloat16, device=DEV)
+    packed, scales = K.int4_pack_k(key, 32)
+    chan, _ = K.select_channels(packed, scales, 64, 32, 32)
+    assert chan.cpu().numpy()[0, 0].tolist() == list(range(32))
+
+
+@pytest.mark.parametrize("count", [16, 32, 64, 128])
+def test_slab_matches_oracle(count):
+    key = rand_k(1, 3, 513, 128, seed=100 + count).to(DEV)
+    g = torch.Generator().manual_seed(count)
+    chan = torch.stack([torch.randperm(128, generator=g)[:count].sort().values for _ in range(3)])
+    chan = chan.view(1, 3, count).to(torch.int32).to(DEV)
+    slab, ss = K.build_slab(key, chan)
+    want, want_s = O.build_slab(f32(key).reshape(3, 513, 128), chan.cpu().numpy().reshape(3, count))
+    assert np.array_equal(slab[:, :, :513].cpu().numpy().reshape(3, 513, count // 2), want)
+    assert np.array_equal(bits16(ss[:, :, :513]).reshape(3, 513), want_s)
+
+
+# ---------------------------------------------------------------------------
+# decode scoring + block max
+# ---------------------------------------------------------------------------
+
+def _score_case(b, hq, hkv, t, count, block, seed):
+    g = torch.Generator().manual_seed(seed)
+    key = rand_k(b, hkv, t, 128, seed=seed).to(DEV)
+    q = torch.randn((b, hq, 128), generator=g).to(torch.bfloat16).to(DEV)
+    cache = K.Int4KCache.from_prefill(key, 32 if count <= 32 else 128, count)
+    bmax, isum, keys, qs = K.decode_scores(q, cache.chan_idx, cache.slab, cache.slab_scales, t, block, debug=True)
+    bmax_only = K.decode_scores(q, cache.chan_idx, cache.slab, cache.slab_scales, t, block)
+    rows = b * hkv
+    chan = cache.chan_idx.cpu().numpy().reshape(rows, count)
+    slab = cache.slab[:, :, :t].cpu().numpy().reshape(rows, t, count // 2)
+    sbits = bits16(cache.slab_scales[:, :, :t]).reshape(rows, t)
+    q8, want_qs = O.quantize_query_group(f32(q), chan, hkv)
+    want_i = O.partial_scores_i32(q8, slab)
+    want_k = O.ranking_keys(want_i, sbits)
+    want_b = O.block_max(want_k, block)
+    assert np.array_equal(qs.cpu().numpy().reshape(rows), want_qs)
+    assert np.array_equal(isum.cpu().numpy().reshape(rows, t), want_i)
+    assert np.array_equal(keys.cpu().numpy().reshape(rows, t).view(np.uint32), want_k.view(np.uint32))
+    assert np.array_equal(bmax.cpu().numpy().reshape(rows, -1), want_b)
+    assert np.array_equal(bmax_only.cpu().numpy().reshape(rows, -1), want_b)
+    return want_b
+
+
+@pytest.mark.parametrize("count", [16, 32, 64, 128])
+@pytest.mark.parametrize("block", [1, 16, 64])
+def test_decode_scores_matches_oracle(count, block):
+    _score_case(2, 8, 4, 1000, count, block, seed=count * 7 + block)
+
+
+@pytest.mark.parametrize("b,hq,hkv,t", [(1, 8, 8, 64), (1, 16, 8, 4096), (3, 32, 8, 5003), (1, 64, 8, 2500)])
+def test_decode_scores_shapes(b, hq, hkv, t):
+    _score_case(b, hq, hkv, t, 32, 16, seed=t)
+
+
+def test_decode_scores_many_chunks():
+    # enough tokens that one row spans several workgroups
+    _score_case(1, 2, 1, 70000, 32, 16, seed=11)
+
+
+# ---------------------------------------------------------------------------
+# top-k
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(5, 2), (100, 1), (100, 100), (2048, 128), (2048, 256), (4096, 256),
+                                 (5000, 999), (12288, 64), (20000, 1024), (131072, 1024)])
+def test_topk_matches_oracle(n, k):
+    g = torch.Generator().manual_seed(n + k)
+    vals = torch.randint(-50, 50, (6, n), generator=g).float()   # heavy ties
+    vals[0] = torch.randn(n, generator=g)
+    vals[1, ::3] = -0.0
+    vals[1, 1::3] = 0.0
+    vals[2, : n // 2] = -float("inf")
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
+def test_topk_strided_rows():
+    g = torch.Generator().manual_seed(3)
+    base = torch.randint(0, 4, (4, 300), generator=g).float().to(DEV)
+    view = base[:, :256]
+    got = K.block_topk(view, 17).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(view.cpu().numpy(), 17))
+
+
+# ---------------------------------------------------------------------------
+# sparse attention
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("g_size", [1, 2, 4, 8])
+@pytest.mark.parametrize("block,nsel", [(1, 256), (1, 300), (16, 128), (64, 7)])
+def test_sparse_attention_matches_fp64(g_size, block, nsel):
+    b, hkv, t = 2, 2, 3000
+    hq = hkv * g_size
+    gen = torch.Generator().manual_seed(g_size * 1000 + block)
+    q = torch.randn((b, hq, 128), generator=gen).to(torch.bfloat16)
+    k = (torch.randn((b, hkv, t, 128), generator=gen) * 2).to(torch.bfloat16)
+    v = torch.randn((b, hkv, t, 128), generator=gen).to(torch.bfloat16)
+    nb = -(-t // block)
+    sel = torch.stack([torch.randperm(nb, generator=gen)[:nsel].sort().values for _ in range(b * hkv)])
+    sel = sel.view(b, hkv, nsel).to(torch.int32)
+    sel[0, 0, 0] = -1                  # invalid ids are skipped
+    sel[0, 1, -1] = nb - 1             # the partial last block
+    out = K.sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV), block, t, 128 ** -0.5)
+    want = O.sparse_attention(f32(q), f32(k), f32(v), sel.numpy(), block, t, 128 ** -0.5)
+    assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+
+
+def test_sparse_attention_no_valid_block_gives_zero():
+    q = torch.randn((1, 2, 128)).to(torch.bfloat16).to(DEV)
+    k = torch.randn((1, 1, 64, 128)).to(torch.bfloat16).to(DEV)
+    sel = torch.tensor([[[-1, 5, 100]]], dtype=torch.int32, device=DEV)
+    out = K.sparse_attention(q, k, k, sel, 16, 64, 0.1)
+    assert torch.count_nonzero(out.float()) == 0
+
+
+def test_sparse_attention_strided_cache():
+    # K/V live in a larger-capacity cache; only the first `t` tokens exist.
+    gen = torch.Generator().manual_seed(5)
+    kc = torch.randn((1, 2, 512, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((1, 2, 512, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, 4, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    t = 300
+    k, v = kc[:, :, :t], vc[:, :, :t]
+    sel = torch.tensor([[[0, 3, 18], [1, 2, 17]]], dtype=torch.int32, device=DEV)   # 18*16 > t: partial
+    out = K.sparse_attention(q, k, v, sel, 16, t, 0.09)
+    want = O.sparse_attention(f32(q), f32(k), f32(v), sel.cpu().numpy(), 16, t, 0.09)
+    assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+
+
+# ---------------------------------------------------------------------------
+# config 1 end to end (full size)
+# ---------------------------------------------------------------------------
+
+def test_config1_end_to_end():
+    cfg = CONFIGS["cfg1"]
+    q, k, v, _ = make_layer(cfg, 0)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    cache = K.Int4KCache.from_prefill(kd, cfg.group, cfg.selected)
+    step = K.SparseDecodeStep(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.tokens, cfg.block,
+                              cfg.topk, DEV)
+    out = step(qd, cache, kd, vd, cfg.scaling)
+    torch.cuda.synchronize()
+    rows = cfg.rows
+    kn = f32(k).reshape(rows, cfg.tokens, 128)
+    want_p, want_s = O.int4_pack_k(kn, cfg.group)
+    assert np.array_equal(cache.packed[:, :, : cfg.tokens].cpu().numpy().reshape(want_p.shape), want_p)
+    chan = O.select_channels(O.channel_stats(want_p, want_s, cfg.group), cfg.selected)
+    assert np.array_equal(cache.chan_idx.cpu().numpy().reshape(rows, -1), chan)
+    slab, sbits = O.build_slab(kn, chan)
+    _, _, bmax, sel = O.decode_select(f32(q), slab, sbits, chan, cfg.kv_heads, cfg.block, cfg.topk)
+    assert np.array_equal(step.bmax.cpu().numpy().reshape(rows, -1), bmax)
+    assert np.array_equal(step.sel.cpu().numpy().reshape(rows, -1), sel)
+    want = O.sparse_attention(f32(q), f32(k), f32(v), sel.reshape(cfg.batch, cfg.kv_heads, -1), cfg.block,
+                              cfg.tokens, cfg.scaling)
+    assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
