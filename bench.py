@@ -190,8 +190,8 @@ def main() -> int:
                                workspace=step.workspace, out=step.out)
 
     dense_sel = torch.arange(cfg.n_blocks, dtype=torch.int32, device="cuda").repeat(rows, 1).contiguous()
-    dense_ws = torch.empty(K.attention_workspace_bytes(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
-                                                       cfg.n_blocks, cfg.block) // 4 + 1, device="cuda")
+    dense_ws = K.attention_workspace(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.n_blocks,
+                                     cfg.block, "cuda")
     dense_out = torch.empty_like(step.out)
 
     def run_dense():

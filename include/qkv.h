@@ -113,24 +113,43 @@ int qkv_int4_select_channels(const uint8_t* packed, const uint16_t* scales, int6
                              int64_t selected, uint64_t* stats, int32_t* chan_idx, void* stream);
 
 /* Subset slab of tokens [t_begin, t_end): the `selected` channels chan_idx
- * of each K row re-quantized as one int4 group: slab uint8
- * [rows,capacity,selected/2], slab_scales fp16 bits [rows,capacity].
- * selected in {16,32,64,128}.  int4 analogue of EV:2018-2042. */
+ * of each K row re-quantized as one int4 group.  slab holds rows *
+ * capacity * selected/2 bytes, each row's codes in 4096-byte tiles of
+ * 8192/selected keys: lane l of a tile owns keys [l*128/S, (l+1)*128/S) =
+ * 64 logical bytes, whose logical byte b is stored at tile offset
+ * (64*(b/16) + l)*16 + b%16 (b = (key % (128/S)) * S/2 + code byte).
+ * slab_scales fp16 bits [rows,capacity] in key order.  selected in
+ * {16,32,64,128}; capacity a multiple of 8192/selected.  int4 analogue of
+ * the reference's dim-major K copy (EV:2018-2042). */
 int qkv_int4_build_slab(const void* key, const int64_t* k_strides, int64_t batch,
                         int64_t kv_heads, int64_t t_begin, int64_t t_end, int64_t head_dim,
                         const int32_t* chan_idx, int64_t selected, uint8_t* slab,
                         uint16_t* slab_scales, int64_t capacity, void* stream);
 
+/* Per-row int8 query of decode scoring.  query bf16 [B,Hq,D] contiguous,
+ * Hq = G * Hkv.  The G query heads of a row are summed over the row's
+ * channels chan_idx (fp32, head order), quantized to int8 q8[s] =
+ * rint(qg[s] / (amax/127)), and packed as qwords uint32 [rows, selected/4]:
+ * dword 2d holds q8 of channels 8d, 8d+2, 8d+4, 8d+6 (bytes 0..3), dword
+ * 2d+1 channels 8d+1, 8d+3, ...  qscale f32 [rows] (optional) receives
+ * amax/127.  qkv_int4_decode_scores computes the same words itself; this
+ * entry point exposes them.  The reference picks top-|q| dims per query head
+ * instead (EV:4428, QK:123-145). */
+int qkv_int4_query_words(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                         int64_t head_dim, const int32_t* chan_idx, int64_t selected,
+                         uint32_t* qwords, float* qscale, void* stream);
+
 /* Decode scoring over tokens [0, tokens) of every row, fused with block
  * max-pooling.  Replaces qabs_partial_scores_dim_major_forward (QK:63-96)
  * plus the block pool of EV:5038-5044.
- * query bf16 [B,Hq,D] contiguous, Hq = G * Hkv.  Per row the G query heads
- * are summed over the row's channels (fp32, head order), quantized to int8
- * (scale amax/127), and I[t] = sum_s q8[s]*code[t,s] (int32); the ranking
- * key is fp32(slab_scale[t]) * fp32(I[t]).
- * bmax f32 [rows, ceil(tokens/block)] (block a power of two, 1..64*128/S).
- * isum int32 [rows,tokens] and keys f32 [rows,tokens] are optional (NULL to
- * skip); bmax may be NULL when either is given.  qscale f32 [rows] optional. */
+ * query bf16 [B,Hq,D] contiguous, Hq = G * Hkv; chan_idx int32
+ * [rows,selected].  I[t] = sum_s q8[s] * code[t,s] (int32) with q8 as
+ * qkv_int4_query_words defines it; the ranking key is fp32(slab_scale[t]) *
+ * fp32(I[t]).  bmax f32 [rows, ceil(tokens/block)] (block a power of two,
+ * 1..8192/S).  isum int32 [rows,tokens] and keys f32 [rows,tokens] are
+ * optional (NULL to skip); bmax may be NULL when both are given.  qscale f32
+ * [rows] optional.  The slab is the tile layout qkv_int4_build_slab writes
+ * (capacity a multiple of 8192/S). */
 int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads,
                            int64_t head_dim, const int32_t* chan_idx, int64_t selected,
                            const uint8_t* slab, const uint16_t* slab_scales, int64_t capacity,
@@ -145,7 +164,9 @@ int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, in
 int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
              int32_t* out, void* stream);
 
-/* Bytes of f32 workspace qkv_sparse_attention needs for these sizes. */
+/* Bytes of f32 workspace qkv_sparse_attention needs for these sizes (the
+ * per-split partials: G*(D+2) floats per split of 256 token slots, 128 at
+ * G = 8). */
 int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                              int64_t head_dim, int64_t n_sel, int64_t block);
 
@@ -158,7 +179,8 @@ int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int
  * tokens [id*block, min(tokens,(id+1)*block)).  Every query head of a row
  * attends, with softmax(scaling * q.k), over the union of the row's blocks.
  * out bf16 [B,Hq,D]; a head with no valid token gets zeros (QK:388, 404).
- * D must be 128. */
+ * D must be 128.  Rows of more than one split are merged by a second kernel
+ * on the same stream.  Calls sharing a workspace must not overlap in time. */
 int qkv_sparse_attention(const void* query, const void* key, const void* value,
                          const int64_t* kv_strides, int64_t batch, int64_t q_heads,
                          int64_t kv_heads, int64_t tokens, int64_t head_dim,

@@ -14,6 +14,7 @@ from .int4 import (
     build_slab,
     decode_scores,
     int4_pack_k,
+    query_words,
     select_channels,
     sparse_attention,
 )
@@ -27,7 +28,7 @@ from .qabs_cuda_kernels import (
 load = _lib.load
 
 __all__ = [
-    "Int4KCache", "SparseDecodeStep", "block_topk", "build_slab", "decode_scores", "int4_pack_k",
+    "Int4KCache", "SparseDecodeStep", "block_topk", "build_slab", "decode_scores", "int4_pack_k", "query_words",
     "select_channels", "sparse_attention", "candidate_full_scores", "final_attention",
     "partial_scores", "partial_scores_dim_major", "load",
 ]

@@ -43,6 +43,7 @@ _PROTOTYPES = {
     "qkv_int4_select_channels": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "qkv_int4_build_slab": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
                                    _i64, _vp]),
+    "qkv_int4_query_words": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "qkv_int4_decode_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64,
                                       _i64, _vp, _vp, _vp, _vp, _vp]),
     "qkv_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),

@@ -1,20 +1,34 @@
 // GQA-native sparse gather attention over selected KV blocks (bf16 K/V,
-// fp32 accumulation), split over the selected tokens with a log-sum-exp merge.
+// fp32 softmax and accumulation), one launch per call.
 //
 // The reference expands K/V to every query head (evaluate_qwen3_top2_head_
 // limit3_ppl.py:6248-6251) and then gathers per head (EV:4490-4502, kernel
 // qabs_cuda_kernels.py:335-419).  Here the G query heads of a KV head share
-// one pass over the selected rows: each 256-token split is read once from
-// HBM (512 bytes per token), scored for all G heads, and its partial
-// (max, sum, weighted V) goes to a workspace that a second kernel merges.
+// one pass over the selected rows, so every selected K/V row is read from HBM
+// once (512 bytes per token at D = 128).
+//
+// Work split: a workgroup (4 waves) owns 16*NI consecutive token slots of one
+// (sequence, KV head) row, where slot s is token (block_ids[s / block] * block
+// + s % block).  Inside a wave, 16 lanes share a token: lane (16*g + c) holds
+// channels 8c..8c+7 of the token of slot 4i + g in iteration i, so each load
+// instruction reads four whole 256-byte K (or V) rows.  All K and V loads of a
+// wave are issued before any arithmetic.  QK is v_dot2_f32_bf16 on the packed
+// channel pairs followed by a 16-lane DPP reduction; softmax runs in the log2
+// domain; P.V accumulates in fp32.  Each workgroup reduces its waves through
+// LDS into (max, sum, weighted V) per head.  A row that fits one workgroup
+// writes its bf16 output directly; otherwise the partials go to the workspace
+// and a second, small kernel merges them.  (An in-kernel last-arriver merge
+// would need an agent-scope fence per workgroup, which on gfx950 writes back
+// and invalidates the XCD's whole L2: measured several times slower.)
 #include "common.h"
 
 namespace qkv {
 namespace {
 
 constexpr int kD = 128;     // head dim
-constexpr int kCT = 256;    // tokens per split workgroup
 constexpr int kNT = 256;    // threads per workgroup
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -23,196 +37,233 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
-__device__ __forceinline__ void bf16x8(const uint4& raw, float* x) {
-  x[0] = bf16lo(raw.x); x[1] = bf16hi(raw.x);
-  x[2] = bf16lo(raw.y); x[3] = bf16hi(raw.y);
-  x[4] = bf16lo(raw.z); x[5] = bf16hi(raw.z);
-  x[6] = bf16lo(raw.w); x[7] = bf16hi(raw.w);
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
 }
 
-template <int G>
-__global__ __launch_bounds__(kNT) void attn_partial_kernel(
+template <int DPP>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP, 0xF, 0xF, false));
+}
+
+// Sum over each row of 16 lanes; every lane of the row receives the sum.
+// quad_perm [1,0,3,2] and [2,3,0,1] reduce each quad, then row_half_mirror
+// and row_mirror pair every lane with the other quad / other half.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return v;
+}
+
+template <int G, int NI>
+__global__ __launch_bounds__(kNT) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
-    int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
-    int bps, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml) {
-  __shared__ float q_s[G][kD];
-  __shared__ int tok_s[kCT];
-  __shared__ float p_s[G][kCT];
-  __shared__ float red[kNT / 64][G];
-  __shared__ float red_acc[kNT / 64][G][kD];
-  __shared__ float ml_s[G][2];
+    int kv_heads, int64_t tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
+    int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    uint16_t* __restrict__ out) {
+  constexpr int SLOTS_W = 4 * NI;          // token slots per wave
+  constexpr int SLOTS_WG = 4 * SLOTS_W;    // token slots per workgroup
+  static_assert(SLOTS_W <= 64, "one slot per lane when resolving token ids");
+
+  __shared__ float red_acc[4][G][kD];   // per wave weighted V
+  __shared__ float red_m[4][G], red_l[4][G];
 
   const int r = blockIdx.y, split = blockIdx.x;
   const int b = r / kv_heads, j = r - b * kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nb = (tokens + block - 1) / block;
+  const int grp = lane >> 4, cc = lane & 15;
   const float ninf = -__builtin_huge_valf();
 
-  const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * kD;
-  for (int i = tid; i < G * kD; i += kNT) q_s[i / kD][i % kD] = bf16_to_f32(qrow[i]);
-  {
-    int tok = -1;
-    if (tid < bps * block) {
-      const int slot = split * bps + tid / block;
-      if (slot < n_sel) {
-        const int id = block_ids[static_cast<int64_t>(r) * n_sel + slot];
-        if (id >= 0 && id < nb) {
-          const int tt = id * block + tid % block;
-          if (tt < tokens) tok = tt;
-        }
+  // Token id of slot (wave base + lane), then of this lane's slot 4i + grp.
+  int my_tok = -1;
+  if (lane < SLOTS_W) {
+    const int64_t slot = static_cast<int64_t>(split) * SLOTS_WG + wave * SLOTS_W + lane;
+    const int64_t bs = slot / block;
+    if (bs < n_sel) {
+      const int id = block_ids[static_cast<int64_t>(r) * n_sel + bs];
+      if (id >= 0 && id < nb) {
+        const int64_t t = static_cast<int64_t>(id) * block + (slot - bs * block);
+        if (t < tokens) my_tok = static_cast<int>(t);
       }
     }
-    tok_s[tid] = tok;
   }
-  __syncthreads();
+  int tok[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) tok[i] = __builtin_amdgcn_ds_bpermute((4 * i + grp) << 2, my_tok);
 
-  const uint16_t* kbase = key + b * sb + j * sh;
-  const uint16_t* vbase = value + b * sb + j * sh;
+  const uint16_t* kb = key + b * sb + j * sh + cc * 8;
+  const uint16_t* vb = value + b * sb + j * sh + cc * 8;
+  uint4 kx[NI], vx[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    kx[i] = make_uint4(0, 0, 0, 0);
+    if (tok[i] >= 0) kx[i] = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(tok[i]) * st);
+  }
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    vx[i] = make_uint4(0, 0, 0, 0);
+    if (tok[i] >= 0) vx[i] = *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(tok[i]) * st);
+  }
+  uint4 qx[G];
+  const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * kD + cc * 8;
+#pragma unroll
+  for (int h = 0; h < G; ++h) qx[h] = *reinterpret_cast<const uint4*>(qrow + h * kD);
 
-  // Phase 1: one token per thread, scores for all G heads (log2 domain).
-  float s[G];
-  {
-    const int tok = tok_s[tid];
-    if (tok >= 0) {
-      const uint4* krow = reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(tok) * st);
-      float acc[G];
+  // Scores (log2 domain) and the wave max per head.
+  float s[G][NI];
+  float m[G];
 #pragma unroll
-      for (int h = 0; h < G; ++h) acc[h] = 0.0f;
-#pragma unroll 4
-      for (int c = 0; c < kD / 8; ++c) {
-        float kx[8];
-        bf16x8(krow[c], kx);
+  for (int h = 0; h < G; ++h) m[h] = ninf;
 #pragma unroll
-        for (int h = 0; h < G; ++h)
+  for (int i = 0; i < NI; ++i) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[h] = __builtin_fmaf(q_s[h][c * 8 + i], kx[i], acc[h]);
-      }
-#pragma unroll
-      for (int h = 0; h < G; ++h) s[h] = acc[h] * scale_log2;
-    } else {
-#pragma unroll
-      for (int h = 0; h < G; ++h) s[h] = ninf;
+    for (int h = 0; h < G; ++h) {
+      float a = dot2_bf16(qx[h].x, kx[i].x, 0.0f);
+      a = dot2_bf16(qx[h].y, kx[i].y, a);
+      a = dot2_bf16(qx[h].z, kx[i].z, a);
+      a = dot2_bf16(qx[h].w, kx[i].w, a);
+      a = row16_sum(a) * scale_log2;
+      s[h][i] = tok[i] >= 0 ? a : ninf;
+      m[h] = fmaxf(m[h], s[h][i]);
     }
   }
-
-  // Phase 2: split-local softmax statistics.
-  float m[G], l[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float v = wave_max(s[h]);
-    if (lane == 0) red[wave][h] = v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float v = red[0][h];
-    for (int w = 1; w < kNT / 64; ++w) v = fmaxf(v, red[w][h]);
-    m[h] = v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float p = (s[h] == ninf) ? 0.0f : exp2f(s[h] - m[h]);
-    p_s[h][tid] = p;
-    const float v = wave_sum(p);
-    if (lane == 0) red[wave][h] = v;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float v = 0.0f;
-    for (int w = 0; w < kNT / 64; ++w) v += red[w][h];
-    l[h] = v;
+    m[h] = fmaxf(m[h], shfl_xor(m[h], 16));
+    m[h] = fmaxf(m[h], shfl_xor(m[h], 32));
   }
 
-  // Phase 3: P.V with 16 dim groups (8 channels, one 128-bit load) x 16 token lanes.
-  const int dg = tid & 15, tl = tid >> 4;
+  // p = 2^(s - m); per-group sums and P.V over this lane's 8 channels.
   float acc[G][8];
+  float l[G];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int h = 0; h < G; ++h) {
+    l[h] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.0f;
-  for (int tt = tl; tt < kCT; tt += 16) {
-    const int tk = tok_s[tt];
-    if (tk < 0) continue;
-    float vx[8];
-    bf16x8(reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(tk) * st)[dg], vx);
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float p = p_s[h][tt];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] = __builtin_fmaf(p, vx[i], acc[h][i]);
-    }
+    for (int c = 0; c < 8; ++c) acc[h][c] = 0.0f;
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[h][i];
-      v += shfl_xor(v, 16);
-      v += shfl_xor(v, 32);
-      acc[h][i] = v;
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) red_acc[wave][h][dg * 8 + i] = acc[h][i];
-  }
-  if (tid == 0) {
+  for (int i = 0; i < NI; ++i) {
+    float v[8];
+    v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
+    v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
+    v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
+    v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      ml_s[h][0] = m[h];
-      ml_s[h][1] = l[h];
+      const float p = (s[h][i] == ninf) ? 0.0f : exp2f(s[h][i] - m[h]);
+      l[h] += p;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[h][c] = __builtin_fmaf(p, v[c], acc[h][c]);
+    }
+  }
+
+  // The four token groups of a wave share the wave max: sum them in
+  // registers, then combine the four waves through LDS.
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    l[h] += shfl_xor(l[h], 16);
+    l[h] += shfl_xor(l[h], 32);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      acc[h][c] += shfl_xor(acc[h][c], 16);
+      acc[h][c] += shfl_xor(acc[h][c], 32);
+    }
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) red_acc[wave][h][cc * 8 + c] = acc[h][c];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      red_m[wave][h] = m[h];
+      red_l[wave][h] = l[h];
     }
   }
   __syncthreads();
+
+  // Workgroup max per head and the rescale factor of each wave.
+  float wg_m[G], wg_l[G], fs[G][4];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float mx = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
+    wg_m[h] = mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      fs[h][w] = (red_m[w][h] == ninf) ? 0.0f : exp2f(red_m[w][h] - mx);
+      sum = __builtin_fmaf(red_l[w][h], fs[h][w], sum);
+    }
+    wg_l[h] = sum;
+  }
+  auto wg_acc = [&](int h, int d) -> float {
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o = __builtin_fmaf(red_acc[w][h][d], fs[h][w], o);
+    return o;
+  };
+
+  if (nsplit == 1) {
+    for (int idx = tid; idx < G * kD; idx += kNT) {
+      const int h = idx / kD, d = idx - h * kD;
+      const float o = (wg_m[h] == ninf) ? 0.0f : wg_acc(h, d) / wg_l[h];
+      out[(static_cast<int64_t>(b) * q_heads + j * G + h) * kD + d] = f32_to_bf16_rne(o);
+    }
+    return;
+  }
+
   const int64_t part = static_cast<int64_t>(r) * nsplit + split;
-  float* pacc = ws_acc + part * G * kD;
   for (int idx = tid; idx < G * kD; idx += kNT) {
     const int h = idx / kD, d = idx - h * kD;
-    float v = red_acc[0][h][d];
-    for (int w = 1; w < kNT / 64; ++w) v += red_acc[w][h][d];
-    pacc[idx] = v;
+    ws_acc[part * G * kD + idx] = wg_acc(h, d);
   }
   if (tid < G) {
-    ws_ml[(part * G + tid) * 2 + 0] = ml_s[tid][0];
-    ws_ml[(part * G + tid) * 2 + 1] = ml_s[tid][1];
+    ws_ml[(part * G + tid) * 2 + 0] = wg_m[tid];
+    ws_ml[(part * G + tid) * 2 + 1] = wg_l[tid];
   }
 }
 
+// Merges the split partials of one row: thread (h, d) rescales every split's
+// weighted V by 2^(m_i - max) and divides by the rescaled sum.
 template <int G>
-__global__ __launch_bounds__(kD) void attn_merge_kernel(const float* __restrict__ ws_acc,
-                                                        const float* __restrict__ ws_ml, int nsplit,
-                                                        int q_heads, int kv_heads,
-                                                        uint16_t* __restrict__ out) {
-  const int r = blockIdx.x, d = threadIdx.x;
+__global__ __launch_bounds__(G * kD) void sparse_attn_merge_kernel(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml, int nsplit, int q_heads,
+    int kv_heads, uint16_t* __restrict__ out) {
+  const int r = blockIdx.x, idx = threadIdx.x, h = idx / kD;
   const int b = r / kv_heads, j = r - b * kv_heads;
   const float ninf = -__builtin_huge_valf();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float mx = ninf;
-    for (int i = 0; i < nsplit; ++i) mx = fmaxf(mx, ws_ml[((static_cast<int64_t>(r) * nsplit + i) * G + h) * 2]);
-    float o = 0.0f;
-    if (mx != ninf) {
-      float den = 0.0f;
-      for (int i = 0; i < nsplit; ++i) {
-        const int64_t part = static_cast<int64_t>(r) * nsplit + i;
-        const float mi = ws_ml[(part * G + h) * 2];
-        const float w = (mi == ninf) ? 0.0f : exp2f(mi - mx);
-        den = __builtin_fmaf(ws_ml[(part * G + h) * 2 + 1], w, den);
-        o = __builtin_fmaf(ws_acc[(part * G + h) * kD + d], w, o);
-      }
-      o = o / den;
+  const float* ml = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2 + h * 2;
+  const float* pa = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD + idx;
+  float mx = ninf;
+  for (int i = 0; i < nsplit; ++i) mx = fmaxf(mx, ml[i * G * 2]);
+  float o = 0.0f;
+  if (mx != ninf) {
+    float den = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < nsplit; ++i) {
+      const float mi = ml[i * G * 2];
+      const float w = (mi == ninf) ? 0.0f : exp2f(mi - mx);
+      den = __builtin_fmaf(ml[i * G * 2 + 1], w, den);
+      o = __builtin_fmaf(pa[static_cast<int64_t>(i) * G * kD], w, o);
     }
-    out[(static_cast<int64_t>(b) * q_heads + j * G + h) * kD + d] = f32_to_bf16_rne(o);
+    o = o / den;
   }
+  out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(o);
 }
 
-int64_t splits_for(int64_t n_sel, int64_t block) {
-  const int64_t bps = std::max<int64_t>(1, kCT / block);
-  return cdiv(n_sel, bps);
+// Token slots per workgroup for a group size (fewer for G = 8 to bound registers).
+constexpr int ni_for(int64_t g) { return g >= 8 ? 8 : 16; }
+
+int64_t splits_for(int64_t n_sel, int64_t block, int64_t g) {
+  return cdiv(n_sel * block, 16 * ni_for(g));
 }
 
 }  // namespace
@@ -224,10 +275,12 @@ QKV_EXPORT int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q
                                                         int64_t kv_heads, int64_t head_dim,
                                                         int64_t n_sel, int64_t block) {
   if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads || head_dim != kD || n_sel <= 0 ||
-      block <= 0 || block > kCT)
+      block <= 0 || n_sel * block >= (int64_t(1) << 31))
     return -1;
   const int64_t g = q_heads / kv_heads;
-  return 4 * batch * kv_heads * splits_for(n_sel, block) * g * (kD + 2);
+  const int64_t rows = batch * kv_heads;
+  // per split: weighted V per head, then (max, sum) per head
+  return 4 * rows * splits_for(n_sel, block, g) * g * (kD + 2);
 }
 
 QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const void* value,
@@ -245,20 +298,22 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   if (g != 1 && g != 2 && g != 4 && g != 8)
     return fail(QKV_ERR_UNSUPPORTED, "qkv_sparse_attention: group size %lld not built", (long long)g);
   if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many rows");
-  if (tokens <= 0 || tokens >= (int64_t(1) << 30) || n_sel <= 0 || block <= 0 || block > kCT)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: need tokens > 0, n_sel > 0, 1 <= block <= %d", kCT);
-  if (!aligned(key, 16) || !aligned(value, 16) || (kv_strides[0] | kv_strides[1] | kv_strides[2]) % 8)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: K/V rows must be 16-byte aligned");
+  if (tokens <= 0 || tokens >= (int64_t(1) << 31) || n_sel <= 0 || block <= 0 ||
+      n_sel * block >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: need tokens > 0, n_sel > 0, block > 0");
+  if (!aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16) ||
+      (kv_strides[0] | kv_strides[1] | kv_strides[2]) % 8)
+    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: q/K/V rows must be 16-byte aligned");
   const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block);
   if (workspace_bytes < need)
     return fail(QKV_ERR_INVALID, "qkv_sparse_attention: workspace needs %lld bytes, got %lld",
                 (long long)need, (long long)workspace_bytes);
   const int64_t rows = batch * kv_heads;
-  const int64_t nsplit = splits_for(n_sel, block);
+  const int64_t nsplit = splits_for(n_sel, block, g);
   if (nsplit > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many selected blocks");
-  const int bps = static_cast<int>(std::max<int64_t>(1, kCT / block));
   float* ws_acc = workspace;
-  float* ws_ml = workspace + rows * nsplit * g * kD;
+  float* ws_ml = ws_acc + rows * nsplit * g * kD;
+  const int nb = static_cast<int>(cdiv(tokens, block));
   const float scale_log2 = scaling * 1.4426950408889634f;
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(rows));
@@ -266,16 +321,16 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   const uint16_t* k = static_cast<const uint16_t*>(key);
   const uint16_t* v = static_cast<const uint16_t*>(value);
   uint16_t* o = static_cast<uint16_t*>(out);
-#define QKV_ATTN(GG)                                                                                    \
-  attn_partial_kernel<GG><<<grid, kNT, 0, st>>>(q, k, v, kv_strides[0], kv_strides[1], kv_strides[2],   \
-                                                static_cast<int>(q_heads), static_cast<int>(kv_heads),  \
-                                                static_cast<int>(tokens), block_ids,                    \
-                                                static_cast<int>(n_sel), static_cast<int>(block), bps,  \
-                                                scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml);   \
-  if (int rc = check_launch("qkv_sparse_attention(partial)")) return rc;                              \
-  attn_merge_kernel<GG><<<static_cast<unsigned>(rows), kD, 0, st>>>(ws_acc, ws_ml, static_cast<int>(nsplit), \
-                                                                    static_cast<int>(q_heads),          \
-                                                                    static_cast<int>(kv_heads), o);
+#define QKV_ATTN(GG)                                                                                   \
+  sparse_attn_kernel<GG, ni_for(GG)><<<grid, kNT, 0, st>>>(                                            \
+      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                 \
+      static_cast<int>(kv_heads), tokens, block_ids, static_cast<int>(n_sel), static_cast<int>(block), \
+      nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, o);                                     \
+  if (nsplit > 1) {                                                                                    \
+    if (int rc = check_launch("qkv_sparse_attention(partial)")) return rc;                             \
+    sparse_attn_merge_kernel<GG><<<static_cast<unsigned>(rows), GG * kD, 0, st>>>(                     \
+        ws_acc, ws_ml, static_cast<int>(nsplit), static_cast<int>(q_heads), static_cast<int>(kv_heads), o); \
+  }
   switch (g) {
     case 1: QKV_ATTN(1); break;
     case 2: QKV_ATTN(2); break;
@@ -283,5 +338,5 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
     default: QKV_ATTN(8); break;
   }
 #undef QKV_ATTN
-  return check_launch("qkv_sparse_attention(merge)");
+  return check_launch("qkv_sparse_attention");
 }

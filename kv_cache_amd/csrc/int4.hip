@@ -15,10 +15,7 @@
 #include "common.h"
 
 #ifndef QKV_SCORE_TARGET_WGS
-#define QKV_SCORE_TARGET_WGS 2048
-#endif
-#ifndef QKV_SCORE_UNROLL
-#define QKV_SCORE_UNROLL 2
+#define QKV_SCORE_TARGET_WGS 4096
 #endif
 
 namespace qkv {
@@ -163,7 +160,26 @@ __global__ __launch_bounds__(64) void select_channels_kernel(const uint64_t* __r
 
 // ---------------------------------------------------------------------------
 // Subset slab: S/8 lanes per token, each gathers 8 selected channels.
+//
+// The slab's codes are stored in tiles of 4096 bytes = 64 lanes x 4 chunks of
+// 16 bytes, one tile per 8192/S keys.  Lane l of a tile owns the 128/S
+// consecutive keys [l * 128/S, (l+1) * 128/S), i.e. 64 logical bytes; its
+// logical byte b sits at tile offset (64 * (b / 16) + l) * 16 + b % 16.  A
+// wave reading chunk 64j + l in load j therefore issues fully coalesced
+// 16-byte loads and still ends with whole, consecutive keys in each lane.
 // ---------------------------------------------------------------------------
+__host__ __device__ constexpr int64_t slab_tile_keys(int s) { return 8192 / s; }
+
+// Byte offset, within a row's slab, of logical code byte x of key t.
+template <int S>
+__device__ __forceinline__ int64_t slab_offset(int64_t t, int x) {
+  constexpr int KPLN = 128 / S;            // keys per lane
+  const int64_t tile = t / slab_tile_keys(S);
+  const int k = static_cast<int>(t - tile * slab_tile_keys(S));
+  const int lane = k / KPLN;
+  const int b = (k - lane * KPLN) * (S / 2) + x;
+  return tile * 4096 + (64 * (b >> 4) + lane) * 16 + (b & 15);
+}
 template <int S>
 __global__ __launch_bounds__(kThreads) void build_slab_kernel(
     const uint16_t* __restrict__ key, int64_t ksb, int64_t ksh, int64_t kst, int kv_heads,
@@ -196,7 +212,7 @@ __global__ __launch_bounds__(kThreads) void build_slab_kernel(
   uint32_t word = quantize8(x, a, &sbits);
   if (active) {
     const int64_t tok = r * capacity + t;
-    reinterpret_cast<uint32_t*>(slab)[tok * TPT + jj] = word;
+    *reinterpret_cast<uint32_t*>(slab + r * capacity * (S / 2) + slab_offset<S>(t, 4 * jj)) = word;
     if (jj == 0) slab_scales[tok] = static_cast<uint16_t>(sbits);
   }
 }
@@ -204,26 +220,153 @@ __global__ __launch_bounds__(kThreads) void build_slab_kernel(
 // ---------------------------------------------------------------------------
 // Decode scoring fused with block max-pooling.
 //
-// Each lane owns KPL = 128/S consecutive keys of a wave tile (64 bytes of
-// codes = four 128-bit loads, plus KPL fp16 scales in one load).  Nibble
-// pairs are moved to the high half of each byte -- (w << 4) & 0xF0F0F0F0 for
-// even channels, w & 0xF0F0F0F0 for odd ones -- so each byte is 16 * code as
-// a signed int8, and two v_dot4_i32_i8 per code dword give 16 * I exactly.
+// One wave stage is one slab tile: lane l issues four coalesced 16-byte
+// non-temporal loads (chunks 64j + l) and one coalesced load of its KPLN
+// scales, and then holds whole keys [l*KPLN, (l+1)*KPLN) of the tile.  The
+// dot is v_dot4_i32_i8 on nibbles moved to the high half of each byte --
+// (w << 4) & 0xF0F0F0F0 for even channels, w & 0xF0F0F0F0 for odd ones -- so
+// each byte is 16 * code as a signed int8 and the int32 sum is 16 * I.
+// Block maxima are an in-lane max and a DPP reduction over block/KPLN lanes;
+// a stage's maxima leave in one store.
 // ---------------------------------------------------------------------------
-template <int KPL> struct ScaleVec;
-template <> struct ScaleVec<1> { using T = uint16_t; static __device__ uint32_t get(T v, int) { return v; } };
-template <> struct ScaleVec<2> { using T = uint32_t; static __device__ uint32_t get(T v, int i) { return (v >> (16 * i)) & 0xFFFFu; } };
-template <> struct ScaleVec<4> {
-  using T = uint2;
-  static __device__ uint32_t get(T v, int i) { uint32_t w = (i < 2) ? v.x : v.y; return (w >> (16 * (i & 1))) & 0xFFFFu; }
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int DPP>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP, 0xF, 0xF, false));
+}
+
+// Max over aligned groups of n lanes (n a power of two <= 64); every lane of
+// a group receives it.  quad_perm xor 1 / xor 2, then row_half_mirror and
+// row_mirror pair each quad / half-row with its partner, then 32 and 64.
+__device__ __forceinline__ float lanes_max(float v, int n) {
+  if (n >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
+  if (n >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
+  if (n >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+  if (n >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+  if (n >= 32) v = fmaxf(v, swz_xor<16>(v));
+  if (n >= 64) v = fmaxf(v, shfl_xor(v, 32));
+  return v;
+}
+
+// The KPLN fp16 scales of one lane, loaded with one coalesced load.
+template <int KPLN> struct LaneScales;
+template <> struct LaneScales<1> {
+  uint32_t w[1];
+  __device__ void load(const uint16_t* p) { w[0] = __builtin_nontemporal_load(p); }
+  __device__ uint32_t get(int) const { return w[0] & 0xFFFFu; }
 };
-template <> struct ScaleVec<8> {
-  using T = uint4;
-  static __device__ uint32_t get(T v, int i) {
-    uint32_t w = (i < 2) ? v.x : (i < 4) ? v.y : (i < 6) ? v.z : v.w;
-    return (w >> (16 * (i & 1))) & 0xFFFFu;
+template <> struct LaneScales<2> {
+  uint32_t w[1];
+  __device__ void load(const uint16_t* p) { w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p)); }
+  __device__ uint32_t get(int i) const { return (w[0] >> (16 * i)) & 0xFFFFu; }
+};
+template <> struct LaneScales<4> {
+  uint32_t w[2];
+  __device__ void load(const uint16_t* p) {
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    w[0] = v.x;
+    w[1] = v.y;
   }
+  __device__ uint32_t get(int i) const { return (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu; }
 };
+template <> struct LaneScales<8> {
+  uint32_t w[4];
+  __device__ void load(const uint16_t* p) {
+    const uint4 v = ld_nt(reinterpret_cast<const uint4*>(p));
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  }
+  __device__ uint32_t get(int i) const { return (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu; }
+};
+
+// Per-row int8 query of decode scoring, computed by one wave: q8[s] =
+// rint(qg[s] / (amax/127)), qg the fp32 sum of the row's G query heads over
+// its channels in head order, amax = max |qg|.  Code dword d of a key holds
+// channels 8d..8d+7 (channel 8d+i in nibble i), so qlo[d] packs the int8
+// query of its even channels and qhi[d] the odd ones; both arrays and *qs
+// come back wave-uniform.
+template <int S>
+__device__ __forceinline__ void row_query_words(const uint16_t* __restrict__ query, int q_heads,
+                                                int kv_heads, int head_dim,
+                                                const int32_t* __restrict__ chan_idx, int r,
+                                                uint32_t (&qlo)[S / 8], uint32_t (&qhi)[S / 8],
+                                                float* qs_out) {
+  const int lane = threadIdx.x & 63;
+  const int G = q_heads / kv_heads;
+  const int b = r / kv_heads, j = r - b * kv_heads;
+  const int32_t* cidx = chan_idx + static_cast<int64_t>(r) * S;
+  const uint32_t* qrow = reinterpret_cast<const uint32_t*>(
+      query + (static_cast<int64_t>(b) * q_heads + j * G) * head_dim);
+  const int hd2 = head_dim / 2;   // channel pairs per head row
+  const int c0 = lane < S ? cidx[lane] : 0;
+  const int c1 = S > 64 ? cidx[lane + 64] : 0;
+  float lo = 0.0f, hi = 0.0f;     // fp32 head sums of channels 2*lane, 2*lane+1
+  if (lane < hd2) {
+    for (int i = 0; i < G; ++i) {
+      const uint32_t w = qrow[i * hd2 + lane];
+      lo = lo + bf16lo(w);
+      hi = hi + bf16hi(w);
+    }
+  }
+  // qg of channel c, read from lane c/2 (ds_bpermute reads only lanes that
+  // execute it, so every lane runs it).
+  auto pick = [&](int c) -> float {
+    c = min(max(c, 0), head_dim - 1);
+    const float vl = __int_as_float(__builtin_amdgcn_ds_bpermute((c >> 1) << 2, __float_as_int(lo)));
+    const float vh = __int_as_float(__builtin_amdgcn_ds_bpermute((c >> 1) << 2, __float_as_int(hi)));
+    return (c & 1) ? vh : vl;
+  };
+  const float p0 = pick(c0);
+  const float qg0 = lane < S ? p0 : 0.0f;
+  const float qg1 = S > 64 ? pick(c1) : 0.0f;
+  const float amax = wave_max(fmaxf(fabsf(qg0), fabsf(qg1)));
+  const float qs = amax / 127.0f;
+  auto q8 = [&](float v) -> int {
+    if (qs == 0.0f) return 0;
+    float t = __builtin_rintf(v / qs);
+    return static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f));
+  };
+  const int q8v0 = q8(qg0), q8v1 = q8(qg1);
+#pragma unroll
+  for (int d = 0; d < S / 8; ++d) {
+    uint32_t lo8 = 0, hi8 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int se = 8 * d + 2 * e, so = se + 1;
+      const int ve = se < 64 ? __builtin_amdgcn_readlane(q8v0, se) : __builtin_amdgcn_readlane(q8v1, se - 64);
+      const int vo = so < 64 ? __builtin_amdgcn_readlane(q8v0, so) : __builtin_amdgcn_readlane(q8v1, so - 64);
+      lo8 |= (static_cast<uint32_t>(ve) & 0xFFu) << (8 * e);
+      hi8 |= (static_cast<uint32_t>(vo) & 0xFFu) << (8 * e);
+    }
+    qlo[d] = lo8;
+    qhi[d] = hi8;
+  }
+  *qs_out = qs;
+}
+
+// The row's query words as a table: qwords[2d] = qlo[d], qwords[2d+1] = qhi[d].
+template <int S>
+__global__ __launch_bounds__(64) void query_words_kernel(
+    const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
+    const int32_t* __restrict__ chan_idx, uint32_t* __restrict__ qwords, float* __restrict__ qscale_out) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  uint32_t qlo[S / 8], qhi[S / 8];
+  float qs;
+  row_query_words<S>(query, q_heads, kv_heads, head_dim, chan_idx, r, qlo, qhi, &qs);
+  uint32_t* out = qwords + static_cast<int64_t>(r) * (S / 4);
+#pragma unroll
+  for (int d = 0; d < S / 8; ++d) {
+    if (lane == 2 * d) out[2 * d] = qlo[d];
+    if (lane == 2 * d + 1) out[2 * d + 1] = qhi[d];
+  }
+  if (qscale_out && lane == 0) qscale_out[r] = qs;
+}
 
 template <int S, bool DEBUG>
 __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
@@ -232,122 +375,112 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
     const uint16_t* __restrict__ slab_scales, int64_t capacity, int tokens, int block,
     int chunk, float* __restrict__ bmax, int nb, int32_t* __restrict__ isum,
     float* __restrict__ keys_out, float* __restrict__ qscale_out) {
-  constexpr int KPL = 128 / S;          // keys per lane
-  constexpr int DW = S / 8;             // code dwords per key
-  constexpr int TILE = 64 * KPL;        // keys per wave tile
-  constexpr int U = QKV_SCORE_UNROLL;   // tiles in flight per wave
-  using SV = ScaleVec<KPL>;
+  constexpr int KPLN = 128 / S;                        // keys per lane per stage
+  constexpr int STAGE = static_cast<int>(slab_tile_keys(S));   // keys per wave stage = 64 * KPLN
+  constexpr int DW = S / 8;                            // code dwords per key
+  using LS = LaneScales<KPLN>;
 
-  __shared__ uint32_t q_lds[2 * DW];   // per code dword: {even-channel bytes, odd-channel bytes}
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int G = q_heads / kv_heads;
-  const int b = r / kv_heads, j = r - b * kv_heads;
 
-  // Prologue (wave 0): q8[s] = rint(qg[s] / (amax/127)), qg = sum of the G heads.
-  if (wave == 0) {
-    float qg0 = 0.0f, qg1 = 0.0f;
-    const int32_t* cidx = chan_idx + static_cast<int64_t>(r) * S;
-    const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * head_dim;
-    if (lane < S) {
-      const int c = min(max(cidx[lane], 0), head_dim - 1);
-      for (int i = 0; i < G; ++i) qg0 = qg0 + bf16_to_f32(qrow[i * head_dim + c]);
-    }
-    if (S > 64) {
-      const int c = min(max(cidx[lane + 64], 0), head_dim - 1);
-      for (int i = 0; i < G; ++i) qg1 = qg1 + bf16_to_f32(qrow[i * head_dim + c]);
-    }
-    const float amax = wave_max(fmaxf(fabsf(qg0), fabsf(qg1)));
-    const float qs = amax / 127.0f;
-    auto q8 = [&](float v) -> int {
-      if (qs == 0.0f) return 0;
-      float t = __builtin_rintf(v / qs);
-      return static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f));
-    };
-    // byte position of channel s: dword 2*(s/8) + (s&1), byte (s%8)/2
-    uint8_t* qb = reinterpret_cast<uint8_t*>(q_lds);
-    if (lane < S) qb[8 * (lane >> 3) + 4 * (lane & 1) + ((lane & 7) >> 1)] = static_cast<uint8_t>(q8(qg0));
-    if (S > 64) {
-      const int s = lane + 64;
-      qb[8 * (s >> 3) + 4 * (s & 1) + ((s & 7) >> 1)] = static_cast<uint8_t>(q8(qg1));
-    }
-    if (qscale_out && blockIdx.x == 0 && lane == 0) qscale_out[r] = qs;
-  }
-  __syncthreads();
+  // Every wave builds the row's query words first and only then starts its
+  // slab stream: the prologue's few loads then meet idle memory queues
+  // instead of waiting behind the CU's slab traffic (measured faster than a
+  // separate per-row kernel, whose launch costs more than the redundancy).
   uint32_t qlo[DW], qhi[DW];
-#pragma unroll
-  for (int d = 0; d < DW; ++d) {
-    qlo[d] = __builtin_amdgcn_readfirstlane(q_lds[2 * d]);
-    qhi[d] = __builtin_amdgcn_readfirstlane(q_lds[2 * d + 1]);
-  }
+  float qs;
+  row_query_words<S>(query, q_heads, kv_heads, head_dim, chan_idx, r, qlo, qhi, &qs);
+  if (qscale_out && blockIdx.x == 0 && wave == 0 && lane == 0) qscale_out[r] = qs;
+  __builtin_amdgcn_sched_barrier(0);
 
   const int64_t row_tok = static_cast<int64_t>(r) * capacity;
-  const uint4* codes = reinterpret_cast<const uint4*>(slab) + row_tok * S / 32;
-  const typename SV::T* scl = reinterpret_cast<const typename SV::T*>(slab_scales + row_tok);
+  const uint4* codes = reinterpret_cast<const uint4*>(slab + row_tok * (S / 2));
+  const uint16_t* scl = slab_scales + row_tok;
   const int t_lo = blockIdx.x * chunk;
   const int t_hi = min(tokens, t_lo + chunk);
-  const float ninf = -__builtin_huge_valf();
-  const int lanes_per_block = block >= KPL ? block / KPL : 1;
 
-  for (int tb = t_lo + wave * TILE * U; tb < t_hi; tb += 4 * TILE * U) {
-    uint4 cw[U][4];
-    typename SV::T sv[U];
+  auto load_stage = [&](int tb, uint4 (&cw)[4], LS& sv) {
+    if (tb + lane * KPLN < t_hi) {
+      const uint4* tile = codes + (static_cast<int64_t>(tb) / STAGE) * 256;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k0 = tb + u * TILE + lane * KPL;
-      if (k0 < t_hi) {
+      for (int i = 0; i < 4; ++i) cw[i] = ld_nt(tile + i * 64 + lane);
+      sv.load(scl + tb + lane * KPLN);
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cw[u][i] = codes[(static_cast<int64_t>(k0) * S) / 32 + i];
-        sv[u] = scl[k0 / KPL];
+      for (int i = 0; i < 4; ++i) cw[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < (KPLN + 1) / 2; ++i) sv.w[i] = 0;
+    }
+  };
+
+  int tb = t_lo + wave * STAGE;
+  uint4 cw[4];
+  LS sv;
+  load_stage(tb, cw, sv);
+
+  const float ninf = -__builtin_huge_valf();
+  // block <= KPLN: each lane writes KPLN / block maxima; else lanes in groups
+  // of blk_lanes share a block and the group's first lane writes it.
+  const int blk_lanes = block > KPLN ? block / KPLN : 1;
+
+  auto score_stage = [&](int tbase, const uint4 (&cwr)[4], const LS& svr) {
+    const uint32_t w[16] = {cwr[0].x, cwr[0].y, cwr[0].z, cwr[0].w, cwr[1].x, cwr[1].y, cwr[1].z, cwr[1].w,
+                            cwr[2].x, cwr[2].y, cwr[2].z, cwr[2].w, cwr[3].x, cwr[3].y, cwr[3].z, cwr[3].w};
+    const int k0 = tbase + lane * KPLN;
+    float key[KPLN];
+#pragma unroll
+    for (int e = 0; e < KPLN; ++e) {
+      int acc = 0;
+#pragma unroll
+      for (int d = 0; d < DW; ++d) {
+        const uint32_t x = w[e * DW + d];
+        acc = __builtin_amdgcn_sdot4(static_cast<int>(qlo[d]), static_cast<int>((x << 4) & 0xF0F0F0F0u), acc, false);
+        acc = __builtin_amdgcn_sdot4(static_cast<int>(qhi[d]), static_cast<int>(x & 0xF0F0F0F0u), acc, false);
+      }
+      const int isc = acc >> 4;   // exact: every term is a multiple of 16
+      float kf = f16bits_to_f32(svr.get(e)) * static_cast<float>(isc);
+      kf = (kf == 0.0f) ? 0.0f : kf;
+      // Keys past this workgroup's range (the row end or the next chunk)
+      // take no part: blocks never straddle chunks, which are whole stages.
+      const int t = k0 + e;
+      if (t >= t_hi) kf = ninf;
+      key[e] = kf;
+      if (DEBUG && t < t_hi) {
+        isum[static_cast<int64_t>(r) * tokens + t] = isc;
+        keys_out[static_cast<int64_t>(r) * tokens + t] = kf;
+      }
+    }
+    if (bmax) {
+      float* brow = bmax + static_cast<int64_t>(r) * nb;
+      if (block <= KPLN) {
+#pragma unroll
+        for (int e0 = 0; e0 < KPLN; e0 += 1) {
+          if (e0 % block) continue;
+          float m = key[e0];
+          for (int e = 1; e < block; ++e) m = fmaxf(m, key[e0 + e]);
+          if (k0 + e0 < t_hi) brow[(k0 + e0) / block] = m;
+        }
       } else {
+        float m = key[0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cw[u][i] = make_uint4(0, 0, 0, 0);
-        sv[u] = typename SV::T{};
+        for (int e = 1; e < KPLN; ++e) m = fmaxf(m, key[e]);
+        m = lanes_max(m, blk_lanes);
+        if ((lane % blk_lanes) == 0 && k0 < t_hi) brow[k0 / block] = m;
       }
     }
+  };
+
+  // Each wave walks its stages with the next stage's loads in flight.
+  while (tb < t_hi) {
+    const int tn = tb + 4 * STAGE;
+    uint4 nw[4];
+    LS nsv;
+    if (tn < t_hi) load_stage(tn, nw, nsv);
+    score_stage(tb, cw, sv);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k0 = tb + u * TILE + lane * KPL;
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(&cw[u][0]);
-      float key[KPL];
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) {
-        int acc = 0;
-#pragma unroll
-        for (int d = 0; d < DW; ++d) {
-          const uint32_t x = w[q * DW + d];
-          acc = __builtin_amdgcn_sdot4(static_cast<int>(qlo[d]), static_cast<int>((x << 4) & 0xF0F0F0F0u), acc, false);
-          acc = __builtin_amdgcn_sdot4(static_cast<int>(qhi[d]), static_cast<int>(x & 0xF0F0F0F0u), acc, false);
-        }
-        const int isc = acc >> 4;   // exact: every term is a multiple of 16
-        float kf = f16bits_to_f32(SV::get(sv[u], q)) * static_cast<float>(isc);
-        kf = (kf == 0.0f) ? 0.0f : kf;
-        // Keys past this workgroup's range (the row end or the next chunk)
-        // take no part: blocks never straddle chunks, which are whole tiles.
-        const int t = k0 + q;
-        if (t >= t_hi) kf = ninf;
-        key[q] = kf;
-        if (DEBUG && t < t_hi) {
-          isum[static_cast<int64_t>(r) * tokens + t] = isc;
-          keys_out[static_cast<int64_t>(r) * tokens + t] = kf;
-        }
-      }
-      if (bmax) {
-        if (block >= KPL) {
-          float m = key[0];
-#pragma unroll
-          for (int q = 1; q < KPL; ++q) m = fmaxf(m, key[q]);
-          for (int msk = 1; msk < lanes_per_block; msk <<= 1) m = fmaxf(m, shfl_xor(m, msk));
-          if ((lane % lanes_per_block) == 0 && k0 < t_hi) bmax[static_cast<int64_t>(r) * nb + k0 / block] = m;
-        } else {
-          for (int q0 = 0; q0 < KPL; q0 += block) {
-            float m = key[q0];
-            for (int q = 1; q < block; ++q) m = fmaxf(m, key[q0 + q]);
-            if (k0 + q0 < t_hi) bmax[static_cast<int64_t>(r) * nb + (k0 + q0) / block] = m;
-          }
-        }
-      }
-    }
+    for (int i = 0; i < 4; ++i) cw[i] = nw[i];
+    sv = nsv;
+    tb = tn;
   }
 }
 
@@ -356,11 +489,11 @@ int launch_scores(int S, dim3 grid, hipStream_t st, const uint16_t* q, int hq, i
                   const int32_t* ci, const uint8_t* slab, const uint16_t* ss, int64_t cap, int T,
                   int block, int chunk, float* bmax, int nb, int32_t* isum, float* keys, float* qs) {
   switch (S) {
-#define QKV_CASE(SS)                                                                         \
-  case SS:                                                                                   \
-    decode_scores_kernel<SS, DEBUG><<<grid, kThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, \
-                                                               cap, T, block, chunk, bmax, nb, \
-                                                               isum, keys, qs);              \
+#define QKV_CASE(SS)                                                                               \
+  case SS:                                                                                         \
+    decode_scores_kernel<SS, DEBUG><<<grid, kThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
+                                                               block, chunk, bmax, nb, isum, keys, \
+                                                               qs);                                \
     break;
     QKV_CASE(16) QKV_CASE(32) QKV_CASE(64) QKV_CASE(128)
 #undef QKV_CASE
@@ -454,8 +587,9 @@ QKV_EXPORT int qkv_int4_build_slab(const void* key, const int64_t* k_strides, in
   if (selected != 16 && selected != 32 && selected != 64 && selected != 128)
     return fail(QKV_ERR_UNSUPPORTED, "qkv_int4_build_slab: selected must be 16, 32, 64 or 128");
   if (selected > head_dim) return fail(QKV_ERR_INVALID, "qkv_int4_build_slab: selected > head_dim");
-  if (capacity % 64 || !aligned(slab, 16) || !aligned(slab_scales, 16))
-    return fail(QKV_ERR_INVALID, "qkv_int4_build_slab: capacity must be a multiple of 64 and outputs 16-byte aligned");
+  if (capacity % slab_tile_keys(static_cast<int>(selected)) || !aligned(slab, 16) || !aligned(slab_scales, 16))
+    return fail(QKV_ERR_INVALID, "qkv_int4_build_slab: capacity must be a multiple of %lld and outputs 16-byte aligned",
+                (long long)slab_tile_keys(static_cast<int>(selected)));
   const int64_t ntok = t_end - t_begin;
   if (ntok == 0) return QKV_OK;
   const int64_t total = batch * kv_heads * ntok * (selected / 8);
@@ -478,46 +612,78 @@ QKV_EXPORT int qkv_int4_build_slab(const void* key, const int64_t* k_strides, in
   return check_launch("qkv_int4_build_slab");
 }
 
+// Shared argument checks of the query side (scoring and query words).
+static int check_query(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                const int32_t* chan_idx, int64_t selected, const char* what) {
+  if (!query || !chan_idx) return fail(QKV_ERR_INVALID, "%s: null query pointer", what);
+  if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads)
+    return fail(QKV_ERR_INVALID, "%s: q_heads must be a multiple of kv_heads", what);
+  if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "%s: too many rows", what);
+  if (head_dim != 64 && head_dim != 128) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128", what);
+  if (selected != 16 && selected != 32 && selected != 64 && selected != 128)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: selected must be 16, 32, 64 or 128", what);
+  if (selected > head_dim) return fail(QKV_ERR_INVALID, "%s: selected > head_dim", what);
+  if (!aligned(query, 4)) return fail(QKV_ERR_INVALID, "%s: query must be 4-byte aligned", what);
+  return QKV_OK;
+}
+
+QKV_EXPORT int qkv_int4_query_words(const void* query, int64_t batch, int64_t q_heads,
+                                    int64_t kv_heads, int64_t head_dim, const int32_t* chan_idx,
+                                    int64_t selected, uint32_t* qwords, float* qscale, void* stream) {
+  if (int rc = check_query(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected, "qkv_int4_query_words"))
+    return rc;
+  if (!qwords) return fail(QKV_ERR_INVALID, "qkv_int4_query_words: null qwords pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>(batch * kv_heads);
+  const uint16_t* q = static_cast<const uint16_t*>(query);
+  const int hq = static_cast<int>(q_heads), hkv = static_cast<int>(kv_heads), hd = static_cast<int>(head_dim);
+  switch (selected) {
+    case 16: query_words_kernel<16><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
+    case 32: query_words_kernel<32><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
+    case 64: query_words_kernel<64><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
+    default: query_words_kernel<128><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
+  }
+  return check_launch("qkv_int4_query_words");
+}
+
 QKV_EXPORT int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads,
                                       int64_t kv_heads, int64_t head_dim, const int32_t* chan_idx,
                                       int64_t selected, const uint8_t* slab,
                                       const uint16_t* slab_scales, int64_t capacity, int64_t tokens,
                                       int64_t block, float* bmax, int32_t* isum, float* keys,
                                       float* qscale, void* stream) {
-  if (!query || !chan_idx || !slab || !slab_scales)
-    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: null input pointer");
+  if (int rc = check_query(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected,
+                           "qkv_int4_decode_scores"))
+    return rc;
+  if (!slab || !slab_scales) return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: null slab pointer");
   if (!bmax && !(isum && keys))
     return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: need bmax or both isum and keys");
   if ((isum == nullptr) != (keys == nullptr))
     return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: isum and keys go together");
-  if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads || q_heads / kv_heads > 64)
-    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: q_heads must be a multiple of kv_heads");
-  if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: too many rows");
-  if (selected != 16 && selected != 32 && selected != 64 && selected != 128)
-    return fail(QKV_ERR_UNSUPPORTED, "qkv_int4_decode_scores: selected must be 16, 32, 64 or 128");
-  if (selected > head_dim) return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: selected > head_dim");
   if (tokens <= 0 || tokens > capacity || tokens >= (int64_t(1) << 30))
     return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: need 1 <= tokens <= capacity");
-  if (capacity % 64 || !aligned(slab, 16) || !aligned(slab_scales, 16))
-    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: capacity must be a multiple of 64 and slab 16-byte aligned");
-  const int kpl = static_cast<int>(128 / selected);
-  if (!pow2(block) || block > 64 * kpl)
-    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: block must be a power of two <= %d", 64 * kpl);
+  if (!aligned(slab, 16) || !aligned(slab_scales, 16))
+    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: slab and scales must be 16-byte aligned");
+  if (capacity % slab_tile_keys(static_cast<int>(selected)))
+    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: capacity must be a multiple of %lld for %lld channels",
+                (long long)slab_tile_keys(static_cast<int>(selected)), (long long)selected);
+  const int stage = static_cast<int>(slab_tile_keys(static_cast<int>(selected)));   // keys per wave stage
+  if (!pow2(block) || block > stage)
+    return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: block must be a power of two <= %d", stage);
   const int64_t rows = batch * kv_heads;
-  const int tile_wg = 4 * 64 * kpl * QKV_SCORE_UNROLL;   // keys one workgroup pass covers
+  const int stage_wg = 4 * stage;   // keys one workgroup stage covers
   int64_t chunk = cdiv(rows * tokens, QKV_SCORE_TARGET_WGS);
-  chunk = std::max<int64_t>(tile_wg, cdiv(chunk, tile_wg) * tile_wg);
+  chunk = std::max<int64_t>(stage_wg, cdiv(chunk, stage_wg) * stage_wg);
   dim3 grid(static_cast<unsigned>(cdiv(tokens, chunk)), static_cast<unsigned>(rows));
   const int nb = static_cast<int>(cdiv(tokens, block));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* q = static_cast<const uint16_t*>(query);
+  const int hq = static_cast<int>(q_heads), hkv = static_cast<int>(kv_heads), hd = static_cast<int>(head_dim);
   if (isum)
-    return launch_scores<true>(static_cast<int>(selected), grid, st, q, static_cast<int>(q_heads),
-                               static_cast<int>(kv_heads), static_cast<int>(head_dim), chan_idx, slab,
-                               slab_scales, capacity, static_cast<int>(tokens), static_cast<int>(block),
+    return launch_scores<true>(static_cast<int>(selected), grid, st, q, hq, hkv, hd, chan_idx, slab, slab_scales,
+                               capacity, static_cast<int>(tokens), static_cast<int>(block),
                                static_cast<int>(chunk), bmax, nb, isum, keys, qscale);
-  return launch_scores<false>(static_cast<int>(selected), grid, st, q, static_cast<int>(q_heads),
-                              static_cast<int>(kv_heads), static_cast<int>(head_dim), chan_idx, slab,
-                              slab_scales, capacity, static_cast<int>(tokens), static_cast<int>(block),
+  return launch_scores<false>(static_cast<int>(selected), grid, st, q, hq, hkv, hd, chan_idx, slab, slab_scales,
+                              capacity, static_cast<int>(tokens), static_cast<int>(block),
                               static_cast<int>(chunk), bmax, nb, nullptr, nullptr, qscale);
 }

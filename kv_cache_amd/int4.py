@@ -7,9 +7,11 @@ limit3_ppl.py:4400-4502 and 5008-5097):
 1. ``int4_pack_k``      -- K bf16 -> symmetric int4, fp16 scale per group.
 2. ``select_channels``  -- per KV head, the S channels of largest mean |K|.
 3. ``build_slab``       -- those S channels re-quantized as one int4 group:
-                           the S/2 + 2 bytes per token that decode scoring streams.
+                           the S/2 + 2 bytes per token that decode scoring streams
+                           (codes swizzled in 4 KiB tiles, scales in key order).
 4. ``decode_scores``    -- GQA-summed int8 query . int4 slab -> int32, ranking
-                           key fp32(scale) * I, max-pooled per block.
+                           key fp32(scale) * I, max-pooled per block
+                           (``query_words`` exposes the int8 query alone).
 5. ``block_topk``       -- top-k blocks, lowest index wins ties, ascending.
 6. ``sparse_attention`` -- every query head of a KV head attends over the
                            selected blocks of bf16 K/V.
@@ -17,7 +19,9 @@ limit3_ppl.py:4400-4502 and 5008-5097):
 All tensors live on the GPU; every function launches on the current stream
 and raises ``RuntimeError`` on bad input or a missing library (there is no
 CPU fallback).  Layouts: K/V [B, Hkv, T, D] bf16 with contiguous channels;
-packed/slab tensors [B, Hkv, capacity, ...] with capacity a multiple of 64.
+packed/slab tensors [B, Hkv, capacity, ...] with capacity a multiple of 512
+(the slab's [B, Hkv, capacity, S/2] bytes hold the swizzled tile layout, so
+the per-key view of it is not meaningful without un-swizzling).
 """
 
 from __future__ import annotations
@@ -28,7 +32,9 @@ import torch
 
 from . import _lib
 
-CAPACITY_MULTIPLE = 64
+# Token capacity of packed K / slab buffers: a multiple of the largest slab
+# tile (8192/S keys at S = 16), so one capacity serves every channel count.
+CAPACITY_MULTIPLE = 512
 
 
 def round_capacity(tokens: int) -> int:
@@ -113,6 +119,26 @@ def build_slab(key: torch.Tensor, chan_idx: torch.Tensor, *, capacity: int | Non
     return slab, slab_scales
 
 
+def query_words(query: torch.Tensor, chan_idx: torch.Tensor, *, qwords: torch.Tensor | None = None,
+                qscale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Per-row int8 query of decode scoring: (qwords int32 [B,Hkv,S/4] holding
+    the packed uint32 words, qscale f32 [B,Hkv] or None)."""
+    lib = _lib.load()
+    _require(query.is_cuda and query.dtype == torch.bfloat16 and query.dim() == 3, "query must be CUDA bf16 [B,Hq,D]")
+    q = query.contiguous()
+    b, hq, d = q.shape
+    _require(chan_idx.dtype == torch.int32 and chan_idx.is_contiguous() and chan_idx.dim() == 3,
+             "chan_idx must be contiguous int32 [B,Hkv,S]")
+    hkv, s = chan_idx.size(1), chan_idx.size(2)
+    _require(chan_idx.size(0) == b, "chan_idx batch mismatch")
+    if qwords is None:
+        qwords = torch.empty((b, hkv, s // 4), dtype=torch.int32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_int4_query_words(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s,
+                                            qwords.data_ptr(), _lib.ptr(qscale), _lib.stream_of(q)))
+    return qwords, qscale
+
+
 def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tensor,
                   slab_scales: torch.Tensor, tokens: int, block: int, *,
                   bmax: torch.Tensor | None = None, debug: bool = False):
@@ -123,11 +149,13 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
     [B,Hkv,T], qscale f32 [B,Hkv])."""
     lib = _lib.load()
     _require(query.is_cuda and query.dtype == torch.bfloat16 and query.dim() == 3, "query must be CUDA bf16 [B,Hq,D]")
+    _require(slab.is_cuda and slab.dtype == torch.uint8 and slab.is_contiguous(), "slab must be contiguous CUDA uint8")
     q = query.contiguous()
     b, hq, d = q.shape
     _, hkv, cap, half = slab.shape
     s = half * 2
-    _require(tuple(chan_idx.shape) == (b, hkv, s), "chan_idx shape mismatch")
+    _require(tuple(chan_idx.shape) == (b, hkv, s) and chan_idx.dtype == torch.int32 and chan_idx.is_contiguous(),
+             "chan_idx must be contiguous int32 [B,Hkv,S]")
     nb = -(-int(tokens) // int(block))
     if bmax is None:
         bmax = torch.empty((b, hkv, nb), dtype=torch.float32, device=q.device)
@@ -169,6 +197,14 @@ def attention_workspace_bytes(batch: int, q_heads: int, kv_heads: int, head_dim:
     return int(n)
 
 
+def attention_workspace(batch: int, q_heads: int, kv_heads: int, head_dim: int, n_sel: int, block: int,
+                        device) -> torch.Tensor:
+    """Workspace for ``sparse_attention`` calls up to these sizes (split
+    partials; calls sharing one must not overlap in time)."""
+    need = attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block)
+    return torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
+
+
 def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                      block_ids: torch.Tensor, block: int, tokens: int, scaling: float, *,
                      workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -185,7 +221,7 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     n = block_ids.size(-1)
     need = attention_workspace_bytes(b, hq, hkv, d, n, block)
     if workspace is None:
-        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
+        workspace = attention_workspace(b, hq, hkv, d, n, block, q.device)
     if out is None:
         out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
     with torch.cuda.device(q.device):
@@ -243,8 +279,7 @@ class SparseDecodeStep:
         _require(1 <= topk <= nb, f"topk {topk} must be in [1, {nb}]")
         self.bmax = torch.empty((batch, kv_heads, nb), dtype=torch.float32, device=device)
         self.sel = torch.empty((batch, kv_heads, topk), dtype=torch.int32, device=device)
-        need = attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, topk, block)
-        self.workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
+        self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, topk, block, device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
 
     def __call__(self, query: torch.Tensor, cache: Int4KCache, key: torch.Tensor, value: torch.Tensor,

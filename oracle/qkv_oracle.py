@@ -160,9 +160,11 @@ def build_slab(k, chan_idx) -> tuple[np.ndarray, np.ndarray]:
     int4 group of S channels.
 
     k: [R, T, D] (bf16-exact f32); chan_idx: int32 [R, S] ascending.
-    Returns (slab uint8 [R, T, S/2], slab scale bits uint16 [R, T]).
-    The reference keeps a transposed bf16 copy of K for its scoring kernel
-    (EV:2018-2042); this is the int4 analogue with the channel gather folded in.
+    Returns (slab uint8 [R, T, S/2], slab scale bits uint16 [R, T]) in logical
+    key order; the device stores the codes swizzled (``swizzle_slab``) and the
+    scales in key order.  The reference keeps a transposed bf16 copy of K for
+    its scoring kernel (EV:2018-2042); this is the int4 analogue with the
+    channel gather folded in.
     """
     k = _f32(k)
     idx = np.asarray(chan_idx, dtype=np.int64)
@@ -170,6 +172,56 @@ def build_slab(k, chan_idx) -> tuple[np.ndarray, np.ndarray]:
     s = gathered.shape[-1]
     codes, scale_bits = quantize_int4(gathered, s)
     return pack_int4(codes), scale_bits[..., 0]
+
+
+def slab_tile_keys(selected: int) -> int:
+    """Keys per 4096-byte slab tile: 64 lanes x 64 bytes of S/2-byte codes."""
+    return 8192 // selected
+
+
+def slab_storage_offset(t, x, selected: int):
+    """Storage byte offset, within a row's slab, of logical code byte ``x`` of
+    key ``t`` (the swizzle that lets a 64-lane wave read whole keys per lane
+    with coalesced 16-byte loads).
+
+    Tile = t // (8192/S); lane = (t % (8192/S)) // (128/S) owns 128/S
+    consecutive keys = 64 logical bytes; its logical byte b = (t % (128/S)) *
+    S/2 + x is stored at tile * 4096 + (64 * (b // 16) + lane) * 16 + b % 16.
+    """
+    t = np.asarray(t, dtype=np.int64)
+    x = np.asarray(x, dtype=np.int64)
+    kpln = 128 // selected
+    tk = slab_tile_keys(selected)
+    tile, k = np.divmod(t, tk)
+    lane, e = np.divmod(k, kpln)
+    b = e * (selected // 2) + x
+    return tile * 4096 + (64 * (b // 16) + lane) * 16 + b % 16
+
+
+def swizzle_slab(slab, capacity: int) -> np.ndarray:
+    """Logical slab uint8 [R, T, S/2] -> stored bytes uint8 [R, capacity * S/2]
+    (positions past T stay zero); capacity is a multiple of the tile."""
+    slab = np.asarray(slab, dtype=np.uint8)
+    r, t, half = slab.shape
+    sel = 2 * half
+    if capacity % slab_tile_keys(sel) or capacity < t:
+        raise ValueError("capacity must be a multiple of the slab tile and hold every key")
+    out = np.zeros((r, capacity * half), dtype=np.uint8)
+    tt, xx = np.meshgrid(np.arange(t), np.arange(half), indexing="ij")
+    off = slab_storage_offset(tt, xx, sel)
+    out[:, off.reshape(-1)] = slab.reshape(r, -1)
+    return out
+
+
+def unswizzle_slab(stored, selected: int, tokens: int) -> np.ndarray:
+    """Inverse of ``swizzle_slab``: stored bytes [R, >= cap * S/2] -> [R, T, S/2]."""
+    stored = np.asarray(stored, dtype=np.uint8)
+    r = stored.shape[0]
+    flat = stored.reshape(r, -1)
+    half = selected // 2
+    tt, xx = np.meshgrid(np.arange(tokens), np.arange(half), indexing="ij")
+    off = slab_storage_offset(tt, xx, selected)
+    return flat[:, off.reshape(-1)].reshape(r, tokens, half)
 
 
 # ---------------------------------------------------------------------------
@@ -201,6 +253,17 @@ def quantize_query_group(q, chan_idx, kv_heads: int) -> tuple[np.ndarray, np.nda
     q8 = np.clip(np.rint(acc / safe[..., None]), -Q8_MAX, Q8_MAX)
     q8 = np.where(qscale[..., None] == 0, np.float32(0.0), q8)
     return q8.astype(np.int8).reshape(b * kv_heads, -1), qscale.reshape(-1)
+
+
+def pack_query_words(q8) -> np.ndarray:
+    """int8 query [R, S] -> uint32 words [R, S/4] in the order the int4 code
+    dwords pair with: word 2d holds channels 8d, 8d+2, 8d+4, 8d+6 (bytes 0..3),
+    word 2d+1 channels 8d+1, 8d+3, 8d+5, 8d+7."""
+    q = np.asarray(q8, dtype=np.int8).view(np.uint8)
+    r, s = q.shape
+    g = q.reshape(r, s // 8, 4, 2)                            # [R, d, pair, parity]
+    ordered = np.ascontiguousarray(g.transpose(0, 1, 3, 2))   # [R, d, parity, pair]
+    return ordered.reshape(r, s).view("<u4").reshape(r, s // 4)
 
 
 def partial_scores_i32(q8, slab) -> np.ndarray:

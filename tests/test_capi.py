@@ -36,14 +36,24 @@ def _err():
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
                                         ctypes.c_void_p(16), None, None, None, None), "selected must be"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
-                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4000, 4000, 16,
-                                        ctypes.c_void_p(16), None, None, None, None), "multiple of 64"),
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4032, 4000, 16,
+                                        ctypes.c_void_p(16), None, None, None, None), "multiple of 256"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 12,
                                         ctypes.c_void_p(16), None, None, None, None), "power of two"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 64,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 256,
+                                        ctypes.c_void_p(16), None, None, None, None), "<= 128"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
+                                        None, None, None, None, None), "need bmax"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 15, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
                                         ctypes.c_void_p(16), None, None, None, None), "multiple of kv_heads"),
+    (lambda: lib.qkv_int4_query_words(ctypes.c_void_p(16), 1, 15, 8, 128, ctypes.c_void_p(16), 32,
+                                      ctypes.c_void_p(16), None, None), "multiple of kv_heads"),
+    (lambda: lib.qkv_int4_query_words(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 48,
+                                      ctypes.c_void_p(16), None, None), "selected must be"),
     (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 48,
                                  ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "group"),
     (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 100, 128, 32,
@@ -69,9 +79,12 @@ def test_host_side_validation(call, msg):
 
 
 def test_workspace_size_formula():
-    # rows * splits * G * (D + 2) floats; splits = ceil(n_sel / (256 // block))
-    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * 64 * 8 * 2 * 130
-    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * 8 * 1 * 2 * 130
+    # rows * splits * G * (D + 2) floats;
+    # splits = ceil(n_sel * block / slots), slots = 256 token slots (128 at G = 8)
+    t = 0
+    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * (t + 64 * 8 * 2 * 130)
+    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * (t + 8 * 1 * 2 * 130)
+    assert lib.qkv_sparse_attention_workspace_bytes(1, 64, 8, 128, 300, 1) == 4 * (t + 8 * 3 * 8 * 130)
     assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 64, 256, 1) == -1
 
 

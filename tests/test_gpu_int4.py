@@ -106,9 +106,15 @@ def test_slab_matches_oracle(count):
     g = torch.Generator().manual_seed(count)
     chan = torch.stack([torch.randperm(128, generator=g)[:count].sort().values for _ in range(3)])
     chan = chan.view(1, 3, count).to(torch.int32).to(DEV)
-    slab, ss = K.build_slab(key, chan)
+    cap = K.round_capacity(513)
+    slab = torch.zeros((1, 3, cap, count // 2), dtype=torch.uint8, device=DEV)
+    ss = torch.zeros((1, 3, cap), dtype=torch.float16, device=DEV)
+    K.build_slab(key, chan, slab=slab, slab_scales=ss)
     want, want_s = O.build_slab(f32(key).reshape(3, 513, 128), chan.cpu().numpy().reshape(3, count))
-    assert np.array_equal(slab[:, :, :513].cpu().numpy().reshape(3, 513, count // 2), want)
+    stored = slab.cpu().numpy().reshape(3, -1)
+    assert np.array_equal(O.unswizzle_slab(stored, count, 513), want)
+    # the stored bytes are exactly the oracle's swizzled slab (padding untouched)
+    assert np.array_equal(stored, O.swizzle_slab(want, slab.size(2)))
     assert np.array_equal(bits16(ss[:, :, :513]).reshape(3, 513), want_s)
 
 
@@ -125,7 +131,7 @@ def _score_case(b, hq, hkv, t, count, block, seed):
     bmax_only = K.decode_scores(q, cache.chan_idx, cache.slab, cache.slab_scales, t, block)
     rows = b * hkv
     chan = cache.chan_idx.cpu().numpy().reshape(rows, count)
-    slab = cache.slab[:, :, :t].cpu().numpy().reshape(rows, t, count // 2)
+    slab = O.unswizzle_slab(cache.slab.cpu().numpy().reshape(rows, -1), count, t)
     sbits = bits16(cache.slab_scales[:, :, :t]).reshape(rows, t)
     q8, want_qs = O.quantize_query_group(f32(q), chan, hkv)
     want_i = O.partial_scores_i32(q8, slab)
@@ -137,6 +143,20 @@ def _score_case(b, hq, hkv, t, count, block, seed):
     assert np.array_equal(bmax.cpu().numpy().reshape(rows, -1), want_b)
     assert np.array_equal(bmax_only.cpu().numpy().reshape(rows, -1), want_b)
     return want_b
+
+
+@pytest.mark.parametrize("count", [16, 32, 64, 128])
+def test_query_words_match_oracle(count):
+    g = torch.Generator().manual_seed(count)
+    b, hq, hkv = 2, 16, 4
+    q = torch.randn((b, hq, 128), generator=g).to(torch.bfloat16)
+    chan = torch.stack([torch.randperm(128, generator=g)[:count].sort().values for _ in range(b * hkv)])
+    chan = chan.view(b, hkv, count).to(torch.int32)
+    words, qs = K.query_words(q.to(DEV), chan.to(DEV), qscale=torch.empty((b, hkv), device=DEV))
+    q8, want_qs = O.quantize_query_group(f32(q), chan.numpy().reshape(b * hkv, count), hkv)
+    got = words.cpu().numpy().reshape(b * hkv, count // 4).view(np.uint32)
+    assert np.array_equal(got, O.pack_query_words(q8))
+    assert np.array_equal(qs.cpu().numpy().reshape(-1), want_qs)
 
 
 @pytest.mark.parametrize("count", [16, 32, 64, 128])
@@ -201,6 +221,24 @@ def test_sparse_attention_matches_fp64(g_size, block, nsel):
     out = K.sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), sel.to(DEV), block, t, 128 ** -0.5)
     want = O.sparse_attention(f32(q), f32(k), f32(v), sel.numpy(), block, t, 128 ** -0.5)
     assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+
+
+def test_sparse_attention_workspace_reuse():
+    # One workspace serves successive calls with different split counts.
+    gen = torch.Generator().manual_seed(9)
+    b, hkv, g_size, t = 2, 4, 2, 5000
+    q = torch.randn((b, hkv * g_size, 128), generator=gen).to(torch.bfloat16)
+    k = torch.randn((b, hkv, t, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((b, hkv, t, 128), generator=gen).to(torch.bfloat16)
+    ws = K.attention_workspace(b, hkv * g_size, hkv, 128, 313, 16, DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    for nsel, block in [(313, 16), (40, 16), (200, 1), (313, 16), (700, 1), (16, 16), (99, 16)]:
+        nb = -(-t // block)
+        sel = torch.stack([torch.randperm(nb, generator=gen)[:nsel].sort().values for _ in range(b * hkv)])
+        sel = sel.view(b, hkv, nsel).to(torch.int32)
+        out = K.sparse_attention(qd, kd, vd, sel.to(DEV), block, t, 0.088, workspace=ws)
+        want = O.sparse_attention(f32(q), f32(k), f32(v), sel.numpy(), block, t, 0.088)
+        assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL), (nsel, block)
 
 
 def test_sparse_attention_no_valid_block_gives_zero():

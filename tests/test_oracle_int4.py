@@ -360,3 +360,54 @@ def test_pack_roundtrip_groups(group):
     deq = O.dequantize_int4(packed, scale, group)
     s = np.repeat(O.fp16_bits_to_f32(scale), group, axis=-1)
     assert np.all(np.abs(deq - k) <= 0.5 * s * (1 + 2 ** -9))
+
+
+# ---------------------------------------------------------------------------
+# slab storage swizzle
+# ---------------------------------------------------------------------------
+
+def test_slab_swizzle_known_positions():
+    # S = 32: 4 keys of 16 bytes per lane; lane l owns keys 4l..4l+3
+    off = lambda t, x: int(O.slab_storage_offset(t, x, 32))  # noqa: E731
+    assert [off(0, x) for x in (0, 15)] == [0, 15]
+    assert off(1, 0) == 1024          # key 1 = lane 0's second 16-byte chunk
+    assert off(4, 3) == 16 + 3        # key 4 = lane 1's first chunk
+    assert off(255, 15) == (64 * 3 + 63) * 16 + 15
+    assert off(256, 0) == 4096        # next tile
+    # S = 128: one key of 64 bytes per lane
+    assert int(O.slab_storage_offset(5, 17, 128)) == (64 * 1 + 5) * 16 + 1
+    # S = 16: 8 keys of 8 bytes per lane
+    assert int(O.slab_storage_offset(9, 2, 16)) == (64 * 0 + 1) * 16 + 8 + 2
+
+
+@pytest.mark.parametrize("sel", [16, 32, 64, 128])
+def test_slab_swizzle_is_a_permutation_per_tile(sel):
+    cap = O.slab_tile_keys(sel) * 2
+    t, x = np.meshgrid(np.arange(cap), np.arange(sel // 2), indexing="ij")
+    off = O.slab_storage_offset(t, x, sel).reshape(-1)
+    assert np.array_equal(np.sort(off), np.arange(cap * sel // 2))
+    # each lane's four loads of one tile are 16-byte chunks 64j + l
+    k = np.arange(O.slab_tile_keys(sel))
+    first = O.slab_storage_offset(k, 0, sel) // 16
+    assert np.array_equal(np.unique(first % 64), np.arange(64))
+
+
+@pytest.mark.parametrize("sel", [16, 32, 64, 128])
+def test_slab_swizzle_round_trip(sel):
+    rng = np.random.default_rng(sel)
+    t = 777
+    cap = -(-t // 512) * 512
+    slab = rng.integers(0, 256, size=(3, t, sel // 2), dtype=np.uint8)
+    stored = O.swizzle_slab(slab, cap)
+    assert stored.shape == (3, cap * sel // 2)
+    assert np.array_equal(O.unswizzle_slab(stored, sel, t), slab)
+    assert int(stored.astype(np.int64).sum()) == int(slab.astype(np.int64).sum())
+
+
+def test_pack_query_words_layout():
+    q8 = np.arange(-8, 8, dtype=np.int8).reshape(1, 16)        # channel c holds c - 8
+    w = O.pack_query_words(q8)
+    assert w.shape == (1, 4) and w.dtype == np.uint32
+    b = w.view(np.uint8).view(np.int8).reshape(-1).tolist()
+    # word 0: even channels 0,2,4,6; word 1: odd channels 1,3,5,7; then 8..15
+    assert b == [-8, -6, -4, -2, -7, -5, -3, -1, 0, 2, 4, 6, 1, 3, 5, 7]
