@@ -37,6 +37,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte load with the non-temporal hint: K/V rows are read once per step.
+__device__ __forceinline__ uint4 ld_nt(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
                                          false);
@@ -101,12 +109,12 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     kx[i] = make_uint4(0, 0, 0, 0);
-    if (tok[i] >= 0) kx[i] = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(tok[i]) * st);
+    if (tok[i] >= 0) kx[i] = ld_nt(kb + static_cast<int64_t>(tok[i]) * st);
   }
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     vx[i] = make_uint4(0, 0, 0, 0);
-    if (tok[i] >= 0) vx[i] = *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(tok[i]) * st);
+    if (tok[i] >= 0) vx[i] = ld_nt(vb + static_cast<int64_t>(tok[i]) * st);
   }
   uint4 qx[G];
   const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * kD + cc * 8;
@@ -232,30 +240,47 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
 }
 
 // Merges the split partials of one row: thread (h, d) rescales every split's
-// weighted V by 2^(m_i - max) and divides by the rescaled sum.
+// weighted V by 2^(m_i - max) and divides by the rescaled sum.  Splits are
+// taken MS at a time with all their loads issued before any arithmetic.
 template <int G>
 __global__ __launch_bounds__(G * kD) void sparse_attn_merge_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml, int nsplit, int q_heads,
     int kv_heads, uint16_t* __restrict__ out) {
+  constexpr int MS = 8;
   const int r = blockIdx.x, idx = threadIdx.x, h = idx / kD;
   const int b = r / kv_heads, j = r - b * kv_heads;
   const float ninf = -__builtin_huge_valf();
   const float* ml = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2 + h * 2;
   const float* pa = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD + idx;
-  float mx = ninf;
-  for (int i = 0; i < nsplit; ++i) mx = fmaxf(mx, ml[i * G * 2]);
-  float o = 0.0f;
-  if (mx != ninf) {
-    float den = 0.0f;
-#pragma unroll 8
-    for (int i = 0; i < nsplit; ++i) {
-      const float mi = ml[i * G * 2];
-      const float w = (mi == ninf) ? 0.0f : exp2f(mi - mx);
-      den = __builtin_fmaf(ml[i * G * 2 + 1], w, den);
-      o = __builtin_fmaf(pa[static_cast<int64_t>(i) * G * kD], w, o);
+  float mx = ninf, den = 0.0f, o = 0.0f;   // running max, rescaled sum and output
+  for (int i0 = 0; i0 < nsplit; i0 += MS) {
+    float mi[MS], li[MS], ai[MS];
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      const int i = min(i0 + u, nsplit - 1);
+      mi[u] = ml[i * G * 2];
+      li[u] = ml[i * G * 2 + 1];
+      ai[u] = pa[static_cast<int64_t>(i) * G * kD];
     }
-    o = o / den;
+    float m2 = mx;
+#pragma unroll
+    for (int u = 0; u < MS; ++u)
+      if (i0 + u < nsplit) m2 = fmaxf(m2, mi[u]);
+    if (m2 == ninf) continue;
+    const float c = (mx == ninf) ? 0.0f : exp2f(mx - m2);
+    den *= c;
+    o *= c;
+#pragma unroll
+    for (int u = 0; u < MS; ++u) {
+      if (i0 + u < nsplit && mi[u] != ninf) {
+        const float w = exp2f(mi[u] - m2);
+        den = __builtin_fmaf(li[u], w, den);
+        o = __builtin_fmaf(ai[u], w, o);
+      }
+    }
+    mx = m2;
   }
+  o = (mx == ninf) ? 0.0f : o / den;
   out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(o);
 }
 
