@@ -164,9 +164,9 @@ int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, in
 int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
              int32_t* out, void* stream);
 
-/* Bytes of f32 workspace qkv_sparse_attention needs for these sizes (the
- * per-split partials: G*(D+2) floats per split of 256 token slots, 128 at
- * G = 8). */
+/* Bytes of workspace qkv_sparse_attention needs for these sizes: 65536
+ * uint32 row tickets (the same words for every call shape), then G*(D+2)
+ * floats per split of 128 token slots. */
 int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                              int64_t head_dim, int64_t n_sel, int64_t block);
 
@@ -179,8 +179,10 @@ int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int
  * tokens [id*block, min(tokens,(id+1)*block)).  Every query head of a row
  * attends, with softmax(scaling * q.k), over the union of the row's blocks.
  * out bf16 [B,Hq,D]; a head with no valid token gets zeros (QK:388, 404).
- * D must be 128.  Rows of more than one split are merged by a second kernel
- * on the same stream.  Calls sharing a workspace must not overlap in time. */
+ * D must be 128.  One launch: the last workgroup of each row merges the
+ * row's split partials.  The workspace's ticket words must be zero before
+ * the first call that uses it (allocate it zero-filled); each completed call
+ * leaves them zero.  Calls sharing a workspace must not overlap in time. */
 int qkv_sparse_attention(const void* query, const void* key, const void* value,
                          const int64_t* kv_strides, int64_t batch, int64_t q_heads,
                          int64_t kv_heads, int64_t tokens, int64_t head_dim,

@@ -16,10 +16,13 @@
 // channel pairs followed by a 16-lane DPP reduction; softmax runs in the log2
 // domain; P.V accumulates in fp32.  Each workgroup reduces its waves through
 // LDS into (max, sum, weighted V) per head.  A row that fits one workgroup
-// writes its bf16 output directly; otherwise the partials go to the workspace
-// and a second, small kernel merges them.  (An in-kernel last-arriver merge
-// would need an agent-scope fence per workgroup, which on gfx950 writes back
-// and invalidates the XCD's whole L2: measured several times slower.)
+// writes its bf16 output directly.  Otherwise every workgroup publishes its
+// partial with device-coherent stores (relaxed agent-scope atomic stores:
+// global_store sc1, written through the XCD's L2), waits for them to
+// complete, and takes a ticket; the row's last workgroup reads the partials
+// back with device-coherent loads (sc1) and writes the output.  No release /
+// acquire fence is used: on gfx950 those write back and invalidate the whole
+// L2 of the XCD (buffer_wbl2 / buffer_inv), which measured 3x slower here.
 #include "common.h"
 
 namespace qkv {
@@ -27,6 +30,16 @@ namespace {
 
 constexpr int kD = 128;     // head dim
 constexpr int kNT = 256;    // threads per workgroup
+// Ticket words at the start of the workspace, one per possible row, so calls
+// of any shape that share a workspace find their tickets at the same place.
+constexpr int64_t kTicketWords = 65536;
+
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -72,13 +85,14 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
     int kv_heads, int64_t tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
     int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    uint16_t* __restrict__ out) {
+    uint32_t* __restrict__ tickets, uint16_t* __restrict__ out) {
   constexpr int SLOTS_W = 4 * NI;          // token slots per wave
   constexpr int SLOTS_WG = 4 * SLOTS_W;    // token slots per workgroup
   static_assert(SLOTS_W <= 64, "one slot per lane when resolving token ids");
 
   __shared__ float red_acc[4][G][kD];   // per wave weighted V
   __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ int last_flag;
 
   const int r = blockIdx.y, split = blockIdx.x;
   const int b = r / kv_heads, j = r - b * kv_heads;
@@ -231,61 +245,66 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
   const int64_t part = static_cast<int64_t>(r) * nsplit + split;
   for (int idx = tid; idx < G * kD; idx += kNT) {
     const int h = idx / kD, d = idx - h * kD;
-    ws_acc[part * G * kD + idx] = wg_acc(h, d);
+    st_coherent(ws_acc + part * G * kD + idx, wg_acc(h, d));
   }
   if (tid < G) {
-    ws_ml[(part * G + tid) * 2 + 0] = wg_m[tid];
-    ws_ml[(part * G + tid) * 2 + 1] = wg_l[tid];
+    st_coherent(ws_ml + (part * G + tid) * 2 + 0, wg_m[tid]);
+    st_coherent(ws_ml + (part * G + tid) * 2 + 1, wg_l[tid]);
   }
-}
+  // Every store of this workgroup has completed before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t t = __hip_atomic_fetch_add(tickets + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = t == static_cast<uint32_t>(nsplit - 1);
+    if (last) __hip_atomic_store(tickets + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = last;
+  }
+  __syncthreads();
+  if (!last_flag) return;
 
-// Merges the split partials of one row: thread (h, d) rescales every split's
-// weighted V by 2^(m_i - max) and divides by the rescaled sum.  Splits are
-// taken MS at a time with all their loads issued before any arithmetic.
-template <int G>
-__global__ __launch_bounds__(G * kD) void sparse_attn_merge_kernel(
-    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml, int nsplit, int q_heads,
-    int kv_heads, uint16_t* __restrict__ out) {
+  // Last workgroup of the row: merge the splits, MS at a time with every load
+  // in flight before any arithmetic.
   constexpr int MS = 8;
-  const int r = blockIdx.x, idx = threadIdx.x, h = idx / kD;
-  const int b = r / kv_heads, j = r - b * kv_heads;
-  const float ninf = -__builtin_huge_valf();
-  const float* ml = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2 + h * 2;
-  const float* pa = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD + idx;
-  float mx = ninf, den = 0.0f, o = 0.0f;   // running max, rescaled sum and output
-  for (int i0 = 0; i0 < nsplit; i0 += MS) {
-    float mi[MS], li[MS], ai[MS];
+  for (int idx = tid; idx < G * kD; idx += kNT) {
+    const int h = idx / kD;
+    const float* ml = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2 + h * 2;
+    const float* pa = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD + idx;
+    float mx = ninf, den = 0.0f, o = 0.0f;
+    for (int i0 = 0; i0 < nsplit; i0 += MS) {
+      float mi[MS], li[MS], ai[MS];
 #pragma unroll
-    for (int u = 0; u < MS; ++u) {
-      const int i = min(i0 + u, nsplit - 1);
-      mi[u] = ml[i * G * 2];
-      li[u] = ml[i * G * 2 + 1];
-      ai[u] = pa[static_cast<int64_t>(i) * G * kD];
-    }
-    float m2 = mx;
-#pragma unroll
-    for (int u = 0; u < MS; ++u)
-      if (i0 + u < nsplit) m2 = fmaxf(m2, mi[u]);
-    if (m2 == ninf) continue;
-    const float c = (mx == ninf) ? 0.0f : exp2f(mx - m2);
-    den *= c;
-    o *= c;
-#pragma unroll
-    for (int u = 0; u < MS; ++u) {
-      if (i0 + u < nsplit && mi[u] != ninf) {
-        const float w = exp2f(mi[u] - m2);
-        den = __builtin_fmaf(li[u], w, den);
-        o = __builtin_fmaf(ai[u], w, o);
+      for (int u = 0; u < MS; ++u) {
+        const int i = min(i0 + u, nsplit - 1);
+        mi[u] = ld_coherent(ml + i * G * 2);
+        li[u] = ld_coherent(ml + i * G * 2 + 1);
+        ai[u] = ld_coherent(pa + static_cast<int64_t>(i) * G * kD);
       }
+      float m2 = mx;
+#pragma unroll
+      for (int u = 0; u < MS; ++u)
+        if (i0 + u < nsplit) m2 = fmaxf(m2, mi[u]);
+      if (m2 == ninf) continue;
+      const float c = (mx == ninf) ? 0.0f : exp2f(mx - m2);
+      den *= c;
+      o *= c;
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        if (i0 + u < nsplit && mi[u] != ninf) {
+          const float w = exp2f(mi[u] - m2);
+          den = __builtin_fmaf(li[u], w, den);
+          o = __builtin_fmaf(ai[u], w, o);
+        }
+      }
+      mx = m2;
     }
-    mx = m2;
+    o = (mx == ninf) ? 0.0f : o / den;
+    out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(o);
   }
-  o = (mx == ninf) ? 0.0f : o / den;
-  out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(o);
 }
 
-// Token slots per workgroup for a group size (fewer for G = 8 to bound registers).
-constexpr int ni_for(int64_t g) { return g >= 8 ? 8 : 16; }
+// Token slots per wave / 4 (128 slots per workgroup: measured faster than 256 at cfg2).
+constexpr int ni_for(int64_t g) { return 8; }
 
 int64_t splits_for(int64_t n_sel, int64_t block, int64_t g) {
   return cdiv(n_sel * block, 16 * ni_for(g));
@@ -304,8 +323,8 @@ QKV_EXPORT int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q
     return -1;
   const int64_t g = q_heads / kv_heads;
   const int64_t rows = batch * kv_heads;
-  // per split: weighted V per head, then (max, sum) per head
-  return 4 * rows * splits_for(n_sel, block, g) * g * (kD + 2);
+  // tickets, then per split: weighted V per head, then (max, sum) per head
+  return 4 * (kTicketWords + rows * splits_for(n_sel, block, g) * g * (kD + 2));
 }
 
 QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const void* value,
@@ -336,7 +355,8 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   const int64_t rows = batch * kv_heads;
   const int64_t nsplit = splits_for(n_sel, block, g);
   if (nsplit > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many selected blocks");
-  float* ws_acc = workspace;
+  uint32_t* tickets = reinterpret_cast<uint32_t*>(workspace);
+  float* ws_acc = workspace + kTicketWords;
   float* ws_ml = ws_acc + rows * nsplit * g * kD;
   const int nb = static_cast<int>(cdiv(tokens, block));
   const float scale_log2 = scaling * 1.4426950408889634f;
@@ -350,12 +370,7 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   sparse_attn_kernel<GG, ni_for(GG)><<<grid, kNT, 0, st>>>(                                            \
       q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                 \
       static_cast<int>(kv_heads), tokens, block_ids, static_cast<int>(n_sel), static_cast<int>(block), \
-      nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, o);                                     \
-  if (nsplit > 1) {                                                                                    \
-    if (int rc = check_launch("qkv_sparse_attention(partial)")) return rc;                             \
-    sparse_attn_merge_kernel<GG><<<static_cast<unsigned>(rows), GG * kD, 0, st>>>(                     \
-        ws_acc, ws_ml, static_cast<int>(nsplit), static_cast<int>(q_heads), static_cast<int>(kv_heads), o); \
-  }
+      nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o)
   switch (g) {
     case 1: QKV_ATTN(1); break;
     case 2: QKV_ATTN(2); break;

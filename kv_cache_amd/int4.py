@@ -199,10 +199,12 @@ def attention_workspace_bytes(batch: int, q_heads: int, kv_heads: int, head_dim:
 
 def attention_workspace(batch: int, q_heads: int, kv_heads: int, head_dim: int, n_sel: int, block: int,
                         device) -> torch.Tensor:
-    """Workspace for ``sparse_attention`` calls up to these sizes (split
-    partials; calls sharing one must not overlap in time)."""
+    """Zero-filled workspace for ``sparse_attention`` calls up to these sizes.
+    Its leading ticket words must be zero before the first call; every
+    completed call leaves them zero, so one workspace serves any number of
+    calls.  Calls sharing a workspace must not overlap in time."""
     need = attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block)
-    return torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
+    return torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
 
 
 def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,

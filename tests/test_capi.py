@@ -79,11 +79,11 @@ def test_host_side_validation(call, msg):
 
 
 def test_workspace_size_formula():
-    # rows * splits * G * (D + 2) floats;
-    # splits = ceil(n_sel * block / slots), slots = 256 token slots (128 at G = 8)
-    t = 0
-    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * (t + 64 * 8 * 2 * 130)
-    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * (t + 8 * 1 * 2 * 130)
+    # 65536 ticket words + rows * splits * G * (D + 2) floats;
+    # splits = ceil(n_sel * block / 128 token slots)
+    t = 65536
+    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * (t + 64 * 16 * 2 * 130)
+    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * (t + 8 * 2 * 2 * 130)
     assert lib.qkv_sparse_attention_workspace_bytes(1, 64, 8, 128, 300, 1) == 4 * (t + 8 * 3 * 8 * 130)
     assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 64, 256, 1) == -1
 

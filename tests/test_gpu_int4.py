@@ -224,7 +224,8 @@ def test_sparse_attention_matches_fp64(g_size, block, nsel):
 
 
 def test_sparse_attention_workspace_reuse():
-    # One workspace serves successive calls with different split counts.
+    # One zero-filled workspace serves successive calls with different split
+    # counts: the row tickets return to zero after every call.
     gen = torch.Generator().manual_seed(9)
     b, hkv, g_size, t = 2, 4, 2, 5000
     q = torch.randn((b, hkv * g_size, 128), generator=gen).to(torch.bfloat16)
@@ -239,6 +240,8 @@ def test_sparse_attention_workspace_reuse():
         out = K.sparse_attention(qd, kd, vd, sel.to(DEV), block, t, 0.088, workspace=ws)
         want = O.sparse_attention(f32(q), f32(k), f32(v), sel.numpy(), block, t, 0.088)
         assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL), (nsel, block)
+    tickets = ws[:65536].view(torch.int32).cpu()
+    assert int(tickets.abs().sum()) == 0
 
 
 def test_sparse_attention_no_valid_block_gives_zero():
