@@ -189,6 +189,39 @@ int qkv_sparse_attention(const void* query, const void* key, const void* value,
                          const int32_t* block_ids, int64_t n_sel, int64_t block, float scaling,
                          float* workspace, int64_t workspace_bytes, void* out, void* stream);
 
+/* ======================================================================
+ * Chunked-prefill block selection (no reference counterpart: the reference
+ * prefills with dense attention, EV:7079-7111, dense QK at EV:6602-6604).
+ * ====================================================================== */
+
+/* Per-row int8 quantization of prefill queries: query bf16 rows of 128
+ * channels (row_stride elements apart), q8 = clamp(rint(q / (amax/127)),
+ * +-127) per row, written as int8 [rows,128] in the permuted order the MFMA
+ * scoring kernel consumes: channel c at byte 32*(c/32) + 16*((c/16)%2) +
+ * 8*((c%16)/8) + 4*(c%2) + (c%8)/2.  qscale f32 [rows] optional. */
+int qkv_prefill_quantize_query(const void* query, int64_t rows, int64_t head_dim, int64_t row_stride,
+                               int8_t* q8, float* qscale, void* stream);
+
+/* Block maxima of a query chunk against the whole cached K, on int8 MFMA.
+ * q8 [B,Hq,queries,128] from qkv_prefill_quantize_query; packed uint8
+ * [B,Hkv,capacity,64] and scales fp16 bits [B,Hkv,capacity] are K packed
+ * with group 128 (qkv_int4_pack_k).  Query i sits at position q_pos0 + i and
+ * sees keys t <= q_pos0 + i, t < tokens.  key = fp32(scale[t]) * fp32(I),
+ * I = sum over 128 channels of q8 * code (exact int32); bmax f32
+ * [B,Hq,queries,ceil(tokens/block)] is the max over each block's visible
+ * keys (-inf if none), -0 read as +0.  block must be 64. */
+int qkv_prefill_block_scores(const int8_t* q8, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             int64_t queries, const uint8_t* packed, const uint16_t* scales,
+                             int64_t capacity, int64_t tokens, int64_t q_pos0, int64_t head_dim,
+                             int64_t block, float* bmax, void* stream);
+
+/* Top-k blocks per row of bmax f32 [rows,n] (row stride ld, n <= 4096) as
+ * qkv_topk does it, except that blocks whose value is -inf are never
+ * selected: a row with fewer than k finite blocks lists those in ascending
+ * order and pads with -1.  out int32 [rows,k]. */
+int qkv_prefill_block_topk(const float* bmax, int64_t rows, int64_t n, int64_t ld, int64_t k,
+                           int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,6 +13,7 @@ namespace qkv {
 namespace {
 
 constexpr int kBins = 2048;
+constexpr uint32_t kNegInfKey = 0x007FFFFFu;   // f32_sortable(-inf)
 constexpr int kLdsKeys = 12288;   // rows up to this many keys are staged in LDS (48 KB)
 
 template <int NT>
@@ -159,12 +160,14 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 // Output positions follow index order: the keys taken before slot (i, wave)
 // are the keys > theta before it plus min(kr, keys == theta before it), both
 // known from per-(slot, wave) ballot counts, so one pass places every key.
-template <int VPL>
+// FINITE: keys equal to -inf are not selectable; a row with fewer than k
+// other keys selects them all and pads its output with -1.
+template <int VPL, bool FINITE>
 __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict__ values, int n, int64_t ld,
                                                         int k, int32_t* __restrict__ out) {
   __shared__ int hist[4][260];             // one copy per wave, padded across banks
   __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
-  __shared__ uint32_t red[4][2];
+  __shared__ uint32_t red[4][3];
   __shared__ int sh_bin, sh_kr, sh_whole;
   __shared__ int32_t sel[256 * VPL];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -176,34 +179,44 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int idx = i * 256 + tid;
-    valid[i] = idx < n;
     u[i] = f32_sortable(vals[min(idx, n - 1)]);
+    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey);
   }
   uint32_t umax = 0, umin = 0xFFFFFFFFu;
+  int nval = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     if (valid[i]) {
       umax = max(umax, u[i]);
       umin = min(umin, u[i]);
     }
+    nval += __popcll(__ballot(valid[i]));
   }
   umax = wave_minmax_u32<true>(umax);
   umin = wave_minmax_u32<false>(umin);
   if (lane == 0) {
     red[wave][0] = umax;
     red[wave][1] = umin;
+    red[wave][2] = nval;
   }
   __syncthreads();
   umax = max(max(red[0][0], red[1][0]), max(red[2][0], red[3][0]));
   umin = min(min(red[0][1], red[1][1]), min(red[2][1], red[3][1]));
+  nval = red[0][2] + red[1][2] + red[2][2] + red[3][2];
+  const int kk = min(k, nval);   // keys selected; k unless FINITE drops some
 
   // Radix select over the bits below the common prefix of umax and umin.
-  int kr = k;
+  int kr = kk;
   uint32_t prefix = umax, mask = 0xFFFFFFFFu;
-  int remaining = (umax == umin) ? 0 : 32 - __builtin_clz(umax ^ umin);
+  int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
   if (remaining) {
     mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
     prefix = umax & mask;
+  }
+  if (kk == nval) {   // every valid key is taken: no select needed
+    prefix = umin;
+    kr = 0x7FFFFFFF;
+    remaining = 0;
   }
   while (remaining > 0) {   // uniform across the workgroup
     const int shift = remaining > 8 ? remaining - 8 : 0;
@@ -286,7 +299,20 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
   }
   __syncthreads();
   int32_t* orow = out + static_cast<int64_t>(row) * k;
-  for (int j = tid; j < k; j += 256) orow[j] = sel[j];
+  for (int j = tid; j < k; j += 256) orow[j] = j < kk ? sel[j] : -1;
+}
+
+template <bool FINITE>
+int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
+                hipStream_t st) {
+  const unsigned wg = static_cast<unsigned>(rows);
+  const int nn = static_cast<int>(n), kk = static_cast<int>(k);
+  if (n <= 256) topk_rows_kernel<1, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
+  else if (n <= 512) topk_rows_kernel<2, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
+  else if (n <= 1024) topk_rows_kernel<4, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
+  else if (n <= 2048) topk_rows_kernel<8, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
+  else topk_rows_kernel<16, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
+  return check_launch("qkv_topk");
 }
 
 }  // namespace
@@ -304,16 +330,7 @@ QKV_EXPORT int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld
                                   (long long)k, (long long)n);
   if (rows > 0x7FFFFFFF) return fail(QKV_ERR_INVALID, "qkv_topk: too many rows");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (n <= 4096) {
-    const unsigned wg = static_cast<unsigned>(rows);
-    const int nn = static_cast<int>(n), kk = static_cast<int>(k);
-    if (n <= 256) topk_rows_kernel<1><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
-    else if (n <= 512) topk_rows_kernel<2><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
-    else if (n <= 1024) topk_rows_kernel<4><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
-    else if (n <= 2048) topk_rows_kernel<8><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
-    else topk_rows_kernel<16><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
-    return check_launch("qkv_topk");
-  }
+  if (n <= 4096) return launch_rows<false>(values, rows, n, ld, k, out, st);
   const unsigned grid = static_cast<unsigned>(rows);
   if (n <= kLdsKeys) {
     topk_kernel<1024, true><<<grid, 1024, n * sizeof(uint32_t), st>>>(values, static_cast<int>(n), ld,
@@ -323,4 +340,15 @@ QKV_EXPORT int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld
                                                     static_cast<int>(k), out);
   }
   return check_launch("qkv_topk");
+}
+
+QKV_EXPORT int qkv_prefill_block_topk(const float* bmax, int64_t rows, int64_t n, int64_t ld, int64_t k,
+                                      int32_t* out, void* stream) {
+  if (!bmax || !out) return fail(QKV_ERR_INVALID, "qkv_prefill_block_topk: null pointer");
+  if (rows <= 0 || rows > 0x7FFFFFFF || n <= 0 || ld < n)
+    return fail(QKV_ERR_INVALID, "qkv_prefill_block_topk: bad sizes rows=%lld n=%lld ld=%lld", (long long)rows,
+                (long long)n, (long long)ld);
+  if (n > 4096) return fail(QKV_ERR_UNSUPPORTED, "qkv_prefill_block_topk: at most 4096 blocks per row");
+  if (k < 1 || k > n) return fail(QKV_ERR_INVALID, "qkv_prefill_block_topk: need 1 <= k <= n");
+  return launch_rows<true>(bmax, rows, n, ld, k, out, static_cast<hipStream_t>(stream));
 }

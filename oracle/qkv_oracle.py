@@ -381,6 +381,23 @@ def quantize_query_rows(q) -> tuple[np.ndarray, np.ndarray]:
     return q8.astype(np.int8), qscale
 
 
+def prefill_query_slot(c):
+    """Byte position of channel c in a permuted 128-channel prefill query row:
+    32*(c/32) + 16*((c/16)%2) + 8*((c%16)/8) + 4*(c%2) + (c%8)/2 (the order in
+    which the MFMA scoring kernel's unpacked K bytes list channels)."""
+    c = np.asarray(c, dtype=np.int64)
+    c16 = c % 16
+    return 32 * (c // 32) + 16 * ((c // 16) % 2) + 8 * (c16 // 8) + 4 * (c16 % 2) + (c16 % 8) // 2
+
+
+def permute_prefill_query(q8) -> np.ndarray:
+    """int8 [..., 128] logical channel order -> the device's permuted order."""
+    q8 = np.asarray(q8, dtype=np.int8)
+    out = np.empty_like(q8)
+    out[..., prefill_query_slot(np.arange(128))] = q8
+    return out
+
+
 def prefill_block_scores(q8, kpacked, kscale_bits, block: int, q_pos0: int) -> np.ndarray:
     """Block-max ranking keys of a query chunk against the whole packed K.
 

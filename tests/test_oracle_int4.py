@@ -411,3 +411,14 @@ def test_pack_query_words_layout():
     b = w.view(np.uint8).view(np.int8).reshape(-1).tolist()
     # word 0: even channels 0,2,4,6; word 1: odd channels 1,3,5,7; then 8..15
     assert b == [-8, -6, -4, -2, -7, -5, -3, -1, 0, 2, 4, 6, 1, 3, 5, 7]
+
+
+def test_prefill_query_slot_layout():
+    slot = O.prefill_query_slot(np.arange(128))
+    assert np.array_equal(np.sort(slot), np.arange(128))            # a permutation
+    # channels 0..15 (group 0, half 0): even channels of 0..7, odd of 0..7, then 8..15
+    assert slot[:16].tolist() == [0, 4, 1, 5, 2, 6, 3, 7, 8, 12, 9, 13, 10, 14, 11, 15]
+    assert slot[16] == 16 and slot[32] == 32 and slot[127] == 127
+    q = np.arange(-64, 64, dtype=np.int8)
+    perm = O.permute_prefill_query(q)
+    assert perm[slot[5]] == q[5] and perm[1] == q[2]
