@@ -130,14 +130,16 @@ def cpu_baseline(cfg, budget_s: float) -> dict:
     }
 
 
-def read_traffic(kernel: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc, from profiles/."""
+def read_traffic(config: str, kernel: str):
+    """HBM bytes per launch of ``kernel`` at ``config``, measured by two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) scaled by a device copy
+    of known size; recorded in profiles/hbm_traffic.json (None if absent)."""
     p = ROOT / "profiles" / "hbm_traffic.json"
     if not p.exists():
         return None
     try:
         data = json.loads(p.read_text())
-        return data.get(kernel, {}).get("bytes_per_launch")
+        return data.get(config, {}).get(kernel, {}).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
 
@@ -271,7 +273,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": sc["gbs"] / HBM_PEAK_GBS,
-            "traffic": read_traffic("decode_scores_kernel"),
+            "traffic": read_traffic(args.config, "decode_scores_kernel"),
         },
         "kernels": kernels,
         "cpu_baseline": cpu,

@@ -291,12 +291,24 @@ template <> struct LaneScales<8> {
 // channels 8d..8d+7 (channel 8d+i in nibble i), so qlo[d] packs the int8
 // query of its even channels and qhi[d] the odd ones; both arrays and *qs
 // come back wave-uniform.
+//
+// Split in two so that a caller can put other loads between them: the load
+// phase issues every global load the query needs (the channel ids and the
+// first kQPre head rows, lane l holding channels 2l, 2l+1), the finish phase
+// does the arithmetic.  Loads return in issue order, so loads issued after
+// the load phase stay in flight while the finish phase waits for its own.
+constexpr int kQPre = 8;   // head rows loaded ahead; rows beyond are loaded in the finish phase
+
 template <int S>
-__device__ __forceinline__ void row_query_words(const uint16_t* __restrict__ query, int q_heads,
-                                                int kv_heads, int head_dim,
-                                                const int32_t* __restrict__ chan_idx, int r,
-                                                uint32_t (&qlo)[S / 8], uint32_t (&qhi)[S / 8],
-                                                float* qs_out) {
+struct RowQueryLoads {
+  uint32_t w[kQPre];
+  int c0, c1;
+};
+
+template <int S>
+__device__ __forceinline__ RowQueryLoads<S> row_query_load(const uint16_t* __restrict__ query, int q_heads,
+                                                           int kv_heads, int head_dim,
+                                                           const int32_t* __restrict__ chan_idx, int r) {
   const int lane = threadIdx.x & 63;
   const int G = q_heads / kv_heads;
   const int b = r / kv_heads, j = r - b * kv_heads;
@@ -304,11 +316,40 @@ __device__ __forceinline__ void row_query_words(const uint16_t* __restrict__ que
   const uint32_t* qrow = reinterpret_cast<const uint32_t*>(
       query + (static_cast<int64_t>(b) * q_heads + j * G) * head_dim);
   const int hd2 = head_dim / 2;   // channel pairs per head row
-  const int c0 = lane < S ? cidx[lane] : 0;
-  const int c1 = S > 64 ? cidx[lane + 64] : 0;
-  float lo = 0.0f, hi = 0.0f;     // fp32 head sums of channels 2*lane, 2*lane+1
-  if (lane < hd2) {
-    for (int i = 0; i < G; ++i) {
+  // Unconditional loads from clamped indices (redundant ones hit in cache);
+  // the finish phase ignores the lanes and rows they stand in for.
+  RowQueryLoads<S> L;
+  L.c0 = cidx[min(lane, S - 1)];
+  L.c1 = S > 64 ? cidx[lane + 64] : 0;
+  const int lw = min(lane, hd2 - 1);
+#pragma unroll
+  for (int i = 0; i < kQPre; ++i) L.w[i] = qrow[min(i, G - 1) * hd2 + lw];
+  return L;
+}
+
+template <int S>
+__device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, const uint16_t* __restrict__ query,
+                                                 int q_heads, int kv_heads, int head_dim, int r,
+                                                 uint32_t (&qlo)[S / 8], uint32_t (&qhi)[S / 8],
+                                                 float* qs_out) {
+  const int lane = threadIdx.x & 63;
+  const int G = q_heads / kv_heads;
+  const int hd2 = head_dim / 2;
+  const int c0 = L.c0, c1 = L.c1;
+  float lo = 0.0f, hi = 0.0f;     // fp32 head sums of channels 2*lane, 2*lane+1, in head order
+#pragma unroll
+  for (int i = 0; i < kQPre; ++i) {
+    if (i < G) {
+      lo = lo + bf16lo(L.w[i]);
+      hi = hi + bf16hi(L.w[i]);
+    }
+  }
+  if (lane >= hd2) lo = hi = 0.0f;   // no channel pair: never picked
+  if (G > kQPre && lane < hd2) {
+    const int b = r / kv_heads, j = r - b * kv_heads;
+    const uint32_t* qrow = reinterpret_cast<const uint32_t*>(
+        query + (static_cast<int64_t>(b) * q_heads + j * G) * head_dim);
+    for (int i = kQPre; i < G; ++i) {
       const uint32_t w = qrow[i * hd2 + lane];
       lo = lo + bf16lo(w);
       hi = hi + bf16hi(w);
@@ -358,7 +399,8 @@ __global__ __launch_bounds__(64) void query_words_kernel(
   const int r = blockIdx.x, lane = threadIdx.x;
   uint32_t qlo[S / 8], qhi[S / 8];
   float qs;
-  row_query_words<S>(query, q_heads, kv_heads, head_dim, chan_idx, r, qlo, qhi, &qs);
+  const RowQueryLoads<S> ql = row_query_load<S>(query, q_heads, kv_heads, head_dim, chan_idx, r);
+  row_query_finish<S>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
   uint32_t* out = qwords + static_cast<int64_t>(r) * (S / 4);
 #pragma unroll
   for (int d = 0; d < S / 8; ++d) {
@@ -383,14 +425,11 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
   const int r = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
-  // Every wave builds the row's query words first and only then starts its
-  // slab stream: the prologue's few loads then meet idle memory queues
-  // instead of waiting behind the CU's slab traffic (measured faster than a
-  // separate per-row kernel, whose launch costs more than the redundancy).
-  uint32_t qlo[DW], qhi[DW];
-  float qs;
-  row_query_words<S>(query, q_heads, kv_heads, head_dim, chan_idx, r, qlo, qhi, &qs);
-  if (qscale_out && blockIdx.x == 0 && wave == 0 && lane == 0) qscale_out[r] = qs;
+  // Every wave builds the row's int8 query itself (a separate per-row kernel
+  // costs a launch, more than the redundancy).  Its few loads go out first,
+  // the first slab stage's loads right behind them; the query arithmetic
+  // then waits only for its own loads and overlaps the slab loads in flight.
+  const RowQueryLoads<S> ql = row_query_load<S>(query, q_heads, kv_heads, head_dim, chan_idx, r);
   __builtin_amdgcn_sched_barrier(0);
 
   const int64_t row_tok = static_cast<int64_t>(r) * capacity;
@@ -399,24 +438,32 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
   const int t_lo = blockIdx.x * chunk;
   const int t_hi = min(tokens, t_lo + chunk);
 
+  // A wave's stages start at t_lo + wave*STAGE and step by 4*STAGE; t_lo is
+  // a multiple of 4*STAGE, so every stage is one whole tile.  A stage with
+  // tb < t_hi <= tokens <= capacity lies inside the row's slab and scales
+  // (capacity is a multiple of STAGE), so its loads need no per-lane guard:
+  // lanes past t_hi read padding that score_stage masks to -inf.  Loads
+  // issued without branches let the compiler count them exactly, so a wait
+  // for older loads never waits for the stage loads behind them.
   auto load_stage = [&](int tb, uint4 (&cw)[4], LS& sv) {
-    if (tb + lane * KPLN < t_hi) {
-      const uint4* tile = codes + (static_cast<int64_t>(tb) / STAGE) * 256;
+    const uint4* tile = codes + (static_cast<int64_t>(tb) / STAGE) * 256;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cw[i] = ld_nt(tile + i * 64 + lane);
-      sv.load(scl + tb + lane * KPLN);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cw[i] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < (KPLN + 1) / 2; ++i) sv.w[i] = 0;
-    }
+    for (int i = 0; i < 4; ++i) cw[i] = ld_nt(tile + i * 64 + lane);
+    sv.load(scl + tb + lane * KPLN);
   };
 
   int tb = t_lo + wave * STAGE;
+  if (tb >= t_hi) return;   // wave-uniform; the kernel has no workgroup barrier
+  const int nst = (t_hi - tb + 4 * STAGE - 1) / (4 * STAGE);   // stages of this wave
   uint4 cw[4];
   LS sv;
   load_stage(tb, cw, sv);
+  __builtin_amdgcn_sched_barrier(0);
+
+  uint32_t qlo[DW], qhi[DW];
+  float qs;
+  row_query_finish<S>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
+  if (qscale_out && blockIdx.x == 0 && wave == 0 && lane == 0) qscale_out[r] = qs;
 
   const float ninf = -__builtin_huge_valf();
   // block <= KPLN: each lane writes KPLN / block maxima; else lanes in groups
@@ -471,17 +518,18 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
   };
 
   // Each wave walks its stages with the next stage's loads in flight.
-  while (tb < t_hi) {
+  for (int i = 1; i < nst; ++i) {
     const int tn = tb + 4 * STAGE;
     uint4 nw[4];
     LS nsv;
-    if (tn < t_hi) load_stage(tn, nw, nsv);
+    load_stage(tn, nw, nsv);
     score_stage(tb, cw, sv);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) cw[i] = nw[i];
+    for (int u = 0; u < 4; ++u) cw[u] = nw[u];
     sv = nsv;
     tb = tn;
   }
+  score_stage(tb, cw, sv);
 }
 
 template <bool DEBUG>

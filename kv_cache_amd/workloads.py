@@ -66,6 +66,28 @@ class PrefillConfig:
     topk: int
     seed: int = 1234
 
+    @property
+    def g(self) -> int:
+        return self.q_heads // self.kv_heads
+
+    @property
+    def q_pos0(self) -> int:
+        """Position of the chunk's first query: the last chunk of the prefill."""
+        return self.tokens - self.queries
+
+    @property
+    def n_blocks(self) -> int:
+        return -(-self.tokens // self.block)
+
+    def visible_keys(self) -> int:
+        """Sum over query rows of one head of the keys each one sees (causal)."""
+        return sum(min(self.tokens, self.q_pos0 + i + 1) for i in range(self.queries))
+
+    def int_ops(self) -> int:
+        """Algorithmic int8 ops of one scoring pass: 2 * D per visible (query
+        head, key) pair."""
+        return 2 * self.head_dim * self.batch * self.q_heads * self.visible_keys()
+
 
 CONFIGS = {
     "cfg1": DecodeConfig("qwen3-0.6b-1layer-b1-t4096", 1, 16, 8, 128, 4096, 32, 32, 1, 256, 1, False),
@@ -83,8 +105,9 @@ def outlier_channels(head_dim: int, seed: int, count: int = 4) -> torch.Tensor:
 
 
 def rope_tables(positions: torch.Tensor, head_dim: int, theta: float = 1.0e6):
+    """cos/sin tables fp32 [P, head_dim], computed in fp64 on the CPU."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
-    ang = positions.to(torch.float64)[:, None] * inv[None, :]
+    ang = positions.cpu().to(torch.float64)[:, None] * inv[None, :]
     ang = torch.cat([ang, ang], dim=-1)
     return ang.cos().float(), ang.sin().float()
 
@@ -134,3 +157,21 @@ def make_layer(cfg: DecodeConfig, layer: int = 0, device: str | torch.device = "
         norm = k[bi, hi, planted].norm(dim=-1, keepdim=True)
         k[bi, hi, planted] = norm * (0.9 * u + math.sqrt(1.0 - 0.81) * w)
     return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16), planted
+
+
+def make_prefill(cfg: PrefillConfig, device: str | torch.device = "cpu", tokens: int | None = None,
+                 queries: int | None = None):
+    """Seeded (q bf16 [B, Hq, Nq, D], k bf16 [B, Hkv, T, D]) of a prefill
+    chunk: N(0, 1) with the 4 outlier channels of ``outlier_channels`` scaled
+    x8 in both.  ``tokens``/``queries`` shrink the shape for tests."""
+    t = cfg.tokens if tokens is None else int(tokens)
+    nq = cfg.queries if queries is None else int(queries)
+    dev = torch.device(device)
+    gen = torch.Generator(device=dev).manual_seed(cfg.seed)
+    d = cfg.head_dim
+    k = torch.randn((cfg.batch, cfg.kv_heads, t, d), generator=gen, device=dev, dtype=torch.float32)
+    q = torch.randn((cfg.batch, cfg.q_heads, nq, d), generator=gen, device=dev, dtype=torch.float32)
+    out_ch = outlier_channels(d, cfg.seed).to(dev)
+    k[..., out_ch] *= 8.0
+    q[..., out_ch] *= 8.0
+    return q.to(torch.bfloat16), k.to(torch.bfloat16)

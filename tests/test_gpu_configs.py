@@ -1,0 +1,127 @@
+"""Parity at the real shapes of the five benchmark configurations.
+
+Every (sequence, KV head) row is independent through packing, channel
+choice, scoring, pooling, top-k and attention, so the GPU runs each
+configuration's whole layer while the CPU oracle recomputes a sample of
+full-length rows from the same bf16 K/V and q (bit-exact packing, channel
+ids, slab, block maxima and top-k; attention within 1e-2 relative / 2e-2
+absolute of fp64).  On every row, the GPU's top-k is checked against a
+stable sort of the GPU's own block maxima, which is exact at any size.
+Config 4 also reports the recall of its planted key at k = 64, 256 and
+1024 tokens, which must equal the oracle's.  Config 3 runs at batch 8 of
+its 32 (64 rows of 32768 keys; rows do not interact)."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import int4 as K
+from kv_cache_amd import prefill as P
+from kv_cache_amd.workloads import CONFIGS, PREFILL, make_layer, make_prefill
+from oracle import qkv_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def _bits16(t):
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _sample_rows(rows: int, n: int, seed: int) -> list[int]:
+    rng = np.random.default_rng(seed)
+    picks = {0, rows - 1}
+    picks.update(int(x) for x in rng.choice(rows, size=min(rows, n), replace=False))
+    return sorted(picks)[: max(n, 2)]
+
+
+def _decode_case(name: str, batch: int | None = None, n_rows: int = 3):
+    cfg = CONFIGS[name]
+    q, k, v, planted = make_layer(cfg, 0, device=DEV, batch=batch)
+    b = q.size(0)
+    rows = b * cfg.kv_heads
+    cache = K.Int4KCache.from_prefill(k, cfg.group, cfg.selected)
+    step = K.SparseDecodeStep(b, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.tokens, cfg.block, cfg.topk, DEV)
+    out = step(q, cache, k, v, cfg.scaling)
+    torch.cuda.synchronize()
+
+    bmax = step.bmax.cpu().numpy().reshape(rows, -1)
+    sel = step.sel.cpu().numpy().reshape(rows, -1)
+    # top-k of every row, against the GPU's own block maxima
+    assert np.array_equal(sel, O.topk_lowest_index(bmax, cfg.topk))
+
+    g = cfg.g
+    for r in _sample_rows(rows, n_rows, seed=rows):
+        bi, j = divmod(r, cfg.kv_heads)
+        kr = k[bi, j].float().cpu().numpy()[None]                     # [1, T, D]
+        packed, scales = O.int4_pack_k(kr, cfg.group)
+        assert np.array_equal(cache.packed[bi, j, : cfg.tokens].cpu().numpy(), packed[0])
+        assert np.array_equal(_bits16(cache.scales[bi, j, : cfg.tokens]), scales[0])
+        chan = O.select_channels(O.channel_stats(packed, scales, cfg.group), cfg.selected)
+        assert np.array_equal(cache.chan_idx[bi, j].cpu().numpy(), chan[0])
+        slab, sbits = O.build_slab(kr, chan)
+        stored = cache.slab[bi, j].cpu().numpy().reshape(1, -1)
+        assert np.array_equal(O.unswizzle_slab(stored, cfg.selected, cfg.tokens), slab)
+        qr = q[bi : bi + 1, j * g : (j + 1) * g].float().cpu().numpy()   # the row's G query heads
+        _, _, want_bmax, want_sel = O.decode_select(qr, slab, sbits, chan, 1, cfg.block, cfg.topk)
+        assert np.array_equal(bmax[r], want_bmax[0]), f"row {r}: block maxima differ"
+        assert np.array_equal(sel[r], want_sel[0]), f"row {r}: top-k differs"
+        want_out = O.sparse_attention(qr, k[bi : bi + 1, j : j + 1].float().cpu().numpy(),
+                                      v[bi : bi + 1, j : j + 1].float().cpu().numpy(), want_sel[None],
+                                      cfg.block, cfg.tokens, cfg.scaling)
+        got_out = out[bi, j * g : (j + 1) * g].float().cpu().numpy()
+        np.testing.assert_allclose(got_out, want_out[0], rtol=RTOL, atol=ATOL)
+    return cfg, step, planted
+
+
+def test_config1_full():
+    _decode_case("cfg1", n_rows=8)
+
+
+def test_config2_full_layer():
+    _decode_case("cfg2", n_rows=3)
+
+
+def test_config3_rows():
+    _decode_case("cfg3", batch=8, n_rows=3)
+
+
+def test_config4_planted_recall():
+    cfg, step, planted = _decode_case("cfg4", n_rows=2)
+    rows = cfg.rows
+    bmax = step.bmax.cpu().numpy().reshape(rows, -1)
+    pl = planted.cpu().numpy().reshape(rows)
+    recalls = {}
+    for kk in (64, 256, 1024):
+        sel = K.block_topk(step.bmax, kk).cpu().numpy().reshape(rows, -1)
+        assert np.array_equal(sel, O.topk_lowest_index(bmax, kk))
+        recalls[kk] = O.recall_at(O.expand_blocks(sel, cfg.block, cfg.tokens), pl)
+    print(f"cfg4 planted-key recall: {recalls}")
+    # planted keys are built with cosine 0.9 to the group's mean query: they rank first by far
+    assert recalls[1024] == 1.0
+
+
+def test_config5_sampled_rows():
+    cfg = PREFILL
+    q, k = make_prefill(cfg, device=DEV)
+    packed, scales = K.int4_pack_k(k, 128)
+    sel, bmax = P.select_blocks(q, packed, scales, cfg.tokens, cfg.q_pos0, cfg.topk)
+    torch.cuda.synchronize()
+    nb = cfg.n_blocks
+    bm = bmax.cpu().numpy().reshape(-1, nb)
+    sl = sel.cpu().numpy().reshape(-1, cfg.topk)
+    assert np.array_equal(sl, O.prefill_block_topk(bm, cfg.topk))        # every query row
+    # oracle on sampled query rows of two heads (the whole key range)
+    kp, ks = O.int4_pack_k(k.float().cpu().numpy(), 128)
+    for head in (0, cfg.q_heads - 1):
+        qi = np.array([0, 1, 63, 64, 1000, cfg.queries - 1])
+        qh = q[:, head : head + 1, qi].float().cpu().numpy()             # [1, 1, 6, D]
+        q8, _ = O.quantize_query_rows(qh)
+        j = head // cfg.g
+        for n, i in enumerate(qi):
+            want = O.prefill_block_scores(q8[:, :, n : n + 1], kp[:, j : j + 1], ks[:, j : j + 1, :, 0], cfg.block,
+                                          cfg.q_pos0 + int(i))
+            got = bmax[0, head, i].cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)), f"head {head} q {i}"
+            assert np.array_equal(sel[0, head, i].cpu().numpy(), O.prefill_block_topk(want.reshape(1, -1), cfg.topk)[0])
