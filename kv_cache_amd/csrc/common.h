@@ -96,6 +96,29 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// DPP move: lane i receives `v` of the lane CTRL selects (row_shl:n = lane
+// i + n of the same row of 16, quad_perm, row mirrors, row_bcast ...).
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t old, uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), CTRL,
+                                                           ROW_MASK, BANK_MASK, false));
+}
+
+// Max of a non-negative float over the 64 lanes, wave-uniform: row
+// reductions (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror),
+// then row_bcast:15 and row_bcast:31 leave the wave's maximum in lane 63.
+// Non-negative floats order like their bit patterns, so the max is exact.
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  uint32_t v = __float_as_uint(x);
+  v = max(v, dpp_mov<0xB1>(v, v));
+  v = max(v, dpp_mov<0x4E>(v, v));
+  v = max(v, dpp_mov<0x141>(v, v));
+  v = max(v, dpp_mov<0x140>(v, v));
+  v = max(v, dpp_mov<0x142, 0xA>(v, v));
+  v = max(v, dpp_mov<0x143, 0xC>(v, v));
+  return __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63)));
+}
+
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v) {
   int lane = __lane_id();

@@ -335,7 +335,10 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
   const int lane = threadIdx.x & 63;
   const int G = q_heads / kv_heads;
   const int hd2 = head_dim / 2;
-  const int c0 = L.c0, c1 = L.c1;
+  // The empty asm keeps every use of the loaded ids here, after whatever
+  // loads the caller issued since the load phase.
+  int c0 = L.c0, c1 = L.c1;
+  asm volatile("" : "+v"(c0), "+v"(c1));
   float lo = 0.0f, hi = 0.0f;     // fp32 head sums of channels 2*lane, 2*lane+1, in head order
 #pragma unroll
   for (int i = 0; i < kQPre; ++i) {
@@ -356,9 +359,9 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
     }
   }
   // qg of channel c, read from lane c/2 (ds_bpermute reads only lanes that
-  // execute it, so every lane runs it).
+  // execute it, so every lane runs it; it takes the lane index modulo 64, so
+  // an id outside the row cannot fault).
   auto pick = [&](int c) -> float {
-    c = min(max(c, 0), head_dim - 1);
     const float vl = __int_as_float(__builtin_amdgcn_ds_bpermute((c >> 1) << 2, __float_as_int(lo)));
     const float vh = __int_as_float(__builtin_amdgcn_ds_bpermute((c >> 1) << 2, __float_as_int(hi)));
     return (c & 1) ? vh : vl;
@@ -366,27 +369,28 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
   const float p0 = pick(c0);
   const float qg0 = lane < S ? p0 : 0.0f;
   const float qg1 = S > 64 ? pick(c1) : 0.0f;
-  const float amax = wave_max(fmaxf(fabsf(qg0), fabsf(qg1)));
+  const float amax = wave_max_nonneg(fmaxf(fabsf(qg0), fabsf(qg1)));
   const float qs = amax / 127.0f;
-  auto q8 = [&](float v) -> int {
-    if (qs == 0.0f) return 0;
+  auto q8 = [&](float v) -> uint32_t {
+    if (qs == 0.0f) return 0u;
     float t = __builtin_rintf(v / qs);
-    return static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f));
+    return static_cast<uint32_t>(static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f))) & 0xFFu;
   };
-  const int q8v0 = q8(qg0), q8v1 = q8(qg1);
+  // Lane s holds the int8 query of subset channel s (s + 64 in the second
+  // word).  Three DPP row shifts gather channels s, s+2, s+4, s+6 into lane
+  // s's bytes 0..3, so lane 8d holds qlo[d] and lane 8d+1 holds qhi[d]
+  // (8d+7 stays inside the lane's row of 16).
+  auto gather4 = [](uint32_t b) -> uint32_t {
+    return b | (dpp_mov<0x102>(0u, b) << 8) | (dpp_mov<0x104>(0u, b) << 16) | (dpp_mov<0x106>(0u, b) << 24);
+  };
+  const uint32_t w0 = gather4(q8(qg0));
+  const uint32_t w1 = S > 64 ? gather4(q8(qg1)) : 0u;
 #pragma unroll
   for (int d = 0; d < S / 8; ++d) {
-    uint32_t lo8 = 0, hi8 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int se = 8 * d + 2 * e, so = se + 1;
-      const int ve = se < 64 ? __builtin_amdgcn_readlane(q8v0, se) : __builtin_amdgcn_readlane(q8v1, se - 64);
-      const int vo = so < 64 ? __builtin_amdgcn_readlane(q8v0, so) : __builtin_amdgcn_readlane(q8v1, so - 64);
-      lo8 |= (static_cast<uint32_t>(ve) & 0xFFu) << (8 * e);
-      hi8 |= (static_cast<uint32_t>(vo) & 0xFFu) << (8 * e);
-    }
-    qlo[d] = lo8;
-    qhi[d] = hi8;
+    const uint32_t w = d < 8 ? w0 : w1;
+    const int l = (8 * d) & 63;
+    qlo[d] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(w), l));
+    qhi[d] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(w), l + 1));
   }
   *qs_out = qs;
 }
@@ -426,9 +430,10 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 
   // Every wave builds the row's int8 query itself (a separate per-row kernel
-  // costs a launch, more than the redundancy).  Its few loads go out first,
-  // the first slab stage's loads right behind them; the query arithmetic
-  // then waits only for its own loads and overlaps the slab loads in flight.
+  // costs a launch; sharing one wave's result through LDS puts its latency in
+  // front of every wave, measured slower).  Its few loads go out first, the
+  // first slab stage's loads right behind them; the query arithmetic then
+  // waits only for its own loads and overlaps the slab loads in flight.
   const RowQueryLoads<S> ql = row_query_load<S>(query, q_heads, kv_heads, head_dim, chan_idx, r);
   __builtin_amdgcn_sched_barrier(0);
 
