@@ -7,29 +7,47 @@
 // one pass over the selected rows, so every selected K/V row is read from HBM
 // once (512 bytes per token at D = 128).
 //
-// Work split: a workgroup (4 waves) owns 16*NI consecutive token slots of one
-// (sequence, KV head) row, where slot s is token (block_ids[s / block] * block
-// + s % block).  Inside a wave, 16 lanes share a token: lane (16*g + c) holds
-// channels 8c..8c+7 of the token of slot 4i + g in iteration i, so each load
-// instruction reads four whole 256-byte K (or V) rows.  All K and V loads of a
-// wave are issued before any arithmetic.  QK is v_dot2_f32_bf16 on the packed
-// channel pairs followed by a 16-lane DPP reduction; softmax runs in the log2
-// domain; P.V accumulates in fp32.  Each workgroup reduces its waves through
-// LDS into (max, sum, weighted V) per head.  A row that fits one workgroup
-// writes its bf16 output directly.  Otherwise every workgroup publishes its
-// partial with device-coherent stores (relaxed agent-scope atomic stores:
-// global_store sc1, written through the XCD's L2), waits for them to
-// complete, and takes a ticket; the row's last workgroup reads the partials
-// back with device-coherent loads (sc1) and writes the output.  No release /
-// acquire fence is used: on gfx950 those write back and invalidate the whole
-// L2 of the XCD (buffer_wbl2 / buffer_inv), which measured 3x slower here.
+// Work split: slot s of a row is token (block_ids[s / block] * block +
+// s % block).  A workgroup (4 waves) owns a contiguous range of slots of one
+// (sequence, KV head) row; its waves take chunks of 4*NI slots in turn
+// (chunk c of wave w is the workgroup's chunk 4c + w).  Inside a chunk, 16
+// lanes share a token: lane (16*g + c) holds channels 8c..8c+7 of the token
+// of slot 4i + g in step i, so each load instruction reads four whole
+// 256-byte K (or V) rows.  While a wave computes chunk c, the K/V loads of
+// chunk c+1 and the block ids of chunk c+2 are in flight; the chunk loop is
+// unrolled at compile time and every load is issued without a branch, so
+// each wait covers exactly the loads it needs.
+//
+// QK is v_dot2_f32_bf16 on the packed channel pairs followed by a 16-lane
+// DPP sum; softmax runs in the log2 domain with a running maximum per
+// 16-lane token group (no cross-group traffic inside the loop); P.V
+// accumulates in fp32.  A wave combines its four token groups with the
+// gfx950 VALU lane swaps (v_permlane16_swap / v_permlane32_swap), and a
+// workgroup combines its waves through LDS into (max, sum, weighted V) per
+// head.  A row that fits one workgroup writes its bf16 output directly.
+// Otherwise every workgroup publishes its partial with device-coherent
+// stores (relaxed agent-scope atomic stores: global_store sc1, written
+// through the XCD's L2), waits for them to complete, and takes a ticket; the
+// row's last workgroup reads all partials back with device-coherent loads
+// (sc1), every load of a batch in flight at once, and writes the output.
+// No release / acquire fence is used: on gfx950 those write back and
+// invalidate the whole L2 of the XCD (buffer_wbl2 / buffer_inv).
 #include "common.h"
+
+#ifndef QKV_ATTN_TARGET_WGS
+#define QKV_ATTN_TARGET_WGS 1024
+#endif
+// Workgroups per CU the register budget is sized for (4 waves each).
+#ifndef QKV_ATTN_WG_PER_CU
+#define QKV_ATTN_WG_PER_CU 2
+#endif
 
 namespace qkv {
 namespace {
 
 constexpr int kD = 128;     // head dim
 constexpr int kNT = 256;    // threads per workgroup
+constexpr int kMaxIters = 8;
 // Ticket words at the start of the workspace, one per possible row, so calls
 // of any shape that share a workspace find their tickets at the same place.
 constexpr int64_t kTicketWords = 65536;
@@ -79,16 +97,50 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-template <int G, int NI>
-__global__ __launch_bounds__(kNT) void sparse_attn_kernel(
+// Pairs of lanes 16 and 32 apart, exchanged on the VALU.  v_permlane16_swap
+// swaps the odd rows of its first operand with the even rows of its second;
+// with both operands x, the two results hold x of the even and of the odd
+// row of each pair of rows, in every lane of the pair.  v_permlane32_swap
+// does the same for the two halves of the wave.  Both orders of the two
+// values are the same in every lane, so sums come out identical.
+__device__ __forceinline__ float sum_x16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_x16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Zero that the compiler cannot see through, available only once `dep` is:
+// adding it to an address keeps a load after the code that produced `dep`.
+__device__ __forceinline__ int zero_after(float dep) {
+  int z = 0;
+  asm volatile("" : "+v"(z) : "v"(dep));
+  return z;
+}
+// Marks x as final at this point: the volatile asm statements keep their
+// order, so whatever comes after a later one cannot move above the code
+// that computed x.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
+template <int G, int NI, int ITERS>
+__global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
-    int kv_heads, int64_t tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
+    int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
     int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
     uint32_t* __restrict__ tickets, uint16_t* __restrict__ out) {
-  constexpr int SLOTS_W = 4 * NI;          // token slots per wave
-  constexpr int SLOTS_WG = 4 * SLOTS_W;    // token slots per workgroup
-  static_assert(SLOTS_W <= 64, "one slot per lane when resolving token ids");
+  constexpr int CH = 4 * NI;               // token slots per wave chunk
+  static_assert(CH <= 64, "one slot per lane when resolving token ids");
 
   __shared__ float red_acc[4][G][kD];   // per wave weighted V
   __shared__ float red_m[4][G], red_l[4][G];
@@ -99,102 +151,149 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = lane >> 4, cc = lane & 15;
   const float ninf = -__builtin_huge_valf();
+  const int n_slots = n_sel * block;
+  const int32_t* ids = block_ids + static_cast<int64_t>(r) * n_sel;
 
-  // Token id of slot (wave base + lane), then of this lane's slot 4i + grp.
-  int my_tok = -1;
-  if (lane < SLOTS_W) {
-    const int64_t slot = static_cast<int64_t>(split) * SLOTS_WG + wave * SLOTS_W + lane;
-    const int64_t bs = slot / block;
-    if (bs < n_sel) {
-      const int id = block_ids[static_cast<int64_t>(r) * n_sel + bs];
-      if (id >= 0 && id < nb) {
-        const int64_t t = static_cast<int64_t>(id) * block + (slot - bs * block);
-        if (t < tokens) my_tok = static_cast<int>(t);
-      }
-    }
-  }
-  int tok[NI];
+  // Slot of this lane in chunk c (meaningful for lane < CH).
+  const int wg_base = split * (4 * CH * ITERS);
+  auto slot_of = [&](int c) -> int { return wg_base + (4 * c + wave) * CH + lane; };
+  // Block id of the lane's slot; lanes past CH and slots past the end get -1
+  // (the load itself always happens, from a clamped index).
+  auto load_id = [&](int c) -> int {
+    const int slot = slot_of(c);
+    const bool ok = lane < CH && slot < n_slots;
+    const int v = ids[ok ? slot / block : 0];
+    return ok ? v : -1;
+  };
+  // Token of the lane's slot from its block id, or -1.
+  auto token_of = [&](int c, int id) -> int {
+    if (id < 0 || id >= nb) return -1;
+    const int slot = slot_of(c);
+    const int t = id * block + (slot - (slot / block) * block);
+    return t < tokens ? t : -1;
+  };
+  // Token of slot 4i + grp (the lane's token in step i), from lane 4i + grp.
+  auto spread = [&](int my_tok, int (&tk)[NI]) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i) tok[i] = __builtin_amdgcn_ds_bpermute((4 * i + grp) << 2, my_tok);
+    for (int i = 0; i < NI; ++i) tk[i] = __builtin_amdgcn_ds_bpermute((4 * i + grp) << 2, my_tok);
+  };
 
   const uint16_t* kb = key + b * sb + j * sh + cc * 8;
   const uint16_t* vb = value + b * sb + j * sh + cc * 8;
-  uint4 kx[NI], vx[NI];
+  // Invalid slots load token 0 of the row (in bounds) and are masked later.
+  auto load_kv = [&](const int (&tk)[NI], uint4 (&kx)[NI], uint4 (&vx)[NI]) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    kx[i] = make_uint4(0, 0, 0, 0);
-    if (tok[i] >= 0) kx[i] = ld_nt(kb + static_cast<int64_t>(tok[i]) * st);
-  }
+    for (int i = 0; i < NI; ++i) kx[i] = ld_nt(kb + static_cast<int64_t>(max(tk[i], 0)) * st);
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    vx[i] = make_uint4(0, 0, 0, 0);
-    if (tok[i] >= 0) vx[i] = ld_nt(vb + static_cast<int64_t>(tok[i]) * st);
-  }
+    for (int i = 0; i < NI; ++i) vx[i] = ld_nt(vb + static_cast<int64_t>(max(tk[i], 0)) * st);
+  };
+
   uint4 qx[G];
   const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * kD + cc * 8;
 #pragma unroll
   for (int h = 0; h < G; ++h) qx[h] = *reinterpret_cast<const uint4*>(qrow + h * kD);
 
-  // Scores (log2 domain) and the wave max per head.
-  float s[G][NI];
-  float m[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) m[h] = ninf;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float a = dot2_bf16(qx[h].x, kx[i].x, 0.0f);
-      a = dot2_bf16(qx[h].y, kx[i].y, a);
-      a = dot2_bf16(qx[h].z, kx[i].z, a);
-      a = dot2_bf16(qx[h].w, kx[i].w, a);
-      a = row16_sum(a) * scale_log2;
-      s[h][i] = tok[i] >= 0 ? a : ninf;
-      m[h] = fmaxf(m[h], s[h][i]);
-    }
-  }
+  // Running state of this lane's token group: max (log2 domain), sum, P.V.
+  float m[G], l[G], acc[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    m[h] = fmaxf(m[h], shfl_xor(m[h], 16));
-    m[h] = fmaxf(m[h], shfl_xor(m[h], 32));
-  }
-
-  // p = 2^(s - m); per-group sums and P.V over this lane's 8 channels.
-  float acc[G][8];
-  float l[G];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
+    m[h] = ninf;
     l[h] = 0.0f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[h][c] = 0.0f;
   }
+
+  auto compute = [&](const int (&tk)[NI], const uint4 (&kx)[NI], const uint4 (&vx)[NI]) {
+    float s[G][NI], cm[G];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    float v[8];
-    v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
-    v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
-    v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
-    v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
+    for (int h = 0; h < G; ++h) cm[h] = ninf;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float a = dot2_bf16(qx[h].x, kx[i].x, 0.0f);
+        a = dot2_bf16(qx[h].y, kx[i].y, a);
+        a = dot2_bf16(qx[h].z, kx[i].z, a);
+        a = dot2_bf16(qx[h].w, kx[i].w, a);
+        a = row16_sum(a) * scale_log2;
+        s[h][i] = tk[i] >= 0 ? a : ninf;
+        cm[h] = fmaxf(cm[h], s[h][i]);
+      }
+    }
+    // Rescale the group's state to the new maximum.  A group that has seen no
+    // valid token keeps m = -inf; its exponent base is 0 so every p is 0.
+    float ms[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float p = (s[h][i] == ninf) ? 0.0f : exp2f(s[h][i] - m[h]);
-      l[h] += p;
+      const float mn = fmaxf(m[h], cm[h]);
+      ms[h] = (mn == ninf) ? 0.0f : mn;
+      const float al = exp2f(m[h] - ms[h]);   // 0 while m = -inf
+      l[h] *= al;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) acc[h][c] = __builtin_fmaf(p, v[c], acc[h][c]);
+      for (int c = 0; c < 8; ++c) acc[h][c] *= al;
+      m[h] = mn;
     }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float v[8];
+      v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
+      v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
+      v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
+      v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float p = exp2f(s[h][i] - ms[h]);   // 0 for masked slots
+        l[h] += p;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[h][c] = __builtin_fmaf(p, v[c], acc[h][c]);
+      }
+    }
+    // The chunk is done here: its K/V registers are free for the next one.
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      pin(l[h]);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) pin(acc[h][c]);
+    }
+  };
+
+  // Chunk pipeline: ids(c+2) and K/V(c+1) in flight while chunk c computes.
+  uint4 kx[2][NI], vx[2][NI];
+  int tk[2][NI];
+  int id_next = -1;
+  {
+    const int id0 = load_id(0);
+    if (ITERS > 1) id_next = load_id(1);
+    spread(token_of(0, id0), tk[0]);
+    load_kv(tk[0], kx[0], vx[0]);
+  }
+  // Chunk c+1's loads go out only after chunk c-1 is computed (zero_after on
+  // its state), so at most two chunks of K/V occupy registers; the
+  // scheduling barriers keep them ahead of chunk c's arithmetic.
+#pragma unroll
+  for (int c = 0; c < ITERS; ++c) {
+    const int cur = c & 1, nxt = cur ^ 1;
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < ITERS) {
+      const int dz = c > 0 ? zero_after(l[0]) : 0;
+      const int tn = token_of(c + 1, id_next + dz);
+      if (c + 2 < ITERS) id_next = load_id(c + 2 + dz);
+      spread(tn, tk[nxt]);
+      load_kv(tk[nxt], kx[nxt], vx[nxt]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compute(tk[cur], kx[cur], vx[cur]);
   }
 
-  // The four token groups of a wave share the wave max: sum them in
-  // registers, then combine the four waves through LDS.
+  // Combine the wave's four token groups: common max, rescale, sum.
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    l[h] += shfl_xor(l[h], 16);
-    l[h] += shfl_xor(l[h], 32);
+    const float mw = max_x32(max_x16(m[h]));
+    const float f = (m[h] == ninf) ? 0.0f : exp2f(m[h] - mw);
+    l[h] = sum_x32(sum_x16(l[h] * f));
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      acc[h][c] += shfl_xor(acc[h][c], 16);
-      acc[h][c] += shfl_xor(acc[h][c], 32);
-    }
+    for (int c = 0; c < 8; ++c) acc[h][c] = sum_x32(sum_x16(acc[h][c] * f));
+    m[h] = mw;
   }
   if (grp == 0) {
 #pragma unroll
@@ -263,51 +362,80 @@ __global__ __launch_bounds__(kNT) void sparse_attn_kernel(
   __syncthreads();
   if (!last_flag) return;
 
-  // Last workgroup of the row: merge the splits, MS at a time with every load
-  // in flight before any arithmetic.
-  constexpr int MS = 8;
-  for (int idx = tid; idx < G * kD; idx += kNT) {
-    const int h = idx / kD;
-    const float* ml = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2 + h * 2;
-    const float* pa = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD + idx;
-    float mx = ninf, den = 0.0f, o = 0.0f;
-    for (int i0 = 0; i0 < nsplit; i0 += MS) {
-      float mi[MS], li[MS], ai[MS];
+  // Last workgroup of the row: merge the splits.  Thread t owns outputs
+  // t + 256k; the (max, sum, weighted V) loads of MS splits of every owned
+  // output are all issued before any arithmetic.
+  constexpr int OPT = (G * kD + kNT - 1) / kNT;
+  constexpr int MS = OPT >= 4 ? 4 : 16 / OPT;   // splits per batch of loads
+  float mx[OPT], den[OPT], o[OPT];
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    mx[k] = ninf;
+    den[k] = 0.0f;
+    o[k] = 0.0f;
+  }
+  const float* ml_row = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2;
+  const float* acc_row = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD;
+  for (int i0 = 0; i0 < nsplit; i0 += MS) {
+    float mi[OPT][MS], li[OPT][MS], ai[OPT][MS];
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int idx = min(tid + k * kNT, G * kD - 1);
+      const int h = idx / kD;
 #pragma unroll
       for (int u = 0; u < MS; ++u) {
         const int i = min(i0 + u, nsplit - 1);
-        mi[u] = ld_coherent(ml + i * G * 2);
-        li[u] = ld_coherent(ml + i * G * 2 + 1);
-        ai[u] = ld_coherent(pa + static_cast<int64_t>(i) * G * kD);
+        ai[k][u] = ld_coherent(acc_row + static_cast<int64_t>(i) * G * kD + idx);
+        mi[k][u] = ld_coherent(ml_row + (i * G + h) * 2);
+        li[k][u] = ld_coherent(ml_row + (i * G + h) * 2 + 1);
       }
-      float m2 = mx;
+    }
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      float m2 = mx[k];
 #pragma unroll
       for (int u = 0; u < MS; ++u)
-        if (i0 + u < nsplit) m2 = fmaxf(m2, mi[u]);
+        if (i0 + u < nsplit) m2 = fmaxf(m2, mi[k][u]);
       if (m2 == ninf) continue;
-      const float c = (mx == ninf) ? 0.0f : exp2f(mx - m2);
-      den *= c;
-      o *= c;
+      const float c = (mx[k] == ninf) ? 0.0f : exp2f(mx[k] - m2);
+      den[k] *= c;
+      o[k] *= c;
 #pragma unroll
       for (int u = 0; u < MS; ++u) {
-        if (i0 + u < nsplit && mi[u] != ninf) {
-          const float w = exp2f(mi[u] - m2);
-          den = __builtin_fmaf(li[u], w, den);
-          o = __builtin_fmaf(ai[u], w, o);
+        if (i0 + u < nsplit && mi[k][u] != ninf) {
+          const float w = exp2f(mi[k][u] - m2);
+          den[k] = __builtin_fmaf(li[k][u], w, den[k]);
+          o[k] = __builtin_fmaf(ai[k][u], w, o[k]);
         }
       }
-      mx = m2;
+      mx[k] = m2;
     }
-    o = (mx == ninf) ? 0.0f : o / den;
-    out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(o);
+  }
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    const int idx = tid + k * kNT;
+    if (idx < G * kD) {
+      const float v = (mx[k] == ninf) ? 0.0f : o[k] / den[k];
+      out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(v);
+    }
   }
 }
 
-// Token slots per wave / 4 (128 slots per workgroup: measured faster than 256 at cfg2).
-constexpr int ni_for(int64_t g) { return 8; }
+// 4-token steps per wave chunk: 8 while the G heads' state leaves room for
+// two chunks of K/V in registers, 4 above that.
+constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 
-int64_t splits_for(int64_t n_sel, int64_t block, int64_t g) {
-  return cdiv(n_sel * block, 16 * ni_for(g));
+// Chunks per wave: doubled while the grid keeps QKV_ATTN_TARGET_WGS
+// workgroups, so long selections take few splits per row.
+int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
+  const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
+  int it = 1;
+  while (it < kMaxIters && rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS) it *= 2;
+  return it;
+}
+
+int64_t splits_for(int64_t rows, int64_t n_slots, int64_t g) {
+  return cdiv(n_slots, 4 * 4 * ni_for(g) * iters_for(rows, n_slots, g));
 }
 
 }  // namespace
@@ -319,12 +447,12 @@ QKV_EXPORT int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q
                                                         int64_t kv_heads, int64_t head_dim,
                                                         int64_t n_sel, int64_t block) {
   if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads || head_dim != kD || n_sel <= 0 ||
-      block <= 0 || n_sel * block >= (int64_t(1) << 31))
+      block <= 0 || n_sel * block >= (int64_t(1) << 30))
     return -1;
   const int64_t g = q_heads / kv_heads;
   const int64_t rows = batch * kv_heads;
   // tickets, then per split: weighted V per head, then (max, sum) per head
-  return 4 * (kTicketWords + rows * splits_for(n_sel, block, g) * g * (kD + 2));
+  return 4 * (kTicketWords + rows * splits_for(rows, n_sel * block, g) * g * (kD + 2));
 }
 
 QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const void* value,
@@ -343,8 +471,9 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
     return fail(QKV_ERR_UNSUPPORTED, "qkv_sparse_attention: group size %lld not built", (long long)g);
   if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many rows");
   if (tokens <= 0 || tokens >= (int64_t(1) << 31) || n_sel <= 0 || block <= 0 ||
-      n_sel * block >= (int64_t(1) << 31))
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: need tokens > 0, n_sel > 0, block > 0");
+      n_sel * block >= (int64_t(1) << 30))
+    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: need tokens > 0, n_sel > 0, block > 0, "
+                                 "n_sel * block < 2^30");
   if (!aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16) ||
       (kv_strides[0] | kv_strides[1] | kv_strides[2]) % 8)
     return fail(QKV_ERR_INVALID, "qkv_sparse_attention: q/K/V rows must be 16-byte aligned");
@@ -353,7 +482,9 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
     return fail(QKV_ERR_INVALID, "qkv_sparse_attention: workspace needs %lld bytes, got %lld",
                 (long long)need, (long long)workspace_bytes);
   const int64_t rows = batch * kv_heads;
-  const int64_t nsplit = splits_for(n_sel, block, g);
+  const int64_t n_slots = n_sel * block;
+  const int iters = iters_for(rows, n_slots, g);
+  const int64_t nsplit = splits_for(rows, n_slots, g);
   if (nsplit > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many selected blocks");
   uint32_t* tickets = reinterpret_cast<uint32_t*>(workspace);
   float* ws_acc = workspace + kTicketWords;
@@ -366,17 +497,25 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   const uint16_t* k = static_cast<const uint16_t*>(key);
   const uint16_t* v = static_cast<const uint16_t*>(value);
   uint16_t* o = static_cast<uint16_t*>(out);
-#define QKV_ATTN(GG)                                                                                   \
-  sparse_attn_kernel<GG, ni_for(GG)><<<grid, kNT, 0, st>>>(                                            \
-      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                 \
-      static_cast<int>(kv_heads), tokens, block_ids, static_cast<int>(n_sel), static_cast<int>(block), \
-      nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o)
-  switch (g) {
-    case 1: QKV_ATTN(1); break;
-    case 2: QKV_ATTN(2); break;
-    case 4: QKV_ATTN(4); break;
-    default: QKV_ATTN(8); break;
+#define QKV_ATTN(GG, IT)                                                                                   \
+  sparse_attn_kernel<GG, ni_for(GG), IT><<<grid, kNT, 0, st>>>(                                             \
+      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                     \
+      static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),            \
+      static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o)
+#define QKV_ATTN_G(GG)                  \
+  switch (iters) {                      \
+    case 1: QKV_ATTN(GG, 1); break;     \
+    case 2: QKV_ATTN(GG, 2); break;     \
+    case 4: QKV_ATTN(GG, 4); break;     \
+    default: QKV_ATTN(GG, 8); break;    \
   }
+  switch (g) {
+    case 1: QKV_ATTN_G(1); break;
+    case 2: QKV_ATTN_G(2); break;
+    case 4: QKV_ATTN_G(4); break;
+    default: QKV_ATTN_G(8); break;
+  }
+#undef QKV_ATTN_G
 #undef QKV_ATTN
   return check_launch("qkv_sparse_attention");
 }

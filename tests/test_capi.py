@@ -78,13 +78,28 @@ def test_host_side_validation(call, msg):
     assert msg in _err()
 
 
+def _attn_splits(rows, n_slots, g, target=1024):
+    """Splits per row of qkv_sparse_attention: a workgroup round covers
+    4 waves x 4*NI slots (NI = 8 for G <= 2, else 4); chunks per wave double
+    (up to 8) while the grid keeps at least ``target`` workgroups."""
+    per_iter = 16 * (8 if g <= 2 else 4)
+    it = 1
+    while it < 8 and rows * -(-n_slots // (per_iter * it * 2)) >= target:
+        it *= 2
+    return -(-n_slots // (per_iter * it))
+
+
 def test_workspace_size_formula():
-    # 65536 ticket words + rows * splits * G * (D + 2) floats;
-    # splits = ceil(n_sel * block / 128 token slots)
+    # 65536 ticket words + rows * splits * G * (D + 2) floats
     t = 65536
-    assert lib.qkv_sparse_attention_workspace_bytes(8, 16, 8, 128, 128, 16) == 4 * (t + 64 * 16 * 2 * 130)
-    assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 128, 256, 1) == 4 * (t + 8 * 2 * 2 * 130)
-    assert lib.qkv_sparse_attention_workspace_bytes(1, 64, 8, 128, 300, 1) == 4 * (t + 8 * 3 * 8 * 130)
+    assert _attn_splits(64, 2048, 2) == 16            # cfg2: 16 splits of 128 slots
+    assert _attn_splits(256, 4096, 4) == 8            # cfg3: 8 splits of 512 slots
+    assert _attn_splits(8, 300, 8) == 5
+    for b, hq, hkv, n_sel, block in [(8, 16, 8, 128, 16), (1, 16, 8, 256, 1), (1, 64, 8, 300, 1),
+                                     (32, 32, 8, 256, 16), (8, 16, 8, 2048, 16), (1, 8, 8, 7, 64)]:
+        rows, g = b * hkv, hq // hkv
+        want = 4 * (t + rows * _attn_splits(rows, n_sel * block, g) * g * 130)
+        assert lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, block) == want
     assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 64, 256, 1) == -1
 
 

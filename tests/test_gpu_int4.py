@@ -223,6 +223,39 @@ def test_sparse_attention_matches_fp64(g_size, block, nsel):
     assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("g_size,batch,t,block,nsel", [
+    (2, 8, 20000, 16, 1024),    # 64 rows x 16384 slots: 8 chunks per wave, 16 splits
+    (2, 4, 9000, 16, 512),      # 32 rows x 8192 slots: 2 chunks per wave
+    (4, 4, 9000, 16, 512),      # G = 4 (4-token steps): 4 chunks per wave
+    (8, 4, 20000, 1, 4000),     # G = 8, block 1, slots not a multiple of a chunk
+    (1, 8, 20000, 64, 300),     # G = 1
+])
+def test_sparse_attention_long_selections(g_size, batch, t, block, nsel):
+    # Long selections take several chunks per wave and few splits per row;
+    # sampled rows are checked against fp64 (rows are independent).
+    hkv = 8
+    hq = hkv * g_size
+    gen = torch.Generator().manual_seed(g_size * 31 + nsel)
+    q = torch.randn((batch, hq, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    k = (torch.randn((batch, hkv, t, 128), generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    v = torch.randn((batch, hkv, t, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    nb = -(-t // block)
+    rows = batch * hkv
+    sel = torch.stack([torch.randperm(nb, generator=gen)[:nsel].sort().values for _ in range(rows)])
+    sel = sel.view(batch, hkv, nsel).to(torch.int32)
+    sel[0, 0, :5] = -1                  # invalid ids are skipped
+    sel[0, 0, 7] = nb + 3               # ids past the last block too
+    sel[-1, -1, -1] = nb - 1            # the partial last block
+    out = K.sparse_attention(q, k, v, sel.to(DEV), block, t, 128 ** -0.5)
+    got = f32(out)
+    for r in (0, rows // 2, rows - 1):
+        bi, j = divmod(r, hkv)
+        want = O.sparse_attention(f32(q[bi:bi + 1, j * g_size:(j + 1) * g_size]), f32(k[bi:bi + 1, j:j + 1]),
+                                  f32(v[bi:bi + 1, j:j + 1]), sel[bi:bi + 1, j:j + 1].numpy(), block, t,
+                                  128 ** -0.5)
+        np.testing.assert_allclose(got[bi, j * g_size:(j + 1) * g_size], want[0], rtol=RTOL, atol=ATOL)
+
+
 def test_sparse_attention_workspace_reuse():
     # One zero-filled workspace serves successive calls with different split
     # counts: the row tickets return to zero after every call.
