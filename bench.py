@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark of the int4 sparse-attention KV-retrieval decode step on one MI355X.
+"""Benchmark of the int4 sparse-attention KV-retrieval path on one MI355X.
 
-A "step" is one decode step of every layer of the workload: per layer, the
-fused int4 scoring + block max kernel, the top-k kernel and the GQA sparse
-attention (partial + merge).  Inputs (K/V bf16, int4 packed K, subset slab,
-q) are generated and quantized before the timed region and stay resident in
-HBM; every layer has its own buffers, so a step streams far more than the
-256 MB Infinity Cache.  The step is captured once in a HIP graph and
-replayed.
+Decode configs (cfg1-cfg4; default cfg2): a "step" is one decode step of
+every layer of the workload: per layer, the fused int4 scoring + block max
+kernel, the top-k kernel and the GQA sparse attention.  Inputs (K/V bf16,
+int4 packed K, subset slab, q) are generated and quantized before the timed
+region and stay resident in HBM; every layer has its own buffers, so a step
+streams far more than the 256 MB Infinity Cache.  The step is captured once
+in a HIP graph and replayed.  value = keys scored per second over the whole
+step, where a key is one (sequence, KV head, token) row; "roofline" is the
+scoring kernel's achieved algorithmic GB/s (HIP events around graph-replayed
+launches of that kernel alone) against 8 TB/s.  cfg4 also reports the
+recall of its planted keys at k = 64, 256, 1024 tokens.
 
-Prints ONE JSON line (the driver contract): value = keys scored per second
-over the whole step, where a key is one (sequence, KV head, token) row.
-"roofline" is the scoring kernel's achieved algorithmic GB/s (HIP events
-around graph-replayed launches of that kernel alone) against 8 TB/s.
-"cpu_baseline" is the reference's PyTorch CPU op sequence (restated in
-oracle/ref_semantics.py) timed on the host cores on a bounded sample.
+cfg5 (chunked prefill): a step is one layer's block selection for a chunk of
+2048 queries against 65536 cached int4 keys (int8 query quantization, int8
+MFMA block scores with the causal mask, top-64 blocks per query row), over
+rotating per-layer buffers; value = (query head, visible key) pairs scored
+per second; "roofline" is the MFMA scoring kernel's algorithmic int8 ops
+per second against the 5.0 POP/s dense int8 peak.
+
+"cpu_baseline" is timed on the host cores on a bounded sample: for decode
+the reference's PyTorch op sequence (restated in oracle/ref_semantics.py),
+for prefill the numpy restatement of the scoring (oracle/qkv_oracle.py).
+Prints ONE JSON line (the driver contract).
 """
 
 from __future__ import annotations
@@ -32,6 +41,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
 METRIC = "int4 partial-QK keys scored/s + HBM GB/s % of peak; sparse decode µs/layer"
 
 
@@ -40,7 +50,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4"])
+    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    p.add_argument("--layers", type=int, default=None,
+                   help="layer buffers to rotate through (default: the config's layer count, at least 8)")
     p.add_argument("--kernel-reps", type=int, default=20, help="graph replays for per-kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -150,24 +162,70 @@ def main() -> int:
         log(f"bench.py measures one GPU only (got --gpus {args.gpus}); this path shards per "
             "(sequence, KV head) without exchange and is not run across GPUs here")
         return 2
+    import torch
 
+    torch.cuda.set_device(0)
+    if args.config == "cfg5":
+        line = run_prefill(args)
+    else:
+        line = run_decode(args)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def copy_probe(mb: int) -> None:
+    """Plain device copies of a known size (HBM counter calibration)."""
+    import torch
+
+    if mb:
+        n = mb * 2**20 // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+
+def planted_recall(cfg, qs, caches, planted, ks=(64, 256, 1024)) -> dict:
+    """Fraction of (layer, row) planted keys inside the top-k tokens of the
+    decode scoring, per k (OV:260-322's hits / true-count, one planted key)."""
+    import torch
+
+    from kv_cache_amd import int4 as K
+
+    hits = {k: 0 for k in ks}
+    total = 0
+    for q, c, pl in zip(qs, caches, planted):
+        bmax = K.decode_scores(q, c.chan_idx, c.slab, c.slab_scales, cfg.tokens, cfg.block)
+        for k in ks:
+            sel = K.block_topk(bmax, k // cfg.block)                        # [B, Hkv, k/block] block ids
+            first = sel.to(torch.int64) * cfg.block
+            inside = (pl[..., None] >= first) & (pl[..., None] < first + cfg.block)
+            hits[k] += int(inside.any(dim=-1).sum())
+        total += pl.numel()
+    return {str(k): hits[k] / total for k in ks}
+
+
+def run_decode(args) -> dict:
     import torch
 
     from kv_cache_amd import int4 as K
     from kv_cache_amd.workloads import CONFIGS, make_layer
 
-    torch.cuda.set_device(0)
     cfg = CONFIGS[args.config]
-    layers, rows, T = cfg.layers, cfg.rows, cfg.tokens
+    # Single-layer configs rotate 8 distinct layer buffers (seeds seed..seed+7)
+    # so that repeated steps do not run out of the 256 MB Infinity Cache.
+    layers, rows, T = (args.layers or max(cfg.layers, 8)), cfg.rows, cfg.tokens
     log(f"[bench] setup {cfg.name}: {layers} layers, rows={rows}, T={T}, S={cfg.selected}, "
         f"block={cfg.block}, top-{cfg.topk}")
-    qs, ks, vs, caches = [], [], [], []
+    qs, ks, vs, caches, planted = [], [], [], [], []
     for layer in range(layers):
-        q, k, v, _ = make_layer(cfg, layer, device="cuda")
+        q, k, v, pl = make_layer(cfg, layer, device="cuda")
         caches.append(K.Int4KCache.from_prefill(k, cfg.group, cfg.selected))
         qs.append(q)
         ks.append(k)
         vs.append(v)
+        planted.append(pl)
     torch.cuda.synchronize()
     log(f"[bench] resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
 
@@ -184,7 +242,7 @@ def main() -> int:
 
     def run_topk():
         for _ in range(layers):
-            K.block_topk(step.bmax, cfg.topk, out=step.sel)
+            K.block_topk(step.bmax, cfg.topk, out=step.sel, workspace=step.topk_ws)
 
     def run_attn():
         for layer in range(layers):
@@ -206,8 +264,18 @@ def main() -> int:
     torch.cuda.synchronize()
     log("[bench] warmup done")
 
-    replay = run_step if args.eager else graph_of(run_step).replay
-    ms_per_step = time_replays(replay, args.steps)
+    # A graph of a few launches would time the host's graph launch, not the
+    # GPU: short workloads are repeated inside the graph (>= 28 layer steps).
+    reps = max(1, -(-28 // layers))
+
+    def repeated(fn):
+        def run():
+            for _ in range(reps):
+                fn()
+        return run
+
+    replay = run_step if args.eager else graph_of(repeated(run_step)).replay
+    ms_per_step = time_replays(replay, args.steps) / (1 if args.eager else reps)
     log(f"[bench] step: {ms_per_step:.3f} ms ({ms_per_step * 1e3 / layers:.1f} us/layer)")
 
     kernels = {}
@@ -220,8 +288,8 @@ def main() -> int:
         ("dense_bf16_attention", run_dense, rows * T * cfg.head_dim * 2 * 2),
     ]
     for name, fn, nbytes in plan:
-        g = graph_of(fn)
-        ms = time_replays(g.replay, args.kernel_reps) / layers
+        g = graph_of(repeated(fn))
+        ms = time_replays(g.replay, args.kernel_reps) / (layers * reps)
         kernels[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes,
                          "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
@@ -229,13 +297,11 @@ def main() -> int:
 
     for _ in range(args.profile_steps):
         run_step()
-    if args.copy_probe_mb:
-        n = args.copy_probe_mb * 2**20 // 4
-        src = torch.ones(n, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
     torch.cuda.synchronize()
+    copy_probe(args.copy_probe_mb)
+    recall = planted_recall(cfg, qs, caches, planted) if cfg.planted else None
+    if recall:
+        log(f"[bench] planted-key recall at k tokens: {recall}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -278,8 +344,139 @@ def main() -> int:
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
-    return 0
+    if recall:
+        line["planted_recall"] = recall
+    return line
+
+
+def cpu_baseline_prefill(cfg, budget_s: float) -> dict:
+    """The numpy restatement of prefill block scoring (oracle/qkv_oracle.py)
+    on the host cores, for a few query rows of one head against all keys."""
+    import numpy as np
+    import torch
+
+    from kv_cache_amd.workloads import make_prefill
+    from oracle import qkv_oracle as O
+
+    q, k = make_prefill(cfg, device="cpu")
+    kp, ks = O.int4_pack_k(k[:, :1].float().numpy(), 128)
+    rows = q[:, :1, -4:].float().numpy()                        # the chunk's last 4 queries of head 0
+    q8, _ = O.quantize_query_rows(rows)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        bm = O.prefill_block_scores(q8, kp, ks[..., 0], cfg.block, cfg.tokens - 4)
+        O.prefill_block_topk(bm, cfg.topk)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    pairs = sum(min(cfg.tokens, cfg.tokens - 4 + i + 1) for i in range(4))
+    return {
+        "value": pairs / med,
+        "unit": "query-key pairs/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"4 query rows x {cfg.tokens} int4 keys of one head: numpy int64 scoring, causal block-64 "
+                   f"max, top-{cfg.topk}; median of {len(times)} calls = {med * 1e3:.1f} ms"),
+    }
+
+
+def run_prefill(args) -> dict:
+    import torch
+
+    from kv_cache_amd import int4 as K
+    from kv_cache_amd import prefill as P
+    from kv_cache_amd.workloads import PREFILL, make_prefill
+
+    cfg = PREFILL
+    layers = args.layers or 8
+    nb = cfg.n_blocks
+    log(f"[bench] setup {cfg.name}: {layers} layer buffers, {cfg.queries} queries x {cfg.tokens} keys, "
+        f"{cfg.q_heads}/{cfg.kv_heads} heads, block {cfg.block}, top-{cfg.topk}, q_pos0 {cfg.q_pos0}")
+    qs, packs, scs = [], [], []
+    for layer in range(layers):
+        q, k = make_prefill(cfg, device="cuda")
+        q = q + 0.0 * layer   # distinct buffers per layer, same values
+        packed, scales = K.int4_pack_k(k, 128)
+        del k
+        qs.append(q.contiguous())
+        packs.append(packed)
+        scs.append(scales)
+    q8 = torch.empty((cfg.batch, cfg.q_heads, cfg.queries, 128), dtype=torch.int8, device="cuda")
+    bmax = torch.empty((cfg.batch, cfg.q_heads, cfg.queries, nb), dtype=torch.float32, device="cuda")
+    sel = torch.empty((cfg.batch, cfg.q_heads, cfg.queries, cfg.topk), dtype=torch.int32, device="cuda")
+    q8s = [P.quantize_query(qs[layer])[0] for layer in range(layers)]
+    torch.cuda.synchronize()
+
+    def run_step():
+        for layer in range(layers):
+            q8l, _ = P.quantize_query(qs[layer])
+            P.block_scores(q8l, packs[layer], scs[layer], cfg.tokens, cfg.q_pos0, bmax=bmax)
+            P.block_topk(bmax, cfg.topk, out=sel)
+
+    def run_scores():
+        for layer in range(layers):
+            P.block_scores(q8s[layer], packs[layer], scs[layer], cfg.tokens, cfg.q_pos0, bmax=bmax)
+
+    def run_topk():
+        for _ in range(layers):
+            P.block_topk(bmax, cfg.topk, out=sel)
+
+    for _ in range(args.warmup):
+        run_step()
+    torch.cuda.synchronize()
+    replay = run_step if args.eager else graph_of(run_step).replay
+    ms_per_step = time_replays(replay, args.steps) / layers
+    ops = cfg.int_ops()
+    pairs = cfg.batch * cfg.q_heads * cfg.visible_keys()
+    kernels = {}
+    for name, fn in [("prefill_block_scores", run_scores), ("prefill_block_topk", run_topk)]:
+        g = graph_of(fn)
+        ms = time_replays(g.replay, args.kernel_reps) / layers
+        kernels[name] = {"us_per_launch": ms * 1e3}
+        del g
+    sc_ms = kernels["prefill_block_scores"]["us_per_launch"] * 1e-3
+    kernels["prefill_block_scores"]["tops"] = ops / (sc_ms * 1e-3) / 1e12
+    log(f"[bench] layer step {ms_per_step * 1e3:.1f} us; scores {sc_ms * 1e3:.1f} us = "
+        f"{kernels['prefill_block_scores']['tops']:.0f} TOP/s; top-k {kernels['prefill_block_topk']['us_per_launch']:.1f} us")
+    for _ in range(args.profile_steps):
+        run_step()
+    torch.cuda.synchronize()
+    copy_probe(args.copy_probe_mb)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_prefill(cfg, args.cpu_seconds)
+    achieved = kernels["prefill_block_scores"]["tops"]
+    return {
+        "metric": METRIC,
+        "value": pairs / (ms_per_step * 1e-3),
+        "unit": "query-key pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i32 (int8 query x int4 K)",
+        "data": "synthetic (seeded N(0,1) q/K, 4 outlier channels x8)",
+        "config": {
+            "workload": f"cfg5: {cfg.name}", "batch": cfg.batch, "q_heads": cfg.q_heads,
+            "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "queries": cfg.queries, "context": cfg.tokens,
+            "q_pos0": cfg.q_pos0, "block": cfg.block, "topk_blocks": cfg.topk, "layer_buffers": layers,
+            "graph": not args.eager,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "prefill_scores_kernel (v_mfma_i32_16x16x64_i8, causal block-64 max)",
+            "achieved": achieved,
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s (int8)",
+            "frac": achieved / INT8_PEAK_TOPS,
+            "traffic": read_traffic("cfg5", "prefill_scores_kernel"),
+            "ops_per_launch": ops,
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
 
 
 if __name__ == "__main__":

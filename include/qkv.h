@@ -164,6 +164,19 @@ int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, in
 int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
              int32_t* out, void* stream);
 
+/* Bytes of workspace qkv_topk_ws needs: 0 when qkv_topk's one workgroup per
+ * row is used (n <= 4096 or k > 1024), else two candidate buffers of
+ * rows * (k * ceil(n/4096)) (value, index) pairs; -1 for bad sizes. */
+int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
+
+/* qkv_topk with a caller-owned workspace (16-byte aligned, contents
+ * irrelevant): rows longer than 4096 keys with k <= 1024 are reduced in
+ * stages, each 4096-key chunk keeping its local top-k, until one chunk is
+ * left; the result equals qkv_topk's.  Same replaced call sites as
+ * qkv_topk (EV:4448 token-level top-k over long contexts). */
+int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Bytes of workspace qkv_sparse_attention needs for these sizes: 65536
  * uint32 row tickets (the same words for every call shape), then G*(D+2)
  * floats per split of 128 token slots. */

@@ -47,6 +47,8 @@ _PROTOTYPES = {
     "qkv_int4_decode_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64,
                                       _i64, _vp, _vp, _vp, _vp, _vp]),
     "qkv_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "qkv_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "qkv_topk_ws": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "qkv_prefill_quantize_query": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "qkv_prefill_block_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         _vp, _vp]),

@@ -1,4 +1,5 @@
-// Row-wise top-k with the lowest-index tie-break, one workgroup per row.
+// Row-wise top-k with the lowest-index tie-break: one workgroup per row, or,
+// for long rows, a staged reduction over 4096-key chunks (topk_stage_kernel).
 //
 // The reference calls torch.topk over partial scores or block maxima
 // (evaluate_qwen3_top2_head_limit3_ppl.py:4448, 5046), whose tie order is
@@ -162,17 +163,18 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 // known from per-(slot, wave) ballot counts, so one pass places every key.
 // FINITE: keys equal to -inf are not selectable; a row with fewer than k
 // other keys selects them all and pads its output with -1.
+//
+// select_row runs the selection for one row inside a 256-thread workgroup:
+// it writes the positions of the kk selected keys, ascending, to sel (LDS,
+// 256*VPL entries) and returns kk (k, or with FINITE possibly fewer).  Every
+// thread of the workgroup must call it; it ends with a barrier.
 template <int VPL, bool FINITE>
-__global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict__ values, int n, int64_t ld,
-                                                        int k, int32_t* __restrict__ out) {
+__device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel) {
   __shared__ int hist[4][260];             // one copy per wave, padded across banks
   __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
   __shared__ uint32_t red[4][3];
   __shared__ int sh_bin, sh_kr, sh_whole;
-  __shared__ int32_t sel[256 * VPL];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = blockIdx.x;
-  const float* vals = values + static_cast<int64_t>(row) * ld;
 
   uint32_t u[VPL];
   bool valid[VPL];
@@ -298,9 +300,68 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
     if (take) sel[g0 + min(e0, kr) + __popcll(tb & below)] = i * 256 + tid;
   }
   __syncthreads();
-  int32_t* orow = out + static_cast<int64_t>(row) * k;
-  for (int j = tid; j < k; j += 256) orow[j] = j < kk ? sel[j] : -1;
+  return kk;
 }
+
+template <int VPL, bool FINITE>
+__global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict__ values, int n, int64_t ld,
+                                                        int k, int32_t* __restrict__ out) {
+  __shared__ int32_t sel[256 * VPL];
+  const int row = blockIdx.x;
+  const int kk = select_row<VPL, FINITE>(values + static_cast<int64_t>(row) * ld, n, k, sel);
+  int32_t* orow = out + static_cast<int64_t>(row) * k;
+  for (int j = threadIdx.x; j < k; j += 256) orow[j] = j < kk ? sel[j] : -1;
+}
+
+// ---------------------------------------------------------------------------
+// Staged top-k for long rows (n > kStageChunk, k <= kStageMaxK).  Stage s
+// splits each row of candidates into chunks of kStageChunk; a workgroup keeps
+// its chunk's local top-k (value and original index), so every key of the
+// row's top-k survives: a key beaten by fewer than k keys of the row is beaten
+// by fewer than k keys of its chunk (ties broken by position, and positions
+// follow the original index order).  Chunk c of a full stage writes its k
+// candidates at c*k, in ascending position order, so the candidate rows stay
+// in ascending original index order.  The last stage (one chunk) writes the
+// original indices of its top-k to out.
+// ---------------------------------------------------------------------------
+constexpr int kStageChunk = 4096;
+constexpr int kStageMaxK = 1024;
+
+__global__ __launch_bounds__(256) void topk_stage_kernel(const float* __restrict__ in_val,
+                                                         const int32_t* __restrict__ in_idx, int64_t in_ld,
+                                                         int n, int k, float* __restrict__ out_val,
+                                                         int32_t* __restrict__ out_idx, int64_t out_ld,
+                                                         int32_t* __restrict__ out) {
+  constexpr int VPL = kStageChunk / 256;
+  __shared__ int32_t sel[kStageChunk];
+  const int row = blockIdx.y, c = blockIdx.x;
+  const int base = c * kStageChunk;
+  const int len = min(kStageChunk, n - base);
+  const int kc = min(k, len);
+  const float* vals = in_val + static_cast<int64_t>(row) * in_ld + base;
+  const int32_t* idx = in_idx ? in_idx + static_cast<int64_t>(row) * in_ld + base : nullptr;
+  select_row<VPL, false>(vals, len, kc, sel);
+  if (out) {   // last stage: original indices, ascending
+    int32_t* orow = out + static_cast<int64_t>(row) * k;
+    for (int j = threadIdx.x; j < kc; j += 256) orow[j] = idx ? idx[sel[j]] : base + sel[j];
+    return;
+  }
+  const int64_t o = static_cast<int64_t>(row) * out_ld + static_cast<int64_t>(c) * k;
+  for (int j = threadIdx.x; j < kc; j += 256) {
+    const int pos = sel[j];
+    out_val[o + j] = vals[pos];
+    out_idx[o + j] = idx ? idx[pos] : base + pos;
+  }
+}
+
+// Candidates left after a stage over n keys: k from every full chunk, and
+// min(k, rest) from the last.
+int64_t stage_out(int64_t n, int64_t k) {
+  const int64_t c = cdiv(n, kStageChunk);
+  return (c - 1) * k + std::min<int64_t>(k, n - (c - 1) * kStageChunk);
+}
+
+bool staged(int64_t n, int64_t k) { return n > kStageChunk && k <= kStageMaxK; }
 
 template <bool FINITE>
 int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
@@ -340,6 +401,54 @@ QKV_EXPORT int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld
                                                     static_cast<int>(k), out);
   }
   return check_launch("qkv_topk");
+}
+
+QKV_EXPORT int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+  if (rows <= 0 || n <= 0 || k < 1 || k > n) return -1;
+  if (!staged(n, k)) return 0;
+  // two candidate buffers (value + index) sized for the first stage's output
+  return 2 * rows * stage_out(n, k) * static_cast<int64_t>(sizeof(float) + sizeof(int32_t));
+}
+
+QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!staged(n, k)) return qkv_topk(values, rows, n, ld, k, out, stream);
+  if (!values || !out || !workspace) return fail(QKV_ERR_INVALID, "qkv_topk_ws: null pointer");
+  if (rows <= 0 || rows > 65535 || ld < n || n >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "qkv_topk_ws: bad sizes rows=%lld n=%lld ld=%lld", (long long)rows,
+                (long long)n, (long long)ld);
+  const int64_t need = qkv_topk_workspace_bytes(rows, n, k);
+  if (workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "qkv_topk_ws: workspace needs %lld bytes, got %lld", (long long)need,
+                (long long)workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(QKV_ERR_INVALID, "qkv_topk_ws: workspace must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n1 = stage_out(n, k);
+  float* val_buf[2];
+  int32_t* idx_buf[2];
+  val_buf[0] = static_cast<float*>(workspace);
+  idx_buf[0] = reinterpret_cast<int32_t*>(val_buf[0] + rows * n1);
+  val_buf[1] = reinterpret_cast<float*>(idx_buf[0] + rows * n1);
+  idx_buf[1] = reinterpret_cast<int32_t*>(val_buf[1] + rows * n1);
+  const float* cur_val = values;
+  const int32_t* cur_idx = nullptr;
+  int64_t cur_ld = ld, cur_n = n;
+  int buf = 0;
+  while (true) {
+    const int64_t chunks = cdiv(cur_n, kStageChunk);
+    const bool last = chunks == 1;
+    dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
+    topk_stage_kernel<<<grid, 256, 0, st>>>(cur_val, cur_idx, cur_ld, static_cast<int>(cur_n), static_cast<int>(k),
+                                            last ? nullptr : val_buf[buf], last ? nullptr : idx_buf[buf], n1,
+                                            last ? out : nullptr);
+    if (int rc = check_launch("qkv_topk_ws")) return rc;
+    if (last) return QKV_OK;
+    cur_val = val_buf[buf];
+    cur_idx = idx_buf[buf];
+    cur_ld = n1;
+    cur_n = stage_out(cur_n, k);
+    buf ^= 1;
+  }
 }
 
 QKV_EXPORT int qkv_prefill_block_topk(const float* bmax, int64_t rows, int64_t n, int64_t ld, int64_t k,

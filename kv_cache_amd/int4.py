@@ -174,8 +174,18 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
     return bmax
 
 
-def block_topk(values: torch.Tensor, k: int, *, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Top-k indices along the last axis, lowest index wins ties, ascending order (int32)."""
+def topk_workspace(rows: int, n: int, k: int, device) -> torch.Tensor | None:
+    """Workspace for ``block_topk`` on rows of n values (None when not needed)."""
+    need = _lib.load().qkv_topk_workspace_bytes(int(rows), int(n), int(k))
+    _require(need >= 0, f"bad top-k sizes rows={rows} n={n} k={k}")
+    return torch.empty((need + 3) // 4, dtype=torch.float32, device=device) if need else None
+
+
+def block_topk(values: torch.Tensor, k: int, *, out: torch.Tensor | None = None,
+               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-k indices along the last axis, lowest index wins ties, ascending order (int32).
+    Rows longer than 4096 values use a staged selection with a workspace
+    (allocated here unless one from ``topk_workspace`` is passed)."""
     lib = _lib.load()
     _require(values.is_cuda and values.dtype == torch.float32, "values must be CUDA float32")
     n = values.size(-1)
@@ -184,9 +194,16 @@ def block_topk(values: torch.Tensor, k: int, *, out: torch.Tensor | None = None)
     rows = v2.size(0)
     if out is None:
         out = torch.empty((*values.shape[:-1], int(k)), dtype=torch.int32, device=values.device)
+    need = lib.qkv_topk_workspace_bytes(rows, n, int(k))
     with torch.cuda.device(values.device):
-        _lib.check(lib.qkv_topk(v2.data_ptr(), rows, n, v2.stride(0), int(k), out.data_ptr(),
-                                _lib.stream_of(values)))
+        if need > 0:
+            if workspace is None or workspace.numel() * 4 < need:
+                workspace = topk_workspace(rows, n, k, values.device)
+            _lib.check(lib.qkv_topk_ws(v2.data_ptr(), rows, n, v2.stride(0), int(k), out.data_ptr(),
+                                       workspace.data_ptr(), workspace.numel() * 4, _lib.stream_of(values)))
+        else:
+            _lib.check(lib.qkv_topk(v2.data_ptr(), rows, n, v2.stride(0), int(k), out.data_ptr(),
+                                    _lib.stream_of(values)))
     return out
 
 
@@ -281,6 +298,7 @@ class SparseDecodeStep:
         _require(1 <= topk <= nb, f"topk {topk} must be in [1, {nb}]")
         self.bmax = torch.empty((batch, kv_heads, nb), dtype=torch.float32, device=device)
         self.sel = torch.empty((batch, kv_heads, topk), dtype=torch.int32, device=device)
+        self.topk_ws = topk_workspace(batch * kv_heads, nb, topk, device)
         self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, topk, block, device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
 
@@ -288,6 +306,6 @@ class SparseDecodeStep:
                  scaling: float) -> torch.Tensor:
         decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.tokens, self.block,
                       bmax=self.bmax)
-        block_topk(self.bmax, self.topk, out=self.sel)
+        block_topk(self.bmax, self.topk, out=self.sel, workspace=self.topk_ws)
         return sparse_attention(query, key, value, self.sel, self.block, self.tokens, scaling,
                                 workspace=self.workspace, out=self.out)

@@ -180,7 +180,8 @@ def test_decode_scores_many_chunks():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n,k", [(5, 2), (100, 1), (100, 100), (2048, 128), (2048, 256), (4096, 256),
-                                 (5000, 999), (12288, 64), (20000, 1024), (131072, 1024)])
+                                 (5000, 999), (12288, 64), (20000, 1024), (131072, 1024),
+                                 (4097, 1), (4097, 1024), (8192, 1024), (300000, 1000), (20000, 1025)])
 def test_topk_matches_oracle(n, k):
     g = torch.Generator().manual_seed(n + k)
     vals = torch.randint(-50, 50, (6, n), generator=g).float()   # heavy ties
@@ -190,6 +191,22 @@ def test_topk_matches_oracle(n, k):
     vals[2, : n // 2] = -float("inf")
     got = K.block_topk(vals.to(DEV), k).cpu().numpy()
     assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
+def test_topk_staged_equals_single_workgroup():
+    # Rows longer than 4096 keys go through the staged reduction; qkv_topk
+    # (one workgroup per row) must give the same indices.
+    from kv_cache_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(77)
+    vals = torch.randint(-1000, 1000, (5, 70000), generator=g).float().to(DEV)
+    vals[1, 10000:] = -float("inf")
+    for k in (1, 64, 1024):
+        want = torch.empty((5, k), dtype=torch.int32, device=DEV)
+        _lib.check(lib.qkv_topk(vals.data_ptr(), 5, 70000, 70000, k, want.data_ptr(), _lib.stream_of(vals)))
+        assert lib.qkv_topk_workspace_bytes(5, 70000, k) > 0
+        got = K.block_topk(vals, k)
+        assert torch.equal(got, want)
 
 
 def test_topk_strided_rows():
