@@ -16,7 +16,9 @@
 // channels, w & 0xF0F0F0F0 for odd ones); the query rows are stored
 // pre-permuted (prefill_query_kernel) so that B byte slot s of lane group g
 // holds the same channel as A byte slot s.  The result is 16*I, and
-// fp32(scale/16) * fp32(16*I) equals fp32(scale) * fp32(I) exactly.
+// fp32(scale) * fp32(16*I), rounded once, is exactly 16 times
+// fp32(scale) * fp32(I), so block maxima are taken on 16*key and scaled
+// back by 1/16 (exact).
 // The output tile has lane l hold keys 4*(l/16)+i of query l%16: a block max
 // is an in-lane max plus two cross-row shuffles.
 #include "common.h"
@@ -76,11 +78,21 @@ __device__ __forceinline__ v4i unpack_half(uint32_t w0, uint32_t w1) {
 // Block scores.  Grid: x = key chunk (kChunkBlocks blocks), y = group of 4
 // (query tile, head) pairs of one KV head, z = (batch, KV head).  Each wave
 // owns one pair: kQTile query rows of one head, resident as B fragments, and
-// streams the chunk's keys.  No workgroup barrier: the 4 waves of a group
-// read the same keys (the other waves' loads hit in cache) and stage their
-// block maxima in their own LDS region before a coalesced write.
+// streams the chunk's blocks that its queries can see.  No workgroup barrier:
+// the 4 waves of a group read the same keys (the other waves' loads hit in
+// cache) and stage their block maxima in their own LDS region before a
+// coalesced write.
+//
+// Per block a wave loads the next block's codes and scales while it issues
+// the current block's 32 MFMAs back to back (the first half of every tile's
+// channels, then the second half, so dependent MFMAs are 4 apart) and then
+// runs the epilogue: 16*key = fp32(scale) * fp32(16*I) as one v_fma_f32 per
+// key on the biased int32 accumulator (below), maximum over the 16 keys a
+// lane holds with v_max3, then over the 4 row groups with VALU lane swaps,
+// times 1/16.  Only blocks on the causal diagonal or past the last token take the
+// masked epilogue (a wave-uniform branch).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prefill_scores_kernel(
+__global__ __launch_bounds__(256, 3) void prefill_scores_kernel(
     const int8_t* __restrict__ q8, const uint8_t* __restrict__ kpacked, const uint16_t* __restrict__ kscales,
     int q_heads, int kv_heads, int nq, int tokens, int64_t capacity, int q_pos0, int nb,
     float* __restrict__ bmax) {
@@ -117,59 +129,125 @@ __global__ __launch_bounds__(256) void prefill_scores_kernel(
 
   const int blk0 = blockIdx.x * kChunkBlocks;
   const int nblk = min(kChunkBlocks, nb - blk0);
+  // Blocks [0, nvis) of the chunk hold a key some query of the wave sees.
+  const int nvis = pos_hi < blk0 * kBlock ? 0 : min(nblk, (pos_hi - blk0 * kBlock) / kBlock + 1);
   const uint8_t* krow = kpacked + static_cast<int64_t>(bj) * capacity * (kD / 2);
   const uint16_t* srow = kscales + static_cast<int64_t>(bj) * capacity;
   const float ninf = -__builtin_huge_valf();
 
-  for (int kb = 0; kb < nblk; ++kb) {
+  // Lane l loads key (base + 16kt + l%16), channels 32g..32g+31, and the
+  // scales of the 4 keys its output rows hold (base + 16kt + 4g + i).  Every
+  // block below nb lies inside the capacity (a multiple of 64).
+  auto load_block = [&](int kb, uint4 (&ka)[4], uint2 (&ks)[4]) {
     const int base = (blk0 + kb) * kBlock;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      ka[kt] = *reinterpret_cast<const uint4*>(krow + static_cast<int64_t>(base + kt * 16 + col) * (kD / 2) + g * 16);
+      ks[kt] = *reinterpret_cast<const uint2*>(srow + base + kt * 16 + 4 * g);
+    }
+  };
+
+  // One block: two halves of 2 key tiles each (16 MFMAs, then their
+  // epilogue), which keeps the accumulators at 32 registers.
+  //
+  // Every accumulator starts at the bit pattern of 1.5 * 2^23, so the int32
+  // result 0x4B400000 + 16*I read as fp32 is exactly 12582912 + 16*I (|16*I|
+  // < 2^22).  Then fma(s, f, -12582912 * s) = round(s * 16*I): one rounding
+  // of the exact product, i.e. 16 times fp32(s) * fp32(I), with no integer
+  // conversion (-12582912 * s is exact: s has 11 significant bits).
+  const v4i kBias = v4i{0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
+  auto process = [&](int kb, const uint4 (&ka)[4], const uint2 (&ks)[4]) {
+    const int base = (blk0 + kb) * kBlock;
+    const bool need_mask = base + kBlock - 1 > pos_lo || base + kBlock > tokens;
     float run[kNT];
 #pragma unroll
     for (int n = 0; n < kNT; ++n) run[n] = ninf;
-    if (base <= pos_hi) {   // some key of the block is visible to some query
-      const bool need_mask = base + kBlock - 1 > pos_lo || base + kBlock > tokens;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = base + kt * 16 + col;
-        const uint4 raw = *reinterpret_cast<const uint4*>(krow + static_cast<int64_t>(key) * (kD / 2) + g * 16);
-        const v4i a0 = unpack_half(raw.x, raw.y);
-        const v4i a1 = unpack_half(raw.z, raw.w);
-        // scales of the 4 keys this lane's output rows hold: base + 16kt + 4g + i
-        const uint2 sraw = *reinterpret_cast<const uint2*>(srow + base + kt * 16 + 4 * g);
-        float s16[4];
-        s16[0] = f16bits_to_f32(sraw.x & 0xFFFFu) * 0.0625f;
-        s16[1] = f16bits_to_f32(sraw.x >> 16) * 0.0625f;
-        s16[2] = f16bits_to_f32(sraw.y & 0xFFFFu) * 0.0625f;
-        s16[3] = f16bits_to_f32(sraw.y >> 16) * 0.0625f;
+    for (int half = 0; half < 2; ++half) {
+      v4i acc[2][kNT];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int kt = 2 * half + u;
+        const v4i a0 = unpack_half(ka[kt].x, ka[kt].y);
+        const v4i a1 = unpack_half(ka[kt].z, ka[kt].w);
+#pragma unroll
+        for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], kBias, 0, 0, 0);
+#pragma unroll
+        for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc[u][n], 0, 0, 0);
+      }
+      // The fp16 scales feed v_fma_mix_f32 straight from their packed words.
+      _Float16 sc[2][4];
+      float cb[2][4];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint2 sr = ks[2 * half + u];
+        sc[u][0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x & 0xFFFFu));
+        sc[u][1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x >> 16));
+        sc[u][2] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y & 0xFFFFu));
+        sc[u][3] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y >> 16));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cb[u][i] = __builtin_fmaf(static_cast<float>(sc[u][i]), -12582912.0f, 0.0f);
+      }
+      auto key16 = [&](int u, int i, int a) -> float {
+        return __builtin_fmaf(static_cast<float>(sc[u][i]), __int_as_float(a), cb[u][i]);
+      };
+      if (!need_mask) {
 #pragma unroll
         for (int n = 0; n < kNT; ++n) {
-          v4i acc = v4i{0, 0, 0, 0};
-          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc, 0, 0, 0);
-          const int accs[4] = {acc.x, acc.y, acc.z, acc.w};
-          if (!need_mask) {
+          float m = run[n];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) run[n] = fmaxf(run[n], s16[i] * static_cast<float>(accs[i]));
-          } else {
-            const int qpos = q_pos0 + q0 + 16 * n + col;
+          for (int u = 0; u < 2; ++u) {
+            m = fmaxf(fmaxf(m, key16(u, 0, acc[u][n].x)), key16(u, 1, acc[u][n].y));
+            m = fmaxf(fmaxf(m, key16(u, 2, acc[u][n].z)), key16(u, 3, acc[u][n].w));
+          }
+          run[n] = m;
+        }
+      } else {
+        // Key t of the lane's rows is visible to query q when t <= pos(q) and
+        // t < tokens; lim = min(pos(q), tokens - 1) - (first key of the row
+        // group) compares once per key.
+#pragma unroll
+        for (int n = 0; n < kNT; ++n) {
+          const int lim = min(q_pos0 + q0 + 16 * n + col, tokens - 1) - (base + 4 * g);
+          float m = run[n];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int accs[4] = {acc[u][n].x, acc[u][n].y, acc[u][n].z, acc[u][n].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int t = base + kt * 16 + 4 * g + i;
-              const float v = s16[i] * static_cast<float>(accs[i]);
-              run[n] = fmaxf(run[n], (t <= qpos && t < tokens) ? v : ninf);
+              const float v = key16(u, i, accs[i]);
+              m = fmaxf(m, ((2 * half + u) * 16 + i <= lim) ? v : ninf);
             }
           }
+          run[n] = m;
         }
       }
     }
-    // Max over the 4 row groups; -0 (only from a zero scale) reads as +0.
+    // Max over the 4 row groups, back to key scale (exact); adding +0 turns
+    // a -0 into +0 and leaves every other value alone.
 #pragma unroll
     for (int n = 0; n < kNT; ++n) {
-      float m = run[n];
-      m = fmaxf(m, swz_xor<16>(m));
-      m = fmaxf(m, shfl_xor(m, 32));
-      m = (m == 0.0f) ? 0.0f : m;
+      const float m = __builtin_fmaf(max_x32(max_x16(run[n])), 0.0625f, 0.0f);
       if (lane < 16) tile[wave][16 * n + col][kb] = m;
+    }
+  };
+
+  // Two register buffers, the block loop unrolled by two; an odd count ends
+  // by processing its last block twice (same result, same LDS slot).
+  uint4 ka[2][4];
+  uint2 ks[2][4];
+  if (nvis > 0) load_block(0, ka[0], ks[0]);
+  for (int kb = 0; kb < nvis; kb += 2) {
+    const int k1 = min(kb + 1, nvis - 1), k2 = min(kb + 2, nvis - 1);
+    load_block(k1, ka[1], ks[1]);
+    process(kb, ka[0], ks[0]);
+    load_block(k2, ka[0], ks[0]);
+    process(k1, ka[1], ks[1]);
+  }
+  for (int kb = nvis; kb < nblk; ++kb) {
+    if (lane < 16) {
+#pragma unroll
+      for (int n = 0; n < kNT; ++n) tile[wave][16 * n + col][kb] = ninf;
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
