@@ -35,7 +35,7 @@
 #include "common.h"
 
 #ifndef QKV_ATTN_TARGET_WGS
-#define QKV_ATTN_TARGET_WGS 1024
+#define QKV_ATTN_TARGET_WGS 256
 #endif
 // Workgroups per CU the register budget is sized for (4 waves each).
 #ifndef QKV_ATTN_WG_PER_CU
@@ -47,7 +47,10 @@ namespace {
 
 constexpr int kD = 128;     // head dim
 constexpr int kNT = 256;    // threads per workgroup
-constexpr int kMaxIters = 8;
+#ifndef QKV_ATTN_MAX_ITERS
+#define QKV_ATTN_MAX_ITERS 16
+#endif
+constexpr int kMaxIters = QKV_ATTN_MAX_ITERS;
 // Ticket words at the start of the workspace, one per possible row, so calls
 // of any shape that share a workspace find their tickets at the same place.
 constexpr int64_t kTicketWords = 65536;
@@ -402,8 +405,10 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
 // two chunks of K/V in registers, 4 above that.
 constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 
-// Chunks per wave: doubled while the grid keeps QKV_ATTN_TARGET_WGS
-// workgroups, so long selections take few splits per row.
+// Chunks per wave: doubled (up to kMaxIters) while the grid keeps
+// QKV_ATTN_TARGET_WGS workgroups, so long selections take few splits per
+// row.  Measured at cfg2 (64 rows x 2048 slots): 256 workgroups of 4 chunks
+// per wave 18.0 us, 1024 workgroups of 1 chunk 20.4 us, 128 of 8 22.2 us.
 int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
   const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
   int it = 1;
@@ -479,11 +484,17 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
       q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                     \
       static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),            \
       static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o)
+#if QKV_ATTN_MAX_ITERS > 8
+#define QKV_ATTN_16(GG) case 16: QKV_ATTN(GG, 16); break;
+#else
+#define QKV_ATTN_16(GG)
+#endif
 #define QKV_ATTN_G(GG)                  \
   switch (iters) {                      \
     case 1: QKV_ATTN(GG, 1); break;     \
     case 2: QKV_ATTN(GG, 2); break;     \
     case 4: QKV_ATTN(GG, 4); break;     \
+    QKV_ATTN_16(GG)                     \
     default: QKV_ATTN(GG, 8); break;    \
   }
   switch (g) {

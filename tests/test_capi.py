@@ -78,13 +78,13 @@ def test_host_side_validation(call, msg):
     assert msg in _err()
 
 
-def _attn_splits(rows, n_slots, g, target=1024):
+def _attn_splits(rows, n_slots, g, target=256, max_iters=16):
     """Splits per row of qkv_sparse_attention: a workgroup round covers
     4 waves x 4*NI slots (NI = 8 for G <= 2, else 4); chunks per wave double
-    (up to 8) while the grid keeps at least ``target`` workgroups."""
+    (up to 16) while the grid keeps at least ``target`` workgroups."""
     per_iter = 16 * (8 if g <= 2 else 4)
     it = 1
-    while it < 8 and rows * -(-n_slots // (per_iter * it * 2)) >= target:
+    while it < max_iters and rows * -(-n_slots // (per_iter * it * 2)) >= target:
         it *= 2
     return -(-n_slots // (per_iter * it))
 
@@ -92,8 +92,8 @@ def _attn_splits(rows, n_slots, g, target=1024):
 def test_workspace_size_formula():
     # 65536 ticket words + rows * splits * G * (D + 2) floats
     t = 65536
-    assert _attn_splits(64, 2048, 2) == 16            # cfg2: 16 splits of 128 slots
-    assert _attn_splits(256, 4096, 4) == 8            # cfg3: 8 splits of 512 slots
+    assert _attn_splits(64, 2048, 2) == 4             # cfg2: 4 splits of 512 slots
+    assert _attn_splits(256, 4096, 4) == 4            # cfg3: 4 splits of 1024 slots
     assert _attn_splits(8, 300, 8) == 5
     for b, hq, hkv, n_sel, block in [(8, 16, 8, 128, 16), (1, 16, 8, 256, 1), (1, 64, 8, 300, 1),
                                      (32, 32, 8, 256, 16), (8, 16, 8, 2048, 16), (1, 8, 8, 7, 64)]:

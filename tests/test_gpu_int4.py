@@ -241,11 +241,11 @@ def test_sparse_attention_matches_fp64(g_size, block, nsel):
 
 
 @pytest.mark.parametrize("g_size,batch,t,block,nsel", [
-    (2, 8, 20000, 16, 1024),    # 64 rows x 16384 slots: 8 chunks per wave, 16 splits
-    (2, 4, 9000, 16, 512),      # 32 rows x 8192 slots: 2 chunks per wave
-    (4, 4, 9000, 16, 512),      # G = 4 (4-token steps): 4 chunks per wave
-    (8, 4, 20000, 1, 4000),     # G = 8, block 1, slots not a multiple of a chunk
-    (1, 8, 20000, 64, 300),     # G = 1
+    (2, 8, 20000, 16, 1024),    # 64 rows x 16384 slots: 16 chunks per wave, 8 splits
+    (2, 1, 9000, 16, 512),      # 8 rows x 8192 slots: 2 chunks per wave
+    (4, 1, 9000, 16, 512),      # G = 4 (4-token steps): 4 chunks per wave
+    (8, 4, 20000, 1, 4000),     # G = 8, block 1: 8 chunks per wave, slots not a multiple of a chunk
+    (1, 8, 20000, 64, 300),     # G = 1: 16 chunks per wave, partial last split
 ])
 def test_sparse_attention_long_selections(g_size, batch, t, block, nsel):
     # Long selections take several chunks per wave and few splits per row;
