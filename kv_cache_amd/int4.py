@@ -302,6 +302,21 @@ class SparseDecodeStep:
         self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, topk, block, device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
 
+    @classmethod
+    def for_mode(cls, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
+                 device: torch.device | str = "cuda") -> "SparseDecodeStep":
+        """The step for a reference mode string (``qabs{S}cand{pct}attn`` or
+        ``qboracle{bs}q{S}s{scan}cand{pct}``) at ``tokens`` keys; the cache it
+        runs on must have ``plan.selected`` channels (``modes.decode_plan``)."""
+        from .modes import decode_plan
+
+        plan = decode_plan(mode, tokens, head_dim)
+        _require(plan is not None, f"mode {mode!r} is not a decode mode of this path (or no history yet)")
+        step = cls(batch, q_heads, kv_heads, head_dim, tokens, plan.block,
+                   min(plan.topk, math.ceil(tokens / plan.block)), device)
+        step.plan = plan
+        return step
+
     def __call__(self, query: torch.Tensor, cache: Int4KCache, key: torch.Tensor, value: torch.Tensor,
                  scaling: float) -> torch.Tensor:
         decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.tokens, self.block,

@@ -342,3 +342,27 @@ def test_config1_end_to_end():
     want = O.sparse_attention(f32(q), f32(k), f32(v), sel.reshape(cfg.batch, cfg.kv_heads, -1), cfg.block,
                               cfg.tokens, cfg.scaling)
     assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+
+
+def test_step_for_reference_mode():
+    # qboracle16q32s6p25cand2 at 4097 keys: 4096 history keys, 32 channels,
+    # blocks of 16, ceil(6.25% * 4096 / 16) = 16 blocks kept.
+    from kv_cache_amd import modes as M
+    mode, t = "qboracle16q32s6p25cand2", 4097
+    cfg = CONFIGS["cfg1"]
+    q, k, v, _ = make_layer(cfg, 0, tokens=t)
+    step = K.SparseDecodeStep.for_mode(mode, 1, 16, 8, 128, t, DEV)
+    assert (step.plan.selected, step.block, step.topk) == (32, 16, 16)
+    cache = K.Int4KCache.from_prefill(k.to(DEV), 32, step.plan.selected)
+    out = step(q.to(DEV), cache, k.to(DEV), v.to(DEV), cfg.scaling)
+    kn = f32(k).reshape(8, t, 128)
+    packed, scales = O.int4_pack_k(kn, 32)
+    chan = O.select_channels(O.channel_stats(packed, scales, 32), 32)
+    slab, sbits = O.build_slab(kn, chan)
+    _, _, _, sel = O.decode_select(f32(q), slab, sbits, chan, 8, 16, 16)
+    assert np.array_equal(step.sel.cpu().numpy().reshape(8, -1), sel)
+    want = O.sparse_attention(f32(q), f32(k), f32(v), sel.reshape(1, 8, -1), 16, t, cfg.scaling)
+    np.testing.assert_allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+    with pytest.raises(RuntimeError, match="not a decode mode"):
+        K.SparseDecodeStep.for_mode("qabs8cand3reuse", 1, 16, 8, 128, t, DEV)
+    assert M.decode_plan(mode, t).tokens_kept == 256

@@ -1,0 +1,69 @@
+"""Mode-string parsing and budget arithmetic of the path (host logic, CPU).
+
+Pinned by known answers written from the reference's grammar (EV:748-754,
+798-806) and by the closed forms of the budget (brute force over small
+counts: the smallest integer at least fraction * history, clamped)."""
+
+import math
+
+import pytest
+
+from kv_cache_amd import modes as M
+
+
+@pytest.mark.parametrize("mode,want", [
+    ("qabs32cand6p25attn", (32, 0.0625)),
+    ("qabs8cand3reuse", (8, 0.03)),
+    ("qabs16cand10rerank", (16, 0.10)),
+    ("qabs64cand2p5reusefinalblk16", (64, 0.025)),
+    ("lagtop2qabs32cand5", (32, 0.05)),
+    ("qabs32cand6p25", (32, 0.0625)),
+    ("qabs32cand6p25attnx", None),
+    ("qboracle16q32s6p25cand2", None),
+])
+def test_parse_qabs(mode, want):
+    got = M.parse_qabs_partial_rerank_params(mode)
+    if want is None:
+        assert got is None
+    else:
+        assert got[0] == want[0] and got[1] == pytest.approx(want[1], abs=0)
+
+
+@pytest.mark.parametrize("mode,want", [
+    ("qboracle16q32s6p25cand2", (16, 32, 0.0625, 0.02)),
+    ("qboracle0q8s50cand1p5", (1, 8, 0.5, 0.015)),
+    ("qboracle16q32s6p25", None),
+])
+def test_parse_qboracle(mode, want):
+    assert M.parse_qboracle_params(mode) == want
+
+
+def test_candidate_count_closed_form():
+    for history in range(0, 300):
+        for frac in (0.0, 0.001, 0.02, 0.0625, 0.5, 1.0, 1.7):
+            got = M.candidate_count(frac, history)
+            # smallest c >= frac*history, at least 1, at most history
+            want = min(history, max(1, next(c for c in range(0, 10 ** 6) if c >= frac * history)))
+            assert got == want
+
+
+def test_scan_block_count_closed_form():
+    for history in range(1, 200):
+        for block in (1, 3, 16, 64):
+            for scan in (0.01, 0.0625, 0.5, 1.0):
+                nb = len(range(0, history, block))                      # blocks covering the history
+                least = next(c for c in range(0, 10 ** 6) if c * block >= scan * history)
+                assert M.scan_block_count(scan, history, block) == min(nb, max(1, least))
+
+
+def test_decode_plan():
+    p = M.decode_plan("qabs32cand6p25attn", 32769)
+    assert (p.selected, p.block, p.topk, p.history) == (32, 1, 2048, 32768)
+    p = M.decode_plan("qboracle16q32s6p25cand2", 32769)
+    assert (p.selected, p.block, p.topk) == (32, 16, 128)          # cfg2's 128 blocks of 16
+    assert p.tokens_kept == 2048
+    p = M.decode_plan("qabs8cand3attn", 4097)
+    assert p.selected == 16 and p.topk == math.ceil(0.03 * 4096)   # 8 channels round up to the 16-slab
+    assert M.decode_plan("qabs8cand3reuse", 4097) is None          # not a mode of this path
+    assert M.decode_plan("qabs32cand5attn", 1) is None             # no history yet
+    assert M.selected_dims(500, 128) == 128 and M.selected_dims(0, 128) == 16
