@@ -1,0 +1,198 @@
+"""HuggingFace transformers integration: decode-time append of the int4 K
+structures inside a ``Cache``, and an attention function that runs the int4
+sparse decode step on it.
+
+The reference reaches its selection through HF's eager attention, which it
+patches (evaluate_qwen3_top2_head_limit3_ppl.py:6934-6944), and keeps an
+auxiliary K copy (dim-major bf16) that it grows by one column per decode step
+(EV:2018-2042).  Here the auxiliary structure is the int4 cache of
+``int4.Int4KCache``: after prefill the packed K, the static channel subset and
+the subset slab are built once; every later token is quantized into them in
+place (``int4_pack_k`` / ``build_slab`` over ``[t, t+1)``) as HF appends it to
+the bf16 cache.  K/V live in preallocated buffers of a fixed capacity, so no
+step reallocates or copies the history.
+
+Use:
+
+    from kv_cache_amd import hf
+    hf.register()                                         # attn_implementation "int4_sparse"
+    model.config._attn_implementation = "int4_sparse"
+    cache = hf.Int4SparseCache(capacity=40960, group=32, selected=32, block=16, topk=128)
+    out = model(input_ids, past_key_values=cache, use_cache=True)       # prefill: dense SDPA
+    out = model(next_ids, past_key_values=cache, use_cache=True)        # decode: int4 sparse
+
+Prefill (more than one query per call) runs dense SDPA on the GPU, as the
+reference's prefill runs dense HF attention (EV:7079-7111).  Decode steps with
+one query per sequence run the int4 path; attention masks are not applied
+there (decode attends over the whole cache, no padding).
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+import weakref
+
+import torch
+
+from . import int4 as K
+
+# Cache layers by the address of their K buffer: the attention function gets
+# K as a view of that buffer and finds the layer's int4 state through it.
+# Weak references, so a freed cache's address cannot match a later tensor.
+_LAYERS: "weakref.WeakValueDictionary[int, Int4CacheLayer]" = weakref.WeakValueDictionary()
+
+
+class Int4CacheLayer:
+    """One layer's bf16 K/V in preallocated buffers plus its int4 structures."""
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, group: int, selected: int, block: int, topk: int):
+        self.capacity = K.round_capacity(capacity)
+        self.group, self.selected, self.block, self.topk = int(group), int(selected), int(block), int(topk)
+        self.keys = self.values = None
+        self.is_initialized = False
+        self.length = 0
+        self.int4 = None          # Int4KCache once built
+        self.bufs = None          # decode-step buffers
+
+    def __repr__(self):
+        return f"Int4CacheLayer(length={self.length}, capacity={self.capacity})"
+
+    # -- CacheLayerMixin protocol ------------------------------------------
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        b, h, _, d = key_states.shape
+        dev = key_states.device
+        self.dtype, self.device = key_states.dtype, dev
+        self._k = torch.empty((b, h, self.capacity, d), dtype=key_states.dtype, device=dev)
+        self._v = torch.empty((b, h, self.capacity, d), dtype=value_states.dtype, device=dev)
+        _LAYERS[self._k.data_ptr()] = self
+        self.is_initialized = True
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        n = key_states.size(-2)
+        t0, t1 = self.length, self.length + n
+        if t1 > self.capacity:
+            raise RuntimeError(f"Int4 cache capacity {self.capacity} exceeded ({t1} tokens)")
+        self._k[:, :, t0:t1].copy_(key_states)
+        self._v[:, :, t0:t1].copy_(value_states)
+        self.length = t1
+        self.keys, self.values = self._k[:, :, :t1], self._v[:, :, :t1]
+        if self.int4 is not None:
+            self.append_int4(t0, t1)
+        return self.keys, self.values
+
+    def get_mask_sizes(self, query_length: int):
+        return self.length + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def reset(self) -> None:
+        self.length = 0
+        self.int4 = None
+
+    def offload(self):
+        raise RuntimeError("Int4CacheLayer cannot be offloaded")
+
+    prefetch = offload
+
+    # -- int4 structures ---------------------------------------------------
+    def build_int4(self) -> None:
+        """Pack the cached tokens, choose the channel subset, build the slab."""
+        if self.keys.dtype != torch.bfloat16:
+            raise RuntimeError("the int4 path needs bfloat16 K/V")
+        t = self.length
+        packed, scales = K.int4_pack_k(self._k, self.group, capacity=self.capacity, t_end=t)
+        chan, _ = K.select_channels(packed, scales, t, self.group, self.selected)
+        slab, slab_scales = K.build_slab(self._k, chan, capacity=self.capacity, t_end=t)
+        self.int4 = K.Int4KCache(packed, scales, chan, slab, slab_scales, t, self.group)
+
+    def append_int4(self, t0: int, t1: int) -> None:
+        """Quantize tokens [t0, t1) into the packed K and the slab (the channel
+        subset stays the one chosen at prefill)."""
+        c = self.int4
+        K.int4_pack_k(self._k, self.group, packed=c.packed, scales=c.scales, t_begin=t0, t_end=t1)
+        K.build_slab(self._k, c.chan_idx, slab=c.slab, slab_scales=c.slab_scales, t_begin=t0, t_end=t1)
+        c.tokens = t1
+
+    def decode_buffers(self, batch: int, q_heads: int, kv_heads: int, head_dim: int):
+        """Block maxima, selection, workspaces and output sized for the full
+        capacity, allocated once (flat, so that each step takes a contiguous
+        view of its own size)."""
+        if self.bufs is None:
+            nb = math.ceil(self.capacity / self.block)
+            dev = self.device
+            self.bufs = {
+                "bmax": torch.empty(batch * kv_heads * nb, dtype=torch.float32, device=dev),
+                "sel": torch.empty(batch * kv_heads * min(self.topk, nb), dtype=torch.int32, device=dev),
+                "topk_ws": K.topk_workspace(batch * kv_heads, nb, min(self.topk, nb), dev),
+                "attn_ws": K.attention_workspace(batch, q_heads, kv_heads, head_dim, min(self.topk, nb), self.block, dev),
+                "out": torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=dev),
+            }
+        return self.bufs
+
+
+class Int4SparseCache:
+    """A transformers ``Cache`` whose layers keep K/V in preallocated buffers
+    and append the int4 structures at every decode step."""
+
+    def __new__(cls, capacity: int, group: int = 32, selected: int = 32, block: int = 16, topk: int = 128):
+        from transformers.cache_utils import Cache, CacheLayerMixin
+
+        layer_cls = _layer_class(CacheLayerMixin)
+        cache = Cache(layer_class_to_replicate=functools.partial(layer_cls, capacity, group, selected, block, topk))
+        return cache
+
+
+@functools.lru_cache(maxsize=1)
+def _layer_class(mixin):
+    # Int4CacheLayer registered as a CacheLayerMixin so transformers' checks accept it.
+    return type("Int4CacheLayerHF", (Int4CacheLayer, mixin), {"__init__": Int4CacheLayer.__init__})
+
+
+def int4_sparse_attention_forward(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                  attention_mask, scaling: float | None = None, dropout: float = 0.0, **kwargs):
+    """HF attention interface (query [B,Hq,q,D]; key/value [B,Hkv,T,D]) ->
+    (out [B,q,Hq,D], None).  One query per sequence on an Int4SparseCache:
+    int4 scoring + top-k blocks + GQA sparse attention; otherwise dense SDPA."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    layer = _LAYERS.get(key.data_ptr())
+    if query.size(2) != 1 or layer is None or layer.keys is None or key.size(2) != layer.length:
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
+    if layer.int4 is None:
+        layer.build_int4()
+    b, hq, _, d = query.shape
+    hkv = key.size(1)
+    t = layer.length
+    scaling = d ** -0.5 if scaling is None else float(scaling)
+    bufs = layer.decode_buffers(b, hq, hkv, d)
+    c = layer.int4
+    nb = math.ceil(t / layer.block)
+    k = min(layer.topk, nb)
+    q = query[:, :, 0, :].contiguous()
+    bmax = bufs["bmax"][: b * hkv * nb].view(b, hkv, nb)
+    K.decode_scores(q, c.chan_idx, c.slab, c.slab_scales, t, layer.block, bmax=bmax)
+    sel = bufs["sel"][: b * hkv * k].view(b, hkv, k)
+    K.block_topk(bmax, k, out=sel, workspace=bufs["topk_ws"])
+    out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, t, scaling,
+                             workspace=bufs["attn_ws"], out=bufs["out"])
+    return out[:, None].to(query.dtype), None
+
+
+def register(name: str = "int4_sparse") -> str:
+    """Register the attention function with transformers under ``name``."""
+    from transformers import AttentionInterface
+
+    AttentionInterface.register(name, int4_sparse_attention_forward)
+    return name

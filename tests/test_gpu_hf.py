@@ -1,0 +1,100 @@
+"""The int4 path inside a transformers Qwen3 model (random init, no weights
+needed): decode-time append into the int4 cache and the sparse attention
+function behind transformers' attention interface.
+
+* With every block kept, the decode logits equal dense SDPA's within bf16
+  tolerance (the selection covers the whole cache, so only the attention
+  arithmetic differs).
+* With a sparse selection, the packed K, scales and slab that were appended
+  token by token equal the oracle's on the final K (bit-exact); the channel
+  subset is the one chosen when the int4 cache was built.
+* ``generate`` runs end to end on the cache."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import hf
+from oracle import qkv_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _model(layers=2):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    torch.manual_seed(0)
+    cfg = Qwen3Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=layers,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=128, max_position_embeddings=4096,
+                      rope_theta=1.0e6)
+    return Qwen3ForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+
+
+def _decode(model, impl, cache, prompt, steps):
+    model.config._attn_implementation = impl
+    logits = []
+    with torch.no_grad():
+        out = model(prompt, past_key_values=cache, use_cache=True)
+        nxt = out.logits[:, -1:].argmax(-1)
+        for i in range(steps):
+            out = model(nxt, past_key_values=cache, use_cache=True)
+            logits.append(out.logits[:, -1].float())
+            # teacher-force a fixed token stream so both runs see the same inputs
+            nxt = torch.full_like(nxt, (37 * i + 11) % 512)
+    return logits
+
+
+def test_all_blocks_kept_matches_dense():
+    from transformers.cache_utils import DynamicCache
+
+    hf.register()
+    model = _model()
+    prompt = torch.randint(0, 512, (2, 300), generator=torch.Generator().manual_seed(1)).to(DEV)
+    cache = hf.Int4SparseCache(capacity=1024, group=32, selected=32, block=16, topk=64)   # 64 x 16 = all
+    got = _decode(model, "int4_sparse", cache, prompt, 6)
+    want = _decode(model, "sdpa", DynamicCache(config=model.config), prompt, 6)
+    for g, w in zip(got, want):
+        torch.testing.assert_close(g, w, rtol=3e-2, atol=3e-2)
+    assert all(layer.int4 is not None for layer in cache.layers)
+    assert cache.get_seq_length() == 306
+
+
+def test_append_matches_rebuild():
+    hf.register()
+    model = _model()
+    prompt = torch.randint(0, 512, (1, 200), generator=torch.Generator().manual_seed(2)).to(DEV)
+    cache = hf.Int4SparseCache(capacity=512, group=32, selected=32, block=16, topk=4)
+    logits = _decode(model, "int4_sparse", cache, prompt, 9)
+    assert all(torch.isfinite(x).all() for x in logits)
+    t = cache.get_seq_length()
+    assert t == 209
+    for layer in cache.layers:
+        c = layer.int4
+        assert c.tokens == t
+        k = layer.keys.float().cpu().numpy().reshape(2, t, 128)          # 2 KV heads
+        want_p, want_s = O.int4_pack_k(k, 32)
+        assert np.array_equal(c.packed[0, :, :t].cpu().numpy(), want_p)
+        assert np.array_equal(c.scales[0, :, :t].contiguous().cpu().view(torch.int16).numpy().view(np.uint16),
+                              want_s)
+        # channels chosen when the int4 cache was built: prefill + the first decode token
+        pp, ps = O.int4_pack_k(k[:, :201], 32)
+        chan = O.select_channels(O.channel_stats(pp, ps, 32), 32)
+        assert np.array_equal(c.chan_idx[0].cpu().numpy(), chan)
+        slab, sbits = O.build_slab(k, chan)
+        stored = c.slab[0].cpu().numpy().reshape(2, -1)
+        assert np.array_equal(O.unswizzle_slab(stored, 32, t), slab)
+        assert np.array_equal(c.slab_scales[0, :, :t].contiguous().cpu().view(torch.int16).numpy().view(np.uint16),
+                              sbits)
+
+
+def test_generate_runs():
+    hf.register()
+    model = _model()
+    model.config._attn_implementation = "int4_sparse"
+    prompt = torch.randint(0, 512, (1, 150), generator=torch.Generator().manual_seed(3)).to(DEV)
+    cache = hf.Int4SparseCache(capacity=256, group=32, selected=32, block=16, topk=4)
+    with torch.no_grad():
+        out = model.generate(prompt, past_key_values=cache, max_new_tokens=8, do_sample=False)
+    assert out.shape == (1, 158)
+    assert cache.get_seq_length() == 157
