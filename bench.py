@@ -249,6 +249,11 @@ def run_decode(args) -> dict:
             K.sparse_attention(qs[layer], ks[layer], vs[layer], step.sel, cfg.block, T, cfg.scaling,
                                workspace=step.workspace, out=step.out)
 
+    def run_select_attn():
+        for layer in range(layers):
+            K.sparse_attention_select(qs[layer], ks[layer], vs[layer], step.bmax, cfg.topk, cfg.block, T,
+                                      cfg.scaling, workspace=step.workspace, sel_out=step.sel, out=step.out)
+
     dense_sel = torch.arange(cfg.n_blocks, dtype=torch.int32, device="cuda").repeat(rows, 1).contiguous()
     dense_ws = K.attention_workspace(cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.n_blocks,
                                      cfg.block, "cuda")
@@ -287,6 +292,9 @@ def run_decode(args) -> dict:
         ("sparse_attention", run_attn, rows * sel_tokens * cfg.head_dim * 2 * 2),
         ("dense_bf16_attention", run_dense, rows * T * cfg.head_dim * 2 * 2),
     ]
+    if step.fused:   # the step's own second launch: selection inside the attention kernel
+        plan.insert(3, ("select_sparse_attention", run_select_attn,
+                        rows * (cfg.n_blocks * 4 + sel_tokens * cfg.head_dim * 2 * 2)))
     for name, fn, nbytes in plan:
         g = graph_of(repeated(fn))
         ms = time_replays(g.replay, args.kernel_reps) / (layers * reps)
@@ -328,7 +336,7 @@ def run_decode(args) -> dict:
             "workload": f"{args.config}: {cfg.name}",
             "batch": cfg.batch, "q_heads": cfg.q_heads, "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
             "context": T, "layers": layers, "int4_group": cfg.group, "channels": cfg.selected,
-            "block": cfg.block, "topk_blocks": cfg.topk, "graph": not args.eager,
+            "block": cfg.block, "topk_blocks": cfg.topk, "graph": not args.eager, "fused_select": step.fused,
         },
         "us_per_layer": ms_per_step * 1e3 / layers,
         "dense_bf16_us_per_layer": kernels["dense_bf16_attention"]["us_per_launch"],

@@ -179,7 +179,9 @@ int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_
 
 /* Bytes of workspace qkv_sparse_attention needs for these sizes: 65536
  * uint32 row tickets (the same words for every call shape), then G*(D+2)
- * floats per split of 128 token slots. */
+ * floats per split.  The size also covers every call with the same batch
+ * and heads and fewer selected slots (n_sel * block), so one workspace
+ * serves all of them. */
 int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                              int64_t head_dim, int64_t n_sel, int64_t block);
 
@@ -201,6 +203,22 @@ int qkv_sparse_attention(const void* query, const void* key, const void* value,
                          int64_t kv_heads, int64_t tokens, int64_t head_dim,
                          const int32_t* block_ids, int64_t n_sel, int64_t block, float scaling,
                          float* workspace, int64_t workspace_bytes, void* out, void* stream);
+
+/* qkv_sparse_attention with the block selection fused in: replaces the
+ * reference's top-k over pooled block scores (EV:5046) followed by its
+ * final-attention kernel (QK:335-419).  bmax f32 [rows, >= bmax_ld] holds
+ * the row's ceil(tokens/block) block maxima (as qkv_int4_decode_scores writes
+ * them); each workgroup selects the n_sel largest (lowest index wins ties,
+ * ascending -- exactly qkv_topk's selection) and attends over those blocks.
+ * sel_out int32 [rows,n_sel], when not NULL, receives the selection.  At
+ * most 4096 blocks per row (longer rows: qkv_topk_ws, then
+ * qkv_sparse_attention).  Workspace as for qkv_sparse_attention. */
+int qkv_sparse_attention_select(const void* query, const void* key, const void* value,
+                                const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                int64_t kv_heads, int64_t tokens, int64_t head_dim, const float* bmax,
+                                int64_t bmax_ld, int64_t n_sel, int64_t block, float scaling,
+                                float* workspace, int64_t workspace_bytes, int32_t* sel_out, void* out,
+                                void* stream);
 
 /* ======================================================================
  * Chunked-prefill block selection (no reference counterpart: the reference

@@ -56,6 +56,8 @@ _PROTOTYPES = {
     "qkv_sparse_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "qkv_sparse_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                     _i64, _f32, _vp, _i64, _vp, _vp]),
+    "qkv_sparse_attention_select": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                                           _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
 }
 
 _LIB = None

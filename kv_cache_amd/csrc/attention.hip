@@ -33,6 +33,7 @@
 // No release / acquire fence is used: on gfx950 those write back and
 // invalidate the whole L2 of the XCD (buffer_wbl2 / buffer_inv).
 #include "common.h"
+#include "select.h"
 
 #ifndef QKV_ATTN_TARGET_WGS
 #define QKV_ATTN_TARGET_WGS 256
@@ -112,19 +113,30 @@ __device__ __forceinline__ int zero_after(float dep) {
 // that computed x.
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
-template <int G, int NI, int ITERS>
+// Rows of at most kSelMaxBlocks block maxima can select in the kernel.
+constexpr int kSelVPL = 16;
+constexpr int kSelMaxBlocks = 256 * kSelVPL;
+
+// SEL: the row's block ids are not given; every workgroup of the row selects
+// the n_sel largest of its block maxima (bmax row r at bmax + r*bmax_ld,
+// lowest index wins ties, ascending) into LDS first -- the selection of
+// qkv_topk, repeated per split instead of launched separately.  The row's
+// first workgroup also writes it to sel_out (when given).
+template <int G, int NI, int ITERS, bool SEL>
 __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
     int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
     int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    uint32_t* __restrict__ tickets, uint16_t* __restrict__ out) {
+    uint32_t* __restrict__ tickets, uint16_t* __restrict__ out, const float* __restrict__ bmax,
+    int64_t bmax_ld, int32_t* __restrict__ sel_out) {
   constexpr int CH = 4 * NI;               // token slots per wave chunk
   static_assert(CH <= 64, "one slot per lane when resolving token ids");
 
   __shared__ float red_acc[4][G][kD];   // per wave weighted V
   __shared__ float red_m[4][G], red_l[4][G];
   __shared__ int last_flag;
+  __shared__ int32_t sel_lds[SEL ? kSelMaxBlocks : 1];
 
   const int r = blockIdx.y, split = blockIdx.x;
   const int b = r / kv_heads, j = r - b * kv_heads;
@@ -133,6 +145,11 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   const float ninf = -__builtin_huge_valf();
   const int n_slots = n_sel * block;
   const int32_t* ids = block_ids + static_cast<int64_t>(r) * n_sel;
+  if constexpr (SEL) {
+    select_row<kSelVPL, false>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
+    if (sel_out && split == 0)
+      for (int i = tid; i < n_sel; i += kNT) sel_out[static_cast<int64_t>(r) * n_sel + i] = sel_lds[i];
+  }
 
   // Slot of this lane in chunk c (meaningful for lane < CH).
   const int wg_base = split * (4 * CH * ITERS);
@@ -142,7 +159,7 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   auto load_id = [&](int c) -> int {
     const int slot = slot_of(c);
     const bool ok = lane < CH && slot < n_slots;
-    const int v = ids[ok ? slot / block : 0];
+    const int v = SEL ? sel_lds[ok ? slot / block : 0] : ids[ok ? slot / block : 0];
     return ok ? v : -1;
   };
   // Token of the lane's slot from its block id, or -1.
@@ -409,10 +426,13 @@ constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 // QKV_ATTN_TARGET_WGS workgroups, so long selections take few splits per
 // row.  Measured at cfg2 (64 rows x 2048 slots): 256 workgroups of 4 chunks
 // per wave 18.0 us, 1024 workgroups of 1 chunk 20.4 us, 128 of 8 22.2 us.
+// G = 8 stops at 8 chunks: its 16-chunk variant does not fit the registers.
+constexpr int max_iters_for(int64_t g) { return g >= 8 && kMaxIters > 8 ? 8 : kMaxIters; }
+
 int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
   const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
   int it = 1;
-  while (it < kMaxIters && rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS) it *= 2;
+  while (it < max_iters_for(g) && rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS) it *= 2;
   return it;
 }
 
@@ -433,45 +453,63 @@ QKV_EXPORT int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q
     return -1;
   const int64_t g = q_heads / kv_heads;
   const int64_t rows = batch * kv_heads;
+  const int64_t n_slots = n_sel * block;
+  // The split count is not monotonic in the slot count, but below the chunk
+  // cap a doubling that failed bounds it: splits <= 2 * (ceil(target/rows) - 1);
+  // at the cap it grows with the slots.  The larger of that bound and this
+  // size's own count covers every call with fewer slots, so one workspace
+  // serves all smaller selections.
+  const int64_t below_cap = std::min(cdiv(n_slots, 4 * 4 * ni_for(g)),
+                                     2 * (cdiv(QKV_ATTN_TARGET_WGS, rows) - 1));
+  const int64_t splits = std::max(splits_for(rows, n_slots, g), below_cap);
   // tickets, then per split: weighted V per head, then (max, sum) per head
-  return 4 * (kTicketWords + rows * splits_for(rows, n_sel * block, g) * g * (kD + 2));
+  return 4 * (kTicketWords + rows * splits * g * (kD + 2));
 }
 
-QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const void* value,
-                                    const int64_t* kv_strides, int64_t batch, int64_t q_heads,
-                                    int64_t kv_heads, int64_t tokens, int64_t head_dim,
-                                    const int32_t* block_ids, int64_t n_sel, int64_t block,
-                                    float scaling, float* workspace, int64_t workspace_bytes,
-                                    void* out, void* stream) {
-  if (!query || !key || !value || !kv_strides || !block_ids || !workspace || !out)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: null pointer");
-  if (head_dim != kD) return fail(QKV_ERR_UNSUPPORTED, "qkv_sparse_attention: head_dim must be 128");
+namespace {
+
+// Shared argument checks and launch of both entry points; sel selects the
+// in-kernel selection from bmax (block_ids unused), else block_ids is read.
+int launch_attention(const char* what, const void* query, const void* key, const void* value,
+                     const int64_t* kv_strides, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                     int64_t tokens, int64_t head_dim, const int32_t* block_ids, const float* bmax,
+                     int64_t bmax_ld, int32_t* sel_out, int64_t n_sel, int64_t block, float scaling,
+                     float* workspace, int64_t workspace_bytes, void* out, void* stream) {
+  const bool sel = bmax != nullptr;
+  if (!query || !key || !value || !kv_strides || !(sel || block_ids) || !workspace || !out)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (head_dim != kD) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be 128", what);
   if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: q_heads must be a multiple of kv_heads");
+    return fail(QKV_ERR_INVALID, "%s: q_heads must be a multiple of kv_heads", what);
   const int64_t g = q_heads / kv_heads;
   if (g != 1 && g != 2 && g != 4 && g != 8)
-    return fail(QKV_ERR_UNSUPPORTED, "qkv_sparse_attention: group size %lld not built", (long long)g);
-  if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many rows");
+    return fail(QKV_ERR_UNSUPPORTED, "%s: group size %lld not built", what, (long long)g);
+  if (batch * kv_heads > 65535) return fail(QKV_ERR_INVALID, "%s: too many rows", what);
   if (tokens <= 0 || tokens >= (int64_t(1) << 31) || n_sel <= 0 || block <= 0 ||
       n_sel * block >= (int64_t(1) << 30))
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: need tokens > 0, n_sel > 0, block > 0, "
-                                 "n_sel * block < 2^30");
+    return fail(QKV_ERR_INVALID, "%s: need tokens > 0, n_sel > 0, block > 0, n_sel * block < 2^30", what);
   if (!aligned(query, 16) || !aligned(key, 16) || !aligned(value, 16) ||
       (kv_strides[0] | kv_strides[1] | kv_strides[2]) % 8)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: q/K/V rows must be 16-byte aligned");
+    return fail(QKV_ERR_INVALID, "%s: q/K/V rows must be 16-byte aligned", what);
+  const int nb = static_cast<int>(cdiv(tokens, block));
+  if (sel) {
+    if (nb > kSelMaxBlocks)
+      return fail(QKV_ERR_UNSUPPORTED, "%s: at most %d blocks (got %d); select with qkv_topk_ws first", what,
+                  kSelMaxBlocks, nb);
+    if (n_sel > nb || bmax_ld < nb) return fail(QKV_ERR_INVALID, "%s: need n_sel <= blocks <= bmax_ld", what);
+  }
   const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block);
   if (workspace_bytes < need)
-    return fail(QKV_ERR_INVALID, "qkv_sparse_attention: workspace needs %lld bytes, got %lld",
-                (long long)need, (long long)workspace_bytes);
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
   const int64_t rows = batch * kv_heads;
   const int64_t n_slots = n_sel * block;
   const int iters = iters_for(rows, n_slots, g);
   const int64_t nsplit = splits_for(rows, n_slots, g);
-  if (nsplit > 65535) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: too many selected blocks");
+  if (nsplit > 65535) return fail(QKV_ERR_INVALID, "%s: too many selected blocks", what);
   uint32_t* tickets = reinterpret_cast<uint32_t*>(workspace);
   float* ws_acc = workspace + kTicketWords;
   float* ws_ml = ws_acc + rows * nsplit * g * kD;
-  const int nb = static_cast<int>(cdiv(tokens, block));
   const float scale_log2 = scaling * 1.4426950408889634f;
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(rows));
@@ -479,31 +517,63 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   const uint16_t* k = static_cast<const uint16_t*>(key);
   const uint16_t* v = static_cast<const uint16_t*>(value);
   uint16_t* o = static_cast<uint16_t*>(out);
-#define QKV_ATTN(GG, IT)                                                                                   \
-  sparse_attn_kernel<GG, ni_for(GG), IT><<<grid, kNT, 0, st>>>(                                             \
-      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                     \
-      static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),            \
-      static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o)
+#define QKV_ATTN_S(GG, IT, SS)                                                                              \
+  sparse_attn_kernel<GG, ni_for(GG), IT, SS><<<grid, kNT, 0, st>>>(                                         \
+      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                      \
+      static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),             \
+      static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o, bmax,   \
+      bmax_ld, sel_out)
+#define QKV_ATTN(GG, IT)             \
+  if (sel) QKV_ATTN_S(GG, IT, true); \
+  else QKV_ATTN_S(GG, IT, false);
 #if QKV_ATTN_MAX_ITERS > 8
 #define QKV_ATTN_16(GG) case 16: QKV_ATTN(GG, 16); break;
 #else
 #define QKV_ATTN_16(GG)
 #endif
-#define QKV_ATTN_G(GG)                  \
+#define QKV_ATTN_G(GG, LONG)            \
   switch (iters) {                      \
     case 1: QKV_ATTN(GG, 1); break;     \
     case 2: QKV_ATTN(GG, 2); break;     \
     case 4: QKV_ATTN(GG, 4); break;     \
-    QKV_ATTN_16(GG)                     \
+    LONG                                \
     default: QKV_ATTN(GG, 8); break;    \
   }
   switch (g) {
-    case 1: QKV_ATTN_G(1); break;
-    case 2: QKV_ATTN_G(2); break;
-    case 4: QKV_ATTN_G(4); break;
-    default: QKV_ATTN_G(8); break;
+    case 1: QKV_ATTN_G(1, QKV_ATTN_16(1)); break;
+    case 2: QKV_ATTN_G(2, QKV_ATTN_16(2)); break;
+    case 4: QKV_ATTN_G(4, QKV_ATTN_16(4)); break;
+    default: QKV_ATTN_G(8, ); break;
   }
 #undef QKV_ATTN_G
+#undef QKV_ATTN_16
 #undef QKV_ATTN
-  return check_launch("qkv_sparse_attention");
+#undef QKV_ATTN_S
+  return check_launch(what);
+}
+
+}  // namespace
+
+QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const void* value,
+                                    const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                    int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                                    const int32_t* block_ids, int64_t n_sel, int64_t block,
+                                    float scaling, float* workspace, int64_t workspace_bytes,
+                                    void* out, void* stream) {
+  if (!block_ids) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: null pointer");
+  return launch_attention("qkv_sparse_attention", query, key, value, kv_strides, batch, q_heads, kv_heads,
+                          tokens, head_dim, block_ids, nullptr, 0, nullptr, n_sel, block, scaling, workspace,
+                          workspace_bytes, out, stream);
+}
+
+QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, const void* value,
+                                           const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                           int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                                           const float* bmax, int64_t bmax_ld, int64_t n_sel, int64_t block,
+                                           float scaling, float* workspace, int64_t workspace_bytes,
+                                           int32_t* sel_out, void* out, void* stream) {
+  if (!bmax) return fail(QKV_ERR_INVALID, "qkv_sparse_attention_select: null pointer");
+  return launch_attention("qkv_sparse_attention_select", query, key, value, kv_strides, batch, q_heads,
+                          kv_heads, tokens, head_dim, nullptr, bmax, bmax_ld, sel_out, n_sel, block, scaling,
+                          workspace, workspace_bytes, out, stream);
 }

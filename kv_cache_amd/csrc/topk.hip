@@ -9,12 +9,12 @@
 // index order then writes every key > theta plus the lowest-index keys equal
 // to theta, so the output is already in ascending index order.
 #include "common.h"
+#include "select.h"
 
 namespace qkv {
 namespace {
 
 constexpr int kBins = 2048;
-constexpr uint32_t kNegInfKey = 0x007FFFFFu;   // f32_sortable(-inf)
 constexpr int kLdsKeys = 12288;   // rows up to this many keys are staged in LDS (48 KB)
 #ifndef QKV_TOPK_WAVE_MAX_VPL
 #define QKV_TOPK_WAVE_MAX_VPL 16
@@ -119,195 +119,6 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* __restrict__ valu
       --take;
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// Wave-level helpers.  Reductions and scans use DPP (a few cycles a step,
-// where an LDS permute round trip costs ~100).
-// ---------------------------------------------------------------------------
-template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), CTRL,
-                                                           ROW_MASK, BANK_MASK, false));
-}
-
-// Max (IS_MAX) or min over the wave, via the row reduction (quad_perm,
-// row_half_mirror, row_mirror) and then row_bcast:15 / row_bcast:31, which
-// leave the wave's result in lane 63.
-template <bool IS_MAX>
-__device__ __forceinline__ uint32_t wave_minmax_u32(uint32_t v) {
-  auto op = [](uint32_t a, uint32_t b) { return IS_MAX ? max(a, b) : min(a, b); };
-  v = op(v, dpp_u32<0xB1>(v, v));
-  v = op(v, dpp_u32<0x4E>(v, v));
-  v = op(v, dpp_u32<0x141>(v, v));
-  v = op(v, dpp_u32<0x140>(v, v));
-  v = op(v, dpp_u32<0x142, 0xA>(v, v));
-  v = op(v, dpp_u32<0x143, 0xC>(v, v));
-  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
-}
-
-// Inclusive prefix sum over the 64 lanes (row_shr 1,2,3 then 4 and 8 within
-// each row of 16, then row_bcast:15 / row_bcast:31 across rows).
-__device__ __forceinline__ int wave_incl_scan_dpp(int v) {
-  uint32_t x = static_cast<uint32_t>(v);
-  uint32_t r = x + dpp_u32<0x111>(0u, x);
-  r += dpp_u32<0x112>(0u, x);
-  r += dpp_u32<0x113>(0u, x);
-  r += dpp_u32<0x114, 0xF, 0xE>(0u, r);
-  r += dpp_u32<0x118, 0xF, 0xC>(0u, r);
-  r += dpp_u32<0x142, 0xA>(0u, r);
-  r += dpp_u32<0x143, 0xC>(0u, r);
-  return static_cast<int>(r);
-}
-
-// Rows of at most 256*VPL keys: one workgroup of 4 waves per row.  Thread t
-// holds keys t + 256i (i < VPL) as order-preserving uint32, loaded without
-// branches so that every load is in flight at once.  The bits shared by the
-// row's largest and smallest key are skipped; the rest are resolved 8 bits
-// at a time with a shared 256-bin histogram that wave 0 scans with DPP.
-// Output positions follow index order: the keys taken before slot (i, wave)
-// are the keys > theta before it plus min(kr, keys == theta before it), both
-// known from per-(slot, wave) ballot counts, so one pass places every key.
-// FINITE: keys equal to -inf are not selectable; a row with fewer than k
-// other keys selects them all and pads its output with -1.
-//
-// select_row runs the selection for one row inside a 256-thread workgroup:
-// it writes the positions of the kk selected keys, ascending, to sel (LDS,
-// 256*VPL entries) and returns kk (k, or with FINITE possibly fewer).  Every
-// thread of the workgroup must call it; it ends with a barrier.
-template <int VPL, bool FINITE>
-__device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel) {
-  __shared__ int hist[4][260];             // one copy per wave, padded across banks
-  __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
-  __shared__ uint32_t red[4][3];
-  __shared__ int sh_bin, sh_kr, sh_whole;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-
-  uint32_t u[VPL];
-  bool valid[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int idx = i * 256 + tid;
-    u[i] = f32_sortable(vals[min(idx, n - 1)]);
-    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey);
-  }
-  uint32_t umax = 0, umin = 0xFFFFFFFFu;
-  int nval = 0;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    if (valid[i]) {
-      umax = max(umax, u[i]);
-      umin = min(umin, u[i]);
-    }
-    nval += __popcll(__ballot(valid[i]));
-  }
-  umax = wave_minmax_u32<true>(umax);
-  umin = wave_minmax_u32<false>(umin);
-  if (lane == 0) {
-    red[wave][0] = umax;
-    red[wave][1] = umin;
-    red[wave][2] = nval;
-  }
-  __syncthreads();
-  umax = max(max(red[0][0], red[1][0]), max(red[2][0], red[3][0]));
-  umin = min(min(red[0][1], red[1][1]), min(red[2][1], red[3][1]));
-  nval = red[0][2] + red[1][2] + red[2][2] + red[3][2];
-  const int kk = min(k, nval);   // keys selected; k unless FINITE drops some
-
-  // Radix select over the bits below the common prefix of umax and umin.
-  int kr = kk;
-  uint32_t prefix = umax, mask = 0xFFFFFFFFu;
-  int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
-  if (remaining) {
-    mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
-    prefix = umax & mask;
-  }
-  if (kk == nval) {   // every valid key is taken: no select needed
-    prefix = umin;
-    kr = 0x7FFFFFFF;
-    remaining = 0;
-  }
-  while (remaining > 0) {   // uniform across the workgroup
-    const int shift = remaining > 8 ? remaining - 8 : 0;
-    const uint32_t dmask = (1u << (remaining - shift)) - 1u;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
-    __syncthreads();
-    // Only keys on the prefix count: after the first pass they are few, and
-    // sending the rest to a dummy bin would serialize on one LDS address.
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      if (valid[i] && (u[i] & mask) == prefix) atomicAdd(&hist[wave][(u[i] >> shift) & dmask], 1);
-    }
-    __syncthreads();
-    if (wave == 0) {
-      // Lane l owns bins 255-4l .. 252-4l (descending); the exclusive scan of
-      // the lane totals counts the keys in higher bins.  Exactly one bin
-      // holds the kr-th key, since kr never exceeds the keys on the prefix.
-      int c[4], tot = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int bin = 255 - 4 * lane - i;
-        c[i] = hist[0][bin] + hist[1][bin] + hist[2][bin] + hist[3][bin];
-        tot += c[i];
-      }
-      int above = wave_incl_scan_dpp(tot) - tot;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (above < kr && kr <= above + c[i]) {
-          sh_bin = 255 - 4 * lane - i;
-          sh_kr = kr - above;
-          sh_whole = (kr - above) == c[i];
-        }
-        above += c[i];
-      }
-    }
-    __syncthreads();
-    prefix |= static_cast<uint32_t>(sh_bin) << shift;
-    mask |= dmask << shift;
-    kr = sh_kr;
-    remaining = shift;
-    // The boundary bin is taken whole: every key on the new prefix is
-    // >= prefix (low bits zero), so theta = prefix with all ties taken
-    // selects exactly the same keys.
-    if (sh_whole) {
-      kr = 0x7FFFFFFF;
-      break;
-    }
-  }
-  const uint32_t theta = prefix;
-
-  // Per-(slot, wave) counts of keys > theta and == theta, in output order
-  // j = 4*slot + wave; one DPP scan over j gives each (slot, wave) the counts
-  // before it.
-  const uint64_t below = (1ull << lane) - 1ull;
-  uint64_t bgt[VPL], beq[VPL];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    bgt[i] = __ballot(valid[i] && u[i] > theta);
-    beq[i] = __ballot(valid[i] && u[i] == theta);
-    if (lane == 0) {
-      cnt_gt[4 * i + wave] = __popcll(bgt[i]);
-      cnt_eq[4 * i + wave] = __popcll(beq[i]);
-    }
-  }
-  __syncthreads();
-  const int cg = lane < 4 * VPL ? cnt_gt[lane] : 0;
-  const int ce = lane < 4 * VPL ? cnt_eq[lane] : 0;
-  const int gt_excl = wave_incl_scan_dpp(cg) - cg;
-  const int eq_excl = wave_incl_scan_dpp(ce) - ce;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int g0 = __builtin_amdgcn_readlane(gt_excl, 4 * i + wave);
-    const int e0 = __builtin_amdgcn_readlane(eq_excl, 4 * i + wave);
-    const bool gt = (bgt[i] >> lane) & 1ull;
-    const bool eq = (beq[i] >> lane) & 1ull;
-    const bool take = gt || (eq && e0 + __popcll(beq[i] & below) < kr);
-    const uint64_t tb = __ballot(take);
-    if (take) sel[g0 + min(e0, kr) + __popcll(tb & below)] = i * 256 + tid;
-  }
-  __syncthreads();
-  return kk;
 }
 
 // Rows of at most 64*VPL keys: one wave per row, four rows per workgroup,

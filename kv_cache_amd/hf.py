@@ -184,9 +184,13 @@ def int4_sparse_attention_forward(module, query: torch.Tensor, key: torch.Tensor
     bmax = bufs["bmax"][: b * hkv * nb].view(b, hkv, nb)
     K.decode_scores(q, c.chan_idx, c.slab, c.slab_scales, t, layer.block, bmax=bmax)
     sel = bufs["sel"][: b * hkv * k].view(b, hkv, k)
-    K.block_topk(bmax, k, out=sel, workspace=bufs["topk_ws"])
-    out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, t, scaling,
-                             workspace=bufs["attn_ws"], out=bufs["out"])
+    if nb <= K.SELECT_MAX_BLOCKS:
+        out = K.sparse_attention_select(q, layer.keys, layer.values, bmax, k, layer.block, t, scaling,
+                                        workspace=bufs["attn_ws"], sel_out=sel, out=bufs["out"])
+    else:
+        K.block_topk(bmax, k, out=sel, workspace=bufs["topk_ws"])
+        out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, t, scaling,
+                                 workspace=bufs["attn_ws"], out=bufs["out"])
     return out[:, None].to(query.dtype), None
 
 

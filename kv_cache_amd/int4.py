@@ -216,8 +216,8 @@ def attention_workspace_bytes(batch: int, q_heads: int, kv_heads: int, head_dim:
 
 def attention_workspace(batch: int, q_heads: int, kv_heads: int, head_dim: int, n_sel: int, block: int,
                         device) -> torch.Tensor:
-    """Zero-filled workspace for ``sparse_attention`` calls up to these sizes.
-    Its leading ticket words must be zero before the first call; every
+    """Zero-filled workspace for ``sparse_attention`` calls with these
+    heads and at most n_sel * block selected slots.  Its leading ticket words must be zero before the first call; every
     completed call leaves them zero, so one workspace serves any number of
     calls.  Calls sharing a workspace must not overlap in time."""
     need = attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block)
@@ -249,6 +249,45 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
                                             block_ids.data_ptr(), n, int(block), float(scaling),
                                             workspace.data_ptr(), workspace.numel() * 4, out.data_ptr(),
                                             _lib.stream_of(q)))
+    return out
+
+
+# Rows of at most this many blocks can select inside the attention kernel.
+SELECT_MAX_BLOCKS = 4096
+
+
+def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                            bmax: torch.Tensor, n_sel: int, block: int, tokens: int, scaling: float, *,
+                            workspace: torch.Tensor | None = None, sel_out: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """``sparse_attention`` over the n_sel blocks with the largest block
+    maxima (f32 [B,Hkv,>=ceil(tokens/block)], the selection of ``block_topk``),
+    selected inside the attention kernel.  sel_out (int32 [B,Hkv,n_sel]), when
+    given, receives the selection.  Returns bf16 [B,Hq,D]."""
+    lib = _lib.load()
+    _check_kv("key", key)
+    _check_kv("value", value)
+    _require(key.stride() == value.stride() and key.shape == value.shape, "key/value layout mismatch")
+    q = query.contiguous()
+    b, hq, d = q.shape
+    hkv = key.size(1)
+    _require(bmax.is_cuda and bmax.dtype == torch.float32, "bmax must be CUDA float32")
+    nb = math.ceil(int(tokens) / int(block))
+    _require(bmax.dim() == 3 and bmax.shape[:2] == (b, hkv) and bmax.size(2) >= nb and bmax.stride(2) == 1
+             and bmax.stride(1) == bmax.size(2) and bmax.stride(0) == hkv * bmax.size(2),
+             "bmax must be contiguous [B, Hkv, >= blocks]")
+    if sel_out is not None:
+        _require(sel_out.dtype == torch.int32 and sel_out.is_contiguous() and sel_out.numel() == b * hkv * n_sel,
+                 "sel_out must be contiguous int32 [B, Hkv, n_sel]")
+    if workspace is None:
+        workspace = attention_workspace(b, hq, hkv, d, n_sel, block, q.device)
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_sparse_attention_select(
+            q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
+            int(tokens), d, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), float(scaling),
+            workspace.data_ptr(), workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
     return out
 
 
@@ -301,6 +340,7 @@ class SparseDecodeStep:
         self.topk_ws = topk_workspace(batch * kv_heads, nb, topk, device)
         self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, topk, block, device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.fused = nb <= SELECT_MAX_BLOCKS
 
     @classmethod
     def for_mode(cls, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
@@ -319,8 +359,14 @@ class SparseDecodeStep:
 
     def __call__(self, query: torch.Tensor, cache: Int4KCache, key: torch.Tensor, value: torch.Tensor,
                  scaling: float) -> torch.Tensor:
+        """Rows of at most SELECT_MAX_BLOCKS blocks select inside the attention
+        kernel (two launches); longer rows run the top-k launch between.  The
+        selection lands in ``self.sel`` either way."""
         decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.tokens, self.block,
                       bmax=self.bmax)
+        if self.fused:
+            return sparse_attention_select(query, key, value, self.bmax, self.topk, self.block, self.tokens,
+                                           scaling, workspace=self.workspace, sel_out=self.sel, out=self.out)
         block_topk(self.bmax, self.topk, out=self.sel, workspace=self.topk_ws)
         return sparse_attention(query, key, value, self.sel, self.block, self.tokens, scaling,
                                 workspace=self.workspace, out=self.out)

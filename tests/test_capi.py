@@ -81,8 +81,9 @@ def test_host_side_validation(call, msg):
 def _attn_splits(rows, n_slots, g, target=256, max_iters=16):
     """Splits per row of qkv_sparse_attention: a workgroup round covers
     4 waves x 4*NI slots (NI = 8 for G <= 2, else 4); chunks per wave double
-    (up to 16) while the grid keeps at least ``target`` workgroups."""
+    (up to 16, 8 for G = 8) while the grid keeps at least ``target`` workgroups."""
     per_iter = 16 * (8 if g <= 2 else 4)
+    max_iters = min(max_iters, 8) if g >= 8 else max_iters
     it = 1
     while it < max_iters and rows * -(-n_slots // (per_iter * it * 2)) >= target:
         it *= 2
@@ -95,12 +96,29 @@ def test_workspace_size_formula():
     assert _attn_splits(64, 2048, 2) == 4             # cfg2: 4 splits of 512 slots
     assert _attn_splits(256, 4096, 4) == 4            # cfg3: 4 splits of 1024 slots
     assert _attn_splits(8, 300, 8) == 5
-    for b, hq, hkv, n_sel, block in [(8, 16, 8, 128, 16), (1, 16, 8, 256, 1), (1, 64, 8, 300, 1),
-                                     (32, 32, 8, 256, 16), (8, 16, 8, 2048, 16), (1, 8, 8, 7, 64)]:
+    # sized for the larger of the call's own splits and the bound on the
+    # splits of smaller calls, 2 * (ceil(256 / rows) - 1) (capped by the
+    # slot count): 6 at cfg2 (64 rows), 0 at cfg3 (256 rows)
+    for b, hq, hkv, n_sel, block, splits in [(8, 32, 8, 128, 16, 6), (32, 32, 8, 256, 16, 4),
+                                             (1, 8, 8, 7, 64, 4), (8, 16, 8, 2048, 16, 16)]:
         rows, g = b * hkv, hq // hkv
-        want = 4 * (t + rows * _attn_splits(rows, n_sel * block, g) * g * 130)
-        assert lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, block) == want
+        assert lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, block) == \
+            4 * (t + rows * splits * g * 130)
     assert lib.qkv_sparse_attention_workspace_bytes(1, 16, 8, 64, 256, 1) == -1
+
+
+@pytest.mark.parametrize("b,hq,hkv,block", [(1, 32, 8, 16), (8, 32, 8, 16), (1, 16, 8, 1), (1, 64, 8, 1),
+                                            (2, 8, 4, 16), (4, 16, 8, 64), (32, 32, 8, 16)])
+def test_workspace_covers_every_smaller_selection(b, hq, hkv, block):
+    # The split count is not monotonic in the slot count; a workspace sized
+    # for n_sel must still serve every call with fewer blocks (brute force).
+    rows, g = b * hkv, hq // hkv
+    t = 65536
+    worst = 0
+    for n_sel in range(1, 1200 if block > 1 else 9000, 1 if block > 1 else 7):
+        worst = max(worst, 4 * (t + rows * _attn_splits(rows, n_sel * block, g) * g * 130))
+        got = lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, block)
+        assert got >= worst, (n_sel, got, worst)
 
 
 def test_python_wrappers_refuse_cpu_tensors():

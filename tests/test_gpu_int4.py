@@ -294,6 +294,74 @@ def test_sparse_attention_workspace_reuse():
     assert int(tickets.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("g_size,batch,t,block,nsel", [
+    (4, 8, 32768, 16, 128),     # cfg2's shape: 2048 blocks, 128 kept
+    (2, 2, 65536, 16, 256),     # 4096 blocks: the largest row that selects in the kernel
+    (4, 1, 4096, 1, 4096),      # every block kept
+    (1, 3, 3000, 64, 7),        # partial last block, G = 1
+    (8, 2, 700, 16, 44),        # G = 8
+    (4, 1, 10, 16, 1),          # one block
+])
+def test_sparse_attention_select_equals_unfused(g_size, batch, t, block, nsel):
+    # The fused selection equals block_topk on the same maxima (bit-exact,
+    # lowest index wins ties) and the attention equals the unfused call's.
+    hkv = 8 if batch > 1 else 4
+    hq = hkv * g_size
+    nb = -(-t // block)
+    gen = torch.Generator().manual_seed(t + nsel)
+    q = torch.randn((batch, hq, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    k = torch.randn((batch, hkv, t, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn((batch, hkv, t, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    bmax = torch.randint(-40, 40, (batch, hkv, nb), generator=gen).float()   # heavy ties
+    bmax[0, 0] = torch.randn(nb, generator=gen)
+    bmax[-1, -1, : nb // 2] = -float("inf")
+    bmax = bmax.to(DEV)
+    sel = torch.empty((batch, hkv, nsel), dtype=torch.int32, device=DEV)
+    out = K.sparse_attention_select(q, k, v, bmax, nsel, block, t, 0.088, sel_out=sel)
+    want_sel = K.block_topk(bmax, nsel)
+    assert torch.equal(sel, want_sel)
+    assert np.array_equal(sel.cpu().numpy().reshape(-1, nsel),
+                          O.topk_lowest_index(bmax.cpu().numpy().reshape(-1, nb), nsel))
+    want = K.sparse_attention(q, k, v, want_sel, block, t, 0.088)
+    assert torch.equal(out, want)
+
+
+def test_sparse_attention_select_wide_rows_and_reuse():
+    # bmax rows wider than the block count (a capacity-sized buffer): values
+    # past the last block are never selected; one workspace serves calls of
+    # different sizes, with and without sel_out.
+    gen = torch.Generator().manual_seed(12)
+    b, hkv, g_size, cap = 2, 4, 4, 9000
+    q = torch.randn((b, hkv * g_size, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    kc = torch.randn((b, hkv, cap, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((b, hkv, cap, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    ws = K.attention_workspace(b, hkv * g_size, hkv, 128, 512, 16, DEV)
+    for t, nsel in [(8000, 300), (1000, 17), (8999, 512), (33, 2)]:
+        nb = -(-t // 16)
+        wide = torch.randn((b, hkv, 600), generator=gen).to(DEV)
+        wide[..., nb:] = 1e30
+        k, v = kc[:, :, :t], vc[:, :, :t]
+        sel = torch.empty((b, hkv, nsel), dtype=torch.int32, device=DEV)
+        out = K.sparse_attention_select(q, k, v, wide, nsel, 16, t, 0.09, workspace=ws, sel_out=sel)
+        out2 = K.sparse_attention_select(q, k, v, wide, nsel, 16, t, 0.09, workspace=ws)
+        want_sel = K.block_topk(wide[..., :nb].contiguous(), nsel)
+        assert torch.equal(sel, want_sel), t
+        assert torch.equal(out, out2)
+        want = O.sparse_attention(f32(q), f32(k), f32(v), want_sel.cpu().numpy(), 16, t, 0.09)
+        assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL), t
+    assert int(ws[:65536].view(torch.int32).abs().sum()) == 0
+
+
+def test_sparse_attention_select_rejects_long_rows():
+    q = torch.randn((1, 8, 128)).to(torch.bfloat16).to(DEV)
+    k = torch.randn((1, 2, 4097, 128)).to(torch.bfloat16).to(DEV)
+    bmax = torch.randn((1, 2, 4097), device=DEV)
+    with pytest.raises(RuntimeError, match="at most 4096 blocks"):
+        K.sparse_attention_select(q, k, k, bmax, 16, 1, 4097, 0.1)
+    with pytest.raises(RuntimeError, match="n_sel <= blocks"):
+        K.sparse_attention_select(q, k[:, :, :64], k[:, :, :64], bmax, 65, 1, 64, 0.1)
+
+
 def test_sparse_attention_no_valid_block_gives_zero():
     q = torch.randn((1, 2, 128)).to(torch.bfloat16).to(DEV)
     k = torch.randn((1, 1, 64, 128)).to(torch.bfloat16).to(DEV)
