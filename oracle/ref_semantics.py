@@ -214,3 +214,143 @@ def qabs_candidate_attention_cpu(query_states, key_states, value_states, dim_cou
     weights = F.softmax(scores, dim=-1, dtype=torch.float32).to(query_states.dtype)
     out = torch.sum(weights[:, :, :, None] * sel_v, dim=2)
     return out[:, None, :, :].contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Candidate reuse and exact rerank (qabs{S}cand{pct}reuse[final|2set])
+# ---------------------------------------------------------------------------
+
+def budget_count(history: int, fraction: float) -> int:
+    """``min(history, max(1, ceil(fraction * history)))`` (EV:4132, 4270)."""
+    return min(int(history), max(1, math.ceil(float(fraction) * int(history))))
+
+
+def threshold_mask(partial, requested: int) -> np.ndarray:
+    """EV:3988-3989: every value >= the row's ``requested``-th largest (ties
+    at the threshold are all kept, so a row may hold more than requested)."""
+    p = np.asarray(partial, dtype=np.float32)
+    thr = -np.sort(-p, axis=-1)[..., requested - 1:requested]
+    return p >= thr
+
+
+def final_indices_np(selected, selected_valid, history: int, key_count: int, sink: int, recent: int,
+                     keep_self: bool):
+    """EV:2938-2982 in numpy: the selected history indices with the sink and
+    recent ranges masked invalid, then the sink range, the recent range (not
+    overlapping the sink) and the current token appended."""
+    sel = np.asarray(selected, dtype=np.int64)
+    valid = np.asarray(selected_valid, dtype=bool).copy()
+    lead = sel.shape[:-1]
+    sink_end = min(sink, history) if sink > 0 else 0
+    recent_start = history
+    if recent > 0:
+        recent_start = max(0, history - recent)
+        valid &= ~((sel >= recent_start) & (sel < history))
+    if sink_end > 0:
+        valid &= sel >= sink_end
+    parts, vparts = [sel], [valid]
+    if sink_end > 0:
+        parts.append(np.broadcast_to(np.arange(sink_end), (*lead, sink_end)))
+        vparts.append(np.ones((*lead, sink_end), dtype=bool))
+    if recent > 0 and recent_start < history:
+        start = max(recent_start, sink_end)
+        if start < history:
+            parts.append(np.broadcast_to(np.arange(start, history), (*lead, history - start)))
+            vparts.append(np.ones((*lead, history - start), dtype=bool))
+    if keep_self:
+        parts.append(np.full((*lead, 1), key_count - 1, dtype=np.int64))
+        vparts.append(np.ones((*lead, 1), dtype=bool))
+    return np.concatenate(parts, axis=-1).astype(np.int64), np.concatenate(vparts, axis=-1)
+
+
+def reuse_select(query, key_states, current, previous, previous_final, sink: int, recent: int,
+                 top_fraction: float, keep_self: bool, scaling: float):
+    """The selection the reference asks of its absent ``reuse_select`` kernel
+    (called at EV:3901-3914 with the signature of EV:3881-3892), restated from
+    the fallback that runs when the kernel is missing (EV:4257-4365, no
+    block or evidence-span option):
+
+    * scores: full-D fp32 dot * scaling on the union current | previous |
+      previous_final, -inf elsewhere (candidate_full_scores with no sink or
+      recent protection, EV:4257-4267: the non-lagged modes pass 0 there);
+    * the ``budget_count(history, top_fraction)`` largest scores (EV:4270-4274;
+      ``torch.topk``, ties here to the lower index), valid where finite;
+    * history_final: the valid selections, then the sink and recent ranges
+      set (EV:4301-4307);
+    * final indices and validity by ``final_indices_np`` (EV:4365, 2938-2982).
+
+    query [B,H,D]; key_states [B,H,K,D] with K = history + 1; masks bool
+    [B,H,history] (previous ones may be None).  Selected indices come in
+    ascending order (the reference's come in descending score order; only the
+    set and its validity carry meaning).  Returns (final_indices int64,
+    final_valid bool, history_final bool [B,H,history]).
+    """
+    from .qkv_oracle import topk_lowest_index
+
+    cur = np.asarray(current, dtype=bool)
+    b, h, history = cur.shape
+    key = np.asarray(key_states, dtype=np.float32)
+    key_count = key.shape[2]
+    scores = candidate_full_scores(query, key[:, :, :history], cur, previous, previous_final, 0, 0,
+                                   scaling)
+    keep = budget_count(history, top_fraction)
+    sel = topk_lowest_index(scores.reshape(-1, history), keep).reshape(b, h, keep).astype(np.int64)
+    valid = np.isfinite(np.take_along_axis(scores, sel, axis=-1))
+    hist_final = np.zeros((b, h, history), dtype=bool)
+    for bi in range(b):
+        for hi in range(h):
+            hist_final[bi, hi, sel[bi, hi][valid[bi, hi]]] = True
+    if sink > 0:
+        hist_final[..., : min(sink, history)] = True
+    if recent > 0:
+        hist_final[..., max(0, history - recent):] = True
+    fi, fv = final_indices_np(sel, valid, history, key_count, sink, recent, keep_self)
+    return fi, fv, hist_final
+
+
+def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: float, top_fraction: float,
+                      sink: int, recent: int, keep_self: bool, scaling: float,
+                      previous_candidate=None, previous_final=None):
+    """One decode step of ``_qabs_reuse_fast_attention_forward`` (EV:3991-4397)
+    for the default candidate selection (``topk``) without block expansion.
+
+    query [B,Hq,D]; key/value [B,Hkv,T,D] (query head h reads KV head
+    h // (Hq/Hkv), the grouping of EV:6248-6251).  previous_* are the masks
+    the previous step left (bool [B,Hq,>= T-2]; pass None when there is no
+    previous step, or to leave one out as the ``reusefinal`` / ``reuse2set``
+    modes do, EV:955-960).  They are cut or padded with False to the history
+    length, as ``ReuseCandidateState.previous_layer_masks`` does (EV:1645-1662).
+
+    Steps: top-|q| dims and fp32 partial scores (EV:4068, 4123-4135), the
+    threshold mask (EV:4136-4144, 3988-3989), ``reuse_select``, and the
+    attention over the final indices (QK:335-419, fp64 here).  A cache of at
+    most one key returns the last value (EV:4012-4014).
+
+    Returns (out float64 [B,1,Hq,D], current bool [B,Hq,history],
+    history_final bool [B,Hq,history]); the last two are the state the next
+    step reads (EV:4384-4393).
+    """
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, hq, d = q.shape
+    g = hq // k.shape[1]
+    kx, vx = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    key_count = k.shape[2]
+    if key_count <= 1:
+        return vx[:, :, -1:, :].transpose(0, 2, 1, 3).astype(np.float64), None, None
+    history = key_count - 1
+    partial = partial_scores(q, kx[:, :, :history], dim_count)
+    current = threshold_mask(partial, budget_count(history, candidate_fraction))
+
+    def fit(m):
+        if m is None:
+            return None
+        m = np.asarray(m, dtype=bool)[..., :history]
+        pad = history - m.shape[-1]
+        return np.concatenate([m, np.zeros((*m.shape[:-1], pad), dtype=bool)], axis=-1) if pad else m
+
+    fi, fv, hist_final = reuse_select(q, kx, current, fit(previous_candidate), fit(previous_final), sink, recent,
+                                      top_fraction, keep_self, scaling)
+    out = final_attention(q, kx, vx, fi, fv, scaling)
+    return out, current, hist_final

@@ -1,0 +1,127 @@
+"""Pins the candidate-reuse restatement (oracle/ref_semantics.py: reuse_select,
+reuse_decode_step) against golden vectors written by the reference itself
+(tests/golden/make_reuse_vectors.py: consecutive decode steps of the
+reference's reuse driver, run on the CPU), plus known answers and invariants
+of the selection."""
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import ref_semantics as R
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+SCENARIOS = ["s8c5_fp32", "s16c10_final_fp32", "s8c3_2set_fp32", "s8c5_bf16"]
+
+
+def load_golden(name):
+    """Inputs and per-step outputs of one golden scenario."""
+    z = np.load(GOLDEN / f"reuse_{name}.npz")
+    t_max = int(z["t_max"])
+    bf = lambda a: (a.astype(np.int32) << 16).view(np.float32)   # bf16 bits -> fp32
+    m = re.fullmatch(r"qabs(\d+)cand(\d+)reuse(2set|final)?", str(z["mode"]))
+    return {
+        "mode": str(z["mode"]), "dtype": str(z["dtype"]), "dims": int(m.group(1)), "cand": int(m.group(2)) / 100,
+        "use_prev_candidate": m.group(3) != "final", "use_prev_final": m.group(3) != "2set",
+        "q": z["q"][:, :, :, 0, :], "k": bf(z["k_bf16"]), "v": bf(z["v_bf16"]), "t0": int(z["t0"]),
+        "steps": int(z["steps"]), "top_fraction": float(z["top_fraction"]), "sink": int(z["sink"]),
+        "recent": int(z["recent"]), "keep_self": bool(z["keep_self"]), "scaling": float(z["scaling"]),
+        "out": z["out"][:, :, 0],   # [steps, B, Hq, D]
+        "candidate": np.unpackbits(z["candidate"], axis=-1)[..., :t_max].astype(bool),
+        "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
+    }
+
+
+@pytest.mark.parametrize("name", SCENARIOS)
+def test_decode_steps_match_reference_vectors(name):
+    g = load_golden(name)
+    pc = pf = None
+    # fp32: only the attention's summation order differs; bf16: the reference
+    # rounds the softmax weights to bf16 (EV:4372-4373)
+    tol = dict(rtol=1e-5, atol=1e-5) if g["dtype"] == "float32" else dict(rtol=1e-2, atol=2e-2)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        out, cur, hf = R.reuse_decode_step(
+            g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"], g["top_fraction"], g["sink"],
+            g["recent"], g["keep_self"], g["scaling"], pc if g["use_prev_candidate"] else None,
+            pf if g["use_prev_final"] else None)
+        assert np.array_equal(cur, g["candidate"][s][..., : n - 1]), (name, s)
+        assert np.array_equal(hf, g["final"][s][..., : n - 1]), (name, s)
+        np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
+        pc, pf = cur, hf
+
+
+def test_threshold_mask_keeps_ties():
+    p = np.array([[3.0, 1.0, 3.0, 2.0]], np.float32)
+    assert R.threshold_mask(p, 1).tolist() == [[True, False, True, False]]
+    assert R.threshold_mask(p, 3).tolist() == [[True, False, True, True]]
+    assert R.budget_count(240, 0.05) == 12 and R.budget_count(10, 0.0) == 1 and R.budget_count(3, 2.0) == 3
+
+
+def _row(scores):
+    """q = e0, K[t] = (s_t, 0, ...) so that the full score of t is s_t."""
+    t = len(scores)
+    k = np.zeros((1, 1, t + 1, 4), np.float32)
+    k[0, 0, :t, 0] = scores
+    q = np.zeros((1, 1, 4), np.float32)
+    q[0, 0, 0] = 1.0
+    return q, k
+
+
+def _mask(t, ids):
+    m = np.zeros((1, 1, t), bool)
+    m[0, 0, list(ids)] = True
+    return m
+
+
+def test_reuse_select_known_answer():
+    q, k = _row([9, 5, 7, 1, 0, 8, 3, 2])
+    fi, fv, hf = R.reuse_select(q, k, _mask(8, [1, 3, 5]), _mask(8, [2]), _mask(8, [6]), sink=1, recent=2,
+                                top_fraction=0.3, keep_self=True, scaling=1.0)
+    # union {1,2,3,5,6} scores {5,7,1,8,3}: top 3 = {5, 2, 1}, ascending
+    assert fi.tolist() == [[[1, 2, 5, 0, 6, 7, 8]]]
+    assert fv.tolist() == [[[True] * 7]]
+    assert np.flatnonzero(hf[0, 0]).tolist() == [0, 1, 2, 5, 6, 7]
+
+
+def test_reuse_select_protected_and_short_union():
+    q, k = _row([9, 5, 7, 1, 0, 8, 3, 2])
+    # union {1, 6}: 3 slots, the third is the lowest -inf index (0), invalid;
+    # 6 lies in the recent range, so it is masked and the range appended
+    fi, fv, hf = R.reuse_select(q, k, _mask(8, [1]), None, _mask(8, [6]), sink=0, recent=2, top_fraction=0.3,
+                                keep_self=False, scaling=1.0)
+    assert fi.tolist() == [[[0, 1, 6, 6, 7]]]
+    assert fv.tolist() == [[[False, True, False, True, True]]]
+    assert np.flatnonzero(hf[0, 0]).tolist() == [1, 6, 7]
+
+
+def test_reuse_select_ties_take_lower_index():
+    q, k = _row([4, 4, 4, 4, 4, 4])
+    fi, fv, _ = R.reuse_select(q, k, _mask(6, [5, 3, 1, 2]), None, None, 0, 0, 0.5, False, 1.0)
+    assert fi.tolist() == [[[1, 2, 3]]] and fv.all()
+
+
+def test_reuse_select_invariants():
+    rng = np.random.default_rng(3)
+    b, h, t, d = 2, 3, 97, 16
+    q = rng.standard_normal((b, h, d)).astype(np.float32)
+    k = rng.standard_normal((b, h, t + 1, d)).astype(np.float32)
+    masks = [rng.random((b, h, t)) < p for p in (0.1, 0.05, 0.03)]
+    fi, fv, hf = R.reuse_select(q, k, *masks, 3, 4, 0.1, True, 0.25)
+    union = masks[0] | masks[1] | masks[2]
+    keep = R.budget_count(t, 0.1)
+    full = np.einsum("bhd,bhtd->bht", q.astype(np.float64), k[:, :, :t].astype(np.float64)) * 0.25
+    for bi in range(b):
+        for hi in range(h):
+            sel = fi[bi, hi, :keep]
+            ok = np.isfinite(np.where(union[bi, hi], full[bi, hi], -np.inf))[sel]
+            chosen = set(sel[ok].tolist())
+            assert len(chosen) == min(keep, int(union[bi, hi].sum()))
+            rest = [x for x in np.flatnonzero(union[bi, hi]) if x not in chosen]
+            if rest and chosen:
+                assert min(full[bi, hi, list(chosen)]) >= max(full[bi, hi, rest]) - 1e-5
+            assert hf[bi, hi, :3].all() and hf[bi, hi, t - 4:].all()
+            assert set(np.flatnonzero(hf[bi, hi]).tolist()) == chosen | {0, 1, 2} | set(range(t - 4, t))
+            assert fi[bi, hi, -1] == t and fv[bi, hi, -1]
