@@ -220,6 +220,86 @@ int qkv_sparse_attention_select(const void* query, const void* key, const void* 
                                 float* workspace, int64_t workspace_bytes, int32_t* sel_out, void* out,
                                 void* stream);
 
+/* qkv_sparse_attention with one token list per query head (group size 1,
+ * one-token blocks): row (b, h) attends over token_ids [B,Hq,n_ids] (ids
+ * outside [0, tokens) skipped) of K/V head h / (Hq/Hkv).  Replaces the
+ * reference's final-attention kernel (QK:335-419) on GQA-shaped K/V without
+ * the repeat_interleave of EV:6248-6251.  Workspace:
+ * qkv_sparse_attention_workspace_bytes(B, Hq, Hq, D, n_ids, 1). */
+int qkv_token_attention(const void* query, const void* key, const void* value, const int64_t* kv_strides,
+                        int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                        const int32_t* token_ids, int64_t n_ids, float scaling, float* workspace,
+                        int64_t workspace_bytes, void* out, void* stream);
+
+/* ======================================================================
+ * Candidate reuse and exact rerank (the qabs{S}cand{pct}reuse[final|2set]
+ * decode step, EV:3991-4397).  Rows are (sequence, query head)
+ * r = b * Hq + h; a row reads K head h / (Hq/Hkv).  dtype selects bf16,
+ * fp16 or fp32 for query and K.  Masks are uint8 0/1 (torch.bool) with
+ * row stride mask_ld.
+ * ====================================================================== */
+
+/* Entries per row of the final index list: keep + sink range + recent
+ * range (not overlapping the sink) + 1 when keep_self, with
+ * keep = min(history, max(1, ceil(top_fraction * history))) (EV:4270,
+ * 2938-2982).  -1 for history <= 0. */
+int64_t qkv_reuse_final_count(int64_t history, int64_t protect_sink, int64_t protect_recent,
+                              double top_fraction, int keep_self);
+
+/* Workspace bytes of qkv_reuse_select for rows x history. */
+int64_t qkv_reuse_select_workspace_bytes(int64_t rows, int64_t history, double top_fraction);
+
+/* The reference's absent reuse_select kernel (EV:3881-3919, called at
+ * EV:4200-4216), with the semantics of the fallback it replaces
+ * (EV:4257-4365): full-D fp32 scores * scaling of the union current |
+ * previous | previous_final (previous masks may be NULL; no sink/recent
+ * protection in the union), the keep largest (lowest index wins ties),
+ * valid where finite; history_final = the valid selections plus the first
+ * protect_sink and last protect_recent history positions; final_indices /
+ * final_valid [rows, n_out] = the selection in ascending index order with
+ * protected entries invalid, then the sink range, the recent range and the
+ * current token key_count - 1 (when keep_self).  attn_ids (optional) int32
+ * [rows, n_out] holds the same list with -1 for invalid entries, ready for
+ * qkv_token_attention.  query [B,Hq,D]; key [B,Hkv,key_count,D] with
+ * k_strides {b,h,t,d} (d contiguous); history = key_count - 1.
+ * history_final (row stride history_final_ld) may be the previous_final
+ * buffer: it is written after every read of the masks. */
+int qkv_reuse_select(const void* query, const void* key, const int64_t* k_strides, int dtype, int64_t batch,
+                     int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
+                     const uint8_t* current, const uint8_t* previous, const uint8_t* previous_final,
+                     int64_t mask_ld, int64_t protect_sink, int64_t protect_recent, double top_fraction,
+                     int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
+                     int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                     uint8_t* history_final, int64_t history_final_ld, void* stream);
+
+/* Partial scores of the reuse step (EV:4123-4135 on the dim-major copy,
+ * partial_scores_dim_major QK:63-96 with the dims of QK:120-145): for each
+ * row, the top-|q| dim_count dims (descending |q|, lower dim first on ties,
+ * clamped to [1, min(D, 128)]) and out[r, t] = sum_s q[d_s] * K[d_s, t] in
+ * selection order, fp32.  key_dim_major [B,Hkv,D,*] with strides {b,h,d,t}
+ * (t contiguous); out row stride out_ld. */
+int qkv_reuse_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
+                             int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
+                             int64_t dim_count, float* out, int64_t out_ld, void* stream);
+
+/* Workspace bytes of qkv_threshold_mask. */
+int64_t qkv_threshold_mask_workspace_bytes(int64_t rows, int64_t n, int64_t k);
+
+/* Candidate mask of the reuse step (EV:4136-4144, 3988-3989):
+ * mask[r, t] = values[r, t] >= the row's k-th largest value (ties at the
+ * threshold all kept).  values f32 [rows, >= ld]; mask uint8 row stride
+ * mask_ld. */
+int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, uint8_t* mask,
+                       int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Dim-major copy of K tokens [t_begin, t_end): key_dim_major[b, j, d, t] =
+ * key[b, j, t, d] (the reference's incremental transposed copy,
+ * EV:2018-2042, kept per KV head).  k_strides {b,h,t,d} (d contiguous);
+ * kdm_strides {b,h,d,t} (t contiguous).  head_dim <= 512 (256 for fp32). */
+int qkv_dim_major_append(const void* key, const int64_t* k_strides, int dtype, int64_t batch, int64_t kv_heads,
+                         int64_t head_dim, int64_t t_begin, int64_t t_end, void* key_dim_major,
+                         const int64_t* kdm_strides, void* stream);
+
 /* ======================================================================
  * Chunked-prefill block selection (no reference counterpart: the reference
  * prefills with dense attention, EV:7079-7111, dense QK at EV:6602-6604).

@@ -25,7 +25,7 @@ ABI_VERSION = 1
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _c = ctypes
-_vp, _i64, _i32, _f32 = _c.c_void_p, _c.c_int64, _c.c_int, _c.c_float
+_vp, _i64, _i32, _f32, _f64 = _c.c_void_p, _c.c_int64, _c.c_int, _c.c_float, _c.c_double
 _P = _c.POINTER
 
 # name -> (restype, argtypes); mirrors include/qkv.h.
@@ -58,6 +58,17 @@ _PROTOTYPES = {
                                     _i64, _f32, _vp, _i64, _vp, _vp]),
     "qkv_sparse_attention_select": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                            _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
+    "qkv_token_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _f32, _vp,
+                                   _i64, _vp, _vp]),
+    "qkv_reuse_final_count": (_i64, [_i64, _i64, _i64, _f64, _i32]),
+    "qkv_reuse_select_workspace_bytes": (_i64, [_i64, _i64, _f64]),
+    "qkv_reuse_select": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
+                                _i64, _f64, _i32, _f32, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "qkv_reuse_partial_scores": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                                        _vp]),
+    "qkv_threshold_mask_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "qkv_threshold_mask": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "qkv_dim_major_append": (_i32, [_vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _P(_i64), _vp]),
 }
 
 _LIB = None

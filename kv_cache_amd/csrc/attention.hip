@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
     int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
     uint32_t* __restrict__ tickets, uint16_t* __restrict__ out, const float* __restrict__ bmax,
-    int64_t bmax_ld, int32_t* __restrict__ sel_out) {
+    int64_t bmax_ld, int32_t* __restrict__ sel_out, int kv_div) {
   constexpr int CH = 4 * NI;               // token slots per wave chunk
   static_assert(CH <= 64, "one slot per lane when resolving token ids");
 
@@ -175,8 +175,9 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     for (int i = 0; i < NI; ++i) tk[i] = __builtin_amdgcn_ds_bpermute((4 * i + grp) << 2, my_tok);
   };
 
-  const uint16_t* kb = key + b * sb + j * sh + cc * 8;
-  const uint16_t* vb = value + b * sb + j * sh + cc * 8;
+  const int jk = j / kv_div;   // the K/V head this row reads
+  const uint16_t* kb = key + b * sb + jk * sh + cc * 8;
+  const uint16_t* vb = value + b * sb + jk * sh + cc * 8;
   // Invalid slots load token 0 of the row (in bounds) and are masked later.
   auto load_kv = [&](const int (&tk)[NI], uint4 (&kx)[NI], uint4 (&vx)[NI]) {
 #pragma unroll
@@ -474,7 +475,7 @@ int launch_attention(const char* what, const void* query, const void* key, const
                      const int64_t* kv_strides, int64_t batch, int64_t q_heads, int64_t kv_heads,
                      int64_t tokens, int64_t head_dim, const int32_t* block_ids, const float* bmax,
                      int64_t bmax_ld, int32_t* sel_out, int64_t n_sel, int64_t block, float scaling,
-                     float* workspace, int64_t workspace_bytes, void* out, void* stream) {
+                     float* workspace, int64_t workspace_bytes, void* out, void* stream, int kv_div = 1) {
   const bool sel = bmax != nullptr;
   if (!query || !key || !value || !kv_strides || !(sel || block_ids) || !workspace || !out)
     return fail(QKV_ERR_INVALID, "%s: null pointer", what);
@@ -522,7 +523,7 @@ int launch_attention(const char* what, const void* query, const void* key, const
       q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                      \
       static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),             \
       static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o, bmax,   \
-      bmax_ld, sel_out)
+      bmax_ld, sel_out, kv_div)
 #define QKV_ATTN(GG, IT)             \
   if (sel) QKV_ATTN_S(GG, IT, true); \
   else QKV_ATTN_S(GG, IT, false);
@@ -576,4 +577,19 @@ QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, c
   return launch_attention("qkv_sparse_attention_select", query, key, value, kv_strides, batch, q_heads,
                           kv_heads, tokens, head_dim, nullptr, bmax, bmax_ld, sel_out, n_sel, block, scaling,
                           workspace, workspace_bytes, out, stream);
+}
+
+QKV_EXPORT int qkv_token_attention(const void* query, const void* key, const void* value,
+                                   const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                   int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                                   const int32_t* token_ids, int64_t n_ids, float scaling,
+                                   float* workspace, int64_t workspace_bytes, void* out, void* stream) {
+  // Every query head is its own row (group size 1) with one-token blocks;
+  // row (b, h) reads K/V head h / (q_heads / kv_heads).
+  if (!token_ids) return fail(QKV_ERR_INVALID, "qkv_token_attention: null pointer");
+  if (kv_heads <= 0 || q_heads % kv_heads)
+    return fail(QKV_ERR_INVALID, "qkv_token_attention: q_heads must be a multiple of kv_heads");
+  return launch_attention("qkv_token_attention", query, key, value, kv_strides, batch, q_heads, q_heads, tokens,
+                          head_dim, token_ids, nullptr, 0, nullptr, n_ids, 1, scaling, workspace, workspace_bytes,
+                          out, stream, static_cast<int>(q_heads / kv_heads));
 }

@@ -7,66 +7,12 @@
 //
 // Built with -ffp-contract=off: every `acc + a * b` below is a separately
 // rounded multiply and add, so results equal a sequential fp32 loop.
-#include "common.h"
+#include "ref_common.h"
 
 namespace qkv {
 namespace {
 
-constexpr int kMaxDims = 128;   // QK:60
 constexpr int kTile = 256;      // tokens per workgroup (QK:61)
-
-template <int DT> struct Elem;
-template <> struct Elem<QKV_DTYPE_BF16> {
-  using T = uint16_t;
-  static __device__ __forceinline__ float load(const T* p) { return bf16_to_f32(*p); }
-  static __device__ __forceinline__ T store(float f) {
-    // round-to-nearest-even fp32 -> bf16 (finite inputs)
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return static_cast<T>(u >> 16);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return static_cast<T>(u >> 16);
-  }
-};
-template <> struct Elem<QKV_DTYPE_FP16> {
-  using T = uint16_t;
-  static __device__ __forceinline__ float load(const T* p) { return f16bits_to_f32(*p); }
-  static __device__ __forceinline__ T store(float f) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-  }
-};
-template <> struct Elem<QKV_DTYPE_FP32> {
-  using T = float;
-  static __device__ __forceinline__ float load(const T* p) { return *p; }
-  static __device__ __forceinline__ T store(float f) { return f; }
-};
-
-// Selects the top-|q| dims of one query row into LDS in the reference's order:
-// descending |q|, equal magnitudes by ascending dim (QK:123-145 uses a strict
-// '>' over ascending d).  rank(d) = #{d' : |q_d'| > |q_d| or (== and d' < d)}.
-template <int DT>
-__device__ void select_dims(const typename Elem<DT>::T* q_row, int head_dim, int count,
-                            int* sel_idx, float* sel_q) {
-  int tid = threadIdx.x;
-  // Every slot starts valid, so a NaN query (whose rank is ill-defined)
-  // cannot leave a slot holding an out-of-range dim.
-  for (int s = tid; s < count; s += blockDim.x) {
-    sel_idx[s] = 0;
-    sel_q[s] = Elem<DT>::load(q_row);
-  }
-  __syncthreads();
-  for (int d = tid; d < head_dim; d += blockDim.x) {
-    float a = fabsf(Elem<DT>::load(q_row + d));
-    int rank = 0;
-    for (int e = 0; e < head_dim; ++e) {
-      float b = fabsf(Elem<DT>::load(q_row + e));
-      rank += (b > a) || (b == a && e < d);
-    }
-    if (rank < count) {
-      sel_idx[rank] = d;
-      sel_q[rank] = Elem<DT>::load(q_row + d);
-    }
-  }
-}
 
 template <int DT>
 __global__ __launch_bounds__(kTile) void partial_scores_kernel(
@@ -215,16 +161,6 @@ __global__ __launch_bounds__(256) void final_attention_kernel(
       }
     }
     out[static_cast<int64_t>(row) * head_dim + d] = Elem<DT>::store(acc);
-  }
-}
-
-template <template <int> class F, typename... A>
-int dispatch_dtype(int dtype, A&&... args) {
-  switch (dtype) {
-    case QKV_DTYPE_BF16: return F<QKV_DTYPE_BF16>::run(args...);
-    case QKV_DTYPE_FP16: return F<QKV_DTYPE_FP16>::run(args...);
-    case QKV_DTYPE_FP32: return F<QKV_DTYPE_FP32>::run(args...);
-    default: return fail(QKV_ERR_INVALID, "unsupported dtype %d", dtype);
   }
 }
 

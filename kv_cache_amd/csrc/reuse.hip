@@ -1,0 +1,498 @@
+// Candidate reuse and exact rerank: the decode step of the reference's
+// qabs{S}cand{pct}reuse[final|2set] modes (EV:3991-4397) and the selector it
+// asks of its absent reuse_select kernel (EV:3881-3919), on GQA-shaped K/V.
+//
+// A row is one (sequence, query head) r = b * Hq + h; it reads K/V head
+// h / (Hq / Hkv).  Per step:
+//   reuse_partial_kernel    fp32 partial scores over the row's top-|q| dims,
+//                           read from the dim-major K copy (one coalesced
+//                           stream of S * 2 bytes per token);
+//   (top-k) + reuse_mask_kernel   candidates = scores >= the k-th largest;
+//   reuse_scores_kernel     union of the current / previous candidate and
+//                           previous final masks, compacted per 1024-token
+//                           tile in LDS; full-D fp32 scores of the union only;
+//   (top-k) + reuse_finalize_kernel  the final selection, its validity, the
+//                           final mask with the protected ranges, and the
+//                           final index list (EV:2938-2982).
+// The fp32 dot products add separately rounded products in dim order
+// (built with -ffp-contract=off), as the reference's kernels do (QK:91-94,
+// 210-213), so scores, masks and indices match the CPU restatement bit for
+// bit.  EV = ymluo/projects/qwen3_top2_head_limit3_ppl/src/
+// evaluate_qwen3_top2_head_limit3_ppl.py, QK = .../qabs_cuda_kernels.py.
+#include <math.h>
+
+#include "ref_common.h"
+#include "select.h"
+
+namespace qkv {
+namespace {
+
+constexpr int kRT = 256;          // threads per workgroup
+constexpr int kScoreTile = 1024;  // tokens per workgroup in reuse_scores_kernel
+constexpr int kMaskTile = 4096;   // tokens per workgroup in reuse_mask_kernel
+
+// Eight consecutive elements at p as fp32 (p 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, float (&v)[8]) {
+  if constexpr (DT == QKV_DTYPE_FP32) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 c = *reinterpret_cast<const uint4*>(p + 4);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
+    v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
+      v[2 * i] = Elem<DT>::load(&lo);
+      v[2 * i + 1] = Elem<DT>::load(&hi);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Partial scores: out[r, t] = sum_s q[d_s] * K[d_s, t] over the row's
+// top-|q| dims d_s in selection order (QK:63-96 on the dim-major copy of
+// EV:2018-2042; dims chosen as QK:120-145).  Eight tokens per thread.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kRT) void reuse_partial_kernel(
+    const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm,
+    int q_heads, int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd,
+    bool vec, float* __restrict__ out, int64_t out_ld) {
+  using E = typename Elem<DT>::T;
+  __shared__ int sel_idx[kMaxDims];
+  __shared__ float sel_q[kMaxDims];
+  const int row = blockIdx.y;
+  const int b = row / q_heads, h = row - b * q_heads;
+  select_dims<DT>(query + static_cast<int64_t>(row) * head_dim, head_dim, count, sel_idx, sel_q);
+  __syncthreads();
+  const int t0 = (blockIdx.x * kRT + threadIdx.x) * 8;
+  if (t0 >= history) return;
+  const E* base = kdm + b * sb + (h / group) * sh + t0;
+  float* o = out + static_cast<int64_t>(row) * out_ld + t0;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  if (vec && t0 + 8 <= history) {
+    for (int s = 0; s < count; ++s) {
+      float v[8];
+      load8<DT>(base + sel_idx[s] * sd, v);
+      const float qs = sel_q[s];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = acc[i];
+  } else {
+    const int n = min(8, history - t0);
+    for (int s = 0; s < count; ++s) {
+      const E* p = base + sel_idx[s] * sd;
+      const float qs = sel_q[s];
+      for (int i = 0; i < n; ++i) acc[i] = acc[i] + qs * Elem<DT>::load(p + i);
+    }
+    for (int i = 0; i < n; ++i) o[i] = acc[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Candidate mask: mask[r, t] = values[r, t] >= the smallest of the row's k
+// selected values, i.e. the k-th largest (EV:3988-3989; ties at the
+// threshold are all kept).  Sixteen tokens per thread.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRT) void reuse_mask_kernel(const float* __restrict__ values, int64_t ld, int n,
+                                                         const int32_t* __restrict__ sel, int k,
+                                                         uint8_t* __restrict__ mask, int64_t mask_ld,
+                                                         bool vec) {
+  __shared__ float red[kRT / 64];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const float* vrow = values + static_cast<int64_t>(row) * ld;
+  const int32_t* srow = sel + static_cast<int64_t>(row) * k;
+  float thr = __builtin_huge_valf();
+  for (int i = tid; i < k; i += kRT) thr = fminf(thr, vrow[srow[i]]);
+  for (int off = 32; off > 0; off >>= 1) thr = fminf(thr, __shfl_xor(thr, off));
+  if ((tid & 63) == 0) red[tid >> 6] = thr;
+  __syncthreads();
+  thr = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+  uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
+  const int t0 = blockIdx.x * kMaskTile + tid * 16;
+  if (t0 >= n) return;
+  if (vec && t0 + 16 <= n) {
+    const float4* v4 = reinterpret_cast<const float4*>(vrow + t0);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 x = v4[i];
+      w[i] = static_cast<uint32_t>(x.x >= thr) | static_cast<uint32_t>(x.y >= thr) << 8 |
+             static_cast<uint32_t>(x.z >= thr) << 16 | static_cast<uint32_t>(x.w >= thr) << 24;
+    }
+    *reinterpret_cast<uint4*>(mrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (int t = t0; t < min(n, t0 + 16); ++t) mrow[t] = vrow[t] >= thr;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Union scores: out[r, t] = scaling * sum_d q[d] * K[t, d] (d ascending)
+// where current | previous | previous_final is set at t, else -inf
+// (QK:160-216 without sink/recent protection, as EV:4257-4267 calls it).
+// The tile's union tokens are compacted in LDS so that every lane scores one.
+// DFIX = 128 fixes the head size so that a token's 16 row loads issue at once.
+// ---------------------------------------------------------------------------
+template <int DT, int DFIX>
+__global__ __launch_bounds__(kRT) void reuse_scores_kernel(
+    const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ key,
+    int q_heads, int group, int history, int head_dim, int64_t sb, int64_t sh, int64_t st, bool kvec,
+    const uint8_t* __restrict__ cur, const uint8_t* __restrict__ prev, const uint8_t* __restrict__ fin,
+    int64_t mask_ld, bool mvec, float scaling, float* __restrict__ out, int64_t out_ld) {
+  using E = typename Elem<DT>::T;
+  __shared__ float q_s[512];
+  __shared__ uint16_t list[kScoreTile];
+  __shared__ int wave_tot[kRT / 64];
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = row / q_heads, h = row - b * q_heads;
+  for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(query + static_cast<int64_t>(row) * head_dim + d);
+
+  const int tile0 = blockIdx.x * kScoreTile;
+  const int t0 = tile0 + tid * 4;
+  const int64_t moff = static_cast<int64_t>(row) * mask_ld + t0;
+  uint32_t bits = 0;
+  if (mvec && t0 + 4 <= history) {
+    uint32_t u = *reinterpret_cast<const uint32_t*>(cur + moff);
+    if (prev) u |= *reinterpret_cast<const uint32_t*>(prev + moff);
+    if (fin) u |= *reinterpret_cast<const uint32_t*>(fin + moff);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bits |= static_cast<uint32_t>(((u >> (8 * i)) & 0xFFu) != 0) << i;
+  } else {
+    for (int i = 0; i < 4 && t0 + i < history; ++i) {
+      bool f = cur[moff + i] != 0;
+      if (prev) f = f || prev[moff + i] != 0;
+      if (fin) f = f || fin[moff + i] != 0;
+      bits |= static_cast<uint32_t>(f) << i;
+    }
+  }
+  float* orow = out + static_cast<int64_t>(row) * out_ld;
+  const float ninf = -__builtin_huge_valf();
+  for (int i = 0; i < 4 && t0 + i < history; ++i)
+    if (!((bits >> i) & 1u)) orow[t0 + i] = ninf;
+
+  // Compaction: the tile's union tokens in index order.
+  const int cnt = __popc(bits);
+  const int incl = wave_incl_scan_dpp(cnt);
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = incl - cnt;
+  for (int w = 0; w < wave; ++w) base += wave_tot[w];
+  for (int i = 0; i < 4; ++i)
+    if ((bits >> i) & 1u) list[base++] = static_cast<uint16_t>(tid * 4 + i);
+  __syncthreads();
+  const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+
+  const E* kbase = key + b * sb + (h / group) * sh;
+  for (int i = tid; i < total; i += kRT) {
+    const int t = tile0 + list[i];
+    const E* kr = kbase + static_cast<int64_t>(t) * st;
+    float acc = 0.0f;
+    if (kvec) {
+      const int hd = DFIX ? DFIX : head_dim;
+#pragma unroll
+      for (int d = 0; d < hd; d += 8) {
+        float v[8];
+        load8<DT>(kr + d, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = acc + q_s[d + e] * v[e];
+      }
+    } else {
+      for (int d = 0; d < head_dim; ++d) acc = acc + q_s[d] * Elem<DT>::load(kr + d);
+    }
+    orow[t] = acc * scaling;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Final selection of one row (EV:4270-4307, 4365, 2938-2982): the final
+// mask is the protected ranges plus every selected index whose score is
+// finite; the index list is the selection (sink and recent entries marked
+// invalid), then the sink range, the recent range and the current token.
+// attn_ids (optional) repeats the list with -1 for invalid entries.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
+    const float* __restrict__ scores, int64_t scores_ld, const int32_t* __restrict__ sel, int keep,
+    int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
+    int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids,
+    int n_out, uint8_t* __restrict__ hf, int64_t hf_ld) {
+  const int row = blockIdx.x, tid = threadIdx.x;
+  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  for (int t = tid; t < history; t += kRT) hrow[t] = (t < sink_end) || (t >= recent_start);
+  __syncthreads();
+  const int32_t* srow = sel + static_cast<int64_t>(row) * keep;
+  const float* sc = scores + static_cast<int64_t>(row) * scores_ld;
+  const int64_t o = static_cast<int64_t>(row) * n_out;
+  for (int i = tid; i < keep; i += kRT) {
+    const int idx = srow[i];
+    const float s = sc[idx];
+    const bool valid = isfinite(s);
+    if (valid) hrow[idx] = 1;
+    const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
+    final_idx[o + i] = idx;
+    final_valid[o + i] = fv;
+    if (attn_ids) attn_ids[o + i] = fv ? idx : -1;
+  }
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kRT) {
+    const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+    final_idx[o + keep + i] = idx;
+    final_valid[o + keep + i] = 1;
+    if (attn_ids) attn_ids[o + keep + i] = idx;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dim-major copy of K: kdm[b, j, d, t] = K[b, j, t, d] for t in [t0, t1),
+// through a 32-token LDS tile (coalesced on both sides).
+// ---------------------------------------------------------------------------
+constexpr int kDmTile = 32;
+
+template <int DT>
+__global__ __launch_bounds__(kRT) void dim_major_kernel(const typename Elem<DT>::T* __restrict__ key, int kv_heads,
+                                                         int head_dim, int t0, int t1, int64_t sb, int64_t sh,
+                                                         int64_t st, typename Elem<DT>::T* __restrict__ kdm,
+                                                         int64_t db, int64_t dh, int64_t dd) {
+  using E = typename Elem<DT>::T;
+  __shared__ E tile[kDmTile][DT == QKV_DTYPE_FP32 ? 257 : 513];   // head_dim <= 256 (fp32) / 512
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / kv_heads, j = row - b * kv_heads;
+  const int tb = t0 + blockIdx.x * kDmTile;
+  const int n = min(kDmTile, t1 - tb);
+  const E* src = key + b * sb + j * sh;
+  for (int e = tid; e < n * head_dim; e += kRT) {
+    const int t = e / head_dim, d = e - t * head_dim;
+    tile[t][d] = src[static_cast<int64_t>(tb + t) * st + d];
+  }
+  __syncthreads();
+  E* dst = kdm + b * db + j * dh + tb;
+  for (int e = tid; e < n * head_dim; e += kRT) {
+    const int d = e / n, t = e - d * n;
+    dst[d * dd + t] = tile[t][d];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct ReuseCounts {
+  int64_t keep, sink_end, recent_start, rec_begin, n_rec, n_out;
+};
+
+ReuseCounts reuse_counts(int64_t history, int64_t sink, int64_t recent, double top_fraction, int keep_self) {
+  ReuseCounts c;
+  c.keep = std::min<int64_t>(history, std::max<int64_t>(1, static_cast<int64_t>(ceil(top_fraction * history))));
+  c.sink_end = sink > 0 ? std::min(sink, history) : 0;
+  c.recent_start = recent > 0 ? std::max<int64_t>(0, history - recent) : history;
+  c.rec_begin = std::max(c.recent_start, c.sink_end);
+  c.n_rec = (recent > 0 && c.rec_begin < history) ? history - c.rec_begin : 0;
+  c.n_out = c.keep + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+  return c;
+}
+
+constexpr int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+int64_t reuse_ws_bytes(int64_t rows, int64_t history, int64_t keep) {
+  const int64_t tk = qkv_topk_workspace_bytes(rows, history, keep);
+  if (tk < 0) return -1;
+  return align256(rows * history * 4) + align256(rows * keep * 4) + align256(tk);
+}
+
+int64_t mask_ws_bytes(int64_t rows, int64_t n, int64_t k) {
+  const int64_t tk = qkv_topk_workspace_bytes(rows, n, k);
+  if (tk < 0) return -1;
+  return align256(rows * k * 4) + align256(tk);
+}
+
+template <int DT> struct RunReusePartial {
+  static int run(const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv,
+                 int64_t T, int64_t D, int count, float* out, int64_t out_ld, hipStream_t st) {
+    using E = typename Elem<DT>::T;
+    const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
+    const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
+    dim3 grid(static_cast<unsigned>(cdiv(T, 8 * kRT)), static_cast<unsigned>(B * Hq));
+    reuse_partial_kernel<DT><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),
+                                                   static_cast<int>(Hq), static_cast<int>(Hq / Hkv),
+                                                   static_cast<int>(T), static_cast<int>(D), count, ks[0], ks[1],
+                                                   ks[2], vec, out, out_ld);
+    return check_launch("qkv_reuse_partial_scores");
+  }
+};
+
+template <int DT> struct RunReuseScores {
+  static int run(const void* q, const void* k, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
+                 int64_t D, const uint8_t* cur, const uint8_t* prev, const uint8_t* fin, int64_t mask_ld,
+                 float scaling, float* out, int64_t out_ld, hipStream_t st) {
+    using E = typename Elem<DT>::T;
+    const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;
+    const bool kvec = ks[3] == 1 && D % 8 == 0 && aligned(k, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 &&
+                      ks[2] % ev == 0;
+    const bool mvec = mask_ld % 4 == 0 && aligned(cur, 4) && (!prev || aligned(prev, 4)) && (!fin || aligned(fin, 4));
+    dim3 grid(static_cast<unsigned>(cdiv(T, kScoreTile)), static_cast<unsigned>(B * Hq));
+    if (ks[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "qkv_reuse_select: K channels must be contiguous");
+#define QKV_REUSE_SCORES(DF)                                                                                   \
+  reuse_scores_kernel<DT, DF><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),        \
+                                                    static_cast<int>(Hq), static_cast<int>(Hq / Hkv),          \
+                                                    static_cast<int>(T), static_cast<int>(D), ks[0], ks[1], ks[2], \
+                                                    kvec, cur, prev, fin, mask_ld, mvec, scaling, out, out_ld)
+    if (kvec && D == 128) QKV_REUSE_SCORES(128);
+    else QKV_REUSE_SCORES(0);
+#undef QKV_REUSE_SCORES
+    return check_launch("qkv_reuse_select");
+  }
+};
+
+template <int DT> struct RunDimMajor2 {
+  static int run(const void* k, const int64_t* ks, int64_t B, int64_t Hkv, int64_t D, int64_t t0, int64_t t1,
+                 void* kdm, const int64_t* ds, hipStream_t st) {
+    using E = typename Elem<DT>::T;
+    dim3 grid(static_cast<unsigned>(cdiv(t1 - t0, kDmTile)), static_cast<unsigned>(B * Hkv));
+    dim_major_kernel<DT><<<grid, kRT, 0, st>>>(static_cast<const E*>(k), static_cast<int>(Hkv), static_cast<int>(D),
+                                               static_cast<int>(t0), static_cast<int>(t1), ks[0], ks[1], ks[2],
+                                               static_cast<E*>(kdm), ds[0], ds[1], ds[2]);
+    return check_launch("qkv_dim_major_append");
+  }
+};
+
+int check_heads(const char* what, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim) {
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
+    return fail(QKV_ERR_INVALID, "%s: need batch > 0 and q_heads a positive multiple of kv_heads", what);
+  if (batch * q_heads > 65535) return fail(QKV_ERR_INVALID, "%s: batch * q_heads must be <= 65535", what);
+  if (head_dim <= 0 || head_dim > 512) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be in [1, 512]", what);
+  return QKV_OK;
+}
+
+}  // namespace
+}  // namespace qkv
+
+using namespace qkv;
+
+QKV_EXPORT int64_t qkv_reuse_final_count(int64_t history, int64_t protect_sink, int64_t protect_recent,
+                                         double top_fraction, int keep_self) {
+  if (history <= 0) return -1;
+  return reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self).n_out;
+}
+
+QKV_EXPORT int64_t qkv_reuse_select_workspace_bytes(int64_t rows, int64_t history, double top_fraction) {
+  if (rows <= 0 || history <= 0 || history >= (int64_t(1) << 31)) return -1;
+  return reuse_ws_bytes(rows, history, reuse_counts(history, 0, 0, top_fraction, 0).keep);
+}
+
+QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_t* k_strides, int dtype,
+                                int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                int64_t head_dim, const uint8_t* current, const uint8_t* previous,
+                                const uint8_t* previous_final, int64_t mask_ld, int64_t protect_sink,
+                                int64_t protect_recent, double top_fraction, int keep_self, float scaling,
+                                void* workspace, int64_t workspace_bytes, int64_t* final_indices,
+                                uint8_t* final_valid, int32_t* attn_ids, int64_t n_out, uint8_t* history_final,
+                                int64_t history_final_ld, void* stream) {
+  const char* what = "qkv_reuse_select";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key || !k_strides || !current || !workspace || !final_indices || !final_valid || !history_final)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t history = key_count - 1;
+  if (history <= 0 || key_count >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 (history excludes the current token)", what);
+  if (mask_ld < history || history_final_ld < history)
+    return fail(QKV_ERR_INVALID, "%s: mask row strides must cover the history", what);
+  if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
+  if (n_out != c.n_out)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the selection needs %lld", what,
+                (long long)n_out, (long long)c.n_out);
+  const int64_t rows = batch * q_heads;
+  const int64_t need = reuse_ws_bytes(rows, history, c.keep);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  float* scores = reinterpret_cast<float*>(ws);
+  int32_t* sel = reinterpret_cast<int32_t*>(ws + align256(rows * history * 4));
+  void* tk_ws = ws + align256(rows * history * 4) + align256(rows * c.keep * 4);
+  const int64_t tk_bytes = workspace_bytes - align256(rows * history * 4) - align256(rows * c.keep * 4);
+
+  rc = dispatch_dtype<RunReuseScores>(dtype, query, key, k_strides, batch, q_heads, kv_heads, history, head_dim,
+                                      current, previous, previous_final, mask_ld, scaling, scores, history, st);
+  if (rc) return rc;
+  rc = qkv_topk_ws(scores, rows, history, history, c.keep, sel, tk_ws, tk_bytes, stream);
+  if (rc) return rc;
+  reuse_finalize_kernel<<<static_cast<unsigned>(rows), kRT, 0, st>>>(
+      scores, history, sel, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
+      static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+      static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
+      history_final, history_final_ld);
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_reuse_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                        int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                        int64_t history, int64_t head_dim, int64_t dim_count, float* out,
+                                        int64_t out_ld, void* stream) {
+  const char* what = "qkv_reuse_partial_scores";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || out_ld < history)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31 and out_ld >= history", what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
+                                                       std::min<int64_t>(head_dim, kMaxDims)));
+  return dispatch_dtype<RunReusePartial>(dtype, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
+                                         history, head_dim, count, out, out_ld, static_cast<hipStream_t>(stream));
+}
+
+QKV_EXPORT int64_t qkv_threshold_mask_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+  if (rows <= 0 || n <= 0 || k < 1 || k > n) return -1;
+  return mask_ws_bytes(rows, n, k);
+}
+
+QKV_EXPORT int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
+                                  uint8_t* mask, int64_t mask_ld, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  const char* what = "qkv_threshold_mask";
+  if (!values || !mask || !workspace) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (rows <= 0 || rows > 65535 || n <= 0 || n >= (int64_t(1) << 31) || k < 1 || k > n || ld < n || mask_ld < n)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535, 1 <= k <= n, ld and mask_ld >= n", what);
+  const int64_t need = mask_ws_bytes(rows, n, k);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t* sel = static_cast<int32_t*>(workspace);
+  void* tk_ws = static_cast<char*>(workspace) + align256(rows * k * 4);
+  int rc = qkv_topk_ws(values, rows, n, ld, k, sel, tk_ws, workspace_bytes - align256(rows * k * 4), stream);
+  if (rc) return rc;
+  const bool vec = ld % 4 == 0 && aligned(values, 16) && mask_ld % 16 == 0 && aligned(mask, 16);
+  dim3 grid(static_cast<unsigned>(cdiv(n, kMaskTile)), static_cast<unsigned>(rows));
+  reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sel, static_cast<int>(k), mask, mask_ld,
+                                          vec);
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_dim_major_append(const void* key, const int64_t* k_strides, int dtype, int64_t batch,
+                                    int64_t kv_heads, int64_t head_dim, int64_t t_begin, int64_t t_end,
+                                    void* key_dim_major, const int64_t* kdm_strides, void* stream) {
+  const char* what = "qkv_dim_major_append";
+  if (!key || !k_strides || !key_dim_major || !kdm_strides) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (batch <= 0 || kv_heads <= 0 || batch * kv_heads > 65535 || head_dim <= 0 || head_dim > 512)
+    return fail(QKV_ERR_INVALID, "%s: bad sizes", what);
+  if (t_begin < 0 || t_end < t_begin || t_end >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need 0 <= t_begin <= t_end < 2^31", what);
+  if (k_strides[3] != 1 || kdm_strides[3] != 1)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: K channels and the copy's token axis must be contiguous", what);
+  if (dtype == QKV_DTYPE_FP32 && head_dim > 256)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: fp32 K needs head_dim <= 256", what);
+  if (t_end == t_begin) return QKV_OK;
+  return dispatch_dtype<RunDimMajor2>(dtype, key, k_strides, batch, kv_heads, head_dim, t_begin, t_end,
+                                      key_dim_major, kdm_strides, static_cast<hipStream_t>(stream));
+}

@@ -164,3 +164,54 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(),
             _dtype_code(q), b, h, t, n, d, float(scaling), _lib.stream_of(q)))
     return out[:, None, :, :].contiguous()
+
+
+def reuse_select(query: torch.Tensor, key_states: torch.Tensor, current_candidate: torch.Tensor,
+                 previous_candidate: torch.Tensor | None, previous_final: torch.Tensor | None,
+                 protect_sink_tokens: int, protect_recent_tokens: int, top_fraction: float,
+                 always_keep_self: bool, scaling: float):
+    """The fused selector the reference imports from this module but never
+    shipped (called at EV:3901-3914, signature EV:3881-3892): rerank the
+    union of the candidate masks by full-D scores, keep the
+    ``ceil(top_fraction * history)`` best, and build the final index list.
+
+    query [B,H,D]; key_states [B,H,K,D] including the current token
+    (history = K - 1); masks bool [B,H,history].  Returns (final_indices
+    int64 [B,H,N], final_valid bool [B,H,N], history_final bool
+    [B,H,history]) with the meaning of the fallback path EV:4257-4365.  The
+    selection comes in ascending index order (the fallback's comes in
+    descending score order; the attention over it is the same set)."""
+    lib = _lib.load()
+    _check(query.is_cuda and key_states.is_cuda and current_candidate.is_cuda, "inputs must be CUDA")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key_states.dim() == 4, "key must have shape [batch, heads, key, dim]")
+    _check(query.dtype == key_states.dtype, "query/key dtype mismatch")
+    _check(current_candidate.dtype == torch.bool, "current_candidate must be bool")
+    b, h, d = query.shape
+    key_count = key_states.size(2)
+    history = key_count - 1
+    _check(key_states.size(0) == b and key_states.size(1) == h and key_states.size(3) == d, "query/key shape mismatch")
+    _check(history >= 1, "reuse_select needs at least one history token")
+    _check(tuple(current_candidate.shape) == (b, h, history), "candidate shape mismatch")
+    masks = []
+    for name, m in (("previous_candidate", previous_candidate), ("previous_final", previous_final)):
+        _check(m is None or (m.dtype == torch.bool and tuple(m.shape) == (b, h, history)), f"{name} shape mismatch")
+        masks.append(m.contiguous() if m is not None else None)
+    q = query.contiguous()
+    k = key_states if key_states.stride(3) == 1 else key_states.contiguous()
+    cur = current_candidate.contiguous()
+    sink, recent = max(0, int(protect_sink_tokens)), max(0, int(protect_recent_tokens))
+    n_out = lib.qkv_reuse_final_count(history, sink, recent, float(top_fraction), int(bool(always_keep_self)))
+    ws_bytes = lib.qkv_reuse_select_workspace_bytes(b * h, history, float(top_fraction))
+    _check(n_out > 0 and ws_bytes > 0, "bad reuse_select sizes")
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device)
+    final_indices = torch.empty((b, h, n_out), dtype=torch.int64, device=q.device)
+    final_valid = torch.empty((b, h, n_out), dtype=torch.bool, device=q.device)
+    history_final = torch.empty((b, h, history), dtype=torch.bool, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_reuse_select(
+            q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), _dtype_code(q), b, h, h, key_count, d,
+            cur.data_ptr(), _lib.ptr(masks[0]), _lib.ptr(masks[1]), history, sink, recent, float(top_fraction),
+            int(bool(always_keep_self)), float(scaling), ws.data_ptr(), ws.numel() * 4, final_indices.data_ptr(),
+            final_valid.data_ptr(), None, n_out, history_final.data_ptr(), history, _lib.stream_of(q)))
+    return final_indices, final_valid, history_final

@@ -1,0 +1,257 @@
+"""Candidate reuse and exact rerank: the reference's
+``qabs{S}cand{pct}reuse[final|2set]`` decode step on MI355X.
+
+Per layer and decode token the reference (``_qabs_reuse_fast_attention_forward``,
+evaluate_qwen3_top2_head_limit3_ppl.py:3991-4397, "EV") scores every history
+token on the S largest-|q| dims of each query head, keeps the
+``ceil(cand * history)`` best as the current candidates, unions them with the
+previous step's candidates and/or final selection, reranks the union by the
+full-D score, keeps ``ceil(top_fraction * history)`` of it, and attends over
+that selection plus the protected sink/recent tokens and the current token.
+The previous masks live in ``ReuseCandidateState`` (EV:1596-1759).
+
+``ReuseDecodeStep`` runs that step with libqkv kernels on GQA-shaped K/V (no
+``repeat_interleave``): the dim-major K copy for the partial scores
+(``qkv_dim_major_append``, EV:2018-2042), ``qkv_reuse_partial_scores``,
+``qkv_threshold_mask``, ``qkv_reuse_select`` and ``qkv_token_attention``.
+The masks stay on the GPU in capacity-sized buffers; nothing is allocated per
+step once the step is built.
+"""
+
+from __future__ import annotations
+
+import math
+import re
+
+import torch
+
+from . import _lib
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    code = _lib.DTYPE_CODES.get(t.dtype)
+    _require(code is not None, f"unsupported dtype {t.dtype}")
+    return code
+
+
+def budget_count(history: int, fraction: float) -> int:
+    """``min(history, max(1, ceil(fraction * history)))`` (EV:4132, 4270)."""
+    return min(int(history), max(1, math.ceil(float(fraction) * int(history))))
+
+
+def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool]:
+    """``qabs{S}cand{pct}reuse[final|2set]`` -> (S, candidate fraction, use the
+    previous candidates, use the previous final selection).  The percentage
+    takes ``p`` as the decimal point (``cand6p25`` = 6.25 %), as
+    ``parse_qabs_partial_rerank_params`` reads it (EV:748-754); ``reusefinal``
+    drops the previous candidates and ``reuse2set`` the previous final
+    selection (EV:955-960).  Block-expanded (``blk``) modes are not built."""
+    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)reuse(2set|final)?", mode)
+    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}reuse[final|2set] mode")
+    frac = float(m.group(2).replace("p", ".")) / 100.0
+    return int(m.group(1)), frac, m.group(3) != "final", m.group(3) != "2set"
+
+
+def reuse_partial_scores(query: torch.Tensor, key_dim_major: torch.Tensor, history: int, dim_count: int, *,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [B*Hq, >= history] partial scores over each head's top-|q| dims;
+    key_dim_major [B, Hkv, D, *] with the token axis contiguous."""
+    lib = _lib.load()
+    q = query.contiguous()
+    b, hq, d = q.shape
+    hkv = key_dim_major.size(1)
+    _require(q.is_cuda and key_dim_major.device == q.device, "query and key_dim_major must be on one CUDA device")
+    _require(key_dim_major.dim() == 4 and key_dim_major.size(0) == b and key_dim_major.size(2) == d
+             and key_dim_major.size(3) >= history and key_dim_major.dtype == q.dtype,
+             "key_dim_major must be [B, Hkv, D, >= history] in the query dtype")
+    if out is None:
+        out = torch.empty((b * hq, history), dtype=torch.float32, device=q.device)
+    _require(out.dtype == torch.float32 and out.dim() == 2 and out.size(0) == b * hq and out.size(1) >= history
+             and out.stride(1) == 1, "out must be f32 [B*Hq, >= history]")
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_reuse_partial_scores(
+            q.data_ptr(), key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _dtype_code(q), b, hq,
+            hkv, int(history), d, int(dim_count), out.data_ptr(), out.stride(0), _lib.stream_of(q)))
+    return out
+
+
+def threshold_mask(values: torch.Tensor, n: int, k: int, mask: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
+    """mask[:, :n] = values[:, :n] >= each row's k-th largest value."""
+    lib = _lib.load()
+    _require(values.is_cuda and values.dtype == torch.float32 and values.dim() == 2 and values.stride(1) == 1
+             and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
+    _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
+             and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
+    with torch.cuda.device(values.device):
+        _lib.check(lib.qkv_threshold_mask(values.data_ptr(), values.size(0), int(n), values.stride(0), int(k),
+                                          mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
+                                          workspace.numel() * 4, _lib.stream_of(values)))
+    return mask
+
+
+def dim_major_append(key: torch.Tensor, key_dim_major: torch.Tensor, t_begin: int, t_end: int) -> None:
+    """key_dim_major[:, :, :, t] = key[:, :, t, :] for t in [t_begin, t_end)."""
+    lib = _lib.load()
+    b, hkv, _, d = key.shape
+    _require(key.is_cuda and key_dim_major.device == key.device and key_dim_major.dtype == key.dtype,
+             "key and key_dim_major must share a CUDA device and dtype")
+    _require(0 <= t_begin <= t_end <= key.size(2), "token range outside the key cache")
+    _require(key_dim_major.dim() == 4 and tuple(key_dim_major.shape[:3]) == (b, hkv, d)
+             and key_dim_major.size(3) >= t_end, "key_dim_major must be [B, Hkv, D, >= t_end]")
+    with torch.cuda.device(key.device):
+        _lib.check(lib.qkv_dim_major_append(
+            key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(key), b, hkv, d, int(t_begin), int(t_end),
+            key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _lib.stream_of(key)))
+
+
+def token_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, token_ids: torch.Tensor,
+                    scaling: float, *, workspace: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Each query head attends over its own token list (int32 [B*Hq, n], -1
+    skipped) of its K/V head; bf16 [B, Hq, D]."""
+    lib = _lib.load()
+    q = query.contiguous()
+    b, hq, d = q.shape
+    _require(q.dtype == key.dtype == value.dtype == torch.bfloat16, "token attention takes bf16 q/K/V")
+    _require(key.shape == value.shape and key.stride() == value.stride() and key.stride(3) == 1,
+             "key/value layout mismatch")
+    _require(token_ids.dtype == torch.int32 and token_ids.is_contiguous() and token_ids.numel() ==
+             b * hq * token_ids.size(-1), "token_ids must be contiguous int32 [B*Hq, n]")
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_token_attention(
+            q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, key.size(1),
+            key.size(2), d, token_ids.data_ptr(), token_ids.size(-1), float(scaling), workspace.data_ptr(),
+            workspace.numel() * 4, out.data_ptr(), _lib.stream_of(q)))
+    return out
+
+
+class ReuseDecodeStep:
+    """One layer's reuse decode step with its state, for K/V caches of up to
+    ``capacity`` tokens (bf16 K/V as HF stores them, [B, Hkv, T, D]).
+
+    Call it once per decode token with the cache including the current token
+    (T = history + 1).  The previous step's masks are used when the previous
+    call had history - 1 tokens (the ``query_token`` check of EV:1651); call
+    ``reset()`` before a new sequence."""
+
+    def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
+                 top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
+                 keep_self: bool = True, device: torch.device | str = "cuda"):
+        lib = _lib.load()
+        self.device = device
+        self.mode = mode
+        self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final = parse_reuse_mode(mode)
+        _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
+        self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
+        self.capacity = int(capacity)
+        self.top_fraction = float(top_fraction)
+        self.sink, self.recent, self.keep_self = max(0, int(protect_sink)), max(0, int(protect_recent)), bool(keep_self)
+        rows = batch * q_heads
+        cap = self.capacity
+        self.rows = rows
+        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
+        self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
+        self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
+        self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
+        hist_max = cap - 1
+        # every term of the count grows with the history
+        self.n_out_max = int(lib.qkv_reuse_final_count(hist_max, self.sink, self.recent, self.top_fraction,
+                                                       int(self.keep_self)))
+        self.final_idx = torch.empty(rows * self.n_out_max, dtype=torch.int64, device=device)
+        self.final_valid = torch.empty(rows * self.n_out_max, dtype=torch.uint8, device=device)
+        self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
+        self.mask_ws = self._ws(lib.qkv_threshold_mask_workspace_bytes(rows, hist_max, budget_count(hist_max,
+                                                                                                    self.cand_fraction)))
+        self.select_ws = self._ws(lib.qkv_reuse_select_workspace_bytes(rows, hist_max, self.top_fraction))
+        need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
+        _require(need > 0, "unsupported attention shape (head_dim must be 128)")
+        self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.reset()
+
+    def _ws(self, nbytes: int) -> torch.Tensor:
+        _require(nbytes >= 0, "bad workspace size")
+        return torch.empty(max(1, (nbytes + 3) // 4), dtype=torch.float32, device=self.device)
+
+    def _grow(self, ws: torch.Tensor, nbytes: int) -> torch.Tensor:
+        return ws if ws.numel() * 4 >= nbytes else self._ws(nbytes)
+
+    def reset(self) -> None:
+        """Forget the previous step and the dim-major copy (a new sequence)."""
+        for m in (*self.cand, self.fin):
+            m.zero_()
+        self.kdm_len = 0
+        self.flip = 0
+        self.last_history = None
+
+    def prefill(self, key: torch.Tensor) -> None:
+        """Build the dim-major copy of the cached history in one launch."""
+        t = key.size(2)
+        if t > self.kdm_len:
+            dim_major_append(key, self.kdm, self.kdm_len, t)
+            self.kdm_len = t
+
+    def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
+        """query bf16 [B, Hq, D]; key/value bf16 [B, Hkv, T, D] (the current
+        token last).  Returns bf16 [B, Hq, D]."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
+        g = self.q_heads // self.kv_heads
+        if key_count <= 1:   # EV:4012-4014: only the current token
+            self.out.copy_(value[:, :, -1, :].repeat_interleave(g, dim=1))
+            return self.out
+        history = key_count - 1
+        if self.last_history is not None and history <= self.last_history:
+            self.reset()     # a shorter or equal history is a new sequence
+        if self.kdm_len < history:
+            dim_major_append(key, self.kdm, self.kdm_len, history)
+            self.kdm_len = history
+        q = query.contiguous()
+        reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
+        requested = budget_count(history, self.cand_fraction)
+        cur, prev = self.cand[self.flip], self.cand[1 - self.flip]
+        self.mask_ws = self._grow(self.mask_ws, lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+        threshold_mask(self.partial, history, requested, cur, self.mask_ws)
+        consecutive = self.last_history == history - 1
+        use_prev = prev if consecutive and self.use_prev_candidate else None
+        use_fin = self.fin if consecutive and self.use_prev_final else None
+        n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
+        self.select_ws = self._grow(self.select_ws,
+                                    lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
+        ids = self.attn_ids[: self.rows * n_out]
+        with torch.cuda.device(q.device):
+            _lib.check(lib.qkv_reuse_select(
+                q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch, self.q_heads,
+                self.kv_heads, key_count, self.head_dim, cur.data_ptr(), _lib.ptr(use_prev), _lib.ptr(use_fin),
+                self.capacity, self.sink, self.recent, self.top_fraction, int(self.keep_self), float(scaling),
+                self.select_ws.data_ptr(), self.select_ws.numel() * 4, self.final_idx.data_ptr(),
+                self.final_valid.data_ptr(), ids.data_ptr(), n_out, self.fin.data_ptr(), self.capacity,
+                _lib.stream_of(q)))
+        token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+        self.flip ^= 1
+        self.last_history = history
+        self.n_out = n_out
+        return self.out
+
+    # -- state views (tests, tracing) ------------------------------------------
+    def candidate_mask(self) -> torch.Tensor:
+        """The last step's current candidates, bool [B, Hq, history]."""
+        return self.cand[1 - self.flip][:, : self.last_history].view(torch.bool).view(
+            self.batch, self.q_heads, self.last_history)
+
+    def final_mask(self) -> torch.Tensor:
+        """The last step's final selection with the protected ranges, bool [B, Hq, history]."""
+        return self.fin[:, : self.last_history].view(torch.bool).view(self.batch, self.q_heads, self.last_history)
+
+    def final_indices(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The last step's final index list and validity, [B, Hq, N]."""
+        n = self.n_out
+        shape = (self.batch, self.q_heads, n)
+        return (self.final_idx[: self.rows * n].view(shape), self.final_valid[: self.rows * n].view(torch.bool).view(shape))

@@ -1,0 +1,172 @@
+"""GPU parity of candidate reuse and exact rerank against the oracle and the
+reference's own golden vectors: masks and final index sets bit-exact,
+attention within 1e-2 relative / 2e-2 absolute."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import qabs_cuda_kernels as Q
+from kv_cache_amd import reuse as RU
+from oracle import ref_semantics as R
+from tests.test_oracle_reuse import SCENARIOS, load_golden
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+DT = {"float32": torch.float32, "bfloat16": torch.bfloat16}
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", SCENARIOS)
+def test_pieces_match_reference_vectors(name):
+    # The step composed from the C-ABI pieces in the scenario's dtype, on
+    # GQA-expanded K as the reference's hook passes it; every step's masks
+    # equal the reference's, the attention is within tolerance.
+    g = load_golden(name)
+    dt = DT[g["dtype"]]
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k_all = torch.from_numpy(np.repeat(g["k"], hq // hkv, axis=1)).to(dt).to(DEV)
+    v_all = torch.from_numpy(np.repeat(g["v"], hq // hkv, axis=1)).to(dt).to(DEV)
+    pc = pf = None
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        hist = n - 1
+        q = torch.from_numpy(g["q"][s]).to(dt).to(DEV)
+        k, v = k_all[:, :, :n], v_all[:, :, :n]
+        partial = Q.partial_scores(q, k[:, :, :hist], g["dims"])
+        req = R.budget_count(hist, g["cand"])
+        ws = torch.empty(max(1, Q._lib.load().qkv_threshold_mask_workspace_bytes(hq, hist, req)) // 4 + 1,
+                         dtype=torch.float32, device=DEV)
+        cur = torch.empty((1, hq, hist), dtype=torch.bool, device=DEV)
+        RU.threshold_mask(partial.view(hq, hist), hist, req, cur.view(torch.uint8).view(hq, hist), ws)
+        assert np.array_equal(cur.cpu().numpy(), g["candidate"][s][..., :hist]), (name, s, "candidate")
+        fi, fv, hf = Q.reuse_select(q, k, cur, pc if g["use_prev_candidate"] else None,
+                                    pf if g["use_prev_final"] else None, g["sink"], g["recent"], g["top_fraction"],
+                                    g["keep_self"], g["scaling"])
+        assert np.array_equal(hf.cpu().numpy(), g["final"][s][..., :hist]), (name, s, "final")
+        out = Q.final_attention(q, k, v, fi, fv, g["scaling"])
+        np.testing.assert_allclose(f32(out)[:, 0], g["out"][s], rtol=RTOL, atol=ATOL)
+        # the next step reads them padded with False to its history (EV:1645-1662)
+        pc, pf = (torch.cat([m, torch.zeros_like(m[..., :1])], dim=-1) for m in (cur, hf))
+
+
+def test_step_matches_reference_vectors_bf16():
+    # The GQA-native step (dim-major K, no head expansion) on the bf16
+    # scenario: the state it leaves equals the reference's at every step.
+    g = load_golden("s8c5_bf16")
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
+    v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
+    step = RU.ReuseDecodeStep(g["mode"], 1, hq, hkv, 128, 1024, top_fraction=g["top_fraction"],
+                              protect_sink=g["sink"], protect_recent=g["recent"], keep_self=g["keep_self"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
+        out = step(q, k[:, :, :n], v[:, :, :n], g["scaling"])
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), g["candidate"][s][..., : n - 1]), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), g["final"][s][..., : n - 1]), s
+        np.testing.assert_allclose(f32(out), g["out"][s], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("b,h,t,sink,recent,frac,keep_self", [
+    (2, 4, 5000, 4, 16, 0.02, True),
+    (1, 3, 777, 0, 0, 0.3, False),       # keep larger than the union: invalid -inf picks
+    (1, 2, 2, 1, 1, 1.0, True),          # history 1
+    (1, 2, 9000, 100, 100, 0.01, True),  # protected ranges overlap the selection
+])
+def test_reuse_select_matches_oracle(dtype, b, h, t, sink, recent, frac, keep_self):
+    gen = torch.Generator().manual_seed(t + h)
+    q = torch.randn((b, h, 128), generator=gen).to(dtype)
+    k = torch.randn((b, h, t, 128), generator=gen).to(dtype)
+    hist = t - 1
+    masks = [torch.rand((b, h, hist), generator=gen) < p for p in (0.05, 0.04, 0.02)]
+    fi, fv, hf = Q.reuse_select(q.to(DEV), k.to(DEV), masks[0].to(DEV), masks[1].to(DEV), masks[2].to(DEV), sink,
+                                recent, frac, keep_self, 0.088)
+    wi, wv, whf = R.reuse_select(f32(q), f32(k), masks[0].numpy(), masks[1].numpy(), masks[2].numpy(), sink, recent,
+                                 frac, keep_self, 0.088)
+    assert fi.shape == wi.shape
+    assert np.array_equal(fi.cpu().numpy(), wi)        # same order: ascending selection, then the ranges
+    assert np.array_equal(fv.cpu().numpy(), wv)
+    assert np.array_equal(hf.cpu().numpy(), whf)
+
+
+def test_reuse_select_ties_and_missing_masks():
+    # Duplicate keys give equal scores: the lower index wins; previous masks absent.
+    gen = torch.Generator().manual_seed(1)
+    q = torch.randn((1, 2, 128), generator=gen).to(torch.bfloat16)
+    base = torch.randn((1, 2, 40, 128), generator=gen).to(torch.bfloat16)
+    k = base.repeat(1, 1, 50, 1)[:, :, :1999]          # every row repeats 50 times
+    cur = torch.rand((1, 2, 1998), generator=gen) < 0.3
+    fi, fv, hf = Q.reuse_select(q.to(DEV), k.to(DEV), cur.to(DEV), None, None, 0, 0, 0.05, True, 0.1)
+    wi, wv, whf = R.reuse_select(f32(q), f32(k), cur.numpy(), None, None, 0, 0, 0.05, True, 0.1)
+    assert np.array_equal(fi.cpu().numpy(), wi) and np.array_equal(fv.cpu().numpy(), wv)
+    assert np.array_equal(hf.cpu().numpy(), whf)
+
+
+@pytest.mark.parametrize("hq,hkv,t,steps,mode", [
+    (8, 2, 3000, 4, "qabs8cand5reuse"),
+    (32, 8, 9000, 3, "qabs16cand10reusefinal"),
+    (4, 4, 1500, 3, "qabs8cand3reuse2set"),
+])
+def test_step_matches_oracle(hq, hkv, t, steps, mode):
+    gen = torch.Generator().manual_seed(hq * t)
+    s_dims, cand, use_pc, use_pf = RU.parse_reuse_mode(mode)
+    k = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    qs = torch.randn((steps, 1, hq, 128), generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = RU.ReuseDecodeStep(mode, 1, hq, hkv, 128, t + steps + 64, top_fraction=0.02, protect_sink=4,
+                              protect_recent=8)
+    step.prefill(kd[:, :, :t - 1])
+    pc = pf = None
+    for s in range(steps):
+        n = t + s + 1
+        out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        want, wc, wf = R.reuse_decode_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), s_dims, cand, 0.02, 4, 8,
+                                           True, 128 ** -0.5, pc if use_pc else None, pf if use_pf else None)
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+        pc, pf = wc, wf
+
+
+def test_step_resets_on_shorter_history():
+    gen = torch.Generator().manual_seed(5)
+    k = torch.randn((1, 2, 600, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, 4, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    step = RU.ReuseDecodeStep("qabs8cand5reuse", 1, 4, 2, 128, 1024)
+    step(q, k[:, :, :500], k[:, :, :500], 0.1)
+    step(q, k[:, :, :501], k[:, :, :501], 0.1)
+    a = step(q, k[:, :, :300], k[:, :, :300], 0.1).clone()       # new sequence: no previous masks
+    fresh = RU.ReuseDecodeStep("qabs8cand5reuse", 1, 4, 2, 128, 1024)
+    assert torch.equal(a, fresh(q, k[:, :, :300], k[:, :, :300], 0.1))
+    assert torch.equal(step.final_mask(), fresh.final_mask())
+
+
+def test_dim_major_append_and_token_attention():
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn((2, 3, 700, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    kdm = torch.zeros((2, 3, 128, 1024), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k, kdm, 0, 333)
+    RU.dim_major_append(k, kdm, 333, 700)
+    assert torch.equal(kdm[..., :700], k.transpose(-1, -2))
+    assert int(torch.count_nonzero(kdm[..., 700:])) == 0
+    # token attention: per-head lists with invalid (-1) and out-of-range ids skipped
+    q = torch.randn((2, 6, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn((2, 3, 700, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    ids = torch.randint(0, 700, (12, 50), generator=gen, dtype=torch.int32)
+    ids[0, :10] = -1
+    ids[3, 5] = 900
+    ws = torch.zeros(Q._lib.load().qkv_sparse_attention_workspace_bytes(2, 6, 6, 128, 50, 1) // 4,
+                     dtype=torch.float32, device=DEV)
+    out = RU.token_attention(q, k, v, ids.to(DEV), 0.09, workspace=ws)
+    idx = ids.view(2, 6, 50).long()
+    valid = (idx >= 0) & (idx < 700)
+    kx, vx = k.repeat_interleave(2, dim=1), v.repeat_interleave(2, dim=1)
+    want = R.final_attention(f32(q), f32(kx), f32(vx), idx.clamp(0, 699).numpy(), valid.numpy(), 0.09)
+    np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
