@@ -20,9 +20,14 @@ rotating per-layer buffers; value = (query head, visible key) pairs scored
 per second; "roofline" is the MFMA scoring kernel's algorithmic int8 ops
 per second against the 5.0 POP/s dense int8 peak.
 
+reuse (candidate reuse + exact rerank, kv_cache_amd.reuse): a step is one decode
+token through 8 layers of the qabs8cand5reuse step at Qwen3-8B heads and history
+32768; value = history tokens x KV heads x layers per second.
+
 "cpu_baseline" is timed on the host cores on a bounded sample: for decode
 the reference's PyTorch op sequence (restated in oracle/ref_semantics.py),
-for prefill the numpy restatement of the scoring (oracle/qkv_oracle.py).
+for prefill the numpy restatement of the scoring (oracle/qkv_oracle.py), for
+reuse the reference's reuse op sequence (oracle/ref_semantics.py).
 Prints ONE JSON line (the driver contract).
 """
 
@@ -50,7 +55,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse"])
     p.add_argument("--layers", type=int, default=None,
                    help="layer buffers to rotate through (default: the config's layer count, at least 8)")
     p.add_argument("--kernel-reps", type=int, default=20, help="graph replays for per-kernel timing")
@@ -167,6 +172,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.config == "cfg5":
         line = run_prefill(args)
+    elif args.config == "reuse":
+        line = run_reuse(args)
     else:
         line = run_decode(args)
     print(json.dumps(line), flush=True)
@@ -481,6 +488,230 @@ def run_prefill(args) -> dict:
             "frac": achieved / INT8_PEAK_TOPS,
             "traffic": read_traffic("cfg5", "prefill_scores_kernel"),
             "ops_per_launch": ops,
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+
+
+# The candidate-reuse workload: Qwen3-8B heads, one sequence, 32768 history
+# tokens, the reference's most-run reuse mode with its default final
+# fraction and the sink/recent protection of its timed runs.
+REUSE = {"name": "qwen3-8b-reuse-b1-h32768", "batch": 1, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+         "history": 32768, "mode": "qabs8cand5reuse", "top_fraction": 0.02, "sink": 10, "recent": 10}
+
+
+def cpu_baseline_reuse(budget_s: float, steps: int = 3) -> dict:
+    """The reference's reuse op sequence (oracle/ref_semantics.py
+    qabs_reuse_step_cpu) for consecutive decode steps of one layer on CPU
+    tensors, about ``budget_s`` seconds."""
+    import torch
+
+    from oracle import ref_semantics as R
+    from kv_cache_amd.reuse import parse_reuse_mode
+
+    c = REUSE
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    t = c["history"] + steps + 1
+    k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    dims, cand, _, _ = parse_reuse_mode(c["mode"])
+    pc = pf = None
+    times = []
+    t_end = time.perf_counter() + budget_s
+    for s in range(steps):
+        n = c["history"] + s + 1
+        q = torch.randn((1, c["q_heads"], 1, c["head_dim"]), generator=g).to(torch.bfloat16)
+        fit = (lambda m: None if m is None else torch.cat([m, torch.zeros_like(m[..., :1])], dim=-1))
+        t0 = time.perf_counter()
+        _, pc, pf = R.qabs_reuse_step_cpu(q, k[:, :, :n], v[:, :, :n], dims, cand, c["top_fraction"],
+                                          c["head_dim"] ** -0.5, c["sink"], c["recent"], True, fit(pc), fit(pf))
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
+    med = statistics.median(times[1:] if len(times) > 1 else times)
+    keys = c["kv_heads"] * c["history"]
+    return {
+        "value": keys / med,
+        "unit": "keys/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} consecutive decode steps of one layer ({c['mode']}, {c['q_heads']}/{c['kv_heads']} "
+                   f"heads, history {c['history']}): the reference's reuse op sequence on CPU tensors; "
+                   f"median of the steps after the first = {med * 1e3:.1f} ms per layer-step"),
+    }
+
+
+def run_reuse(args) -> dict:
+    """Decode steps of the candidate-reuse path (kv_cache_amd.reuse).  A step
+    is one decode token through every layer; each layer keeps its own K/V,
+    dim-major K copy and masks, and the history grows by one token per step.
+    Timed eagerly (the step sizes change every token; host launch time
+    included), then one step at a fixed history is captured in a HIP graph
+    (GPU time), and each piece alone (per-kernel time)."""
+    import torch
+
+    from kv_cache_amd import reuse as RU
+
+    c = REUSE
+    layers = args.layers or 8
+    b, hq, hkv, d, t0 = c["batch"], c["q_heads"], c["kv_heads"], c["head_dim"], c["history"]
+    cap = -(-(t0 + args.warmup + args.steps + 2) // 64) * 64
+    scaling = d ** -0.5
+    log(f"[bench] setup {c['name']}: {layers} layers, {c['mode']}, top {c['top_fraction']}, sink/recent "
+        f"{c['sink']}/{c['recent']}, capacity {cap}")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ks, vs, qs, steps = [], [], [], []
+    for layer in range(layers):
+        k = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        q = torch.randn((b, hq, d), generator=g, device="cuda").to(torch.bfloat16)
+        st = RU.ReuseDecodeStep(c["mode"], b, hq, hkv, d, cap, top_fraction=c["top_fraction"],
+                                protect_sink=c["sink"], protect_recent=c["recent"])
+        st.prefill(k[:, :, :t0])
+        ks.append(k)
+        vs.append(v)
+        qs.append(q)
+        steps.append(st)
+    torch.cuda.synchronize()
+    log(f"[bench] resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
+
+    hist = t0
+
+    def decode_step():
+        nonlocal hist
+        for layer in range(layers):
+            steps[layer](qs[layer], ks[layer][:, :, : hist + 1], vs[layer][:, :, : hist + 1], scaling)
+        hist += 1
+
+    for _ in range(args.warmup):
+        decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0 = hist
+    e0.record()
+    for _ in range(args.steps):
+        decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    log(f"[bench] eager step: {ms_per_step:.3f} ms ({ms_per_step * 1e3 / layers:.1f} us/layer), "
+        f"history {h0}..{hist - 1}")
+
+    # Union size and final list of the last step (layer 0), for the byte counts.
+    st0 = steps[0]
+    hist_fixed = hist - 1
+    cur, prev, fin = st0.cand[1 - st0.flip], st0.cand[st0.flip], st0.fin
+    union = int(((cur[:, :hist_fixed] | prev[:, :hist_fixed]) | fin[:, :hist_fixed]).count_nonzero())
+    n_out = st0.n_out
+    rows = b * hq
+
+    # One step at a fixed history with steady-state masks, as a graph.
+    def fixed(layer):
+        st = steps[layer]
+        kk, vv = ks[layer][:, :, : hist_fixed + 1], vs[layer][:, :, : hist_fixed + 1]
+        return st, kk, vv
+
+    def run_fixed():
+        for layer in range(layers):
+            st, kk, vv = fixed(layer)
+            st.launch(qs[layer], kk, vv, scaling, st.cand[0], st.cand[1], st.fin)
+
+    reps = max(1, -(-16 // layers))
+
+    def repeated(fn):
+        def run():
+            for _ in range(reps):
+                fn()
+        return run
+
+    gr = graph_of(repeated(run_fixed))
+    ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
+    del gr
+    log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
+
+    mask_ws = [steps[l].mask_ws for l in range(layers)]
+    s_dims, cand_frac, _, _ = RU.parse_reuse_mode(c["mode"])
+    requested = RU.budget_count(hist_fixed, cand_frac)
+
+    def run_partial():
+        for layer in range(layers):
+            RU.reuse_partial_scores(qs[layer], steps[layer].kdm, hist_fixed, s_dims, out=steps[layer].partial)
+
+    def run_mask():
+        for layer in range(layers):
+            RU.threshold_mask(steps[layer].partial, hist_fixed, requested, steps[layer].cand[0], mask_ws[layer])
+
+    lib = RU._lib.load()
+
+    def run_select():
+        for layer in range(layers):
+            st, kk, _ = fixed(layer)
+            RU._lib.check(lib.qkv_reuse_select(
+                qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv, hist_fixed + 1, d,
+                st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), cap, c["sink"], c["recent"],
+                c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
+                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_out, st.fin.data_ptr(),
+                cap, RU._lib.stream_of(qs[layer])))
+
+    def run_attn():
+        for layer in range(layers):
+            st, kk, vv = fixed(layer)
+            RU.token_attention(qs[layer], kk, vv, st.attn_ids[: rows * n_out].view(rows, n_out), scaling,
+                               workspace=st.attn_ws, out=st.out)
+
+    plan = [
+        ("reuse_partial_scores", run_partial, rows * hist_fixed * (s_dims * 2 + 4)),
+        ("threshold_mask", run_mask, rows * hist_fixed * (4 + 1)),
+        # three mask bytes, the f32 score and the final mask byte per token, plus
+        # the K row of every union token
+        ("reuse_select", run_select, rows * hist_fixed * (3 + 4 + 1) + union * d * 2),
+        ("token_attention", run_attn, rows * n_out * d * 2 * 2),
+    ]
+    kernels = {}
+    for name, fn, nbytes in plan:
+        gk = graph_of(repeated(fn))
+        ms = time_replays(gk.replay, args.kernel_reps) / (layers * reps)
+        kernels[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                         "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
+        del gk
+    for _ in range(args.profile_steps):
+        run_fixed()
+    torch.cuda.synchronize()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline_reuse(args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
+    dom = max(kernels, key=lambda n: kernels[n]["us_per_launch"])
+    keys_per_layer = b * hkv * hist_fixed
+    return {
+        "metric": "reuse decode: keys/s (history tokens x KV heads) through the qabs reuse step; us/layer",
+        "value": layers * keys_per_layer / (ms_per_step * 1e-3),
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 -> f32 scores and attention",
+        "data": "synthetic (seeded N(0,1) K/V/q)",
+        "config": {"workload": f"reuse: {c['name']}", "batch": b, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                   "history": t0, "layers": layers, "mode": c["mode"], "top_fraction": c["top_fraction"],
+                   "sink": c["sink"], "recent": c["recent"], "graph": False},
+        "us_per_layer": ms_per_step * 1e3 / layers,
+        "graph_us_per_layer": ms_graph * 1e3 / layers,
+        "union_tokens_per_row": union / rows,
+        "final_entries_per_row": n_out,
+        "roofline": {
+            "bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": kernels[dom]["gbs"] / HBM_PEAK_GBS, "traffic": read_traffic("reuse", dom),
         },
         "kernels": kernels,
         "cpu_baseline": cpu,

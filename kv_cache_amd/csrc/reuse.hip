@@ -21,6 +21,8 @@
 // evaluate_qwen3_top2_head_limit3_ppl.py, QK = .../qabs_cuda_kernels.py.
 #include <math.h>
 
+#include <type_traits>
+
 #include "ref_common.h"
 #include "select.h"
 
@@ -64,13 +66,33 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     int q_heads, int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd,
     bool vec, float* __restrict__ out, int64_t out_ld) {
   using E = typename Elem<DT>::T;
+  __shared__ float q_s[512];
   __shared__ int sel_idx[kMaxDims];
   __shared__ float sel_q[kMaxDims];
-  const int row = blockIdx.y;
+  const int row = blockIdx.y, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
-  select_dims<DT>(query + static_cast<int64_t>(row) * head_dim, head_dim, count, sel_idx, sel_q);
+  const typename Elem<DT>::T* q_row = query + static_cast<int64_t>(row) * head_dim;
+  for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
+  for (int s = tid; s < count; s += kRT) {   // valid even for a NaN query
+    sel_idx[s] = 0;
+    sel_q[s] = q_s[0];
+  }
   __syncthreads();
-  const int t0 = (blockIdx.x * kRT + threadIdx.x) * 8;
+  // rank(d) = #{e : |q_e| > |q_d| or (|q_e| == |q_d| and e < d)} (QK:123-145)
+  for (int d = tid; d < head_dim; d += kRT) {
+    const float a = fabsf(q_s[d]);
+    int rank = 0;
+    for (int e = 0; e < head_dim; ++e) {
+      const float c = fabsf(q_s[e]);
+      rank += (c > a) || (c == a && e < d);
+    }
+    if (rank < count) {
+      sel_idx[rank] = d;
+      sel_q[rank] = q_s[d];
+    }
+  }
+  __syncthreads();
+  const int t0 = (blockIdx.x * kRT + tid) * 8;
   if (t0 >= history) return;
   const E* base = kdm + b * sb + (h / group) * sh + t0;
   float* o = out + static_cast<int64_t>(row) * out_ld + t0;
@@ -78,12 +100,20 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   if (vec && t0 + 8 <= history) {
-    for (int s = 0; s < count; ++s) {
-      float v[8];
-      load8<DT>(base + sel_idx[s] * sd, v);
-      const float qs = sel_q[s];
+    // eight dims' loads in flight at once (clamped, in bounds), then the
+    // products added in selection order
+    for (int s0 = 0; s0 < count; s0 += 8) {
+      float v[8][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[i];
+      for (int j = 0; j < 8; ++j) load8<DT>(base + sel_idx[min(s0 + j, count - 1)] * sd, v[j]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < count) {
+          const float qs = sel_q[s0 + j];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[j][i];
+        }
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = acc[i];
@@ -248,6 +278,106 @@ __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
     final_valid[o + keep + i] = 1;
     if (attn_ids) attn_ids[o + keep + i] = idx;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Rows of at most kWideMax values: one 1024-thread workgroup per row holds
+// the row in registers (WideSelect) and does the whole selection in one
+// launch.  Longer rows take the staged top-k and the kernels above.
+// ---------------------------------------------------------------------------
+constexpr int kWideNT = 1024;
+constexpr int kWideMax = kWideNT * 40;
+
+// mask[r, t] = values[r, t] >= the row's k-th largest value.
+template <int VPL>
+__global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* __restrict__ values, int64_t ld, int n,
+                                                                  int k, uint8_t* __restrict__ mask, int64_t mask_ld) {
+  using WS = WideSelect<VPL, false>;
+  __shared__ typename WS::Shared sh;
+  WS ws;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  ws.load(values + static_cast<int64_t>(row) * ld, n);
+  ws.run(k, sh);
+  // A slot of a wave covers 64 consecutive positions: its flags are one
+  // ballot, written by 16 lanes as dwords (bytes one by one at the row end
+  // or when the rows are not 4-byte aligned).
+  uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
+  const int lane = tid & 63;
+  const bool dwords = (reinterpret_cast<uintptr_t>(mrow) & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int t = WS::pos(i);
+    const bool f = ws.u[i] >= ws.theta;
+    const uint64_t m = __ballot(f);
+    const int chunk = t - lane;
+    if (dwords && chunk + 64 <= n) {
+      if (lane < 16) {
+        const uint32_t nib = static_cast<uint32_t>(m >> (4 * lane)) & 0xFu;
+        const uint32_t w = (nib & 1u) | ((nib >> 1) & 1u) << 8 | ((nib >> 2) & 1u) << 16 | ((nib >> 3) & 1u) << 24;
+        *reinterpret_cast<uint32_t*>(mrow + chunk + 4 * lane) = w;
+      }
+    } else if (t < n) {
+      mrow[t] = f;
+    }
+  }
+}
+
+// The final selection of reuse_finalize_kernel, with the keep largest scores
+// selected in the same launch.
+template <int VPL>
+__global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
+    const float* __restrict__ scores, int64_t scores_ld, int keep, int history, int key_count, int sink_end,
+    int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
+    uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out, uint8_t* __restrict__ hf,
+    int64_t hf_ld) {
+  using WS = WideSelect<VPL, false>;
+  __shared__ typename WS::Shared sh;
+  WS ws;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  // the protected ranges, 16 bytes per store where the row is 16-byte aligned
+  const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
+  for (int t0 = 16 * tid; t0 < body; t0 += 16 * kWideNT) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int t = t0 + 4 * j + b;
+        x |= static_cast<uint32_t>((t < sink_end) || (t >= recent_start)) << (8 * b);
+      }
+      w[j] = x;
+    }
+    *reinterpret_cast<uint4*>(hrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
+  ws.load(scores + static_cast<int64_t>(row) * scores_ld, history);
+  ws.run(keep, sh);   // its barriers order the writes above before the scatter below
+  const int64_t o = static_cast<int64_t>(row) * n_out;
+  ws.place(sh, [&](int idx, uint32_t key, int p) {
+    const bool valid = isfinite(sortable_f32(key));
+    if (valid) hrow[idx] = 1;
+    const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
+    final_idx[o + p] = idx;
+    final_valid[o + p] = fv;
+    if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
+  });
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kWideNT) {
+    const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+    final_idx[o + keep + i] = idx;
+    final_valid[o + keep + i] = 1;
+    if (attn_ids) attn_ids[o + keep + i] = idx;
+  }
+}
+
+// VPL for a row of n values: 16, 32 or 40 (n <= kWideMax).
+template <typename F>
+int with_wide_vpl(int64_t n, F&& f) {
+  if (n <= 16 * kWideNT) return f(std::integral_constant<int, 16>{});
+  if (n <= 32 * kWideNT) return f(std::integral_constant<int, 32>{});
+  return f(std::integral_constant<int, 40>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -424,6 +554,16 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
   rc = dispatch_dtype<RunReuseScores>(dtype, query, key, k_strides, batch, q_heads, kv_heads, history, head_dim,
                                       current, previous, previous_final, mask_ld, scaling, scores, history, st);
   if (rc) return rc;
+  if (history <= kWideMax) {
+    return with_wide_vpl(history, [&](auto vpl) {
+      reuse_final_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          scores, history, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
+          static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+          static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
+          static_cast<int>(n_out), history_final, history_final_ld);
+      return check_launch(what);
+    });
+  }
   rc = qkv_topk_ws(scores, rows, history, history, c.keep, sel, tk_ws, tk_bytes, stream);
   if (rc) return rc;
   reuse_finalize_kernel<<<static_cast<unsigned>(rows), kRT, 0, st>>>(
@@ -468,6 +608,13 @@ QKV_EXPORT int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, 
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n <= kWideMax) {
+    return with_wide_vpl(n, [&](auto vpl) {
+      reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld);
+      return check_launch(what);
+    });
+  }
   int32_t* sel = static_cast<int32_t*>(workspace);
   void* tk_ws = static_cast<char*>(workspace) + align256(rows * k * 4);
   int rc = qkv_topk_ws(values, rows, n, ld, k, sel, tk_ws, workspace_bytes - align256(rows * k * 4), stream);

@@ -200,5 +200,217 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   return kk;
 }
 
+
+// ---------------------------------------------------------------------------
+// Rows of up to 1024 * VPL keys in one 1024-thread workgroup (16 waves).
+// Wave w owns positions [w*64*VPL, (w+1)*64*VPL); its lane l holds the keys
+// at w*64*VPL + 64*i + l (i < VPL) in registers, so every load and every
+// mask store is one contiguous 256-byte run per wave, the row is read once,
+// and position order is (wave, slot, lane) order.  The radix resolution is
+// select_row's, with one histogram per wave.  run() finds theta (the
+// smallest taken key) and kr (how many keys equal to theta are taken, the
+// lowest positions first); place() then hands every taken position, in
+// ascending order, to a callback with its output slot.  Positions at or past
+// n are never taken.
+// ---------------------------------------------------------------------------
+template <int VPL, bool FINITE>
+struct WideSelect {
+  static constexpr int NW = 16, NT = 64 * NW;
+  static_assert(VPL <= 64, "one validity bit per key");
+  uint32_t u[VPL];
+  uint64_t valid = 0;   // bit i: key i of this thread takes part
+  uint32_t theta = 0;
+  int kr = 0, kk = 0;
+
+  // LDS of the selection (the caller declares one and passes it in).
+  static constexpr int RB = 12, NB = 1 << RB;   // radix digit: 12 bits, 4096 bins
+  struct Shared {
+    int hist[NB];
+    int wave_sum[NW];
+    int wave_gt[NW], wave_eq[NW];
+    uint32_t red[NW][3];
+    int bin, kr, whole;
+  };
+
+  // Position of key i of this thread.
+  __device__ static int pos(int i) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    return wave * 64 * VPL + 64 * i + lane;
+  }
+
+  // A raw buffer of exactly the row's n * 4 bytes: positions past the row
+  // read 0 from the range check instead of touching memory.
+  __device__ void load(const float* __restrict__ vals, int n) {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
+    const int base = pos(0);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      u[i] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (base + 64 * i) * 4, 0, 0));
+    // key i is inside the row while 64 i < n - base
+    const int nv = min(max((n - base + 63) / 64, 0), VPL);
+    valid = nv >= 64 ? ~0ull : ((1ull << nv) - 1ull);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      u[i] = f32_sortable(__uint_as_float(u[i]));
+      if (FINITE && u[i] == kNegInfKey) valid &= ~(1ull << i);
+    }
+  }
+
+  __device__ bool on(int i) const { return (valid >> i) & 1ull; }
+
+  // Marks the validity bits as changed here, so each phase derives its
+  // per-slot lane masks anew instead of keeping VPL scalar-register pairs
+  // alive across the whole kernel.
+  __device__ void refresh() { asm volatile("" : "+v"(valid)); }
+
+  // theta and kr for the k largest valid keys; returns kk = min(k, valid keys).
+  __device__ int run(int k, Shared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t umax = 0, umin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      if (on(i)) {
+        umax = max(umax, u[i]);
+        umin = min(umin, u[i]);
+      }
+    }
+    int nval = wave_incl_scan_dpp(__popcll(valid));
+    umax = wave_minmax_u32<true>(umax);
+    umin = wave_minmax_u32<false>(umin);
+    if (lane == 63) {
+      sh.red[wave][0] = umax;
+      sh.red[wave][1] = umin;
+      sh.red[wave][2] = nval;
+    }
+    __syncthreads();
+    umax = 0;
+    umin = 0xFFFFFFFFu;
+    nval = 0;
+#pragma unroll 4
+    for (int w = 0; w < NW; ++w) {
+      umax = max(umax, sh.red[w][0]);
+      umin = min(umin, sh.red[w][1]);
+      nval += static_cast<int>(sh.red[w][2]);
+    }
+    kk = min(k, nval);
+    kr = kk;
+    uint32_t prefix = umax, mask = 0xFFFFFFFFu;
+    int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
+    if (remaining) {
+      mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
+      prefix = umax & mask;
+    }
+    if (kk == nval) {   // every valid key is taken
+      prefix = umin;
+      kr = 0x7FFFFFFF;
+      remaining = 0;
+    }
+    // One shared histogram of 4096 bins: a 12-bit digit of sign, exponent
+    // and top mantissa bits spreads typical scores over enough bins that a
+    // wave's atomics rarely collide (an 8-bit digit of such floats holds a
+    // handful of exponents and serializes on them).
+    while (remaining > 0) {   // uniform across the workgroup
+      refresh();
+      const int shift = remaining > RB ? remaining - RB : 0;
+      const uint32_t dmask = (1u << (remaining - shift)) - 1u;
+      for (int e = tid; e < NB; e += NT) sh.hist[e] = 0;
+      __syncthreads();
+      // Keys equal to the row minimum are counted per wave instead: a flood
+      // of equal keys (the -inf of unscored positions) would serialize on
+      // one LDS address.
+      int at_min = 0;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        if (on(i) && (u[i] & mask) == prefix) {
+          if (u[i] == umin) ++at_min;
+          else atomicAdd(&sh.hist[(u[i] >> shift) & dmask], 1);
+        }
+      }
+      at_min = wave_incl_scan_dpp(at_min);
+      if (lane == 63 && at_min) atomicAdd(&sh.hist[(umin >> shift) & dmask], at_min);
+      __syncthreads();
+      // Thread t owns bins NB-1-4t .. NB-4-4t (descending), so the keys in
+      // higher bins are those of lower threads and of its own earlier bins.
+      int c[4], tot = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = sh.hist[NB - 1 - 4 * tid - j];
+        tot += c[j];
+      }
+      const int incl = wave_incl_scan_dpp(tot);
+      if (lane == 63) sh.wave_sum[wave] = incl;
+      __syncthreads();
+      int above = incl - tot;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) above += w < wave ? sh.wave_sum[w] : 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (above < kr && kr <= above + c[j]) {
+          sh.bin = NB - 1 - 4 * tid - j;
+          sh.kr = kr - above;
+          sh.whole = (kr - above) == c[j];
+        }
+        above += c[j];
+      }
+      __syncthreads();
+      prefix |= static_cast<uint32_t>(sh.bin) << shift;
+      mask |= dmask << shift;
+      kr = sh.kr;
+      remaining = shift;
+      if (sh.whole) {   // the boundary bin is taken whole: theta = its lower bound
+        kr = 0x7FFFFFFF;
+        break;
+      }
+      __syncthreads();   // sh.bin / sh.kr are read before the next pass rewrites them
+    }
+    theta = prefix;
+    return kk;
+  }
+
+  // Calls emit(position, key, output index) for every taken key, output
+  // indices 0..kk-1 in ascending position order: a taken key's index is the
+  // number of keys above theta before it plus min(keys equal to theta before
+  // it, kr).  Ends with a barrier.
+  template <typename Emit>
+  __device__ void place(Shared& sh, Emit&& emit) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1ull;
+    refresh();
+    uint64_t gtm = 0, eqm = 0;   // bit i: key i above / equal to theta
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      gtm |= static_cast<uint64_t>(on(i) && u[i] > theta) << i;
+      eqm |= static_cast<uint64_t>(on(i) && u[i] == theta) << i;
+    }
+    asm volatile("" : "+v"(gtm), "+v"(eqm));
+    const int cg = __popcll(gtm), ce = __popcll(eqm);
+    const int ig = wave_incl_scan_dpp(cg), ie = wave_incl_scan_dpp(ce);
+    if (lane == 63) {
+      sh.wave_gt[wave] = ig;
+      sh.wave_eq[wave] = ie;
+    }
+    __syncthreads();
+    int g = 0, e = 0;   // keys of the earlier waves, then of the earlier slots of this wave
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      g += w < wave ? sh.wave_gt[w] : 0;
+      e += w < wave ? sh.wave_eq[w] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const bool gt = (gtm >> i) & 1ull, eq = (eqm >> i) & 1ull;
+      const uint64_t bgt = __ballot(gt), beq = __ballot(eq);
+      if (bgt | beq) {   // wave-uniform
+        const int gl = g + __popcll(bgt & below), el = e + __popcll(beq & below);
+        if (gt || (eq && el < kr)) emit(pos(i), u[i], gl + min(el, kr));
+        g += __popcll(bgt);
+        e += __popcll(beq);
+      }
+    }
+    __syncthreads();
+  }
+};
+
 }  // namespace
 }  // namespace qkv

@@ -200,7 +200,6 @@ class ReuseDecodeStep:
     def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
         """query bf16 [B, Hq, D]; key/value bf16 [B, Hkv, T, D] (the current
         token last).  Returns bf16 [B, Hq, D]."""
-        lib = _lib.load()
         key_count = key.size(2)
         _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
         g = self.q_heads // self.kv_heads
@@ -213,15 +212,30 @@ class ReuseDecodeStep:
         if self.kdm_len < history:
             dim_major_append(key, self.kdm, self.kdm_len, history)
             self.kdm_len = history
+        consecutive = self.last_history == history - 1
+        cur, prev = self.cand[self.flip], self.cand[1 - self.flip]
+        self.launch(query, key, value, scaling, cur, prev if consecutive and self.use_prev_candidate else None,
+                    self.fin if consecutive and self.use_prev_final else None)
+        self.flip ^= 1
+        self.last_history = history
+        return self.out
+
+    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
+               current: torch.Tensor, previous: torch.Tensor | None, previous_final: torch.Tensor | None) -> None:
+        """The step's kernels at the history key.size(2) - 1 with explicit
+        mask buffers (rows of ``capacity`` bytes): the current candidates go to
+        ``current``, the final mask to the final buffer (it may also be the
+        ``previous_final`` read).  Touches no Python state but ``n_out``; the
+        dim-major copy must already hold the history.  Output in ``self.out``."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        history = key_count - 1
+        _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
         q = query.contiguous()
         reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
-        cur, prev = self.cand[self.flip], self.cand[1 - self.flip]
         self.mask_ws = self._grow(self.mask_ws, lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
-        threshold_mask(self.partial, history, requested, cur, self.mask_ws)
-        consecutive = self.last_history == history - 1
-        use_prev = prev if consecutive and self.use_prev_candidate else None
-        use_fin = self.fin if consecutive and self.use_prev_final else None
+        threshold_mask(self.partial, history, requested, current, self.mask_ws)
         n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
         self.select_ws = self._grow(self.select_ws,
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
@@ -229,16 +243,13 @@ class ReuseDecodeStep:
         with torch.cuda.device(q.device):
             _lib.check(lib.qkv_reuse_select(
                 q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch, self.q_heads,
-                self.kv_heads, key_count, self.head_dim, cur.data_ptr(), _lib.ptr(use_prev), _lib.ptr(use_fin),
-                self.capacity, self.sink, self.recent, self.top_fraction, int(self.keep_self), float(scaling),
-                self.select_ws.data_ptr(), self.select_ws.numel() * 4, self.final_idx.data_ptr(),
-                self.final_valid.data_ptr(), ids.data_ptr(), n_out, self.fin.data_ptr(), self.capacity,
-                _lib.stream_of(q)))
+                self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
+                _lib.ptr(previous_final), self.capacity, self.sink, self.recent, self.top_fraction,
+                int(self.keep_self), float(scaling), self.select_ws.data_ptr(), self.select_ws.numel() * 4,
+                self.final_idx.data_ptr(), self.final_valid.data_ptr(), ids.data_ptr(), n_out, self.fin.data_ptr(),
+                self.capacity, _lib.stream_of(q)))
         token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
-        self.flip ^= 1
-        self.last_history = history
         self.n_out = n_out
-        return self.out
 
     # -- state views (tests, tracing) ------------------------------------------
     def candidate_mask(self) -> torch.Tensor:

@@ -354,3 +354,73 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
                                       top_fraction, keep_self, scaling)
     out = final_attention(q, kx, vx, fi, fv, scaling)
     return out, current, hist_final
+
+
+def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, candidate_fraction: float,
+                        top_fraction: float, scaling: float, sink: int = 0, recent: int = 0, keep_self: bool = True,
+                        previous_candidate=None, previous_final=None):
+    """One ``qabs{S}cand{pct}reuse`` decode step in the reference's PyTorch
+    ops on CPU tensors: the path ``_qabs_reuse_fast_attention_forward`` takes
+    when no CUDA kernel is available (EV:3991-4397 with the dense-mask
+    fallbacks of EV:4161-4167, 4276-4303 and the gather attention of
+    EV:4365-4374).  It is the CPU baseline that ``bench.py`` times next to the
+    GPU reuse step.
+
+    query_states [B,Hq,1,D]; key/value_states [B,Hkv,T,D] (GQA-expanded
+    first, EV:6248-6251); previous_* bool [B,Hq,T-1] or None.  Returns
+    (out [B,1,Hq,D], current, history_final)."""
+    import torch
+    import torch.nn.functional as F
+
+    b, hq, _, d = query_states.shape
+    if key_states.shape[1] != hq:
+        rep = hq // key_states.shape[1]
+        key_states = key_states.repeat_interleave(rep, dim=1)
+        value_states = value_states.repeat_interleave(rep, dim=1)
+    key_count = key_states.shape[-2]
+    history = key_count - 1
+    q_raw = query_states[:, :, 0, :]
+    k_hist = key_states[:, :, :history, :]
+    sdims = min(max(1, dim_count), d)
+    qdims = torch.topk(q_raw.float().abs(), k=sdims, dim=-1, largest=True).indices               # EV:4068
+    q_sel = torch.gather(q_raw.float(), dim=-1, index=qdims)
+    k_sel = torch.gather(k_hist.float(), dim=-1, index=qdims[:, :, None, :].expand(-1, -1, history, -1))
+    partial = (k_sel * q_sel[:, :, None, :]).sum(dim=-1)                                          # EV:4130-4135
+    requested = budget_count(history, candidate_fraction)
+    thr = torch.topk(partial, k=requested, dim=-1, largest=True).values[:, :, -1:]
+    current = partial >= thr                                                                      # EV:3988-3989
+    union = current.clone()                                                                       # EV:4161-4167
+    if previous_candidate is not None:
+        union |= previous_candidate
+    if previous_final is not None:
+        union |= previous_final
+    # _indices_from_keep_mask (EV:2896-2911): descending positions of the mask
+    counts = union.sum(dim=-1)
+    width = max(1, int(counts.max().item()))
+    pos = torch.arange(history).view(1, 1, -1).expand_as(union)
+    cand_idx = torch.topk(torch.where(union, pos, torch.full_like(pos, -1)), k=width, dim=-1, largest=True).values
+    cand_valid = cand_idx >= 0
+    cand_idx = cand_idx.clamp_min(0)
+    keys = torch.gather(k_hist, dim=2, index=cand_idx[:, :, :, None].expand(-1, -1, -1, d))       # EV:4290-4296
+    scores = torch.matmul(query_states[:, :, 0:1, :], keys.transpose(2, 3)).squeeze(2) * scaling
+    scores = scores.masked_fill(~cand_valid, torch.finfo(scores.dtype).min)
+    keep = min(budget_count(history, top_fraction), scores.shape[-1])
+    _, sel_pos = torch.topk(scores, k=keep, dim=-1, largest=True)                                # EV:4298-4303
+    selected = torch.gather(cand_idx, dim=-1, index=sel_pos)
+    selected_valid = torch.gather(cand_valid, dim=-1, index=sel_pos)
+    history_final = torch.zeros_like(current)                                                     # EV:4305-4312
+    history_final.scatter_(dim=-1, index=selected, src=selected_valid)
+    if sink > 0:
+        history_final[:, :, : min(sink, history)] = True
+    if recent > 0:
+        history_final[:, :, max(0, history - recent):history] = True
+    final_idx, final_valid = final_indices_from_selected(selected, selected_valid, history, key_count, sink,
+                                                         recent, keep_self)                     # EV:4365
+    gather = final_idx[:, :, :, None].expand(-1, -1, -1, d)                                       # EV:4366-4374
+    sel_k = torch.gather(key_states, dim=2, index=gather)
+    sel_v = torch.gather(value_states, dim=2, index=gather)
+    att = torch.matmul(query_states[:, :, 0:1, :], sel_k.transpose(2, 3)).squeeze(2) * scaling
+    att = att.masked_fill(~final_valid, torch.finfo(att.dtype).min)
+    weights = F.softmax(att, dim=-1, dtype=torch.float32).to(query_states.dtype)
+    out = torch.sum(weights[:, :, :, None] * sel_v, dim=2)
+    return out[:, None, :, :].contiguous(), current, history_final

@@ -78,6 +78,8 @@ def test_step_matches_reference_vectors_bf16():
     (1, 3, 777, 0, 0, 0.3, False),       # keep larger than the union: invalid -inf picks
     (1, 2, 2, 1, 1, 1.0, True),          # history 1
     (1, 2, 9000, 100, 100, 0.01, True),  # protected ranges overlap the selection
+    (1, 2, 40961, 3, 3, 0.02, True),     # the longest row selected in one workgroup
+    (1, 1, 45001, 0, 7, 0.05, False),    # longer rows: staged top-k
 ])
 def test_reuse_select_matches_oracle(dtype, b, h, t, sink, recent, frac, keep_self):
     gen = torch.Generator().manual_seed(t + h)
@@ -93,6 +95,22 @@ def test_reuse_select_matches_oracle(dtype, b, h, t, sink, recent, frac, keep_se
     assert np.array_equal(fi.cpu().numpy(), wi)        # same order: ascending selection, then the ranges
     assert np.array_equal(fv.cpu().numpy(), wv)
     assert np.array_equal(hf.cpu().numpy(), whf)
+
+
+@pytest.mark.parametrize("rows,n,k,ld", [(3, 1000, 50, 1000), (2, 16384, 1, 16400), (2, 16385, 819, 16385),
+                                         (1, 40960, 2048, 40960), (2, 45000, 2250, 45056), (4, 7, 7, 9)])
+def test_threshold_mask_matches_oracle(rows, n, k, ld):
+    gen = torch.Generator().manual_seed(n + k)
+    vals = torch.randint(-30, 30, (rows, ld), generator=gen).float()      # heavy ties at the threshold
+    vals[0] = torch.randn(ld, generator=gen)
+    mask = torch.full((rows, ld + 5), 7, dtype=torch.uint8)
+    lib = Q._lib.load()
+    ws = torch.empty(lib.qkv_threshold_mask_workspace_bytes(rows, n, k) // 4 + 1, dtype=torch.float32, device=DEV)
+    md = mask.to(DEV)
+    RU.threshold_mask(vals.to(DEV), n, k, md, ws)
+    got = md.cpu().numpy()
+    assert np.array_equal(got[:, :n].astype(bool), R.threshold_mask(vals[:, :n].numpy(), k))
+    assert set(np.unique(got[:, :n]).tolist()) <= {0, 1} and (got[:, n:] == 7).all()   # nothing past n
 
 
 def test_reuse_select_ties_and_missing_masks():

@@ -125,3 +125,27 @@ def test_reuse_select_invariants():
             assert hf[bi, hi, :3].all() and hf[bi, hi, t - 4:].all()
             assert set(np.flatnonzero(hf[bi, hi]).tolist()) == chosen | {0, 1, 2} | set(range(t - 4, t))
             assert fi[bi, hi, -1] == t and fv[bi, hi, -1]
+
+
+@pytest.mark.parametrize("name", SCENARIOS)
+def test_cpu_baseline_op_sequence_matches_reference_vectors(name):
+    # The torch op sequence bench.py times as the reuse CPU baseline leaves
+    # the reference's state and output at every step.
+    import torch
+
+    g = load_golden(name)
+    dt = torch.float32 if g["dtype"] == "float32" else torch.bfloat16
+    k, v = torch.from_numpy(g["k"]).to(dt), torch.from_numpy(g["v"]).to(dt)
+    pc = pf = None
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(dt)[:, :, None, :]
+        fit = lambda m: None if m is None else torch.cat([m, torch.zeros_like(m[..., :1])], dim=-1)
+        out, cur, hf = R.qabs_reuse_step_cpu(q, k[:, :, :n], v[:, :, :n], g["dims"], g["cand"], g["top_fraction"],
+                                             g["scaling"], g["sink"], g["recent"], g["keep_self"],
+                                             fit(pc) if g["use_prev_candidate"] else None,
+                                             fit(pf) if g["use_prev_final"] else None)
+        assert np.array_equal(cur.numpy(), g["candidate"][s][..., : n - 1]), (name, s)
+        assert np.array_equal(hf.numpy(), g["final"][s][..., : n - 1]), (name, s)
+        np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], rtol=1e-5, atol=1e-6)
+        pc, pf = cur, hf
