@@ -424,3 +424,151 @@ def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, 
     weights = F.softmax(att, dim=-1, dtype=torch.float32).to(query_states.dtype)
     out = torch.sum(weights[:, :, :, None] * sel_v, dim=2)
     return out[:, None, :, :].contiguous(), current, history_final
+
+
+# ---------------------------------------------------------------------------
+# Block-metadata selectors: Quest-style channel bounds (qbb) and block
+# representatives (brep)
+# ---------------------------------------------------------------------------
+
+def block_minmax(key, block: int):
+    """Per block of ``block`` tokens and per channel, the min and max of K
+    over the block's tokens (the last block may be partial; EV:5536-5553).
+    key [..., T, D] -> (kmin, kmax) [..., ceil(T/block), D] float32."""
+    k = np.asarray(key, dtype=np.float32)
+    t = k.shape[-2]
+    nb = -(-t // block)
+    pad = nb * block - t
+    hi = np.concatenate([k, np.full((*k.shape[:-2], pad, k.shape[-1]), -np.inf, np.float32)], axis=-2)
+    lo = np.concatenate([k, np.full((*k.shape[:-2], pad, k.shape[-1]), np.inf, np.float32)], axis=-2)
+    shape = (*k.shape[:-2], nb, block, k.shape[-1])
+    return lo.reshape(shape).min(axis=-2), hi.reshape(shape).max(axis=-2)
+
+
+def qbb_block_bounds(query, kmin, kmax, dim_count: int) -> np.ndarray:
+    """Quest-style upper bound of q.k over a block on the row's top-|q| dims
+    (EV:5554): sum over dims d_s, in selection order, of q_s * max_d when
+    q_s >= 0 else q_s * min_d, fp32 with separately rounded products and
+    sums.  query [B,H,D]; kmin/kmax [B,H,nb,D] -> f32 [B,H,nb]."""
+    q = np.asarray(query, dtype=np.float32)
+    b, h, _ = q.shape
+    out = np.zeros((b, h, kmin.shape[2]), dtype=np.float32)
+    for bi in range(b):
+        for hi in range(h):
+            dims = select_dims_by_abs(q[bi, hi], dim_count)
+            acc = np.zeros(kmin.shape[2], dtype=np.float32)
+            for d in dims:
+                qs = np.float32(q[bi, hi, d])
+                ext = kmax[bi, hi, :, d] if qs >= 0 else kmin[bi, hi, :, d]
+                acc = (acc + (qs * ext).astype(np.float32)).astype(np.float32)
+            out[bi, hi] = acc
+    return out
+
+
+def block_representatives(key, block: int, reps: int):
+    """Per block, the ``reps`` tokens of largest squared norm (fp32 sum of
+    squares in channel order), ties to the lower position, in descending
+    norm order (BlockRepState.representatives, EV:1857-1918).
+    key [..., T, D] -> (indices int64 [..., nb, R], valid bool [..., nb, R]);
+    a partial last block with fewer tokens pads with index 0, invalid."""
+    k = np.asarray(key, dtype=np.float32)
+    t, d = k.shape[-2], k.shape[-1]
+    nb = -(-t // block)
+    r = max(1, min(reps, block))
+    lead = k.shape[:-2]
+    norms = np.zeros((*lead, t), dtype=np.float32)
+    for c in range(d):
+        norms = (norms + (k[..., c] * k[..., c]).astype(np.float32)).astype(np.float32)
+    idx = np.zeros((*lead, nb, r), dtype=np.int64)
+    valid = np.zeros((*lead, nb, r), dtype=bool)
+    flat_n = norms.reshape(-1, t)
+    fi, fv = idx.reshape(-1, nb, r), valid.reshape(-1, nb, r)
+    for row in range(flat_n.shape[0]):
+        for j in range(nb):
+            s, e = j * block, min(t, (j + 1) * block)
+            order = np.lexsort((np.arange(s, e), -flat_n[row, s:e]))[: min(r, e - s)]
+            fi[row, j, : order.size] = s + order
+            fv[row, j, : order.size] = True
+    return idx, valid
+
+
+def brep_block_scores(query, key, rep_idx, rep_valid, dim_count: int) -> np.ndarray:
+    """Block score = max over the block's valid representatives of the fp32
+    partial score on the row's top-|q| dims (EV:5431-5435); a block with no
+    valid representative scores finfo(float32).min.  query [B,H,D]; key
+    [B,H,T,D]; rep_* [B,H,nb,R] -> f32 [B,H,nb]."""
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    b, h, _ = q.shape
+    nb = rep_idx.shape[2]
+    lowest = np.finfo(np.float32).min
+    out = np.full((b, h, nb), lowest, dtype=np.float32)
+    for bi in range(b):
+        for hi in range(h):
+            dims = select_dims_by_abs(q[bi, hi], dim_count)
+            sc = _seq_dot(q[bi, hi, dims], k[bi, hi][rep_idx[bi, hi]][..., dims])   # [nb, R]
+            sc = np.where(rep_valid[bi, hi], sc, lowest)
+            out[bi, hi] = sc.max(axis=-1)
+    return out
+
+
+def block_select_step(query, key, value, kind: str, block: int, dim_count: int, scan_fraction: float,
+                      candidate_fraction: float, top_fraction: float, scaling: float, sink: int = 0,
+                      recent: int = 0, keep_self: bool = True, reps: int = 1):
+    """One decode step of the qbb (EV:5508-5617) or brep (EV:5361-5505)
+    selector: block scores -> the ``ceil(scan * history / block)`` best blocks
+    -> partial scores of their tokens on the top-|q| dims -> the
+    ``ceil(cand * history)`` best tokens -> full-D fp32 scores * scaling ->
+    the ``ceil(top * history)`` best -> final mask with the sink / recent
+    ranges and the current token -> attention over the mask.
+
+    query [B,Hq,D]; key/value [B,Hkv,T,D] (head h reads KV head h // G).
+    Ties go to the lower block / token index at every selection (the
+    reference's ``torch.topk`` leaves them unspecified).  Returns (out
+    float64 [B,1,Hq,D], final_keep bool [B,Hq,T])."""
+    from .qkv_oracle import topk_lowest_index
+
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, hq, d = q.shape
+    g = hq // k.shape[1]
+    kx, vx = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    key_count = k.shape[2]
+    if key_count <= 1:
+        return vx[:, :, -1:, :].transpose(0, 2, 1, 3).astype(np.float64), np.ones((b, hq, key_count), bool)
+    history = key_count - 1
+    kh = kx[:, :, :history]
+    nb = -(-history // block)
+    if kind == "qbb":
+        kmin, kmax = block_minmax(kh, block)
+        bscore = qbb_block_bounds(q, kmin, kmax, dim_count)
+    elif kind == "brep":
+        ridx, rvalid = block_representatives(kh, block, reps)
+        bscore = brep_block_scores(q, kh, ridx, rvalid, dim_count)
+    else:
+        raise ValueError(kind)
+    n_scan = min(nb, max(1, math.ceil(scan_fraction * history / block)))
+    blocks = topk_lowest_index(bscore.reshape(-1, nb), n_scan).reshape(b, hq, n_scan)
+    final_keep = np.zeros((b, hq, key_count), dtype=bool)
+    n_req = max(1, math.ceil(candidate_fraction * history))
+    n_keep = max(1, math.ceil(top_fraction * history))
+    for bi in range(b):
+        for hi in range(hq):
+            toks = np.concatenate([np.arange(j * block, min(history, (j + 1) * block)) for j in blocks[bi, hi]])
+            toks.sort()
+            dims = select_dims_by_abs(q[bi, hi], dim_count)
+            part = _seq_dot(q[bi, hi, dims], kh[bi, hi][toks][:, dims])
+            cand = toks[np.sort(topk_lowest_index(part[None], min(toks.size, n_req))[0])]
+            full = (_seq_dot(q[bi, hi], kh[bi, hi][cand]) * np.float32(scaling)).astype(np.float32)
+            keep = cand[topk_lowest_index(full[None], min(cand.size, n_keep))[0]]
+            final_keep[bi, hi, keep] = True
+    if sink > 0:
+        final_keep[..., : min(sink, history)] = True
+    if recent > 0:
+        final_keep[..., max(0, history - recent):history] = True
+    if keep_self:
+        final_keep[..., history] = True
+    idx = np.broadcast_to(np.arange(key_count), final_keep.shape)
+    out = final_attention(q, kx, vx, idx, final_keep, scaling)
+    return out, final_keep

@@ -1,4 +1,5 @@
-"""Writes golden vectors for the stateful candidate-reuse decode step.
+"""Writes golden vectors for the stateful candidate-reuse decode step and the
+block-metadata selectors (qbb, brep).
 
 The reference's ``qabs{S}cand{pct}reuse[final|2set]`` driver
 (``_qabs_reuse_fast_attention_forward``,
@@ -20,7 +21,7 @@ Run from the repository root with the reference checked out at
 
     python tests/golden/make_reuse_vectors.py
 
-Outputs ``tests/golden/reuse_<name>.npz`` (a few hundred KB in all).
+Outputs ``tests/golden/reuse_<name>.npz`` and ``tests/golden/block_<name>.npz``.
 """
 
 from __future__ import annotations
@@ -84,6 +85,65 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
     print(f"{name}: {mode} {dtype} Hq={hq} T0={t0} steps={steps} -> reuse_{name}.npz")
 
 
+# Block-metadata selectors (qbb: Quest-style channel bounds, EV:5508-5617;
+# brep: block representatives with their BlockRepState, EV:5361-5505, 1853-1918).
+# name: (mode, dtype, Hq, Hkv, T0, steps, top_fraction, sink, recent, keep_self, seed)
+BLOCK_SCENARIOS = {
+    "qbb16q8s12cand4_fp32": ("qbb16q8s12cand4", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 11),
+    "qbb8q16s25cand6p25_fp32": ("qbb8q16s25cand6p25", torch.float32, 4, 4, 201, 3, 0.03, 0, 0, False, 12),
+    "brep16r2q8s12cand4_fp32": ("brep16r2q8s12cand4", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 13),
+    "brep8r1q16s25cand6p25_fp32": ("brep8r1q16s25cand6p25", torch.float32, 2, 1, 233, 3, 0.03, 0, 4, True, 14),
+}
+
+
+def run_block(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, keep_self, seed):
+    """Consecutive decode steps of a block selector; the final index list the
+    step hands to its attention (its argument to _maybe_cuda_final_attention,
+    which returns None on the CPU) is recorded as the final keep mask."""
+    g = torch.Generator().manual_seed(seed)
+    d = 128
+    t_max = t0 + steps
+    q = torch.randn((steps, 1, hq, 1, d), generator=g).to(dtype)
+    k = (torch.randn((1, hkv, t_max, d), generator=g) * 1.5).to(torch.bfloat16).to(dtype)
+    v = torch.randn((1, hkv, t_max, d), generator=g).to(torch.bfloat16).to(dtype)
+    scaling = d ** -0.5
+    module = types.SimpleNamespace(layer_idx=0, scaling=scaling)
+    seen = []
+    original = ev._maybe_cuda_final_attention
+
+    def record(query_states, key_states, value_states, attention_mask, final_indices, final_valid, scaling_):
+        seen.append((final_indices.clone(), final_valid.clone()))
+        return original(query_states, key_states, value_states, attention_mask, final_indices, final_valid, scaling_)
+
+    ev._maybe_cuda_final_attention = record
+    brep_state = ev.BlockRepState() if mode.startswith("brep") else None
+    outs, finals = [], []
+    try:
+        with ev.attention_mode(mode=mode, top_fraction=top_fraction, max_heads_per_token=3,
+                               always_keep_self=keep_self, protect_sink_tokens=sink,
+                               protect_recent_tokens=recent, load_stats=None, brep_state=brep_state):
+            for s in range(steps):
+                n = t0 + s + 1
+                seen.clear()
+                out, _ = ev._limited_eager_attention_forward(module, q[s], k[:, :, :n], v[:, :, :n], None,
+                                                             scaling=scaling)
+                idx, val = seen[-1]
+                keep = np.zeros((1, hq, t_max), dtype=bool)
+                for h in range(hq):
+                    keep[0, h, idx[0, h][val[0, h]].numpy()] = True
+                outs.append(out.float().numpy())
+                finals.append(keep)
+    finally:
+        ev._maybe_cuda_final_attention = original
+    np.savez_compressed(
+        OUT / f"block_{name}.npz", mode=np.array(mode), dtype=np.array(str(dtype).split(".")[-1]),
+        q=q.float().numpy(), k_bf16=k.to(torch.bfloat16).view(torch.int16).numpy(),
+        v_bf16=v.to(torch.bfloat16).view(torch.int16).numpy(), t0=t0, steps=steps,
+        top_fraction=top_fraction, sink=sink, recent=recent, keep_self=keep_self, scaling=scaling,
+        out=np.stack(outs), final=np.packbits(np.stack(finals), axis=-1), t_max=t_max)
+    print(f"{name}: {mode} {dtype} Hq={hq} T0={t0} steps={steps} -> block_{name}.npz")
+
+
 def main():
     sys.path.insert(0, str(REF_SRC))
     import evaluate_qwen3_top2_head_limit3_ppl as ev   # the reference module, CPU only
@@ -91,6 +151,8 @@ def main():
     torch.set_num_threads(1)
     for name, args in SCENARIOS.items():
         run(ev, name, *args)
+    for name, args in BLOCK_SCENARIOS.items():
+        run_block(ev, name, *args)
 
 
 if __name__ == "__main__":

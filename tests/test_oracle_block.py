@@ -1,0 +1,105 @@
+"""Pins the block-metadata selectors of oracle/ref_semantics.py (qbb: Quest-style
+channel bounds; brep: block representatives) against golden vectors written
+by the reference's own drivers (tests/golden/make_reuse_vectors.py), the
+upper-bound property that defines the Quest bound, and known answers."""
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import ref_semantics as R
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+BLOCK_SCENARIOS = ["qbb16q8s12cand4_fp32", "qbb8q16s25cand6p25_fp32", "brep16r2q8s12cand4_fp32",
+                   "brep8r1q16s25cand6p25_fp32"]
+
+
+def parse_block_mode(mode):
+    """(kind, block, reps, dims, scan fraction, candidate fraction) of a qbb / brep mode."""
+    pct = lambda x: float(x.replace("p", ".")) / 100.0   # noqa: E731
+    m = re.fullmatch(r"qbb(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
+    if m:
+        return "qbb", int(m.group(1)), 1, int(m.group(2)), pct(m.group(3)), pct(m.group(4))
+    m = re.fullmatch(r"brep(\d+)r(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
+    return "brep", int(m.group(1)), int(m.group(2)), int(m.group(3)), pct(m.group(4)), pct(m.group(5))
+
+
+def load_block_golden(name):
+    z = np.load(GOLDEN / f"block_{name}.npz")
+    t_max = int(z["t_max"])
+    bf = lambda a: (a.astype(np.int32) << 16).view(np.float32)   # noqa: E731
+    kind, block, reps, dims, scan, cand = parse_block_mode(str(z["mode"]))
+    return {
+        "mode": str(z["mode"]), "kind": kind, "block": block, "reps": reps, "dims": dims, "scan": scan,
+        "cand": cand, "q": z["q"][:, :, :, 0, :], "k": bf(z["k_bf16"]), "v": bf(z["v_bf16"]), "t0": int(z["t0"]),
+        "steps": int(z["steps"]), "top_fraction": float(z["top_fraction"]), "sink": int(z["sink"]),
+        "recent": int(z["recent"]), "keep_self": bool(z["keep_self"]), "scaling": float(z["scaling"]),
+        "out": z["out"][:, :, 0], "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
+    }
+
+
+@pytest.mark.parametrize("name", BLOCK_SCENARIOS)
+def test_block_steps_match_reference_vectors(name):
+    g = load_block_golden(name)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        out, keep = R.block_select_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["kind"], g["block"],
+                                        g["dims"], g["scan"], g["cand"], g["top_fraction"], g["scaling"], g["sink"],
+                                        g["recent"], g["keep_self"], g["reps"])
+        assert np.array_equal(keep, g["final"][s][..., :n]), (name, s)
+        np.testing.assert_allclose(out[:, 0], g["out"][s], rtol=1e-5, atol=1e-5)
+
+
+def test_block_minmax_brute_force():
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((2, 37, 5)).astype(np.float32)
+    lo, hi = R.block_minmax(k, 8)
+    assert lo.shape == (2, 5, 5)
+    for j in range(5):
+        seg = k[:, 8 * j: min(37, 8 * j + 8)]
+        assert np.array_equal(lo[:, j], seg.min(axis=1)) and np.array_equal(hi[:, j], seg.max(axis=1))
+
+
+def test_qbb_bound_is_an_upper_bound():
+    # q.k over the selected dims never exceeds the block's bound, and a block
+    # holding the maximizing corner reaches it (a sign slip breaks one of them)
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 3, 16)).astype(np.float32)
+    k = rng.standard_normal((1, 3, 96, 16)).astype(np.float32)
+    lo, hi = R.block_minmax(k, 16)
+    bound = R.qbb_block_bounds(q, lo, hi, 6)
+    part = R.partial_scores(q, k, 6)
+    for h in range(3):
+        for j in range(6):
+            assert part[0, h, 16 * j: 16 * j + 16].max() <= bound[0, h, j] + 1e-5
+    dims = R.select_dims_by_abs(q[0, 0], 6)
+    corner = np.where(q[0, 0] >= 0, hi[0, 0, 2], lo[0, 0, 2])
+    kc = k.copy()
+    kc[0, 0, 32] = corner                       # block 2 now holds its own corner
+    assert np.isclose(R.partial_scores(q, kc, 6)[0, 0, 32], bound[0, 0, 2], rtol=1e-6)
+    assert dims.size == 6
+
+
+def test_block_representatives_known_answer():
+    # norms 1, 9, 4, 9 | 16, 0 : ties to the lower position, descending norm
+    k = np.array([1, 3, 2, -3, 4, 0], np.float32).reshape(1, 6, 1)
+    idx, valid = R.block_representatives(k, 4, 2)
+    assert idx.tolist() == [[[1, 3], [4, 5]]] and valid.all()
+    idx, valid = R.block_representatives(k[:, :5], 4, 3)
+    assert idx.tolist() == [[[1, 3, 2], [4, 0, 0]]]
+    assert valid.tolist() == [[[True, True, True], [True, False, False]]]
+
+
+def test_brep_score_is_max_over_representatives():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 40, 8)).astype(np.float32)
+    idx, valid = R.block_representatives(k, 16, 3)
+    sc = R.brep_block_scores(q, k, idx, valid, 4)
+    part = R.partial_scores(q, k, 4)
+    for h in range(2):
+        for j in range(3):
+            reps = idx[0, h, j][valid[0, h, j]]
+            assert sc[0, h, j] == part[0, h, reps].max()
