@@ -33,6 +33,10 @@ extern "C" {
 #define QKV_DTYPE_FP16 1
 #define QKV_DTYPE_FP32 2
 
+/* Block-metadata selector kinds (qkv_block_*). */
+#define QKV_BLOCK_QBB 0  /* Quest-style per-block channel min/max bounds */
+#define QKV_BLOCK_BREP 1 /* per-block representative tokens */
+
 #define QKV_ABI_VERSION 1
 
 /* ABI version of the loaded library (QKV_ABI_VERSION it was built with). */
@@ -299,6 +303,66 @@ int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld,
 int qkv_dim_major_append(const void* key, const int64_t* k_strides, int dtype, int64_t batch, int64_t kv_heads,
                          int64_t head_dim, int64_t t_begin, int64_t t_end, void* key_dim_major,
                          const int64_t* kdm_strides, void* stream);
+
+/* ======================================================================
+ * Block-metadata selectors: the qbb{bs}q{S}s{scan}cand{c} (Quest-style
+ * channel bounds, EV:5508-5617) and brep{bs}r{R}q{S}s{scan}cand{c} (block
+ * representatives, EV:5361-5505, BlockRepState EV:1853-1918) decode steps.
+ * bf16 K/V [B,Hkv,*,128] with k_strides {b,h,t,d} (d contiguous, rows
+ * 16-byte aligned); rows r = b * Hq + h read K head h / (Hq/Hkv).
+ * ====================================================================== */
+
+/* Bytes of block metadata for meta_blocks blocks per (sequence, KV head):
+ * qbb 512 per block ([min(128) | max(128)] bf16), brep 4*reps per block
+ * (int32 token ids).  -1 for a bad kind or size. */
+int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_heads, int64_t meta_blocks, int64_t reps);
+
+/* Rebuilds the metadata of the blocks holding tokens [t_begin, t_end) from
+ * K's tokens below t_end: per-channel min/max (qbb), or the reps tokens of
+ * largest squared norm (fp32 sum in channel order), descending, lower index
+ * on ties, -1 padding (brep; block <= 64).  The reference recomputes these
+ * every step (EV:5536-5553) or per new block (EV:1884-1918). */
+int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, int64_t batch, int64_t kv_heads,
+                          int64_t head_dim, int64_t block, int64_t reps, int64_t t_begin, int64_t t_end, void* meta,
+                          int64_t meta_blocks, void* stream);
+
+/* Block scores of each row over ceil(history/block) blocks: qbb the bound
+ * sum_s q_s * (q_s >= 0 ? max : min) over the row's top-|q| dims (EV:5554),
+ * brep the largest partial score of the block's representatives
+ * (EV:5431-5435).  Dims as qkv_reuse_partial_scores.  out f32 [rows, out_ld]. */
+int qkv_block_scores(int kind, const void* query, const void* key, const int64_t* k_strides, const void* meta,
+                     int64_t meta_blocks, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                     int64_t head_dim, int64_t block, int64_t reps, int64_t dim_count, float* out, int64_t out_ld,
+                     void* stream);
+
+/* Partial scores of the tokens of each row's chosen blocks (EV:5576-5581):
+ * position p is token blocks[r, p / block] * block + p % block, scored on
+ * the row's top-|q| dims from the dim-major K copy (qkv_dim_major_append);
+ * positions at or past history get -inf.  out f32 [rows, >= n_scan*block]. */
+int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int64_t batch,
+                          int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
+                          const int32_t* blocks, int64_t n_scan, int64_t block, int64_t dim_count, float* out,
+                          int64_t out_ld, void* stream);
+
+/* Entries of a final token list: n_keep + sink range + recent range (not
+ * overlapping the sink) + 1 when keep_self.  -1 for history <= 0. */
+int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t protect_sink, int64_t protect_recent,
+                             int keep_self);
+
+/* Rerank of each row (EV:5583-5605), one workgroup per row: the n_cand best
+ * scanned positions by partial score, their full-D fp32 scores * scaling,
+ * the n_keep best of those (ties to the lower index throughout), then
+ * keep_mask [rows, key_count] (kept tokens, the first protect_sink and last
+ * protect_recent history tokens, the current token when keep_self;
+ * EV:5607-5615) and attn_ids [rows, n_out] for qkv_token_attention: the kept
+ * tokens ascending (-1 where protected or not filled), the sink range, the
+ * recent range, the current token.  n_scan * block <= 40960,
+ * n_keep <= n_cand <= 4096. */
+int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
+                     int64_t kv_heads, int64_t key_count, int64_t head_dim, const float* partial, int64_t partial_ld,
+                     const int32_t* blocks, int64_t n_scan, int64_t block, int64_t n_cand, int64_t n_keep,
+                     int64_t protect_sink, int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
+                     int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream);
 
 /* ======================================================================
  * Chunked-prefill block selection (no reference counterpart: the reference

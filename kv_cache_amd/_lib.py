@@ -69,6 +69,16 @@ _PROTOTYPES = {
     "qkv_threshold_mask_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qkv_threshold_mask": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "qkv_dim_major_append": (_i32, [_vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _P(_i64), _vp]),
+    "qkv_block_meta_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64]),
+    "qkv_block_meta_update": (_i32, [_i32, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                                     _vp]),
+    "qkv_block_scores": (_i32, [_i32, _vp, _vp, _P(_i64), _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                _vp, _i64, _vp]),
+    "qkv_block_scan_scores": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
+                                     _i64, _vp]),
+    "qkv_final_list_count": (_i64, [_i64, _i64, _i64, _i64, _i32]),
+    "qkv_block_rerank": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
+                                _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _vp]),
 }
 
 _LIB = None

@@ -1,0 +1,464 @@
+// Block-metadata selectors: the decode steps of the reference's qbb modes
+// (Quest-style per-block channel bounds, EV:5508-5617) and brep modes (block
+// representatives, EV:5361-5505, with their BlockRepState, EV:1853-1918), on
+// GQA-shaped bf16 K/V (D = 128).
+//
+// Rows are (sequence, query head) r = b * Hq + h, reading K head h / (Hq/Hkv).
+// Per step:
+//   qbb_meta_kernel / brep_meta_kernel  per-KV-head block metadata, kept
+//       across steps and refreshed only for the blocks new tokens touch:
+//       per-channel min and max (qbb), or the R tokens of largest squared
+//       norm (brep);
+//   block_scores_kernel  per (row, block): the bound sum_s q_s * (q_s >= 0 ?
+//       max : min) over the row's top-|q| dims, or the best representative's
+//       partial score;
+//   (qkv_topk)           the best blocks;
+//   scan_partial_kernel  partial scores of the chosen blocks' tokens from the
+//       dim-major K copy (the blocks' tokens are contiguous there);
+//   rerank_kernel        one 1024-thread workgroup per row: the best
+//       candidates by partial score, their full-D scores, the best of those,
+//       the final mask and the final token list (sink / recent / current).
+// Arithmetic follows the reference's fp32 formulas with separately rounded
+// products and sums in dim order (built with -ffp-contract=off); selections
+// keep the lower index on ties.  EV = ymluo/projects/qwen3_top2_head_limit3_ppl/
+// src/evaluate_qwen3_top2_head_limit3_ppl.py.
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "select.h"
+
+namespace qkv {
+namespace {
+
+constexpr int kBT = 256;
+constexpr int kHD = 128;             // head size
+constexpr int kMaxCand = 4096;       // candidates per row (rerank LDS list)
+constexpr int kRerankNT = 1024;
+constexpr int kMaxScan = kRerankNT * 40;   // scanned tokens per row in one workgroup
+
+// The row's top-|q| dims in selection order (descending |q|, lower dim on
+// ties; QK:123-145), from an LDS copy of q.  Ends with a barrier.
+__device__ void rank_dims(const float* q_s, int count, int* sel_idx, float* sel_q) {
+  const int tid = threadIdx.x;
+  for (int s = tid; s < count; s += blockDim.x) {   // valid even for a NaN query
+    sel_idx[s] = 0;
+    sel_q[s] = q_s[0];
+  }
+  __syncthreads();
+  for (int d = tid; d < kHD; d += blockDim.x) {
+    const float a = fabsf(q_s[d]);
+    int rank = 0;
+    for (int e = 0; e < kHD; ++e) {
+      const float c = fabsf(q_s[e]);
+      rank += (c > a) || (c == a && e < d);
+    }
+    if (rank < count) {
+      sel_idx[rank] = d;
+      sel_q[rank] = q_s[d];
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
+
+// ---------------------------------------------------------------------------
+// Metadata.  qbb: per block a 512-byte record [min(128) | max(128)] of bf16
+// (exact: K is bf16).  brep: per block R int32 token indices, descending
+// squared norm, lower index on ties, -1 where the block has fewer tokens.
+// Blocks [j0, j0 + grid.x) over tokens below t_end are rebuilt.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBT) void qbb_meta_kernel(const uint16_t* __restrict__ key, int kv_heads, int64_t sb,
+                                                       int64_t sh, int64_t st, int block, int t_end, int j0,
+                                                       uint16_t* __restrict__ meta, int64_t meta_blocks) {
+  const int j = j0 + blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / kv_heads, h = row - b * kv_heads;
+  const int t_lo = j * block, t_hi = min(t_end, t_lo + block);
+  const uint16_t* kb = key + b * sb + h * sh;
+  uint16_t* rec = meta + (static_cast<int64_t>(row) * meta_blocks + j) * 2 * kHD;
+  for (int c = tid; c < kHD; c += kBT) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (int t = t_lo; t < t_hi; ++t) {
+      const float v = bf16f(kb[static_cast<int64_t>(t) * st + c]);
+      mn = fminf(mn, v);
+      mx = fmaxf(mx, v);
+    }
+    rec[c] = static_cast<uint16_t>(__float_as_uint(mn) >> 16);
+    rec[kHD + c] = static_cast<uint16_t>(__float_as_uint(mx) >> 16);
+  }
+}
+
+// One wave per block (block <= 64): lane l scores token j*block + l.
+__global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restrict__ key, int kv_heads, int64_t sb,
+                                                        int64_t sh, int64_t st, int block, int reps, int t_end,
+                                                        int j0, int j_end, int32_t* __restrict__ meta,
+                                                        int64_t meta_blocks) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, row = blockIdx.y;
+  const int j = j0 + blockIdx.x * (kBT / 64) + wave;
+  if (j >= j_end) return;   // whole waves leave; no workgroup barrier below
+  const int b = row / kv_heads, h = row - b * kv_heads;
+  const int t = j * block + lane;
+  const bool ok = lane < block && t < t_end;
+  float norm = -1.0f;   // below every real norm
+  if (ok) {
+    const uint4* kr = reinterpret_cast<const uint4*>(key + b * sb + h * sh + static_cast<int64_t>(t) * st);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kHD / 8; ++c) {
+      const uint4 x = kr[c];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
+        acc = acc + lo * lo;
+        acc = acc + hi * hi;
+      }
+    }
+    norm = acc;
+  }
+  int32_t* rec = meta + (static_cast<int64_t>(row) * meta_blocks + j) * reps;
+  for (int r = 0; r < reps; ++r) {
+    // the lane with the largest (norm, -lane)
+    float bn = norm;
+    int bl = lane;
+    for (int off = 32; off > 0; off >>= 1) {
+      const float on = __shfl_xor(bn, off);
+      const int ol = __shfl_xor(bl, off);
+      if (on > bn || (on == bn && ol < bl)) {
+        bn = on;
+        bl = ol;
+      }
+    }
+    if (lane == 0) rec[r] = bn >= 0.0f ? j * block + bl : -1;
+    if (lane == bl) norm = -1.0f;   // taken
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block scores of one row: qbb bound (EV:5554) or best representative
+// (EV:5431-5435; no valid representative -> finfo(float32).min).
+// ---------------------------------------------------------------------------
+template <int KIND>   // 0: qbb, 1: brep
+__global__ __launch_bounds__(kBT) void block_scores_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, int q_heads, int group, int kv_heads,
+    int64_t sb, int64_t sh, int64_t st, const void* __restrict__ meta, int64_t meta_blocks, int reps, int nb,
+    int count, float* __restrict__ out, int64_t out_ld) {
+  __shared__ float q_s[kHD];
+  __shared__ int sel_idx[kHD];
+  __shared__ float sel_q[kHD];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / q_heads, h = row - b * q_heads;
+  const int kvrow = b * kv_heads + h / group;
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  __syncthreads();
+  rank_dims(q_s, count, sel_idx, sel_q);
+  const int j = blockIdx.x * kBT + tid;
+  if (j >= nb) return;
+  float acc;
+  if constexpr (KIND == 0) {
+    const uint16_t* rec = static_cast<const uint16_t*>(meta) + (static_cast<int64_t>(kvrow) * meta_blocks + j) * 2 * kHD;
+    acc = 0.0f;
+    for (int s = 0; s < count; ++s) {
+      const float qs = sel_q[s];
+      const int d = sel_idx[s];
+      const float e = bf16f(qs >= 0.0f ? rec[kHD + d] : rec[d]);
+      acc = acc + qs * e;
+    }
+  } else {
+    const int32_t* rec = static_cast<const int32_t*>(meta) + (static_cast<int64_t>(kvrow) * meta_blocks + j) * reps;
+    const uint16_t* kb = key + b * sb + (h / group) * sh;
+    acc = -3.40282347e38f;   // finfo(float32).min
+    for (int r = 0; r < reps; ++r) {
+      const int tok = rec[r];
+      if (tok < 0) continue;
+      const uint16_t* kr = kb + static_cast<int64_t>(tok) * st;
+      float sc = 0.0f;
+      for (int s = 0; s < count; ++s) sc = sc + sel_q[s] * bf16f(kr[sel_idx[s]]);
+      acc = fmaxf(acc, sc);
+    }
+  }
+  out[static_cast<int64_t>(row) * out_ld + j] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Partial scores of the chosen blocks' tokens (EV:5576-5581) from the
+// dim-major copy: position p of a row is token blocks[p / block] * block +
+// p % block; positions at or past the history score -inf.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBT) void scan_partial_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ kdm, int q_heads, int group, int64_t db,
+    int64_t dh, int64_t dd, const int32_t* __restrict__ blocks, int n_scan, int block, int history, int count,
+    float* __restrict__ out, int64_t out_ld) {
+  __shared__ float q_s[kHD];
+  __shared__ int sel_idx[kHD];
+  __shared__ float sel_q[kHD];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / q_heads, h = row - b * q_heads;
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  __syncthreads();
+  rank_dims(q_s, count, sel_idx, sel_q);
+  const int p = blockIdx.x * kBT + tid;
+  if (p >= n_scan * block) return;
+  const int jb = p / block;
+  const int tok = blocks[static_cast<int64_t>(row) * n_scan + jb] * block + (p - jb * block);
+  float acc = -__builtin_huge_valf();
+  if (tok >= 0 && tok < history) {
+    const uint16_t* base = kdm + b * db + (h / group) * dh + tok;
+    acc = 0.0f;
+    for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in order
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = bf16f(base[sel_idx[min(s0 + j, count - 1)] * dd]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < count) acc = acc + sel_q[s0 + j] * v[j];
+    }
+  }
+  out[static_cast<int64_t>(row) * out_ld + p] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Rerank of one row (EV:5583-5605): the n_cand best scanned tokens by partial
+// score (-inf positions never taken), their full-D scores * scaling, the
+// n_keep best of those, then the final mask over [0, key_count) (the kept
+// tokens, the first sink_end and the recent history positions, the current
+// token) and the token list for attention: kept tokens (ascending; -1 where
+// a kept token lies in a protected range or past the kept count), then the
+// sink range, the recent range and the current token.
+// ---------------------------------------------------------------------------
+template <int VPL1, int VPL2>
+__global__ __launch_bounds__(kRerankNT) void rerank_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, int q_heads, int group, int64_t sb,
+    int64_t sh, int64_t st, const float* __restrict__ partial, int64_t partial_ld, const int32_t* __restrict__ blocks,
+    int n_scan, int block, int history, int key_count, int n_cand, int n_keep, int sink_end, int recent_start,
+    int rec_begin, int n_rec, int keep_self, float scaling, uint8_t* __restrict__ keep_mask, int64_t keep_ld,
+    int32_t* __restrict__ attn_ids, int n_out) {
+  using WS1 = WideSelect<VPL1, true>;
+  using WS2 = WideSelect<VPL2, false>;
+  __shared__ union {
+    typename WS1::Shared a;
+    typename WS2::Shared b;
+  } lds;
+  __shared__ float q_s[kHD];
+  __shared__ int32_t cand[kMaxCand];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int b = row / q_heads, h = row - b * q_heads;
+  for (int d = tid; d < kHD; d += kRerankNT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  uint8_t* mrow = keep_mask + static_cast<int64_t>(row) * keep_ld;
+  for (int t = tid; t < key_count; t += kRerankNT)
+    mrow[t] = (t < sink_end) || (t >= recent_start && t < history) || (keep_self && t == history);
+
+  // 1. candidates
+  WS1 ws1;
+  ws1.load(partial + static_cast<int64_t>(row) * partial_ld, n_scan * block);
+  const int kk1 = ws1.run(n_cand, lds.a);
+  const int32_t* brow = blocks + static_cast<int64_t>(row) * n_scan;
+  ws1.place(lds.a, [&](int pos, uint32_t, int o) {
+    const int jb = pos / block;
+    cand[o] = brow[jb] * block + (pos - jb * block);
+  });
+
+  // 2. full scores of the candidates, 3. the kept ones
+  WS2 ws2;
+  const uint16_t* kb = key + b * sb + (h / group) * sh;
+#pragma unroll
+  for (int i = 0; i < VPL2; ++i) {
+    const int ci = WS2::pos(i);
+    const bool ok = ci < kk1;
+    float acc = 0.0f;
+    if (ok) {
+      const uint4* kr = reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(cand[ci]) * st);
+      uint4 x[kHD / 8];
+#pragma unroll
+      for (int c = 0; c < kHD / 8; ++c) x[c] = kr[c];
+#pragma unroll
+      for (int c = 0; c < kHD / 8; ++c) {
+        const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = acc + q_s[8 * c + 2 * e] * __uint_as_float(w[e] << 16);
+          acc = acc + q_s[8 * c + 2 * e + 1] * __uint_as_float(w[e] & 0xFFFF0000u);
+        }
+      }
+      acc = acc * scaling;
+    }
+    ws2.set(i, acc, ok);
+  }
+  const int kk2 = ws2.run(n_keep, lds.b);
+  int32_t* ids = attn_ids + static_cast<int64_t>(row) * n_out;
+  ws2.place(lds.b, [&](int ci, uint32_t, int o) {
+    const int tok = cand[ci];
+    mrow[tok] = 1;
+    const bool fv = tok >= sink_end && !(tok >= recent_start && tok < history);
+    ids[o] = fv ? tok : -1;
+  });
+  for (int o = kk2 + tid; o < n_keep; o += kRerankNT) ids[o] = -1;
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kRerankNT)
+    ids[n_keep + i] = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+}
+
+template <typename F>
+int with_scan_vpl(int64_t n, F&& f) {
+  if (n <= 16 * kRerankNT) return f(std::integral_constant<int, 16>{});
+  if (n <= 32 * kRerankNT) return f(std::integral_constant<int, 32>{});
+  return f(std::integral_constant<int, 40>{});
+}
+
+int check_rows(const char* what, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim) {
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
+    return fail(QKV_ERR_INVALID, "%s: need batch > 0 and q_heads a positive multiple of kv_heads", what);
+  if (batch * q_heads > 65535) return fail(QKV_ERR_INVALID, "%s: batch * q_heads must be <= 65535", what);
+  if (head_dim != kHD) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be 128", what);
+  return QKV_OK;
+}
+
+bool kv_aligned(const void* p, const int64_t* s) { return aligned(p, 16) && (s[0] | s[1] | s[2]) % 8 == 0; }
+
+}  // namespace
+}  // namespace qkv
+
+using namespace qkv;
+
+QKV_EXPORT int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_heads, int64_t meta_blocks,
+                                        int64_t reps) {
+  if (batch <= 0 || kv_heads <= 0 || meta_blocks <= 0) return -1;
+  if (kind == QKV_BLOCK_QBB) return batch * kv_heads * meta_blocks * 2 * kHD * 2;
+  if (kind == QKV_BLOCK_BREP && reps >= 1 && reps <= 64) return batch * kv_heads * meta_blocks * reps * 4;
+  return -1;
+}
+
+QKV_EXPORT int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, int64_t batch,
+                                     int64_t kv_heads, int64_t head_dim, int64_t block, int64_t reps, int64_t t_begin,
+                                     int64_t t_end, void* meta, int64_t meta_blocks, void* stream) {
+  const char* what = "qkv_block_meta_update";
+  if (!key || !k_strides || !meta) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (batch <= 0 || kv_heads <= 0 || batch * kv_heads > 65535 || head_dim != kHD)
+    return fail(QKV_ERR_INVALID, "%s: need batch, kv_heads > 0 and head_dim 128", what);
+  if (block <= 0 || t_begin < 0 || t_end < t_begin || cdiv(t_end, block) > meta_blocks || t_end >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need block > 0, 0 <= t_begin <= t_end, ceil(t_end/block) <= meta_blocks", what);
+  if (k_strides[3] != 1 || !kv_aligned(key, k_strides))
+    return fail(QKV_ERR_INVALID, "%s: K rows must be contiguous and 16-byte aligned", what);
+  if (t_end == t_begin) return QKV_OK;
+  const int64_t j0 = t_begin / block, j1 = cdiv(t_end, block);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* k = static_cast<const uint16_t*>(key);
+  if (kind == QKV_BLOCK_QBB) {
+    dim3 grid(static_cast<unsigned>(j1 - j0), static_cast<unsigned>(batch * kv_heads));
+    qbb_meta_kernel<<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2],
+                                          static_cast<int>(block), static_cast<int>(t_end), static_cast<int>(j0),
+                                          static_cast<uint16_t*>(meta), meta_blocks);
+  } else if (kind == QKV_BLOCK_BREP) {
+    if (block > 64 || reps < 1 || reps > block)
+      return fail(QKV_ERR_UNSUPPORTED, "%s: brep needs block <= 64 and 1 <= reps <= block", what);
+    dim3 grid(static_cast<unsigned>(cdiv(j1 - j0, kBT / 64)), static_cast<unsigned>(batch * kv_heads));
+    brep_meta_kernel<<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2],
+                                           static_cast<int>(block), static_cast<int>(reps), static_cast<int>(t_end),
+                                           static_cast<int>(j0), static_cast<int>(j1), static_cast<int32_t*>(meta),
+                                           meta_blocks);
+  } else {
+    return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
+  }
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_block_scores(int kind, const void* query, const void* key, const int64_t* k_strides,
+                                const void* meta, int64_t meta_blocks, int64_t batch, int64_t q_heads,
+                                int64_t kv_heads, int64_t history, int64_t head_dim, int64_t block, int64_t reps,
+                                int64_t dim_count, float* out, int64_t out_ld, void* stream) {
+  const char* what = "qkv_block_scores";
+  int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key || !k_strides || !meta || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t nb = block > 0 ? cdiv(history, block) : 0;
+  if (history <= 0 || block <= 0 || nb > meta_blocks || out_ld < nb || history >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need history, block > 0, ceil(history/block) <= meta_blocks and out_ld", what);
+  if (kind == QKV_BLOCK_BREP && (reps < 1 || reps > 64)) return fail(QKV_ERR_INVALID, "%s: reps in [1, 64]", what);
+  if (k_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: K channels must be contiguous", what);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
+  dim3 grid(static_cast<unsigned>(cdiv(nb, kBT)), static_cast<unsigned>(batch * q_heads));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define QKV_BLOCK_SCORES(K)                                                                                    \
+  block_scores_kernel<K><<<grid, kBT, 0, st>>>(                                                                \
+      static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),       \
+      static_cast<int>(q_heads / kv_heads), static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2], \
+      meta, meta_blocks, static_cast<int>(reps), static_cast<int>(nb), count, out, out_ld)
+  if (kind == QKV_BLOCK_QBB) QKV_BLOCK_SCORES(0);
+  else if (kind == QKV_BLOCK_BREP) QKV_BLOCK_SCORES(1);
+  else return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
+#undef QKV_BLOCK_SCORES
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                                     int64_t head_dim, const int32_t* blocks, int64_t n_scan, int64_t block,
+                                     int64_t dim_count, float* out, int64_t out_ld, void* stream) {
+  const char* what = "qkv_block_scan_scores";
+  int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !blocks || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (history <= 0 || block <= 0 || n_scan <= 0 || n_scan * block >= (int64_t(1) << 30) || out_ld < n_scan * block)
+    return fail(QKV_ERR_INVALID, "%s: need history, block, n_scan > 0 and out_ld >= n_scan * block", what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the copy's token axis must be contiguous", what);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
+  dim3 grid(static_cast<unsigned>(cdiv(n_scan * block, kBT)), static_cast<unsigned>(batch * q_heads));
+  scan_partial_kernel<<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
+      static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], blocks,
+      static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld);
+  return check_launch(what);
+}
+
+QKV_EXPORT int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t protect_sink, int64_t protect_recent,
+                                        int keep_self) {
+  if (history <= 0 || n_keep < 0) return -1;
+  const int64_t sink_end = protect_sink > 0 ? std::min(protect_sink, history) : 0;
+  const int64_t recent_start = protect_recent > 0 ? std::max<int64_t>(0, history - protect_recent) : history;
+  const int64_t rec_begin = std::max(recent_start, sink_end);
+  const int64_t n_rec = (protect_recent > 0 && rec_begin < history) ? history - rec_begin : 0;
+  return n_keep + sink_end + n_rec + (keep_self ? 1 : 0);
+}
+
+QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch,
+                                int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
+                                const float* partial, int64_t partial_ld, const int32_t* blocks, int64_t n_scan,
+                                int64_t block, int64_t n_cand, int64_t n_keep, int64_t protect_sink,
+                                int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
+                                int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream) {
+  const char* what = "qkv_block_rerank";
+  int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key || !k_strides || !partial || !blocks || !keep_mask || !attn_ids)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t history = key_count - 1;
+  if (history <= 0 || key_count >= (int64_t(1) << 31) || keep_ld < key_count)
+    return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 and keep_ld >= key_count", what);
+  if (block <= 0 || n_scan <= 0 || n_scan * block > kMaxScan || partial_ld < n_scan * block)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: at most %d scanned tokens per row (got %lld)", what, kMaxScan,
+                (long long)(n_scan * block));
+  if (n_cand < 1 || n_cand > kMaxCand || n_keep < 1 || n_keep > n_cand)
+    return fail(QKV_ERR_INVALID, "%s: need 1 <= n_keep <= n_cand <= %d", what, kMaxCand);
+  if (k_strides[3] != 1 || !kv_aligned(key, k_strides))
+    return fail(QKV_ERR_INVALID, "%s: K rows must be contiguous and 16-byte aligned", what);
+  const int64_t sink_end = protect_sink > 0 ? std::min(protect_sink, history) : 0;
+  const int64_t recent_start = protect_recent > 0 ? std::max<int64_t>(0, history - protect_recent) : history;
+  const int64_t rec_begin = std::max(recent_start, sink_end);
+  const int64_t n_rec = (protect_recent > 0 && rec_begin < history) ? history - rec_begin : 0;
+  if (n_out != n_keep + sink_end + n_rec + (keep_self ? 1 : 0))
+    return fail(QKV_ERR_INVALID, "%s: token lists hold %lld entries, the selection needs %lld", what,
+                (long long)n_out, (long long)(n_keep + sink_end + n_rec + (keep_self ? 1 : 0)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_scan_vpl(n_scan * block, [&](auto vpl) {
+    rerank_kernel<decltype(vpl)::value, kMaxCand / kRerankNT><<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
+        static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),
+        static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], partial, partial_ld, blocks,
+        static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), static_cast<int>(key_count),
+        static_cast<int>(n_cand), static_cast<int>(n_keep), static_cast<int>(sink_end),
+        static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec), keep_self ? 1 : 0,
+        scaling, keep_mask, keep_ld, attn_ids, static_cast<int>(n_out));
+    return check_launch(what);
+  });
+}

@@ -257,6 +257,12 @@ struct WideSelect {
     }
   }
 
+  // Key i from a value computed in place (ok = false: never taken).
+  __device__ void set(int i, float v, bool ok) {
+    u[i] = f32_sortable(v);
+    valid = ok ? (valid | (1ull << i)) : (valid & ~(1ull << i));
+  }
+
   __device__ bool on(int i) const { return (valid >> i) & 1ull; }
 
   // Marks the validity bits as changed here, so each phase derives its

@@ -1,0 +1,122 @@
+"""GPU parity of the block-metadata selectors (qbb, brep) against the oracle,
+which the reference's own drivers pin (tests/test_oracle_block.py): metadata,
+block scores and final masks bit-exact; attention within 1e-2 / 2e-2."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import _lib
+from kv_cache_amd import blocksel as BS
+from oracle import ref_semantics as R
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def _kv(b, hkv, t, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn((b, hkv, t, 128), generator=g) * 1.5).to(torch.bfloat16)
+    v = torch.randn((b, hkv, t, 128), generator=g).to(torch.bfloat16)
+    return k, v, g
+
+
+@pytest.mark.parametrize("block,t", [(16, 1000), (8, 333), (64, 700), (1, 50)])
+def test_qbb_metadata_and_bounds(block, t):
+    lib = _lib.load()
+    k, _, g = _kv(2, 2, t, block + t)
+    q = torch.randn((2, 4, 128), generator=g).to(torch.bfloat16)
+    kd, qd = k.to(DEV), q.to(DEV)
+    mb = -(-t // block) + 3
+    meta = torch.zeros(lib.qkv_block_meta_bytes(BS.QBB, 2, 2, mb, 1), dtype=torch.uint8, device=DEV)
+    ks = _lib.strides(*kd.stride())
+    # built in two pieces: the second rebuilds the block the first ended inside
+    for t0, t1 in ((0, t // 2 + 1), (t // 2 + 1, t)):
+        _lib.check(lib.qkv_block_meta_update(BS.QBB, kd.data_ptr(), ks, 2, 2, 128, block, 1, t0, t1,
+                                             meta.data_ptr(), mb, _lib.stream_of(kd)))
+    rec = meta.view(torch.int16).view(2, 2, mb, 2, 128)[:, :, : -(-t // block)]
+    lo, hi = R.block_minmax(f32(k), block)
+    assert np.array_equal(f32(rec[:, :, :, 0].view(torch.bfloat16)), lo)
+    assert np.array_equal(f32(rec[:, :, :, 1].view(torch.bfloat16)), hi)
+    nb = -(-t // block)
+    out = torch.empty((8, nb + 5), dtype=torch.float32, device=DEV)
+    _lib.check(lib.qkv_block_scores(BS.QBB, qd.data_ptr(), kd.data_ptr(), ks, meta.data_ptr(), mb, 2, 4, 2, t, 128,
+                                    block, 1, 8, out.data_ptr(), nb + 5, _lib.stream_of(kd)))
+    want = R.qbb_block_bounds(f32(q), np.repeat(lo, 2, axis=1), np.repeat(hi, 2, axis=1), 8)
+    assert np.array_equal(out[:, :nb].cpu().numpy().reshape(2, 4, nb), want)
+
+
+@pytest.mark.parametrize("block,reps,t", [(16, 2, 1000), (8, 1, 333), (64, 5, 700), (16, 16, 40)])
+def test_brep_metadata_and_scores(block, reps, t):
+    lib = _lib.load()
+    k, _, g = _kv(1, 2, t, block * reps + t)
+    k[0, 0, 3] = k[0, 0, 5]          # equal norms: the lower index first
+    q = torch.randn((1, 8, 128), generator=g).to(torch.bfloat16)
+    kd, qd = k.to(DEV), q.to(DEV)
+    mb = -(-t // block)
+    meta = torch.zeros(lib.qkv_block_meta_bytes(BS.BREP, 1, 2, mb, reps), dtype=torch.uint8, device=DEV)
+    ks = _lib.strides(*kd.stride())
+    for t0, t1 in ((0, 1), (1, t - 7), (t - 7, t)):
+        _lib.check(lib.qkv_block_meta_update(BS.BREP, kd.data_ptr(), ks, 1, 2, 128, block, reps, t0, t1,
+                                             meta.data_ptr(), mb, _lib.stream_of(kd)))
+    got = meta.view(torch.int32).view(1, 2, mb, reps).cpu().numpy()
+    idx, valid = R.block_representatives(f32(k), block, reps)
+    assert np.array_equal(np.where(valid, idx, -1), got)
+    out = torch.empty((8, mb), dtype=torch.float32, device=DEV)
+    _lib.check(lib.qkv_block_scores(BS.BREP, qd.data_ptr(), kd.data_ptr(), ks, meta.data_ptr(), mb, 1, 8, 2, t, 128,
+                                    block, reps, 16, out.data_ptr(), mb, _lib.stream_of(kd)))
+    kx = np.repeat(f32(k), 4, axis=1)
+    want = R.brep_block_scores(f32(q), kx, np.repeat(idx, 4, axis=1), np.repeat(valid, 4, axis=1), 16)
+    assert np.array_equal(out.cpu().numpy().reshape(1, 8, mb), want)
+
+
+@pytest.mark.parametrize("mode,hq,hkv,t,steps,sink,recent,keep_self", [
+    ("qbb16q8s12cand4", 8, 2, 3000, 3, 3, 5, True),
+    ("qbb8q16s25cand6p25", 4, 4, 1500, 2, 0, 0, False),
+    ("qbb32q8s6p25cand2", 32, 8, 9000, 2, 4, 8, True),
+    ("brep16r2q8s12cand4", 8, 2, 3000, 3, 3, 5, True),
+    ("brep8r1q16s25cand6p25", 4, 1, 1200, 2, 0, 4, True),
+    ("brep16r4q8s6p25cand2", 32, 8, 9000, 2, 4, 8, True),
+])
+def test_step_matches_oracle(mode, hq, hkv, t, steps, sink, recent, keep_self):
+    kind, block, reps, dims, scan, cand = BS.parse_block_mode(mode)
+    k, v, g = _kv(1, hkv, t + steps, hq * t)
+    qs = torch.randn((steps, 1, hq, 128), generator=g).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = BS.BlockSelectDecodeStep(mode, 1, hq, hkv, 128, t + steps + 40, top_fraction=0.02, protect_sink=sink,
+                                    protect_recent=recent, keep_self=keep_self)
+    step.prefill(kd[:, :, : t - 3])
+    for s in range(steps):
+        n = t + s + 1
+        out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        want, keep = R.block_select_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), "qbb" if kind == BS.QBB
+                                         else "brep", block, dims, scan, cand, 0.02, 128 ** -0.5, sink, recent,
+                                         keep_self, reps)
+        assert np.array_equal(step.final_mask().cpu().numpy(), keep), (mode, s)
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+
+
+def test_new_sequence_resets():
+    k, v, g = _kv(1, 2, 800, 3)
+    q = torch.randn((1, 4, 128), generator=g).to(torch.bfloat16).to(DEV)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = BS.BlockSelectDecodeStep("qbb16q8s12cand4", 1, 4, 2, 128, 1024)
+    step(q, kd[:, :, :700], vd[:, :, :700], 0.1)
+    a = step(q, kd[:, :, :400], vd[:, :, :400], 0.1).clone()
+    fresh = BS.BlockSelectDecodeStep("qbb16q8s12cand4", 1, 4, 2, 128, 1024)
+    assert torch.equal(a, fresh(q, kd[:, :, :400], vd[:, :, :400], 0.1))
+    assert torch.equal(step.final_mask(), fresh.final_mask())
+
+
+def test_limits_are_errors():
+    with pytest.raises(RuntimeError, match="at most 40960"):
+        BS.BlockSelectDecodeStep("qbb16q8s50cand4", 1, 4, 2, 128, 100000)
+    with pytest.raises(RuntimeError, match="at most 4096"):
+        BS.BlockSelectDecodeStep("qbb16q8s50cand20", 1, 4, 2, 128, 40000)
+    with pytest.raises(RuntimeError, match="at most 64"):
+        BS.BlockSelectDecodeStep("brep128r2q8s6cand2", 1, 4, 2, 128, 4000)
