@@ -20,14 +20,17 @@ rotating per-layer buffers; value = (query head, visible key) pairs scored
 per second; "roofline" is the MFMA scoring kernel's algorithmic int8 ops
 per second against the 5.0 POP/s dense int8 peak.
 
-reuse (candidate reuse + exact rerank, kv_cache_amd.reuse): a step is one decode
-token through 8 layers of the qabs8cand5reuse step at Qwen3-8B heads and history
-32768; value = history tokens x KV heads x layers per second.
+reuse (candidate reuse + exact rerank, kv_cache_amd.reuse) and qbb / brep
+(block-metadata selectors, kv_cache_amd.blocksel): a step is one decode token
+through 8 layers of the qabs8cand5reuse / qbb64q8s3cand3 / brep64r4q8s3cand3
+step at Qwen3-8B heads and history 32768; value = history tokens x KV heads x
+layers per second.
 
 "cpu_baseline" is timed on the host cores on a bounded sample: for decode
 the reference's PyTorch op sequence (restated in oracle/ref_semantics.py),
 for prefill the numpy restatement of the scoring (oracle/qkv_oracle.py), for
-reuse the reference's reuse op sequence (oracle/ref_semantics.py).
+reuse / qbb / brep the reference's op sequence of that mode
+(oracle/ref_semantics.py).
 Prints ONE JSON line (the driver contract).
 """
 
@@ -55,7 +58,7 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse"])
+    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse", "qbb", "brep"])
     p.add_argument("--layers", type=int, default=None,
                    help="layer buffers to rotate through (default: the config's layer count, at least 8)")
     p.add_argument("--kernel-reps", type=int, default=20, help="graph replays for per-kernel timing")
@@ -174,6 +177,8 @@ def main() -> int:
         line = run_prefill(args)
     elif args.config == "reuse":
         line = run_reuse(args)
+    elif args.config in ("qbb", "brep"):
+        line = run_blocksel(args)
     else:
         line = run_decode(args)
     print(json.dumps(line), flush=True)
@@ -713,6 +718,221 @@ def run_reuse(args) -> dict:
             "bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": kernels[dom]["gbs"] / HBM_PEAK_GBS, "traffic": read_traffic("reuse", dom),
         },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+
+
+# Block-metadata selector workloads (Qwen3-8B heads, one sequence, 32768
+# history tokens): the reference's own qbb mode string, and brep at the same
+# block size, scan and candidate fractions.
+BLOCKSEL = {"qbb": "qbb64q8s3cand3", "brep": "brep64r4q8s3cand3"}
+
+
+def cpu_baseline_blocksel(mode: str, budget_s: float, steps: int = 3) -> dict:
+    """The reference's qbb / brep op sequence (oracle/ref_semantics.py
+    block_select_step_cpu) for consecutive decode steps of one layer."""
+    import torch
+
+    from kv_cache_amd.blocksel import BREP, parse_block_mode
+    from oracle import ref_semantics as R
+
+    c = REUSE
+    kind, block, reps, dims, scan, cand = parse_block_mode(mode)
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    t = c["history"] + steps + 1
+    k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    for s in range(steps):
+        n = c["history"] + s + 1
+        q = torch.randn((1, c["q_heads"], 1, c["head_dim"]), generator=g).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        R.block_select_step_cpu(q, k[:, :, :n], v[:, :, :n], "brep" if kind == BREP else "qbb", block, dims, scan,
+                                cand, c["top_fraction"], c["head_dim"] ** -0.5, c["sink"], c["recent"], True, reps)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
+    med = statistics.median(times[1:] if len(times) > 1 else times)
+    keys = c["kv_heads"] * c["history"]
+    return {
+        "value": keys / med,
+        "unit": "keys/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} decode steps of one layer ({mode}, {c['q_heads']}/{c['kv_heads']} heads, history "
+                   f"{c['history']}): the reference's op sequence on CPU tensors; median of the steps after the "
+                   f"first = {med * 1e3:.1f} ms per layer-step"),
+    }
+
+
+def run_blocksel(args) -> dict:
+    """Decode steps of a block-metadata selector (kv_cache_amd.blocksel) over
+    8 layers with their own K/V, metadata and dim-major copy; the history
+    grows one token per step.  Timed eagerly, as a graph of one
+    fixed-history step, and per kernel."""
+    import torch
+
+    from kv_cache_amd import _lib
+    from kv_cache_amd import blocksel as BS
+    from kv_cache_amd.int4 import block_topk
+    from kv_cache_amd.reuse import token_attention
+
+    c = REUSE
+    mode = BLOCKSEL[args.config]
+    layers = args.layers or 8
+    b, hq, hkv, d, t0 = c["batch"], c["q_heads"], c["kv_heads"], c["head_dim"], c["history"]
+    cap = -(-(t0 + args.warmup + args.steps + 2) // 64) * 64
+    scaling = d ** -0.5
+    log(f"[bench] setup {mode}: {layers} layers, Qwen3-8B heads, history {t0}, top {c['top_fraction']}, "
+        f"sink/recent {c['sink']}/{c['recent']}")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ks, vs, qs, steps = [], [], [], []
+    for _ in range(layers):
+        k = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        st = BS.BlockSelectDecodeStep(mode, b, hq, hkv, d, cap, top_fraction=c["top_fraction"],
+                                      protect_sink=c["sink"], protect_recent=c["recent"])
+        st.prefill(k[:, :, :t0])
+        ks.append(k)
+        vs.append(v)
+        qs.append(torch.randn((b, hq, d), generator=g, device="cuda").to(torch.bfloat16))
+        steps.append(st)
+    torch.cuda.synchronize()
+    hist = t0
+
+    def decode_step():
+        nonlocal hist
+        for layer in range(layers):
+            steps[layer](qs[layer], ks[layer][:, :, : hist + 1], vs[layer][:, :, : hist + 1], scaling)
+        hist += 1
+
+    for _ in range(args.warmup):
+        decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    log(f"[bench] eager step: {ms_per_step:.3f} ms ({ms_per_step * 1e3 / layers:.1f} us/layer)")
+
+    hf = hist - 1
+    kc = hf + 1
+    nb, n_scan, n_cand, n_keep = BS.step_counts(hf, steps[0].block, steps[0].scan, steps[0].cand, c["top_fraction"])
+    lib = _lib.load()
+    reps = max(1, -(-16 // layers))
+
+    def repeated(fn):
+        def run():
+            for _ in range(reps):
+                fn()
+        return run
+
+    def run_fixed():
+        for layer in range(layers):
+            steps[layer].launch(qs[layer], ks[layer][:, :, :kc], vs[layer][:, :, :kc], scaling)
+
+    gr = graph_of(repeated(run_fixed))
+    ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
+    del gr
+    log(f"[bench] graph step (history {hf}): {ms_graph * 1e3 / layers:.1f} us/layer")
+    rows = b * hq
+    n_tok = n_scan * steps[0].block
+    n_out = steps[0].n_out
+
+    def run_scores():
+        for layer in range(layers):
+            st, k = steps[layer], ks[layer][:, :, :kc]
+            _lib.check(lib.qkv_block_scores(st.kind, qs[layer].data_ptr(), k.data_ptr(), _lib.strides(*k.stride()),
+                                            st.meta.data_ptr(), st.meta_blocks, b, hq, hkv, hf, d, st.block,
+                                            st.reps, st.dims, st.bscore.data_ptr(), st.meta_blocks,
+                                            _lib.stream_of(k)))
+
+    def run_topk():
+        for layer in range(layers):
+            st = steps[layer]
+            block_topk(st.bscore[:, :nb], n_scan, out=st.blocks[: rows * n_scan].view(rows, n_scan),
+                       workspace=st.topk_ws)
+
+    def run_scan():
+        for layer in range(layers):
+            st = steps[layer]
+            _lib.check(lib.qkv_block_scan_scores(qs[layer].data_ptr(), st.kdm.data_ptr(),
+                                                 _lib.strides(*st.kdm.stride()), b, hq, hkv, hf, d,
+                                                 st.blocks.data_ptr(), n_scan, st.block, st.dims,
+                                                 st.partial.data_ptr(), n_tok, _lib.stream_of(qs[layer])))
+
+    def run_rerank():
+        for layer in range(layers):
+            st, k = steps[layer], ks[layer][:, :, :kc]
+            _lib.check(lib.qkv_block_rerank(qs[layer].data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), b, hq, hkv,
+                                            kc, d, st.partial.data_ptr(), n_tok, st.blocks.data_ptr(), n_scan,
+                                            st.block, n_cand, n_keep, c["sink"], c["recent"], 1, scaling,
+                                            st.keep.data_ptr(), st.capacity, st.attn_ids.data_ptr(), n_out,
+                                            _lib.stream_of(k)))
+
+    def run_attn():
+        for layer in range(layers):
+            st = steps[layer]
+            token_attention(qs[layer], ks[layer][:, :, :kc], vs[layer][:, :, :kc],
+                            st.attn_ids[: rows * n_out].view(rows, n_out), scaling, workspace=st.attn_ws, out=st.out)
+
+    meta_bytes = {BS.QBB: 2 * 2 * d, BS.BREP: 4 * steps[0].reps}[steps[0].kind]   # per block, per KV head
+    plan = [
+        # a block's metadata record per query head, plus the f32 score written
+        ("block_scores", run_scores, rows * nb * (meta_bytes + 4)),
+        ("block_topk", run_topk, rows * nb * 4),
+        # the S dims of every scanned token (dim-major) and its f32 partial score
+        ("scan_partial", run_scan, rows * n_tok * (steps[0].dims * 2 + 4)),
+        # partial scores read once, the candidates' bf16 K rows, the final mask bytes
+        ("rerank", run_rerank, rows * (n_tok * 4 + n_cand * d * 2 + kc)),
+        ("token_attention", run_attn, rows * n_out * d * 2 * 2),
+    ]
+    kernels = {}
+    for name, fn, nbytes in plan:
+        gk = graph_of(repeated(fn))
+        ms = time_replays(gk.replay, args.kernel_reps) / (layers * reps)
+        kernels[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                         "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
+        del gk
+    for _ in range(args.profile_steps):
+        run_fixed()
+    torch.cuda.synchronize()
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline_blocksel(mode, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
+    dom = max(kernels, key=lambda n: kernels[n]["us_per_launch"])
+    return {
+        "metric": f"{mode} decode: keys/s (history tokens x KV heads) through the block selector step; us/layer",
+        "value": layers * b * hkv * hf / (ms_per_step * 1e-3),
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 -> f32 scores and attention",
+        "data": "synthetic (seeded N(0,1) K/V/q)",
+        "config": {"workload": f"{args.config}: {mode}, Qwen3-8B heads, history {t0}", "batch": b, "q_heads": hq,
+                   "kv_heads": hkv, "head_dim": d, "history": t0, "layers": layers, "mode": mode,
+                   "top_fraction": c["top_fraction"], "sink": c["sink"], "recent": c["recent"], "graph": False,
+                   "scanned_tokens": n_tok, "candidates": n_cand, "kept": n_keep},
+        "us_per_layer": ms_per_step * 1e3 / layers,
+        "graph_us_per_layer": ms_graph * 1e3 / layers,
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": kernels[dom]["gbs"] / HBM_PEAK_GBS,
+                     "traffic": read_traffic(args.config, dom)},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

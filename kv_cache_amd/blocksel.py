@@ -136,7 +136,6 @@ class BlockSelectDecodeStep:
     def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
         """query bf16 [B, Hq, 128]; key/value bf16 [B, Hkv, T, 128], the
         current token last.  Returns bf16 [B, Hq, 128]."""
-        lib = _lib.load()
         key_count = key.size(2)
         _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
         _require(query.dtype == key.dtype == value.dtype == torch.bfloat16, "block selectors take bf16 q/K/V")
@@ -151,6 +150,16 @@ class BlockSelectDecodeStep:
             self.reset()
         self._sync_cache(key, history)
         self.last_history = history
+        return self.launch(query, key, value, scaling)
+
+    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
+        """The step's selection and attention kernels at the history
+        key.size(2) - 1, with the metadata and the dim-major copy already
+        holding it (``__call__`` brings them up to date first)."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        history = key_count - 1
+        _require(self.meta_len >= history and self.kdm_len >= history, "block metadata does not hold the history")
         q = query.contiguous()
         nb, n_scan, n_cand, n_keep = step_counts(history, self.block, self.scan, self.cand, self.top_fraction)
         stream = _lib.stream_of(q)

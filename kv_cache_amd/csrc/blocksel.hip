@@ -300,11 +300,24 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     ids[n_keep + i] = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
 }
 
+// Keys per thread for rows of n scanned tokens / n candidates: the fewest
+// that hold the row, so short rows run short loops.
 template <typename F>
 int with_scan_vpl(int64_t n, F&& f) {
+  if (n <= kRerankNT) return f(std::integral_constant<int, 1>{});
+  if (n <= 2 * kRerankNT) return f(std::integral_constant<int, 2>{});
+  if (n <= 4 * kRerankNT) return f(std::integral_constant<int, 4>{});
+  if (n <= 8 * kRerankNT) return f(std::integral_constant<int, 8>{});
   if (n <= 16 * kRerankNT) return f(std::integral_constant<int, 16>{});
   if (n <= 32 * kRerankNT) return f(std::integral_constant<int, 32>{});
   return f(std::integral_constant<int, 40>{});
+}
+
+template <typename F>
+int with_cand_vpl(int64_t n, F&& f) {
+  if (n <= kRerankNT) return f(std::integral_constant<int, 1>{});
+  if (n <= 2 * kRerankNT) return f(std::integral_constant<int, 2>{});
+  return f(std::integral_constant<int, 4>{});
 }
 
 int check_rows(const char* what, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim) {
@@ -452,7 +465,8 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
                 (long long)n_out, (long long)(n_keep + sink_end + n_rec + (keep_self ? 1 : 0)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_scan_vpl(n_scan * block, [&](auto vpl) {
-    rerank_kernel<decltype(vpl)::value, kMaxCand / kRerankNT><<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
+   return with_cand_vpl(n_cand, [&](auto vpl2) {
+    rerank_kernel<decltype(vpl)::value, decltype(vpl2)::value><<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
         static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),
         static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], partial, partial_ld, blocks,
         static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), static_cast<int>(key_count),
@@ -460,5 +474,6 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
         static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec), keep_self ? 1 : 0,
         scaling, keep_mask, keep_ld, attn_ids, static_cast<int>(n_out));
     return check_launch(what);
+   });
   });
 }

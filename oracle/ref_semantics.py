@@ -572,3 +572,90 @@ def block_select_step(query, key, value, kind: str, block: int, dim_count: int, 
     idx = np.broadcast_to(np.arange(key_count), final_keep.shape)
     out = final_attention(q, kx, vx, idx, final_keep, scaling)
     return out, final_keep
+
+
+def block_select_step_cpu(query_states, key_states, value_states, kind: str, block: int, dim_count: int,
+                          scan_fraction: float, candidate_fraction: float, top_fraction: float, scaling: float,
+                          sink: int = 0, recent: int = 0, keep_self: bool = True, reps: int = 1):
+    """One qbb (EV:5516-5617) or brep (EV:5369-5505, representatives as
+    BlockRepState computes them, EV:1899-1913) decode step in the
+    reference's PyTorch ops on CPU tensors: the CPU baseline ``bench.py``
+    times next to the GPU block selectors.  query_states [B,Hq,1,D];
+    key/value_states [B,Hkv,T,D] (GQA-expanded first, EV:6248-6251).
+    Returns (out [B,1,Hq,D], final_keep bool [B,Hq,T])."""
+    import torch
+    import torch.nn.functional as F
+
+    b, hq, _, d = query_states.shape
+    if key_states.shape[1] != hq:
+        rep = hq // key_states.shape[1]
+        key_states = key_states.repeat_interleave(rep, dim=1)
+        value_states = value_states.repeat_interleave(rep, dim=1)
+    key_count = key_states.shape[-2]
+    history = key_count - 1
+    sdims = min(max(1, dim_count), d)
+    q = query_states[:, :, 0, :].float()
+    qdims = torch.topk(q.abs(), k=sdims, dim=-1, largest=True).indices
+    q_sel = torch.gather(q, dim=-1, index=qdims)
+    k_hist = key_states[:, :, :history, :]
+    nb = math.ceil(history / block)
+    padded = nb * block
+    k_blocks = F.pad(k_hist.float(), (0, 0, 0, padded - history), value=0.0) if padded != history else k_hist.float()
+    valid_b = torch.zeros((b, hq, padded), dtype=torch.bool)
+    valid_b[:, :, :history] = True
+    block_k = k_blocks.view(b, hq, nb, block, d)
+    block_valid = valid_b.view(b, hq, nb, block)
+    if kind == "qbb":
+        gidx = qdims[:, :, None, None, :].expand(-1, -1, nb, block, -1)
+        sel = torch.gather(block_k, dim=-1, index=gidx)
+        smax = sel.masked_fill(~block_valid[..., None], -torch.inf).amax(dim=3)
+        smin = sel.masked_fill(~block_valid[..., None], torch.inf).amin(dim=3)
+        qb = q_sel[:, :, None, :]
+        bscore = torch.where(qb >= 0, qb * smax, qb * smin).sum(dim=-1)
+    else:
+        r = min(reps, block)
+        norms = block_k.square().sum(dim=-1).masked_fill(~block_valid, -torch.inf)
+        _, rpos = torch.topk(norms, k=r, dim=-1, largest=True)
+        rkeys = torch.gather(block_k, dim=3, index=rpos[..., None].expand(-1, -1, -1, -1, d))
+        rvalid = torch.gather(block_valid, dim=3, index=rpos)
+        rsel = torch.gather(rkeys, dim=-1, index=qdims[:, :, None, None, :].expand(-1, -1, nb, r, -1))
+        rsc = (rsel * q_sel[:, :, None, None, :]).sum(dim=-1).masked_fill(~rvalid, torch.finfo(torch.float32).min)
+        bscore = rsc.amax(dim=-1)
+    n_scan = min(nb, max(1, math.ceil(scan_fraction * history / block)))
+    _, blocks = torch.topk(bscore, k=n_scan, dim=-1, largest=True)
+    tok = (blocks[..., None] * block + torch.arange(block)).reshape(b, hq, -1)
+    tvalid = tok < history
+    tok = tok.clamp_max(history - 1)
+    skeys = torch.gather(k_hist, dim=2, index=tok[..., None].expand(-1, -1, -1, d))
+    ssel = torch.gather(skeys.float(), dim=-1, index=qdims[:, :, None, :].expand(-1, -1, tok.shape[-1], -1))
+    part = (ssel * q_sel[:, :, None, :]).sum(dim=-1).masked_fill(~tvalid, torch.finfo(torch.float32).min)
+    req = min(tok.shape[-1], max(1, math.ceil(candidate_fraction * history)))
+    _, cpos = torch.topk(part, k=req, dim=-1, largest=True)
+    ctok = torch.gather(tok, dim=-1, index=cpos)
+    cvalid = torch.gather(tvalid, dim=-1, index=cpos)
+    ckeys = torch.gather(k_hist, dim=2, index=ctok[..., None].expand(-1, -1, -1, d))
+    cs = torch.matmul(query_states[:, :, 0:1, :], ckeys.transpose(2, 3)).squeeze(2) * scaling
+    cs = cs.masked_fill(~cvalid, torch.finfo(cs.dtype).min)
+    keep_n = min(cs.shape[-1], max(1, math.ceil(top_fraction * history)))
+    _, kpos = torch.topk(cs, k=keep_n, dim=-1, largest=True)
+    final_keep = torch.zeros((b, hq, key_count), dtype=torch.bool)
+    final_keep[:, :, :history].scatter_(dim=-1, index=torch.gather(ctok, -1, kpos), src=torch.gather(cvalid, -1, kpos))
+    if sink > 0:
+        final_keep[:, :, : min(sink, history)] = True
+    if recent > 0:
+        final_keep[:, :, max(0, history - recent):history] = True
+    if keep_self:
+        final_keep[:, :, history] = True
+    # gather attention over the mask (EV:5607-5617, via _indices_from_keep_mask)
+    width = int(final_keep.sum(dim=-1).max().item())
+    pos = torch.arange(key_count).view(1, 1, -1).expand_as(final_keep)
+    fidx = torch.topk(torch.where(final_keep, pos, torch.full_like(pos, -1)), k=width, dim=-1).values
+    fvalid = fidx >= 0
+    fidx = fidx.clamp_min(0)
+    g = fidx[..., None].expand(-1, -1, -1, d)
+    sk, sv = torch.gather(key_states, 2, g), torch.gather(value_states, 2, g)
+    att = torch.matmul(query_states[:, :, 0:1, :], sk.transpose(2, 3)).squeeze(2) * scaling
+    att = att.masked_fill(~fvalid, torch.finfo(att.dtype).min)
+    w = F.softmax(att, dim=-1, dtype=torch.float32).to(query_states.dtype)
+    out = torch.sum(w[:, :, :, None] * sv, dim=2)
+    return out[:, None, :, :].contiguous(), final_keep

@@ -82,6 +82,8 @@ def test_brep_metadata_and_scores(block, reps, t):
     ("brep16r2q8s12cand4", 8, 2, 3000, 3, 3, 5, True),
     ("brep8r1q16s25cand6p25", 4, 1, 1200, 2, 0, 4, True),
     ("brep16r4q8s6p25cand2", 32, 8, 9000, 2, 4, 8, True),
+    ("qbb16q8s40cand10", 8, 2, 20000, 1, 2, 2, True),          # 8000 scanned tokens, 2000 candidates
+    ("brep32r2q8s90cand11", 4, 1, 36000, 1, 0, 0, True),       # 32400 scanned, 3960 candidates
 ])
 def test_step_matches_oracle(mode, hq, hkv, t, steps, sink, recent, keep_self):
     kind, block, reps, dims, scan, cand = BS.parse_block_mode(mode)

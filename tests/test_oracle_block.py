@@ -103,3 +103,20 @@ def test_brep_score_is_max_over_representatives():
         for j in range(3):
             reps = idx[0, h, j][valid[0, h, j]]
             assert sc[0, h, j] == part[0, h, reps].max()
+
+
+@pytest.mark.parametrize("name", BLOCK_SCENARIOS)
+def test_cpu_baseline_op_sequence_matches_reference_vectors(name):
+    # the torch op sequence bench.py times as the block-selector CPU baseline
+    import torch
+
+    g = load_block_golden(name)
+    k, v = torch.from_numpy(g["k"]), torch.from_numpy(g["v"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s])[:, :, None, :]
+        out, keep = R.block_select_step_cpu(q, k[:, :, :n], v[:, :, :n], g["kind"], g["block"], g["dims"], g["scan"],
+                                            g["cand"], g["top_fraction"], g["scaling"], g["sink"], g["recent"],
+                                            g["keep_self"], g["reps"])
+        assert np.array_equal(keep.numpy(), g["final"][s][..., :n]), (name, s)
+        np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], rtol=1e-5, atol=1e-6)
