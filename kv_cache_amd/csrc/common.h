@@ -142,6 +142,37 @@ __device__ __forceinline__ float max_x32(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Maximum of two lane-swap results that are never NaN, as one v_med3_f32
+// against +inf: fmaxf would first quiet each operand (the compiler cannot
+// tell that a swapped value is no signalling NaN), two more instructions.
+// The +inf comes from a scalar move the compiler cannot see through;
+// against a visible constant it rewrites the median back into fmaxf.
+__device__ __forceinline__ float max_swapped(uint32_t a, uint32_t b) {
+  float pinf;
+  asm("s_mov_b32 %0, 0x7f800000" : "=s"(pinf));
+  return __builtin_amdgcn_fmed3f(__uint_as_float(a), __uint_as_float(b), pinf);
+}
+// Four maxima over the wave's 4 rows (lanes 16r..16r+15) at once: row r of
+// the result holds, lane by lane, the maximum of x_r over the 4 rows.
+// v_permlane16_swap(x0, x1) leaves (x0.0, x1.0, x0.2, x1.2) and
+// (x0.1, x1.1, x0.3, x1.3), whose maximum is (x0.01, x1.01, x0.23, x1.23);
+// v_permlane32_swap of that and the same for x2, x3 pairs the halves.
+__device__ __forceinline__ float max_rows4(float x0, float x1, float x2, float x3) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x2), __float_as_uint(x3), false, false);
+  const float ma = max_swapped(a[0], a[1]), mb = max_swapped(b[0], b[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(ma), __float_as_uint(mb), false, false);
+  return max_swapped(c[0], c[1]);
+}
+// Two maxima over the 4 rows: rows 0 and 2 of the result hold x0's, rows 1
+// and 3 x1's.
+__device__ __forceinline__ float max_rows2(float x0, float x1) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x0), __float_as_uint(x1), false, false);
+  const float ma = max_swapped(a[0], a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(ma), __float_as_uint(ma), false, false);
+  return max_swapped(c[0], c[1]);
+}
+
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v) {
   int lane = __lane_id();

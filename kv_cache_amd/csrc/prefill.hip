@@ -30,9 +30,22 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
 constexpr int kBlock = 64;          // keys per selection block
-constexpr int kChunkBlocks = 32;    // blocks per workgroup key chunk
-constexpr int kQTile = 64;          // queries per wave (4 MFMA column tiles)
-constexpr int kNT = 4;              // 16-query column tiles per wave
+#ifndef QKV_PF_NT
+#define QKV_PF_NT 6
+#endif
+#ifndef QKV_PF_CHUNK
+#define QKV_PF_CHUNK 32
+#endif
+#ifndef QKV_PF_WG_PER_CU
+#define QKV_PF_WG_PER_CU 2
+#endif
+#ifndef QKV_PF_INTERLEAVE
+#define QKV_PF_INTERLEAVE 0
+#endif
+constexpr int kNT = QKV_PF_NT;              // 16-query column tiles per wave
+constexpr int kQTile = 16 * kNT;            // queries per wave
+constexpr int kChunkBlocks = QKV_PF_CHUNK;  // blocks per workgroup key chunk
+static_assert(kNT % 2 == 0, "the block-end reduction pairs the query tiles");
 
 // Byte position, within a permuted query row, of channel c.
 __host__ __device__ constexpr int perm_slot(int c) {
@@ -92,12 +105,14 @@ __device__ __forceinline__ v4i unpack_half(uint32_t w0, uint32_t w1) {
 // times 1/16.  Only blocks on the causal diagonal or past the last token take the
 // masked epilogue (a wave-uniform branch).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 3) void prefill_scores_kernel(
+__global__ __launch_bounds__(256, QKV_PF_WG_PER_CU) void prefill_scores_kernel(
     const int8_t* __restrict__ q8, const uint8_t* __restrict__ kpacked, const uint16_t* __restrict__ kscales,
     int q_heads, int kv_heads, int nq, int tokens, int64_t capacity, int q_pos0, int nb,
     float* __restrict__ bmax) {
   __shared__ float tile[4][kQTile][kChunkBlocks + 1];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform: read it into a scalar register, so that the
+  // query tile, the visible block count and the block offsets are scalar too.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = q_heads / kv_heads;
   const int n_qtiles = (nq + kQTile - 1) / kQTile;
   const int combo = blockIdx.y * 4 + wave;
@@ -137,13 +152,22 @@ __global__ __launch_bounds__(256, 3) void prefill_scores_kernel(
 
   // Lane l loads key (base + 16kt + l%16), channels 32g..32g+31, and the
   // scales of the 4 keys its output rows hold (base + 16kt + 4g + i).  Every
-  // block below nb lies inside the capacity (a multiple of 64).
+  // block below nb lies inside the capacity (a multiple of 64).  Buffer
+  // loads over the chunk: a per-lane constant offset plus the block's scalar
+  // offset, so no per-load address arithmetic on the VALU.
+  const int64_t key0 = static_cast<int64_t>(blk0) * kBlock;
+  const auto krsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(krow + key0 * (kD / 2)), 0,
+                                                       nblk * kBlock * (kD / 2), 0x00020000);
+  const auto srsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(srow + key0), 0, nblk * kBlock * 2,
+                                                       0x00020000);
+  const int kvoff = col * (kD / 2) + g * 16, svoff = 8 * g;
   auto load_block = [&](int kb, uint4 (&ka)[4], uint2 (&ks)[4]) {
-    const int base = (blk0 + kb) * kBlock;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      ka[kt] = *reinterpret_cast<const uint4*>(krow + static_cast<int64_t>(base + kt * 16 + col) * (kD / 2) + g * 16);
-      ks[kt] = *reinterpret_cast<const uint2*>(srow + base + kt * 16 + 4 * g);
+      const auto a = __builtin_amdgcn_raw_buffer_load_b128(krsrc, kvoff + kt * 16 * (kD / 2), kb * kBlock * (kD / 2), 0);
+      const auto s = __builtin_amdgcn_raw_buffer_load_b64(srsrc, svoff + kt * 32, kb * kBlock * 2, 0);
+      ka[kt] = uint4{a[0], a[1], a[2], a[3]};
+      ks[kt] = uint2{s[0], s[1]};
     }
   };
 
@@ -156,79 +180,108 @@ __global__ __launch_bounds__(256, 3) void prefill_scores_kernel(
   // of the exact product, i.e. 16 times fp32(s) * fp32(I), with no integer
   // conversion (-12582912 * s is exact: s has 11 significant bits).
   const v4i kBias = v4i{0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
+  // MFMAs of one half block (key tiles 2h, 2h+1) into acc.
+  auto mfma_half = [&](int half, const uint4 (&ka)[4], v4i (&acc)[2][kNT]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int kt = 2 * half + u;
+      const v4i a0 = unpack_half(ka[kt].x, ka[kt].y);
+      const v4i a1 = unpack_half(ka[kt].z, ka[kt].w);
+#pragma unroll
+      for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], kBias, 0, 0, 0);
+#pragma unroll
+      for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc[u][n], 0, 0, 0);
+    }
+  };
+  // Epilogue of one half block: 16*key per accumulator, running block max.
+  auto epi_half = [&](int half, const uint2 (&ks)[4], const v4i (&acc)[2][kNT], bool masked, int base,
+                      float (&run)[kNT]) {
+    // The fp16 scales feed v_fma_mix_f32 straight from their packed words.
+    _Float16 sc[2][4];
+    float cb[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint2 sr = ks[2 * half + u];
+      sc[u][0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x & 0xFFFFu));
+      sc[u][1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x >> 16));
+      sc[u][2] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y & 0xFFFFu));
+      sc[u][3] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y >> 16));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cb[u][i] = __builtin_fmaf(static_cast<float>(sc[u][i]), -12582912.0f, 0.0f);
+    }
+    auto key16 = [&](int u, int i, int a) -> float {
+      return __builtin_fmaf(static_cast<float>(sc[u][i]), __int_as_float(a), cb[u][i]);
+    };
+    if (!masked) {
+#pragma unroll
+      for (int n = 0; n < kNT; ++n) {
+        float m = run[n];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          m = fmaxf(fmaxf(m, key16(u, 0, acc[u][n].x)), key16(u, 1, acc[u][n].y));
+          m = fmaxf(fmaxf(m, key16(u, 2, acc[u][n].z)), key16(u, 3, acc[u][n].w));
+        }
+        run[n] = m;
+      }
+    } else {
+      // Key t of the lane's rows is visible to query q when t <= pos(q) and
+      // t < tokens; lim = min(pos(q), tokens - 1) - (first key of the row
+      // group) compares once per key.
+#pragma unroll
+      for (int n = 0; n < kNT; ++n) {
+        const int lim = min(q_pos0 + q0 + 16 * n + col, tokens - 1) - (base + 4 * g);
+        float m = run[n];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int accs[4] = {acc[u][n].x, acc[u][n].y, acc[u][n].z, acc[u][n].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = key16(u, i, accs[i]);
+            m = fmaxf(m, ((2 * half + u) * 16 + i <= lim) ? v : ninf);
+          }
+        }
+        run[n] = m;
+      }
+    }
+  };
   auto process = [&](int kb, const uint4 (&ka)[4], const uint2 (&ks)[4]) {
     const int base = (blk0 + kb) * kBlock;
     const bool need_mask = base + kBlock - 1 > pos_lo || base + kBlock > tokens;
     float run[kNT];
 #pragma unroll
     for (int n = 0; n < kNT; ++n) run[n] = ninf;
+    v4i acc0[2][kNT], acc1[2][kNT];
+    mfma_half(0, ka, acc0);
+    if (!need_mask) {
+      // The second half's MFMAs go out between the first half's epilogue
+      // instructions, so the matrix and vector units work at once.
+      mfma_half(1, ka, acc1);
+      epi_half(0, ks, acc0, false, base, run);
+#if QKV_PF_INTERLEAVE
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      v4i acc[2][kNT];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int kt = 2 * half + u;
-        const v4i a0 = unpack_half(ka[kt].x, ka[kt].y);
-        const v4i a1 = unpack_half(ka[kt].z, ka[kt].w);
-#pragma unroll
-        for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], kBias, 0, 0, 0);
-#pragma unroll
-        for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc[u][n], 0, 0, 0);
+      for (int i = 0; i < 2 * 2 * kNT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, QKV_PF_INTERLEAVE, 0);   // then VALU
       }
-      // The fp16 scales feed v_fma_mix_f32 straight from their packed words.
-      _Float16 sc[2][4];
-      float cb[2][4];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const uint2 sr = ks[2 * half + u];
-        sc[u][0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x & 0xFFFFu));
-        sc[u][1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x >> 16));
-        sc[u][2] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y & 0xFFFFu));
-        sc[u][3] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y >> 16));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cb[u][i] = __builtin_fmaf(static_cast<float>(sc[u][i]), -12582912.0f, 0.0f);
-      }
-      auto key16 = [&](int u, int i, int a) -> float {
-        return __builtin_fmaf(static_cast<float>(sc[u][i]), __int_as_float(a), cb[u][i]);
-      };
-      if (!need_mask) {
-#pragma unroll
-        for (int n = 0; n < kNT; ++n) {
-          float m = run[n];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            m = fmaxf(fmaxf(m, key16(u, 0, acc[u][n].x)), key16(u, 1, acc[u][n].y));
-            m = fmaxf(fmaxf(m, key16(u, 2, acc[u][n].z)), key16(u, 3, acc[u][n].w));
-          }
-          run[n] = m;
-        }
-      } else {
-        // Key t of the lane's rows is visible to query q when t <= pos(q) and
-        // t < tokens; lim = min(pos(q), tokens - 1) - (first key of the row
-        // group) compares once per key.
-#pragma unroll
-        for (int n = 0; n < kNT; ++n) {
-          const int lim = min(q_pos0 + q0 + 16 * n + col, tokens - 1) - (base + 4 * g);
-          float m = run[n];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int accs[4] = {acc[u][n].x, acc[u][n].y, acc[u][n].z, acc[u][n].w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float v = key16(u, i, accs[i]);
-              m = fmaxf(m, ((2 * half + u) * 16 + i <= lim) ? v : ninf);
-            }
-          }
-          run[n] = m;
-        }
-      }
+#endif
+      epi_half(1, ks, acc1, false, base, run);
+    } else {
+      mfma_half(1, ka, acc1);
+      epi_half(0, ks, acc0, true, base, run);
+      epi_half(1, ks, acc1, true, base, run);
     }
-    // Max over the 4 row groups, back to key scale (exact); adding +0 turns
-    // a -0 into +0 and leaves every other value alone.
+    // Max over the 4 row groups, four (then two) tiles per round of lane
+    // swaps, after which row group g holds tile n0 + g; back to key scale
+    // (exact), where adding +0 turns a -0 into +0 and leaves every other
+    // value alone.
 #pragma unroll
-    for (int n = 0; n < kNT; ++n) {
-      const float m = __builtin_fmaf(max_x32(max_x16(run[n])), 0.0625f, 0.0f);
-      if (lane < 16) tile[wave][16 * n + col][kb] = m;
+    for (int n0 = 0; n0 + 4 <= kNT; n0 += 4) {
+      const float m = max_rows4(run[n0], run[n0 + 1], run[n0 + 2], run[n0 + 3]);
+      tile[wave][16 * (n0 + g) + col][kb] = __builtin_fmaf(m, 0.0625f, 0.0f);
+    }
+    if constexpr (kNT % 4 == 2) {
+      const float m = max_rows2(run[kNT - 2], run[kNT - 1]);
+      if (lane < 32) tile[wave][16 * (kNT - 2 + g) + col][kb] = __builtin_fmaf(m, 0.0625f, 0.0f);
     }
   };
 
