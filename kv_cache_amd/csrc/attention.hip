@@ -114,15 +114,17 @@ __device__ __forceinline__ int zero_after(float dep) {
 __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 
 // Rows of at most kSelMaxBlocks block maxima can select in the kernel.
-constexpr int kSelVPL = 16;
-constexpr int kSelMaxBlocks = 256 * kSelVPL;
+constexpr int kSelMaxVPL = 16;
+constexpr int kSelMaxBlocks = 256 * kSelMaxVPL;
 
-// SEL: the row's block ids are not given; every workgroup of the row selects
-// the n_sel largest of its block maxima (bmax row r at bmax + r*bmax_ld,
-// lowest index wins ties, ascending) into LDS first -- the selection of
-// qkv_topk, repeated per split instead of launched separately.  The row's
-// first workgroup also writes it to sel_out (when given).
-template <int G, int NI, int ITERS, bool SEL>
+// SELV > 0: the row's block ids are not given; every workgroup of the row
+// selects the n_sel largest of its block maxima (bmax row r at bmax +
+// r*bmax_ld, lowest index wins ties, ascending) into LDS first -- the
+// selection of qkv_topk, repeated per split instead of launched separately,
+// with SELV keys per thread (rows of at most 256*SELV blocks; the selection's
+// latency grows with SELV).  The row's first workgroup also writes it to
+// sel_out (when given).
+template <int G, int NI, int ITERS, int SELV>
 __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
@@ -136,7 +138,8 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   __shared__ float red_acc[4][G][kD];   // per wave weighted V
   __shared__ float red_m[4][G], red_l[4][G];
   __shared__ int last_flag;
-  __shared__ int32_t sel_lds[SEL ? kSelMaxBlocks : 1];
+  constexpr bool SEL = SELV > 0;
+  __shared__ int32_t sel_lds[SEL ? 256 * SELV : 1];
 
   const int r = blockIdx.y, split = blockIdx.x;
   const int b = r / kv_heads, j = r - b * kv_heads;
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   const int n_slots = n_sel * block;
   const int32_t* ids = block_ids + static_cast<int64_t>(r) * n_sel;
   if constexpr (SEL) {
-    select_row<kSelVPL, false>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
+    select_row<SEL ? SELV : 1, false>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
     if (sel_out && split == 0)
       for (int i = tid; i < n_sel; i += kNT) sel_out[static_cast<int64_t>(r) * n_sel + i] = sel_lds[i];
   }
@@ -524,9 +527,10 @@ int launch_attention(const char* what, const void* query, const void* key, const
       static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),             \
       static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o, bmax,   \
       bmax_ld, sel_out, kv_div)
-#define QKV_ATTN(GG, IT)             \
-  if (sel) QKV_ATTN_S(GG, IT, true); \
-  else QKV_ATTN_S(GG, IT, false);
+#define QKV_ATTN(GG, IT)                  \
+  if (!sel) QKV_ATTN_S(GG, IT, 0);        \
+  else if (nb <= 2048) QKV_ATTN_S(GG, IT, 8); \
+  else QKV_ATTN_S(GG, IT, 16);
 #if QKV_ATTN_MAX_ITERS > 8
 #define QKV_ATTN_16(GG) case 16: QKV_ATTN(GG, 16); break;
 #else

@@ -54,10 +54,14 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 // holds keys t + 256i (i < VPL) as order-preserving uint32, loaded without
 // branches so that every load is in flight at once.  The bits shared by the
 // row's largest and smallest key are skipped; the rest are resolved 8 bits
-// at a time with a shared 256-bin histogram that wave 0 scans with DPP.
+// at a time with per-wave 256-bin histograms that wave 0 sums, scans with
+// DPP and clears again for the next digit (two barriers per digit).
 // Output positions follow index order: the keys taken before slot (i, wave)
 // are the keys > theta before it plus min(kr, keys == theta before it), both
 // known from per-(slot, wave) ballot counts, so one pass places every key.
+// A row is one workgroup and so runs on few waves: the code keeps the wave
+// index scalar and avoids per-slot branches, since every dependent
+// instruction's latency is exposed.
 // FINITE: keys equal to -inf are not selectable; a row with fewer than k
 // other keys selects them all and pads its output with -1.
 //
@@ -67,11 +71,13 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 // thread of the workgroup must call it; it ends with a barrier.
 template <int VPL, bool FINITE>
 __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel) {
-  __shared__ int hist[4][260];             // one copy per wave, padded across banks
+  static_assert(4 * VPL <= 64, "one lane per (slot, wave) count");
+  __shared__ __attribute__((aligned(16))) int hist[4][260];   // one copy per wave, padded across banks
   __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
   __shared__ uint32_t red[4][3];
   __shared__ int sh_bin, sh_kr, sh_whole;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   uint32_t u[VPL];
   bool valid[VPL];
@@ -81,14 +87,14 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     u[i] = f32_sortable(vals[min(idx, n - 1)]);
     valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey);
   }
+#pragma unroll
+  for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
   uint32_t umax = 0, umin = 0xFFFFFFFFu;
   int nval = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    if (valid[i]) {
-      umax = max(umax, u[i]);
-      umin = min(umin, u[i]);
-    }
+    umax = max(umax, valid[i] ? u[i] : 0u);
+    umin = min(umin, valid[i] ? u[i] : 0xFFFFFFFFu);
     nval += __popcll(__ballot(valid[i]));
   }
   umax = wave_minmax_u32<true>(umax);
@@ -120,10 +126,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   while (remaining > 0) {   // uniform across the workgroup
     const int shift = remaining > 8 ? remaining - 8 : 0;
     const uint32_t dmask = (1u << (remaining - shift)) - 1u;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
-    __syncthreads();
-    // Only keys on the prefix count: after the first pass they are few, and
+    // Only keys on the prefix count: after the first digit they are few, and
     // sending the rest to a dummy bin would serialize on one LDS address.
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -131,16 +134,24 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     }
     __syncthreads();
     if (wave == 0) {
-      // Lane l owns bins 255-4l .. 252-4l (descending); the exclusive scan of
-      // the lane totals counts the keys in higher bins.  Exactly one bin
-      // holds the kr-th key, since kr never exceeds the keys on the prefix.
-      int c[4], tot = 0;
+      // Lane l owns bins 252-4l .. 255-4l, read and cleared as one 16-byte
+      // word per histogram; the exclusive scan of the lane totals (highest
+      // bins first) counts the keys in higher bins.  Exactly one bin holds
+      // the kr-th key, since kr never exceeds the keys on the prefix.
+      const int b0 = 252 - 4 * lane;
+      int4 h = *reinterpret_cast<const int4*>(&hist[0][b0]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int bin = 255 - 4 * lane - i;
-        c[i] = hist[0][bin] + hist[1][bin] + hist[2][bin] + hist[3][bin];
-        tot += c[i];
+      for (int w = 1; w < 4; ++w) {
+        const int4 x = *reinterpret_cast<const int4*>(&hist[w][b0]);
+        h.x += x.x;
+        h.y += x.y;
+        h.z += x.z;
+        h.w += x.w;
       }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) *reinterpret_cast<int4*>(&hist[w][b0]) = int4{0, 0, 0, 0};
+      const int c[4] = {h.w, h.z, h.y, h.x};   // bins 255-4l, 254-4l, 253-4l, 252-4l
+      const int tot = c[0] + c[1] + c[2] + c[3];
       int above = wave_incl_scan_dpp(tot) - tot;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -168,18 +179,19 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   const uint32_t theta = prefix;
 
   // Per-(slot, wave) counts of keys > theta and == theta, in output order
-  // j = 4*slot + wave; one DPP scan over j gives each (slot, wave) the counts
-  // before it.
-  const uint64_t below = (1ull << lane) - 1ull;
-  uint64_t bgt[VPL], beq[VPL];
+  // j = 4*slot + wave (lane i of each wave writes its slot i's counts); one
+  // DPP scan over j gives each (slot, wave) the counts before it.
+  int my_gt = 0, my_eq = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    bgt[i] = __ballot(valid[i] && u[i] > theta);
-    beq[i] = __ballot(valid[i] && u[i] == theta);
-    if (lane == 0) {
-      cnt_gt[4 * i + wave] = __popcll(bgt[i]);
-      cnt_eq[4 * i + wave] = __popcll(beq[i]);
-    }
+    const int g = __popcll(__ballot(valid[i] && u[i] > theta));
+    const int e = __popcll(__ballot(valid[i] && u[i] == theta));
+    my_gt = lane == i ? g : my_gt;
+    my_eq = lane == i ? e : my_eq;
+  }
+  if (lane < VPL) {
+    cnt_gt[4 * lane + wave] = my_gt;
+    cnt_eq[4 * lane + wave] = my_eq;
   }
   __syncthreads();
   const int cg = lane < 4 * VPL ? cnt_gt[lane] : 0;
@@ -190,16 +202,20 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   for (int i = 0; i < VPL; ++i) {
     const int g0 = __builtin_amdgcn_readlane(gt_excl, 4 * i + wave);
     const int e0 = __builtin_amdgcn_readlane(eq_excl, 4 * i + wave);
-    const bool gt = (bgt[i] >> lane) & 1ull;
-    const bool eq = (beq[i] >> lane) & 1ull;
-    const bool take = gt || (eq && e0 + __popcll(beq[i] & below) < kr);
+    const bool gt = valid[i] && u[i] > theta;
+    const bool eq = valid[i] && u[i] == theta;
+    const uint64_t be = __ballot(eq);
+    const int eq_before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(be >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(be), 0));
+    const bool take = gt || (eq && e0 + eq_before < kr);
     const uint64_t tb = __ballot(take);
-    if (take) sel[g0 + min(e0, kr) + __popcll(tb & below)] = i * 256 + tid;
+    const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(tb >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(tb), 0));
+    if (take) sel[g0 + min(e0, kr) + before] = i * 256 + tid;
   }
   __syncthreads();
   return kk;
 }
-
 
 // ---------------------------------------------------------------------------
 // Rows of up to 1024 * VPL keys in one 1024-thread workgroup (16 waves).
