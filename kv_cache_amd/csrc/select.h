@@ -11,6 +11,7 @@ namespace {
 
 constexpr uint32_t kNegInfKey = 0x007FFFFFu;   // f32_sortable(-inf)
 
+
 // ---------------------------------------------------------------------------
 // Wave-level helpers.  Reductions and scans use DPP (a few cycles a step,
 // where an LDS permute round trip costs ~100).
@@ -73,8 +74,9 @@ template <int VPL, bool FINITE>
 __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel) {
   static_assert(4 * VPL <= 64, "one lane per (slot, wave) count");
   __shared__ __attribute__((aligned(16))) int hist[4][260];   // one copy per wave, padded across banks
+  __shared__ int32_t spare[64];   // where lanes that place nothing write
   __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
-  __shared__ uint32_t red[4][3];
+  __shared__ uint32_t red[4][4];
   __shared__ int sh_bin, sh_kr, sh_whole;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -97,23 +99,44 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     umin = min(umin, valid[i] ? u[i] : 0xFFFFFFFFu);
     nval += __popcll(__ballot(valid[i]));
   }
+  const uint32_t lane_max = umax;   // 0 when the lane holds no valid key
   umax = wave_minmax_u32<true>(umax);
   umin = wave_minmax_u32<false>(umin);
+  // A lower bound of the k-th largest key: when j = ceil(k/4) lanes of every
+  // wave hold a key >= x_w, at least k keys are >= min_w x_w.  x_w is the
+  // wave's j-th largest lane maximum to 8 bits below the bits its largest and
+  // smallest keys share (the lower bits left zero keep it a lower bound);
+  // keys under the bound cannot be selected and stay out of the histograms.
+  uint32_t lbound = 0;
+  const int j = (k + 3) / 4;
+  if (j <= 64 && umax != umin && __popcll(__ballot(lane_max != 0)) >= j) {   // uniform
+    // j lanes hold a valid key, and every valid key is >= the shared prefix
+    const int top = 31 - __builtin_clz(umax ^ umin);
+    lbound = top == 31 ? 0u : umax & ~((2u << top) - 1u);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      if (top - b < 0) break;
+      const uint32_t c = lbound | (1u << (top - b));
+      if (__popcll(__ballot(lane_max >= c)) >= j) lbound = c;
+    }
+  }
   if (lane == 0) {
     red[wave][0] = umax;
     red[wave][1] = umin;
     red[wave][2] = nval;
+    red[wave][3] = lbound;
   }
   __syncthreads();
   umax = max(max(red[0][0], red[1][0]), max(red[2][0], red[3][0]));
   umin = min(min(red[0][1], red[1][1]), min(red[2][1], red[3][1]));
   nval = red[0][2] + red[1][2] + red[2][2] + red[3][2];
   const int kk = min(k, nval);   // keys selected; k unless FINITE drops some
+  const uint32_t lo = max(umin, min(min(red[0][3], red[1][3]), min(red[2][3], red[3][3])));
 
-  // Radix select over the bits below the common prefix of umax and umin.
+  // Radix select over the bits below the common prefix of umax and lo.
   int kr = kk;
   uint32_t prefix = umax, mask = 0xFFFFFFFFu;
-  int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
+  int remaining = (umax == lo || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ lo);
   if (remaining) {
     mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
     prefix = umax & mask;
@@ -126,11 +149,11 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   while (remaining > 0) {   // uniform across the workgroup
     const int shift = remaining > 8 ? remaining - 8 : 0;
     const uint32_t dmask = (1u << (remaining - shift)) - 1u;
-    // Only keys on the prefix count: after the first digit they are few, and
-    // sending the rest to a dummy bin would serialize on one LDS address.
+    // Only keys >= lo on the prefix count: they are few, and sending the
+    // rest to a dummy bin would serialize on one LDS address.
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      if (valid[i] && (u[i] & mask) == prefix) atomicAdd(&hist[wave][(u[i] >> shift) & dmask], 1);
+      if (valid[i] && u[i] >= lo && (u[i] & mask) == prefix) atomicAdd(&hist[wave][(u[i] >> shift) & dmask], 1);
     }
     __syncthreads();
     if (wave == 0) {
@@ -211,7 +234,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     const uint64_t tb = __ballot(take);
     const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(tb >> 32),
                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(tb), 0));
-    if (take) sel[g0 + min(e0, kr) + before] = i * 256 + tid;
+    *(take ? &sel[g0 + min(e0, kr) + before] : &spare[lane]) = i * 256 + tid;   // no branch per slot
   }
   __syncthreads();
   return kk;

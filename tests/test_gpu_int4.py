@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from kv_cache_amd import int4 as K
+from kv_cache_amd import prefill as P
 from kv_cache_amd.workloads import CONFIGS, make_layer
 from oracle import qkv_oracle as O
 
@@ -207,6 +208,32 @@ def test_topk_staged_equals_single_workgroup():
         assert lib.qkv_topk_workspace_bytes(5, 70000, k) > 0
         got = K.block_topk(vals, k)
         assert torch.equal(got, want)
+
+
+def _adversarial_rows(n, seed):
+    """Rows that stress the selection's lower bound (thread t of a 256-thread
+    row holds keys t + 256i, so key x sits in wave (x % 256) // 64)."""
+    g = torch.Generator().manual_seed(seed)
+    rows = [torch.randn(n, generator=g) for _ in range(7)]
+    wave = (torch.arange(n) % 256) // 64
+    rows[0][wave == 0] += 50.0                               # every large key in one wave
+    rows[1] = torch.where(wave == 3, rows[1] + 50.0, rows[1])  # ... in the last wave
+    rows[2] = torch.full((n,), 2.5)                          # all equal
+    rows[3] = (torch.arange(n) % 5).float()                  # 5 values, heavy ties at the boundary
+    rows[4][(torch.arange(n) % 64) != 7] = -float("inf")     # one lane per wave holds finite keys
+    rows[5] = torch.where(torch.arange(n) % 256 < 3, rows[5] + 9.0, -rows[5].abs() - 20.0)
+    rows[6] = torch.ldexp(torch.ones(n), torch.randint(-30, 30, (n,), generator=g))   # wide exponent range
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize("n,k", [(2048, 128), (2048, 1), (2048, 7), (2048, 256), (2048, 300), (1000, 64),
+                                 (4096, 255), (4096, 129), (2049, 128)])
+def test_topk_adversarial_layouts(n, k):
+    vals = _adversarial_rows(n, n + k)
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+    got = P.block_topk(vals.to(DEV), k).cpu().numpy()    # -inf keys not selectable, -1 padding
+    assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
 
 
 def test_topk_strided_rows():
