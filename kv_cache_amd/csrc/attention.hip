@@ -48,10 +48,6 @@ namespace {
 
 constexpr int kD = 128;     // head dim
 constexpr int kNT = 256;    // threads per workgroup
-#ifndef QKV_ATTN_MAX_ITERS
-#define QKV_ATTN_MAX_ITERS 16
-#endif
-constexpr int kMaxIters = QKV_ATTN_MAX_ITERS;
 // Ticket words at the start of the workspace, one per possible row, so calls
 // of any shape that share a workspace find their tickets at the same place.
 constexpr int64_t kTicketWords = 65536;
@@ -426,12 +422,15 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
 // two chunks of K/V in registers, 4 above that.
 constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 
-// Chunks per wave: doubled (up to kMaxIters) while the grid keeps
+// Chunks per wave: doubled (up to max_iters_for) while the grid keeps
 // QKV_ATTN_TARGET_WGS workgroups, so long selections take few splits per
 // row.  Measured at cfg2 (64 rows x 2048 slots): 256 workgroups of 4 chunks
 // per wave 18.0 us, 1024 workgroups of 1 chunk 20.4 us, 128 of 8 22.2 us.
 // G = 8 stops at 8 chunks: its 16-chunk variant does not fit the registers.
-constexpr int max_iters_for(int64_t g) { return g >= 8 && kMaxIters > 8 ? 8 : kMaxIters; }
+// G = 4 goes on to 32: at cfg3 (256 rows x 4096 slots) 512 workgroups of 32
+// chunks, all resident at two per CU, take 101.4 us against 106.0 us for
+// 1024 workgroups of 16 chunks in two rounds.
+constexpr int max_iters_for(int64_t g) { return g >= 8 ? 8 : g == 4 ? 32 : 16; }
 
 int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
   const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
@@ -531,11 +530,7 @@ int launch_attention(const char* what, const void* query, const void* key, const
   if (!sel) QKV_ATTN_S(GG, IT, 0);        \
   else if (nb <= 2048) QKV_ATTN_S(GG, IT, 8); \
   else QKV_ATTN_S(GG, IT, 16);
-#if QKV_ATTN_MAX_ITERS > 8
 #define QKV_ATTN_16(GG) case 16: QKV_ATTN(GG, 16); break;
-#else
-#define QKV_ATTN_16(GG)
-#endif
 #define QKV_ATTN_G(GG, LONG)            \
   switch (iters) {                      \
     case 1: QKV_ATTN(GG, 1); break;     \
@@ -547,7 +542,7 @@ int launch_attention(const char* what, const void* query, const void* key, const
   switch (g) {
     case 1: QKV_ATTN_G(1, QKV_ATTN_16(1)); break;
     case 2: QKV_ATTN_G(2, QKV_ATTN_16(2)); break;
-    case 4: QKV_ATTN_G(4, QKV_ATTN_16(4)); break;
+    case 4: QKV_ATTN_G(4, QKV_ATTN_16(4) case 32: QKV_ATTN(4, 32); break;); break;
     default: QKV_ATTN_G(8, ); break;
   }
 #undef QKV_ATTN_G

@@ -78,12 +78,13 @@ def test_host_side_validation(call, msg):
     assert msg in _err()
 
 
-def _attn_splits(rows, n_slots, g, target=256, max_iters=16):
+def _attn_splits(rows, n_slots, g, target=256):
     """Splits per row of qkv_sparse_attention: a workgroup round covers
     4 waves x 4*NI slots (NI = 8 for G <= 2, else 4); chunks per wave double
-    (up to 16, 8 for G = 8) while the grid keeps at least ``target`` workgroups."""
+    (up to 16; 8 for G = 8, 32 for G = 4) while the grid keeps at least
+    ``target`` workgroups."""
     per_iter = 16 * (8 if g <= 2 else 4)
-    max_iters = min(max_iters, 8) if g >= 8 else max_iters
+    max_iters = 8 if g >= 8 else 32 if g == 4 else 16
     it = 1
     while it < max_iters and rows * -(-n_slots // (per_iter * it * 2)) >= target:
         it *= 2
@@ -94,12 +95,12 @@ def test_workspace_size_formula():
     # 65536 ticket words + rows * splits * G * (D + 2) floats
     t = 65536
     assert _attn_splits(64, 2048, 2) == 4             # cfg2: 4 splits of 512 slots
-    assert _attn_splits(256, 4096, 4) == 4            # cfg3: 4 splits of 1024 slots
+    assert _attn_splits(256, 4096, 4) == 2            # cfg3: 2 splits of 2048 slots
     assert _attn_splits(8, 300, 8) == 5
     # sized for the larger of the call's own splits and the bound on the
     # splits of smaller calls, 2 * (ceil(256 / rows) - 1) (capped by the
     # slot count): 6 at cfg2 (64 rows), 0 at cfg3 (256 rows)
-    for b, hq, hkv, n_sel, block, splits in [(8, 32, 8, 128, 16, 6), (32, 32, 8, 256, 16, 4),
+    for b, hq, hkv, n_sel, block, splits in [(8, 32, 8, 128, 16, 6), (32, 32, 8, 256, 16, 2),
                                              (1, 8, 8, 7, 64, 4), (8, 16, 8, 2048, 16, 16)]:
         rows, g = b * hkv, hq // hkv
         assert lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, block) == \

@@ -271,6 +271,7 @@ def test_sparse_attention_matches_fp64(g_size, block, nsel):
     (2, 8, 20000, 16, 1024),    # 64 rows x 16384 slots: 16 chunks per wave, 8 splits
     (2, 1, 9000, 16, 512),      # 8 rows x 8192 slots: 2 chunks per wave
     (4, 1, 9000, 16, 512),      # G = 4 (4-token steps): 4 chunks per wave
+    (4, 16, 9000, 16, 300),     # G = 4, 128 rows x 4800 slots: 32 chunks per wave, partial last split
     (8, 4, 20000, 1, 4000),     # G = 8, block 1: 8 chunks per wave, slots not a multiple of a chunk
     (1, 8, 20000, 64, 300),     # G = 1: 16 chunks per wave, partial last split
 ])
