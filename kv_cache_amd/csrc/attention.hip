@@ -189,9 +189,29 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G) * kD + cc * 8;
 #pragma unroll
   for (int h = 0; h < G; ++h) qx[h] = *reinterpret_cast<const uint4*>(qrow + h * kD);
+  // G = 2, 4: each lane of a 16-lane token group ends up with the full QK sum
+  // of one head, own = 2*b0 + b1 (G = 4) or b0 (G = 2) from the lane's low
+  // bits.  Register k holds head own ^ k, so the pairwise reduce-scatter over
+  // lanes l^1 and l^2 needs no per-lane select: the partner's register k + G/2
+  // (step 1) and register 1 (step 2, G = 4) hold this lane's head.
+  constexpr bool kScatter = G == 2 || G == 4;
+  const int own = G == 4 ? 2 * (lane & 1) + ((lane >> 1) & 1) : (lane & 1);
+  if constexpr (kScatter) {
+    uint4 qp[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      qp[k] = qx[0];
+#pragma unroll
+      for (int h = 1; h < G; ++h)
+        if ((own ^ k) == h) qp[k] = qx[h];
+    }
+#pragma unroll
+    for (int k = 0; k < G; ++k) qx[k] = qp[k];
+  }
 
   // Running state of this lane's token group: max (log2 domain), sum, P.V.
   float m[G], l[G], acc[G][8];
+  float m_own = ninf, l_own = 0.0f;   // scattered path: running max / sum of head `own`
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     m[h] = ninf;
@@ -200,7 +220,78 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     for (int c = 0; c < 8; ++c) acc[h][c] = 0.0f;
   }
 
+  // Head value of the scattered path from the quad lane that owns head h.
+  auto from_head = [](float v, int h) -> float {
+    const int o = G == 4 ? (h >> 1) | ((h & 1) << 1) : h;   // quad lane of head h
+    return o == 0 ? dpp_f<0x00>(v) : o == 1 ? dpp_f<0x55>(v) : o == 2 ? dpp_f<0xAA>(v) : dpp_f<0xFF>(v);
+  };
+  auto compute_scatter = [&](const int (&tk)[NI], const uint4 (&kx)[NI], const uint4 (&vx)[NI]) {
+    float s[NI];
+    float cm = ninf;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float r[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        float a = dot2_bf16(qx[k].x, kx[i].x, 0.0f);
+        a = dot2_bf16(qx[k].y, kx[i].y, a);
+        a = dot2_bf16(qx[k].z, kx[i].z, a);
+        r[k] = dot2_bf16(qx[k].w, kx[i].w, a);
+      }
+      float y;
+      if constexpr (G == 4) {
+        const float x0 = r[0] + dpp_f<0xB1>(r[2]);   // lanes l, l^1
+        const float x1 = r[1] + dpp_f<0xB1>(r[3]);
+        y = x0 + dpp_f<0x4E>(x1);                    // lanes l, l^2
+      } else {
+        y = r[0] + dpp_f<0xB1>(r[1]);
+        y = y + dpp_f<0x4E>(y);
+      }
+      // Rotations by 8 then 4 give the 4 lanes of a head the same sum, bit for bit.
+      y = y + dpp_f<0x128>(y);
+      y = y + dpp_f<0x124>(y);
+      s[i] = tk[i] >= 0 ? y * scale_log2 : ninf;
+      cm = fmaxf(cm, s[i]);
+    }
+    const float mn = fmaxf(m_own, cm);
+    const float ms = (mn == ninf) ? 0.0f : mn;
+    const float al = exp2f(m_own - ms);   // 0 while m_own = -inf
+    l_own *= al;
+    m_own = mn;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float ah = from_head(al, h);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[h][c] *= ah;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float v[8];
+      v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
+      v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
+      v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
+      v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
+      const float p = exp2f(s[i] - ms);   // 0 for masked slots
+      l_own += p;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float ph = from_head(p, h);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[h][c] = __builtin_fmaf(ph, v[c], acc[h][c]);
+      }
+    }
+    pin(l_own);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) pin(acc[h][c]);
+    }
+  };
   auto compute = [&](const int (&tk)[NI], const uint4 (&kx)[NI], const uint4 (&vx)[NI]) {
+    if constexpr (kScatter) {
+      compute_scatter(tk, kx, vx);
+      return;
+    }
     float s[G][NI], cm[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) cm[h] = ninf;
@@ -272,7 +363,7 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     const int cur = c & 1, nxt = cur ^ 1;
     __builtin_amdgcn_sched_barrier(0);
     if (c + 1 < ITERS) {
-      const int dz = c > 0 ? zero_after(l[0]) : 0;
+      const int dz = c > 0 ? zero_after(kScatter ? l_own : l[0]) : 0;
       const int tn = token_of(c + 1, id_next + dz);
       if (c + 2 < ITERS) id_next = load_id(c + 2 + dz);
       spread(tn, tk[nxt]);
@@ -282,6 +373,13 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     compute(tk[cur], kx[cur], vx[cur]);
   }
 
+  if constexpr (kScatter) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      m[h] = from_head(m_own, h);
+      l[h] = from_head(l_own, h);
+    }
+  }
   // Combine the wave's four token groups: common max, rescale, sum.
 #pragma unroll
   for (int h = 0; h < G; ++h) {
