@@ -39,9 +39,6 @@ constexpr int kBlock = 64;          // keys per selection block
 #ifndef QKV_PF_WG_PER_CU
 #define QKV_PF_WG_PER_CU 2
 #endif
-#ifndef QKV_PF_INTERLEAVE
-#define QKV_PF_INTERLEAVE 0
-#endif
 constexpr int kNT = QKV_PF_NT;              // 16-query column tiles per wave
 constexpr int kQTile = 16 * kNT;            // queries per wave
 constexpr int kChunkBlocks = QKV_PF_CHUNK;  // blocks per workgroup key chunk
@@ -253,17 +250,8 @@ __global__ __launch_bounds__(256, QKV_PF_WG_PER_CU) void prefill_scores_kernel(
     v4i acc0[2][kNT], acc1[2][kNT];
     mfma_half(0, ka, acc0);
     if (!need_mask) {
-      // The second half's MFMAs go out between the first half's epilogue
-      // instructions, so the matrix and vector units work at once.
       mfma_half(1, ka, acc1);
       epi_half(0, ks, acc0, false, base, run);
-#if QKV_PF_INTERLEAVE
-#pragma unroll
-      for (int i = 0; i < 2 * 2 * kNT; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, QKV_PF_INTERLEAVE, 0);   // then VALU
-      }
-#endif
       epi_half(1, ks, acc1, false, base, run);
     } else {
       mfma_half(1, ka, acc1);
