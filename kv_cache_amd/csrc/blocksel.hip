@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   ws1.load(partial + static_cast<int64_t>(row) * partial_ld, n_scan * block);
   const int kk1 = ws1.run(n_cand, lds.a);
   const int32_t* brow = blocks + static_cast<int64_t>(row) * n_scan;
-  ws1.place(lds.a, [&](int pos, uint32_t, int o) {
+  ws1.place(lds.a, [&](int pos, int o, int) {
     const int jb = pos / block;
     cand[o] = brow[jb] * block + (pos - jb * block);
   });
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   }
   const int kk2 = ws2.run(n_keep, lds.b);
   int32_t* ids = attn_ids + static_cast<int64_t>(row) * n_out;
-  ws2.place(lds.b, [&](int ci, uint32_t, int o) {
+  ws2.place(lds.b, [&](int ci, int o, int) {
     const int tok = cand[ci];
     mrow[tok] = 1;
     const bool fv = tok >= sink_end && !(tok >= recent_start && tok < history);

@@ -355,8 +355,11 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   ws.load(scores + static_cast<int64_t>(row) * scores_ld, history);
   ws.run(keep, sh);   // its barriers order the writes above before the scatter below
   const int64_t o = static_cast<int64_t>(row) * n_out;
-  ws.place(sh, [&](int idx, uint32_t key, int p) {
-    const bool valid = isfinite(sortable_f32(key));
+  uint64_t fin = 0;   // bit i: key i is a finite score
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(ws.u[i]))) << i;
+  ws.place(sh, [&](int idx, int p, int slot) {
+    const bool valid = (fin >> slot) & 1ull;
     if (valid) hrow[idx] = 1;
     const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
     final_idx[o + p] = idx;

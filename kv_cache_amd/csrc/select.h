@@ -263,8 +263,13 @@ struct WideSelect {
 
   // LDS of the selection (the caller declares one and passes it in).
   static constexpr int RB = 12, NB = 1 << RB;   // radix digit: 12 bits, 4096 bins
+  static constexpr int RECW = 6;                // dwords per slot record (place)
+  static_assert(NW * VPL * RECW <= NB, "slot records fit in the histogram's place");
   struct Shared {
-    int hist[NB];
+    union {
+      int hist[NB];                   // run(): the radix histogram
+      uint32_t rec[NW * VPL * RECW];  // place(): per (wave, slot) prefix counts and lane masks
+    };
     int wave_sum[NW];
     int wave_gt[NW], wave_eq[NW];
     uint32_t red[NW][3];
@@ -413,45 +418,68 @@ struct WideSelect {
     return kk;
   }
 
-  // Calls emit(position, key, output index) for every taken key, output
+  // Calls emit(position, output index, slot) for every taken key, output
   // indices 0..kk-1 in ascending position order: a taken key's index is the
   // number of keys above theta before it plus min(keys equal to theta before
-  // it, kr).  Ends with a barrier.
+  // it, kr).  Lane i of each wave first gathers slot i's lane masks and
+  // within-wave prefix counts into an LDS record; then every thread visits
+  // only its own taken keys (a few), instead of the wave stepping through
+  // all VPL slots.  Ends with a barrier.
   template <typename Emit>
   __device__ void place(Shared& sh, Emit&& emit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t below = (1ull << lane) - 1ull;
     refresh();
     uint64_t gtm = 0, eqm = 0;   // bit i: key i above / equal to theta
+    uint32_t g_lo = 0, g_hi = 0, e_lo = 0, e_hi = 0;   // lane i: slot i's lane masks
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      gtm |= static_cast<uint64_t>(on(i) && u[i] > theta) << i;
-      eqm |= static_cast<uint64_t>(on(i) && u[i] == theta) << i;
+      const bool gt = on(i) && u[i] > theta, eq = on(i) && u[i] == theta;
+      gtm |= static_cast<uint64_t>(gt) << i;
+      eqm |= static_cast<uint64_t>(eq) << i;
+      const uint64_t bg = __ballot(gt), be = __ballot(eq);
+      g_lo = lane == i ? static_cast<uint32_t>(bg) : g_lo;
+      g_hi = lane == i ? static_cast<uint32_t>(bg >> 32) : g_hi;
+      e_lo = lane == i ? static_cast<uint32_t>(be) : e_lo;
+      e_hi = lane == i ? static_cast<uint32_t>(be >> 32) : e_hi;
     }
     asm volatile("" : "+v"(gtm), "+v"(eqm));
-    const int cg = __popcll(gtm), ce = __popcll(eqm);
+    const int cg = __popc(g_lo) + __popc(g_hi), ce = __popc(e_lo) + __popc(e_hi);   // 0 past VPL
     const int ig = wave_incl_scan_dpp(cg), ie = wave_incl_scan_dpp(ce);
+    if (lane < VPL) {
+      uint32_t* rp = sh.rec + (wave * VPL + lane) * RECW;
+      *reinterpret_cast<uint2*>(rp) = make_uint2(static_cast<uint32_t>(ig - cg), static_cast<uint32_t>(ie - ce));
+      *reinterpret_cast<uint2*>(rp + 2) = make_uint2(g_lo, g_hi);
+      *reinterpret_cast<uint2*>(rp + 4) = make_uint2(e_lo, e_hi);
+    }
     if (lane == 63) {
       sh.wave_gt[wave] = ig;
       sh.wave_eq[wave] = ie;
     }
     __syncthreads();
-    int g = 0, e = 0;   // keys of the earlier waves, then of the earlier slots of this wave
+    int g = 0, e = 0;   // keys of the earlier waves
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       g += w < wave ? sh.wave_gt[w] : 0;
       e += w < wave ? sh.wave_eq[w] : 0;
     }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const bool gt = (gtm >> i) & 1ull, eq = (eqm >> i) & 1ull;
-      const uint64_t bgt = __ballot(gt), beq = __ballot(eq);
-      if (bgt | beq) {   // wave-uniform
-        const int gl = g + __popcll(bgt & below), el = e + __popcll(beq & below);
-        if (gt || (eq && el < kr)) emit(pos(i), u[i], gl + min(el, kr));
-        g += __popcll(bgt);
-        e += __popcll(beq);
+    uint64_t cand = gtm | eqm;
+    while (cand) {   // a thread's candidates in slot (position) order
+      const int i = __builtin_ctzll(cand);
+      cand &= cand - 1;
+      const uint32_t* rp = sh.rec + (wave * VPL + i) * RECW;
+      const uint2 pc = *reinterpret_cast<const uint2*>(rp);
+      const uint2 mg = *reinterpret_cast<const uint2*>(rp + 2);
+      const uint2 me = *reinterpret_cast<const uint2*>(rp + 4);
+      const uint64_t bgt = (static_cast<uint64_t>(mg.y) << 32) | mg.x;
+      const uint64_t beq = (static_cast<uint64_t>(me.y) << 32) | me.x;
+      const int el = e + static_cast<int>(pc.y) + __popcll(beq & below);
+      if (!((gtm >> i) & 1ull) && el >= kr) {   // equal keys after it are not taken either
+        cand &= gtm;
+        continue;
       }
+      const int gl = g + static_cast<int>(pc.x) + __popcll(bgt & below);
+      emit(pos(i), gl + min(el, kr), i);
     }
     __syncthreads();
   }
