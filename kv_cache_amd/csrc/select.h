@@ -51,6 +51,25 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
   return static_cast<int>(r);
 }
 
+// A lower bound of the wave's j-th largest lane value v (0: the lane has
+// none), given the wave's largest value vmax and a value vmin <= every
+// nonzero v: the largest x with at least j lanes at or above it, resolved to
+// 8 bits below the bits vmax and vmin share (the lower bits left zero keep it
+// a lower bound); 0 when fewer than j lanes hold a value.  Wave-uniform.
+__device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t vmax, uint32_t vmin) {
+  if (j > 64 || __popcll(__ballot(v != 0)) < j) return 0;
+  if (vmax == vmin) return vmax;   // every value is vmax
+  const int top = 31 - __builtin_clz(vmax ^ vmin);
+  uint32_t x = top == 31 ? 0u : vmax & ~((2u << top) - 1u);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    if (top - b < 0) break;
+    const uint32_t c = x | (1u << (top - b));
+    if (__popcll(__ballot(v >= c)) >= j) x = c;
+  }
+  return x;
+}
+
 // Rows of at most 256*VPL keys: one workgroup of 4 waves per row.  Thread t
 // holds keys t + 256i (i < VPL) as order-preserving uint32, loaded without
 // branches so that every load is in flight at once.  The bits shared by the
@@ -66,12 +85,17 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
 // FINITE: keys equal to -inf are not selectable; a row with fewer than k
 // other keys selects them all and pads its output with -1.
 //
+// floor: keys whose order-preserving value is below it are not selectable
+// either (0: none excluded), and kk counts only the others.  lane_max_out,
+// when given, receives the largest selectable key of this thread (0: none).
+//
 // select_row runs the selection for one row inside a 256-thread workgroup:
 // it writes the positions of the kk selected keys, ascending, to sel (LDS,
-// 256*VPL entries) and returns kk (k, or with FINITE possibly fewer).  Every
-// thread of the workgroup must call it; it ends with a barrier.
+// 256*VPL entries) and returns kk (k, or with FINITE or a floor possibly
+// fewer).  Every thread of the workgroup must call it; it ends with a barrier.
 template <int VPL, bool FINITE>
-__device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel) {
+__device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
+                          uint32_t* lane_max_out = nullptr) {
   static_assert(4 * VPL <= 64, "one lane per (slot, wave) count");
   __shared__ __attribute__((aligned(16))) int hist[4][260];   // one copy per wave, padded across banks
   __shared__ int32_t spare[64];   // where lanes that place nothing write
@@ -87,7 +111,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   for (int i = 0; i < VPL; ++i) {
     const int idx = i * 256 + tid;
     u[i] = f32_sortable(vals[min(idx, n - 1)]);
-    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey);
+    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey) && u[i] >= floor;
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
@@ -100,26 +124,13 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     nval += __popcll(__ballot(valid[i]));
   }
   const uint32_t lane_max = umax;   // 0 when the lane holds no valid key
+  if (lane_max_out) *lane_max_out = lane_max;
   umax = wave_minmax_u32<true>(umax);
   umin = wave_minmax_u32<false>(umin);
   // A lower bound of the k-th largest key: when j = ceil(k/4) lanes of every
-  // wave hold a key >= x_w, at least k keys are >= min_w x_w.  x_w is the
-  // wave's j-th largest lane maximum to 8 bits below the bits its largest and
-  // smallest keys share (the lower bits left zero keep it a lower bound);
-  // keys under the bound cannot be selected and stay out of the histograms.
-  uint32_t lbound = 0;
-  const int j = (k + 3) / 4;
-  if (j <= 64 && umax != umin && __popcll(__ballot(lane_max != 0)) >= j) {   // uniform
-    // j lanes hold a valid key, and every valid key is >= the shared prefix
-    const int top = 31 - __builtin_clz(umax ^ umin);
-    lbound = top == 31 ? 0u : umax & ~((2u << top) - 1u);
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      if (top - b < 0) break;
-      const uint32_t c = lbound | (1u << (top - b));
-      if (__popcll(__ballot(lane_max >= c)) >= j) lbound = c;
-    }
-  }
+  // wave hold a key >= x_w, at least k keys are >= min_w x_w.  Keys under the
+  // bound cannot be selected and stay out of the histograms.
+  const uint32_t lbound = wave_lower_bound(lane_max, (k + 3) / 4, umax, umin);
   if (lane == 0) {
     red[wave][0] = umax;
     red[wave][1] = umin;

@@ -252,6 +252,14 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
 // candidates at c*k, in ascending position order, so the candidate rows stay
 // in ascending original index order.  The last stage (one chunk) writes the
 // original indices of its top-k to out.
+//
+// The first stage also bounds the row's k-th key from below: chunk c writes
+// x_c, a lower bound of its ceil(k/C)-th largest key (C chunks; the waves'
+// lane-maximum bound of select_row), so at least k keys of the row are >=
+// min_c x_c.  Later stages treat keys under that minimum as unselectable:
+// their chunks hold few selectable candidates and end in select_row's
+// take-all path, and a chunk with fewer than k writes -inf after them (below
+// the floor whenever a chunk can run short).
 // ---------------------------------------------------------------------------
 constexpr int kStageChunk = 4096;
 constexpr int kStageMaxK = 1024;
@@ -260,25 +268,44 @@ __global__ __launch_bounds__(256) void topk_stage_kernel(const float* __restrict
                                                          const int32_t* __restrict__ in_idx, int64_t in_ld,
                                                          int n, int k, float* __restrict__ out_val,
                                                          int32_t* __restrict__ out_idx, int64_t out_ld,
-                                                         int32_t* __restrict__ out) {
+                                                         int32_t* __restrict__ out, uint32_t* __restrict__ bounds,
+                                                         int n_bounds, int bound_j) {
   constexpr int VPL = kStageChunk / 256;
   __shared__ int32_t sel[kStageChunk];
+  __shared__ uint32_t wave_bound[4];
   const int row = blockIdx.y, c = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int base = c * kStageChunk;
   const int len = min(kStageChunk, n - base);
   const int kc = min(k, len);
   const float* vals = in_val + static_cast<int64_t>(row) * in_ld + base;
   const int32_t* idx = in_idx ? in_idx + static_cast<int64_t>(row) * in_ld + base : nullptr;
-  select_row<VPL, false>(vals, len, kc, sel);
-  if (out) {   // last stage: original indices, ascending
+  const bool first = in_idx == nullptr;
+  uint32_t floor = 0;
+  if (!first) {   // the smallest of the first stage's chunk bounds
+    floor = 0xFFFFFFFFu;
+    for (int b = 0; b < n_bounds; ++b) floor = min(floor, bounds[static_cast<int64_t>(row) * n_bounds + b]);
+  }
+  uint32_t lane_max = 0;
+  const int kk = select_row<VPL, false>(vals, len, kc, sel, floor, &lane_max);
+  if (first && bounds) {
+    const uint32_t x = wave_lower_bound(lane_max, bound_j, wave_minmax_u32<true>(lane_max),
+                                        wave_minmax_u32<false>(lane_max != 0 ? lane_max : 0xFFFFFFFFu));
+    if (lane == 0) wave_bound[wave] = x;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      bounds[static_cast<int64_t>(row) * n_bounds + c] =
+          min(min(wave_bound[0], wave_bound[1]), min(wave_bound[2], wave_bound[3]));
+  }
+  if (out) {   // last stage: original indices, ascending (kk = k: at least k keys reach it)
     int32_t* orow = out + static_cast<int64_t>(row) * k;
-    for (int j = threadIdx.x; j < kc; j += 256) orow[j] = idx ? idx[sel[j]] : base + sel[j];
+    for (int j = threadIdx.x; j < kc; j += 256) orow[j] = j >= kk ? -1 : idx ? idx[sel[j]] : base + sel[j];
     return;
   }
   const int64_t o = static_cast<int64_t>(row) * out_ld + static_cast<int64_t>(c) * k;
   for (int j = threadIdx.x; j < kc; j += 256) {
-    const int pos = sel[j];
-    out_val[o + j] = vals[pos];
+    const int pos = j < kk ? sel[j] : 0;
+    out_val[o + j] = j < kk ? vals[pos] : -__builtin_huge_valf();
     out_idx[o + j] = idx ? idx[pos] : base + pos;
   }
 }
@@ -345,8 +372,10 @@ QKV_EXPORT int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld
 QKV_EXPORT int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
   if (rows <= 0 || n <= 0 || k < 1 || k > n) return -1;
   if (!staged(n, k)) return 0;
-  // two candidate buffers (value + index) sized for the first stage's output
-  return 2 * rows * stage_out(n, k) * static_cast<int64_t>(sizeof(float) + sizeof(int32_t));
+  // two candidate buffers (value + index) sized for the first stage's output,
+  // then the first stage's chunk bounds
+  return 2 * rows * stage_out(n, k) * static_cast<int64_t>(sizeof(float) + sizeof(int32_t)) +
+         rows * cdiv(n, kStageChunk) * static_cast<int64_t>(sizeof(uint32_t));
 }
 
 QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
@@ -369,6 +398,9 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
   idx_buf[0] = reinterpret_cast<int32_t*>(val_buf[0] + rows * n1);
   val_buf[1] = reinterpret_cast<float*>(idx_buf[0] + rows * n1);
   idx_buf[1] = reinterpret_cast<int32_t*>(val_buf[1] + rows * n1);
+  uint32_t* bounds = reinterpret_cast<uint32_t*>(idx_buf[1] + rows * n1);
+  const int n_bounds = static_cast<int>(cdiv(n, kStageChunk));
+  const int bound_j = static_cast<int>(cdiv(cdiv(k, n_bounds), 4));   // per wave; above 64: no bound
   const float* cur_val = values;
   const int32_t* cur_idx = nullptr;
   int64_t cur_ld = ld, cur_n = n;
@@ -379,7 +411,7 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
     dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
     topk_stage_kernel<<<grid, 256, 0, st>>>(cur_val, cur_idx, cur_ld, static_cast<int>(cur_n), static_cast<int>(k),
                                             last ? nullptr : val_buf[buf], last ? nullptr : idx_buf[buf], n1,
-                                            last ? out : nullptr);
+                                            last ? out : nullptr, bounds, n_bounds, bound_j);
     if (int rc = check_launch("qkv_topk_ws")) return rc;
     if (last) return QKV_OK;
     cur_val = val_buf[buf];
