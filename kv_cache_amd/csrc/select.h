@@ -294,8 +294,9 @@ struct WideSelect {
   }
 
   // A raw buffer of exactly the row's n * 4 bytes: positions past the row
-  // read 0 from the range check instead of touching memory.
-  __device__ void load(const float* __restrict__ vals, int n) {
+  // read 0 from the range check instead of touching memory.  Keys whose
+  // order-preserving value is below floor never take part.
+  __device__ void load(const float* __restrict__ vals, int n, uint32_t floor = 0) {
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
     const int base = pos(0);
@@ -308,7 +309,7 @@ struct WideSelect {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       u[i] = f32_sortable(__uint_as_float(u[i]));
-      if (FINITE && u[i] == kNegInfKey) valid &= ~(1ull << i);
+      if ((FINITE && u[i] == kNegInfKey) || u[i] < floor) valid &= ~(1ull << i);
     }
   }
 

@@ -310,6 +310,31 @@ __global__ __launch_bounds__(256) void topk_stage_kernel(const float* __restrict
   }
 }
 
+// The last stage of rows whose candidates outgrow one 4096-key chunk but fit
+// one 1024-thread workgroup (at most kWideFinal): WideSelect over the whole
+// candidate row, keys under the first stage's floor left out, in place of
+// further 4096-key stages (cfg4: one launch instead of three).
+constexpr int kWideFinal = 1024 * 40;
+
+template <int VPL>
+__global__ __launch_bounds__(1024) void topk_wide_final_kernel(const float* __restrict__ in_val,
+                                                               const int32_t* __restrict__ in_idx, int64_t in_ld,
+                                                               int n, int k, const uint32_t* __restrict__ bounds,
+                                                               int n_bounds, int32_t* __restrict__ out) {
+  using WS = WideSelect<VPL, false>;
+  __shared__ typename WS::Shared sh;
+  const int row = blockIdx.x;
+  uint32_t floor = 0xFFFFFFFFu;
+  for (int b = 0; b < n_bounds; ++b) floor = min(floor, bounds[static_cast<int64_t>(row) * n_bounds + b]);
+  WS ws;
+  ws.load(in_val + static_cast<int64_t>(row) * in_ld, n, floor);
+  const int kk = ws.run(k, sh);
+  int32_t* orow = out + static_cast<int64_t>(row) * k;
+  const int32_t* irow = in_idx + static_cast<int64_t>(row) * in_ld;
+  ws.place(sh, [&](int pos, int o, int) { orow[o] = irow[pos]; });
+  for (int o = kk + static_cast<int>(threadIdx.x); o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
+}
+
 // Candidates left after a stage over n keys: k from every full chunk, and
 // min(k, rest) from the last.
 int64_t stage_out(int64_t n, int64_t k) {
@@ -407,6 +432,17 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
   int buf = 0;
   while (true) {
     const int64_t chunks = cdiv(cur_n, kStageChunk);
+    if (cur_idx && chunks > 1 && cur_n <= kWideFinal) {   // the rest in one 1024-thread workgroup per row
+      const unsigned wg = static_cast<unsigned>(rows);
+      const int nn = static_cast<int>(cur_n), kk = static_cast<int>(k);
+      if (cur_n <= 16 * 1024)
+        topk_wide_final_kernel<16><<<wg, 1024, 0, st>>>(cur_val, cur_idx, cur_ld, nn, kk, bounds, n_bounds, out);
+      else if (cur_n <= 32 * 1024)
+        topk_wide_final_kernel<32><<<wg, 1024, 0, st>>>(cur_val, cur_idx, cur_ld, nn, kk, bounds, n_bounds, out);
+      else
+        topk_wide_final_kernel<40><<<wg, 1024, 0, st>>>(cur_val, cur_idx, cur_ld, nn, kk, bounds, n_bounds, out);
+      return check_launch("qkv_topk_ws");
+    }
     const bool last = chunks == 1;
     dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
     topk_stage_kernel<<<grid, 256, 0, st>>>(cur_val, cur_idx, cur_ld, static_cast<int>(cur_n), static_cast<int>(k),
