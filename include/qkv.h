@@ -170,14 +170,17 @@ int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k
 
 /* Bytes of workspace qkv_topk_ws needs: 0 when qkv_topk's one workgroup per
  * row is used (n <= 4096 or k > 1024), else two candidate buffers of
- * rows * (k * ceil(n/4096)) (value, index) pairs; -1 for bad sizes. */
+ * rows * (k * ceil(n/4096)) (value, index) pairs and rows * ceil(n/4096)
+ * uint32 chunk bounds; -1 for bad sizes. */
 int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 
 /* qkv_topk with a caller-owned workspace (16-byte aligned, contents
  * irrelevant): rows longer than 4096 keys with k <= 1024 are reduced in
- * stages, each 4096-key chunk keeping its local top-k, until one chunk is
- * left; the result equals qkv_topk's.  Same replaced call sites as
- * qkv_topk (EV:4448 token-level top-k over long contexts). */
+ * stages, each 4096-key chunk keeping its local top-k, until the candidates
+ * fit one chunk or one 1024-thread workgroup (40960); keys below a lower
+ * bound of the row's k-th key, taken in the first stage, are left out after
+ * it.  The result equals qkv_topk's.  Same replaced call sites as qkv_topk
+ * (EV:4448 token-level top-k over long contexts). */
 int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
