@@ -122,10 +122,13 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* __restrict__ valu
 }
 
 // Rows of at most 64*VPL keys: one wave per row, four rows per workgroup,
-// no workgroup barrier.  Lane l holds keys l + 64i (i < VPL); the radix
-// select uses a wave-private 256-bin LDS histogram (a wave's LDS operations
-// complete in order) and a DPP scan; the compaction is ballots and popcounts
-// over the slots in index order.  Same contract as select_row.
+// no workgroup barrier.  Lane l holds the VPL consecutive keys from l*VPL
+// (16-byte loads where the row allows), so the output, in index order, is
+// lane order: a lane's taken keys go after those of the lanes before it (one
+// DPP scan of per-lane counts) instead of a ballot round per slot.  The
+// radix select uses a wave-private 256-bin LDS histogram (a wave's LDS
+// operations complete in order) and a DPP scan.  With many rows the kernel
+// is bound by instruction issue, not latency.  Same contract as select_row.
 template <int VPL, bool FINITE>
 __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict__ values, int64_t rows, int n,
                                                         int64_t ld, int k, int32_t* __restrict__ out) {
@@ -138,11 +141,24 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
 
   uint32_t u[VPL];
   bool valid[VPL];
+  const int first = lane * VPL;
+  if (VPL % 4 == 0 && n == 64 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // wave-uniform
+#pragma unroll
+    for (int i = 0; i < VPL; i += 4) {
+      const uint4 w = *reinterpret_cast<const uint4*>(vals + first + i);
+      u[i] = w.x;
+      u[i + 1] = w.y;
+      u[i + 2] = w.z;
+      u[i + 3] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) u[i] = __float_as_uint(vals[min(first + i, n - 1)]);
+  }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int idx = i * 64 + lane;
-    u[i] = f32_sortable(vals[min(idx, n - 1)]);
-    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey);
+    u[i] = f32_sortable(__uint_as_float(u[i]));
+    valid[i] = first + i < n && (!FINITE || u[i] != kNegInfKey);
   }
   uint32_t umax = 0, umin = 0xFFFFFFFFu;
   int nval = 0;
@@ -214,20 +230,28 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
   }
   const uint32_t theta = prefix;
 
-  const uint64_t below = (1ull << lane) - 1ull;
   int32_t* orow = out + row * k;
-  int ngt = 0, neq = 0;   // keys > theta and == theta in earlier slots
+  // Keys > theta and == theta of this lane, then of the lanes before it; the
+  // lane takes its first min(ce, kr - eq_before) keys equal to theta.
+  uint32_t gtm = 0, eqm = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const uint64_t bgt = __ballot(valid[i] && u[i] > theta);
-    const uint64_t beq = __ballot(valid[i] && u[i] == theta);
-    const bool gt = (bgt >> lane) & 1ull;
-    const bool eq = (beq >> lane) & 1ull;
-    const bool take = gt || (eq && neq + __popcll(beq & below) < kr);
-    const uint64_t tb = __ballot(take);
-    if (take) orow[ngt + min(neq, kr) + __popcll(tb & below)] = i * 64 + lane;
-    ngt += __popcll(bgt);
-    neq += __popcll(beq);
+    gtm |= static_cast<uint32_t>(valid[i] && u[i] > theta) << i;
+    eqm |= static_cast<uint32_t>(valid[i] && u[i] == theta) << i;
+  }
+  const int cg = __popc(gtm), ce = __popc(eqm);
+  const int gt_before = wave_incl_scan_dpp(cg) - cg;
+  const int eq_before = wave_incl_scan_dpp(ce) - ce;
+  const int eq_take = min(ce, max(kr - eq_before, 0));
+  int o = gt_before + min(eq_before, kr);
+  int eq_seen = 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const bool gt = (gtm >> i) & 1u, eq = (eqm >> i) & 1u;
+    const bool take = gt || (eq && eq_seen < eq_take);
+    if (take) orow[o] = first + i;
+    o += take ? 1 : 0;
+    eq_seen += eq ? 1 : 0;
   }
   for (int j = kk + lane; j < k; j += 64) orow[j] = -1;
 }

@@ -236,6 +236,26 @@ def test_topk_adversarial_layouts(n, k):
     assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
 
 
+@pytest.mark.parametrize("n,k,ld", [(1024, 64, 1024), (1024, 1, 1025), (1000, 100, 1000), (200, 64, 203),
+                                    (513, 7, 513)])
+def test_topk_many_short_rows(n, k, ld):
+    # >= 1024 rows of <= 1024 keys take the one-wave-per-row kernel (16-byte
+    # loads only for full, aligned rows); ties, signed zeros and -inf rows.
+    rows = 1100
+    g = torch.Generator().manual_seed(n * 7 + k)
+    base = torch.randn((rows, ld), generator=g)
+    base[::3] = torch.randint(-4, 4, (len(range(0, rows, 3)), ld), generator=g).float()   # heavy ties
+    base[1::7, : n // 2] = -float("inf")
+    base[2::11] = 0.0
+    base[2::22] = -0.0
+    vals = base[:, :n]
+    dev = base.to(DEV)[:, :n]   # rows ld apart on the device too
+    got = K.block_topk(dev, k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+    got = P.block_topk(dev, k).cpu().numpy()   # -inf keys not selectable, -1 padding
+    assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
+
+
 def test_topk_strided_rows():
     g = torch.Generator().manual_seed(3)
     base = torch.randint(0, 4, (4, 300), generator=g).float().to(DEV)
