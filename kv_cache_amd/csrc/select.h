@@ -71,14 +71,16 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
 }
 
 // Rows of at most 256*VPL keys: one workgroup of 4 waves per row.  Thread t
-// holds keys t + 256i (i < VPL) as order-preserving uint32, loaded without
-// branches so that every load is in flight at once.  The bits shared by the
+// holds the VPL consecutive keys from t*VPL as order-preserving uint32
+// (16-byte loads where the row allows), loaded without branches so that
+// every load is in flight at once.  The bits shared by the
 // row's largest and smallest key are skipped; the rest are resolved 8 bits
 // at a time with per-wave 256-bin histograms that wave 0 sums, scans with
 // DPP and clears again for the next digit (two barriers per digit).
-// Output positions follow index order: the keys taken before slot (i, wave)
-// are the keys > theta before it plus min(kr, keys == theta before it), both
-// known from per-(slot, wave) ballot counts, so one pass places every key.
+// Output positions follow index order, which is thread order: the keys taken
+// before thread t's are the keys > theta of threads before it plus min(kr,
+// keys == theta of threads before it), one workgroup scan of per-thread
+// counts, and each thread writes its own taken keys in turn.
 // A row is one workgroup and so runs on few waves: the code keeps the wave
 // index scalar and avoids per-slot branches, since every dependent
 // instruction's latency is exposed.
@@ -96,10 +98,9 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
 template <int VPL, bool FINITE>
 __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
                           uint32_t* lane_max_out = nullptr) {
-  static_assert(4 * VPL <= 64, "one lane per (slot, wave) count");
+  static_assert(VPL <= 32, "one mask bit per key of a thread");
   __shared__ __attribute__((aligned(16))) int hist[4][260];   // one copy per wave, padded across banks
-  __shared__ int32_t spare[64];   // where lanes that place nothing write
-  __shared__ int cnt_gt[VPL * 4], cnt_eq[VPL * 4];
+  __shared__ int wave_cnt[4][2];
   __shared__ uint32_t red[4][4];
   __shared__ int sh_bin, sh_kr, sh_whole;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -107,11 +108,24 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
 
   uint32_t u[VPL];
   bool valid[VPL];
+  const int first = tid * VPL;
+  if (VPL % 4 == 0 && n == 256 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // uniform
+#pragma unroll
+    for (int i = 0; i < VPL; i += 4) {
+      const uint4 w = *reinterpret_cast<const uint4*>(vals + first + i);
+      u[i] = w.x;
+      u[i + 1] = w.y;
+      u[i + 2] = w.z;
+      u[i + 3] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) u[i] = __float_as_uint(vals[min(first + i, n - 1)]);
+  }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int idx = i * 256 + tid;
-    u[i] = f32_sortable(vals[min(idx, n - 1)]);
-    valid[i] = idx < n && (!FINITE || u[i] != kNegInfKey) && u[i] >= floor;
+    u[i] = f32_sortable(__uint_as_float(u[i]));
+    valid[i] = first + i < n && (!FINITE || u[i] != kNegInfKey) && u[i] >= floor;
   }
 #pragma unroll
   for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
@@ -212,40 +226,36 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   }
   const uint32_t theta = prefix;
 
-  // Per-(slot, wave) counts of keys > theta and == theta, in output order
-  // j = 4*slot + wave (lane i of each wave writes its slot i's counts); one
-  // DPP scan over j gives each (slot, wave) the counts before it.
-  int my_gt = 0, my_eq = 0;
+  // Keys > theta and == theta of this thread, then of the threads before
+  // it; the thread takes its first min(ce, kr - eq_before) keys equal to theta.
+  uint32_t gtm = 0, eqm = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int g = __popcll(__ballot(valid[i] && u[i] > theta));
-    const int e = __popcll(__ballot(valid[i] && u[i] == theta));
-    my_gt = lane == i ? g : my_gt;
-    my_eq = lane == i ? e : my_eq;
+    gtm |= static_cast<uint32_t>(valid[i] && u[i] > theta) << i;
+    eqm |= static_cast<uint32_t>(valid[i] && u[i] == theta) << i;
   }
-  if (lane < VPL) {
-    cnt_gt[4 * lane + wave] = my_gt;
-    cnt_eq[4 * lane + wave] = my_eq;
+  const int cg = __popc(gtm), ce = __popc(eqm);
+  const int ig = wave_incl_scan_dpp(cg), ie = wave_incl_scan_dpp(ce);
+  if (lane == 63) {
+    wave_cnt[wave][0] = ig;
+    wave_cnt[wave][1] = ie;
   }
   __syncthreads();
-  const int cg = lane < 4 * VPL ? cnt_gt[lane] : 0;
-  const int ce = lane < 4 * VPL ? cnt_eq[lane] : 0;
-  const int gt_excl = wave_incl_scan_dpp(cg) - cg;
-  const int eq_excl = wave_incl_scan_dpp(ce) - ce;
+  int gt_before = ig - cg, eq_before = ie - ce;
+#pragma unroll
+  for (int w = 0; w < 3; ++w) {
+    gt_before += w < wave ? wave_cnt[w][0] : 0;
+    eq_before += w < wave ? wave_cnt[w][1] : 0;
+  }
+  const int eq_take = min(ce, max(kr - eq_before, 0));
+  int o = gt_before + min(eq_before, kr), eq_seen = 0;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int g0 = __builtin_amdgcn_readlane(gt_excl, 4 * i + wave);
-    const int e0 = __builtin_amdgcn_readlane(eq_excl, 4 * i + wave);
-    const bool gt = valid[i] && u[i] > theta;
-    const bool eq = valid[i] && u[i] == theta;
-    const uint64_t be = __ballot(eq);
-    const int eq_before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(be >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(be), 0));
-    const bool take = gt || (eq && e0 + eq_before < kr);
-    const uint64_t tb = __ballot(take);
-    const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(tb >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(tb), 0));
-    *(take ? &sel[g0 + min(e0, kr) + before] : &spare[lane]) = i * 256 + tid;   // no branch per slot
+    const bool gt = (gtm >> i) & 1u, eq = (eqm >> i) & 1u;
+    const bool take = gt || (eq && eq_seen < eq_take);
+    if (take) sel[o] = first + i;
+    o += take ? 1 : 0;
+    eq_seen += eq ? 1 : 0;
   }
   __syncthreads();
   return kk;
