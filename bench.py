@@ -522,7 +522,7 @@ def cpu_baseline_reuse(budget_s: float, steps: int = 3) -> dict:
     t = c["history"] + steps + 1
     k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
     v = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
-    dims, cand, _, _ = parse_reuse_mode(c["mode"])
+    dims, cand, _, _, _ = parse_reuse_mode(c["mode"])
     pc = pf = None
     times = []
     t_end = time.perf_counter() + budget_s
@@ -638,7 +638,7 @@ def run_reuse(args) -> dict:
     log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
 
     mask_ws = [steps[l].mask_ws for l in range(layers)]
-    s_dims, cand_frac, _, _ = RU.parse_reuse_mode(c["mode"])
+    s_dims, cand_frac, _, _, _ = RU.parse_reuse_mode(c["mode"])
     requested = RU.budget_count(hist_fixed, cand_frac)
 
     def run_partial():

@@ -279,6 +279,34 @@ int qkv_reuse_select(const void* query, const void* key, const int64_t* k_stride
                      int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                      uint8_t* history_final, int64_t history_final_ld, void* stream);
 
+/* Entries per row of the final index list of a block-expanded reuse step
+ * (the qabs{S}cand{pct}reuse[final|2set]blk{block} modes): body + sink
+ * range + recent range (not overlapping the sink) + 1 when keep_self, where
+ * body = min(history positions outside the protected ranges,
+ * keep * block + 2 * (block - 1)) bounds the expanded selection outside the
+ * protected ranges.  -1 for history <= 0 or block < 1. */
+int64_t qkv_reuse_block_final_count(int64_t history, int64_t block, int64_t protect_sink,
+                                    int64_t protect_recent, double top_fraction, int keep_self);
+
+/* Block expansion of a reuse step's final selection, replacing the
+ * reference's mask-level steps for the blk modes (EV:4314-4316:
+ * _expand_history_keep_to_aligned_blocks EV:2914-2922, then the selection
+ * re-read by _indices_from_keep_mask EV:2896-2911 and the final list of
+ * EV:2938-2982).  history_final [rows, history] (row stride
+ * history_final_ld, as qkv_reuse_select left it) is expanded in place:
+ * every aligned block of `block` positions (1 <= block <= 4096; the last
+ * block cut at the history) that holds a set flag becomes wholly set.
+ * final_indices / final_valid / attn_ids (optional) [rows, n_out] are
+ * rewritten: the expanded positions outside the sink and recent ranges in
+ * ascending order (the reference lists them descending; the set is the
+ * same), padded to the body bound of qkv_reuse_block_final_count with
+ * (0, invalid, -1), then the sink range, the recent range and the current
+ * token key_count - 1 (when keep_self). */
+int qkv_reuse_expand_blocks(uint8_t* history_final, int64_t history_final_ld, int64_t rows, int64_t key_count,
+                            int64_t block, int64_t protect_sink, int64_t protect_recent, double top_fraction,
+                            int keep_self, int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                            int64_t n_out, void* stream);
+
 /* Partial scores of the reuse step (EV:4123-4135 on the dim-major copy,
  * partial_scores_dim_major QK:63-96 with the dims of QK:120-145): for each
  * row, the top-|q| dim_count dims (descending |q|, lower dim first on ties,

@@ -375,6 +375,86 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block expansion of the final selection (the reuse...blk{bs} modes,
+// EV:4314-4316 with EV:2914-2922) and the final index list re-read from the
+// expanded mask (EV:2896-2911, 2938-2982).  One workgroup per row walks the
+// row in tiles of whole blocks (at most kExpandTile positions): the tile's
+// flags go to LDS, each thread that holds a set flag marks its block, the
+// expanded flags go back to the mask in place, and the positions outside
+// the protected ranges are numbered by a workgroup scan (each thread takes
+// consecutive positions) and listed in ascending order.  The list holds at
+// most body_cap entries, padded with (0, invalid, -1); the sink range, the
+// recent range and the current token follow.
+// ---------------------------------------------------------------------------
+constexpr int kExpandTile = 4096;
+
+__global__ __launch_bounds__(kRT) void reuse_expand_kernel(
+    uint8_t* __restrict__ hf, int64_t hf_ld, int history, int block, int tile, int body_cap, int key_count,
+    int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
+    uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out) {
+  __shared__ uint8_t flags[kExpandTile];
+  __shared__ uint8_t hit[kExpandTile];   // one flag per block of the tile
+  __shared__ int wave_tot[kRT / 64];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  const int64_t o = static_cast<int64_t>(row) * n_out;
+  const int nblk = tile / block;
+  int base = 0;   // body entries listed so far
+  for (int t0 = 0; t0 < history; t0 += tile) {
+    const int len = min(tile, history - t0);
+    for (int i = tid; i < len; i += kRT) flags[i] = hrow[t0 + i];
+    for (int i = tid; i < nblk; i += kRT) hit[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < len; i += kRT)
+      if (flags[i]) hit[i / block] = 1;
+    __syncthreads();
+    for (int i = tid; i < len; i += kRT) hrow[t0 + i] = hit[i / block];
+    const int c = (len + kRT - 1) / kRT;
+    const int lo = min(tid * c, len), hi = min(lo + c, len);
+    int cnt = 0;
+    for (int i = lo; i < hi; ++i) {
+      const int t = t0 + i;
+      cnt += (hit[i / block] && t >= sink_end && t < recent_start) ? 1 : 0;
+    }
+    const int incl = wave_incl_scan_dpp(cnt);
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int p = base + incl - cnt, total = 0;
+#pragma unroll
+    for (int w = 0; w < kRT / 64; ++w) {
+      p += w < wave ? wave_tot[w] : 0;
+      total += wave_tot[w];
+    }
+    for (int i = lo; i < hi; ++i) {
+      const int t = t0 + i;
+      if (hit[i / block] && t >= sink_end && t < recent_start) {
+        if (p < body_cap) {
+          final_idx[o + p] = t;
+          final_valid[o + p] = 1;
+          if (attn_ids) attn_ids[o + p] = t;
+        }
+        ++p;
+      }
+    }
+    base += total;
+    __syncthreads();   // the next tile reuses flags, hit and wave_tot
+  }
+  for (int p = min(base, body_cap) + tid; p < body_cap; p += kRT) {
+    final_idx[o + p] = 0;
+    final_valid[o + p] = 0;
+    if (attn_ids) attn_ids[o + p] = -1;
+  }
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kRT) {
+    const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+    final_idx[o + body_cap + i] = idx;
+    final_valid[o + body_cap + i] = 1;
+    if (attn_ids) attn_ids[o + body_cap + i] = idx;
+  }
+}
+
 // VPL for a row of n values: 16, 32 or 40 (n <= kWideMax).
 template <typename F>
 int with_wide_vpl(int64_t n, F&& f) {
@@ -429,6 +509,16 @@ ReuseCounts reuse_counts(int64_t history, int64_t sink, int64_t recent, double t
   c.n_rec = (recent > 0 && c.rec_begin < history) ? history - c.rec_begin : 0;
   c.n_out = c.keep + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
   return c;
+}
+
+// Entries of the body of a block-expanded final list: the expanded
+// selection outside the protected ranges [0, sink_end) and
+// [recent_start, history).  Each of the keep selections adds at most one
+// block, and the blocks that hold the ends of the two protected ranges add at
+// most block - 1 positions each.
+int64_t block_body_cap(const ReuseCounts& c, int64_t block) {
+  const int64_t open = std::max<int64_t>(0, c.recent_start - c.sink_end);
+  return std::min(open, c.keep * block + 2 * (block - 1));
 }
 
 constexpr int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -574,6 +664,42 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
       static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
       static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
       history_final, history_final_ld);
+  return check_launch(what);
+}
+
+QKV_EXPORT int64_t qkv_reuse_block_final_count(int64_t history, int64_t block, int64_t protect_sink,
+                                               int64_t protect_recent, double top_fraction, int keep_self) {
+  if (history <= 0 || block < 1) return -1;
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
+  return block_body_cap(c, block) + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+}
+
+QKV_EXPORT int qkv_reuse_expand_blocks(uint8_t* history_final, int64_t history_final_ld, int64_t rows,
+                                       int64_t key_count, int64_t block, int64_t protect_sink,
+                                       int64_t protect_recent, double top_fraction, int keep_self,
+                                       int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                                       int64_t n_out, void* stream) {
+  const char* what = "qkv_reuse_expand_blocks";
+  if (!history_final || !final_indices || !final_valid) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (rows <= 0 || rows > 65535) return fail(QKV_ERR_INVALID, "%s: need 1 <= rows <= 65535", what);
+  const int64_t history = key_count - 1;
+  if (history <= 0 || key_count >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 (history excludes the current token)", what);
+  if (history_final_ld < history) return fail(QKV_ERR_INVALID, "%s: mask row stride must cover the history", what);
+  if (block < 1 || block > kExpandTile) return fail(QKV_ERR_INVALID, "%s: block must be in [1, %d]", what, kExpandTile);
+  if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
+  const int64_t body = block_body_cap(c, block);
+  const int64_t need = body + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+  if (n_out != need)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the expanded selection needs %lld", what,
+                (long long)n_out, (long long)need);
+  const int64_t tile = block * (kExpandTile / block);
+  reuse_expand_kernel<<<static_cast<unsigned>(rows), kRT, 0, static_cast<hipStream_t>(stream)>>>(
+      history_final, history_final_ld, static_cast<int>(history), static_cast<int>(block), static_cast<int>(tile),
+      static_cast<int>(body), static_cast<int>(key_count), static_cast<int>(c.sink_end),
+      static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin), static_cast<int>(c.n_rec), keep_self ? 1 : 0,
+      final_indices, final_valid, attn_ids, static_cast<int>(n_out));
   return check_launch(what);
 }
 

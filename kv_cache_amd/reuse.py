@@ -1,5 +1,5 @@
 """Candidate reuse and exact rerank: the reference's
-``qabs{S}cand{pct}reuse[final|2set]`` decode step on MI355X.
+``qabs{S}cand{pct}reuse[final|2set][blk{bs}]`` decode step on MI355X.
 
 Per layer and decode token the reference (``_qabs_reuse_fast_attention_forward``,
 evaluate_qwen3_top2_head_limit3_ppl.py:3991-4397, "EV") scores every history
@@ -13,7 +13,8 @@ The previous masks live in ``ReuseCandidateState`` (EV:1596-1759).
 ``ReuseDecodeStep`` runs that step with libqkv kernels on GQA-shaped K/V (no
 ``repeat_interleave``): the dim-major K copy for the partial scores
 (``qkv_dim_major_append``, EV:2018-2042), ``qkv_reuse_partial_scores``,
-``qkv_threshold_mask``, ``qkv_reuse_select`` and ``qkv_token_attention``.
+``qkv_threshold_mask``, ``qkv_reuse_select`` (+ ``qkv_reuse_expand_blocks``
+for the blk modes) and ``qkv_token_attention``.
 The masks stay on the GPU in capacity-sized buffers; nothing is allocated per
 step once the step is built.
 """
@@ -44,17 +45,21 @@ def budget_count(history: int, fraction: float) -> int:
     return min(int(history), max(1, math.ceil(float(fraction) * int(history))))
 
 
-def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool]:
-    """``qabs{S}cand{pct}reuse[final|2set]`` -> (S, candidate fraction, use the
-    previous candidates, use the previous final selection).  The percentage
-    takes ``p`` as the decimal point (``cand6p25`` = 6.25 %), as
-    ``parse_qabs_partial_rerank_params`` reads it (EV:748-754); ``reusefinal``
-    drops the previous candidates and ``reuse2set`` the previous final
-    selection (EV:955-960).  Block-expanded (``blk``) modes are not built."""
-    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)reuse(2set|final)?", mode)
-    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}reuse[final|2set] mode")
+def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool, int | None]:
+    """``qabs{S}cand{pct}reuse[final|2set][blk{bs}]`` -> (S, candidate
+    fraction, use the previous candidates, use the previous final selection,
+    block size or None).  The percentage takes ``p`` as the decimal point
+    (``cand6p25`` = 6.25 %), as ``parse_qabs_partial_rerank_params`` reads it
+    (EV:748-754).  A mode ending in ``reusefinal`` drops the previous
+    candidates and one ending in ``reuse2set`` the previous final selection
+    (EV:955-960): the reference tests the suffix, so a ``finalblk`` or
+    ``2setblk`` mode keeps both.  ``blk{bs}`` expands the final selection to
+    aligned blocks of max(1, bs) positions (EV:757-761, 4314-4316)."""
+    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)reuse(2set|final)?(?:blk(\d+))?", mode)
+    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}reuse[final|2set][blk{{bs}}] mode")
     frac = float(m.group(2).replace("p", ".")) / 100.0
-    return int(m.group(1)), frac, m.group(3) != "final", m.group(3) != "2set"
+    block = max(1, int(m.group(4))) if m.group(4) is not None else None
+    return int(m.group(1)), frac, not mode.endswith("reusefinal"), not mode.endswith("reuse2set"), block
 
 
 def reuse_partial_scores(query: torch.Tensor, key_dim_major: torch.Tensor, history: int, dim_count: int, *,
@@ -92,6 +97,33 @@ def threshold_mask(values: torch.Tensor, n: int, k: int, mask: torch.Tensor, wor
                                           mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
                                           workspace.numel() * 4, _lib.stream_of(values)))
     return mask
+
+
+def expand_blocks(history_final: torch.Tensor, key_count: int, block: int, protect_sink: int, protect_recent: int,
+                  top_fraction: float, keep_self: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Expands the final mask (uint8 [rows, >= history], in place) to whole
+    aligned blocks and returns the final list (int64 indices, bool validity,
+    int32 attention ids), [rows, n] with n from
+    ``qkv_reuse_block_final_count`` (EV:4314-4316, 2914-2922, 2938-2982)."""
+    lib = _lib.load()
+    history = int(key_count) - 1
+    _require(history_final.is_cuda and history_final.dtype == torch.uint8 and history_final.dim() == 2
+             and history_final.stride(1) == 1 and history_final.size(1) >= history,
+             "history_final must be CUDA uint8 [rows, >= history]")
+    rows = history_final.size(0)
+    n = int(lib.qkv_reuse_block_final_count(history, int(block), int(protect_sink), int(protect_recent),
+                                            float(top_fraction), int(keep_self)))
+    _require(n >= 0, "need history >= 1 and block >= 1")
+    dev = history_final.device
+    idx = torch.empty((rows, n), dtype=torch.int64, device=dev)
+    valid = torch.empty((rows, n), dtype=torch.uint8, device=dev)
+    ids = torch.empty((rows, n), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.qkv_reuse_expand_blocks(
+            history_final.data_ptr(), history_final.stride(0), rows, int(key_count), int(block), int(protect_sink),
+            int(protect_recent), float(top_fraction), int(keep_self), idx.data_ptr(), valid.data_ptr(),
+            ids.data_ptr(), n, _lib.stream_of(history_final)))
+    return idx, valid.view(torch.bool), ids
 
 
 def dim_major_append(key: torch.Tensor, key_dim_major: torch.Tensor, t_begin: int, t_end: int) -> None:
@@ -146,7 +178,9 @@ class ReuseDecodeStep:
         lib = _lib.load()
         self.device = device
         self.mode = mode
-        self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final = parse_reuse_mode(mode)
+        (self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final,
+         self.block) = parse_reuse_mode(mode)
+        _require(self.block is None or self.block <= 4096, "reuse blocks hold at most 4096 tokens")
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
         self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
         self.capacity = int(capacity)
@@ -160,9 +194,9 @@ class ReuseDecodeStep:
         self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
         hist_max = cap - 1
-        # every term of the count grows with the history
-        self.n_out_max = int(lib.qkv_reuse_final_count(hist_max, self.sink, self.recent, self.top_fraction,
-                                                       int(self.keep_self)))
+        # every term of the counts grows with the history
+        self.n_out_max = max(self._final_count(hist_max), int(lib.qkv_reuse_final_count(
+            hist_max, self.sink, self.recent, self.top_fraction, int(self.keep_self))))
         self.final_idx = torch.empty(rows * self.n_out_max, dtype=torch.int64, device=device)
         self.final_valid = torch.empty(rows * self.n_out_max, dtype=torch.uint8, device=device)
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
@@ -174,6 +208,15 @@ class ReuseDecodeStep:
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
         self.reset()
+
+    def _final_count(self, history: int) -> int:
+        """Entries per row of the step's final index list."""
+        lib = _lib.load()
+        if self.block is None:
+            return int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction,
+                                                 int(self.keep_self)))
+        return int(lib.qkv_reuse_block_final_count(history, self.block, self.sink, self.recent, self.top_fraction,
+                                                   int(self.keep_self)))
 
     def _ws(self, nbytes: int) -> torch.Tensor:
         _require(nbytes >= 0, "bad workspace size")
@@ -236,7 +279,8 @@ class ReuseDecodeStep:
         requested = budget_count(history, self.cand_fraction)
         self.mask_ws = self._grow(self.mask_ws, lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
         threshold_mask(self.partial, history, requested, current, self.mask_ws)
-        n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
+        n_sel = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
+        n_out = self._final_count(history)
         self.select_ws = self._grow(self.select_ws,
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
         ids = self.attn_ids[: self.rows * n_out]
@@ -246,8 +290,14 @@ class ReuseDecodeStep:
                 self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
                 _lib.ptr(previous_final), self.capacity, self.sink, self.recent, self.top_fraction,
                 int(self.keep_self), float(scaling), self.select_ws.data_ptr(), self.select_ws.numel() * 4,
-                self.final_idx.data_ptr(), self.final_valid.data_ptr(), ids.data_ptr(), n_out, self.fin.data_ptr(),
-                self.capacity, _lib.stream_of(q)))
+                self.final_idx.data_ptr(), self.final_valid.data_ptr(),
+                ids.data_ptr() if self.block is None else None, n_sel, self.fin.data_ptr(), self.capacity,
+                _lib.stream_of(q)))
+            if self.block is not None:   # EV:4314-4316: the final selection grows to whole blocks
+                _lib.check(lib.qkv_reuse_expand_blocks(
+                    self.fin.data_ptr(), self.capacity, self.rows, key_count, self.block, self.sink, self.recent,
+                    self.top_fraction, int(self.keep_self), self.final_idx.data_ptr(), self.final_valid.data_ptr(),
+                    ids.data_ptr(), n_out, _lib.stream_of(q)))
         token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
         self.n_out = n_out
 

@@ -263,8 +263,38 @@ def final_indices_np(selected, selected_valid, history: int, key_count: int, sin
     return np.concatenate(parts, axis=-1).astype(np.int64), np.concatenate(vparts, axis=-1)
 
 
+def expand_to_blocks(keep, block):
+    """EV:2914-2922: every aligned block of ``block`` history positions
+    (block j = positions [j*block, (j+1)*block), the last one cut at the
+    history) that holds a set flag becomes wholly set.  Unchanged for
+    ``block`` None or <= 1, or a history of at most one position."""
+    m = np.asarray(keep, dtype=bool)
+    history = m.shape[-1]
+    if block is None or block <= 1 or history <= 1:
+        return m.copy()
+    blocks = -(-history // block)
+    padded = np.zeros((*m.shape[:-1], blocks * block), dtype=bool)
+    padded[..., :history] = m
+    hit = padded.reshape(*m.shape[:-1], blocks, block).any(axis=-1)
+    return np.repeat(hit, block, axis=-1)[..., :history]
+
+
+def indices_from_keep_mask(keep):
+    """EV:2896-2911: the set positions of each row in descending order,
+    padded to the largest count over the rows with (0, invalid)."""
+    m = np.asarray(keep, dtype=bool)
+    width = int(m.sum(axis=-1).max()) if m.size else 0
+    idx = np.zeros((*m.shape[:-1], width), dtype=np.int64)
+    valid = np.zeros((*m.shape[:-1], width), dtype=bool)
+    for lead in np.ndindex(*m.shape[:-1]):
+        pos = np.flatnonzero(m[lead])[::-1]
+        idx[lead][: len(pos)] = pos
+        valid[lead][: len(pos)] = True
+    return idx, valid
+
+
 def reuse_select(query, key_states, current, previous, previous_final, sink: int, recent: int,
-                 top_fraction: float, keep_self: bool, scaling: float):
+                 top_fraction: float, keep_self: bool, scaling: float, block: int | None = None):
     """The selection the reference asks of its absent ``reuse_select`` kernel
     (called at EV:3901-3914 with the signature of EV:3881-3892), restated from
     the fallback that runs when the kernel is missing (EV:4257-4365, no
@@ -277,13 +307,17 @@ def reuse_select(query, key_states, current, previous, previous_final, sink: int
       ``torch.topk``, ties here to the lower index), valid where finite;
     * history_final: the valid selections, then the sink and recent ranges
       set (EV:4301-4307);
+    * with ``block`` (the ``reuse…blk{block}`` modes, EV:4022, 4314-4316):
+      history_final expanded to whole aligned blocks (``expand_to_blocks``)
+      and the selection re-read from it (``indices_from_keep_mask``);
     * final indices and validity by ``final_indices_np`` (EV:4365, 2938-2982).
 
     query [B,H,D]; key_states [B,H,K,D] with K = history + 1; masks bool
-    [B,H,history] (previous ones may be None).  Selected indices come in
-    ascending order (the reference's come in descending score order; only the
-    set and its validity carry meaning).  Returns (final_indices int64,
-    final_valid bool, history_final bool [B,H,history]).
+    [B,H,history] (previous ones may be None).  Without ``block`` the
+    selected indices come in ascending order (the reference's come in
+    descending score order; only the set and its validity carry meaning).
+    Returns (final_indices int64, final_valid bool, history_final bool
+    [B,H,history]).
     """
     from .qkv_oracle import topk_lowest_index
 
@@ -304,15 +338,19 @@ def reuse_select(query, key_states, current, previous, previous_final, sink: int
         hist_final[..., : min(sink, history)] = True
     if recent > 0:
         hist_final[..., max(0, history - recent):] = True
+    if block is not None:
+        hist_final = expand_to_blocks(hist_final, block)
+        sel, valid = indices_from_keep_mask(hist_final)
     fi, fv = final_indices_np(sel, valid, history, key_count, sink, recent, keep_self)
     return fi, fv, hist_final
 
 
 def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: float, top_fraction: float,
                       sink: int, recent: int, keep_self: bool, scaling: float,
-                      previous_candidate=None, previous_final=None):
+                      previous_candidate=None, previous_final=None, block: int | None = None):
     """One decode step of ``_qabs_reuse_fast_attention_forward`` (EV:3991-4397)
-    for the default candidate selection (``topk``) without block expansion.
+    for the default candidate selection (``topk``), block-expanded when
+    ``block`` is given (``reuse…blk{block}``, EV:757-761, 4314-4316).
 
     query [B,Hq,D]; key/value [B,Hkv,T,D] (query head h reads KV head
     h // (Hq/Hkv), the grouping of EV:6248-6251).  previous_* are the masks
@@ -351,20 +389,21 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
         return np.concatenate([m, np.zeros((*m.shape[:-1], pad), dtype=bool)], axis=-1) if pad else m
 
     fi, fv, hist_final = reuse_select(q, kx, current, fit(previous_candidate), fit(previous_final), sink, recent,
-                                      top_fraction, keep_self, scaling)
+                                      top_fraction, keep_self, scaling, block)
     out = final_attention(q, kx, vx, fi, fv, scaling)
     return out, current, hist_final
 
 
 def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, candidate_fraction: float,
                         top_fraction: float, scaling: float, sink: int = 0, recent: int = 0, keep_self: bool = True,
-                        previous_candidate=None, previous_final=None):
+                        previous_candidate=None, previous_final=None, block: int | None = None):
     """One ``qabs{S}cand{pct}reuse`` decode step in the reference's PyTorch
     ops on CPU tensors: the path ``_qabs_reuse_fast_attention_forward`` takes
     when no CUDA kernel is available (EV:3991-4397 with the dense-mask
     fallbacks of EV:4161-4167, 4276-4303 and the gather attention of
-    EV:4365-4374).  It is the CPU baseline that ``bench.py`` times next to the
-    GPU reuse step.
+    EV:4365-4374), block-expanded when ``block`` is given (EV:4314-4316).
+    It is the CPU baseline that ``bench.py`` times next to the GPU reuse
+    step.
 
     query_states [B,Hq,1,D]; key/value_states [B,Hkv,T,D] (GQA-expanded
     first, EV:6248-6251); previous_* bool [B,Hq,T-1] or None.  Returns
@@ -414,6 +453,18 @@ def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, 
         history_final[:, :, : min(sink, history)] = True
     if recent > 0:
         history_final[:, :, max(0, history - recent):history] = True
+    if block is not None and block > 1 and history > 1:                                           # EV:2914-2922
+        blocks = -(-history // block)
+        padded = F.pad(history_final, (0, blocks * block - history), value=False)
+        hit = padded.view(b, hq, blocks, block).any(dim=-1, keepdim=True)
+        history_final = hit.expand(-1, -1, -1, block).reshape(b, hq, blocks * block)[..., :history]
+    if block is not None:                                                                         # EV:4316
+        width = int(history_final.sum(dim=-1).max().item())
+        pos = torch.arange(history).view(1, 1, -1).expand_as(history_final)
+        selected = torch.topk(torch.where(history_final, pos, torch.full_like(pos, -1)), k=width, dim=-1,
+                              largest=True).values
+        selected_valid = selected >= 0
+        selected = selected.clamp_min(0)
     final_idx, final_valid = final_indices_from_selected(selected, selected_valid, history, key_count, sink,
                                                          recent, keep_self)                     # EV:4365
     gather = final_idx[:, :, :, None].expand(-1, -1, -1, d)                                       # EV:4366-4374

@@ -19,7 +19,7 @@ EV:6236) on seeded synthetic q/K/V, and saves inputs and outputs:
 Run from the repository root with the reference checked out at
 /root/reference:
 
-    python tests/golden/make_reuse_vectors.py
+    python tests/golden/make_reuse_vectors.py [scenario ...]
 
 Outputs ``tests/golden/reuse_<name>.npz`` and ``tests/golden/block_<name>.npz``.
 """
@@ -42,6 +42,18 @@ SCENARIOS = {
     "s16c10_final_fp32": ("qabs16cand10reusefinal", torch.float32, 4, 2, 193, 4, 0.03, 0, 0, True, 2),
     "s8c3_2set_fp32": ("qabs8cand3reuse2set", torch.float32, 2, 1, 300, 4, 0.02, 2, 0, False, 3),
     "s8c5_bf16": ("qabs8cand5reuse", torch.bfloat16, 4, 2, 240, 4, 0.05, 3, 5, True, 4),
+    # block-expanded final selections (reuse…blk{bs}, EV:757-761, 4314-4316);
+    # the histories run across block boundaries.  EV:955-960 test the mode's
+    # suffix, so a "finalblk" or "2setblk" mode keeps both previous masks.
+    # The bf16 seed is one where no tie decides a selection: neither a bf16
+    # |q| tie at the S-th channel (torch.topk's order among ties is
+    # unspecified, the reference's kernels take the lower channel,
+    # QK:123-145) nor a tie of bf16-rounded rerank scores at the keep-th
+    # place (the CPU fallback ranks bf16 products, EV:4290-4296; its kernel
+    # ranks fp32 ones)
+    "s8c5_blk16_fp32": ("qabs8cand5reuseblk16", torch.float32, 4, 2, 240, 5, 0.05, 4, 4, True, 5),
+    "s16c10_finalblk8_bf16": ("qabs16cand10reusefinalblk8", torch.bfloat16, 4, 2, 203, 4, 0.03, 0, 6, True, 15),
+    "s8c3_2setblk32_fp32": ("qabs8cand3reuse2setblk32", torch.float32, 2, 1, 300, 4, 0.02, 3, 0, False, 7),
 }
 
 
@@ -144,16 +156,19 @@ def run_block(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, rec
     print(f"{name}: {mode} {dtype} Hq={hq} T0={t0} steps={steps} -> block_{name}.npz")
 
 
-def main():
+def main(names):
+    """Writes the named scenarios (every scenario when none is named)."""
     sys.path.insert(0, str(REF_SRC))
     import evaluate_qwen3_top2_head_limit3_ppl as ev   # the reference module, CPU only
 
     torch.set_num_threads(1)
     for name, args in SCENARIOS.items():
-        run(ev, name, *args)
+        if not names or name in names:
+            run(ev, name, *args)
     for name, args in BLOCK_SCENARIOS.items():
-        run_block(ev, name, *args)
+        if not names or name in names:
+            run_block(ev, name, *args)
 
 
 if __name__ == "__main__":
-    main()
+    main(set(sys.argv[1:]))

@@ -71,6 +71,14 @@ def _err():
                                      1, 1, 10, 0, 128, 1.0, None), "select_count must be positive"),
     (lambda: lib.qkv_partial_scores(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 7,
                                     1, 1, 10, 128, _lib.strides(1, 1, 1, 1), 8, None), "dtype"),
+    (lambda: lib.qkv_reuse_expand_blocks(None, 10, 1, 11, 4, 0, 0, 0.1, 1, ctypes.c_void_p(16),
+                                         ctypes.c_void_p(16), None, 5, None), "null pointer"),
+    (lambda: lib.qkv_reuse_expand_blocks(ctypes.c_void_p(16), 10, 1, 11, 5000, 0, 0, 0.1, 1, ctypes.c_void_p(16),
+                                         ctypes.c_void_p(16), None, 5, None), "block must be"),
+    (lambda: lib.qkv_reuse_expand_blocks(ctypes.c_void_p(16), 10, 1, 11, 4, 0, 0, 0.1, 1, ctypes.c_void_p(16),
+                                         ctypes.c_void_p(16), None, 5, None), "expanded selection needs"),
+    (lambda: lib.qkv_reuse_expand_blocks(ctypes.c_void_p(16), 8, 1, 11, 4, 0, 0, 0.1, 1, ctypes.c_void_p(16),
+                                         ctypes.c_void_p(16), None, 5, None), "stride"),
 ])
 def test_host_side_validation(call, msg):
     rc = call()
@@ -133,3 +141,20 @@ def test_python_wrappers_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="query must be CUDA"):
         Q.final_attention(q, torch.zeros(1, 2, 4, 8), torch.zeros(1, 2, 4, 8),
                           torch.zeros(1, 2, 3, dtype=torch.long), torch.ones(1, 2, 3, dtype=torch.bool), 1.0)
+
+
+def test_reuse_block_final_count():
+    # keep = ceil(0.02 * 100) = 2; body = min(open range, keep * bs + 2 * (bs - 1))
+    assert lib.qkv_reuse_block_final_count(100, 16, 0, 0, 0.02, 0) == min(100, 2 * 16 + 30)
+    # sink 4, recent 8: open range 88, body 62, + 4 + 8 + self
+    assert lib.qkv_reuse_block_final_count(100, 16, 4, 8, 0.02, 1) == 62 + 4 + 8 + 1
+    assert lib.qkv_reuse_block_final_count(1000, 64, 0, 0, 0.5, 0) == 1000
+    for hist, sink, recent, frac, ks in [(100, 4, 8, 0.02, 1), (5000, 10, 10, 0.03, 1)]:
+        # blocks of one position: the plain final list
+        assert lib.qkv_reuse_block_final_count(hist, 1, sink, recent, frac, ks) == \
+            lib.qkv_reuse_final_count(hist, sink, recent, frac, ks)
+    # a sink over the whole history leaves no body; the plain list keeps 4 invalid slots
+    assert lib.qkv_reuse_block_final_count(37, 1, 50, 0, 0.1, 0) == 37
+    assert lib.qkv_reuse_final_count(37, 50, 0, 0.1, 0) == 4 + 37
+    assert lib.qkv_reuse_block_final_count(0, 16, 0, 0, 0.1, 1) == -1
+    assert lib.qkv_reuse_block_final_count(10, 0, 0, 0, 0.1, 1) == -1

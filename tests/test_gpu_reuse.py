@@ -47,6 +47,10 @@ def test_pieces_match_reference_vectors(name):
         fi, fv, hf = Q.reuse_select(q, k, cur, pc if g["use_prev_candidate"] else None,
                                     pf if g["use_prev_final"] else None, g["sink"], g["recent"], g["top_fraction"],
                                     g["keep_self"], g["scaling"])
+        if g["block"] is not None:   # the blk modes expand the selection to whole blocks (EV:4314-4316)
+            fi, fv, _ = RU.expand_blocks(hf.view(torch.uint8).view(hq, hist), n, g["block"], g["sink"],
+                                         g["recent"], g["top_fraction"], g["keep_self"])
+            fi, fv = fi.view(1, hq, -1), fv.view(1, hq, -1)
         assert np.array_equal(hf.cpu().numpy(), g["final"][s][..., :hist]), (name, s, "final")
         out = Q.final_attention(q, k, v, fi, fv, g["scaling"])
         np.testing.assert_allclose(f32(out)[:, 0], g["out"][s], rtol=RTOL, atol=ATOL)
@@ -54,10 +58,11 @@ def test_pieces_match_reference_vectors(name):
         pc, pf = (torch.cat([m, torch.zeros_like(m[..., :1])], dim=-1) for m in (cur, hf))
 
 
-def test_step_matches_reference_vectors_bf16():
+@pytest.mark.parametrize("name", ["s8c5_bf16", "s16c10_finalblk8_bf16"])
+def test_step_matches_reference_vectors_bf16(name):
     # The GQA-native step (dim-major K, no head expansion) on the bf16
-    # scenario: the state it leaves equals the reference's at every step.
-    g = load_golden("s8c5_bf16")
+    # scenarios: the state it leaves equals the reference's at every step.
+    g = load_golden(name)
     hq, hkv = g["q"].shape[2], g["k"].shape[1]
     k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
     v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
@@ -130,10 +135,15 @@ def test_reuse_select_ties_and_missing_masks():
     (8, 2, 3000, 4, "qabs8cand5reuse"),
     (32, 8, 9000, 3, "qabs16cand10reusefinal"),
     (4, 4, 1500, 3, "qabs8cand3reuse2set"),
+    (8, 2, 3000, 4, "qabs8cand5reuseblk16"),
+    (32, 8, 9000, 3, "qabs16cand10reusefinalblk32"),
+    (4, 4, 1500, 3, "qabs8cand3reuse2setblk64"),
+    (4, 2, 1000, 3, "qabs8cand5reuseblk7"),
+    (4, 2, 50000, 2, "qabs8cand2reuseblk64"),     # staged selection, 13 expansion tiles
 ])
 def test_step_matches_oracle(hq, hkv, t, steps, mode):
     gen = torch.Generator().manual_seed(hq * t)
-    s_dims, cand, use_pc, use_pf = RU.parse_reuse_mode(mode)
+    s_dims, cand, use_pc, use_pf, block = RU.parse_reuse_mode(mode)
     k = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
     v = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
     qs = torch.randn((steps, 1, hq, 128), generator=gen).to(torch.bfloat16)
@@ -146,11 +156,64 @@ def test_step_matches_oracle(hq, hkv, t, steps, mode):
         n = t + s + 1
         out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
         want, wc, wf = R.reuse_decode_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), s_dims, cand, 0.02, 4, 8,
-                                           True, 128 ** -0.5, pc if use_pc else None, pf if use_pf else None)
+                                           True, 128 ** -0.5, pc if use_pc else None, pf if use_pf else None, block)
         assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
         assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
+        # the final list: the final mask plus the current token, each once
+        fi, fv = (x.cpu().numpy() for x in step.final_indices())
+        for r in range(hq):
+            got = fi[0, r][fv[0, r]]
+            assert len(got) == len(set(got.tolist())), (s, r)
+            assert set(got.tolist()) == set(np.flatnonzero(wf[0, r]).tolist()) | {n - 1}, (s, r)
         np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
         pc, pf = wc, wf
+
+
+@pytest.mark.parametrize("rows,history,block,sink,recent,keep_self,density", [
+    (3, 1000, 16, 4, 8, True, 0.01),
+    (2, 9000, 64, 0, 0, False, 0.002),      # three tiles of 4096
+    (4, 777, 7, 3, 5, True, 0.02),          # blocks that do not divide the tile or the history
+    (2, 300, 4096, 2, 2, True, 0.01),       # one block wider than the history
+    (2, 5000, 1, 10, 10, True, 0.05),       # no expansion: the list is the mask
+    (3, 40, 8, 50, 0, True, 0.2),           # the sink covers the history
+    (2, 50, 8, 0, 60, False, 0.2),          # the recent range covers the history
+    (1, 1, 16, 0, 0, True, 1.0),
+    (2, 5000, 32, 5, 5, True, 0.0),         # only the protected ranges
+])
+def test_expand_blocks_matches_oracle(rows, history, block, sink, recent, keep_self, density):
+    gen = torch.Generator().manual_seed(history + block)
+    # a final mask as qkv_reuse_select leaves it: selections plus the protected ranges
+    mask = torch.rand((rows, history), generator=gen) < density
+    mask[:, :min(sink, history)] = True
+    mask[:, max(0, history - recent):] = True
+    keep = int(mask.sum(dim=1).max())
+    top_fraction = keep / history
+    buf = torch.zeros((rows, history + 37), dtype=torch.uint8)   # padded row stride
+    buf[:, :history] = mask.to(torch.uint8)
+    dbuf = buf.to(DEV)
+    idx, valid, ids = RU.expand_blocks(dbuf, history + 1, block, sink, recent, top_fraction, keep_self)
+    want = R.expand_to_blocks(mask.numpy(), block)
+    assert np.array_equal(dbuf[:, :history].cpu().numpy().astype(bool), want)
+    assert int(torch.count_nonzero(dbuf[:, history:])) == 0
+    sel, sv = R.indices_from_keep_mask(want)
+    wi, wv = R.final_indices_np(sel, sv, history, history + 1, sink, recent, keep_self)
+    idx, valid, ids = idx.cpu().numpy(), valid.cpu().numpy(), ids.cpu().numpy()
+    assert np.array_equal(np.where(valid, idx, -1), ids)
+    for r in range(rows):
+        got = idx[r][valid[r]]
+        assert sorted(got.tolist()) == sorted(wi[r][wv[r]].tolist()), r
+        sink_end = min(sink, history)
+        rec_begin = max(history - recent, sink_end)
+        body = idx.shape[1] - sink_end - (history - rec_begin if recent > 0 else 0) - int(keep_self)
+        assert np.all(np.diff(idx[r, :body][valid[r, :body]]) > 0), r      # ascending body
+
+
+def test_expand_blocks_rejects_bad_arguments():
+    m = torch.zeros((2, 100), dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="block must be"):
+        RU.expand_blocks(m, 101, 5000, 0, 0, 0.1, True)
+    with pytest.raises(RuntimeError, match="need history >= 1"):
+        RU.expand_blocks(m, 101, 0, 0, 0, 0.1, True)
 
 
 def test_step_resets_on_shorter_history():

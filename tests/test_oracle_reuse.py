@@ -13,7 +13,8 @@ import pytest
 from oracle import ref_semantics as R
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-SCENARIOS = ["s8c5_fp32", "s16c10_final_fp32", "s8c3_2set_fp32", "s8c5_bf16"]
+SCENARIOS = ["s8c5_fp32", "s16c10_final_fp32", "s8c3_2set_fp32", "s8c5_bf16",
+             "s8c5_blk16_fp32", "s16c10_finalblk8_bf16", "s8c3_2setblk32_fp32"]
 
 
 def load_golden(name):
@@ -21,10 +22,13 @@ def load_golden(name):
     z = np.load(GOLDEN / f"reuse_{name}.npz")
     t_max = int(z["t_max"])
     bf = lambda a: (a.astype(np.int32) << 16).view(np.float32)   # bf16 bits -> fp32
-    m = re.fullmatch(r"qabs(\d+)cand(\d+)reuse(2set|final)?", str(z["mode"]))
+    m = re.fullmatch(r"qabs(\d+)cand(\d+)reuse(2set|final)?(?:blk(\d+))?", str(z["mode"]))
     return {
         "mode": str(z["mode"]), "dtype": str(z["dtype"]), "dims": int(m.group(1)), "cand": int(m.group(2)) / 100,
-        "use_prev_candidate": m.group(3) != "final", "use_prev_final": m.group(3) != "2set",
+        # EV:955-960 test the suffix: a blk mode keeps both previous masks
+        "use_prev_candidate": not str(z["mode"]).endswith("reusefinal"),
+        "use_prev_final": not str(z["mode"]).endswith("reuse2set"),
+        "block": int(m.group(4)) if m.group(4) else None,
         "q": z["q"][:, :, :, 0, :], "k": bf(z["k_bf16"]), "v": bf(z["v_bf16"]), "t0": int(z["t0"]),
         "steps": int(z["steps"]), "top_fraction": float(z["top_fraction"]), "sink": int(z["sink"]),
         "recent": int(z["recent"]), "keep_self": bool(z["keep_self"]), "scaling": float(z["scaling"]),
@@ -46,11 +50,62 @@ def test_decode_steps_match_reference_vectors(name):
         out, cur, hf = R.reuse_decode_step(
             g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"], g["top_fraction"], g["sink"],
             g["recent"], g["keep_self"], g["scaling"], pc if g["use_prev_candidate"] else None,
-            pf if g["use_prev_final"] else None)
+            pf if g["use_prev_final"] else None, g["block"])
         assert np.array_equal(cur, g["candidate"][s][..., : n - 1]), (name, s)
         assert np.array_equal(hf, g["final"][s][..., : n - 1]), (name, s)
         np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
         pc, pf = cur, hf
+
+
+def test_expand_to_blocks_known_answers():
+    m = np.zeros((1, 1, 10), bool)
+    m[0, 0, [1, 8]] = True
+    # blocks of 4: [0,4) and [8,10) (the last one cut at the history)
+    assert np.flatnonzero(R.expand_to_blocks(m, 4)[0, 0]).tolist() == [0, 1, 2, 3, 8, 9]
+    assert np.flatnonzero(R.expand_to_blocks(m, 3)[0, 0]).tolist() == [0, 1, 2, 6, 7, 8]
+    assert np.flatnonzero(R.expand_to_blocks(m, 16)[0, 0]).tolist() == list(range(10))
+    for b in (None, 0, 1):
+        assert np.array_equal(R.expand_to_blocks(m, b), m)
+    one = np.ones((2, 1), bool)
+    assert np.array_equal(R.expand_to_blocks(one, 8), one)
+    assert not R.expand_to_blocks(np.zeros((3, 17), bool), 5).any()
+
+
+def test_expand_to_blocks_is_idempotent_and_brute_force():
+    rng = np.random.default_rng(3)
+    m = rng.random((6, 97)) < 0.03
+    for b in (2, 5, 16, 33, 97, 200):
+        e = R.expand_to_blocks(m, b)
+        assert np.array_equal(R.expand_to_blocks(e, b), e)
+        for r in range(m.shape[0]):
+            for t in range(m.shape[1]):
+                assert e[r, t] == m[r, (t // b) * b:(t // b + 1) * b].any()
+
+
+def test_indices_from_keep_mask_descending_and_padded():
+    m = np.array([[False, True, True, False, True], [False, False, False, True, False]])
+    idx, valid = R.indices_from_keep_mask(m)
+    assert idx.tolist() == [[4, 2, 1], [3, 0, 0]]
+    assert valid.tolist() == [[True, True, True], [True, False, False]]
+    idx, valid = R.indices_from_keep_mask(np.zeros((2, 4), bool))
+    assert idx.shape == (2, 0) and valid.shape == (2, 0)
+
+
+def test_reuse_select_block_expansion():
+    # scores 9 5 7 1 0 8 3 2 1 1; keep = 2 -> {0, 5}; blocks of 4 -> {0..3, 4..7};
+    # sink 1 is in block 0, recent 1 (position 9) is block [8, 10)
+    q, k = _row([9, 5, 7, 1, 0, 8, 3, 2, 1, 1])
+    allm = _mask(10, range(10))
+    fi, fv, hf = R.reuse_select(q, k, allm, None, None, sink=1, recent=1, top_fraction=0.2, keep_self=True,
+                                scaling=1.0, block=4)
+    assert np.flatnonzero(hf[0, 0]).tolist() == list(range(10))
+    got = sorted(fi[0, 0][fv[0, 0]].tolist())
+    assert got == list(range(11))           # all history + the current token 10
+    assert len(got) == len(set(got))        # protected entries appear once
+    fi, fv, hf = R.reuse_select(q, k, allm, None, None, sink=0, recent=0, top_fraction=0.2, keep_self=False,
+                                scaling=1.0, block=4)
+    assert np.flatnonzero(hf[0, 0]).tolist() == list(range(8))
+    assert fi[0, 0][fv[0, 0]].tolist() == [7, 6, 5, 4, 3, 2, 1, 0]
 
 
 def test_threshold_mask_keeps_ties():
@@ -144,7 +199,7 @@ def test_cpu_baseline_op_sequence_matches_reference_vectors(name):
         out, cur, hf = R.qabs_reuse_step_cpu(q, k[:, :, :n], v[:, :, :n], g["dims"], g["cand"], g["top_fraction"],
                                              g["scaling"], g["sink"], g["recent"], g["keep_self"],
                                              fit(pc) if g["use_prev_candidate"] else None,
-                                             fit(pf) if g["use_prev_final"] else None)
+                                             fit(pf) if g["use_prev_final"] else None, g["block"])
         assert np.array_equal(cur.numpy(), g["candidate"][s][..., : n - 1]), (name, s)
         assert np.array_equal(hf.numpy(), g["final"][s][..., : n - 1]), (name, s)
         np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], rtol=1e-5, atol=1e-6)
