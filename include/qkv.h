@@ -37,6 +37,12 @@ extern "C" {
 #define QKV_BLOCK_QBB 0  /* Quest-style per-block channel min/max bounds */
 #define QKV_BLOCK_BREP 1 /* per-block representative tokens */
 
+/* Candidate selections of the reuse step (--qabs_candidate_selection,
+ * EV:3958-3989). */
+#define QKV_CAND_TOPK 0               /* the row's k-th largest value             */
+#define QKV_CAND_SAMPLE_QUANTILE 1    /* the k-th largest of sampled columns      */
+#define QKV_CAND_PREVIOUS_THRESHOLD 2 /* the previous step's threshold            */
+
 #define QKV_ABI_VERSION 1
 
 /* ABI version of the loaded library (QKV_ABI_VERSION it was built with). */
@@ -278,6 +284,27 @@ int qkv_reuse_select(const void* query, const void* key, const int64_t* k_stride
                      int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
                      int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                      uint8_t* history_final, int64_t history_final_ld, void* stream);
+
+/* Workspace bytes of qkv_candidate_mask (0 for previous_threshold, -1 for
+ * bad arguments). */
+int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k, int64_t n_sample);
+
+/* Candidate mask of the reuse step under each candidate selection of the
+ * reference (_select_qabs_candidate_from_partial_scores EV:3958-3989):
+ * mask[r, t] = values[r, t] >= thresholds[r] for t < n, where the
+ * threshold is
+ *   QKV_CAND_TOPK: the row's k-th largest value (EV:3988; written to
+ *     thresholds when that is not NULL);
+ *   QKV_CAND_SAMPLE_QUANTILE: the k-th largest of values[r, sample_cols[i]],
+ *     i < n_sample (EV:3972-3987; the caller passes the sampled columns,
+ *     the reference's rounded linspace, and k = the sample's budget),
+ *     written to thresholds;
+ *   QKV_CAND_PREVIOUS_THRESHOLD: thresholds[r] as given (EV:3967-3971).
+ * values f32 [rows, ld]; mask uint8 row stride mask_ld; thresholds f32
+ * [rows] (required for the last two). */
+int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int selection, int64_t k,
+                       const int32_t* sample_cols, int64_t n_sample, float* thresholds, uint8_t* mask,
+                       int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Entries per row of the final index list of a block-expanded reuse step
  * (the qabs{S}cand{pct}reuse[final|2set]blk{block} modes): body + sink

@@ -133,20 +133,30 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
 // selected values, i.e. the k-th largest (EV:3988-3989; ties at the
 // threshold are all kept).  Sixteen tokens per thread.
 // ---------------------------------------------------------------------------
+// The threshold is the smallest of the k values at sel's indices, or, with
+// sel null, thr_in[row] (a given threshold, EV:3967-3971).  thr_out
+// (optional) receives it.
 __global__ __launch_bounds__(kRT) void reuse_mask_kernel(const float* __restrict__ values, int64_t ld, int n,
                                                          const int32_t* __restrict__ sel, int k,
+                                                         const float* __restrict__ thr_in,
                                                          uint8_t* __restrict__ mask, int64_t mask_ld,
-                                                         bool vec) {
+                                                         bool vec, float* __restrict__ thr_out) {
   __shared__ float red[kRT / 64];
   const int row = blockIdx.y, tid = threadIdx.x;
   const float* vrow = values + static_cast<int64_t>(row) * ld;
-  const int32_t* srow = sel + static_cast<int64_t>(row) * k;
-  float thr = __builtin_huge_valf();
-  for (int i = tid; i < k; i += kRT) thr = fminf(thr, vrow[srow[i]]);
-  for (int off = 32; off > 0; off >>= 1) thr = fminf(thr, __shfl_xor(thr, off));
-  if ((tid & 63) == 0) red[tid >> 6] = thr;
-  __syncthreads();
-  thr = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+  float thr;
+  if (sel) {
+    const int32_t* srow = sel + static_cast<int64_t>(row) * k;
+    thr = __builtin_huge_valf();
+    for (int i = tid; i < k; i += kRT) thr = fminf(thr, vrow[srow[i]]);
+    for (int off = 32; off > 0; off >>= 1) thr = fminf(thr, __shfl_xor(thr, off));
+    if ((tid & 63) == 0) red[tid >> 6] = thr;
+    __syncthreads();
+    thr = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+  } else {
+    thr = thr_in[row];
+  }
+  if (thr_out && blockIdx.x == 0 && tid == 0) thr_out[row] = thr;
   uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
   const int t0 = blockIdx.x * kMaskTile + tid * 16;
   if (t0 >= n) return;
@@ -289,15 +299,35 @@ constexpr int kWideNT = 1024;
 constexpr int kWideMax = kWideNT * 40;
 
 // mask[r, t] = values[r, t] >= the row's k-th largest value.
+// thr_out (optional) receives the k-th largest value; with mask null only
+// the threshold is written.
 template <int VPL>
 __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* __restrict__ values, int64_t ld, int n,
-                                                                  int k, uint8_t* __restrict__ mask, int64_t mask_ld) {
+                                                                  int k, uint8_t* __restrict__ mask, int64_t mask_ld,
+                                                                  float* __restrict__ thr_out) {
   using WS = WideSelect<VPL, false>;
   __shared__ typename WS::Shared sh;
   WS ws;
   const int row = blockIdx.x, tid = threadIdx.x;
   ws.load(values + static_cast<int64_t>(row) * ld, n);
   ws.run(k, sh);
+  if (thr_out) {
+    // theta may be the lower bound of a boundary bin taken whole: the k-th
+    // largest is the smallest key at or above it
+    __shared__ uint32_t wave_min[kWideNT / 64];
+    uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (WS::pos(i) < n && ws.u[i] >= ws.theta) m = min(m, ws.u[i]);
+    m = wave_minmax_u32<false>(m);
+    if ((tid & 63) == 0) wave_min[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < kWideNT / 64; ++w) m = min(m, wave_min[w]);
+      thr_out[row] = sortable_f32(min(m, wave_min[0]));
+    }
+  }
+  if (!mask) return;
   // A slot of a wave covers 64 consecutive positions: its flags are one
   // ballot, written by 16 lanes as dwords (bytes one by one at the row end
   // or when the rows are not 4-byte aligned).
@@ -320,6 +350,16 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
       mrow[t] = f;
     }
   }
+}
+
+// out[r, i] = values[r, cols[i]] for i < n_cols (the sampled partial scores
+// of the sample_quantile candidate selection, EV:3972-3984).
+__global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restrict__ values, int64_t ld,
+                                                          const int32_t* __restrict__ cols, int n_cols,
+                                                          float* __restrict__ out) {
+  const int row = blockIdx.y;
+  const int i = blockIdx.x * kRT + threadIdx.x;
+  if (i < n_cols) out[static_cast<int64_t>(row) * n_cols + i] = values[static_cast<int64_t>(row) * ld + cols[i]];
 }
 
 // The final selection of reuse_finalize_kernel, with the keep largest scores
@@ -593,6 +633,28 @@ int check_heads(const char* what, int64_t batch, int64_t q_heads, int64_t kv_hea
   return QKV_OK;
 }
 
+// mask = values >= the row's k-th largest (threshold to thr_out when given).
+int threshold_mask_impl(const char* what, const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
+                        uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
+                        hipStream_t st) {
+  if (n <= kWideMax) {
+    return with_wide_vpl(n, [&](auto vpl) {
+      reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld, thr_out);
+      return check_launch(what);
+    });
+  }
+  int32_t* sel = static_cast<int32_t*>(workspace);
+  void* tk_ws = static_cast<char*>(workspace) + align256(rows * k * 4);
+  int rc = qkv_topk_ws(values, rows, n, ld, k, sel, tk_ws, workspace_bytes - align256(rows * k * 4), st);
+  if (rc) return rc;
+  const bool vec = ld % 4 == 0 && aligned(values, 16) && mask_ld % 16 == 0 && aligned(mask, 16);
+  dim3 grid(static_cast<unsigned>(cdiv(n, kMaskTile)), static_cast<unsigned>(rows));
+  reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sel, static_cast<int>(k), nullptr, mask,
+                                          mask_ld, vec, thr_out);
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace qkv
 
@@ -736,22 +798,81 @@ QKV_EXPORT int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, 
   if (need < 0 || workspace_bytes < need)
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
+  return threshold_mask_impl(what, values, rows, n, ld, k, mask, mask_ld, nullptr, workspace, workspace_bytes,
+                             static_cast<hipStream_t>(stream));
+}
+
+QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k,
+                                                      int64_t n_sample) {
+  if (rows <= 0 || n <= 0) return -1;
+  if (selection == QKV_CAND_TOPK) return qkv_threshold_mask_workspace_bytes(rows, n, k);
+  if (selection == QKV_CAND_PREVIOUS_THRESHOLD) return 0;
+  if (selection != QKV_CAND_SAMPLE_QUANTILE || n_sample < 1 || n_sample > n || k < 1 || k > n_sample) return -1;
+  const int64_t kth = n_sample <= kWideMax ? 0 : mask_ws_bytes(rows, n_sample, k);
+  return kth < 0 ? -1 : align256(rows * n_sample * 4) + kth;
+}
+
+QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int selection,
+                                  int64_t k, const int32_t* sample_cols, int64_t n_sample, float* thresholds,
+                                  uint8_t* mask, int64_t mask_ld, void* workspace, int64_t workspace_bytes,
+                                  void* stream) {
+  const char* what = "qkv_candidate_mask";
+  if (!values || !mask) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (rows <= 0 || rows > 65535 || n <= 0 || n >= (int64_t(1) << 31) || ld < n || mask_ld < n)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535, ld and mask_ld >= n", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (n <= kWideMax) {
-    return with_wide_vpl(n, [&](auto vpl) {
-      reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
-          values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld);
-      return check_launch(what);
-    });
+  if (selection == QKV_CAND_TOPK) {
+    if (k < 1 || k > n) return fail(QKV_ERR_INVALID, "%s: need 1 <= k <= n", what);
+    if (!workspace) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+    const int64_t need = mask_ws_bytes(rows, n, k);
+    if (need < 0 || workspace_bytes < need)
+      return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                  (long long)workspace_bytes);
+    return threshold_mask_impl(what, values, rows, n, ld, k, mask, mask_ld, thresholds, workspace, workspace_bytes,
+                               st);
   }
-  int32_t* sel = static_cast<int32_t*>(workspace);
-  void* tk_ws = static_cast<char*>(workspace) + align256(rows * k * 4);
-  int rc = qkv_topk_ws(values, rows, n, ld, k, sel, tk_ws, workspace_bytes - align256(rows * k * 4), stream);
-  if (rc) return rc;
+  if (!thresholds) return fail(QKV_ERR_INVALID, "%s: this selection needs the thresholds array", what);
   const bool vec = ld % 4 == 0 && aligned(values, 16) && mask_ld % 16 == 0 && aligned(mask, 16);
   dim3 grid(static_cast<unsigned>(cdiv(n, kMaskTile)), static_cast<unsigned>(rows));
-  reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sel, static_cast<int>(k), mask, mask_ld,
-                                          vec);
+  if (selection == QKV_CAND_PREVIOUS_THRESHOLD) {
+    reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
+                                            vec, nullptr);
+    return check_launch(what);
+  }
+  if (selection != QKV_CAND_SAMPLE_QUANTILE) return fail(QKV_ERR_INVALID, "%s: unknown selection %d", what, selection);
+  if (!sample_cols || !workspace) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (n_sample < 1 || n_sample > n || k < 1 || k > n_sample)
+    return fail(QKV_ERR_INVALID, "%s: need 1 <= k <= n_sample <= n", what);
+  const int64_t need = qkv_candidate_mask_workspace_bytes(rows, n, selection, k, n_sample);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  float* sampled = static_cast<float*>(workspace);
+  gather_cols_kernel<<<dim3(static_cast<unsigned>(cdiv(n_sample, kRT)), static_cast<unsigned>(rows)), kRT, 0, st>>>(
+      values, ld, sample_cols, static_cast<int>(n_sample), sampled);
+  int rc = check_launch(what);
+  if (rc) return rc;
+  // the k-th largest sampled value, then the mask over the whole row
+  if (n_sample <= kWideMax) {
+    rc = with_wide_vpl(n_sample, [&](auto vpl) {
+      reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          sampled, n_sample, static_cast<int>(n_sample), static_cast<int>(k), nullptr, 0, thresholds);
+      return check_launch(what);
+    });
+  } else {
+    char* rest = static_cast<char*>(workspace) + align256(rows * n_sample * 4);
+    int32_t* sel = reinterpret_cast<int32_t*>(rest);
+    rc = qkv_topk_ws(sampled, rows, n_sample, n_sample, k, sel, rest + align256(rows * k * 4),
+                     workspace_bytes - align256(rows * n_sample * 4) - align256(rows * k * 4), stream);
+    if (rc) return rc;
+    // a one-token-tile launch of the mask kernel writes the threshold only
+    reuse_mask_kernel<<<dim3(1, static_cast<unsigned>(rows)), kRT, 0, st>>>(
+        sampled, n_sample, 0, sel, static_cast<int>(k), nullptr, mask, mask_ld, false, thresholds);
+    rc = check_launch(what);
+  }
+  if (rc) return rc;
+  reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
+                                          vec, nullptr);
   return check_launch(what);
 }
 

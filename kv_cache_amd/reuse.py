@@ -62,6 +62,47 @@ def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool, int | None]:
     return int(m.group(1)), frac, not mode.endswith("reusefinal"), not mode.endswith("reuse2set"), block
 
 
+CANDIDATE_SELECTIONS = {"topk": 0, "sample_quantile": 1, "previous_threshold": 2}   # QKV_CAND_*
+
+
+def sample_columns(history: int, sample_size: int) -> torch.Tensor | None:
+    """Sampled positions of the ``sample_quantile`` candidate selection, int32
+    on the host: the reference's ``linspace(0, history - 1, steps)`` in
+    float32, rounded and deduplicated (EV:3973-3981), by the same torch call
+    (its float32 values at .5 ties are torch's own).  None when the sample
+    covers the row."""
+    count = min(int(history), max(1, int(sample_size)))
+    if count >= history:
+        return None
+    cols = torch.linspace(0, history - 1, steps=count, dtype=torch.float32).round().long().unique()
+    return cols.to(torch.int32)
+
+
+def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: torch.Tensor,
+                   thresholds: torch.Tensor, workspace: torch.Tensor, sample_cols: torch.Tensor | None = None,
+                   n_sample: int = 0) -> torch.Tensor:
+    """mask[:, :n] = values[:, :n] >= the row's threshold under ``selection``
+    (EV:3958-3989): the k-th largest value (``topk``), the k-th largest of
+    the ``n_sample`` columns ``sample_cols`` (``sample_quantile``), or
+    ``thresholds`` as given (``previous_threshold``).  The first two write
+    the threshold to ``thresholds`` (f32 [rows])."""
+    lib = _lib.load()
+    code = CANDIDATE_SELECTIONS.get(selection)
+    _require(code is not None, f"unknown candidate selection {selection!r}")
+    _require(values.is_cuda and values.dtype == torch.float32 and values.dim() == 2 and values.stride(1) == 1
+             and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
+    _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
+             and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
+    _require(thresholds.dtype == torch.float32 and thresholds.is_contiguous()
+             and thresholds.numel() >= values.size(0), "thresholds must be f32 [rows]")
+    with torch.cuda.device(values.device):
+        _lib.check(lib.qkv_candidate_mask(
+            values.data_ptr(), values.size(0), int(n), values.stride(0), code, int(k), _lib.ptr(sample_cols),
+            int(n_sample), thresholds.data_ptr(), mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
+            workspace.numel() * 4, _lib.stream_of(values)))
+    return mask
+
+
 def reuse_partial_scores(query: torch.Tensor, key_dim_major: torch.Tensor, history: int, dim_count: int, *,
                          out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 [B*Hq, >= history] partial scores over each head's top-|q| dims;
@@ -174,13 +215,18 @@ class ReuseDecodeStep:
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
-                 keep_self: bool = True, device: torch.device | str = "cuda"):
+                 keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
+                 device: torch.device | str = "cuda"):
         lib = _lib.load()
         self.device = device
         self.mode = mode
         (self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final,
          self.block) = parse_reuse_mode(mode)
         _require(self.block is None or self.block <= 4096, "reuse blocks hold at most 4096 tokens")
+        # --qabs_candidate_selection / --qabs_threshold_sample_size (EV:245-258, 3958-3989)
+        _require(candidate_selection in CANDIDATE_SELECTIONS, f"unknown candidate selection {candidate_selection!r}")
+        self.selection = candidate_selection
+        self.sample_size = max(1, int(threshold_sample_size))
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
         self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
         self.capacity = int(capacity)
@@ -193,6 +239,8 @@ class ReuseDecodeStep:
         self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
         self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
+        self.thresholds = torch.zeros(rows, dtype=torch.float32, device=device)   # the last step's, per row
+        self.sample_cols = torch.empty(min(self.sample_size, cap), dtype=torch.int32, device=device)
         hist_max = cap - 1
         # every term of the counts grows with the history
         self.n_out_max = max(self._final_count(hist_max), int(lib.qkv_reuse_final_count(
@@ -258,18 +306,23 @@ class ReuseDecodeStep:
         consecutive = self.last_history == history - 1
         cur, prev = self.cand[self.flip], self.cand[1 - self.flip]
         self.launch(query, key, value, scaling, cur, prev if consecutive and self.use_prev_candidate else None,
-                    self.fin if consecutive and self.use_prev_final else None)
+                    self.fin if consecutive and self.use_prev_final else None,
+                    previous_thresholds=consecutive and self.selection == "previous_threshold")
         self.flip ^= 1
         self.last_history = history
         return self.out
 
     def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
-               current: torch.Tensor, previous: torch.Tensor | None, previous_final: torch.Tensor | None) -> None:
+               current: torch.Tensor, previous: torch.Tensor | None, previous_final: torch.Tensor | None, *,
+               previous_thresholds: bool = False) -> None:
         """The step's kernels at the history key.size(2) - 1 with explicit
         mask buffers (rows of ``capacity`` bytes): the current candidates go to
         ``current``, the final mask to the final buffer (it may also be the
-        ``previous_final`` read).  Touches no Python state but ``n_out``; the
-        dim-major copy must already hold the history.  Output in ``self.out``."""
+        ``previous_final`` read).  With ``previous_thresholds`` the
+        ``previous_threshold`` selection compares with the thresholds the last
+        step left (else it selects as ``topk``).  Touches no Python state but
+        ``n_out``; the dim-major copy must already hold the history.  Output
+        in ``self.out``; the step's thresholds in ``self.thresholds``."""
         lib = _lib.load()
         key_count = key.size(2)
         history = key_count - 1
@@ -277,8 +330,22 @@ class ReuseDecodeStep:
         q = query.contiguous()
         reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
-        self.mask_ws = self._grow(self.mask_ws, lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
-        threshold_mask(self.partial, history, requested, current, self.mask_ws)
+        cols = sample_columns(history, self.sample_size) if self.selection == "sample_quantile" else None
+        if self.selection == "previous_threshold" and previous_thresholds:   # EV:3967-3971
+            candidate_mask(self.partial, history, "previous_threshold", requested, current, self.thresholds,
+                           self.mask_ws)
+        elif cols is not None:                                                # EV:3972-3987
+            n_s = cols.numel()
+            k_s = budget_count(n_s, self.cand_fraction)
+            self.sample_cols[:n_s].copy_(cols)
+            self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
+                self.rows, history, CANDIDATE_SELECTIONS["sample_quantile"], k_s, n_s))
+            candidate_mask(self.partial, history, "sample_quantile", k_s, current, self.thresholds, self.mask_ws,
+                           self.sample_cols, n_s)
+        else:                                                                 # EV:3988
+            self.mask_ws = self._grow(self.mask_ws,
+                                      lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+            candidate_mask(self.partial, history, "topk", requested, current, self.thresholds, self.mask_ws)
         n_sel = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
         n_out = self._final_count(history)
         self.select_ws = self._grow(self.select_ws,

@@ -233,6 +233,46 @@ def threshold_mask(partial, requested: int) -> np.ndarray:
     return p >= thr
 
 
+def sample_columns(history: int, sample_size: int):
+    """The sampled positions of the ``sample_quantile`` candidate selection
+    (EV:3973-3981): ``linspace(0, history - 1, steps=min(history,
+    max(1, sample_size)))`` in float32, rounded half to even, deduplicated;
+    None when the sample covers the row.  The float32 linspace is torch's
+    own (its CPU kernel fills vector lanes from a running base, which a
+    closed form does not reproduce at .5 ties), so this calls it."""
+    import torch
+
+    count = min(int(history), max(1, int(sample_size)))
+    if count >= history:
+        return None
+    cols = torch.linspace(0, history - 1, steps=count, dtype=torch.float32).round().long().unique()
+    return cols.numpy()
+
+
+def candidate_mask(partial, requested: int, fraction: float, selection: str = "topk", previous_thresholds=None,
+                   sample_size: int = 256):
+    """``_select_qabs_candidate_from_partial_scores`` (EV:3958-3989):
+    (mask, thresholds [..., 1] float32, selection used).  ``topk``: every
+    value >= the ``requested``-th largest; ``sample_quantile``: the
+    threshold is the ``min(n, max(1, ceil(fraction * n)))``-th largest of
+    the n sampled columns (the whole row when the sample covers it);
+    ``previous_threshold``: the given per-row thresholds, falling back to
+    ``topk`` when there are none."""
+    p = np.asarray(partial, dtype=np.float32)
+    history = p.shape[-1]
+    if selection == "previous_threshold" and previous_thresholds is not None:
+        thr = np.asarray(previous_thresholds, dtype=np.float32).reshape(*p.shape[:-1], 1)
+        return p >= thr, thr, "previous_threshold"
+    if selection == "sample_quantile" and history > 0:
+        cols = sample_columns(history, sample_size)
+        sampled = p if cols is None else p[..., cols]
+        k = min(sampled.shape[-1], max(1, math.ceil(fraction * sampled.shape[-1])))
+        thr = -np.sort(-sampled, axis=-1)[..., k - 1:k]
+        return p >= thr, thr, "sample_quantile"
+    thr = -np.sort(-p, axis=-1)[..., requested - 1:requested]
+    return p >= thr, thr, "topk"
+
+
 def final_indices_np(selected, selected_valid, history: int, key_count: int, sink: int, recent: int,
                      keep_self: bool):
     """EV:2938-2982 in numpy: the selected history indices with the sink and
@@ -347,7 +387,9 @@ def reuse_select(query, key_states, current, previous, previous_final, sink: int
 
 def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: float, top_fraction: float,
                       sink: int, recent: int, keep_self: bool, scaling: float,
-                      previous_candidate=None, previous_final=None, block: int | None = None):
+                      previous_candidate=None, previous_final=None, block: int | None = None, *,
+                      selection: str = "topk", sample_size: int = 256, previous_thresholds=None,
+                      thresholds_out: list | None = None):
     """One decode step of ``_qabs_reuse_fast_attention_forward`` (EV:3991-4397)
     for the default candidate selection (``topk``), block-expanded when
     ``block`` is given (``reuse…blk{block}``, EV:757-761, 4314-4316).
@@ -360,9 +402,13 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
     length, as ``ReuseCandidateState.previous_layer_masks`` does (EV:1645-1662).
 
     Steps: top-|q| dims and fp32 partial scores (EV:4068, 4123-4135), the
-    threshold mask (EV:4136-4144, 3988-3989), ``reuse_select``, and the
-    attention over the final indices (QK:335-419, fp64 here).  A cache of at
-    most one key returns the last value (EV:4012-4014).
+    candidate mask under ``selection`` (``candidate_mask``, EV:4136-4144;
+    ``previous_thresholds`` are the thresholds the previous step left, the
+    step's own are appended to ``thresholds_out`` when given; the
+    reference keeps them in its state, EV:1686-1694, 1744-1745),
+    ``reuse_select``, and the attention over the final indices (QK:335-419,
+    fp64 here).  A cache of at most one key returns the last value
+    (EV:4012-4014).
 
     Returns (out float64 [B,1,Hq,D], current bool [B,Hq,history],
     history_final bool [B,Hq,history]); the last two are the state the next
@@ -379,7 +425,10 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
         return vx[:, :, -1:, :].transpose(0, 2, 1, 3).astype(np.float64), None, None
     history = key_count - 1
     partial = partial_scores(q, kx[:, :, :history], dim_count)
-    current = threshold_mask(partial, budget_count(history, candidate_fraction))
+    current, thr, _ = candidate_mask(partial, budget_count(history, candidate_fraction), candidate_fraction,
+                                     selection, previous_thresholds, sample_size)
+    if thresholds_out is not None:
+        thresholds_out.append(thr)
 
     def fit(m):
         if m is None:
@@ -396,7 +445,9 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
 
 def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, candidate_fraction: float,
                         top_fraction: float, scaling: float, sink: int = 0, recent: int = 0, keep_self: bool = True,
-                        previous_candidate=None, previous_final=None, block: int | None = None):
+                        previous_candidate=None, previous_final=None, block: int | None = None, *,
+                      selection: str = "topk", sample_size: int = 256, previous_thresholds=None,
+                      thresholds_out: list | None = None):
     """One ``qabs{S}cand{pct}reuse`` decode step in the reference's PyTorch
     ops on CPU tensors: the path ``_qabs_reuse_fast_attention_forward`` takes
     when no CUDA kernel is available (EV:3991-4397 with the dense-mask

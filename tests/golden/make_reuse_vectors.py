@@ -54,10 +54,19 @@ SCENARIOS = {
     "s8c5_blk16_fp32": ("qabs8cand5reuseblk16", torch.float32, 4, 2, 240, 5, 0.05, 4, 4, True, 5),
     "s16c10_finalblk8_bf16": ("qabs16cand10reusefinalblk8", torch.bfloat16, 4, 2, 203, 4, 0.03, 0, 6, True, 15),
     "s8c3_2setblk32_fp32": ("qabs8cand3reuse2setblk32", torch.float32, 2, 1, 300, 4, 0.02, 3, 0, False, 7),
+    # the other candidate selections (--qabs_candidate_selection, EV:3958-3989):
+    # + (selection, threshold sample size)
+    "s8c5_sample64_fp32": ("qabs8cand5reuse", torch.float32, 4, 2, 600, 4, 0.05, 4, 4, True, 21,
+                           "sample_quantile", 64),
+    "s8c5_samplecover_fp32": ("qabs8cand5reusefinal", torch.float32, 2, 1, 100, 3, 0.05, 2, 2, False, 23,
+                              "sample_quantile", 256),
+    "s8c10_prevthr_fp32": ("qabs8cand10reuse", torch.float32, 4, 2, 400, 4, 0.03, 0, 6, True, 22,
+                           "previous_threshold", 256),
 }
 
 
-def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, keep_self, seed):
+def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, keep_self, seed, selection="topk",
+        sample_size=256):
     g = torch.Generator().manual_seed(seed)
     d = 128
     t_max = t0 + steps
@@ -69,11 +78,12 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
     scaling = d ** -0.5
     state = ev.ReuseCandidateState()
     module = types.SimpleNamespace(layer_idx=0, scaling=scaling)
-    outs, cands, finals = [], [], []
+    outs, cands, finals, thresholds = [], [], [], []
     with ev.attention_mode(mode=mode, top_fraction=top_fraction, max_heads_per_token=3,
                            always_keep_self=keep_self, protect_sink_tokens=sink,
                            protect_recent_tokens=recent, load_stats=None, reuse_state=state,
-                           qabs_fast_path=True):
+                           qabs_fast_path=True, qabs_candidate_selection=selection,
+                           qabs_threshold_sample_size=sample_size):
         for s in range(steps):
             n = t0 + s + 1
             out, _ = ev._limited_eager_attention_forward(module, q[s], k[:, :, :n], v[:, :, :n], None,
@@ -87,14 +97,16 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
             fin[..., :hist] = rec["final"].numpy()
             cands.append(cand)
             finals.append(fin)
+            thresholds.append(rec["candidate_thresholds"].float().numpy().reshape(1, hq))
     np.savez_compressed(
         OUT / f"reuse_{name}.npz", mode=np.array(mode), dtype=np.array(str(dtype).split(".")[-1]),
         q=q.float().numpy(), k_bf16=k.to(torch.bfloat16).view(torch.int16).numpy(),
         v_bf16=v.to(torch.bfloat16).view(torch.int16).numpy(), t0=t0, steps=steps,
         top_fraction=top_fraction, sink=sink, recent=recent, keep_self=keep_self, scaling=scaling,
         out=np.stack(outs), candidate=np.packbits(np.stack(cands), axis=-1),
-        final=np.packbits(np.stack(finals), axis=-1), t_max=t_max)
-    print(f"{name}: {mode} {dtype} Hq={hq} T0={t0} steps={steps} -> reuse_{name}.npz")
+        final=np.packbits(np.stack(finals), axis=-1), t_max=t_max, selection=np.array(selection),
+        sample_size=sample_size, thresholds=np.stack(thresholds))
+    print(f"{name}: {mode} {dtype} {selection} Hq={hq} T0={t0} steps={steps} -> reuse_{name}.npz")
 
 
 # Block-metadata selectors (qbb: Quest-style channel bounds, EV:5508-5617;

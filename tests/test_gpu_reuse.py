@@ -42,7 +42,21 @@ def test_pieces_match_reference_vectors(name):
         ws = torch.empty(max(1, Q._lib.load().qkv_threshold_mask_workspace_bytes(hq, hist, req)) // 4 + 1,
                          dtype=torch.float32, device=DEV)
         cur = torch.empty((1, hq, hist), dtype=torch.bool, device=DEV)
-        RU.threshold_mask(partial.view(hq, hist), hist, req, cur.view(torch.uint8).view(hq, hist), ws)
+        if g["selection"] == "topk":
+            RU.threshold_mask(partial.view(hq, hist), hist, req, cur.view(torch.uint8).view(hq, hist), ws)
+        else:   # the candidate selections of EV:3958-3989, thresholds carried between steps
+            cols = RU.sample_columns(hist, g["sample_size"]) if g["selection"] == "sample_quantile" else None
+            use_prev = g["selection"] == "previous_threshold" and s > 0
+            sel = "previous_threshold" if use_prev else "sample_quantile" if cols is not None else "topk"
+            n_s = cols.numel() if cols is not None else 0
+            kk = R.budget_count(n_s, g["cand"]) if cols is not None else req
+            ws = torch.empty(max(1, Q._lib.load().qkv_candidate_mask_workspace_bytes(
+                hq, hist, RU.CANDIDATE_SELECTIONS[sel], kk, n_s)) // 4 + 1, dtype=torch.float32, device=DEV)
+            if s == 0:
+                thr = torch.zeros(hq, dtype=torch.float32, device=DEV)
+            RU.candidate_mask(partial.view(hq, hist), hist, sel, kk, cur.view(torch.uint8).view(hq, hist), thr, ws,
+                              cols.to(DEV) if cols is not None else None, n_s)
+            assert np.array_equal(thr.cpu().numpy(), g["thresholds"][s].reshape(-1)), (name, s, "thresholds")
         assert np.array_equal(cur.cpu().numpy(), g["candidate"][s][..., :hist]), (name, s, "candidate")
         fi, fv, hf = Q.reuse_select(q, k, cur, pc if g["use_prev_candidate"] else None,
                                     pf if g["use_prev_final"] else None, g["sink"], g["recent"], g["top_fraction"],
@@ -165,6 +179,39 @@ def test_step_matches_oracle(hq, hkv, t, steps, mode):
             got = fi[0, r][fv[0, r]]
             assert len(got) == len(set(got.tolist())), (s, r)
             assert set(got.tolist()) == set(np.flatnonzero(wf[0, r]).tolist()) | {n - 1}, (s, r)
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+        pc, pf = wc, wf
+
+
+@pytest.mark.parametrize("hq,hkv,t,steps,mode,selection,sample", [
+    (8, 2, 3000, 4, "qabs8cand5reuse", "sample_quantile", 256),
+    (4, 2, 1000, 3, "qabs16cand10reusefinal", "sample_quantile", 2000),   # the sample covers the row
+    (4, 2, 50000, 2, "qabs8cand5reuse", "sample_quantile", 45000),        # staged threshold of the sample
+    (8, 2, 3000, 4, "qabs8cand5reuse", "previous_threshold", 256),
+    (4, 2, 50000, 3, "qabs8cand2reuseblk16", "previous_threshold", 256),  # staged first threshold
+])
+def test_step_selections_match_oracle(hq, hkv, t, steps, mode, selection, sample):
+    gen = torch.Generator().manual_seed(hq * t + len(selection))
+    s_dims, cand, use_pc, use_pf, block = RU.parse_reuse_mode(mode)
+    k = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    qs = torch.randn((steps, 1, hq, 128), generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = RU.ReuseDecodeStep(mode, 1, hq, hkv, 128, t + steps + 64, top_fraction=0.02, protect_sink=4,
+                              protect_recent=8, candidate_selection=selection, threshold_sample_size=sample)
+    pc = pf = thr = None
+    for s in range(steps):
+        n = t + s + 1
+        out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        got = []
+        want, wc, wf = R.reuse_decode_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), s_dims, cand, 0.02, 4, 8,
+                                           True, 128 ** -0.5, pc if use_pc else None, pf if use_pf else None, block,
+                                           selection=selection, sample_size=sample, previous_thresholds=thr,
+                                           thresholds_out=got)
+        thr = got[0]
+        assert np.array_equal(step.thresholds.cpu().numpy(), thr.reshape(-1)), s
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
         np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
         pc, pf = wc, wf
 

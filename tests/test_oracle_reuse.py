@@ -14,7 +14,8 @@ from oracle import ref_semantics as R
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 SCENARIOS = ["s8c5_fp32", "s16c10_final_fp32", "s8c3_2set_fp32", "s8c5_bf16",
-             "s8c5_blk16_fp32", "s16c10_finalblk8_bf16", "s8c3_2setblk32_fp32"]
+             "s8c5_blk16_fp32", "s16c10_finalblk8_bf16", "s8c3_2setblk32_fp32",
+             "s8c5_sample64_fp32", "s8c5_samplecover_fp32", "s8c10_prevthr_fp32"]
 
 
 def load_golden(name):
@@ -35,6 +36,9 @@ def load_golden(name):
         "out": z["out"][:, :, 0],   # [steps, B, Hq, D]
         "candidate": np.unpackbits(z["candidate"], axis=-1)[..., :t_max].astype(bool),
         "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
+        "selection": str(z["selection"]) if "selection" in z else "topk",
+        "sample_size": int(z["sample_size"]) if "sample_size" in z else 256,
+        "thresholds": z["thresholds"] if "thresholds" in z else None,   # [steps, B, Hq]
     }
 
 
@@ -45,12 +49,18 @@ def test_decode_steps_match_reference_vectors(name):
     # fp32: only the attention's summation order differs; bf16: the reference
     # rounds the softmax weights to bf16 (EV:4372-4373)
     tol = dict(rtol=1e-5, atol=1e-5) if g["dtype"] == "float32" else dict(rtol=1e-2, atol=2e-2)
+    thr = None
     for s in range(g["steps"]):
         n = g["t0"] + s + 1
+        got_thr = []
         out, cur, hf = R.reuse_decode_step(
             g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"], g["top_fraction"], g["sink"],
             g["recent"], g["keep_self"], g["scaling"], pc if g["use_prev_candidate"] else None,
-            pf if g["use_prev_final"] else None, g["block"])
+            pf if g["use_prev_final"] else None, g["block"], selection=g["selection"],
+            sample_size=g["sample_size"], previous_thresholds=thr, thresholds_out=got_thr)
+        thr = got_thr[0]
+        if g["thresholds"] is not None:
+            assert np.array_equal(thr[..., 0], g["thresholds"][s]), (name, s, "thresholds")
         assert np.array_equal(cur, g["candidate"][s][..., : n - 1]), (name, s)
         assert np.array_equal(hf, g["final"][s][..., : n - 1]), (name, s)
         np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
@@ -106,6 +116,34 @@ def test_reuse_select_block_expansion():
                                 scaling=1.0, block=4)
     assert np.flatnonzero(hf[0, 0]).tolist() == list(range(8))
     assert fi[0, 0][fv[0, 0]].tolist() == [7, 6, 5, 4, 3, 2, 1, 0]
+
+
+def test_candidate_mask_selections_known_answers():
+    p = np.array([[[5.0, 1.0, 4.0, 2.0, 3.0, 0.0, 6.0, 7.0]]], np.float32)
+    m, thr, used = R.candidate_mask(p, 3, 0.3, "topk")
+    assert used == "topk" and thr.tolist() == [[[5.0]]] and np.flatnonzero(m).tolist() == [0, 6, 7]
+    m, thr, used = R.candidate_mask(p, 3, 0.3, "previous_threshold", np.array([[3.5]], np.float32))
+    assert used == "previous_threshold" and np.flatnonzero(m).tolist() == [0, 2, 6, 7]
+    m, thr, used = R.candidate_mask(p, 3, 0.3, "previous_threshold", None)      # no previous step: topk
+    assert used == "topk" and thr.tolist() == [[[5.0]]]
+    # a sample of 4 of the 8 columns: linspace(0, 7, 4) = 0, 2.33, 4.67, 7 -> 0, 2, 5, 7; values 5, 4, 0, 7;
+    # ceil(0.3 * 4) = 2 -> threshold 5
+    assert R.sample_columns(8, 4).tolist() == [0, 2, 5, 7]
+    m, thr, used = R.candidate_mask(p, 3, 0.3, "sample_quantile", sample_size=4)
+    assert used == "sample_quantile" and thr.tolist() == [[[5.0]]] and np.flatnonzero(m).tolist() == [0, 6, 7]
+    assert R.sample_columns(8, 8) is None and R.sample_columns(8, 100) is None
+    # a sample of one column: the middle is not sampled, column 0 is
+    assert R.sample_columns(8, 1).tolist() == [0]
+
+
+def test_sample_columns_are_the_rounded_linspace():
+    # |position - i * (n - 1) / (s - 1)| <= 1/2 (+ float32 slack), ascending, unique, ends kept
+    for n, size in [(1000, 256), (32768, 256), (257, 256), (5000, 7), (99, 2)]:
+        cols = R.sample_columns(n, size)
+        exact = np.arange(size) * (n - 1) / (size - 1)
+        assert cols[0] == 0 and cols[-1] == n - 1 and np.all(np.diff(cols) > 0)
+        if len(cols) == size:
+            assert np.all(np.abs(cols - exact) <= 0.5 + 1e-3)
 
 
 def test_threshold_mask_keeps_ties():
@@ -189,6 +227,8 @@ def test_cpu_baseline_op_sequence_matches_reference_vectors(name):
     import torch
 
     g = load_golden(name)
+    if g["selection"] != "topk":
+        pytest.skip("the CPU baseline times the default candidate selection")
     dt = torch.float32 if g["dtype"] == "float32" else torch.bfloat16
     k, v = torch.from_numpy(g["k"]).to(dt), torch.from_numpy(g["v"]).to(dt)
     pc = pf = None
