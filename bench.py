@@ -64,6 +64,10 @@ def parse_args():
     p.add_argument("--kernel-reps", type=int, default=20, help="graph replays for per-kernel timing")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--reuse-mode", default=None,
+                   help="--config reuse: a qabs{S}cand{pct}reuse[final|2set][blk{bs}] mode (default qabs8cand5reuse)")
+    p.add_argument("--candidate-selection", default="topk", choices=["topk", "sample_quantile", "previous_threshold"],
+                   help="--config reuse: the reference's --qabs_candidate_selection")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
     p.add_argument("--profile-steps", type=int, default=0,
                    help="extra eager steps after timing, for rocprofv3 kernel statistics")
@@ -560,7 +564,8 @@ def run_reuse(args) -> dict:
 
     from kv_cache_amd import reuse as RU
 
-    c = REUSE
+    c = dict(REUSE, mode=args.reuse_mode or REUSE["mode"])
+    selection = args.candidate_selection
     layers = args.layers or 8
     b, hq, hkv, d, t0 = c["batch"], c["q_heads"], c["kv_heads"], c["head_dim"], c["history"]
     cap = -(-(t0 + args.warmup + args.steps + 2) // 64) * 64
@@ -574,7 +579,7 @@ def run_reuse(args) -> dict:
         v = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
         q = torch.randn((b, hq, d), generator=g, device="cuda").to(torch.bfloat16)
         st = RU.ReuseDecodeStep(c["mode"], b, hq, hkv, d, cap, top_fraction=c["top_fraction"],
-                                protect_sink=c["sink"], protect_recent=c["recent"])
+                                protect_sink=c["sink"], protect_recent=c["recent"], candidate_selection=selection)
         st.prefill(k[:, :, :t0])
         ks.append(k)
         vs.append(v)
@@ -622,7 +627,8 @@ def run_reuse(args) -> dict:
     def run_fixed():
         for layer in range(layers):
             st, kk, vv = fixed(layer)
-            st.launch(qs[layer], kk, vv, scaling, st.cand[0], st.cand[1], st.fin)
+            st.launch(qs[layer], kk, vv, scaling, st.cand[0], st.cand[1], st.fin,
+                      previous_thresholds=selection == "previous_threshold")
 
     reps = max(1, -(-16 // layers))
 
@@ -632,13 +638,15 @@ def run_reuse(args) -> dict:
                 fn()
         return run
 
-    gr = graph_of(repeated(run_fixed))
-    ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
-    del gr
-    log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
+    ms_graph = None
+    if selection != "sample_quantile":   # its sampled columns are copied from the host every step
+        gr = graph_of(repeated(run_fixed))
+        ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
+        del gr
+        log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
 
     mask_ws = [steps[l].mask_ws for l in range(layers)]
-    s_dims, cand_frac, _, _, _ = RU.parse_reuse_mode(c["mode"])
+    s_dims, cand_frac, _, _, block = RU.parse_reuse_mode(c["mode"])
     requested = RU.budget_count(hist_fixed, cand_frac)
 
     def run_partial():
@@ -650,6 +658,7 @@ def run_reuse(args) -> dict:
             RU.threshold_mask(steps[layer].partial, hist_fixed, requested, steps[layer].cand[0], mask_ws[layer])
 
     lib = RU._lib.load()
+    n_sel = int(lib.qkv_reuse_final_count(hist_fixed, c["sink"], c["recent"], c["top_fraction"], 1))
 
     def run_select():
         for layer in range(layers):
@@ -658,8 +667,16 @@ def run_reuse(args) -> dict:
                 qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv, hist_fixed + 1, d,
                 st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), cap, c["sink"], c["recent"],
                 c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
-                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_out, st.fin.data_ptr(),
+                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_sel, st.fin.data_ptr(),
                 cap, RU._lib.stream_of(qs[layer])))
+
+    def run_expand():
+        for layer in range(layers):
+            st = steps[layer]
+            RU._lib.check(lib.qkv_reuse_expand_blocks(
+                st.fin.data_ptr(), cap, rows, hist_fixed + 1, block, c["sink"], c["recent"], c["top_fraction"], 1,
+                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_out,
+                RU._lib.stream_of(qs[layer])))
 
     def run_attn():
         for layer in range(layers):
@@ -675,6 +692,8 @@ def run_reuse(args) -> dict:
         ("reuse_select", run_select, rows * hist_fixed * (3 + 4 + 1) + union * d * 2),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
+    if block is not None:   # one byte read and one written per history position
+        plan.insert(3, ("reuse_expand_blocks", run_expand, rows * hist_fixed * 2))
     kernels = {}
     for name, fn, nbytes in plan:
         gk = graph_of(repeated(fn))
@@ -708,10 +727,10 @@ def run_reuse(args) -> dict:
         "dtype": "bf16 -> f32 scores and attention",
         "data": "synthetic (seeded N(0,1) K/V/q)",
         "config": {"workload": f"reuse: {c['name']}", "batch": b, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
-                   "history": t0, "layers": layers, "mode": c["mode"], "top_fraction": c["top_fraction"],
-                   "sink": c["sink"], "recent": c["recent"], "graph": False},
+                   "history": t0, "layers": layers, "mode": c["mode"], "candidate_selection": selection,
+                   "top_fraction": c["top_fraction"], "sink": c["sink"], "recent": c["recent"], "graph": False},
         "us_per_layer": ms_per_step * 1e3 / layers,
-        "graph_us_per_layer": ms_graph * 1e3 / layers,
+        "graph_us_per_layer": None if ms_graph is None else ms_graph * 1e3 / layers,
         "union_tokens_per_row": union / rows,
         "final_entries_per_row": n_out,
         "roofline": {
@@ -894,6 +913,8 @@ def run_blocksel(args) -> dict:
         ("rerank", run_rerank, rows * (n_tok * 4 + n_cand * d * 2 + kc)),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
+    if block is not None:   # one byte read and one written per history position
+        plan.insert(3, ("reuse_expand_blocks", run_expand, rows * hist_fixed * 2))
     kernels = {}
     for name, fn, nbytes in plan:
         gk = graph_of(repeated(fn))

@@ -418,76 +418,96 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
 // ---------------------------------------------------------------------------
 // Block expansion of the final selection (the reuse...blk{bs} modes,
 // EV:4314-4316 with EV:2914-2922) and the final index list re-read from the
-// expanded mask (EV:2896-2911, 2938-2982).  One workgroup per row walks the
-// row in tiles of whole blocks (at most kExpandTile positions): the tile's
-// flags go to LDS, each thread that holds a set flag marks its block, the
-// expanded flags go back to the mask in place, and the positions outside
-// the protected ranges are numbered by a workgroup scan (each thread takes
-// consecutive positions) and listed in ascending order.  The list holds at
-// most body_cap entries, padded with (0, invalid, -1); the sink range, the
-// recent range and the current token follow.
+// expanded mask (EV:2896-2911, 2938-2982).  One 1024-thread workgroup per
+// row; thread j of a round owns block j0 + j: it ORs the block's flags
+// (16-byte loads when the block is a multiple of 16 bytes and the row is
+// aligned), fills a hit block with ones in place (a block without a set flag
+// is already all zero), and counts the block's positions outside the
+// protected ranges [0, sink_end) and [recent_start, history) from its span.
+// A workgroup scan of the counts numbers the entries, so the body lists the
+// expanded positions in ascending order; each wave then writes its share of
+// the list with consecutive lanes on consecutive entries (an entry's owning
+// thread found by a binary search over the wave's 64 run offsets in LDS).
+// At most body_cap entries, padded with (0, invalid, -1); the sink range,
+// the recent range and the current token follow.
 // ---------------------------------------------------------------------------
-constexpr int kExpandTile = 4096;
+constexpr int kExpandNT = 1024;
+constexpr int kMaxExpandBlock = 4096;   // one thread scans a block
 
-__global__ __launch_bounds__(kRT) void reuse_expand_kernel(
-    uint8_t* __restrict__ hf, int64_t hf_ld, int history, int block, int tile, int body_cap, int key_count,
-    int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
+__global__ __launch_bounds__(kExpandNT) void reuse_expand_kernel(
+    uint8_t* __restrict__ hf, int64_t hf_ld, int history, int block, int body_cap, int key_count, int sink_end,
+    int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
     uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out) {
-  __shared__ uint8_t flags[kExpandTile];
-  __shared__ uint8_t hit[kExpandTile];   // one flag per block of the tile
-  __shared__ int wave_tot[kRT / 64];
+  __shared__ int wave_tot[kExpandNT / 64];
+  __shared__ int run_off[kExpandNT], run_lo[kExpandNT];   // a thread's first entry within its wave, position
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
   const int64_t o = static_cast<int64_t>(row) * n_out;
-  const int nblk = tile / block;
+  const bool vec = (block & 15) == 0 && (reinterpret_cast<uintptr_t>(hrow) & 15) == 0;
+  const int nblk = static_cast<int>((static_cast<int64_t>(history) + block - 1) / block);
   int base = 0;   // body entries listed so far
-  for (int t0 = 0; t0 < history; t0 += tile) {
-    const int len = min(tile, history - t0);
-    for (int i = tid; i < len; i += kRT) flags[i] = hrow[t0 + i];
-    for (int i = tid; i < nblk; i += kRT) hit[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < len; i += kRT)
-      if (flags[i]) hit[i / block] = 1;
-    __syncthreads();
-    for (int i = tid; i < len; i += kRT) hrow[t0 + i] = hit[i / block];
-    const int c = (len + kRT - 1) / kRT;
-    const int lo = min(tid * c, len), hi = min(lo + c, len);
-    int cnt = 0;
-    for (int i = lo; i < hi; ++i) {
-      const int t = t0 + i;
-      cnt += (hit[i / block] && t >= sink_end && t < recent_start) ? 1 : 0;
-    }
-    const int incl = wave_incl_scan_dpp(cnt);
-    if (lane == 63) wave_tot[wave] = incl;
-    __syncthreads();
-    int p = base + incl - cnt, total = 0;
-#pragma unroll
-    for (int w = 0; w < kRT / 64; ++w) {
-      p += w < wave ? wave_tot[w] : 0;
-      total += wave_tot[w];
-    }
-    for (int i = lo; i < hi; ++i) {
-      const int t = t0 + i;
-      if (hit[i / block] && t >= sink_end && t < recent_start) {
-        if (p < body_cap) {
-          final_idx[o + p] = t;
-          final_valid[o + p] = 1;
-          if (attn_ids) attn_ids[o + p] = t;
+  for (int j0 = 0; j0 < nblk; j0 += kExpandNT) {
+    const int j = j0 + tid;
+    int64_t lo = 0, hi = 0;   // the block's body positions [lo, hi) when it is hit
+    if (j < nblk) {
+      const int64_t b_lo = static_cast<int64_t>(j) * block;
+      const int64_t b_hi = std::min<int64_t>(b_lo + block, history);
+      bool any = false;
+      if (vec && b_hi - b_lo == block) {
+        uint32_t acc = 0;
+        for (int64_t t = b_lo; t < b_hi; t += 16) {
+          const uint4 w = *reinterpret_cast<const uint4*>(hrow + t);
+          acc |= w.x | w.y | w.z | w.w;
         }
-        ++p;
+        any = acc != 0;
+        if (any)
+          for (int64_t t = b_lo; t < b_hi; t += 16)
+            *reinterpret_cast<uint4*>(hrow + t) = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
+      } else {
+        for (int64_t t = b_lo; t < b_hi; ++t) any |= hrow[t] != 0;
+        if (any)
+          for (int64_t t = b_lo; t < b_hi; ++t) hrow[t] = 1;
+      }
+      if (any) {
+        lo = std::max<int64_t>(b_lo, sink_end);
+        hi = std::min<int64_t>(b_hi, recent_start);
       }
     }
+    const int cnt = hi > lo ? static_cast<int>(hi - lo) : 0;
+    const int incl = wave_incl_scan_dpp(cnt);
+    run_off[tid] = incl - cnt;
+    run_lo[tid] = static_cast<int>(lo);
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int wave_base = base, total = 0;
+#pragma unroll
+    for (int w = 0; w < kExpandNT / 64; ++w) {
+      const int x = wave_tot[w];
+      wave_base += w < wave ? x : 0;
+      total += x;
+    }
+    const int w64 = wave * 64, wave_cnt = wave_tot[wave];
+    for (int q = lane; q < wave_cnt && wave_base + q < body_cap; q += 64) {
+      int k = 0;   // the last lane whose run starts at or before q
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1) k += run_off[w64 + k + step] <= q ? step : 0;
+      const int t = run_lo[w64 + k] + (q - run_off[w64 + k]);
+      const int64_t e = o + wave_base + q;
+      final_idx[e] = t;
+      final_valid[e] = 1;
+      if (attn_ids) attn_ids[e] = t;
+    }
     base += total;
-    __syncthreads();   // the next tile reuses flags, hit and wave_tot
+    __syncthreads();   // wave_tot is rewritten by the next round
   }
-  for (int p = min(base, body_cap) + tid; p < body_cap; p += kRT) {
+  for (int p = min(base, body_cap) + tid; p < body_cap; p += kExpandNT) {
     final_idx[o + p] = 0;
     final_valid[o + p] = 0;
     if (attn_ids) attn_ids[o + p] = -1;
   }
   const int extra = sink_end + n_rec + keep_self;
-  for (int i = tid; i < extra; i += kRT) {
+  for (int i = tid; i < extra; i += kExpandNT) {
     const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
     final_idx[o + body_cap + i] = idx;
     final_valid[o + body_cap + i] = 1;
@@ -748,7 +768,8 @@ QKV_EXPORT int qkv_reuse_expand_blocks(uint8_t* history_final, int64_t history_f
   if (history <= 0 || key_count >= (int64_t(1) << 31))
     return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 (history excludes the current token)", what);
   if (history_final_ld < history) return fail(QKV_ERR_INVALID, "%s: mask row stride must cover the history", what);
-  if (block < 1 || block > kExpandTile) return fail(QKV_ERR_INVALID, "%s: block must be in [1, %d]", what, kExpandTile);
+  if (block < 1 || block > kMaxExpandBlock)
+    return fail(QKV_ERR_INVALID, "%s: block must be in [1, %d]", what, kMaxExpandBlock);
   if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
   const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
   const int64_t body = block_body_cap(c, block);
@@ -756,9 +777,8 @@ QKV_EXPORT int qkv_reuse_expand_blocks(uint8_t* history_final, int64_t history_f
   if (n_out != need)
     return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the expanded selection needs %lld", what,
                 (long long)n_out, (long long)need);
-  const int64_t tile = block * (kExpandTile / block);
-  reuse_expand_kernel<<<static_cast<unsigned>(rows), kRT, 0, static_cast<hipStream_t>(stream)>>>(
-      history_final, history_final_ld, static_cast<int>(history), static_cast<int>(block), static_cast<int>(tile),
+  reuse_expand_kernel<<<static_cast<unsigned>(rows), kExpandNT, 0, static_cast<hipStream_t>(stream)>>>(
+      history_final, history_final_ld, static_cast<int>(history), static_cast<int>(block),
       static_cast<int>(body), static_cast<int>(key_count), static_cast<int>(c.sink_end),
       static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin), static_cast<int>(c.n_rec), keep_self ? 1 : 0,
       final_indices, final_valid, attn_ids, static_cast<int>(n_out));
