@@ -297,8 +297,9 @@ int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selectio
  *     thresholds when that is not NULL);
  *   QKV_CAND_SAMPLE_QUANTILE: the k-th largest of values[r, sample_cols[i]],
  *     i < n_sample (EV:3972-3987; the caller passes the sampled columns,
- *     the reference's rounded linspace, and k = the sample's budget),
- *     written to thresholds;
+ *     the reference's rounded linspace, each in [0, n) - they are device
+ *     data and not checked - and k = the sample's budget), written to
+ *     thresholds;
  *   QKV_CAND_PREVIOUS_THRESHOLD: thresholds[r] as given (EV:3967-3971).
  * values f32 [rows, ld]; mask uint8 row stride mask_ld; thresholds f32
  * [rows] (required for the last two). */

@@ -93,8 +93,15 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
              and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
     _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
              and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
-    _require(thresholds.dtype == torch.float32 and thresholds.is_contiguous()
-             and thresholds.numel() >= values.size(0), "thresholds must be f32 [rows]")
+    _require(thresholds.dtype == torch.float32 and thresholds.is_contiguous() and thresholds.is_cuda
+             and thresholds.numel() >= values.size(0), "thresholds must be CUDA f32 [rows]")
+    if selection == "sample_quantile":
+        _require(sample_cols is not None and sample_cols.dtype == torch.int32 and sample_cols.is_contiguous()
+                 and 1 <= n_sample <= sample_cols.numel(), "sample_cols must be int32 [>= n_sample]")
+        if not sample_cols.is_cuda:   # host columns are checked, then copied (device ones must lie in [0, n))
+            _require(bool(((sample_cols[:n_sample] >= 0) & (sample_cols[:n_sample] < n)).all()),
+                     "sample_cols must lie in [0, n)")
+            sample_cols = sample_cols.to(values.device)
     with torch.cuda.device(values.device):
         _lib.check(lib.qkv_candidate_mask(
             values.data_ptr(), values.size(0), int(n), values.stride(0), code, int(k), _lib.ptr(sample_cols),
