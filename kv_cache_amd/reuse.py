@@ -79,13 +79,13 @@ def sample_columns(history: int, sample_size: int) -> torch.Tensor | None:
 
 
 def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: torch.Tensor,
-                   thresholds: torch.Tensor, workspace: torch.Tensor, sample_cols: torch.Tensor | None = None,
+                   thresholds: torch.Tensor | None, workspace: torch.Tensor, sample_cols: torch.Tensor | None = None,
                    n_sample: int = 0) -> torch.Tensor:
     """mask[:, :n] = values[:, :n] >= the row's threshold under ``selection``
     (EV:3958-3989): the k-th largest value (``topk``), the k-th largest of
     the ``n_sample`` columns ``sample_cols`` (``sample_quantile``), or
     ``thresholds`` as given (``previous_threshold``).  The first two write
-    the threshold to ``thresholds`` (f32 [rows])."""
+    the threshold to ``thresholds`` (f32 [rows]; optional for ``topk``)."""
     lib = _lib.load()
     code = CANDIDATE_SELECTIONS.get(selection)
     _require(code is not None, f"unknown candidate selection {selection!r}")
@@ -93,8 +93,10 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
              and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
     _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
              and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
-    _require(thresholds.dtype == torch.float32 and thresholds.is_contiguous() and thresholds.is_cuda
-             and thresholds.numel() >= values.size(0), "thresholds must be CUDA f32 [rows]")
+    _require(thresholds is not None or selection == "topk", f"{selection} needs the thresholds array")
+    _require(thresholds is None or (thresholds.dtype == torch.float32 and thresholds.is_contiguous()
+                                    and thresholds.is_cuda and thresholds.numel() >= values.size(0)),
+             "thresholds must be CUDA f32 [rows]")
     if selection == "sample_quantile":
         _require(sample_cols is not None and sample_cols.dtype == torch.int32 and sample_cols.is_contiguous()
                  and 1 <= n_sample <= sample_cols.numel(), "sample_cols must be int32 [>= n_sample]")
@@ -105,7 +107,7 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
     with torch.cuda.device(values.device):
         _lib.check(lib.qkv_candidate_mask(
             values.data_ptr(), values.size(0), int(n), values.stride(0), code, int(k), _lib.ptr(sample_cols),
-            int(n_sample), thresholds.data_ptr(), mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
+            int(n_sample), _lib.ptr(thresholds), mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
             workspace.numel() * 4, _lib.stream_of(values)))
     return mask
 
@@ -246,7 +248,9 @@ class ReuseDecodeStep:
         self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
         self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
-        self.thresholds = torch.zeros(rows, dtype=torch.float32, device=device)   # the last step's, per row
+        # the last step's candidate threshold per row (EV:1744-1745), written by the
+        # previous_threshold and sample_quantile selections
+        self.thresholds = torch.zeros(rows, dtype=torch.float32, device=device)
         self.sample_cols = torch.empty(min(self.sample_size, cap), dtype=torch.int32, device=device)
         hist_max = cap - 1
         # every term of the counts grows with the history
@@ -352,7 +356,9 @@ class ReuseDecodeStep:
         else:                                                                 # EV:3988
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
-            candidate_mask(self.partial, history, "topk", requested, current, self.thresholds, self.mask_ws)
+            # the threshold is kept only where a later step reads it
+            candidate_mask(self.partial, history, "topk", requested, current,
+                           self.thresholds if self.selection != "topk" else None, self.mask_ws)
         n_sel = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
         n_out = self._final_count(history)
         self.select_ws = self._grow(self.select_ws,
