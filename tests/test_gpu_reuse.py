@@ -216,6 +216,36 @@ def test_step_selections_match_oracle(hq, hkv, t, steps, mode, selection, sample
         pc, pf = wc, wf
 
 
+@pytest.mark.parametrize("mode,selection", [("qabs8cand5reuseblk8", "previous_threshold"),
+                                            ("qabs16cand10reusefinal", "sample_quantile"),
+                                            ("qabs8cand5reuse2setblk32", "topk")])
+def test_step_batches_match_oracle(mode, selection):
+    # two sequences: rows b * Hq + h read their own K/V, dim-major copy and masks
+    gen = torch.Generator().manual_seed(len(mode) * 31 + len(selection))
+    b, hq, hkv, t, steps = 2, 4, 2, 700, 3
+    s_dims, cand, use_pc, use_pf, block = RU.parse_reuse_mode(mode)
+    k = torch.randn((b, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((b, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    qs = torch.randn((steps, b, hq, 128), generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = RU.ReuseDecodeStep(mode, b, hq, hkv, 128, t + steps + 8, top_fraction=0.03, protect_sink=2,
+                              protect_recent=5, candidate_selection=selection, threshold_sample_size=64)
+    pc = pf = thr = None
+    for s in range(steps):
+        n = t + s + 1
+        out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 0.09)
+        got = []
+        want, wc, wf = R.reuse_decode_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), s_dims, cand, 0.03, 2, 5,
+                                           True, 0.09, pc if use_pc else None, pf if use_pf else None, block,
+                                           selection=selection, sample_size=64, previous_thresholds=thr,
+                                           thresholds_out=got)
+        thr = got[0]
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+        pc, pf = wc, wf
+
+
 @pytest.mark.parametrize("rows,history,block,sink,recent,keep_self,density", [
     (3, 1000, 16, 4, 8, True, 0.01),
     (2, 9000, 64, 0, 0, False, 0.002),      # three tiles of 4096
