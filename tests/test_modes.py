@@ -67,3 +67,38 @@ def test_decode_plan():
     assert M.decode_plan("qabs8cand3reuse", 4097) is None          # not a mode of this path
     assert M.decode_plan("qabs32cand5attn", 1) is None             # no history yet
     assert M.selected_dims(500, 128) == 128 and M.selected_dims(0, 128) == 16
+
+
+@pytest.mark.parametrize("mode,want", [
+    ("qabs8cand5reuse", (8, 0.05, True, True, None)),
+    ("qabs16cand10reusefinal", (16, 0.10, False, True, None)),
+    ("qabs8cand3reuse2set", (8, 0.03, True, False, None)),
+    ("qabs8cand6p25reuseblk16", (8, 0.0625, True, True, 16)),
+    # EV:955-960 test the suffix: with a blk suffix both previous masks stay on
+    ("qabs16cand10reusefinalblk8", (16, 0.10, True, True, 8)),
+    ("qabs8cand3reuse2setblk32", (8, 0.03, True, True, 32)),
+    ("qabs8cand5reuseblk0", (8, 0.05, True, True, 1)),     # max(1, bs) (EV:757-761)
+])
+def test_parse_reuse_mode(mode, want):
+    from kv_cache_amd import reuse as RU
+
+    dims, frac, use_pc, use_pf, block = RU.parse_reuse_mode(mode)
+    assert (dims, use_pc, use_pf, block) == (want[0], want[2], want[3], want[4])
+    assert math.isclose(frac, want[1])
+
+
+@pytest.mark.parametrize("mode", ["qabs8cand5attn", "qabs8cand5reuseblk", "qabs8cand5reusefinal2set", "reuse"])
+def test_parse_reuse_mode_rejects(mode):
+    from kv_cache_amd import reuse as RU
+
+    with pytest.raises(RuntimeError, match="is not a qabs"):
+        RU.parse_reuse_mode(mode)
+
+
+def test_sample_columns_host():
+    from kv_cache_amd import reuse as RU
+
+    assert RU.sample_columns(100, 256) is None and RU.sample_columns(100, 100) is None
+    cols = RU.sample_columns(1000, 64)
+    assert cols.dtype.is_floating_point is False and cols.numel() == 64
+    assert int(cols[0]) == 0 and int(cols[-1]) == 999
