@@ -1,9 +1,12 @@
 #!/usr/bin/env python3
 """Benchmark of the int4 sparse-attention KV-retrieval path on one MI355X.
 
-Decode configs (cfg1-cfg4; default cfg2): a "step" is one decode step of
-every layer of the workload: per layer, the fused int4 scoring + block max
-kernel, the top-k kernel and the GQA sparse attention.  Inputs (K/V bf16,
+Decode configs (cfg1-cfg4): a "step" is one decode step of every layer of
+the workload: per layer, the fused int4 scoring + block max kernel, the
+top-k selection and the GQA sparse attention.  The default is cfg3, the
+largest configuration that fits one GPU (Qwen3-8B heads, batch 32, context
+32768, all 36 layers resident: about 172 GiB), followed in the same run by
+cfg2 (Qwen3-0.6B, 28 layers), whose figures go under "secondary".  Inputs (K/V bf16,
 int4 packed K, subset slab, q) are generated and quantized before the timed
 region and stay resident in HBM; every layer has its own buffers, so a step
 streams far more than the 256 MB Infinity Cache.  The step is captured once
@@ -58,7 +61,11 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse", "qbb", "brep"])
+    p.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse", "qbb", "brep"],
+                   help="workload (default cfg3: the largest single-GPU config, all 36 layers resident)")
+    p.add_argument("--secondary", default=None,
+                   help="a second decode config measured in the same run, reported under 'secondary' "
+                        "(default: cfg2 when --config is cfg3; 'none' to skip)")
     p.add_argument("--layers", type=int, default=None,
                    help="layer buffers to rotate through (default: the config's layer count, at least 8)")
     p.add_argument("--kernel-reps", type=int, default=20, help="graph replays for per-kernel timing")
@@ -73,7 +80,14 @@ def parse_args():
                    help="extra eager steps after timing, for rocprofv3 kernel statistics")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="also run a plain device copy of this many MiB (HBM counter calibration)")
-    return p.parse_args()
+    args = p.parse_args()
+    if args.secondary is None:
+        args.secondary = "cfg2" if args.config == "cfg3" else None
+    elif args.secondary == "none":
+        args.secondary = None
+    elif args.secondary not in ("cfg1", "cfg2", "cfg3", "cfg4"):
+        p.error("--secondary must be a decode config (cfg1-cfg4) or 'none'")
+    return args
 
 
 def log(msg: str) -> None:
@@ -111,16 +125,46 @@ def time_replays(replay, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def host_threads() -> int:
+    """Threads of the CPU baselines: every core this process may run on (its
+    affinity set), capped by OMP_NUM_THREADS where the host sets it -- the GPU
+    box sets it to the CPU share of its one GPU, which the whole host's
+    os.cpu_count() does not reflect."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        cap = 0
+    return max(1, min(avail, cap) if cap > 0 else avail)
+
+
+def cpu_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def host_note(threads: int) -> str:
+    return f"{threads} threads on {cpu_name() or 'unknown CPU'} (os.cpu_count() = {os.cpu_count()})"
+
+
 def cpu_baseline(cfg, budget_s: float) -> dict:
     """The reference's qabs{S}cand{pct}attn op sequence on CPU tensors for one
-    sequence of one layer, repeated for about ``budget_s`` seconds."""
+    sequence of one layer, repeated for about ``budget_s`` seconds.  Rows are
+    independent, so the keys/s of one sequence is the rate of the full batch."""
     import torch
 
     from kv_cache_amd.workloads import make_layer
     from oracle import ref_semantics as R
 
-    cores = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(cores)
+    torch.set_num_threads(host_threads())
     q, k, v, _ = make_layer(cfg, 0, device="cpu", batch=1)
     qs = q[:, :, None, :]
     frac = cfg.topk * cfg.block / cfg.tokens
@@ -134,23 +178,16 @@ def cpu_baseline(cfg, budget_s: float) -> dict:
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     keys = cfg.kv_heads * cfg.tokens
-    cpu_name = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {
         "value": keys / med,
         "unit": "keys/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"one sequence x one layer of {cfg.name}: reference op sequence (top-|q| {cfg.selected} "
-                   f"dims, fp32 partial scores over GQA-expanded bf16 K, top {frac:.4%} tokens, gather "
-                   f"attention) on CPU tensors; {keys} keys/call, median of {len(times)} calls "
-                   f"= {med * 1e3:.1f} ms; {cpu_name}"),
+        "sample": (f"one sequence (of {cfg.batch}) x one layer of {cfg.name}: reference op sequence (top-|q| "
+                   f"{cfg.selected} dims, fp32 partial scores over GQA-expanded bf16 K, top {frac:.4%} tokens, "
+                   f"gather attention) on CPU tensors; {keys} keys/call, median of {len(times)} calls "
+                   f"= {med * 1e3:.1f} ms, keys/s scales linearly to the batch (rows are independent); "
+                   f"{host_note(torch.get_num_threads())}"),
     }
 
 
@@ -184,7 +221,20 @@ def main() -> int:
     elif args.config in ("qbb", "brep"):
         line = run_blocksel(args)
     else:
-        line = run_decode(args)
+        line = run_decode(args, args.config, args.layers)
+        if args.secondary and args.secondary != args.config:
+            # A second decode workload in the same run (default: cfg2 after the
+            # cfg3 headline); its own buffers are built after the first's are freed.
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            try:
+                sec = run_decode(args, args.secondary, with_cpu=True)
+                line["secondary"] = {k: sec[k] for k in ("config", "value", "unit", "ms_per_step", "us_per_layer",
+                                                         "dense_bf16_us_per_layer", "roofline", "kernels",
+                                                         "cpu_baseline")}
+            except Exception as exc:   # the headline line is still printed
+                log(f"[bench] secondary workload {args.secondary} failed: {exc!r}")
+                line["secondary"] = {"config": {"workload": args.secondary}, "error": repr(exc)}
     print(json.dumps(line), flush=True)
     return 0
 
@@ -222,16 +272,16 @@ def planted_recall(cfg, qs, caches, planted, ks=(64, 256, 1024)) -> dict:
     return {str(k): hits[k] / total for k in ks}
 
 
-def run_decode(args) -> dict:
+def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True) -> dict:
     import torch
 
     from kv_cache_amd import int4 as K
     from kv_cache_amd.workloads import CONFIGS, make_layer
 
-    cfg = CONFIGS[args.config]
+    cfg = CONFIGS[name]
     # Single-layer configs rotate 8 distinct layer buffers (seeds seed..seed+7)
     # so that repeated steps do not run out of the 256 MB Infinity Cache.
-    layers, rows, T = (args.layers or max(cfg.layers, 8)), cfg.rows, cfg.tokens
+    layers, rows, T = (layers or max(cfg.layers, 8)), cfg.rows, cfg.tokens
     log(f"[bench] setup {cfg.name}: {layers} layers, rows={rows}, T={T}, S={cfg.selected}, "
         f"block={cfg.block}, top-{cfg.topk}")
     qs, ks, vs, caches, planted = [], [], [], [], []
@@ -242,6 +292,9 @@ def run_decode(args) -> dict:
         ks.append(k)
         vs.append(v)
         planted.append(pl)
+        if (layer + 1) % 8 == 0 and layer + 1 < layers:
+            torch.cuda.synchronize()
+            log(f"[bench] {layer + 1} layers built, {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
     torch.cuda.synchronize()
     log(f"[bench] resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
 
@@ -328,7 +381,7 @@ def run_decode(args) -> dict:
         log(f"[bench] planted-key recall at k tokens: {recall}")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if with_cpu and not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline(cfg, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
@@ -349,7 +402,7 @@ def run_decode(args) -> dict:
         "dtype": "i32 (int8 query x int4 K); bf16->f32 attention",
         "data": "synthetic (seeded N(0,1) K/V/q, 4 outlier channels x8)",
         "config": {
-            "workload": f"{args.config}: {cfg.name}",
+            "workload": f"{name}: {cfg.name}",
             "batch": cfg.batch, "q_heads": cfg.q_heads, "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
             "context": T, "layers": layers, "int4_group": cfg.group, "channels": cfg.selected,
             "block": cfg.block, "topk_blocks": cfg.topk, "graph": not args.eager, "fused_select": step.fused,
@@ -363,7 +416,7 @@ def run_decode(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": sc["gbs"] / HBM_PEAK_GBS,
-            "traffic": read_traffic(args.config, "decode_scores_kernel"),
+            "traffic": read_traffic(name, "decode_scores_kernel"),
         },
         "kernels": kernels,
         "cpu_baseline": cpu,
@@ -398,10 +451,11 @@ def cpu_baseline_prefill(cfg, budget_s: float) -> dict:
     return {
         "value": pairs / med,
         "unit": "query-key pairs/s",
-        "cores": torch.get_num_threads(),
+        "cores": 1,
         "kind": "port",
-        "sample": (f"4 query rows x {cfg.tokens} int4 keys of one head: numpy int64 scoring, causal block-64 "
-                   f"max, top-{cfg.topk}; median of {len(times)} calls = {med * 1e3:.1f} ms"),
+        "sample": (f"4 query rows x {cfg.tokens} int4 keys of one head: numpy int64 scoring (einsum, one "
+                   f"thread), causal block-64 max, top-{cfg.topk}; median of {len(times)} calls = "
+                   f"{med * 1e3:.1f} ms; {cpu_name() or 'unknown CPU'}"),
     }
 
 
@@ -520,8 +574,7 @@ def cpu_baseline_reuse(budget_s: float, steps: int = 3) -> dict:
     from kv_cache_amd.reuse import parse_reuse_mode
 
     c = REUSE
-    cores = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(cores)
+    torch.set_num_threads(host_threads())
     g = torch.Generator().manual_seed(0)
     t = c["history"] + steps + 1
     k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
@@ -758,8 +811,7 @@ def cpu_baseline_blocksel(mode: str, budget_s: float, steps: int = 3) -> dict:
 
     c = REUSE
     kind, block, reps, dims, scan, cand = parse_block_mode(mode)
-    cores = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(cores)
+    torch.set_num_threads(host_threads())
     g = torch.Generator().manual_seed(0)
     t = c["history"] + steps + 1
     k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)

@@ -8,8 +8,10 @@ ids, slab, block maxima and top-k; attention within 1e-2 relative / 2e-2
 absolute of fp64).  On every row, the GPU's top-k is checked against a
 stable sort of the GPU's own block maxima, which is exact at any size.
 Config 4 also reports the recall of its planted key at k = 64, 256 and
-1024 tokens, which must equal the oracle's.  Config 3 runs at batch 8 of
-its 32 (64 rows of 32768 keys; rows do not interact)."""
+1024 tokens, which must equal the oracle's.  Config 3 runs at its full
+batch of 32 (256 rows of 32768 keys, one layer), so the step launches the
+same kernels on the same grids as the benchmark: the fused selection +
+attention with 32 chunks per wave on 2 x 256 workgroups."""
 
 import numpy as np
 import pytest
@@ -83,8 +85,8 @@ def test_config2_full_layer():
     _decode_case("cfg2", n_rows=3)
 
 
-def test_config3_rows():
-    _decode_case("cfg3", batch=8, n_rows=3)
+def test_config3_full_batch():
+    _decode_case("cfg3", n_rows=4)
 
 
 def test_config4_planted_recall():
