@@ -233,6 +233,26 @@ int qkv_sparse_attention_select(const void* query, const void* key, const void* 
                                 float* workspace, int64_t workspace_bytes, int32_t* sel_out, void* out,
                                 void* stream);
 
+/* Bytes of the static device scratch behind
+ * qkv_sparse_attention_select_noalloc (one copy per GPU, held until the
+ * process ends). */
+#define QKV_NOALLOC_SCRATCH_BYTES (8LL << 20)
+
+/* qkv_sparse_attention_select without a workspace argument and without any
+ * allocation: no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc.  The workspace lives in a
+ * static device array of QKV_NOALLOC_SCRATCH_BYTES per GPU; sizes whose
+ * qkv_sparse_attention_workspace_bytes exceeds it fail with
+ * QKV_ERR_UNSUPPORTED.  All calls on one GPU share that array, so calls that
+ * overlap in time on one GPU (other streams, other threads) race; serialize
+ * them.  Arguments and results as for qkv_sparse_attention_select. */
+int qkv_sparse_attention_select_noalloc(const void* query, const void* key, const void* value,
+                                        const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                        int64_t kv_heads, int64_t tokens, int64_t head_dim, const float* bmax,
+                                        int64_t bmax_ld, int64_t n_sel, int64_t block, float scaling,
+                                        int32_t* sel_out, void* out, void* stream);
+
 /* qkv_sparse_attention with one token list per query head (group size 1,
  * one-token blocks): row (b, h) attends over token_ids [B,Hq,n_ids] (ids
  * outside [0, tokens) skipped) of K/V head h / (Hq/Hkv).  Replaces the

@@ -58,6 +58,8 @@ _PROTOTYPES = {
                                     _i64, _f32, _vp, _i64, _vp, _vp]),
     "qkv_sparse_attention_select": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                            _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
+    "qkv_sparse_attention_select_noalloc": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp,
+                                                   _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
     "qkv_token_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _f32, _vp,
                                    _i64, _vp, _vp]),
     "qkv_reuse_final_count": (_i64, [_i64, _i64, _i64, _f64, _i32]),

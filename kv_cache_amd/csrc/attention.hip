@@ -32,6 +32,8 @@
 // (sc1), every load of a batch in flight at once, and writes the output.
 // No release / acquire fence is used: on gfx950 those write back and
 // invalidate the whole L2 of the XCD (buffer_wbl2 / buffer_inv).
+#include <mutex>
+
 #include "common.h"
 #include "select.h"
 
@@ -674,6 +676,87 @@ QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, c
   return launch_attention("qkv_sparse_attention_select", query, key, value, kv_strides, batch, q_heads,
                           kv_heads, tokens, head_dim, nullptr, bmax, bmax_ld, sel_out, n_sel, block, scaling,
                           workspace, workspace_bytes, out, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of qkv_sparse_attention_select.  Its workspace
+// (row tickets, then per-split partials) is this file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel: the name is a host-side stand-in, and the device
+// address of each GPU's copy comes from hipGetSymbolAddress, taken once per
+// device with that device current.  Every call on a GPU shares that GPU's
+// copy, so calls that overlap in time on one GPU race; the ticket words are
+// cleared once per device (by a fill kernel on the caller's stream) and every
+// completed call leaves them zero again.
+static __device__ __align__(256) float scratch[QKV_NOALLOC_SCRATCH_BYTES / 4];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices];   // device address of `scratch` on each device
+bool g_scratch_clear[kMaxDevices];   // ticket words cleared by an eager (uncaptured) fill
+
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+}  // namespace
+
+QKV_EXPORT int qkv_sparse_attention_select_noalloc(const void* query, const void* key, const void* value,
+                                                   const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                                   int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                                                   const float* bmax, int64_t bmax_ld, int64_t n_sel,
+                                                   int64_t block, float scaling, int32_t* sel_out, void* out,
+                                                   void* stream) {
+  static const char* what = "qkv_sparse_attention_select_noalloc";
+  if (!bmax) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block);
+  if (need < 0)
+    return fail(QKV_ERR_INVALID, "%s: unsupported sizes (head_dim 128, q_heads a multiple of kv_heads, n_sel > 0)",
+                what);
+  if (need > QKV_NOALLOC_SCRATCH_BYTES)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: these sizes need %lld bytes of scratch; the static scratch holds %lld",
+                what, (long long)need, (long long)QKV_NOALLOC_SCRATCH_BYTES);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(QKV_ERR_LAUNCH, "%s: no current device below %d", what, kMaxDevices);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* ws = nullptr;
+  bool clear = false;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(QKV_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    ws = g_scratch_ptr[dev];
+    clear = g_scratch_clear[dev];
+  }
+  if (!clear) {
+    // Clear the ticket words ahead of the attention kernel on the same
+    // stream.  Under graph capture the fill becomes part of the graph (and
+    // runs on every replay), so only an eager fill marks the device done.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess)
+      return fail(QKV_ERR_LAUNCH, "%s: hipStreamIsCapturing failed", what);
+    zero_words_kernel<<<64, 256, 0, st>>>(reinterpret_cast<uint32_t*>(ws), kTicketWords);
+    const int rc = check_launch(what);
+    if (rc != QKV_OK) return rc;
+    if (cs == hipStreamCaptureStatusNone) {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      g_scratch_clear[dev] = true;
+    }
+  }
+  return launch_attention(what, query, key, value, kv_strides, batch, q_heads, kv_heads, tokens, head_dim, nullptr,
+                          bmax, bmax_ld, sel_out, n_sel, block, scaling, ws, QKV_NOALLOC_SCRATCH_BYTES, out,
+                          stream);
 }
 
 QKV_EXPORT int qkv_token_attention(const void* query, const void* key, const void* value,

@@ -79,6 +79,17 @@ def _err():
                                          ctypes.c_void_p(16), None, 5, None), "expanded selection needs"),
     (lambda: lib.qkv_reuse_expand_blocks(ctypes.c_void_p(16), 8, 1, 11, 4, 0, 0, 0.1, 1, ctypes.c_void_p(16),
                                          ctypes.c_void_p(16), None, 5, None), "stride"),
+    (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                                     _lib.strides(8, 8, 8), 1, 16, 8, 100, 128, None, 7, 4, 16,
+                                                     1.0, None, ctypes.c_void_p(16), None), "null pointer"),
+    (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                                     _lib.strides(8, 8, 8), 1, 16, 8, 100, 64, ctypes.c_void_p(16), 7,
+                                                     4, 16, 1.0, None, ctypes.c_void_p(16), None), "unsupported sizes"),
+    # 4096 rows x 65536 selected slots: far beyond the 8 MiB static scratch
+    (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                                     _lib.strides(8, 8, 8), 64, 64, 64, 65536, 128,
+                                                     ctypes.c_void_p(16), 4096, 4096, 16, 1.0, None,
+                                                     ctypes.c_void_p(16), None), "static scratch holds"),
 ])
 def test_host_side_validation(call, msg):
     rc = call()
