@@ -364,12 +364,13 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
     if step.fused:   # the step's own second launch: selection inside the attention kernel
         plan.insert(3, ("select_sparse_attention", run_select_attn,
                         rows * (cfg.n_blocks * 4 + sel_tokens * cfg.head_dim * 2 * 2)))
-    for name, fn, nbytes in plan:
+    for kname, fn, nbytes in plan:
         g = graph_of(repeated(fn))
         ms = time_replays(g.replay, args.kernel_reps) / (layers * reps)
-        kernels[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes,
-                         "gbs": nbytes / (ms * 1e-3) / 1e9, "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
-        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
+        kernels[kname] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes,
+                          "gbs": nbytes / (ms * 1e-3) / 1e9,
+                          "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"[bench] {kname}: {ms * 1e3:.2f} us/launch, {kernels[kname]['gbs']:.0f} GB/s")
         del g
 
     for _ in range(args.profile_steps):
