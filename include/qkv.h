@@ -233,6 +233,26 @@ int qkv_sparse_attention_select(const void* query, const void* key, const void* 
                                 float* workspace, int64_t workspace_bytes, int32_t* sel_out, void* out,
                                 void* stream);
 
+/* qkv_sparse_attention / qkv_sparse_attention_select with the reference's
+ * protected tokens (EV:2938-2982, applied at EV:4460): the n_sel blocks are
+ * chosen over the history [0, history) -- given in block_ids, or selected
+ * in the kernel from bmax when block_ids is NULL (exactly one of the two) --
+ * and the attention set is those blocks' tokens minus the sink range
+ * [0, min(protect_sink, history)) and the recent range
+ * [max(0, history - protect_recent), history), plus both ranges in full and,
+ * when keep_self, the current token `history`; every token once.  K/V hold
+ * at least history + 1 tokens when keep_self.  Workspace: at least
+ * qkv_sparse_attention_workspace_bytes(B, Hq, Hkv, D, n_sel +
+ * ceil(n_protected / block), block) with n_protected = sink + recent
+ * tokens (not overlapping) + keep_self.  sel_out (with bmax only, may be
+ * NULL) receives the selection. */
+int qkv_sparse_attention_protected(const void* query, const void* key, const void* value,
+                                   const int64_t* kv_strides, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                   int64_t history, int64_t head_dim, const int32_t* block_ids, const float* bmax,
+                                   int64_t bmax_ld, int64_t n_sel, int64_t block, int64_t protect_sink,
+                                   int64_t protect_recent, int keep_self, float scaling, float* workspace,
+                                   int64_t workspace_bytes, int32_t* sel_out, void* out, void* stream);
+
 /* Bytes of the static device scratch behind
  * qkv_sparse_attention_select_noalloc (one copy per GPU, held until the
  * process ends). */
@@ -422,6 +442,35 @@ int qkv_block_scan_scores(const void* query, const void* key_dim_major, const in
                           int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
                           const int32_t* blocks, int64_t n_scan, int64_t block, int64_t dim_count, float* out,
                           int64_t out_ld, void* stream);
+
+/* Block scores of the qboracle selector (EV:5030-5044): out[r, j] = the
+ * largest partial score, on row r's top-|q| dims (ties to the lower dim,
+ * summed in selection order), of block j's history tokens
+ * [j*block, min(history, (j+1)*block)), read from the dim-major K copy
+ * (qkv_dim_major_append).  query bf16 [B,Hq,D]; out f32 [rows, >= out_ld],
+ * rows = B*Hq.  block <= 2048. */
+int qkv_block_max_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
+                                 int64_t block, int64_t dim_count, float* out, int64_t out_ld, void* stream);
+
+/* Replaces brep_partial_scores, which the reference imports from its
+ * extension module but never shipped (wrapper EV:3847-3877, call
+ * EV:5419-5431, signature `brep_partial_scores(query, key_history,
+ * rep_indices, rep_valid, block_size, dim_count, scan_fraction)`).
+ * query f32 [B,H,D] contiguous (the reference passes the fp32 query);
+ * key_history [B,H,T,D] of key_dtype with k_strides {b,h,t,d}, d contiguous;
+ * rep_indices int64 and rep_valid u8, both [B,H,ceil(T/block_size),reps]
+ * contiguous (the reference's BlockRepState, EV:1857-1918).  out f32
+ * [B,H,T]: the partial score over the row's min(max(dim_count,1), D, 128)
+ * largest-|q| dims (ties to the lower dim), summed in that order, for every
+ * token of the min(blocks, max(1, ceil(scan_fraction * T / block_size)))
+ * blocks whose best valid representative scores highest (a block without
+ * one scores finfo(float32).min; ties to the lower block); -inf elsewhere.
+ * At most 40960 blocks per row. */
+int qkv_brep_partial_scores(const float* query, const void* key_history, const int64_t* rep_indices,
+                            const uint8_t* rep_valid, float* out, int key_dtype, int64_t batch, int64_t heads,
+                            int64_t history, int64_t head_dim, const int64_t* k_strides, int64_t reps,
+                            int64_t block_size, int64_t dim_count, double scan_fraction, void* stream);
 
 /* Entries of a final token list: n_keep + sink range + recent range (not
  * overlapping the sink) + 1 when keep_self.  -1 for history <= 0. */

@@ -1,6 +1,7 @@
-"""Block-metadata selectors: the reference's ``qbb{bs}q{S}s{scan}cand{c}``
-(Quest-style per-block channel bounds) and ``brep{bs}r{R}q{S}s{scan}cand{c}``
-(block representatives) decode steps on MI355X.
+"""Block selectors: the reference's ``qbb{bs}q{S}s{scan}cand{c}``
+(Quest-style per-block channel bounds), ``brep{bs}r{R}q{S}s{scan}cand{c}``
+(block representatives) and ``qboracle{bs}q{S}s{scan}cand{c}`` (block maxima
+of the partial scores, EV:5008-5097) decode steps on MI355X.
 
 Per layer and decode token the reference ("EV" =
 evaluate_qwen3_top2_head_limit3_ppl.py) scores every block of the history by
@@ -31,6 +32,7 @@ from .int4 import block_topk, topk_workspace
 from .reuse import dim_major_append, token_attention
 
 QBB, BREP = 0, 1   # QKV_BLOCK_QBB, QKV_BLOCK_BREP
+QBORACLE = 2       # block maxima of the partial scores: no per-block metadata
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -43,15 +45,20 @@ def _pct(x: str) -> float:
 
 
 def parse_block_mode(mode: str) -> tuple[int, int, int, int, float, float]:
-    """``qbb{bs}q{S}s{scan}cand{c}`` / ``brep{bs}r{R}q{S}s{scan}cand{c}`` ->
-    (kind, block, reps, dims, scan fraction, candidate fraction), with the
-    reference's readings (parse_qbb_params EV:856-864, parse_brep_params
-    EV:835-844: block and reps at least 1, ``p`` as the decimal point)."""
+    """``qbb{bs}q{S}s{scan}cand{c}`` / ``brep{bs}r{R}q{S}s{scan}cand{c}`` /
+    ``qboracle{bs}q{S}s{scan}cand{c}`` -> (kind, block, reps, dims, scan
+    fraction, candidate fraction), with the reference's readings
+    (parse_qbb_params EV:856-864, parse_brep_params EV:835-844,
+    parse_qboracle_params EV:798-806: block and reps at least 1, ``p`` as the
+    decimal point)."""
     m = re.fullmatch(r"qbb(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
     if m:
         return QBB, max(1, int(m.group(1))), 1, int(m.group(2)), _pct(m.group(3)), _pct(m.group(4))
+    m = re.fullmatch(r"qboracle(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
+    if m:   # parse_qboracle_params, EV:798-806
+        return QBORACLE, max(1, int(m.group(1))), 1, int(m.group(2)), _pct(m.group(3)), _pct(m.group(4))
     m = re.fullmatch(r"brep(\d+)r(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
-    _require(m is not None, f"{mode!r} is not a qbb or brep mode")
+    _require(m is not None, f"{mode!r} is not a qbb, brep or qboracle mode")
     return (BREP, max(1, int(m.group(1))), max(1, int(m.group(2))), int(m.group(3)), _pct(m.group(4)),
             _pct(m.group(5)))
 
@@ -67,7 +74,7 @@ def step_counts(history: int, block: int, scan: float, cand: float, top: float) 
 
 
 class BlockSelectDecodeStep:
-    """One layer's qbb / brep decode step with its block metadata, for bf16
+    """One layer's qbb / brep / qboracle decode step with its block metadata, for bf16
     K/V caches [B, Hkv, T, 128] of up to ``capacity`` tokens.  Call it once
     per decode token with the cache including the current token; a shorter
     history than the previous call's starts a new sequence."""
@@ -81,7 +88,7 @@ class BlockSelectDecodeStep:
         self.reps = max(1, min(reps, self.block))
         _require(head_dim == 128, "block selectors need head_dim 128")
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
-        _require(self.kind == QBB or self.block <= 64, "brep needs blocks of at most 64 tokens")
+        _require(self.kind != BREP or self.block <= 64, "brep needs blocks of at most 64 tokens")
         self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
         self.capacity = int(capacity)
         self.top_fraction = float(top_fraction)
@@ -91,9 +98,13 @@ class BlockSelectDecodeStep:
         self.rows = rows
         cap = self.capacity
         self.meta_blocks = math.ceil(cap / self.block)
-        nbytes = lib.qkv_block_meta_bytes(self.kind, batch, kv_heads, self.meta_blocks, self.reps)
-        _require(nbytes > 0, "bad block metadata size")
-        self.meta = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        if self.kind == QBORACLE:   # scores every block from the dim-major copy
+            _require(self.block <= 2048, "qboracle needs blocks of at most 2048 tokens")
+            self.meta = None
+        else:
+            nbytes = lib.qkv_block_meta_bytes(self.kind, batch, kv_heads, self.meta_blocks, self.reps)
+            _require(nbytes > 0, "bad block metadata size")
+            self.meta = torch.empty(nbytes, dtype=torch.uint8, device=device)
         self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
         nb, n_scan, n_cand, n_keep = step_counts(cap - 1, self.block, self.scan, self.cand, self.top_fraction)
         _require(n_scan * self.block <= 40960, f"{n_scan * self.block} scanned tokens per row; at most 40960")
@@ -118,6 +129,8 @@ class BlockSelectDecodeStep:
 
     def _sync_cache(self, key: torch.Tensor, history: int) -> None:
         lib = _lib.load()
+        if self.meta_len < history and self.meta is None:
+            self.meta_len = history
         if self.meta_len < history:
             with torch.cuda.device(key.device):
                 _lib.check(lib.qkv_block_meta_update(
@@ -164,11 +177,25 @@ class BlockSelectDecodeStep:
         nb, n_scan, n_cand, n_keep = step_counts(history, self.block, self.scan, self.cand, self.top_fraction)
         stream = _lib.stream_of(q)
         ks = _lib.strides(*key.stride())
+        if self.kind == QBORACLE:
+            # the reference ranks every history token for its candidates, the
+            # unscanned ones at finfo.min (EV:5055-5058); those only enter once
+            # the scanned tokens run out, which this step does not support
+            fewest = n_scan * self.block - (nb * self.block - history)
+            _require(math.ceil(self.cand * history) <= fewest,
+                     f"{self.mode}: {math.ceil(self.cand * history)} candidates from as few as {fewest} scanned "
+                     "tokens (more candidates than scanned tokens is not supported)")
         with torch.cuda.device(q.device):
-            _lib.check(lib.qkv_block_scores(
-                self.kind, q.data_ptr(), key.data_ptr(), ks, self.meta.data_ptr(), self.meta_blocks, self.batch,
-                self.q_heads, self.kv_heads, history, self.head_dim, self.block, self.reps, self.dims,
-                self.bscore.data_ptr(), self.meta_blocks, stream))
+            if self.kind == QBORACLE:
+                _lib.check(lib.qkv_block_max_partial_scores(
+                    q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), self.batch, self.q_heads,
+                    self.kv_heads, history, self.head_dim, self.block, self.dims, self.bscore.data_ptr(),
+                    self.meta_blocks, stream))
+            else:
+                _lib.check(lib.qkv_block_scores(
+                    self.kind, q.data_ptr(), key.data_ptr(), ks, self.meta.data_ptr(), self.meta_blocks, self.batch,
+                    self.q_heads, self.kv_heads, history, self.head_dim, self.block, self.reps, self.dims,
+                    self.bscore.data_ptr(), self.meta_blocks, stream))
             blocks = self.blocks[: self.rows * n_scan].view(self.rows, n_scan)
             block_topk(self.bscore[:, :nb], n_scan, out=blocks, workspace=self.topk_ws)
             n_tok = n_scan * self.block

@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
     int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
     uint32_t* __restrict__ tickets, uint16_t* __restrict__ out, const float* __restrict__ bmax,
-    int64_t bmax_ld, int32_t* __restrict__ sel_out, int kv_div) {
+    int64_t bmax_ld, int32_t* __restrict__ sel_out, int kv_div, int n_prot, int sink_end, int recent_start,
+    int rec_begin, int n_rec, int self_tok) {
   constexpr int CH = 4 * NI;               // token slots per wave chunk
   static_assert(CH <= 64, "one slot per lane when resolving token ids");
 
@@ -144,7 +145,8 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = lane >> 4, cc = lane & 15;
   const float ninf = -__builtin_huge_valf();
-  const int n_slots = n_sel * block;
+  const int n_blk_slots = n_sel * block;
+  const int n_slots = n_blk_slots + n_prot;
   const int32_t* ids = block_ids + static_cast<int64_t>(r) * n_sel;
   if constexpr (SEL) {
     select_row<SEL ? SELV : 1, false>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
@@ -156,19 +158,27 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   const int wg_base = split * (4 * CH * ITERS);
   auto slot_of = [&](int c) -> int { return wg_base + (4 * c + wave) * CH + lane; };
   // Block id of the lane's slot; lanes past CH and slots past the end get -1
-  // (the load itself always happens, from a clamped index).
+  // (the load itself always happens, from a clamped index).  Slot
+  // n_blk_slots + i (a protected token) gets -2 - i.
   auto load_id = [&](int c) -> int {
     const int slot = slot_of(c);
-    const bool ok = lane < CH && slot < n_slots;
+    const bool ok = lane < CH && slot < n_blk_slots;
     const int v = SEL ? sel_lds[ok ? slot / block : 0] : ids[ok ? slot / block : 0];
-    return ok ? v : -1;
+    return ok ? v : (lane < CH && slot < n_slots ? n_blk_slots - 2 - slot : -1);
   };
-  // Token of the lane's slot from its block id, or -1.
+  // Token of the lane's slot from its block id, or -1.  Protected slots are
+  // the sink range, the recent range and the current token, in that order;
+  // block slots inside the sink or recent range are masked, so no token is
+  // attended twice.
   auto token_of = [&](int c, int id) -> int {
+    if (id <= -2) {
+      const int i = -2 - id;
+      return i < sink_end ? i : i < sink_end + n_rec ? rec_begin + (i - sink_end) : self_tok;
+    }
     if (id < 0 || id >= nb) return -1;
     const int slot = slot_of(c);
     const int t = id * block + (slot - (slot / block) * block);
-    return t < tokens ? t : -1;
+    return (t < tokens && t >= sink_end && t < recent_start) ? t : -1;
   };
   // Token of slot 4i + grp (the lane's token in step i), from lane 4i + grp.
   auto spread = [&](int my_tok, int (&tk)[NI]) {
@@ -577,7 +587,8 @@ int launch_attention(const char* what, const void* query, const void* key, const
                      const int64_t* kv_strides, int64_t batch, int64_t q_heads, int64_t kv_heads,
                      int64_t tokens, int64_t head_dim, const int32_t* block_ids, const float* bmax,
                      int64_t bmax_ld, int32_t* sel_out, int64_t n_sel, int64_t block, float scaling,
-                     float* workspace, int64_t workspace_bytes, void* out, void* stream, int kv_div = 1) {
+                     float* workspace, int64_t workspace_bytes, void* out, void* stream, int kv_div = 1,
+                     int64_t protect_sink = 0, int64_t protect_recent = 0, bool keep_self = false) {
   const bool sel = bmax != nullptr;
   if (!query || !key || !value || !kv_strides || !(sel || block_ids) || !workspace || !out)
     return fail(QKV_ERR_INVALID, "%s: null pointer", what);
@@ -601,12 +612,23 @@ int launch_attention(const char* what, const void* query, const void* key, const
                   kSelMaxBlocks, nb);
     if (n_sel > nb || bmax_ld < nb) return fail(QKV_ERR_INVALID, "%s: need n_sel <= blocks <= bmax_ld", what);
   }
-  const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block);
+  // Protected tokens (EV:2938-2982): the sink range [0, sink_end), the
+  // recent range [rec_begin, tokens) and the current token `tokens` (the
+  // selection covers the history [0, tokens); K/V then hold tokens + 1 rows).
+  const int64_t sink_end = protect_sink > 0 ? std::min(protect_sink, tokens) : 0;
+  const int64_t recent_start = protect_recent > 0 ? std::max<int64_t>(0, tokens - protect_recent) : tokens;
+  const int64_t rec_begin = std::max(recent_start, sink_end);
+  const int64_t n_rec = protect_recent > 0 && rec_begin < tokens ? tokens - rec_begin : 0;
+  const int64_t n_prot = sink_end + n_rec + (keep_self ? 1 : 0);
+  if (n_sel * block + n_prot >= (int64_t(1) << 30)) return fail(QKV_ERR_INVALID, "%s: too many slots", what);
+  // the workspace of a selection of n_sel + ceil(n_prot / block) blocks covers the protected slots
+  const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim,
+                                                            n_sel + cdiv(n_prot, block), block);
   if (workspace_bytes < need)
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
   const int64_t rows = batch * kv_heads;
-  const int64_t n_slots = n_sel * block;
+  const int64_t n_slots = n_sel * block + n_prot;
   const int iters = iters_for(rows, n_slots, g);
   const int64_t nsplit = splits_for(rows, n_slots, g);
   if (nsplit > 65535) return fail(QKV_ERR_INVALID, "%s: too many selected blocks", what);
@@ -625,7 +647,9 @@ int launch_attention(const char* what, const void* query, const void* key, const
       q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                      \
       static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),             \
       static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o, bmax,   \
-      bmax_ld, sel_out, kv_div)
+      bmax_ld, sel_out, kv_div, static_cast<int>(n_prot), static_cast<int>(sink_end),                       \
+      static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec),                 \
+      static_cast<int>(tokens))
 #define QKV_ATTN(GG, IT)                  \
   if (!sel) QKV_ATTN_S(GG, IT, 0);        \
   else if (nb <= 2048) QKV_ATTN_S(GG, IT, 8); \
@@ -664,6 +688,22 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
   return launch_attention("qkv_sparse_attention", query, key, value, kv_strides, batch, q_heads, kv_heads,
                           tokens, head_dim, block_ids, nullptr, 0, nullptr, n_sel, block, scaling, workspace,
                           workspace_bytes, out, stream);
+}
+
+QKV_EXPORT int qkv_sparse_attention_protected(const void* query, const void* key, const void* value,
+                                              const int64_t* kv_strides, int64_t batch, int64_t q_heads,
+                                              int64_t kv_heads, int64_t history, int64_t head_dim,
+                                              const int32_t* block_ids, const float* bmax, int64_t bmax_ld,
+                                              int64_t n_sel, int64_t block, int64_t protect_sink,
+                                              int64_t protect_recent, int keep_self, float scaling, float* workspace,
+                                              int64_t workspace_bytes, int32_t* sel_out, void* out, void* stream) {
+  static const char* what = "qkv_sparse_attention_protected";
+  if (!block_ids == !bmax) return fail(QKV_ERR_INVALID, "%s: pass exactly one of block_ids and bmax", what);
+  if (protect_sink < 0 || protect_recent < 0)
+    return fail(QKV_ERR_INVALID, "%s: protected token counts must be >= 0", what);
+  return launch_attention(what, query, key, value, kv_strides, batch, q_heads, kv_heads, history, head_dim,
+                          block_ids, bmax, bmax_ld, bmax ? sel_out : nullptr, n_sel, block, scaling, workspace,
+                          workspace_bytes, out, stream, 1, protect_sink, protect_recent, keep_self != 0);
 }
 
 QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, const void* value,

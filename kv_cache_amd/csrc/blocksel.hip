@@ -1,6 +1,7 @@
-// Block-metadata selectors: the decode steps of the reference's qbb modes
-// (Quest-style per-block channel bounds, EV:5508-5617) and brep modes (block
-// representatives, EV:5361-5505, with their BlockRepState, EV:1853-1918), on
+// Block selectors: the decode steps of the reference's qbb modes
+// (Quest-style per-block channel bounds, EV:5508-5617), brep modes (block
+// representatives, EV:5361-5505, with their BlockRepState, EV:1853-1918) and
+// qboracle modes (block maxima of the partial scores, EV:5008-5097), on
 // GQA-shaped bf16 K/V (D = 128).
 //
 // Rows are (sequence, query head) r = b * Hq + h, reading K head h / (Hq/Hkv).
@@ -12,6 +13,8 @@
 //   block_scores_kernel  per (row, block): the bound sum_s q_s * (q_s >= 0 ?
 //       max : min) over the row's top-|q| dims, or the best representative's
 //       partial score;
+//   block_max_partial_kernel  (qboracle, no metadata) per (row, block): the
+//       largest partial score of the block's tokens, from the dim-major copy;
 //   (qkv_topk)           the best blocks;
 //   scan_partial_kernel  partial scores of the chosen blocks' tokens from the
 //       dim-major K copy (the blocks' tokens are contiguous there);
@@ -27,6 +30,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "ref_common.h"
 #include "select.h"
 
 namespace qkv {
@@ -220,6 +224,53 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// qboracle block scores (EV:5030-5044): per block, the maximum over its
+// history tokens of the partial score on the row's top-|q| dims, from the
+// dim-major copy (consecutive lanes read consecutive tokens of a dim).  A
+// workgroup owns whole blocks, at most kQboTokens tokens; the scores go
+// through LDS to the block maxima.
+// ---------------------------------------------------------------------------
+constexpr int kQboTokens = kBT * 8;
+
+__global__ __launch_bounds__(kBT) void block_max_partial_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ kdm, int q_heads, int group, int64_t db,
+    int64_t dh, int64_t dd, int history, int block, int nb, int blocks_per_wg, int count, float* __restrict__ out,
+    int64_t out_ld) {
+  __shared__ float q_s[kHD];
+  __shared__ int sel_idx[kHD];
+  __shared__ float sel_q[kHD];
+  __shared__ float sc[kQboTokens];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / q_heads, h = row - b * q_heads;
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  __syncthreads();
+  rank_dims(q_s, count, sel_idx, sel_q);
+  const int j0 = blockIdx.x * blocks_per_wg, j1 = min(nb, j0 + blocks_per_wg);
+  const int t0 = j0 * block, t1 = min(history, j1 * block);
+  const uint16_t* base = kdm + b * db + (h / group) * dh;
+  for (int i = tid; i < t1 - t0; i += kBT) {
+    const uint16_t* kt = base + t0 + i;
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in order
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = bf16f(kt[sel_idx[min(s0 + e, count - 1)] * dd]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (s0 + e < count) acc = acc + sel_q[s0 + e] * v[e];
+    }
+    sc[i] = acc;
+  }
+  __syncthreads();
+  for (int j = j0 + tid; j < j1; j += kBT) {
+    const int a = j * block - t0, e = min(t1, (j + 1) * block) - t0;
+    float m = -__builtin_huge_valf();
+    for (int i = a; i < e; ++i) m = fmaxf(m, sc[i]);
+    out[static_cast<int64_t>(row) * out_ld + j] = m;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Rerank of one row (EV:5583-5605): the n_cand best scanned tokens by partial
 // score (-inf positions never taken), their full-D scores * scaling, the
 // n_keep best of those, then the final mask over [0, key_count) (the kept
@@ -299,6 +350,87 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   for (int i = tid; i < extra; i += kRerankNT)
     ids[n_keep + i] = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
 }
+
+// ---------------------------------------------------------------------------
+// brep_partial_scores, the kernel the reference imports but never shipped
+// (wrapper EV:3847-3877, used at EV:5419-5431): the partial score of every
+// history token on the row's top-|q| dims (fp32 query, K in its own dtype,
+// products and sums in selection order), then -inf on every token outside
+// the scanned blocks -- the n_scan blocks whose best valid representative
+// scores highest (ties to the lower block), as the reference's fallback
+// ranks them (EV:5431-5443).
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kBT) void brep_token_scores_kernel(
+    const float* __restrict__ query, const typename Elem<DT>::T* __restrict__ key, float* __restrict__ out,
+    int heads, int tokens, int head_dim, int count, int64_t ksb, int64_t ksh, int64_t kst) {
+  __shared__ int sel_idx[kMaxDims];
+  __shared__ float sel_q[kMaxDims];
+  const int row = blockIdx.y;
+  const int b = row / heads, h = row - b * heads;
+  select_dims<QKV_DTYPE_FP32>(query + static_cast<int64_t>(row) * head_dim, head_dim, count, sel_idx, sel_q);
+  __syncthreads();
+  const int t = blockIdx.x * kBT + threadIdx.x;
+  if (t >= tokens) return;
+  const typename Elem<DT>::T* k_row = key + b * ksb + h * ksh + t * kst;
+  float acc = 0.0f;
+  for (int s = 0; s < count; ++s) acc = acc + sel_q[s] * Elem<DT>::load(k_row + sel_idx[s]);
+  out[static_cast<int64_t>(row) * tokens + t] = acc;
+}
+
+constexpr int kBrepMaxBlocks = kRerankNT * 40;
+
+// One 1024-thread workgroup per row: block scores from the token scores of
+// the representatives (finfo(float32).min without a valid one), the n_scan
+// best blocks into an LDS bitmap, then -inf on the tokens of every other
+// block.  Every read of the row's scores happens before the selection's
+// first barrier, every write after its last one.
+template <int VPL>
+__global__ __launch_bounds__(kRerankNT) void brep_scan_mask_kernel(float* __restrict__ scores, int tokens,
+                                                                   const int64_t* __restrict__ rep_idx,
+                                                                   const uint8_t* __restrict__ rep_valid,
+                                                                   int reps, int block, int nb, int n_scan) {
+  using WS = WideSelect<VPL, false>;
+  __shared__ typename WS::Shared lds;
+  __shared__ uint32_t scanned[kBrepMaxBlocks / 32];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  float* srow = scores + static_cast<int64_t>(row) * tokens;
+  const int64_t* irow = rep_idx + static_cast<int64_t>(row) * nb * reps;
+  const uint8_t* vrow = rep_valid + static_cast<int64_t>(row) * nb * reps;
+  for (int w = tid; w < (nb + 31) / 32; w += kRerankNT) scanned[w] = 0u;
+  WS ws;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int j = WS::pos(i);
+    float best = -3.40282347e38f;   // finfo(float32).min
+    if (j < nb) {
+      for (int r = 0; r < reps; ++r) {
+        const int64_t e = static_cast<int64_t>(j) * reps + r;
+        const int64_t tok = irow[e];
+        if (vrow[e] && tok >= 0 && tok < tokens) best = fmaxf(best, srow[tok]);
+      }
+    }
+    ws.set(i, best, j < nb);
+  }
+  ws.run(n_scan, lds);
+  ws.place(lds, [&](int pos, int, int) { atomicOr(&scanned[pos >> 5], 1u << (pos & 31)); });
+  __syncthreads();
+  for (int t = tid; t < tokens; t += kRerankNT) {
+    const int j = t / block;
+    if (!((scanned[j >> 5] >> (j & 31)) & 1u)) srow[t] = -__builtin_huge_valf();
+  }
+}
+
+template <int DT> struct RunBrepTokens {
+  static int run(const float* q, const void* k, float* out, int64_t B, int64_t H, int64_t T, int64_t D,
+                 const int64_t* ks, int count, hipStream_t st) {
+    dim3 grid(static_cast<unsigned>(cdiv(T, kBT)), static_cast<unsigned>(B * H));
+    brep_token_scores_kernel<DT><<<grid, kBT, 0, st>>>(q, static_cast<const typename Elem<DT>::T*>(k), out,
+                                                       static_cast<int>(H), static_cast<int>(T),
+                                                       static_cast<int>(D), count, ks[0], ks[1], ks[2]);
+    return check_launch("qkv_brep_partial_scores");
+  }
+};
 
 // Keys per thread for rows of n scanned tokens / n candidates: the fewest
 // that hold the row, so short rows run short loops.
@@ -423,6 +555,63 @@ QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_majo
       static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], blocks,
       static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld);
   return check_launch(what);
+}
+
+QKV_EXPORT int qkv_block_max_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                            int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                                            int64_t head_dim, int64_t block, int64_t dim_count, float* out,
+                                            int64_t out_ld, void* stream) {
+  const char* what = "qkv_block_max_partial_scores";
+  int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t nb = block > 0 ? cdiv(history, block) : 0;
+  if (history <= 0 || history >= (int64_t(1) << 31) || block <= 0 || out_ld < nb)
+    return fail(QKV_ERR_INVALID, "%s: need history, block > 0 and out_ld >= ceil(history/block)", what);
+  if (block > kQboTokens) return fail(QKV_ERR_UNSUPPORTED, "%s: block must be <= %d", what, kQboTokens);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the copy's token axis must be contiguous", what);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
+  const int64_t per_wg = std::max<int64_t>(1, kQboTokens / block);
+  dim3 grid(static_cast<unsigned>(cdiv(nb, per_wg)), static_cast<unsigned>(batch * q_heads));
+  block_max_partial_kernel<<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
+      static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], static_cast<int>(history),
+      static_cast<int>(block), static_cast<int>(nb), static_cast<int>(per_wg), count, out, out_ld);
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_brep_partial_scores(const float* query, const void* key_history, const int64_t* rep_indices,
+                                       const uint8_t* rep_valid, float* out, int key_dtype, int64_t batch,
+                                       int64_t heads, int64_t history, int64_t head_dim, const int64_t* k_strides,
+                                       int64_t reps, int64_t block_size, int64_t dim_count, double scan_fraction,
+                                       void* stream) {
+  const char* what = "qkv_brep_partial_scores";
+  if (!query || !key_history || !rep_indices || !rep_valid || !out || !k_strides)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (batch <= 0 || heads <= 0 || batch * heads > 65535)
+    return fail(QKV_ERR_INVALID, "%s: need batch, heads > 0 and batch * heads <= 65535", what);
+  if (head_dim <= 0 || head_dim > 1024) return fail(QKV_ERR_INVALID, "%s: need 0 < head_dim <= 1024", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || block_size <= 0 || reps <= 0)
+    return fail(QKV_ERR_INVALID, "%s: need history, block_size, reps > 0", what);
+  if (scan_fraction != scan_fraction) return fail(QKV_ERR_INVALID, "%s: scan_fraction is NaN", what);
+  const int64_t nb = cdiv(history, block_size);
+  if (nb > kBrepMaxBlocks)
+    return fail(QKV_ERR_UNSUPPORTED, "%s: at most %d blocks per row (got %lld)", what, kBrepMaxBlocks, (long long)nb);
+  if (k_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: K channels must be contiguous", what);
+  // min(blocks, max(1, ceil(scan_fraction * history / block_size))) in double, as EV:5442 computes it
+  const double want = std::ceil(scan_fraction * static_cast<double>(history) / static_cast<double>(block_size));
+  const int64_t n_scan = want >= static_cast<double>(nb) ? nb : want < 1.0 ? 1 : static_cast<int64_t>(want);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), std::min<int64_t>(head_dim, kMaxDims)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = dispatch_dtype<RunBrepTokens>(key_dtype, query, key_history, out, batch, heads, history, head_dim,
+                                         k_strides, count, st);
+  if (rc != QKV_OK) return rc;
+  return with_scan_vpl(nb, [&](auto vpl) {
+    brep_scan_mask_kernel<decltype(vpl)::value><<<static_cast<unsigned>(batch * heads), kRerankNT, 0, st>>>(
+        out, static_cast<int>(history), rep_indices, rep_valid, static_cast<int>(reps), static_cast<int>(block_size),
+        static_cast<int>(nb), static_cast<int>(n_scan));
+    return check_launch(what);
+  });
 }
 
 QKV_EXPORT int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t protect_sink, int64_t protect_recent,

@@ -22,9 +22,19 @@ Use:
     out = model(next_ids, past_key_values=cache, use_cache=True)        # decode: int4 sparse
 
 Prefill (more than one query per call) runs dense SDPA on the GPU, as the
-reference's prefill runs dense HF attention (EV:7079-7111).  Decode steps with
-one query per sequence run the int4 path; attention masks are not applied
-there (decode attends over the whole cache, no padding).
+reference's prefill runs dense HF attention (EV:7079-7111), with transformers'
+SDPA mask (``register`` registers it for the new name, so padding is applied).
+Decode steps with one query per sequence run the int4 path with the
+reference's decode semantics (EV:4419-4460, 2938-2982): the blocks are chosen
+over the history (every cached token but the current one), and the attention
+covers them plus the protected tokens -- ``protect_sink`` first tokens,
+``protect_recent`` last history tokens and, with ``keep_self`` (the
+reference's default), the current token.  The int4 kernels take no per-token
+mask, so a decode step on a padded batch (a mask that hides cached positions)
+raises instead of attending to the padding.  The channel subset is the one
+chosen when the int4 structures are built at the first decode step (the
+static per-KV-head subset of the int4 design); later tokens are quantized
+into it.
 """
 
 from __future__ import annotations
@@ -50,9 +60,12 @@ class Int4CacheLayer:
     is_compileable = False
     supports_early_init = False
 
-    def __init__(self, capacity: int, group: int, selected: int, block: int, topk: int):
+    def __init__(self, capacity: int, group: int, selected: int, block: int, topk: int, protect_sink: int = 0,
+                 protect_recent: int = 0, keep_self: bool = True):
         self.capacity = K.round_capacity(capacity)
         self.group, self.selected, self.block, self.topk = int(group), int(selected), int(block), int(topk)
+        self.protect = dict(protect_sink=max(0, int(protect_sink)), protect_recent=max(0, int(protect_recent)),
+                            keep_self=bool(keep_self))
         self.keys = self.values = None
         self.is_initialized = False
         self.length = 0
@@ -130,12 +143,14 @@ class Int4CacheLayer:
         view of its own size)."""
         if self.bufs is None:
             nb = math.ceil(self.capacity / self.block)
+            k = min(self.topk, nb)
             dev = self.device
+            n_ws = K.protected_workspace_blocks(k, self.block, self.capacity - 1, **self.protect)
             self.bufs = {
                 "bmax": torch.empty(batch * kv_heads * nb, dtype=torch.float32, device=dev),
-                "sel": torch.empty(batch * kv_heads * min(self.topk, nb), dtype=torch.int32, device=dev),
-                "topk_ws": K.topk_workspace(batch * kv_heads, nb, min(self.topk, nb), dev),
-                "attn_ws": K.attention_workspace(batch, q_heads, kv_heads, head_dim, min(self.topk, nb), self.block, dev),
+                "sel": torch.empty(batch * kv_heads * k, dtype=torch.int32, device=dev),
+                "topk_ws": K.topk_workspace(batch * kv_heads, nb, k, dev),
+                "attn_ws": K.attention_workspace(batch, q_heads, kv_heads, head_dim, n_ws, self.block, dev),
                 "out": torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=dev),
             }
         return self.bufs
@@ -145,11 +160,13 @@ class Int4SparseCache:
     """A transformers ``Cache`` whose layers keep K/V in preallocated buffers
     and append the int4 structures at every decode step."""
 
-    def __new__(cls, capacity: int, group: int = 32, selected: int = 32, block: int = 16, topk: int = 128):
+    def __new__(cls, capacity: int, group: int = 32, selected: int = 32, block: int = 16, topk: int = 128, *,
+                protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = True):
         from transformers.cache_utils import Cache, CacheLayerMixin
 
         layer_cls = _layer_class(CacheLayerMixin)
-        cache = Cache(layer_class_to_replicate=functools.partial(layer_cls, capacity, group, selected, block, topk))
+        cache = Cache(layer_class_to_replicate=functools.partial(
+            layer_cls, capacity, group, selected, block, topk, protect_sink, protect_recent, keep_self))
         return cache
 
 
@@ -163,7 +180,8 @@ def int4_sparse_attention_forward(module, query: torch.Tensor, key: torch.Tensor
                                   attention_mask, scaling: float | None = None, dropout: float = 0.0, **kwargs):
     """HF attention interface (query [B,Hq,q,D]; key/value [B,Hkv,T,D]) ->
     (out [B,q,Hq,D], None).  One query per sequence on an Int4SparseCache:
-    int4 scoring + top-k blocks + GQA sparse attention; otherwise dense SDPA."""
+    int4 scoring of the history + top-k blocks + GQA sparse attention over
+    them and the protected tokens; otherwise dense SDPA."""
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
     layer = _LAYERS.get(key.data_ptr())
@@ -171,32 +189,52 @@ def int4_sparse_attention_forward(module, query: torch.Tensor, key: torch.Tensor
         return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
                                       **kwargs)
     if layer.int4 is None:
+        # once per sequence, when the int4 structures are built: the cached
+        # positions' padding does not change later, and new tokens are real
+        if attention_mask is not None and not _all_visible(attention_mask, layer.length):
+            raise RuntimeError("int4 sparse decode does not support padded batches (the attention mask hides cached "
+                               "positions); decode such batches with dense attention")
         layer.build_int4()
     b, hq, _, d = query.shape
     hkv = key.size(1)
     t = layer.length
+    history = t - 1                       # the current token is not a candidate (EV:4414-4415)
+    if history < 1:
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
     scaling = d ** -0.5 if scaling is None else float(scaling)
     bufs = layer.decode_buffers(b, hq, hkv, d)
     c = layer.int4
-    nb = math.ceil(t / layer.block)
+    nb = math.ceil(history / layer.block)
     k = min(layer.topk, nb)
     q = query[:, :, 0, :].contiguous()
     bmax = bufs["bmax"][: b * hkv * nb].view(b, hkv, nb)
-    K.decode_scores(q, c.chan_idx, c.slab, c.slab_scales, t, layer.block, bmax=bmax)
+    K.decode_scores(q, c.chan_idx, c.slab, c.slab_scales, history, layer.block, bmax=bmax)
     sel = bufs["sel"][: b * hkv * k].view(b, hkv, k)
     if nb <= K.SELECT_MAX_BLOCKS:
-        out = K.sparse_attention_select(q, layer.keys, layer.values, bmax, k, layer.block, t, scaling,
-                                        workspace=bufs["attn_ws"], sel_out=sel, out=bufs["out"])
+        out = K.sparse_attention_select(q, layer.keys, layer.values, bmax, k, layer.block, history, scaling,
+                                        workspace=bufs["attn_ws"], sel_out=sel, out=bufs["out"], **layer.protect)
     else:
         K.block_topk(bmax, k, out=sel, workspace=bufs["topk_ws"])
-        out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, t, scaling,
-                                 workspace=bufs["attn_ws"], out=bufs["out"])
+        out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, history, scaling,
+                                 workspace=bufs["attn_ws"], out=bufs["out"], **layer.protect)
     return out[:, None].to(query.dtype), None
+
+
+def _all_visible(mask: torch.Tensor, length: int) -> bool:
+    """True when a decode step's attention mask ([B, 1, q, T], bool or
+    additive float) hides none of the first ``length`` positions."""
+    m = mask[..., -1, :length]
+    return bool(m.all()) if m.dtype == torch.bool else bool((m == 0).all())
 
 
 def register(name: str = "int4_sparse") -> str:
     """Register the attention function with transformers under ``name``."""
     from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 
     AttentionInterface.register(name, int4_sparse_attention_forward)
+    # without a mask function of its own a custom implementation gets no mask
+    # at all, padding included; SDPA's mask is the one its prefill path uses
+    AttentionMaskInterface.register(name, sdpa_mask)
     return name

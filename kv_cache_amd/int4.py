@@ -224,11 +224,38 @@ def attention_workspace(batch: int, q_heads: int, kv_heads: int, head_dim: int, 
     return torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
 
 
+def protected_count(history: int, protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = False) -> int:
+    """Tokens the reference adds to every selection (EV:2938-2982): the sink
+    range, the recent range (not overlapping the sink) and the current token."""
+    if not (protect_sink > 0 or protect_recent > 0 or keep_self):
+        return 0
+    n = _lib.load().qkv_final_list_count(int(history), 0, int(protect_sink), int(protect_recent), int(bool(keep_self)))
+    _require(n >= 0, f"bad history {history}")
+    return int(n)
+
+
+def protected_workspace_blocks(n_sel: int, block: int, history: int, protect_sink: int = 0,
+                               protect_recent: int = 0, keep_self: bool = False) -> int:
+    """Selection size whose attention workspace also covers the protected slots."""
+    return int(n_sel) + -(-protected_count(history, protect_sink, protect_recent, keep_self) // int(block))
+
+
+def _protected(protect_sink: int, protect_recent: int, keep_self: bool) -> bool:
+    return protect_sink > 0 or protect_recent > 0 or bool(keep_self)
+
+
 def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                      block_ids: torch.Tensor, block: int, tokens: int, scaling: float, *,
-                     workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                     workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                     protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = False) -> torch.Tensor:
     """GQA-native attention of query bf16 [B,Hq,D] over the selected blocks
-    (int32 [B,Hkv,n]) of K/V bf16 [B,Hkv,*,D]; returns bf16 [B,Hq,D]."""
+    (int32 [B,Hkv,n]) of K/V bf16 [B,Hkv,*,D]; returns bf16 [B,Hq,D].
+
+    With protection (the reference's --protect_sink_tokens,
+    --protect_recent_tokens, --always_keep_self; EV:2938-2982) ``tokens`` is
+    the history the blocks were chosen from, and the attention also covers
+    the sink range, the recent range and the current token ``tokens`` (each
+    token once; K/V then hold tokens + 1 rows)."""
     lib = _lib.load()
     _check_kv("key", key)
     _check_kv("value", value)
@@ -238,17 +265,26 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     hkv = key.size(1)
     _require(block_ids.dtype == torch.int32 and block_ids.is_contiguous(), "block_ids must be contiguous int32")
     n = block_ids.size(-1)
-    need = attention_workspace_bytes(b, hq, hkv, d, n, block)
+    prot = _protected(protect_sink, protect_recent, keep_self)
+    _require(not keep_self or key.size(2) > int(tokens), "keep_self needs the current token's K/V row")
+    n_ws = protected_workspace_blocks(n, block, tokens, protect_sink, protect_recent, keep_self) if prot else n
     if workspace is None:
-        workspace = attention_workspace(b, hq, hkv, d, n, block, q.device)
+        workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
     if out is None:
         out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
     with torch.cuda.device(q.device):
-        _lib.check(lib.qkv_sparse_attention(q.data_ptr(), key.data_ptr(), value.data_ptr(),
-                                            _lib.strides(*key.stride()[:3]), b, hq, hkv, int(tokens), d,
-                                            block_ids.data_ptr(), n, int(block), float(scaling),
-                                            workspace.data_ptr(), workspace.numel() * 4, out.data_ptr(),
-                                            _lib.stream_of(q)))
+        if prot:
+            _lib.check(lib.qkv_sparse_attention_protected(
+                q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
+                int(tokens), d, block_ids.data_ptr(), None, 0, n, int(block), int(protect_sink), int(protect_recent),
+                int(bool(keep_self)), float(scaling), workspace.data_ptr(), workspace.numel() * 4, None,
+                out.data_ptr(), _lib.stream_of(q)))
+        else:
+            _lib.check(lib.qkv_sparse_attention(q.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                                _lib.strides(*key.stride()[:3]), b, hq, hkv, int(tokens), d,
+                                                block_ids.data_ptr(), n, int(block), float(scaling),
+                                                workspace.data_ptr(), workspace.numel() * 4, out.data_ptr(),
+                                                _lib.stream_of(q)))
     return out
 
 
@@ -259,11 +295,13 @@ SELECT_MAX_BLOCKS = 4096
 def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                             bmax: torch.Tensor, n_sel: int, block: int, tokens: int, scaling: float, *,
                             workspace: torch.Tensor | None = None, sel_out: torch.Tensor | None = None,
-                            out: torch.Tensor | None = None) -> torch.Tensor:
+                            out: torch.Tensor | None = None, protect_sink: int = 0, protect_recent: int = 0,
+                            keep_self: bool = False) -> torch.Tensor:
     """``sparse_attention`` over the n_sel blocks with the largest block
     maxima (f32 [B,Hkv,>=ceil(tokens/block)], the selection of ``block_topk``),
     selected inside the attention kernel.  sel_out (int32 [B,Hkv,n_sel]), when
-    given, receives the selection.  Returns bf16 [B,Hq,D]."""
+    given, receives the selection.  Protection as for ``sparse_attention``.
+    Returns bf16 [B,Hq,D]."""
     lib = _lib.load()
     _check_kv("key", key)
     _check_kv("value", value)
@@ -279,15 +317,25 @@ def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch
     if sel_out is not None:
         _require(sel_out.dtype == torch.int32 and sel_out.is_contiguous() and sel_out.numel() == b * hkv * n_sel,
                  "sel_out must be contiguous int32 [B, Hkv, n_sel]")
+    prot = _protected(protect_sink, protect_recent, keep_self)
+    _require(not keep_self or key.size(2) > int(tokens), "keep_self needs the current token's K/V row")
+    n_ws = protected_workspace_blocks(n_sel, block, tokens, protect_sink, protect_recent, keep_self) if prot else n_sel
     if workspace is None:
-        workspace = attention_workspace(b, hq, hkv, d, n_sel, block, q.device)
+        workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
     if out is None:
         out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
     with torch.cuda.device(q.device):
-        _lib.check(lib.qkv_sparse_attention_select(
-            q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
-            int(tokens), d, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), float(scaling),
-            workspace.data_ptr(), workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
+        if prot:
+            _lib.check(lib.qkv_sparse_attention_protected(
+                q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
+                int(tokens), d, None, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), int(protect_sink),
+                int(protect_recent), int(bool(keep_self)), float(scaling), workspace.data_ptr(),
+                workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
+        else:
+            _lib.check(lib.qkv_sparse_attention_select(
+                q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
+                int(tokens), d, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), float(scaling),
+                workspace.data_ptr(), workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
     return out
 
 
@@ -327,33 +375,61 @@ class Int4KCache:
 
 class SparseDecodeStep:
     """One layer's decode step with every buffer allocated up front:
-    scoring + block max -> top-k blocks -> GQA sparse attention."""
+    scoring + block max -> top-k blocks -> GQA sparse attention.
+
+    ``tokens`` is the cache length the step runs at.  With protection (the
+    reference's --protect_sink_tokens, --protect_recent_tokens,
+    --always_keep_self) or ``history_only``, the step follows the
+    reference's decode semantics (EV:4419-4460): the blocks are chosen over
+    the history ``tokens - 1`` (the current token is not a candidate), and the
+    attention covers them plus the sink range, the recent range and, with
+    keep_self, the current token, each token once (EV:2938-2982)."""
 
     def __init__(self, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
-                 block: int, topk: int, device: torch.device | str = "cuda"):
+                 block: int, topk: int, device: torch.device | str = "cuda", *, protect_sink: int = 0,
+                 protect_recent: int = 0, keep_self: bool = False, history_only: bool | None = None):
         self.batch, self.q_heads, self.kv_heads = batch, q_heads, kv_heads
         self.head_dim, self.tokens, self.block, self.topk = head_dim, tokens, block, topk
-        nb = math.ceil(tokens / block)
+        self.protect_sink, self.protect_recent = max(0, int(protect_sink)), max(0, int(protect_recent))
+        self.keep_self = bool(keep_self)
+        prot = _protected(self.protect_sink, self.protect_recent, self.keep_self)
+        self.history_only = prot if history_only is None else bool(history_only)
+        _require(self.history_only or not prot, "protected tokens need history_only (the current token is not scored)")
+        self.scored = tokens - 1 if self.history_only else tokens   # keys the selection ranks
+        _require(self.scored >= 1, f"no keys to select from at {tokens} tokens")
+        nb = math.ceil(self.scored / block)
         _require(1 <= topk <= nb, f"topk {topk} must be in [1, {nb}]")
         self.bmax = torch.empty((batch, kv_heads, nb), dtype=torch.float32, device=device)
         self.sel = torch.empty((batch, kv_heads, topk), dtype=torch.int32, device=device)
         self.topk_ws = topk_workspace(batch * kv_heads, nb, topk, device)
-        self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, topk, block, device)
+        n_ws = protected_workspace_blocks(topk, block, self.scored, self.protect_sink, self.protect_recent,
+                                          self.keep_self)
+        self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, n_ws, block, device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
         self.fused = nb <= SELECT_MAX_BLOCKS
 
     @classmethod
     def for_mode(cls, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
-                 device: torch.device | str = "cuda") -> "SparseDecodeStep":
-        """The step for a reference mode string (``qabs{S}cand{pct}attn`` or
-        ``qboracle{bs}q{S}s{scan}cand{pct}``) at ``tokens`` keys; the cache it
-        runs on must have ``plan.selected`` channels (``modes.decode_plan``)."""
+                 device: torch.device | str = "cuda", *, protect_sink: int = 0, protect_recent: int = 0,
+                 keep_self: bool = True) -> "SparseDecodeStep":
+        """The int4 step for a reference mode string at a cache of ``tokens``
+        keys (the current token included): ``qabs{S}cand{pct}attn`` keeps
+        ``ceil(pct * history)`` tokens (one-token blocks), ``qboracle{bs}q{S}
+        s{scan}cand{pct}`` the ``ceil(scan * history / bs)`` best blocks; both
+        add the protected tokens (the reference's defaults: no sink or recent
+        tokens, keep the current token) and select over the history only.
+        What stays the int4 path's own is the scoring: one GQA-summed int8
+        query per KV head over a static channel subset, instead of the
+        reference's per-head top-|q| channels in fp32, so the G heads of a KV
+        head share their selection.  The cache must have ``plan.selected``
+        channels (``modes.decode_plan``)."""
         from .modes import decode_plan
 
         plan = decode_plan(mode, tokens, head_dim)
         _require(plan is not None, f"mode {mode!r} is not a decode mode of this path (or no history yet)")
         step = cls(batch, q_heads, kv_heads, head_dim, tokens, plan.block,
-                   min(plan.topk, math.ceil(tokens / plan.block)), device)
+                   min(plan.topk, math.ceil(plan.history / plan.block)), device, protect_sink=protect_sink,
+                   protect_recent=protect_recent, keep_self=keep_self, history_only=True)
         step.plan = plan
         return step
 
@@ -362,11 +438,13 @@ class SparseDecodeStep:
         """Rows of at most SELECT_MAX_BLOCKS blocks select inside the attention
         kernel (two launches); longer rows run the top-k launch between.  The
         selection lands in ``self.sel`` either way."""
-        decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.tokens, self.block,
+        _require(key.size(2) >= self.tokens, f"K/V hold {key.size(2)} tokens, the step needs {self.tokens}")
+        prot = dict(protect_sink=self.protect_sink, protect_recent=self.protect_recent, keep_self=self.keep_self)
+        decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.block,
                       bmax=self.bmax)
         if self.fused:
-            return sparse_attention_select(query, key, value, self.bmax, self.topk, self.block, self.tokens,
-                                           scaling, workspace=self.workspace, sel_out=self.sel, out=self.out)
+            return sparse_attention_select(query, key, value, self.bmax, self.topk, self.block, self.scored,
+                                           scaling, workspace=self.workspace, sel_out=self.sel, out=self.out, **prot)
         block_topk(self.bmax, self.topk, out=self.sel, workspace=self.topk_ws)
-        return sparse_attention(query, key, value, self.sel, self.block, self.tokens, scaling,
-                                workspace=self.workspace, out=self.out)
+        return sparse_attention(query, key, value, self.sel, self.block, self.scored, scaling,
+                                workspace=self.workspace, out=self.out, **prot)

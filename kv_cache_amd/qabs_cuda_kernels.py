@@ -2,7 +2,10 @@
 
 Same four functions, argument meaning, output shapes and error behaviour as
 ymluo/projects/qwen3_top2_head_limit3_ppl/src/qabs_cuda_kernels.py:654-705,
-backed by libqkv's gfx950 kernels instead of a JIT-built CUDA extension.
+backed by libqkv's gfx950 kernels instead of a JIT-built CUDA extension,
+plus the two the reference's harness imports from that module but which it
+never shipped: ``reuse_select`` (EV:3881-3919) and ``brep_partial_scores``
+(EV:3847-3877).
 Shape/dtype violations raise ``RuntimeError`` with the reference's
 ``TORCH_CHECK`` messages; inputs are made contiguous exactly where the
 reference does so; outputs are allocated here (fp32 scores, query-dtype
@@ -164,6 +167,52 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
             q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(),
             _dtype_code(q), b, h, t, n, d, float(scaling), _lib.stream_of(q)))
     return out[:, None, :, :].contiguous()
+
+
+def brep_partial_scores(query: torch.Tensor, key_history: torch.Tensor, rep_indices: torch.Tensor,
+                        rep_valid: torch.Tensor, block_size: int, dim_count: int, scan_fraction: float) -> torch.Tensor:
+    """The block-representative scan the reference imports from this module
+    but never shipped (wrapper EV:3847-3877, called at EV:5419-5431 with the
+    fp32 query, the history keys and BlockRepState's representatives).
+
+    query [B,H,D] (any float dtype; scored as fp32); key_history [B,H,T,D];
+    rep_indices int64 / rep_valid bool [B,H,ceil(T/block_size),R].  Returns
+    fp32 [B,H,T]: the partial score on the ``dim_count`` largest-|q| dims of
+    every token of the ``min(blocks, max(1, ceil(scan_fraction*T/block_size)))``
+    blocks whose best valid representative scores highest, -inf elsewhere --
+    so the caller's ``topk`` + ``isfinite`` (EV:5426-5428) picks candidates
+    from the scanned blocks only, as its fallback does (EV:5442-5470)."""
+    lib = _lib.load()
+    _check(query.is_cuda, "query must be CUDA")
+    _check(key_history.is_cuda, "key must be CUDA")
+    _check(rep_indices.is_cuda and rep_valid.is_cuda, "representatives must be CUDA")
+    _check(query.dim() == 3, "query must have shape [batch, heads, dim]")
+    _check(key_history.dim() == 4, "key must have shape [batch, heads, key, dim]")
+    _check(query.is_floating_point(), "query must be floating point")
+    _check(query.size(0) == key_history.size(0) and query.size(1) == key_history.size(1)
+           and query.size(2) == key_history.size(3), "query/key shape mismatch")
+    _check(int(block_size) > 0, "block_size must be positive")
+    b, h, d = query.shape
+    t = key_history.size(2)
+    nb = -(-t // int(block_size))
+    _check(rep_indices.dim() == 4 and tuple(rep_indices.shape[:3]) == (b, h, nb),
+           "rep_indices must have shape [batch, heads, blocks, reps]")
+    _check(rep_indices.dtype == torch.int64, "rep_indices must be int64")
+    _check(rep_valid.dtype == torch.bool and rep_valid.shape == rep_indices.shape,
+           "rep_valid must be bool with the shape of rep_indices")
+    out = torch.empty((b, h, t), dtype=torch.float32, device=query.device)
+    if t == 0:
+        return out
+    q = query.float().contiguous()
+    k = key_history.contiguous()
+    idx = rep_indices.contiguous()
+    val = rep_valid.contiguous().view(torch.uint8)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_brep_partial_scores(
+            q.data_ptr(), k.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(), _dtype_code(k), b, h, t, d,
+            _lib.strides(*k.stride()), idx.size(3), int(block_size), int(dim_count), float(scan_fraction),
+            _lib.stream_of(q)))
+    return out
 
 
 def reuse_select(query: torch.Tensor, key_states: torch.Tensor, current_candidate: torch.Tensor,

@@ -342,13 +342,40 @@ def sparse_attention(q, k, v, block_ids, block: int, tokens: int, scaling: float
     skipped); only tokens < ``tokens`` exist.  A row with no valid token
     outputs zeros (QK:388, 404).  Returns float64 [B, Hq, D].
     """
+    return _attend(q, k, v, expand_blocks(block_ids, block, tokens), scaling)
+
+
+def protected_tokens(history: int, sink: int, recent: int, keep_self: bool) -> np.ndarray:
+    """The tokens every reference selection adds (EV:2938-2982): the sink
+    range [0, min(sink, history)), the recent range [max(0, history - recent),
+    history) without the sink's tokens, and the current token ``history``."""
+    sink_end = min(sink, history) if sink > 0 else 0
+    recent_start = max(0, history - recent) if recent > 0 else history
+    parts = [np.arange(sink_end), np.arange(max(recent_start, sink_end), history)]
+    if keep_self:
+        parts.append(np.array([history]))
+    return np.concatenate(parts).astype(np.int64)
+
+
+def sparse_attention_protected(q, k, v, block_ids, block: int, history: int, scaling: float, sink: int = 0,
+                               recent: int = 0, keep_self: bool = False) -> np.ndarray:
+    """``sparse_attention`` over the selected blocks of the history [0,
+    history) together with the protected tokens, every token once (the
+    reference masks selected tokens that fall in the protected ranges,
+    EV:2946-2953).  Returns float64 [B, Hq, D]."""
+    prot = protected_tokens(history, sink, recent, keep_self)
+    toks = [np.union1d(t, prot) for t in expand_blocks(block_ids, block, history)]
+    return _attend(q, k, v, toks, scaling)
+
+
+def _attend(q, k, v, toks, scaling: float) -> np.ndarray:
+    """fp64 softmax attention of each row's G query heads over its token list."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
     b, hq, d = q.shape
     hkv = k.shape[1]
     g = hq // hkv
-    toks = expand_blocks(block_ids, block, tokens)
     out = np.zeros((b, hq, d), dtype=np.float64)
     for bi in range(b):
         for j in range(hkv):

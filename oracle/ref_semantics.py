@@ -216,6 +216,44 @@ def qabs_candidate_attention_cpu(query_states, key_states, value_states, dim_cou
     return out[:, None, :, :].contiguous()
 
 
+def qabs_attn_step(query, key, value, dim_count: int, candidate_fraction: float, scaling: float,
+                   sink: int = 0, recent: int = 0, keep_self: bool = True):
+    """One ``qabs{S}cand{pct}attn`` decode step (EV:4400-4502) in numpy with
+    the kernels' arithmetic: per query head, the fp32 partial score of every
+    history token on its top-|q| dims (selection order, QK:63-96), the
+    ``min(history, max(1, ceil(pct * history)))`` best (ties to the lower
+    index), plus the sink / recent ranges and the current token
+    (EV:2938-2982), then softmax attention over that set (QK:335-419).
+
+    query [B,Hq,D]; key/value [B,Hkv,T,D] (head h reads KV head h // G).
+    Returns (out float64 [B,1,Hq,D], final_keep bool [B,Hq,T])."""
+    from .qkv_oracle import topk_lowest_index
+
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, hq, d = q.shape
+    g = hq // k.shape[1]
+    kx, vx = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    key_count = k.shape[2]
+    if key_count <= 1:
+        return vx[:, :, -1:, :].transpose(0, 2, 1, 3).astype(np.float64), np.ones((b, hq, key_count), bool)
+    history = key_count - 1
+    requested = min(history, max(1, math.ceil(candidate_fraction * history)))
+    part = partial_scores(q, kx[:, :, :history], dim_count)
+    sel = topk_lowest_index(part.reshape(-1, history), requested).reshape(b, hq, requested)
+    final_keep = np.zeros((b, hq, key_count), dtype=bool)
+    np.put_along_axis(final_keep, sel.astype(np.int64), True, axis=-1)
+    if sink > 0:
+        final_keep[..., : min(sink, history)] = True
+    if recent > 0:
+        final_keep[..., max(0, history - recent):history] = True
+    if keep_self:
+        final_keep[..., history] = True
+    idx = np.broadcast_to(np.arange(key_count), final_keep.shape)
+    return final_attention(q, kx, vx, idx, final_keep, scaling), final_keep
+
+
 # ---------------------------------------------------------------------------
 # Candidate reuse and exact rerank (qabs{S}cand{pct}reuse[final|2set])
 # ---------------------------------------------------------------------------
@@ -614,11 +652,65 @@ def brep_block_scores(query, key, rep_idx, rep_valid, dim_count: int) -> np.ndar
     return out
 
 
+def brep_partial_scores(query, key, rep_idx, rep_valid, block: int, dim_count: int, scan_fraction: float):
+    """The absent ``brep_partial_scores`` kernel (wrapper EV:3847-3877, call
+    EV:5419-5431): the partial scores of the tokens of the
+    ``min(blocks, max(1, ceil(scan * T / block)))`` blocks with the best
+    representative score (``brep_block_scores``, ties to the lower block),
+    -inf elsewhere, so the caller's ``topk`` + ``isfinite`` (EV:5426-5428)
+    draws candidates from the scanned blocks as its fallback does
+    (EV:5442-5470).  query [B,H,D]; key [B,H,T,D]; rep_* [B,H,nb,R] ->
+    f32 [B,H,T]."""
+    from .qkv_oracle import topk_lowest_index
+
+    k = np.asarray(key, dtype=np.float32)
+    b, h, t, _ = k.shape
+    nb = -(-t // block)
+    bscore = brep_block_scores(query, k, rep_idx, rep_valid, dim_count)
+    n_scan = min(nb, max(1, math.ceil(scan_fraction * t / block)))
+    blocks = topk_lowest_index(bscore.reshape(-1, nb), n_scan).reshape(b, h, n_scan)
+    keep = np.zeros((b, h, nb), dtype=bool)
+    np.put_along_axis(keep, blocks.astype(np.int64), True, axis=-1)
+    tok_keep = np.repeat(keep, block, axis=-1)[..., :t]
+    return np.where(tok_keep, partial_scores(query, k, dim_count), np.float32(-np.inf)).astype(np.float32)
+
+
+def brep_caller_final_mask(partial, query, key_history, key_count: int, candidate_fraction: float,
+                           top_fraction: float, scaling: float, sink: int, recent: int, keep_self: bool):
+    """What the reference's brep step does with ``brep_partial_scores``'
+    output on one (b, h) row (EV:5426-5428, 5470-5491), ties to the lower
+    index: the ``ceil(cand * history)`` best finite partial scores, their
+    full-D scores * scaling, the ``ceil(top * history)`` best of those, then
+    the final mask with the sink / recent ranges and the current token.
+    partial [history]; query [D]; key_history [history, D] -> bool [key_count]."""
+    from .qkv_oracle import topk_lowest_index
+
+    partial = np.asarray(partial, dtype=np.float32)
+    history = key_count - 1
+    requested = min(history, max(1, math.ceil(candidate_fraction * history)))
+    order = topk_lowest_index(partial[None], requested)[0]
+    cidx = order[np.isfinite(partial[order])]
+    final = np.zeros(key_count, dtype=bool)
+    if cidx.size:
+        q = np.asarray(query, dtype=np.float32)
+        full = (_seq_dot(q, np.asarray(key_history, dtype=np.float32)[cidx]) * np.float32(scaling)).astype(np.float32)
+        keep_count = min(cidx.size, requested, max(1, math.ceil(top_fraction * history)))
+        final[cidx[topk_lowest_index(full[None], keep_count)[0]]] = True
+    if sink > 0:
+        final[: min(sink, history)] = True
+    if recent > 0:
+        final[max(0, history - recent):history] = True
+    if keep_self:
+        final[history] = True
+    return final
+
+
 def block_select_step(query, key, value, kind: str, block: int, dim_count: int, scan_fraction: float,
                       candidate_fraction: float, top_fraction: float, scaling: float, sink: int = 0,
                       recent: int = 0, keep_self: bool = True, reps: int = 1):
-    """One decode step of the qbb (EV:5508-5617) or brep (EV:5361-5505)
-    selector: block scores -> the ``ceil(scan * history / block)`` best blocks
+    """One decode step of the qbb (EV:5508-5617), brep (EV:5361-5505) or
+    qboracle (block max of the partial scores, EV:5008-5097) selector:
+    block scores -> the ``ceil(scan * history / block)`` best blocks
     -> partial scores of their tokens on the top-|q| dims -> the
     ``ceil(cand * history)`` best tokens -> full-D fp32 scores * scaling ->
     the ``ceil(top * history)`` best -> final mask with the sink / recent
@@ -642,12 +734,18 @@ def block_select_step(query, key, value, kind: str, block: int, dim_count: int, 
     history = key_count - 1
     kh = kx[:, :, :history]
     nb = -(-history // block)
+    part_all = None
     if kind == "qbb":
         kmin, kmax = block_minmax(kh, block)
         bscore = qbb_block_bounds(q, kmin, kmax, dim_count)
     elif kind == "brep":
         ridx, rvalid = block_representatives(kh, block, reps)
         bscore = brep_block_scores(q, kh, ridx, rvalid, dim_count)
+    elif kind == "qboracle":
+        from .qkv_oracle import block_max
+
+        part_all = partial_scores(q, kh, dim_count)
+        bscore = block_max(part_all, block)
     else:
         raise ValueError(kind)
     n_scan = min(nb, max(1, math.ceil(scan_fraction * history / block)))
@@ -655,10 +753,22 @@ def block_select_step(query, key, value, kind: str, block: int, dim_count: int, 
     final_keep = np.zeros((b, hq, key_count), dtype=bool)
     n_req = max(1, math.ceil(candidate_fraction * history))
     n_keep = max(1, math.ceil(top_fraction * history))
+    lowest = np.float32(np.finfo(np.float32).min)
     for bi in range(b):
         for hi in range(hq):
             toks = np.concatenate([np.arange(j * block, min(history, (j + 1) * block)) for j in blocks[bi, hi]])
             toks.sort()
+            if part_all is not None:
+                # qboracle ranks every history token, the unscanned ones at
+                # finfo(float32).min -- finite, so still valid candidates once
+                # the scanned ones run out (EV:5055-5058)
+                scores = np.full(history, lowest, dtype=np.float32)
+                scores[toks] = part_all[bi, hi, toks]
+                cand = np.sort(topk_lowest_index(scores[None], min(history, n_req))[0])
+                full = (_seq_dot(q[bi, hi], kh[bi, hi][cand]) * np.float32(scaling)).astype(np.float32)
+                keep = cand[topk_lowest_index(full[None], min(cand.size, n_keep))[0]]
+                final_keep[bi, hi, keep] = True
+                continue
             dims = select_dims_by_abs(q[bi, hi], dim_count)
             part = _seq_dot(q[bi, hi, dims], kh[bi, hi][toks][:, dims])
             cand = toks[np.sort(topk_lowest_index(part[None], min(toks.size, n_req))[0])]
@@ -679,9 +789,9 @@ def block_select_step(query, key, value, kind: str, block: int, dim_count: int, 
 def block_select_step_cpu(query_states, key_states, value_states, kind: str, block: int, dim_count: int,
                           scan_fraction: float, candidate_fraction: float, top_fraction: float, scaling: float,
                           sink: int = 0, recent: int = 0, keep_self: bool = True, reps: int = 1):
-    """One qbb (EV:5516-5617) or brep (EV:5369-5505, representatives as
-    BlockRepState computes them, EV:1899-1913) decode step in the
-    reference's PyTorch ops on CPU tensors: the CPU baseline ``bench.py``
+    """One qbb (EV:5516-5617), brep (EV:5369-5505, representatives as
+    BlockRepState computes them, EV:1899-1913) or qboracle (EV:5008-5097)
+    decode step in the reference's PyTorch ops on CPU tensors: the CPU baseline ``bench.py``
     times next to the GPU block selectors.  query_states [B,Hq,1,D];
     key/value_states [B,Hkv,T,D] (GQA-expanded first, EV:6248-6251).
     Returns (out [B,1,Hq,D], final_keep bool [B,Hq,T])."""
@@ -707,7 +817,13 @@ def block_select_step_cpu(query_states, key_states, value_states, kind: str, blo
     valid_b[:, :, :history] = True
     block_k = k_blocks.view(b, hq, nb, block, d)
     block_valid = valid_b.view(b, hq, nb, block)
-    if kind == "qbb":
+    if kind == "qboracle":
+        # partial scores of every history token, -inf padding, block max (EV:5030-5044)
+        kall = torch.gather(k_hist.float(), dim=-1, index=qdims[:, :, None, :].expand(-1, -1, history, -1))
+        part_all = (kall * q_sel[:, :, None, :]).sum(dim=-1)
+        pscores = F.pad(part_all, (0, padded - history), value=-torch.inf) if padded != history else part_all
+        bscore = pscores.view(b, hq, nb, block).amax(dim=-1)
+    elif kind == "qbb":
         gidx = qdims[:, :, None, None, :].expand(-1, -1, nb, block, -1)
         sel = torch.gather(block_k, dim=-1, index=gidx)
         smax = sel.masked_fill(~block_valid[..., None], -torch.inf).amax(dim=3)
@@ -725,16 +841,26 @@ def block_select_step_cpu(query_states, key_states, value_states, kind: str, blo
         bscore = rsc.amax(dim=-1)
     n_scan = min(nb, max(1, math.ceil(scan_fraction * history / block)))
     _, blocks = torch.topk(bscore, k=n_scan, dim=-1, largest=True)
-    tok = (blocks[..., None] * block + torch.arange(block)).reshape(b, hq, -1)
-    tvalid = tok < history
-    tok = tok.clamp_max(history - 1)
-    skeys = torch.gather(k_hist, dim=2, index=tok[..., None].expand(-1, -1, -1, d))
-    ssel = torch.gather(skeys.float(), dim=-1, index=qdims[:, :, None, :].expand(-1, -1, tok.shape[-1], -1))
-    part = (ssel * q_sel[:, :, None, :]).sum(dim=-1).masked_fill(~tvalid, torch.finfo(torch.float32).min)
-    req = min(tok.shape[-1], max(1, math.ceil(candidate_fraction * history)))
-    _, cpos = torch.topk(part, k=req, dim=-1, largest=True)
-    ctok = torch.gather(tok, dim=-1, index=cpos)
-    cvalid = torch.gather(tvalid, dim=-1, index=cpos)
+    if kind == "qboracle":
+        # candidates over the whole history, unscanned tokens at finfo.min,
+        # which isfinite() keeps valid (EV:5048-5058)
+        scan_blocks = torch.zeros((b, hq, nb), dtype=torch.bool).scatter_(-1, blocks, True)
+        scan_keep = scan_blocks.repeat_interleave(block, dim=-1)[..., :history]
+        cpart = part_all.masked_fill(~scan_keep, torch.finfo(part_all.dtype).min)
+        req = min(history, max(1, math.ceil(candidate_fraction * history)))
+        cps, ctok = torch.topk(cpart, k=req, dim=-1, largest=True)
+        cvalid = torch.isfinite(cps)
+    else:
+        tok = (blocks[..., None] * block + torch.arange(block)).reshape(b, hq, -1)
+        tvalid = tok < history
+        tok = tok.clamp_max(history - 1)
+        skeys = torch.gather(k_hist, dim=2, index=tok[..., None].expand(-1, -1, -1, d))
+        ssel = torch.gather(skeys.float(), dim=-1, index=qdims[:, :, None, :].expand(-1, -1, tok.shape[-1], -1))
+        part = (ssel * q_sel[:, :, None, :]).sum(dim=-1).masked_fill(~tvalid, torch.finfo(torch.float32).min)
+        req = min(tok.shape[-1], max(1, math.ceil(candidate_fraction * history)))
+        _, cpos = torch.topk(part, k=req, dim=-1, largest=True)
+        ctok = torch.gather(tok, dim=-1, index=cpos)
+        cvalid = torch.gather(tvalid, dim=-1, index=cpos)
     ckeys = torch.gather(k_hist, dim=2, index=ctok[..., None].expand(-1, -1, -1, d))
     cs = torch.matmul(query_states[:, :, 0:1, :], ckeys.transpose(2, 3)).squeeze(2) * scaling
     cs = cs.masked_fill(~cvalid, torch.finfo(cs.dtype).min)

@@ -21,7 +21,8 @@ Run from the repository root with the reference checked out at
 
     python tests/golden/make_reuse_vectors.py [scenario ...]
 
-Outputs ``tests/golden/reuse_<name>.npz`` and ``tests/golden/block_<name>.npz``.
+Outputs ``tests/golden/reuse_<name>.npz`` and ``tests/golden/block_<name>.npz``
+(the stateless modes: qbb, brep, qboracle and qabs{S}cand{pct}attn).
 """
 
 from __future__ import annotations
@@ -110,13 +111,27 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
 
 
 # Block-metadata selectors (qbb: Quest-style channel bounds, EV:5508-5617;
-# brep: block representatives with their BlockRepState, EV:5361-5505, 1853-1918).
+# brep: block representatives with their BlockRepState, EV:5361-5505, 1853-1918)
+# and the other stateless decode modes whose final index list goes through
+# _maybe_cuda_final_attention (qboracle, qabs{S}cand{pct}attn).
 # name: (mode, dtype, Hq, Hkv, T0, steps, top_fraction, sink, recent, keep_self, seed)
 BLOCK_SCENARIOS = {
     "qbb16q8s12cand4_fp32": ("qbb16q8s12cand4", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 11),
     "qbb8q16s25cand6p25_fp32": ("qbb8q16s25cand6p25", torch.float32, 4, 4, 201, 3, 0.03, 0, 0, False, 12),
     "brep16r2q8s12cand4_fp32": ("brep16r2q8s12cand4", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 13),
     "brep8r1q16s25cand6p25_fp32": ("brep8r1q16s25cand6p25", torch.float32, 2, 1, 233, 3, 0.03, 0, 4, True, 14),
+    # block max-pool of the partial scores (qboracle, EV:5008-5097)
+    "qboracle16q8s12cand4_fp32": ("qboracle16q8s12cand4", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 16),
+    "qboracle8q16s25cand6p25_fp32": ("qboracle8q16s25cand6p25", torch.float32, 2, 1, 233, 3, 0.03, 0, 4, False, 17),
+    # bf16 inputs, as the GPU step takes them; the seed is one where no tie of
+    # bf16-rounded rerank scores decides the kept set (the CPU fallback ranks
+    # bf16 matmul outputs, EV:5060-5067; kernels rank the fp32 scores)
+    "qboracle16q8s12cand4_bf16": ("qboracle16q8s12cand4", torch.bfloat16, 8, 2, 400, 3, 0.02, 3, 5, True, 35),
+    # the timed candidate-attention mode (qabs{S}cand{pct}attn, EV:4400-4502;
+    # top_fraction is not used by it)
+    "qabs8cand3attn_fp32": ("qabs8cand3attn", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 18),
+    "qabs16cand10attn_fp32": ("qabs16cand10attn", torch.float32, 4, 4, 211, 3, 0.02, 0, 0, False, 19),
+    "qabs8cand5attn_bf16": ("qabs8cand5attn", torch.bfloat16, 4, 2, 257, 3, 0.02, 4, 4, True, 20),
 }
 
 
@@ -143,9 +158,12 @@ def run_block(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, rec
     brep_state = ev.BlockRepState() if mode.startswith("brep") else None
     outs, finals = [], []
     try:
+        # qabs{S}cand{pct}attn runs its candidate path only with the fast-path
+        # flag (EV:6436-6449), as the reference's timed runs set it
         with ev.attention_mode(mode=mode, top_fraction=top_fraction, max_heads_per_token=3,
                                always_keep_self=keep_self, protect_sink_tokens=sink,
-                               protect_recent_tokens=recent, load_stats=None, brep_state=brep_state):
+                               protect_recent_tokens=recent, load_stats=None, brep_state=brep_state,
+                               qabs_fast_path=mode.startswith("qabs")):
             for s in range(steps):
                 n = t0 + s + 1
                 seen.clear()

@@ -1,6 +1,7 @@
-"""GPU parity of the block-metadata selectors (qbb, brep) against the oracle,
-which the reference's own drivers pin (tests/test_oracle_block.py): metadata,
-block scores and final masks bit-exact; attention within 1e-2 / 2e-2."""
+"""GPU parity of the block selectors (qbb, brep, qboracle) against the
+oracle, which the reference's own drivers pin (tests/test_oracle_block.py):
+metadata, block scores and final masks bit-exact; attention within 1e-2 /
+2e-2.  The reference's bf16 qboracle vectors also run through the GPU step."""
 
 import numpy as np
 import pytest
@@ -8,11 +9,16 @@ import torch
 
 from kv_cache_amd import _lib
 from kv_cache_amd import blocksel as BS
+from oracle import qkv_oracle as O
 from oracle import ref_semantics as R
+from tests.test_oracle_block import load_block_golden
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 RTOL, ATOL = 1e-2, 2e-2
+
+
+KINDS = {BS.QBB: "qbb", BS.BREP: "brep", BS.QBORACLE: "qboracle"}
 
 
 def f32(t):
@@ -84,6 +90,10 @@ def test_brep_metadata_and_scores(block, reps, t):
     ("brep16r4q8s6p25cand2", 32, 8, 9000, 2, 4, 8, True),
     ("qbb16q8s40cand10", 8, 2, 20000, 1, 2, 2, True),          # 8000 scanned tokens, 2000 candidates
     ("brep32r2q8s90cand11", 4, 1, 36000, 1, 0, 0, True),       # 32400 scanned, 3960 candidates
+    ("qboracle16q8s12cand4", 8, 2, 3000, 3, 3, 5, True),
+    ("qboracle8q16s25cand6p25", 4, 4, 1500, 2, 0, 0, False),
+    ("qboracle64q8s6p25cand2", 32, 8, 9000, 2, 4, 8, True),
+    ("qboracle1q8s5cand3", 8, 2, 5000, 2, 2, 2, True),          # one-token blocks: 250 scanned tokens
 ])
 def test_step_matches_oracle(mode, hq, hkv, t, steps, sink, recent, keep_self):
     kind, block, reps, dims, scan, cand = BS.parse_block_mode(mode)
@@ -96,11 +106,59 @@ def test_step_matches_oracle(mode, hq, hkv, t, steps, sink, recent, keep_self):
     for s in range(steps):
         n = t + s + 1
         out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
-        want, keep = R.block_select_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), "qbb" if kind == BS.QBB
-                                         else "brep", block, dims, scan, cand, 0.02, 128 ** -0.5, sink, recent,
-                                         keep_self, reps)
+        want, keep = R.block_select_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), KINDS[kind], block, dims,
+                                         scan, cand, 0.02, 128 ** -0.5, sink, recent, keep_self, reps)
         assert np.array_equal(step.final_mask().cpu().numpy(), keep), (mode, s)
         np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("block,t,hq,hkv,dims", [(16, 1000, 8, 2, 8), (7, 333, 4, 4, 16), (64, 2100, 4, 1, 12),
+                                                 (1, 300, 8, 2, 8), (300, 4000, 4, 2, 128), (2048, 5000, 2, 1, 8)])
+def test_qboracle_block_scores_match_oracle(block, t, hq, hkv, dims):
+    # block maxima of the partial scores (EV:5030-5044), bit for bit
+    from kv_cache_amd.reuse import dim_major_append
+
+    lib = _lib.load()
+    k, _, g = _kv(1, hkv, t, block + t)
+    k[0, 0, 5] = k[0, 0, 3]
+    q = torch.randn((1, hq, 128), generator=g).to(torch.bfloat16)
+    kd, qd = k.to(DEV), q.to(DEV)
+    kdm = torch.empty((1, hkv, 128, t + 64), dtype=torch.bfloat16, device=DEV)
+    dim_major_append(kd, kdm, 0, t)
+    nb = -(-t // block)
+    out = torch.full((hq, nb + 3), 7.0, dtype=torch.float32, device=DEV)
+    _lib.check(lib.qkv_block_max_partial_scores(qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), 1, hq, hkv,
+                                                t, 128, block, dims, out.data_ptr(), nb + 3, _lib.stream_of(kd)))
+    want = O.block_max(R.partial_scores(f32(q), np.repeat(f32(k), hq // hkv, axis=1), dims), block)
+    got = out.cpu().numpy()
+    assert np.array_equal(got[:, :nb].reshape(1, hq, nb), want)
+    assert (got[:, nb:] == 7.0).all()
+
+
+@pytest.mark.parametrize("name", ["qboracle16q8s12cand4_bf16"])
+def test_step_reproduces_reference_vectors(name):
+    # the reference's qboracle driver on bf16 inputs, replayed through the GPU
+    # step: every step's final mask bit-exact, outputs within tolerance
+    g = load_block_golden(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    kd = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
+    vd = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
+    step = BS.BlockSelectDecodeStep(g["mode"], 1, hq, hkv, 128, kd.size(2) + 8, top_fraction=g["top_fraction"],
+                                    protect_sink=g["sink"], protect_recent=g["recent"], keep_self=g["keep_self"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
+        out = step(q, kd[:, :, :n], vd[:, :, :n], g["scaling"])
+        assert np.array_equal(step.final_mask().cpu().numpy(), g["final"][s][..., :n]), (name, s)
+        np.testing.assert_allclose(f32(out), g["out"][s], rtol=RTOL, atol=ATOL)
+
+
+def test_qboracle_more_candidates_than_scanned_is_an_error():
+    k, v, g = _kv(1, 2, 600, 9)
+    q = torch.randn((1, 4, 128), generator=g).to(torch.bfloat16).to(DEV)
+    step = BS.BlockSelectDecodeStep("qboracle16q8s2cand10", 1, 4, 2, 128, 1024)
+    with pytest.raises(RuntimeError, match="more candidates than scanned tokens"):
+        step(q, k.to(DEV), v.to(DEV), 0.1)
 
 
 def test_new_sequence_resets():

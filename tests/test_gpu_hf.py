@@ -98,3 +98,50 @@ def test_generate_runs():
         out = model.generate(prompt, past_key_values=cache, max_new_tokens=8, do_sample=False)
     assert out.shape == (1, 158)
     assert cache.get_seq_length() == 157
+
+
+def test_keep_self_flag():
+    # every history block kept: with keep_self (the reference's default) the
+    # attention covers the whole cache and equals dense SDPA; without it the
+    # current token is left out, as the reference's --always_keep_self false
+    from transformers.cache_utils import DynamicCache
+
+    hf.register()
+    model = _model(layers=1)
+    prompt = torch.randint(0, 512, (1, 120), generator=torch.Generator().manual_seed(4)).to(DEV)
+    want = _decode(model, "sdpa", DynamicCache(config=model.config), prompt, 3)
+    kept = _decode(model, "int4_sparse", hf.Int4SparseCache(capacity=512, topk=32, keep_self=True), prompt, 3)
+    dropped = _decode(model, "int4_sparse", hf.Int4SparseCache(capacity=512, topk=32, keep_self=False), prompt, 3)
+    for g, w in zip(kept, want):
+        torch.testing.assert_close(g, w, rtol=3e-2, atol=3e-2)
+    assert max(float((d - k).abs().max()) for d, k in zip(dropped, kept)) > 1e-3
+
+
+def test_protected_tokens_flow_through():
+    # a one-block selection plus sink / recent tokens: logits stay finite and
+    # differ from the same cache without protection
+    hf.register()
+    model = _model(layers=1)
+    prompt = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(5)).to(DEV)
+    a = _decode(model, "int4_sparse", hf.Int4SparseCache(capacity=512, topk=1, protect_sink=8, protect_recent=32),
+                prompt, 3)
+    b = _decode(model, "int4_sparse", hf.Int4SparseCache(capacity=512, topk=1), prompt, 3)
+    assert all(torch.isfinite(x).all() for x in a)
+    assert max(float((x - y).abs().max()) for x, y in zip(a, b)) > 1e-3
+
+
+def test_padded_batch_is_refused_at_decode():
+    # the int4 kernels take no per-token mask: a left-padded batch must not
+    # silently attend to its padding
+    hf.register()
+    model = _model(layers=1)
+    model.config._attn_implementation = "int4_sparse"
+    ids = torch.randint(0, 512, (2, 40), generator=torch.Generator().manual_seed(6)).to(DEV)
+    mask = torch.ones((2, 40), dtype=torch.long, device=DEV)
+    mask[0, :7] = 0
+    cache = hf.Int4SparseCache(capacity=128, topk=2)
+    with torch.no_grad():
+        model(ids, attention_mask=mask, past_key_values=cache, use_cache=True)     # prefill: SDPA with the mask
+        with pytest.raises(RuntimeError, match="padded batches"):
+            model(ids[:, :1], attention_mask=torch.cat([mask, mask[:, :1] * 0 + 1], dim=1), past_key_values=cache,
+                  use_cache=True)

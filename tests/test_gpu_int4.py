@@ -460,25 +460,85 @@ def test_config1_end_to_end():
     assert np.allclose(f32(out), want, rtol=RTOL, atol=ATOL)
 
 
+def _protected_case(g_size, batch, t, block, n_sel, sink, recent, keep_self, mode=None):
+    """A decode step with the reference's protected tokens against the oracle:
+    the top-k over the history's block maxima bit-exact, the attention over
+    the kept blocks plus the sink / recent / current tokens within tolerance."""
+    hkv = 8 if g_size < 8 else 4
+    hq = hkv * g_size
+    g = torch.Generator().manual_seed(t + (n_sel or 0))
+    k = rand_k(batch, hkv, t, 128, t)
+    v = torch.randn((batch, hkv, t, 128), generator=g).to(torch.bfloat16)
+    q = torch.randn((batch, hq, 128), generator=g).to(torch.bfloat16)
+    if mode is None:
+        step = K.SparseDecodeStep(batch, hq, hkv, 128, t, block, n_sel, DEV, protect_sink=sink,
+                                  protect_recent=recent, keep_self=keep_self)
+    else:
+        step = K.SparseDecodeStep.for_mode(mode, batch, hq, hkv, 128, t, DEV, protect_sink=sink,
+                                           protect_recent=recent, keep_self=keep_self)
+    channels = step.plan.selected if mode else 32
+    cache = K.Int4KCache.from_prefill(k.to(DEV), 32, channels)
+    out = step(q.to(DEV), cache, k.to(DEV), v.to(DEV), 128 ** -0.5)
+    history = t - 1
+    rows = batch * hkv
+    kn = f32(k).reshape(rows, t, 128)
+    packed, scales = O.int4_pack_k(kn, 32)
+    chan = O.select_channels(O.channel_stats(packed, scales, 32), channels)   # chosen over the whole cache
+    slab, sbits = O.build_slab(kn[:, :history], chan)                     # the history is what is scored
+    _, _, bmax, sel = O.decode_select(f32(q), slab, sbits, chan, hkv, step.block, step.topk)
+    assert np.array_equal(step.sel.cpu().numpy().reshape(rows, -1), sel)
+    want = O.sparse_attention_protected(f32(q), f32(k), f32(v), sel.reshape(batch, hkv, -1), step.block, history,
+                                        128 ** -0.5, sink, recent, keep_self)
+    np.testing.assert_allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+    return step
+
+
+@pytest.mark.parametrize("g_size,batch,t,block,n_sel,sink,recent,keep_self", [
+    (2, 2, 4097, 16, 64, 4, 8, True),       # fused selection, every kind of protected token
+    (4, 1, 2001, 16, 32, 0, 0, True),       # keep the current token only; partial last block
+    (1, 1, 1025, 1, 256, 10, 10, True),     # one-token blocks
+    (8, 1, 3000, 16, 16, 100, 0, False),    # a long sink that overlaps selected blocks
+    (4, 1, 1500, 64, 4, 0, 700, True),      # a recent range over many selected blocks
+    (2, 1, 70001, 16, 128, 4, 16, True),    # 4375 blocks: top-k launch, then attention
+])
+def test_decode_step_protected(g_size, batch, t, block, n_sel, sink, recent, keep_self):
+    _protected_case(g_size, batch, t, block, n_sel, sink, recent, keep_self)
+
+
+def test_decode_step_current_token_only_through_keep_self():
+    # the current token is never a candidate (the selection ranks the history,
+    # EV:4414-4415) and is attended only with keep_self (EV:2978): give it the
+    # highest score and a value of 50, so whether it is attended shows
+    batch, hkv, hq, t = 1, 8, 16, 2049
+    g = torch.Generator().manual_seed(3)
+    k = rand_k(batch, hkv, t, 128, 5)
+    v = torch.randn((batch, hkv, t, 128), generator=g).to(torch.bfloat16)
+    q = torch.randn((batch, hq, 128), generator=g).to(torch.bfloat16)
+    qs = q.float().view(batch, hkv, 2, 128).sum(2)
+    k[:, :, t - 1] = (4.0 * qs).to(torch.bfloat16)
+    v[:, :, t - 1] = 50.0
+    for keep_self in (True, False):
+        step = K.SparseDecodeStep(batch, hq, hkv, 128, t, 16, 8, DEV, keep_self=keep_self, history_only=True)
+        cache = K.Int4KCache.from_prefill(k.to(DEV), 32, 32)
+        out = step(q.to(DEV), cache, k.to(DEV), v.to(DEV), 128 ** -0.5)
+        assert (step.sel.cpu() < (t - 1) // 16).all()          # blocks of the history only
+        w = O.sparse_attention_protected(f32(q), f32(k), f32(v), step.sel.cpu().numpy(), 16, t - 1, 128 ** -0.5,
+                                         0, 0, keep_self)
+        np.testing.assert_allclose(f32(out), w, rtol=RTOL, atol=ATOL)
+        assert (f32(out).mean() > 40) == keep_self
+
+
 def test_step_for_reference_mode():
     # qboracle16q32s6p25cand2 at 4097 keys: 4096 history keys, 32 channels,
-    # blocks of 16, ceil(6.25% * 4096 / 16) = 16 blocks kept.
+    # blocks of 16, ceil(6.25% * 4096 / 16) = 16 blocks kept, plus the
+    # current token (the reference's default --always_keep_self)
     from kv_cache_amd import modes as M
     mode, t = "qboracle16q32s6p25cand2", 4097
-    cfg = CONFIGS["cfg1"]
-    q, k, v, _ = make_layer(cfg, 0, tokens=t)
-    step = K.SparseDecodeStep.for_mode(mode, 1, 16, 8, 128, t, DEV)
-    assert (step.plan.selected, step.block, step.topk) == (32, 16, 16)
-    cache = K.Int4KCache.from_prefill(k.to(DEV), 32, step.plan.selected)
-    out = step(q.to(DEV), cache, k.to(DEV), v.to(DEV), cfg.scaling)
-    kn = f32(k).reshape(8, t, 128)
-    packed, scales = O.int4_pack_k(kn, 32)
-    chan = O.select_channels(O.channel_stats(packed, scales, 32), 32)
-    slab, sbits = O.build_slab(kn, chan)
-    _, _, _, sel = O.decode_select(f32(q), slab, sbits, chan, 8, 16, 16)
-    assert np.array_equal(step.sel.cpu().numpy().reshape(8, -1), sel)
-    want = O.sparse_attention(f32(q), f32(k), f32(v), sel.reshape(1, 8, -1), 16, t, cfg.scaling)
-    np.testing.assert_allclose(f32(out), want, rtol=RTOL, atol=ATOL)
+    step = _protected_case(2, 1, t, 16, None, 0, 0, True, mode=mode)
+    assert (step.plan.selected, step.block, step.topk, step.scored) == (32, 16, 16, 4096)
+    # qabs8cand3attn at 4097 keys: one-token blocks, ceil(3% * 4096) = 123 tokens
+    step = _protected_case(2, 1, t, 1, None, 2, 4, True, mode="qabs8cand3attn")
+    assert (step.block, step.topk) == (1, 123)
     with pytest.raises(RuntimeError, match="not a decode mode"):
         K.SparseDecodeStep.for_mode("qabs8cand3reuse", 1, 16, 8, 128, t, DEV)
     assert M.decode_plan(mode, t).tokens_kept == 256

@@ -13,15 +13,24 @@ from oracle import ref_semantics as R
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 BLOCK_SCENARIOS = ["qbb16q8s12cand4_fp32", "qbb8q16s25cand6p25_fp32", "brep16r2q8s12cand4_fp32",
-                   "brep8r1q16s25cand6p25_fp32"]
+                   "brep8r1q16s25cand6p25_fp32", "qboracle16q8s12cand4_fp32", "qboracle8q16s25cand6p25_fp32",
+                   "qboracle16q8s12cand4_bf16"]
+ATTN_SCENARIOS = ["qabs8cand3attn_fp32", "qabs16cand10attn_fp32", "qabs8cand5attn_bf16"]
 
 
 def parse_block_mode(mode):
-    """(kind, block, reps, dims, scan fraction, candidate fraction) of a qbb / brep mode."""
+    """(kind, block, reps, dims, scan fraction, candidate fraction) of a qbb / brep /
+    qboracle mode; ("qabs", 1, 1, dims, 1.0, candidate fraction) of a qabs{S}cand{pct}attn mode."""
     pct = lambda x: float(x.replace("p", ".")) / 100.0   # noqa: E731
     m = re.fullmatch(r"qbb(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
     if m:
         return "qbb", int(m.group(1)), 1, int(m.group(2)), pct(m.group(3)), pct(m.group(4))
+    m = re.fullmatch(r"qboracle(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
+    if m:
+        return "qboracle", int(m.group(1)), 1, int(m.group(2)), pct(m.group(3)), pct(m.group(4))
+    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)attn", mode)
+    if m:
+        return "qabs", 1, 1, int(m.group(1)), 1.0, pct(m.group(2))
     m = re.fullmatch(r"brep(\d+)r(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
     return "brep", int(m.group(1)), int(m.group(2)), int(m.group(3)), pct(m.group(4)), pct(m.group(5))
 
@@ -49,7 +58,40 @@ def test_block_steps_match_reference_vectors(name):
                                         g["dims"], g["scan"], g["cand"], g["top_fraction"], g["scaling"], g["sink"],
                                         g["recent"], g["keep_self"], g["reps"])
         assert np.array_equal(keep, g["final"][s][..., :n]), (name, s)
-        np.testing.assert_allclose(out[:, 0], g["out"][s], rtol=1e-5, atol=1e-5)
+        tol = dict(rtol=1e-2, atol=2e-2) if name.endswith("bf16") else dict(rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
+
+
+@pytest.mark.parametrize("name", ATTN_SCENARIOS)
+def test_qabs_attn_steps_match_reference_vectors(name):
+    # the timed qabs{S}cand{pct}attn mode: every step's final index set
+    # bit-exact, outputs to 1e-5 (fp32) / the bf16 attention tolerance
+    g = load_block_golden(name)
+    tol = dict(rtol=1e-5, atol=1e-5) if name.endswith("fp32") else dict(rtol=1e-2, atol=2e-2)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        out, keep = R.qabs_attn_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"],
+                                     g["scaling"], g["sink"], g["recent"], g["keep_self"])
+        assert np.array_equal(keep, g["final"][s][..., :n]), (name, s)
+        np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
+
+
+@pytest.mark.parametrize("name", ATTN_SCENARIOS)
+def test_qabs_attn_cpu_baseline_matches_reference_vectors(name):
+    # the torch op sequence bench.py times as the decode CPU baseline
+    # (qabs_candidate_attention_cpu) gives the reference driver's outputs
+    import torch
+
+    g = load_block_golden(name)
+    dt = torch.bfloat16 if name.endswith("bf16") else torch.float32
+    k, v = torch.from_numpy(g["k"]).to(dt), torch.from_numpy(g["v"]).to(dt)
+    tol = dict(rtol=1e-5, atol=1e-6) if dt == torch.float32 else dict(rtol=0, atol=0)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s])[:, :, None, :].to(dt)
+        out = R.qabs_candidate_attention_cpu(q, k[:, :, :n], v[:, :, :n], g["dims"], g["cand"], g["scaling"],
+                                             g["sink"], g["recent"], g["keep_self"])
+        np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], **tol)
 
 
 def test_block_minmax_brute_force():
@@ -111,12 +153,47 @@ def test_cpu_baseline_op_sequence_matches_reference_vectors(name):
     import torch
 
     g = load_block_golden(name)
-    k, v = torch.from_numpy(g["k"]), torch.from_numpy(g["v"])
+    dt = torch.bfloat16 if name.endswith("bf16") else torch.float32
+    k, v = torch.from_numpy(g["k"]).to(dt), torch.from_numpy(g["v"]).to(dt)
     for s in range(g["steps"]):
         n = g["t0"] + s + 1
-        q = torch.from_numpy(g["q"][s])[:, :, None, :]
+        q = torch.from_numpy(g["q"][s])[:, :, None, :].to(dt)
         out, keep = R.block_select_step_cpu(q, k[:, :, :n], v[:, :, :n], g["kind"], g["block"], g["dims"], g["scan"],
                                             g["cand"], g["top_fraction"], g["scaling"], g["sink"], g["recent"],
                                             g["keep_self"], g["reps"])
         assert np.array_equal(keep.numpy(), g["final"][s][..., :n]), (name, s)
-        np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(out.float().numpy()[:, 0], g["out"][s], rtol=1e-5, atol=1e-6)   # same ops
+
+
+@pytest.mark.parametrize("name", ["brep16r2q8s12cand4_fp32", "brep8r1q16s25cand6p25_fp32"])
+def test_brep_partial_scores_drive_the_reference_caller(name):
+    # brep_partial_scores' oracle, fed through the caller's remaining steps
+    # (EV:5426-5505), gives the final mask the reference's brep driver wrote
+    import math
+    g = load_block_golden(name)
+    gqa = g["q"].shape[2] // g["k"].shape[1]
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        kh = np.repeat(g["k"][:, :, : n - 1], gqa, axis=1)
+        q = g["q"][s]
+        ridx, rvalid = R.block_representatives(kh, g["block"], g["reps"])
+        part = R.brep_partial_scores(q, kh, ridx, rvalid, g["block"], g["dims"], g["scan"])
+        nb = -(-(n - 1) // g["block"])
+        n_scan = min(nb, max(1, math.ceil(g["scan"] * (n - 1) / g["block"])))
+        assert (np.isfinite(part).sum(axis=-1) <= n_scan * g["block"]).all()
+        for bi in range(q.shape[0]):
+            for hi in range(q.shape[1]):
+                final = R.brep_caller_final_mask(part[bi, hi], q[bi, hi], kh[bi, hi], n, g["cand"], g["top_fraction"],
+                                                 g["scaling"], g["sink"], g["recent"], g["keep_self"])
+                assert np.array_equal(final, g["final"][s][bi, hi, :n]), (name, s, bi, hi)
+
+
+def test_brep_partial_scores_known_answer():
+    # 2 blocks of 2 tokens, one dim: representative = larger |k|; block 1 wins
+    q = np.array([[[2.0]]], np.float32)
+    k = np.array([[[[1.0], [-3.0], [2.0], [0.5]]]], np.float32)
+    idx, valid = R.block_representatives(k, 2, 1)
+    assert idx.tolist() == [[[[1], [2]]]]
+    part = R.brep_partial_scores(q, k, idx, valid, 2, 1, 0.25)     # ceil(0.25 * 4 / 2) = 1 block
+    assert part.tolist() == [[[-np.inf, -np.inf, 4.0, 1.0]]]
+

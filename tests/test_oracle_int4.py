@@ -310,6 +310,58 @@ def test_attention_matches_dense_softmax():
         assert np.allclose(out[bi, h], w @ v[bi, h // 2])
 
 
+def test_protected_tokens_known_answers():
+    # history 10: sink 2 -> 0, 1; recent 3 -> 7, 8, 9; self -> 10
+    assert O.protected_tokens(10, 2, 3, True).tolist() == [0, 1, 7, 8, 9, 10]
+    # a recent range reaching into the sink keeps each token once
+    assert O.protected_tokens(4, 3, 3, False).tolist() == [0, 1, 2, 3]
+    assert O.protected_tokens(5, 0, 0, True).tolist() == [5]
+    assert O.protected_tokens(5, 9, 0, False).tolist() == [0, 1, 2, 3, 4]
+    assert O.protected_tokens(5, 0, 0, False).size == 0
+
+
+def test_protected_tokens_match_reference_index_build():
+    # the valid entries of the reference's own final index build
+    # (ref_semantics.final_indices_from_selected, EV:2938-2982, pinned by the
+    # reference's qabs-attn vectors) are the selection plus protected_tokens
+    import torch
+
+    from oracle import ref_semantics as R
+
+    rng = np.random.default_rng(11)
+    for history, sink, recent, keep_self in [(40, 4, 6, True), (40, 0, 0, True), (12, 8, 8, False),
+                                             (25, 0, 5, True), (25, 3, 0, False)]:
+        sel = np.sort(rng.choice(history, size=7, replace=False))
+        idx, valid = R.final_indices_from_selected(torch.from_numpy(sel).view(1, 1, -1),
+                                                   torch.ones((1, 1, 7), dtype=torch.bool), history, history + 1,
+                                                   sink, recent, keep_self)
+        got = idx[valid].numpy()
+        assert got.size == np.unique(got).size                       # every token once
+        assert np.array_equal(np.sort(got), np.union1d(sel, O.protected_tokens(history, sink, recent, keep_self)))
+
+
+def test_protected_attention_closed_forms():
+    rng = np.random.default_rng(12)
+    b, hq, hkv, t, d = 1, 4, 2, 33, 8                  # history 32 + the current token
+    q = rng.standard_normal((b, hq, d))
+    k = rng.standard_normal((b, hkv, t, d))
+    v = rng.standard_normal((b, hkv, t, d))
+    # every history block selected + protected ranges + self == dense softmax
+    # over all 33 tokens (a protected token counted twice would not be)
+    all_blocks = np.tile(np.arange(8), (b, hkv, 1))
+    out = O.sparse_attention_protected(q, k, v, all_blocks, 4, 32, 0.3, sink=3, recent=5, keep_self=True)
+    for h in range(hq):
+        s = k[0, h // 2] @ q[0, h] * 0.3
+        w = np.exp(s - s.max())
+        assert np.allclose(out[0, h], (w / w.sum()) @ v[0, h // 2])
+    # nothing selected, no sink / recent, keep_self: the current token's value
+    out = O.sparse_attention_protected(q, k, v, np.full((b, hkv, 1), -1), 4, 32, 0.3, keep_self=True)
+    assert np.allclose(out[0], v[0, np.arange(hq) // 2, 32])
+    # one selected block overlapping the sink: tokens 0..3 with sink 2 -> {0, 1, 2, 3} once
+    out = O.sparse_attention_protected(np.zeros((b, hq, d)), k, v, np.zeros((b, hkv, 1), int), 4, 32, 1.0, sink=2)
+    assert np.allclose(out[0, 0], v[0, 0, :4].mean(0))
+
+
 # ---------------------------------------------------------------------------
 # Prefill scoring
 # ---------------------------------------------------------------------------
