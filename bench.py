@@ -231,7 +231,7 @@ def main() -> int:
                 sec = run_decode(args, args.secondary, with_cpu=True)
                 line["secondary"] = {k: sec[k] for k in ("config", "value", "unit", "ms_per_step", "us_per_layer",
                                                          "dense_bf16_us_per_layer", "roofline", "kernels",
-                                                         "cpu_baseline")}
+                                                         "hbm_read_probe", "cpu_baseline")}
             except Exception as exc:   # the headline line is still printed
                 log(f"[bench] secondary workload {args.secondary} failed: {exc!r}")
                 line["secondary"] = {"config": {"workload": args.secondary}, "error": repr(exc)}
@@ -250,6 +250,34 @@ def copy_probe(mb: int) -> None:
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
+
+
+def hbm_read_probe(nbytes: int, reps: int = 20, min_total: int = 1 << 30) -> dict:
+    """The read ceiling of one launch of ``nbytes``: libqkv's streaming-read
+    probe (the scoring kernel's access shape, no arithmetic) over rotating
+    buffers of that size (>= 1 GiB in all, so no launch finds its buffer in
+    the 256 MB Infinity Cache), graph-replayed; HIP events on the stream the
+    probe runs on."""
+    import torch
+
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    n_buf = max(2, -(-min_total // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(b) for b in range(n_buf)]
+    words = lib.qkv_hbm_read_probe_sink_words(nbytes)
+    sink = torch.empty(words, dtype=torch.int32, device="cuda")
+
+    def run():
+        for b in bufs:
+            _lib.check(lib.qkv_hbm_read_probe(b.data_ptr(), nbytes, sink.data_ptr(), words,
+                                              torch.cuda.current_stream().cuda_stream))
+
+    g = graph_of(run)
+    ms = time_replays(g.replay, reps) / n_buf
+    del g, bufs
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bytes": nbytes, "us_per_launch": ms * 1e3, "gbs": gbs, "frac_hbm_peak": gbs / HBM_PEAK_GBS}
 
 
 def planted_recall(cfg, qs, caches, planted, ks=(64, 256, 1024)) -> dict:
@@ -378,6 +406,14 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
     torch.cuda.synchronize()
     copy_probe(args.copy_probe_mb)
     recall = planted_recall(cfg, qs, caches, planted) if cfg.planted else None
+    # the read ceiling of one launch of the scoring kernel's size (layer buffers freed first)
+    fused = step.fused
+    del qs, ks, vs, caches, planted, step, replay
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    probe = hbm_read_probe(keys_per_layer * cfg.slab_bytes_per_key())
+    log(f"[bench] read probe of {probe['bytes'] / 1e6:.1f} MB: {probe['us_per_launch']:.2f} us/launch, "
+        f"{probe['gbs']:.0f} GB/s ({probe['frac_hbm_peak']:.1%} of peak)")
     if recall:
         log(f"[bench] planted-key recall at k tokens: {recall}")
 
@@ -406,7 +442,7 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
             "workload": f"{name}: {cfg.name}",
             "batch": cfg.batch, "q_heads": cfg.q_heads, "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
             "context": T, "layers": layers, "int4_group": cfg.group, "channels": cfg.selected,
-            "block": cfg.block, "topk_blocks": cfg.topk, "graph": not args.eager, "fused_select": step.fused,
+            "block": cfg.block, "topk_blocks": cfg.topk, "graph": not args.eager, "fused_select": fused,
         },
         "us_per_layer": ms_per_step * 1e3 / layers,
         "dense_bf16_us_per_layer": kernels["dense_bf16_attention"]["us_per_launch"],
@@ -420,6 +456,7 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
             "traffic": read_traffic(name, "decode_scores_kernel"),
         },
         "kernels": kernels,
+        "hbm_read_probe": probe,
         "cpu_baseline": cpu,
     }
     if recall:

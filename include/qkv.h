@@ -253,6 +253,15 @@ int qkv_sparse_attention_protected(const void* query, const void* key, const voi
                                    int64_t protect_recent, int keep_self, float scaling, float* workspace,
                                    int64_t workspace_bytes, int32_t* sel_out, void* out, void* stream);
 
+/* Streaming-read probe, no counterpart in the reference: reads `bytes` (a
+ * positive multiple of 16 KiB, 16-byte aligned) once with the access shape
+ * of qkv_int4_decode_scores -- whole 4 KiB tiles per wave, 16-byte
+ * non-temporal loads, the next tile in flight -- and stores one fold word
+ * per wave into sink (qkv_hbm_read_probe_sink_words words).  Its time is the
+ * read ceiling of one launch of that size; the benchmark reports it. */
+int64_t qkv_hbm_read_probe_sink_words(int64_t bytes);
+int qkv_hbm_read_probe(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_words, void* stream);
+
 /* Bytes of the static device scratch behind
  * qkv_sparse_attention_select_noalloc (one copy per GPU, held until the
  * process ends). */

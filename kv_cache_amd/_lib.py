@@ -60,6 +60,8 @@ _PROTOTYPES = {
                                            _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
     "qkv_sparse_attention_protected": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64,
                                               _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _vp, _vp]),
+    "qkv_hbm_read_probe_sink_words": (_i64, [_i64]),
+    "qkv_hbm_read_probe": (_i32, [_vp, _i64, _vp, _i64, _vp]),
     "qkv_sparse_attention_select_noalloc": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp,
                                                    _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
     "qkv_token_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _f32, _vp,

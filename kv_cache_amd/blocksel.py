@@ -76,8 +76,9 @@ def step_counts(history: int, block: int, scan: float, cand: float, top: float) 
 class BlockSelectDecodeStep:
     """One layer's qbb / brep / qboracle decode step with its block metadata, for bf16
     K/V caches [B, Hkv, T, 128] of up to ``capacity`` tokens.  Call it once
-    per decode token with the cache including the current token; a shorter
-    history than the previous call's starts a new sequence."""
+    per decode token with the cache including the current token; a call
+    whose history is not the previous call's plus one starts a new sequence
+    (the metadata and the dim-major copy are rebuilt)."""
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
@@ -157,8 +158,8 @@ class BlockSelectDecodeStep:
             self.out.copy_(value[:, :, -1, :].repeat_interleave(g, dim=1))
             return self.out
         history = key_count - 1
-        if self.last_history is not None and history <= self.last_history:
-            self.reset()
+        if self.last_history is not None and history != self.last_history + 1:
+            self.reset()     # not the next token of the last sequence: a new sequence
         if self.meta_len > history or self.kdm_len > history:
             self.reset()
         self._sync_cache(key, history)

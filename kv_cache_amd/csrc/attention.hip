@@ -542,10 +542,14 @@ constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 // 1024 workgroups of 16 chunks in two rounds.
 constexpr int max_iters_for(int64_t g) { return g >= 8 ? 8 : g == 4 ? 32 : 16; }
 
+// Doubling stops once one workgroup covers the whole row: further chunks
+// would only walk empty slots.
 int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
   const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
   int it = 1;
-  while (it < max_iters_for(g) && rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS) it *= 2;
+  while (it < max_iters_for(g) && per_iter * it < n_slots &&
+         rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS)
+    it *= 2;
   return it;
 }
 

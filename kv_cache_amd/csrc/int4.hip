@@ -17,11 +17,18 @@
 #ifndef QKV_SCORE_TARGET_WGS
 #define QKV_SCORE_TARGET_WGS 4096
 #endif
+// Waves per decode-scoring workgroup (the kernel has no workgroup barrier:
+// the waves only share the workgroup's chunk of the row).
+#ifndef QKV_SCORE_WAVES
+#define QKV_SCORE_WAVES 4
+#endif
 
 namespace qkv {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kScoreWaves = QKV_SCORE_WAVES;
+constexpr int kScoreThreads = 64 * kScoreWaves;
 
 // Exact fp16 value times 2^24 (every finite fp16 is a multiple of 2^-24).
 __device__ __forceinline__ uint64_t fp16_fixed24(uint32_t bits) {
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(64) void query_words_kernel(
 }
 
 template <int S, bool DEBUG>
-__global__ __launch_bounds__(kThreads) void decode_scores_kernel(
+__global__ __launch_bounds__(kScoreThreads) void decode_scores_kernel(
     const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
     const int32_t* __restrict__ chan_idx, const uint8_t* __restrict__ slab,
     const uint16_t* __restrict__ slab_scales, int64_t capacity, int tokens, int block,
@@ -443,8 +450,8 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
   const int t_lo = blockIdx.x * chunk;
   const int t_hi = min(tokens, t_lo + chunk);
 
-  // A wave's stages start at t_lo + wave*STAGE and step by 4*STAGE; t_lo is
-  // a multiple of 4*STAGE, so every stage is one whole tile.  A stage with
+  // A wave's stages start at t_lo + wave*STAGE and step by kScoreWaves*STAGE;
+  // t_lo is a multiple of kScoreWaves*STAGE, so every stage is one whole tile.  A stage with
   // tb < t_hi <= tokens <= capacity lies inside the row's slab and scales
   // (capacity is a multiple of STAGE), so its loads need no per-lane guard:
   // lanes past t_hi read padding that score_stage masks to -inf.  Loads
@@ -459,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
 
   int tb = t_lo + wave * STAGE;
   if (tb >= t_hi) return;   // wave-uniform; the kernel has no workgroup barrier
-  const int nst = (t_hi - tb + 4 * STAGE - 1) / (4 * STAGE);   // stages of this wave
+  const int nst = (t_hi - tb + kScoreWaves * STAGE - 1) / (kScoreWaves * STAGE);   // stages of this wave
   uint4 cw[4];
   LS sv;
   load_stage(tb, cw, sv);
@@ -524,7 +531,7 @@ __global__ __launch_bounds__(kThreads) void decode_scores_kernel(
 
   // Each wave walks its stages with the next stage's loads in flight.
   for (int i = 1; i < nst; ++i) {
-    const int tn = tb + 4 * STAGE;
+    const int tn = tb + kScoreWaves * STAGE;
     uint4 nw[4];
     LS nsv;
     load_stage(tn, nw, nsv);
@@ -544,7 +551,7 @@ int launch_scores(int S, dim3 grid, hipStream_t st, const uint16_t* q, int hq, i
   switch (S) {
 #define QKV_CASE(SS)                                                                               \
   case SS:                                                                                         \
-    decode_scores_kernel<SS, DEBUG><<<grid, kThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
+    decode_scores_kernel<SS, DEBUG><<<grid, kScoreThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
                                                                block, chunk, bmax, nb, isum, keys, \
                                                                qs);                                \
     break;
@@ -724,7 +731,7 @@ QKV_EXPORT int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t 
   if (!pow2(block) || block > stage)
     return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: block must be a power of two <= %d", stage);
   const int64_t rows = batch * kv_heads;
-  const int stage_wg = 4 * stage;   // keys one workgroup stage covers
+  const int stage_wg = kScoreWaves * stage;   // keys one workgroup stage covers
   int64_t chunk = cdiv(rows * tokens, QKV_SCORE_TARGET_WGS);
   chunk = std::max<int64_t>(stage_wg, cdiv(chunk, stage_wg) * stage_wg);
   dim3 grid(static_cast<unsigned>(cdiv(tokens, chunk)), static_cast<unsigned>(rows));

@@ -219,8 +219,10 @@ class ReuseDecodeStep:
 
     Call it once per decode token with the cache including the current token
     (T = history + 1).  The previous step's masks are used when the previous
-    call had history - 1 tokens (the ``query_token`` check of EV:1651); call
-    ``reset()`` before a new sequence."""
+    call had history - 1 tokens (the ``query_token`` check of EV:1651); any
+    other history starts a new sequence (the dim-major copy is rebuilt and no
+    previous mask is read), so ``reset()`` is needed only to restart a
+    sequence at the very next history length."""
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
@@ -309,8 +311,10 @@ class ReuseDecodeStep:
             self.out.copy_(value[:, :, -1, :].repeat_interleave(g, dim=1))
             return self.out
         history = key_count - 1
-        if self.last_history is not None and history <= self.last_history:
-            self.reset()     # a shorter or equal history is a new sequence
+        if self.last_history is not None and history != self.last_history + 1:
+            # not the next token of the last sequence: a new sequence, whose
+            # dim-major copy and previous masks must not carry over
+            self.reset()
         if self.kdm_len < history:
             dim_major_append(key, self.kdm, self.kdm_len, history)
             self.kdm_len = history

@@ -173,6 +173,20 @@ def test_new_sequence_resets():
     assert torch.equal(step.final_mask(), fresh.final_mask())
 
 
+def test_longer_new_sequence_resets():
+    k, v, g = _kv(1, 2, 900, 4)
+    k2, v2, _ = _kv(1, 2, 900, 8)
+    q = torch.randn((1, 4, 128), generator=g).to(torch.bfloat16).to(DEV)
+    kd, vd, kd2, vd2 = k.to(DEV), v.to(DEV), k2.to(DEV), v2.to(DEV)
+    for mode in ("qbb16q8s12cand4", "brep16r2q8s12cand4", "qboracle16q8s12cand4"):
+        step = BS.BlockSelectDecodeStep(mode, 1, 4, 2, 128, 1024)
+        step(q, kd[:, :, :500], vd[:, :, :500], 0.1)
+        a = step(q, kd2[:, :, :800], vd2[:, :, :800], 0.1).clone()     # another sequence, longer
+        fresh = BS.BlockSelectDecodeStep(mode, 1, 4, 2, 128, 1024)
+        assert torch.equal(a, fresh(q, kd2[:, :, :800], vd2[:, :, :800], 0.1)), mode
+        assert torch.equal(step.final_mask(), fresh.final_mask()), mode
+
+
 def test_limits_are_errors():
     with pytest.raises(RuntimeError, match="at most 40960"):
         BS.BlockSelectDecodeStep("qbb16q8s50cand4", 1, 4, 2, 128, 100000)

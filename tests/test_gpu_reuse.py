@@ -306,6 +306,25 @@ def test_step_resets_on_shorter_history():
     assert torch.equal(step.final_mask(), fresh.final_mask())
 
 
+def test_step_resets_on_longer_new_sequence():
+    # a second sequence with a longer history, without reset(): its dim-major
+    # copy must be rebuilt and no previous mask read, as for a fresh step
+    gen = torch.Generator().manual_seed(6)
+    k1 = torch.randn((1, 2, 600, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    k2 = torch.randn((1, 2, 900, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, 4, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    for n2 in (502, 800):       # the previous history + 1, and a jump past it
+        step = RU.ReuseDecodeStep("qabs8cand5reusefinal", 1, 4, 2, 128, 1024)
+        step(q, k1[:, :, :500], k1[:, :, :500], 0.1)
+        step(q, k1[:, :, :501], k1[:, :, :501], 0.1)
+        if n2 == 502:
+            step.reset()        # the very next length: only an explicit reset marks a new sequence
+        a = step(q, k2[:, :, :n2], k2[:, :, :n2], 0.1).clone()
+        fresh = RU.ReuseDecodeStep("qabs8cand5reusefinal", 1, 4, 2, 128, 1024)
+        assert torch.equal(a, fresh(q, k2[:, :, :n2], k2[:, :, :n2], 0.1))
+        assert torch.equal(step.final_mask(), fresh.final_mask())
+
+
 def test_dim_major_append_and_token_attention():
     gen = torch.Generator().manual_seed(7)
     k = torch.randn((2, 3, 700, 128), generator=gen).to(torch.bfloat16).to(DEV)
