@@ -187,11 +187,13 @@ __global__ __launch_bounds__(kRT) void reuse_scores_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ key,
     int q_heads, int group, int history, int head_dim, int64_t sb, int64_t sh, int64_t st, bool kvec,
     const uint8_t* __restrict__ cur, const uint8_t* __restrict__ prev, const uint8_t* __restrict__ fin,
-    int64_t mask_ld, bool mvec, float scaling, float* __restrict__ out, int64_t out_ld) {
+    int64_t mask_ld, bool mvec, float scaling, float* __restrict__ out, int64_t out_ld,
+    float* __restrict__ cscore, int32_t* __restrict__ ctok, int32_t* __restrict__ ccnt, int64_t c_ld) {
   using E = typename Elem<DT>::T;
   __shared__ float q_s[512];
   __shared__ uint16_t list[kScoreTile];
   __shared__ int wave_tot[kRT / 64];
+  __shared__ int n_finite;
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = row / q_heads, h = row - b * q_heads;
   for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(query + static_cast<int64_t>(row) * head_dim + d);
@@ -228,9 +230,16 @@ __global__ __launch_bounds__(kRT) void reuse_scores_kernel(
   for (int w = 0; w < wave; ++w) base += wave_tot[w];
   for (int i = 0; i < 4; ++i)
     if ((bits >> i) & 1u) list[base++] = static_cast<uint16_t>(tid * 4 + i);
+  if (tid == 0) n_finite = 0;
   __syncthreads();
   const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
 
+  // cscore (optional): the tile's union scores again, compacted at the
+  // tile's offset, with their tokens and (list length, finite scores) per
+  // tile, so that the final selection can rank the union alone
+  float* crow = cscore ? cscore + static_cast<int64_t>(row) * c_ld + tile0 : nullptr;
+  int32_t* trow = cscore ? ctok + static_cast<int64_t>(row) * c_ld + tile0 : nullptr;
+  int n_fin_own = 0;
   const E* kbase = key + b * sb + (h / group) * sh;
   for (int i = tid; i < total; i += kRT) {
     const int t = tile0 + list[i];
@@ -248,7 +257,22 @@ __global__ __launch_bounds__(kRT) void reuse_scores_kernel(
     } else {
       for (int d = 0; d < head_dim; ++d) acc = acc + q_s[d] * Elem<DT>::load(kr + d);
     }
-    orow[t] = acc * scaling;
+    const float sc = acc * scaling;
+    orow[t] = sc;
+    if (crow) {
+      crow[i] = sc;
+      trow[i] = t;
+      n_fin_own += isfinite(sc) ? 1 : 0;
+    }
+  }
+  if (crow) {
+    if (n_fin_own) atomicAdd(&n_finite, n_fin_own);
+    __syncthreads();
+    if (tid == 0) {
+      int32_t* cn = ccnt + (static_cast<int64_t>(row) * gridDim.x + blockIdx.x) * 2;
+      cn[0] = total;
+      cn[1] = n_finite;
+    }
   }
 }
 
@@ -363,16 +387,30 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 }
 
 // The final selection of reuse_finalize_kernel, with the keep largest scores
-// selected in the same launch.
-template <int VPL>
+// selected in the same launch.  When the row's union holds at least keep
+// finite scores and at most VPLC * 1024 entries (the usual case: the union
+// is a few percent of the history), the selection ranks the compacted union
+// lists of reuse_scores_kernel (VPLC keys per thread) instead of the whole
+// row (VPL keys per thread).  The keep largest are then finite union scores
+// either way, and the lists keep token order, so both paths select and
+// place the same entries (ties to the lower token).
+constexpr int kMaxTiles = kWideMax / kScoreTile;
+
+template <int VPL, int VPLC>
 __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
-    const float* __restrict__ scores, int64_t scores_ld, int keep, int history, int key_count, int sink_end,
-    int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
-    uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out, uint8_t* __restrict__ hf,
-    int64_t hf_ld) {
+    const float* __restrict__ scores, int64_t scores_ld, const float* __restrict__ cscore,
+    const int32_t* __restrict__ ctok, const int32_t* __restrict__ ccnt, int n_tiles, int64_t c_ld, int keep,
+    int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
+    int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out,
+    uint8_t* __restrict__ hf, int64_t hf_ld) {
   using WS = WideSelect<VPL, false>;
-  __shared__ typename WS::Shared sh;
-  WS ws;
+  using WC = WideSelect<VPLC, false>;
+  __shared__ union {
+    typename WS::Shared d;
+    typename WC::Shared c;
+  } sh;
+  __shared__ int tile_off[kMaxTiles + 1];
+  __shared__ int n_fin;
   const int row = blockIdx.x, tid = threadIdx.x;
   uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
   // the protected ranges, 16 bytes per store where the row is 16-byte aligned
@@ -392,20 +430,57 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     *reinterpret_cast<uint4*>(hrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
   }
   for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
-  ws.load(scores + static_cast<int64_t>(row) * scores_ld, history);
-  ws.run(keep, sh);   // its barriers order the writes above before the scatter below
+  if (tid < 64) {   // tile list offsets: one load per tile, a wave scan (n_tiles <= 40)
+    const int32_t* cn = ccnt + static_cast<int64_t>(row) * n_tiles * 2;
+    const bool on = cscore && tid < n_tiles;
+    const int len = on ? cn[2 * tid] : 0, nf = on ? cn[2 * tid + 1] : 0;
+    const int incl = wave_incl_scan_dpp(len), fin_all = wave_incl_scan_dpp(nf);
+    if (tid <= n_tiles) tile_off[tid] = incl - len;   // tile_off[n_tiles] = the total
+    if (tid == 63) n_fin = fin_all;
+  }
+  __syncthreads();   // also orders the protected-range writes above before the scatter below
   const int64_t o = static_cast<int64_t>(row) * n_out;
-  uint64_t fin = 0;   // bit i: key i is a finite score
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(ws.u[i]))) << i;
-  ws.place(sh, [&](int idx, int p, int slot) {
-    const bool valid = (fin >> slot) & 1ull;
+  auto emit = [&](int idx, int p, bool valid) {
     if (valid) hrow[idx] = 1;
     const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
     final_idx[o + p] = idx;
     final_valid[o + p] = fv;
     if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
-  });
+  };
+  const int total = tile_off[n_tiles];
+  if (cscore && n_fin >= keep && total <= VPLC * kWideNT) {   // uniform across the workgroup
+    WC wc;
+    int tok[VPLC];
+    const float* crow = cscore + static_cast<int64_t>(row) * c_ld;
+    const int32_t* trow = ctok + static_cast<int64_t>(row) * c_ld;
+#pragma unroll
+    for (int i = 0; i < VPLC; ++i) {
+      const int p = WC::pos(i);
+      const bool ok = p < total;
+      int lo = 0, hi = n_tiles - 1;   // the last tile whose list starts at or before p
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_off[mid] <= p) lo = mid;
+        else hi = mid - 1;
+      }
+      const int64_t e = static_cast<int64_t>(lo) * kScoreTile + (p - tile_off[lo]);
+      tok[i] = ok ? trow[e] : 0;
+      wc.set(i, ok ? crow[e] : 0.0f, ok);
+    }
+    wc.run(keep, sh.c);
+    uint64_t fin = 0;
+#pragma unroll
+    for (int i = 0; i < VPLC; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(wc.u[i]))) << i;
+    wc.place(sh.c, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
+  } else {
+    WS ws;
+    ws.load(scores + static_cast<int64_t>(row) * scores_ld, history);
+    ws.run(keep, sh.d);
+    uint64_t fin = 0;   // bit i: key i is a finite score
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(ws.u[i]))) << i;
+    ws.place(sh.d, [&](int idx, int p, int slot) { emit(idx, p, (fin >> slot) & 1ull); });
+  }
   const int extra = sink_end + n_rec + keep_self;
   for (int i = tid; i < extra; i += kWideNT) {
     const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
@@ -583,10 +658,18 @@ int64_t block_body_cap(const ReuseCounts& c, int64_t block) {
 
 constexpr int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
+// Scores, selection, staged top-k workspace, then (rows the wide kernel
+// selects in one workgroup) the compacted union lists and their counts.
+int64_t reuse_compact_bytes(int64_t rows, int64_t history) {
+  if (history > kWideMax) return 0;
+  const int64_t slots = cdiv(history, kScoreTile) * kScoreTile;
+  return 2 * align256(rows * slots * 4) + align256(rows * cdiv(history, kScoreTile) * 2 * 4);
+}
+
 int64_t reuse_ws_bytes(int64_t rows, int64_t history, int64_t keep) {
   const int64_t tk = qkv_topk_workspace_bytes(rows, history, keep);
   if (tk < 0) return -1;
-  return align256(rows * history * 4) + align256(rows * keep * 4) + align256(tk);
+  return align256(rows * history * 4) + align256(rows * keep * 4) + align256(tk) + reuse_compact_bytes(rows, history);
 }
 
 int64_t mask_ws_bytes(int64_t rows, int64_t n, int64_t k) {
@@ -613,7 +696,8 @@ template <int DT> struct RunReusePartial {
 template <int DT> struct RunReuseScores {
   static int run(const void* q, const void* k, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
                  int64_t D, const uint8_t* cur, const uint8_t* prev, const uint8_t* fin, int64_t mask_ld,
-                 float scaling, float* out, int64_t out_ld, hipStream_t st) {
+                 float scaling, float* out, int64_t out_ld, float* cscore, int32_t* ctok, int32_t* ccnt,
+                 int64_t c_ld, hipStream_t st) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;
     const bool kvec = ks[3] == 1 && D % 8 == 0 && aligned(k, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 &&
@@ -625,7 +709,8 @@ template <int DT> struct RunReuseScores {
   reuse_scores_kernel<DT, DF><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),        \
                                                     static_cast<int>(Hq), static_cast<int>(Hq / Hkv),          \
                                                     static_cast<int>(T), static_cast<int>(D), ks[0], ks[1], ks[2], \
-                                                    kvec, cur, prev, fin, mask_ld, mvec, scaling, out, out_ld)
+                                                    kvec, cur, prev, fin, mask_ld, mvec, scaling, out, out_ld, \
+                                                    cscore, ctok, ccnt, c_ld)
     if (kvec && D == 128) QKV_REUSE_SCORES(128);
     else QKV_REUSE_SCORES(0);
 #undef QKV_REUSE_SCORES
@@ -722,17 +807,29 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   float* scores = reinterpret_cast<float*>(ws);
-  int32_t* sel = reinterpret_cast<int32_t*>(ws + align256(rows * history * 4));
-  void* tk_ws = ws + align256(rows * history * 4) + align256(rows * c.keep * 4);
-  const int64_t tk_bytes = workspace_bytes - align256(rows * history * 4) - align256(rows * c.keep * 4);
+  int64_t off = align256(rows * history * 4);
+  int32_t* sel = reinterpret_cast<int32_t*>(ws + off);
+  off += align256(rows * c.keep * 4);
+  void* tk_ws = ws + off;
+  const int64_t tk_bytes = align256(qkv_topk_workspace_bytes(rows, history, c.keep));
+  off += tk_bytes;
+  const bool wide = history <= kWideMax;
+  const int64_t n_tiles = cdiv(history, kScoreTile), c_ld = n_tiles * kScoreTile;
+  float* cscore = wide ? reinterpret_cast<float*>(ws + off) : nullptr;
+  int32_t* ctok = wide ? reinterpret_cast<int32_t*>(ws + off + align256(rows * c_ld * 4)) : nullptr;
+  int32_t* ccnt = wide ? reinterpret_cast<int32_t*>(ws + off + 2 * align256(rows * c_ld * 4)) : nullptr;
 
   rc = dispatch_dtype<RunReuseScores>(dtype, query, key, k_strides, batch, q_heads, kv_heads, history, head_dim,
-                                      current, previous, previous_final, mask_ld, scaling, scores, history, st);
+                                      current, previous, previous_final, mask_ld, scaling, scores, history, cscore,
+                                      ctok, ccnt, c_ld, st);
   if (rc) return rc;
-  if (history <= kWideMax) {
+  if (wide) {
+    // compacted unions of up to 1/8 of the row's width (at least 2048 entries)
     return with_wide_vpl(history, [&](auto vpl) {
-      reuse_final_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
-          scores, history, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
+      constexpr int VPL = decltype(vpl)::value;
+      reuse_final_wide_kernel<VPL, (VPL / 8 > 2 ? VPL / 8 : 2)><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          scores, history, cscore, ctok, ccnt, static_cast<int>(n_tiles), c_ld, static_cast<int>(c.keep),
+          static_cast<int>(history), static_cast<int>(key_count),
           static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
           static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
           static_cast<int>(n_out), history_final, history_final_ld);

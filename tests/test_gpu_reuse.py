@@ -116,6 +116,41 @@ def test_reuse_select_matches_oracle(dtype, b, h, t, sink, recent, frac, keep_se
     assert np.array_equal(hf.cpu().numpy(), whf)
 
 
+@pytest.mark.parametrize("t,dens,frac", [
+    (8001, (0.4, 0.3, 0.1), 0.05),      # union ~60% of the row: beyond the compacted lists, the whole row is ranked
+    (8001, (0.08, 0.0, 0.0), 0.05),     # union just above keep
+    (30001, (0.06, 0.05, 0.02), 0.02),  # the bench's proportions
+])
+def test_reuse_select_union_sizes(t, dens, frac):
+    gen = torch.Generator().manual_seed(t + int(100 * dens[0]))
+    q = torch.randn((1, 4, 128), generator=gen).to(torch.bfloat16)
+    k = torch.randn((1, 4, t, 128), generator=gen).to(torch.bfloat16)
+    hist = t - 1
+    masks = [torch.rand((1, 4, hist), generator=gen) < p for p in dens]
+    fi, fv, hf = Q.reuse_select(q.to(DEV), k.to(DEV), *(m.to(DEV) for m in masks), 3, 5, frac, True, 0.088)
+    wi, wv, whf = R.reuse_select(f32(q), f32(k), *(m.numpy() for m in masks), 3, 5, frac, True, 0.088)
+    assert np.array_equal(fi.cpu().numpy(), wi)
+    assert np.array_equal(fv.cpu().numpy(), wv)
+    assert np.array_equal(hf.cpu().numpy(), whf)
+
+
+def test_reuse_select_exact_ties():
+    # K rows repeat every 37 tokens, so union scores tie exactly: the lower
+    # token wins, whether the union is ranked compacted or over the whole row
+    gen = torch.Generator().manual_seed(12)
+    q = torch.randn((1, 2, 128), generator=gen).to(torch.bfloat16)
+    base = torch.randn((1, 2, 37, 128), generator=gen).to(torch.bfloat16)
+    t = 3701
+    k = base.repeat(1, 1, 101, 1)[:, :, :t].contiguous()
+    hist = t - 1
+    for dens in ((0.1, 0.05, 0.02), (0.7, 0.0, 0.0)):
+        masks = [torch.rand((1, 2, hist), generator=gen) < p for p in dens]
+        fi, fv, hf = Q.reuse_select(q.to(DEV), k.to(DEV), *(m.to(DEV) for m in masks), 0, 0, 0.03, False, 0.088)
+        wi, wv, whf = R.reuse_select(f32(q), f32(k), *(m.numpy() for m in masks), 0, 0, 0.03, False, 0.088)
+        assert np.array_equal(fi.cpu().numpy(), wi) and np.array_equal(fv.cpu().numpy(), wv)
+        assert np.array_equal(hf.cpu().numpy(), whf)
+
+
 @pytest.mark.parametrize("rows,n,k,ld", [(3, 1000, 50, 1000), (2, 16384, 1, 16400), (2, 16385, 819, 16385),
                                          (1, 40960, 2048, 40960), (2, 45000, 2250, 45056), (4, 7, 7, 9)])
 def test_threshold_mask_matches_oracle(rows, n, k, ld):
