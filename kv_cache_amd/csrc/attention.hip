@@ -9,21 +9,23 @@
 //
 // Work split: slot s of a row is token (block_ids[s / block] * block +
 // s % block).  A workgroup (4 waves) owns a contiguous range of slots of one
-// (sequence, KV head) row; its waves take chunks of 4*NI slots in turn
-// (chunk c of wave w is the workgroup's chunk 4c + w).  Inside a chunk, 16
-// lanes share a token: lane (16*g + c) holds channels 8c..8c+7 of the token
-// of slot 4i + g in step i, so each load instruction reads four whole
-// 256-byte K (or V) rows.  While a wave computes chunk c, the K/V loads of
-// chunk c+1 and the block ids of chunk c+2 are in flight; the chunk loop is
-// unrolled at compile time and every load is issued without a branch, so
-// each wait covers exactly the loads it needs.
+// (sequence, KV head) row; its waves take chunks of slots in turn (chunk c of
+// wave w is the workgroup's chunk 4c + w).  While a wave computes chunk c,
+// the K/V loads of chunk c+1 and the block ids of chunk c+2 are in flight;
+// the chunk loop is unrolled at compile time and every load is issued
+// without a branch, so each wait covers exactly the loads it needs.
 //
-// QK is v_dot2_f32_bf16 on the packed channel pairs followed by a 16-lane
-// DPP sum; softmax runs in the log2 domain with a running maximum per
-// 16-lane token group (no cross-group traffic inside the loop); P.V
-// accumulates in fp32.  A wave combines its four token groups with the
-// gfx950 VALU lane swaps (v_permlane16_swap / v_permlane32_swap), and a
-// workgroup combines its waves through LDS into (max, sum, weighted V) per
+// Two chunk kernels share that frame.  sparse_attn_mfma_kernel (G >= 2) runs
+// QK and P.V on the matrix cores over 16-slot chunks (its comment has the
+// operand layouts).  sparse_attn_kernel (G = 1) runs them on the VALU: 16
+// lanes share a token (lane 16g + c holds channels 8c..8c+7 of the token of
+// slot 4i + g in step i, so each load instruction reads four whole 256-byte
+// rows), QK is v_dot2_f32_bf16 on the packed channel pairs and a 16-lane DPP
+// sum, softmax runs in the log2 domain with a running maximum per 16-lane
+// token group, P.V accumulates in fp32, and a wave combines its four token
+// groups with the gfx950 lane swaps (v_permlane16_swap / v_permlane32_swap).
+//
+// A workgroup combines its waves through LDS into (max, sum, weighted V) per
 // head.  A row that fits one workgroup writes its bf16 output directly.
 // Otherwise every workgroup publishes its partial with device-coherent
 // stores (relaxed agent-scope atomic stores: global_store sc1, written
@@ -40,16 +42,29 @@
 #ifndef QKV_ATTN_TARGET_WGS
 #define QKV_ATTN_TARGET_WGS 256
 #endif
-// Workgroups per CU the register budget is sized for (4 waves each).
+// Workgroups per CU the register budget is sized for (at 4 waves each; an
+// 8-wave workgroup counts as two).
 #ifndef QKV_ATTN_WG_PER_CU
 #define QKV_ATTN_WG_PER_CU 2
+#endif
+// Waves per workgroup (4 or 8).
+#ifndef QKV_ATTN_WAVES
+#define QKV_ATTN_WAVES 4
+#endif
+// Chunks of K/V a wave holds in registers: the one it computes and
+// QKV_ATTN_DEPTH - 1 in flight.
+#ifndef QKV_ATTN_DEPTH
+#define QKV_ATTN_DEPTH 2
 #endif
 
 namespace qkv {
 namespace {
 
 constexpr int kD = 128;     // head dim
-constexpr int kNT = 256;    // threads per workgroup
+constexpr int kWaves = QKV_ATTN_WAVES;
+static_assert(kWaves == 4 || kWaves == 8, "4 or 8 waves per workgroup");
+constexpr int kDepth = QKV_ATTN_DEPTH;
+static_assert(kDepth == 2 || kDepth == 3, "2 or 3 chunks of K/V in registers");
 // Ticket words at the start of the workspace, one per possible row, so calls
 // of any shape that share a workspace find their tickets at the same place.
 constexpr int64_t kTicketWords = 65536;
@@ -115,15 +130,169 @@ __device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
 constexpr int kSelMaxVPL = 16;
 constexpr int kSelMaxBlocks = 256 * kSelMaxVPL;
 
+// Slot -> token map of one row.  Slot s < n_blk_slots is token
+// ids[s / block] * block + s % block, masked (-1) where that lies past the
+// history or inside the sink or recent range; protected slot n_blk_slots + i
+// is sink token i, then recent token rec_begin + (i - sink_end), then the
+// current token (EV:2938-2982).
+struct RowSlots {
+  const int32_t* ids;   // the row's block ids (global memory, or the LDS selection)
+  int n_blk_slots, n_slots, block, nb, tokens, sink_end, recent_start, rec_begin, n_rec, self_tok;
+
+  // Block id of `slot` for a lane that has one (ok), -2 - i for protected
+  // slot i, else -1.  The id load always happens, from a clamped index.
+  __device__ __forceinline__ int id_of(int slot, bool ok) const {
+    const bool blk = ok && slot < n_blk_slots;
+    const int v = ids[blk ? slot / block : 0];
+    return blk ? v : (ok && slot < n_slots ? n_blk_slots - 2 - slot : -1);
+  }
+  // Token of `slot` given its id_of, or -1.
+  __device__ __forceinline__ int token_of(int slot, int id) const {
+    if (id <= -2) {
+      const int i = -2 - id;
+      return i < sink_end ? i : i < sink_end + n_rec ? rec_begin + (i - sink_end) : self_tok;
+    }
+    if (id < 0 || id >= nb) return -1;
+    const int t = id * block + (slot - (slot / block) * block);
+    return (t < tokens && t >= sink_end && t < recent_start) ? t : -1;
+  }
+};
+
+// Workgroup epilogue of both attention kernels, entered by every thread once
+// red_m / red_l / red_acc hold each wave's (max, sum, weighted V) per head
+// and a barrier has passed.  A row that fits one workgroup writes its bf16
+// output; otherwise the workgroup publishes its partial, takes a ticket, and
+// the row's last workgroup merges all partials.
+template <int G, int NW>
+__device__ __forceinline__ void finish_workgroup(const float (&red_acc)[NW][G][kD], const float (&red_m)[NW][G],
+                                                 const float (&red_l)[NW][G], int& last_flag, int r, int split,
+                                                 int nsplit, uint16_t* __restrict__ out_row,
+                                                 float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+                                                 uint32_t* __restrict__ tickets) {
+  constexpr int NT = 64 * NW;
+  const int tid = threadIdx.x;
+  const float ninf = -__builtin_huge_valf();
+  // Workgroup max per head and the rescale factor of each wave.
+  float wg_m[G], wg_l[G], fs[G][NW];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float mx = red_m[0][h];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red_m[w][h]);
+    wg_m[h] = mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      fs[h][w] = (red_m[w][h] == ninf) ? 0.0f : exp2f(red_m[w][h] - mx);
+      sum = __builtin_fmaf(red_l[w][h], fs[h][w], sum);
+    }
+    wg_l[h] = sum;
+  }
+  auto wg_acc = [&](int h, int d) -> float {
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) o = __builtin_fmaf(red_acc[w][h][d], fs[h][w], o);
+    return o;
+  };
+
+  if (nsplit == 1) {
+    for (int idx = tid; idx < G * kD; idx += NT) {
+      const int h = idx / kD, d = idx - h * kD;
+      const float o = (wg_m[h] == ninf) ? 0.0f : wg_acc(h, d) / wg_l[h];
+      out_row[h * kD + d] = f32_to_bf16_rne(o);
+    }
+    return;
+  }
+
+  const int64_t part = static_cast<int64_t>(r) * nsplit + split;
+  for (int idx = tid; idx < G * kD; idx += NT) {
+    const int h = idx / kD, d = idx - h * kD;
+    st_coherent(ws_acc + part * G * kD + idx, wg_acc(h, d));
+  }
+  if (tid < G) {
+    st_coherent(ws_ml + (part * G + tid) * 2 + 0, wg_m[tid]);
+    st_coherent(ws_ml + (part * G + tid) * 2 + 1, wg_l[tid]);
+  }
+  // Every store of this workgroup has completed before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t t = __hip_atomic_fetch_add(tickets + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = t == static_cast<uint32_t>(nsplit - 1);
+    if (last) __hip_atomic_store(tickets + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = last;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+
+  // Last workgroup of the row: merge the splits.  Thread t owns outputs
+  // t + NT*k; the (max, sum, weighted V) loads of MS splits of every owned
+  // output are all issued before any arithmetic.
+  constexpr int OPT = (G * kD + NT - 1) / NT;
+  constexpr int MS = OPT >= 4 ? 4 : 16 / OPT;   // splits per batch of loads
+  float mx[OPT], den[OPT], o[OPT];
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    mx[k] = ninf;
+    den[k] = 0.0f;
+    o[k] = 0.0f;
+  }
+  const float* ml_row = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2;
+  const float* acc_row = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD;
+  for (int i0 = 0; i0 < nsplit; i0 += MS) {
+    float mi[OPT][MS], li[OPT][MS], ai[OPT][MS];
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int idx = min(tid + k * NT, G * kD - 1);
+      const int h = idx / kD;
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        const int i = min(i0 + u, nsplit - 1);
+        ai[k][u] = ld_coherent(acc_row + static_cast<int64_t>(i) * G * kD + idx);
+        mi[k][u] = ld_coherent(ml_row + (i * G + h) * 2);
+        li[k][u] = ld_coherent(ml_row + (i * G + h) * 2 + 1);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      float m2 = mx[k];
+#pragma unroll
+      for (int u = 0; u < MS; ++u)
+        if (i0 + u < nsplit) m2 = fmaxf(m2, mi[k][u]);
+      if (m2 == ninf) continue;
+      const float c = (mx[k] == ninf) ? 0.0f : exp2f(mx[k] - m2);
+      den[k] *= c;
+      o[k] *= c;
+#pragma unroll
+      for (int u = 0; u < MS; ++u) {
+        if (i0 + u < nsplit && mi[k][u] != ninf) {
+          const float w = exp2f(mi[k][u] - m2);
+          den[k] = __builtin_fmaf(li[k][u], w, den[k]);
+          o[k] = __builtin_fmaf(ai[k][u], w, o[k]);
+        }
+      }
+      mx[k] = m2;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    const int idx = tid + k * NT;
+    if (idx < G * kD) {
+      const float v = (mx[k] == ninf) ? 0.0f : o[k] / den[k];
+      out_row[idx] = f32_to_bf16_rne(v);
+    }
+  }
+}
+
 // SELV > 0: the row's block ids are not given; every workgroup of the row
 // selects the n_sel largest of its block maxima (bmax row r at bmax +
 // r*bmax_ld, lowest index wins ties, ascending) into LDS first -- the
 // selection of qkv_topk, repeated per split instead of launched separately,
-// with SELV keys per thread (rows of at most 256*SELV blocks; the selection's
+// with SELV keys per thread (rows of at most 64*NW*SELV blocks; the selection's
 // latency grows with SELV).  The row's first workgroup also writes it to
 // sel_out (when given).
-template <int G, int NI, int ITERS, int SELV>
-__global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
+template <int G, int NI, int ITERS, int SELV, int NW>
+__global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
     int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
@@ -132,54 +301,34 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     int64_t bmax_ld, int32_t* __restrict__ sel_out, int kv_div, int n_prot, int sink_end, int recent_start,
     int rec_begin, int n_rec, int self_tok) {
   constexpr int CH = 4 * NI;               // token slots per wave chunk
+  constexpr int NT = 64 * NW;              // threads per workgroup
   static_assert(CH <= 64, "one slot per lane when resolving token ids");
 
-  __shared__ float red_acc[4][G][kD];   // per wave weighted V
-  __shared__ float red_m[4][G], red_l[4][G];
+  __shared__ float red_acc[NW][G][kD];   // per wave weighted V
+  __shared__ float red_m[NW][G], red_l[NW][G];
   __shared__ int last_flag;
   constexpr bool SEL = SELV > 0;
-  __shared__ int32_t sel_lds[SEL ? 256 * SELV : 1];
+  __shared__ int32_t sel_lds[SEL ? NT * SELV : 1];
 
   const int r = blockIdx.y, split = blockIdx.x;
   const int b = r / kv_heads, j = r - b * kv_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = lane >> 4, cc = lane & 15;
   const float ninf = -__builtin_huge_valf();
-  const int n_blk_slots = n_sel * block;
-  const int n_slots = n_blk_slots + n_prot;
-  const int32_t* ids = block_ids + static_cast<int64_t>(r) * n_sel;
   if constexpr (SEL) {
-    select_row<SEL ? SELV : 1, false>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
+    select_row<SEL ? SELV : 1, false, NW>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
     if (sel_out && split == 0)
-      for (int i = tid; i < n_sel; i += kNT) sel_out[static_cast<int64_t>(r) * n_sel + i] = sel_lds[i];
+      for (int i = tid; i < n_sel; i += NT) sel_out[static_cast<int64_t>(r) * n_sel + i] = sel_lds[i];
   }
+  const int n_blk_slots = n_sel * block;
+  const RowSlots rs{SEL ? sel_lds : block_ids + static_cast<int64_t>(r) * n_sel, n_blk_slots, n_blk_slots + n_prot,
+                    block, nb, tokens, sink_end, recent_start, rec_begin, n_rec, self_tok};
 
   // Slot of this lane in chunk c (meaningful for lane < CH).
-  const int wg_base = split * (4 * CH * ITERS);
-  auto slot_of = [&](int c) -> int { return wg_base + (4 * c + wave) * CH + lane; };
-  // Block id of the lane's slot; lanes past CH and slots past the end get -1
-  // (the load itself always happens, from a clamped index).  Slot
-  // n_blk_slots + i (a protected token) gets -2 - i.
-  auto load_id = [&](int c) -> int {
-    const int slot = slot_of(c);
-    const bool ok = lane < CH && slot < n_blk_slots;
-    const int v = SEL ? sel_lds[ok ? slot / block : 0] : ids[ok ? slot / block : 0];
-    return ok ? v : (lane < CH && slot < n_slots ? n_blk_slots - 2 - slot : -1);
-  };
-  // Token of the lane's slot from its block id, or -1.  Protected slots are
-  // the sink range, the recent range and the current token, in that order;
-  // block slots inside the sink or recent range are masked, so no token is
-  // attended twice.
-  auto token_of = [&](int c, int id) -> int {
-    if (id <= -2) {
-      const int i = -2 - id;
-      return i < sink_end ? i : i < sink_end + n_rec ? rec_begin + (i - sink_end) : self_tok;
-    }
-    if (id < 0 || id >= nb) return -1;
-    const int slot = slot_of(c);
-    const int t = id * block + (slot - (slot / block) * block);
-    return (t < tokens && t >= sink_end && t < recent_start) ? t : -1;
-  };
+  const int wg_base = split * (NW * CH * ITERS);
+  auto slot_of = [&](int c) -> int { return wg_base + (NW * c + wave) * CH + lane; };
+  auto load_id = [&](int c) -> int { return rs.id_of(slot_of(c), lane < CH); };
+  auto token_of = [&](int c, int id) -> int { return rs.token_of(slot_of(c), id); };
   // Token of slot 4i + grp (the lane's token in step i), from lane 4i + grp.
   auto spread = [&](int my_tok, int (&tk)[NI]) {
 #pragma unroll
@@ -357,32 +506,46 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
     }
   };
 
-  // Chunk pipeline: ids(c+2) and K/V(c+1) in flight while chunk c computes.
-  uint4 kx[2][NI], vx[2][NI];
-  int tk[2][NI];
+  // Chunk pipeline: K/V of chunks c+1 .. c+P and the ids of chunk c+P+1 in
+  // flight while chunk c computes (P = kDepth - 1).
+  constexpr int P = kDepth - 1;
+  uint4 kx[kDepth][NI], vx[kDepth][NI];
+  int tk[kDepth][NI];
   int id_next = -1;
   {
-    const int id0 = load_id(0);
-    if (ITERS > 1) id_next = load_id(1);
-    spread(token_of(0, id0), tk[0]);
-    load_kv(tk[0], kx[0], vx[0]);
-  }
-  // Chunk c+1's loads go out only after chunk c-1 is computed (zero_after on
-  // its state), so at most two chunks of K/V occupy registers; the
-  // scheduling barriers keep them ahead of chunk c's arithmetic.
+    int id = load_id(0);
 #pragma unroll
-  for (int c = 0; c < ITERS; ++c) {
-    const int cur = c & 1, nxt = cur ^ 1;
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < ITERS) {
-      const int dz = c > 0 ? zero_after(kScatter ? l_own : l[0]) : 0;
-      const int tn = token_of(c + 1, id_next + dz);
-      if (c + 2 < ITERS) id_next = load_id(c + 2 + dz);
-      spread(tn, tk[nxt]);
-      load_kv(tk[nxt], kx[nxt], vx[nxt]);
+    for (int c = 0; c < P && c < ITERS; ++c) {
+      const int idn = c + 1 < ITERS ? load_id(c + 1) : -1;
+      spread(token_of(c, id), tk[c]);
+      load_kv(tk[c], kx[c], vx[c]);
+      id = idn;
     }
-    __builtin_amdgcn_sched_barrier(0);
-    compute(tk[cur], kx[cur], vx[cur]);
+    id_next = id;
+  }
+  // Chunk c+P's loads go out only after chunk c-1 is computed (zero_after on
+  // its state), so at most kDepth chunks of K/V occupy registers; the
+  // scheduling barriers keep them ahead of chunk c's arithmetic.
+  // (Register buffer u holds chunks u, u + kDepth, ...: the inner loop keeps
+  // every buffer index a constant even where the outer one stays a loop.)
+#pragma unroll
+  for (int c0 = 0; c0 < ITERS; c0 += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      const int c = c0 + u;
+      if (c >= ITERS) break;
+      const int nxt = (u + P) % kDepth;
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + P < ITERS) {
+        const int dz = c > 0 ? zero_after(kScatter ? l_own : l[0]) : 0;
+        const int tn = token_of(c + P, id_next + dz);
+        if (c + P + 1 < ITERS) id_next = load_id(c + P + 1 + dz);
+        spread(tn, tk[nxt]);
+        load_kv(tk[nxt], kx[nxt], vx[nxt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(tk[u], kx[u], vx[u]);
+    }
   }
 
   if constexpr (kScatter) {
@@ -418,134 +581,259 @@ __global__ __launch_bounds__(kNT, QKV_ATTN_WG_PER_CU) void sparse_attn_kernel(
   }
   __syncthreads();
 
-  // Workgroup max per head and the rescale factor of each wave.
-  float wg_m[G], wg_l[G], fs[G][4];
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float mx = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
-    wg_m[h] = mx;
-    float sum = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      fs[h][w] = (red_m[w][h] == ninf) ? 0.0f : exp2f(red_m[w][h] - mx);
-      sum = __builtin_fmaf(red_l[w][h], fs[h][w], sum);
-    }
-    wg_l[h] = sum;
+  finish_workgroup<G, NW>(red_acc, red_m, red_l, last_flag, r, split, nsplit,
+                          out + (static_cast<int64_t>(b) * q_heads + j * G) * kD, ws_acc, ws_ml, tickets);
+}
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x4_t ld_nt4(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+
+// Lazy rescaling in the MFMA kernel: the maximum a wave exponentiates against
+// is raised only when some head's chunk maximum exceeds it by more than this
+// (log2 units).  P then stays below 2^8, and the accumulators are rescaled on
+// the few chunks that raise it instead of on every chunk; O / l is unchanged.
+constexpr float kLazyLog2 = 8.0f;
+// A wave's V tile in LDS, channel-major: 16 slots (32 bytes) per channel plus
+// 4 bytes of padding, so the transposing 16-bit stores and the 8-byte reads
+// of one instruction spread over the banks.
+constexpr int kVtStride = 18;   // uint16 per channel
+
+// Sparse attention on the matrix cores, any G <= 16.  Work split, selection,
+// protected slots and the workgroup epilogue are those of sparse_attn_kernel;
+// a wave's chunk is 16 slots.
+//   QK: S^T[slot][head] = sum_k K[slot][k] Q[head][k], four
+//   v_mfma_f32_16x16x32_bf16 over k = 32s..32s+31 with A = K (lane 16g+c
+//   reads 16 bytes of slot c's row: channels 32s+8g..32s+8g+7) and B = Q^T
+//   (heads past G are zero columns).  Lane 16g+c then holds head c for slots
+//   4g..4g+3.
+//   P.V: O[head][ch] += sum_slot P[head][slot] V[slot][ch], eight
+//   v_mfma_f32_16x16x16_bf16 of 16 channels each.  P (rounded to bf16, as the
+//   reference's bf16 attention does) is already in the A layout; V is loaded
+//   as in sparse_attn_kernel (lane 16g+c: slot 4i+g, channels 8c..8c+7),
+//   stored channel-major into the wave's LDS tile, and read back as B, four
+//   slots of one channel per lane.
+// Softmax is per head over the lanes of its column (in-lane over 4 slots, then
+// the lane swaps), in the log2 domain with lazy rescaling.
+template <int G, int ITERS, int SELV>
+__global__ __launch_bounds__(256, QKV_ATTN_WG_PER_CU) void sparse_attn_mfma_kernel(
+    const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
+    const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
+    int kv_heads, int tokens, const int32_t* __restrict__ block_ids, int n_sel, int block,
+    int nb, float scale_log2, int nsplit, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    uint32_t* __restrict__ tickets, uint16_t* __restrict__ out, const float* __restrict__ bmax,
+    int64_t bmax_ld, int32_t* __restrict__ sel_out, int kv_div, int n_prot, int sink_end, int recent_start,
+    int rec_begin, int n_rec, int self_tok) {
+  constexpr int NW = 4, NT = 256, CH = 16;
+  static_assert(G <= 16, "the heads are the 16 columns of the QK tile");
+
+  __shared__ float red_acc[NW][G][kD];
+  __shared__ float red_m[NW][G], red_l[NW][G];
+  __shared__ int last_flag;
+  constexpr bool SEL = SELV > 0;
+  __shared__ int32_t sel_lds[SEL ? NT * SELV : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[NW][kD * kVtStride];
+
+  const int r = blockIdx.y, split = blockIdx.x;
+  const int b = r / kv_heads, j = r - b * kv_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, c16 = lane & 15;
+  const float ninf = -__builtin_huge_valf();
+  if constexpr (SEL) {
+    select_row<SEL ? SELV : 1, false, NW>(bmax + static_cast<int64_t>(r) * bmax_ld, nb, n_sel, sel_lds);
+    if (sel_out && split == 0)
+      for (int i = tid; i < n_sel; i += NT) sel_out[static_cast<int64_t>(r) * n_sel + i] = sel_lds[i];
   }
-  auto wg_acc = [&](int h, int d) -> float {
-    float o = 0.0f;
+  const int n_blk_slots = n_sel * block;
+  const RowSlots rs{SEL ? sel_lds : block_ids + static_cast<int64_t>(r) * n_sel, n_blk_slots, n_blk_slots + n_prot,
+                    block, nb, tokens, sink_end, recent_start, rec_begin, n_rec, self_tok};
+  const int wg_base = split * (NW * CH * ITERS);
+  auto slot_of = [&](int c) -> int { return wg_base + (NW * c + wave) * CH + lane; };
+  auto load_id = [&](int c) -> int { return rs.id_of(slot_of(c), lane < CH); };
+  auto token_of = [&](int c, int id) -> int { return rs.token_of(slot_of(c), id); };
+
+  const int jk = j / kv_div;   // the K/V head this row reads
+  const uint16_t* kb = key + b * sb + jk * sh + 8 * g4;
+  const uint16_t* vb = value + b * sb + jk * sh + 8 * c16;
+
+  bf16x8_t qb[4];   // B operand of QK: Q[head c16][32s + 8g4 ..], zero for heads >= G
+  {
+    const uint16_t* qrow = query + (static_cast<int64_t>(b) * q_heads + j * G + min(c16, G - 1)) * kD + 8 * g4;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) o = __builtin_fmaf(red_acc[w][h][d], fs[h][w], o);
-    return o;
+    for (int s = 0; s < 4; ++s) {
+      u32x4_t w = *reinterpret_cast<const u32x4_t*>(qrow + 32 * s);
+      if (c16 >= G) w = u32x4_t{0u, 0u, 0u, 0u};
+      qb[s] = __builtin_bit_cast(bf16x8_t, w);
+    }
+  }
+
+  // Loads of one chunk from the tokens its 16 lanes resolved (-1 elsewhere):
+  // K rows of slot c16, V rows of slot 4i + g4 (invalid slots read token 0 of
+  // the row and are masked), and the chunk's valid-slot mask.
+  auto gather = [&](int my_tok, u32x4_t (&kx)[4], u32x4_t (&vx)[4], uint32_t& vm) {
+    const int ta = __builtin_amdgcn_ds_bpermute(c16 << 2, my_tok);
+    vm = static_cast<uint32_t>(__ballot(my_tok >= 0));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kx[s] = ld_nt4(kb + static_cast<int64_t>(max(ta, 0)) * st + 32 * s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tv = __builtin_amdgcn_ds_bpermute((4 * i + g4) << 2, my_tok);
+      vx[i] = ld_nt4(vb + static_cast<int64_t>(max(tv, 0)) * st);
+    }
   };
 
-  if (nsplit == 1) {
-    for (int idx = tid; idx < G * kD; idx += kNT) {
-      const int h = idx / kD, d = idx - h * kD;
-      const float o = (wg_m[h] == ninf) ? 0.0f : wg_acc(h, d) / wg_l[h];
-      out[(static_cast<int64_t>(b) * q_heads + j * G + h) * kD + d] = f32_to_bf16_rne(o);
-    }
-    return;
-  }
+  f32x4_t o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = ninf, lsum = 0.0f;   // head c16: running maximum (log2) and this lane's share of the sum
+  uint16_t* vtw = vt[wave];
+  const uint32_t* vt32 = reinterpret_cast<const uint32_t*>(vt[wave]);
 
-  const int64_t part = static_cast<int64_t>(r) * nsplit + split;
-  for (int idx = tid; idx < G * kD; idx += kNT) {
-    const int h = idx / kD, d = idx - h * kD;
-    st_coherent(ws_acc + part * G * kD + idx, wg_acc(h, d));
-  }
-  if (tid < G) {
-    st_coherent(ws_ml + (part * G + tid) * 2 + 0, wg_m[tid]);
-    st_coherent(ws_ml + (part * G + tid) * 2 + 1, wg_l[tid]);
-  }
-  // Every store of this workgroup has completed before the ticket is taken.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t t = __hip_atomic_fetch_add(tickets + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = t == static_cast<uint32_t>(nsplit - 1);
-    if (last) __hip_atomic_store(tickets + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = last;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-
-  // Last workgroup of the row: merge the splits.  Thread t owns outputs
-  // t + 256k; the (max, sum, weighted V) loads of MS splits of every owned
-  // output are all issued before any arithmetic.
-  constexpr int OPT = (G * kD + kNT - 1) / kNT;
-  constexpr int MS = OPT >= 4 ? 4 : 16 / OPT;   // splits per batch of loads
-  float mx[OPT], den[OPT], o[OPT];
+  auto compute = [&](const u32x4_t (&kx)[4], const u32x4_t (&vx)[4], uint32_t vm) {
+    // V tile, channel-major (the stores run while the QK tile computes).
 #pragma unroll
-  for (int k = 0; k < OPT; ++k) {
-    mx[k] = ninf;
-    den[k] = 0.0f;
-    o[k] = 0.0f;
-  }
-  const float* ml_row = ws_ml + static_cast<int64_t>(r) * nsplit * G * 2;
-  const float* acc_row = ws_acc + static_cast<int64_t>(r) * nsplit * G * kD;
-  for (int i0 = 0; i0 < nsplit; i0 += MS) {
-    float mi[OPT][MS], li[OPT][MS], ai[OPT][MS];
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int k = 0; k < OPT; ++k) {
-      const int idx = min(tid + k * kNT, G * kD - 1);
-      const int h = idx / kD;
-#pragma unroll
-      for (int u = 0; u < MS; ++u) {
-        const int i = min(i0 + u, nsplit - 1);
-        ai[k][u] = ld_coherent(acc_row + static_cast<int64_t>(i) * G * kD + idx);
-        mi[k][u] = ld_coherent(ml_row + (i * G + h) * 2);
-        li[k][u] = ld_coherent(ml_row + (i * G + h) * 2 + 1);
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = vx[i][e];
+        const int at = (8 * c16 + 2 * e) * kVtStride + 4 * i + g4;
+        vtw[at] = static_cast<uint16_t>(w);
+        vtw[at + kVtStride] = static_cast<uint16_t>(w >> 16);
       }
     }
+    f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < OPT; ++k) {
-      float m2 = mx[k];
+    for (int s = 0; s < 4; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kx[s]), qb[s], sacc, 0, 0, 0);
+    float sv[4], cm = ninf;
 #pragma unroll
-      for (int u = 0; u < MS; ++u)
-        if (i0 + u < nsplit) m2 = fmaxf(m2, mi[k][u]);
-      if (m2 == ninf) continue;
-      const float c = (mx[k] == ninf) ? 0.0f : exp2f(mx[k] - m2);
-      den[k] *= c;
-      o[k] *= c;
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = ((vm >> (4 * g4 + i)) & 1u) ? sacc[i] * scale_log2 : ninf;
+      cm = fmaxf(cm, sv[i]);
+    }
+    cm = max_x32(max_x16(cm));   // the chunk maximum of head c16, in all four of its lanes
+    const float mn = fmaxf(m, cm);
+    if (__ballot(c16 < G && mn > m + kLazyLog2)) {   // wave-uniform
+      const float al = (mn == ninf) ? 1.0f : exp2f(m - mn);   // 0 while m = -inf
+      lsum *= al;
 #pragma unroll
-      for (int u = 0; u < MS; ++u) {
-        if (i0 + u < nsplit && mi[k][u] != ninf) {
-          const float w = exp2f(mi[k][u] - m2);
-          den[k] = __builtin_fmaf(li[k][u], w, den[k]);
-          o[k] = __builtin_fmaf(ai[k][u], w, o[k]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        // accumulator row i of this lane is head 4*g4 + i, whose factor lane 4*g4 + i holds
+        const float a = __int_as_float(__builtin_amdgcn_ds_bpermute((4 * g4 + i) << 2, __float_as_int(al)));
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q][i] *= a;
       }
-      mx[k] = m2;
+      m = mn;
     }
+    const float ms = (m == ninf) ? 0.0f : m;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = exp2f(sv[i] - ms);   // 0 for masked slots
+      lsum += p[i];
+    }
+    const s16x4_t pa = __builtin_bit_cast(s16x4_t, bf16x4_t{static_cast<__bf16>(p[0]), static_cast<__bf16>(p[1]),
+                                                           static_cast<__bf16>(p[2]), static_cast<__bf16>(p[3])});
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int at = ((16 * q + c16) * kVtStride + 4 * g4) >> 1;
+      const u32x2_t w = {vt32[at], vt32[at + 1]};
+      o[q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(s16x4_t, w), o[q], 0, 0, 0);
+    }
+    pin(lsum);
+  };
+
+  // Chunk pipeline as in sparse_attn_kernel.
+  constexpr int P = kDepth - 1;
+  u32x4_t kx[kDepth][4], vx[kDepth][4];
+  uint32_t vm[kDepth];
+  int id_next = -1;
+  {
+    int id = load_id(0);
+#pragma unroll
+    for (int c = 0; c < P && c < ITERS; ++c) {
+      const int idn = c + 1 < ITERS ? load_id(c + 1) : -1;
+      gather(token_of(c, id), kx[c], vx[c], vm[c]);
+      id = idn;
+    }
+    id_next = id;
   }
 #pragma unroll
-  for (int k = 0; k < OPT; ++k) {
-    const int idx = tid + k * kNT;
-    if (idx < G * kD) {
-      const float v = (mx[k] == ninf) ? 0.0f : o[k] / den[k];
-      out[(static_cast<int64_t>(b) * q_heads + j * G) * kD + idx] = f32_to_bf16_rne(v);
+  for (int c0 = 0; c0 < ITERS; c0 += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      const int c = c0 + u;
+      if (c >= ITERS) break;
+      const int nxt = (u + P) % kDepth;
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + P < ITERS) {
+        const int dz = c > 0 ? zero_after(lsum) : 0;
+        const int tn = token_of(c + P, id_next + dz);
+        if (c + P + 1 < ITERS) id_next = load_id(c + P + 1 + dz);
+        gather(tn, kx[nxt], vx[nxt], vm[nxt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(kx[u], vx[u], vm[u]);
     }
   }
+
+  // The four lanes of a head hold the same maximum; their sums add up.
+  const float lw = sum_x32(sum_x16(lsum));
+  if (lane < G) {
+    red_m[wave][lane] = m;
+    red_l[wave][lane] = lw;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = 4 * g4 + i;
+    if (h < G) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) red_acc[wave][h][16 * q + c16] = o[q][i];
+    }
+  }
+  __syncthreads();
+  finish_workgroup<G, NW>(red_acc, red_m, red_l, last_flag, r, split, nsplit,
+                          out + (static_cast<int64_t>(b) * q_heads + j * G) * kD, ws_acc, ws_ml, tickets);
 }
 
 // 4-token steps per wave chunk: 8 while the G heads' state leaves room for
 // two chunks of K/V in registers, 4 above that.
 constexpr int ni_for(int64_t g) { return g <= 2 ? 8 : 4; }
 
+// Group sizes from QKV_ATTN_MFMA_MIN_G up run sparse_attn_mfma_kernel.
+// Measured with 256 selected blocks of 16 on 256 rows (cfg3's bytes), random
+// block ids: VALU kernel G = 1 / 2 / 4 / 8: 91.2 / 95.8 / 101.0 / 199.3 us;
+// MFMA kernel 94.8 / 95.4 / 97.0 / 100.0 us.  G = 1 keeps the VALU kernel,
+// whose QK and P.V are a few instructions per token there.
+#ifndef QKV_ATTN_MFMA_MIN_G
+#define QKV_ATTN_MFMA_MIN_G 2
+#endif
+constexpr bool mfma_for(int64_t g) { return g >= QKV_ATTN_MFMA_MIN_G; }
+
+// Slots a workgroup covers per chunk round.
+constexpr int64_t per_iter_for(int64_t g) { return mfma_for(g) ? 4 * 16 : kWaves * 4 * ni_for(g); }
+
 // Chunks per wave: doubled (up to max_iters_for) while the grid keeps
 // QKV_ATTN_TARGET_WGS workgroups, so long selections take few splits per
 // row.  Measured at cfg2 (64 rows x 2048 slots): 256 workgroups of 4 chunks
 // per wave 18.0 us, 1024 workgroups of 1 chunk 20.4 us, 128 of 8 22.2 us.
-// G = 8 stops at 8 chunks: its 16-chunk variant does not fit the registers.
-// G = 4 goes on to 32: at cfg3 (256 rows x 4096 slots) 512 workgroups of 32
-// chunks, all resident at two per CU, take 101.4 us against 106.0 us for
-// 1024 workgroups of 16 chunks in two rounds.
-constexpr int max_iters_for(int64_t g) { return g >= 8 ? 8 : g == 4 ? 32 : 16; }
+// VALU kernel: G = 8 stops at 8 chunks (its 16-chunk variant does not fit
+// the registers); G = 4 goes on to 32: at cfg3 (256 rows x 4096 slots) 512
+// workgroups of 32 chunks, all resident at two per CU, take 101.4 us against
+// 106.0 us for 1024 workgroups of 16 chunks in two rounds.  The MFMA kernel's
+// 16-slot chunks go to 32 for every G.
+constexpr int max_iters_for(int64_t g) { return mfma_for(g) ? 32 : g >= 8 ? 8 : g == 4 ? 32 : 16; }
 
 // Doubling stops once one workgroup covers the whole row: further chunks
 // would only walk empty slots.
 int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
-  const int64_t per_iter = 4 * 4 * ni_for(g);   // slots per workgroup per chunk round
+  const int64_t per_iter = per_iter_for(g);
   int it = 1;
   while (it < max_iters_for(g) && per_iter * it < n_slots &&
          rows * cdiv(n_slots, per_iter * it * 2) >= QKV_ATTN_TARGET_WGS)
@@ -554,7 +842,61 @@ int iters_for(int64_t rows, int64_t n_slots, int64_t g) {
 }
 
 int64_t splits_for(int64_t rows, int64_t n_slots, int64_t g) {
-  return cdiv(n_slots, 4 * 4 * ni_for(g) * iters_for(rows, n_slots, g));
+  return cdiv(n_slots, per_iter_for(g) * iters_for(rows, n_slots, g));
+}
+
+// Arguments of both attention kernels.
+struct AttnArgs {
+  const uint16_t *q, *k, *v;
+  int64_t sb, sh, st;
+  int q_heads, kv_heads, tokens;
+  const int32_t* block_ids;
+  int n_sel, block, nb;
+  float scale_log2;
+  int nsplit;
+  float *ws_acc, *ws_ml;
+  uint32_t* tickets;
+  uint16_t* out;
+  const float* bmax;
+  int64_t bmax_ld;
+  int32_t* sel_out;
+  int kv_div, n_prot, sink_end, recent_start, rec_begin, n_rec, self_tok;
+};
+
+template <int GG, int IT, int SS>
+void launch_attn(dim3 grid, hipStream_t st, const AttnArgs& a) {
+#define QKV_ATTN_ARGS                                                                                          \
+  a.q, a.k, a.v, a.sb, a.sh, a.st, a.q_heads, a.kv_heads, a.tokens, a.block_ids, a.n_sel, a.block, a.nb,    \
+      a.scale_log2, a.nsplit, a.ws_acc, a.ws_ml, a.tickets, a.out, a.bmax, a.bmax_ld, a.sel_out, a.kv_div,   \
+      a.n_prot, a.sink_end, a.recent_start, a.rec_begin, a.n_rec, a.self_tok
+  if constexpr (mfma_for(GG))
+    sparse_attn_mfma_kernel<GG, IT, SS><<<grid, 256, 0, st>>>(QKV_ATTN_ARGS);
+  else
+    sparse_attn_kernel<GG, ni_for(GG), IT, SS, kWaves><<<grid, 64 * kWaves, 0, st>>>(QKV_ATTN_ARGS);
+#undef QKV_ATTN_ARGS
+}
+
+// The selection's keys per thread: 8 (at 4 waves) for rows of <= 2048
+// blocks, 16 above.
+template <int GG, int IT>
+void launch_attn_sel(dim3 grid, hipStream_t st, const AttnArgs& a, bool sel) {
+  constexpr int W = mfma_for(GG) ? 4 : kWaves;
+  if (!sel) launch_attn<GG, IT, 0>(grid, st, a);
+  else if (a.nb <= 2048) launch_attn<GG, IT, 32 / W>(grid, st, a);
+  else launch_attn<GG, IT, 64 / W>(grid, st, a);
+}
+
+template <int GG>
+void launch_attn_g(int iters, dim3 grid, hipStream_t st, const AttnArgs& a, bool sel) {
+  constexpr int MAXI = max_iters_for(GG);
+  switch (iters) {
+    case 1: launch_attn_sel<GG, 1>(grid, st, a, sel); break;
+    case 2: launch_attn_sel<GG, 2>(grid, st, a, sel); break;
+    case 4: launch_attn_sel<GG, 4>(grid, st, a, sel); break;
+    case 8: launch_attn_sel<GG, 8>(grid, st, a, sel); break;
+    case 16: if constexpr (MAXI >= 16) launch_attn_sel<GG, 16>(grid, st, a, sel); break;
+    default: if constexpr (MAXI >= 32) launch_attn_sel<GG, 32>(grid, st, a, sel); break;
+  }
 }
 
 }  // namespace
@@ -576,7 +918,7 @@ QKV_EXPORT int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q
   // at the cap it grows with the slots.  The larger of that bound and this
   // size's own count covers every call with fewer slots, so one workspace
   // serves all smaller selections.
-  const int64_t below_cap = std::min(cdiv(n_slots, 4 * 4 * ni_for(g)),
+  const int64_t below_cap = std::min(cdiv(n_slots, per_iter_for(g)),
                                      2 * (cdiv(QKV_ATTN_TARGET_WGS, rows) - 1));
   const int64_t splits = std::max(splits_for(rows, n_slots, g), below_cap);
   // tickets, then per split: weighted V per head, then (max, sum) per head
@@ -646,37 +988,18 @@ int launch_attention(const char* what, const void* query, const void* key, const
   const uint16_t* k = static_cast<const uint16_t*>(key);
   const uint16_t* v = static_cast<const uint16_t*>(value);
   uint16_t* o = static_cast<uint16_t*>(out);
-#define QKV_ATTN_S(GG, IT, SS)                                                                              \
-  sparse_attn_kernel<GG, ni_for(GG), IT, SS><<<grid, kNT, 0, st>>>(                                         \
-      q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),                      \
-      static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),             \
-      static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o, bmax,   \
-      bmax_ld, sel_out, kv_div, static_cast<int>(n_prot), static_cast<int>(sink_end),                       \
-      static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec),                 \
-      static_cast<int>(tokens))
-#define QKV_ATTN(GG, IT)                  \
-  if (!sel) QKV_ATTN_S(GG, IT, 0);        \
-  else if (nb <= 2048) QKV_ATTN_S(GG, IT, 8); \
-  else QKV_ATTN_S(GG, IT, 16);
-#define QKV_ATTN_16(GG) case 16: QKV_ATTN(GG, 16); break;
-#define QKV_ATTN_G(GG, LONG)            \
-  switch (iters) {                      \
-    case 1: QKV_ATTN(GG, 1); break;     \
-    case 2: QKV_ATTN(GG, 2); break;     \
-    case 4: QKV_ATTN(GG, 4); break;     \
-    LONG                                \
-    default: QKV_ATTN(GG, 8); break;    \
-  }
+  const AttnArgs a{q, k, v, kv_strides[0], kv_strides[1], kv_strides[2], static_cast<int>(q_heads),
+                   static_cast<int>(kv_heads), static_cast<int>(tokens), block_ids, static_cast<int>(n_sel),
+                   static_cast<int>(block), nb, scale_log2, static_cast<int>(nsplit), ws_acc, ws_ml, tickets, o,
+                   bmax, bmax_ld, sel_out, kv_div, static_cast<int>(n_prot), static_cast<int>(sink_end),
+                   static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec),
+                   static_cast<int>(tokens)};
   switch (g) {
-    case 1: QKV_ATTN_G(1, QKV_ATTN_16(1)); break;
-    case 2: QKV_ATTN_G(2, QKV_ATTN_16(2)); break;
-    case 4: QKV_ATTN_G(4, QKV_ATTN_16(4) case 32: QKV_ATTN(4, 32); break;); break;
-    default: QKV_ATTN_G(8, ); break;
+    case 1: launch_attn_g<1>(iters, grid, st, a, sel); break;
+    case 2: launch_attn_g<2>(iters, grid, st, a, sel); break;
+    case 4: launch_attn_g<4>(iters, grid, st, a, sel); break;
+    default: launch_attn_g<8>(iters, grid, st, a, sel); break;
   }
-#undef QKV_ATTN_G
-#undef QKV_ATTN_16
-#undef QKV_ATTN
-#undef QKV_ATTN_S
   return check_launch(what);
 }
 

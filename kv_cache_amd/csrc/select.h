@@ -1,4 +1,4 @@
-// Exact top-k selection of one row inside a 256-thread workgroup, shared by
+// Exact top-k selection of one row inside one workgroup, shared by
 // the top-k kernels and the fused selection in sparse attention.  Keys map to
 // order-preserving uint32 (-0 folded onto +0); the k largest are kept, ties to
 // the lower position.
@@ -70,7 +70,7 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
   return x;
 }
 
-// Rows of at most 256*VPL keys: one workgroup of 4 waves per row.  Thread t
+// Rows of at most 64*NW*VPL keys: one workgroup of NW waves per row.  Thread t
 // holds the VPL consecutive keys from t*VPL as order-preserving uint32
 // (16-byte loads where the row allows), loaded without branches so that
 // every load is in flight at once.  The bits shared by the
@@ -91,17 +91,20 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
 // either (0: none excluded), and kk counts only the others.  lane_max_out,
 // when given, receives the largest selectable key of this thread (0: none).
 //
-// select_row runs the selection for one row inside a 256-thread workgroup:
-// it writes the positions of the kk selected keys, ascending, to sel (LDS,
-// 256*VPL entries) and returns kk (k, or with FINITE or a floor possibly
-// fewer).  Every thread of the workgroup must call it; it ends with a barrier.
-template <int VPL, bool FINITE>
+// select_row runs the selection for one row inside a workgroup of NW waves
+// (64*NW threads): it writes the positions of the kk selected keys,
+// ascending, to sel (LDS, 64*NW*VPL entries) and returns kk (k, or with
+// FINITE or a floor possibly fewer).  Every thread of the workgroup must
+// call it; it ends with a barrier.
+template <int VPL, bool FINITE, int NW = 4>
 __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
                           uint32_t* lane_max_out = nullptr) {
   static_assert(VPL <= 32, "one mask bit per key of a thread");
-  __shared__ __attribute__((aligned(16))) int hist[4][260];   // one copy per wave, padded across banks
-  __shared__ int wave_cnt[4][2];
-  __shared__ uint32_t red[4][4];
+  static_assert(NW >= 4 && NW <= 16, "4 to 16 waves");
+  constexpr int NT = 64 * NW;
+  __shared__ __attribute__((aligned(16))) int hist[NW][260];   // one copy per wave, padded across banks
+  __shared__ int wave_cnt[NW][2];
+  __shared__ uint32_t red[NW][4];
   __shared__ int sh_bin, sh_kr, sh_whole;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,7 +112,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   uint32_t u[VPL];
   bool valid[VPL];
   const int first = tid * VPL;
-  if (VPL % 4 == 0 && n == 256 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // uniform
+  if (VPL % 4 == 0 && n == NT * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // uniform
 #pragma unroll
     for (int i = 0; i < VPL; i += 4) {
       const uint4 w = *reinterpret_cast<const uint4*>(vals + first + i);
@@ -127,8 +130,10 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     u[i] = f32_sortable(__uint_as_float(u[i]));
     valid[i] = first + i < n && (!FINITE || u[i] != kNegInfKey) && u[i] >= floor;
   }
+  if (tid < 256) {
 #pragma unroll
-  for (int w = 0; w < 4; ++w) hist[w][tid] = 0;
+    for (int w = 0; w < NW; ++w) hist[w][tid] = 0;
+  }
   uint32_t umax = 0, umin = 0xFFFFFFFFu;
   int nval = 0;
 #pragma unroll
@@ -141,10 +146,10 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   if (lane_max_out) *lane_max_out = lane_max;
   umax = wave_minmax_u32<true>(umax);
   umin = wave_minmax_u32<false>(umin);
-  // A lower bound of the k-th largest key: when j = ceil(k/4) lanes of every
+  // A lower bound of the k-th largest key: when j = ceil(k/NW) lanes of every
   // wave hold a key >= x_w, at least k keys are >= min_w x_w.  Keys under the
   // bound cannot be selected and stay out of the histograms.
-  const uint32_t lbound = wave_lower_bound(lane_max, (k + 3) / 4, umax, umin);
+  const uint32_t lbound = wave_lower_bound(lane_max, (k + NW - 1) / NW, umax, umin);
   if (lane == 0) {
     red[wave][0] = umax;
     red[wave][1] = umin;
@@ -152,11 +157,19 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
     red[wave][3] = lbound;
   }
   __syncthreads();
-  umax = max(max(red[0][0], red[1][0]), max(red[2][0], red[3][0]));
-  umin = min(min(red[0][1], red[1][1]), min(red[2][1], red[3][1]));
-  nval = red[0][2] + red[1][2] + red[2][2] + red[3][2];
+  uint32_t lb_min = red[0][3];
+  umax = red[0][0];
+  umin = red[0][1];
+  nval = red[0][2];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    umax = max(umax, red[w][0]);
+    umin = min(umin, red[w][1]);
+    nval += red[w][2];
+    lb_min = min(lb_min, red[w][3]);
+  }
   const int kk = min(k, nval);   // keys selected; k unless FINITE drops some
-  const uint32_t lo = max(umin, min(min(red[0][3], red[1][3]), min(red[2][3], red[3][3])));
+  const uint32_t lo = max(umin, lb_min);
 
   // Radix select over the bits below the common prefix of umax and lo.
   int kr = kk;
@@ -189,7 +202,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
       const int b0 = 252 - 4 * lane;
       int4 h = *reinterpret_cast<const int4*>(&hist[0][b0]);
 #pragma unroll
-      for (int w = 1; w < 4; ++w) {
+      for (int w = 1; w < NW; ++w) {
         const int4 x = *reinterpret_cast<const int4*>(&hist[w][b0]);
         h.x += x.x;
         h.y += x.y;
@@ -197,7 +210,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
         h.w += x.w;
       }
 #pragma unroll
-      for (int w = 0; w < 4; ++w) *reinterpret_cast<int4*>(&hist[w][b0]) = int4{0, 0, 0, 0};
+      for (int w = 0; w < NW; ++w) *reinterpret_cast<int4*>(&hist[w][b0]) = int4{0, 0, 0, 0};
       const int c[4] = {h.w, h.z, h.y, h.x};   // bins 255-4l, 254-4l, 253-4l, 252-4l
       const int tot = c[0] + c[1] + c[2] + c[3];
       int above = wave_incl_scan_dpp(tot) - tot;
@@ -243,7 +256,7 @@ __device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t*
   __syncthreads();
   int gt_before = ig - cg, eq_before = ie - ce;
 #pragma unroll
-  for (int w = 0; w < 3; ++w) {
+  for (int w = 0; w < NW - 1; ++w) {
     gt_before += w < wave ? wave_cnt[w][0] : 0;
     eq_before += w < wave ? wave_cnt[w][1] : 0;
   }

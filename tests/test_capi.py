@@ -99,11 +99,12 @@ def test_host_side_validation(call, msg):
 
 def _attn_splits(rows, n_slots, g, target=256):
     """Splits per row of qkv_sparse_attention: a workgroup round covers
-    4 waves x 4*NI slots (NI = 8 for G <= 2, else 4); chunks per wave double
-    (up to 16; 8 for G = 8, 32 for G = 4) while one workgroup does not cover
-    the row and the grid keeps at least ``target`` workgroups."""
-    per_iter = 16 * (8 if g <= 2 else 4)
-    max_iters = 8 if g >= 8 else 32 if g == 4 else 16
+    4 waves x 32 slots (G = 1, VALU kernel) or 4 waves x 16 slots (G >= 2,
+    MFMA kernel); chunks per wave double (up to 16 for G = 1, else 32) while
+    one workgroup does not cover the row and the grid keeps at least
+    ``target`` workgroups."""
+    per_iter = 128 if g == 1 else 64
+    max_iters = 16 if g == 1 else 32
     it = 1
     while it < max_iters and per_iter * it < n_slots and rows * -(-n_slots // (per_iter * it * 2)) >= target:
         it *= 2
