@@ -19,9 +19,6 @@
 #endif
 // Waves per decode-scoring workgroup (the kernel has no workgroup barrier:
 // the waves only share the workgroup's chunk of the row).
-#ifndef QKV_SCORE_LDS_PAD
-#define QKV_SCORE_LDS_PAD 0
-#endif
 #ifndef QKV_SCORE_WAVES
 #define QKV_SCORE_WAVES 4
 #endif
@@ -554,7 +551,7 @@ int launch_scores(int S, dim3 grid, hipStream_t st, const uint16_t* q, int hq, i
   switch (S) {
 #define QKV_CASE(SS)                                                                               \
   case SS:                                                                                         \
-    decode_scores_kernel<SS, DEBUG><<<grid, kScoreThreads, QKV_SCORE_LDS_PAD, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
+    decode_scores_kernel<SS, DEBUG><<<grid, kScoreThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
                                                                block, chunk, bmax, nb, isum, keys, \
                                                                qs);                                \
     break;
