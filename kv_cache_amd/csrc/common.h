@@ -183,4 +183,35 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// DPP move within rows of 16 lanes (quad_perm, row_shl/shr, row mirrors ...),
+// every row and bank enabled.
+template <int DPP>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP, 0xF, 0xF, false));
+}
+
+// Device-coherent stores and loads (relaxed agent-scope atomics: sc1, written
+// through / read past the XCD's L2), for data one workgroup hands another
+// inside a launch (the attention's split partials).
+__device__ __forceinline__ void st_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Zero that the compiler cannot see through, available only once `dep` is:
+// adding it to an address keeps a load after the code that produced `dep`.
+__device__ __forceinline__ int zero_after(float dep) {
+  int z = 0;
+  asm volatile("" : "+v"(z) : "v"(dep));
+  return z;
+}
+// Marks x as final at this point: the volatile asm statements keep their
+// order, so whatever comes after a later one cannot move above the code
+// that computed x.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
 }  // namespace qkv

@@ -17,8 +17,6 @@ constexpr int kProbeThreads = 256;
 constexpr int64_t kTile = 4096;                  // bytes per wave stage
 constexpr int64_t kWgStage = 4 * kTile;          // bytes per workgroup stage
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
