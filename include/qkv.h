@@ -175,18 +175,25 @@ int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k
              int32_t* out, void* stream);
 
 /* Bytes of workspace qkv_topk_ws needs: 0 when qkv_topk's one workgroup per
- * row is used (n <= 4096 or k > 1024), else two candidate buffers of
- * rows * (k * ceil(n/4096)) (value, index) pairs and rows * ceil(n/4096)
- * uint32 chunk bounds; -1 for bad sizes. */
+ * row is used (n <= 4096 or k > 1024); for rows of at most 64 chunks of 4096
+ * keys with ceil(n/4096) * k <= 32768, per chunk a 66-word histogram window
+ * and a list of k (value, index) pairs with its count; otherwise two
+ * candidate buffers of rows * (k * ceil(n/4096)) (value, index) pairs and
+ * rows * ceil(n/4096) uint32 chunk bounds; -1 for bad sizes. */
 int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 
 /* qkv_topk with a caller-owned workspace (16-byte aligned, contents
- * irrelevant): rows longer than 4096 keys with k <= 1024 are reduced in
- * stages, each 4096-key chunk keeping its local top-k, until the candidates
- * fit one chunk or one 1024-thread workgroup (40960); keys below a lower
- * bound of the row's k-th key, taken in the first stage, are left out after
- * it.  The result equals qkv_topk's.  Same replaced call sites as qkv_topk
- * (EV:4448 token-level top-k over long contexts). */
+ * irrelevant): rows longer than 4096 keys with k <= 1024 are split into
+ * 4096-key chunks.  Rows of at most 64 chunks with chunks * k <= 32768:
+ * every chunk histograms its keys (1/8-octave bins) around its own k-th key,
+ * the row's floor is the bin where the merged count from the top reaches k,
+ * each chunk keeps its keys at or above it (its exact top-k among them when
+ * more than k pass), and one workgroup per row selects from those lists
+ * (three launches).  Longer rows: stages in which each chunk keeps its local
+ * top-k until the candidates fit one chunk or one 1024-thread workgroup
+ * (40960), keys below a lower bound of the row's k-th key left out after the
+ * first stage.  The result equals qkv_topk's.  Same replaced call sites as
+ * qkv_topk (EV:4448 token-level top-k over long contexts). */
 int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
                 void* workspace, int64_t workspace_bytes, void* stream);
 

@@ -359,6 +359,303 @@ __global__ __launch_bounds__(1024) void topk_wide_final_kernel(const float* __re
   for (int o = kk + static_cast<int>(threadIdx.x); o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
 }
 
+// ---------------------------------------------------------------------------
+// Histogram-and-filter top-k for long rows of at most kFilterMaxChunks chunks
+// of kStageChunk keys whose candidate lists fit one WideSelect (chunks * k <=
+// kFilterMaxLists): three light launches instead of exact per-chunk
+// selections.
+//  1. topk_hist_kernel: each chunk histograms its keys over the top
+//     kHistBits bits of the order-preserving key (sign, exponent, 3 mantissa
+//     bits: bins 1/8 of an octave wide) and writes the part that can hold the
+//     row's k-th key: t_c, the bin where its own count from the top reaches
+//     k (its lowest bin if it holds fewer keys), the kWin bins from t_c up,
+//     and how many of its keys lie above them.  The row's k-th key x is never
+//     below a chunk's own k-th key (else that chunk alone would hold k keys
+//     above x), so x lies in a bin >= t_c for every full chunk.
+//  2. topk_filter_kernel: the row's floor is the lower edge of the highest
+//     bin b whose count from the top reaches k, with every chunk's count
+//     taken from its window: exact for b in [max t_c, min t_c + kWin], never
+//     more than the true count elsewhere (a chunk's keys below t_c, or above
+//     a bin past its window, are left out), so at least k keys are >= floor
+//     and, with b in the exact range, fewer than k + (b's count) pass.  Each
+//     chunk keeps its keys >= floor, in position order, in its own list of k
+//     slots (value, original index) with a count; a chunk where more than k
+//     pass keeps its exact top-k among them (only those can be in the row's
+//     top-k).
+//  3. topk_lists_final_kernel: one 1024-thread WideSelect per row over the
+//     concatenated lists (chunk offsets from one wave scan of the counts),
+//     which are in ascending original index order, so the output is too.
+// A minimum of per-chunk lower bounds (the staged path's floor) let 5k-31k of
+// cfg4's 131072 scores per row through.
+// ---------------------------------------------------------------------------
+constexpr int kFilterMaxChunks = 64;
+constexpr int kFilterMaxLists = 32 * 1024;   // list slots per row (chunks * k): 32 keys per thread
+constexpr int kFilterVPL = kStageChunk / 256;   // keys per thread of a chunk
+constexpr int kHistBits = 12, kHistBins = 1 << kHistBits;
+constexpr int kWin = 64;                     // window bins per chunk
+constexpr int kWinWords = kWin + 2;          // t_c, the count above the window, the window
+
+__global__ __launch_bounds__(256) void topk_hist_kernel(const float* __restrict__ values, int64_t ld, int n, int k,
+                                                        int n_chunks, int32_t* __restrict__ win) {
+  constexpr int BPT = kHistBins / 256;   // bins per thread: thread t holds bins [4096 - 16(t+1), 4096 - 16t)
+  __shared__ uint32_t h[kHistBins];
+  __shared__ int wave_sum[4];
+  __shared__ int t_sh;
+  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int i = tid; i < kHistBins; i += 256) h[i] = 0;
+  if (tid == 0) t_sh = 0;
+  __syncthreads();
+  const int base = c * kStageChunk;
+  const int len = min(kStageChunk, n - base);
+  const float* vals = values + static_cast<int64_t>(row) * ld + base;
+  uint32_t key[kFilterVPL];   // every load in flight before the first atomic
+#pragma unroll
+  for (int i = 0; i < kFilterVPL; ++i) key[i] = f32_sortable(vals[min(tid * kFilterVPL + i, len - 1)]);
+#pragma unroll
+  for (int i = 0; i < kFilterVPL; ++i)
+    if (tid * kFilterVPL + i < len) atomicAdd(&h[key[i] >> (32 - kHistBits)], 1u);
+  __syncthreads();
+  // t_c: where the count from the top reaches min(k, len)
+  const int target = min(k, len);
+  const int b0 = kHistBins - BPT * (tid + 1);
+  int hb[BPT], cnt = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    hb[i] = static_cast<int>(h[b0 + i]);
+    cnt += hb[i];
+  }
+  const int incl = wave_incl_scan_dpp(cnt);
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+  int above = incl - cnt;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) above += w < wave ? wave_sum[w] : 0;
+  if (above < target && above + cnt >= target) {   // one thread
+    int t = b0;
+#pragma unroll
+    for (int i = BPT - 1; i >= 0; --i) {
+      if (above < target && above + hb[i] >= target) t = b0 + i;
+      above += hb[i];
+    }
+    t_sh = t;
+  }
+  __syncthreads();
+  const int t = t_sh;
+  int32_t* w = win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords;
+  if (tid < kWin) w[2 + tid] = t + tid < kHistBins ? static_cast<int32_t>(h[t + tid]) : 0;
+  // the keys above the window: this thread's bins from t + kWin up, summed over the workgroup
+  int over = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) over += b0 + i >= t + kWin ? hb[i] : 0;
+  over = wave_incl_scan_dpp(over);
+  __syncthreads();   // wave_sum is reused
+  if (lane == 63) wave_sum[wave] = over;
+  __syncthreads();
+  if (tid == 0) {
+    w[0] = t;
+    w[1] = wave_sum[0] + wave_sum[1] + wave_sum[2] + wave_sum[3];
+  }
+}
+
+__global__ __launch_bounds__(256) void topk_filter_kernel(const float* __restrict__ values, int64_t ld, int n, int k,
+                                                          const int32_t* __restrict__ win, int n_chunks,
+                                                          float* __restrict__ lval, int32_t* __restrict__ lidx,
+                                                          int32_t* __restrict__ lcnt) {
+  __shared__ int32_t sel[kStageChunk];
+  __shared__ int wave_sum[4];
+  __shared__ int wl[kFilterMaxChunks * kWinWords];   // the row's windows, then their suffix sums in place
+  __shared__ int best_sh;
+  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int base = c * kStageChunk;
+  const int len = min(kStageChunk, n - base);
+  const float* vals = values + static_cast<int64_t>(row) * ld + base;
+  // this thread's keys [tid * VPL, tid * VPL + VPL) of the chunk, and the
+  // row's windows, all loads in flight before the floor is worked out
+  float v[kFilterVPL];
+#pragma unroll
+  for (int i = 0; i < kFilterVPL; ++i) v[i] = vals[min(tid * kFilterVPL + i, len - 1)];
+  const int32_t* wr = win + static_cast<int64_t>(row) * n_chunks * kWinWords;
+  {
+    constexpr int U = (kFilterMaxChunks * kWinWords + 255) / 256;
+    const int nw = n_chunks * kWinWords;
+    int x[U];   // every load issued before the first LDS store
+#pragma unroll
+    for (int u = 0; u < U; ++u) x[u] = wr[min(tid + 256 * u, nw - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (tid + 256 * u < nw) wl[tid + 256 * u] = x[u];
+  }
+  if (tid == 0) best_sh = 0x7FFFFFFF;
+  __syncthreads();
+  // window j: wl[j*W] = t_j, wl[j*W + 1] = keys above it, wl[j*W + 2 + i] = bin t_j + i;
+  // in place: wl[j*W + 1 + d] = keys of chunk j in bins >= t_j + d (d = 0..64)
+  int top = 0;
+  for (int j0 = wave; j0 < n_chunks; j0 += 8) {   // windows j0 and j0 + 4 of this wave at a time
+    const bool two = j0 + 4 < n_chunks;            // wave-uniform
+    int* w0 = wl + j0 * kWinWords;
+    int* w1 = wl + (two ? j0 + 4 : j0) * kWinWords;
+    const int t0 = w0[0], t1 = w1[0], over0 = w0[1], over1 = w1[1];
+    const int b0 = w0[2 + kWin - 1 - lane], b1 = w1[2 + kWin - 1 - lane];   // bins 63 - lane
+    const int x0 = wave_incl_scan_dpp(b0), x1 = wave_incl_scan_dpp(b1);   // bins 63 - lane .. 63
+    __builtin_amdgcn_wave_barrier();   // (a wave's LDS reads complete before its writes)
+    w0[kWin - lane] = x0 + over0;      // d = 63 - lane, at 1 + d
+    if (lane == 0) w0[1 + kWin] = over0;   // d = 64
+    if (two) {
+      w1[kWin - lane] = x1 + over1;
+      if (lane == 0) w1[1 + kWin] = over1;
+    }
+    top = max(top, max(t0, t1) + kWin - 1);
+  }
+  if (lane == 0) wave_sum[wave] = top;
+  __syncthreads();
+  const int top_bin = min(max(max(wave_sum[0], wave_sum[1]), max(wave_sum[2], wave_sum[3])), kHistBins - 1);
+  {
+    const int b = top_bin - tid;   // thread j evaluates bin top - j
+    if (b >= 0) {
+      int cum = 0;   // never above the row's true count of keys in bins >= b
+      for (int j0 = 0; j0 < n_chunks; j0 += 8) {   // eight windows' reads in flight at a time
+        int t8[8], v8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t8[u] = wl[min(j0 + u, n_chunks - 1) * kWinWords];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int d = b - t8[u];
+          v8[u] = wl[min(j0 + u, n_chunks - 1) * kWinWords + 1 + min(max(d, 0), kWin)];
+          v8[u] = d > kWin || j0 + u >= n_chunks ? 0 : v8[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cum += v8[u];
+      }
+      if (cum >= k) atomicMin(&best_sh, tid);   // the highest such bin
+    }
+  }
+  __syncthreads();
+  const uint32_t floor = best_sh == 0x7FFFFFFF ? 0u : static_cast<uint32_t>(top_bin - best_sh) << (32 - kHistBits);
+  uint32_t pass = 0;
+#pragma unroll
+  for (int i = 0; i < kFilterVPL; ++i) {
+    const int p = tid * kFilterVPL + i;
+    pass |= static_cast<uint32_t>(p < len && f32_sortable(v[i]) >= floor) << i;
+  }
+  const int cnt = __popc(pass);
+  const int incl = wave_incl_scan_dpp(cnt);
+  if (lane == 63) wave_sum[wave] = incl;
+  __syncthreads();
+  int before = incl - cnt, total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    before += w < wave ? wave_sum[w] : 0;
+    total += wave_sum[w];
+  }
+  const int64_t o = (static_cast<int64_t>(row) * n_chunks + c) * k;
+  if (total <= k) {   // uniform: every passing key, in position order
+#pragma unroll
+    for (int i = 0; i < kFilterVPL; ++i) {
+      if ((pass >> i) & 1u) {
+        lval[o + before] = v[i];
+        lidx[o + before] = base + tid * kFilterVPL + i;
+        ++before;
+      }
+    }
+    if (tid == 0) lcnt[static_cast<int64_t>(row) * n_chunks + c] = total;
+    return;
+  }
+  // more than k pass: the chunk's exact top-k among them
+  const int kk = select_row<kFilterVPL, false>(vals, len, k, sel, floor);
+  for (int j = tid; j < kk; j += 256) {
+    lval[o + j] = vals[sel[j]];
+    lidx[o + j] = base + sel[j];
+  }
+  if (tid == 0) lcnt[static_cast<int64_t>(row) * n_chunks + c] = kk;
+}
+
+// Rows whose lists hold at most kFinalLds keys: gathered into LDS in list
+// order and selected by WideSelect with kFinalLds / 1024 keys per thread;
+// longer lists: WideSelect with VPLB keys per thread (covering chunks * k),
+// read from the lists directly.
+constexpr int kFinalLds = 4096;
+
+template <int VPLB>
+__global__ __launch_bounds__(1024) void topk_lists_final_kernel(const float* __restrict__ lval,
+                                                                const int32_t* __restrict__ lidx,
+                                                                const int32_t* __restrict__ lcnt, int n_chunks,
+                                                                int k, int32_t* __restrict__ out) {
+  using WB = WideSelect<VPLB, false>;
+  using WC = WideSelect<kFinalLds / 1024, false>;
+  __shared__ union {
+    typename WB::Shared b;
+    typename WC::Shared c;
+  } sh;
+  __shared__ float cval[kFinalLds];
+  __shared__ int32_t cidx[kFinalLds];
+  __shared__ int off[kFilterMaxChunks + 1];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  if (tid < 64) {   // list offsets: one load per chunk, a wave scan
+    const int len = tid < n_chunks ? lcnt[static_cast<int64_t>(row) * n_chunks + tid] : 0;
+    const int incl = wave_incl_scan_dpp(len);
+    if (tid < n_chunks) off[tid] = incl - len;
+    if (tid == 63) off[n_chunks] = incl;   // the total
+  }
+  __syncthreads();
+  const int total = off[n_chunks];
+  const int64_t rbase = static_cast<int64_t>(row) * n_chunks * k;
+  int32_t* orow = out + static_cast<int64_t>(row) * k;
+  auto entry = [&](int p) -> int64_t {   // list slot of concatenated position p < total
+    int lo = 0, hi = n_chunks - 1;        // the last chunk whose list starts at or before p
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    return rbase + static_cast<int64_t>(lo) * k + (p - off[lo]);
+  };
+  if (total <= kFinalLds) {   // uniform across the workgroup
+    constexpr int U = kFinalLds / 1024;
+    float xv[U];
+    int32_t xi[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {   // every load issued before the first LDS store
+      const int p = tid + 1024 * u;
+      const int64_t e = p < total ? entry(p) : 0;
+      xv[u] = lval[e];
+      xi[u] = lidx[e];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = tid + 1024 * u;
+      if (p < total) {
+        cval[p] = xv[u];
+        cidx[p] = xi[u];
+      }
+    }
+    __syncthreads();
+    WC wc;
+#pragma unroll
+    for (int i = 0; i < kFinalLds / 1024; ++i) {
+      const int p = WC::pos(i);
+      wc.set(i, p < total ? cval[p] : 0.0f, p < total);
+    }
+    const int kk = wc.run(k, sh.c);
+    wc.place(sh.c, [&](int p, int o, int) { orow[o] = cidx[p]; });
+    for (int o = kk + tid; o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
+    return;
+  }
+  // (the original index of a taken key is looked up again from its position:
+  // a register array indexed by the taken slot would live in scratch)
+  WB wb;
+#pragma unroll
+  for (int i = 0; i < VPLB; ++i) {
+    const int p = wb.pos(i);
+    const bool ok = p < total;
+    wb.set(i, ok ? lval[ok ? entry(p) : 0] : 0.0f, ok);
+  }
+  const int kk = wb.run(k, sh.b);
+  wb.place(sh.b, [&](int p, int o, int) { orow[o] = lidx[entry(p)]; });
+  for (int o = kk + tid; o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
+}
+
 // Candidates left after a stage over n keys: k from every full chunk, and
 // min(k, rest) from the last.
 int64_t stage_out(int64_t n, int64_t k) {
@@ -367,6 +664,12 @@ int64_t stage_out(int64_t n, int64_t k) {
 }
 
 bool staged(int64_t n, int64_t k) { return n > kStageChunk && k <= kStageMaxK; }
+
+// Staged rows that take the histogram-and-filter path.
+bool filtered(int64_t n, int64_t k) {
+  const int64_t chunks = cdiv(n, kStageChunk);
+  return staged(n, k) && chunks <= kFilterMaxChunks && chunks * k <= kFilterMaxLists;
+}
 
 template <bool FINITE>
 int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
@@ -421,10 +724,13 @@ QKV_EXPORT int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld
 QKV_EXPORT int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
   if (rows <= 0 || n <= 0 || k < 1 || k > n) return -1;
   if (!staged(n, k)) return 0;
+  const int64_t chunks = cdiv(n, kStageChunk);
+  if (filtered(n, k))   // chunk windows, then per-chunk lists of k (value, index) and their counts
+    return rows * chunks * (kWinWords + k * 2 + 1) * 4;
   // two candidate buffers (value + index) sized for the first stage's output,
   // then the first stage's chunk bounds
   return 2 * rows * stage_out(n, k) * static_cast<int64_t>(sizeof(float) + sizeof(int32_t)) +
-         rows * cdiv(n, kStageChunk) * static_cast<int64_t>(sizeof(uint32_t));
+         rows * chunks * static_cast<int64_t>(sizeof(uint32_t));
 }
 
 QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
@@ -450,6 +756,22 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
   uint32_t* bounds = reinterpret_cast<uint32_t*>(idx_buf[1] + rows * n1);
   const int n_bounds = static_cast<int>(cdiv(n, kStageChunk));
   const int bound_j = static_cast<int>(cdiv(cdiv(k, n_bounds), 4));   // per wave; above 64: no bound
+  if (filtered(n, k)) {
+    // histogram and filter: the chunk windows, then the lists
+    int32_t* win = static_cast<int32_t*>(workspace);
+    float* lval = reinterpret_cast<float*>(win + rows * n_bounds * kWinWords);
+    int32_t* lidx = reinterpret_cast<int32_t*>(lval + rows * n_bounds * k);
+    int32_t* lcnt = lidx + rows * n_bounds * k;
+    dim3 grid(static_cast<unsigned>(n_bounds), static_cast<unsigned>(rows));
+    topk_hist_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds, win);
+    if (int rc = check_launch("qkv_topk_ws")) return rc;
+    topk_filter_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), win, n_bounds,
+                                             lval, lidx, lcnt);
+    if (int rc = check_launch("qkv_topk_ws")) return rc;
+    topk_lists_final_kernel<kFilterMaxLists / 1024><<<static_cast<unsigned>(rows), 1024, 0, st>>>(
+        lval, lidx, lcnt, n_bounds, static_cast<int>(k), out);
+    return check_launch("qkv_topk_ws");
+  }
   const float* cur_val = values;
   const int32_t* cur_idx = nullptr;
   int64_t cur_ld = ld, cur_n = n;

@@ -236,6 +236,29 @@ def test_topk_adversarial_layouts(n, k):
     assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
 
 
+@pytest.mark.parametrize("n,k", [(131072, 1024), (70000, 64), (8193, 1000), (40000, 1), (16384, 513)])
+def test_topk_long_rows_adversarial(n, k):
+    # long rows (the bound-and-filter path: per-chunk bounds, filtered
+    # per-chunk lists, one WideSelect per row): all-equal rows and heavy ties
+    # pass more than k keys per chunk, one-lane rows leave most chunks empty,
+    # a partial last chunk adds no bound
+    vals = _adversarial_rows(n, n + k)
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
+def test_topk_long_rows_one_chunk_over_k():
+    # one chunk holds far more than k keys above the floor, the others a few
+    n, k = 65536, 256
+    g = torch.Generator().manual_seed(5)
+    vals = torch.randn((3, n), generator=g)
+    vals[0, 8192:12288] += 10.0                 # chunk 2: 4096 keys above every other chunk's
+    vals[1, 5::4096] = 100.0                   # one huge key per chunk
+    vals[2, 4096 * 15:] = -float("inf")        # the last chunk -inf only
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
 @pytest.mark.parametrize("n,k,ld", [(1024, 64, 1024), (1024, 1, 1025), (1000, 100, 1000), (200, 64, 203),
                                     (513, 7, 513)])
 def test_topk_many_short_rows(n, k, ld):
