@@ -353,25 +353,31 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
   }
   if (!mask) return;
   // A slot of a wave covers 64 consecutive positions: its flags are one
-  // ballot, written by 16 lanes as dwords (bytes one by one at the row end
-  // or when the rows are not 4-byte aligned).
+  // ballot.  The wave's VPL ballots go to LDS; lane l then writes the 16
+  // flags of positions 16q..16q+15 of the wave's range (q = l, l + 64, ...)
+  // as one 16-byte store (bytes one by one past the row end or when the row
+  // is not 16-byte aligned).
+  __shared__ uint64_t bal[kWideNT / 64][VPL];
   uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
-  const int lane = tid & 63;
-  const bool dwords = (reinterpret_cast<uintptr_t>(mrow) & 3) == 0;
+  const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int t = WS::pos(i);
-    const bool f = ws.u[i] >= ws.theta;
-    const uint64_t m = __ballot(f);
-    const int chunk = t - lane;
-    if (dwords && chunk + 64 <= n) {
-      if (lane < 16) {
-        const uint32_t nib = static_cast<uint32_t>(m >> (4 * lane)) & 0xFu;
-        const uint32_t w = (nib & 1u) | ((nib >> 1) & 1u) << 8 | ((nib >> 2) & 1u) << 16 | ((nib >> 3) & 1u) << 24;
-        *reinterpret_cast<uint32_t*>(mrow + chunk + 4 * lane) = w;
-      }
-    } else if (t < n) {
-      mrow[t] = f;
+    const uint64_t m = __ballot(ws.u[i] >= ws.theta);
+    if (lane == 0) bal[wave][i] = m;
+  }
+  __builtin_amdgcn_wave_barrier();   // (a wave's LDS writes complete before its reads)
+  const bool vec = (reinterpret_cast<uintptr_t>(mrow) & 15) == 0;
+  const int wbase = wave * 64 * VPL;
+  for (int q = lane; q < 4 * VPL; q += 64) {
+    const uint32_t bits = static_cast<uint32_t>(bal[wave][q >> 2] >> (16 * (q & 3))) & 0xFFFFu;
+    const int t0 = wbase + 16 * q;
+    if (vec && t0 + 16 <= n) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (((bits >> (4 * j)) & 0xFu) * 0x00204081u) & 0x01010101u;   // 4 bits -> 4 bytes
+      *reinterpret_cast<uint4*>(mrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      for (int j = 0; j < 16 && t0 + j < n; ++j) mrow[t0 + j] = (bits >> j) & 1u;
     }
   }
 }
