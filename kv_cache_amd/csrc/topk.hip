@@ -170,13 +170,18 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
     }
     nval += __popcll(__ballot(valid[i]));
   }
+  const uint32_t lane_max = umax;   // 0 when the lane holds no valid key
   umax = wave_minmax_u32<true>(umax);
   umin = wave_minmax_u32<false>(umin);
   const int kk = min(k, nval);
+  // A lower bound of the k-th largest key (k <= 64: at least k lanes' maxima
+  // are >= it); the radix passes start from the bits it shares with the
+  // largest key, and keys under it stay out of the histograms.
+  const uint32_t lo = max(umin, wave_lower_bound(lane_max, kk, umax, umin));
 
   int kr = kk;
   uint32_t prefix = umax, mask = 0xFFFFFFFFu;
-  int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
+  int remaining = (umax == lo || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ lo);
   if (remaining) {
     mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
     prefix = umax & mask;
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
-      if (valid[i] && (u[i] & mask) == prefix) atomicAdd(&wh[(u[i] >> shift) & dmask], 1);
+      if (valid[i] && u[i] >= lo && (u[i] & mask) == prefix) atomicAdd(&wh[(u[i] >> shift) & dmask], 1);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // Lane l owns bins 255-4l .. 252-4l (descending order of keys).
