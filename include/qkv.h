@@ -183,19 +183,31 @@ int qkv_topk(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k
 int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 
 /* qkv_topk with a caller-owned workspace (16-byte aligned, contents
- * irrelevant): rows longer than 4096 keys with k <= 1024 are split into
- * 4096-key chunks.  Rows of at most 64 chunks with chunks * k <= 32768:
- * every chunk histograms its keys (1/8-octave bins) around its own k-th key,
- * the row's floor is the bin where the merged count from the top reaches k,
- * each chunk keeps its keys at or above it (its exact top-k among them when
- * more than k pass), and one workgroup per row selects from those lists
- * (three launches).  Longer rows: stages in which each chunk keeps its local
+ * irrelevant; calls sharing a workspace must not overlap in time): rows
+ * longer than 4096 keys with k <= 1024 are split into 4096-key chunks.  Rows
+ * of at most 64 chunks with chunks * k <= 32768: every chunk histograms its
+ * keys (1/8-octave bins) around its own k-th key, the row's floor is the bin
+ * where the merged count from the top reaches k, each chunk keeps its keys
+ * at or above it (its exact top-k among them when more than k pass), and
+ * the row's last chunk to finish selects from those lists -- one launch when
+ * rows * chunks <= 256 (every workgroup resident at once; the row's chunks
+ * count in ticket words the library keeps per GPU, 4 MiB held until the
+ * process ends), three otherwise.  Longer rows: stages
+ * in which each chunk keeps its local
  * top-k until the candidates fit one chunk or one 1024-thread workgroup
  * (40960), keys below a lower bound of the row's k-th key left out after the
  * first stage.  The result equals qkv_topk's.  Same replaced call sites as
  * qkv_topk (EV:4448 token-level top-k over long contexts). */
 int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* No counterpart in the reference; for tests of qkv_topk_ws's one-launch
+ * path.  Sets how long (ticks of the 100 MHz real-time clock) a chunk waits
+ * for the other chunks of its row before keeping its exact top-k instead of
+ * filtering by the row's floor (the result is the same either way); ticks < 0
+ * restores the default (131072, about 1.3 ms).  Process-wide; takes effect
+ * for launches after the call. */
+int qkv_topk_set_wait_limit(int64_t ticks);
 
 /* Bytes of workspace qkv_sparse_attention needs for these sizes: 65536
  * uint32 row tickets (the same words for every call shape), then G*(D+2)

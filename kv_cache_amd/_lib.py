@@ -49,6 +49,7 @@ _PROTOTYPES = {
     "qkv_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "qkv_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qkv_topk_ws": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "qkv_topk_set_wait_limit": (_i32, [_i64]),
     "qkv_prefill_quantize_query": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
     "qkv_prefill_block_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         _vp, _vp]),

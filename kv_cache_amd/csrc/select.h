@@ -301,13 +301,12 @@ struct WideSelect {
   static_assert(NW * VPL * RECW <= NB, "slot records fit in the histogram's place");
   struct Shared {
     union {
-      int hist[NB];                   // run(): the radix histogram
+      int hist[2][NB];                // run(): the radix histograms of even and odd passes
       uint32_t rec[NW * VPL * RECW];  // place(): per (wave, slot) prefix counts and lane masks
     };
     int wave_sum[NW];
     int wave_gt[NW], wave_eq[NW];
     uint32_t red[NW][3];
-    int bin, kr, whole;
   };
 
   // Position of key i of this thread.
@@ -350,8 +349,19 @@ struct WideSelect {
   __device__ void refresh() { asm volatile("" : "+v"(valid)); }
 
   // theta and kr for the k largest valid keys; returns kk = min(k, valid keys).
+  // Every thread calls it; the caller's earlier uses of sh have completed
+  // (a barrier since).
+  //
+  // Two barriers per 12-bit digit: the histograms alternate between passes,
+  // so a pass clears the next pass's histogram after its first barrier
+  // instead of behind a barrier of its own, and after the second barrier
+  // (the per-wave sums) every wave finds the boundary bin itself -- the wave
+  // of bins holding the kr-th key from the top, then the bin among its 256 --
+  // instead of waiting for one thread to publish it.
   __device__ int run(int k, Shared& sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int j = 0; j < NB / NT; ++j) sh.hist[0][tid + NT * j] = 0;
     uint32_t umax = 0, umin = 0xFFFFFFFFu;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -391,16 +401,17 @@ struct WideSelect {
       kr = 0x7FFFFFFF;
       remaining = 0;
     }
-    // One shared histogram of 4096 bins: a 12-bit digit of sign, exponent
-    // and top mantissa bits spreads typical scores over enough bins that a
-    // wave's atomics rarely collide (an 8-bit digit of such floats holds a
-    // handful of exponents and serializes on them).
+    // One shared histogram of 4096 bins per pass: a 12-bit digit of sign,
+    // exponent and top mantissa bits spreads typical scores over enough bins
+    // that a wave's atomics rarely collide (an 8-bit digit of such floats
+    // holds a handful of exponents and serializes on them).
+    const bool passes = remaining > 0;
+    int buf = 0;
     while (remaining > 0) {   // uniform across the workgroup
       refresh();
       const int shift = remaining > RB ? remaining - RB : 0;
       const uint32_t dmask = (1u << (remaining - shift)) - 1u;
-      for (int e = tid; e < NB; e += NT) sh.hist[e] = 0;
-      __syncthreads();
+      int* hist = sh.hist[buf];
       // Keys equal to the row minimum are counted per wave instead: a flood
       // of equal keys (the -inf of unscored positions) would serialize on
       // one LDS address.
@@ -409,46 +420,59 @@ struct WideSelect {
       for (int i = 0; i < VPL; ++i) {
         if (on(i) && (u[i] & mask) == prefix) {
           if (u[i] == umin) ++at_min;
-          else atomicAdd(&sh.hist[(u[i] >> shift) & dmask], 1);
+          else atomicAdd(&hist[(u[i] >> shift) & dmask], 1);
         }
       }
       at_min = wave_incl_scan_dpp(at_min);
-      if (lane == 63 && at_min) atomicAdd(&sh.hist[(umin >> shift) & dmask], at_min);
+      if (lane == 63 && at_min) atomicAdd(&hist[(umin >> shift) & dmask], at_min);
       __syncthreads();
+      // (the other histogram was last read before this pass's atomics)
+#pragma unroll
+      for (int j = 0; j < NB / NT; ++j) sh.hist[buf ^ 1][tid + NT * j] = 0;
       // Thread t owns bins NB-1-4t .. NB-4-4t (descending), so the keys in
       // higher bins are those of lower threads and of its own earlier bins.
-      int c[4], tot = 0;
+      int tot = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = sh.hist[NB - 1 - 4 * tid - j];
-        tot += c[j];
-      }
+      for (int j = 0; j < 4; ++j) tot += hist[NB - 1 - 4 * tid - j];
       const int incl = wave_incl_scan_dpp(tot);
       if (lane == 63) sh.wave_sum[wave] = incl;
       __syncthreads();
-      int above = incl - tot;
+      const int wsum = lane < NW ? sh.wave_sum[lane] : 0;
+      const int wcum = wave_incl_scan_dpp(wsum);
+      const int bw = __builtin_ctzll(__ballot(lane < NW && wcum >= kr));   // the boundary's wave of bins
+      const int t2 = bw * 64 + lane;
+      int c[4], tot2 = 0;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) above += w < wave ? sh.wave_sum[w] : 0;
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[NB - 1 - 4 * t2 - j];
+        tot2 += c[j];
+      }
+      int above = __builtin_amdgcn_readlane(wcum - wsum, bw) + wave_incl_scan_dpp(tot2) - tot2;
+      const int bl = __builtin_ctzll(__ballot(above < kr && kr <= above + tot2));   // its lane
+      int bin = 0, krl = 0, whole = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (above < kr && kr <= above + c[j]) {
-          sh.bin = NB - 1 - 4 * tid - j;
-          sh.kr = kr - above;
-          sh.whole = (kr - above) == c[j];
+          bin = NB - 1 - 4 * t2 - j;
+          krl = kr - above;
+          whole = krl == c[j];
         }
         above += c[j];
       }
-      __syncthreads();
-      prefix |= static_cast<uint32_t>(sh.bin) << shift;
+      bin = __builtin_amdgcn_readlane(bin, bl);
+      krl = __builtin_amdgcn_readlane(krl, bl);
+      whole = __builtin_amdgcn_readlane(whole, bl);
+      prefix |= static_cast<uint32_t>(bin) << shift;
       mask |= dmask << shift;
-      kr = sh.kr;
+      kr = krl;
       remaining = shift;
-      if (sh.whole) {   // the boundary bin is taken whole: theta = its lower bound
+      buf ^= 1;
+      if (whole) {   // the boundary bin is taken whole: theta = its lower bound
         kr = 0x7FFFFFFF;
         break;
       }
-      __syncthreads();   // sh.bin / sh.kr are read before the next pass rewrites them
     }
+    if (passes) __syncthreads();   // the last pass's histogram reads are done before sh is reused
     theta = prefix;
     return kk;
   }

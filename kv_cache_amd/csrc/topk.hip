@@ -8,6 +8,9 @@
 // theta and how many keys equal to theta are kept; a stable compaction in
 // index order then writes every key > theta plus the lowest-index keys equal
 // to theta, so the output is already in ascending index order.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "select.h"
 
@@ -518,6 +521,7 @@ __global__ __launch_bounds__(256) void topk_filter_kernel(const float* __restric
   const int top_bin = min(max(max(wave_sum[0], wave_sum[1]), max(wave_sum[2], wave_sum[3])), kHistBins - 1);
   {
     const int b = top_bin - tid;   // thread j evaluates bin top - j
+    bool hit = false;
     if (b >= 0) {
       int cum = 0;   // never above the row's true count of keys in bins >= b
       for (int j0 = 0; j0 < n_chunks; j0 += 8) {   // eight windows' reads in flight at a time
@@ -533,8 +537,12 @@ __global__ __launch_bounds__(256) void topk_filter_kernel(const float* __restric
 #pragma unroll
         for (int u = 0; u < 8; ++u) cum += v8[u];
       }
-      if (cum >= k) atomicMin(&best_sh, tid);   // the highest such bin
+      hit = cum >= k;
     }
+    // The count only grows with the thread index (lower bins): a wave's first
+    // hit is its candidate for the highest such bin, one LDS atomic per wave.
+    const uint64_t hits = __ballot(hit);
+    if (hits != 0 && lane == 0) atomicMin(&best_sh, wave * 64 + static_cast<int>(__builtin_ctzll(hits)));
   }
   __syncthreads();
   const uint32_t floor = best_sh == 0x7FFFFFFF ? 0u : static_cast<uint32_t>(top_bin - best_sh) << (32 - kHistBits);
@@ -580,7 +588,7 @@ __global__ __launch_bounds__(256) void topk_filter_kernel(const float* __restric
 // order and selected by WideSelect with kFinalLds / 1024 keys per thread;
 // longer lists: WideSelect with VPLB keys per thread (covering chunks * k),
 // read from the lists directly.
-constexpr int kFinalLds = 4096;
+constexpr int kFinalLds = 4096, kFinalLdsLog2 = 12;
 
 template <int VPLB>
 __global__ __launch_bounds__(1024) void topk_lists_final_kernel(const float* __restrict__ lval,
@@ -661,6 +669,330 @@ __global__ __launch_bounds__(1024) void topk_lists_final_kernel(const float* __r
   for (int o = kk + tid; o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
 }
 
+// ---------------------------------------------------------------------------
+// The three steps above in one launch, for grids whose workgroups are all
+// resident at once (rows * chunks <= kFusedMaxWGs; one 1024-thread workgroup
+// per chunk, 4 keys per thread held in registers throughout):
+//  a. the chunk's histogram and window, published with device-coherent
+//     stores, then the row's first ticket;
+//  b. the workgroup waits until every chunk of its row has published (a
+//     bounded wait: past g_spin_ticks of the real-time clock it takes floor 0,
+//     i.e. keeps its exact top-k, which is always a valid list, so the launch
+//     ends whatever the residency);
+//  c. the row's floor exactly as topk_filter_kernel computes it, and the
+//     chunk's list;
+//  d. the row's second ticket: the last chunk to arrive selects from the lists
+//     as topk_lists_final_kernel does and returns both tickets to zero.
+// ---------------------------------------------------------------------------
+constexpr int kFusedMaxWGs = 256;
+constexpr int kFusedVPL = kStageChunk / 1024;   // keys per thread
+constexpr int kTicketSlotWords = kFusedMaxWGs;  // (windows published, lists written) per row; rows <= 128
+constexpr int kTicketSlots = 4096;
+constexpr int64_t kSpinTicks = 1 << 17;           // ~1.3 ms of the 100 MHz real-time clock
+int64_t g_spin_ticks = kSpinTicks;                // qkv_topk_set_wait_limit
+
+__global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restrict__ values, int64_t ld, int n,
+                                                          int k, int n_chunks, uint64_t spin_ticks,
+                                                          uint32_t* __restrict__ tickets, int32_t* __restrict__ win,
+                                                          float* __restrict__ lval, int32_t* __restrict__ lidx,
+                                                          int32_t* __restrict__ lcnt, int32_t* __restrict__ out) {
+  using WS = WideSelect<kFusedVPL, false>;
+  using WB = WideSelect<kFilterMaxLists / 1024, false>;
+  constexpr int NW = 16, BPT = kHistBins / 1024;
+  __shared__ union {
+    uint32_t h[kHistBins];                  // a: the chunk's histogram
+    int wl[kFilterMaxChunks * kWinWords];   // c: the row's windows, then their suffix sums
+    struct {
+      typename WS::Shared s;
+      float cval[kFinalLds];
+      int32_t cidx[kFinalLds];
+    } fin;                                  // c (more than k pass) and d
+    typename WB::Shared b;                  // d, lists longer than kFinalLds
+  } sh;
+  __shared__ int wave_a[NW], wave_b[NW];
+  __shared__ int t_sh, best_sh, flag_sh;
+  __shared__ int off[kFilterMaxChunks + 1], lens[kFilterMaxChunks];
+  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int base = c * kStageChunk;
+  const int len = min(kStageChunk, n - base);
+  const float* vals = values + static_cast<int64_t>(row) * ld + base;
+  uint32_t* tk = tickets + 2 * static_cast<int64_t>(row);
+
+  // a. histogram of the keys' top kHistBits bits
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) sh.h[tid + 1024 * i] = 0;
+  if (tid == 0) {
+    t_sh = 0;
+    best_sh = 0x7FFFFFFF;
+  }
+  WS ws;
+  ws.load(vals, len);   // key i of this thread: chunk position WS::pos(i)
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kFusedVPL; ++i)
+    if (ws.on(i)) atomicAdd(&sh.h[ws.u[i] >> (32 - kHistBits)], 1u);
+  __syncthreads();
+  const int target = min(k, len);
+  const int b0 = kHistBins - BPT * (tid + 1);   // thread t holds bins [4096 - 4(t+1), 4096 - 4t)
+  int hb[BPT], cnt = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    hb[i] = static_cast<int>(sh.h[b0 + i]);
+    cnt += hb[i];
+  }
+  const int incl = wave_incl_scan_dpp(cnt);
+  if (lane == 63) wave_a[wave] = incl;
+  __syncthreads();
+  int above = incl - cnt;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) above += w < wave ? wave_a[w] : 0;
+  if (above < target && above + cnt >= target) {   // one thread
+    int t = b0;
+#pragma unroll
+    for (int i = BPT - 1; i >= 0; --i) {
+      if (above < target && above + hb[i] >= target) t = b0 + i;
+      above += hb[i];
+    }
+    t_sh = t;
+  }
+  __syncthreads();
+  const int t = t_sh;
+  int32_t* w = win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords;
+  if (tid < kWin) st_coherent(w + 2 + tid, t + tid < kHistBins ? static_cast<int32_t>(sh.h[t + tid]) : 0);
+  int over = 0;   // keys above the window
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) over += b0 + i >= t + kWin ? hb[i] : 0;
+  over = wave_incl_scan_dpp(over);
+  if (lane == 63) wave_b[wave] = over;
+  __syncthreads();
+  if (tid == 0) {
+    int sum = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) sum += wave_b[v];
+    st_coherent(w, t);
+    st_coherent(w + 1, sum);
+  }
+  // Every window store of this workgroup has completed before the ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // b. wait for the row's other chunks
+  if (tid == 0) {
+    __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    int ok = 1;
+    while (__hip_atomic_load(tk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < static_cast<uint32_t>(n_chunks)) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__builtin_amdgcn_s_memrealtime() - t0 >= spin_ticks) {
+        ok = 0;
+        break;
+      }
+    }
+    flag_sh = ok;
+  }
+  __syncthreads();
+
+  // c. the row's floor (as in topk_filter_kernel), then this chunk's list
+  uint32_t floor = 0;
+  if (flag_sh) {   // uniform
+    const int32_t* wr = win + static_cast<int64_t>(row) * n_chunks * kWinWords;
+    {
+      constexpr int U = (kFilterMaxChunks * kWinWords + 1023) / 1024;
+      const int nw = n_chunks * kWinWords;
+      int x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) x[u] = ld_coherent(wr + min(tid + 1024 * u, nw - 1));
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (tid + 1024 * u < nw) sh.wl[tid + 1024 * u] = x[u];
+    }
+    __syncthreads();
+    int top = 0;
+    for (int j = wave; j < n_chunks; j += NW) {   // window j: suffix sums in place
+      int* wj = sh.wl + j * kWinWords;
+      const int tj = wj[0], overj = wj[1];
+      const int x = wave_incl_scan_dpp(wj[2 + kWin - 1 - lane]);   // bins 63 - lane .. 63
+      __builtin_amdgcn_wave_barrier();   // (a wave's LDS reads complete before its writes)
+      wj[kWin - lane] = x + overj;
+      if (lane == 0) wj[1 + kWin] = overj;
+      top = max(top, tj + kWin - 1);
+    }
+    if (lane == 0) wave_a[wave] = top;
+    __syncthreads();
+    int top_bin = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) top_bin = max(top_bin, wave_a[v]);
+    top_bin = min(top_bin, kHistBins - 1);
+    const int b = top_bin - tid;   // thread j evaluates bin top - j
+    bool hit = false;
+    if (b >= 0) {
+      int cum = 0;   // never above the row's true count of keys in bins >= b
+      for (int j0 = 0; j0 < n_chunks; j0 += 8) {
+        int t8[8], v8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t8[u] = sh.wl[min(j0 + u, n_chunks - 1) * kWinWords];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int d = b - t8[u];
+          v8[u] = sh.wl[min(j0 + u, n_chunks - 1) * kWinWords + 1 + min(max(d, 0), kWin)];
+          v8[u] = d > kWin || j0 + u >= n_chunks ? 0 : v8[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) cum += v8[u];
+      }
+      hit = cum >= k;
+    }
+    const uint64_t hits = __ballot(hit);   // one LDS atomic per wave, as in topk_filter_kernel
+    if (hits != 0 && lane == 0) atomicMin(&best_sh, wave * 64 + static_cast<int>(__builtin_ctzll(hits)));
+    __syncthreads();
+    floor = best_sh == 0x7FFFFFFF ? 0u : static_cast<uint32_t>(top_bin - best_sh) << (32 - kHistBits);
+  }
+  uint64_t bl[kFusedVPL];
+  int wtot = 0;
+#pragma unroll
+  for (int i = 0; i < kFusedVPL; ++i) {
+    bl[i] = __ballot(ws.on(i) && ws.u[i] >= floor);
+    wtot += __popcll(bl[i]);
+  }
+  if (lane == 0) wave_b[wave] = wtot;   // wave_b's last reads were before two barriers
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    before += v < wave ? wave_b[v] : 0;
+    total += wave_b[v];
+  }
+  const int64_t o = (static_cast<int64_t>(row) * n_chunks + c) * k;
+  if (total <= k) {   // uniform: every passing key, in position order
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int i = 0; i < kFusedVPL; ++i) {
+      if ((bl[i] >> lane) & 1ull) {
+        const int at = before + __popcll(bl[i] & below);
+        st_coherent(lval + o + at, sortable_f32(ws.u[i]));
+        st_coherent(lidx + o + at, base + WS::pos(i));
+      }
+      before += __popcll(bl[i]);
+    }
+    if (tid == 0) st_coherent(lcnt + static_cast<int64_t>(row) * n_chunks + c, total);
+  } else {   // more than k pass: the chunk's exact top-k among them
+#pragma unroll
+    for (int i = 0; i < kFusedVPL; ++i)
+      if (ws.on(i) && ws.u[i] < floor) ws.valid &= ~(1ull << i);
+    const int kk = ws.run(k, sh.fin.s);
+    ws.place(sh.fin.s, [&](int p, int at, int) {
+      st_coherent(lval + o + at, vals[p]);
+      st_coherent(lidx + o + at, base + p);
+    });
+    if (tid == 0) st_coherent(lcnt + static_cast<int64_t>(row) * n_chunks + c, kk);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // d. the row's last chunk selects from the lists
+  if (tid == 0) {
+    const uint32_t a = __hip_atomic_fetch_add(tk + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = a == static_cast<uint32_t>(n_chunks - 1);
+    if (last) {   // every chunk of the row has left its wait
+      __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(tk + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    flag_sh = last;
+  }
+  __syncthreads();
+  if (!flag_sh) return;
+  // The lists' counts and the first S entries of every list in one batch of
+  // loads (S = kFinalLds / chunks rounded up to a power of two); a list
+  // longer than S sends the row through a second round of loads.
+  const int64_t rbase = static_cast<int64_t>(row) * n_chunks * k;
+  const int sh_s = kFinalLdsLog2 - (n_chunks <= 1 ? 0 : 32 - __builtin_clz(n_chunks - 1));
+  constexpr int U = kFinalLds / 1024;
+  float xv[U];
+  int32_t xi[U];
+  int l = 0;
+  if (tid < 64)   // (clamped: a count outside [0, k] cannot send a load outside the lists)
+    l = tid < n_chunks ? min(max(ld_coherent(lcnt + static_cast<int64_t>(row) * n_chunks + tid), 0), k) : 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int f = tid + 1024 * u, j = f >> sh_s, slot = f & ((1 << sh_s) - 1);
+    const int64_t e = j < n_chunks && slot < k ? rbase + static_cast<int64_t>(j) * k + slot : rbase;
+    xv[u] = ld_coherent(lval + e);
+    xi[u] = ld_coherent(lidx + e);
+  }
+  if (tid < 64) {   // list offsets: a wave scan of the counts
+    const int x = wave_incl_scan_dpp(l);
+    if (tid < n_chunks) {
+      off[tid] = x - l;
+      lens[tid] = l;
+    }
+    if (tid == 63) off[n_chunks] = x;
+    const bool longer = __ballot(l > (1 << sh_s)) != 0;
+    if (tid == 0) flag_sh = longer;
+  }
+  __syncthreads();
+  const int all = off[n_chunks];
+  int32_t* orow = out + static_cast<int64_t>(row) * k;
+  auto entry = [&](int p) -> int64_t {   // list slot of concatenated position p < all
+    int lo = 0, hi = n_chunks - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (off[mid] <= p) lo = mid;
+      else hi = mid - 1;
+    }
+    return rbase + static_cast<int64_t>(lo) * k + (p - off[lo]);
+  };
+  if (all <= kFinalLds) {   // uniform
+    if (!flag_sh) {   // every entry is among those loaded
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int f = tid + 1024 * u, j = f >> sh_s, slot = f & ((1 << sh_s) - 1);
+        if (j < n_chunks && slot < lens[j]) {
+          sh.fin.cval[off[j] + slot] = xv[u];
+          sh.fin.cidx[off[j] + slot] = xi[u];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int p = tid + 1024 * u;
+        const int64_t e = p < all ? entry(p) : rbase;
+        xv[u] = ld_coherent(lval + e);
+        xi[u] = ld_coherent(lidx + e);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int p = tid + 1024 * u;
+        if (p < all) {
+          sh.fin.cval[p] = xv[u];
+          sh.fin.cidx[p] = xi[u];
+        }
+      }
+    }
+    __syncthreads();
+    WS wc;
+#pragma unroll
+    for (int i = 0; i < kFusedVPL; ++i) {
+      const int p = WS::pos(i);
+      wc.set(i, p < all ? sh.fin.cval[p] : 0.0f, p < all);
+    }
+    const int kk = wc.run(k, sh.fin.s);
+    wc.place(sh.fin.s, [&](int p, int at, int) { orow[at] = sh.fin.cidx[p]; });
+    for (int at = kk + tid; at < k; at += 1024) orow[at] = -1;   // not reached: k keys pass the floor
+    return;
+  }
+  WB wb;
+#pragma unroll
+  for (int i = 0; i < kFilterMaxLists / 1024; ++i) {
+    const int p = wb.pos(i);
+    const bool ok = p < all;
+    wb.set(i, ok ? ld_coherent(lval + (ok ? entry(p) : rbase)) : 0.0f, ok);
+  }
+  const int kk = wb.run(k, sh.b);
+  wb.place(sh.b, [&](int p, int at, int) { orow[at] = ld_coherent(lidx + entry(p)); });
+  for (int at = kk + tid; at < k; at += 1024) orow[at] = -1;   // not reached: k keys pass the floor
+}
+
 // Candidates left after a stage over n keys: k from every full chunk, and
 // min(k, rest) from the last.
 int64_t stage_out(int64_t n, int64_t k) {
@@ -697,6 +1029,49 @@ int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_
   else if (n <= 2048) topk_rows_kernel<8, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
   else topk_rows_kernel<16, FINITE><<<wg, 256, 0, st>>>(values, nn, ld, kk, out);
   return check_launch("qkv_topk");
+}
+
+}  // namespace
+}  // namespace qkv
+
+// Row tickets of topk_fused_kernel: a file-scope device array, one copy per
+// GPU, held until the process ends, zero when the code object loads.  Host
+// code never passes the array's name to a kernel (it is a host-side stand-in);
+// each GPU's copy is found with hipGetSymbolAddress once, with that GPU
+// current.  Calls take its slots in turn, so calls in flight together on one
+// GPU (on different streams) count in different words unless kTicketSlots
+// calls were issued between them; every completed call leaves its words zero.
+static __device__ __align__(256) uint32_t topk_tickets[qkv::kTicketSlots * qkv::kTicketSlotWords];
+
+namespace qkv {
+namespace {
+
+constexpr int kTicketDevices = 64;
+std::mutex g_ticket_mu;
+uint32_t* g_ticket_pool[kTicketDevices];
+std::atomic<uint32_t> g_ticket_next[kTicketDevices];
+
+// This call's ticket words on the current device.
+int ticket_slot(uint32_t** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kTicketDevices)
+    return fail(QKV_ERR_LAUNCH, "qkv_topk_ws: no current device below %d", kTicketDevices);
+  uint32_t* pool = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_ticket_mu);
+    if (!g_ticket_pool[dev]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(topk_tickets));
+      if (e != hipSuccess || !p)
+        return fail(QKV_ERR_LAUNCH, "qkv_topk_ws: hipGetSymbolAddress(topk_tickets) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_ticket_pool[dev] = static_cast<uint32_t*>(p);
+    }
+    pool = g_ticket_pool[dev];
+  }
+  const uint32_t slot = g_ticket_next[dev].fetch_add(1u, std::memory_order_relaxed) % kTicketSlots;
+  *out = pool + static_cast<int64_t>(slot) * kTicketSlotWords;
+  return QKV_OK;
 }
 
 }  // namespace
@@ -768,6 +1143,14 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
     int32_t* lidx = reinterpret_cast<int32_t*>(lval + rows * n_bounds * k);
     int32_t* lcnt = lidx + rows * n_bounds * k;
     dim3 grid(static_cast<unsigned>(n_bounds), static_cast<unsigned>(rows));
+    if (rows * n_bounds <= kFusedMaxWGs) {
+      uint32_t* tickets = nullptr;
+      if (int rc = ticket_slot(&tickets)) return rc;
+      topk_fused_kernel<<<grid, 1024, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds,
+                                               static_cast<uint64_t>(g_spin_ticks), tickets, win, lval, lidx,
+                                               lcnt, out);
+      return check_launch("qkv_topk_ws");
+    }
     topk_hist_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds, win);
     if (int rc = check_launch("qkv_topk_ws")) return rc;
     topk_filter_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), win, n_bounds,
@@ -807,6 +1190,11 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
     cur_n = stage_out(cur_n, k);
     buf ^= 1;
   }
+}
+
+QKV_EXPORT int qkv_topk_set_wait_limit(int64_t ticks) {
+  g_spin_ticks = ticks < 0 ? kSpinTicks : ticks;
+  return QKV_OK;
 }
 
 QKV_EXPORT int qkv_prefill_block_topk(const float* bmax, int64_t rows, int64_t n, int64_t ld, int64_t k,

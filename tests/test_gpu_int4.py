@@ -259,6 +259,93 @@ def test_topk_long_rows_one_chunk_over_k():
     assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
 
 
+def test_topk_long_rows_three_launch_grid():
+    # rows * chunks above 256: histogram, filter and final selection as three
+    # launches (the one-launch form needs every workgroup resident)
+    n, k = 131072, 1024
+    vals = torch.cat([_adversarial_rows(n, 11), _adversarial_rows(n, 12)[:2]])   # 9 rows x 32 chunks
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
+def test_topk_one_launch_workspace_reuse():
+    # the one-launch path's row tickets return to zero: one workspace serves
+    # calls of different shapes in a row, and every call is exact
+    g = torch.Generator().manual_seed(21)
+    ws = K.topk_workspace(8, 131072, 1024, DEV)
+    for rows, n, k in [(8, 131072, 1024), (3, 131072, 1024), (8, 131072, 1024), (5, 70000, 64),
+                       (8, 131072, 1)]:
+        vals = torch.randn((rows, n), generator=g)
+        vals[rows // 2, ::2] = 7.0   # ties across every chunk
+        got = K.block_topk(vals.to(DEV), k, workspace=ws).cpu().numpy()
+        assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k)), (rows, n, k)
+
+
+def test_topk_one_launch_ticket_pool_wraps():
+    # more one-launch calls than the library's ticket slots (4096): every
+    # completed call leaves its words zero, so a reused slot counts from zero
+    g = torch.Generator().manual_seed(23)
+    xs = [torch.randn((2, 9000), generator=g) for _ in range(3)]
+    xs[1][0, ::3] = 0.5   # ties
+    want = [O.topk_lowest_index(x.numpy(), 64) for x in xs]
+    dev = [x.to(DEV) for x in xs]
+    out = torch.empty((2, 64), dtype=torch.int32, device=DEV)
+    ws = K.topk_workspace(2, 9000, 64, DEV)
+    for i in range(4200):
+        K.block_topk(dev[i % 3], 64, out=out, workspace=ws)
+        if i % 700 == 0 or i >= 4197:
+            assert np.array_equal(out.cpu().numpy(), want[i % 3]), i
+
+
+def test_topk_one_launch_graph_replays():
+    # the one-launch path captured in a graph: replays with new inputs between
+    # them, each checked
+    n, k, rows = 131072, 1024, 8
+    g = torch.Generator().manual_seed(31)
+    x = torch.empty((rows, n), device=DEV)
+    out = torch.empty((rows, k), dtype=torch.int32, device=DEV)
+    ws = K.topk_workspace(rows, n, k, DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        K.block_topk(x.normal_(), k, out=out, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.block_topk(x, k, out=out, workspace=ws)
+    for rep in range(4):
+        host = torch.randn((rows, n), generator=g)
+        if rep == 2:
+            host[3] = 1.0
+        x.copy_(host)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), O.topk_lowest_index(host.numpy(), k)), rep
+
+
+def test_topk_one_launch_wait_limit_zero():
+    # a chunk that stops waiting for its row keeps its exact top-k instead of
+    # filtering by the row's floor (forced here from the host with a zero
+    # wait): the lists then exceed what the final step gathers into LDS, and
+    # the result is still exact
+    from kv_cache_amd import _lib
+    lib = _lib.load()
+    n, k = 131072, 1024
+    vals = _adversarial_rows(n, 41)
+    _lib.check(lib.qkv_topk_set_wait_limit(0))
+    try:
+        got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+        got2 = K.block_topk(vals.to(DEV), 3).cpu().numpy()
+    finally:
+        _lib.check(lib.qkv_topk_set_wait_limit(-1))
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+    assert np.array_equal(got2, O.topk_lowest_index(vals.numpy(), 3))
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()   # default wait again
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+
+
 @pytest.mark.parametrize("n,k,ld", [(1024, 64, 1024), (1024, 1, 1025), (1000, 100, 1000), (200, 64, 203),
                                     (513, 7, 513)])
 def test_topk_many_short_rows(n, k, ld):
