@@ -1003,8 +1003,6 @@ def run_blocksel(args) -> dict:
         ("rerank", run_rerank, rows * (n_tok * 4 + n_cand * d * 2 + kc)),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
-    if block is not None:   # one byte read and one written per history position
-        plan.insert(3, ("reuse_expand_blocks", run_expand, rows * hist_fixed * 2))
     kernels = {}
     for name, fn, nbytes in plan:
         gk = graph_of(repeated(fn))

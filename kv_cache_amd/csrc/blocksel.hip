@@ -43,27 +43,12 @@ constexpr int kRerankNT = 1024;
 constexpr int kMaxScan = kRerankNT * 40;   // scanned tokens per row in one workgroup
 
 // The row's top-|q| dims in selection order (descending |q|, lower dim on
-// ties; QK:123-145), from an LDS copy of q.  Ends with a barrier.
+// ties; QK:123-145), from an LDS copy of q (published by the barrier this
+// begins with).  Ends with a barrier.
 __device__ void rank_dims(const float* q_s, int count, int* sel_idx, float* sel_q) {
-  const int tid = threadIdx.x;
-  for (int s = tid; s < count; s += blockDim.x) {   // valid even for a NaN query
-    sel_idx[s] = 0;
-    sel_q[s] = q_s[0];
-  }
+  __shared__ __attribute__((aligned(16))) uint64_t key_s[kHD];
   __syncthreads();
-  for (int d = tid; d < kHD; d += blockDim.x) {
-    const float a = fabsf(q_s[d]);
-    int rank = 0;
-    for (int e = 0; e < kHD; ++e) {
-      const float c = fabsf(q_s[e]);
-      rank += (c > a) || (c == a && e < d);
-    }
-    if (rank < count) {
-      sel_idx[rank] = d;
-      sel_q[rank] = q_s[d];
-    }
-  }
-  __syncthreads();
+  rank_dims128(q_s, key_s, kHD, count, sel_idx, sel_q);
 }
 
 __device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }

@@ -62,6 +62,42 @@ __device__ void select_dims(const typename Elem<DT>::T* q_row, int head_dim, int
   }
 }
 
+// The same order for head_dim <= 128 dims whose query values sit in LDS
+// (q_s), with one 64-bit key per dim: the bits of |q_d| (for non-negative
+// floats the integer order is the numeric order) above 255 - d, so that
+// "larger |q|, or equal |q| and lower dim" is one unsigned compare and
+// rank(d) is the number of keys above d's.  The 128 keys (dims past head_dim
+// pad with 0, under every real key) are read back by broadcast 16-byte LDS
+// loads.  key_s: 128 LDS words of 8 bytes.  Every thread calls it; it begins
+// after a barrier that published q_s and ends with one.
+__device__ inline void rank_dims128(const float* q_s, uint64_t* key_s, int head_dim, int count, int* sel_idx,
+                                    float* sel_q) {
+  const int tid = threadIdx.x;
+  for (int s = tid; s < count; s += blockDim.x) {   // valid even for a NaN query
+    sel_idx[s] = 0;
+    sel_q[s] = q_s[0];
+  }
+  for (int d = tid; d < 128; d += blockDim.x)
+    key_s[d] = d < head_dim ? (static_cast<uint64_t>(__float_as_uint(q_s[d]) & 0x7FFFFFFFu) << 8) |
+                                  static_cast<uint64_t>(255 - d)
+                            : 0ull;
+  __syncthreads();
+  for (int d = tid; d < head_dim; d += blockDim.x) {
+    const uint64_t own = key_s[d];
+    int rank = 0;
+#pragma unroll 8   // (eight 16-byte reads in flight; a full unroll holds all 128 keys in registers)
+    for (int e = 0; e < 128; e += 2) {
+      const ulonglong2 c = *reinterpret_cast<const ulonglong2*>(key_s + e);
+      rank += (c.x > own ? 1 : 0) + (c.y > own ? 1 : 0);
+    }
+    if (rank < count) {
+      sel_idx[rank] = d;
+      sel_q[rank] = q_s[d];
+    }
+  }
+  __syncthreads();
+}
+
 template <template <int> class F, typename... A>
 int dispatch_dtype(int dtype, A&&... args) {
   switch (dtype) {

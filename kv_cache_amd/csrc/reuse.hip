@@ -67,31 +67,37 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     bool vec, float* __restrict__ out, int64_t out_ld) {
   using E = typename Elem<DT>::T;
   __shared__ float q_s[512];
+  __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
   __shared__ int sel_idx[kMaxDims];
   __shared__ float sel_q[kMaxDims];
   const int row = blockIdx.y, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
   const typename Elem<DT>::T* q_row = query + static_cast<int64_t>(row) * head_dim;
   for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
-  for (int s = tid; s < count; s += kRT) {   // valid even for a NaN query
-    sel_idx[s] = 0;
-    sel_q[s] = q_s[0];
-  }
   __syncthreads();
-  // rank(d) = #{e : |q_e| > |q_d| or (|q_e| == |q_d| and e < d)} (QK:123-145)
-  for (int d = tid; d < head_dim; d += kRT) {
-    const float a = fabsf(q_s[d]);
-    int rank = 0;
-    for (int e = 0; e < head_dim; ++e) {
-      const float c = fabsf(q_s[e]);
-      rank += (c > a) || (c == a && e < d);
+  if (head_dim <= 128) {   // uniform
+    rank_dims128(q_s, key_s, head_dim, count, sel_idx, sel_q);
+  } else {
+    for (int s = tid; s < count; s += kRT) {   // valid even for a NaN query
+      sel_idx[s] = 0;
+      sel_q[s] = q_s[0];
     }
-    if (rank < count) {
-      sel_idx[rank] = d;
-      sel_q[rank] = q_s[d];
+    __syncthreads();
+    // rank(d) = #{e : |q_e| > |q_d| or (|q_e| == |q_d| and e < d)} (QK:123-145)
+    for (int d = tid; d < head_dim; d += kRT) {
+      const float a = fabsf(q_s[d]);
+      int rank = 0;
+      for (int e = 0; e < head_dim; ++e) {
+        const float c = fabsf(q_s[e]);
+        rank += (c > a) || (c == a && e < d);
+      }
+      if (rank < count) {
+        sel_idx[rank] = d;
+        sel_q[rank] = q_s[d];
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
   const int t0 = (blockIdx.x * kRT + tid) * 8;
   if (t0 >= history) return;
   const E* base = kdm + b * sb + (h / group) * sh + t0;
@@ -118,13 +124,31 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = acc[i];
   } else {
+    // the row's last n < 8 tokens (or an unaligned copy): the same order,
+    // every load in flight at once at clamped in-row addresses, then only
+    // the n tokens stored (a load-then-add loop over runtime n waits for
+    // each load in turn)
     const int n = min(8, history - t0);
-    for (int s = 0; s < count; ++s) {
-      const E* p = base + sel_idx[s] * sd;
-      const float qs = sel_q[s];
-      for (int i = 0; i < n; ++i) acc[i] = acc[i] + qs * Elem<DT>::load(p + i);
+    for (int s0 = 0; s0 < count; s0 += 8) {
+      float v[8][8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const E* p = base + sel_idx[min(s0 + j, count - 1)] * sd;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[j][i] = Elem<DT>::load(p + min(i, n - 1));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < count) {
+          const float qs = sel_q[s0 + j];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[j][i];
+        }
+      }
     }
-    for (int i = 0; i < n; ++i) o[i] = acc[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < n) o[i] = acc[i];
   }
 }
 

@@ -167,6 +167,26 @@ def test_threshold_mask_matches_oracle(rows, n, k, ld):
     assert set(np.unique(got[:, :n]).tolist()) <= {0, 1} and (got[:, n:] == 7).all()   # nothing past n
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("d,hist,dims", [(128, 32790, 8), (128, 5, 8), (128, 4103, 16), (64, 1001, 8),
+                                         (200, 333, 12)])
+def test_reuse_partial_scores_ties_and_ragged_tails(dtype, d, hist, dims):
+    # GQA-native partial scores from the dim-major copy: queries with many
+    # equal magnitudes (the lower dim first), histories whose last 8-token
+    # group is short, head sizes under 128 (padded ranking keys) and above
+    # it (the general ranking)
+    gen = torch.Generator().manual_seed(d * 7 + hist + dims)
+    b, hq, hkv = 2, 4, 2
+    q = torch.randint(-3, 4, (b, hq, d), generator=gen).float() * 0.5
+    q[0, 1] = torch.randn(d, generator=gen)
+    k = torch.randn((b, hkv, hist, d), generator=gen).to(dtype)
+    kdm = torch.zeros((b, hkv, d, hist + 40), dtype=dtype, device=DEV)
+    RU.dim_major_append(k.to(DEV), kdm, 0, hist)
+    got = RU.reuse_partial_scores(q.to(dtype).to(DEV), kdm, hist, dims).cpu().numpy().reshape(b, hq, hist)
+    want = R.partial_scores(f32(q.to(dtype)), np.repeat(f32(k), hq // hkv, axis=1), dims)
+    assert np.array_equal(got, want)
+
+
 def test_reuse_select_ties_and_missing_masks():
     # Duplicate keys give equal scores: the lower index wins; previous masks absent.
     gen = torch.Generator().manual_seed(1)
