@@ -204,17 +204,19 @@ __global__ __launch_bounds__(kRT) void reuse_mask_kernel(const float* __restrict
 // where current | previous | previous_final is set at t, else -inf
 // (QK:160-216 without sink/recent protection, as EV:4257-4267 calls it).
 // The tile's union tokens are compacted in LDS so that every lane scores one.
-// DFIX = 128 fixes the head size so that a token's 16 row loads issue at once.
+// DFIX = 128 fixes the head size so that a token's 16 row loads issue at once;
+// registers are held to five waves per SIMD so that a row's 33 workgroups
+// times 32 rows are resident together (at three, a second batch waited).
 // ---------------------------------------------------------------------------
 template <int DT, int DFIX>
-__global__ __launch_bounds__(kRT) void reuse_scores_kernel(
+__global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void reuse_scores_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ key,
     int q_heads, int group, int history, int head_dim, int64_t sb, int64_t sh, int64_t st, bool kvec,
     const uint8_t* __restrict__ cur, const uint8_t* __restrict__ prev, const uint8_t* __restrict__ fin,
     int64_t mask_ld, bool mvec, float scaling, float* __restrict__ out, int64_t out_ld,
     float* __restrict__ cscore, int32_t* __restrict__ ctok, int32_t* __restrict__ ccnt, int64_t c_ld) {
   using E = typename Elem<DT>::T;
-  __shared__ float q_s[512];
+  __shared__ __attribute__((aligned(16))) float q_s[512];
   __shared__ uint16_t list[kScoreTile];
   __shared__ int wave_tot[kRT / 64];
   __shared__ int n_finite;
@@ -232,13 +234,21 @@ __global__ __launch_bounds__(kRT) void reuse_scores_kernel(
     if (fin) u |= *reinterpret_cast<const uint32_t*>(fin + moff);
 #pragma unroll
     for (int i = 0; i < 4; ++i) bits |= static_cast<uint32_t>(((u >> (8 * i)) & 0xFFu) != 0) << i;
-  } else {
-    for (int i = 0; i < 4 && t0 + i < history; ++i) {
-      bool f = cur[moff + i] != 0;
-      if (prev) f = f || prev[moff + i] != 0;
-      if (fin) f = f || fin[moff + i] != 0;
-      bits |= static_cast<uint32_t>(f) << i;
+  } else if (t0 < history) {
+    // the row's last few positions (or unaligned masks): every byte load in
+    // flight at once at clamped in-row positions, then the positions past
+    // the row dropped (short-circuit loads would wait for one another)
+    const int n = min(4, history - t0);
+    uint8_t c[4], p[4], f[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t at = moff + min(i, n - 1);
+      c[i] = cur[at];
+      p[i] = prev ? prev[at] : 0;
+      f[i] = fin ? fin[at] : 0;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bits |= static_cast<uint32_t>(i < n && (c[i] | p[i] | f[i]) != 0) << i;
   }
   float* orow = out + static_cast<int64_t>(row) * out_ld;
   const float ninf = -__builtin_huge_valf();
@@ -269,10 +279,44 @@ __global__ __launch_bounds__(kRT) void reuse_scores_kernel(
     const int t = tile0 + list[i];
     const E* kr = kbase + static_cast<int64_t>(t) * st;
     float acc = 0.0f;
-    if (kvec) {
-      const int hd = DFIX ? DFIX : head_dim;
+    if (DFIX && kvec) {
+      // the row's 16-byte loads first, 16 at a time (the whole row for
+      // 16-bit types), kept packed; q comes from LDS four values at a time
+      // where it is used (the empty asm keeps those reads from being
+      // hoisted next to the loads, which held 128 q values in registers)
+      constexpr int EPL = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
+      constexpr int NL = DFIX ? DFIX / EPL : 1, NB = NL < 16 ? NL : 16;   // (DFIX = 0 never gets here)
+      const float4* q4 = reinterpret_cast<const float4*>(q_s);
 #pragma unroll
-      for (int d = 0; d < hd; d += 8) {
+      for (int c0 = 0; c0 < NL; c0 += NB) {
+        uint4 w[NB];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) w[c] = *reinterpret_cast<const uint4*>(kr + (c0 + c) * EPL);
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+          asm volatile("" ::: "memory");
+          const uint32_t ww[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+          for (int h2 = 0; h2 < EPL / 4; ++h2) {
+            const float4 qv = q4[((c0 + c) * EPL) / 4 + h2];
+            const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float kv;
+              if constexpr (DT == QKV_DTYPE_FP32) {
+                kv = __uint_as_float(ww[e]);
+              } else {
+                const uint32_t half = (ww[(h2 * 4 + e) >> 1] >> (16 * ((h2 * 4 + e) & 1))) & 0xFFFFu;
+                kv = DT == QKV_DTYPE_BF16 ? bf16_to_f32(half) : f16bits_to_f32(half);
+              }
+              acc = acc + qa[e] * kv;
+            }
+          }
+        }
+      }
+    } else if (kvec) {
+#pragma unroll
+      for (int d = 0; d < head_dim; d += 8) {
         float v[8];
         load8<DT>(kr + d, v);
 #pragma unroll
