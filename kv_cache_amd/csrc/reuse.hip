@@ -401,8 +401,8 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
   __shared__ typename WS::Shared sh;
   WS ws;
   const int row = blockIdx.x, tid = threadIdx.x;
-  ws.load(values + static_cast<int64_t>(row) * ld, n);
-  ws.run(k, sh);
+  ws.load_count(values + static_cast<int64_t>(row) * ld, n, sh);   // the first digit counted as keys arrive
+  ws.run_counted(k, sh);
   if (thr_out) {
     // theta may be the lower bound of a boundary bin taken whole: the k-th
     // largest is the smallest key at or above it

@@ -348,21 +348,12 @@ struct WideSelect {
   // alive across the whole kernel.
   __device__ void refresh() { asm volatile("" : "+v"(valid)); }
 
-  // theta and kr for the k largest valid keys; returns kk = min(k, valid keys).
-  // Every thread calls it; the caller's earlier uses of sh have completed
-  // (a barrier since).
-  //
-  // Two barriers per 12-bit digit: the histograms alternate between passes,
-  // so a pass clears the next pass's histogram after its first barrier
-  // instead of behind a barrier of its own, and after the second barrier
-  // (the per-wave sums) every wave finds the boundary bin itself -- the wave
-  // of bins holding the kr-th key from the top, then the bin among its 256 --
-  // instead of waiting for one thread to publish it.
-  __device__ int run(int k, Shared& sh) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int j = 0; j < NB / NT; ++j) sh.hist[0][tid + NT * j] = 0;
-    uint32_t umax = 0, umin = 0xFFFFFFFFu;
+  // The row's largest and smallest valid key and the count of valid keys,
+  // reduced over the workgroup through sh.red (one barrier).
+  __device__ void reduce_row(Shared& sh, uint32_t& umax, uint32_t& umin, int& nval) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    umax = 0;
+    umin = 0xFFFFFFFFu;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       if (on(i)) {
@@ -370,7 +361,7 @@ struct WideSelect {
         umin = min(umin, u[i]);
       }
     }
-    int nval = wave_incl_scan_dpp(__popcll(valid));
+    nval = wave_incl_scan_dpp(__popcll(valid));
     umax = wave_minmax_u32<true>(umax);
     umin = wave_minmax_u32<false>(umin);
     if (lane == 63) {
@@ -388,25 +379,67 @@ struct WideSelect {
       umin = min(umin, sh.red[w][1]);
       nval += static_cast<int>(sh.red[w][2]);
     }
-    kk = min(k, nval);
-    kr = kk;
-    uint32_t prefix = umax, mask = 0xFFFFFFFFu;
-    int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
-    if (remaining) {
-      mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
-      prefix = umax & mask;
+  }
+
+  // The bin of a complete 4096-bin histogram that holds the kr-th key from
+  // the top, the rank kr within it, and whether the bin is taken whole.
+  // Every thread reads its 4 bins (clearing other's in the same step, the
+  // next pass's histogram) and publishes its wave's sum; after that one
+  // barrier every wave finds the boundary itself -- the wave of bins holding
+  // the kr-th key, then the bin among its 256 -- instead of waiting for one
+  // thread to publish it.
+  __device__ void boundary(Shared& sh, const int* hist, int* other, int& bin, int& krl, int& whole) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // (the other histogram was last read before this pass's atomics)
+#pragma unroll
+    for (int j = 0; j < NB / NT; ++j) other[tid + NT * j] = 0;
+    // Thread t owns bins NB-1-4t .. NB-4-4t (descending), so the keys in
+    // higher bins are those of lower threads and of its own earlier bins.
+    int tot = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tot += hist[NB - 1 - 4 * tid - j];
+    const int incl = wave_incl_scan_dpp(tot);
+    if (lane == 63) sh.wave_sum[wave] = incl;
+    __syncthreads();
+    const int wsum = lane < NW ? sh.wave_sum[lane] : 0;
+    const int wcum = wave_incl_scan_dpp(wsum);
+    const int bw = __builtin_ctzll(__ballot(lane < NW && wcum >= kr));   // the boundary's wave of bins
+    const int t2 = bw * 64 + lane;
+    int c[4], tot2 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = hist[NB - 1 - 4 * t2 - j];
+      tot2 += c[j];
     }
-    if (kk == nval) {   // every valid key is taken
-      prefix = umin;
-      kr = 0x7FFFFFFF;
-      remaining = 0;
+    int above = __builtin_amdgcn_readlane(wcum - wsum, bw) + wave_incl_scan_dpp(tot2) - tot2;
+    const int bl = __builtin_ctzll(__ballot(above < kr && kr <= above + tot2));   // its lane
+    bin = 0;
+    krl = 0;
+    whole = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (above < kr && kr <= above + c[j]) {
+        bin = NB - 1 - 4 * t2 - j;
+        krl = kr - above;
+        whole = krl == c[j];
+      }
+      above += c[j];
     }
-    // One shared histogram of 4096 bins per pass: a 12-bit digit of sign,
-    // exponent and top mantissa bits spreads typical scores over enough bins
-    // that a wave's atomics rarely collide (an 8-bit digit of such floats
-    // holds a handful of exponents and serializes on them).
-    const bool passes = remaining > 0;
-    int buf = 0;
+    bin = __builtin_amdgcn_readlane(bin, bl);
+    krl = __builtin_amdgcn_readlane(krl, bl);
+    whole = __builtin_amdgcn_readlane(whole, bl);
+  }
+
+  // Radix passes over the bits below the resolved prefix: one shared
+  // histogram of 4096 bins per pass (a 12-bit digit of sign, exponent and
+  // top mantissa bits spreads typical scores over enough bins that a wave's
+  // atomics rarely collide; an 8-bit digit of such floats holds a handful of
+  // exponents and serializes on them), alternating between sh.hist[buf] and
+  // the other, two barriers per digit.  Ends with a barrier when it counted.
+  __device__ void passes(Shared& sh, uint32_t prefix, uint32_t mask, int remaining, int buf, uint32_t umin,
+                         bool counted) {
+    const int lane = threadIdx.x & 63;
+    const bool any = counted || remaining > 0;
     while (remaining > 0) {   // uniform across the workgroup
       refresh();
       const int shift = remaining > RB ? remaining - RB : 0;
@@ -426,42 +459,8 @@ struct WideSelect {
       at_min = wave_incl_scan_dpp(at_min);
       if (lane == 63 && at_min) atomicAdd(&hist[(umin >> shift) & dmask], at_min);
       __syncthreads();
-      // (the other histogram was last read before this pass's atomics)
-#pragma unroll
-      for (int j = 0; j < NB / NT; ++j) sh.hist[buf ^ 1][tid + NT * j] = 0;
-      // Thread t owns bins NB-1-4t .. NB-4-4t (descending), so the keys in
-      // higher bins are those of lower threads and of its own earlier bins.
-      int tot = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) tot += hist[NB - 1 - 4 * tid - j];
-      const int incl = wave_incl_scan_dpp(tot);
-      if (lane == 63) sh.wave_sum[wave] = incl;
-      __syncthreads();
-      const int wsum = lane < NW ? sh.wave_sum[lane] : 0;
-      const int wcum = wave_incl_scan_dpp(wsum);
-      const int bw = __builtin_ctzll(__ballot(lane < NW && wcum >= kr));   // the boundary's wave of bins
-      const int t2 = bw * 64 + lane;
-      int c[4], tot2 = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = hist[NB - 1 - 4 * t2 - j];
-        tot2 += c[j];
-      }
-      int above = __builtin_amdgcn_readlane(wcum - wsum, bw) + wave_incl_scan_dpp(tot2) - tot2;
-      const int bl = __builtin_ctzll(__ballot(above < kr && kr <= above + tot2));   // its lane
-      int bin = 0, krl = 0, whole = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (above < kr && kr <= above + c[j]) {
-          bin = NB - 1 - 4 * t2 - j;
-          krl = kr - above;
-          whole = krl == c[j];
-        }
-        above += c[j];
-      }
-      bin = __builtin_amdgcn_readlane(bin, bl);
-      krl = __builtin_amdgcn_readlane(krl, bl);
-      whole = __builtin_amdgcn_readlane(whole, bl);
+      int bin, krl, whole;
+      boundary(sh, hist, sh.hist[buf ^ 1], bin, krl, whole);
       prefix |= static_cast<uint32_t>(bin) << shift;
       mask |= dmask << shift;
       kr = krl;
@@ -472,8 +471,93 @@ struct WideSelect {
         break;
       }
     }
-    if (passes) __syncthreads();   // the last pass's histogram reads are done before sh is reused
+    if (any) __syncthreads();   // the last histogram reads are done before sh is reused
     theta = prefix;
+  }
+
+  // theta and kr for the k largest valid keys; returns kk = min(k, valid keys).
+  // Every thread calls it; the caller's earlier uses of sh have completed
+  // (a barrier since).  The bits the row's largest and smallest keys share
+  // are skipped.
+  __device__ int run(int k, Shared& sh) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < NB / NT; ++j) sh.hist[0][tid + NT * j] = 0;
+    uint32_t umax, umin;
+    int nval;
+    reduce_row(sh, umax, umin, nval);
+    kk = min(k, nval);
+    kr = kk;
+    uint32_t prefix = umax, mask = 0xFFFFFFFFu;
+    int remaining = (umax == umin || kk == 0) ? 0 : 32 - __builtin_clz(umax ^ umin);
+    if (remaining) {
+      mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
+      prefix = umax & mask;
+    }
+    if (kk == nval) {   // every valid key is taken
+      prefix = umin;
+      kr = 0x7FFFFFFF;
+      remaining = 0;
+    }
+    passes(sh, prefix, mask, remaining, 0, umin, false);
+    return kk;
+  }
+
+  // load() with run()'s first digit counted on the way: every load is
+  // issued first, then each key's top 12 bits go into sh.hist[0] as the key
+  // arrives, so the LDS atomics overlap the row's transfer instead of
+  // following it.  run_counted() then resolves that digit and continues
+  // with run()'s passes.  -inf keys (a flood of unscored positions) are
+  // counted by ballot.  Every thread calls both; the caller's earlier uses
+  // of sh have completed (a barrier since).
+  __device__ void load_count(const float* __restrict__ vals, int n, Shared& sh) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
+    const int base = pos(0);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      u[i] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(rsrc, (base + 64 * i) * 4, 0, 0));
+#pragma unroll
+    for (int j = 0; j < NB / NT; ++j) sh.hist[0][tid + NT * j] = 0;
+    const int nv = min(max((n - base + 63) / 64, 0), VPL);
+    valid = nv >= 64 ? ~0ull : ((1ull << nv) - 1ull);
+    __syncthreads();   // the histogram is clear (the loads are in flight meanwhile)
+    int ninf = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      u[i] = f32_sortable(__uint_as_float(u[i]));
+      if (FINITE && u[i] == kNegInfKey) valid &= ~(1ull << i);
+      if (on(i)) {
+        if (u[i] == kNegInfKey) ++ninf;
+        else atomicAdd(&sh.hist[0][u[i] >> (32 - RB)], 1);
+      }
+    }
+    ninf = wave_incl_scan_dpp(ninf);
+    if (lane == 63 && ninf) atomicAdd(&sh.hist[0][kNegInfKey >> (32 - RB)], ninf);
+  }
+
+  __device__ int run_counted(int k, Shared& sh) {
+    uint32_t umax, umin;
+    int nval;
+    reduce_row(sh, umax, umin, nval);   // (its barrier also completes load_count's atomics)
+    kk = min(k, nval);
+    kr = kk;
+    if (kk == nval) {   // every valid key is taken
+      kr = 0x7FFFFFFF;
+      passes(sh, umin, 0xFFFFFFFFu, 0, 0, umin, true);
+      return kk;
+    }
+    int bin, krl, whole;
+    boundary(sh, sh.hist[0], sh.hist[1], bin, krl, whole);
+    kr = krl;
+    const uint32_t prefix = static_cast<uint32_t>(bin) << (32 - RB);
+    if (whole) {
+      kr = 0x7FFFFFFF;
+      passes(sh, prefix, 0xFFFFFFFFu, 0, 1, umin, true);
+    } else {
+      passes(sh, prefix, ~((1u << (32 - RB)) - 1u), 32 - RB, 1, umin, true);
+    }
     return kk;
   }
 
