@@ -469,6 +469,7 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 // either way, and the lists keep token order, so both paths select and
 // place the same entries (ties to the lower token).
 constexpr int kMaxTiles = kWideMax / kScoreTile;
+static_assert(kMaxTiles < 64, "the final selection's tile search takes six steps");
 
 template <int VPL, int VPLC>
 __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
@@ -487,6 +488,14 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   __shared__ int n_fin;
   const int row = blockIdx.x, tid = threadIdx.x;
   uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  // the tile lists' lengths first (one load per tile, n_tiles <= 40), in
+  // flight while the protected ranges are written
+  int len = 0, nf = 0;
+  if (tid < 64 && cscore && tid < n_tiles) {
+    const int32_t* cn = ccnt + static_cast<int64_t>(row) * n_tiles * 2;
+    len = cn[2 * tid];
+    nf = cn[2 * tid + 1];
+  }
   // the protected ranges, 16 bytes per store where the row is 16-byte aligned
   const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
   for (int t0 = 16 * tid; t0 < body; t0 += 16 * kWideNT) {
@@ -504,10 +513,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     *reinterpret_cast<uint4*>(hrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
   }
   for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
-  if (tid < 64) {   // tile list offsets: one load per tile, a wave scan (n_tiles <= 40)
-    const int32_t* cn = ccnt + static_cast<int64_t>(row) * n_tiles * 2;
-    const bool on = cscore && tid < n_tiles;
-    const int len = on ? cn[2 * tid] : 0, nf = on ? cn[2 * tid + 1] : 0;
+  if (tid < 64) {   // tile list offsets: a wave scan of the lengths
     const int incl = wave_incl_scan_dpp(len), fin_all = wave_incl_scan_dpp(nf);
     if (tid <= n_tiles) tile_off[tid] = incl - len;   // tile_off[n_tiles] = the total
     if (tid == 63) n_fin = fin_all;
@@ -531,11 +537,13 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     for (int i = 0; i < VPLC; ++i) {
       const int p = WC::pos(i);
       const bool ok = p < total;
-      int lo = 0, hi = n_tiles - 1;   // the last tile whose list starts at or before p
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tile_off[mid] <= p) lo = mid;
-        else hi = mid - 1;
+      // the last tile whose list starts at or before p, in six fixed steps
+      // (so the VPLC searches interleave instead of running one by one)
+      int lo = 0;
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1) {
+        const int mid = lo + step;
+        lo = (mid < n_tiles && tile_off[min(mid, n_tiles)] <= p) ? mid : lo;
       }
       const int64_t e = static_cast<int64_t>(lo) * kScoreTile + (p - tile_off[lo]);
       tok[i] = ok ? trow[e] : 0;

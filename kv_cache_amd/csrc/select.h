@@ -511,7 +511,7 @@ struct WideSelect {
   // counted by ballot.  Every thread calls both; the caller's earlier uses
   // of sh have completed (a barrier since).
   __device__ void load_count(const float* __restrict__ vals, int n, Shared& sh) {
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
     const int base = pos(0);
@@ -528,13 +528,24 @@ struct WideSelect {
     for (int i = 0; i < VPL; ++i) {
       u[i] = f32_sortable(__uint_as_float(u[i]));
       if (FINITE && u[i] == kNegInfKey) valid &= ~(1ull << i);
-      if (on(i)) {
-        if (u[i] == kNegInfKey) ++ninf;
-        else atomicAdd(&sh.hist[0][u[i] >> (32 - RB)], 1);
-      }
+      count(i, sh, ninf);
     }
+    count_done(sh, ninf);
+  }
+
+  // The counting of load_count() for keys given one by one with set(): the
+  // caller clears sh.hist[0] before a barrier, then calls count(i) after
+  // each set(i) (so the atomics follow the keys' loads as they arrive) and
+  // count_done() once; run_counted() follows.
+  __device__ void count(int i, Shared& sh, int& ninf) {
+    if (on(i)) {
+      if (u[i] == kNegInfKey) ++ninf;
+      else atomicAdd(&sh.hist[0][u[i] >> (32 - RB)], 1);
+    }
+  }
+  __device__ void count_done(Shared& sh, int ninf) {
     ninf = wave_incl_scan_dpp(ninf);
-    if (lane == 63 && ninf) atomicAdd(&sh.hist[0][kNegInfKey >> (32 - RB)], ninf);
+    if ((threadIdx.x & 63) == 63 && ninf) atomicAdd(&sh.hist[0][kNegInfKey >> (32 - RB)], ninf);
   }
 
   __device__ int run_counted(int k, Shared& sh) {
