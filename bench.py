@@ -972,16 +972,20 @@ def run_blocksel(args) -> dict:
     def run_scan():
         for layer in range(layers):
             st = steps[layer]
+            k = ks[layer][:, :, :kc]
             _lib.check(lib.qkv_block_scan_scores(qs[layer].data_ptr(), st.kdm.data_ptr(),
-                                                 _lib.strides(*st.kdm.stride()), b, hq, hkv, hf, d,
-                                                 st.blocks.data_ptr(), n_scan, st.block, st.dims,
-                                                 st.partial.data_ptr(), n_tok, _lib.stream_of(qs[layer])))
+                                                 _lib.strides(*st.kdm.stride()), k.data_ptr(),
+                                                 _lib.strides(*k.stride()), b, hq, hkv, hf, d,
+                                                 st.blocks.data_ptr(), n_scan, st.block, st.dims, scaling,
+                                                 st.partial.data_ptr(), st.full.data_ptr(), n_tok,
+                                                 _lib.stream_of(qs[layer])))
 
     def run_rerank():
         for layer in range(layers):
             st, k = steps[layer], ks[layer][:, :, :kc]
             _lib.check(lib.qkv_block_rerank(qs[layer].data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), b, hq, hkv,
-                                            kc, d, st.partial.data_ptr(), n_tok, st.blocks.data_ptr(), n_scan,
+                                            kc, d, st.partial.data_ptr(), st.full.data_ptr(), n_tok,
+                                            st.blocks.data_ptr(), n_scan,
                                             st.block, n_cand, n_keep, c["sink"], c["recent"], 1, scaling,
                                             st.keep.data_ptr(), st.capacity, st.attn_ids.data_ptr(), n_out,
                                             _lib.stream_of(k)))
@@ -997,10 +1001,10 @@ def run_blocksel(args) -> dict:
         # a block's metadata record per query head, plus the f32 score written
         ("block_scores", run_scores, rows * nb * (meta_bytes + 4)),
         ("block_topk", run_topk, rows * nb * 4),
-        # the S dims of every scanned token (dim-major) and its f32 partial score
-        ("scan_partial", run_scan, rows * n_tok * (steps[0].dims * 2 + 4)),
-        # partial scores read once, the candidates' bf16 K rows, the final mask bytes
-        ("rerank", run_rerank, rows * (n_tok * 4 + n_cand * d * 2 + kc)),
+        # every scanned token's S dims (dim-major) and bf16 K row, its f32 partial and full scores
+        ("scan_partial", run_scan, rows * n_tok * (steps[0].dims * 2 + d * 2 + 8)),
+        # partial scores read once, the candidates' full scores, the final mask bytes
+        ("rerank", run_rerank, rows * (n_tok * 4 + n_cand * 4 + kc)),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
     kernels = {}

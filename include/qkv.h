@@ -465,11 +465,17 @@ int qkv_block_scores(int kind, const void* query, const void* key, const int64_t
 /* Partial scores of the tokens of each row's chosen blocks (EV:5576-5581):
  * position p is token blocks[r, p / block] * block + p % block, scored on
  * the row's top-|q| dims from the dim-major K copy (qkv_dim_major_append);
- * positions at or past history get -inf.  out f32 [rows, >= n_scan*block]. */
-int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int64_t batch,
-                          int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
-                          const int32_t* blocks, int64_t n_scan, int64_t block, int64_t dim_count, float* out,
-                          int64_t out_ld, void* stream);
+ * positions at or past history get -inf.  out f32 [rows, >= n_scan*block].
+ * full (optional, same layout and out_ld; NULL: not written): each
+ * position's full-D score scaling * q.K in the reference's fp32 order, read
+ * from key (bf16 [B,Hkv,*,D] with k_strides, rows 16-byte aligned) -- the
+ * scores qkv_block_rerank ranks its candidates by, computed here across the
+ * launch's workgroups instead of in one workgroup per row. */
+int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                          const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
+                          int64_t kv_heads, int64_t history, int64_t head_dim, const int32_t* blocks, int64_t n_scan,
+                          int64_t block, int64_t dim_count, float scaling, float* out, float* full, int64_t out_ld,
+                          void* stream);
 
 /* Block scores of the qboracle selector (EV:5030-5044): out[r, j] = the
  * largest partial score, on row r's top-|q| dims (ties to the lower dim,
@@ -513,10 +519,12 @@ int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t protect_si
  * EV:5607-5615) and attn_ids [rows, n_out] for qkv_token_attention: the kept
  * tokens ascending (-1 where protected or not filled), the sink range, the
  * recent range, the current token.  n_scan * block <= 40960,
- * n_keep <= n_cand <= 4096. */
+ * n_keep <= n_cand <= 4096.  full (optional, partial's layout): the full
+ * scores qkv_block_scan_scores wrote; NULL computes them here from key. */
 int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
-                     int64_t kv_heads, int64_t key_count, int64_t head_dim, const float* partial, int64_t partial_ld,
-                     const int32_t* blocks, int64_t n_scan, int64_t block, int64_t n_cand, int64_t n_keep,
+                     int64_t kv_heads, int64_t key_count, int64_t head_dim, const float* partial, const float* full,
+                     int64_t partial_ld, const int32_t* blocks, int64_t n_scan, int64_t block, int64_t n_cand,
+                     int64_t n_keep,
                      int64_t protect_sink, int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
                      int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream);
 

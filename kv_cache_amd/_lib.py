@@ -86,15 +86,15 @@ _PROTOTYPES = {
                                      _vp]),
     "qkv_block_scores": (_i32, [_i32, _vp, _vp, _P(_i64), _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _vp, _i64, _vp]),
-    "qkv_block_scan_scores": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
-                                     _i64, _vp]),
+    "qkv_block_scan_scores": (_i32, [_vp, _vp, _P(_i64), _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
+                                     _i64, _i64, _f32, _vp, _vp, _i64, _vp]),
     "qkv_block_max_partial_scores": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
                                             _i64, _vp]),
     "qkv_brep_partial_scores": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _P(_i64), _i64, _i64,
                                        _i64, _f64, _vp]),
     "qkv_final_list_count": (_i64, [_i64, _i64, _i64, _i64, _i32]),
-    "qkv_block_rerank": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
-                                _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _vp]),
+    "qkv_block_rerank": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
+                                _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _vp]),
 }
 
 _LIB = None

@@ -114,6 +114,7 @@ class BlockSelectDecodeStep:
         self.blocks = torch.empty(rows * n_scan, dtype=torch.int32, device=device)
         self.topk_ws = topk_workspace(rows, self.meta_blocks, n_scan, device)
         self.partial = torch.empty(rows * n_scan * self.block, dtype=torch.float32, device=device)
+        self.full = torch.empty_like(self.partial)   # full-D scores of the scanned tokens (rerank's candidates)
         self.keep = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.n_out_max = int(lib.qkv_final_list_count(cap - 1, n_keep, self.sink, self.recent, int(self.keep_self)))
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
@@ -201,15 +202,17 @@ class BlockSelectDecodeStep:
             block_topk(self.bscore[:, :nb], n_scan, out=blocks, workspace=self.topk_ws)
             n_tok = n_scan * self.block
             partial = self.partial[: self.rows * n_tok]
+            full = self.full[: self.rows * n_tok]
             _lib.check(lib.qkv_block_scan_scores(
-                q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), self.batch, self.q_heads,
-                self.kv_heads, history, self.head_dim, blocks.data_ptr(), n_scan, self.block, self.dims,
-                partial.data_ptr(), n_tok, stream))
+                q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), key.data_ptr(), ks, self.batch,
+                self.q_heads, self.kv_heads, history, self.head_dim, blocks.data_ptr(), n_scan, self.block,
+                self.dims, float(scaling), partial.data_ptr(), full.data_ptr(), n_tok, stream))
             n_out = int(lib.qkv_final_list_count(history, n_keep, self.sink, self.recent, int(self.keep_self)))
             ids = self.attn_ids[: self.rows * n_out]
             _lib.check(lib.qkv_block_rerank(
                 q.data_ptr(), key.data_ptr(), ks, self.batch, self.q_heads, self.kv_heads, key_count, self.head_dim,
-                partial.data_ptr(), n_tok, blocks.data_ptr(), n_scan, self.block, n_cand, n_keep, self.sink,
+                partial.data_ptr(), full.data_ptr(), n_tok, blocks.data_ptr(), n_scan, self.block, n_cand, n_keep,
+                self.sink,
                 self.recent, int(self.keep_self), float(scaling), self.keep.data_ptr(), self.capacity,
                 ids.data_ptr(), n_out, stream))
         self.n_out = n_out

@@ -53,6 +53,33 @@ __device__ void rank_dims(const float* q_s, int count, int* sel_idx, float* sel_
 
 __device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
 
+// scaling * sum_d q[d] * K[d] over d ascending, separately rounded (the
+// reference's fp32 order), for one bf16 K row of kHD values (16-byte
+// aligned) and q in LDS (16-byte aligned).  The row's loads go out first;
+// q is read eight values per 16-byte word where it is used (the empty asm
+// keeps those reads from being hoisted all at once next to the row loads).
+__device__ __forceinline__ float full_score(const uint16_t* __restrict__ krow, const float* q_s, float scaling) {
+  const uint4* kr = reinterpret_cast<const uint4*>(krow);
+  uint4 x[kHD / 8];
+#pragma unroll
+  for (int c = 0; c < kHD / 8; ++c) x[c] = kr[c];
+  const float4* q4 = reinterpret_cast<const float4*>(q_s);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kHD / 8; ++c) {
+    asm volatile("" ::: "memory");
+    const float4 qa = q4[2 * c], qb = q4[2 * c + 1];
+    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = acc + qv[2 * e] * __uint_as_float(w[e] << 16);
+      acc = acc + qv[2 * e + 1] * __uint_as_float(w[e] & 0xFFFF0000u);
+    }
+  }
+  return acc * scaling;
+}
+
 // ---------------------------------------------------------------------------
 // Metadata.  qbb: per block a 512-byte record [min(128) | max(128)] of bf16
 // (exact: K is bf16).  brep: per block R int32 token indices, descending
@@ -179,8 +206,9 @@ __global__ __launch_bounds__(kBT) void block_scores_kernel(
 __global__ __launch_bounds__(kBT) void scan_partial_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ kdm, int q_heads, int group, int64_t db,
     int64_t dh, int64_t dd, const int32_t* __restrict__ blocks, int n_scan, int block, int history, int count,
-    float* __restrict__ out, int64_t out_ld) {
-  __shared__ float q_s[kHD];
+    float* __restrict__ out, int64_t out_ld, const uint16_t* __restrict__ key, int64_t sb, int64_t sh, int64_t st,
+    float scaling, float* __restrict__ full) {
+  __shared__ __attribute__((aligned(16))) float q_s[kHD];
   __shared__ int sel_idx[kHD];
   __shared__ float sel_q[kHD];
   const int row = blockIdx.y, tid = threadIdx.x;
@@ -206,6 +234,12 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
     }
   }
   out[static_cast<int64_t>(row) * out_ld + p] = acc;
+  if (full) {   // the full-D score the rerank ranks its candidates by (every scanned position)
+    const bool in = tok >= 0 && tok < history;
+    const float f = in ? full_score(key + b * sb + (h / group) * sh + static_cast<int64_t>(tok) * st, q_s, scaling)
+                       : -__builtin_huge_valf();
+    full[static_cast<int64_t>(row) * out_ld + p] = f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -267,8 +301,9 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
 template <int VPL1, int VPL2>
 __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, int q_heads, int group, int64_t sb,
-    int64_t sh, int64_t st, const float* __restrict__ partial, int64_t partial_ld, const int32_t* __restrict__ blocks,
-    int n_scan, int block, int history, int key_count, int n_cand, int n_keep, int sink_end, int recent_start,
+    int64_t sh, int64_t st, const float* __restrict__ partial, const float* __restrict__ full, int64_t partial_ld,
+    const int32_t* __restrict__ blocks, int n_scan, int block, int history, int key_count, int n_cand, int n_keep,
+    int sink_end, int recent_start,
     int rec_begin, int n_rec, int keep_self, float scaling, uint8_t* __restrict__ keep_mask, int64_t keep_ld,
     int32_t* __restrict__ attn_ids, int n_out) {
   using WS1 = WideSelect<VPL1, true>;
@@ -277,8 +312,8 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     typename WS1::Shared a;
     typename WS2::Shared b;
   } lds;
-  __shared__ float q_s[kHD];
-  __shared__ int32_t cand[kMaxCand];
+  __shared__ __attribute__((aligned(16))) float q_s[kHD];
+  __shared__ int32_t cand[kMaxCand], cand_pos[kMaxCand];
   const int row = blockIdx.x, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
   for (int d = tid; d < kHD; d += kRerankNT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
@@ -294,32 +329,20 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   ws1.place(lds.a, [&](int pos, int o, int) {
     const int jb = pos / block;
     cand[o] = brow[jb] * block + (pos - jb * block);
+    cand_pos[o] = pos;
   });
 
-  // 2. full scores of the candidates, 3. the kept ones
+  // 2. full scores of the candidates (computed by the scan launch when full
+  // is given: then only read back here), 3. the kept ones
   WS2 ws2;
   const uint16_t* kb = key + b * sb + (h / group) * sh;
+  const float* frow = full ? full + static_cast<int64_t>(row) * partial_ld : nullptr;
 #pragma unroll
   for (int i = 0; i < VPL2; ++i) {
     const int ci = WS2::pos(i);
     const bool ok = ci < kk1;
     float acc = 0.0f;
-    if (ok) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(cand[ci]) * st);
-      uint4 x[kHD / 8];
-#pragma unroll
-      for (int c = 0; c < kHD / 8; ++c) x[c] = kr[c];
-#pragma unroll
-      for (int c = 0; c < kHD / 8; ++c) {
-        const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc = acc + q_s[8 * c + 2 * e] * __uint_as_float(w[e] << 16);
-          acc = acc + q_s[8 * c + 2 * e + 1] * __uint_as_float(w[e] & 0xFFFF0000u);
-        }
-      }
-      acc = acc * scaling;
-    }
+    if (ok) acc = frow ? frow[cand_pos[ci]] : full_score(kb + static_cast<int64_t>(cand[ci]) * st, q_s, scaling);
     ws2.set(i, acc, ok);
   }
   const int kk2 = ws2.run(n_keep, lds.b);
@@ -523,9 +546,10 @@ QKV_EXPORT int qkv_block_scores(int kind, const void* query, const void* key, co
 }
 
 QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
-                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
-                                     int64_t head_dim, const int32_t* blocks, int64_t n_scan, int64_t block,
-                                     int64_t dim_count, float* out, int64_t out_ld, void* stream) {
+                                     const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
+                                     int64_t kv_heads, int64_t history, int64_t head_dim, const int32_t* blocks,
+                                     int64_t n_scan, int64_t block, int64_t dim_count, float scaling, float* out,
+                                     float* full, int64_t out_ld, void* stream) {
   const char* what = "qkv_block_scan_scores";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
@@ -533,12 +557,17 @@ QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_majo
   if (history <= 0 || block <= 0 || n_scan <= 0 || n_scan * block >= (int64_t(1) << 30) || out_ld < n_scan * block)
     return fail(QKV_ERR_INVALID, "%s: need history, block, n_scan > 0 and out_ld >= n_scan * block", what);
   if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the copy's token axis must be contiguous", what);
+  if (full && (!key || !k_strides)) return fail(QKV_ERR_INVALID, "%s: full scores need key and k_strides", what);
+  if (full && (k_strides[3] != 1 || !kv_aligned(key, k_strides)))
+    return fail(QKV_ERR_INVALID, "%s: K rows must be contiguous and 16-byte aligned", what);
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
   dim3 grid(static_cast<unsigned>(cdiv(n_scan * block, kBT)), static_cast<unsigned>(batch * q_heads));
   scan_partial_kernel<<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
       static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], blocks,
-      static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld);
+      static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld,
+      static_cast<const uint16_t*>(key), full ? k_strides[0] : 0, full ? k_strides[1] : 0, full ? k_strides[2] : 0,
+      scaling, full);
   return check_launch(what);
 }
 
@@ -611,8 +640,8 @@ QKV_EXPORT int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t
 
 QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch,
                                 int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
-                                const float* partial, int64_t partial_ld, const int32_t* blocks, int64_t n_scan,
-                                int64_t block, int64_t n_cand, int64_t n_keep, int64_t protect_sink,
+                                const float* partial, const float* full, int64_t partial_ld, const int32_t* blocks,
+                                int64_t n_scan, int64_t block, int64_t n_cand, int64_t n_keep, int64_t protect_sink,
                                 int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
                                 int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream) {
   const char* what = "qkv_block_rerank";
@@ -642,7 +671,8 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
    return with_cand_vpl(n_cand, [&](auto vpl2) {
     rerank_kernel<decltype(vpl)::value, decltype(vpl2)::value><<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
         static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),
-        static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], partial, partial_ld, blocks,
+        static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], partial, full, partial_ld,
+        blocks,
         static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), static_cast<int>(key_count),
         static_cast<int>(n_cand), static_cast<int>(n_keep), static_cast<int>(sink_end),
         static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec), keep_self ? 1 : 0,

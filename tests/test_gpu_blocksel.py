@@ -194,3 +194,33 @@ def test_limits_are_errors():
         BS.BlockSelectDecodeStep("qbb16q8s50cand20", 1, 4, 2, 128, 40000)
     with pytest.raises(RuntimeError, match="at most 64"):
         BS.BlockSelectDecodeStep("brep128r2q8s6cand2", 1, 4, 2, 128, 4000)
+
+
+@pytest.mark.parametrize("mode,t", [("qbb64q8s3cand3", 4000), ("brep16r4q8s12cand4", 3001)])
+def test_rerank_with_and_without_scan_full_scores(mode, t):
+    # The step hands the rerank the full-D scores its scan launch computed;
+    # the rerank computing them itself (full = NULL) keeps the same masks and
+    # token lists, and both match the step's.
+    hq, hkv = 8, 2
+    k, v, g = _kv(1, hkv, t, 41)
+    q = torch.randn((1, hq, 128), generator=g).to(torch.bfloat16).to(DEV)
+    step = BS.BlockSelectDecodeStep(mode, 1, hq, hkv, 128, t + 8, top_fraction=0.02, protect_sink=3,
+                                    protect_recent=5, keep_self=True)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step(q, kd, vd, 0.088)
+    history = t - 1
+    nb, n_scan, n_cand, n_keep = BS.step_counts(history, step.block, step.scan, step.cand, step.top_fraction)
+    lib = _lib.load()
+    rows, n_tok = hq, n_scan * step.block
+    n_out = int(lib.qkv_final_list_count(history, n_keep, 3, 5, 1))
+    want_mask, want_ids = step.keep[:, :t].clone(), step.attn_ids[: rows * n_out].clone()
+    for full in (step.full[: rows * n_tok], None):
+        keep = torch.zeros_like(step.keep)
+        ids = torch.full((rows * n_out,), -7, dtype=torch.int32, device=DEV)
+        _lib.check(lib.qkv_block_rerank(
+            q.data_ptr(), kd.data_ptr(), _lib.strides(*kd.stride()), 1, hq, hkv, t, 128,
+            step.partial[: rows * n_tok].data_ptr(), _lib.ptr(full), n_tok, step.blocks[: rows * n_scan].data_ptr(),
+            n_scan, step.block, n_cand, n_keep, 3, 5, 1, 0.088, keep.data_ptr(), step.capacity, ids.data_ptr(), n_out,
+            _lib.stream_of(q)))
+        assert torch.equal(keep[:, :t], want_mask), full is None
+        assert torch.equal(ids, want_ids), full is None
