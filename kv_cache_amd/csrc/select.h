@@ -294,6 +294,7 @@ struct WideSelect {
   uint64_t valid = 0;   // bit i: key i of this thread takes part
   uint32_t theta = 0;
   int kr = 0, kk = 0;
+  uint32_t lane_max = 0, lane_min = 0xFFFFFFFFu;   // load_count(): this thread's valid keys
 
   // LDS of the selection (the caller declares one and passes it in).
   static constexpr int RB = 12, NB = 1 << RB;   // radix digit: 12 bits, 4096 bins
@@ -349,16 +350,22 @@ struct WideSelect {
   __device__ void refresh() { asm volatile("" : "+v"(valid)); }
 
   // The row's largest and smallest valid key and the count of valid keys,
-  // reduced over the workgroup through sh.red (one barrier).
+  // reduced over the workgroup through sh.red (one barrier); LANE: this
+  // thread's extremes are lane_max / lane_min already (load_count).
+  template <bool LANE = false>
   __device__ void reduce_row(Shared& sh, uint32_t& umax, uint32_t& umin, int& nval) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    umax = 0;
-    umin = 0xFFFFFFFFu;
+    umax = lane_max;
+    umin = lane_min;
+    if (!LANE) {
+      umax = 0;
+      umin = 0xFFFFFFFFu;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      if (on(i)) {
-        umax = max(umax, u[i]);
-        umin = min(umin, u[i]);
+      for (int i = 0; i < VPL; ++i) {
+        if (on(i)) {
+          umax = max(umax, u[i]);
+          umin = min(umin, u[i]);
+        }
       }
     }
     nval = wave_incl_scan_dpp(__popcll(valid));
@@ -539,6 +546,8 @@ struct WideSelect {
   // count_done() once; run_counted() follows.
   __device__ void count(int i, Shared& sh, int& ninf) {
     if (on(i)) {
+      lane_max = max(lane_max, u[i]);
+      lane_min = min(lane_min, u[i]);
       if (u[i] == kNegInfKey) ++ninf;
       else atomicAdd(&sh.hist[0][u[i] >> (32 - RB)], 1);
     }
@@ -551,7 +560,7 @@ struct WideSelect {
   __device__ int run_counted(int k, Shared& sh) {
     uint32_t umax, umin;
     int nval;
-    reduce_row(sh, umax, umin, nval);   // (its barrier also completes load_count's atomics)
+    reduce_row<true>(sh, umax, umin, nval);   // (its barrier also completes load_count's atomics)
     kk = min(k, nval);
     kr = kk;
     if (kk == nval) {   // every valid key is taken
