@@ -264,7 +264,7 @@ def hbm_read_probe(nbytes: int, reps: int = 20, min_total: int = 1 << 30) -> dic
 
     lib = _lib.load()
     n_buf = max(2, -(-min_total // nbytes))
-    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(b) for b in range(n_buf)]
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(b % 251) for b in range(n_buf)]
     words = lib.qkv_hbm_read_probe_sink_words(nbytes)
     sink = torch.empty(words, dtype=torch.int32, device="cuda")
 
