@@ -97,7 +97,7 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
 // FINITE or a floor possibly fewer).  Every thread of the workgroup must
 // call it; it ends with a barrier.
 template <int VPL, bool FINITE, int NW = 4>
-__device__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
+__device__ __forceinline__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
                           uint32_t* lane_max_out = nullptr) {
   static_assert(VPL <= 32, "one mask bit per key of a thread");
   static_assert(NW >= 4 && NW <= 16, "4 to 16 waves");
