@@ -96,12 +96,64 @@ __device__ __forceinline__ uint32_t wave_lower_bound(uint32_t v, int j, uint32_t
 // ascending, to sel (LDS, 64*NW*VPL entries) and returns kk (k, or with
 // FINITE or a floor possibly fewer).  Every thread of the workgroup must
 // call it; it ends with a barrier.
+//
+// Rows of at most 64*NW keys (when lane_max_out is not asked for) take
+// select_small instead: one key per thread, each selectable key's rank (the
+// keys above it plus the equal keys at lower positions) counted against
+// every key of the row in LDS, read back by broadcast 16-byte loads; a key is
+// taken when its rank is under kk, which is exactly the lowest-position tie
+// rule, and positions follow from one scan of the taken flags.  Three
+// barriers instead of a radix pass's two per 8 bits.  A key that is not
+// selectable is kept as 0, under every selectable key (only a -NaN maps to
+// 0, and NaN is outside the contract).
+template <bool FINITE, int NW>
+__device__ __forceinline__ int select_small(const float* __restrict__ vals, int n, int k, int32_t* sel,
+                                            uint32_t floor) {
+  constexpr int NT = 64 * NW;
+  __shared__ __attribute__((aligned(16))) uint32_t keys[NT];
+  __shared__ int small_cnt[NW][2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t u = f32_sortable(vals[min(tid, n - 1)]);
+  const bool ok = tid < n && (!FINITE || u != kNegInfKey) && u >= floor && u != 0u;
+  const uint32_t key = ok ? u : 0u;
+  keys[tid] = key;
+  const int nw_ok = static_cast<int>(__popcll(__ballot(ok)));
+  if (lane == 0) small_cnt[wave][0] = nw_ok;
+  __syncthreads();
+  int nval = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) nval += small_cnt[w][0];
+  const int kk = min(k, nval);
+  int rank = 0;   // keys above this one, then equal keys at lower positions
+  const int nr = (n + 3) & ~3;   // (keys at or past n are 0)
+#pragma unroll 4
+  for (int i = 0; i < nr; i += 4) {
+    const uint4 c = *reinterpret_cast<const uint4*>(keys + i);
+    rank += (c.x > key || (c.x == key && i < tid)) ? 1 : 0;
+    rank += (c.y > key || (c.y == key && i + 1 < tid)) ? 1 : 0;
+    rank += (c.z > key || (c.z == key && i + 2 < tid)) ? 1 : 0;
+    rank += (c.w > key || (c.w == key && i + 3 < tid)) ? 1 : 0;
+  }
+  const bool take = ok && rank < kk;
+  const uint64_t tb = __ballot(take);
+  if (lane == 0) small_cnt[wave][1] = static_cast<int>(__popcll(tb));
+  __syncthreads();
+  int pos = static_cast<int>(__popcll(tb & ((1ull << lane) - 1ull)));
+#pragma unroll
+  for (int w = 0; w < NW - 1; ++w) pos += w < wave ? small_cnt[w][1] : 0;
+  if (take) sel[pos] = tid;
+  __syncthreads();
+  return kk;
+}
+
 template <int VPL, bool FINITE, int NW = 4>
 __device__ __forceinline__ int select_row(const float* __restrict__ vals, int n, int k, int32_t* sel, uint32_t floor = 0,
                           uint32_t* lane_max_out = nullptr) {
   static_assert(VPL <= 32, "one mask bit per key of a thread");
   static_assert(NW >= 4 && NW <= 16, "4 to 16 waves");
   constexpr int NT = 64 * NW;
+  if (n <= NT && !lane_max_out) return select_small<FINITE, NW>(vals, n, k, sel, floor);   // uniform
   __shared__ __attribute__((aligned(16))) int hist[NW][260];   // one copy per wave, padded across banks
   __shared__ int wave_cnt[NW][2];
   __shared__ uint32_t red[NW][4];

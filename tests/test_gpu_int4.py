@@ -346,6 +346,25 @@ def test_topk_one_launch_wait_limit_zero():
     assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
 
 
+@pytest.mark.parametrize("n,k", [(1, 1), (7, 3), (64, 64), (200, 17), (255, 128), (256, 1), (256, 255), (257, 100)])
+def test_topk_small_rows(n, k):
+    # rows of at most 256 keys rank every key against the row (one key per
+    # thread): ties, signed zeros, -inf (selectable for qkv_topk, not for the
+    # prefill selection, which pads with -1), an all -inf row
+    g = torch.Generator().manual_seed(n * 31 + k)
+    vals = torch.randint(-5, 5, (6, n), generator=g).float()
+    vals[0] = torch.randn(n, generator=g)
+    vals[1, ::2] = -0.0
+    vals[1, 1::2] = 0.0
+    vals[2, : n // 2] = -float("inf")
+    vals[3] = -float("inf")
+    vals[4] = 3.0
+    got = K.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.topk_lowest_index(vals.numpy(), k))
+    got = P.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
+
+
 @pytest.mark.parametrize("n,k,ld", [(1024, 64, 1024), (1024, 1, 1025), (1000, 100, 1000), (200, 64, 203),
                                     (513, 7, 513)])
 def test_topk_many_short_rows(n, k, ld):
