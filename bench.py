@@ -729,12 +729,10 @@ def run_reuse(args) -> dict:
                 fn()
         return run
 
-    ms_graph = None
-    if selection != "sample_quantile":   # its sampled columns are copied from the host every step
-        gr = graph_of(repeated(run_fixed))
-        ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
-        del gr
-        log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
+    gr = graph_of(repeated(run_fixed))
+    ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
+    del gr
+    log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
 
     mask_ws = [steps[l].mask_ws for l in range(layers)]
     s_dims, cand_frac, _, _, block = RU.parse_reuse_mode(c["mode"])
@@ -744,9 +742,30 @@ def run_reuse(args) -> dict:
         for layer in range(layers):
             RU.reuse_partial_scores(qs[layer], steps[layer].kdm, hist_fixed, s_dims, out=steps[layer].partial)
 
+    n_s = steps[0].col_counts[hist_fixed] if selection == "sample_quantile" else 0
+    mask_name, mask_bytes = "threshold_mask", rows * hist_fixed * (4 + 1)
+
     def run_mask():
         for layer in range(layers):
             RU.threshold_mask(steps[layer].partial, hist_fixed, requested, steps[layer].cand[0], mask_ws[layer])
+
+    if n_s:   # the sampled columns gathered (index and score), then the mask pass
+        mask_name, mask_bytes = "sample_quantile_mask", n_s * 4 + rows * n_s * 8 + rows * hist_fixed * (4 + 1)
+
+        def run_mask():
+            k_s = RU.budget_count(n_s, cand_frac)
+            for layer in range(layers):
+                st = steps[layer]
+                RU.candidate_mask(st.partial, hist_fixed, "sample_quantile", k_s, st.cand[0], st.thresholds,
+                                  mask_ws[layer], st.col_table[hist_fixed], n_s)
+    elif selection == "previous_threshold":   # the row's threshold, then the mask pass
+        mask_name, mask_bytes = "previous_threshold_mask", rows * 4 + rows * hist_fixed * (4 + 1)
+
+        def run_mask():
+            for layer in range(layers):
+                st = steps[layer]
+                RU.candidate_mask(st.partial, hist_fixed, "previous_threshold", requested, st.cand[0], st.thresholds,
+                                  mask_ws[layer])
 
     lib = RU._lib.load()
     n_sel = int(lib.qkv_reuse_final_count(hist_fixed, c["sink"], c["recent"], c["top_fraction"], 1))
@@ -777,7 +796,7 @@ def run_reuse(args) -> dict:
 
     plan = [
         ("reuse_partial_scores", run_partial, rows * hist_fixed * (s_dims * 2 + 4)),
-        ("threshold_mask", run_mask, rows * hist_fixed * (4 + 1)),
+        (mask_name, run_mask, mask_bytes),
         # three mask bytes, the f32 score and the final mask byte per token, plus
         # the K row of every union token
         ("reuse_select", run_select, rows * hist_fixed * (3 + 4 + 1) + union * d * 2),

@@ -78,6 +78,38 @@ def sample_columns(history: int, sample_size: int) -> torch.Tensor | None:
     return cols.to(torch.int32)
 
 
+_COLUMN_TABLES: dict = {}
+
+
+def sample_column_table(capacity: int, sample_size: int, device) -> tuple[torch.Tensor, list[int]]:
+    """``sample_columns`` for every history below ``capacity``, built once on
+    the host by the same torch call and kept on the device: int32
+    [capacity, sample_size] (row h padded with its last column) and the host
+    list of each row's column count (0 where the sample covers the row).  A
+    decode step then reads its row in place instead of copying the columns
+    from the host every token, so the step can be captured in a graph.
+    Shared by every step of the same sizes and device."""
+    dev = torch.device(device)
+    key = (int(capacity), int(sample_size), dev)
+    hit = _COLUMN_TABLES.get(key)
+    if hit is not None:
+        return hit
+    size = max(1, int(sample_size))
+    host = torch.zeros((int(capacity), size), dtype=torch.int32)
+    counts = [0] * int(capacity)
+    for h in range(1, int(capacity)):
+        cols = sample_columns(h, size)
+        if cols is None:
+            continue
+        n = cols.numel()
+        host[h, :n] = cols
+        host[h, n:] = cols[-1]
+        counts[h] = n
+    table = (host.to(dev), counts)
+    _COLUMN_TABLES[key] = table
+    return table
+
+
 def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: torch.Tensor,
                    thresholds: torch.Tensor | None, workspace: torch.Tensor, sample_cols: torch.Tensor | None = None,
                    n_sample: int = 0) -> torch.Tensor:
@@ -253,7 +285,8 @@ class ReuseDecodeStep:
         # the last step's candidate threshold per row (EV:1744-1745), written by the
         # previous_threshold and sample_quantile selections
         self.thresholds = torch.zeros(rows, dtype=torch.float32, device=device)
-        self.sample_cols = torch.empty(min(self.sample_size, cap), dtype=torch.int32, device=device)
+        self.col_table, self.col_counts = (sample_column_table(cap, self.sample_size, device)
+                                           if self.selection == "sample_quantile" else (None, None))
         hist_max = cap - 1
         # every term of the counts grows with the history
         self.n_out_max = max(self._final_count(hist_max), int(lib.qkv_reuse_final_count(
@@ -263,6 +296,11 @@ class ReuseDecodeStep:
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
         self.mask_ws = self._ws(lib.qkv_threshold_mask_workspace_bytes(rows, hist_max, budget_count(hist_max,
                                                                                                     self.cand_fraction)))
+        n_s_max = max(self.col_counts) if self.col_counts else 0
+        if n_s_max:   # sized once for the largest sample, so a captured step never reallocates
+            self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
+                rows, hist_max, CANDIDATE_SELECTIONS["sample_quantile"], budget_count(n_s_max, self.cand_fraction),
+                n_s_max))
         self.select_ws = self._ws(lib.qkv_reuse_select_workspace_bytes(rows, hist_max, self.top_fraction))
         need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
         _require(need > 0, "unsupported attention shape (head_dim must be 128)")
@@ -345,18 +383,16 @@ class ReuseDecodeStep:
         q = query.contiguous()
         reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
-        cols = sample_columns(history, self.sample_size) if self.selection == "sample_quantile" else None
+        n_s = self.col_counts[history] if self.selection == "sample_quantile" else 0
         if self.selection == "previous_threshold" and previous_thresholds:   # EV:3967-3971
             candidate_mask(self.partial, history, "previous_threshold", requested, current, self.thresholds,
                            self.mask_ws)
-        elif cols is not None:                                                # EV:3972-3987
-            n_s = cols.numel()
+        elif n_s:                                                             # EV:3972-3987
             k_s = budget_count(n_s, self.cand_fraction)
-            self.sample_cols[:n_s].copy_(cols)
             self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
                 self.rows, history, CANDIDATE_SELECTIONS["sample_quantile"], k_s, n_s))
             candidate_mask(self.partial, history, "sample_quantile", k_s, current, self.thresholds, self.mask_ws,
-                           self.sample_cols, n_s)
+                           self.col_table[history], n_s)
         else:                                                                 # EV:3988
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))

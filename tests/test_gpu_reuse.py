@@ -271,6 +271,48 @@ def test_step_selections_match_oracle(hq, hkv, t, steps, mode, selection, sample
         pc, pf = wc, wf
 
 
+def test_step_sample_quantile_graph_replays():
+    # the sample_quantile step reads its sampled columns from a device table,
+    # so it can be captured: every replay, with a new query copied in and the
+    # outputs cleared between replays, matches the eager launch bit for bit
+    gen = torch.Generator().manual_seed(17)
+    t = 3000
+    k = torch.randn((1, 2, t + 3, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn((1, 2, t + 3, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, 8, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    step = RU.ReuseDecodeStep("qabs8cand5reuse", 1, 8, 2, 128, t + 64, top_fraction=0.02, protect_sink=4,
+                              protect_recent=8, candidate_selection="sample_quantile", threshold_sample_size=256)
+    for n in (t, t + 1, t + 2):
+        step(q, k[:, :, :n], v[:, :, :n], 128 ** -0.5)
+    cur, prev = step.cand[1 - step.flip], step.cand[step.flip]
+    kk, vv = k[:, :, : t + 2], v[:, :, : t + 2]
+
+    def launch():
+        step.launch(q, kk, vv, 128 ** -0.5, cur, prev, None)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    for rep in range(4):
+        q.copy_(torch.randn((1, 8, 128), generator=gen).to(torch.bfloat16))
+        launch()
+        want = [x.clone() for x in (cur, step.fin, step.thresholds, step.out)]
+        for x in (cur, step.fin, step.thresholds, step.out):
+            x.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for w, x in zip(want, (cur, step.fin, step.thresholds, step.out)):
+            assert torch.equal(w, x), rep
+    assert int(cur.count_nonzero()) > 0
+
+
 @pytest.mark.parametrize("mode,selection", [("qabs8cand5reuseblk8", "previous_threshold"),
                                             ("qabs16cand10reusefinal", "sample_quantile"),
                                             ("qabs8cand5reuse2setblk32", "topk")])

@@ -7,6 +7,7 @@ counts: the smallest integer at least fraction * history, clamped)."""
 import math
 
 import pytest
+import torch
 
 from kv_cache_amd import modes as M
 
@@ -102,3 +103,21 @@ def test_sample_columns_host():
     cols = RU.sample_columns(1000, 64)
     assert cols.dtype.is_floating_point is False and cols.numel() == 64
     assert int(cols[0]) == 0 and int(cols[-1]) == 999
+
+
+def test_sample_column_table_rows_are_the_host_columns():
+    # the device table a sample_quantile step reads: row h is sample_columns(h)
+    # padded with its last column, count 0 where the sample covers the row
+    from kv_cache_amd import reuse as RU
+
+    table, counts = RU.sample_column_table(300, 40, "cpu")
+    assert table.shape == (300, 40) and table.dtype == torch.int32
+    assert RU.sample_column_table(300, 40, "cpu")[0] is table   # built once per sizes and device
+    for h in range(300):
+        cols = RU.sample_columns(h, 40) if h else None
+        if cols is None:
+            assert counts[h] == 0
+            continue
+        n = counts[h]
+        assert n == cols.numel() and torch.equal(table[h, :n], cols)
+        assert bool((table[h, n:] == cols[-1]).all())
