@@ -481,6 +481,138 @@ def reuse_decode_step(query, key, value, dim_count: int, candidate_fraction: flo
     return out, current, hist_final
 
 
+# The lagged reuse family (EV:473-476, 918-955): kind -> the mode prefix.
+LAGGED_KINDS = ("lagtop2", "lagrefresh", "qdrift", "qdriftmaj", "qdrifthead", "qdriftshare", "qdriftcos",
+                "qdriftcoshead", "pconf")
+_PER_HEAD_KINDS = ("qdrifthead", "qdriftcoshead", "qdriftshare", "pconf")   # EV:4089
+
+
+def _bf16_round(x):
+    """float32 -> nearest bf16 (ties to even), returned as float32."""
+    b = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return b.astype(np.uint32).view(np.float32)
+
+
+def previous_final_ess_fraction(query, key, previous_final, scaling: float, bf16_scores: bool = False):
+    """The pconf test's statistic (EV:4071-4085): per row, the softmax weights
+    of q over the tokens of the previous final mask (full-D dot * scaling;
+    with ``bf16_scores`` the dot and the scaled score rounded to bf16, as a
+    bf16 matmul and multiply leave them), the effective sample size
+    1 / max(sum w^2, 1e-12), divided by max(count, 1).  A row with no token
+    has all weights 0, hence 1e12.  query [B,H,D]; key [B,H,>=hist,D];
+    previous_final bool [B,H,hist].  Returns float64 [B,H]."""
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    m = np.asarray(previous_final, dtype=bool)
+    b, h, _ = q.shape
+    out = np.empty((b, h), dtype=np.float64)
+    for bi in range(b):
+        for hi in range(h):
+            pos = np.flatnonzero(m[bi, hi])
+            if pos.size == 0:
+                out[bi, hi] = 1e12
+                continue
+            sc = (k[bi, hi, pos].astype(np.float64) @ q[bi, hi].astype(np.float64)).astype(np.float32)
+            if bf16_scores:
+                sc = _bf16_round(_bf16_round(sc) * np.float32(scaling))
+            else:
+                sc = sc * np.float32(scaling)
+            w = np.exp(sc.astype(np.float64) - sc.max())
+            w /= w.sum()
+            out[bi, hi] = 1.0 / max(float((w * w).sum()), 1e-12) / pos.size
+    return out
+
+
+def lagged_reuse_decode_step(query, key, value, kind: str, param, dim_count: int, candidate_fraction: float,
+                             top_fraction: float, sink: int, recent: int, keep_self: bool, scaling: float,
+                             previous=None, bf16_scores: bool = False):
+    """One decode step of the lagged reuse modes (``lagtop2``, ``lagrefresh{N}``,
+    ``qdrift[maj|head|share|cos|coshead]`` and ``pconf{T}`` before
+    ``qabs{S}cand{pct}``), ``_qabs_reuse_fast_attention_forward`` EV:4020-4198
+    with the default ``topk`` candidate selection, then the rerank of EV:4257-4365.
+
+    ``param`` is N for lagrefresh and T (a fraction) for pconf.  ``previous``
+    is None or the previous step's state: dict(final=bool [B,Hq,>= hist-1],
+    dims=int [B,Hq,S], values=float [B,Hq,S]) (EV:1645-1694, present only when
+    the previous step was query token - 1).
+
+    * refresh test: lagrefresh refreshes when history % N == 0 (EV:4024); the
+      qdrift kinds flag a head whose current top-S dims share fewer than
+      max(1, ceil(S/2)) with the previous ones, or (cos kinds) whose q on the
+      previous dims has cosine < 0.5 with the previous values (EV:4045-4066);
+      the step refreshes if any head is flagged (a majority for qdriftmaj);
+      pconf flags heads whose ``previous_final_ess_fraction`` > T (EV:4068-4087);
+    * candidates: with a previous final mask, the per-head kinds (head,
+      coshead, share, pconf) score only flagged heads, others keep an empty
+      candidate set (EV:4089-4109); the other kinds reuse the previous final
+      mask alone unless the step refreshes (EV:4110-4115); otherwise every head
+      thresholds its partial scores (EV:4116-4145);
+    * union = candidates | previous final (| for share, the OR over the
+      batch's heads) | the sink and recent ranges (EV:4147-4175); the rerank
+      and final selection of ``reuse_select`` on it.
+
+    Returns (out float64 [B,1,Hq,D], current bool [B,Hq,hist], history_final
+    bool [B,Hq,hist], state dict for the next step, flagged bool [B,Hq] or
+    None)."""
+    if kind not in LAGGED_KINDS:
+        raise ValueError(f"unknown lagged kind {kind!r}")
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, hq, d = q.shape
+    g = hq // k.shape[1]
+    kx, vx = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    history = k.shape[2] - 1
+    s_count = min(max(1, int(dim_count)), d)
+    dims = np.stack([np.stack([select_dims_by_abs(q[bi, hi], s_count) for hi in range(hq)]) for bi in range(b)])
+    values = np.take_along_axis(q, dims, axis=-1)
+    refresh = kind == "lagrefresh" and history % int(param) == 0
+    prev_final = None
+    if previous is not None:
+        m = np.asarray(previous["final"], dtype=bool)[..., :history]
+        pad = history - m.shape[-1]
+        prev_final = np.concatenate([m, np.zeros((*m.shape[:-1], pad), dtype=bool)], axis=-1) if pad else m
+    flagged = None
+    if kind.startswith("qdrift"):
+        refresh = True
+        if previous is not None:
+            pd = np.asarray(previous["dims"])
+            overlap = (dims[..., :, None] == pd[..., None, :]).any(axis=-1).sum(axis=-1)
+            flagged = overlap < max(1, math.ceil(s_count / 2))
+            if kind in ("qdriftcos", "qdriftcoshead"):
+                on_prev = np.take_along_axis(q, pd, axis=-1).astype(np.float64)
+                pv = np.asarray(previous["values"], dtype=np.float64)
+                den = np.linalg.norm(on_prev, axis=-1) * np.linalg.norm(pv, axis=-1)
+                flagged = flagged | ((on_prev * pv).sum(axis=-1) / np.maximum(den, 1e-6) < 0.5)
+            refresh = bool(flagged.mean() > 0.5) if kind == "qdriftmaj" else bool(flagged.any())
+    if kind == "pconf":
+        refresh = True
+        if prev_final is not None:
+            flagged = previous_final_ess_fraction(q, kx, prev_final, scaling, bf16_scores) > float(param)
+            refresh = bool(flagged.any())
+    requested = budget_count(history, candidate_fraction)
+    if kind in _PER_HEAD_KINDS and prev_final is not None and flagged is not None:
+        partial = partial_scores(q, kx[:, :, :history], dim_count)
+        current = threshold_mask(partial, requested) & flagged[..., None]
+        union = prev_final | current
+        if kind == "qdriftshare":
+            union = union | current.any(axis=1, keepdims=True)
+    elif prev_final is not None and not refresh:
+        current = np.zeros((b, hq, history), dtype=bool)
+        union = prev_final.copy()
+    else:
+        current = threshold_mask(partial_scores(q, kx[:, :, :history], dim_count), requested)
+        union = current | prev_final if prev_final is not None else current.copy()
+    if sink > 0:
+        union[..., : min(sink, history)] = True
+    if recent > 0:
+        union[..., max(0, history - recent):] = True
+    fi, fv, hist_final = reuse_select(q, kx, union, None, None, sink, recent, top_fraction, keep_self, scaling)
+    out = final_attention(q, kx, vx, fi, fv, scaling)
+    return out, current, hist_final, {"final": hist_final, "dims": dims, "values": values}, flagged
+
+
 def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, candidate_fraction: float,
                         top_fraction: float, scaling: float, sink: int = 0, recent: int = 0, keep_self: bool = True,
                         previous_candidate=None, previous_final=None, block: int | None = None, *,

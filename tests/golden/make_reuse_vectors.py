@@ -12,7 +12,9 @@ through the attention hook the model calls (``_limited_eager_attention_forward``
 EV:6236) on seeded synthetic q/K/V, and saves inputs and outputs:
 
 * per step: the attention output [B, 1, Hq, D], and the reuse state the step
-  leaves behind (current candidate mask and final mask, bool [B, Hq, hist]);
+  leaves behind (current candidate mask and final mask, bool [B, Hq, hist];
+  the candidate thresholds, NaN where the step kept none; the top-|q| dims and
+  their q values; the state's running count of refreshed heads);
 * the inputs: q for every step, K/V of the longest step (each step uses the
   prefix of the first T0 + step + 1 tokens).
 
@@ -66,12 +68,48 @@ SCENARIOS = {
 }
 
 
+# The lagged reuse modes (EV:4020-4198): lagtop2 (reuse the previous final
+# selection), lagrefresh{N} (refresh every N-th query token), qdrift* (refresh
+# when the top-|q| dims drift: any / majority / per head / shared across heads /
+# with the cosine test) and pconf{T} (refresh heads whose previous final
+# attention has an effective-sample fraction above T).  Their queries drift
+# slowly on some heads and jump on others, so refreshes are mixed: q of head h
+# at step s is scale_h * (base_h + eps_h * noise_{s,h}) / sqrt(1 + eps_h^2).  The bf16 seeds are
+# ones with no |q| tie at the S-th dim in any step (torch.topk's order among
+# ties is unspecified); scales stay at or below 1 so that the reference's bf16
+# attention scores (rounded to bf16 before the softmax) stay within the bf16
+# tolerance of an fp32 attention.
+# name: (mode, dtype, Hq, Hkv, T0, steps, top_fraction, sink, recent, keep_self, seed)
+LAG_EPS = (0.02, 3.0, 0.05, 0.3, 0.01, 2.0, 0.1, 1.0)
+LAG_SCALE = (1.0, 0.3, 0.7, 1.0, 0.5, 0.9, 0.6, 0.8)
+LAG_SCENARIOS = {
+    "lagtop2_s8c5_bf16": ("lagtop2qabs8cand5", torch.bfloat16, 4, 2, 240, 4, 0.05, 4, 4, True, 641),
+    "lagrefresh3_s8c5_bf16": ("lagrefresh3qabs8cand5", torch.bfloat16, 4, 2, 238, 5, 0.05, 3, 5, True, 142),
+    "qdrift_s8c5_bf16": ("qdriftqabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 4, 4, True, 7943),
+    "qdriftmaj_s8c5_bf16": ("qdriftmajqabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 4, 4, True, 6744),
+    "qdrifthead_s8c5_bf16": ("qdriftheadqabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 2, 6, True, 4845),
+    "qdriftshare_s8c5_bf16": ("qdriftshareqabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 4, 0, False, 4546),
+    "qdriftcos_s16c10_bf16": ("qdriftcosqabs16cand10", torch.bfloat16, 8, 4, 230, 5, 0.03, 4, 4, True, 188247),
+    "qdriftcoshead_s8c5_bf16": ("qdriftcosheadqabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 0, 4, True, 2448),
+    "pconf50_s8c5_bf16": ("pconf50qabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 4, 4, True, 5349),
+    "pconf37p5_s16c10_fp32": ("pconf37p5qabs16cand10", torch.float32, 8, 4, 230, 4, 0.03, 2, 3, True, 50),
+    "qdrifthead_s8c5_fp32": ("qdriftheadqabs8cand5", torch.float32, 8, 2, 260, 4, 0.04, 2, 6, True, 51),
+}
+
+
 def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, keep_self, seed, selection="topk",
-        sample_size=256):
+        sample_size=256, lagged=False):
     g = torch.Generator().manual_seed(seed)
     d = 128
     t_max = t0 + steps
-    q = torch.randn((steps, 1, hq, 1, d), generator=g).to(dtype)
+    if lagged:
+        eps = torch.tensor([LAG_EPS[h % len(LAG_EPS)] for h in range(hq)]).view(1, 1, hq, 1, 1)
+        scale = torch.tensor([LAG_SCALE[h % len(LAG_SCALE)] for h in range(hq)]).view(1, 1, hq, 1, 1)
+        base = torch.randn((1, 1, hq, 1, d), generator=g)
+        noise = torch.randn((steps, 1, hq, 1, d), generator=g)
+        q = (scale * (base + eps * noise) / torch.sqrt(1 + eps * eps)).to(dtype)
+    else:
+        q = torch.randn((steps, 1, hq, 1, d), generator=g).to(dtype)
     # K/V values are bf16-representable (stored as bf16 bits); the fp32
     # scenarios still compute in fp32
     k = (torch.randn((1, hkv, t_max, d), generator=g) * 1.5).to(torch.bfloat16).to(dtype)
@@ -79,7 +117,7 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
     scaling = d ** -0.5
     state = ev.ReuseCandidateState()
     module = types.SimpleNamespace(layer_idx=0, scaling=scaling)
-    outs, cands, finals, thresholds = [], [], [], []
+    outs, cands, finals, thresholds, qdims, qvals, refreshed = [], [], [], [], [], [], []
     with ev.attention_mode(mode=mode, top_fraction=top_fraction, max_heads_per_token=3,
                            always_keep_self=keep_self, protect_sink_tokens=sink,
                            protect_recent_tokens=recent, load_stats=None, reuse_state=state,
@@ -98,7 +136,12 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
             fin[..., :hist] = rec["final"].numpy()
             cands.append(cand)
             finals.append(fin)
-            thresholds.append(rec["candidate_thresholds"].float().numpy().reshape(1, hq))
+            thr = rec.get("candidate_thresholds")   # None on the lagged modes' reuse steps
+            thresholds.append(np.full((1, hq), np.nan, np.float32) if thr is None
+                              else thr.float().numpy().reshape(1, hq))
+            qdims.append(rec["qdim_indices"].numpy().astype(np.int32))
+            qvals.append(rec["qdim_values"].float().numpy())
+            refreshed.append(state.refresh_head_count)
     np.savez_compressed(
         OUT / f"reuse_{name}.npz", mode=np.array(mode), dtype=np.array(str(dtype).split(".")[-1]),
         q=q.float().numpy(), k_bf16=k.to(torch.bfloat16).view(torch.int16).numpy(),
@@ -106,7 +149,8 @@ def run(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, recent, k
         top_fraction=top_fraction, sink=sink, recent=recent, keep_self=keep_self, scaling=scaling,
         out=np.stack(outs), candidate=np.packbits(np.stack(cands), axis=-1),
         final=np.packbits(np.stack(finals), axis=-1), t_max=t_max, selection=np.array(selection),
-        sample_size=sample_size, thresholds=np.stack(thresholds))
+        sample_size=sample_size, thresholds=np.stack(thresholds), qdim_indices=np.stack(qdims),
+        qdim_values=np.stack(qvals), refresh_head_count=np.array(refreshed, dtype=np.int64))
     print(f"{name}: {mode} {dtype} {selection} Hq={hq} T0={t0} steps={steps} -> reuse_{name}.npz")
 
 
@@ -195,6 +239,9 @@ def main(names):
     for name, args in SCENARIOS.items():
         if not names or name in names:
             run(ev, name, *args)
+    for name, args in LAG_SCENARIOS.items():
+        if not names or name in names:
+            run(ev, name, *args, lagged=True)
     for name, args in BLOCK_SCENARIOS.items():
         if not names or name in names:
             run_block(ev, name, *args)
