@@ -43,6 +43,19 @@ extern "C" {
 #define QKV_CAND_SAMPLE_QUANTILE 1    /* the k-th largest of sampled columns      */
 #define QKV_CAND_PREVIOUS_THRESHOLD 2 /* the previous step's threshold            */
 
+/* Refresh tests of the lagged reuse modes (qkv_reuse_lag_flags, EV:4026-4087). */
+#define QKV_LAG_DIMS 0    /* record the top-|q| dims and values only               */
+#define QKV_LAG_OVERLAP 1 /* qdrift[maj|head|share]: top dims shared with the last */
+#define QKV_LAG_COS 2     /* qdriftcos[head]: overlap, or cosine on the last dims  */
+#define QKV_LAG_ESS 3     /* pconf{T}: effective sample size of the last selection */
+
+/* Which rows of a lagged step take new candidates (qkv_reuse_lag_union). */
+#define QKV_REFRESH_NONE 0     /* none: the previous final selection alone       */
+#define QKV_REFRESH_ALL 1      /* every row                                      */
+#define QKV_REFRESH_PER_ROW 2  /* the rows whose flag is set                     */
+#define QKV_REFRESH_ANY 3      /* every row when any flag is set                 */
+#define QKV_REFRESH_MAJORITY 4 /* every row when more than half the flags are    */
+
 #define QKV_ABI_VERSION 1
 
 /* ABI version of the loaded library (QKV_ABI_VERSION it was built with). */
@@ -374,6 +387,45 @@ int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selectio
 int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int selection, int64_t k,
                        const int32_t* sample_cols, int64_t n_sample, float* thresholds, uint8_t* mask,
                        int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The refresh test of the lagged reuse modes (lagtop2 / lagrefresh{N} /
+ * qdrift[maj|head|share|cos|coshead] / pconf{T} before qabs{S}cand{pct},
+ * _qabs_reuse_fast_attention_forward EV:4020-4087).  One row per (sequence,
+ * query head).  Always writes the row's top-|q| dims (count = clamp(dim_count,
+ * 1, head_dim); descending |q|, equal magnitudes to the lower dim, EV:4026)
+ * to dims_out and q at them to values_out, both [rows, count]: the state the
+ * next step's test reads as previous_dims / previous_values.  Then, into
+ * flags[r] (1 = the row refreshes):
+ *   QKV_LAG_OVERLAP: fewer than max(1, ceil(count / 2)) of the dims are among
+ *     previous_dims[r] (EV:4045-4048);
+ *   QKV_LAG_COS: that, or the cosine of q on previous_dims[r] with
+ *     previous_values[r] (denominator clamped to 1e-6) is below 0.5
+ *     (EV:4049-4056);
+ *   QKV_LAG_ESS: over the set positions t < history of previous_final[r]
+ *     (row stride mask_ld), s_t = q . K[t] rounded to the input dtype, times
+ *     scaling rounded again; weights softmax(s); flagged when the mask is
+ *     empty or (1 / sum w^2) / count > ess_threshold (EV:4068-4087).
+ * query [B,Hq,D] (D <= 128); key [B,Hkv,>=history,D] with k_strides
+ * {b,h,t,d} (d contiguous), read by QKV_LAG_ESS only.  history < 2^30. */
+int qkv_reuse_lag_flags(const void* query, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                        int64_t head_dim, int64_t dim_count, int test, const int32_t* previous_dims,
+                        const float* previous_values, int32_t* dims_out, float* values_out, const void* key,
+                        const int64_t* k_strides, int64_t history, const uint8_t* previous_final, int64_t mask_ld,
+                        float scaling, float ess_threshold, uint8_t* flags, void* stream);
+
+/* The candidate union of a lagged reuse step (EV:4089-4175), for
+ * qkv_reuse_select with no previous masks.  A row refreshes per `refresh`
+ * (QKV_REFRESH_*, from flags [batch * q_heads] for the last three); the
+ * current candidates of a row that does not refresh are set to 0 (read
+ * only for rows that refresh).  union_out[r, t] = current[r, t] (refreshed
+ * rows) | previous_final[r, t] (when not NULL) | (with share) current[r', t]
+ * for any refreshed row r' of the same sequence | t < protect_sink | t >=
+ * history - protect_recent, for t < history.  current, previous_final row
+ * stride mask_ld; union_out row stride union_ld; q_heads <= 1024. */
+int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_final, int64_t mask_ld, const uint8_t* flags,
+                        int64_t batch, int64_t q_heads, int64_t history, int refresh, int share,
+                        int64_t protect_sink, int64_t protect_recent, uint8_t* union_out, int64_t union_ld,
+                        void* stream);
 
 /* Entries per row of the final index list of a block-expanded reuse step
  * (the qabs{S}cand{pct}reuse[final|2set]blk{block} modes): body + sink

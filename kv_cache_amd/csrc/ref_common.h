@@ -98,6 +98,28 @@ __device__ inline void rank_dims128(const float* q_s, uint64_t* key_s, int head_
   __syncthreads();
 }
 
+// Eight consecutive elements at p as fp32 (p 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, float (&v)[8]) {
+  if constexpr (DT == QKV_DTYPE_FP32) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint4 c = *reinterpret_cast<const uint4*>(p + 4);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
+    v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
+      v[2 * i] = Elem<DT>::load(&lo);
+      v[2 * i + 1] = Elem<DT>::load(&hi);
+    }
+  }
+}
+
 template <template <int> class F, typename... A>
 int dispatch_dtype(int dtype, A&&... args) {
   switch (dtype) {

@@ -33,28 +33,6 @@ constexpr int kRT = 256;          // threads per workgroup
 constexpr int kScoreTile = 1024;  // tokens per workgroup in reuse_scores_kernel
 constexpr int kMaskTile = 4096;   // tokens per workgroup in reuse_mask_kernel
 
-// Eight consecutive elements at p as fp32 (p 16-byte aligned).
-template <int DT>
-__device__ __forceinline__ void load8(const typename Elem<DT>::T* p, float (&v)[8]) {
-  if constexpr (DT == QKV_DTYPE_FP32) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint4 c = *reinterpret_cast<const uint4*>(p + 4);
-    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
-    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
-    v[4] = __uint_as_float(c.x); v[5] = __uint_as_float(c.y);
-    v[6] = __uint_as_float(c.z); v[7] = __uint_as_float(c.w);
-  } else {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t lo = static_cast<uint16_t>(w[i] & 0xFFFFu), hi = static_cast<uint16_t>(w[i] >> 16);
-      v[2 * i] = Elem<DT>::load(&lo);
-      v[2 * i + 1] = Elem<DT>::load(&hi);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Partial scores: out[r, t] = sum_s q[d_s] * K[d_s, t] over the row's
 // top-|q| dims d_s in selection order (QK:63-96 on the dim-major copy of

@@ -264,7 +264,7 @@ class ReuseDecodeStep:
         self.device = device
         self.mode = mode
         (self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final,
-         self.block) = parse_reuse_mode(mode)
+         self.block) = self._parse_mode(mode)
         _require(self.block is None or self.block <= 4096, "reuse blocks hold at most 4096 tokens")
         # --qabs_candidate_selection / --qabs_threshold_sample_size (EV:245-258, 3958-3989)
         _require(candidate_selection in CANDIDATE_SELECTIONS, f"unknown candidate selection {candidate_selection!r}")
@@ -307,6 +307,9 @@ class ReuseDecodeStep:
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
         self.reset()
+
+    def _parse_mode(self, mode: str) -> tuple[int, float, bool, bool, int | None]:
+        return parse_reuse_mode(mode)
 
     def _final_count(self, history: int) -> int:
         """Entries per row of the step's final index list."""
@@ -399,6 +402,16 @@ class ReuseDecodeStep:
             # the threshold is kept only where a later step reads it
             candidate_mask(self.partial, history, "topk", requested, current,
                            self.thresholds if self.selection != "topk" else None, self.mask_ws)
+        self._select_attend(q, key, value, scaling, current, previous, previous_final)
+
+    def _select_attend(self, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
+                       current: torch.Tensor, previous: torch.Tensor | None,
+                       previous_final: torch.Tensor | None) -> None:
+        """The rerank of the union, the final selection (into ``self.fin``),
+        its block expansion and the attention over it (EV:4200-4397)."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        history = key_count - 1
         n_sel = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.top_fraction, int(self.keep_self)))
         n_out = self._final_count(history)
         self.select_ws = self._grow(self.select_ws,
@@ -436,3 +449,153 @@ class ReuseDecodeStep:
         n = self.n_out
         shape = (self.batch, self.q_heads, n)
         return (self.final_idx[: self.rows * n].view(shape), self.final_valid[: self.rows * n].view(torch.bool).view(shape))
+
+
+# -- lagged reuse (EV:4020-4198) ----------------------------------------------
+LAG_TESTS = {"dims": 0, "overlap": 1, "cos": 2, "ess": 3}                          # QKV_LAG_*
+REFRESH = {"none": 0, "all": 1, "per_row": 2, "any": 3, "majority": 4}           # QKV_REFRESH_*
+# kind -> (refresh test, which rows refresh once a previous step exists)
+LAGGED_KINDS = {
+    "lagtop2": (None, "none"),              # the previous final selection alone (EV:4110-4115)
+    "lagrefresh": (None, None),             # every row when history % N == 0 (EV:4024)
+    "qdrift": ("overlap", "any"),           # EV:4045-4048, 4064-4066
+    "qdriftmaj": ("overlap", "majority"),   # EV:4062-4063
+    "qdriftcos": ("cos", "any"),            # EV:4049-4057
+    "qdrifthead": ("overlap", "per_row"),   # EV:4058-4059, 4089-4106
+    "qdriftcoshead": ("cos", "per_row"),
+    "qdriftshare": ("overlap", "per_row"),  # + the candidates shared across heads (EV:4107-4109)
+    "pconf": ("ess", "per_row"),            # EV:4068-4087
+}
+_LAGGED = re.compile(r"(lagtop2|lagrefresh(\d+)|qdrift(?:maj|head|share|cos|coshead)?|pconf(\d+(?:p\d+)?))"
+                     r"qabs(\d+)cand(\d+(?:p\d+)?)")
+
+
+def parse_lagged_mode(mode: str) -> tuple[str, float | int | None, int, float]:
+    """``lagtop2 | lagrefresh{N} | qdrift[maj|head|share|cos|coshead] | pconf{T}``
+    + ``qabs{S}cand{pct}`` -> (kind, parameter, S, candidate fraction): the
+    parameter is max(1, N) for lagrefresh (EV:924-928) and T / 100 for pconf
+    (``p`` as the decimal point, EV:918-922), else None; S and the fraction as
+    ``parse_qabs_partial_rerank_params`` reads them (EV:748-754)."""
+    m = _LAGGED.fullmatch(mode)
+    _require(m is not None, f"{mode!r} is not a lagged reuse mode (lagtop2 / lagrefresh{{N}} / qdrift* / pconf{{T}} "
+                            f"+ qabs{{S}}cand{{pct}})")
+    if m.group(2) is not None:
+        kind, param = "lagrefresh", max(1, int(m.group(2)))
+    elif m.group(3) is not None:
+        kind, param = "pconf", float(m.group(3).replace("p", ".")) / 100.0
+    else:
+        kind, param = m.group(1), None
+    return kind, param, int(m.group(4)), float(m.group(5).replace("p", ".")) / 100.0
+
+
+def lag_flags(query: torch.Tensor, kv_heads: int, test: str, dim_count: int, dims_out: torch.Tensor,
+              values_out: torch.Tensor, flags: torch.Tensor | None = None, *, previous_dims: torch.Tensor | None = None,
+              previous_values: torch.Tensor | None = None, key: torch.Tensor | None = None, history: int = 0,
+              previous_final: torch.Tensor | None = None, scaling: float = 1.0, ess_threshold: float = 0.0) -> None:
+    """The lagged modes' per-row refresh test (``qkv_reuse_lag_flags``):
+    query [B, Hq, D]; dims_out int32 / values_out f32 [B*Hq, S] receive the
+    row's top-|q| dims and q at them; flags uint8 [B*Hq] the test's result
+    (``test`` in ``LAG_TESTS``).  The ``ess`` test reads key [B, Hkv, T, D]
+    and previous_final uint8 rows of the history."""
+    lib = _lib.load()
+    q = query.contiguous()
+    b, hq, d = q.shape
+    mask_ld = previous_final.stride(0) if previous_final is not None else 0
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_reuse_lag_flags(
+            q.data_ptr(), _dtype_code(q), b, hq, kv_heads, d, dim_count, LAG_TESTS[test], _lib.ptr(previous_dims),
+            _lib.ptr(previous_values), dims_out.data_ptr(), values_out.data_ptr(), _lib.ptr(key),
+            _lib.strides(*key.stride()) if key is not None else None, history, _lib.ptr(previous_final), mask_ld,
+            float(scaling), float(ess_threshold), _lib.ptr(flags), _lib.stream_of(q)))
+
+
+def lag_union(current: torch.Tensor, previous_final: torch.Tensor | None, flags: torch.Tensor | None, batch: int,
+              q_heads: int, history: int, refresh: str, share: bool, protect_sink: int, protect_recent: int,
+              out: torch.Tensor) -> torch.Tensor:
+    """The lagged modes' candidate union (``qkv_reuse_lag_union``) into
+    ``out``; ``current`` rows of the rows that do not refresh are cleared.
+    Masks uint8 [B*Hq, >= history] (row strides of their own)."""
+    lib = _lib.load()
+    _require(previous_final is None or previous_final.stride(0) == current.stride(0),
+             "current and previous_final must share a row stride")
+    with torch.cuda.device(current.device):
+        _lib.check(lib.qkv_reuse_lag_union(
+            current.data_ptr(), _lib.ptr(previous_final), current.stride(0), _lib.ptr(flags), batch, q_heads, history,
+            REFRESH[refresh], int(share), protect_sink, protect_recent, out.data_ptr(), out.stride(0),
+            _lib.stream_of(current)))
+    return out
+
+
+class LaggedReuseDecodeStep(ReuseDecodeStep):
+    """The lagged reuse modes' decode step (``lagtop2qabs8cand5``,
+    ``lagrefresh4qabs8cand5``, ``qdriftheadqabs8cand5``, ``pconf50qabs8cand5``
+    ...; ``_qabs_reuse_fast_attention_forward`` EV:4020-4198 with the default
+    ``topk`` candidate selection).  Per step: the refresh test on the GPU
+    (``lag_flags``, also recording the top-|q| dims for the next step), the
+    partial scores and candidate threshold of every row unless no row can
+    refresh, the union with the previous final selection (``lag_union``: the
+    rows that do not refresh keep no candidates; the step-wide any / majority
+    decisions are taken on the GPU, so a step needs no host round trip and
+    can be captured), then the rerank, final selection and attention of the
+    reuse step.  Same call convention and state views as ``ReuseDecodeStep``."""
+
+    def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
+                 top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
+                 keep_self: bool = True, candidate_selection: str = "topk", device: torch.device | str = "cuda"):
+        _require(candidate_selection == "topk",
+                 "the lagged reuse modes are built for the topk candidate selection only")
+        super().__init__(mode, batch, q_heads, kv_heads, head_dim, capacity, top_fraction=top_fraction,
+                         protect_sink=protect_sink, protect_recent=protect_recent, keep_self=keep_self,
+                         candidate_selection="topk", device=device)
+        s = min(max(1, self.dims), head_dim)
+        _require(head_dim <= 128, "the lagged reuse modes take head_dim <= 128")
+        self.qdims = [torch.zeros((self.rows, s), dtype=torch.int32, device=device) for _ in range(2)]
+        self.qvals = [torch.zeros((self.rows, s), dtype=torch.float32, device=device) for _ in range(2)]
+        self.flags = torch.zeros(self.rows, dtype=torch.uint8, device=device)
+        self.union = torch.zeros((self.rows, self.capacity), dtype=torch.uint8, device=device)
+
+    def _parse_mode(self, mode: str) -> tuple[int, float, bool, bool, int | None]:
+        self.kind, self.param, dims, frac = parse_lagged_mode(mode)
+        # the lagged modes read the previous final selection only (EV:4147-4152)
+        return dims, frac, False, True, None
+
+    def refresh_of(self, history: int, has_previous: bool) -> str:
+        """Which rows take new candidates at ``history`` (``REFRESH`` key)."""
+        if not has_previous:
+            return "all"   # no previous final selection: every row selects (EV:4116)
+        if self.kind == "lagrefresh":
+            return "all" if history % int(self.param) == 0 else "none"
+        return LAGGED_KINDS[self.kind][1]
+
+    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
+               current: torch.Tensor, previous: torch.Tensor | None, previous_final: torch.Tensor | None, *,
+               previous_thresholds: bool = False) -> None:
+        """The lagged step's kernels at the history key.size(2) - 1:
+        ``previous_final`` (None on a sequence's first step) is the last
+        step's final mask; ``previous`` is not read.  The top-|q| dims go to
+        ``self.qdims[self.flip]``, the last step's are read from the other."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        history = key_count - 1
+        _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
+        q = query.contiguous()
+        has_prev = previous_final is not None
+        test = LAGGED_KINDS[self.kind][0]
+        refresh = self.refresh_of(history, has_prev)
+        if test is not None:
+            cur_d, prev_d = self.qdims[self.flip], self.qdims[1 - self.flip]
+            cur_v, prev_v = self.qvals[self.flip], self.qvals[1 - self.flip]
+            run = test if has_prev else "dims"
+            lag_flags(q, self.kv_heads, run, self.dims, cur_d, cur_v, self.flags, previous_dims=prev_d,
+                      previous_values=prev_v, key=key if run == "ess" else None, history=history,
+                      previous_final=previous_final if run == "ess" else None, scaling=scaling,
+                      ess_threshold=float(self.param) if self.kind == "pconf" else 0.0)
+        if refresh != "none":
+            reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
+            requested = budget_count(history, self.cand_fraction)
+            self.mask_ws = self._grow(self.mask_ws,
+                                      lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+            threshold_mask(self.partial, history, requested, current, self.mask_ws)   # EV:3988-3989
+        lag_union(current, previous_final, self.flags, self.batch, self.q_heads, history, refresh,
+                  self.kind == "qdriftshare" and has_prev, self.sink, self.recent, self.union)
+        self._select_attend(q, key, value, scaling, self.union, None, None)

@@ -1,0 +1,255 @@
+"""GPU parity of the lagged reuse modes (lagtop2, lagrefresh{N}, qdrift*,
+pconf{T}) against the reference's own golden vectors and the oracle: masks,
+refresh flags and recorded dims bit-exact, attention within 1e-2 relative /
+2e-2 absolute (bf16)."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import qabs_cuda_kernels as Q
+from kv_cache_amd import reuse as RU
+from oracle import ref_semantics as R
+from tests.test_oracle_lagged import LAG_SCENARIOS, load_lagged
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 1e-2, 2e-2
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", [n for n in LAG_SCENARIOS if n.endswith("bf16")])
+def test_lagged_step_matches_reference_vectors(name):
+    # The GQA-native step on the reference's bf16 scenarios: at every step the
+    # candidates, the final mask, the recorded top-|q| dims and the output
+    # equal the reference's.
+    g = load_lagged(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
+    v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
+    step = RU.LaggedReuseDecodeStep(g["mode"], 1, hq, hkv, 128, 1024, top_fraction=g["top_fraction"],
+                                    protect_sink=g["sink"], protect_recent=g["recent"], keep_self=g["keep_self"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
+        out = step(q, k[:, :, :n], v[:, :, :n], g["scaling"])
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), g["candidate"][s][..., : n - 1]), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), g["final"][s][..., : n - 1]), s
+        if RU.LAGGED_KINDS[g["kind"]][0] is not None:
+            dims = step.qdims[1 - step.flip].view(1, hq, -1).cpu().numpy()
+            assert np.array_equal(np.sort(dims, axis=-1), np.sort(g["qdims"][s], axis=-1)), s
+        np.testing.assert_allclose(f32(out), g["out"][s], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("name", [n for n in LAG_SCENARIOS if n.endswith("fp32")])
+def test_lagged_pieces_match_reference_vectors(name):
+    # The fp32 scenarios through the C-ABI pieces on GQA-expanded K (the
+    # reference's hook expands it): refresh flags, union, rerank and final
+    # mask equal the reference's at every step.
+    g = load_lagged(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k_all = torch.from_numpy(np.repeat(g["k"], hq // hkv, axis=1)).to(DEV)
+    v_all = torch.from_numpy(np.repeat(g["v"], hq // hkv, axis=1)).to(DEV)
+    test, per = RU.LAGGED_KINDS[g["kind"]]
+    t_max = k_all.shape[2]
+    s_count = g["dims"]
+    dims = [torch.zeros((hq, s_count), dtype=torch.int32, device=DEV) for _ in range(2)]
+    vals = [torch.zeros((hq, s_count), dtype=torch.float32, device=DEV) for _ in range(2)]
+    flags = torch.zeros(hq, dtype=torch.uint8, device=DEV)
+    cur = torch.zeros((hq, t_max), dtype=torch.uint8, device=DEV)
+    fin = torch.zeros((hq, t_max), dtype=torch.uint8, device=DEV)
+    uni = torch.zeros((hq, t_max), dtype=torch.uint8, device=DEV)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        hist = n - 1
+        q = torch.from_numpy(g["q"][s]).to(DEV)
+        k, v = k_all[:, :, :n], v_all[:, :, :n]
+        has_prev = s > 0
+        run = test if has_prev else "dims"
+        RU.lag_flags(q, hq, run, s_count, dims[s % 2], vals[s % 2], flags, previous_dims=dims[1 - s % 2],
+                     previous_values=vals[1 - s % 2], key=k, history=hist, previous_final=fin,
+                     scaling=g["scaling"], ess_threshold=g["param"] or 0.0)
+        refresh = per if has_prev else "all"
+        part = Q.partial_scores(q, k[:, :, :hist], s_count).view(hq, hist)
+        req = R.budget_count(hist, g["cand"])
+        ws = torch.empty(max(1, Q._lib.load().qkv_threshold_mask_workspace_bytes(hq, hist, req)) // 4 + 1,
+                         dtype=torch.float32, device=DEV)
+        RU.threshold_mask(part, hist, req, cur, ws)
+        RU.lag_union(cur, fin if has_prev else None, flags, 1, hq, hist, refresh,
+                     g["kind"] == "qdriftshare" and has_prev, g["sink"], g["recent"], uni)
+        assert np.array_equal(cur[:, :hist].cpu().numpy().astype(bool), g["candidate"][s][0, :, :hist]), s
+        fi, fv, hf = Q.reuse_select(q, k, uni[:, :hist].view(torch.bool).view(1, hq, hist), None, None, g["sink"],
+                                    g["recent"], g["top_fraction"], g["keep_self"], g["scaling"])
+        assert np.array_equal(hf.cpu().numpy(), g["final"][s][..., :hist]), s
+        np.testing.assert_allclose(f32(Q.final_attention(q, k, v, fi, fv, g["scaling"]))[:, 0], g["out"][s],
+                                   rtol=1e-3, atol=1e-3)
+        fin.zero_()
+        fin[:, :hist] = hf.view(hq, hist).view(torch.uint8)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,hkv,hist,dens", [(8, 2, 3000, 0.03), (4, 4, 70000, 0.2), (6, 3, 37, 0.5),
+                                                 (2, 1, 20000, 0.0)])
+def test_lag_flags_ess_matches_oracle(dtype, rows, hkv, hist, dens):
+    # the ESS statistic over a random previous final mask, every pass size:
+    # rows longer than one 32768-position pass, lists past the 8192-entry LDS
+    # list, empty masks (flagged); rows within 1e-4 of the threshold are left out
+    gen = torch.Generator().manual_seed(rows * 7 + hist)
+    q = (torch.randn((1, rows, 128), generator=gen) * 0.5).to(dtype)
+    k = torch.randn((1, hkv, hist + 1, 128), generator=gen).to(dtype)
+    m = torch.rand((rows, hist), generator=gen) < dens
+    if rows > 2:
+        m[1] = False
+    ld = hist + 13 if hist % 2 else (hist + 15) // 16 * 16 + 16   # byte loads, then 16-byte loads
+    mask = torch.zeros((rows, ld), dtype=torch.uint8)
+    mask[:, :hist] = m.to(torch.uint8)
+    mask[:, hist:] = 1   # past the history: never read
+    kx = np.repeat(f32(k), rows // hkv, axis=1)
+    ess = R.previous_final_ess_fraction(f32(q), kx, m.numpy()[None], 128 ** -0.5, dtype == torch.bfloat16)[0]
+    thr = float(np.median(ess[ess < 1e11])) if (ess < 1e11).any() else 0.5
+    flags = torch.full((rows,), 7, dtype=torch.uint8, device=DEV)
+    dims = torch.empty((rows, 8), dtype=torch.int32, device=DEV)
+    vals = torch.empty((rows, 8), dtype=torch.float32, device=DEV)
+    RU.lag_flags(q.to(DEV), hkv, "ess", 8, dims, vals, flags, key=k.to(DEV), history=hist,
+                 previous_final=mask.to(DEV), scaling=128 ** -0.5, ess_threshold=thr)
+    got = flags.cpu().numpy()
+    assert set(got.tolist()) <= {0, 1}
+    clear = np.abs(ess - thr) > 1e-4
+    assert np.array_equal(got[clear].astype(bool), (ess > thr)[clear])
+    if rows > 2:
+        assert got[1] == 1   # an empty previous selection refreshes
+
+
+@pytest.mark.parametrize("s_count", [1, 4, 8, 16, 33, 128])
+def test_lag_flags_overlap_and_cos_match_oracle(s_count):
+    gen = torch.Generator().manual_seed(s_count)
+    rows = 16
+    base = torch.randn((1, rows, 128), generator=gen)
+    eps = torch.linspace(0, 3, rows).view(1, rows, 1)
+    q0 = base.to(torch.bfloat16)
+    q1 = (base + eps * torch.randn((1, rows, 128), generator=gen)).to(torch.bfloat16)
+    q1[0, 3] = -q0[0, 3]   # same dims, opposite direction: only the cosine test flags it
+    dims = [torch.empty((rows, s_count), dtype=torch.int32, device=DEV) for _ in range(2)]
+    vals = [torch.empty((rows, s_count), dtype=torch.float32, device=DEV) for _ in range(2)]
+    RU.lag_flags(q0.to(DEV), 1, "dims", s_count, dims[0], vals[0])
+    want_d = np.stack([R.select_dims_by_abs(f32(q0)[0, r], s_count) for r in range(rows)])
+    assert np.array_equal(dims[0].cpu().numpy(), want_d)
+    assert np.array_equal(vals[0].cpu().numpy(), np.take_along_axis(f32(q0)[0], want_d, -1))
+    prev = {"final": np.ones((1, rows, 4), bool), "dims": want_d[None], "values": vals[0].cpu().numpy()[None]}
+    kk = np.zeros((1, 1, 5, 128), np.float32)
+    for test, kind in (("overlap", "qdrifthead"), ("cos", "qdriftcoshead")):
+        flags = torch.full((rows,), 9, dtype=torch.uint8, device=DEV)
+        RU.lag_flags(q1.to(DEV), 1, test, s_count, dims[1], vals[1], flags, previous_dims=dims[0],
+                     previous_values=vals[0])
+        *_, want = R.lagged_reuse_decode_step(f32(q1), kk, kk, kind, None, s_count, 0.5, 0.5, 0, 0, True, 0.1,
+                                              prev)
+        assert np.array_equal(flags.cpu().numpy().astype(bool), want[0]), test
+        assert 0 < int(flags.sum()) < rows or s_count == 128
+        if test == "cos":
+            assert flags[3].item() == 1
+
+
+@pytest.mark.parametrize("refresh,share", [("none", False), ("all", False), ("per_row", False), ("per_row", True),
+                                           ("any", False), ("majority", False)])
+@pytest.mark.parametrize("batch,hq,hist,ld", [(2, 4, 1000, 1024), (1, 3, 37, 37), (3, 2, 4113, 4200)])
+def test_lag_union_matches_numpy(refresh, share, batch, hq, hist, ld):
+    gen = torch.Generator().manual_seed(hist + hq)
+    rows = batch * hq
+    cur = (torch.rand((rows, ld), generator=gen) < 0.05).to(torch.uint8)
+    fin = (torch.rand((rows, ld), generator=gen) < 0.03).to(torch.uint8)
+    flags = (torch.rand(rows, generator=gen) < 0.4).to(torch.uint8)
+    if refresh == "majority":
+        flags[: rows // 2 + 1] = 1
+    sink, recent = 3, 11
+    c, f, fl = cur.numpy().astype(bool)[:, :hist], fin.numpy().astype(bool)[:, :hist], flags.numpy().astype(bool)
+    fresh = {"none": np.zeros(rows, bool), "all": np.ones(rows, bool), "per_row": fl,
+             "any": np.full(rows, fl.any()), "majority": np.full(rows, fl.sum() * 2 > rows)}[refresh]
+    want_cur = c & fresh[:, None]
+    want = want_cur | f
+    if share:
+        want |= np.repeat(want_cur.reshape(batch, hq, hist).any(axis=1), hq, axis=0)
+    want[:, :sink] = True
+    want[:, max(0, hist - recent):] = True
+    cur_d = cur.to(DEV)
+    out = torch.full((rows, ld), 5, dtype=torch.uint8, device=DEV)
+    RU.lag_union(cur_d, fin.to(DEV), flags.to(DEV), batch, hq, hist, refresh, share, sink, recent, out)
+    assert np.array_equal(out[:, :hist].cpu().numpy().astype(bool), want)
+    assert (out[:, hist:] == 5).all()
+    got_cur = cur_d.cpu().numpy()
+    assert np.array_equal(got_cur[:, :hist].astype(bool), want_cur)
+    assert np.array_equal(got_cur[:, hist:], cur.numpy()[:, hist:])   # past the history: untouched
+    # no previous final mask (a sequence's first step)
+    out2 = torch.zeros((rows, ld), dtype=torch.uint8, device=DEV)
+    RU.lag_union(cur.to(DEV), None, flags.to(DEV), batch, hq, hist, "all", False, 0, 0, out2)
+    assert np.array_equal(out2[:, :hist].cpu().numpy().astype(bool), c)
+
+
+def test_lag_entry_points_reject_bad_arguments():
+    q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device=DEV)
+    d = torch.zeros((4, 8), dtype=torch.int32, device=DEV)
+    v = torch.zeros((4, 8), dtype=torch.float32, device=DEV)
+    fl = torch.zeros(4, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="need the previous dims"):
+        RU.lag_flags(q, 2, "overlap", 8, d, v, fl)
+    with pytest.raises(RuntimeError, match="ESS test needs K"):
+        RU.lag_flags(q, 2, "ess", 8, d, v, fl, history=10)
+    with pytest.raises(RuntimeError, match="head_dim must be in"):
+        RU.lag_flags(torch.zeros((1, 4, 256), dtype=torch.bfloat16, device=DEV), 2, "dims", 8, d, v)
+    m = torch.zeros((4, 64), dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="null flags"):
+        RU.lag_union(m, None, None, 1, 4, 64, "any", False, 0, 0, m.clone())
+    with pytest.raises(RuntimeError, match="mask_ld and union_ld"):
+        RU.lag_union(m, None, fl, 1, 4, 65, "all", False, 0, 0, m.clone())
+    with pytest.raises(RuntimeError, match="not a lagged reuse mode"):
+        RU.LaggedReuseDecodeStep("qabs8cand5reuse", 1, 4, 2, 128, 256)
+    with pytest.raises(RuntimeError, match="topk candidate selection only"):
+        RU.LaggedReuseDecodeStep("pconf50qabs8cand5", 1, 4, 2, 128, 256, candidate_selection="sample_quantile")
+
+
+@pytest.mark.parametrize("mode", ["pconf50qabs8cand5", "qdriftmajqabs8cand5", "lagrefresh2qabs8cand5"])
+def test_lagged_step_graph_replays(mode):
+    # a lagged step captured at a fixed history: every replay, with a new query
+    # copied in and the outputs cleared between replays, matches the eager launch
+    gen = torch.Generator().manual_seed(len(mode))
+    t = 2000
+    k = torch.randn((1, 2, t + 3, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn((1, 2, t + 3, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, 8, 128), generator=gen).to(torch.bfloat16).to(DEV)
+    step = RU.LaggedReuseDecodeStep(mode, 1, 8, 2, 128, t + 64, top_fraction=0.02, protect_sink=4, protect_recent=8)
+    for n in (t, t + 1, t + 2):
+        step(q, k[:, :, :n], v[:, :, :n], 128 ** -0.5)
+    cur = step.cand[step.flip]
+    fin_prev = step.fin.clone()
+    kk, vv = k[:, :, : t + 3], v[:, :, : t + 3]
+    if step.kdm_len < t + 2:
+        RU.dim_major_append(kk, step.kdm, step.kdm_len, t + 2)
+        step.kdm_len = t + 2
+
+    def launch():
+        step.fin.copy_(fin_prev)
+        step.launch(q, kk, vv, 128 ** -0.5, cur, None, step.fin)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    outs = (cur, step.fin, step.flags, step.out, step.union)
+    for rep in range(4):
+        q.copy_(torch.randn((1, 8, 128), generator=gen).to(torch.bfloat16))
+        launch()
+        want = [x.clone() for x in outs]
+        for x in outs:
+            x.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for w, x in zip(want, outs):
+            assert torch.equal(w, x), rep
