@@ -663,14 +663,17 @@ def run_reuse(args) -> dict:
     scaling = d ** -0.5
     log(f"[bench] setup {c['name']}: {layers} layers, {c['mode']}, top {c['top_fraction']}, sink/recent "
         f"{c['sink']}/{c['recent']}, capacity {cap}")
+    # the lagged modes (lagtop2 / lagrefresh{N} / qdrift* / pconf{T}) run their own step
+    lagged = RU._LAGGED.fullmatch(c["mode"]) is not None
+    step_cls = RU.LaggedReuseDecodeStep if lagged else RU.ReuseDecodeStep
     g = torch.Generator(device="cuda").manual_seed(0)
     ks, vs, qs, steps = [], [], [], []
     for layer in range(layers):
         k = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
         v = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
         q = torch.randn((b, hq, d), generator=g, device="cuda").to(torch.bfloat16)
-        st = RU.ReuseDecodeStep(c["mode"], b, hq, hkv, d, cap, top_fraction=c["top_fraction"],
-                                protect_sink=c["sink"], protect_recent=c["recent"], candidate_selection=selection)
+        st = step_cls(c["mode"], b, hq, hkv, d, cap, top_fraction=c["top_fraction"],
+                      protect_sink=c["sink"], protect_recent=c["recent"], candidate_selection=selection)
         st.prefill(k[:, :, :t0])
         ks.append(k)
         vs.append(v)
@@ -705,7 +708,10 @@ def run_reuse(args) -> dict:
     st0 = steps[0]
     hist_fixed = hist - 1
     cur, prev, fin = st0.cand[1 - st0.flip], st0.cand[st0.flip], st0.fin
-    union = int(((cur[:, :hist_fixed] | prev[:, :hist_fixed]) | fin[:, :hist_fixed]).count_nonzero())
+    if lagged:   # the union the lagged step reranked (previous final | candidates | protected ranges)
+        union = int(st0.union[:, :hist_fixed].count_nonzero())
+    else:
+        union = int(((cur[:, :hist_fixed] | prev[:, :hist_fixed]) | fin[:, :hist_fixed]).count_nonzero())
     n_out = st0.n_out
     rows = b * hq
 
@@ -735,7 +741,11 @@ def run_reuse(args) -> dict:
     log(f"[bench] graph step (history {hist_fixed}): {ms_graph * 1e3 / layers:.1f} us/layer")
 
     mask_ws = [steps[l].mask_ws for l in range(layers)]
-    s_dims, cand_frac, _, _, block = RU.parse_reuse_mode(c["mode"])
+    if lagged:
+        _, _, s_dims, cand_frac = RU.parse_lagged_mode(c["mode"])
+        block = None
+    else:
+        s_dims, cand_frac, _, _, block = RU.parse_reuse_mode(c["mode"])
     requested = RU.budget_count(hist_fixed, cand_frac)
 
     def run_partial():
@@ -804,6 +814,47 @@ def run_reuse(args) -> dict:
     ]
     if block is not None:   # one byte read and one written per history position
         plan.insert(3, ("reuse_expand_blocks", run_expand, rows * hist_fixed * 2))
+    if lagged:
+        test = RU.LAGGED_KINDS[st0.kind][0]
+        refresh = st0.refresh_of(hist_fixed, True)
+        share = st0.kind == "qdriftshare"
+
+        def run_flags():
+            for layer in range(layers):
+                st, kk, _ = fixed(layer)
+                RU.lag_flags(qs[layer], hkv, test, s_dims, st.qdims[st.flip], st.qvals[st.flip], st.flags,
+                             previous_dims=st.qdims[1 - st.flip], previous_values=st.qvals[1 - st.flip], key=kk,
+                             history=hist_fixed, previous_final=st.fin, scaling=scaling,
+                             ess_threshold=float(st.param) if st.kind == "pconf" else 0.0,
+                             workspace=st.ess_ws if test == "ess" else None)
+
+        def run_union():
+            for layer in range(layers):
+                st = steps[layer]
+                RU.lag_union(st.cand[0], st.fin, st.flags, b, hq, hist_fixed, refresh, share, c["sink"], c["recent"],
+                             st.union)
+
+        # candidates and previous final read, union written per position
+        plan.insert(2, ("lag_union", run_union, rows * hist_fixed * 3))
+        if test is not None:   # ess: the mask row, then the K row of every previous final token
+            fin_tokens = int(st0.fin[:, :hist_fixed].count_nonzero())
+            plan.insert(0, ("lag_flags", run_flags, rows * hist_fixed + fin_tokens * d * 2 if test == "ess"
+                            else rows * (d * 2 + s_dims * 16)))
+        # partial scores and candidate mask of the rows that refresh only
+        flagged = int(st0.flags.count_nonzero())
+        n_fresh = {"none": 0, "all": rows, "per_row": flagged, "any": rows if flagged else 0,
+                   "majority": rows if 2 * flagged > rows else 0}[refresh]
+
+        def run_cands():
+            for layer in range(layers):
+                st = steps[layer]
+                RU.lag_candidates(qs[layer], st.kdm, hist_fixed, s_dims, requested, st.flags, refresh, st.partial,
+                                  st.cand[0], mask_ws[layer])
+
+        plan = [p for p in plan if p[0] not in ("reuse_partial_scores", mask_name)]
+        if refresh != "none":
+            plan.insert(1 if test is not None else 0,
+                        ("lag_candidates", run_cands, n_fresh * hist_fixed * (s_dims * 2 + 4 + 4 + 1)))
     kernels = {}
     for name, fn, nbytes in plan:
         gk = graph_of(repeated(fn))
@@ -838,7 +889,9 @@ def run_reuse(args) -> dict:
         "data": "synthetic (seeded N(0,1) K/V/q)",
         "config": {"workload": f"reuse: {c['name']}", "batch": b, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
                    "history": t0, "layers": layers, "mode": c["mode"], "candidate_selection": selection,
-                   "top_fraction": c["top_fraction"], "sink": c["sink"], "recent": c["recent"], "graph": False},
+                   "top_fraction": c["top_fraction"], "sink": c["sink"], "recent": c["recent"], "graph": False,
+                   **({"refresh": st0.refresh_of(hist_fixed, True),
+                       "flagged_rows": int(st0.flags.count_nonzero())} if lagged else {})},
         "us_per_layer": ms_per_step * 1e3 / layers,
         "graph_us_per_layer": None if ms_graph is None else ms_graph * 1e3 / layers,
         "union_tokens_per_row": union / rows,

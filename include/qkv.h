@@ -406,12 +406,33 @@ int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld,
  *     scaling rounded again; weights softmax(s); flagged when the mask is
  *     empty or (1 / sum w^2) / count > ess_threshold (EV:4068-4087).
  * query [B,Hq,D] (D <= 128); key [B,Hkv,>=history,D] with k_strides
- * {b,h,t,d} (d contiguous), read by QKV_LAG_ESS only.  history < 2^30. */
+ * {b,h,t,d} (d contiguous), read by QKV_LAG_ESS only.  history < 2^30.
+ * QKV_LAG_ESS also takes a workspace of
+ * qkv_reuse_lag_flags_workspace_bytes(batch * q_heads, history) bytes (its
+ * per-span partial sums; contents need no clearing); the other tests none. */
 int qkv_reuse_lag_flags(const void* query, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                         int64_t head_dim, int64_t dim_count, int test, const int32_t* previous_dims,
                         const float* previous_values, int32_t* dims_out, float* values_out, const void* key,
                         const int64_t* k_strides, int64_t history, const uint8_t* previous_final, int64_t mask_ld,
-                        float scaling, float ess_threshold, uint8_t* flags, void* stream);
+                        float scaling, float ess_threshold, uint8_t* flags, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of qkv_reuse_lag_flags' QKV_LAG_ESS test (-1 for bad sizes). */
+int64_t qkv_reuse_lag_flags_workspace_bytes(int64_t rows, int64_t history);
+
+/* The candidates of a lagged reuse step (EV:4089-4145): qkv_reuse_partial_scores
+ * into partial, then qkv_threshold_mask (mask = partial >= the row's k-th
+ * largest; workspace of qkv_threshold_mask_workspace_bytes(batch * q_heads,
+ * history, k) bytes), for the rows that refresh under `refresh`
+ * (QKV_REFRESH_*, from flags [batch * q_heads] for the last three; nothing
+ * runs under QKV_REFRESH_NONE).  The other rows' partial and mask rows are
+ * left as they were (qkv_reuse_lag_union clears their candidates); rows
+ * longer than 40960 positions are all computed. */
+int qkv_reuse_lag_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
+                             int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
+                             int64_t dim_count, int64_t k, const uint8_t* flags, int refresh, float* partial,
+                             int64_t partial_ld, uint8_t* mask, int64_t mask_ld, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 
 /* The candidate union of a lagged reuse step (EV:4089-4175), for
  * qkv_reuse_select with no previous masks.  A row refreshes per `refresh`
@@ -421,7 +442,7 @@ int qkv_reuse_lag_flags(const void* query, int dtype, int64_t batch, int64_t q_h
  * rows) | previous_final[r, t] (when not NULL) | (with share) current[r', t]
  * for any refreshed row r' of the same sequence | t < protect_sink | t >=
  * history - protect_recent, for t < history.  current, previous_final row
- * stride mask_ld; union_out row stride union_ld; q_heads <= 1024. */
+ * stride mask_ld; union_out row stride union_ld. */
 int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_final, int64_t mask_ld, const uint8_t* flags,
                         int64_t batch, int64_t q_heads, int64_t history, int refresh, int share,
                         int64_t protect_sink, int64_t protect_recent, uint8_t* union_out, int64_t union_ld,

@@ -5,11 +5,14 @@
 //
 //   lag_flags_kernel   one workgroup per row: the row's top-|q| dims and their
 //                      q values (the state the next step compares with), then
-//                      the row's refresh test: top-dim overlap, overlap or
-//                      cosine, or the effective sample size of the previous
-//                      final selection's attention weights;
-//   lag_union_kernel   16 positions per thread, every head of a sequence:
-//                      keeps the current candidates of the rows that refresh
+//                      the row's refresh test: top-dim overlap, or overlap or
+//                      cosine;
+//   lag_ess_kernel     the pconf test, a row's positions split over several
+//     + lag_ess_merge_kernel  workgroups: the effective sample size of the
+//                      attention weights over the previous final selection;
+//   lag_union_kernel   16 positions of one row per thread (a workgroup per
+//                      4096 positions of a row): keeps the current candidates
+//                      of the rows that refresh
 //                      (zeroes the others), and writes the union with the
 //                      previous final mask, the candidates shared across heads
 //                      (qdriftshare) and the sink / recent ranges.
@@ -25,11 +28,9 @@ namespace {
 
 constexpr int kLagNT = 256;                    // threads per workgroup (4 waves)
 constexpr int kLagWaves = kLagNT / 64;
-constexpr int kLagChunks = 8;                  // ESS: 16-position mask chunks per thread and pass
-constexpr int kLagSpan = kLagNT * 16 * kLagChunks;   // ESS: positions per pass
-constexpr int kLagList = 8192;                 // ESS: positions gathered in LDS per pass
+constexpr int kLagPass = kLagNT * 16;          // ESS: mask positions per pass (16 per thread)
+constexpr int kLagWGs = 1024;                  // ESS: target workgroups (rows x splits)
 constexpr int kUnionChunk = 16;                // union: positions per thread
-constexpr int kMaxLagHeads = 1024;             // union: query heads per sequence
 
 // Bit j set when byte j of the 16 bytes is nonzero.
 __device__ __forceinline__ uint32_t nonzero_bytes(uint4 w) {
@@ -44,11 +45,9 @@ __device__ __forceinline__ uint32_t nonzero_bytes(uint4 w) {
 
 template <int DT>
 __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
-    const typename Elem<DT>::T* __restrict__ query, int q_heads, int group, int head_dim, int count, int test,
+    const typename Elem<DT>::T* __restrict__ query, int head_dim, int count, int test,
     const int32_t* __restrict__ prev_dims, const float* __restrict__ prev_vals, int32_t* __restrict__ dims_out,
-    float* __restrict__ vals_out, const typename Elem<DT>::T* __restrict__ key, int64_t sb, int64_t sh, int64_t st,
-    bool kvec, int history, const uint8_t* __restrict__ prev_final, int64_t mask_ld, bool mvec, float scaling,
-    float ess_threshold, uint8_t* __restrict__ flags) {
+    float* __restrict__ vals_out, uint8_t* __restrict__ flags) {
   using E = typename Elem<DT>::T;
   __shared__ float q_s[128];
   __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
@@ -57,10 +56,12 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
   __shared__ int pd_s[128];
   __shared__ int cnt_s[kLagWaves];
   __shared__ float red_s[3][kLagWaves];
-  __shared__ int list[kLagList];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const E* q_row = query + static_cast<int64_t>(row) * head_dim;
   for (int d = tid; d < 128; d += kLagNT) q_s[d] = d < head_dim ? Elem<DT>::load(q_row + d) : 0.f;
+  if (test != QKV_LAG_DIMS)   // the previous dims load beside q (published by the ranking's barriers)
+    for (int s = tid; s < count; s += kLagNT)
+      pd_s[s] = min(max(prev_dims[static_cast<int64_t>(row) * count + s], 0), head_dim - 1);
   __syncthreads();
   // the step's top-|q| dims, descending |q| with ties to the lower dim, and
   // q at them (EV:4026-4027, recorded at EV:4384-4393)
@@ -70,11 +71,7 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
     vals_out[static_cast<int64_t>(row) * count + s] = sel_q[s];
   }
   if (test == QKV_LAG_DIMS) return;
-
-  if (test == QKV_LAG_OVERLAP || test == QKV_LAG_COS) {
-    for (int s = tid; s < count; s += kLagNT)
-      pd_s[s] = min(max(prev_dims[static_cast<int64_t>(row) * count + s], 0), head_dim - 1);
-    __syncthreads();
+  {
     // current dims found among the previous ones (EV:4047-4048)
     int hit = 0;
     for (int s = tid; s < count; s += kLagNT) {
@@ -119,58 +116,60 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
     return;
   }
 
-  // QKV_LAG_ESS (EV:4068-4087): softmax weights of q over the tokens of the
-  // previous final mask (full-D dot rounded to the input dtype, times
-  // scaling rounded again, as the reference's matmul and multiply in that
-  // dtype leave them), ESS = (sum e)^2 / sum e^2 with e = exp(s - max),
-  // flagged when ESS / count > the threshold or the mask is empty.  Each
-  // pass gathers up to kLagList set positions of kLagSpan mask bytes in LDS
-  // and spreads their dot products over the workgroup; positions past the
-  // list are scored by the thread that found them.
+}
+
+// QKV_LAG_ESS (EV:4068-4087): softmax weights of q over the tokens of the
+// previous final mask (full-D dot rounded to the input dtype, times scaling
+// rounded again, as the reference's matmul and multiply in that dtype leave
+// them), ESS = (sum e)^2 / sum e^2 with e = exp(s - max), flagged when
+// ESS / count > the threshold or the mask is empty.  A row's positions are
+// cut into `splits` spans of `span` positions, one workgroup each (the first
+// also records the row's top-|q| dims); a pass gathers the set positions of
+// kLagPass mask bytes in LDS and spreads their dot products over the
+// workgroup.  Each workgroup leaves (max, sum e, sum e^2, count) of its span
+// in part[row * splits + split]; lag_ess_merge_kernel combines them.
+template <int DT>
+__global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
+    const typename Elem<DT>::T* __restrict__ query, int q_heads, int group, int head_dim, int count,
+    int32_t* __restrict__ dims_out, float* __restrict__ vals_out, const typename Elem<DT>::T* __restrict__ key,
+    int64_t sb, int64_t sh, int64_t st, bool kvec, int history, int span, const uint8_t* __restrict__ prev_final,
+    int64_t mask_ld, bool mvec, float scaling, float4* __restrict__ part) {
+  using E = typename Elem<DT>::T;
+  __shared__ float q_s[128];
+  __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
+  __shared__ int sel_idx[128];
+  __shared__ float sel_q[128];
+  __shared__ int cnt_s[kLagWaves];
+  __shared__ float red_s[3][kLagWaves];
+  __shared__ int list[kLagPass];
+  const int split = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const E* q_row = query + static_cast<int64_t>(row) * head_dim;
+  for (int d = tid; d < 128; d += kLagNT) q_s[d] = d < head_dim ? Elem<DT>::load(q_row + d) : 0.f;
+  __syncthreads();
+  if (split == 0) {   // uniform: the row's top-|q| dims, as lag_flags_kernel records them
+    rank_dims128(q_s, key_s, head_dim, count, sel_idx, sel_q);
+    for (int s = tid; s < count; s += kLagNT) {
+      dims_out[static_cast<int64_t>(row) * count + s] = sel_idx[s];
+      vals_out[static_cast<int64_t>(row) * count + s] = sel_q[s];
+    }
+  }
   const int bq = row / q_heads, kvh = (row - bq * q_heads) / group;
   const E* krow = key + bq * sb + kvh * sh;
   const uint8_t* mrow = prev_final + static_cast<int64_t>(row) * mask_ld;
   float m_t = -INFINITY, z_t = 0.f, z2_t = 0.f;
-  auto add = [&](int p) {
-    const E* kp = krow + static_cast<int64_t>(p) * st;
-    float acc = 0.f;
-    if (kvec) {
-      for (int d = 0; d < head_dim; d += 8) {
-        float kv[8];
-        load8<DT>(kp + d, kv);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc += q_s[d + j] * kv[j];
-      }
-    } else {
-      for (int d = 0; d < head_dim; ++d) acc += q_s[d] * Elem<DT>::load(kp + d);
-    }
-    E r = Elem<DT>::store(acc);
-    float s = Elem<DT>::load(&r) * scaling;
-    r = Elem<DT>::store(s);
-    s = Elem<DT>::load(&r);
-    const float m = fmaxf(m_t, s);
-    const float c = __expf(m_t - m), e = __expf(s - m);
-    z_t = z_t * c + e;
-    z2_t = z2_t * c * c + e * e;
-    m_t = m;
-  };
   int total = 0;
-  for (int p0 = 0; p0 < history; p0 += kLagSpan) {
-    uint32_t set[kLagChunks];
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < kLagChunks; ++i) {
-      const int p = p0 + (i * kLagNT + tid) * 16;
-      uint32_t bm = 0;
-      if (mvec && p + 16 <= history) {
-        bm = nonzero_bytes(*reinterpret_cast<const uint4*>(mrow + p));
-      } else {
-        for (int j = 0; j < 16; ++j)
-          if (p + j < history && mrow[p + j]) bm |= 1u << j;
-      }
-      set[i] = bm;
-      c += __builtin_popcount(bm);
+  const int p_begin = split * span, p_end = min(history, p_begin + span);
+  for (int p0 = p_begin; p0 < p_end; p0 += kLagPass) {
+    const int p = p0 + tid * 16;
+    const int n = min(16, p_end - p);
+    uint32_t bm = 0;
+    if (mvec && n == 16) {
+      bm = nonzero_bytes(*reinterpret_cast<const uint4*>(mrow + p));
+    } else {
+      for (int j = 0; j < n; ++j)
+        if (mrow[p + j]) bm |= 1u << j;
     }
+    const int c = __builtin_popcount(bm);
     const int inc = wave_incl_scan(c);
     if (lane == 63) cnt_s[wave] = inc;
     __syncthreads();
@@ -179,33 +178,67 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
       off += w < wave ? cnt_s[w] : 0;
       pass += cnt_s[w];
     }
-#pragma unroll
-    for (int i = 0; i < kLagChunks; ++i) {
-      uint32_t bm = set[i];
-      const int p = p0 + (i * kLagNT + tid) * 16;
-      while (bm) {
-        const int j = __builtin_ctz(bm);
-        bm &= bm - 1;
-        if (off < kLagList) list[off] = p + j;
-        else add(p + j);
-        ++off;
-      }
+    while (bm) {
+      const int j = __builtin_ctz(bm);
+      bm &= bm - 1;
+      list[off++] = p + j;
     }
     __syncthreads();
-    const int n = min(pass, kLagList);
-    for (int e = tid; e < n; e += kLagNT) add(list[e]);
+    for (int e = tid; e < pass; e += kLagNT) {
+      const E* kp = krow + static_cast<int64_t>(list[e]) * st;
+      float acc = 0.f;
+      if (kvec && head_dim == 128) {   // every load of the row in flight before the arithmetic
+        constexpr int kWords = DT == QKV_DTYPE_FP32 ? 32 : 16;   // 16-byte words of a 128-dim row
+        constexpr int kPer = 128 / kWords;
+        uint4 raw[kWords];
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) raw[i] = reinterpret_cast<const uint4*>(kp)[i];
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) {
+          const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+          for (int j = 0; j < kPer; ++j) {
+            float x;
+            if constexpr (DT == QKV_DTYPE_FP32) {
+              x = __uint_as_float(w[j]);
+            } else {
+              const uint16_t h = static_cast<uint16_t>(w[j >> 1] >> (16 * (j & 1)));
+              x = Elem<DT>::load(&h);
+            }
+            acc += q_s[i * kPer + j] * x;
+          }
+        }
+      } else if (kvec) {
+        for (int d = 0; d < head_dim; d += 8) {
+          float kv[8];
+          load8<DT>(kp + d, kv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc += q_s[d + j] * kv[j];
+        }
+      } else {
+        for (int d = 0; d < head_dim; ++d) acc += q_s[d] * Elem<DT>::load(kp + d);
+      }
+      E rr = Elem<DT>::store(acc);
+      float sc = Elem<DT>::load(&rr) * scaling;
+      rr = Elem<DT>::store(sc);
+      sc = Elem<DT>::load(&rr);
+      const float m = fmaxf(m_t, sc);
+      const float a = __expf(m_t - m), ex = __expf(sc - m);
+      z_t = z_t * a + ex;
+      z2_t = z2_t * a * a + ex * ex;
+      m_t = m;
+    }
     total += pass;
     __syncthreads();   // list and cnt_s are rewritten by the next pass
   }
-  // merge the threads' (max, sum e, sum e^2)
-  float mw = wave_max(m_t);
+  // the workgroup's (max, sum e, sum e^2)
+  const float mw = wave_max(m_t);
   if (lane == 0) red_s[0][wave] = mw;
   __syncthreads();
   float mx = red_s[0][0];
   for (int w = 1; w < kLagWaves; ++w) mx = fmaxf(mx, red_s[0][w]);
-  const float sc = m_t == -INFINITY ? 0.f : __expf(m_t - mx);
-  const float z = wave_sum(z_t * sc), z2 = wave_sum(z2_t * sc * sc);
-  __syncthreads();
+  const float f = m_t == -INFINITY ? 0.f : __expf(m_t - mx);
+  const float z = wave_sum(z_t * f), z2 = wave_sum(z2_t * f * f);
   if (lane == 0) {
     red_s[1][wave] = z;
     red_s[2][wave] = z2;
@@ -217,9 +250,31 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
       zs += red_s[1][w];
       z2s += red_s[2][w];
     }
-    const bool flagged = total == 0 || (zs * zs / z2s) / static_cast<float>(total) > ess_threshold;
-    flags[row] = flagged ? 1 : 0;
+    part[static_cast<int64_t>(row) * gridDim.x + split] = make_float4(mx, zs, z2s, __int_as_float(total));
   }
+}
+
+__global__ __launch_bounds__(kLagNT) void lag_ess_merge_kernel(const float4* __restrict__ part, int rows, int splits,
+                                                            float ess_threshold, uint8_t* __restrict__ flags) {
+  const int row = blockIdx.x * kLagNT + threadIdx.x;
+  if (row >= rows) return;
+  const float4* pr = part + static_cast<int64_t>(row) * splits;
+  float mx = -INFINITY;
+  int total = 0;
+  for (int i = 0; i < splits; ++i) {
+    const float4 v = pr[i];
+    mx = fmaxf(mx, v.x);
+    total += __float_as_int(v.w);
+  }
+  float z = 0.f, z2 = 0.f;
+  for (int i = 0; i < splits; ++i) {
+    const float4 v = pr[i];
+    if (v.x == -INFINITY) continue;   // an empty span
+    const float f = __expf(v.x - mx);
+    z += v.y * f;
+    z2 += v.z * f * f;
+  }
+  flags[row] = total == 0 || (z * z / z2) / static_cast<float>(total) > ess_threshold ? 1 : 0;
 }
 
 // 16 mask bytes at p, bytes at or past `n` read as 0.
@@ -245,14 +300,14 @@ __global__ __launch_bounds__(kLagNT) void lag_union_kernel(
     uint8_t* __restrict__ cur, const uint8_t* __restrict__ prev_final, int64_t mask_ld,
     const uint8_t* __restrict__ flags, int rows, int q_heads, int history, int refresh, int share, int sink_end,
     int recent_start, uint8_t* __restrict__ uni, int64_t uni_ld, bool vec) {
-  __shared__ uint8_t fresh[kMaxLagHeads];
   __shared__ int cnt_s[kLagWaves];
-  const int b = blockIdx.y, tid = threadIdx.x;
-  // which heads of sequence b keep their current candidates (EV:4024-4115)
+  const int r = blockIdx.y, tid = threadIdx.x;
+  const int b = r / q_heads;
+  // which rows keep their current candidates (EV:4024-4115)
   bool all = refresh == QKV_REFRESH_ALL;
   if (refresh == QKV_REFRESH_ANY || refresh == QKV_REFRESH_MAJORITY) {
     int c = 0;
-    for (int r = tid; r < rows; r += kLagNT) c += flags[r] ? 1 : 0;
+    for (int i = tid; i < rows; i += kLagNT) c += flags[i] ? 1 : 0;
     c = wave_sum_i(c);
     if ((tid & 63) == 0) cnt_s[tid >> 6] = c;
     __syncthreads();
@@ -260,47 +315,65 @@ __global__ __launch_bounds__(kLagNT) void lag_union_kernel(
     for (int w = 0; w < kLagWaves; ++w) t += cnt_s[w];
     all = refresh == QKV_REFRESH_ANY ? t > 0 : 2 * t > rows;   // EV:4057-4066
   }
-  for (int h = tid; h < q_heads; h += kLagNT)
-    fresh[h] = (refresh == QKV_REFRESH_PER_ROW ? flags[b * q_heads + h] != 0 : all) ? 1 : 0;
-  __syncthreads();
+  const bool per_row = refresh == QKV_REFRESH_PER_ROW;
   const int p = (blockIdx.x * kLagNT + tid) * kUnionChunk;
   if (p >= history) return;
   const int n = min(kUnionChunk, history - p);
   uint32_t pw[4] = {0, 0, 0, 0};   // the sink and recent ranges (EV:4166-4171)
   for (int j = 0; j < n; ++j)
     if (p + j < sink_end || p + j >= recent_start) pw[j >> 2] |= 1u << (8 * (j & 3));
-  uint4 base = make_uint4(pw[0], pw[1], pw[2], pw[3]);
-  if (share) {   // the candidates of every refreshed head of the sequence (EV:4107-4109)
-    for (int h = 0; h < q_heads; ++h)
-      if (fresh[h]) base = or4(base, load16(cur + static_cast<int64_t>(b * q_heads + h) * mask_ld, p, n, vec));
+  uint4 u = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+  if (share) {   // the candidates of every refreshed row of the sequence (EV:4107-4109)
+    for (int h = 0; h < q_heads; ++h) {
+      const int i = b * q_heads + h;
+      if (per_row ? flags[i] != 0 : all) u = or4(u, load16(cur + static_cast<int64_t>(i) * mask_ld, p, n, vec));
+    }
   }
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-  for (int h = 0; h < q_heads; ++h) {
-    const int64_t r = b * q_heads + h;
-    uint8_t* crow = cur + r * mask_ld;
-    uint4 u = base;
-    if (fresh[h]) u = or4(u, load16(crow, p, n, vec));
-    else store16(crow, p, n, vec, zero);   // a row that does not refresh has no current candidates
-    if (prev_final) u = or4(u, load16(prev_final + r * mask_ld, p, n, vec));
-    store16(uni + r * uni_ld, p, n, vec, u);
-  }
+  uint8_t* crow = cur + static_cast<int64_t>(r) * mask_ld;
+  if (per_row ? flags[r] != 0 : all) u = or4(u, load16(crow, p, n, vec));
+  else store16(crow, p, n, vec, make_uint4(0, 0, 0, 0));   // a row that does not refresh has no candidates
+  if (prev_final) u = or4(u, load16(prev_final + static_cast<int64_t>(r) * mask_ld, p, n, vec));
+  store16(uni + static_cast<int64_t>(r) * uni_ld, p, n, vec, u);
+}
+
+// Spans of the ESS test: about kLagWGs workgroups over the rows, each span a
+// whole number of passes.
+struct EssSplit {
+  int splits, span;
+};
+EssSplit ess_split(int64_t rows, int64_t history) {
+  const int64_t passes = cdiv(history, kLagPass);
+  const int64_t want = std::min<int64_t>(std::max<int64_t>(cdiv(kLagWGs, rows), 1), passes);
+  const int64_t span = cdiv(passes, want) * kLagPass;
+  return {static_cast<int>(cdiv(history, span)), static_cast<int>(span)};
 }
 
 template <int DT> struct RunLagFlags {
   static int run(const void* q, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int count, int test,
                  const int32_t* pd, const float* pv, int32_t* dims_out, float* vals_out, const void* key,
                  const int64_t* ks, int64_t history, const uint8_t* prev_final, int64_t mask_ld, float scaling,
-                 float ess_threshold, uint8_t* flags, hipStream_t st) {
+                 float ess_threshold, uint8_t* flags, void* workspace, hipStream_t st) {
     using E = typename Elem<DT>::T;
+    const char* what = "qkv_reuse_lag_flags";
+    if (test != QKV_LAG_ESS) {
+      lag_flags_kernel<DT><<<static_cast<unsigned>(B * Hq), kLagNT, 0, st>>>(
+          static_cast<const E*>(q), static_cast<int>(D), count, test, pd, pv, dims_out, vals_out, flags);
+      return check_launch(what);
+    }
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
-    const bool kvec = key && D % 8 == 0 && aligned(key, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 &&
-                      ks[2] % ev == 0;
-    const bool mvec = prev_final && aligned(prev_final, 16) && mask_ld % 16 == 0;
-    lag_flags_kernel<DT><<<static_cast<unsigned>(B * Hq), kLagNT, 0, st>>>(
+    const bool kvec = D % 8 == 0 && aligned(key, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
+    const bool mvec = aligned(prev_final, 16) && mask_ld % 16 == 0;
+    const EssSplit sp = ess_split(B * Hq, history);
+    float4* part = static_cast<float4*>(workspace);
+    lag_ess_kernel<DT><<<dim3(static_cast<unsigned>(sp.splits), static_cast<unsigned>(B * Hq)), kLagNT, 0, st>>>(
         static_cast<const E*>(q), static_cast<int>(Hq), static_cast<int>(Hq / Hkv), static_cast<int>(D), count,
-        test, pd, pv, dims_out, vals_out, static_cast<const E*>(key), key ? ks[0] : 0, key ? ks[1] : 0,
-        key ? ks[2] : 0, kvec, static_cast<int>(history), prev_final, mask_ld, mvec, scaling, ess_threshold, flags);
-    return check_launch("qkv_reuse_lag_flags");
+        dims_out, vals_out, static_cast<const E*>(key), ks[0], ks[1], ks[2], kvec, static_cast<int>(history),
+        sp.span, prev_final, mask_ld, mvec, scaling, part);
+    int rc = check_launch(what);
+    if (rc) return rc;
+    lag_ess_merge_kernel<<<static_cast<unsigned>(cdiv(B * Hq, kLagNT)), kLagNT, 0, st>>>(
+        part, static_cast<int>(B * Hq), sp.splits, ess_threshold, flags);
+    return check_launch(what);
   }
 };
 
@@ -309,12 +382,18 @@ template <int DT> struct RunLagFlags {
 
 using namespace qkv;
 
+QKV_EXPORT int64_t qkv_reuse_lag_flags_workspace_bytes(int64_t rows, int64_t history) {
+  if (rows <= 0 || history <= 0 || history >= (int64_t(1) << 30)) return -1;
+  return rows * ess_split(rows, history).splits * static_cast<int64_t>(sizeof(float4));
+}
+
 QKV_EXPORT int qkv_reuse_lag_flags(const void* query, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                                    int64_t head_dim, int64_t dim_count, int test, const int32_t* previous_dims,
                                    const float* previous_values, int32_t* dims_out, float* values_out,
                                    const void* key, const int64_t* k_strides, int64_t history,
                                    const uint8_t* previous_final, int64_t mask_ld, float scaling,
-                                   float ess_threshold, uint8_t* flags, void* stream) {
+                                   float ess_threshold, uint8_t* flags, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
   const char* what = "qkv_reuse_lag_flags";
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || batch * q_heads > 65535)
     return fail(QKV_ERR_INVALID, "%s: need batch * q_heads <= 65535, q_heads a positive multiple of kv_heads", what);
@@ -331,12 +410,16 @@ QKV_EXPORT int qkv_reuse_lag_flags(const void* query, int dtype, int64_t batch, 
     if (k_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: K channels must be contiguous", what);
     if (history <= 0 || history >= (int64_t(1) << 30) || mask_ld < history)
       return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^30 and mask_ld >= history", what);
+    const int64_t need = qkv_reuse_lag_flags_workspace_bytes(batch * q_heads, history);
+    if (!workspace || workspace_bytes < need)
+      return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                  (long long)workspace_bytes);
   }
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), head_dim));
   return dispatch_dtype<RunLagFlags>(dtype, query, batch, q_heads, kv_heads, head_dim, count, test, previous_dims,
                                      previous_values, dims_out, values_out, test == QKV_LAG_ESS ? key : nullptr,
                                      k_strides, history, test == QKV_LAG_ESS ? previous_final : nullptr, mask_ld,
-                                     scaling, ess_threshold, flags, static_cast<hipStream_t>(stream));
+                                     scaling, ess_threshold, flags, workspace, static_cast<hipStream_t>(stream));
 }
 
 QKV_EXPORT int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_final, int64_t mask_ld,
@@ -345,8 +428,8 @@ QKV_EXPORT int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_fin
                                    uint8_t* union_out, int64_t union_ld, void* stream) {
   const char* what = "qkv_reuse_lag_union";
   if (!current || !union_out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
-  if (batch <= 0 || q_heads <= 0 || q_heads > kMaxLagHeads || batch * q_heads > 65535)
-    return fail(QKV_ERR_INVALID, "%s: need 0 < q_heads <= %d and batch * q_heads <= 65535", what, kMaxLagHeads);
+  if (batch <= 0 || q_heads <= 0 || batch * q_heads > 65535)
+    return fail(QKV_ERR_INVALID, "%s: need batch, q_heads > 0 and batch * q_heads <= 65535", what);
   if (history <= 0 || history >= (int64_t(1) << 31) || mask_ld < history || union_ld < history)
     return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, mask_ld and union_ld >= history", what);
   if (refresh < QKV_REFRESH_NONE || refresh > QKV_REFRESH_MAJORITY)
@@ -357,7 +440,7 @@ QKV_EXPORT int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_fin
   const int recent_start = static_cast<int>(std::max<int64_t>(0, history - protect_recent));
   const bool vec = mask_ld % 16 == 0 && union_ld % 16 == 0 && aligned(current, 16) && aligned(union_out, 16) &&
                    (!previous_final || aligned(previous_final, 16));
-  dim3 grid(static_cast<unsigned>(cdiv(history, kLagNT * kUnionChunk)), static_cast<unsigned>(batch));
+  dim3 grid(static_cast<unsigned>(cdiv(history, kLagNT * kUnionChunk)), static_cast<unsigned>(batch * q_heads));
   lag_union_kernel<<<grid, kLagNT, 0, static_cast<hipStream_t>(stream)>>>(
       current, previous_final, mask_ld, flags, static_cast<int>(batch * q_heads), static_cast<int>(q_heads),
       static_cast<int>(history), refresh, share ? 1 : 0, sink_end, recent_start, union_out, union_ld, vec);

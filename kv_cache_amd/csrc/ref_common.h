@@ -120,6 +120,24 @@ __device__ __forceinline__ void load8(const typename Elem<DT>::T* p, float (&v)[
   }
 }
 
+// Whether row `row` takes new candidates in a lagged reuse step (QKV_REFRESH_*
+// over the per-row flags, EV:4024-4115).  Every thread of the workgroup
+// calls it at the same point (the step-wide kinds synchronize); cnt_s holds
+// one int per wave.
+__device__ __forceinline__ bool lag_refreshes(const uint8_t* flags, int refresh, int rows, int row, int* cnt_s) {
+  if (refresh == QKV_REFRESH_ALL) return true;
+  if (refresh == QKV_REFRESH_NONE) return false;
+  if (refresh == QKV_REFRESH_PER_ROW) return flags[row] != 0;
+  int c = 0;
+  for (int i = threadIdx.x; i < rows; i += blockDim.x) c += flags[i] ? 1 : 0;
+  c = wave_sum_i(c);
+  if ((threadIdx.x & 63) == 0) cnt_s[threadIdx.x >> 6] = c;
+  __syncthreads();
+  int t = 0;
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) t += cnt_s[w];
+  return refresh == QKV_REFRESH_ANY ? t > 0 : 2 * t > rows;
+}
+
 template <template <int> class F, typename... A>
 int dispatch_dtype(int dtype, A&&... args) {
   switch (dtype) {

@@ -42,13 +42,18 @@ template <int DT>
 __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm,
     int q_heads, int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd,
-    bool vec, float* __restrict__ out, int64_t out_ld) {
+    bool vec, float* __restrict__ out, int64_t out_ld, const uint8_t* __restrict__ gate, int gate_refresh,
+    int gate_rows) {
   using E = typename Elem<DT>::T;
   __shared__ float q_s[512];
   __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
   __shared__ int sel_idx[kMaxDims];
   __shared__ float sel_q[kMaxDims];
   const int row = blockIdx.y, tid = threadIdx.x;
+  if (gate) {   // a lagged step: rows that keep no new candidates are skipped (uniform)
+    __shared__ int gate_cnt[kRT / 64];
+    if (!lag_refreshes(gate, gate_refresh, gate_rows, row, gate_cnt)) return;
+  }
   const int b = row / q_heads, h = row - b * q_heads;
   const typename Elem<DT>::T* q_row = query + static_cast<int64_t>(row) * head_dim;
   for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
@@ -374,11 +379,17 @@ constexpr int kWideMax = kWideNT * 40;
 template <int VPL>
 __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* __restrict__ values, int64_t ld, int n,
                                                                   int k, uint8_t* __restrict__ mask, int64_t mask_ld,
-                                                                  float* __restrict__ thr_out) {
+                                                                  float* __restrict__ thr_out,
+                                                                  const uint8_t* __restrict__ gate = nullptr,
+                                                                  int gate_refresh = 0, int gate_rows = 0) {
   using WS = WideSelect<VPL, false>;
   __shared__ typename WS::Shared sh;
   WS ws;
   const int row = blockIdx.x, tid = threadIdx.x;
+  if (gate) {   // a lagged step: rows that keep no new candidates are skipped (uniform)
+    __shared__ int gate_cnt[kWideNT / 64];
+    if (!lag_refreshes(gate, gate_refresh, gate_rows, row, gate_cnt)) return;
+  }
   ws.load_count(values + static_cast<int64_t>(row) * ld, n, sh);   // the first digit counted as keys arrive
   ws.run_counted(k, sh);
   if (thr_out) {
@@ -740,7 +751,8 @@ int64_t mask_ws_bytes(int64_t rows, int64_t n, int64_t k) {
 
 template <int DT> struct RunReusePartial {
   static int run(const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv,
-                 int64_t T, int64_t D, int count, float* out, int64_t out_ld, hipStream_t st) {
+                 int64_t T, int64_t D, int count, float* out, int64_t out_ld, hipStream_t st,
+                 const uint8_t* gate = nullptr, int gate_refresh = 0) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
     const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
@@ -748,7 +760,8 @@ template <int DT> struct RunReusePartial {
     reuse_partial_kernel<DT><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),
                                                    static_cast<int>(Hq), static_cast<int>(Hq / Hkv),
                                                    static_cast<int>(T), static_cast<int>(D), count, ks[0], ks[1],
-                                                   ks[2], vec, out, out_ld);
+                                                   ks[2], vec, out, out_ld, gate, gate_refresh,
+                                                   static_cast<int>(B * Hq));
     return check_launch("qkv_reuse_partial_scores");
   }
 };
@@ -801,11 +814,12 @@ int check_heads(const char* what, int64_t batch, int64_t q_heads, int64_t kv_hea
 // mask = values >= the row's k-th largest (threshold to thr_out when given).
 int threshold_mask_impl(const char* what, const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
                         uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
-                        hipStream_t st) {
-  if (n <= kWideMax) {
+                        hipStream_t st, const uint8_t* gate = nullptr, int gate_refresh = 0) {
+  if (n <= kWideMax) {   // (rows past the one-workgroup length are selected whatever the gate says)
     return with_wide_vpl(n, [&](auto vpl) {
       reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
-          values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld, thr_out);
+          values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld, thr_out, gate, gate_refresh,
+          static_cast<int>(rows));
       return check_launch(what);
     });
   }
@@ -977,6 +991,55 @@ QKV_EXPORT int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, 
                 (long long)workspace_bytes);
   return threshold_mask_impl(what, values, rows, n, ld, k, mask, mask_ld, nullptr, workspace, workspace_bytes,
                              static_cast<hipStream_t>(stream));
+}
+
+QKV_EXPORT int qkv_reuse_lag_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                        int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                                        int64_t head_dim, int64_t dim_count, int64_t k, const uint8_t* flags,
+                                        int refresh, float* partial, int64_t partial_ld, uint8_t* mask,
+                                        int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* what = "qkv_reuse_lag_candidates";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !partial || !mask || !workspace)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || partial_ld < history || mask_ld < history || k < 1 ||
+      k > history)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, partial_ld and mask_ld >= history",
+                what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
+  if (refresh < QKV_REFRESH_NONE || refresh > QKV_REFRESH_MAJORITY)
+    return fail(QKV_ERR_INVALID, "%s: unknown refresh %d", what, refresh);
+  if (refresh >= QKV_REFRESH_PER_ROW && !flags) return fail(QKV_ERR_INVALID, "%s: null flags", what);
+  const int64_t rows = batch * q_heads;
+  const int64_t need = mask_ws_bytes(rows, history, k);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  if (refresh == QKV_REFRESH_NONE) return QKV_OK;   // no row takes new candidates
+  const uint8_t* gate = refresh == QKV_REFRESH_ALL ? nullptr : flags;
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
+                                                       std::min<int64_t>(head_dim, kMaxDims)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case QKV_DTYPE_BF16:
+      rc = RunReusePartial<QKV_DTYPE_BF16>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
+                                                head_dim, count, partial, partial_ld, st, gate, refresh);
+      break;
+    case QKV_DTYPE_FP16:
+      rc = RunReusePartial<QKV_DTYPE_FP16>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
+                                                head_dim, count, partial, partial_ld, st, gate, refresh);
+      break;
+    case QKV_DTYPE_FP32:
+      rc = RunReusePartial<QKV_DTYPE_FP32>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
+                                                head_dim, count, partial, partial_ld, st, gate, refresh);
+      break;
+    default:
+      return fail(QKV_ERR_INVALID, "%s: unsupported dtype %d", what, dtype);
+  }
+  if (rc) return rc;
+  return threshold_mask_impl(what, partial, rows, history, partial_ld, k, mask, mask_ld, nullptr, workspace,
+                             workspace_bytes, st, gate, refresh);
 }
 
 QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k,

@@ -491,22 +491,47 @@ def parse_lagged_mode(mode: str) -> tuple[str, float | int | None, int, float]:
 def lag_flags(query: torch.Tensor, kv_heads: int, test: str, dim_count: int, dims_out: torch.Tensor,
               values_out: torch.Tensor, flags: torch.Tensor | None = None, *, previous_dims: torch.Tensor | None = None,
               previous_values: torch.Tensor | None = None, key: torch.Tensor | None = None, history: int = 0,
-              previous_final: torch.Tensor | None = None, scaling: float = 1.0, ess_threshold: float = 0.0) -> None:
+              previous_final: torch.Tensor | None = None, scaling: float = 1.0, ess_threshold: float = 0.0,
+              workspace: torch.Tensor | None = None) -> None:
     """The lagged modes' per-row refresh test (``qkv_reuse_lag_flags``):
     query [B, Hq, D]; dims_out int32 / values_out f32 [B*Hq, S] receive the
     row's top-|q| dims and q at them; flags uint8 [B*Hq] the test's result
     (``test`` in ``LAG_TESTS``).  The ``ess`` test reads key [B, Hkv, T, D]
-    and previous_final uint8 rows of the history."""
+    and previous_final uint8 rows of the history, and takes a workspace
+    (allocated here when not given)."""
     lib = _lib.load()
     q = query.contiguous()
     b, hq, d = q.shape
     mask_ld = previous_final.stride(0) if previous_final is not None else 0
+    if test == "ess" and workspace is None:
+        need = int(lib.qkv_reuse_lag_flags_workspace_bytes(b * hq, history))
+        _require(need > 0, "bad ESS sizes")
+        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
         _lib.check(lib.qkv_reuse_lag_flags(
             q.data_ptr(), _dtype_code(q), b, hq, kv_heads, d, dim_count, LAG_TESTS[test], _lib.ptr(previous_dims),
             _lib.ptr(previous_values), dims_out.data_ptr(), values_out.data_ptr(), _lib.ptr(key),
             _lib.strides(*key.stride()) if key is not None else None, history, _lib.ptr(previous_final), mask_ld,
-            float(scaling), float(ess_threshold), _lib.ptr(flags), _lib.stream_of(q)))
+            float(scaling), float(ess_threshold), _lib.ptr(flags), _lib.ptr(workspace),
+            workspace.numel() * workspace.element_size() if workspace is not None else 0, _lib.stream_of(q)))
+
+
+def lag_candidates(query: torch.Tensor, key_dim_major: torch.Tensor, history: int, dim_count: int, k: int,
+                   flags: torch.Tensor | None, refresh: str, partial: torch.Tensor, mask: torch.Tensor,
+                   workspace: torch.Tensor) -> None:
+    """Partial scores and candidate mask (``partial >= the row's k-th
+    largest``) of the rows that refresh (``qkv_reuse_lag_candidates``);
+    query [B, Hq, D], key_dim_major [B, Hkv, D, >= history]; partial f32 /
+    mask uint8 rows of >= history."""
+    lib = _lib.load()
+    q = query.contiguous()
+    b, hq, d = q.shape
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_reuse_lag_candidates(
+            q.data_ptr(), key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _dtype_code(q), b, hq,
+            key_dim_major.size(1), history, d, dim_count, k, _lib.ptr(flags), REFRESH[refresh], partial.data_ptr(),
+            partial.stride(0), mask.data_ptr(), mask.stride(0), workspace.data_ptr(), workspace.numel() * 4,
+            _lib.stream_of(q)))
 
 
 def lag_union(current: torch.Tensor, previous_final: torch.Tensor | None, flags: torch.Tensor | None, batch: int,
@@ -553,6 +578,9 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
         self.qvals = [torch.zeros((self.rows, s), dtype=torch.float32, device=device) for _ in range(2)]
         self.flags = torch.zeros(self.rows, dtype=torch.uint8, device=device)
         self.union = torch.zeros((self.rows, self.capacity), dtype=torch.uint8, device=device)
+        # the ESS test's per-span sums: at most rows * ceil(1024 / rows) spans
+        self.ess_ws = torch.empty(self.rows * -(-1024 // self.rows) * 4 if self.kind == "pconf" else 1,
+                                  dtype=torch.float32, device=device)
 
     def _parse_mode(self, mode: str) -> tuple[int, float, bool, bool, int | None]:
         self.kind, self.param, dims, frac = parse_lagged_mode(mode)
@@ -589,13 +617,14 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
             lag_flags(q, self.kv_heads, run, self.dims, cur_d, cur_v, self.flags, previous_dims=prev_d,
                       previous_values=prev_v, key=key if run == "ess" else None, history=history,
                       previous_final=previous_final if run == "ess" else None, scaling=scaling,
-                      ess_threshold=float(self.param) if self.kind == "pconf" else 0.0)
-        if refresh != "none":
-            reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
+                      ess_threshold=float(self.param) if self.kind == "pconf" else 0.0,
+                      workspace=self.ess_ws if run == "ess" else None)
+        if refresh != "none":   # the rows that refresh score and threshold (EV:3988-3989, 4089-4106)
             requested = budget_count(history, self.cand_fraction)
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
-            threshold_mask(self.partial, history, requested, current, self.mask_ws)   # EV:3988-3989
+            lag_candidates(q, self.kdm, history, self.dims, requested, self.flags, refresh, self.partial, current,
+                           self.mask_ws)
         lag_union(current, previous_final, self.flags, self.batch, self.q_heads, history, refresh,
                   self.kind == "qdriftshare" and has_prev, self.sink, self.recent, self.union)
         self._select_attend(q, key, value, scaling, self.union, None, None)

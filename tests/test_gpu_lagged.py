@@ -253,3 +253,37 @@ def test_lagged_step_graph_replays(mode):
         torch.cuda.synchronize()
         for w, x in zip(want, outs):
             assert torch.equal(w, x), rep
+
+
+@pytest.mark.parametrize("refresh", ["all", "per_row", "any", "majority", "none"])
+@pytest.mark.parametrize("hist", [3000, 50000])   # one workgroup per row; past it, every row is computed
+def test_lag_candidates_skip_rows_that_keep(refresh, hist):
+    gen = torch.Generator().manual_seed(hist)
+    b, hq, hkv, d, s_count = 2, 4, 2, 128, 8
+    rows = b * hq
+    k = torch.randn((b, hkv, hist + 1, d), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16).to(DEV)
+    kdm = torch.zeros((b, hkv, d, hist + 64), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k, kdm, 0, hist)
+    flags = torch.tensor([1, 0, 0, 1, 0, 1, 0, 0], dtype=torch.uint8, device=DEV)
+    if refresh == "majority":
+        flags[:5] = 1
+    req = R.budget_count(hist, 0.05)
+    ws = torch.empty(Q._lib.load().qkv_threshold_mask_workspace_bytes(rows, hist, req) // 4 + 1,
+                     dtype=torch.float32, device=DEV)
+    part = torch.full((rows, hist + 64), -7.0, device=DEV)
+    mask = torch.full((rows, hist + 64), 9, dtype=torch.uint8, device=DEV)
+    RU.lag_candidates(q, kdm, hist, s_count, req, flags, refresh, part, mask, ws)
+    want_p = RU.reuse_partial_scores(q, kdm, hist, s_count)
+    want_m = torch.zeros((rows, hist), dtype=torch.uint8, device=DEV)
+    RU.threshold_mask(want_p, hist, req, want_m, ws)
+    fl = flags.cpu().numpy().astype(bool)
+    fresh = {"all": np.ones(rows, bool), "none": np.zeros(rows, bool), "per_row": fl,
+             "any": np.full(rows, fl.any()), "majority": np.full(rows, 2 * fl.sum() > rows)}[refresh]
+    for r in range(rows):
+        if fresh[r]:
+            assert torch.equal(part[r, :hist], want_p[r]), r
+            assert torch.equal(mask[r, :hist], want_m[r]), r
+        elif hist <= 40960:   # rows that keep are not touched
+            assert bool((part[r] == -7.0).all()) and bool((mask[r] == 9).all()), r
+    assert bool((mask[:, hist:] == 9).all())
