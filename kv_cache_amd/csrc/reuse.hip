@@ -182,6 +182,62 @@ __global__ __launch_bounds__(kRT) void reuse_mask_kernel(const float* __restrict
   }
 }
 
+// The sample_quantile candidate mask (EV:3972-3987) of rows with at most kRT
+// sampled columns, in one launch: every workgroup of a row gathers the row's
+// samples (one per thread, its own tile's values already in flight), counts
+// for each sample the samples above it and at or above it in LDS (the k-th
+// largest value, which torch.topk(...).values[-1] returns, is the one with
+// fewer than k above and at least k at or above), and compares its tile
+// with it.  The row's first workgroup writes the threshold.  Columns
+// lie in [0, n) (the caller's contract).
+__global__ __launch_bounds__(kRT) void sample_mask_kernel(const float* __restrict__ values, int64_t ld, int n,
+                                                          const int32_t* __restrict__ cols, int n_sample, int k,
+                                                          uint8_t* __restrict__ mask, int64_t mask_ld, bool vec,
+                                                          float* __restrict__ thr_out) {
+  __shared__ __attribute__((aligned(16))) uint32_t keys[kRT];
+  __shared__ float thr_s;
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const float* vrow = values + static_cast<int64_t>(row) * ld;
+  const int t0 = blockIdx.x * kMaskTile + tid * 16;
+  const bool full = vec && t0 + 16 <= n;
+  float4 x[4];
+  if (full) {
+    const float4* v4 = reinterpret_cast<const float4*>(vrow + t0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = v4[i];
+  }
+  const bool sampled = tid < n_sample;
+  const float sv = vrow[sampled ? cols[tid] : 0];
+  keys[tid] = sampled ? f32_sortable(sv) : 0u;   // below every finite key
+  __syncthreads();
+  if (sampled) {   // own is the k-th largest when fewer than k samples lie above it and k at or above
+    const uint32_t own = keys[tid];
+    int gt = 0, ge = 0;
+#pragma unroll 8
+    for (int j = 0; j < kRT; j += 4) {
+      const uint4 c = *reinterpret_cast<const uint4*>(keys + j);
+      gt += (c.x > own) + (c.y > own) + (c.z > own) + (c.w > own);
+      ge += (c.x >= own) + (c.y >= own) + (c.z >= own) + (c.w >= own);
+    }
+    if (gt < k && ge >= k) thr_s = sv;   // equal keys hold equal values (signed zeros compare equal)
+  }
+  __syncthreads();
+  const float thr = thr_s;
+  if (thr_out && blockIdx.x == 0 && tid == 0) thr_out[row] = thr;
+  if (t0 >= n) return;
+  uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
+  if (full) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(x[i].x >= thr) | static_cast<uint32_t>(x[i].y >= thr) << 8 |
+             static_cast<uint32_t>(x[i].z >= thr) << 16 | static_cast<uint32_t>(x[i].w >= thr) << 24;
+    *reinterpret_cast<uint4*>(mrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (int t = t0; t < min(n, t0 + 16); ++t) mrow[t] = vrow[t] >= thr;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Union scores: out[r, t] = scaling * sum_d q[d] * K[t, d] (d ascending)
 // where current | previous | previous_final is set at t, else -inf
@@ -1087,6 +1143,11 @@ QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, 
   if (need < 0 || workspace_bytes < need)
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
+  if (n_sample <= kRT) {   // gather, k-th of the sample and compare in one launch
+    sample_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sample_cols, static_cast<int>(n_sample),
+                                             static_cast<int>(k), mask, mask_ld, vec, thresholds);
+    return check_launch(what);
+  }
   float* sampled = static_cast<float*>(workspace);
   gather_cols_kernel<<<dim3(static_cast<unsigned>(cdiv(n_sample, kRT)), static_cast<unsigned>(rows)), kRT, 0, st>>>(
       values, ld, sample_cols, static_cast<int>(n_sample), sampled);

@@ -167,6 +167,36 @@ def test_threshold_mask_matches_oracle(rows, n, k, ld):
     assert set(np.unique(got[:, :n]).tolist()) <= {0, 1} and (got[:, n:] == 7).all()   # nothing past n
 
 
+@pytest.mark.parametrize("rows,n,n_s,frac,ld", [(3, 1000, 256, 0.05, 1000), (2, 32790, 256, 0.05, 32800),
+                                               (2, 5000, 255, 0.5, 5003), (2, 300, 64, 1.0, 300),
+                                               (4, 9000, 1, 0.05, 9000), (2, 20000, 257, 0.05, 20000),
+                                               (2, 50000, 4000, 0.05, 50000)])
+def test_sample_quantile_mask_matches_oracle(rows, n, n_s, frac, ld):
+    # the sample's k-th largest and the mask over the row: one launch up to
+    # 256 samples, the gather + selection + compare launches above; integer
+    # scores put many ties at the threshold, one row has signed zeros there
+    gen = torch.Generator().manual_seed(n + n_s)
+    vals = torch.randint(-20, 20, (rows, ld), generator=gen).float()
+    vals[0] = torch.randn(ld, generator=gen)
+    vals[-1, ::3] = -0.0
+    vals[-1, 1::3] = 0.0
+    cols = RU.sample_columns(n, n_s)
+    k = R.budget_count(cols.numel(), frac)
+    want_m, want_t, _ = R.candidate_mask(vals[:, :n].numpy(), R.budget_count(n, frac), frac, "sample_quantile",
+                                         sample_size=n_s)
+    lib = Q._lib.load()
+    ws = torch.empty(max(1, lib.qkv_candidate_mask_workspace_bytes(rows, n, 1, k, cols.numel())) // 4 + 1,
+                     dtype=torch.float32, device=DEV)
+    mask = torch.full((rows, ld + 3), 7, dtype=torch.uint8, device=DEV)
+    thr = torch.full((rows,), 5.0, device=DEV)
+    for c in (cols.to(DEV), cols):   # device columns as given, host columns checked and copied
+        RU.candidate_mask(vals.to(DEV), n, "sample_quantile", k, mask, thr, ws, c, cols.numel())
+        got = mask.cpu().numpy()
+        assert np.array_equal(got[:, :n].astype(bool), want_m)
+        assert set(np.unique(got[:, :n]).tolist()) <= {0, 1} and (got[:, n:] == 7).all()
+        assert np.array_equal(thr.cpu().numpy(), want_t.reshape(-1))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("d,hist,dims", [(128, 32790, 8), (128, 5, 8), (128, 4103, 16), (64, 1001, 8),
                                          (200, 333, 12)])
