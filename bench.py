@@ -664,7 +664,7 @@ def run_reuse(args) -> dict:
     log(f"[bench] setup {c['name']}: {layers} layers, {c['mode']}, top {c['top_fraction']}, sink/recent "
         f"{c['sink']}/{c['recent']}, capacity {cap}")
     # the lagged modes (lagtop2 / lagrefresh{N} / qdrift* / pconf{T}) run their own step
-    lagged = RU._LAGGED.fullmatch(c["mode"]) is not None
+    lagged = RU.is_lagged_mode(c["mode"])
     step_cls = RU.LaggedReuseDecodeStep if lagged else RU.ReuseDecodeStep
     g = torch.Generator(device="cuda").manual_seed(0)
     ks, vs, qs, steps = [], [], [], []
@@ -868,7 +868,9 @@ def run_reuse(args) -> dict:
     torch.cuda.synchronize()
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if lagged:   # the CPU leg restates the default reuse mode's op sequence only
+        log("[bench] cpu baseline: not measured for the lagged modes")
+    elif not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline_reuse(args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")

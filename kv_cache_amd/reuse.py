@@ -470,6 +470,11 @@ _LAGGED = re.compile(r"(lagtop2|lagrefresh(\d+)|qdrift(?:maj|head|share|cos|cosh
                      r"qabs(\d+)cand(\d+(?:p\d+)?)")
 
 
+def is_lagged_mode(mode: str) -> bool:
+    """Whether ``mode`` is one of the lagged reuse modes (EV:475)."""
+    return _LAGGED.fullmatch(mode) is not None
+
+
 def parse_lagged_mode(mode: str) -> tuple[str, float | int | None, int, float]:
     """``lagtop2 | lagrefresh{N} | qdrift[maj|head|share|cos|coshead] | pconf{T}``
     + ``qabs{S}cand{pct}`` -> (kind, parameter, S, candidate fraction): the
