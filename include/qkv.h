@@ -366,6 +366,31 @@ int qkv_reuse_select(const void* query, const void* key, const int64_t* k_stride
                      int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                      uint8_t* history_final, int64_t history_final_ld, void* stream);
 
+/* Workspace bytes of qkv_qabs_candidate_select (0 for histories of at most
+ * 40960 positions, which one workgroup per row selects; -1 for bad sizes). */
+int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history, double candidate_fraction);
+
+/* The candidate selection of the qabs{S}cand{pct}attn / appendattn modes
+ * (_qabs_candidate_attention_forward EV:4419-4464): the keep =
+ * min(history, max(1, ceil(candidate_fraction * history))) largest of
+ * scores [rows, history] (row stride scores_ld; the fp32 partial scores of
+ * qkv_reuse_partial_scores or partial_scores; lowest index wins ties), then
+ * the final list of _qabs_final_indices_from_selected (EV:2938-2982) or,
+ * with append, _qabs_final_indices_append_protected (EV:2985-3022, the
+ * selected copies of protected tokens stay valid): final_indices /
+ * final_valid / attn_ids (optional, -1 where invalid) [rows, n_out] = the
+ * selection in ascending index order, then the sink range, the recent range
+ * and the current token key_count - 1 (when keep_self); n_out =
+ * qkv_reuse_final_count(history, protect_sink, protect_recent,
+ * candidate_fraction, keep_self).  history_final [rows, history] (row stride
+ * history_final_ld) = the selection plus the protected ranges.  workspace:
+ * qkv_qabs_candidate_select_workspace_bytes bytes. */
+int qkv_qabs_candidate_select(const float* scores, int64_t rows, int64_t key_count, int64_t scores_ld,
+                              double candidate_fraction, int64_t protect_sink, int64_t protect_recent,
+                              int keep_self, int append, void* workspace, int64_t workspace_bytes,
+                              int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                              uint8_t* history_final, int64_t history_final_ld, void* stream);
+
 /* Workspace bytes of qkv_candidate_mask (0 for previous_threshold, -1 for
  * bad arguments). */
 int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k, int64_t n_sample);

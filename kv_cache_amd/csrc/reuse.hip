@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
     const float* __restrict__ scores, int64_t scores_ld, const int32_t* __restrict__ sel, int keep,
     int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids,
-    int n_out, uint8_t* __restrict__ hf, int64_t hf_ld) {
+    int n_out, uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0) {
   const int row = blockIdx.x, tid = threadIdx.x;
   uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
   for (int t = tid; t < history; t += kRT) hrow[t] = (t < sink_end) || (t >= recent_start);
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
     const float s = sc[idx];
     const bool valid = isfinite(s);
     if (valid) hrow[idx] = 1;
-    const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
+    const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
     final_idx[o + i] = idx;
     final_valid[o + i] = fv;
     if (attn_ids) attn_ids[o + i] = fv ? idx : -1;
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     const int32_t* __restrict__ ctok, const int32_t* __restrict__ ccnt, int n_tiles, int64_t c_ld, int keep,
     int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out,
-    uint8_t* __restrict__ hf, int64_t hf_ld) {
+    uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0) {
   using WS = WideSelect<VPL, false>;
   using WC = WideSelect<VPLC, false>;
   __shared__ union {
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   const int64_t o = static_cast<int64_t>(row) * n_out;
   auto emit = [&](int idx, int p, bool valid) {
     if (valid) hrow[idx] = 1;
-    const bool fv = valid && idx >= sink_end && !(idx >= recent_start && idx < history);
+    const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
     final_idx[o + p] = idx;
     final_valid[o + p] = fv;
     if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
@@ -973,6 +973,60 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
       static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
       static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
       history_final, history_final_ld);
+  return check_launch(what);
+}
+
+QKV_EXPORT int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history,
+                                                            double candidate_fraction) {
+  if (rows <= 0 || history <= 0 || history >= (int64_t(1) << 31) || !(candidate_fraction >= 0.0)) return -1;
+  if (history <= kWideMax) return 0;   // one workgroup per row: no workspace
+  return mask_ws_bytes(rows, history, reuse_counts(history, 0, 0, candidate_fraction, 0).keep);
+}
+
+QKV_EXPORT int qkv_qabs_candidate_select(const float* scores, int64_t rows, int64_t key_count, int64_t scores_ld,
+                                         double candidate_fraction, int64_t protect_sink, int64_t protect_recent,
+                                         int keep_self, int append, void* workspace, int64_t workspace_bytes,
+                                         int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                                         int64_t n_out, uint8_t* history_final, int64_t history_final_ld,
+                                         void* stream) {
+  const char* what = "qkv_qabs_candidate_select";
+  if (!scores || !final_indices || !final_valid || !history_final) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t history = key_count - 1;
+  if (rows <= 0 || rows > 65535 || history <= 0 || key_count >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535 and 2 <= key_count < 2^31", what);
+  if (scores_ld < history || history_final_ld < history)
+    return fail(QKV_ERR_INVALID, "%s: row strides must cover the history", what);
+  if (!(candidate_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: candidate_fraction must be >= 0", what);
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, candidate_fraction, keep_self);
+  if (n_out != c.n_out)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the selection needs %lld", what,
+                (long long)n_out, (long long)c.n_out);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (history <= kWideMax) {   // the whole row in one workgroup
+    return with_wide_vpl(history, [&](auto vpl) {
+      constexpr int VPL = decltype(vpl)::value;
+      reuse_final_wide_kernel<VPL, 2><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+          scores, scores_ld, nullptr, nullptr, nullptr, 0, 0, static_cast<int>(c.keep), static_cast<int>(history),
+          static_cast<int>(key_count), static_cast<int>(c.sink_end), static_cast<int>(c.recent_start),
+          static_cast<int>(c.rec_begin), static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid,
+          attn_ids, static_cast<int>(n_out), history_final, history_final_ld, append ? 1 : 0);
+      return check_launch(what);
+    });
+  }
+  const int64_t need = mask_ws_bytes(rows, history, c.keep);
+  if (!workspace || need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  int32_t* sel = static_cast<int32_t*>(workspace);
+  void* tk_ws = static_cast<char*>(workspace) + align256(rows * c.keep * 4);
+  int rc = qkv_topk_ws(scores, rows, history, scores_ld, c.keep, sel, tk_ws,
+                       workspace_bytes - align256(rows * c.keep * 4), stream);
+  if (rc) return rc;
+  reuse_finalize_kernel<<<static_cast<unsigned>(rows), kRT, 0, st>>>(
+      scores, scores_ld, sel, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
+      static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+      static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
+      history_final, history_final_ld, append ? 1 : 0);
   return check_launch(what);
 }
 

@@ -633,3 +633,158 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
         lag_union(current, previous_final, self.flags, self.batch, self.q_heads, history, refresh,
                   self.kind == "qdriftshare" and has_prev, self.sink, self.recent, self.union)
         self._select_attend(q, key, value, scaling, self.union, None, None)
+
+
+# -- candidate attention (qabs{S}cand{pct}attn / appendattn, EV:4400-4502) ----
+_QABS_ATTN = re.compile(r"qabs(\d+)cand(\d+(?:p\d+)?)(append)?attn")
+
+
+def parse_qabs_attn_mode(mode: str) -> tuple[int, float, bool]:
+    """``qabs{S}cand{pct}[append]attn`` -> (S, candidate fraction, append):
+    ``appendattn`` keeps the selected copies of protected tokens (EV:4451,
+    2985-3022); the fraction reads ``p`` as the decimal point (EV:748-754)."""
+    m = _QABS_ATTN.fullmatch(mode)
+    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}[append]attn mode")
+    return int(m.group(1)), float(m.group(2).replace("p", ".")) / 100.0, m.group(3) is not None
+
+
+def qabs_candidate_select(scores: torch.Tensor, key_count: int, candidate_fraction: float, protect_sink: int,
+                          protect_recent: int, keep_self: bool, append: bool = False, *,
+                          workspace: torch.Tensor | None = None, out: tuple | None = None):
+    """The qabs{S}cand{pct}attn candidate selection (``qkv_qabs_candidate_select``)
+    on fp32 scores [rows, >= history]: returns (final_indices int64 [rows, N],
+    final_valid bool [rows, N], attn_ids int32 [rows, N], history_final bool
+    [rows, history]), the selection in ascending order, then the sink range,
+    the recent range and the current token (EV:2938-3022)."""
+    lib = _lib.load()
+    _require(scores.is_cuda and scores.dtype == torch.float32 and scores.dim() == 2 and scores.stride(1) == 1,
+             "scores must be CUDA f32 [rows, >= history]")
+    rows, history = scores.size(0), int(key_count) - 1
+    _require(history >= 1 and scores.size(1) >= history, "need 2 <= key_count <= scores' width + 1")
+    n_out = int(lib.qkv_reuse_final_count(history, protect_sink, protect_recent, float(candidate_fraction),
+                                          int(keep_self)))
+    if out is None:
+        dev = scores.device
+        out = (torch.empty((rows, n_out), dtype=torch.int64, device=dev),
+               torch.empty((rows, n_out), dtype=torch.bool, device=dev),
+               torch.empty((rows, n_out), dtype=torch.int32, device=dev),
+               torch.empty((rows, history), dtype=torch.bool, device=dev))
+    fi, fv, ids, hf = out
+    need = int(lib.qkv_qabs_candidate_select_workspace_bytes(rows, history, float(candidate_fraction)))
+    _require(need >= 0, "bad candidate selection sizes")
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=scores.device)
+    with torch.cuda.device(scores.device):
+        _lib.check(lib.qkv_qabs_candidate_select(
+            scores.data_ptr(), rows, key_count, scores.stride(0), float(candidate_fraction), protect_sink,
+            protect_recent, int(keep_self), int(append), _lib.ptr(workspace) if need else None,
+            workspace.numel() * workspace.element_size() if need else 0, fi.data_ptr(), fv.data_ptr(),
+            _lib.ptr(ids), n_out, hf.data_ptr(), hf.stride(0), _lib.stream_of(scores)))
+    return fi, fv, ids, hf
+
+
+class QabsCandidateAttentionStep:
+    """One layer's ``qabs{S}cand{pct}attn`` / ``appendattn`` decode step
+    (``_qabs_candidate_attention_forward`` EV:4400-4502) with the reference's
+    exact arithmetic, for bf16 K/V caches of up to ``capacity`` tokens
+    ([B, Hkv, T, D], D = 128): per query head the fp32 partial score of every
+    history token on its top-|q| dims (from a per-KV-head dim-major K copy kept
+    current one token per step; products and sums in selection order as
+    QK:63-96), the ``min(history, max(1, ceil(pct * history)))`` best (ties to
+    the lower index), the protected tokens (EV:2938-3022), then attention
+    over that list.  Rows are (sequence, query head), each reading its KV head
+    directly.  A call whose history is not the previous call's plus one starts
+    a new sequence (the dim-major copy is rebuilt)."""
+
+    def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
+                 protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = True,
+                 device: torch.device | str = "cuda"):
+        lib = _lib.load()
+        self.mode = mode
+        self.dims, self.cand_fraction, self.append = parse_qabs_attn_mode(mode)
+        _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
+        self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
+        self.capacity = int(capacity)
+        self.sink, self.recent, self.keep_self = max(0, int(protect_sink)), max(0, int(protect_recent)), bool(keep_self)
+        self.device = device
+        rows = batch * q_heads
+        self.rows = rows
+        cap = self.capacity
+        hist_max = cap - 1
+        self.n_out_max = int(lib.qkv_reuse_final_count(hist_max, self.sink, self.recent, self.cand_fraction,
+                                                       int(self.keep_self)))
+        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
+        self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
+        self.final_idx = torch.empty(rows * self.n_out_max, dtype=torch.int64, device=device)
+        self.final_valid = torch.empty(rows * self.n_out_max, dtype=torch.bool, device=device)
+        self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
+        self.hf = torch.zeros((rows, cap), dtype=torch.bool, device=device)
+        need = int(lib.qkv_qabs_candidate_select_workspace_bytes(rows, hist_max, self.cand_fraction))
+        self.sel_ws = torch.empty(max(1, (need + 3) // 4), dtype=torch.float32, device=device)
+        need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
+        _require(need > 0, "unsupported attention shape (head_dim must be 128)")
+        self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.kdm_len = 0
+        self.last_history = None
+        self.n_out = 0
+
+    def reset(self) -> None:
+        """Forget the dim-major copy (a new sequence)."""
+        self.kdm_len = 0
+        self.last_history = None
+
+    def prefill(self, key: torch.Tensor) -> None:
+        """Build the dim-major copy of the cached history in one launch."""
+        t = key.size(2)
+        if t > self.kdm_len:
+            dim_major_append(key, self.kdm, self.kdm_len, t)
+            self.kdm_len = t
+
+    def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
+        """query bf16 [B, Hq, D]; key/value bf16 [B, Hkv, T, D] (the current
+        token last).  Returns bf16 [B, Hq, D]."""
+        key_count = key.size(2)
+        _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
+        if key_count <= 1:   # EV:4415-4417: only the current token
+            self.out.copy_(value[:, :, -1, :].repeat_interleave(self.q_heads // self.kv_heads, dim=1))
+            return self.out
+        history = key_count - 1
+        if self.last_history is not None and history != self.last_history + 1:
+            self.reset()
+        if self.kdm_len < history:
+            dim_major_append(key, self.kdm, self.kdm_len, history)
+            self.kdm_len = history
+        self.launch(query, key, value, scaling)
+        self.last_history = history
+        return self.out
+
+    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> None:
+        """The step's kernels at the history key.size(2) - 1 (the dim-major
+        copy must hold it); output in ``self.out``."""
+        lib = _lib.load()
+        key_count = key.size(2)
+        history = key_count - 1
+        _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
+        q = query.contiguous()
+        reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
+        n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.cand_fraction,
+                                              int(self.keep_self)))
+        rows = self.rows
+        out = (self.final_idx[: rows * n_out].view(rows, n_out), self.final_valid[: rows * n_out].view(rows, n_out),
+               self.attn_ids[: rows * n_out].view(rows, n_out), self.hf)
+        qabs_candidate_select(self.partial, key_count, self.cand_fraction, self.sink, self.recent, self.keep_self,
+                              self.append, workspace=self.sel_ws, out=out)
+        token_attention(q, key, value, out[2], scaling, workspace=self.attn_ws, out=self.out)
+        self.n_out = n_out
+
+    def final_indices(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The last step's final index list and validity, [B, Hq, N]."""
+        n = self.n_out
+        shape = (self.batch, self.q_heads, n)
+        return self.final_idx[: self.rows * n].view(shape), self.final_valid[: self.rows * n].view(shape)
+
+    def final_mask(self) -> torch.Tensor:
+        """The last step's selection plus the protected ranges, bool [B, Hq, history]."""
+        h = self.last_history
+        return self.hf[:, :h].reshape(self.batch, self.q_heads, h)

@@ -217,13 +217,16 @@ def qabs_candidate_attention_cpu(query_states, key_states, value_states, dim_cou
 
 
 def qabs_attn_step(query, key, value, dim_count: int, candidate_fraction: float, scaling: float,
-                   sink: int = 0, recent: int = 0, keep_self: bool = True):
+                   sink: int = 0, recent: int = 0, keep_self: bool = True, append: bool = False):
     """One ``qabs{S}cand{pct}attn`` decode step (EV:4400-4502) in numpy with
     the kernels' arithmetic: per query head, the fp32 partial score of every
     history token on its top-|q| dims (selection order, QK:63-96), the
     ``min(history, max(1, ceil(pct * history)))`` best (ties to the lower
     index), plus the sink / recent ranges and the current token
     (EV:2938-2982), then softmax attention over that set (QK:335-419).
+    With ``append`` (the ``appendattn`` modes, EV:4451-4458, 2985-3022) the
+    selected copies of protected tokens stay in the list, so those tokens
+    are attended twice.
 
     query [B,Hq,D]; key/value [B,Hkv,T,D] (head h reads KV head h // G).
     Returns (out float64 [B,1,Hq,D], final_keep bool [B,Hq,T])."""
@@ -250,6 +253,13 @@ def qabs_attn_step(query, key, value, dim_count: int, candidate_fraction: float,
         final_keep[..., max(0, history - recent):history] = True
     if keep_self:
         final_keep[..., history] = True
+    if append:   # the selection as it is, then the protected tokens (EV:2992-3022)
+        sink_end = min(sink, history) if sink > 0 else 0
+        rec_begin = max(max(0, history - recent), sink_end) if recent > 0 else history
+        tail = list(range(sink_end)) + list(range(rec_begin, history)) + ([history] if keep_self else [])
+        idx = np.concatenate([sel.astype(np.int64), np.broadcast_to(np.array(tail, dtype=np.int64),
+                                                                       (b, hq, len(tail)))], axis=-1)
+        return final_attention(q, kx, vx, idx, np.ones(idx.shape, dtype=bool), scaling), final_keep
     idx = np.broadcast_to(np.arange(key_count), final_keep.shape)
     return final_attention(q, kx, vx, idx, final_keep, scaling), final_keep
 

@@ -176,6 +176,11 @@ BLOCK_SCENARIOS = {
     "qabs8cand3attn_fp32": ("qabs8cand3attn", torch.float32, 4, 2, 300, 3, 0.02, 3, 5, True, 18),
     "qabs16cand10attn_fp32": ("qabs16cand10attn", torch.float32, 4, 4, 211, 3, 0.02, 0, 0, False, 19),
     "qabs8cand5attn_bf16": ("qabs8cand5attn", torch.bfloat16, 4, 2, 257, 3, 0.02, 4, 4, True, 20),
+    # the appendattn variant keeps the selected copies of protected tokens
+    # (EV:4451-4458, 2985-3022): wide protected ranges so that copies occur
+    "qabs8cand5appendattn_fp32": ("qabs8cand5appendattn", torch.float32, 4, 2, 260, 3, 0.02, 12, 20, True, 24),
+    "qabs16cand10appendattn_bf16": ("qabs16cand10appendattn", torch.bfloat16, 4, 2, 230, 3, 0.02, 8, 16, False,
+                                    125),
 }
 
 

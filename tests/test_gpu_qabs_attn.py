@@ -1,0 +1,121 @@
+"""GPU parity of the exact qabs{S}cand{pct}attn / appendattn decode step
+(kv_cache_amd.reuse.QabsCandidateAttentionStep, qkv_qabs_candidate_select)
+against the reference's own golden vectors and the oracle: selections and
+final index lists bit-exact, attention within 1e-2 relative / 2e-2 absolute
+(bf16) or 1e-4 (fp32)."""
+
+import numpy as np
+import pytest
+import torch
+
+from kv_cache_amd import qabs_cuda_kernels as Q
+from kv_cache_amd import reuse as RU
+from oracle import ref_semantics as R
+from oracle.qkv_oracle import topk_lowest_index
+from tests.test_oracle_block import APPEND_SCENARIOS, ATTN_SCENARIOS, load_block_golden
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", [n for n in ATTN_SCENARIOS + APPEND_SCENARIOS if n.endswith("bf16")])
+def test_candidate_attention_step_matches_reference_vectors(name):
+    # the GQA-native step (dim-major K copy, no head expansion) on the
+    # reference's bf16 scenarios: every step's final set and output
+    g = load_block_golden(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
+    v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
+    step = RU.QabsCandidateAttentionStep(g["mode"], 1, hq, hkv, 128, 1024, protect_sink=g["sink"],
+                                         protect_recent=g["recent"], keep_self=g["keep_self"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
+        out = step(q, k[:, :, :n], v[:, :, :n], g["scaling"])
+        assert np.array_equal(step.final_mask().cpu().numpy(), g["final"][s][..., : n - 1]), s
+        assert bool((g["final"][s][..., n - 1] == g["keep_self"]).all()), s
+        np.testing.assert_allclose(f32(out), g["out"][s], rtol=1e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("name", [n for n in ATTN_SCENARIOS + APPEND_SCENARIOS if n.endswith("fp32")])
+def test_candidate_attention_pieces_match_reference_vectors(name):
+    # the fp32 scenarios through the reference-signature kernels and the
+    # C-ABI selection, on GQA-expanded K as the reference's hook passes it
+    g = load_block_golden(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k_all = torch.from_numpy(np.repeat(g["k"], hq // hkv, axis=1)).to(DEV)
+    v_all = torch.from_numpy(np.repeat(g["v"], hq // hkv, axis=1)).to(DEV)
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(DEV)
+        k, v = k_all[:, :, :n], v_all[:, :, :n]
+        part = Q.partial_scores(q, k[:, :, : n - 1], g["dims"]).view(hq, n - 1)
+        fi, fv, ids, hf = RU.qabs_candidate_select(part, n, g["cand"], g["sink"], g["recent"], g["keep_self"],
+                                                   g["append"])
+        assert np.array_equal(hf.cpu().numpy(), g["final"][s][0, :, : n - 1]), s
+        out = Q.final_attention(q, k, v, fi.view(1, hq, -1), fv.view(1, hq, -1), g["scaling"])
+        np.testing.assert_allclose(f32(out)[:, 0], g["out"][s], rtol=1e-4, atol=1e-4)
+        assert torch.equal(ids, torch.where(fv, fi, torch.full_like(fi, -1)).to(torch.int32))
+
+
+@pytest.mark.parametrize("append", [False, True])
+@pytest.mark.parametrize("rows,hist,frac,sink,recent,keep_self", [
+    (4, 5000, 0.03, 4, 16, True),
+    (2, 40960, 0.05, 0, 0, False),      # the longest row one workgroup selects
+    (2, 50000, 0.02, 10, 10, True),     # the staged top-k
+    (3, 300, 0.5, 100, 100, True),      # the protected ranges cover most of the selection
+    (2, 1, 0.03, 1, 1, True),           # history 1
+])
+def test_candidate_select_matches_oracle(append, rows, hist, frac, sink, recent, keep_self):
+    gen = torch.Generator().manual_seed(hist + rows)
+    scores = torch.randint(-40, 40, (rows, hist + 7), generator=gen).float()   # ties at the boundary
+    scores[0, :hist] = torch.randn(hist, generator=gen)
+    fi, fv, ids, hf = RU.qabs_candidate_select(scores.to(DEV), hist + 1, frac, sink, recent, keep_self, append)
+    keep = R.budget_count(hist, frac)
+    sel = np.sort(topk_lowest_index(scores[:, :hist].numpy(), keep), axis=-1)
+    sink_end = min(sink, hist)
+    rec_begin = max(hist - recent, sink_end) if recent else hist
+    tail = list(range(sink_end)) + list(range(rec_begin, hist)) + ([hist] if keep_self else [])
+    want_i = np.concatenate([sel, np.tile(np.array(tail, dtype=np.int64), (rows, 1))], axis=-1)
+    prot = (sel < sink_end) | ((sel >= hist - recent) if recent else np.zeros_like(sel, bool))
+    want_v = np.concatenate([np.ones_like(sel, bool) if append else ~prot, np.ones((rows, len(tail)), bool)], -1)
+    assert np.array_equal(fi.cpu().numpy(), want_i)
+    assert np.array_equal(fv.cpu().numpy(), want_v)
+    want_hf = np.zeros((rows, hist), bool)
+    np.put_along_axis(want_hf, sel, True, axis=-1)
+    want_hf[:, :sink_end] = True
+    if recent:
+        want_hf[:, max(0, hist - recent):] = True
+    assert np.array_equal(hf.cpu().numpy(), want_hf)
+
+
+def test_candidate_attention_step_resets_and_matches_oracle_at_length():
+    # a longer history than the vectors (4 rows of 9000), GQA 4, and a new
+    # sequence of the same length after reset: outputs from the oracle step
+    gen = torch.Generator().manual_seed(3)
+    t = 9000
+    k = torch.randn((1, 2, t + 1, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((1, 2, t + 1, 128), generator=gen).to(torch.bfloat16)
+    q = torch.randn((1, 8, 128), generator=gen).to(torch.bfloat16)
+    step = RU.QabsCandidateAttentionStep("qabs8cand3attn", 1, 8, 2, 128, t + 64, protect_sink=4, protect_recent=8)
+    out = step(q.to(DEV), k.to(DEV), v.to(DEV), 128 ** -0.5)
+    want, keep = R.qabs_attn_step(f32(q), f32(k), f32(v), 8, 0.03, 128 ** -0.5, 4, 8, True)
+    np.testing.assert_allclose(f32(out), want[:, 0], rtol=1e-2, atol=2e-2)
+    assert np.array_equal(step.final_mask().cpu().numpy(), keep[..., :t])
+    k2 = torch.randn((1, 2, t + 1, 128), generator=gen).to(torch.bfloat16)
+    step.reset()
+    out2 = step(q.to(DEV), k2.to(DEV), v.to(DEV), 128 ** -0.5)
+    want2, _ = R.qabs_attn_step(f32(q), f32(k2), f32(v), 8, 0.03, 128 ** -0.5, 4, 8, True)
+    np.testing.assert_allclose(f32(out2), want2[:, 0], rtol=1e-2, atol=2e-2)
+
+
+def test_candidate_select_rejects_bad_arguments():
+    s = torch.zeros((2, 10), device=DEV)
+    with pytest.raises(RuntimeError, match="need 2 <= key_count"):
+        RU.qabs_candidate_select(s, 1, 0.1, 0, 0, True)
+    with pytest.raises(RuntimeError, match="not a qabs"):
+        RU.QabsCandidateAttentionStep("qabs8cand3reuse", 1, 4, 2, 128, 256)

@@ -16,6 +16,7 @@ BLOCK_SCENARIOS = ["qbb16q8s12cand4_fp32", "qbb8q16s25cand6p25_fp32", "brep16r2q
                    "brep8r1q16s25cand6p25_fp32", "qboracle16q8s12cand4_fp32", "qboracle8q16s25cand6p25_fp32",
                    "qboracle16q8s12cand4_bf16"]
 ATTN_SCENARIOS = ["qabs8cand3attn_fp32", "qabs16cand10attn_fp32", "qabs8cand5attn_bf16"]
+APPEND_SCENARIOS = ["qabs8cand5appendattn_fp32", "qabs16cand10appendattn_bf16"]
 
 
 def parse_block_mode(mode):
@@ -28,7 +29,7 @@ def parse_block_mode(mode):
     m = re.fullmatch(r"qboracle(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
     if m:
         return "qboracle", int(m.group(1)), 1, int(m.group(2)), pct(m.group(3)), pct(m.group(4))
-    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)attn", mode)
+    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)(?:append)?attn", mode)
     if m:
         return "qabs", 1, 1, int(m.group(1)), 1.0, pct(m.group(2))
     m = re.fullmatch(r"brep(\d+)r(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
@@ -46,6 +47,7 @@ def load_block_golden(name):
         "steps": int(z["steps"]), "top_fraction": float(z["top_fraction"]), "sink": int(z["sink"]),
         "recent": int(z["recent"]), "keep_self": bool(z["keep_self"]), "scaling": float(z["scaling"]),
         "out": z["out"][:, :, 0], "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
+        "append": str(z["mode"]).endswith("appendattn"),
     }
 
 
@@ -62,7 +64,7 @@ def test_block_steps_match_reference_vectors(name):
         np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
 
 
-@pytest.mark.parametrize("name", ATTN_SCENARIOS)
+@pytest.mark.parametrize("name", ATTN_SCENARIOS + APPEND_SCENARIOS)
 def test_qabs_attn_steps_match_reference_vectors(name):
     # the timed qabs{S}cand{pct}attn mode: every step's final index set
     # bit-exact, outputs to 1e-5 (fp32) / the bf16 attention tolerance
@@ -71,9 +73,13 @@ def test_qabs_attn_steps_match_reference_vectors(name):
     for s in range(g["steps"]):
         n = g["t0"] + s + 1
         out, keep = R.qabs_attn_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"],
-                                     g["scaling"], g["sink"], g["recent"], g["keep_self"])
+                                     g["scaling"], g["sink"], g["recent"], g["keep_self"], g["append"])
         assert np.array_equal(keep, g["final"][s][..., :n]), (name, s)
         np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
+        if g["append"]:   # the vectors hold selected copies of protected tokens, which count twice
+            plain, _ = R.qabs_attn_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"],
+                                        g["scaling"], g["sink"], g["recent"], g["keep_self"])
+            assert np.abs(plain - out).max() > 1e-3, (name, s)
 
 
 @pytest.mark.parametrize("name", ATTN_SCENARIOS)
