@@ -61,7 +61,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg3", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse", "qbb", "brep"],
+    p.add_argument("--config", default="cfg3",
+                   choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "reuse", "qbb", "brep", "qabsattn"],
                    help="workload (default cfg3: the largest single-GPU config, all 36 layers resident)")
     p.add_argument("--secondary", default=None,
                    help="a second decode config measured in the same run, reported under 'secondary' "
@@ -73,6 +74,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--reuse-mode", default=None,
                    help="--config reuse: a qabs{S}cand{pct}reuse[final|2set][blk{bs}] mode (default qabs8cand5reuse)")
+    p.add_argument("--qabs-mode", default="qabs8cand3attn",
+                   help="--config qabsattn: a qabs{S}cand{pct}[append]attn mode")
     p.add_argument("--candidate-selection", default="topk", choices=["topk", "sample_quantile", "previous_threshold"],
                    help="--config reuse: the reference's --qabs_candidate_selection")
     p.add_argument("--eager", action="store_true", help="time eager launches instead of a HIP graph")
@@ -220,6 +223,8 @@ def main() -> int:
         line = run_reuse(args)
     elif args.config in ("qbb", "brep"):
         line = run_blocksel(args)
+    elif args.config == "qabsattn":
+        line = run_qabs_attn(args)
     else:
         line = run_decode(args, args.config, args.layers)
         if args.secondary and args.secondary != args.config:
@@ -901,6 +906,191 @@ def run_reuse(args) -> dict:
         "roofline": {
             "bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": kernels[dom]["gbs"] / HBM_PEAK_GBS, "traffic": read_traffic("reuse", dom),
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_baseline_qabs_attn(mode: str, budget_s: float) -> dict:
+    """The reference's qabs{S}cand{pct}attn op sequence (oracle/ref_semantics.py
+    qabs_candidate_attention_cpu, pinned to the reference's vectors) for one
+    layer of the REUSE shape, repeated for about ``budget_s`` seconds."""
+    import torch
+
+    from kv_cache_amd.reuse import parse_qabs_attn_mode
+    from oracle import ref_semantics as R
+
+    c = REUSE
+    dims, frac, _ = parse_qabs_attn_mode(mode)
+    torch.set_num_threads(host_threads())
+    g = torch.Generator().manual_seed(0)
+    t = c["history"] + 1
+    k = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, c["kv_heads"], t, c["head_dim"]), generator=g).to(torch.bfloat16)
+    q = torch.randn((1, c["q_heads"], 1, c["head_dim"]), generator=g).to(torch.bfloat16)
+    run = lambda: R.qabs_candidate_attention_cpu(q, k, v, dims, frac, c["head_dim"] ** -0.5,  # noqa: E731
+                                                 c["sink"], c["recent"], True)
+    run()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 100):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    keys = c["kv_heads"] * c["history"]
+    return {
+        "value": keys / med,
+        "unit": "keys/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one layer ({mode}, {c['q_heads']}/{c['kv_heads']} heads, history {c['history']}): the "
+                   f"reference's candidate-attention op sequence on CPU tensors; median of {len(times)} calls = "
+                   f"{med * 1e3:.1f} ms; {host_note(torch.get_num_threads())}"),
+    }
+
+
+def run_qabs_attn(args) -> dict:
+    """Decode steps of the exact qabs{S}cand{pct}[append]attn mode
+    (kv_cache_amd.reuse.QabsCandidateAttentionStep) on the REUSE shape: eager
+    steps with a growing history, one fixed-history step as a HIP graph, and
+    each kernel alone."""
+    import torch
+
+    from kv_cache_amd import reuse as RU
+
+    c = REUSE
+    mode = args.qabs_mode
+    dims, frac, append = RU.parse_qabs_attn_mode(mode)
+    layers = args.layers or 8
+    b, hq, hkv, d, t0 = c["batch"], c["q_heads"], c["kv_heads"], c["head_dim"], c["history"]
+    cap = -(-(t0 + args.warmup + args.steps + 2) // 64) * 64
+    scaling = d ** -0.5
+    log(f"[bench] setup qabsattn {mode}: {layers} layers, {hq}/{hkv} heads, history {t0}, sink/recent "
+        f"{c['sink']}/{c['recent']}, capacity {cap}")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    ks, vs, qs, steps = [], [], [], []
+    for _ in range(layers):
+        k = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        v = torch.randn((b, hkv, cap, d), generator=g, device="cuda").to(torch.bfloat16)
+        q = torch.randn((b, hq, d), generator=g, device="cuda").to(torch.bfloat16)
+        st = RU.QabsCandidateAttentionStep(mode, b, hq, hkv, d, cap, protect_sink=c["sink"],
+                                           protect_recent=c["recent"])
+        st.prefill(k[:, :, :t0])
+        ks.append(k)
+        vs.append(v)
+        qs.append(q)
+        steps.append(st)
+    torch.cuda.synchronize()
+    hist = t0
+
+    def decode_step():
+        nonlocal hist
+        for layer in range(layers):
+            steps[layer](qs[layer], ks[layer][:, :, : hist + 1], vs[layer][:, :, : hist + 1], scaling)
+        hist += 1
+
+    for _ in range(args.warmup):
+        decode_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0 = hist
+    e0.record()
+    for _ in range(args.steps):
+        decode_step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    log(f"[bench] eager step: {ms_per_step:.3f} ms ({ms_per_step * 1e3 / layers:.1f} us/layer), "
+        f"history {h0}..{hist - 1}")
+    hf = hist - 1
+    rows = b * hq
+    lib = RU._lib.load()
+    n_out = int(lib.qkv_reuse_final_count(hf, c["sink"], c["recent"], frac, 1))
+    reps = max(1, -(-16 // layers))
+
+    def repeated(fn):
+        def run():
+            for _ in range(reps):
+                fn()
+        return run
+
+    def run_fixed():
+        for layer in range(layers):
+            steps[layer].launch(qs[layer], ks[layer][:, :, : hf + 1], vs[layer][:, :, : hf + 1], scaling)
+
+    gr = graph_of(repeated(run_fixed))
+    ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
+    del gr
+    log(f"[bench] graph step (history {hf}): {ms_graph * 1e3 / layers:.1f} us/layer")
+
+    def run_partial():
+        for layer in range(layers):
+            RU.reuse_partial_scores(qs[layer], steps[layer].kdm, hf, dims, out=steps[layer].partial)
+
+    def run_select():
+        for layer in range(layers):
+            st = steps[layer]
+            out = (st.final_idx[: rows * n_out].view(rows, n_out), st.final_valid[: rows * n_out].view(rows, n_out),
+                   st.attn_ids[: rows * n_out].view(rows, n_out), st.hf)
+            RU.qabs_candidate_select(st.partial, hf + 1, frac, c["sink"], c["recent"], True, append,
+                                     workspace=st.sel_ws, out=out)
+
+    def run_attn():
+        for layer in range(layers):
+            st = steps[layer]
+            RU.token_attention(qs[layer], ks[layer][:, :, : hf + 1], vs[layer][:, :, : hf + 1],
+                               st.attn_ids[: rows * n_out].view(rows, n_out), scaling, workspace=st.attn_ws,
+                               out=st.out)
+
+    plan = [
+        ("reuse_partial_scores", run_partial, rows * hf * (dims * 2 + 4)),
+        # the scores read, the history mask and the index lists written
+        ("qabs_candidate_select", run_select, rows * hf * (4 + 1) + rows * n_out * (8 + 1 + 4)),
+        ("token_attention", run_attn, rows * n_out * d * 2 * 2),
+    ]
+    kernels = {}
+    for name, fn, nbytes in plan:
+        gk = graph_of(repeated(fn))
+        ms = time_replays(gk.replay, args.kernel_reps) / (layers * reps)
+        kernels[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                         "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
+        del gk
+    for _ in range(args.profile_steps):
+        run_fixed()
+    torch.cuda.synchronize()
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline_qabs_attn(mode, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
+    dom = max(kernels, key=lambda n: kernels[n]["us_per_launch"])
+    keys_per_layer = b * hkv * hf
+    return {
+        "metric": "candidate attention decode: keys/s (history tokens x KV heads) through the exact "
+                  "qabs{S}cand{pct}attn step; us/layer",
+        "value": layers * keys_per_layer / (ms_per_step * 1e-3),
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 -> f32 scores and attention",
+        "data": "synthetic (seeded N(0,1) K/V/q)",
+        "config": {"workload": f"qabsattn: {c['name']}", "batch": b, "q_heads": hq, "kv_heads": hkv, "head_dim": d,
+                   "history": t0, "layers": layers, "mode": mode, "sink": c["sink"], "recent": c["recent"],
+                   "graph": False},
+        "us_per_layer": ms_per_step * 1e3 / layers,
+        "graph_us_per_layer": ms_graph * 1e3 / layers,
+        "final_entries_per_row": n_out,
+        "roofline": {
+            "bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": kernels[dom]["gbs"] / HBM_PEAK_GBS, "traffic": read_traffic("qabsattn", dom),
         },
         "kernels": kernels,
         "cpu_baseline": cpu,
