@@ -601,8 +601,8 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     wc.place(sh.c, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
   } else {
     WS ws;
-    ws.load(scores + static_cast<int64_t>(row) * scores_ld, history);
-    ws.run(keep, sh.d);
+    ws.load_count(scores + static_cast<int64_t>(row) * scores_ld, history, sh.d);   // first digit counted on load
+    ws.run_counted(keep, sh.d);
     uint64_t fin = 0;   // bit i: key i is a finite score
 #pragma unroll
     for (int i = 0; i < VPL; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(ws.u[i]))) << i;
