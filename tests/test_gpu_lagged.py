@@ -287,3 +287,39 @@ def test_lag_candidates_skip_rows_that_keep(refresh, hist):
         elif hist <= 40960:   # rows that keep are not touched
             assert bool((part[r] == -7.0).all()) and bool((mask[r] == 9).all()), r
     assert bool((mask[:, hist:] == 9).all())
+
+
+@pytest.mark.parametrize("mode", ["lagtop2qabs8cand5", "lagrefresh2qabs8cand5", "qdriftqabs8cand5",
+                                  "qdriftmajqabs8cand5", "qdriftheadqabs8cand5", "qdriftshareqabs8cand5",
+                                  "qdriftcosqabs16cand10", "qdriftcosheadqabs8cand5", "pconf60qabs8cand5"])
+def test_lagged_step_matches_oracle_multistep(mode):
+    # every lagged kind over 5 steps at 3000 history tokens, GQA 4, queries
+    # drifting slowly on some heads and jumping on others (refreshes of no,
+    # some and every head); masks bit-exact to the oracle at every step
+    gen = torch.Generator().manual_seed(len(mode) * 7 + 1)
+    t, steps, hq, hkv = 3000, 5, 8, 2
+    kind, param, dims, cand = RU.parse_lagged_mode(mode)
+    eps = torch.tensor([0.02, 3.0, 0.05, 0.3, 0.01, 2.0, 0.1, 1.0]).view(1, 1, hq, 1)
+    base = torch.randn((1, 1, hq, 128), generator=gen)
+    q = ((base + eps * torch.randn((steps, 1, hq, 128), generator=gen)) / torch.sqrt(1 + eps * eps)).to(torch.bfloat16)
+    k = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = RU.LaggedReuseDecodeStep(mode, 1, hq, hkv, 128, t + 64, top_fraction=0.02, protect_sink=4,
+                                    protect_recent=8)
+    prev = None
+    for s in range(steps):
+        n = t + s + 1
+        if kind == "pconf" and prev is not None:   # the seed keeps every row's ESS clear of the threshold
+            kx = np.repeat(f32(k[:, :, :n]), hq // hkv, axis=1)
+            ess = R.previous_final_ess_fraction(f32(q[s]), kx, prev["final"], 128 ** -0.5, True)
+            assert np.abs(ess - param).min() > 1e-3, s
+        out = step(q[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        want, wc, wf, prev, flagged = R.lagged_reuse_decode_step(f32(q[s]), f32(k[:, :, :n]), f32(v[:, :, :n]),
+                                                                 kind, param, dims, cand, 0.02, 4, 8, True,
+                                                                 128 ** -0.5, prev, True)
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
+        if flagged is not None and kind in ("qdrifthead", "qdriftcoshead", "qdriftshare", "pconf"):
+            assert np.array_equal(step.flags.cpu().numpy().astype(bool), flagged.reshape(-1)), s
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
