@@ -922,7 +922,7 @@ def cpu_baseline_qabs_attn(mode: str, budget_s: float) -> dict:
     from oracle import ref_semantics as R
 
     c = REUSE
-    dims, frac, _ = parse_qabs_attn_mode(mode)
+    dims, frac, _, _ = parse_qabs_attn_mode(mode)
     torch.set_num_threads(host_threads())
     g = torch.Generator().manual_seed(0)
     t = c["history"] + 1
@@ -962,7 +962,7 @@ def run_qabs_attn(args) -> dict:
 
     c = REUSE
     mode = args.qabs_mode
-    dims, frac, append = RU.parse_qabs_attn_mode(mode)
+    dims, frac, append, interval = RU.parse_qabs_attn_mode(mode)
     layers = args.layers or 8
     b, hq, hkv, d, t0 = c["batch"], c["q_heads"], c["kv_heads"], c["head_dim"], c["history"]
     cap = -(-(t0 + args.warmup + args.steps + 2) // 64) * 64
@@ -1006,6 +1006,11 @@ def run_qabs_attn(args) -> dict:
         f"history {h0}..{hist - 1}")
     hf = hist - 1
     rows = b * hq
+    for layer in range(layers):   # (r{N}attn steps between refreshes leave the copy behind)
+        st = steps[layer]
+        if st.kdm_len < hf:
+            RU.dim_major_append(ks[layer][:, :, : hf + 1], st.kdm, st.kdm_len, hf)
+            st.kdm_len = hf
     lib = RU._lib.load()
     n_out = int(lib.qkv_reuse_final_count(hf, c["sink"], c["recent"], frac, 1))
     reps = max(1, -(-16 // layers))
@@ -1024,6 +1029,17 @@ def run_qabs_attn(args) -> dict:
     ms_graph = time_replays(gr.replay, args.kernel_reps) / reps
     del gr
     log(f"[bench] graph step (history {hf}): {ms_graph * 1e3 / layers:.1f} us/layer")
+    ms_graph_reuse = None
+    if interval is not None:   # r{N}attn: a step between refreshes rebuilds the list from the kept selection
+        def run_fixed_reuse():
+            for layer in range(layers):
+                steps[layer].launch(qs[layer], ks[layer][:, :, : hf + 1], vs[layer][:, :, : hf + 1], scaling,
+                                    reuse_selection=True)
+
+        gr = graph_of(repeated(run_fixed_reuse))
+        ms_graph_reuse = time_replays(gr.replay, args.kernel_reps) / reps
+        del gr
+        log(f"[bench] graph step between refreshes: {ms_graph_reuse * 1e3 / layers:.1f} us/layer")
 
     def run_partial():
         for layer in range(layers):
@@ -1062,7 +1078,9 @@ def run_qabs_attn(args) -> dict:
         run_fixed()
     torch.cuda.synchronize()
     cpu = None
-    if not args.no_cpu_baseline:
+    if interval is not None or append:   # the CPU leg restates the plain attn op sequence only
+        log("[bench] cpu baseline: not measured for the r{N}attn / appendattn variants")
+    elif not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline_qabs_attn(mode, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
@@ -1087,6 +1105,7 @@ def run_qabs_attn(args) -> dict:
                    "graph": False},
         "us_per_layer": ms_per_step * 1e3 / layers,
         "graph_us_per_layer": ms_graph * 1e3 / layers,
+        **({"graph_us_per_layer_between_refreshes": ms_graph_reuse * 1e3 / layers} if interval else {}),
         "final_entries_per_row": n_out,
         "roofline": {
             "bound": "hbm", "kernel": dom, "achieved": kernels[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -391,6 +391,20 @@ int qkv_qabs_candidate_select(const float* scores, int64_t rows, int64_t key_cou
                               int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                               uint8_t* history_final, int64_t history_final_ld, void* stream);
 
+/* The final index list of a given selection (_qabs_final_indices_from_selected
+ * EV:2938-2982), as the periodic qabs{S}cand{pct}r{N}attn mode rebuilds it
+ * from the indices the last refreshing step kept (EV:4535-4548, 4592-4600):
+ * final_indices / final_valid / attn_ids (optional, -1 where invalid) [rows,
+ * n_out] = selected[r, :n_sel] (row stride selected_ld), valid where the
+ * index lies in [0, history) outside the first protect_sink and last
+ * protect_recent history positions, then the sink range, the recent range
+ * (not overlapping the sink) and the current token key_count - 1 (when
+ * keep_self); n_out = n_sel + that many protected entries. */
+int qkv_final_indices_from_selected(const int64_t* selected, int64_t selected_ld, int64_t n_sel, int64_t rows,
+                                    int64_t key_count, int64_t protect_sink, int64_t protect_recent, int keep_self,
+                                    int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                                    void* stream);
+
 /* Workspace bytes of qkv_candidate_mask (0 for previous_threshold, -1 for
  * bad arguments). */
 int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k, int64_t n_sample);

@@ -77,6 +77,8 @@ _PROTOTYPES = {
                                    _i64, _vp, _i64, _f32, _f32, _vp, _vp, _i64, _vp]),
     "qkv_reuse_lag_flags_workspace_bytes": (_i64, [_i64, _i64]),
     "qkv_qabs_candidate_select_workspace_bytes": (_i64, [_i64, _i64, _f64]),
+    "qkv_final_indices_from_selected": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i64,
+                                               _vp]),
     "qkv_qabs_candidate_select": (_i32, [_vp, _i64, _i64, _i64, _f64, _i64, _i64, _i32, _i32, _vp, _i64, _vp, _vp,
                                          _vp, _i64, _vp, _i64, _vp]),
     "qkv_reuse_lag_candidates": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,

@@ -421,6 +421,32 @@ __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
   }
 }
 
+// The final list of a given selection (EV:2938-2982, as the periodic
+// candidate mode rebuilds it from the indices a previous step kept,
+// EV:4535-4548 and 4592-4600): entry i < n_sel is selected index i, valid
+// where it lies in [0, history) outside the sink and recent ranges; then the
+// sink range, the recent range and the current token.  One thread per entry.
+__global__ __launch_bounds__(kRT) void final_from_selected_kernel(
+    const int64_t* __restrict__ sel, int64_t sel_ld, int n_sel, int history, int key_count, int sink_end,
+    int recent_start, int rec_begin, int n_rec, int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid,
+    int32_t* __restrict__ attn_ids, int n_out) {
+  const int row = blockIdx.y, i = blockIdx.x * kRT + threadIdx.x;
+  if (i >= n_out) return;
+  int64_t idx;
+  bool fv = true;
+  if (i < n_sel) {
+    idx = sel[static_cast<int64_t>(row) * sel_ld + i];
+    fv = idx >= sink_end && idx < history && !(idx >= recent_start);
+  } else {
+    const int e = i - n_sel;
+    idx = e < sink_end ? e : (e < sink_end + n_rec ? rec_begin + (e - sink_end) : key_count - 1);
+  }
+  const int64_t o = static_cast<int64_t>(row) * n_out + i;
+  final_idx[o] = idx;
+  final_valid[o] = fv ? 1 : 0;
+  if (attn_ids) attn_ids[o] = fv ? static_cast<int32_t>(idx) : -1;
+}
+
 // ---------------------------------------------------------------------------
 // Rows of at most kWideMax values: one 1024-thread workgroup per row holds
 // the row in registers (WideSelect) and does the whole selection in one
@@ -1027,6 +1053,31 @@ QKV_EXPORT int qkv_qabs_candidate_select(const float* scores, int64_t rows, int6
       static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
       static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
       history_final, history_final_ld, append ? 1 : 0);
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_final_indices_from_selected(const int64_t* selected, int64_t selected_ld, int64_t n_sel,
+                                              int64_t rows, int64_t key_count, int64_t protect_sink,
+                                              int64_t protect_recent, int keep_self, int64_t* final_indices,
+                                              uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                                              void* stream) {
+  const char* what = "qkv_final_indices_from_selected";
+  if (!final_indices || !final_valid || (n_sel > 0 && !selected)) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t history = key_count - 1;
+  if (rows <= 0 || rows > 65535 || history <= 0 || key_count >= (int64_t(1) << 31) || n_sel < 0 ||
+      (n_sel > 0 && selected_ld < n_sel))
+    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535, 2 <= key_count < 2^31, selected_ld >= n_sel >= 0", what);
+  if (protect_sink < 0 || protect_recent < 0) return fail(QKV_ERR_INVALID, "%s: negative protection", what);
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, 0.0, keep_self);
+  const int64_t need = n_sel + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+  if (n_out != need)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the list needs %lld", what, (long long)n_out,
+                (long long)need);
+  final_from_selected_kernel<<<dim3(static_cast<unsigned>(cdiv(n_out, kRT)), static_cast<unsigned>(rows)), kRT, 0,
+                               static_cast<hipStream_t>(stream)>>>(
+      selected, selected_ld, static_cast<int>(n_sel), static_cast<int>(history), static_cast<int>(key_count),
+      static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+      static_cast<int>(c.n_rec), final_indices, final_valid, attn_ids, static_cast<int>(n_out));
   return check_launch(what);
 }
 

@@ -636,16 +636,44 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
 
 
 # -- candidate attention (qabs{S}cand{pct}attn / appendattn, EV:4400-4502) ----
-_QABS_ATTN = re.compile(r"qabs(\d+)cand(\d+(?:p\d+)?)(append)?attn")
+_QABS_ATTN = re.compile(r"qabs(\d+)cand(\d+(?:p\d+)?)(?:(append)|r(\d+))?attn")
 
 
-def parse_qabs_attn_mode(mode: str) -> tuple[int, float, bool]:
-    """``qabs{S}cand{pct}[append]attn`` -> (S, candidate fraction, append):
-    ``appendattn`` keeps the selected copies of protected tokens (EV:4451,
-    2985-3022); the fraction reads ``p`` as the decimal point (EV:748-754)."""
+def parse_qabs_attn_mode(mode: str) -> tuple[int, float, bool, int | None]:
+    """``qabs{S}cand{pct}[append|r{N}]attn`` -> (S, candidate fraction, append,
+    refresh interval or None): ``appendattn`` keeps the selected copies of
+    protected tokens (EV:4451, 2985-3022); ``r{N}attn`` reselects only when the
+    query token is a multiple of max(1, N) and otherwise reuses the last
+    selection (EV:778-782, 4505-4609); the fraction reads ``p`` as the decimal
+    point (EV:748-754)."""
     m = _QABS_ATTN.fullmatch(mode)
-    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}[append]attn mode")
-    return int(m.group(1)), float(m.group(2).replace("p", ".")) / 100.0, m.group(3) is not None
+    _require(m is not None, f"{mode!r} is not a qabs{{S}}cand{{pct}}[append|r{{N}}]attn mode")
+    return (int(m.group(1)), float(m.group(2).replace("p", ".")) / 100.0, m.group(3) is not None,
+            max(1, int(m.group(4))) if m.group(4) is not None else None)
+
+
+def final_indices_from_selected(selected: torch.Tensor, n_sel: int, key_count: int, protect_sink: int,
+                                protect_recent: int, keep_self: bool, *, out: tuple | None = None):
+    """The final index list of a given selection (``qkv_final_indices_from_selected``,
+    EV:2938-2982): selected int64 [rows, >= n_sel]; returns (final_indices
+    int64, final_valid bool, attn_ids int32), each [rows, n_sel + protected]."""
+    lib = _lib.load()
+    _require(selected.dtype == torch.int64 and selected.dim() == 2 and selected.stride(1) == 1
+             and selected.size(1) >= n_sel, "selected must be int64 [rows, >= n_sel]")
+    rows, history = selected.size(0), int(key_count) - 1
+    _require(history >= 1, "need key_count >= 2")
+    n_out = n_sel + int(lib.qkv_reuse_final_count(history, protect_sink, protect_recent, 0.0, int(keep_self))) - 1
+    if out is None:
+        dev = selected.device
+        out = (torch.empty((rows, n_out), dtype=torch.int64, device=dev),
+               torch.empty((rows, n_out), dtype=torch.bool, device=dev),
+               torch.empty((rows, n_out), dtype=torch.int32, device=dev))
+    fi, fv, ids = out
+    with torch.cuda.device(selected.device):
+        _lib.check(lib.qkv_final_indices_from_selected(
+            selected.data_ptr(), selected.stride(0), n_sel, rows, key_count, protect_sink, protect_recent,
+            int(keep_self), fi.data_ptr(), fv.data_ptr(), _lib.ptr(ids), n_out, _lib.stream_of(selected)))
+    return fi, fv, ids
 
 
 def qabs_candidate_select(scores: torch.Tensor, key_count: int, candidate_fraction: float, protect_sink: int,
@@ -701,7 +729,7 @@ class QabsCandidateAttentionStep:
                  device: torch.device | str = "cuda"):
         lib = _lib.load()
         self.mode = mode
-        self.dims, self.cand_fraction, self.append = parse_qabs_attn_mode(mode)
+        self.dims, self.cand_fraction, self.append, self.interval = parse_qabs_attn_mode(mode)
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
         self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
         self.capacity = int(capacity)
@@ -725,14 +753,18 @@ class QabsCandidateAttentionStep:
         _require(need > 0, "unsupported attention shape (head_dim must be 128)")
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
         self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        # r{N}attn: the last refreshing step's selection (EV:1722-1733), its length
+        self.kept = torch.empty((rows, self.n_out_max), dtype=torch.int64, device=device) if self.interval else None
+        self.n_kept = 0
         self.kdm_len = 0
         self.last_history = None
         self.n_out = 0
 
     def reset(self) -> None:
-        """Forget the dim-major copy (a new sequence)."""
+        """Forget the dim-major copy and the kept selection (a new sequence)."""
         self.kdm_len = 0
         self.last_history = None
+        self.n_kept = 0
 
     def prefill(self, key: torch.Tensor) -> None:
         """Build the dim-major copy of the cached history in one launch."""
@@ -752,29 +784,47 @@ class QabsCandidateAttentionStep:
         history = key_count - 1
         if self.last_history is not None and history != self.last_history + 1:
             self.reset()
-        if self.kdm_len < history:
+        # r{N}attn: between refreshes the previous step's selection is reused (EV:4534-4548)
+        reuse = (self.interval is not None and history % self.interval != 0 and self.n_kept > 0
+                 and self.last_history == history - 1)
+        if self.kdm_len < history and not reuse:
             dim_major_append(key, self.kdm, self.kdm_len, history)
             self.kdm_len = history
-        self.launch(query, key, value, scaling)
+        self.launch(query, key, value, scaling, reuse_selection=reuse)
         self.last_history = history
         return self.out
 
-    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> None:
+    def launch(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float, *,
+               reuse_selection: bool = False) -> None:
         """The step's kernels at the history key.size(2) - 1 (the dim-major
-        copy must hold it); output in ``self.out``."""
+        copy must hold it unless ``reuse_selection``, which rebuilds the final
+        list from the kept selection instead, r{N}attn); output in ``self.out``."""
         lib = _lib.load()
         key_count = key.size(2)
         history = key_count - 1
-        _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
         q = query.contiguous()
-        reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
-        n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.cand_fraction,
-                                              int(self.keep_self)))
         rows = self.rows
-        out = (self.final_idx[: rows * n_out].view(rows, n_out), self.final_valid[: rows * n_out].view(rows, n_out),
-               self.attn_ids[: rows * n_out].view(rows, n_out), self.hf)
-        qabs_candidate_select(self.partial, key_count, self.cand_fraction, self.sink, self.recent, self.keep_self,
-                              self.append, workspace=self.sel_ws, out=out)
+        if reuse_selection:
+            n_out = self.n_kept + int(lib.qkv_reuse_final_count(history, self.sink, self.recent, 0.0,
+                                                                int(self.keep_self))) - 1
+            out = (self.final_idx[: rows * n_out].view(rows, n_out),
+                   self.final_valid[: rows * n_out].view(rows, n_out), self.attn_ids[: rows * n_out].view(rows, n_out))
+            final_indices_from_selected(self.kept, self.n_kept, key_count, self.sink, self.recent, self.keep_self,
+                                        out=out)
+        else:
+            _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
+            reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
+            n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.cand_fraction,
+                                                  int(self.keep_self)))
+            out = (self.final_idx[: rows * n_out].view(rows, n_out),
+                   self.final_valid[: rows * n_out].view(rows, n_out), self.attn_ids[: rows * n_out].view(rows, n_out),
+                   self.hf)
+            qabs_candidate_select(self.partial, key_count, self.cand_fraction, self.sink, self.recent,
+                                  self.keep_self, self.append, workspace=self.sel_ws, out=out)
+            if self.interval is not None:   # the selection the next steps reuse (EV:4574-4580)
+                keep = budget_count(history, self.cand_fraction)
+                self.kept[:, :keep].copy_(out[0][:, :keep])
+                self.n_kept = keep
         token_attention(q, key, value, out[2], scaling, workspace=self.attn_ws, out=self.out)
         self.n_out = n_out
 
@@ -785,6 +835,8 @@ class QabsCandidateAttentionStep:
         return self.final_idx[: self.rows * n].view(shape), self.final_valid[: self.rows * n].view(shape)
 
     def final_mask(self) -> torch.Tensor:
-        """The last step's selection plus the protected ranges, bool [B, Hq, history]."""
+        """The last selecting step's selection plus the protected ranges, bool
+        [B, Hq, history] (r{N}attn steps that reuse a selection leave it as it
+        was; their list is ``final_indices()``)."""
         h = self.last_history
         return self.hf[:, :h].reshape(self.batch, self.q_heads, h)

@@ -264,6 +264,45 @@ def qabs_attn_step(query, key, value, dim_count: int, candidate_fraction: float,
     return final_attention(q, kx, vx, idx, final_keep, scaling), final_keep
 
 
+def qabs_periodic_step(query, key, value, dim_count: int, candidate_fraction: float, interval: int,
+                       scaling: float, sink: int = 0, recent: int = 0, keep_self: bool = True, previous=None):
+    """One ``qabs{S}cand{pct}r{N}attn`` decode step (EV:4505-4609, the default
+    path without QABS_PERIODIC_FUSED_REMOTE_RECENT): when the query token
+    (= history) is not a multiple of ``interval`` and ``previous`` holds the
+    last step's selected indices (the state keeps them for query token - 1
+    only, EV:1702-1733), they are reused as they are; otherwise the
+    ``min(history, max(1, ceil(pct * history)))`` best fp32 partial scores
+    are selected (ties to the lower index).  The final list is
+    ``final_indices_np`` of the selection at the current history
+    (EV:2938-2982), then attention over it.
+
+    Returns (out float64 [B,1,Hq,D], final_keep bool [B,Hq,T], the selection
+    int64 [B,Hq,n] the next step may reuse)."""
+    from .qkv_oracle import topk_lowest_index
+
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, hq, _ = q.shape
+    g = hq // k.shape[1]
+    kx, vx = np.repeat(k, g, axis=1), np.repeat(v, g, axis=1)
+    key_count = k.shape[2]
+    history = key_count - 1
+    if previous is not None and history % max(1, int(interval)) != 0:
+        sel = np.asarray(previous, dtype=np.int64)
+    else:
+        requested = min(history, max(1, math.ceil(candidate_fraction * history)))
+        part = partial_scores(q, kx[:, :, :history], dim_count)
+        sel = np.sort(topk_lowest_index(part.reshape(-1, history), requested), axis=-1)
+        sel = sel.reshape(b, hq, requested).astype(np.int64)
+    valid = (sel >= 0) & (sel < history)
+    fi, fv = final_indices_np(np.maximum(sel, 0), valid, history, key_count, sink, recent, keep_self)
+    keep = np.zeros((b, hq, key_count), dtype=bool)
+    for lead in np.ndindex(b, hq):
+        keep[lead][fi[lead][fv[lead]]] = True
+    return final_attention(q, kx, vx, fi, fv, scaling), keep, sel
+
+
 # ---------------------------------------------------------------------------
 # Candidate reuse and exact rerank (qabs{S}cand{pct}reuse[final|2set])
 # ---------------------------------------------------------------------------

@@ -29,6 +29,7 @@ Outputs ``tests/golden/reuse_<name>.npz`` and ``tests/golden/block_<name>.npz``
 
 from __future__ import annotations
 
+import re
 import sys
 import types
 from pathlib import Path
@@ -181,6 +182,11 @@ BLOCK_SCENARIOS = {
     "qabs8cand5appendattn_fp32": ("qabs8cand5appendattn", torch.float32, 4, 2, 260, 3, 0.02, 12, 20, True, 24),
     "qabs16cand10appendattn_bf16": ("qabs16cand10appendattn", torch.bfloat16, 4, 2, 230, 3, 0.02, 8, 16, False,
                                     125),
+    # the periodic variant reselects when the query token is a multiple of N
+    # and otherwise reuses the last step's selection (EV:4505-4609; its state
+    # is a ReuseCandidateState); the steps cross a multiple of N
+    "qabs8cand5r3attn_fp32": ("qabs8cand5r3attn", torch.float32, 4, 2, 268, 5, 0.02, 4, 6, True, 26),
+    "qabs8cand3r2attn_bf16": ("qabs8cand3r2attn", torch.bfloat16, 4, 2, 251, 5, 0.02, 2, 3, True, 727),
 }
 
 
@@ -205,6 +211,8 @@ def run_block(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, rec
 
     ev._maybe_cuda_final_attention = record
     brep_state = ev.BlockRepState() if mode.startswith("brep") else None
+    periodic = re.fullmatch(r"qabs\d+cand\d+(?:p\d+)?r\d+attn", mode) is not None
+    reuse_state = ev.ReuseCandidateState() if periodic else None
     outs, finals = [], []
     try:
         # qabs{S}cand{pct}attn runs its candidate path only with the fast-path
@@ -212,7 +220,7 @@ def run_block(ev, name, mode, dtype, hq, hkv, t0, steps, top_fraction, sink, rec
         with ev.attention_mode(mode=mode, top_fraction=top_fraction, max_heads_per_token=3,
                                always_keep_self=keep_self, protect_sink_tokens=sink,
                                protect_recent_tokens=recent, load_stats=None, brep_state=brep_state,
-                               qabs_fast_path=mode.startswith("qabs")):
+                               reuse_state=reuse_state, qabs_fast_path=mode.startswith("qabs")):
             for s in range(steps):
                 n = t0 + s + 1
                 seen.clear()

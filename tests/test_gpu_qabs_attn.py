@@ -12,7 +12,7 @@ from kv_cache_amd import qabs_cuda_kernels as Q
 from kv_cache_amd import reuse as RU
 from oracle import ref_semantics as R
 from oracle.qkv_oracle import topk_lowest_index
-from tests.test_oracle_block import APPEND_SCENARIOS, ATTN_SCENARIOS, load_block_golden
+from tests.test_oracle_block import APPEND_SCENARIOS, ATTN_SCENARIOS, PERIODIC_SCENARIOS, load_block_golden
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -119,3 +119,72 @@ def test_candidate_select_rejects_bad_arguments():
         RU.qabs_candidate_select(s, 1, 0.1, 0, 0, True)
     with pytest.raises(RuntimeError, match="not a qabs"):
         RU.QabsCandidateAttentionStep("qabs8cand3reuse", 1, 4, 2, 128, 256)
+
+
+def _keep_of(fi, fv, key_count):
+    fi, fv = fi.cpu().numpy(), fv.cpu().numpy().astype(bool)
+    keep = np.zeros((*fi.shape[:-1], key_count), dtype=bool)
+    for lead in np.ndindex(*fi.shape[:-1]):
+        keep[lead][fi[lead][fv[lead]]] = True
+    return keep
+
+
+@pytest.mark.parametrize("name", [n for n in PERIODIC_SCENARIOS if n.endswith("bf16")])
+def test_periodic_step_matches_reference_vectors(name):
+    # qabs{S}cand{pct}r{N}attn: steps at a multiple of N reselect, the others
+    # rebuild the list from the kept selection at their own history
+    g = load_block_golden(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
+    v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
+    step = RU.QabsCandidateAttentionStep(g["mode"], 1, hq, hkv, 128, 1024, protect_sink=g["sink"],
+                                         protect_recent=g["recent"], keep_self=g["keep_self"])
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
+        out = step(q, k[:, :, :n], v[:, :, :n], g["scaling"])
+        fi, fv = step.final_indices()
+        assert np.array_equal(_keep_of(fi, fv, n), g["final"][s][..., :n]), s
+        np.testing.assert_allclose(f32(out), g["out"][s], rtol=1e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("name", [n for n in PERIODIC_SCENARIOS if n.endswith("fp32")])
+def test_periodic_pieces_match_reference_vectors(name):
+    g = load_block_golden(name)
+    hq, hkv = g["q"].shape[2], g["k"].shape[1]
+    k_all = torch.from_numpy(np.repeat(g["k"], hq // hkv, axis=1)).to(DEV)
+    v_all = torch.from_numpy(np.repeat(g["v"], hq // hkv, axis=1)).to(DEV)
+    kept = None
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        q = torch.from_numpy(g["q"][s]).to(DEV)
+        k, v = k_all[:, :, :n], v_all[:, :, :n]
+        if kept is not None and (n - 1) % g["interval"] != 0:
+            fi, fv, ids = RU.final_indices_from_selected(kept, kept.size(1), n, g["sink"], g["recent"],
+                                                         g["keep_self"])
+        else:
+            part = Q.partial_scores(q, k[:, :, : n - 1], g["dims"]).view(hq, n - 1)
+            fi, fv, ids, _ = RU.qabs_candidate_select(part, n, g["cand"], g["sink"], g["recent"], g["keep_self"])
+            keep_n = R.budget_count(n - 1, g["cand"])
+            kept = fi[:, :keep_n].contiguous()
+        assert np.array_equal(_keep_of(fi.view(1, hq, -1), fv.view(1, hq, -1), n), g["final"][s][..., :n]), s
+        out = Q.final_attention(q, k, v, fi.view(1, hq, -1), fv.view(1, hq, -1), g["scaling"])
+        np.testing.assert_allclose(f32(out)[:, 0], g["out"][s], rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("hist,n_sel,sink,recent,keep_self", [(500, 40, 4, 8, True), (33, 20, 0, 0, False),
+                                                              (100, 1, 60, 60, True), (2000, 0, 3, 3, True)])
+def test_final_indices_from_selected_matches_oracle(hist, n_sel, sink, recent, keep_self):
+    # selections with indices in the protected ranges, past the history and
+    # negative; every entry and its validity as EV:2938-2982 builds them
+    gen = torch.Generator().manual_seed(hist + n_sel)
+    rows = 3
+    sel = torch.randint(-3, hist + 5, (rows, n_sel + 2), generator=gen)
+    fi, fv, ids = RU.final_indices_from_selected(sel.to(DEV), n_sel, hist + 1, sink, recent, keep_self)
+    s = sel[:, :n_sel].numpy()
+    want_i, want_v = R.final_indices_np(np.maximum(s, 0), (s >= 0) & (s < hist), hist, hist + 1, sink, recent,
+                                        keep_self)
+    got_i, got_v = fi.cpu().numpy(), fv.cpu().numpy()
+    assert np.array_equal(got_v, want_v)
+    assert np.array_equal(got_i[got_v], want_i[want_v])   # invalid entries' indices are not read
+    assert np.array_equal(ids.cpu().numpy(), np.where(got_v, got_i, -1))

@@ -17,6 +17,7 @@ BLOCK_SCENARIOS = ["qbb16q8s12cand4_fp32", "qbb8q16s25cand6p25_fp32", "brep16r2q
                    "qboracle16q8s12cand4_bf16"]
 ATTN_SCENARIOS = ["qabs8cand3attn_fp32", "qabs16cand10attn_fp32", "qabs8cand5attn_bf16"]
 APPEND_SCENARIOS = ["qabs8cand5appendattn_fp32", "qabs16cand10appendattn_bf16"]
+PERIODIC_SCENARIOS = ["qabs8cand5r3attn_fp32", "qabs8cand3r2attn_bf16"]
 
 
 def parse_block_mode(mode):
@@ -29,7 +30,7 @@ def parse_block_mode(mode):
     m = re.fullmatch(r"qboracle(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
     if m:
         return "qboracle", int(m.group(1)), 1, int(m.group(2)), pct(m.group(3)), pct(m.group(4))
-    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)(?:append)?attn", mode)
+    m = re.fullmatch(r"qabs(\d+)cand(\d+(?:p\d+)?)(?:append|r\d+)?attn", mode)
     if m:
         return "qabs", 1, 1, int(m.group(1)), 1.0, pct(m.group(2))
     m = re.fullmatch(r"brep(\d+)r(\d+)q(\d+)s(\d+(?:p\d+)?)cand(\d+(?:p\d+)?)", mode)
@@ -48,6 +49,8 @@ def load_block_golden(name):
         "recent": int(z["recent"]), "keep_self": bool(z["keep_self"]), "scaling": float(z["scaling"]),
         "out": z["out"][:, :, 0], "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
         "append": str(z["mode"]).endswith("appendattn"),
+        "interval": (int(re.fullmatch(r"qabs\d+cand\d+(?:p\d+)?r(\d+)attn", str(z["mode"])).group(1))
+                     if re.fullmatch(r"qabs\d+cand\d+(?:p\d+)?r\d+attn", str(z["mode"])) else None),
     }
 
 
@@ -80,6 +83,26 @@ def test_qabs_attn_steps_match_reference_vectors(name):
             plain, _ = R.qabs_attn_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"],
                                         g["scaling"], g["sink"], g["recent"], g["keep_self"])
             assert np.abs(plain - out).max() > 1e-3, (name, s)
+
+
+@pytest.mark.parametrize("name", PERIODIC_SCENARIOS)
+def test_qabs_periodic_steps_match_reference_vectors(name):
+    # qabs{S}cand{pct}r{N}attn: the selection made at a multiple of N (or on
+    # the first step) is reused until the next one, with the protected tokens
+    # of each step's own history; every step's final set and output
+    g = load_block_golden(name)
+    tol = dict(rtol=1e-5, atol=1e-5) if name.endswith("fp32") else dict(rtol=1e-2, atol=2e-2)
+    prev, reused = None, 0
+    for s in range(g["steps"]):
+        n = g["t0"] + s + 1
+        out, keep, sel = R.qabs_periodic_step(g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["dims"], g["cand"],
+                                              g["interval"], g["scaling"], g["sink"], g["recent"], g["keep_self"],
+                                              prev)
+        reused += prev is not None and sel is prev
+        assert np.array_equal(keep, g["final"][s][..., :n]), (name, s)
+        np.testing.assert_allclose(out[:, 0], g["out"][s], **tol)
+        prev = sel
+    assert 0 < reused < g["steps"] - 1   # the steps both reuse and reselect
 
 
 @pytest.mark.parametrize("name", ATTN_SCENARIOS)
