@@ -25,8 +25,11 @@ import math
 import re
 from dataclasses import dataclass
 
-# Suffixes of the qabs family that share the (S, pct) prefix (EV:749); only
-# "attn" is a mode of this path, the others parse but plan nothing.
+# Suffixes of the qabs family that share the (S, pct) prefix (EV:749).  The
+# int4 step plans "attn" only; the exact fp32 "attn" / "appendattn" /
+# "r{N}attn" steps, the "reuse..." steps and the lagged prefixes are served by
+# kv_cache_amd.reuse (QabsCandidateAttentionStep, ReuseDecodeStep,
+# LaggedReuseDecodeStep); the shared / top2 suffixes are other selectors.
 _QABS = re.compile(
     r"(?:qabs|lagtop2qabs|lagrefresh\d+qabs|qdrift(?:maj|head|share|cos|coshead)?qabs|pconf\d+(?:p\d+)?qabs)"
     r"(\d+)cand(\d+(?:p\d+)?)"
