@@ -567,29 +567,33 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     len = cn[2 * tid];
     nf = cn[2 * tid + 1];
   }
-  // the protected ranges, 16 bytes per store where the row is 16-byte aligned
-  const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
-  for (int t0 = 16 * tid; t0 < body; t0 += 16 * kWideNT) {
-    uint32_t w[4];
+  // the protected ranges, 16 bytes per store where the row is 16-byte aligned;
+  // written after the selection's loads are out, and ordered before the
+  // scatter below by the barriers of the selection (run) or of place
+  auto write_protected = [&]() {
+    const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
+    for (int t0 = 16 * tid; t0 < body; t0 += 16 * kWideNT) {
+      uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t x = 0;
+      for (int j = 0; j < 4; ++j) {
+        uint32_t x = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int t = t0 + 4 * j + b;
-        x |= static_cast<uint32_t>((t < sink_end) || (t >= recent_start)) << (8 * b);
+        for (int b = 0; b < 4; ++b) {
+          const int t = t0 + 4 * j + b;
+          x |= static_cast<uint32_t>((t < sink_end) || (t >= recent_start)) << (8 * b);
+        }
+        w[j] = x;
       }
-      w[j] = x;
+      *reinterpret_cast<uint4*>(hrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    *reinterpret_cast<uint4*>(hrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-  for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
+    for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
+  };
   if (tid < 64) {   // tile list offsets: a wave scan of the lengths
     const int incl = wave_incl_scan_dpp(len), fin_all = wave_incl_scan_dpp(nf);
     if (tid <= n_tiles) tile_off[tid] = incl - len;   // tile_off[n_tiles] = the total
     if (tid == 63) n_fin = fin_all;
   }
-  __syncthreads();   // also orders the protected-range writes above before the scatter below
+  __syncthreads();
   const int64_t o = static_cast<int64_t>(row) * n_out;
   auto emit = [&](int idx, int p, bool valid) {
     if (valid) hrow[idx] = 1;
@@ -620,6 +624,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
       tok[i] = ok ? trow[e] : 0;
       wc.set(i, ok ? crow[e] : 0.0f, ok);
     }
+    write_protected();
     wc.run(keep, sh.c);
     uint64_t fin = 0;
 #pragma unroll
@@ -629,6 +634,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     WS ws;
     ws.load_count(scores + static_cast<int64_t>(row) * scores_ld, history, sh.d);   // first digit counted on load
     ws.run_counted(keep, sh.d);
+    write_protected();
     uint64_t fin = 0;   // bit i: key i is a finite score
 #pragma unroll
     for (int i = 0; i < VPL; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(ws.u[i]))) << i;
