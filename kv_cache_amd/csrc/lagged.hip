@@ -3,19 +3,20 @@
 // pconf{T} modes (EV:4020-4198), ahead of the exact rerank of the union
 // (qkv_reuse_select).  A row is one (sequence, query head) r = b * Hq + h.
 //
-//   lag_flags_kernel   one workgroup per row: the row's top-|q| dims and their
-//                      q values (the state the next step compares with), then
-//                      the row's refresh test: top-dim overlap, or overlap or
-//                      cosine;
-//   lag_ess_kernel     the pconf test, a row's positions split over several
-//     + lag_ess_merge_kernel  workgroups: the effective sample size of the
-//                      attention weights over the previous final selection;
-//   lag_union_kernel   16 positions of one row per thread (a workgroup per
-//                      4096 positions of a row): keeps the current candidates
-//                      of the rows that refresh
-//                      (zeroes the others), and writes the union with the
-//                      previous final mask, the candidates shared across heads
-//                      (qdriftshare) and the sink / recent ranges.
+//   lag_flags_kernel      one workgroup per row: the row's top-|q| dims and
+//                         their q values (the state the next step compares
+//                         with), then the row's refresh test: top-dim overlap,
+//                         or overlap or cosine;
+//   lag_ess_kernel        the pconf test, a row's positions split over several
+//   lag_ess_merge_kernel  workgroups, then merged: the effective sample size of
+//                         the attention weights over the previous final
+//                         selection;
+//   lag_union_kernel      16 positions of one row per thread (a workgroup per
+//                         4096 positions of a row): keeps the current
+//                         candidates of the rows that refresh (zeroes the
+//                         others) and writes the union with the previous final
+//                         mask, the candidates shared across heads
+//                         (qdriftshare) and the sink / recent ranges.
 // The step-wide decisions (any / majority of the flags) are taken inside the
 // union kernel, so a step needs no host round trip.  EV = ymluo/projects/
 // qwen3_top2_head_limit3_ppl/src/evaluate_qwen3_top2_head_limit3_ppl.py.
