@@ -121,3 +121,50 @@ def test_sample_column_table_rows_are_the_host_columns():
         n = counts[h]
         assert n == cols.numel() and torch.equal(table[h, :n], cols)
         assert bool((table[h, n:] == cols[-1]).all())
+
+
+@pytest.mark.parametrize("mode,want", [
+    ("lagtop2qabs8cand5", ("lagtop2", None, 8, 0.05)),
+    ("lagrefresh3qabs16cand6p25", ("lagrefresh", 3, 16, 0.0625)),
+    ("lagrefresh0qabs8cand5", ("lagrefresh", 1, 8, 0.05)),          # max(1, N) (EV:924-928)
+    ("qdriftqabs8cand5", ("qdrift", None, 8, 0.05)),
+    ("qdriftcosheadqabs8cand10", ("qdriftcoshead", None, 8, 0.1)),
+    ("pconf37p5qabs16cand10", ("pconf", 0.375, 16, 0.1)),            # T / 100, 'p' as the point (EV:918-922)
+])
+def test_parse_lagged_mode(mode, want):
+    from kv_cache_amd import reuse as RU
+
+    kind, param, dims, frac = RU.parse_lagged_mode(mode)
+    assert (kind, dims) == (want[0], want[2]) and frac == pytest.approx(want[3])
+    assert param == (pytest.approx(want[1]) if isinstance(want[1], float) else want[1])
+    assert RU.is_lagged_mode(mode)
+
+
+@pytest.mark.parametrize("mode", ["qabs8cand5reuse", "lagtop2qabs8cand5reuse", "qdriftfooqabs8cand5", "pconfqabs8cand5"])
+def test_parse_lagged_mode_rejects(mode):
+    from kv_cache_amd import reuse as RU
+
+    assert not RU.is_lagged_mode(mode)
+    with pytest.raises(RuntimeError, match="not a lagged reuse mode"):
+        RU.parse_lagged_mode(mode)
+
+
+@pytest.mark.parametrize("mode,want", [
+    ("qabs8cand3attn", (8, 0.03, False, None)),
+    ("qabs16cand6p25appendattn", (16, 0.0625, True, None)),
+    ("qabs8cand5r4attn", (8, 0.05, False, 4)),
+    ("qabs8cand5r0attn", (8, 0.05, False, 1)),                       # max(1, N) (EV:778-782)
+])
+def test_parse_qabs_attn_mode(mode, want):
+    from kv_cache_amd import reuse as RU
+
+    dims, frac, append, interval = RU.parse_qabs_attn_mode(mode)
+    assert (dims, append, interval) == (want[0], want[2], want[3]) and frac == pytest.approx(want[1])
+
+
+@pytest.mark.parametrize("mode", ["qabs8cand3", "qabs8cand3r4appendattn", "qabs8cand3sharedattn", "qabs8cand3reuse"])
+def test_parse_qabs_attn_mode_rejects(mode):
+    from kv_cache_amd import reuse as RU
+
+    with pytest.raises(RuntimeError, match="is not a qabs"):
+        RU.parse_qabs_attn_mode(mode)
