@@ -579,6 +579,9 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
                          candidate_selection="topk", device=device)
         s = min(max(1, self.dims), head_dim)
         _require(head_dim <= 128, "the lagged reuse modes take head_dim <= 128")
+        # rows that keep skip the partial scores; past 40960 positions the staged
+        # top-k still reads their rows, which then hold finite (stale) scores
+        self.partial.zero_()
         self.qdims = [torch.zeros((self.rows, s), dtype=torch.int32, device=device) for _ in range(2)]
         self.qvals = [torch.zeros((self.rows, s), dtype=torch.float32, device=device) for _ in range(2)]
         self.flags = torch.zeros(self.rows, dtype=torch.uint8, device=device)
