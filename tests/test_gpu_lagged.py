@@ -323,3 +323,31 @@ def test_lagged_step_matches_oracle_multistep(mode):
         if flagged is not None and kind in ("qdrifthead", "qdriftcoshead", "qdriftshare", "pconf"):
             assert np.array_equal(step.flags.cpu().numpy().astype(bool), flagged.reshape(-1)), s
         np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("mode", ["qdriftheadqabs8cand5", "qdriftmajqabs8cand5"])
+def test_lagged_step_long_rows_match_oracle(mode):
+    # 45000 history tokens: past the one-workgroup selection, the candidates of
+    # every row are thresholded by the staged top-k (rows that keep included,
+    # their scores stale) and the union clears the rows that keep
+    gen = torch.Generator().manual_seed(len(mode) * 11)
+    t, steps, hq, hkv = 45000, 3, 8, 2
+    kind, param, dims, cand = RU.parse_lagged_mode(mode)
+    eps = torch.tensor([0.02, 3.0, 0.05, 0.3, 0.01, 2.0, 0.1, 1.0]).view(1, 1, hq, 1)
+    base = torch.randn((1, 1, hq, 128), generator=gen)
+    q = ((base + eps * torch.randn((steps, 1, hq, 128), generator=gen)) / torch.sqrt(1 + eps * eps)).to(torch.bfloat16)
+    k = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((1, hkv, t + steps, 128), generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = RU.LaggedReuseDecodeStep(mode, 1, hq, hkv, 128, t + 64, top_fraction=0.02, protect_sink=4,
+                                    protect_recent=8)
+    prev = None
+    for s in range(steps):
+        n = t + s + 1
+        out = step(q[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        want, wc, wf, prev, _ = R.lagged_reuse_decode_step(f32(q[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), kind,
+                                                           param, dims, cand, 0.02, 4, 8, True, 128 ** -0.5, prev,
+                                                           True)
+        assert np.array_equal(step.candidate_mask().cpu().numpy(), wc), s
+        assert np.array_equal(step.final_mask().cpu().numpy(), wf), s
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
