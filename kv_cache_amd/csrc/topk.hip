@@ -131,38 +131,16 @@ __global__ __launch_bounds__(NT) void topk_kernel(const float* __restrict__ valu
 // DPP scan of per-lane counts) instead of a ballot round per slot.  The
 // radix select uses a wave-private 256-bin LDS histogram (a wave's LDS
 // operations complete in order) and a DPP scan.  With many rows the kernel
-// is bound by instruction issue, not latency.  Same contract as select_row.
-template <int VPL, bool FINITE>
-__global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict__ values, int64_t rows, int n,
-                                                        int64_t ld, int k, int32_t* __restrict__ out) {
-  __shared__ int hist[4][256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
-  if (row >= rows) return;   // wave-uniform
-  const float* vals = values + row * ld;
-  int* wh = hist[wave];
-
-  uint32_t u[VPL];
-  bool valid[VPL];
-  const int first = lane * VPL;
-  if (VPL % 4 == 0 && n == 64 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // wave-uniform
-#pragma unroll
-    for (int i = 0; i < VPL; i += 4) {
-      const uint4 w = *reinterpret_cast<const uint4*>(vals + first + i);
-      u[i] = w.x;
-      u[i + 1] = w.y;
-      u[i + 2] = w.z;
-      u[i + 3] = w.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) u[i] = __float_as_uint(vals[min(first + i, n - 1)]);
-  }
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    u[i] = f32_sortable(__uint_as_float(u[i]));
-    valid[i] = first + i < n && (!FINITE || u[i] != kNegInfKey);
-  }
+// is bound by VALU issue (about 1000 instructions a row of 1024 keys), not
+// latency.  Same contract as select_row.
+//
+// wave_select_row is the selection once the lane's keys are in registers as
+// order-preserving uint32 (valid[i]: key first + i is selectable); wh is the
+// wave's 256-int LDS histogram, orow the row's k output slots.
+template <int VPL>
+__device__ __forceinline__ void wave_select_row(uint32_t (&u)[VPL], const bool (&valid)[VPL], int first, int k,
+                                                int* wh, int32_t* orow) {
+  const int lane = threadIdx.x & 63;
   uint32_t umax = 0, umin = 0xFFFFFFFFu;
   int nval = 0;
 #pragma unroll
@@ -238,7 +216,6 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
   }
   const uint32_t theta = prefix;
 
-  int32_t* orow = out + row * k;
   // Keys > theta and == theta of this lane, then of the lanes before it; the
   // lane takes its first min(ce, kr - eq_before) keys equal to theta.
   uint32_t gtm = 0, eqm = 0;
@@ -262,6 +239,263 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
     eq_seen += eq ? 1 : 0;
   }
   for (int j = kk + lane; j < k; j += 64) orow[j] = -1;
+}
+
+template <int VPL, bool FINITE>
+__global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict__ values, int64_t rows, int n,
+                                                        int64_t ld, int k, int32_t* __restrict__ out) {
+  __shared__ int hist[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (row >= rows) return;   // wave-uniform
+  const float* vals = values + row * ld;
+
+  uint32_t u[VPL];
+  bool valid[VPL];
+  const int first = lane * VPL;
+  if (VPL % 4 == 0 && n == 64 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // wave-uniform
+#pragma unroll
+    for (int i = 0; i < VPL; i += 4) {
+      const uint4 w = *reinterpret_cast<const uint4*>(vals + first + i);
+      u[i] = w.x;
+      u[i + 1] = w.y;
+      u[i + 2] = w.z;
+      u[i + 3] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) u[i] = __float_as_uint(vals[min(first + i, n - 1)]);
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    u[i] = f32_sortable(__uint_as_float(u[i]));
+    valid[i] = first + i < n && (!FINITE || u[i] != kNegInfKey);
+  }
+  wave_select_row<VPL>(u, valid, first, k, hist[wave], out + row * k);
+}
+
+// Many rows of finite or -inf keys (block maxima of a prefill chunk), k <= 64,
+// -inf never selected: one wave per row as in topk_wave_kernel, but only the
+// keys that can be selected enter the radix passes and the placement.  The k-th
+// largest key of any subset of the row bounds the row's k-th largest from
+// below; the subset here is every lane's two largest keys (128 keys, so a few
+// lanes left empty by a causal -inf tail still leave k of them), and its k-th
+// largest is resolved to 10 bits by ballot counts.  For i.i.d. keys about 72
+// of a 1024-key row reach that bound (sampled: at most 91 in 20000 rows, with
+// or without a 32-key -inf tail).  Those candidates are compacted, in index
+// order, into a wave-private LDS list, and each lane then works on list
+// entries lane, lane + 64, ... (one or two, where the full row puts 16 keys on
+// a lane).  The list being in index order, a taken entry's output position is
+// the count of taken entries in the slots before plus mbcnt of the slot's
+// ballot.  Candidates are found with a float compare against the bound's
+// float, which keeps every key whose order-preserving form is at or above the
+// bound (the map folds -0 onto +0 as the compare does); a row with more than
+// kCandCap candidates (heavy ties) takes the full-row selection.
+constexpr int kCandCap = 256;
+
+// A lower bound of the j-th largest of the wave's values v1, v2 (two per
+// lane, 0 = none), given the largest value vmax and a value vmin <= every
+// nonzero one: the largest x with at least j values at or above it, resolved
+// to BITS bits below the bits vmax and vmin share; 0 when fewer than j values
+// exist.  Wave-uniform.
+template <int BITS>
+__device__ __forceinline__ uint32_t wave_lower_bound2(uint32_t v1, uint32_t v2, int j, uint32_t vmax,
+                                                      uint32_t vmin) {
+  if (__popcll(__ballot(v1 != 0)) + __popcll(__ballot(v2 != 0)) < j) return 0;
+  if (vmax == vmin) return vmax;   // every value is vmax
+  const int top = 31 - __builtin_clz(vmax ^ vmin);
+  uint32_t x = top == 31 ? 0u : vmax & ~((2u << top) - 1u);
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) {
+    if (top - b < 0) break;
+    const uint32_t c = x | (1u << (top - b));
+    if (__popcll(__ballot(v1 >= c)) + __popcll(__ballot(v2 >= c)) >= j) x = c;
+  }
+  return x;
+}
+
+// Keys of one row into registers, positions past n as -inf.
+template <int VPL>
+__device__ __forceinline__ void load_row_keys(const float* vals, int n, int first, uint32_t (&w)[VPL]) {
+  if (VPL % 4 == 0 && n == 64 * VPL && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {   // wave-uniform
+#pragma unroll
+    for (int i = 0; i < VPL; i += 4) {
+      const uint4 q = *reinterpret_cast<const uint4*>(vals + first + i);
+      w[i] = q.x;
+      w[i + 1] = q.y;
+      w[i + 2] = q.z;
+      w[i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const uint32_t x = __float_as_uint(vals[min(first + i, n - 1)]);
+      w[i] = first + i < n ? x : 0xFF800000u;
+    }
+  }
+}
+
+template <int VPL>
+__device__ __forceinline__ void cand_select_row(const uint32_t (&w)[VPL], int first, int k, int32_t* orow,
+                                                uint2* cl, int* wh) {
+  constexpr int kSlots = kCandCap / 64;
+  const int lane = threadIdx.x & 63;
+  // the lane's largest (m1) and second largest (m2) key: the median of
+  // {m1, m2, x} is the new second largest
+  float m1 = __uint_as_float(w[0]), m2 = -INFINITY;
+#pragma unroll
+  for (int i = 1; i < VPL; ++i) {
+    const float x = __uint_as_float(w[i]);
+    m2 = __builtin_amdgcn_fmed3f(m1, m2, x);
+    m1 = fmaxf(m1, x);
+  }
+  const uint32_t k1 = m1 > -INFINITY ? f32_sortable(m1) : 0u;   // 0: none
+  const uint32_t k2 = m2 > -INFINITY ? f32_sortable(m2) : 0u;
+  const uint32_t umax = wave_minmax_u32<true>(k1);
+  if (umax == 0) {   // nothing selectable
+    for (int j = lane; j < k; j += 64) orow[j] = -1;
+    return;
+  }
+  const uint32_t vmin = wave_minmax_u32<false>(k2 ? k2 : (k1 ? k1 : 0xFFFFFFFFu));
+  // 0 when fewer than k of the 128 hold a key: then every finite key is a candidate
+  const uint32_t lo = max(wave_lower_bound2<10>(k1, k2, k, umax, vmin), kNegInfKey + 1);
+  const float lo_f = sortable_f32(lo);   // -FLT_MAX at the floor
+
+  int c = 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) c += __uint_as_float(w[i]) >= lo_f ? 1 : 0;
+  const int incl = wave_incl_scan_dpp(c);
+  const int total = __builtin_amdgcn_readlane(incl, 63);
+  if (total > kCandCap) {   // wave-uniform: the full-row selection
+    uint32_t u[VPL];
+    bool valid[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      u[i] = f32_sortable(__uint_as_float(w[i]));
+      valid[i] = u[i] != kNegInfKey;
+    }
+    wave_select_row<VPL>(u, valid, first, k, wh, orow);
+    return;
+  }
+  int pos = incl - c;
+  // total <= k: every candidate is selected (a bound above the floor has at
+  // least k keys at or above it, so total == k; at the floor the candidates
+  // are all the selectable keys)
+  if (total <= k) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (__uint_as_float(w[i]) >= lo_f) orow[pos++] = first + i;
+    for (int j = total + lane; j < k; j += 64) orow[j] = -1;
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+    if (__uint_as_float(w[i]) >= lo_f) cl[pos++] = make_uint2(w[i], static_cast<uint32_t>(first + i));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int ns = (total + 63) >> 6;   // wave-uniform
+  uint32_t cu[kSlots];
+  int32_t ci[kSlots];
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    cu[s] = 0u;   // below every bound: never counted or taken
+    ci[s] = -1;
+    if (s < ns) {
+      const int j = s * 64 + lane;
+      const uint2 e = cl[j];
+      if (j < total) {
+        cu[s] = f32_sortable(__uint_as_float(e.x));
+        ci[s] = static_cast<int32_t>(e.y);
+      }
+    }
+  }
+
+  // Radix select of the k-th largest candidate at or above lo, 8 bits a pass
+  // below the bits it shares with the row's largest key.
+  int kr = k;
+  uint32_t prefix = umax, mask = 0xFFFFFFFFu;
+  int remaining = umax == lo ? 0 : 32 - __builtin_clz(umax ^ lo);
+  if (remaining) {
+    mask = remaining == 32 ? 0u : ~((1u << remaining) - 1u);
+    prefix = umax & mask;
+  }
+  while (remaining > 0) {   // wave-uniform
+    const int shift = remaining > 8 ? remaining - 8 : 0;
+    const uint32_t dmask = (1u << (remaining - shift)) - 1u;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) wh[4 * lane + b] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s)
+      if (s < ns && cu[s] >= lo && (cu[s] & mask) == prefix) atomicAdd(&wh[(cu[s] >> shift) & dmask], 1);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int cb[4], tot = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      cb[b] = wh[255 - 4 * lane - b];
+      tot += cb[b];
+    }
+    int above = wave_incl_scan_dpp(tot) - tot;
+    int my_bin = -1, my_kr = 0, my_whole = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (above < kr && kr <= above + cb[b]) {
+        my_bin = 255 - 4 * lane - b;
+        my_kr = kr - above;
+        my_whole = (kr - above) == cb[b];
+      }
+      above += cb[b];
+    }
+    const uint64_t who = __ballot(my_bin >= 0);
+    const int src = __builtin_ctzll(who);   // exactly one lane holds the kr-th key's bin
+    const int bin = __builtin_amdgcn_readlane(my_bin, src);
+    kr = __builtin_amdgcn_readlane(my_kr, src);
+    prefix |= static_cast<uint32_t>(bin) << shift;
+    mask |= dmask << shift;
+    remaining = shift;
+    if (__builtin_amdgcn_readlane(my_whole, src)) {
+      kr = 0x7FFFFFFF;
+      break;
+    }
+  }
+  const uint32_t theta = prefix;
+
+  // Entries > theta, and the first kr entries == theta, in list (= index) order.
+  int before = 0, eq_seen = 0;
+#pragma unroll
+  for (int s = 0; s < kSlots; ++s) {
+    if (s < ns) {
+      const bool eq = cu[s] == theta;
+      const uint64_t em = __ballot(eq);
+      const int erank = eq_seen + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                      static_cast<uint32_t>(em >> 32),
+                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(em), 0u)));
+      const bool take = cu[s] > theta || (eq && erank < kr);
+      const uint64_t tm = __ballot(take);
+      const int o = before + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                 static_cast<uint32_t>(tm >> 32),
+                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(tm), 0u)));
+      if (take) orow[o] = ci[s];
+      before += __popcll(tm);
+      eq_seen += __popcll(em);
+    }
+  }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void topk_cand_wave_kernel(const float* __restrict__ values, int64_t rows,
+                                                             int n, int64_t ld, int k, int32_t* __restrict__ out) {
+  __shared__ uint2 cand[4][kCandCap];   // (key bits, index)
+  __shared__ int hist[4][256];
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+  if (row >= rows) return;   // wave-uniform
+  const int first = (threadIdx.x & 63) * VPL;
+  uint32_t w[VPL];
+  load_row_keys<VPL>(values + row * ld, n, first, w);
+  cand_select_row<VPL>(w, first, k, out + row * k, cand[wave], hist[wave]);
 }
 
 template <int VPL, bool FINITE>
@@ -1016,6 +1250,11 @@ int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_
   // rows of 1024 keys 181 -> 110 us; 64 rows of 2048 keys 6.7 -> 11.3 us).
   if (n <= 64 * kWaveMaxVPL && rows >= kWaveMinRows) {
     const unsigned wg4 = static_cast<unsigned>(cdiv(rows, 4));
+    if (FINITE && k <= 64 && n > 512) {   // candidate lists (prefill block maxima)
+      if (n <= 1024) topk_cand_wave_kernel<16><<<wg4, 256, 0, st>>>(values, rows, nn, ld, kk, out);
+      else topk_cand_wave_kernel<32><<<wg4, 256, 0, st>>>(values, rows, nn, ld, kk, out);
+      return check_launch("qkv_topk");
+    }
     if (n <= 256) topk_wave_kernel<4, FINITE><<<wg4, 256, 0, st>>>(values, rows, nn, ld, kk, out);
     else if (n <= 512) topk_wave_kernel<8, FINITE><<<wg4, 256, 0, st>>>(values, rows, nn, ld, kk, out);
     else if (n <= 1024) topk_wave_kernel<16, FINITE><<<wg4, 256, 0, st>>>(values, rows, nn, ld, kk, out);

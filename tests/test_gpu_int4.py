@@ -671,3 +671,35 @@ def test_step_for_reference_mode():
     with pytest.raises(RuntimeError, match="not a decode mode"):
         K.SparseDecodeStep.for_mode("qabs8cand3reuse", 1, 16, 8, 128, t, DEV)
     assert M.decode_plan(mode, t).tokens_kept == 256
+
+
+def _prefill_rows(n, seed):
+    """Rows for the prefill top-k's candidate lists (many rows of 513-1024
+    block maxima, k <= 64): i.i.d. rows plus one row of each case the
+    selection branches on."""
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randn((2048, n), generator=g)
+    j = torch.arange(n)
+    rows[0] = 2.5                                             # all equal: the list overflows, full-row path
+    rows[1] = -float("inf")                                   # nothing selectable
+    rows[2] = torch.where(j % 97 == 3, (j % 11).float(), -float("inf"))    # fewer than k finite keys
+    rows[3] = torch.where(j < 40 * 16, torch.randn(n, generator=g), -float("inf"))  # < 64 lanes hold keys
+    rows[4] = (j % 5).float()                                 # ties at the k-th key
+    rows[5] = -1.0 - ((j * 37) % 1000).float()                # negative keys
+    rows[6] = torch.where(j % 3 == 0, -0.0, torch.where(j % 3 == 1, 0.0, -1.0))   # -0 and +0 tie
+    rows[7] = ((j * 7919) % 300).float() * 0.25               # duplicated values across lanes
+    rows[8] = torch.where(j % 16 == 0, 1.0 + j.float(), -float("inf"))   # one key per lane
+    rows[9, n - 5:] = -float("inf")                           # a causal tail
+    rows[10] = torch.ldexp(torch.ones(n), torch.randint(-30, 30, (n,), generator=g))   # wide exponents
+    rows[11] = torch.randint(-3, 3, (n,), generator=g).float()   # 6 values: hundreds of candidates per bin
+    return rows
+
+
+@pytest.mark.parametrize("n", [1024, 1000, 600])
+@pytest.mark.parametrize("k", [64, 1, 17])
+def test_prefill_topk_candidate_lists(n, k):
+    # 2048 rows take the one-wave-per-row kernels; rows of 513-1024 keys with
+    # k <= 64 filter each row by its lane-maxima bound into a candidate list
+    vals = _prefill_rows(n, n * 7 + k)
+    got = P.block_topk(vals.to(DEV), k).cpu().numpy()
+    assert np.array_equal(got, O.prefill_block_topk(vals.numpy(), k))
