@@ -649,7 +649,8 @@ int qkv_block_rerank(const void* query, const void* key, const int64_t* k_stride
  * channels (row_stride elements apart), q8 = clamp(rint(q / (amax/127)),
  * +-127) per row, written as int8 [rows,128] in the permuted order the MFMA
  * scoring kernel consumes: channel c at byte 32*(c/32) + 16*((c/16)%2) +
- * 8*((c%16)/8) + 4*(c%2) + (c%8)/2.  qscale f32 [rows] optional. */
+ * 8*((c%16)/8) + 4*(c%2) + (c%8)/2 (q8 2-byte aligned).  qscale f32 [rows]
+ * optional. */
 int qkv_prefill_quantize_query(const void* query, int64_t rows, int64_t head_dim, int64_t row_stride,
                                int8_t* q8, float* qscale, void* stream);
 
