@@ -65,32 +65,101 @@ constexpr bool perm_inverts() {
 static_assert(perm_inverts(), "perm_channel inverts perm_slot");
 
 // ---------------------------------------------------------------------------
-// Query quantization: one wave per query row.  q8 = clamp(rint(q / (amax/127)),
-// +-127) over the row's 128 channels, written in the permuted MFMA order: lane
-// l loads the two channels of output slots 2l and 2l+1 and writes them as one
-// 2-byte store, so a row's 128 bytes leave in one coalesced store (two byte
-// stores a lane at scattered slots took 14.8 us for cfg5's 65536 rows).
+// Query quantization: q8 = clamp(rint(q / (amax/127)), +-127) over each row's
+// 128 channels, written in the permuted MFMA order.  A wave takes kQRows rows
+// and issues all their loads before the first row is quantized (one row per
+// wave ran 65536 waves in eight rounds of load latency: 15 us at cfg5); lane l
+// loads the two channels of output slots 2l and 2l+1 and writes them as one
+// 2-byte store, so a row's 128 bytes leave in one coalesced store.  The row
+// maximum of |q| is a DPP reduction on the bit patterns (exact for
+// non-negative floats).
 // ---------------------------------------------------------------------------
+constexpr int kQRows = 8;
+
 __global__ __launch_bounds__(256) void prefill_query_kernel(const uint16_t* __restrict__ q, int64_t q_row_stride,
                                                             int64_t rows, int8_t* __restrict__ q8,
                                                             float* __restrict__ qscale) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const uint16_t* qr = q + row * q_row_stride;
-  const float x0 = __uint_as_float(static_cast<uint32_t>(qr[perm_channel(2 * lane)]) << 16);
-  const float x1 = __uint_as_float(static_cast<uint32_t>(qr[perm_channel(2 * lane + 1)]) << 16);
-  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-  const float qs = amax / 127.0f;
-  auto quant = [&](float v) -> int {
-    if (qs == 0.0f) return 0;
-    const float t = __builtin_rintf(v / qs);
-    return static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f));
-  };
-  const uint32_t b0 = static_cast<uint8_t>(static_cast<int8_t>(quant(x0)));
-  const uint32_t b1 = static_cast<uint8_t>(static_cast<int8_t>(quant(x1)));
-  reinterpret_cast<uint16_t*>(q8 + row * kD)[lane] = static_cast<uint16_t>(b0 | (b1 << 8));
-  if (qscale && lane == 0) qscale[row] = qs;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kQRows;
+  if (row0 >= rows) return;   // wave-uniform
+  const int ca = perm_channel(2 * lane), cb = perm_channel(2 * lane + 1);
+  float x0[kQRows], x1[kQRows];
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r) {
+    const uint16_t* qr = q + min(row0 + r, rows - 1) * q_row_stride;
+    x0[r] = __uint_as_float(static_cast<uint32_t>(qr[ca]) << 16);
+    x1[r] = __uint_as_float(static_cast<uint32_t>(qr[cb]) << 16);
+  }
+#pragma unroll
+  for (int r = 0; r < kQRows; ++r) {
+    if (row0 + r >= rows) break;   // wave-uniform
+    const float qs = wave_max_nonneg(fmaxf(fabsf(x0[r]), fabsf(x1[r]))) / 127.0f;
+    auto quant = [&](float v) -> uint32_t {
+      if (qs == 0.0f) return 0u;
+      const float t = __builtin_rintf(v / qs);
+      return static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f))));
+    };
+    const int64_t row = row0 + r;
+    reinterpret_cast<uint16_t*>(q8 + row * kD)[lane] = static_cast<uint16_t>(quant(x0[r]) | (quant(x1[r]) << 8));
+    if (qscale && lane == 0) qscale[row] = qs;
+  }
+}
+
+// The same quantization for rows 16-byte aligned (row stride a multiple of 8
+// channels): channels 8m..8m+7 land in output bytes 8m..8m+7 (perm_slot keeps
+// each aligned group of 8, reordered inside it: channel 8m+e to byte 8m +
+// 4*(e%2) + e/2), so lane l of a 16-lane row group loads channels 8m..8m+7 (m
+// = l%16) of row l/16 in one 16-byte load and writes its 8 bytes in one
+// 8-byte store; a load instruction covers 4 rows, and the row maximum is a
+// DPP reduction within the row of 16 lanes.  kQVRows rows per wave.
+constexpr int kQVRows = 16;
+
+__global__ __launch_bounds__(256) void prefill_query_vec_kernel(const uint16_t* __restrict__ q,
+                                                                int64_t q_row_stride, int64_t rows,
+                                                                int8_t* __restrict__ q8,
+                                                                float* __restrict__ qscale) {
+  constexpr int kLoads = kQVRows / 4;
+  const int lane = threadIdx.x & 63, m = lane & 15;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kQVRows + (lane >> 4);
+  if (row0 - (lane >> 4) >= rows) return;   // wave-uniform
+  uint4 w[kLoads];
+#pragma unroll
+  for (int it = 0; it < kLoads; ++it)
+    w[it] = *reinterpret_cast<const uint4*>(q + min(row0 + 4 * it, rows - 1) * q_row_stride + 8 * m);
+#pragma unroll
+  for (int it = 0; it < kLoads; ++it) {
+    const int64_t row = row0 + 4 * it;
+    float x[8];
+    const uint32_t ws[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16lo(ws[e]);
+      x[2 * e + 1] = bf16hi(ws[e]);
+    }
+    float a = fabsf(x[0]);
+#pragma unroll
+    for (int e = 1; e < 8; ++e) a = fmaxf(a, fabsf(x[e]));
+    // max over the row's 16 lanes, on the bit patterns of non-negative floats
+    uint32_t v = __float_as_uint(a);
+    v = max(v, dpp_mov<0xB1>(v, v));
+    v = max(v, dpp_mov<0x4E>(v, v));
+    v = max(v, dpp_mov<0x141>(v, v));
+    v = max(v, dpp_mov<0x140>(v, v));
+    const float qs = __uint_as_float(v) / 127.0f;
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float t = qs == 0.0f ? 0.0f : __builtin_rintf(x[e] / qs);
+      b[e] = static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(fminf(fmaxf(t, -127.0f), 127.0f))));
+    }
+    if (row < rows) {
+      // byte 4*(e%2) + e/2 holds channel 8m + e
+      const uint2 o = make_uint2(b[0] | (b[2] << 8) | (b[4] << 16) | (b[6] << 24),
+                                 b[1] | (b[3] << 8) | (b[5] << 16) | (b[7] << 24));
+      *reinterpret_cast<uint2*>(q8 + row * kD + 8 * m) = o;
+      if (qscale && m == 0) qscale[row] = qs;
+    }
+  }
 }
 
 __device__ __forceinline__ v4i unpack_half(uint32_t w0, uint32_t w1) {
@@ -330,9 +399,14 @@ QKV_EXPORT int qkv_prefill_quantize_query(const void* query, int64_t rows, int64
   if (rows <= 0 || row_stride < head_dim || row_stride % 2 || !aligned(query, 4))
     return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: bad rows or row stride");
   if (!aligned(q8, 2)) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: q8 must be 2-byte aligned");
-  if (cdiv(rows, 4) > 0x7FFFFFFF) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: too many rows");
+  if (cdiv(rows, 4 * kQRows) > 0x7FFFFFFF) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: too many rows");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  prefill_query_kernel<<<static_cast<unsigned>(cdiv(rows, 4)), 256, 0, st>>>(
+  if (row_stride % 8 == 0 && aligned(query, 16) && aligned(q8, 8)) {
+    prefill_query_vec_kernel<<<static_cast<unsigned>(cdiv(rows, 4 * kQVRows)), 256, 0, st>>>(
+        static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
+    return check_launch("qkv_prefill_quantize_query");
+  }
+  prefill_query_kernel<<<static_cast<unsigned>(cdiv(rows, 4 * kQRows)), 256, 0, st>>>(
       static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
   return check_launch("qkv_prefill_quantize_query");
 }

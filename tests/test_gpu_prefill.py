@@ -30,6 +30,22 @@ def test_quantize_query_matches_oracle():
     assert np.array_equal(qs.cpu().numpy(), want_s)
 
 
+@pytest.mark.parametrize("width,offset", [(132, 0), (136, 2), (256, 64)])
+def test_quantize_query_strided_rows_match_oracle(width, offset):
+    # rows that are not 16-byte aligned (stride 132, or 4 bytes in) take the
+    # kernel that loads two channels a lane; stride 256 takes the 16-byte loads
+    g = torch.Generator().manual_seed(width + offset)
+    big = torch.randn((301, width), generator=g).to(torch.bfloat16)
+    big[7] = 0.0                                     # a zero row: scale 0, codes 0
+    q = big[:, offset:offset + 128]
+    qd = big.to(DEV)[:, offset:offset + 128]          # the strided view itself, on the device
+    assert qd.stride(0) == width
+    q8, qs = P.quantize_query(qd)
+    want, want_s = O.quantize_query_rows(q.float().numpy())
+    assert np.array_equal(q8.cpu().numpy(), O.permute_prefill_query(want))
+    assert np.array_equal(qs.cpu().numpy(), want_s)
+
+
 @pytest.mark.parametrize("b,hq,hkv,nq,t,q_pos0", [
     (1, 4, 2, 100, 1000, 900),     # partial query tile, partial last block, causal cut
     (1, 8, 2, 64, 2500, 0),        # most blocks invisible to the first queries
