@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void prefill_query_kernel(const uint16_t* __re
 // = l%16) of row l/16 in one 16-byte load and writes its 8 bytes in one
 // 8-byte store; a load instruction covers 4 rows, and the row maximum is a
 // DPP reduction within the row of 16 lanes.  kQVRows rows per wave.
-constexpr int kQVRows = 16;
+constexpr int kQVRows = 4;
 
 __global__ __launch_bounds__(256) void prefill_query_vec_kernel(const uint16_t* __restrict__ q,
                                                                 int64_t q_row_stride, int64_t rows,
