@@ -30,19 +30,10 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
 constexpr int kBlock = 64;          // keys per selection block
-#ifndef QKV_PF_NT
-#define QKV_PF_NT 6
-#endif
-#ifndef QKV_PF_CHUNK
-#define QKV_PF_CHUNK 32
-#endif
-#ifndef QKV_PF_WG_PER_CU
-#define QKV_PF_WG_PER_CU 2
-#endif
-constexpr int kNT = QKV_PF_NT;              // 16-query column tiles per wave
-constexpr int kQTile = 16 * kNT;            // queries per wave
-constexpr int kChunkBlocks = QKV_PF_CHUNK;  // blocks per workgroup key chunk
-static_assert(kNT % 2 == 0, "the block-end reduction pairs the query tiles");
+constexpr int kNT = 8;              // 16-query column tiles per wave
+constexpr int kQTile = 16 * kNT;    // queries per wave
+constexpr int kChunkBlocks = 16;    // blocks per workgroup key chunk
+static_assert(kNT % 4 == 0, "the block-end reduction takes four query tiles at a time");
 
 // Byte position, within a permuted query row, of channel c.
 __host__ __device__ constexpr int perm_slot(int c) {
@@ -172,39 +163,61 @@ __device__ __forceinline__ v4i unpack_half(uint32_t w0, uint32_t w1) {
 }
 
 // ---------------------------------------------------------------------------
-// Block scores.  Grid: x = key chunk (kChunkBlocks blocks), y = group of 4
-// (query tile, head) pairs of one KV head, z = (batch, KV head).  Each wave
-// owns one pair: kQTile query rows of one head, resident as B fragments, and
-// streams the chunk's blocks that its queries can see.  No workgroup barrier:
-// the 4 waves of a group read the same keys (the other waves' loads hit in
-// cache) and stage their block maxima in their own LDS region before a
-// coalesced write.
+// Block scores.  A workgroup holds W waves: W query heads of one KV head that
+// share one tile of kQTile query rows (W = 4 when the GQA group size G is a
+// multiple of 4, else 2 or 1), so all its waves see the same keys under the
+// same causal mask.  Grid: x = key chunk (kChunkBlocks blocks of 64 keys),
+// y = (query tile, group of W heads), z = (batch, KV head).
 //
-// Per block a wave loads the next block's codes and scales while it issues
-// the current block's 32 MFMAs back to back (the first half of every tile's
-// channels, then the second half, so dependent MFMAs are 4 apart) and then
-// runs the epilogue: 16*key = fp32(scale) * fp32(16*I) as one v_fma_f32 per
-// key on the biased int32 accumulator (below), maximum over the 16 keys a
-// lane holds with v_max3, then over the 4 row groups with VALU lane swaps,
-// times 1/16.  Only blocks on the causal diagonal or past the last token take the
-// masked epilogue (a wave-uniform branch).
+// Per 64-key block the workgroup stages the block once in LDS: wave w loads
+// the packed codes of key tiles w, w+W, .. (one coalesced kilobyte each) and
+// writes them unpacked (bytes holding 16*code, the MFMA A layout), and wave
+// 0 converts the block's 64 fp16 scales to fp32 s and -12582912*s.  Each wave
+// then issues per 16-key tile 16 MFMAs against its 128 resident query rows
+// and the epilogue: 16*key = fma(s, acc, -12582912*s) per accumulator (the
+// biased accumulator, below), maximum over the keys a lane holds with
+// v_max3, and at the block end over the 4 row groups with lane swaps.  The
+// LDS copy is double-buffered: block kb+1 is staged while block kb is
+// scored, one workgroup barrier per block.  Only blocks on the causal
+// diagonal or past the last token take the masked epilogue (uniform over
+// the workgroup).
+//
+// Every accumulator starts at the bit pattern of 1.5 * 2^23, so the int32
+// result 0x4B400000 + 16*I read as fp32 is exactly 12582912 + 16*I (|16*I| <
+// 2^22).  Then fma(s, f, -12582912 * s) = round(s * 16*I): one rounding of
+// the exact product, i.e. 16 times fp32(s) * fp32(I), with no integer
+// conversion (-12582912 * s is exact: s has 11 significant bits).  Block
+// maxima are taken on 16*key and scaled back by 1/16 (exact).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, QKV_PF_WG_PER_CU) void prefill_scores_kernel(
+// Issue order of one pipelined step: each MFMA followed by three vector
+// instructions (the previous tile's epilogue: 48 per tile), and nothing moved
+// across steps.
+__device__ __forceinline__ void interleave_step() {
+#pragma unroll
+  for (int i = 0; i < 2 * kNT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int W>
+__global__ __launch_bounds__(64 * W, 8 / W) void prefill_scores_kernel(
     const int8_t* __restrict__ q8, const uint8_t* __restrict__ kpacked, const uint16_t* __restrict__ kscales,
     int q_heads, int kv_heads, int nq, int tokens, int64_t capacity, int q_pos0, int nb,
     float* __restrict__ bmax) {
-  __shared__ float tile[4][kQTile][kChunkBlocks + 1];
-  // The wave index is uniform: read it into a scalar register, so that the
-  // query tile, the visible block count and the block offsets are scalar too.
+  static_assert(W == 1 || W == 2 || W == 4, "1, 2 or 4 waves per workgroup");
+  constexpr int kTiles = 4 / W;                       // key tiles a wave stages per block
+  __shared__ v4i abuf[2][4][2][64];                    // [slot][key tile][channel half][lane]
+  __shared__ float sbuf[2][4][4][8];                   // [slot][key tile][row group][s x4, -12582912*s x4]
+  __shared__ float tile[W][kQTile][kChunkBlocks + 1];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = q_heads / kv_heads;
-  const int n_qtiles = (nq + kQTile - 1) / kQTile;
-  const int combo = blockIdx.y * 4 + wave;
-  if (combo >= n_qtiles * G) return;
-  const int qt = combo / G, h = combo - qt * G;
+  const int hgroups = G / W;
+  const int qt = blockIdx.y / hgroups, hg = blockIdx.y - qt * hgroups;
   const int bj = blockIdx.z;                         // b * kv_heads + j
   const int b = bj / kv_heads, j = bj - b * kv_heads;
-  const int head = j * G + h;
+  const int head = j * G + hg * W + wave;
   const int64_t qrow0 = (static_cast<int64_t>(b) * q_heads + head) * nq;
   const int q0 = qt * kQTile;
   const int g = lane >> 4, col = lane & 15;
@@ -224,153 +237,189 @@ __global__ __launch_bounds__(256, QKV_PF_WG_PER_CU) void prefill_scores_kernel(
     }
   }
   const int qlast = min(nq, q0 + kQTile) - 1;
-  const int pos_lo = q_pos0 + q0, pos_hi = q_pos0 + qlast;   // positions of the wave's first/last query
+  const int pos_lo = q_pos0 + q0, pos_hi = q_pos0 + qlast;   // positions of the tile's first/last query
 
   const int blk0 = blockIdx.x * kChunkBlocks;
   const int nblk = min(kChunkBlocks, nb - blk0);
-  // Blocks [0, nvis) of the chunk hold a key some query of the wave sees.
+  // Blocks [0, nvis) of the chunk hold a key some query of the tile sees;
+  // blocks [0, nfull) need no mask: every key is at or before the first
+  // query's position and below `tokens`.
   const int nvis = pos_hi < blk0 * kBlock ? 0 : min(nblk, (pos_hi - blk0 * kBlock) / kBlock + 1);
+  const int lim_pos = pos_lo >= kBlock - 1 ? (pos_lo - (kBlock - 1)) / kBlock + 1 : 0;
+  const int nfull = max(0, min(min(lim_pos, tokens / kBlock) - blk0, nvis));
   const uint8_t* krow = kpacked + static_cast<int64_t>(bj) * capacity * (kD / 2);
   const uint16_t* srow = kscales + static_cast<int64_t>(bj) * capacity;
   const float ninf = -__builtin_huge_valf();
 
-  // Lane l loads key (base + 16kt + l%16), channels 32g..32g+31, and the
-  // scales of the 4 keys its output rows hold (base + 16kt + 4g + i).  Every
-  // block below nb lies inside the capacity (a multiple of 64).  Buffer
-  // loads over the chunk: a per-lane constant offset plus the block's scalar
-  // offset, so no per-load address arithmetic on the VALU.
+  // Buffer loads over the chunk (every block below nb lies inside the
+  // capacity, a multiple of 64): lane l of a key tile loads key l%16,
+  // channels 32g..32g+31; lane l of wave 0 loads the scale of key l.
   const int64_t key0 = static_cast<int64_t>(blk0) * kBlock;
   const auto krsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(krow + key0 * (kD / 2)), 0,
                                                        nblk * kBlock * (kD / 2), 0x00020000);
   const auto srsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(srow + key0), 0, nblk * kBlock * 2,
                                                        0x00020000);
-  const int kvoff = col * (kD / 2) + g * 16, svoff = 8 * g;
-  auto load_block = [&](int kb, uint4 (&ka)[4], uint2 (&ks)[4]) {
+  const int kvoff = col * (kD / 2) + g * 16;
+  uint4 raw[kTiles];
+  uint32_t sraw = 0;
+  auto gload = [&](int kb) {
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int r = 0; r < kTiles; ++r) {
+      const int kt = wave + W * r;
       const auto a = __builtin_amdgcn_raw_buffer_load_b128(krsrc, kvoff + kt * 16 * (kD / 2), kb * kBlock * (kD / 2), 0);
-      const auto s = __builtin_amdgcn_raw_buffer_load_b64(srsrc, svoff + kt * 32, kb * kBlock * 2, 0);
-      ka[kt] = uint4{a[0], a[1], a[2], a[3]};
-      ks[kt] = uint2{s[0], s[1]};
+      raw[r] = uint4{a[0], a[1], a[2], a[3]};
+    }
+    if (wave == 0) sraw = __builtin_amdgcn_raw_buffer_load_b16(srsrc, 2 * lane, kb * kBlock * 2, 0);
+  };
+  auto stage = [&](int slot) {
+#pragma unroll
+    for (int r = 0; r < kTiles; ++r) {
+      const int kt = wave + W * r;
+      abuf[slot][kt][0][lane] = unpack_half(raw[r].x, raw[r].y);
+      abuf[slot][kt][1][lane] = unpack_half(raw[r].z, raw[r].w);
+    }
+    if (wave == 0) {
+      const float s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sraw)));
+      float* e = &sbuf[slot][lane >> 4][(lane >> 2) & 3][lane & 3];
+      e[0] = s;
+      e[4] = __builtin_fmaf(s, -12582912.0f, 0.0f);
     }
   };
 
-  // One block: two halves of 2 key tiles each (16 MFMAs, then their
-  // epilogue), which keeps the accumulators at 32 registers.
-  //
-  // Every accumulator starts at the bit pattern of 1.5 * 2^23, so the int32
-  // result 0x4B400000 + 16*I read as fp32 is exactly 12582912 + 16*I (|16*I|
-  // < 2^22).  Then fma(s, f, -12582912 * s) = round(s * 16*I): one rounding
-  // of the exact product, i.e. 16 times fp32(s) * fp32(I), with no integer
-  // conversion (-12582912 * s is exact: s has 11 significant bits).
   const v4i kBias = v4i{0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
-  // MFMAs of one half block (key tiles 2h, 2h+1) into acc.
-  auto mfma_half = [&](int half, const uint4 (&ka)[4], v4i (&acc)[2][kNT]) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int kt = 2 * half + u;
-      const v4i a0 = unpack_half(ka[kt].x, ka[kt].y);
-      const v4i a1 = unpack_half(ka[kt].z, ka[kt].w);
-#pragma unroll
-      for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], kBias, 0, 0, 0);
-#pragma unroll
-      for (int n = 0; n < kNT; ++n) acc[u][n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc[u][n], 0, 0, 0);
-    }
+  // Fragments of key tile kt from LDS slot `slot`: the A operands of both
+  // channel halves, and s / -12582912*s of the 4 keys the lane's rows hold.
+  auto frag = [&](int slot, int kt, v4i& a0, v4i& a1, float4& s, float4& c) {
+    a0 = abuf[slot][kt][0][lane];
+    a1 = abuf[slot][kt][1][lane];
+    s = *reinterpret_cast<const float4*>(&sbuf[slot][kt][g][0]);
+    c = *reinterpret_cast<const float4*>(&sbuf[slot][kt][g][4]);
   };
-  // Epilogue of one half block: 16*key per accumulator, running block max.
-  auto epi_half = [&](int half, const uint2 (&ks)[4], const v4i (&acc)[2][kNT], bool masked, int base,
-                      float (&run)[kNT]) {
-    // The fp16 scales feed v_fma_mix_f32 straight from their packed words.
-    _Float16 sc[2][4];
-    float cb[2][4];
+  auto mfma_tile = [&](const v4i& a0, const v4i& a1, v4i (&acc)[kNT]) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint2 sr = ks[2 * half + u];
-      sc[u][0] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x & 0xFFFFu));
-      sc[u][1] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.x >> 16));
-      sc[u][2] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y & 0xFFFFu));
-      sc[u][3] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(sr.y >> 16));
+    for (int n = 0; n < kNT; ++n) acc[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bq[n][0], kBias, 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cb[u][i] = __builtin_fmaf(static_cast<float>(sc[u][i]), -12582912.0f, 0.0f);
-    }
-    auto key16 = [&](int u, int i, int a) -> float {
-      return __builtin_fmaf(static_cast<float>(sc[u][i]), __int_as_float(a), cb[u][i]);
-    };
-    if (!masked) {
+    for (int n = 0; n < kNT; ++n) acc[n] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bq[n][1], acc[n], 0, 0, 0);
+  };
+  float run[kNT];
+  // Unmasked epilogue of one key tile into the running block maxima (the
+  // block's first tile starts them).
+  auto epi = [&](const v4i (&acc)[kNT], const float4 s, const float4 c, bool first) {
 #pragma unroll
-      for (int n = 0; n < kNT; ++n) {
-        float m = run[n];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          m = fmaxf(fmaxf(m, key16(u, 0, acc[u][n].x)), key16(u, 1, acc[u][n].y));
-          m = fmaxf(fmaxf(m, key16(u, 2, acc[u][n].z)), key16(u, 3, acc[u][n].w));
-        }
-        run[n] = m;
-      }
-    } else {
-      // Key t of the lane's rows is visible to query q when t <= pos(q) and
-      // t < tokens; lim = min(pos(q), tokens - 1) - (first key of the row
-      // group) compares once per key.
-#pragma unroll
-      for (int n = 0; n < kNT; ++n) {
-        const int lim = min(q_pos0 + q0 + 16 * n + col, tokens - 1) - (base + 4 * g);
-        float m = run[n];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int accs[4] = {acc[u][n].x, acc[u][n].y, acc[u][n].z, acc[u][n].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float v = key16(u, i, accs[i]);
-            m = fmaxf(m, ((2 * half + u) * 16 + i <= lim) ? v : ninf);
-          }
-        }
-        run[n] = m;
+    for (int n = 0; n < kNT; ++n) {
+      const float k0 = __builtin_fmaf(s.x, __int_as_float(acc[n].x), c.x);
+      const float k1 = __builtin_fmaf(s.y, __int_as_float(acc[n].y), c.y);
+      const float k2 = __builtin_fmaf(s.z, __int_as_float(acc[n].z), c.z);
+      const float k3 = __builtin_fmaf(s.w, __int_as_float(acc[n].w), c.w);
+      if (first) {
+        run[n] = fmaxf(fmaxf(fmaxf(k0, k1), k2), k3);
+      } else {
+        run[n] = fmaxf(fmaxf(run[n], k0), k1);
+        run[n] = fmaxf(fmaxf(run[n], k2), k3);
       }
     }
-  };
-  auto process = [&](int kb, const uint4 (&ka)[4], const uint2 (&ks)[4]) {
-    const int base = (blk0 + kb) * kBlock;
-    const bool need_mask = base + kBlock - 1 > pos_lo || base + kBlock > tokens;
-    float run[kNT];
+    // Keep the epilogue in its step (next to the MFMAs it overlaps) rather
+    // than sunk to where the block maxima are consumed.
 #pragma unroll
-    for (int n = 0; n < kNT; ++n) run[n] = ninf;
-    v4i acc0[2][kNT], acc1[2][kNT];
-    mfma_half(0, ka, acc0);
-    if (!need_mask) {
-      mfma_half(1, ka, acc1);
-      epi_half(0, ks, acc0, false, base, run);
-      epi_half(1, ks, acc1, false, base, run);
-    } else {
-      mfma_half(1, ka, acc1);
-      epi_half(0, ks, acc0, true, base, run);
-      epi_half(1, ks, acc1, true, base, run);
+    for (int n = 0; n < kNT; ++n) pin(run[n]);
+  };
+  // Masked epilogue: key t of the lane's rows is visible to query q when t <=
+  // pos(q) and t < tokens; lim = min(pos(q), tokens - 1) - (first key of the
+  // row group) compares once per key.
+  auto epi_masked = [&](const v4i (&acc)[kNT], const float4 s, const float4 c, int kt, int base) {
+#pragma unroll
+    for (int n = 0; n < kNT; ++n) {
+      const int lim = min(q_pos0 + q0 + 16 * n + col, tokens - 1) - (base + 4 * g);
+      const float ks[4] = {__builtin_fmaf(s.x, __int_as_float(acc[n].x), c.x),
+                           __builtin_fmaf(s.y, __int_as_float(acc[n].y), c.y),
+                           __builtin_fmaf(s.z, __int_as_float(acc[n].z), c.z),
+                           __builtin_fmaf(s.w, __int_as_float(acc[n].w), c.w)};
+      float m = kt == 0 ? ninf : run[n];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, (kt * 16 + i <= lim) ? ks[i] : ninf);
+      run[n] = m;
     }
-    // Max over the 4 row groups, four (then two) tiles per round of lane
-    // swaps, after which row group g holds tile n0 + g; back to key scale
-    // (exact), where adding +0 turns a -0 into +0 and leaves every other
-    // value alone.
+  };
+  auto block_end = [&](int kb) {
 #pragma unroll
     for (int n0 = 0; n0 + 4 <= kNT; n0 += 4) {
       const float m = max_rows4(run[n0], run[n0 + 1], run[n0 + 2], run[n0 + 3]);
       tile[wave][16 * (n0 + g) + col][kb] = __builtin_fmaf(m, 0.0625f, 0.0f);
     }
-    if constexpr (kNT % 4 == 2) {
-      const float m = max_rows2(run[kNT - 2], run[kNT - 1]);
-      if (lane < 32) tile[wave][16 * (kNT - 2 + g) + col][kb] = __builtin_fmaf(m, 0.0625f, 0.0f);
+  };
+  // Stages block kb+1 (its codes were loaded one block earlier) and loads
+  // block kb+2.  Slot (kb+1) % 2 was last read for block kb-1, before the
+  // barrier that ended it.
+  auto stage_next = [&](int kb) {
+    if (kb + 1 < nvis) {
+      stage((kb + 1) & 1);
+      if (kb + 2 < nvis) gload(kb + 2);
     }
   };
 
-  // Two register buffers, the block loop unrolled by two; an odd count ends
-  // by processing its last block twice (same result, same LDS slot).
-  uint4 ka[2][4];
-  uint2 ks[2][4];
-  if (nvis > 0) load_block(0, ka[0], ks[0]);
-  for (int kb = 0; kb < nvis; kb += 2) {
-    const int k1 = min(kb + 1, nvis - 1), k2 = min(kb + 2, nvis - 1);
-    load_block(k1, ka[1], ks[1]);
-    process(kb, ka[0], ks[0]);
-    load_block(k2, ka[0], ks[0]);
-    process(k1, ka[1], ks[1]);
+  if (nvis > 0) {
+    gload(0);
+    stage(0);
+    if (nvis > 1) gload(1);
+    __syncthreads();
+  }
+  // Unmasked blocks [0, nfull), pipelined by key tile: the MFMAs of tile kt
+  // are issued ahead of the epilogue of tile kt-1 (the other accumulator
+  // set); the last tile's epilogue runs after the block's barrier, behind
+  // the next block's first MFMAs.
+  v4i acc0[kNT], acc1[kNT];
+  v4i a0, a1, n0, n1;
+  float4 s0, c0, s1, c1;
+  if (nfull > 0) {
+    frag(0, 0, a0, a1, s0, c0);
+    frag(0, 1, n0, n1, s1, c1);
+    mfma_tile(a0, a1, acc0);
+  }
+  for (int kb = 0; kb < nfull; ++kb) {
+    const int slot = kb & 1;
+    float4 s2, c2;
+    frag(slot, 2, a0, a1, s2, c2);          // prefetch tile 2
+    mfma_tile(n0, n1, acc1);                // tile 1
+    epi(acc0, s0, c0, true);                // tile 0
+    interleave_step();
+    frag(slot, 3, n0, n1, s0, c0);          // prefetch tile 3 (s0/c0 now tile 3's)
+    mfma_tile(a0, a1, acc0);                // tile 2
+    epi(acc1, s1, c1, false);               // tile 1
+    interleave_step();
+    mfma_tile(n0, n1, acc1);                // tile 3
+    epi(acc0, s2, c2, false);               // tile 2
+    interleave_step();
+    stage_next(kb);
+    __syncthreads();
+    if (kb + 1 < nfull) {
+      frag(slot ^ 1, 0, a0, a1, s2, c2);
+      frag(slot ^ 1, 1, n0, n1, s1, c1);
+      mfma_tile(a0, a1, acc0);              // next block's tile 0
+      epi(acc1, s0, c0, false);             // tile 3
+      interleave_step();
+      block_end(kb);
+      s0 = s2;
+      c0 = c2;
+    } else {
+      epi(acc1, s0, c0, false);
+      block_end(kb);
+    }
+  }
+  // Blocks [nfull, nvis) hold keys past some query of the tile (the causal
+  // diagonal) or past the last token: masked, one tile at a time.
+  for (int kb = nfull; kb < nvis; ++kb) {
+    const int slot = kb & 1, base = (blk0 + kb) * kBlock;
+    v4i a0, a1;
+    float4 s0, c0;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      frag(slot, kt, a0, a1, s0, c0);
+      mfma_tile(a0, a1, acc0);
+      epi_masked(acc0, s0, c0, kt, base);
+    }
+    block_end(kb);
+    stage_next(kb);
+    __syncthreads();
   }
   for (int kb = nvis; kb < nblk; ++kb) {
     if (lane < 16) {
@@ -428,15 +477,20 @@ QKV_EXPORT int qkv_prefill_block_scores(const int8_t* q8, int64_t batch, int64_t
     return fail(QKV_ERR_INVALID, "qkv_prefill_block_scores: q8 and packed K must be 16-byte aligned");
   const int64_t nb = cdiv(tokens, kBlock);
   const int64_t g = q_heads / kv_heads;
-  const int64_t groups = cdiv(cdiv(queries, kQTile) * g, 4);
-  if (batch * kv_heads > 65535 || groups > 65535 || cdiv(nb, kChunkBlocks) > 0x7FFFFFFF)
+  const int w = g % 4 == 0 ? 4 : (g % 2 == 0 ? 2 : 1);
+  const int64_t ytiles = cdiv(queries, kQTile) * (g / w);
+  if (batch * kv_heads > 65535 || ytiles > 65535 || cdiv(nb, kChunkBlocks) > 0x7FFFFFFF)
     return fail(QKV_ERR_INVALID, "qkv_prefill_block_scores: grid too large");
-  dim3 grid(static_cast<unsigned>(cdiv(nb, kChunkBlocks)), static_cast<unsigned>(groups),
+  dim3 grid(static_cast<unsigned>(cdiv(nb, kChunkBlocks)), static_cast<unsigned>(ytiles),
             static_cast<unsigned>(batch * kv_heads));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  prefill_scores_kernel<<<grid, 256, 0, st>>>(q8, packed, scales, static_cast<int>(q_heads),
-                                              static_cast<int>(kv_heads), static_cast<int>(queries),
-                                              static_cast<int>(tokens), capacity, static_cast<int>(q_pos0),
-                                              static_cast<int>(nb), bmax);
+  const int hq = static_cast<int>(q_heads), hkv = static_cast<int>(kv_heads), nq = static_cast<int>(queries);
+  const int t = static_cast<int>(tokens), p0 = static_cast<int>(q_pos0), nbi = static_cast<int>(nb);
+  if (w == 4)
+    prefill_scores_kernel<4><<<grid, 256, 0, st>>>(q8, packed, scales, hq, hkv, nq, t, capacity, p0, nbi, bmax);
+  else if (w == 2)
+    prefill_scores_kernel<2><<<grid, 128, 0, st>>>(q8, packed, scales, hq, hkv, nq, t, capacity, p0, nbi, bmax);
+  else
+    prefill_scores_kernel<1><<<grid, 64, 0, st>>>(q8, packed, scales, hq, hkv, nq, t, capacity, p0, nbi, bmax);
   return check_launch("qkv_prefill_block_scores");
 }

@@ -51,6 +51,8 @@ def test_quantize_query_strided_rows_match_oracle(width, offset):
     (1, 8, 2, 64, 2500, 0),        # most blocks invisible to the first queries
     (2, 4, 4, 130, 4096, 3966),    # G = 1, last chunk of the context
     (1, 16, 4, 200, 3000, 2800),   # G = 4
+    (1, 16, 2, 150, 3000, 2850),   # G = 8: two workgroups of 4 heads per query tile
+    (1, 6, 2, 300, 2000, 1700),    # G = 3: one head per workgroup, three query tiles
 ])
 def test_block_scores_match_oracle(b, hq, hkv, nq, t, q_pos0):
     q, k = _case(b, hq, hkv, nq, t, q_pos0, seed=nq + t)
