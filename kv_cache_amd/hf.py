@@ -35,6 +35,18 @@ raises instead of attending to the padding.  The channel subset is the one
 chosen when the int4 structures are built at the first decode step (the
 static per-KV-head subset of the int4 design); later tokens are quantized
 into it.
+
+The reference's other decode modes run through ``register_mode(mode,
+capacity)``: the candidate-reuse modes (``qabs{S}cand{pct}reuse…``), the
+lagged modes (``lagtop2`` / ``lagrefresh{N}`` / ``qdrift…`` / ``pconf{T}`` +
+``qabs{S}cand{pct}``), the exact candidate attention (``qabs{S}cand{pct}
+[append|r{N}]attn``) and the block selectors (``qbb…`` / ``brep…`` /
+``qboracle…``), each through its native decode step (``reuse.ReuseDecodeStep``,
+``reuse.LaggedReuseDecodeStep``, ``reuse.QabsCandidateAttentionStep``,
+``blocksel.BlockSelectDecodeStep``), one per attention layer, on any HF cache
+(K/V [B, Hkv, T, D] with the current token last).  As the reference's hook
+dispatches these modes only for one query per sequence (EV:6236, 6308,
+6414-6448), prefill stays dense SDPA.
 """
 
 from __future__ import annotations
@@ -151,7 +163,6 @@ class Int4CacheLayer:
                 "sel": torch.empty(batch * kv_heads * k, dtype=torch.int32, device=dev),
                 "topk_ws": K.topk_workspace(batch * kv_heads, nb, k, dev),
                 "attn_ws": K.attention_workspace(batch, q_heads, kv_heads, head_dim, n_ws, self.block, dev),
-                "out": torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=dev),
             }
         return self.bufs
 
@@ -213,11 +224,13 @@ def int4_sparse_attention_forward(module, query: torch.Tensor, key: torch.Tensor
     sel = bufs["sel"][: b * hkv * k].view(b, hkv, k)
     if nb <= K.SELECT_MAX_BLOCKS:
         out = K.sparse_attention_select(q, layer.keys, layer.values, bmax, k, layer.block, history, scaling,
-                                        workspace=bufs["attn_ws"], sel_out=sel, out=bufs["out"], **layer.protect)
+                                        workspace=bufs["attn_ws"], sel_out=sel, **layer.protect)
     else:
         K.block_topk(bmax, k, out=sel, workspace=bufs["topk_ws"])
         out = K.sparse_attention(q, layer.keys, layer.values, sel, layer.block, history, scaling,
-                                 workspace=bufs["attn_ws"], out=bufs["out"], **layer.protect)
+                                 workspace=bufs["attn_ws"], **layer.protect)
+    # a fresh output per call: callers may keep a step's attention output
+    # (hooks, captured activations) while later steps run
     return out[:, None].to(query.dtype), None
 
 
@@ -238,3 +251,67 @@ def register(name: str = "int4_sparse") -> str:
     # at all, padding included; SDPA's mask is the one its prefill path uses
     AttentionMaskInterface.register(name, sdpa_mask)
     return name
+
+
+def native_step_class(mode: str):
+    """The decode step that serves a reference mode string, or ValueError."""
+    from . import blocksel, reuse
+
+    if reuse.is_lagged_mode(mode):
+        return reuse.LaggedReuseDecodeStep
+    for parse, cls in ((reuse.parse_reuse_mode, reuse.ReuseDecodeStep),
+                       (reuse.parse_qabs_attn_mode, reuse.QabsCandidateAttentionStep),
+                       (blocksel.parse_block_mode, blocksel.BlockSelectDecodeStep)):
+        try:
+            parse(mode)
+        except (RuntimeError, ValueError):
+            continue
+        return cls
+    raise ValueError(f"{mode!r} is not a mode served by a native decode step")
+
+
+def register_mode(mode: str, capacity: int, *, name: str | None = None, **step_kwargs) -> str:
+    """Register an attention implementation (default name ``qkv_<mode>``) that
+    runs ``mode``'s native decode step for one query per sequence and dense
+    SDPA otherwise.  ``capacity`` bounds the cached tokens per sequence;
+    ``step_kwargs`` go to the step (``top_fraction``, ``protect_sink``,
+    ``protect_recent``, ``keep_self``, ``candidate_selection``, …, as the
+    reference's flags).  The steps, one per attention module, are in the
+    returned function's ``steps`` (``ATTENTION_STEPS[name]``); each starts a
+    new sequence by itself when the history does not continue its last call's
+    (EV:1651's query-token check)."""
+    from transformers import AttentionInterface
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+
+    cls = native_step_class(mode)
+    steps: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
+
+    def forward(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attention_mask,
+                scaling: float | None = None, dropout: float = 0.0, **kwargs):
+        if query.size(2) != 1:
+            return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout,
+                                          scaling=scaling, **kwargs)
+        if attention_mask is not None and not _all_visible(attention_mask, key.size(2)):
+            raise RuntimeError(f"{mode} decode does not support padded batches (the attention mask hides cached "
+                               "positions); decode such batches with dense attention")
+        b, hq, _, d = query.shape
+        hkv = key.size(1)
+        step = steps.get(module)
+        if step is None or (step.batch, step.q_heads, step.kv_heads, step.head_dim) != (b, hq, hkv, d):
+            step = cls(mode, b, hq, hkv, d, capacity, device=query.device, **step_kwargs)
+            steps[module] = step
+        scaling = d ** -0.5 if scaling is None else float(scaling)
+        out = step(query[:, :, 0, :], key, value, scaling)
+        # the step's output buffer is overwritten by its next call
+        return out[:, None].clone(), None
+
+    forward.steps = steps
+    name = name or f"qkv_{mode}"
+    AttentionInterface.register(name, forward)
+    AttentionMaskInterface.register(name, sdpa_mask)
+    ATTENTION_STEPS[name] = steps
+    return name
+
+
+ATTENTION_STEPS: dict = {}

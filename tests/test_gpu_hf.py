@@ -145,3 +145,121 @@ def test_padded_batch_is_refused_at_decode():
         with pytest.raises(RuntimeError, match="padded batches"):
             model(ids[:, :1], attention_mask=torch.cat([mask, mask[:, :1] * 0 + 1], dim=1), past_key_values=cache,
                   use_cache=True)
+
+
+def test_decode_output_survives_the_next_step():
+    # the attention output of one decode step is a tensor of its own: the
+    # next step does not overwrite it
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    hf.register()
+    model = _model(layers=1)
+    kept = []
+    fn = ALL_ATTENTION_FUNCTIONS["int4_sparse"]
+
+    def rec(module, query, key, value, attention_mask, **kw):
+        out, w = fn(module, query, key, value, attention_mask, **kw)
+        if query.size(2) == 1:
+            kept.append((out, out.clone()))
+        return out, w
+
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+
+    AttentionInterface.register("rec_int4_sparse", rec)
+    AttentionMaskInterface.register("rec_int4_sparse", sdpa_mask)
+    prompt = torch.randint(0, 512, (1, 200), generator=torch.Generator().manual_seed(6)).to(DEV)
+    _decode(model, "rec_int4_sparse", hf.Int4SparseCache(capacity=512, topk=4), prompt, 4)
+    assert len(kept) == 4
+    for out, copy in kept:
+        assert torch.equal(out, copy)
+
+
+NATIVE_MODES = [
+    ("qabs8cand5reuse", {"top_fraction": 0.05, "protect_sink": 4, "protect_recent": 8}),
+    ("qabs8cand5reusefinal", {"top_fraction": 0.05}),
+    ("qdriftheadqabs8cand5", {"top_fraction": 0.05}),
+    ("lagrefresh3qabs8cand5", {"top_fraction": 0.05}),
+    ("qabs8cand5attn", {"protect_sink": 4}),
+    ("qabs8cand10r2attn", {}),
+    ("qbb16q8s50cand10", {"top_fraction": 0.05}),
+    ("brep16r2q8s50cand10", {"top_fraction": 0.05}),
+    ("qboracle16q8s50cand10", {"top_fraction": 0.05}),
+]
+
+
+def _record(name):
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    fn = ALL_ATTENTION_FUNCTIONS[name]
+    calls = []
+
+    def rec(module, query, key, value, attention_mask, scaling=None, **kw):
+        out, w = fn(module, query, key, value, attention_mask, scaling=scaling, **kw)
+        if query.size(2) == 1:
+            calls.append((module, query.clone(), key.clone(), value.clone(), scaling, out.clone()))
+        return out, w
+
+    AttentionInterface.register("rec_" + name, rec)
+    AttentionMaskInterface.register("rec_" + name, sdpa_mask)
+    return "rec_" + name, calls
+
+
+@pytest.mark.parametrize("mode,kw", NATIVE_MODES, ids=[m for m, _ in NATIVE_MODES])
+def test_native_mode_decode_equals_its_step(mode, kw):
+    # the HF entry runs the mode's decode step per layer with the cache's K/V:
+    # a fresh step fed the recorded decode calls of one layer reproduces the
+    # outputs the model saw, step by step (the step's own state included)
+    from transformers.cache_utils import DynamicCache
+
+    name = hf.register_mode(mode, 512, **kw)
+    rec_name, calls = _record(name)
+    model = _model()
+    prompt = torch.randint(0, 512, (2, 220), generator=torch.Generator().manual_seed(7)).to(DEV)
+    logits = _decode(model, rec_name, DynamicCache(config=model.config), prompt, 5)
+    assert all(torch.isfinite(x).all() for x in logits)
+    assert len(calls) == 2 * 5
+    cls = hf.native_step_class(mode)
+    assert all(type(s) is cls for s in hf.ATTENTION_STEPS[name].values())
+    for layer_module in {c[0] for c in calls}:
+        seq = [c for c in calls if c[0] is layer_module]
+        b, hq, _, d = seq[0][1].shape
+        step = cls(mode, b, hq, seq[0][2].size(1), d, 512, device=DEV, **kw)
+        for _, q, k, v, scaling, out in seq:
+            got = step(q[:, :, 0, :], k, v, d ** -0.5 if scaling is None else scaling)
+            assert torch.equal(got[:, None], out)
+
+
+@pytest.mark.parametrize("mode,kw", [("qabs8cand100reuse", {"top_fraction": 1.0}), ("qabs8cand100attn", {}),
+                                     ("qbb16q8s100cand100", {"top_fraction": 1.0})],
+                         ids=["reuse", "attn", "qbb"])
+def test_native_mode_keeping_everything_matches_dense(mode, kw):
+    from transformers.cache_utils import DynamicCache
+
+    name = hf.register_mode(mode, 512, **kw)
+    model = _model()
+    prompt = torch.randint(0, 512, (1, 180), generator=torch.Generator().manual_seed(8)).to(DEV)
+    got = _decode(model, name, DynamicCache(config=model.config), prompt, 4)
+    want = _decode(model, "sdpa", DynamicCache(config=model.config), prompt, 4)
+    for g, w in zip(got, want):
+        torch.testing.assert_close(g, w, rtol=3e-2, atol=3e-2)
+
+
+def test_native_mode_generate_runs():
+    from transformers.cache_utils import DynamicCache
+
+    name = hf.register_mode("qabs8cand5reuse", 512, top_fraction=0.05)
+    model = _model()
+    model.config._attn_implementation = name
+    prompt = torch.randint(0, 512, (1, 150), generator=torch.Generator().manual_seed(9)).to(DEV)
+    with torch.no_grad():
+        out = model.generate(prompt, past_key_values=DynamicCache(config=model.config), max_new_tokens=6,
+                             do_sample=False)
+    assert out.shape == (1, 156)
+
+
+def test_register_mode_rejects_unknown_modes():
+    with pytest.raises(ValueError):
+        hf.register_mode("int4foo", 512)
