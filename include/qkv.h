@@ -205,7 +205,11 @@ int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
  * the row's last chunk to finish selects from those lists -- one launch when
  * rows * chunks <= 256 (every workgroup resident at once; the row's chunks
  * count in ticket words the library keeps per GPU, 4 MiB held until the
- * process ends), three otherwise.  Longer rows: stages
+ * process ends, in 4096 slots taken in turn: calls in flight together on one
+ * GPU collide only when 4096 other calls were made between them; a call made
+ * under stream capture keeps its slot for the graph's lifetime and the
+ * process's, so at most 4095 captured calls per GPU), three otherwise.
+ * Longer rows: stages
  * in which each chunk keeps its local
  * top-k until the candidates fit one chunk or one 1024-thread workgroup
  * (40960), keys below a lower bound of the row's k-th key left out after the

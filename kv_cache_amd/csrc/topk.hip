@@ -10,6 +10,7 @@
 // to theta, so the output is already in ascending index order.
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "common.h"
 #include "select.h"
@@ -1013,6 +1014,12 @@ __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restric
 
   // b. wait for the row's other chunks
   if (tid == 0) {
+    // The windows went out as coherent (sc1) stores and have completed
+    // (s_waitcnt above) before the ticket; the compiler-only fences keep the
+    // compiler from moving memory operations across the ticket and the wait.
+    // Release/acquire orderings here would add a whole-L2 write-back and
+    // invalidate per workgroup (2.7 us at 8 rows x 32 chunks).
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     int ok = 1;
@@ -1023,6 +1030,7 @@ __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restric
         break;
       }
     }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     flag_sh = ok;
   }
   __syncthreads();
@@ -1126,7 +1134,11 @@ __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restric
 
   // d. the row's last chunk selects from the lists
   if (tid == 0) {
+    // the lists, coherent stores completed above, stay before this ticket
+    // and the last chunk's list reads after it (compiler-only fences)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const uint32_t a = __hip_atomic_fetch_add(tk + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const bool last = a == static_cast<uint32_t>(n_chunks - 1);
     if (last) {   // every chunk of the row has left its wait
       __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1280,6 +1292,9 @@ int launch_rows(const float* values, int64_t rows, int64_t n, int64_t ld, int64_
 // current.  Calls take its slots in turn, so calls in flight together on one
 // GPU (on different streams) count in different words unless kTicketSlots
 // calls were issued between them; every completed call leaves its words zero.
+// A call made while its stream is being captured into a graph keeps its slot
+// for every replay of that graph, so such a slot is reserved: no later call is
+// given it (at most kTicketSlots - 1 captured calls per GPU and process).
 static __device__ __align__(256) uint32_t topk_tickets[qkv::kTicketSlots * qkv::kTicketSlotWords];
 
 namespace qkv {
@@ -1289,9 +1304,11 @@ constexpr int kTicketDevices = 64;
 std::mutex g_ticket_mu;
 uint32_t* g_ticket_pool[kTicketDevices];
 std::atomic<uint32_t> g_ticket_next[kTicketDevices];
+std::vector<bool> g_ticket_reserved[kTicketDevices];   // slots held by captured graphs (under g_ticket_mu)
+uint32_t g_ticket_n_reserved[kTicketDevices];
 
 // This call's ticket words on the current device.
-int ticket_slot(uint32_t** out) {
+int ticket_slot(hipStream_t stream, uint32_t** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kTicketDevices)
     return fail(QKV_ERR_LAUNCH, "qkv_topk_ws: no current device below %d", kTicketDevices);
@@ -1308,7 +1325,26 @@ int ticket_slot(uint32_t** out) {
     }
     pool = g_ticket_pool[dev];
   }
-  const uint32_t slot = g_ticket_next[dev].fetch_add(1u, std::memory_order_relaxed) % kTicketSlots;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess)
+    return fail(QKV_ERR_LAUNCH, "qkv_topk_ws: hipStreamIsCapturing failed");
+  const bool captured = cap == hipStreamCaptureStatusActive;
+  uint32_t slot = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_ticket_mu);
+    std::vector<bool>& reserved = g_ticket_reserved[dev];
+    if (reserved.empty()) reserved.assign(kTicketSlots, false);
+    if (g_ticket_n_reserved[dev] + 1 >= static_cast<uint32_t>(kTicketSlots))
+      return fail(QKV_ERR_UNSUPPORTED, "qkv_topk_ws: %d graph-captured calls hold every ticket slot of device %d",
+                  kTicketSlots - 1, dev);
+    do {
+      slot = g_ticket_next[dev].fetch_add(1u, std::memory_order_relaxed) % kTicketSlots;
+    } while (reserved[slot]);
+    if (captured) {
+      reserved[slot] = true;
+      ++g_ticket_n_reserved[dev];
+    }
+  }
   *out = pool + static_cast<int64_t>(slot) * kTicketSlotWords;
   return QKV_OK;
 }
@@ -1384,7 +1420,7 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
     dim3 grid(static_cast<unsigned>(n_bounds), static_cast<unsigned>(rows));
     if (rows * n_bounds <= kFusedMaxWGs) {
       uint32_t* tickets = nullptr;
-      if (int rc = ticket_slot(&tickets)) return rc;
+      if (int rc = ticket_slot(st, &tickets)) return rc;
       topk_fused_kernel<<<grid, 1024, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds,
                                                static_cast<uint64_t>(g_spin_ticks), tickets, win, lval, lidx,
                                                lcnt, out);
