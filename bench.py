@@ -757,7 +757,7 @@ def run_reuse(args) -> dict:
         for layer in range(layers):
             RU.reuse_partial_scores(qs[layer], steps[layer].kdm, hist_fixed, s_dims, out=steps[layer].partial)
 
-    n_s = steps[0].col_counts[hist_fixed] if selection == "sample_quantile" else 0
+    n_s = steps[0].columns.count(hist_fixed) if selection == "sample_quantile" else 0
     mask_name, mask_bytes = "threshold_mask", rows * hist_fixed * (4 + 1)
 
     def run_mask():
@@ -772,7 +772,7 @@ def run_reuse(args) -> dict:
             for layer in range(layers):
                 st = steps[layer]
                 RU.candidate_mask(st.partial, hist_fixed, "sample_quantile", k_s, st.cand[0], st.thresholds,
-                                  mask_ws[layer], st.col_table[hist_fixed], n_s)
+                                  mask_ws[layer], st.columns.row(hist_fixed), n_s)
     elif selection == "previous_threshold":   # the row's threshold, then the mask pass
         mask_name, mask_bytes = "previous_threshold_mask", rows * 4 + rows * hist_fixed * (4 + 1)
 

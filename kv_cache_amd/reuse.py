@@ -78,36 +78,46 @@ def sample_columns(history: int, sample_size: int) -> torch.Tensor | None:
     return cols.to(torch.int32)
 
 
-_COLUMN_TABLES: dict = {}
+class SampleColumnTable:
+    """``sample_columns`` on the device, one row per history below
+    ``capacity``: int32 [capacity, sample_size], row h padded with its last
+    column, so a decode step reads its row in place (no per-token host copy
+    inside a captured step).  A row is computed (by the same torch call as
+    ``sample_columns``) and copied to the device on the first use of its
+    history, so that use must not be inside a graph capture; the table belongs
+    to the step that made it."""
 
+    def __init__(self, capacity: int, sample_size: int, device):
+        self.capacity = int(capacity)
+        self.size = max(1, int(sample_size))
+        self.rows = torch.empty((self.capacity, self.size), dtype=torch.int32, device=device)
+        self._counts: dict[int, int] = {}
 
-def sample_column_table(capacity: int, sample_size: int, device) -> tuple[torch.Tensor, list[int]]:
-    """``sample_columns`` for every history below ``capacity``, built once on
-    the host by the same torch call and kept on the device: int32
-    [capacity, sample_size] (row h padded with its last column) and the host
-    list of each row's column count (0 where the sample covers the row).  A
-    decode step then reads its row in place instead of copying the columns
-    from the host every token, so the step can be captured in a graph.
-    Shared by every step of the same sizes and device."""
-    dev = torch.device(device)
-    key = (int(capacity), int(sample_size), dev)
-    hit = _COLUMN_TABLES.get(key)
-    if hit is not None:
-        return hit
-    size = max(1, int(sample_size))
-    host = torch.zeros((int(capacity), size), dtype=torch.int32)
-    counts = [0] * int(capacity)
-    for h in range(1, int(capacity)):
-        cols = sample_columns(h, size)
-        if cols is None:
-            continue
-        n = cols.numel()
-        host[h, :n] = cols
-        host[h, n:] = cols[-1]
-        counts[h] = n
-    table = (host.to(dev), counts)
-    _COLUMN_TABLES[key] = table
-    return table
+    @property
+    def max_count(self) -> int:
+        """Largest column count of any row (0 when every row's sample covers it)."""
+        return self.size if self.capacity - 1 > self.size else 0
+
+    def count(self, history: int) -> int:
+        """Columns of ``history``'s sample (0 when the sample covers the row)."""
+        h = int(history)
+        n = self._counts.get(h)
+        if n is None:
+            _require(0 <= h < self.capacity, f"history {h} outside the table (capacity {self.capacity})")
+            cols = sample_columns(h, self.size) if h else None
+            n = 0 if cols is None else cols.numel()
+            if n:
+                host = torch.empty(self.size, dtype=torch.int32)
+                host[:n] = cols
+                host[n:] = cols[-1]
+                self.rows[h].copy_(host)
+            self._counts[h] = n
+        return n
+
+    def row(self, history: int) -> torch.Tensor:
+        """``history``'s row on the device (filled on first use)."""
+        self.count(history)
+        return self.rows[int(history)]
 
 
 def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: torch.Tensor,
@@ -285,8 +295,8 @@ class ReuseDecodeStep:
         # the last step's candidate threshold per row (EV:1744-1745), written by the
         # previous_threshold and sample_quantile selections
         self.thresholds = torch.zeros(rows, dtype=torch.float32, device=device)
-        self.col_table, self.col_counts = (sample_column_table(cap, self.sample_size, device)
-                                           if self.selection == "sample_quantile" else (None, None))
+        self.columns = (SampleColumnTable(cap, self.sample_size, device)
+                        if self.selection == "sample_quantile" else None)
         hist_max = cap - 1
         # every term of the counts grows with the history
         self.n_out_max = max(self._final_count(hist_max), int(lib.qkv_reuse_final_count(
@@ -296,7 +306,7 @@ class ReuseDecodeStep:
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
         self.mask_ws = self._ws(lib.qkv_threshold_mask_workspace_bytes(rows, hist_max, budget_count(hist_max,
                                                                                                     self.cand_fraction)))
-        n_s_max = max(self.col_counts) if self.col_counts else 0
+        n_s_max = self.columns.max_count if self.columns is not None else 0
         if n_s_max:   # sized once for the largest sample, so a captured step never reallocates
             self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
                 rows, hist_max, CANDIDATE_SELECTIONS["sample_quantile"], budget_count(n_s_max, self.cand_fraction),
@@ -386,7 +396,7 @@ class ReuseDecodeStep:
         q = query.contiguous()
         reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
-        n_s = self.col_counts[history] if self.selection == "sample_quantile" else 0
+        n_s = self.columns.count(history) if self.selection == "sample_quantile" else 0
         if self.selection == "previous_threshold" and previous_thresholds:   # EV:3967-3971
             candidate_mask(self.partial, history, "previous_threshold", requested, current, self.thresholds,
                            self.mask_ws)
@@ -395,7 +405,7 @@ class ReuseDecodeStep:
             self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
                 self.rows, history, CANDIDATE_SELECTIONS["sample_quantile"], k_s, n_s))
             candidate_mask(self.partial, history, "sample_quantile", k_s, current, self.thresholds, self.mask_ws,
-                           self.col_table[history], n_s)
+                           self.columns.row(history), n_s)
         else:                                                                 # EV:3988
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))

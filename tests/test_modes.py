@@ -107,20 +107,29 @@ def test_sample_columns_host():
 
 def test_sample_column_table_rows_are_the_host_columns():
     # the device table a sample_quantile step reads: row h is sample_columns(h)
-    # padded with its last column, count 0 where the sample covers the row
+    # padded with its last column, count 0 where the sample covers the row;
+    # rows are filled on first use only
+    import time
+
     from kv_cache_amd import reuse as RU
 
-    table, counts = RU.sample_column_table(300, 40, "cpu")
-    assert table.shape == (300, 40) and table.dtype == torch.int32
-    assert RU.sample_column_table(300, 40, "cpu")[0] is table   # built once per sizes and device
+    t0 = time.perf_counter()
+    big = RU.SampleColumnTable(131072, 256, "cpu")
+    assert time.perf_counter() - t0 < 1.0 and big.max_count == 256
+    assert big.count(131071) == 256 and torch.equal(big.row(131071), RU.sample_columns(131071, 256))
+    table = RU.SampleColumnTable(300, 40, "cpu")
+    assert table.rows.shape == (300, 40) and table.rows.dtype == torch.int32 and table.max_count == 40
     for h in range(300):
         cols = RU.sample_columns(h, 40) if h else None
+        n = table.count(h)
         if cols is None:
-            assert counts[h] == 0
+            assert n == 0
             continue
-        n = counts[h]
-        assert n == cols.numel() and torch.equal(table[h, :n], cols)
-        assert bool((table[h, n:] == cols[-1]).all())
+        row = table.row(h)
+        assert n == cols.numel() and torch.equal(row[:n], cols)
+        assert bool((row[n:] == cols[-1]).all())
+    with pytest.raises(RuntimeError):
+        table.count(300)
 
 
 @pytest.mark.parametrize("mode,want", [
