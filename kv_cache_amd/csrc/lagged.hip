@@ -122,8 +122,8 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
 // QKV_LAG_ESS (EV:4068-4087): softmax weights of q over the tokens of the
 // previous final mask (full-D dot rounded to the input dtype, times scaling
 // rounded again, as the reference's matmul and multiply in that dtype leave
-// them), ESS = (sum e)^2 / sum e^2 with e = exp(s - max), flagged when
-// ESS / count > the threshold or the mask is empty.  A row's positions are
+// them), e = exp(s - max), ESS = 1 / max(sum (e / sum e)^2, 1e-12), flagged
+// when ESS / max(count, 1) > the threshold (always, for an empty mask).  A row's positions are
 // cut into `splits` spans of `span` positions, one workgroup each (the first
 // also records the row's top-|q| dims); a pass gathers the set positions of
 // kLagPass mask bytes in LDS and spreads their dot products over the
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
       rr = Elem<DT>::store(sc);
       sc = Elem<DT>::load(&rr);
       const float m = fmaxf(m_t, sc);
-      const float a = __expf(m_t - m), ex = __expf(sc - m);
+      const float a = expf(m_t - m), ex = expf(sc - m);
       z_t = z_t * a + ex;
       z2_t = z2_t * a * a + ex * ex;
       m_t = m;
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
   __syncthreads();
   float mx = red_s[0][0];
   for (int w = 1; w < kLagWaves; ++w) mx = fmaxf(mx, red_s[0][w]);
-  const float f = m_t == -INFINITY ? 0.f : __expf(m_t - mx);
+  const float f = m_t == -INFINITY ? 0.f : expf(m_t - mx);
   const float z = wave_sum(z_t * f), z2 = wave_sum(z2_t * f * f);
   if (lane == 0) {
     red_s[1][wave] = z;
@@ -271,11 +271,15 @@ __global__ __launch_bounds__(kLagNT) void lag_ess_merge_kernel(const float4* __r
   for (int i = 0; i < splits; ++i) {
     const float4 v = pr[i];
     if (v.x == -INFINITY) continue;   // an empty span
-    const float f = __expf(v.x - mx);
+    const float f = expf(v.x - mx);
     z += v.y * f;
     z2 += v.z * f * f;
   }
-  flags[row] = total == 0 || (z * z / z2) / static_cast<float>(total) > ess_threshold ? 1 : 0;
+  // the reference's expression: sum w^2 over the normalised weights w = e / z,
+  // ESS = 1 / max(sum w^2, 1e-12), over max(count, 1) (EV:4079-4083)
+  const float sum_w2 = total == 0 ? 0.f : z2 / (z * z);
+  const float frac = (1.0f / fmaxf(sum_w2, 1.0e-12f)) / static_cast<float>(max(total, 1));
+  flags[row] = frac > ess_threshold ? 1 : 0;
 }
 
 // 16 mask bytes at p, bytes at or past `n` read as 0.

@@ -548,28 +548,31 @@ def previous_final_ess_fraction(query, key, previous_final, scaling: float, bf16
     of q over the tokens of the previous final mask (full-D dot * scaling;
     with ``bf16_scores`` the dot and the scaled score rounded to bf16, as a
     bf16 matmul and multiply leave them), the effective sample size
-    1 / max(sum w^2, 1e-12), divided by max(count, 1).  A row with no token
-    has all weights 0, hence 1e12.  query [B,H,D]; key [B,H,>=hist,D];
-    previous_final bool [B,H,hist].  Returns float64 [B,H]."""
+    1 / max(sum w^2, 1e-12), divided by max(count, 1), every step in float32
+    as the reference's fp32 softmax and the ops after it (EV:4079-4083).  A
+    row with no token has all weights 0, hence 1e12.  query [B,H,D]; key
+    [B,H,>=hist,D]; previous_final bool [B,H,hist].  Returns float32 [B,H]."""
     q = np.asarray(query, dtype=np.float32)
     k = np.asarray(key, dtype=np.float32)
     m = np.asarray(previous_final, dtype=bool)
     b, h, _ = q.shape
-    out = np.empty((b, h), dtype=np.float64)
+    out = np.empty((b, h), dtype=np.float32)
+    f32 = np.float32
     for bi in range(b):
         for hi in range(h):
             pos = np.flatnonzero(m[bi, hi])
             if pos.size == 0:
-                out[bi, hi] = 1e12
+                out[bi, hi] = f32(1.0) / f32(1e-12)
                 continue
             sc = (k[bi, hi, pos].astype(np.float64) @ q[bi, hi].astype(np.float64)).astype(np.float32)
             if bf16_scores:
-                sc = _bf16_round(_bf16_round(sc) * np.float32(scaling))
+                sc = _bf16_round(_bf16_round(sc) * f32(scaling))
             else:
-                sc = sc * np.float32(scaling)
-            w = np.exp(sc.astype(np.float64) - sc.max())
-            w /= w.sum()
-            out[bi, hi] = 1.0 / max(float((w * w).sum()), 1e-12) / pos.size
+                sc = sc * f32(scaling)
+            e = np.exp(sc - sc.max(), dtype=np.float32)
+            w = e / e.sum(dtype=np.float32)
+            sw2 = (w * w).sum(dtype=np.float32)
+            out[bi, hi] = (f32(1.0) / max(sw2, f32(1e-12))) / f32(pos.size)
     return out
 
 

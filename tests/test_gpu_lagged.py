@@ -123,6 +123,34 @@ def test_lag_flags_ess_matches_oracle(dtype, rows, hkv, hist, dens):
         assert got[1] == 1   # an empty previous selection refreshes
 
 
+def test_lag_flags_known_answers_at_the_thresholds():
+    # pconf: ESS / count exactly 0.5 (weights 1, 0) and exactly 1.0 (four equal
+    # weights) are not above thresholds 0.5 and 1.0 and are above just smaller
+    # ones; qdrift cos: cosine exactly 0.5 is not below 0.5, a smaller one is
+    q = torch.zeros((1, 2, 128), dtype=torch.bfloat16)
+    q[..., 0] = 1.0
+    k = torch.zeros((1, 2, 5, 128), dtype=torch.bfloat16)
+    k[0, 0, 1, 0] = -2000.0          # score -177: its weight underflows to 0
+    mask = torch.zeros((2, 16), dtype=torch.uint8)
+    mask[0, :2] = 1
+    mask[1, :4] = 1
+    dims = torch.empty((2, 8), dtype=torch.int32, device=DEV)
+    vals = torch.empty((2, 8), dtype=torch.float32, device=DEV)
+    for thr, want in ((0.5, [0, 1]), (0.49999997, [1, 1]), (1.0, [0, 0]), (0.99999994, [0, 1])):
+        flags = torch.full((2,), 7, dtype=torch.uint8, device=DEV)
+        RU.lag_flags(q.to(DEV), 2, "ess", 8, dims, vals, flags, key=k.to(DEV), history=4,
+                     previous_final=mask.to(DEV), scaling=128 ** -0.5, ess_threshold=thr)
+        assert flags.cpu().tolist() == want, thr
+    qc = torch.zeros((1, 2, 128), dtype=torch.bfloat16, device=DEV)
+    qc[..., 0] = 1.0                 # top-4 |q| dims 0, 1, 2, 3
+    pd = torch.tensor([[0, 1, 2, 3], [0, 1, 2, 3]], dtype=torch.int32, device=DEV)
+    pv = torch.tensor([[1, 1, 1, 1], [1, 1, 1, 1.01]], dtype=torch.float32, device=DEV)
+    flags = torch.full((2,), 7, dtype=torch.uint8, device=DEV)
+    RU.lag_flags(qc, 2, "cos", 4, dims[:, :4].contiguous(), vals[:, :4].contiguous(), flags, previous_dims=pd,
+                 previous_values=pv)
+    assert flags.cpu().tolist() == [0, 1]
+
+
 @pytest.mark.parametrize("s_count", [1, 4, 8, 16, 33, 128])
 def test_lag_flags_overlap_and_cos_match_oracle(s_count):
     gen = torch.Generator().manual_seed(s_count)

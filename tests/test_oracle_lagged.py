@@ -111,6 +111,40 @@ def test_ess_fraction_known_answers():
     assert R.previous_final_ess_fraction(q, k, m, 1.0)[0, 0] == pytest.approx(1 / (p * p + (1 - p) ** 2) / 2)
 
 
+def test_ess_fraction_at_the_pconf_threshold():
+    # fractions exactly at a threshold (pconf flags only above it, EV:4085), in
+    # the reference's float32: weights (1, 0) give exactly 0.5; four equal
+    # weights exactly 1.0; three equal weights 1/3 each, whose squares sum to
+    # 0.33333337 in float32, 0.99999994 (float64 would give 1.0000000000000002)
+    q = np.zeros((1, 3, 128), np.float32)
+    q[..., 0] = 1.0
+    k = np.zeros((1, 3, 5, 128), np.float32)
+    k[0, 0, 1, 0] = -2000.0          # score -177: exp underflows to 0
+    m = np.zeros((1, 3, 4), bool)
+    m[0, 0, :2] = True
+    m[0, 1, :4] = True
+    m[0, 2, :3] = True
+    fr = R.previous_final_ess_fraction(q, k, m, 128 ** -0.5, bf16_scores=True)[0]
+    assert fr.dtype == np.float32
+    assert fr[0] == np.float32(0.5) and fr[1] == np.float32(1.0)
+    assert fr[2] == np.float32(1.0) - np.float32(2.0 ** -24)
+    assert (fr > np.float32(0.5)).tolist() == [False, True, True]
+    assert (fr > np.float32(1.0)).tolist() == [False, False, False]
+
+
+def test_drift_cosine_at_the_threshold():
+    # q on the previous dims (1, 0, 0, 0) against previous values (1, 1, 1, 1):
+    # cosine exactly 0.5, not flagged (the test is cos < 0.5, EV:4056); a
+    # slightly larger last value takes it below 0.5
+    q = np.zeros((1, 2, 16), np.float32)
+    q[0, :, 0] = 1.0                 # top-4 |q| dims: 0 then the zeros 1, 2, 3 (lowest index first)
+    k = np.zeros((1, 2, 20, 16), np.float32)
+    prev = {"final": np.ones((1, 2, 18), bool), "dims": np.array([[[0, 1, 2, 3], [0, 1, 2, 3]]]),
+            "values": np.array([[[1, 1, 1, 1], [1, 1, 1, 1.01]]], np.float32)}
+    *_, flagged = R.lagged_reuse_decode_step(q, k, k, "qdriftcoshead", None, 4, 0.1, 0.1, 0, 0, True, 0.25, prev)
+    assert flagged.tolist() == [[False, True]]
+
+
 def test_drift_flags_known_answers():
     # S = 4 dims: a head whose top dims keep 2 of 4 is not flagged (2 >= ceil(4/2)),
     # one keeping 1 is; the cosine test flags a head whose q on the previous
