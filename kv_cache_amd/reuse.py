@@ -389,11 +389,18 @@ class ReuseDecodeStep:
         step left (else it selects as ``topk``).  Touches no Python state but
         ``n_out``; the dim-major copy must already hold the history.  Output
         in ``self.out``; the step's thresholds in ``self.thresholds``."""
-        lib = _lib.load()
         key_count = key.size(2)
         history = key_count - 1
         _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
         q = query.contiguous()
+        self._candidates(q, history, current, previous_thresholds)
+        self._select_attend(q, key, value, scaling, current, previous, previous_final)
+
+    def _candidates(self, q: torch.Tensor, history: int, current: torch.Tensor, previous_thresholds: bool) -> None:
+        """Every row's partial scores and its candidate mask under the step's
+        selection (EV:3958-3989, 4116-4145) into ``current``; the thresholds
+        into ``self.thresholds`` where a later step reads them."""
+        lib = _lib.load()
         reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
         n_s = self.columns.count(history) if self.selection == "sample_quantile" else 0
@@ -412,7 +419,6 @@ class ReuseDecodeStep:
             # the threshold is kept only where a later step reads it
             candidate_mask(self.partial, history, "topk", requested, current,
                            self.thresholds if self.selection != "topk" else None, self.mask_ws)
-        self._select_attend(q, key, value, scaling, current, previous, previous_final)
 
     def _select_attend(self, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
                        current: torch.Tensor, previous: torch.Tensor | None,
@@ -569,24 +575,32 @@ def lag_union(current: torch.Tensor, previous_final: torch.Tensor | None, flags:
 class LaggedReuseDecodeStep(ReuseDecodeStep):
     """The lagged reuse modes' decode step (``lagtop2qabs8cand5``,
     ``lagrefresh4qabs8cand5``, ``qdriftheadqabs8cand5``, ``pconf50qabs8cand5``
-    ...; ``_qabs_reuse_fast_attention_forward`` EV:4020-4198 with the default
-    ``topk`` candidate selection).  Per step: the refresh test on the GPU
-    (``lag_flags``, also recording the top-|q| dims for the next step), the
-    partial scores and candidate threshold of every row unless no row can
-    refresh, the union with the previous final selection (``lag_union``: the
-    rows that do not refresh keep no candidates; the step-wide any / majority
-    decisions are taken on the GPU, so a step needs no host round trip and
-    can be captured), then the rerank, final selection and attention of the
-    reuse step.  Same call convention and state views as ``ReuseDecodeStep``."""
+    ...; ``_qabs_reuse_fast_attention_forward`` EV:4020-4198).  Per step: the
+    refresh test on the GPU (``lag_flags``, also recording the top-|q| dims for
+    the next step), the partial scores and candidate threshold of every row
+    unless no row can refresh, the union with the previous final selection
+    (``lag_union``: the rows that do not refresh keep no candidates), then the
+    rerank, final selection and attention of the reuse step.  Same call
+    convention and state views as ``ReuseDecodeStep``.
+
+    ``candidate_selection`` (``--qabs_candidate_selection``) applies where
+    every row thresholds its scores -- a sequence's first step, a
+    ``lagrefresh`` step, a step-wide ``qdrift`` / ``qdriftmaj`` / ``qdriftcos``
+    refresh -- as in the reference (EV:4116-4145); per-row refreshes threshold
+    by ``topk`` (EV:4089-4106), and ``previous_threshold`` reads thresholds only
+    from a step that thresholded every row (EV:1686-1694, 1744-1745).  With
+    ``topk`` the step-wide any / majority decisions are taken on the GPU, so a
+    step needs no host round trip and can be captured; with the other
+    selections those two kinds read the decision on the host."""
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
-                 keep_self: bool = True, candidate_selection: str = "topk", device: torch.device | str = "cuda"):
-        _require(candidate_selection == "topk",
-                 "the lagged reuse modes are built for the topk candidate selection only")
+                 keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
+                 device: torch.device | str = "cuda"):
         super().__init__(mode, batch, q_heads, kv_heads, head_dim, capacity, top_fraction=top_fraction,
                          protect_sink=protect_sink, protect_recent=protect_recent, keep_self=keep_self,
-                         candidate_selection="topk", device=device)
+                         candidate_selection=candidate_selection, threshold_sample_size=threshold_sample_size,
+                         device=device)
         s = min(max(1, self.dims), head_dim)
         _require(head_dim <= 128, "the lagged reuse modes take head_dim <= 128")
         # rows that keep skip the partial scores; past 40960 positions the staged
@@ -599,6 +613,10 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
         # the ESS test's per-span sums: at most rows * ceil(1024 / rows) spans
         self.ess_ws = torch.empty(self.rows * -(-1024 // self.rows) * 4 if self.kind == "pconf" else 1,
                                   dtype=torch.float32, device=device)
+
+    def reset(self) -> None:
+        super().reset()
+        self.thr_valid = False   # the last step thresholded every row (its thresholds are current)
 
     def _parse_mode(self, mode: str) -> tuple[int, float, bool, bool, int | None]:
         self.kind, self.param, dims, frac = parse_lagged_mode(mode)
@@ -637,12 +655,24 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
                       previous_final=previous_final if run == "ess" else None, scaling=scaling,
                       ess_threshold=float(self.param) if self.kind == "pconf" else 0.0,
                       workspace=self.ess_ws if run == "ess" else None)
-        if refresh != "none":   # the rows that refresh score and threshold (EV:3988-3989, 4089-4106)
+        if self.selection != "topk" and refresh in ("any", "majority"):
+            # the step-wide decision decides whether every row thresholds under
+            # the selection (EV:4116-4145) or none takes candidates: read on
+            # the host here (one byte per row); with topk it stays on the GPU
+            n_flagged = int(self.flags[: self.rows].sum())
+            refresh = "all" if (n_flagged > 0 if refresh == "any" else 2 * n_flagged > self.rows) else "none"
+        every_row = refresh == "all"
+        if every_row and self.selection != "topk":
+            # every row thresholds under the selection; previous thresholds only
+            # from a step that did the same (EV:1686-1694, 1744-1745)
+            self._candidates(q, history, current, previous_thresholds and self.thr_valid)
+        elif refresh != "none":   # the rows that refresh score and threshold (EV:3988-3989, 4089-4106)
             requested = budget_count(history, self.cand_fraction)
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
             lag_candidates(q, self.kdm, history, self.dims, requested, self.flags, refresh, self.partial, current,
                            self.mask_ws)
+        self.thr_valid = every_row
         lag_union(current, previous_final, self.flags, self.batch, self.q_heads, history, refresh,
                   self.kind == "qdriftshare" and has_prev, self.sink, self.recent, self.union)
         self._select_attend(q, key, value, scaling, self.union, None, None)

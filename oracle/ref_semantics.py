@@ -578,16 +578,21 @@ def previous_final_ess_fraction(query, key, previous_final, scaling: float, bf16
 
 def lagged_reuse_decode_step(query, key, value, kind: str, param, dim_count: int, candidate_fraction: float,
                              top_fraction: float, sink: int, recent: int, keep_self: bool, scaling: float,
-                             previous=None, bf16_scores: bool = False):
+                             previous=None, bf16_scores: bool = False, *, selection: str = "topk",
+                             sample_size: int = 256):
     """One decode step of the lagged reuse modes (``lagtop2``, ``lagrefresh{N}``,
     ``qdrift[maj|head|share|cos|coshead]`` and ``pconf{T}`` before
-    ``qabs{S}cand{pct}``), ``_qabs_reuse_fast_attention_forward`` EV:4020-4198
-    with the default ``topk`` candidate selection, then the rerank of EV:4257-4365.
+    ``qabs{S}cand{pct}``), ``_qabs_reuse_fast_attention_forward`` EV:4020-4198,
+    then the rerank of EV:4257-4365.  The candidate ``selection`` (``topk``,
+    ``sample_quantile``, ``previous_threshold``; ``candidate_mask``) applies
+    where every head thresholds its partial scores (EV:4116-4145); the per-head
+    refresh scores flagged heads by ``topk`` (EV:4089-4106).
 
     ``param`` is N for lagrefresh and T (a fraction) for pconf.  ``previous``
     is None or the previous step's state: dict(final=bool [B,Hq,>= hist-1],
-    dims=int [B,Hq,S], values=float [B,Hq,S]) (EV:1645-1694, present only when
-    the previous step was query token - 1).
+    dims=int [B,Hq,S], values=float [B,Hq,S], and thresholds [B,Hq,1] when
+    that step thresholded every head) (EV:1645-1694, 1733-1745, present only
+    when the previous step was query token - 1).
 
     * refresh test: lagrefresh refreshes when history % N == 0 (EV:4024); the
       qdrift kinds flag a head whose current top-S dims share fewer than
@@ -644,6 +649,7 @@ def lagged_reuse_decode_step(query, key, value, kind: str, param, dim_count: int
             flagged = previous_final_ess_fraction(q, kx, prev_final, scaling, bf16_scores) > float(param)
             refresh = bool(flagged.any())
     requested = budget_count(history, candidate_fraction)
+    thr = None
     if kind in _PER_HEAD_KINDS and prev_final is not None and flagged is not None:
         partial = partial_scores(q, kx[:, :, :history], dim_count)
         current = threshold_mask(partial, requested) & flagged[..., None]
@@ -654,7 +660,9 @@ def lagged_reuse_decode_step(query, key, value, kind: str, param, dim_count: int
         current = np.zeros((b, hq, history), dtype=bool)
         union = prev_final.copy()
     else:
-        current = threshold_mask(partial_scores(q, kx[:, :, :history], dim_count), requested)
+        prev_thr = previous.get("thresholds") if previous is not None else None
+        current, thr, _ = candidate_mask(partial_scores(q, kx[:, :, :history], dim_count), requested,
+                                         candidate_fraction, selection, prev_thr, sample_size)
         union = current | prev_final if prev_final is not None else current.copy()
     if sink > 0:
         union[..., : min(sink, history)] = True
@@ -662,7 +670,10 @@ def lagged_reuse_decode_step(query, key, value, kind: str, param, dim_count: int
         union[..., max(0, history - recent):] = True
     fi, fv, hist_final = reuse_select(q, kx, union, None, None, sink, recent, top_fraction, keep_self, scaling)
     out = final_attention(q, kx, vx, fi, fv, scaling)
-    return out, current, hist_final, {"final": hist_final, "dims": dims, "values": values}, flagged
+    state = {"final": hist_final, "dims": dims, "values": values}
+    if thr is not None:   # recorded only by a step that thresholded every head (EV:1744-1745)
+        state["thresholds"] = thr
+    return out, current, hist_final, state, flagged
 
 
 def qabs_reuse_step_cpu(query_states, key_states, value_states, dim_count: int, candidate_fraction: float,

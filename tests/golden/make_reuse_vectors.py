@@ -95,6 +95,19 @@ LAG_SCENARIOS = {
     "pconf50_s8c5_bf16": ("pconf50qabs8cand5", torch.bfloat16, 8, 2, 260, 5, 0.04, 4, 4, True, 5349),
     "pconf37p5_s16c10_fp32": ("pconf37p5qabs16cand10", torch.float32, 8, 4, 230, 4, 0.03, 2, 3, True, 50),
     "qdrifthead_s8c5_fp32": ("qdriftheadqabs8cand5", torch.float32, 8, 2, 260, 4, 0.04, 2, 6, True, 51),
+    # the other candidate selections on the lagged modes: they apply where every
+    # head thresholds (a first step, a step-wide refresh, lagrefresh; EV:4116-4145)
+    # + (selection, threshold sample size)
+    "qdrift_sample64_s8c5_bf16": ("qdriftqabs8cand5", torch.bfloat16, 8, 2, 600, 5, 0.04, 4, 4, True, 3273,
+                                  "sample_quantile", 64),
+    "qdrifthead_sample64_s8c5_bf16": ("qdriftheadqabs8cand5", torch.bfloat16, 8, 2, 600, 5, 0.04, 2, 6, True, 3085,
+                                      "sample_quantile", 64),
+    "lagrefresh1_prevthr_s8c5_bf16": ("lagrefresh1qabs8cand5", torch.bfloat16, 4, 2, 300, 5, 0.05, 2, 3, True, 402,
+                                      "previous_threshold", 256),
+    "qdriftmaj_prevthr_s8c5_bf16": ("qdriftmajqabs8cand5", torch.bfloat16, 8, 2, 400, 5, 0.04, 4, 4, True, 803,
+                                    "previous_threshold", 256),
+    "qdriftcos_prevthr_s8c5_bf16": ("qdriftcosqabs8cand5", torch.bfloat16, 8, 2, 400, 5, 0.04, 4, 4, True, 803,
+                                    "previous_threshold", 256),
 }
 
 

@@ -31,13 +31,20 @@ def test_lagged_step_matches_reference_vectors(name):
     k = torch.from_numpy(g["k"]).to(torch.bfloat16).to(DEV)
     v = torch.from_numpy(g["v"]).to(torch.bfloat16).to(DEV)
     step = RU.LaggedReuseDecodeStep(g["mode"], 1, hq, hkv, 128, 1024, top_fraction=g["top_fraction"],
-                                    protect_sink=g["sink"], protect_recent=g["recent"], keep_self=g["keep_self"])
+                                    protect_sink=g["sink"], protect_recent=g["recent"], keep_self=g["keep_self"],
+                                    candidate_selection=g["selection"], threshold_sample_size=g["sample_size"])
     for s in range(g["steps"]):
         n = g["t0"] + s + 1
         q = torch.from_numpy(g["q"][s]).to(torch.bfloat16).to(DEV)
         out = step(q, k[:, :, :n], v[:, :, :n], g["scaling"])
         assert np.array_equal(step.candidate_mask().cpu().numpy(), g["candidate"][s][..., : n - 1]), s
         assert np.array_equal(step.final_mask().cpu().numpy(), g["final"][s][..., : n - 1]), s
+        want_thr = g["thresholds"][s].reshape(-1)
+        if g["selection"] != "topk":
+            # the step keeps thresholds only after thresholding every row
+            assert step.thr_valid == bool(np.isfinite(want_thr).all()), s
+            if step.thr_valid:   # the partial sums' order sets the last bit (QK:91-94 vs the CPU fallback)
+                np.testing.assert_allclose(step.thresholds.cpu().numpy(), want_thr, rtol=1e-6, atol=0)
         if RU.LAGGED_KINDS[g["kind"]][0] is not None:
             dims = step.qdims[1 - step.flip].view(1, hq, -1).cpu().numpy()
             assert np.array_equal(np.sort(dims, axis=-1), np.sort(g["qdims"][s], axis=-1)), s
@@ -233,8 +240,8 @@ def test_lag_entry_points_reject_bad_arguments():
         RU.lag_union(m, None, fl, 1, 4, 65, "all", False, 0, 0, m.clone())
     with pytest.raises(RuntimeError, match="not a lagged reuse mode"):
         RU.LaggedReuseDecodeStep("qabs8cand5reuse", 1, 4, 2, 128, 256)
-    with pytest.raises(RuntimeError, match="topk candidate selection only"):
-        RU.LaggedReuseDecodeStep("pconf50qabs8cand5", 1, 4, 2, 128, 256, candidate_selection="sample_quantile")
+    with pytest.raises(RuntimeError, match="unknown candidate selection"):
+        RU.LaggedReuseDecodeStep("pconf50qabs8cand5", 1, 4, 2, 128, 256, candidate_selection="median")
 
 
 @pytest.mark.parametrize("mode", ["pconf50qabs8cand5", "qdriftmajqabs8cand5", "lagrefresh2qabs8cand5"])

@@ -16,7 +16,10 @@ from oracle import ref_semantics as R
 GOLDEN = Path(__file__).resolve().parent / "golden"
 LAG_SCENARIOS = ["lagtop2_s8c5_bf16", "lagrefresh3_s8c5_bf16", "qdrift_s8c5_bf16", "qdriftmaj_s8c5_bf16",
                  "qdrifthead_s8c5_bf16", "qdriftshare_s8c5_bf16", "qdriftcos_s16c10_bf16",
-                 "qdriftcoshead_s8c5_bf16", "pconf50_s8c5_bf16", "pconf37p5_s16c10_fp32", "qdrifthead_s8c5_fp32"]
+                 "qdriftcoshead_s8c5_bf16", "pconf50_s8c5_bf16", "pconf37p5_s16c10_fp32", "qdrifthead_s8c5_fp32",
+                 # the sample_quantile / previous_threshold candidate selections
+                 "qdrift_sample64_s8c5_bf16", "qdrifthead_sample64_s8c5_bf16", "lagrefresh1_prevthr_s8c5_bf16",
+                 "qdriftmaj_prevthr_s8c5_bf16", "qdriftcos_prevthr_s8c5_bf16"]
 _MODE = re.compile(r"(lagtop2|lagrefresh(\d+)|qdrift(?:maj|head|share|cos|coshead)?|pconf(\d+(?:p\d+)?))"
                    r"qabs(\d+)cand(\d+(?:p\d+)?)")
 
@@ -46,6 +49,7 @@ def load_lagged(name):
         "candidate": np.unpackbits(z["candidate"], axis=-1)[..., :t_max].astype(bool),
         "final": np.unpackbits(z["final"], axis=-1)[..., :t_max].astype(bool),
         "qdims": z["qdim_indices"], "qvals": z["qdim_values"], "refresh_count": z["refresh_head_count"],
+        "selection": str(z["selection"]), "sample_size": int(z["sample_size"]), "thresholds": z["thresholds"],
     }
 
 
@@ -65,8 +69,17 @@ def test_lagged_steps_match_reference_vectors(name):
             assert np.abs(ess - g["param"]).min() > 1e-3, (s, ess)
         out, cur, hf, prev, flagged = R.lagged_reuse_decode_step(
             g["q"][s], g["k"][:, :, :n], g["v"][:, :, :n], g["kind"], g["param"], g["dims"], g["cand"],
-            g["top_fraction"], g["sink"], g["recent"], g["keep_self"], g["scaling"], prev, bf16)
+            g["top_fraction"], g["sink"], g["recent"], g["keep_self"], g["scaling"], prev, bf16,
+            selection=g["selection"], sample_size=g["sample_size"])
         assert np.array_equal(cur, g["candidate"][s][..., :hist]), (s, "candidate")
+        # thresholds are recorded exactly by the steps that thresholded every
+        # head; their last bit follows the order of the S-term partial sums,
+        # which the reference's CPU fallback takes in torch's vector order and
+        # the oracle in the CUDA kernel's sequential one (QK:91-94)
+        want_thr = g["thresholds"][s]
+        assert ("thresholds" in prev) == bool(np.isfinite(want_thr).all()), (s, "thresholds recorded")
+        if "thresholds" in prev:
+            np.testing.assert_allclose(prev["thresholds"].reshape(want_thr.shape), want_thr, rtol=1e-6, atol=0)
         assert np.array_equal(hf, g["final"][s][..., :hist]), (s, "final")
         assert np.array_equal(np.sort(prev["dims"], axis=-1), np.sort(g["qdims"][s], axis=-1)), (s, "dims")
         order = np.argsort(g["qdims"][s], axis=-1)
