@@ -951,6 +951,45 @@ def cpu_baseline_qabs_attn(mode: str, budget_s: float) -> dict:
     }
 
 
+def time_dropin_calls(args, step, q, k, v, hist: int, dims: int, n_out: int, scaling: float, reps: int) -> dict:
+    """The two reference-signature calls the reference's timed qabs{S}cand{pct}attn
+    mode makes (qabs_cuda_kernels.partial_scores_dim_major, QK:659-665, and
+    final_attention, QK:694-705) on one layer of the same workload, with their
+    inputs as the reference builds them: K/V and the dim-major copy expanded to
+    the query heads (EV:6248-6251), int64 top-|q| dims and the step's final
+    index list."""
+    import torch
+
+    from kv_cache_amd import qabs_cuda_kernels as Q
+
+    b, hq, d = q.shape
+    g = hq // k.size(1)
+    kdm = step.kdm[..., :hist].repeat_interleave(g, dim=1).contiguous()        # [B, Hq, D, hist]
+    kx = k[:, :, : hist + 1].repeat_interleave(g, dim=1).contiguous()          # [B, Hq, T, D]
+    vx = v[:, :, : hist + 1].repeat_interleave(g, dim=1).contiguous()
+    dim_idx = torch.topk(q.float().abs(), k=dims, dim=-1).indices                # int64 [B, Hq, S]
+    rows = b * hq
+    idx = step.final_idx[: rows * n_out].view(b, hq, n_out)
+    valid = step.final_valid[: rows * n_out].view(b, hq, n_out)
+    out = {}
+    plan = [("dropin_partial_scores_dim_major", lambda: Q.partial_scores_dim_major(q, kdm, dim_idx),
+             rows * hist * (dims * 2 + 4)),
+            ("dropin_final_attention", lambda: Q.final_attention(q, kx, vx, idx, valid, scaling),
+             rows * n_out * (d * 2 * 2 + 9))]
+    for name, fn, nbytes in plan:
+        def run():
+            for _ in range(reps):
+                fn()
+        gk = graph_of(run)
+        ms = time_replays(gk.replay, args.kernel_reps) / reps
+        out[name] = {"us_per_launch": ms * 1e3, "bytes_per_launch": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                     "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {out[name]['gbs']:.0f} GB/s")
+        del gk
+    del kdm, kx, vx
+    return out
+
+
 def run_qabs_attn(args) -> dict:
     """Decode steps of the exact qabs{S}cand{pct}[append]attn mode
     (kv_cache_amd.reuse.QabsCandidateAttentionStep) on the REUSE shape: eager
@@ -1074,6 +1113,7 @@ def run_qabs_attn(args) -> dict:
                          "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         log(f"[bench] {name}: {ms * 1e3:.2f} us/launch, {kernels[name]['gbs']:.0f} GB/s")
         del gk
+    kernels.update(time_dropin_calls(args, steps[0], qs[0], ks[0], vs[0], hf, dims, n_out, scaling, reps))
     for _ in range(args.profile_steps):
         run_fixed()
     torch.cuda.synchronize()
@@ -1084,7 +1124,7 @@ def run_qabs_attn(args) -> dict:
         log("[bench] cpu baseline ...")
         cpu = cpu_baseline_qabs_attn(mode, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu['value']:.3e} keys/s on {cpu['cores']} cores")
-    dom = max(kernels, key=lambda n: kernels[n]["us_per_launch"])
+    dom = max((n for n in kernels if not n.startswith("dropin_")), key=lambda n: kernels[n]["us_per_launch"])
     keys_per_layer = b * hkv * hf
     return {
         "metric": "candidate attention decode: keys/s (history tokens x KV heads) through the exact "

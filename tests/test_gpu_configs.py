@@ -3,12 +3,13 @@
 Every (sequence, KV head) row is independent through packing, channel
 choice, scoring, pooling, top-k and attention, so the GPU runs each
 configuration's whole layer while the CPU oracle recomputes a sample of
-full-length rows from the same bf16 K/V and q (bit-exact packing, channel
+full-length rows (all 8 at config 4, 8 of 64 at config 2) from the same bf16 K/V and q (bit-exact packing, channel
 ids, slab, block maxima and top-k; attention within 1e-2 relative / 2e-2
 absolute of fp64).  On every row, the GPU's top-k is checked against a
 stable sort of the GPU's own block maxima, which is exact at any size.
-Config 4 also reports the recall of its planted key at k = 64, 256 and
-1024 tokens, which must equal the oracle's.  Config 3 runs at its full
+Config 4 also checks its top-k at k = 64, 256 and 1024 tokens against the
+oracle's block maxima on every row and the recall of its planted key at each
+k.  Config 3 runs at its full
 batch of 32 (256 rows of 32768 keys, one layer), so the step launches the
 same kernels on the same grids as the benchmark: the fused selection +
 attention with 32 chunks per wave on 2 x 256 workgroups."""
@@ -54,6 +55,7 @@ def _decode_case(name: str, batch: int | None = None, n_rows: int = 3):
     assert np.array_equal(sel, O.topk_lowest_index(bmax, cfg.topk))
 
     g = cfg.g
+    oracle_bmax = {}
     for r in _sample_rows(rows, n_rows, seed=rows):
         bi, j = divmod(r, cfg.kv_heads)
         kr = k[bi, j].float().cpu().numpy()[None]                     # [1, T, D]
@@ -68,13 +70,14 @@ def _decode_case(name: str, batch: int | None = None, n_rows: int = 3):
         qr = q[bi : bi + 1, j * g : (j + 1) * g].float().cpu().numpy()   # the row's G query heads
         _, _, want_bmax, want_sel = O.decode_select(qr, slab, sbits, chan, 1, cfg.block, cfg.topk)
         assert np.array_equal(bmax[r], want_bmax[0]), f"row {r}: block maxima differ"
+        oracle_bmax[r] = want_bmax[0]
         assert np.array_equal(sel[r], want_sel[0]), f"row {r}: top-k differs"
         want_out = O.sparse_attention(qr, k[bi : bi + 1, j : j + 1].float().cpu().numpy(),
                                       v[bi : bi + 1, j : j + 1].float().cpu().numpy(), want_sel[None],
                                       cfg.block, cfg.tokens, cfg.scaling)
         got_out = out[bi, j * g : (j + 1) * g].float().cpu().numpy()
         np.testing.assert_allclose(got_out, want_out[0], rtol=RTOL, atol=ATOL)
-    return cfg, step, planted
+    return cfg, step, planted, oracle_bmax
 
 
 def test_config1_full():
@@ -82,7 +85,7 @@ def test_config1_full():
 
 
 def test_config2_full_layer():
-    _decode_case("cfg2", n_rows=3)
+    _decode_case("cfg2", n_rows=8)
 
 
 def test_config3_full_batch():
@@ -90,18 +93,25 @@ def test_config3_full_batch():
 
 
 def test_config4_planted_recall():
-    cfg, step, planted = _decode_case("cfg4", n_rows=2)
+    # every one of the 8 rows against the oracle (packing, channels, slab,
+    # block maxima, top-1024 and attention), then the top-k at 64 and 256
+    # tokens against the oracle's block maxima and the recall of each
+    cfg, step, planted, oracle_bmax = _decode_case("cfg4", n_rows=8)
     rows = cfg.rows
-    bmax = step.bmax.cpu().numpy().reshape(rows, -1)
+    assert sorted(oracle_bmax) == list(range(rows))
+    want_bmax = np.stack([oracle_bmax[r] for r in range(rows)])
     pl = planted.cpu().numpy().reshape(rows)
     recalls = {}
     for kk in (64, 256, 1024):
         sel = K.block_topk(step.bmax, kk).cpu().numpy().reshape(rows, -1)
-        assert np.array_equal(sel, O.topk_lowest_index(bmax, kk))
+        want = O.topk_lowest_index(want_bmax, kk)
+        assert np.array_equal(sel, want), kk
         recalls[kk] = O.recall_at(O.expand_blocks(sel, cfg.block, cfg.tokens), pl)
+        assert recalls[kk] == O.recall_at(O.expand_blocks(want, cfg.block, cfg.tokens), pl)
     print(f"cfg4 planted-key recall: {recalls}")
-    # planted keys are built with cosine 0.9 to the group's mean query: they rank first by far
-    assert recalls[1024] == 1.0
+    # planted keys are built with cosine 0.9 to the group's mean query: at
+    # layer 0 every one ranks inside the top 64 tokens of its row
+    assert recalls == {64: 1.0, 256: 1.0, 1024: 1.0}
 
 
 def test_config5_sampled_rows():
