@@ -1284,7 +1284,7 @@ def run_blocksel(args) -> dict:
             _lib.check(lib.qkv_block_scores(st.kind, qs[layer].data_ptr(), k.data_ptr(), _lib.strides(*k.stride()),
                                             st.meta.data_ptr(), st.meta_blocks, b, hq, hkv, hf, d, st.block,
                                             st.reps, st.dims, st.bscore.data_ptr(), st.meta_blocks,
-                                            _lib.stream_of(k)))
+                                            st.dtype_code, _lib.stream_of(k)))
 
     def run_topk():
         for layer in range(layers):
@@ -1301,7 +1301,7 @@ def run_blocksel(args) -> dict:
                                                  _lib.strides(*k.stride()), b, hq, hkv, hf, d,
                                                  st.blocks.data_ptr(), n_scan, st.block, st.dims, scaling,
                                                  st.partial.data_ptr(), st.full.data_ptr(), n_tok,
-                                                 _lib.stream_of(qs[layer])))
+                                                 st.dtype_code, _lib.stream_of(qs[layer])))
 
     def run_rerank():
         for layer in range(layers):
@@ -1311,7 +1311,7 @@ def run_blocksel(args) -> dict:
                                             st.blocks.data_ptr(), n_scan,
                                             st.block, n_cand, n_keep, c["sink"], c["recent"], 1, scaling,
                                             st.keep.data_ptr(), st.capacity, st.attn_ids.data_ptr(), n_out,
-                                            _lib.stream_of(k)))
+                                            st.dtype_code, _lib.stream_of(k)))
 
     def run_attn():
         for layer in range(layers):

@@ -56,7 +56,7 @@ extern "C" {
 #define QKV_REFRESH_ANY 3      /* every row when any flag is set                 */
 #define QKV_REFRESH_MAJORITY 4 /* every row when more than half the flags are    */
 
-#define QKV_ABI_VERSION 1
+#define QKV_ABI_VERSION 2
 
 /* ABI version of the loaded library (QKV_ABI_VERSION it was built with). */
 int qkv_abi_version(void);
@@ -111,7 +111,9 @@ int qkv_final_attention(const void* query, const void* key, const void* value,
 
 /* ======================================================================
  * int4 family (no reference counterpart: the reference scores fp32 over
- * GQA-expanded bf16 K).  K/V/q are bf16.  A "row" r = b * Hkv + j is one
+ * GQA-expanded bf16 K).  K/V/q are bf16 or fp16, named by the last
+ * argument before the stream (QKV_DTYPE_BF16 / QKV_DTYPE_FP16; FP32 fails
+ * with QKV_ERR_UNSUPPORTED).  A "row" r = b * Hkv + j is one
  * (sequence, KV head).  Packed K, scales and the subset slab are laid out
  * [rows, capacity, ...] with capacity a multiple of 64 tokens.
  * ====================================================================== */
@@ -123,7 +125,7 @@ int qkv_final_attention(const void* query, const void* key, const void* value,
  * dim-major K copy kept per layer (EV:2018-2042). */
 int qkv_int4_pack_k(const void* key, const int64_t* k_strides, int64_t batch, int64_t kv_heads,
                     int64_t t_begin, int64_t t_end, int64_t head_dim, int64_t group,
-                    uint8_t* packed, uint16_t* scales, int64_t capacity, void* stream);
+                    uint8_t* packed, uint16_t* scales, int64_t capacity, int dtype, void* stream);
 
 /* Static channel subset per row: stats[r,c] = sum_t |code| * scale * 2^24
  * (exact uint64, T <= 2^20), then the `selected` channels of largest stat,
@@ -147,9 +149,9 @@ int qkv_int4_select_channels(const uint8_t* packed, const uint16_t* scales, int6
 int qkv_int4_build_slab(const void* key, const int64_t* k_strides, int64_t batch,
                         int64_t kv_heads, int64_t t_begin, int64_t t_end, int64_t head_dim,
                         const int32_t* chan_idx, int64_t selected, uint8_t* slab,
-                        uint16_t* slab_scales, int64_t capacity, void* stream);
+                        uint16_t* slab_scales, int64_t capacity, int dtype, void* stream);
 
-/* Per-row int8 query of decode scoring.  query bf16 [B,Hq,D] contiguous,
+/* Per-row int8 query of decode scoring.  query [B,Hq,D] contiguous,
  * Hq = G * Hkv.  The G query heads of a row are summed over the row's
  * channels chan_idx (fp32, head order), quantized to int8 q8[s] =
  * rint(qg[s] / (amax/127)), and packed as qwords uint32 [rows, selected/4]:
@@ -160,12 +162,12 @@ int qkv_int4_build_slab(const void* key, const int64_t* k_strides, int64_t batch
  * instead (EV:4428, QK:123-145). */
 int qkv_int4_query_words(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads,
                          int64_t head_dim, const int32_t* chan_idx, int64_t selected,
-                         uint32_t* qwords, float* qscale, void* stream);
+                         uint32_t* qwords, float* qscale, int dtype, void* stream);
 
 /* Decode scoring over tokens [0, tokens) of every row, fused with block
  * max-pooling.  Replaces qabs_partial_scores_dim_major_forward (QK:63-96)
  * plus the block pool of EV:5038-5044.
- * query bf16 [B,Hq,D] contiguous, Hq = G * Hkv; chan_idx int32
+ * query [B,Hq,D] contiguous, Hq = G * Hkv; chan_idx int32
  * [rows,selected].  I[t] = sum_s q8[s] * code[t,s] (int32) with q8 as
  * qkv_int4_query_words defines it; the ranking key is fp32(slab_scale[t]) *
  * fp32(I[t]).  bmax f32 [rows, ceil(tokens/block)] (block a power of two,
@@ -177,7 +179,7 @@ int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t q_heads, in
                            int64_t head_dim, const int32_t* chan_idx, int64_t selected,
                            const uint8_t* slab, const uint16_t* slab_scales, int64_t capacity,
                            int64_t tokens, int64_t block, float* bmax, int32_t* isum,
-                           float* keys, float* qscale, void* stream);
+                           float* keys, float* qscale, int dtype, void* stream);
 
 /* Top-k per row with the lowest-index tie-break: out int32 [rows,k] holds the
  * k indices first in (value descending, index ascending) order, written in
@@ -237,12 +239,15 @@ int64_t qkv_sparse_attention_workspace_bytes(int64_t batch, int64_t q_heads, int
 /* GQA-native sparse gather attention.  Replaces the reference's
  * gather/matmul/softmax fallback (EV:4490-4502) and final-attention kernel
  * (QK:335-419) without expanding K/V to the query heads (EV:6248-6251).
- * query bf16 [B,Hq,D] contiguous; key/value bf16 [B,Hkv,*,D] with
+ * query [B,Hq,D] contiguous; key/value [B,Hkv,*,D] with
  * kv_strides = {b,h,t} (rows 16-byte aligned); block_ids int32 [rows,n_sel]
  * (ids outside [0, ceil(tokens/block)) are skipped); each block covers
  * tokens [id*block, min(tokens,(id+1)*block)).  Every query head of a row
  * attends, with softmax(scaling * q.k), over the union of the row's blocks.
- * out bf16 [B,Hq,D]; a head with no valid token gets zeros (QK:388, 404).
+ * out [B,Hq,D]; a head with no valid token gets zeros (QK:388, 404).
+ * query, key, value and out share `dtype` (QKV_DTYPE_BF16 or
+ * QKV_DTYPE_FP16; P is rounded to it before P.V, as the reference's
+ * attention in that dtype does).
  * D must be 128.  One launch: the last workgroup of each row merges the
  * row's split partials.  The workspace's ticket words must be zero before
  * the first call that uses it (allocate it zero-filled); each completed call
@@ -251,7 +256,7 @@ int qkv_sparse_attention(const void* query, const void* key, const void* value,
                          const int64_t* kv_strides, int64_t batch, int64_t q_heads,
                          int64_t kv_heads, int64_t tokens, int64_t head_dim,
                          const int32_t* block_ids, int64_t n_sel, int64_t block, float scaling,
-                         float* workspace, int64_t workspace_bytes, void* out, void* stream);
+                         float* workspace, int64_t workspace_bytes, void* out, int dtype, void* stream);
 
 /* qkv_sparse_attention with the block selection fused in: replaces the
  * reference's top-k over pooled block scores (EV:5046) followed by its
@@ -267,7 +272,7 @@ int qkv_sparse_attention_select(const void* query, const void* key, const void* 
                                 int64_t kv_heads, int64_t tokens, int64_t head_dim, const float* bmax,
                                 int64_t bmax_ld, int64_t n_sel, int64_t block, float scaling,
                                 float* workspace, int64_t workspace_bytes, int32_t* sel_out, void* out,
-                                void* stream);
+                                int dtype, void* stream);
 
 /* qkv_sparse_attention / qkv_sparse_attention_select with the reference's
  * protected tokens (EV:2938-2982, applied at EV:4460): the n_sel blocks are
@@ -287,7 +292,8 @@ int qkv_sparse_attention_protected(const void* query, const void* key, const voi
                                    int64_t history, int64_t head_dim, const int32_t* block_ids, const float* bmax,
                                    int64_t bmax_ld, int64_t n_sel, int64_t block, int64_t protect_sink,
                                    int64_t protect_recent, int keep_self, float scaling, float* workspace,
-                                   int64_t workspace_bytes, int32_t* sel_out, void* out, void* stream);
+                                   int64_t workspace_bytes, int32_t* sel_out, void* out, int dtype,
+                                   void* stream);
 
 /* Streaming-read probe, no counterpart in the reference: reads `bytes` (a
  * positive multiple of 16 KiB, 16-byte aligned) once with the access shape
@@ -316,7 +322,7 @@ int qkv_sparse_attention_select_noalloc(const void* query, const void* key, cons
                                         const int64_t* kv_strides, int64_t batch, int64_t q_heads,
                                         int64_t kv_heads, int64_t tokens, int64_t head_dim, const float* bmax,
                                         int64_t bmax_ld, int64_t n_sel, int64_t block, float scaling,
-                                        int32_t* sel_out, void* out, void* stream);
+                                        int32_t* sel_out, void* out, int dtype, void* stream);
 
 /* qkv_sparse_attention with one token list per query head (group size 1,
  * one-token blocks): row (b, h) attends over token_ids [B,Hq,n_ids] (ids
@@ -327,7 +333,7 @@ int qkv_sparse_attention_select_noalloc(const void* query, const void* key, cons
 int qkv_token_attention(const void* query, const void* key, const void* value, const int64_t* kv_strides,
                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t tokens, int64_t head_dim,
                         const int32_t* token_ids, int64_t n_ids, float scaling, float* workspace,
-                        int64_t workspace_bytes, void* out, void* stream);
+                        int64_t workspace_bytes, void* out, int dtype, void* stream);
 
 /* ======================================================================
  * Candidate reuse and exact rerank (the qabs{S}cand{pct}reuse[final|2set]
@@ -551,12 +557,14 @@ int qkv_dim_major_append(const void* key, const int64_t* k_strides, int dtype, i
  * Block-metadata selectors: the qbb{bs}q{S}s{scan}cand{c} (Quest-style
  * channel bounds, EV:5508-5617) and brep{bs}r{R}q{S}s{scan}cand{c} (block
  * representatives, EV:5361-5505, BlockRepState EV:1853-1918) decode steps.
- * bf16 K/V [B,Hkv,*,128] with k_strides {b,h,t,d} (d contiguous, rows
- * 16-byte aligned); rows r = b * Hq + h read K head h / (Hq/Hkv).
+ * K/V [B,Hkv,*,128] with k_strides {b,h,t,d} (d contiguous, rows 16-byte
+ * aligned); rows r = b * Hq + h read K head h / (Hq/Hkv).  Query, K and the
+ * dim-major copy share `dtype` (QKV_DTYPE_BF16 or QKV_DTYPE_FP16), the last
+ * argument before the stream; qbb metadata is stored in that dtype.
  * ====================================================================== */
 
 /* Bytes of block metadata for meta_blocks blocks per (sequence, KV head):
- * qbb 512 per block ([min(128) | max(128)] bf16), brep 4*reps per block
+ * qbb 512 per block ([min(128) | max(128)] in K's dtype), brep 4*reps per block
  * (int32 token ids).  -1 for a bad kind or size. */
 int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_heads, int64_t meta_blocks, int64_t reps);
 
@@ -567,7 +575,7 @@ int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_heads, int64_t 
  * every step (EV:5536-5553) or per new block (EV:1884-1918). */
 int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, int64_t batch, int64_t kv_heads,
                           int64_t head_dim, int64_t block, int64_t reps, int64_t t_begin, int64_t t_end, void* meta,
-                          int64_t meta_blocks, void* stream);
+                          int64_t meta_blocks, int dtype, void* stream);
 
 /* Block scores of each row over ceil(history/block) blocks: qbb the bound
  * sum_s q_s * (q_s >= 0 ? max : min) over the row's top-|q| dims (EV:5554),
@@ -576,7 +584,7 @@ int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, i
 int qkv_block_scores(int kind, const void* query, const void* key, const int64_t* k_strides, const void* meta,
                      int64_t meta_blocks, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
                      int64_t head_dim, int64_t block, int64_t reps, int64_t dim_count, float* out, int64_t out_ld,
-                     void* stream);
+                     int dtype, void* stream);
 
 /* Partial scores of the tokens of each row's chosen blocks (EV:5576-5581):
  * position p is token blocks[r, p / block] * block + p % block, scored on
@@ -584,24 +592,25 @@ int qkv_block_scores(int kind, const void* query, const void* key, const int64_t
  * positions at or past history get -inf.  out f32 [rows, >= n_scan*block].
  * full (optional, same layout and out_ld; NULL: not written): each
  * position's full-D score scaling * q.K in the reference's fp32 order, read
- * from key (bf16 [B,Hkv,*,D] with k_strides, rows 16-byte aligned) -- the
+ * from key ([B,Hkv,*,D] with k_strides, rows 16-byte aligned) -- the
  * scores qkv_block_rerank ranks its candidates by, computed here across the
  * launch's workgroups instead of in one workgroup per row. */
 int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                           const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
                           int64_t kv_heads, int64_t history, int64_t head_dim, const int32_t* blocks, int64_t n_scan,
                           int64_t block, int64_t dim_count, float scaling, float* out, float* full, int64_t out_ld,
-                          void* stream);
+                          int dtype, void* stream);
 
 /* Block scores of the qboracle selector (EV:5030-5044): out[r, j] = the
  * largest partial score, on row r's top-|q| dims (ties to the lower dim,
  * summed in selection order), of block j's history tokens
  * [j*block, min(history, (j+1)*block)), read from the dim-major K copy
- * (qkv_dim_major_append).  query bf16 [B,Hq,D]; out f32 [rows, >= out_ld],
+ * (qkv_dim_major_append).  query [B,Hq,D]; out f32 [rows, >= out_ld],
  * rows = B*Hq.  block <= 2048. */
 int qkv_block_max_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                                  int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
-                                 int64_t block, int64_t dim_count, float* out, int64_t out_ld, void* stream);
+                                 int64_t block, int64_t dim_count, float* out, int64_t out_ld, int dtype,
+                                 void* stream);
 
 /* Replaces brep_partial_scores, which the reference imports from its
  * extension module but never shipped (wrapper EV:3847-3877, call
@@ -642,21 +651,21 @@ int qkv_block_rerank(const void* query, const void* key, const int64_t* k_stride
                      int64_t partial_ld, const int32_t* blocks, int64_t n_scan, int64_t block, int64_t n_cand,
                      int64_t n_keep,
                      int64_t protect_sink, int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
-                     int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream);
+                     int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int dtype, void* stream);
 
 /* ======================================================================
  * Chunked-prefill block selection (no reference counterpart: the reference
  * prefills with dense attention, EV:7079-7111, dense QK at EV:6602-6604).
  * ====================================================================== */
 
-/* Per-row int8 quantization of prefill queries: query bf16 rows of 128
+/* Per-row int8 quantization of prefill queries: query rows of 128
  * channels (row_stride elements apart), q8 = clamp(rint(q / (amax/127)),
  * +-127) per row, written as int8 [rows,128] in the permuted order the MFMA
  * scoring kernel consumes: channel c at byte 32*(c/32) + 16*((c/16)%2) +
  * 8*((c%16)/8) + 4*(c%2) + (c%8)/2 (q8 2-byte aligned).  qscale f32 [rows]
- * optional. */
+ * optional.  dtype: QKV_DTYPE_BF16 or QKV_DTYPE_FP16. */
 int qkv_prefill_quantize_query(const void* query, int64_t rows, int64_t head_dim, int64_t row_stride,
-                               int8_t* q8, float* qscale, void* stream);
+                               int8_t* q8, float* qscale, int dtype, void* stream);
 
 /* Block maxima of a query chunk against the whole cached K, on int8 MFMA.
  * q8 [B,Hq,queries,128] from qkv_prefill_quantize_query; packed uint8

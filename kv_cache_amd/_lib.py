@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must precede the CDLL so the HIP runtime is shared)
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libqkv.so"
 HEADER = PKG.parent / "include" / "qkv.h"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -39,34 +39,34 @@ _PROTOTYPES = {
                                          _P(_i64), _i64, _i64, _f32, _vp]),
     "qkv_final_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64,
                                    _f32, _vp]),
-    "qkv_int4_pack_k": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "qkv_int4_pack_k": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i32, _vp]),
     "qkv_int4_select_channels": (_i32, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "qkv_int4_build_slab": (_i32, [_vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp,
-                                   _i64, _vp]),
-    "qkv_int4_query_words": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+                                   _i64, _i32, _vp]),
+    "qkv_int4_query_words": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i32, _vp]),
     "qkv_int4_decode_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64,
-                                      _i64, _vp, _vp, _vp, _vp, _vp]),
+                                      _i64, _vp, _vp, _vp, _vp, _i32, _vp]),
     "qkv_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "qkv_topk_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qkv_topk_ws": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "qkv_topk_set_wait_limit": (_i32, [_i64]),
-    "qkv_prefill_quantize_query": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "qkv_prefill_quantize_query": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i32, _vp]),
     "qkv_prefill_block_scores": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                         _vp, _vp]),
     "qkv_prefill_block_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "qkv_sparse_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "qkv_sparse_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
-                                    _i64, _f32, _vp, _i64, _vp, _vp]),
+                                    _i64, _f32, _vp, _i64, _vp, _i32, _vp]),
     "qkv_sparse_attention_select": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
-                                           _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
+                                           _i64, _i64, _f32, _vp, _i64, _vp, _vp, _i32, _vp]),
     "qkv_sparse_attention_protected": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64,
-                                              _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _vp, _vp]),
+                                              _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _vp, _i32, _vp]),
     "qkv_hbm_read_probe_sink_words": (_i64, [_i64]),
     "qkv_hbm_read_probe": (_i32, [_vp, _i64, _vp, _i64, _vp]),
     "qkv_sparse_attention_select_noalloc": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp,
-                                                   _i64, _i64, _i64, _f32, _vp, _vp, _vp]),
+                                                   _i64, _i64, _i64, _f32, _vp, _vp, _i32, _vp]),
     "qkv_token_attention": (_i32, [_vp, _vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64, _f32, _vp,
-                                   _i64, _vp, _vp]),
+                                   _i64, _vp, _i32, _vp]),
     "qkv_reuse_final_count": (_i64, [_i64, _i64, _i64, _f64, _i32]),
     "qkv_reuse_select_workspace_bytes": (_i64, [_i64, _i64, _f64]),
     "qkv_reuse_select": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
@@ -94,18 +94,18 @@ _PROTOTYPES = {
     "qkv_dim_major_append": (_i32, [_vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _P(_i64), _vp]),
     "qkv_block_meta_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64]),
     "qkv_block_meta_update": (_i32, [_i32, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
-                                     _vp]),
+                                     _i32, _vp]),
     "qkv_block_scores": (_i32, [_i32, _vp, _vp, _P(_i64), _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                                _vp, _i64, _vp]),
+                                _vp, _i64, _i32, _vp]),
     "qkv_block_scan_scores": (_i32, [_vp, _vp, _P(_i64), _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _i64,
-                                     _i64, _i64, _f32, _vp, _vp, _i64, _vp]),
+                                     _i64, _i64, _f32, _vp, _vp, _i64, _i32, _vp]),
     "qkv_block_max_partial_scores": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
-                                            _i64, _vp]),
+                                            _i64, _i32, _vp]),
     "qkv_brep_partial_scores": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _P(_i64), _i64, _i64,
                                        _i64, _f64, _vp]),
     "qkv_final_list_count": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "qkv_block_rerank": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
-                                _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _vp]),
+                                _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _i32, _vp]),
 }
 
 _LIB = None
@@ -153,6 +153,14 @@ def ptr(t) -> int | None:
 
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def half_code(name: str, t: torch.Tensor) -> int:
+    """The C ABI dtype code of a bf16 or fp16 tensor (the 16-bit entry points);
+    raises for any other dtype."""
+    if t.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"{name} must be bfloat16 or float16, got {t.dtype}")
+    return DTYPE_CODES[t.dtype]
 
 
 def require_cuda(name: str, t: torch.Tensor) -> None:

@@ -74,16 +74,20 @@ def step_counts(history: int, block: int, scan: float, cand: float, top: float) 
 
 
 class BlockSelectDecodeStep:
-    """One layer's qbb / brep / qboracle decode step with its block metadata, for bf16
-    K/V caches [B, Hkv, T, 128] of up to ``capacity`` tokens.  Call it once
+    """One layer's qbb / brep / qboracle decode step with its block metadata, for
+    K/V caches [B, Hkv, T, 128] of up to ``capacity`` tokens in ``dtype``
+    (bf16 or fp16; the query and the output share it).  Call it once
     per decode token with the cache including the current token; a call
     whose history is not the previous call's plus one starts a new sequence
     (the metadata and the dim-major copy are rebuilt)."""
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
-                 keep_self: bool = True, device: torch.device | str = "cuda"):
+                 keep_self: bool = True, device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16):
         lib = _lib.load()
+        _require(dtype in (torch.bfloat16, torch.float16), f"dtype must be bfloat16 or float16, got {dtype}")
+        self.dtype = dtype
+        self.dtype_code = _lib.DTYPE_CODES[dtype]
         self.mode = mode
         self.kind, self.block, reps, self.dims, self.scan, self.cand = parse_block_mode(mode)
         self.reps = max(1, min(reps, self.block))
@@ -106,7 +110,7 @@ class BlockSelectDecodeStep:
             nbytes = lib.qkv_block_meta_bytes(self.kind, batch, kv_heads, self.meta_blocks, self.reps)
             _require(nbytes > 0, "bad block metadata size")
             self.meta = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
+        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
         nb, n_scan, n_cand, n_keep = step_counts(cap - 1, self.block, self.scan, self.cand, self.top_fraction)
         _require(n_scan * self.block <= 40960, f"{n_scan * self.block} scanned tokens per row; at most 40960")
         _require(n_cand <= 4096, f"{n_cand} candidates per row; at most 4096")
@@ -120,7 +124,7 @@ class BlockSelectDecodeStep:
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
         need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
-        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=dtype, device=device)
         self.reset()
 
     def reset(self) -> None:
@@ -138,7 +142,7 @@ class BlockSelectDecodeStep:
                 _lib.check(lib.qkv_block_meta_update(
                     self.kind, key.data_ptr(), _lib.strides(*key.stride()), self.batch, self.kv_heads, self.head_dim,
                     self.block, self.reps, self.meta_len, history, self.meta.data_ptr(), self.meta_blocks,
-                    _lib.stream_of(key)))
+                    self.dtype_code, _lib.stream_of(key)))
             self.meta_len = history
         if self.kdm_len < history:
             dim_major_append(key, self.kdm, self.kdm_len, history)
@@ -149,11 +153,12 @@ class BlockSelectDecodeStep:
         self._sync_cache(key, key.size(2))
 
     def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
-        """query bf16 [B, Hq, 128]; key/value bf16 [B, Hkv, T, 128], the
-        current token last.  Returns bf16 [B, Hq, 128]."""
+        """query [B, Hq, 128]; key/value [B, Hkv, T, 128], the current token
+        last, all in the step's dtype.  Returns [B, Hq, 128] in that dtype."""
         key_count = key.size(2)
         _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
-        _require(query.dtype == key.dtype == value.dtype == torch.bfloat16, "block selectors take bf16 q/K/V")
+        _require(query.dtype == key.dtype == value.dtype == self.dtype,
+                 f"this step takes {self.dtype} q/K/V (got {query.dtype}, {key.dtype}, {value.dtype})")
         g = self.q_heads // self.kv_heads
         if key_count <= 1:   # EV:5523-5525
             self.out.copy_(value[:, :, -1, :].repeat_interleave(g, dim=1))
@@ -192,12 +197,12 @@ class BlockSelectDecodeStep:
                 _lib.check(lib.qkv_block_max_partial_scores(
                     q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), self.batch, self.q_heads,
                     self.kv_heads, history, self.head_dim, self.block, self.dims, self.bscore.data_ptr(),
-                    self.meta_blocks, stream))
+                    self.meta_blocks, self.dtype_code, stream))
             else:
                 _lib.check(lib.qkv_block_scores(
                     self.kind, q.data_ptr(), key.data_ptr(), ks, self.meta.data_ptr(), self.meta_blocks, self.batch,
                     self.q_heads, self.kv_heads, history, self.head_dim, self.block, self.reps, self.dims,
-                    self.bscore.data_ptr(), self.meta_blocks, stream))
+                    self.bscore.data_ptr(), self.meta_blocks, self.dtype_code, stream))
             blocks = self.blocks[: self.rows * n_scan].view(self.rows, n_scan)
             block_topk(self.bscore[:, :nb], n_scan, out=blocks, workspace=self.topk_ws)
             n_tok = n_scan * self.block
@@ -206,7 +211,7 @@ class BlockSelectDecodeStep:
             _lib.check(lib.qkv_block_scan_scores(
                 q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), key.data_ptr(), ks, self.batch,
                 self.q_heads, self.kv_heads, history, self.head_dim, blocks.data_ptr(), n_scan, self.block,
-                self.dims, float(scaling), partial.data_ptr(), full.data_ptr(), n_tok, stream))
+                self.dims, float(scaling), partial.data_ptr(), full.data_ptr(), n_tok, self.dtype_code, stream))
             n_out = int(lib.qkv_final_list_count(history, n_keep, self.sink, self.recent, int(self.keep_self)))
             ids = self.attn_ids[: self.rows * n_out]
             _lib.check(lib.qkv_block_rerank(
@@ -214,7 +219,7 @@ class BlockSelectDecodeStep:
                 partial.data_ptr(), full.data_ptr(), n_tok, blocks.data_ptr(), n_scan, self.block, n_cand, n_keep,
                 self.sink,
                 self.recent, int(self.keep_self), float(scaling), self.keep.data_ptr(), self.capacity,
-                ids.data_ptr(), n_out, stream))
+                ids.data_ptr(), n_out, self.dtype_code, stream))
         self.n_out = n_out
         self.key_count = key_count
         return token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws,

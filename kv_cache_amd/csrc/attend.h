@@ -52,9 +52,24 @@ __device__ __forceinline__ uint4 ld_nt(const uint16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
-                                         false);
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// Output element of the 16-bit dtype (bf16, or fp16 with F16), rounded to nearest even.
+template <bool F16>
+__device__ __forceinline__ uint16_t f32_to_half(float f) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  else return f32_to_bf16_rne(f);
+}
+
+// c + a.lo * b.lo + a.hi * b.hi over packed pairs of the 16-bit dtype, in fp32
+// (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <bool F16>
+__device__ __forceinline__ float dot2_half(uint32_t a, uint32_t b, float c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                           false);
 }
 
 // Sum over each row of 16 lanes; every lane of the row receives the sum.
@@ -102,10 +117,10 @@ struct RowSlots {
 
 // Workgroup epilogue of both attention kernels, entered by every thread once
 // red_m / red_l / red_acc hold each wave's (max, sum, weighted V) per head
-// and a barrier has passed.  A row that fits one workgroup writes its bf16
-// output; otherwise the workgroup publishes its partial, takes a ticket, and
+// and a barrier has passed.  A row that fits one workgroup writes its output
+// (bf16, or fp16 with F16); otherwise the workgroup publishes its partial, takes a ticket, and
 // the row's last workgroup merges all partials.
-template <int G, int NW>
+template <int G, int NW, bool F16>
 __device__ __forceinline__ void finish_workgroup(const float (&red_acc)[NW][G][kD], const float (&red_m)[NW][G],
                                                  const float (&red_l)[NW][G], int& last_flag, int r, int split,
                                                  int nsplit, uint16_t* __restrict__ out_row,
@@ -141,7 +156,7 @@ __device__ __forceinline__ void finish_workgroup(const float (&red_acc)[NW][G][k
     for (int idx = tid; idx < G * kD; idx += NT) {
       const int h = idx / kD, d = idx - h * kD;
       const float o = (wg_m[h] == ninf) ? 0.0f : wg_acc(h, d) / wg_l[h];
-      out_row[h * kD + d] = f32_to_bf16_rne(o);
+      out_row[h * kD + d] = f32_to_half<F16>(o);
     }
     return;
   }
@@ -221,7 +236,7 @@ __device__ __forceinline__ void finish_workgroup(const float (&red_acc)[NW][G][k
     const int idx = tid + k * NT;
     if (idx < G * kD) {
       const float v = (mx[k] == ninf) ? 0.0f : o[k] / den[k];
-      out_row[idx] = f32_to_bf16_rne(v);
+      out_row[idx] = f32_to_half<F16>(v);
     }
   }
 }
@@ -275,9 +290,46 @@ enum { kIdsGiven = 0, kIdsSelect = 1 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// c + A.B on a 16x16x32 tile, eight 16-bit elements per lane in a and b
+// (v_mfma_f32_16x16x32_bf16 / _f16).
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// c + A.B on a 16x16x16 tile, four 16-bit elements per lane in a and b
+// (v_mfma_f32_16x16x16_bf16 / _f16).
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma_16x16x16(u32x2_t a, u32x2_t b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a), __builtin_bit_cast(s16x4_t, b),
+                                                     c, 0, 0, 0);
+}
+
+// Four fp32 values rounded (nearest even) to the 16-bit dtype and packed.
+template <bool F16>
+__device__ __forceinline__ u32x2_t pack4_half(const float (&p)[4]) {
+  if constexpr (F16)
+    return __builtin_bit_cast(u32x2_t, f16x4_t{static_cast<_Float16>(p[0]), static_cast<_Float16>(p[1]),
+                                               static_cast<_Float16>(p[2]), static_cast<_Float16>(p[3])});
+  else
+    return __builtin_bit_cast(u32x2_t, bf16x4_t{static_cast<__bf16>(p[0]), static_cast<__bf16>(p[1]),
+                                                static_cast<__bf16>(p[2]), static_cast<__bf16>(p[3])});
+}
 
 __device__ __forceinline__ u32x4_t ld_nt4(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
@@ -300,19 +352,19 @@ constexpr int kVtStride = 18;   // uint16 per channel
 // given (kIdsGiven) or selected from the row's block maxima in the
 // workgroup (kIdsSelect, SELV keys per thread).
 //   QK: S^T[slot][head] = sum_k K[slot][k] Q[head][k], four
-//   v_mfma_f32_16x16x32_bf16 over k = 32s..32s+31 with A = K (lane 16g+c
+//   v_mfma_f32_16x16x32_bf16 (_f16 with F16) over k = 32s..32s+31 with A = K (lane 16g+c
 //   reads 16 bytes of slot c's row: channels 32s+8g..32s+8g+7) and B = Q^T
 //   (heads past G are zero columns).  Lane 16g+c then holds head c for slots
 //   4g..4g+3.
 //   P.V: O[head][ch] += sum_slot P[head][slot] V[slot][ch], eight
-//   v_mfma_f32_16x16x16_bf16 of 16 channels each.  P (rounded to bf16, as the
-//   reference's bf16 attention does) is already in the A layout; V is loaded
+//   v_mfma_f32_16x16x16_bf16 (_f16) of 16 channels each.  P (rounded to the
+//   K/V dtype, as the reference's attention does) is already in the A layout; V is loaded
 //   as in sparse_attn_kernel (lane 16g+c: slot 4i+g, channels 8c..8c+7),
 //   stored channel-major into the wave's LDS tile, and read back as B, four
 //   slots of one channel per lane.
 // Softmax is per head over the lanes of its column (in-lane over 4 slots, then
 // the lane swaps), in the log2 domain with lazy rescaling.
-template <int G, int ITERS, int SELV, int IDS>
+template <int G, int ITERS, int SELV, int IDS, bool F16>
 __device__ __forceinline__ void attend_mfma(const AttnArgs& a, int r, int split) {
   constexpr int NW = 4, NT = 256, CH = 16;
   static_assert(G <= 16, "the heads are the 16 columns of the QK tile");
@@ -350,14 +402,14 @@ __device__ __forceinline__ void attend_mfma(const AttnArgs& a, int r, int split)
   const int64_t st = a.st;
   const float scale_log2 = a.scale_log2;
 
-  bf16x8_t qb[4];   // B operand of QK: Q[head c16][32s + 8g4 ..], zero for heads >= G
+  u32x4_t qb[4];   // B operand of QK: Q[head c16][32s + 8g4 ..], zero for heads >= G
   {
     const uint16_t* qrow = a.q + (static_cast<int64_t>(b) * a.q_heads + j * G + min(c16, G - 1)) * kD + 8 * g4;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4_t w = *reinterpret_cast<const u32x4_t*>(qrow + 32 * s);
       if (c16 >= G) w = u32x4_t{0u, 0u, 0u, 0u};
-      qb[s] = __builtin_bit_cast(bf16x8_t, w);
+      qb[s] = w;
     }
   }
 
@@ -398,7 +450,7 @@ __device__ __forceinline__ void attend_mfma(const AttnArgs& a, int r, int split)
     f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kx[s]), qb[s], sacc, 0, 0, 0);
+      sacc = mfma_16x16x32<F16>(kx[s], qb[s], sacc);
     float sv[4], cm = ninf;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -426,13 +478,12 @@ __device__ __forceinline__ void attend_mfma(const AttnArgs& a, int r, int split)
       p[i] = exp2f(sv[i] - ms);   // 0 for masked slots
       lsum += p[i];
     }
-    const s16x4_t pa = __builtin_bit_cast(s16x4_t, bf16x4_t{static_cast<__bf16>(p[0]), static_cast<__bf16>(p[1]),
-                                                           static_cast<__bf16>(p[2]), static_cast<__bf16>(p[3])});
+    const u32x2_t pa = pack4_half<F16>(p);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int at = ((16 * q + c16) * kVtStride + 4 * g4) >> 1;
       const u32x2_t w = {vt32[at], vt32[at + 1]};
-      o[q] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(s16x4_t, w), o[q], 0, 0, 0);
+      o[q] = mfma_16x16x16<F16>(pa, w, o[q]);
     }
     pin(lsum);
   };
@@ -486,7 +537,7 @@ __device__ __forceinline__ void attend_mfma(const AttnArgs& a, int r, int split)
     }
   }
   __syncthreads();
-  finish_workgroup<G, NW>(red_acc, red_m, red_l, last_flag, r, split, a.nsplit,
+  finish_workgroup<G, NW, F16>(red_acc, red_m, red_l, last_flag, r, split, a.nsplit,
                           a.out + (static_cast<int64_t>(b) * a.q_heads + j * G) * kD, a.ws_acc, a.ws_ml, a.tickets);
 }
 

@@ -1,5 +1,5 @@
-// GQA-native sparse gather attention over selected KV blocks (bf16 K/V,
-// fp32 softmax and accumulation), one launch per call.
+// GQA-native sparse gather attention over selected KV blocks (bf16 or fp16
+// q/K/V/output, fp32 softmax and accumulation), one launch per call.
 //
 // The reference expands K/V to every query head (evaluate_qwen3_top2_head_
 // limit3_ppl.py:6248-6251) and then gathers per head (EV:4490-4502, kernel
@@ -20,13 +20,13 @@
 // operand layouts).  sparse_attn_kernel (G = 1) runs them on the VALU: 16
 // lanes share a token (lane 16g + c holds channels 8c..8c+7 of the token of
 // slot 4i + g in step i, so each load instruction reads four whole 256-byte
-// rows), QK is v_dot2_f32_bf16 on the packed channel pairs and a 16-lane DPP
-// sum, softmax runs in the log2 domain with a running maximum per 16-lane
-// token group, P.V accumulates in fp32, and a wave combines its four token
+// rows), QK is v_dot2_f32_bf16 (v_dot2_f32_f16 for fp16) on the packed
+// channel pairs and a 16-lane DPP sum, softmax runs in the log2 domain with a
+// running maximum per 16-lane token group, P.V accumulates in fp32, and a wave combines its four token
 // groups with the gfx950 lane swaps (v_permlane16_swap / v_permlane32_swap).
 //
 // A workgroup combines its waves through LDS into (max, sum, weighted V) per
-// head.  A row that fits one workgroup writes its bf16 output directly.
+// head.  A row that fits one workgroup writes its output directly.
 // Otherwise every workgroup publishes its partial with device-coherent
 // stores (relaxed agent-scope atomic stores: global_store sc1, written
 // through the XCD's L2), waits for them to complete, and takes a ticket; the
@@ -49,7 +49,7 @@ namespace {
 // with SELV keys per thread (rows of at most 64*NW*SELV blocks; the selection's
 // latency grows with SELV).  The row's first workgroup also writes it to
 // sel_out (when given).
-template <int G, int NI, int ITERS, int SELV, int NW>
+template <int G, int NI, int ITERS, int SELV, int NW, bool F16>
 __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_attn_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, int64_t sb, int64_t sh, int64_t st, int q_heads,
@@ -152,10 +152,10 @@ __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_a
       float r[G];
 #pragma unroll
       for (int k = 0; k < G; ++k) {
-        float a = dot2_bf16(qx[k].x, kx[i].x, 0.0f);
-        a = dot2_bf16(qx[k].y, kx[i].y, a);
-        a = dot2_bf16(qx[k].z, kx[i].z, a);
-        r[k] = dot2_bf16(qx[k].w, kx[i].w, a);
+        float a = dot2_half<F16>(qx[k].x, kx[i].x, 0.0f);
+        a = dot2_half<F16>(qx[k].y, kx[i].y, a);
+        a = dot2_half<F16>(qx[k].z, kx[i].z, a);
+        r[k] = dot2_half<F16>(qx[k].w, kx[i].w, a);
       }
       float y;
       if constexpr (G == 4) {
@@ -186,10 +186,10 @@ __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_a
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       float v[8];
-      v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
-      v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
-      v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
-      v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
+      v[0] = half_lo<F16>(vx[i].x); v[1] = half_hi<F16>(vx[i].x);
+      v[2] = half_lo<F16>(vx[i].y); v[3] = half_hi<F16>(vx[i].y);
+      v[4] = half_lo<F16>(vx[i].z); v[5] = half_hi<F16>(vx[i].z);
+      v[6] = half_lo<F16>(vx[i].w); v[7] = half_hi<F16>(vx[i].w);
       const float p = exp2f(s[i] - ms);   // 0 for masked slots
       l_own += p;
 #pragma unroll
@@ -218,10 +218,10 @@ __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_a
     for (int i = 0; i < NI; ++i) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        float a = dot2_bf16(qx[h].x, kx[i].x, 0.0f);
-        a = dot2_bf16(qx[h].y, kx[i].y, a);
-        a = dot2_bf16(qx[h].z, kx[i].z, a);
-        a = dot2_bf16(qx[h].w, kx[i].w, a);
+        float a = dot2_half<F16>(qx[h].x, kx[i].x, 0.0f);
+        a = dot2_half<F16>(qx[h].y, kx[i].y, a);
+        a = dot2_half<F16>(qx[h].z, kx[i].z, a);
+        a = dot2_half<F16>(qx[h].w, kx[i].w, a);
         a = row16_sum(a) * scale_log2;
         s[h][i] = tk[i] >= 0 ? a : ninf;
         cm[h] = fmaxf(cm[h], s[h][i]);
@@ -243,10 +243,10 @@ __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_a
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       float v[8];
-      v[0] = bf16lo(vx[i].x); v[1] = bf16hi(vx[i].x);
-      v[2] = bf16lo(vx[i].y); v[3] = bf16hi(vx[i].y);
-      v[4] = bf16lo(vx[i].z); v[5] = bf16hi(vx[i].z);
-      v[6] = bf16lo(vx[i].w); v[7] = bf16hi(vx[i].w);
+      v[0] = half_lo<F16>(vx[i].x); v[1] = half_hi<F16>(vx[i].x);
+      v[2] = half_lo<F16>(vx[i].y); v[3] = half_hi<F16>(vx[i].y);
+      v[4] = half_lo<F16>(vx[i].z); v[5] = half_hi<F16>(vx[i].z);
+      v[6] = half_lo<F16>(vx[i].w); v[7] = half_hi<F16>(vx[i].w);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float p = exp2f(s[h][i] - ms[h]);   // 0 for masked slots
@@ -339,13 +339,13 @@ __global__ __launch_bounds__(64 * NW, QKV_ATTN_WG_PER_CU * 4 / NW) void sparse_a
   }
   __syncthreads();
 
-  finish_workgroup<G, NW>(red_acc, red_m, red_l, last_flag, r, split, nsplit,
+  finish_workgroup<G, NW, F16>(red_acc, red_m, red_l, last_flag, r, split, nsplit,
                           out + (static_cast<int64_t>(b) * q_heads + j * G) * kD, ws_acc, ws_ml, tickets);
 }
 
-template <int G, int ITERS, int SELV>
+template <int G, int ITERS, int SELV, bool F16>
 __global__ __launch_bounds__(256, QKV_ATTN_WG_PER_CU) void sparse_attn_mfma_kernel(const AttnArgs a) {
-  attend_mfma<G, ITERS, SELV, (SELV > 0 ? kIdsSelect : kIdsGiven)>(a, blockIdx.y, blockIdx.x);
+  attend_mfma<G, ITERS, SELV, (SELV > 0 ? kIdsSelect : kIdsGiven), F16>(a, blockIdx.y, blockIdx.x);
 }
 
 // 4-token steps per wave chunk: 8 while the G heads' state leaves room for
@@ -387,39 +387,49 @@ int64_t splits_for(int64_t rows, int64_t n_slots, int64_t g) {
 }
 
 
-template <int GG, int IT, int SS>
+template <int GG, int IT, int SS, bool FF>
 void launch_attn(dim3 grid, hipStream_t st, const AttnArgs& a) {
 #define QKV_ATTN_ARGS                                                                                          \
   a.q, a.k, a.v, a.sb, a.sh, a.st, a.q_heads, a.kv_heads, a.tokens, a.block_ids, a.n_sel, a.block, a.nb,    \
       a.scale_log2, a.nsplit, a.ws_acc, a.ws_ml, a.tickets, a.out, a.bmax, a.bmax_ld, a.sel_out, a.kv_div,   \
       a.n_prot, a.sink_end, a.recent_start, a.rec_begin, a.n_rec, a.self_tok
   if constexpr (mfma_for(GG))
-    sparse_attn_mfma_kernel<GG, IT, SS><<<grid, 256, 0, st>>>(a);
+    sparse_attn_mfma_kernel<GG, IT, SS, FF><<<grid, 256, 0, st>>>(a);
   else
-    sparse_attn_kernel<GG, ni_for(GG), IT, SS, kWaves><<<grid, 64 * kWaves, 0, st>>>(QKV_ATTN_ARGS);
+    sparse_attn_kernel<GG, ni_for(GG), IT, SS, kWaves, FF><<<grid, 64 * kWaves, 0, st>>>(QKV_ATTN_ARGS);
 #undef QKV_ATTN_ARGS
 }
 
 // The selection's keys per thread: 8 (at 4 waves) for rows of <= 2048
 // blocks, 16 above.
-template <int GG, int IT>
+template <int GG, int IT, bool FF>
 void launch_attn_sel(dim3 grid, hipStream_t st, const AttnArgs& a, bool sel) {
   constexpr int W = mfma_for(GG) ? 4 : kWaves;
-  if (!sel) launch_attn<GG, IT, 0>(grid, st, a);
-  else if (a.nb <= 2048) launch_attn<GG, IT, 32 / W>(grid, st, a);
-  else launch_attn<GG, IT, 64 / W>(grid, st, a);
+  if (!sel) launch_attn<GG, IT, 0, FF>(grid, st, a);
+  else if (a.nb <= 2048) launch_attn<GG, IT, 32 / W, FF>(grid, st, a);
+  else launch_attn<GG, IT, 64 / W, FF>(grid, st, a);
 }
 
-template <int GG>
+template <int GG, bool FF>
 void launch_attn_g(int iters, dim3 grid, hipStream_t st, const AttnArgs& a, bool sel) {
   constexpr int MAXI = max_iters_for(GG);
   switch (iters) {
-    case 1: launch_attn_sel<GG, 1>(grid, st, a, sel); break;
-    case 2: launch_attn_sel<GG, 2>(grid, st, a, sel); break;
-    case 4: launch_attn_sel<GG, 4>(grid, st, a, sel); break;
-    case 8: launch_attn_sel<GG, 8>(grid, st, a, sel); break;
-    case 16: if constexpr (MAXI >= 16) launch_attn_sel<GG, 16>(grid, st, a, sel); break;
-    default: if constexpr (MAXI >= 32) launch_attn_sel<GG, 32>(grid, st, a, sel); break;
+    case 1: launch_attn_sel<GG, 1, FF>(grid, st, a, sel); break;
+    case 2: launch_attn_sel<GG, 2, FF>(grid, st, a, sel); break;
+    case 4: launch_attn_sel<GG, 4, FF>(grid, st, a, sel); break;
+    case 8: launch_attn_sel<GG, 8, FF>(grid, st, a, sel); break;
+    case 16: if constexpr (MAXI >= 16) launch_attn_sel<GG, 16, FF>(grid, st, a, sel); break;
+    default: if constexpr (MAXI >= 32) launch_attn_sel<GG, 32, FF>(grid, st, a, sel); break;
+  }
+}
+
+template <bool FF>
+void launch_attn_dt(int64_t g, int iters, dim3 grid, hipStream_t st, const AttnArgs& a, bool sel) {
+  switch (g) {
+    case 1: launch_attn_g<1, FF>(iters, grid, st, a, sel); break;
+    case 2: launch_attn_g<2, FF>(iters, grid, st, a, sel); break;
+    case 4: launch_attn_g<4, FF>(iters, grid, st, a, sel); break;
+    default: launch_attn_g<8, FF>(iters, grid, st, a, sel); break;
   }
 }
 
@@ -447,11 +457,13 @@ int launch_attention(const char* what, const void* query, const void* key, const
                      const int64_t* kv_strides, int64_t batch, int64_t q_heads, int64_t kv_heads,
                      int64_t tokens, int64_t head_dim, const int32_t* block_ids, const float* bmax,
                      int64_t bmax_ld, int32_t* sel_out, int64_t n_sel, int64_t block, float scaling,
-                     float* workspace, int64_t workspace_bytes, void* out, void* stream, int kv_div = 1,
-                     int64_t protect_sink = 0, int64_t protect_recent = 0, bool keep_self = false) {
+                     float* workspace, int64_t workspace_bytes, void* out, int dtype, void* stream,
+                     int kv_div = 1, int64_t protect_sink = 0, int64_t protect_recent = 0, bool keep_self = false) {
   const bool sel = bmax != nullptr;
   if (!query || !key || !value || !kv_strides || !(sel || block_ids) || !workspace || !out)
     return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  bool f16;
+  if (int rc = half_dtype(dtype, what, &f16)) return rc;
   if (head_dim != kD) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be 128", what);
   if (batch <= 0 || kv_heads <= 0 || q_heads % kv_heads)
     return fail(QKV_ERR_INVALID, "%s: q_heads must be a multiple of kv_heads", what);
@@ -508,12 +520,8 @@ int launch_attention(const char* what, const void* query, const void* key, const
                    bmax, bmax_ld, sel_out, kv_div, static_cast<int>(n_prot), static_cast<int>(sink_end),
                    static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec),
                    static_cast<int>(tokens)};
-  switch (g) {
-    case 1: launch_attn_g<1>(iters, grid, st, a, sel); break;
-    case 2: launch_attn_g<2>(iters, grid, st, a, sel); break;
-    case 4: launch_attn_g<4>(iters, grid, st, a, sel); break;
-    default: launch_attn_g<8>(iters, grid, st, a, sel); break;
-  }
+  if (f16) launch_attn_dt<true>(g, iters, grid, st, a, sel);
+  else launch_attn_dt<false>(g, iters, grid, st, a, sel);
   return check_launch(what);
 }
 
@@ -524,11 +532,11 @@ QKV_EXPORT int qkv_sparse_attention(const void* query, const void* key, const vo
                                     int64_t kv_heads, int64_t tokens, int64_t head_dim,
                                     const int32_t* block_ids, int64_t n_sel, int64_t block,
                                     float scaling, float* workspace, int64_t workspace_bytes,
-                                    void* out, void* stream) {
+                                    void* out, int dtype, void* stream) {
   if (!block_ids) return fail(QKV_ERR_INVALID, "qkv_sparse_attention: null pointer");
   return launch_attention("qkv_sparse_attention", query, key, value, kv_strides, batch, q_heads, kv_heads,
                           tokens, head_dim, block_ids, nullptr, 0, nullptr, n_sel, block, scaling, workspace,
-                          workspace_bytes, out, stream);
+                          workspace_bytes, out, dtype, stream);
 }
 
 QKV_EXPORT int qkv_sparse_attention_protected(const void* query, const void* key, const void* value,
@@ -537,14 +545,15 @@ QKV_EXPORT int qkv_sparse_attention_protected(const void* query, const void* key
                                               const int32_t* block_ids, const float* bmax, int64_t bmax_ld,
                                               int64_t n_sel, int64_t block, int64_t protect_sink,
                                               int64_t protect_recent, int keep_self, float scaling, float* workspace,
-                                              int64_t workspace_bytes, int32_t* sel_out, void* out, void* stream) {
+                                              int64_t workspace_bytes, int32_t* sel_out, void* out, int dtype,
+                                              void* stream) {
   static const char* what = "qkv_sparse_attention_protected";
   if (!block_ids == !bmax) return fail(QKV_ERR_INVALID, "%s: pass exactly one of block_ids and bmax", what);
   if (protect_sink < 0 || protect_recent < 0)
     return fail(QKV_ERR_INVALID, "%s: protected token counts must be >= 0", what);
   return launch_attention(what, query, key, value, kv_strides, batch, q_heads, kv_heads, history, head_dim,
                           block_ids, bmax, bmax_ld, bmax ? sel_out : nullptr, n_sel, block, scaling, workspace,
-                          workspace_bytes, out, stream, 1, protect_sink, protect_recent, keep_self != 0);
+                          workspace_bytes, out, dtype, stream, 1, protect_sink, protect_recent, keep_self != 0);
 }
 
 QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, const void* value,
@@ -552,11 +561,11 @@ QKV_EXPORT int qkv_sparse_attention_select(const void* query, const void* key, c
                                            int64_t kv_heads, int64_t tokens, int64_t head_dim,
                                            const float* bmax, int64_t bmax_ld, int64_t n_sel, int64_t block,
                                            float scaling, float* workspace, int64_t workspace_bytes,
-                                           int32_t* sel_out, void* out, void* stream) {
+                                           int32_t* sel_out, void* out, int dtype, void* stream) {
   if (!bmax) return fail(QKV_ERR_INVALID, "qkv_sparse_attention_select: null pointer");
   return launch_attention("qkv_sparse_attention_select", query, key, value, kv_strides, batch, q_heads,
                           kv_heads, tokens, head_dim, nullptr, bmax, bmax_ld, sel_out, n_sel, block, scaling,
-                          workspace, workspace_bytes, out, stream);
+                          workspace, workspace_bytes, out, dtype, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -591,7 +600,7 @@ QKV_EXPORT int qkv_sparse_attention_select_noalloc(const void* query, const void
                                                    int64_t kv_heads, int64_t tokens, int64_t head_dim,
                                                    const float* bmax, int64_t bmax_ld, int64_t n_sel,
                                                    int64_t block, float scaling, int32_t* sel_out, void* out,
-                                                   void* stream) {
+                                                   int dtype, void* stream) {
   static const char* what = "qkv_sparse_attention_select_noalloc";
   if (!bmax) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
   const int64_t need = qkv_sparse_attention_workspace_bytes(batch, q_heads, kv_heads, head_dim, n_sel, block);
@@ -637,14 +646,15 @@ QKV_EXPORT int qkv_sparse_attention_select_noalloc(const void* query, const void
   }
   return launch_attention(what, query, key, value, kv_strides, batch, q_heads, kv_heads, tokens, head_dim, nullptr,
                           bmax, bmax_ld, sel_out, n_sel, block, scaling, ws, QKV_NOALLOC_SCRATCH_BYTES, out,
-                          stream);
+                          dtype, stream);
 }
 
 QKV_EXPORT int qkv_token_attention(const void* query, const void* key, const void* value,
                                    const int64_t* kv_strides, int64_t batch, int64_t q_heads,
                                    int64_t kv_heads, int64_t tokens, int64_t head_dim,
                                    const int32_t* token_ids, int64_t n_ids, float scaling,
-                                   float* workspace, int64_t workspace_bytes, void* out, void* stream) {
+                                   float* workspace, int64_t workspace_bytes, void* out, int dtype,
+                                   void* stream) {
   // Every query head is its own row (group size 1) with one-token blocks;
   // row (b, h) reads K/V head h / (q_heads / kv_heads).
   if (!token_ids) return fail(QKV_ERR_INVALID, "qkv_token_attention: null pointer");
@@ -652,5 +662,5 @@ QKV_EXPORT int qkv_token_attention(const void* query, const void* key, const voi
     return fail(QKV_ERR_INVALID, "qkv_token_attention: q_heads must be a multiple of kv_heads");
   return launch_attention("qkv_token_attention", query, key, value, kv_strides, batch, q_heads, q_heads, tokens,
                           head_dim, token_ids, nullptr, 0, nullptr, n_ids, 1, scaling, workspace, workspace_bytes,
-                          out, stream, static_cast<int>(q_heads / kv_heads));
+                          out, dtype, stream, static_cast<int>(q_heads / kv_heads));
 }

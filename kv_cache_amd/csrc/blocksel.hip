@@ -2,7 +2,8 @@
 // (Quest-style per-block channel bounds, EV:5508-5617), brep modes (block
 // representatives, EV:5361-5505, with their BlockRepState, EV:1853-1918) and
 // qboracle modes (block maxima of the partial scores, EV:5008-5097), on
-// GQA-shaped bf16 K/V (D = 128).
+// GQA-shaped bf16 or fp16 K/V (D = 128; query, K and the dim-major copy
+// share the dtype).
 //
 // Rows are (sequence, query head) r = b * Hq + h, reading K head h / (Hq/Hkv).
 // Per step:
@@ -51,13 +52,19 @@ __device__ void rank_dims(const float* q_s, int count, int* sel_idx, float* sel_
   rank_dims128(q_s, key_s, kHD, count, sel_idx, sel_q);
 }
 
-__device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(static_cast<uint32_t>(x) << 16); }
+// The 16-bit pattern of v, a value of the dtype (exact).
+template <bool F16>
+__device__ __forceinline__ uint16_t half_bits(float v) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  else return static_cast<uint16_t>(__float_as_uint(v) >> 16);
+}
 
 // scaling * sum_d q[d] * K[d] over d ascending, separately rounded (the
-// reference's fp32 order), for one bf16 K row of kHD values (16-byte
+// reference's fp32 order), for one bf16 (fp16) K row of kHD values (16-byte
 // aligned) and q in LDS (16-byte aligned).  The row's loads go out first;
 // q is read eight values per 16-byte word where it is used (the empty asm
 // keeps those reads from being hoisted all at once next to the row loads).
+template <bool F16>
 __device__ __forceinline__ float full_score(const uint16_t* __restrict__ krow, const float* q_s, float scaling) {
   const uint4* kr = reinterpret_cast<const uint4*>(krow);
   uint4 x[kHD / 8];
@@ -73,19 +80,20 @@ __device__ __forceinline__ float full_score(const uint16_t* __restrict__ krow, c
     const uint32_t w[4] = {x[c].x, x[c].y, x[c].z, x[c].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      acc = acc + qv[2 * e] * __uint_as_float(w[e] << 16);
-      acc = acc + qv[2 * e + 1] * __uint_as_float(w[e] & 0xFFFF0000u);
+      acc = acc + qv[2 * e] * half_lo<F16>(w[e]);
+      acc = acc + qv[2 * e + 1] * half_hi<F16>(w[e]);
     }
   }
   return acc * scaling;
 }
 
 // ---------------------------------------------------------------------------
-// Metadata.  qbb: per block a 512-byte record [min(128) | max(128)] of bf16
-// (exact: K is bf16).  brep: per block R int32 token indices, descending
+// Metadata.  qbb: per block a 512-byte record [min(128) | max(128)] in K's
+// dtype (exact: they are elements of K).  brep: per block R int32 token indices, descending
 // squared norm, lower index on ties, -1 where the block has fewer tokens.
 // Blocks [j0, j0 + grid.x) over tokens below t_end are rebuilt.
 // ---------------------------------------------------------------------------
+template <bool F16>
 __global__ __launch_bounds__(kBT) void qbb_meta_kernel(const uint16_t* __restrict__ key, int kv_heads, int64_t sb,
                                                        int64_t sh, int64_t st, int block, int t_end, int j0,
                                                        uint16_t* __restrict__ meta, int64_t meta_blocks) {
@@ -97,16 +105,17 @@ __global__ __launch_bounds__(kBT) void qbb_meta_kernel(const uint16_t* __restric
   for (int c = tid; c < kHD; c += kBT) {
     float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
     for (int t = t_lo; t < t_hi; ++t) {
-      const float v = bf16f(kb[static_cast<int64_t>(t) * st + c]);
+      const float v = half_to_f32<F16>(kb[static_cast<int64_t>(t) * st + c]);
       mn = fminf(mn, v);
       mx = fmaxf(mx, v);
     }
-    rec[c] = static_cast<uint16_t>(__float_as_uint(mn) >> 16);
-    rec[kHD + c] = static_cast<uint16_t>(__float_as_uint(mx) >> 16);
+    rec[c] = half_bits<F16>(mn);
+    rec[kHD + c] = half_bits<F16>(mx);
   }
 }
 
 // One wave per block (block <= 64): lane l scores token j*block + l.
+template <bool F16>
 __global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restrict__ key, int kv_heads, int64_t sb,
                                                         int64_t sh, int64_t st, int block, int reps, int t_end,
                                                         int j0, int j_end, int32_t* __restrict__ meta,
@@ -127,7 +136,7 @@ __global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restri
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float lo = __uint_as_float(w[e] << 16), hi = __uint_as_float(w[e] & 0xFFFF0000u);
+        const float lo = half_lo<F16>(w[e]), hi = half_hi<F16>(w[e]);
         acc = acc + lo * lo;
         acc = acc + hi * hi;
       }
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restri
 // Block scores of one row: qbb bound (EV:5554) or best representative
 // (EV:5431-5435; no valid representative -> finfo(float32).min).
 // ---------------------------------------------------------------------------
-template <int KIND>   // 0: qbb, 1: brep
+template <int KIND, bool F16>   // KIND 0: qbb, 1: brep
 __global__ __launch_bounds__(kBT) void block_scores_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, int q_heads, int group, int kv_heads,
     int64_t sb, int64_t sh, int64_t st, const void* __restrict__ meta, int64_t meta_blocks, int reps, int nb,
@@ -167,7 +176,7 @@ __global__ __launch_bounds__(kBT) void block_scores_kernel(
   const int row = blockIdx.y, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
   const int kvrow = b * kv_heads + h / group;
-  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
   __syncthreads();
   rank_dims(q_s, count, sel_idx, sel_q);
   const int j = blockIdx.x * kBT + tid;
@@ -179,7 +188,7 @@ __global__ __launch_bounds__(kBT) void block_scores_kernel(
     for (int s = 0; s < count; ++s) {
       const float qs = sel_q[s];
       const int d = sel_idx[s];
-      const float e = bf16f(qs >= 0.0f ? rec[kHD + d] : rec[d]);
+      const float e = half_to_f32<F16>(qs >= 0.0f ? rec[kHD + d] : rec[d]);
       acc = acc + qs * e;
     }
   } else {
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(kBT) void block_scores_kernel(
       if (tok < 0) continue;
       const uint16_t* kr = kb + static_cast<int64_t>(tok) * st;
       float sc = 0.0f;
-      for (int s = 0; s < count; ++s) sc = sc + sel_q[s] * bf16f(kr[sel_idx[s]]);
+      for (int s = 0; s < count; ++s) sc = sc + sel_q[s] * half_to_f32<F16>(kr[sel_idx[s]]);
       acc = fmaxf(acc, sc);
     }
   }
@@ -203,6 +212,7 @@ __global__ __launch_bounds__(kBT) void block_scores_kernel(
 // dim-major copy: position p of a row is token blocks[p / block] * block +
 // p % block; positions at or past the history score -inf.
 // ---------------------------------------------------------------------------
+template <bool F16>
 __global__ __launch_bounds__(kBT) void scan_partial_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ kdm, int q_heads, int group, int64_t db,
     int64_t dh, int64_t dd, const int32_t* __restrict__ blocks, int n_scan, int block, int history, int count,
@@ -213,7 +223,7 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
   __shared__ float sel_q[kHD];
   const int row = blockIdx.y, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
-  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
   __syncthreads();
   rank_dims(q_s, count, sel_idx, sel_q);
   const int p = blockIdx.x * kBT + tid;
@@ -227,7 +237,7 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
     for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in order
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = bf16f(base[sel_idx[min(s0 + j, count - 1)] * dd]);
+      for (int j = 0; j < 8; ++j) v[j] = half_to_f32<F16>(base[sel_idx[min(s0 + j, count - 1)] * dd]);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (s0 + j < count) acc = acc + sel_q[s0 + j] * v[j];
@@ -236,7 +246,7 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
   out[static_cast<int64_t>(row) * out_ld + p] = acc;
   if (full) {   // the full-D score the rerank ranks its candidates by (every scanned position)
     const bool in = tok >= 0 && tok < history;
-    const float f = in ? full_score(key + b * sb + (h / group) * sh + static_cast<int64_t>(tok) * st, q_s, scaling)
+    const float f = in ? full_score<F16>(key + b * sb + (h / group) * sh + static_cast<int64_t>(tok) * st, q_s, scaling)
                        : -__builtin_huge_valf();
     full[static_cast<int64_t>(row) * out_ld + p] = f;
   }
@@ -251,6 +261,7 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kQboTokens = kBT * 8;
 
+template <bool F16>
 __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ kdm, int q_heads, int group, int64_t db,
     int64_t dh, int64_t dd, int history, int block, int nb, int blocks_per_wg, int count, float* __restrict__ out,
@@ -261,7 +272,7 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
   __shared__ float sc[kQboTokens];
   const int row = blockIdx.y, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
-  for (int d = tid; d < kHD; d += kBT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
   __syncthreads();
   rank_dims(q_s, count, sel_idx, sel_q);
   const int j0 = blockIdx.x * blocks_per_wg, j1 = min(nb, j0 + blocks_per_wg);
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
     for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in order
       float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = bf16f(kt[sel_idx[min(s0 + e, count - 1)] * dd]);
+      for (int e = 0; e < 8; ++e) v[e] = half_to_f32<F16>(kt[sel_idx[min(s0 + e, count - 1)] * dd]);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         if (s0 + e < count) acc = acc + sel_q[s0 + e] * v[e];
@@ -298,7 +309,7 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
 // a kept token lies in a protected range or past the kept count), then the
 // sink range, the recent range and the current token.
 // ---------------------------------------------------------------------------
-template <int VPL1, int VPL2>
+template <int VPL1, int VPL2, bool F16>
 __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     const uint16_t* __restrict__ query, const uint16_t* __restrict__ key, int q_heads, int group, int64_t sb,
     int64_t sh, int64_t st, const float* __restrict__ partial, const float* __restrict__ full, int64_t partial_ld,
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   __shared__ int32_t cand[kMaxCand], cand_pos[kMaxCand];
   const int row = blockIdx.x, tid = threadIdx.x;
   const int b = row / q_heads, h = row - b * q_heads;
-  for (int d = tid; d < kHD; d += kRerankNT) q_s[d] = bf16f(query[static_cast<int64_t>(row) * kHD + d]);
+  for (int d = tid; d < kHD; d += kRerankNT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
   uint8_t* mrow = keep_mask + static_cast<int64_t>(row) * keep_ld;
   for (int t = tid; t < key_count; t += kRerankNT)
     mrow[t] = (t < sink_end) || (t >= recent_start && t < history) || (keep_self && t == history);
@@ -342,7 +353,7 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     const int ci = WS2::pos(i);
     const bool ok = ci < kk1;
     float acc = 0.0f;
-    if (ok) acc = frow ? frow[cand_pos[ci]] : full_score(kb + static_cast<int64_t>(cand[ci]) * st, q_s, scaling);
+    if (ok) acc = frow ? frow[cand_pos[ci]] : full_score<F16>(kb + static_cast<int64_t>(cand[ci]) * st, q_s, scaling);
     ws2.set(i, acc, ok);
   }
   const int kk2 = ws2.run(n_keep, lds.b);
@@ -485,9 +496,11 @@ QKV_EXPORT int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_head
 
 QKV_EXPORT int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, int64_t batch,
                                      int64_t kv_heads, int64_t head_dim, int64_t block, int64_t reps, int64_t t_begin,
-                                     int64_t t_end, void* meta, int64_t meta_blocks, void* stream) {
+                                     int64_t t_end, void* meta, int64_t meta_blocks, int dtype, void* stream) {
   const char* what = "qkv_block_meta_update";
   if (!key || !k_strides || !meta) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  bool f16;
+  if (int rc = half_dtype(dtype, what, &f16)) return rc;
   if (batch <= 0 || kv_heads <= 0 || batch * kv_heads > 65535 || head_dim != kHD)
     return fail(QKV_ERR_INVALID, "%s: need batch, kv_heads > 0 and head_dim 128", what);
   if (block <= 0 || t_begin < 0 || t_end < t_begin || cdiv(t_end, block) > meta_blocks || t_end >= (int64_t(1) << 31))
@@ -498,32 +511,37 @@ QKV_EXPORT int qkv_block_meta_update(int kind, const void* key, const int64_t* k
   const int64_t j0 = t_begin / block, j1 = cdiv(t_end, block);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* k = static_cast<const uint16_t*>(key);
-  if (kind == QKV_BLOCK_QBB) {
-    dim3 grid(static_cast<unsigned>(j1 - j0), static_cast<unsigned>(batch * kv_heads));
-    qbb_meta_kernel<<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2],
-                                          static_cast<int>(block), static_cast<int>(t_end), static_cast<int>(j0),
-                                          static_cast<uint16_t*>(meta), meta_blocks);
-  } else if (kind == QKV_BLOCK_BREP) {
-    if (block > 64 || reps < 1 || reps > block)
-      return fail(QKV_ERR_UNSUPPORTED, "%s: brep needs block <= 64 and 1 <= reps <= block", what);
-    dim3 grid(static_cast<unsigned>(cdiv(j1 - j0, kBT / 64)), static_cast<unsigned>(batch * kv_heads));
-    brep_meta_kernel<<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2],
-                                           static_cast<int>(block), static_cast<int>(reps), static_cast<int>(t_end),
-                                           static_cast<int>(j0), static_cast<int>(j1), static_cast<int32_t*>(meta),
-                                           meta_blocks);
-  } else {
+  if (kind != QKV_BLOCK_QBB && kind != QKV_BLOCK_BREP)
     return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
-  }
-  return check_launch(what);
+  if (kind == QKV_BLOCK_BREP && (block > 64 || reps < 1 || reps > block))
+    return fail(QKV_ERR_UNSUPPORTED, "%s: brep needs block <= 64 and 1 <= reps <= block", what);
+  return with_half(f16, [&](auto ff) {
+    constexpr bool F = decltype(ff)::value;
+    if (kind == QKV_BLOCK_QBB) {
+      dim3 grid(static_cast<unsigned>(j1 - j0), static_cast<unsigned>(batch * kv_heads));
+      qbb_meta_kernel<F><<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1],
+                                               k_strides[2], static_cast<int>(block), static_cast<int>(t_end),
+                                               static_cast<int>(j0), static_cast<uint16_t*>(meta), meta_blocks);
+    } else {
+      dim3 grid(static_cast<unsigned>(cdiv(j1 - j0, kBT / 64)), static_cast<unsigned>(batch * kv_heads));
+      brep_meta_kernel<F><<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1],
+                                                k_strides[2], static_cast<int>(block), static_cast<int>(reps),
+                                                static_cast<int>(t_end), static_cast<int>(j0), static_cast<int>(j1),
+                                                static_cast<int32_t*>(meta), meta_blocks);
+    }
+    return check_launch(what);
+  });
 }
 
 QKV_EXPORT int qkv_block_scores(int kind, const void* query, const void* key, const int64_t* k_strides,
                                 const void* meta, int64_t meta_blocks, int64_t batch, int64_t q_heads,
                                 int64_t kv_heads, int64_t history, int64_t head_dim, int64_t block, int64_t reps,
-                                int64_t dim_count, float* out, int64_t out_ld, void* stream) {
+                                int64_t dim_count, float* out, int64_t out_ld, int dtype, void* stream) {
   const char* what = "qkv_block_scores";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
+  bool f16;
+  if ((rc = half_dtype(dtype, what, &f16))) return rc;
   if (!query || !key || !k_strides || !meta || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
   const int64_t nb = block > 0 ? cdiv(history, block) : 0;
   if (history <= 0 || block <= 0 || nb > meta_blocks || out_ld < nb || history >= (int64_t(1) << 31))
@@ -533,26 +551,32 @@ QKV_EXPORT int qkv_block_scores(int kind, const void* query, const void* key, co
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
   dim3 grid(static_cast<unsigned>(cdiv(nb, kBT)), static_cast<unsigned>(batch * q_heads));
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define QKV_BLOCK_SCORES(K)                                                                                    \
-  block_scores_kernel<K><<<grid, kBT, 0, st>>>(                                                                \
+  if (kind != QKV_BLOCK_QBB && kind != QKV_BLOCK_BREP)
+    return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
+#define QKV_BLOCK_SCORES(K, F)                                                                                 \
+  block_scores_kernel<K, F><<<grid, kBT, 0, st>>>(                                                             \
       static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),       \
       static_cast<int>(q_heads / kv_heads), static_cast<int>(kv_heads), k_strides[0], k_strides[1], k_strides[2], \
       meta, meta_blocks, static_cast<int>(reps), static_cast<int>(nb), count, out, out_ld)
-  if (kind == QKV_BLOCK_QBB) QKV_BLOCK_SCORES(0);
-  else if (kind == QKV_BLOCK_BREP) QKV_BLOCK_SCORES(1);
-  else return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
+  return with_half(f16, [&](auto ff) {
+    constexpr bool F = decltype(ff)::value;
+    if (kind == QKV_BLOCK_QBB) QKV_BLOCK_SCORES(0, F);
+    else QKV_BLOCK_SCORES(1, F);
+    return check_launch(what);
+  });
 #undef QKV_BLOCK_SCORES
-  return check_launch(what);
 }
 
 QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                                      const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
                                      int64_t kv_heads, int64_t history, int64_t head_dim, const int32_t* blocks,
                                      int64_t n_scan, int64_t block, int64_t dim_count, float scaling, float* out,
-                                     float* full, int64_t out_ld, void* stream) {
+                                     float* full, int64_t out_ld, int dtype, void* stream) {
   const char* what = "qkv_block_scan_scores";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
+  bool f16;
+  if ((rc = half_dtype(dtype, what, &f16))) return rc;
   if (!query || !key_dim_major || !kdm_strides || !blocks || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
   if (history <= 0 || block <= 0 || n_scan <= 0 || n_scan * block >= (int64_t(1) << 30) || out_ld < n_scan * block)
     return fail(QKV_ERR_INVALID, "%s: need history, block, n_scan > 0 and out_ld >= n_scan * block", what);
@@ -562,22 +586,26 @@ QKV_EXPORT int qkv_block_scan_scores(const void* query, const void* key_dim_majo
     return fail(QKV_ERR_INVALID, "%s: K rows must be contiguous and 16-byte aligned", what);
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
   dim3 grid(static_cast<unsigned>(cdiv(n_scan * block, kBT)), static_cast<unsigned>(batch * q_heads));
-  scan_partial_kernel<<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
-      static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], blocks,
-      static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld,
-      static_cast<const uint16_t*>(key), full ? k_strides[0] : 0, full ? k_strides[1] : 0, full ? k_strides[2] : 0,
-      scaling, full);
-  return check_launch(what);
+  return with_half(f16, [&](auto ff) {
+    scan_partial_kernel<decltype(ff)::value><<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
+        static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], blocks,
+        static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history), count, out, out_ld,
+        static_cast<const uint16_t*>(key), full ? k_strides[0] : 0, full ? k_strides[1] : 0,
+        full ? k_strides[2] : 0, scaling, full);
+    return check_launch(what);
+  });
 }
 
 QKV_EXPORT int qkv_block_max_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                                             int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
                                             int64_t head_dim, int64_t block, int64_t dim_count, float* out,
-                                            int64_t out_ld, void* stream) {
+                                            int64_t out_ld, int dtype, void* stream) {
   const char* what = "qkv_block_max_partial_scores";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
+  bool f16;
+  if ((rc = half_dtype(dtype, what, &f16))) return rc;
   if (!query || !key_dim_major || !kdm_strides || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
   const int64_t nb = block > 0 ? cdiv(history, block) : 0;
   if (history <= 0 || history >= (int64_t(1) << 31) || block <= 0 || out_ld < nb)
@@ -587,11 +615,14 @@ QKV_EXPORT int qkv_block_max_partial_scores(const void* query, const void* key_d
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
   const int64_t per_wg = std::max<int64_t>(1, kQboTokens / block);
   dim3 grid(static_cast<unsigned>(cdiv(nb, per_wg)), static_cast<unsigned>(batch * q_heads));
-  block_max_partial_kernel<<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
-      static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2], static_cast<int>(history),
-      static_cast<int>(block), static_cast<int>(nb), static_cast<int>(per_wg), count, out, out_ld);
-  return check_launch(what);
+  return with_half(f16, [&](auto ff) {
+    block_max_partial_kernel<decltype(ff)::value><<<grid, kBT, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key_dim_major), static_cast<int>(q_heads),
+        static_cast<int>(q_heads / kv_heads), kdm_strides[0], kdm_strides[1], kdm_strides[2],
+        static_cast<int>(history), static_cast<int>(block), static_cast<int>(nb), static_cast<int>(per_wg), count,
+        out, out_ld);
+    return check_launch(what);
+  });
 }
 
 QKV_EXPORT int qkv_brep_partial_scores(const float* query, const void* key_history, const int64_t* rep_indices,
@@ -643,10 +674,12 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
                                 const float* partial, const float* full, int64_t partial_ld, const int32_t* blocks,
                                 int64_t n_scan, int64_t block, int64_t n_cand, int64_t n_keep, int64_t protect_sink,
                                 int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
-                                int64_t keep_ld, int32_t* attn_ids, int64_t n_out, void* stream) {
+                                int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int dtype, void* stream) {
   const char* what = "qkv_block_rerank";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
+  bool f16;
+  if ((rc = half_dtype(dtype, what, &f16))) return rc;
   if (!query || !key || !k_strides || !partial || !blocks || !keep_mask || !attn_ids)
     return fail(QKV_ERR_INVALID, "%s: null pointer", what);
   const int64_t history = key_count - 1;
@@ -669,7 +702,9 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_scan_vpl(n_scan * block, [&](auto vpl) {
    return with_cand_vpl(n_cand, [&](auto vpl2) {
-    rerank_kernel<decltype(vpl)::value, decltype(vpl2)::value><<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
+    return with_half(f16, [&](auto ff) {
+    rerank_kernel<decltype(vpl)::value, decltype(vpl2)::value, decltype(ff)::value>
+        <<<static_cast<unsigned>(batch * q_heads), kRerankNT, 0, st>>>(
         static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),
         static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], partial, full, partial_ld,
         blocks,
@@ -678,6 +713,7 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
         static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec), keep_self ? 1 : 0,
         scaling, keep_mask, keep_ld, attn_ids, static_cast<int>(n_out));
     return check_launch(what);
+    });
    });
   });
 }

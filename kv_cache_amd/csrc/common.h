@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/qkv.h"
 
@@ -20,6 +21,24 @@ int check_launch(const char* what);
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Resolves the dtype of a 16-bit operand (query, K, V): sets *f16 (false for
+// bf16, true for fp16) and returns QKV_OK, or fails for fp32 and unknown codes.
+inline int half_dtype(int dtype, const char* what, bool* f16) {
+  if (dtype == QKV_DTYPE_BF16 || dtype == QKV_DTYPE_FP16) {
+    *f16 = dtype == QKV_DTYPE_FP16;
+    return QKV_OK;
+  }
+  return fail(dtype == QKV_DTYPE_FP32 ? QKV_ERR_UNSUPPORTED : QKV_ERR_INVALID,
+              "%s: dtype %d is not bf16 (%d) or fp16 (%d)", what, dtype, QKV_DTYPE_BF16, QKV_DTYPE_FP16);
+}
+
+// Calls f(std::integral_constant<bool, f16>{}) and returns its result: one
+// template instantiation per 16-bit dtype.
+template <typename F>
+int with_half(bool f16, F&& f) {
+  return f16 ? f(std::integral_constant<bool, true>{}) : f(std::integral_constant<bool, false>{});
+}
+
 // ---------------------------------------------------------------------------
 // Device helpers
 // ---------------------------------------------------------------------------
@@ -31,6 +50,24 @@ __device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w &
 __device__ __forceinline__ float f16bits_to_f32(uint32_t bits16) {
   _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16));
   return static_cast<float>(h);
+}
+
+// The 16-bit floats of q, K and V: bf16 (F16 = false) or fp16 (F16 = true),
+// widened to fp32 exactly -- one value, or the low / high half of a word.
+template <bool F16>
+__device__ __forceinline__ float half_to_f32(uint32_t bits16) {
+  if constexpr (F16) return f16bits_to_f32(bits16 & 0xFFFFu);
+  else return bf16_to_f32(bits16 & 0xFFFFu);
+}
+template <bool F16>
+__device__ __forceinline__ float half_lo(uint32_t w) {
+  if constexpr (F16) return f16bits_to_f32(w & 0xFFFFu);
+  else return bf16lo(w);
+}
+template <bool F16>
+__device__ __forceinline__ float half_hi(uint32_t w) {
+  if constexpr (F16) return f16bits_to_f32(w >> 16);
+  else return bf16hi(w);
 }
 
 // fp32 -> fp16 round-to-nearest-even (v_cvt_f16_f32 in the default mode), with

@@ -33,11 +33,13 @@ __device__ __forceinline__ uint64_t fp16_fixed24(uint32_t bits) {
   return static_cast<uint64_t>(1024u + m) << (e - 1);
 }
 
-__device__ __forceinline__ void bf16x8(const uint4& raw, float* x) {
-  x[0] = bf16lo(raw.x); x[1] = bf16hi(raw.x);
-  x[2] = bf16lo(raw.y); x[3] = bf16hi(raw.y);
-  x[4] = bf16lo(raw.z); x[5] = bf16hi(raw.z);
-  x[6] = bf16lo(raw.w); x[7] = bf16hi(raw.w);
+// Eight bf16 (or, with F16, fp16) channels of a 16-byte load, widened exactly.
+template <bool F16>
+__device__ __forceinline__ void halfx8(const uint4& raw, float* x) {
+  x[0] = half_lo<F16>(raw.x); x[1] = half_hi<F16>(raw.x);
+  x[2] = half_lo<F16>(raw.y); x[3] = half_hi<F16>(raw.y);
+  x[4] = half_lo<F16>(raw.z); x[5] = half_hi<F16>(raw.z);
+  x[6] = half_lo<F16>(raw.w); x[7] = half_hi<F16>(raw.w);
 }
 
 // Quantizes 8 values against the group amax `a` (already reduced) and packs
@@ -57,7 +59,7 @@ __device__ __forceinline__ uint32_t quantize8(const float* x, float a, uint32_t*
 // ---------------------------------------------------------------------------
 // Pack: one thread per 8 channels of a token; GROUP/8 lanes share a scale.
 // ---------------------------------------------------------------------------
-template <int GROUP>
+template <int GROUP, bool F16>
 __global__ __launch_bounds__(kThreads) void pack_kernel(
     const uint16_t* __restrict__ key, int64_t ksb, int64_t ksh, int64_t kst, int kv_heads,
     int t_begin, int ntok, int head_dim, uint8_t* __restrict__ packed,
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
   uint4 raw = make_uint4(0, 0, 0, 0);
   if (active) raw = *reinterpret_cast<const uint4*>(key + b * ksb + h * ksh + t * kst + c8 * 8);
   float x[8];
-  bf16x8(raw, x);
+  halfx8<F16>(raw, x);
   float a = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(x[i]));
@@ -181,7 +183,7 @@ __device__ __forceinline__ int64_t slab_offset(int64_t t, int x) {
   const int b = (k - lane * KPLN) * (S / 2) + x;
   return tile * 4096 + (64 * (b >> 4) + lane) * 16 + (b & 15);
 }
-template <int S>
+template <int S, bool F16>
 __global__ __launch_bounds__(kThreads) void build_slab_kernel(
     const uint16_t* __restrict__ key, int64_t ksb, int64_t ksh, int64_t kst, int kv_heads,
     int t_begin, int ntok, int head_dim, const int32_t* __restrict__ chan_idx,
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void build_slab_kernel(
   for (int i = 0; i < 8; ++i) {
     // channel ids come from qkv_int4_select_channels; clamping keeps a bad id in the row
     const int c = min(max(active ? idx[i] : 0, 0), head_dim - 1);
-    x[i] = active ? bf16_to_f32(row[c]) : 0.0f;
+    x[i] = active ? half_to_f32<F16>(row[c]) : 0.0f;
   }
   float a = 0.0f;
 #pragma unroll
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void build_slab_kernel(
 }
 
 // The row's query words as a table: qwords[2d] = qlo[d], qwords[2d+1] = qhi[d].
-template <int S>
+template <int S, bool F16>
 __global__ __launch_bounds__(64) void query_words_kernel(
     const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
     const int32_t* __restrict__ chan_idx, uint32_t* __restrict__ qwords, float* __restrict__ qscale_out) {
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(64) void query_words_kernel(
   uint32_t qlo[S / 8], qhi[S / 8];
   float qs;
   const RowQueryLoads<S> ql = row_query_load<S>(query, q_heads, kv_heads, head_dim, chan_idx, r);
-  row_query_finish<S>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
+  row_query_finish<S, F16>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
   uint32_t* out = qwords + static_cast<int64_t>(r) * (S / 4);
 #pragma unroll
   for (int d = 0; d < S / 8; ++d) {
@@ -237,25 +239,25 @@ __global__ __launch_bounds__(64) void query_words_kernel(
   if (qscale_out && lane == 0) qscale_out[r] = qs;
 }
 
-template <int S, bool DEBUG>
+template <int S, bool DEBUG, bool F16>
 __global__ __launch_bounds__(kScoreThreads) void decode_scores_kernel(
     const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
     const int32_t* __restrict__ chan_idx, const uint8_t* __restrict__ slab,
     const uint16_t* __restrict__ slab_scales, int64_t capacity, int tokens, int block,
     int chunk, float* __restrict__ bmax, int nb, int32_t* __restrict__ isum,
     float* __restrict__ keys_out, float* __restrict__ qscale_out) {
-  score_chunk<S, DEBUG>(query, q_heads, kv_heads, head_dim, chan_idx, slab, slab_scales, capacity, tokens,
+  score_chunk<S, DEBUG, F16>(query, q_heads, kv_heads, head_dim, chan_idx, slab, slab_scales, capacity, tokens,
                                block, chunk, bmax, nb, isum, keys_out, qscale_out, blockIdx.y, blockIdx.x);
 }
 
-template <bool DEBUG>
+template <bool DEBUG, bool F16>
 int launch_scores(int S, dim3 grid, hipStream_t st, const uint16_t* q, int hq, int hkv, int d,
                   const int32_t* ci, const uint8_t* slab, const uint16_t* ss, int64_t cap, int T,
                   int block, int chunk, float* bmax, int nb, int32_t* isum, float* keys, float* qs) {
   switch (S) {
 #define QKV_CASE(SS)                                                                               \
   case SS:                                                                                         \
-    decode_scores_kernel<SS, DEBUG><<<grid, kScoreThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
+    decode_scores_kernel<SS, DEBUG, F16><<<grid, kScoreThreads, 0, st>>>(q, hq, hkv, d, ci, slab, ss, cap, T, \
                                                                block, chunk, bmax, nb, isum, keys, \
                                                                qs);                                \
     break;
@@ -276,8 +278,10 @@ using namespace qkv;
 QKV_EXPORT int qkv_int4_pack_k(const void* key, const int64_t* k_strides, int64_t batch,
                                int64_t kv_heads, int64_t t_begin, int64_t t_end, int64_t head_dim,
                                int64_t group, uint8_t* packed, uint16_t* scales, int64_t capacity,
-                               void* stream) {
+                               int dtype, void* stream) {
   if (!key || !k_strides || !packed || !scales) return fail(QKV_ERR_INVALID, "qkv_int4_pack_k: null pointer");
+  bool f16;
+  if (int rc = half_dtype(dtype, "qkv_int4_pack_k", &f16)) return rc;
   if (batch <= 0 || kv_heads <= 0 || t_begin < 0 || t_end < t_begin || t_end > capacity)
     return fail(QKV_ERR_INVALID, "qkv_int4_pack_k: bad token range [%lld, %lld) for capacity %lld",
                 (long long)t_begin, (long long)t_end, (long long)capacity);
@@ -295,14 +299,20 @@ QKV_EXPORT int qkv_int4_pack_k(const void* key, const int64_t* k_strides, int64_
   dim3 grid(static_cast<unsigned>(cdiv(total, kThreads)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* k = static_cast<const uint16_t*>(key);
-#define QKV_PACK(GG)                                                                                  \
-  pack_kernel<GG><<<grid, kThreads, 0, st>>>(k, k_strides[0], k_strides[1], k_strides[2],            \
-                                             static_cast<int>(kv_heads), static_cast<int>(t_begin),  \
-                                             static_cast<int>(ntok), static_cast<int>(head_dim),     \
-                                             packed, scales, capacity, total)
-  if (group == 32) QKV_PACK(32);
-  else if (group == 64) QKV_PACK(64);
-  else QKV_PACK(128);
+#define QKV_PACK(GG, FF)                                                                              \
+  pack_kernel<GG, FF><<<grid, kThreads, 0, st>>>(k, k_strides[0], k_strides[1], k_strides[2],        \
+                                                 static_cast<int>(kv_heads), static_cast<int>(t_begin), \
+                                                 static_cast<int>(ntok), static_cast<int>(head_dim),  \
+                                                 packed, scales, capacity, total)
+  if (f16) {
+    if (group == 32) QKV_PACK(32, true);
+    else if (group == 64) QKV_PACK(64, true);
+    else QKV_PACK(128, true);
+  } else {
+    if (group == 32) QKV_PACK(32, false);
+    else if (group == 64) QKV_PACK(64, false);
+    else QKV_PACK(128, false);
+  }
 #undef QKV_PACK
   return check_launch("qkv_int4_pack_k");
 }
@@ -343,9 +353,11 @@ QKV_EXPORT int qkv_int4_build_slab(const void* key, const int64_t* k_strides, in
                                    int64_t kv_heads, int64_t t_begin, int64_t t_end,
                                    int64_t head_dim, const int32_t* chan_idx, int64_t selected,
                                    uint8_t* slab, uint16_t* slab_scales, int64_t capacity,
-                                   void* stream) {
+                                   int dtype, void* stream) {
   if (!key || !k_strides || !chan_idx || !slab || !slab_scales)
     return fail(QKV_ERR_INVALID, "qkv_int4_build_slab: null pointer");
+  bool f16;
+  if (int rc = half_dtype(dtype, "qkv_int4_build_slab", &f16)) return rc;
   if (batch <= 0 || kv_heads <= 0 || t_begin < 0 || t_end < t_begin || t_end > capacity)
     return fail(QKV_ERR_INVALID, "qkv_int4_build_slab: bad token range");
   if (selected != 16 && selected != 32 && selected != 64 && selected != 128)
@@ -360,18 +372,20 @@ QKV_EXPORT int qkv_int4_build_slab(const void* key, const int64_t* k_strides, in
   dim3 grid(static_cast<unsigned>(cdiv(total, kThreads)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* k = static_cast<const uint16_t*>(key);
-#define QKV_SLAB(SS)                                                                                 \
-  build_slab_kernel<SS><<<grid, kThreads, 0, st>>>(k, k_strides[0], k_strides[1], k_strides[2],     \
-                                                   static_cast<int>(kv_heads), static_cast<int>(t_begin), \
-                                                   static_cast<int>(ntok), static_cast<int>(head_dim),   \
-                                                   chan_idx, slab, slab_scales,                        \
-                                                   capacity, total)
-  switch (selected) {
-    case 16: QKV_SLAB(16); break;
-    case 32: QKV_SLAB(32); break;
-    case 64: QKV_SLAB(64); break;
-    default: QKV_SLAB(128); break;
+#define QKV_SLAB(SS, FF)                                                                             \
+  build_slab_kernel<SS, FF><<<grid, kThreads, 0, st>>>(k, k_strides[0], k_strides[1], k_strides[2], \
+                                                       static_cast<int>(kv_heads), static_cast<int>(t_begin), \
+                                                       static_cast<int>(ntok), static_cast<int>(head_dim), \
+                                                       chan_idx, slab, slab_scales, capacity, total)
+#define QKV_SLAB_ALL(FF)                  \
+  switch (selected) {                     \
+    case 16: QKV_SLAB(16, FF); break;     \
+    case 32: QKV_SLAB(32, FF); break;     \
+    case 64: QKV_SLAB(64, FF); break;     \
+    default: QKV_SLAB(128, FF); break;    \
   }
+  if (f16) QKV_SLAB_ALL(true) else QKV_SLAB_ALL(false)
+#undef QKV_SLAB_ALL
 #undef QKV_SLAB
   return check_launch("qkv_int4_build_slab");
 }
@@ -393,20 +407,28 @@ static int check_query(const void* query, int64_t batch, int64_t q_heads, int64_
 
 QKV_EXPORT int qkv_int4_query_words(const void* query, int64_t batch, int64_t q_heads,
                                     int64_t kv_heads, int64_t head_dim, const int32_t* chan_idx,
-                                    int64_t selected, uint32_t* qwords, float* qscale, void* stream) {
+                                    int64_t selected, uint32_t* qwords, float* qscale, int dtype,
+                                    void* stream) {
   if (int rc = check_query(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected, "qkv_int4_query_words"))
     return rc;
+  bool f16;
+  if (int rc = half_dtype(dtype, "qkv_int4_query_words", &f16)) return rc;
   if (!qwords) return fail(QKV_ERR_INVALID, "qkv_int4_query_words: null qwords pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = static_cast<unsigned>(batch * kv_heads);
   const uint16_t* q = static_cast<const uint16_t*>(query);
   const int hq = static_cast<int>(q_heads), hkv = static_cast<int>(kv_heads), hd = static_cast<int>(head_dim);
-  switch (selected) {
-    case 16: query_words_kernel<16><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
-    case 32: query_words_kernel<32><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
-    case 64: query_words_kernel<64><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
-    default: query_words_kernel<128><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale); break;
+#define QKV_QW(SS, FF) query_words_kernel<SS, FF><<<grid, 64, 0, st>>>(q, hq, hkv, hd, chan_idx, qwords, qscale)
+#define QKV_QW_ALL(FF)                \
+  switch (selected) {                 \
+    case 16: QKV_QW(16, FF); break;   \
+    case 32: QKV_QW(32, FF); break;   \
+    case 64: QKV_QW(64, FF); break;   \
+    default: QKV_QW(128, FF); break;  \
   }
+  if (f16) QKV_QW_ALL(true) else QKV_QW_ALL(false)
+#undef QKV_QW_ALL
+#undef QKV_QW
   return check_launch("qkv_int4_query_words");
 }
 
@@ -415,10 +437,12 @@ QKV_EXPORT int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t 
                                       int64_t selected, const uint8_t* slab,
                                       const uint16_t* slab_scales, int64_t capacity, int64_t tokens,
                                       int64_t block, float* bmax, int32_t* isum, float* keys,
-                                      float* qscale, void* stream) {
+                                      float* qscale, int dtype, void* stream) {
   if (int rc = check_query(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected,
                            "qkv_int4_decode_scores"))
     return rc;
+  bool f16;
+  if (int rc = half_dtype(dtype, "qkv_int4_decode_scores", &f16)) return rc;
   if (!slab || !slab_scales) return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: null slab pointer");
   if (!bmax && !(isum && keys))
     return fail(QKV_ERR_INVALID, "qkv_int4_decode_scores: need bmax or both isum and keys");
@@ -443,11 +467,15 @@ QKV_EXPORT int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* q = static_cast<const uint16_t*>(query);
   const int hq = static_cast<int>(q_heads), hkv = static_cast<int>(kv_heads), hd = static_cast<int>(head_dim);
-  if (isum)
-    return launch_scores<true>(static_cast<int>(selected), grid, st, q, hq, hkv, hd, chan_idx, slab, slab_scales,
-                               capacity, static_cast<int>(tokens), static_cast<int>(block),
-                               static_cast<int>(chunk), bmax, nb, isum, keys, qscale);
-  return launch_scores<false>(static_cast<int>(selected), grid, st, q, hq, hkv, hd, chan_idx, slab, slab_scales,
-                              capacity, static_cast<int>(tokens), static_cast<int>(block),
-                              static_cast<int>(chunk), bmax, nb, nullptr, nullptr, qscale);
+#define QKV_SC(DBG, FF, IS, KS)                                                                      \
+  return launch_scores<DBG, FF>(static_cast<int>(selected), grid, st, q, hq, hkv, hd, chan_idx, slab,  \
+                                slab_scales, capacity, static_cast<int>(tokens), static_cast<int>(block), \
+                                static_cast<int>(chunk), bmax, nb, IS, KS, qscale)
+  if (isum) {
+    if (f16) QKV_SC(true, true, isum, keys);
+    QKV_SC(true, false, isum, keys);
+  }
+  if (f16) QKV_SC(false, true, nullptr, nullptr);
+  QKV_SC(false, false, nullptr, nullptr);
+#undef QKV_SC
 }

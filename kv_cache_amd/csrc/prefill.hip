@@ -67,6 +67,7 @@ static_assert(perm_inverts(), "perm_channel inverts perm_slot");
 // ---------------------------------------------------------------------------
 constexpr int kQRows = 8;
 
+template <bool F16>
 __global__ __launch_bounds__(256) void prefill_query_kernel(const uint16_t* __restrict__ q, int64_t q_row_stride,
                                                             int64_t rows, int8_t* __restrict__ q8,
                                                             float* __restrict__ qscale) {
@@ -78,8 +79,8 @@ __global__ __launch_bounds__(256) void prefill_query_kernel(const uint16_t* __re
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) {
     const uint16_t* qr = q + min(row0 + r, rows - 1) * q_row_stride;
-    x0[r] = __uint_as_float(static_cast<uint32_t>(qr[ca]) << 16);
-    x1[r] = __uint_as_float(static_cast<uint32_t>(qr[cb]) << 16);
+    x0[r] = half_to_f32<F16>(qr[ca]);
+    x1[r] = half_to_f32<F16>(qr[cb]);
   }
 #pragma unroll
   for (int r = 0; r < kQRows; ++r) {
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(256) void prefill_query_kernel(const uint16_t* __re
 // DPP reduction within the row of 16 lanes.  kQVRows rows per wave.
 constexpr int kQVRows = 4;
 
+template <bool F16>
 __global__ __launch_bounds__(256) void prefill_query_vec_kernel(const uint16_t* __restrict__ q,
                                                                 int64_t q_row_stride, int64_t rows,
                                                                 int8_t* __restrict__ q8,
@@ -124,8 +126,8 @@ __global__ __launch_bounds__(256) void prefill_query_vec_kernel(const uint16_t* 
     const uint32_t ws[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[2 * e] = bf16lo(ws[e]);
-      x[2 * e + 1] = bf16hi(ws[e]);
+      x[2 * e] = half_lo<F16>(ws[e]);
+      x[2 * e + 1] = half_hi<F16>(ws[e]);
     }
     float a = fabsf(x[0]);
 #pragma unroll
@@ -442,22 +444,27 @@ __global__ __launch_bounds__(64 * W, 8 / W) void prefill_scores_kernel(
 using namespace qkv;
 
 QKV_EXPORT int qkv_prefill_quantize_query(const void* query, int64_t rows, int64_t head_dim,
-                                          int64_t row_stride, int8_t* q8, float* qscale, void* stream) {
+                                          int64_t row_stride, int8_t* q8, float* qscale, int dtype, void* stream) {
   if (!query || !q8) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: null pointer");
+  bool f16;
+  if (int rc = half_dtype(dtype, "qkv_prefill_quantize_query", &f16)) return rc;
   if (head_dim != kD) return fail(QKV_ERR_UNSUPPORTED, "qkv_prefill_quantize_query: head_dim must be 128");
   if (rows <= 0 || row_stride < head_dim || row_stride % 2 || !aligned(query, 4))
     return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: bad rows or row stride");
   if (!aligned(q8, 2)) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: q8 must be 2-byte aligned");
   if (cdiv(rows, 4 * kQRows) > 0x7FFFFFFF) return fail(QKV_ERR_INVALID, "qkv_prefill_quantize_query: too many rows");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (row_stride % 8 == 0 && aligned(query, 16) && aligned(q8, 8)) {
-    prefill_query_vec_kernel<<<static_cast<unsigned>(cdiv(rows, 4 * kQVRows)), 256, 0, st>>>(
-        static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
+  const bool vec = row_stride % 8 == 0 && aligned(query, 16) && aligned(q8, 8);
+  return with_half(f16, [&](auto ff) {
+    constexpr bool F = decltype(ff)::value;
+    if (vec)
+      prefill_query_vec_kernel<F><<<static_cast<unsigned>(cdiv(rows, 4 * kQVRows)), 256, 0, st>>>(
+          static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
+    else
+      prefill_query_kernel<F><<<static_cast<unsigned>(cdiv(rows, 4 * kQRows)), 256, 0, st>>>(
+          static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
     return check_launch("qkv_prefill_quantize_query");
-  }
-  prefill_query_kernel<<<static_cast<unsigned>(cdiv(rows, 4 * kQRows)), 256, 0, st>>>(
-      static_cast<const uint16_t*>(query), row_stride, rows, q8, qscale);
-  return check_launch("qkv_prefill_quantize_query");
+  });
 }
 
 QKV_EXPORT int qkv_prefill_block_scores(const int8_t* q8, int64_t batch, int64_t q_heads,

@@ -81,7 +81,7 @@ template <> struct LaneScales<8> {
   __device__ uint32_t get(int i) const { return (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu; }
 };
 
-// Per-row int8 query of decode scoring, computed by one wave: q8[s] =
+// Per-row int8 query of decode scoring (q bf16, or fp16 with F16), computed by one wave: q8[s] =
 // rint(qg[s] / (amax/127)), qg the fp32 sum of the row's G query heads over
 // its channels in head order, amax = max |qg|.  Code dword d of a key holds
 // channels 8d..8d+7 (channel 8d+i in nibble i), so qlo[d] packs the int8
@@ -123,7 +123,7 @@ __device__ __forceinline__ RowQueryLoads<S> row_query_load(const uint16_t* __res
   return L;
 }
 
-template <int S>
+template <int S, bool F16>
 __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, const uint16_t* __restrict__ query,
                                                  int q_heads, int kv_heads, int head_dim, int r,
                                                  uint32_t (&qlo)[S / 8], uint32_t (&qhi)[S / 8],
@@ -139,8 +139,8 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
 #pragma unroll
   for (int i = 0; i < kQPre; ++i) {
     if (i < G) {
-      lo = lo + bf16lo(L.w[i]);
-      hi = hi + bf16hi(L.w[i]);
+      lo = lo + half_lo<F16>(L.w[i]);
+      hi = hi + half_hi<F16>(L.w[i]);
     }
   }
   if (lane >= hd2) lo = hi = 0.0f;   // no channel pair: never picked
@@ -150,8 +150,8 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
         query + (static_cast<int64_t>(b) * q_heads + j * G) * head_dim);
     for (int i = kQPre; i < G; ++i) {
       const uint32_t w = qrow[i * hd2 + lane];
-      lo = lo + bf16lo(w);
-      hi = hi + bf16hi(w);
+      lo = lo + half_lo<F16>(w);
+      hi = hi + half_hi<F16>(w);
     }
   }
   // qg of channel c, read from lane c/2 (ds_bpermute reads only lanes that
@@ -194,7 +194,7 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
 // Scores chunk `bx` of row r (keys [bx*chunk, min(tokens, (bx+1)*chunk)))
 // in one workgroup of kScoreWaves waves, writing its block maxima to bmax
 // and, with DEBUG, every key's int32 sum and fp32 key.
-template <int S, bool DEBUG>
+template <int S, bool DEBUG, bool F16>
 __device__ __forceinline__ void score_chunk(
     const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
     const int32_t* __restrict__ chan_idx, const uint8_t* __restrict__ slab,
@@ -246,7 +246,7 @@ __device__ __forceinline__ void score_chunk(
 
   uint32_t qlo[DW], qhi[DW];
   float qs;
-  row_query_finish<S>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
+  row_query_finish<S, F16>(ql, query, q_heads, kv_heads, head_dim, r, qlo, qhi, &qs);
   if (qscale_out && bx == 0 && wave == 0 && lane == 0) qscale_out[r] = qs;
 
   const float ninf = -__builtin_huge_valf();

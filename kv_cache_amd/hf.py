@@ -9,7 +9,7 @@ auxiliary K copy (dim-major bf16) that it grows by one column per decode step
 ``int4.Int4KCache``: after prefill the packed K, the static channel subset and
 the subset slab are built once; every later token is quantized into them in
 place (``int4_pack_k`` / ``build_slab`` over ``[t, t+1)``) as HF appends it to
-the bf16 cache.  K/V live in preallocated buffers of a fixed capacity, so no
+the bf16 (or fp16) cache.  K/V live in preallocated buffers of a fixed capacity, so no
 step reallocates or copies the history.
 
 Use:
@@ -66,7 +66,7 @@ _LAYERS: "weakref.WeakValueDictionary[int, Int4CacheLayer]" = weakref.WeakValueD
 
 
 class Int4CacheLayer:
-    """One layer's bf16 K/V in preallocated buffers plus its int4 structures."""
+    """One layer's K/V (bf16 or fp16) in preallocated buffers plus its int4 structures."""
 
     is_sliding = False
     is_compileable = False
@@ -133,8 +133,8 @@ class Int4CacheLayer:
     # -- int4 structures ---------------------------------------------------
     def build_int4(self) -> None:
         """Pack the cached tokens, choose the channel subset, build the slab."""
-        if self.keys.dtype != torch.bfloat16:
-            raise RuntimeError("the int4 path needs bfloat16 K/V")
+        if self.keys.dtype not in (torch.bfloat16, torch.float16):
+            raise RuntimeError(f"the int4 path needs bfloat16 or float16 K/V, got {self.keys.dtype}")
         t = self.length
         packed, scales = K.int4_pack_k(self._k, self.group, capacity=self.capacity, t_end=t)
         chan, _ = K.select_channels(packed, scales, t, self.group, self.selected)
@@ -298,8 +298,9 @@ def register_mode(mode: str, capacity: int, *, name: str | None = None, **step_k
         b, hq, _, d = query.shape
         hkv = key.size(1)
         step = steps.get(module)
-        if step is None or (step.batch, step.q_heads, step.kv_heads, step.head_dim) != (b, hq, hkv, d):
-            step = cls(mode, b, hq, hkv, d, capacity, device=query.device, **step_kwargs)
+        if (step is None or (step.batch, step.q_heads, step.kv_heads, step.head_dim) != (b, hq, hkv, d)
+                or step.dtype != query.dtype):
+            step = cls(mode, b, hq, hkv, d, capacity, device=query.device, **{**step_kwargs, "dtype": query.dtype})
             steps[module] = step
         scaling = d ** -0.5 if scaling is None else float(scaling)
         out = step(query[:, :, 0, :], key, value, scaling)

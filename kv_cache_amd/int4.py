@@ -4,7 +4,7 @@ The path (no int4 counterpart in the reference; its fp32 equivalent is the
 ``qabs{S}cand{pct}attn`` / ``qboracle`` decode of evaluate_qwen3_top2_head_
 limit3_ppl.py:4400-4502 and 5008-5097):
 
-1. ``int4_pack_k``      -- K bf16 -> symmetric int4, fp16 scale per group.
+1. ``int4_pack_k``      -- K (bf16 or fp16) -> symmetric int4, fp16 scale per group.
 2. ``select_channels``  -- per KV head, the S channels of largest mean |K|.
 3. ``build_slab``       -- those S channels re-quantized as one int4 group:
                            the S/2 + 2 bytes per token that decode scoring streams
@@ -14,11 +14,12 @@ limit3_ppl.py:4400-4502 and 5008-5097):
                            (``query_words`` exposes the int8 query alone).
 5. ``block_topk``       -- top-k blocks, lowest index wins ties, ascending.
 6. ``sparse_attention`` -- every query head of a KV head attends over the
-                           selected blocks of bf16 K/V.
+                           selected blocks of K/V.
 
 All tensors live on the GPU; every function launches on the current stream
 and raises ``RuntimeError`` on bad input or a missing library (there is no
-CPU fallback).  Layouts: K/V [B, Hkv, T, D] bf16 with contiguous channels;
+CPU fallback).  Layouts: K/V [B, Hkv, T, D] with contiguous channels, in
+bf16 or fp16 (the query, K, V and the attention output share one dtype);
 packed/slab tensors [B, Hkv, capacity, ...] with capacity a multiple of 512
 (the slab's [B, Hkv, capacity, S/2] bytes hold the swizzled tile layout, so
 the per-key view of it is not meaningful without un-swizzling).
@@ -46,11 +47,28 @@ def _require(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
-def _check_kv(name: str, t: torch.Tensor) -> None:
+def _check_kv(name: str, t: torch.Tensor) -> int:
+    """Checks a K/V tensor; returns its dtype code."""
     _require(t.is_cuda, f"{name} must be CUDA")
-    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16")
+    code = _lib.half_code(name, t)
     _require(t.dim() == 4, f"{name} must have shape [batch, kv_heads, tokens, dim]")
     _require(t.stride(3) == 1, f"{name} channels must be contiguous")
+    return code
+
+
+def _check_query(query: torch.Tensor) -> int:
+    _require(query.is_cuda and query.dim() == 3, "query must be CUDA [B,Hq,D]")
+    return _lib.half_code("query", query)
+
+
+def _check_qkv(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> int:
+    code = _check_kv("key", key)
+    _check_kv("value", value)
+    _check_query(query)
+    _require(query.dtype == key.dtype == value.dtype,
+             f"query, key and value must share one dtype (got {query.dtype}, {key.dtype}, {value.dtype})")
+    _require(key.stride() == value.stride() and key.shape == value.shape, "key/value layout mismatch")
+    return code
 
 
 def int4_pack_k(key: torch.Tensor, group: int, *, capacity: int | None = None,
@@ -59,7 +77,7 @@ def int4_pack_k(key: torch.Tensor, group: int, *, capacity: int | None = None,
     """Quantize tokens [t_begin, t_end) of K into (packed uint8 [B,Hkv,cap,D/2],
     scales fp16 [B,Hkv,cap,D/group]); existing outputs are written in place."""
     lib = _lib.load()
-    _check_kv("key", key)
+    code = _check_kv("key", key)
     b, h, t, d = key.shape
     t_end = t if t_end is None else int(t_end)
     if packed is None or scales is None:
@@ -72,7 +90,7 @@ def int4_pack_k(key: torch.Tensor, group: int, *, capacity: int | None = None,
     _require(tuple(scales.shape) == (b, h, cap, d // group), "scales shape mismatch")
     with torch.cuda.device(key.device):
         _lib.check(lib.qkv_int4_pack_k(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
-                                       t_end, d, int(group), packed.data_ptr(), scales.data_ptr(), cap,
+                                       t_end, d, int(group), packed.data_ptr(), scales.data_ptr(), cap, code,
                                        _lib.stream_of(key)))
     return packed, scales
 
@@ -102,7 +120,7 @@ def build_slab(key: torch.Tensor, chan_idx: torch.Tensor, *, capacity: int | Non
     """Subset slab of tokens [t_begin, t_end): (slab uint8 [B,Hkv,cap,S/2],
     slab_scales fp16 [B,Hkv,cap])."""
     lib = _lib.load()
-    _check_kv("key", key)
+    code = _check_kv("key", key)
     b, h, t, d = key.shape
     _require(chan_idx.dtype == torch.int32 and chan_idx.is_contiguous(), "chan_idx must be contiguous int32")
     s = chan_idx.size(-1)
@@ -115,7 +133,7 @@ def build_slab(key: torch.Tensor, chan_idx: torch.Tensor, *, capacity: int | Non
     with torch.cuda.device(key.device):
         _lib.check(lib.qkv_int4_build_slab(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
                                            t_end, d, chan_idx.data_ptr(), s, slab.data_ptr(),
-                                           slab_scales.data_ptr(), cap, _lib.stream_of(key)))
+                                           slab_scales.data_ptr(), cap, code, _lib.stream_of(key)))
     return slab, slab_scales
 
 
@@ -124,7 +142,7 @@ def query_words(query: torch.Tensor, chan_idx: torch.Tensor, *, qwords: torch.Te
     """Per-row int8 query of decode scoring: (qwords int32 [B,Hkv,S/4] holding
     the packed uint32 words, qscale f32 [B,Hkv] or None)."""
     lib = _lib.load()
-    _require(query.is_cuda and query.dtype == torch.bfloat16 and query.dim() == 3, "query must be CUDA bf16 [B,Hq,D]")
+    code = _check_query(query)
     q = query.contiguous()
     b, hq, d = q.shape
     _require(chan_idx.dtype == torch.int32 and chan_idx.is_contiguous() and chan_idx.dim() == 3,
@@ -135,7 +153,7 @@ def query_words(query: torch.Tensor, chan_idx: torch.Tensor, *, qwords: torch.Te
         qwords = torch.empty((b, hkv, s // 4), dtype=torch.int32, device=q.device)
     with torch.cuda.device(q.device):
         _lib.check(lib.qkv_int4_query_words(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s,
-                                            qwords.data_ptr(), _lib.ptr(qscale), _lib.stream_of(q)))
+                                            qwords.data_ptr(), _lib.ptr(qscale), code, _lib.stream_of(q)))
     return qwords, qscale
 
 
@@ -144,11 +162,11 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
                   bmax: torch.Tensor | None = None, debug: bool = False):
     """Fused int4 scoring + block max over tokens [0, tokens).
 
-    query bf16 [B, Hq, D].  Returns bmax f32 [B, Hkv, ceil(tokens/block)];
+    query bf16 or fp16 [B, Hq, D].  Returns bmax f32 [B, Hkv, ceil(tokens/block)];
     with ``debug=True`` returns (bmax, isum int32 [B,Hkv,T], keys f32
     [B,Hkv,T], qscale f32 [B,Hkv])."""
     lib = _lib.load()
-    _require(query.is_cuda and query.dtype == torch.bfloat16 and query.dim() == 3, "query must be CUDA bf16 [B,Hq,D]")
+    code = _check_query(query)
     _require(slab.is_cuda and slab.dtype == torch.uint8 and slab.is_contiguous(), "slab must be contiguous CUDA uint8")
     q = query.contiguous()
     b, hq, d = q.shape
@@ -168,7 +186,7 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
         _lib.check(lib.qkv_int4_decode_scores(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s, slab.data_ptr(),
                                               slab_scales.data_ptr(), cap, int(tokens), int(block),
                                               bmax.data_ptr(), _lib.ptr(isum), _lib.ptr(keys),
-                                              _lib.ptr(qscale), _lib.stream_of(q)))
+                                              _lib.ptr(qscale), code, _lib.stream_of(q)))
     if debug:
         return bmax, isum, keys, qscale
     return bmax
@@ -244,12 +262,22 @@ def _protected(protect_sink: int, protect_recent: int, keep_self: bool) -> bool:
     return protect_sink > 0 or protect_recent > 0 or bool(keep_self)
 
 
+def _output(out: torch.Tensor | None, q: torch.Tensor) -> torch.Tensor:
+    """The attention output [B,Hq,D] in q's dtype: ``out`` checked, or a new tensor."""
+    if out is None:
+        return torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _require(out.dtype == q.dtype and tuple(out.shape) == tuple(q.shape) and out.is_contiguous(),
+             f"out must be contiguous {q.dtype} {tuple(q.shape)}")
+    return out
+
+
 def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                      block_ids: torch.Tensor, block: int, tokens: int, scaling: float, *,
                      workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
                      protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = False) -> torch.Tensor:
-    """GQA-native attention of query bf16 [B,Hq,D] over the selected blocks
-    (int32 [B,Hkv,n]) of K/V bf16 [B,Hkv,*,D]; returns bf16 [B,Hq,D].
+    """GQA-native attention of query [B,Hq,D] over the selected blocks
+    (int32 [B,Hkv,n]) of K/V [B,Hkv,*,D]; returns [B,Hq,D].  query, K, V and
+    the output share one dtype, bf16 or fp16.
 
     With protection (the reference's --protect_sink_tokens,
     --protect_recent_tokens, --always_keep_self; EV:2938-2982) ``tokens`` is
@@ -257,9 +285,7 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     the sink range, the recent range and the current token ``tokens`` (each
     token once; K/V then hold tokens + 1 rows)."""
     lib = _lib.load()
-    _check_kv("key", key)
-    _check_kv("value", value)
-    _require(key.stride() == value.stride() and key.shape == value.shape, "key/value layout mismatch")
+    code = _check_qkv(query, key, value)
     q = query.contiguous()
     b, hq, d = q.shape
     hkv = key.size(1)
@@ -270,21 +296,20 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     n_ws = protected_workspace_blocks(n, block, tokens, protect_sink, protect_recent, keep_self) if prot else n
     if workspace is None:
         workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
-    if out is None:
-        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    out = _output(out, q)
     with torch.cuda.device(q.device):
         if prot:
             _lib.check(lib.qkv_sparse_attention_protected(
                 q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
                 int(tokens), d, block_ids.data_ptr(), None, 0, n, int(block), int(protect_sink), int(protect_recent),
                 int(bool(keep_self)), float(scaling), workspace.data_ptr(), workspace.numel() * 4, None,
-                out.data_ptr(), _lib.stream_of(q)))
+                out.data_ptr(), code, _lib.stream_of(q)))
         else:
             _lib.check(lib.qkv_sparse_attention(q.data_ptr(), key.data_ptr(), value.data_ptr(),
                                                 _lib.strides(*key.stride()[:3]), b, hq, hkv, int(tokens), d,
                                                 block_ids.data_ptr(), n, int(block), float(scaling),
                                                 workspace.data_ptr(), workspace.numel() * 4, out.data_ptr(),
-                                                _lib.stream_of(q)))
+                                                code, _lib.stream_of(q)))
     return out
 
 
@@ -300,12 +325,10 @@ def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch
     """``sparse_attention`` over the n_sel blocks with the largest block
     maxima (f32 [B,Hkv,>=ceil(tokens/block)], the selection of ``block_topk``),
     selected inside the attention kernel.  sel_out (int32 [B,Hkv,n_sel]), when
-    given, receives the selection.  Protection as for ``sparse_attention``.
-    Returns bf16 [B,Hq,D]."""
+    given, receives the selection.  Protection and dtypes as for
+    ``sparse_attention``.  Returns [B,Hq,D] in the query's dtype."""
     lib = _lib.load()
-    _check_kv("key", key)
-    _check_kv("value", value)
-    _require(key.stride() == value.stride() and key.shape == value.shape, "key/value layout mismatch")
+    code = _check_qkv(query, key, value)
     q = query.contiguous()
     b, hq, d = q.shape
     hkv = key.size(1)
@@ -322,20 +345,20 @@ def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch
     n_ws = protected_workspace_blocks(n_sel, block, tokens, protect_sink, protect_recent, keep_self) if prot else n_sel
     if workspace is None:
         workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
-    if out is None:
-        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+    out = _output(out, q)
     with torch.cuda.device(q.device):
         if prot:
             _lib.check(lib.qkv_sparse_attention_protected(
                 q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
                 int(tokens), d, None, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), int(protect_sink),
                 int(protect_recent), int(bool(keep_self)), float(scaling), workspace.data_ptr(),
-                workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
+                workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), code, _lib.stream_of(q)))
         else:
             _lib.check(lib.qkv_sparse_attention_select(
                 q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
                 int(tokens), d, bmax.data_ptr(), bmax.size(2), int(n_sel), int(block), float(scaling),
-                workspace.data_ptr(), workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), _lib.stream_of(q)))
+                workspace.data_ptr(), workspace.numel() * 4, _lib.ptr(sel_out), out.data_ptr(), code,
+                _lib.stream_of(q)))
     return out
 
 
@@ -383,11 +406,13 @@ class SparseDecodeStep:
     reference's decode semantics (EV:4419-4460): the blocks are chosen over
     the history ``tokens - 1`` (the current token is not a candidate), and the
     attention covers them plus the sink range, the recent range and, with
-    keep_self, the current token, each token once (EV:2938-2982)."""
+    keep_self, the current token, each token once (EV:2938-2982).  ``dtype``
+    (bf16 or fp16) is the query / K / V / output dtype the step runs on."""
 
     def __init__(self, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
                  block: int, topk: int, device: torch.device | str = "cuda", *, protect_sink: int = 0,
-                 protect_recent: int = 0, keep_self: bool = False, history_only: bool | None = None):
+                 protect_recent: int = 0, keep_self: bool = False, history_only: bool | None = None,
+                 dtype: torch.dtype = torch.bfloat16):
         self.batch, self.q_heads, self.kv_heads = batch, q_heads, kv_heads
         self.head_dim, self.tokens, self.block, self.topk = head_dim, tokens, block, topk
         self.protect_sink, self.protect_recent = max(0, int(protect_sink)), max(0, int(protect_recent))
@@ -405,13 +430,14 @@ class SparseDecodeStep:
         n_ws = protected_workspace_blocks(topk, block, self.scored, self.protect_sink, self.protect_recent,
                                           self.keep_self)
         self.workspace = attention_workspace(batch, q_heads, kv_heads, head_dim, n_ws, block, device)
-        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        _require(dtype in (torch.bfloat16, torch.float16), f"dtype must be bfloat16 or float16, got {dtype}")
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=dtype, device=device)
         self.fused = nb <= SELECT_MAX_BLOCKS
 
     @classmethod
     def for_mode(cls, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, tokens: int,
                  device: torch.device | str = "cuda", *, protect_sink: int = 0, protect_recent: int = 0,
-                 keep_self: bool = True) -> "SparseDecodeStep":
+                 keep_self: bool = True, dtype: torch.dtype = torch.bfloat16) -> "SparseDecodeStep":
         """The int4 step for a reference mode string at a cache of ``tokens``
         keys (the current token included): ``qabs{S}cand{pct}attn`` keeps
         ``ceil(pct * history)`` tokens (one-token blocks), ``qboracle{bs}q{S}
@@ -429,7 +455,7 @@ class SparseDecodeStep:
         _require(plan is not None, f"mode {mode!r} is not a decode mode of this path (or no history yet)")
         step = cls(batch, q_heads, kv_heads, head_dim, tokens, plan.block,
                    min(plan.topk, math.ceil(plan.history / plan.block)), device, protect_sink=protect_sink,
-                   protect_recent=protect_recent, keep_self=keep_self, history_only=True)
+                   protect_recent=protect_recent, keep_self=keep_self, history_only=True, dtype=dtype)
         step.plan = plan
         return step
 
@@ -439,6 +465,7 @@ class SparseDecodeStep:
         kernel (two launches); longer rows run the top-k launch between.  The
         selection lands in ``self.sel`` either way."""
         _require(key.size(2) >= self.tokens, f"K/V hold {key.size(2)} tokens, the step needs {self.tokens}")
+        _require(query.dtype == self.out.dtype, f"this step runs on {self.out.dtype}; got a {query.dtype} query")
         prot = dict(protect_sink=self.protect_sink, protect_recent=self.protect_recent, keep_self=self.keep_self)
         decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.block,
                       bmax=self.bmax)

@@ -27,11 +27,11 @@ def _require(cond: bool, msg: str) -> None:
 
 
 def quantize_query(query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """query bf16 [..., 128] -> (q8 int8 [..., 128] in the MFMA operand order,
-    qscale f32 [...])."""
+    """query bf16 or fp16 [..., 128] -> (q8 int8 [..., 128] in the MFMA operand
+    order, qscale f32 [...])."""
     lib = _lib.load()
-    _require(query.is_cuda and query.dtype == torch.bfloat16 and query.size(-1) == 128,
-             "query must be CUDA bf16 [..., 128]")
+    _require(query.is_cuda and query.size(-1) == 128, "query must be CUDA [..., 128]")
+    code = _lib.half_code("query", query)
     q = query.reshape(-1, 128)
     _require(q.stride(1) == 1, "query channels must be contiguous")
     rows = q.size(0)
@@ -39,7 +39,7 @@ def quantize_query(query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     qscale = torch.empty(query.shape[:-1], dtype=torch.float32, device=query.device)
     with torch.cuda.device(query.device):
         _lib.check(lib.qkv_prefill_quantize_query(q.data_ptr(), rows, 128, q.stride(0), q8.data_ptr(),
-                                                  qscale.data_ptr(), _lib.stream_of(query)))
+                                                  qscale.data_ptr(), code, _lib.stream_of(query)))
     return q8, qscale
 
 
@@ -85,7 +85,7 @@ def block_topk(bmax: torch.Tensor, k: int, *, out: torch.Tensor | None = None) -
 
 def select_blocks(query: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, tokens: int, q_pos0: int,
                   k: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """query bf16 [B,Hq,Nq,128] -> (top-k block ids int32 [B,Hq,Nq,k], bmax)."""
+    """query bf16 or fp16 [B,Hq,Nq,128] -> (top-k block ids int32 [B,Hq,Nq,k], bmax)."""
     q8, _ = quantize_query(query)
     bmax = block_scores(q8, packed, scales, tokens, q_pos0)
     return block_topk(bmax, k), bmax

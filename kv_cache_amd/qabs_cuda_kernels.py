@@ -148,9 +148,10 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                     indices: torch.Tensor, valid: torch.Tensor, scaling: float) -> torch.Tensor:
     """QK:694-705 (host QK:569-638): softmax attention over the valid
     ``indices`` of each (b, h); returns [B, 1, H, D] in the query dtype.
-    bf16 inputs run on the matrix-core list attention (``qkv_token_attention``,
-    226 -> ~9 us at 32 heads x ~1000 entries over 32768 keys); fp16 / fp32 on
-    ``qkv_final_attention``'s fp32 loop in the reference's order."""
+    bf16 and fp16 inputs at D = 128 run on the matrix-core list attention
+    (``qkv_token_attention``, 226 -> ~9 us at 32 heads x ~1000 entries over
+    32768 keys); fp32 (or another D) on ``qkv_final_attention``'s fp32 loop in
+    the reference's order."""
     lib = _lib.load()
     valid_u8 = valid   # bool (or uint8) [B,H,N]; the fp32-loop kernel reads it as bytes (QK:703)
     _check(query.is_cuda, "query must be CUDA")
@@ -181,9 +182,10 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     _check(k.size(0) == b and k.size(1) == h and k.size(3) == d, "key shape mismatch")
     _check(idx.size(0) == b and idx.size(1) == h, "indices shape mismatch")
     _check(n > 0, "select_count must be positive")
-    ws_bytes = int(lib.qkv_sparse_attention_workspace_bytes(b, h, h, d, n, 1)) if q.dtype == torch.bfloat16 else 0
+    half = q.dtype in (torch.bfloat16, torch.float16)
+    ws_bytes = int(lib.qkv_sparse_attention_workspace_bytes(b, h, h, d, n, 1)) if half else 0
     if ws_bytes > 0:
-        # bf16: the list-per-head attention on the matrix cores (qkv_token_attention,
+        # bf16 / fp16: the list-per-head attention on the matrix cores (qkv_token_attention,
         # G = 1 on these head-expanded K/V), the invalid and out-of-range entries
         # as skipped ids; a row with none valid gives 0, as QK:388, 404 do
         with torch.cuda.device(q.device):
@@ -194,7 +196,8 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
             out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
             _lib.check(lib.qkv_token_attention(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.strides(*k.stride()[:3]), b, h, h, t, d,
-                ids.data_ptr(), n, float(scaling), ws.data_ptr(), ws_bytes, out.data_ptr(), _lib.stream_of(q)))
+                ids.data_ptr(), n, float(scaling), ws.data_ptr(), ws_bytes, out.data_ptr(), _dtype_code(q),
+                _lib.stream_of(q)))
         return out[:, None, :, :]
     out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
     val = val.to(torch.uint8)

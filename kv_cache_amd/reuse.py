@@ -236,28 +236,39 @@ def dim_major_append(key: torch.Tensor, key_dim_major: torch.Tensor, t_begin: in
 def token_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, token_ids: torch.Tensor,
                     scaling: float, *, workspace: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Each query head attends over its own token list (int32 [B*Hq, n], -1
-    skipped) of its K/V head; bf16 [B, Hq, D]."""
+    skipped) of its K/V head; [B, Hq, D] in the dtype q, K and V share (bf16
+    or fp16)."""
     lib = _lib.load()
     q = query.contiguous()
     b, hq, d = q.shape
-    _require(q.dtype == key.dtype == value.dtype == torch.bfloat16, "token attention takes bf16 q/K/V")
+    code = _lib.half_code("query", q)
+    _require(q.dtype == key.dtype == value.dtype,
+             f"token attention takes one dtype for q/K/V (got {q.dtype}, {key.dtype}, {value.dtype})")
     _require(key.shape == value.shape and key.stride() == value.stride() and key.stride(3) == 1,
              "key/value layout mismatch")
     _require(token_ids.dtype == torch.int32 and token_ids.is_contiguous() and token_ids.numel() ==
              b * hq * token_ids.size(-1), "token_ids must be contiguous int32 [B*Hq, n]")
     if out is None:
-        out = torch.empty((b, hq, d), dtype=torch.bfloat16, device=q.device)
+        out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
+    _require(out.dtype == q.dtype and out.is_contiguous() and out.numel() == b * hq * d,
+             f"out must be contiguous {q.dtype} [B, Hq, D]")
     with torch.cuda.device(q.device):
         _lib.check(lib.qkv_token_attention(
             q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, key.size(1),
             key.size(2), d, token_ids.data_ptr(), token_ids.size(-1), float(scaling), workspace.data_ptr(),
-            workspace.numel() * 4, out.data_ptr(), _lib.stream_of(q)))
+            workspace.numel() * 4, out.data_ptr(), code, _lib.stream_of(q)))
     return out
+
+
+def _check_step_dtype(dtype: torch.dtype, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> None:
+    _require(query.dtype == key.dtype == value.dtype == dtype,
+             f"this step takes {dtype} q/K/V (got {query.dtype}, {key.dtype}, {value.dtype})")
 
 
 class ReuseDecodeStep:
     """One layer's reuse decode step with its state, for K/V caches of up to
-    ``capacity`` tokens (bf16 K/V as HF stores them, [B, Hkv, T, D]).
+    ``capacity`` tokens ([B, Hkv, T, D] as HF stores them, in ``dtype``: bf16
+    or fp16, shared by the query and the output).
 
     Call it once per decode token with the cache including the current token
     (T = history + 1).  The previous step's masks are used when the previous
@@ -269,8 +280,10 @@ class ReuseDecodeStep:
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
                  keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
-                 device: torch.device | str = "cuda"):
+                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16):
         lib = _lib.load()
+        _require(dtype in (torch.bfloat16, torch.float16), f"dtype must be bfloat16 or float16, got {dtype}")
+        self.dtype = dtype
         self.device = device
         self.mode = mode
         (self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final,
@@ -288,7 +301,7 @@ class ReuseDecodeStep:
         rows = batch * q_heads
         cap = self.capacity
         self.rows = rows
-        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
+        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
         self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
         self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
@@ -315,7 +328,7 @@ class ReuseDecodeStep:
         need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
         _require(need > 0, "unsupported attention shape (head_dim must be 128)")
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
-        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=dtype, device=device)
         self.reset()
 
     def _parse_mode(self, mode: str) -> tuple[int, float, bool, bool, int | None]:
@@ -353,10 +366,11 @@ class ReuseDecodeStep:
             self.kdm_len = t
 
     def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
-        """query bf16 [B, Hq, D]; key/value bf16 [B, Hkv, T, D] (the current
-        token last).  Returns bf16 [B, Hq, D]."""
+        """query [B, Hq, D]; key/value [B, Hkv, T, D] (the current token
+        last), in the step's dtype.  Returns [B, Hq, D] in that dtype."""
         key_count = key.size(2)
         _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
+        _check_step_dtype(self.dtype, query, key, value)
         g = self.q_heads // self.kv_heads
         if key_count <= 1:   # EV:4012-4014: only the current token
             self.out.copy_(value[:, :, -1, :].repeat_interleave(g, dim=1))
@@ -596,11 +610,11 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
                  keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
-                 device: torch.device | str = "cuda"):
+                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16):
         super().__init__(mode, batch, q_heads, kv_heads, head_dim, capacity, top_fraction=top_fraction,
                          protect_sink=protect_sink, protect_recent=protect_recent, keep_self=keep_self,
                          candidate_selection=candidate_selection, threshold_sample_size=threshold_sample_size,
-                         device=device)
+                         device=device, dtype=dtype)
         s = min(max(1, self.dims), head_dim)
         _require(head_dim <= 128, "the lagged reuse modes take head_dim <= 128")
         # rows that keep skip the partial scores; past 40960 positions the staged
@@ -757,8 +771,8 @@ def qabs_candidate_select(scores: torch.Tensor, key_count: int, candidate_fracti
 class QabsCandidateAttentionStep:
     """One layer's ``qabs{S}cand{pct}attn`` / ``appendattn`` decode step
     (``_qabs_candidate_attention_forward`` EV:4400-4502) with the reference's
-    exact arithmetic, for bf16 K/V caches of up to ``capacity`` tokens
-    ([B, Hkv, T, D], D = 128): per query head the fp32 partial score of every
+    exact arithmetic, for K/V caches of up to ``capacity`` tokens
+    ([B, Hkv, T, D], D = 128, bf16 or fp16 as ``dtype`` says): per query head the fp32 partial score of every
     history token on its top-|q| dims (from a per-KV-head dim-major K copy kept
     current one token per step; products and sums in selection order as
     QK:63-96), the ``min(history, max(1, ceil(pct * history)))`` best (ties to
@@ -769,8 +783,10 @@ class QabsCandidateAttentionStep:
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  protect_sink: int = 0, protect_recent: int = 0, keep_self: bool = True,
-                 device: torch.device | str = "cuda"):
+                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16):
         lib = _lib.load()
+        _require(dtype in (torch.bfloat16, torch.float16), f"dtype must be bfloat16 or float16, got {dtype}")
+        self.dtype = dtype
         self.mode = mode
         self.dims, self.cand_fraction, self.append, self.interval = parse_qabs_attn_mode(mode)
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
@@ -784,7 +800,7 @@ class QabsCandidateAttentionStep:
         hist_max = cap - 1
         self.n_out_max = int(lib.qkv_reuse_final_count(hist_max, self.sink, self.recent, self.cand_fraction,
                                                        int(self.keep_self)))
-        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=torch.bfloat16, device=device)
+        self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
         self.final_idx = torch.empty(rows * self.n_out_max, dtype=torch.int64, device=device)
         self.final_valid = torch.empty(rows * self.n_out_max, dtype=torch.bool, device=device)
@@ -795,7 +811,7 @@ class QabsCandidateAttentionStep:
         need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
         _require(need > 0, "unsupported attention shape (head_dim must be 128)")
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
-        self.out = torch.empty((batch, q_heads, head_dim), dtype=torch.bfloat16, device=device)
+        self.out = torch.empty((batch, q_heads, head_dim), dtype=dtype, device=device)
         # r{N}attn: the last refreshing step's selection (EV:1722-1733), its length
         self.kept = torch.empty((rows, self.n_out_max), dtype=torch.int64, device=device) if self.interval else None
         self.n_kept = 0
@@ -817,10 +833,11 @@ class QabsCandidateAttentionStep:
             self.kdm_len = t
 
     def __call__(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float) -> torch.Tensor:
-        """query bf16 [B, Hq, D]; key/value bf16 [B, Hkv, T, D] (the current
-        token last).  Returns bf16 [B, Hq, D]."""
+        """query [B, Hq, D]; key/value [B, Hkv, T, D] (the current token
+        last), in the step's dtype.  Returns [B, Hq, D] in that dtype."""
         key_count = key.size(2)
         _require(key_count <= self.capacity, f"cache holds {key_count} tokens, capacity {self.capacity}")
+        _check_step_dtype(self.dtype, query, key, value)
         if key_count <= 1:   # EV:4415-4417: only the current token
             self.out.copy_(value[:, :, -1, :].repeat_interleave(self.q_heads // self.kv_heads, dim=1))
             return self.out

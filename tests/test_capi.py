@@ -34,38 +34,38 @@ def _err():
     (lambda: lib.qkv_topk(ctypes.c_void_p(16), 1, 10, 5, 3, ctypes.c_void_p(16), None), "bad sizes"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 24,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
-                                        ctypes.c_void_p(16), None, None, None, None), "selected must be"),
+                                        ctypes.c_void_p(16), None, None, None, 0, None), "selected must be"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4032, 4000, 16,
-                                        ctypes.c_void_p(16), None, None, None, None), "multiple of 256"),
+                                        ctypes.c_void_p(16), None, None, None, 0, None), "multiple of 256"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 12,
-                                        ctypes.c_void_p(16), None, None, None, None), "power of two"),
+                                        ctypes.c_void_p(16), None, None, None, 0, None), "power of two"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 64,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 256,
-                                        ctypes.c_void_p(16), None, None, None, None), "<= 128"),
+                                        ctypes.c_void_p(16), None, None, None, 0, None), "<= 128"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
-                                        None, None, None, None, None), "need bmax"),
+                                        None, None, None, None, 0, None), "need bmax"),
     (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 15, 8, 128, ctypes.c_void_p(16), 32,
                                         ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
-                                        ctypes.c_void_p(16), None, None, None, None), "multiple of kv_heads"),
+                                        ctypes.c_void_p(16), None, None, None, 0, None), "multiple of kv_heads"),
     (lambda: lib.qkv_int4_query_words(ctypes.c_void_p(16), 1, 15, 8, 128, ctypes.c_void_p(16), 32,
-                                      ctypes.c_void_p(16), None, None), "multiple of kv_heads"),
+                                      ctypes.c_void_p(16), None, 0, None), "multiple of kv_heads"),
     (lambda: lib.qkv_int4_query_words(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 48,
-                                      ctypes.c_void_p(16), None, None), "selected must be"),
+                                      ctypes.c_void_p(16), None, 0, None), "selected must be"),
     (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 48,
-                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "group"),
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 0, None), "group"),
     (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 100, 128, 32,
-                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "token range"),
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 0, None), "token range"),
     (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(18), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 32,
-                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, None), "16-byte aligned"),
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 0, None), "16-byte aligned"),
     (lambda: lib.qkv_sparse_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                       _lib.strides(8, 8, 8), 1, 16, 8, 100, 64, ctypes.c_void_p(16), 4, 16,
-                                      1.0, ctypes.c_void_p(16), 1 << 20, ctypes.c_void_p(16), None), "128"),
+                                      1.0, ctypes.c_void_p(16), 1 << 20, ctypes.c_void_p(16), 0, None), "128"),
     (lambda: lib.qkv_sparse_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                       _lib.strides(8, 8, 8), 1, 16, 8, 100, 128, ctypes.c_void_p(16), 4, 16,
-                                      1.0, ctypes.c_void_p(16), 16, ctypes.c_void_p(16), None), "workspace"),
+                                      1.0, ctypes.c_void_p(16), 16, ctypes.c_void_p(16), 0, None), "workspace"),
     (lambda: lib.qkv_final_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                      ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
                                      1, 1, 10, 0, 128, 1.0, None), "select_count must be positive"),
@@ -81,15 +81,26 @@ def _err():
                                          ctypes.c_void_p(16), None, 5, None), "stride"),
     (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                                      _lib.strides(8, 8, 8), 1, 16, 8, 100, 128, None, 7, 4, 16,
-                                                     1.0, None, ctypes.c_void_p(16), None), "null pointer"),
+                                                     1.0, None, ctypes.c_void_p(16), 0, None), "null pointer"),
     (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                                      _lib.strides(8, 8, 8), 1, 16, 8, 100, 64, ctypes.c_void_p(16), 7,
-                                                     4, 16, 1.0, None, ctypes.c_void_p(16), None), "unsupported sizes"),
+                                                     4, 16, 1.0, None, ctypes.c_void_p(16), 0, None), "unsupported sizes"),
     # 4096 rows x 65536 selected slots: far beyond the 8 MiB static scratch
     (lambda: lib.qkv_sparse_attention_select_noalloc(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                                      _lib.strides(8, 8, 8), 64, 64, 64, 65536, 128,
                                                      ctypes.c_void_p(16), 4096, 4096, 16, 1.0, None,
-                                                     ctypes.c_void_p(16), None), "static scratch holds"),
+                                                     ctypes.c_void_p(16), 0, None), "static scratch holds"),
+    # the 16-bit entry points take bf16 (0) or fp16 (1); fp32 is unsupported, other codes invalid
+    (lambda: lib.qkv_int4_pack_k(ctypes.c_void_p(16), _lib.strides(8, 8, 8), 1, 1, 0, 10, 128, 32,
+                                 ctypes.c_void_p(16), ctypes.c_void_p(16), 64, 2, None), "is not bf16"),
+    (lambda: lib.qkv_int4_decode_scores(ctypes.c_void_p(16), 1, 16, 8, 128, ctypes.c_void_p(16), 32,
+                                        ctypes.c_void_p(16), ctypes.c_void_p(16), 4096, 4096, 16,
+                                        ctypes.c_void_p(16), None, None, None, 5, None), "is not bf16"),
+    (lambda: lib.qkv_sparse_attention(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                      _lib.strides(8, 8, 8), 1, 16, 8, 100, 128, ctypes.c_void_p(16), 4, 16,
+                                      1.0, ctypes.c_void_p(16), 1 << 20, ctypes.c_void_p(16), 2, None), "is not bf16"),
+    (lambda: lib.qkv_prefill_quantize_query(ctypes.c_void_p(16), 4, 128, 128, ctypes.c_void_p(16), None, -1, None),
+     "is not bf16"),
 ])
 def test_host_side_validation(call, msg):
     rc = call()

@@ -44,7 +44,7 @@ def test_qbb_metadata_and_bounds(block, t):
     # built in two pieces: the second rebuilds the block the first ended inside
     for t0, t1 in ((0, t // 2 + 1), (t // 2 + 1, t)):
         _lib.check(lib.qkv_block_meta_update(BS.QBB, kd.data_ptr(), ks, 2, 2, 128, block, 1, t0, t1,
-                                             meta.data_ptr(), mb, _lib.stream_of(kd)))
+                                             meta.data_ptr(), mb, 0, _lib.stream_of(kd)))
     rec = meta.view(torch.int16).view(2, 2, mb, 2, 128)[:, :, : -(-t // block)]
     lo, hi = R.block_minmax(f32(k), block)
     assert np.array_equal(f32(rec[:, :, :, 0].view(torch.bfloat16)), lo)
@@ -52,7 +52,7 @@ def test_qbb_metadata_and_bounds(block, t):
     nb = -(-t // block)
     out = torch.empty((8, nb + 5), dtype=torch.float32, device=DEV)
     _lib.check(lib.qkv_block_scores(BS.QBB, qd.data_ptr(), kd.data_ptr(), ks, meta.data_ptr(), mb, 2, 4, 2, t, 128,
-                                    block, 1, 8, out.data_ptr(), nb + 5, _lib.stream_of(kd)))
+                                    block, 1, 8, out.data_ptr(), nb + 5, 0, _lib.stream_of(kd)))
     want = R.qbb_block_bounds(f32(q), np.repeat(lo, 2, axis=1), np.repeat(hi, 2, axis=1), 8)
     assert np.array_equal(out[:, :nb].cpu().numpy().reshape(2, 4, nb), want)
 
@@ -69,13 +69,13 @@ def test_brep_metadata_and_scores(block, reps, t):
     ks = _lib.strides(*kd.stride())
     for t0, t1 in ((0, 1), (1, t - 7), (t - 7, t)):
         _lib.check(lib.qkv_block_meta_update(BS.BREP, kd.data_ptr(), ks, 1, 2, 128, block, reps, t0, t1,
-                                             meta.data_ptr(), mb, _lib.stream_of(kd)))
+                                             meta.data_ptr(), mb, 0, _lib.stream_of(kd)))
     got = meta.view(torch.int32).view(1, 2, mb, reps).cpu().numpy()
     idx, valid = R.block_representatives(f32(k), block, reps)
     assert np.array_equal(np.where(valid, idx, -1), got)
     out = torch.empty((8, mb), dtype=torch.float32, device=DEV)
     _lib.check(lib.qkv_block_scores(BS.BREP, qd.data_ptr(), kd.data_ptr(), ks, meta.data_ptr(), mb, 1, 8, 2, t, 128,
-                                    block, reps, 16, out.data_ptr(), mb, _lib.stream_of(kd)))
+                                    block, reps, 16, out.data_ptr(), mb, 0, _lib.stream_of(kd)))
     kx = np.repeat(f32(k), 4, axis=1)
     want = R.brep_block_scores(f32(q), kx, np.repeat(idx, 4, axis=1), np.repeat(valid, 4, axis=1), 16)
     assert np.array_equal(out.cpu().numpy().reshape(1, 8, mb), want)
@@ -128,7 +128,7 @@ def test_qboracle_block_scores_match_oracle(block, t, hq, hkv, dims):
     nb = -(-t // block)
     out = torch.full((hq, nb + 3), 7.0, dtype=torch.float32, device=DEV)
     _lib.check(lib.qkv_block_max_partial_scores(qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), 1, hq, hkv,
-                                                t, 128, block, dims, out.data_ptr(), nb + 3, _lib.stream_of(kd)))
+                                                t, 128, block, dims, out.data_ptr(), nb + 3, 0, _lib.stream_of(kd)))
     want = O.block_max(R.partial_scores(f32(q), np.repeat(f32(k), hq // hkv, axis=1), dims), block)
     got = out.cpu().numpy()
     assert np.array_equal(got[:, :nb].reshape(1, hq, nb), want)
@@ -221,6 +221,6 @@ def test_rerank_with_and_without_scan_full_scores(mode, t):
             q.data_ptr(), kd.data_ptr(), _lib.strides(*kd.stride()), 1, hq, hkv, t, 128,
             step.partial[: rows * n_tok].data_ptr(), _lib.ptr(full), n_tok, step.blocks[: rows * n_scan].data_ptr(),
             n_scan, step.block, n_cand, n_keep, 3, 5, 1, 0.088, keep.data_ptr(), step.capacity, ids.data_ptr(), n_out,
-            _lib.stream_of(q)))
+            0, _lib.stream_of(q)))
         assert torch.equal(keep[:, :t], want_mask), full is None
         assert torch.equal(ids, want_ids), full is None

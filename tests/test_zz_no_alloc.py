@@ -41,13 +41,13 @@ def _call(noalloc, q, k, v, bmax, n_sel, block, tokens, scaling):
         if noalloc:
             rc = lib.qkv_sparse_attention_select_noalloc(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), ks, b, hq, hkv, tokens, d, bmax.data_ptr(), bmax.size(2),
-                n_sel, block, ctypes.c_float(scaling), sel.data_ptr(), out.data_ptr(), stream)
+                n_sel, block, ctypes.c_float(scaling), sel.data_ptr(), out.data_ptr(), 0, stream)
         else:
             ws = K.attention_workspace(b, hq, hkv, d, n_sel, block, q.device)
             rc = lib.qkv_sparse_attention_select(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), ks, b, hq, hkv, tokens, d, bmax.data_ptr(), bmax.size(2),
                 n_sel, block, ctypes.c_float(scaling), ws.data_ptr(), ws.numel() * 4, sel.data_ptr(), out.data_ptr(),
-                stream)
+                0, stream)
     _lib.check(rc)
     torch.cuda.synchronize()
     return sel, out
@@ -78,6 +78,6 @@ def test_noalloc_rejects_sizes_beyond_scratch():
     assert lib.qkv_sparse_attention_workspace_bytes(b, hq, hkv, 128, n_sel, blk) > SCRATCH_BYTES
     p = ctypes.c_void_p(256)
     rc = lib.qkv_sparse_attention_select_noalloc(p, p, p, _lib.strides(1024, 1024, 128), b, hq, hkv, t, 128, p,
-                                                 t // blk, n_sel, blk, ctypes.c_float(0.1), None, p, None)
+                                                 t // blk, n_sel, blk, ctypes.c_float(0.1), None, p, 0, None)
     assert rc == -3
     assert "static scratch holds" in lib.qkv_last_error().decode()
