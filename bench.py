@@ -1256,7 +1256,8 @@ def run_blocksel(args) -> dict:
 
     hf = hist - 1
     kc = hf + 1
-    nb, n_scan, n_cand, n_keep = BS.step_counts(hf, steps[0].block, steps[0].scan, steps[0].cand, c["top_fraction"])
+    nb, n_scan, n_cand, n_keep = BS.step_counts(hf, steps[0].block, steps[0].scan, steps[0].cand, c["top_fraction"],
+                                                steps[0].unscanned)
     lib = _lib.load()
     reps = max(1, -(-16 // layers))
 
@@ -1311,6 +1312,7 @@ def run_blocksel(args) -> dict:
                                             st.blocks.data_ptr(), n_scan,
                                             st.block, n_cand, n_keep, c["sink"], c["recent"], 1, scaling,
                                             st.keep.data_ptr(), st.capacity, st.attn_ids.data_ptr(), n_out,
+                                            int(st.unscanned), st.rerank_ws.data_ptr(), st.rerank_ws.numel() * 4,
                                             st.dtype_code, _lib.stream_of(k)))
 
     def run_attn():

@@ -571,7 +571,7 @@ int64_t qkv_block_meta_bytes(int kind, int64_t batch, int64_t kv_heads, int64_t 
 /* Rebuilds the metadata of the blocks holding tokens [t_begin, t_end) from
  * K's tokens below t_end: per-channel min/max (qbb), or the reps tokens of
  * largest squared norm (fp32 sum in channel order), descending, lower index
- * on ties, -1 padding (brep; block <= 64).  The reference recomputes these
+ * on ties, -1 padding (brep; 1 <= reps <= min(block, 64), any block).  The reference recomputes these
  * every step (EV:5536-5553) or per new block (EV:1884-1918). */
 int qkv_block_meta_update(int kind, const void* key, const int64_t* k_strides, int64_t batch, int64_t kv_heads,
                           int64_t head_dim, int64_t block, int64_t reps, int64_t t_begin, int64_t t_end, void* meta,
@@ -606,7 +606,7 @@ int qkv_block_scan_scores(const void* query, const void* key_dim_major, const in
  * summed in selection order), of block j's history tokens
  * [j*block, min(history, (j+1)*block)), read from the dim-major K copy
  * (qkv_dim_major_append).  query [B,Hq,D]; out f32 [rows, >= out_ld],
- * rows = B*Hq.  block <= 2048. */
+ * rows = B*Hq; any block length. */
 int qkv_block_max_partial_scores(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                                  int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
                                  int64_t block, int64_t dim_count, float* out, int64_t out_ld, int dtype,
@@ -636,22 +636,36 @@ int qkv_brep_partial_scores(const float* query, const void* key_history, const i
 int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t protect_sink, int64_t protect_recent,
                              int keep_self);
 
-/* Rerank of each row (EV:5583-5605), one workgroup per row: the n_cand best
- * scanned positions by partial score, their full-D fp32 scores * scaling,
- * the n_keep best of those (ties to the lower index throughout), then
- * keep_mask [rows, key_count] (kept tokens, the first protect_sink and last
- * protect_recent history tokens, the current token when keep_self;
- * EV:5607-5615) and attn_ids [rows, n_out] for qkv_token_attention: the kept
- * tokens ascending (-1 where protected or not filled), the sink range, the
- * recent range, the current token.  n_scan * block <= 40960,
- * n_keep <= n_cand <= 4096.  full (optional, partial's layout): the full
- * scores qkv_block_scan_scores wrote; NULL computes them here from key. */
+/* Rerank of each row (EV:5583-5605): the n_cand best scanned history tokens
+ * by partial score -- with unscanned != 0 (qboracle) every history token
+ * ranks, the unscanned ones at finfo(float32).min behind every scanned one
+ * (EV:5055-5058), so candidates past the scanned tokens are the lowest
+ * unscanned ones -- their full-D fp32 scores * scaling, the n_keep best of
+ * those (ties to the lower token throughout), then keep_mask [rows,
+ * key_count] (kept tokens, the first protect_sink and last protect_recent
+ * history tokens, the current token when keep_self; EV:5607-5615) and
+ * attn_ids [rows, n_out] for qkv_token_attention: the kept tokens ascending
+ * (-1 where protected or not filled), the sink range, the recent range, the
+ * current token.  n_keep <= n_cand.  Rows of at most 40960 scanned positions
+ * and 4096 candidates (and, with unscanned, no more candidates than
+ * scanned history tokens) take one workgroup each and no workspace; full
+ * (optional, partial's layout) then holds the full scores
+ * qkv_block_scan_scores wrote (NULL: computed here from key).  Other rows
+ * take five launches over `workspace` (256-byte aligned, at least
+ * qkv_block_rerank_workspace_bytes; full unused). */
 int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch, int64_t q_heads,
                      int64_t kv_heads, int64_t key_count, int64_t head_dim, const float* partial, const float* full,
                      int64_t partial_ld, const int32_t* blocks, int64_t n_scan, int64_t block, int64_t n_cand,
                      int64_t n_keep,
                      int64_t protect_sink, int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
-                     int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int dtype, void* stream);
+                     int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int unscanned, void* workspace,
+                     int64_t workspace_bytes, int dtype, void* stream);
+
+/* Bytes of workspace qkv_block_rerank needs for these sizes: 0 when every
+ * row fits one workgroup, -1 for bad sizes (rows = B*Hq, history =
+ * key_count - 1). */
+int64_t qkv_block_rerank_workspace_bytes(int64_t rows, int64_t history, int64_t n_scan, int64_t block,
+                                         int64_t n_cand, int64_t n_keep, int unscanned);
 
 /* ======================================================================
  * Chunked-prefill block selection (no reference counterpart: the reference

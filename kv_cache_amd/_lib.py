@@ -105,7 +105,8 @@ _PROTOTYPES = {
                                        _i64, _f64, _vp]),
     "qkv_final_list_count": (_i64, [_i64, _i64, _i64, _i64, _i32]),
     "qkv_block_rerank": (_i32, [_vp, _vp, _P(_i64), _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64,
-                                _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _i32, _vp]),
+                                _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp]),
+    "qkv_block_rerank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
 }
 
 _LIB = None

@@ -63,12 +63,16 @@ def parse_block_mode(mode: str) -> tuple[int, int, int, int, float, float]:
             _pct(m.group(5)))
 
 
-def step_counts(history: int, block: int, scan: float, cand: float, top: float) -> tuple[int, int, int, int]:
+def step_counts(history: int, block: int, scan: float, cand: float, top: float,
+                unscanned: bool = False) -> tuple[int, int, int, int]:
     """(blocks, scanned blocks, candidates, kept) for a history, as the
-    reference computes them (EV:5535, 5563, 5583, 5590)."""
+    reference computes them (EV:5535, 5563, 5583, 5590).  qbb / brep rank
+    the scanned tokens only; qboracle (``unscanned``) ranks every history
+    token (EV:5055-5058)."""
     nb = math.ceil(history / block)
     n_scan = min(nb, max(1, math.ceil(scan * history / block)))
-    n_cand = min(n_scan * block, max(1, math.ceil(cand * history)))
+    n_req = max(1, math.ceil(cand * history))
+    n_cand = min(history, n_req) if unscanned else min(n_scan * block, n_req)
     n_keep = min(n_cand, max(1, math.ceil(top * history)))
     return nb, n_scan, n_cand, n_keep
 
@@ -91,9 +95,9 @@ class BlockSelectDecodeStep:
         self.mode = mode
         self.kind, self.block, reps, self.dims, self.scan, self.cand = parse_block_mode(mode)
         self.reps = max(1, min(reps, self.block))
+        _require(self.reps <= 64, f"{mode}: at most 64 representatives per block")
         _require(head_dim == 128, "block selectors need head_dim 128")
         _require(q_heads % kv_heads == 0, "q_heads must be a multiple of kv_heads")
-        _require(self.kind != BREP or self.block <= 64, "brep needs blocks of at most 64 tokens")
         self.batch, self.q_heads, self.kv_heads, self.head_dim = batch, q_heads, kv_heads, head_dim
         self.capacity = int(capacity)
         self.top_fraction = float(top_fraction)
@@ -104,16 +108,22 @@ class BlockSelectDecodeStep:
         cap = self.capacity
         self.meta_blocks = math.ceil(cap / self.block)
         if self.kind == QBORACLE:   # scores every block from the dim-major copy
-            _require(self.block <= 2048, "qboracle needs blocks of at most 2048 tokens")
             self.meta = None
         else:
             nbytes = lib.qkv_block_meta_bytes(self.kind, batch, kv_heads, self.meta_blocks, self.reps)
             _require(nbytes > 0, "bad block metadata size")
             self.meta = torch.empty(nbytes, dtype=torch.uint8, device=device)
         self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
-        nb, n_scan, n_cand, n_keep = step_counts(cap - 1, self.block, self.scan, self.cand, self.top_fraction)
-        _require(n_scan * self.block <= 40960, f"{n_scan * self.block} scanned tokens per row; at most 40960")
-        _require(n_cand <= 4096, f"{n_cand} candidates per row; at most 4096")
+        self.unscanned = self.kind == QBORACLE
+        nb, n_scan, n_cand, n_keep = step_counts(cap - 1, self.block, self.scan, self.cand, self.top_fraction,
+                                                 self.unscanned)
+        # rows past the one-workgroup rerank (more than 40960 scanned tokens or
+        # 4096 candidates, qboracle candidates past the scanned tokens) rerank
+        # over this workspace; sized at the capacity, grown if a shorter history needs more
+        need = lib.qkv_block_rerank_workspace_bytes(rows, cap - 1, n_scan, self.block, n_cand, n_keep,
+                                                    int(self.unscanned))
+        _require(need >= 0, "bad rerank sizes")
+        self.rerank_ws = torch.empty(max(1, (need + 3) // 4), dtype=torch.float32, device=device)
         self.bscore = torch.empty((rows, self.meta_blocks), dtype=torch.float32, device=device)
         self.blocks = torch.empty(rows * n_scan, dtype=torch.int32, device=device)
         self.topk_ws = topk_workspace(rows, self.meta_blocks, n_scan, device)
@@ -181,17 +191,15 @@ class BlockSelectDecodeStep:
         history = key_count - 1
         _require(self.meta_len >= history and self.kdm_len >= history, "block metadata does not hold the history")
         q = query.contiguous()
-        nb, n_scan, n_cand, n_keep = step_counts(history, self.block, self.scan, self.cand, self.top_fraction)
+        nb, n_scan, n_cand, n_keep = step_counts(history, self.block, self.scan, self.cand, self.top_fraction,
+                                                 self.unscanned)
         stream = _lib.stream_of(q)
         ks = _lib.strides(*key.stride())
-        if self.kind == QBORACLE:
-            # the reference ranks every history token for its candidates, the
-            # unscanned ones at finfo.min (EV:5055-5058); those only enter once
-            # the scanned tokens run out, which this step does not support
-            fewest = n_scan * self.block - (nb * self.block - history)
-            _require(math.ceil(self.cand * history) <= fewest,
-                     f"{self.mode}: {math.ceil(self.cand * history)} candidates from as few as {fewest} scanned "
-                     "tokens (more candidates than scanned tokens is not supported)")
+        ws_need = int(lib.qkv_block_rerank_workspace_bytes(self.rows, history, n_scan, self.block, n_cand, n_keep,
+                                                           int(self.unscanned)))
+        _require(ws_need >= 0, "bad rerank sizes")
+        if ws_need > self.rerank_ws.numel() * 4:
+            self.rerank_ws = torch.empty((ws_need + 3) // 4, dtype=torch.float32, device=q.device)
         with torch.cuda.device(q.device):
             if self.kind == QBORACLE:
                 _lib.check(lib.qkv_block_max_partial_scores(
@@ -207,19 +215,22 @@ class BlockSelectDecodeStep:
             block_topk(self.bscore[:, :nb], n_scan, out=blocks, workspace=self.topk_ws)
             n_tok = n_scan * self.block
             partial = self.partial[: self.rows * n_tok]
-            full = self.full[: self.rows * n_tok]
+            # the one-workgroup rerank ranks its candidates by the full scores the
+            # scan computes for every scanned token; the general one (ws_need > 0)
+            # computes them for its candidates only
+            full = self.full[: self.rows * n_tok] if ws_need == 0 else None
             _lib.check(lib.qkv_block_scan_scores(
                 q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), key.data_ptr(), ks, self.batch,
                 self.q_heads, self.kv_heads, history, self.head_dim, blocks.data_ptr(), n_scan, self.block,
-                self.dims, float(scaling), partial.data_ptr(), full.data_ptr(), n_tok, self.dtype_code, stream))
+                self.dims, float(scaling), partial.data_ptr(), _lib.ptr(full), n_tok, self.dtype_code, stream))
             n_out = int(lib.qkv_final_list_count(history, n_keep, self.sink, self.recent, int(self.keep_self)))
             ids = self.attn_ids[: self.rows * n_out]
             _lib.check(lib.qkv_block_rerank(
                 q.data_ptr(), key.data_ptr(), ks, self.batch, self.q_heads, self.kv_heads, key_count, self.head_dim,
-                partial.data_ptr(), full.data_ptr(), n_tok, blocks.data_ptr(), n_scan, self.block, n_cand, n_keep,
-                self.sink,
-                self.recent, int(self.keep_self), float(scaling), self.keep.data_ptr(), self.capacity,
-                ids.data_ptr(), n_out, self.dtype_code, stream))
+                partial.data_ptr(), _lib.ptr(full), n_tok, blocks.data_ptr(), n_scan, self.block, n_cand, n_keep,
+                self.sink, self.recent, int(self.keep_self), float(scaling), self.keep.data_ptr(), self.capacity,
+                ids.data_ptr(), n_out, int(self.unscanned), self.rerank_ws.data_ptr(), self.rerank_ws.numel() * 4,
+                self.dtype_code, stream))
         self.n_out = n_out
         self.key_count = key_count
         return token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws,

@@ -89,10 +89,39 @@ __device__ __forceinline__ float full_score(const uint16_t* __restrict__ krow, c
 
 // ---------------------------------------------------------------------------
 // Metadata.  qbb: per block a 512-byte record [min(128) | max(128)] in K's
-// dtype (exact: they are elements of K).  brep: per block R int32 token indices, descending
-// squared norm, lower index on ties, -1 where the block has fewer tokens.
-// Blocks [j0, j0 + grid.x) over tokens below t_end are rebuilt.
+// dtype (exact: they are elements of K).  brep: per block R int32 token
+// indices, descending squared norm, lower index on ties, -1 where the block
+// has fewer tokens.  Blocks [j0, j0 + grid.x) over tokens below t_end are
+// rebuilt.
 // ---------------------------------------------------------------------------
+
+// Squared norm of one K row of kHD values (16-byte aligned), an fp32 sum in
+// channel order (BlockRepState's norm, EV:1899-1913).
+template <bool F16>
+__device__ __forceinline__ float sq_norm(const uint16_t* __restrict__ krow) {
+  const uint4* kr = reinterpret_cast<const uint4*>(krow);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kHD / 8; ++c) {
+    const uint4 x = kr[c];
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = half_lo<F16>(w[e]), hi = half_hi<F16>(w[e]);
+      acc = acc + lo * lo;
+      acc = acc + hi * hi;
+    }
+  }
+  return acc;
+}
+
+// (norm, token) of the better representative: larger norm, then lower token.
+__device__ __forceinline__ void rep_better(float& bn, int& bt, float on, int ot) {
+  if (on > bn || (on == bn && ot < bt)) {
+    bn = on;
+    bt = ot;
+  }
+}
 template <bool F16>
 __global__ __launch_bounds__(kBT) void qbb_meta_kernel(const uint16_t* __restrict__ key, int kv_heads, int64_t sb,
                                                        int64_t sh, int64_t st, int block, int t_end, int j0,
@@ -127,22 +156,7 @@ __global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restri
   const int t = j * block + lane;
   const bool ok = lane < block && t < t_end;
   float norm = -1.0f;   // below every real norm
-  if (ok) {
-    const uint4* kr = reinterpret_cast<const uint4*>(key + b * sb + h * sh + static_cast<int64_t>(t) * st);
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kHD / 8; ++c) {
-      const uint4 x = kr[c];
-      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = half_lo<F16>(w[e]), hi = half_hi<F16>(w[e]);
-        acc = acc + lo * lo;
-        acc = acc + hi * hi;
-      }
-    }
-    norm = acc;
-  }
+  if (ok) norm = sq_norm<F16>(key + b * sb + h * sh + static_cast<int64_t>(t) * st);
   int32_t* rec = meta + (static_cast<int64_t>(row) * meta_blocks + j) * reps;
   for (int r = 0; r < reps; ++r) {
     // the lane with the largest (norm, -lane)
@@ -158,6 +172,69 @@ __global__ __launch_bounds__(kBT) void brep_meta_kernel(const uint16_t* __restri
     }
     if (lane == 0) rec[r] = bn >= 0.0f ? j * block + bl : -1;
     if (lane == bl) norm = -1.0f;   // taken
+  }
+}
+
+// Blocks longer than a wave: one workgroup per block.  Thread i holds the
+// norms of its first kRepCache tokens (t_lo + i + kRepNT*c) in registers and
+// recomputes any further ones every round (blocks above kRepNT*kRepCache
+// tokens); each of the R rounds is a workgroup argmax, and the taken tokens
+// are listed in LDS.
+constexpr int kRepNT = 1024;
+constexpr int kRepCache = 16;
+
+template <bool F16>
+__global__ __launch_bounds__(kRepNT) void brep_meta_wide_kernel(const uint16_t* __restrict__ key, int kv_heads,
+                                                                int64_t sb, int64_t sh, int64_t st, int block,
+                                                                int reps, int t_end, int j0,
+                                                                int32_t* __restrict__ meta, int64_t meta_blocks) {
+  constexpr int NW = kRepNT / 64;
+  __shared__ float red_n[NW];
+  __shared__ int red_t[NW];
+  __shared__ int taken[64];
+  const int j = j0 + blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = row / kv_heads, h = row - b * kv_heads;
+  const int t_lo = j * block, t_hi = min(t_end, t_lo + block);
+  const uint16_t* kb = key + b * sb + h * sh;
+  float cache[kRepCache];
+#pragma unroll
+  for (int c = 0; c < kRepCache; ++c) {
+    const int t = t_lo + tid + c * kRepNT;
+    cache[c] = t < t_hi ? sq_norm<F16>(kb + static_cast<int64_t>(t) * st) : -1.0f;
+  }
+  int32_t* rec = meta + (static_cast<int64_t>(row) * meta_blocks + j) * reps;
+  for (int r = 0; r < reps; ++r) {
+    float bn = -1.0f;
+    int bt = 0x7FFFFFFF;
+#pragma unroll
+    for (int c = 0; c < kRepCache; ++c) rep_better(bn, bt, cache[c], t_lo + tid + c * kRepNT);
+    for (int t = t_lo + tid + kRepCache * kRepNT; t < t_hi; t += kRepNT) {
+      bool was = false;
+      for (int i = 0; i < r; ++i) was |= taken[i] == t;
+      if (!was) rep_better(bn, bt, sq_norm<F16>(kb + static_cast<int64_t>(t) * st), t);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float on = __shfl_xor(bn, off);
+      const int ot = __shfl_xor(bt, off);
+      rep_better(bn, bt, on, ot);
+    }
+    if (lane == 0) {
+      red_n[wave] = bn;
+      red_t[wave] = bt;
+    }
+    __syncthreads();
+    bn = red_n[0];
+    bt = red_t[0];
+    for (int w = 1; w < NW; ++w) rep_better(bn, bt, red_n[w], red_t[w]);
+    const int win = bn >= 0.0f ? bt : -1;   // every thread holds the winner
+    if (tid == 0) {
+      rec[r] = win;
+      taken[r] = win;
+    }
+#pragma unroll
+    for (int c = 0; c < kRepCache; ++c)
+      if (win == t_lo + tid + c * kRepNT) cache[c] = -1.0f;
+    __syncthreads();   // red_n / red_t are rewritten next round; taken[r] is visible
   }
 }
 
@@ -256,8 +333,10 @@ __global__ __launch_bounds__(kBT) void scan_partial_kernel(
 // qboracle block scores (EV:5030-5044): per block, the maximum over its
 // history tokens of the partial score on the row's top-|q| dims, from the
 // dim-major copy (consecutive lanes read consecutive tokens of a dim).  A
-// workgroup owns whole blocks, at most kQboTokens tokens; the scores go
-// through LDS to the block maxima.
+// workgroup owns whole blocks, at most kQboTokens tokens, whose scores go
+// through LDS to the block maxima -- or, for blocks longer than that, one
+// block, each thread keeping the maximum of its tokens and the workgroup
+// reducing those.
 // ---------------------------------------------------------------------------
 constexpr int kQboTokens = kBT * 8;
 
@@ -278,8 +357,8 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
   const int j0 = blockIdx.x * blocks_per_wg, j1 = min(nb, j0 + blocks_per_wg);
   const int t0 = j0 * block, t1 = min(history, j1 * block);
   const uint16_t* base = kdm + b * db + (h / group) * dh;
-  for (int i = tid; i < t1 - t0; i += kBT) {
-    const uint16_t* kt = base + t0 + i;
+  auto score = [&](int t) -> float {
+    const uint16_t* kt = base + t;
     float acc = 0.0f;
     for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in order
       float v[8];
@@ -289,8 +368,20 @@ __global__ __launch_bounds__(kBT) void block_max_partial_kernel(
       for (int e = 0; e < 8; ++e)
         if (s0 + e < count) acc = acc + sel_q[s0 + e] * v[e];
     }
-    sc[i] = acc;
+    return acc;
+  };
+  if (block > kQboTokens) {   // one long block (blocks_per_wg = 1)
+    float m = -__builtin_huge_valf();
+    for (int t = t0 + tid; t < t1; t += kBT) m = fmaxf(m, score(t));
+    sc[tid] = m;
+    __syncthreads();
+    if (tid == 0) {
+      for (int i = 1; i < kBT; ++i) m = fmaxf(m, sc[i]);
+      out[static_cast<int64_t>(row) * out_ld + j0] = m;
+    }
+    return;
   }
+  for (int i = tid; i < t1 - t0; i += kBT) sc[i] = score(t0 + i);
   __syncthreads();
   for (int j = j0 + tid; j < j1; j += kBT) {
     const int a = j * block - t0, e = min(t1, (j + 1) * block) - t0;
@@ -365,6 +456,117 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     ids[o] = fv ? tok : -1;
   });
   for (int o = kk2 + tid; o < n_keep; o += kRerankNT) ids[o] = -1;
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kRerankNT)
+    ids[n_keep + i] = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+}
+
+// ---------------------------------------------------------------------------
+// The rerank of rows past rerank_kernel's one-workgroup limits (more than
+// kMaxScan scanned tokens or kMaxCand candidates), and qboracle rows whose
+// candidates run past their scanned tokens, in five launches over a
+// workspace:
+//   dense_partial_kernel  per history token its candidate score: the partial
+//       score where its block was scanned, else `fill` -- finfo(float32).min
+//       for qboracle, which ranks every history token and so reaches unscanned
+//       ones once the scanned run out (EV:5055-5058), -inf (never a
+//       candidate) for qbb / brep;
+//   (qkv_topk_ws)         the n_cand best tokens, ascending;
+//   cand_full_kernel      their full-D scores * scaling, -inf for -inf picks;
+//   (qkv_topk_ws)         the n_keep best candidates;
+//   rerank_finish_kernel  mask and token list as rerank_kernel writes them.
+// Ties go to the lower token at both selections, as in rerank_kernel
+// (ascending positions there are ascending tokens).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBT) void dense_partial_kernel(const float* __restrict__ partial, int64_t partial_ld,
+                                                            const int32_t* __restrict__ blocks, int n_scan,
+                                                            int block, int history, float fill,
+                                                            float* __restrict__ dense, int64_t dense_ld) {
+  const int row = blockIdx.y;
+  const int t = blockIdx.x * kBT + threadIdx.x;
+  if (t >= history) return;
+  const int32_t* br = blocks + static_cast<int64_t>(row) * n_scan;
+  const int j = t / block;
+  int lo = 0, hi = n_scan;   // the first slot whose block id is >= j (ids ascending)
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (br[mid] < j) lo = mid + 1;
+    else hi = mid;
+  }
+  const bool in = lo < n_scan && br[lo] == j;
+  dense[static_cast<int64_t>(row) * dense_ld + t] =
+      in ? partial[static_cast<int64_t>(row) * partial_ld + static_cast<int64_t>(lo) * block + (t - j * block)]
+         : fill;
+}
+
+template <bool F16>
+__global__ __launch_bounds__(kBT) void cand_full_kernel(const uint16_t* __restrict__ query,
+                                                        const uint16_t* __restrict__ key, int q_heads, int group,
+                                                        int64_t sb, int64_t sh, int64_t st,
+                                                        const float* __restrict__ dense, int64_t dense_ld,
+                                                        const int32_t* __restrict__ cand, int n_cand, float scaling,
+                                                        float* __restrict__ cf) {
+  __shared__ __attribute__((aligned(16))) float q_s[kHD];
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int b = row / q_heads, h = row - b * q_heads;
+  for (int d = tid; d < kHD; d += kBT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
+  __syncthreads();
+  const int i = blockIdx.x * kBT + tid;
+  if (i >= n_cand) return;
+  const int tok = cand[static_cast<int64_t>(row) * n_cand + i];
+  const bool ok = dense[static_cast<int64_t>(row) * dense_ld + tok] != -__builtin_huge_valf();
+  cf[static_cast<int64_t>(row) * n_cand + i] =
+      ok ? full_score<F16>(key + b * sb + (h / group) * sh + static_cast<int64_t>(tok) * st, q_s, scaling)
+         : -__builtin_huge_valf();
+}
+
+// One workgroup per row: the protected mask, then the kept candidates (kept
+// holds ascending indices into the row's ascending candidate tokens) in
+// order with the -inf picks dropped, -1 padding, and the protected tail.
+__global__ __launch_bounds__(kRerankNT) void rerank_finish_kernel(
+    const int32_t* __restrict__ cand, const float* __restrict__ cf, int n_cand, const int32_t* __restrict__ kept,
+    int n_kept, int n_keep, int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec,
+    int keep_self, uint8_t* __restrict__ keep_mask, int64_t keep_ld, int32_t* __restrict__ attn_ids, int n_out) {
+  constexpr int NW = kRerankNT / 64;
+  __shared__ int wave_cnt[NW];
+  __shared__ int base_s;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint8_t* mrow = keep_mask + static_cast<int64_t>(row) * keep_ld;
+  for (int t = tid; t < key_count; t += kRerankNT)
+    mrow[t] = (t < sink_end) || (t >= recent_start && t < history) || (keep_self && t == history);
+  if (tid == 0) base_s = 0;
+  __syncthreads();
+  int32_t* ids = attn_ids + static_cast<int64_t>(row) * n_out;
+  const int32_t* krow = kept + static_cast<int64_t>(row) * n_kept;
+  const int32_t* crow = cand + static_cast<int64_t>(row) * n_cand;
+  const float* frow = cf + static_cast<int64_t>(row) * n_cand;
+  for (int o0 = 0; o0 < n_kept; o0 += kRerankNT) {
+    const int o = o0 + tid;
+    int tok = -1;
+    bool ok = false;
+    if (o < n_kept) {
+      const int ci = krow[o];
+      ok = frow[ci] != -__builtin_huge_valf();
+      tok = crow[ci];
+    }
+    const uint64_t m = __ballot(ok);
+    if (lane == 0) wave_cnt[wave] = __popcll(m);
+    __syncthreads();
+    int at = base_s + __popcll(m & ((uint64_t(1) << lane) - 1));
+    for (int w = 0; w < wave; ++w) at += wave_cnt[w];
+    if (ok) {
+      mrow[tok] = 1;
+      ids[at] = (tok >= sink_end && !(tok >= recent_start && tok < history)) ? tok : -1;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int sum = 0;
+      for (int w = 0; w < NW; ++w) sum += wave_cnt[w];
+      base_s += sum;
+    }
+    __syncthreads();
+  }
+  for (int o = base_s + tid; o < n_keep; o += kRerankNT) ids[o] = -1;
   const int extra = sink_end + n_rec + keep_self;
   for (int i = tid; i < extra; i += kRerankNT)
     ids[n_keep + i] = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
@@ -481,6 +683,43 @@ int check_rows(const char* what, int64_t batch, int64_t q_heads, int64_t kv_head
 
 bool kv_aligned(const void* p, const int64_t* s) { return aligned(p, 16) && (s[0] | s[1] | s[2]) % 8 == 0; }
 
+// Whether every row's rerank fits rerank_kernel: at most kMaxScan scanned
+// positions and kMaxCand candidates, and (qboracle, whose candidates may be
+// unscanned tokens) no more candidates than the fewest scanned history
+// tokens a row can have -- then every row's candidates are scanned tokens.
+bool rerank_fits(int64_t history, int64_t n_scan, int64_t block, int64_t n_cand, bool unscanned) {
+  if (n_scan * block > kMaxScan || n_cand > kMaxCand) return false;
+  if (!unscanned) return true;
+  const int64_t fewest = n_scan * block - (cdiv(history, block) * block - history);
+  return n_cand <= fewest;
+}
+
+// Workspace of the general rerank: dense scores [rows, dense_ld], candidate
+// tokens and their full scores [rows, n1], kept indices [rows, n2], then the
+// top-k workspace shared by both selections; 256-byte aligned parts.
+struct WideRerank {
+  int64_t dense_ld, n1, n2, off_cand, off_cf, off_kept, off_topk, topk_bytes, total;
+};
+
+WideRerank wide_rerank_layout(int64_t rows, int64_t history, int64_t n_cand, int64_t n_keep) {
+  auto al = [](int64_t x) { return cdiv(x, 256) * 256; };
+  WideRerank w;
+  w.dense_ld = cdiv(history, 64) * 64;
+  w.n1 = std::min(n_cand, history);
+  w.n2 = std::min(n_keep, w.n1);
+  int64_t off = al(rows * w.dense_ld * 4);
+  w.off_cand = off;
+  off += al(rows * w.n1 * 4);
+  w.off_cf = off;
+  off += al(rows * w.n1 * 4);
+  w.off_kept = off;
+  off += al(rows * w.n2 * 4);
+  w.off_topk = off;
+  w.topk_bytes = std::max(qkv_topk_workspace_bytes(rows, history, w.n1), qkv_topk_workspace_bytes(rows, w.n1, w.n2));
+  w.total = off + al(std::max<int64_t>(w.topk_bytes, 0));
+  return w;
+}
+
 }  // namespace
 }  // namespace qkv
 
@@ -513,8 +752,8 @@ QKV_EXPORT int qkv_block_meta_update(int kind, const void* key, const int64_t* k
   const uint16_t* k = static_cast<const uint16_t*>(key);
   if (kind != QKV_BLOCK_QBB && kind != QKV_BLOCK_BREP)
     return fail(QKV_ERR_INVALID, "%s: unknown selector kind %d", what, kind);
-  if (kind == QKV_BLOCK_BREP && (block > 64 || reps < 1 || reps > block))
-    return fail(QKV_ERR_UNSUPPORTED, "%s: brep needs block <= 64 and 1 <= reps <= block", what);
+  if (kind == QKV_BLOCK_BREP && (reps < 1 || reps > 64 || reps > block))
+    return fail(QKV_ERR_INVALID, "%s: brep needs 1 <= reps <= min(block, 64)", what);
   return with_half(f16, [&](auto ff) {
     constexpr bool F = decltype(ff)::value;
     if (kind == QKV_BLOCK_QBB) {
@@ -522,12 +761,18 @@ QKV_EXPORT int qkv_block_meta_update(int kind, const void* key, const int64_t* k
       qbb_meta_kernel<F><<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1],
                                                k_strides[2], static_cast<int>(block), static_cast<int>(t_end),
                                                static_cast<int>(j0), static_cast<uint16_t*>(meta), meta_blocks);
-    } else {
+    } else if (block <= 64) {
       dim3 grid(static_cast<unsigned>(cdiv(j1 - j0, kBT / 64)), static_cast<unsigned>(batch * kv_heads));
       brep_meta_kernel<F><<<grid, kBT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1],
                                                 k_strides[2], static_cast<int>(block), static_cast<int>(reps),
                                                 static_cast<int>(t_end), static_cast<int>(j0), static_cast<int>(j1),
                                                 static_cast<int32_t*>(meta), meta_blocks);
+    } else {
+      dim3 grid(static_cast<unsigned>(j1 - j0), static_cast<unsigned>(batch * kv_heads));
+      brep_meta_wide_kernel<F><<<grid, kRepNT, 0, st>>>(k, static_cast<int>(kv_heads), k_strides[0], k_strides[1],
+                                                        k_strides[2], static_cast<int>(block), static_cast<int>(reps),
+                                                        static_cast<int>(t_end), static_cast<int>(j0),
+                                                        static_cast<int32_t*>(meta), meta_blocks);
     }
     return check_launch(what);
   });
@@ -610,7 +855,6 @@ QKV_EXPORT int qkv_block_max_partial_scores(const void* query, const void* key_d
   const int64_t nb = block > 0 ? cdiv(history, block) : 0;
   if (history <= 0 || history >= (int64_t(1) << 31) || block <= 0 || out_ld < nb)
     return fail(QKV_ERR_INVALID, "%s: need history, block > 0 and out_ld >= ceil(history/block)", what);
-  if (block > kQboTokens) return fail(QKV_ERR_UNSUPPORTED, "%s: block must be <= %d", what, kQboTokens);
   if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the copy's token axis must be contiguous", what);
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), kHD));
   const int64_t per_wg = std::max<int64_t>(1, kQboTokens / block);
@@ -669,12 +913,22 @@ QKV_EXPORT int64_t qkv_final_list_count(int64_t history, int64_t n_keep, int64_t
   return n_keep + sink_end + n_rec + (keep_self ? 1 : 0);
 }
 
+QKV_EXPORT int64_t qkv_block_rerank_workspace_bytes(int64_t rows, int64_t history, int64_t n_scan, int64_t block,
+                                                    int64_t n_cand, int64_t n_keep, int unscanned) {
+  if (rows <= 0 || rows > 65535 || history <= 0 || history >= (int64_t(1) << 31) || n_scan <= 0 || block <= 0 ||
+      n_cand < 1 || n_keep < 1 || n_keep > n_cand)
+    return -1;
+  if (rerank_fits(history, n_scan, block, n_cand, unscanned != 0)) return 0;
+  return wide_rerank_layout(rows, history, n_cand, n_keep).total;
+}
+
 QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_t* k_strides, int64_t batch,
                                 int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
                                 const float* partial, const float* full, int64_t partial_ld, const int32_t* blocks,
                                 int64_t n_scan, int64_t block, int64_t n_cand, int64_t n_keep, int64_t protect_sink,
                                 int64_t protect_recent, int keep_self, float scaling, uint8_t* keep_mask,
-                                int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int dtype, void* stream) {
+                                int64_t keep_ld, int32_t* attn_ids, int64_t n_out, int unscanned, void* workspace,
+                                int64_t workspace_bytes, int dtype, void* stream) {
   const char* what = "qkv_block_rerank";
   int rc = check_rows(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
@@ -685,11 +939,10 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
   const int64_t history = key_count - 1;
   if (history <= 0 || key_count >= (int64_t(1) << 31) || keep_ld < key_count)
     return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 and keep_ld >= key_count", what);
-  if (block <= 0 || n_scan <= 0 || n_scan * block > kMaxScan || partial_ld < n_scan * block)
-    return fail(QKV_ERR_UNSUPPORTED, "%s: at most %d scanned tokens per row (got %lld)", what, kMaxScan,
-                (long long)(n_scan * block));
-  if (n_cand < 1 || n_cand > kMaxCand || n_keep < 1 || n_keep > n_cand)
-    return fail(QKV_ERR_INVALID, "%s: need 1 <= n_keep <= n_cand <= %d", what, kMaxCand);
+  if (block <= 0 || n_scan <= 0 || n_scan * block >= (int64_t(1) << 30) || partial_ld < n_scan * block)
+    return fail(QKV_ERR_INVALID, "%s: need block, n_scan > 0 and partial_ld >= n_scan * block < 2^30", what);
+  if (n_cand < 1 || n_keep < 1 || n_keep > n_cand)
+    return fail(QKV_ERR_INVALID, "%s: need 1 <= n_keep <= n_cand", what);
   if (k_strides[3] != 1 || !kv_aligned(key, k_strides))
     return fail(QKV_ERR_INVALID, "%s: K rows must be contiguous and 16-byte aligned", what);
   const int64_t sink_end = protect_sink > 0 ? std::min(protect_sink, history) : 0;
@@ -700,6 +953,40 @@ QKV_EXPORT int qkv_block_rerank(const void* query, const void* key, const int64_
     return fail(QKV_ERR_INVALID, "%s: token lists hold %lld entries, the selection needs %lld", what,
                 (long long)n_out, (long long)(n_keep + sink_end + n_rec + (keep_self ? 1 : 0)));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rows = static_cast<int>(batch * q_heads);
+  if (!rerank_fits(history, n_scan, block, n_cand, unscanned != 0)) {
+    const WideRerank w = wide_rerank_layout(rows, history, n_cand, n_keep);
+    if (!workspace || !aligned(workspace, 256) || workspace_bytes < w.total)
+      return fail(QKV_ERR_INVALID, "%s: this rerank needs a 256-byte aligned workspace of %lld bytes, got %lld",
+                  what, (long long)w.total, (long long)workspace_bytes);
+    char* ws = static_cast<char*>(workspace);
+    float* dense = reinterpret_cast<float*>(ws);
+    int32_t* cand = reinterpret_cast<int32_t*>(ws + w.off_cand);
+    float* cf = reinterpret_cast<float*>(ws + w.off_cf);
+    int32_t* kept = reinterpret_cast<int32_t*>(ws + w.off_kept);
+    void* tws = ws + w.off_topk;
+    const float fill = unscanned ? -3.40282347e38f : -__builtin_huge_valf();   // finfo(float32).min / -inf
+    dense_partial_kernel<<<dim3(static_cast<unsigned>(cdiv(history, kBT)), rows), kBT, 0, st>>>(
+        partial, partial_ld, blocks, static_cast<int>(n_scan), static_cast<int>(block), static_cast<int>(history),
+        fill, dense, w.dense_ld);
+    if ((rc = check_launch(what))) return rc;
+    if ((rc = qkv_topk_ws(dense, rows, history, w.dense_ld, w.n1, cand, tws, w.topk_bytes, stream))) return rc;
+    rc = with_half(f16, [&](auto ff) {
+      cand_full_kernel<decltype(ff)::value><<<dim3(static_cast<unsigned>(cdiv(w.n1, kBT)), rows), kBT, 0, st>>>(
+          static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key), static_cast<int>(q_heads),
+          static_cast<int>(q_heads / kv_heads), k_strides[0], k_strides[1], k_strides[2], dense, w.dense_ld, cand,
+          static_cast<int>(w.n1), scaling, cf);
+      return check_launch(what);
+    });
+    if (rc) return rc;
+    if ((rc = qkv_topk_ws(cf, rows, w.n1, w.n1, w.n2, kept, tws, w.topk_bytes, stream))) return rc;
+    rerank_finish_kernel<<<static_cast<unsigned>(rows), kRerankNT, 0, st>>>(
+        cand, cf, static_cast<int>(w.n1), kept, static_cast<int>(w.n2), static_cast<int>(n_keep),
+        static_cast<int>(history), static_cast<int>(key_count), static_cast<int>(sink_end),
+        static_cast<int>(recent_start), static_cast<int>(rec_begin), static_cast<int>(n_rec), keep_self ? 1 : 0,
+        keep_mask, keep_ld, attn_ids, static_cast<int>(n_out));
+    return check_launch(what);
+  }
   return with_scan_vpl(n_scan * block, [&](auto vpl) {
    return with_cand_vpl(n_cand, [&](auto vpl2) {
     return with_half(f16, [&](auto ff) {

@@ -57,7 +57,10 @@ def test_qbb_metadata_and_bounds(block, t):
     assert np.array_equal(out[:, :nb].cpu().numpy().reshape(2, 4, nb), want)
 
 
-@pytest.mark.parametrize("block,reps,t", [(16, 2, 1000), (8, 1, 333), (64, 5, 700), (16, 16, 40)])
+@pytest.mark.parametrize("block,reps,t", [(16, 2, 1000), (8, 1, 333), (64, 5, 700), (16, 16, 40),
+                                          # a workgroup per block: norms in registers, then past 16384 tokens
+                                          # per block recomputed each round
+                                          (128, 3, 1000), (1000, 8, 2500), (20000, 4, 41000)])
 def test_brep_metadata_and_scores(block, reps, t):
     lib = _lib.load()
     k, _, g = _kv(1, 2, t, block * reps + t)
@@ -113,7 +116,8 @@ def test_step_matches_oracle(mode, hq, hkv, t, steps, sink, recent, keep_self):
 
 
 @pytest.mark.parametrize("block,t,hq,hkv,dims", [(16, 1000, 8, 2, 8), (7, 333, 4, 4, 16), (64, 2100, 4, 1, 12),
-                                                 (1, 300, 8, 2, 8), (300, 4000, 4, 2, 128), (2048, 5000, 2, 1, 8)])
+                                                 (1, 300, 8, 2, 8), (300, 4000, 4, 2, 128), (2048, 5000, 2, 1, 8),
+                                                 (3000, 10000, 2, 1, 8), (5000, 12001, 4, 2, 16)])
 def test_qboracle_block_scores_match_oracle(block, t, hq, hkv, dims):
     # block maxima of the partial scores (EV:5030-5044), bit for bit
     from kv_cache_amd.reuse import dim_major_append
@@ -153,12 +157,66 @@ def test_step_reproduces_reference_vectors(name):
         np.testing.assert_allclose(f32(out), g["out"][s], rtol=RTOL, atol=ATOL)
 
 
-def test_qboracle_more_candidates_than_scanned_is_an_error():
-    k, v, g = _kv(1, 2, 600, 9)
-    q = torch.randn((1, 4, 128), generator=g).to(torch.bfloat16).to(DEV)
-    step = BS.BlockSelectDecodeStep("qboracle16q8s2cand10", 1, 4, 2, 128, 1024)
-    with pytest.raises(RuntimeError, match="more candidates than scanned tokens"):
-        step(q, k.to(DEV), v.to(DEV), 0.1)
+@pytest.mark.parametrize("mode,hq,hkv,t,steps", [
+    ("qboracle16q8s2cand10", 4, 2, 3000, 2),      # 10% candidates from 2% scanned: unscanned ones at finfo.min
+    ("qboracle64q8s1cand3", 8, 2, 20000, 1),      # the same at 20000 tokens, 64-token blocks
+    ("qbb16q8s50cand4", 4, 2, 90000, 1),          # 45000 scanned tokens per row
+    ("qbb16q8s20cand10", 4, 1, 60000, 1),         # 6000 candidates per row
+    ("brep20000r2q8s100cand2", 4, 2, 45000, 1),   # every block scanned (45000 tokens), 20000-token blocks
+    ("brep256r2q8s30cand6", 8, 2, 20000, 2),      # 6000 scanned tokens, 1200 candidates: one workgroup
+])
+def test_step_past_the_one_workgroup_rerank_matches_oracle(mode, hq, hkv, t, steps):
+    # rows the one-workgroup rerank cannot hold run the general rerank (dense
+    # candidate scores, two staged top-k selections); masks still bit-exact
+    kind, block, reps, dims, scan, cand = BS.parse_block_mode(mode)
+    k, v, g = _kv(1, hkv, t + steps, hq * t + 5)
+    qs = torch.randn((steps, 1, hq, 128), generator=g).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    step = BS.BlockSelectDecodeStep(mode, 1, hq, hkv, 128, t + steps + 8, top_fraction=0.02, protect_sink=3,
+                                    protect_recent=5, keep_self=True)
+    for s in range(steps):
+        n = t + s + 1
+        out = step(qs[s].to(DEV), kd[:, :, :n], vd[:, :, :n], 128 ** -0.5)
+        want, keep = R.block_select_step(f32(qs[s]), f32(k[:, :, :n]), f32(v[:, :, :n]), KINDS[kind], block, dims,
+                                         scan, cand, 0.02, 128 ** -0.5, 3, 5, True, reps)
+        assert np.array_equal(step.final_mask().cpu().numpy(), keep), (mode, s)
+        np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+
+
+def test_rerank_general_path_equals_one_workgroup_path():
+    # Rows that fit both reranks: the qboracle flag with more candidates than
+    # the fewest scanned history tokens a row could have (its last, partial
+    # block scanned) takes the general path, but these rows never scan that
+    # block, so their candidates are all scanned tokens and both paths must
+    # write the same mask and token list; the partial scores carry ties.
+    lib = _lib.load()
+    hq, hkv, t, block, n_scan = 4, 2, 5000, 16, 40
+    history = t - 1
+    nb = -(-history // block)
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn((1, hkv, t, 128), generator=g).to(torch.bfloat16).to(DEV)
+    q = torch.randn((1, hq, 128), generator=g).to(torch.bfloat16).to(DEV)
+    blocks = torch.stack([torch.randperm(nb - 1, generator=g)[:n_scan].sort().values for _ in range(hq)])
+    blocks = blocks.to(torch.int32).to(DEV).contiguous()
+    partial = (torch.randint(0, 50, (hq, n_scan * block), generator=g).float() / 4).to(DEV)
+    n_cand, n_keep = n_scan * block - 2, 100
+    n_out = int(lib.qkv_final_list_count(history, n_keep, 3, 5, 1))
+    assert lib.qkv_block_rerank_workspace_bytes(hq, history, n_scan, block, n_cand, n_keep, 0) == 0
+    need = int(lib.qkv_block_rerank_workspace_bytes(hq, history, n_scan, block, n_cand, n_keep, 1))
+    assert need > 0
+    outs = []
+    for unscanned in (0, 1):
+        keep = torch.zeros((hq, t + 8), dtype=torch.uint8, device=DEV)
+        ids = torch.full((hq * n_out,), -7, dtype=torch.int32, device=DEV)
+        ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=DEV) if unscanned else None
+        _lib.check(lib.qkv_block_rerank(
+            q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), 1, hq, hkv, t, 128, partial.data_ptr(), None,
+            n_scan * block, blocks.data_ptr(), n_scan, block, n_cand, n_keep, 3, 5, 1, 0.088, keep.data_ptr(), t + 8,
+            ids.data_ptr(), n_out, unscanned, _lib.ptr(ws), need if unscanned else 0, 0, _lib.stream_of(q)))
+        outs.append((keep, ids))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert int(outs[0][0][:, :history].sum()) > hq * n_keep // 2
 
 
 def test_new_sequence_resets():
@@ -187,13 +245,15 @@ def test_longer_new_sequence_resets():
         assert torch.equal(step.final_mask(), fresh.final_mask()), mode
 
 
-def test_limits_are_errors():
-    with pytest.raises(RuntimeError, match="at most 40960"):
-        BS.BlockSelectDecodeStep("qbb16q8s50cand4", 1, 4, 2, 128, 100000)
-    with pytest.raises(RuntimeError, match="at most 4096"):
-        BS.BlockSelectDecodeStep("qbb16q8s50cand20", 1, 4, 2, 128, 40000)
-    with pytest.raises(RuntimeError, match="at most 64"):
-        BS.BlockSelectDecodeStep("brep128r2q8s6cand2", 1, 4, 2, 128, 4000)
+def test_bad_rerank_arguments_are_errors():
+    lib = _lib.load()
+    assert lib.qkv_block_rerank_workspace_bytes(4, 1000, 10, 16, 10, 11, 0) == -1     # n_keep > n_cand
+    assert lib.qkv_block_rerank_workspace_bytes(4, 100000, 3000, 16, 100, 10, 0) > 0  # 48000 scanned tokens
+    assert lib.qkv_block_rerank_workspace_bytes(4, 100000, 100, 16, 5000, 10, 0) > 0  # 5000 candidates
+    assert lib.qkv_block_rerank_workspace_bytes(4, 10000, 10, 16, 200, 10, 1) > 0     # qboracle, 200 > 160 scanned
+    assert lib.qkv_block_rerank_workspace_bytes(4, 10000, 10, 16, 100, 10, 1) == 0
+    with pytest.raises(RuntimeError, match="at most 64 representatives"):
+        BS.BlockSelectDecodeStep("brep128r65q8s6cand2", 1, 4, 2, 128, 4000)
 
 
 @pytest.mark.parametrize("mode,t", [("qbb64q8s3cand3", 4000), ("brep16r4q8s12cand4", 3001)])
@@ -221,6 +281,6 @@ def test_rerank_with_and_without_scan_full_scores(mode, t):
             q.data_ptr(), kd.data_ptr(), _lib.strides(*kd.stride()), 1, hq, hkv, t, 128,
             step.partial[: rows * n_tok].data_ptr(), _lib.ptr(full), n_tok, step.blocks[: rows * n_scan].data_ptr(),
             n_scan, step.block, n_cand, n_keep, 3, 5, 1, 0.088, keep.data_ptr(), step.capacity, ids.data_ptr(), n_out,
-            0, _lib.stream_of(q)))
+            0, None, 0, 0, _lib.stream_of(q)))
         assert torch.equal(keep[:, :t], want_mask), full is None
         assert torch.equal(ids, want_ids), full is None
