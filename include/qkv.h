@@ -545,6 +545,20 @@ int64_t qkv_threshold_mask_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, uint8_t* mask,
                        int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The reuse step's candidates (EV:3988, 4136-4144): qkv_reuse_partial_scores
+ * into partial (row stride partial_ld), then mask = partial >= the row's
+ * k-th largest (qkv_threshold_mask); thr_out f32 [batch * q_heads]
+ * (optional) receives the k-th largest.  One launch per call where the
+ * rows fit one workgroup (history <= 40960, head_dim <= 128, a 16-byte
+ * aligned copy), the two launches otherwise; workspace as for
+ * qkv_threshold_mask (qkv_threshold_mask_workspace_bytes(batch * q_heads,
+ * history, k)).  No reference counterpart as one call: the reference runs
+ * the two steps separately (QK:63-96, then torch.topk at EV:3988). */
+int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
+                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
+                         int64_t dim_count, int64_t k, float* partial, int64_t partial_ld, uint8_t* mask,
+                         int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Dim-major copy of K tokens [t_begin, t_end): key_dim_major[b, j, d, t] =
  * key[b, j, t, d] (the reference's incremental transposed copy,
  * EV:2018-2042, kept per KV head).  k_strides {b,h,t,d} (d contiguous);

@@ -521,6 +521,141 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
   }
 }
 
+// The step's candidates in one launch (rows of at most kWideMax history
+// tokens, head_dim <= 128, a 16-byte aligned dim-major copy): one 1024-thread
+// workgroup per row forms the row's partial scores as reuse_partial_kernel
+// does (eight consecutive tokens per thread and chunk, NCH chunks, the same
+// loads and summation order), writes them, counts their first radix digit
+// as they are formed, selects the k-th largest in registers (WideSelect)
+// and writes mask = score >= it; thr_out (optional) receives it.  The row's
+// scores never make the round trip through memory that the two-launch form
+// (partial scores, then reuse_mask_wide_kernel) takes.  With rows a multiple
+// of 8 the rows are spread so that each XCD (blockIdx.x % 8 on gfx950) runs
+// rows/8 consecutive ones -- the query heads of one KV head, which read the
+// same copy rows, share that XCD's L2.  gate: as reuse_mask_wide_kernel.
+template <int DT, int NCH>
+__global__ __launch_bounds__(kWideNT) void reuse_candidates_kernel(
+    const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm, int q_heads,
+    int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd, float* __restrict__ out,
+    int64_t out_ld, int k, uint8_t* __restrict__ mask, int64_t mask_ld, float* __restrict__ thr_out,
+    const uint8_t* __restrict__ gate, int gate_refresh, int rows) {
+  using E = typename Elem<DT>::T;
+  constexpr int VPL = 8 * NCH;
+  using WS = WideSelect<VPL, false>;
+  __shared__ typename WS::Shared wsh;
+  __shared__ float q_s[128];
+  __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
+  __shared__ int sel_idx[kMaxDims];
+  __shared__ float sel_q[kMaxDims];
+  const int tid = threadIdx.x;
+  const int row = rows % 8 == 0 ? (blockIdx.x % 8) * (rows / 8) + blockIdx.x / 8 : blockIdx.x;
+  if (gate) {   // a lagged step: rows that keep no new candidates are skipped (uniform)
+    __shared__ int gate_cnt[kWideNT / 64];
+    if (!lag_refreshes(gate, gate_refresh, rows, row, gate_cnt)) return;
+  }
+  const int b = row / q_heads, h = row - b * q_heads;
+  if (tid < head_dim) q_s[tid] = Elem<DT>::load(query + static_cast<int64_t>(row) * head_dim + tid);
+#pragma unroll
+  for (int j = 0; j < WS::NB / kWideNT; ++j) wsh.hist[0][tid + kWideNT * j] = 0;
+  __syncthreads();
+  rank_dims128(q_s, key_s, head_dim, count, sel_idx, sel_q);   // (ends with a barrier)
+
+  WS ws;
+  int ninf = 0;
+  const E* base = kdm + b * sb + (h / group) * sh;
+  float* orow = out + static_cast<int64_t>(row) * out_ld;
+  const bool ovec = (reinterpret_cast<uintptr_t>(orow) & 15) == 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int t0 = (c * kWideNT + tid) * 8;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    if (t0 + 8 <= history) {
+      for (int s0 = 0; s0 < count; s0 += 8) {   // eight dims' loads in flight, added in selection order
+        float v[8][8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) load8<DT>(base + sel_idx[min(s0 + j, count - 1)] * sd + t0, v[j]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (s0 + j < count) {
+            const float qs = sel_q[s0 + j];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[j][i];
+          }
+        }
+      }
+      if (ovec) {
+        *reinterpret_cast<float4*>(orow + t0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        *reinterpret_cast<float4*>(orow + t0 + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) orow[t0 + i] = acc[i];
+      }
+    } else if (t0 < history) {   // the row's last n < 8 tokens: clamped in-row loads, n stored
+      const int n = history - t0;
+      for (int s0 = 0; s0 < count; s0 += 8) {
+        float v[8][8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const E* p = base + sel_idx[min(s0 + j, count - 1)] * sd + t0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[j][i] = Elem<DT>::load(p + min(i, n - 1));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (s0 + j < count) {
+            const float qs = sel_q[s0 + j];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + qs * v[j][i];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < n) orow[t0 + i] = acc[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ws.set(8 * c + i, acc[i], t0 + i < history);
+      ws.count(8 * c + i, wsh, ninf);
+    }
+  }
+  ws.count_done(wsh, ninf);
+  ws.run_counted(k, wsh);
+  if (thr_out) {   // the k-th largest: the smallest key at or above theta
+    __shared__ uint32_t wave_min[kWideNT / 64];
+    uint32_t m = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (ws.on(i) && ws.u[i] >= ws.theta) m = min(m, ws.u[i]);
+    m = wave_minmax_u32<false>(m);
+    if ((tid & 63) == 0) wave_min[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < kWideNT / 64; ++w) m = min(m, wave_min[w]);
+      thr_out[row] = sortable_f32(min(m, wave_min[0]));
+    }
+  }
+  uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
+  const bool mvec = (reinterpret_cast<uintptr_t>(mrow) & 7) == 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int t0 = (c * kWideNT + tid) * 8;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      lo |= static_cast<uint32_t>(ws.on(8 * c + i) && ws.u[8 * c + i] >= ws.theta) << (8 * i);
+      hi |= static_cast<uint32_t>(ws.on(8 * c + 4 + i) && ws.u[8 * c + 4 + i] >= ws.theta) << (8 * i);
+    }
+    if (mvec && t0 + 8 <= history) {
+      *reinterpret_cast<uint2*>(mrow + t0) = make_uint2(lo, hi);
+    } else {
+      for (int i = 0; i < 8 && t0 + i < history; ++i) mrow[t0 + i] = ((i < 4 ? lo >> (8 * i) : hi >> (8 * (i - 4))) & 1u);
+    }
+  }
+}
+
 // out[r, i] = values[r, cols[i]] for i < n_cols (the sampled partial scores
 // of the sample_quantile candidate selection, EV:3972-3984).
 __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restrict__ values, int64_t ld,
@@ -922,6 +1057,46 @@ int threshold_mask_impl(const char* what, const float* values, int64_t rows, int
   return check_launch(what);
 }
 
+constexpr int64_t kFusedCandRows = 128;
+
+// Partial scores into partial, then mask = partial >= the row's k-th
+// largest (thr_out: the thresholds): one launch (reuse_candidates_kernel)
+// where the row fits it, else reuse_partial_kernel and threshold_mask_impl.
+template <int DT> struct RunCandidates {
+  static int run(const char* what, const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq,
+                 int64_t Hkv, int64_t T, int64_t D, int count, int64_t k, float* partial, int64_t partial_ld,
+                 uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
+                 hipStream_t st, const uint8_t* gate, int refresh) {
+    using E = typename Elem<DT>::T;
+    const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
+    const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
+    const int64_t rows = B * Hq;
+    // One launch pays off once the rows fill the GPU: measured at 32768 tokens,
+    // 32 rows took 27.1 us fused against 26.3 us for the two launches (and more
+    // inside a decode step, where the copy's rows come from HBM), 128 rows 31.1
+    // against 41.1 us, 256 rows 40.4 against 58.1 us.
+    if (vec && T <= kWideMax && D <= 128 && rows >= kFusedCandRows) {
+      auto launch = [&](auto nch) {
+        reuse_candidates_kernel<DT, decltype(nch)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+            static_cast<const E*>(q), static_cast<const E*>(kdm), static_cast<int>(Hq), static_cast<int>(Hq / Hkv),
+            static_cast<int>(T), static_cast<int>(D), count, ks[0], ks[1], ks[2], partial, partial_ld,
+            static_cast<int>(k), mask, mask_ld, thr_out, gate, refresh, static_cast<int>(rows));
+        return check_launch(what);
+      };
+      const int64_t per = 8 * kWideNT;   // tokens per chunk
+      if (T <= per) return launch(std::integral_constant<int, 1>{});
+      if (T <= 2 * per) return launch(std::integral_constant<int, 2>{});
+      if (T <= 3 * per) return launch(std::integral_constant<int, 3>{});
+      if (T <= 4 * per) return launch(std::integral_constant<int, 4>{});
+      return launch(std::integral_constant<int, 5>{});
+    }
+    int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, gate, refresh);
+    if (rc) return rc;
+    return threshold_mask_impl(what, partial, rows, T, partial_ld, k, mask, mask_ld, thr_out, workspace,
+                               workspace_bytes, st, gate, refresh);
+  }
+};
+
 }  // namespace
 }  // namespace qkv
 
@@ -1187,26 +1362,36 @@ QKV_EXPORT int qkv_reuse_lag_candidates(const void* query, const void* key_dim_m
   const uint8_t* gate = refresh == QKV_REFRESH_ALL ? nullptr : flags;
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
                                                        std::min<int64_t>(head_dim, kMaxDims)));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case QKV_DTYPE_BF16:
-      rc = RunReusePartial<QKV_DTYPE_BF16>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
-                                                head_dim, count, partial, partial_ld, st, gate, refresh);
-      break;
-    case QKV_DTYPE_FP16:
-      rc = RunReusePartial<QKV_DTYPE_FP16>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
-                                                head_dim, count, partial, partial_ld, st, gate, refresh);
-      break;
-    case QKV_DTYPE_FP32:
-      rc = RunReusePartial<QKV_DTYPE_FP32>::run(query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
-                                                head_dim, count, partial, partial_ld, st, gate, refresh);
-      break;
-    default:
-      return fail(QKV_ERR_INVALID, "%s: unsupported dtype %d", what, dtype);
-  }
+  return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
+                                       history, head_dim, count, k, partial, partial_ld, mask, mask_ld, nullptr,
+                                       workspace, workspace_bytes, static_cast<hipStream_t>(stream), gate, refresh);
+}
+
+QKV_EXPORT int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                    int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                                    int64_t head_dim, int64_t dim_count, int64_t k, float* partial,
+                                    int64_t partial_ld, uint8_t* mask, int64_t mask_ld, float* thr_out,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* what = "qkv_reuse_candidates";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
-  return threshold_mask_impl(what, partial, rows, history, partial_ld, k, mask, mask_ld, nullptr, workspace,
-                             workspace_bytes, st, gate, refresh);
+  if (!query || !key_dim_major || !kdm_strides || !partial || !mask || !workspace)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || partial_ld < history || mask_ld < history || k < 1 ||
+      k > history)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, partial_ld and mask_ld >= history",
+                what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
+  const int64_t need = mask_ws_bytes(batch * q_heads, history, k);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
+                                                       std::min<int64_t>(head_dim, kMaxDims)));
+  return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
+                                       history, head_dim, count, k, partial, partial_ld, mask, mask_ld, thr_out,
+                                       workspace, workspace_bytes, static_cast<hipStream_t>(stream), nullptr,
+                                       QKV_REFRESH_ALL);
 }
 
 QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k,

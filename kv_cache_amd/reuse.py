@@ -415,9 +415,11 @@ class ReuseDecodeStep:
         selection (EV:3958-3989, 4116-4145) into ``current``; the thresholds
         into ``self.thresholds`` where a later step reads them."""
         lib = _lib.load()
-        reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         requested = budget_count(history, self.cand_fraction)
         n_s = self.columns.count(history) if self.selection == "sample_quantile" else 0
+        topk_path = not (self.selection == "previous_threshold" and previous_thresholds) and not n_s
+        if not topk_path:
+            reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
         if self.selection == "previous_threshold" and previous_thresholds:   # EV:3967-3971
             candidate_mask(self.partial, history, "previous_threshold", requested, current, self.thresholds,
                            self.mask_ws)
@@ -430,9 +432,15 @@ class ReuseDecodeStep:
         else:                                                                 # EV:3988
             self.mask_ws = self._grow(self.mask_ws,
                                       lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
-            # the threshold is kept only where a later step reads it
-            candidate_mask(self.partial, history, "topk", requested, current,
-                           self.thresholds if self.selection != "topk" else None, self.mask_ws)
+            # partial scores, threshold and mask in one launch where a row fits one
+            # workgroup; the threshold is kept only where a later step reads it
+            with torch.cuda.device(q.device):
+                _lib.check(lib.qkv_reuse_candidates(
+                    q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), _dtype_code(q), self.batch,
+                    self.q_heads, self.kv_heads, history, self.head_dim, self.dims, requested,
+                    self.partial.data_ptr(), self.partial.stride(0), current.data_ptr(), current.stride(0),
+                    _lib.ptr(self.thresholds) if self.selection != "topk" else None, self.mask_ws.data_ptr(),
+                    self.mask_ws.numel() * 4, _lib.stream_of(q)))
 
     def _select_attend(self, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
                        current: torch.Tensor, previous: torch.Tensor | None,

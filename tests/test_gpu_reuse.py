@@ -217,6 +217,58 @@ def test_reuse_partial_scores_ties_and_ragged_tails(dtype, d, hist, dims):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype,b,hist,dims,gated", [
+    (torch.bfloat16, 4, 32790, 8, False),    # 128 rows: the one-launch kernel, five 8192-token chunks
+    (torch.float16, 4, 5001, 16, False),     # one chunk, a short last 8-token group
+    (torch.float32, 8, 20003, 8, False),     # 256 rows, three chunks
+    (torch.bfloat16, 4, 9000, 8, True),      # lagged steps: rows whose flag is clear stay untouched
+    (torch.bfloat16, 1, 9000, 8, False),     # 32 rows: the two-launch form
+])
+def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated):
+    # partial scores, the k-th largest and the mask in one call: scores bit-exact
+    # to the oracle, mask = score >= the k-th largest (ties all kept), threshold
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(hist + b + dims)
+    hq, hkv, d = 32, 8, 128
+    rows = b * hq
+    q = torch.randn((b, hq, d), generator=gen).to(dtype)
+    k = torch.randn((b, hkv, hist, d), generator=gen)
+    k[0, 0, 7] = k[0, 0, 3]   # equal scores at the threshold's neighbourhood are kept together
+    k = k.to(dtype)
+    kdm = torch.zeros((b, hkv, d, hist + 24), dtype=dtype, device=DEV)
+    RU.dim_major_append(k.to(DEV), kdm, 0, hist)
+    kk = -(-hist * 5 // 100)
+    part = torch.full((rows, hist + 9), 7.0, device=DEV)
+    mask = torch.full((rows, hist + 9), 9, dtype=torch.uint8, device=DEV)
+    thr = torch.zeros(rows, device=DEV)
+    ws = torch.empty((lib.qkv_threshold_mask_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
+    flags = (torch.arange(rows) % 3 == 0).to(torch.uint8).to(DEV)
+    qd = q.to(DEV)
+    if gated:
+        _lib.check(lib.qkv_reuse_lag_candidates(
+            qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), _lib.DTYPE_CODES[dtype], b, hq, hkv, hist, d,
+            dims, kk, flags.data_ptr(), 2, part.data_ptr(), part.stride(0), mask.data_ptr(), mask.stride(0),
+            ws.data_ptr(), ws.numel() * 4, _lib.stream_of(qd)))
+    else:
+        _lib.check(lib.qkv_reuse_candidates(
+            qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), _lib.DTYPE_CODES[dtype], b, hq, hkv, hist, d,
+            dims, kk, part.data_ptr(), part.stride(0), mask.data_ptr(), mask.stride(0), thr.data_ptr(),
+            ws.data_ptr(), ws.numel() * 4, _lib.stream_of(qd)))
+    want = R.partial_scores(f32(q), np.repeat(f32(k), hq // hkv, axis=1), dims).reshape(rows, hist)
+    kth = -np.sort(-want, axis=1)[:, kk - 1 : kk]
+    got_p, got_m = part.cpu().numpy(), mask.cpu().numpy()
+    on = flags.cpu().numpy().astype(bool) if gated else np.ones(rows, bool)
+    assert np.array_equal(got_p[on, :hist], want[on])
+    assert np.array_equal(got_m[on, :hist].astype(bool), (want >= kth)[on])
+    assert (got_p[:, hist:] == 7.0).all() and (got_m[:, hist:] == 9).all()   # nothing past the history
+    if gated:
+        assert (got_p[~on] == 7.0).all() and (got_m[~on] == 9).all()
+    else:
+        assert np.array_equal(thr.cpu().numpy(), kth[:, 0])
+
+
 def test_reuse_select_ties_and_missing_masks():
     # Duplicate keys give equal scores: the lower index wins; previous masks absent.
     gen = torch.Generator().manual_seed(1)
