@@ -715,6 +715,8 @@ def run_reuse(args) -> dict:
     cur, prev, fin = st0.cand[1 - st0.flip], st0.cand[st0.flip], st0.fin
     if lagged:   # the union the lagged step reranked (previous final | candidates | protected ranges)
         union = int(st0.union[:, :hist_fixed].count_nonzero())
+    elif st0.bits:
+        union = int(RU.expand_bits((cur | prev) | fin, hist_fixed).count_nonzero())
     else:
         union = int(((cur[:, :hist_fixed] | prev[:, :hist_fixed]) | fin[:, :hist_fixed]).count_nonzero())
     n_out = st0.n_out
@@ -762,7 +764,8 @@ def run_reuse(args) -> dict:
 
     def run_mask():
         for layer in range(layers):
-            RU.threshold_mask(steps[layer].partial, hist_fixed, requested, steps[layer].cand[0], mask_ws[layer])
+            RU.candidate_mask(steps[layer].partial, hist_fixed, "topk", requested, steps[layer].cand[0], None,
+                              mask_ws[layer])
 
     if n_s:   # the sampled columns gathered (index and score), then the mask pass
         mask_name, mask_bytes = "sample_quantile_mask", n_s * 4 + rows * n_s * 8 + rows * hist_fixed * (4 + 1)
@@ -788,12 +791,13 @@ def run_reuse(args) -> dict:
     def run_select():
         for layer in range(layers):
             st, kk, _ = fixed(layer)
-            RU._lib.check(lib.qkv_reuse_select(
+            select = lib.qkv_reuse_select_bits if st.bits else lib.qkv_reuse_select
+            RU._lib.check(select(
                 qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv, hist_fixed + 1, d,
-                st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), cap, c["sink"], c["recent"],
-                c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
+                st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), st.fin.stride(0), c["sink"],
+                c["recent"], c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
                 st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_sel, st.fin.data_ptr(),
-                cap, RU._lib.stream_of(qs[layer])))
+                st.fin.stride(0), RU._lib.stream_of(qs[layer])))
 
     def run_expand():
         for layer in range(layers):

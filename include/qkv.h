@@ -376,6 +376,20 @@ int qkv_reuse_select(const void* query, const void* key, const int64_t* k_stride
                      int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                      uint8_t* history_final, int64_t history_final_ld, void* stream);
 
+/* qkv_reuse_select on bitsets: current, previous, previous_final and
+ * history_final are bitsets (bit t % 64 of uint64 word t / 64, row stride
+ * words_ld / history_final_ld words, 8-byte aligned) instead of byte masks;
+ * everything else as qkv_reuse_select.  The compact state the reference
+ * names for its reuse step (bitset OR of the masks, no dense per-token byte
+ * mask); no reference counterpart as a kernel. */
+int qkv_reuse_select_bits(const void* query, const void* key, const int64_t* k_strides, int dtype, int64_t batch,
+                          int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
+                          const uint64_t* current, const uint64_t* previous, const uint64_t* previous_final,
+                          int64_t words_ld, int64_t protect_sink, int64_t protect_recent, double top_fraction,
+                          int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
+                          int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                          uint64_t* history_final, int64_t history_final_ld, void* stream);
+
 /* Workspace bytes of qkv_qabs_candidate_select (0 for histories of at most
  * 40960 positions, which one workgroup per row selects; -1 for bad sizes). */
 int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history, double candidate_fraction);
@@ -431,11 +445,14 @@ int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selectio
  *     data and not checked - and k = the sample's budget), written to
  *     thresholds;
  *   QKV_CAND_PREVIOUS_THRESHOLD: thresholds[r] as given (EV:3967-3971).
- * values f32 [rows, ld]; mask uint8 row stride mask_ld; thresholds f32
- * [rows] (required for the last two). */
+ * values f32 [rows, ld]; mask uint8 row stride mask_ld, or bits (a bitset:
+ * bit t % 64 of uint64 word t / 64, row stride bits_ld words, 8-byte
+ * aligned) -- exactly one of the two; thresholds f32 [rows] (required for
+ * the last two). */
 int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int selection, int64_t k,
                        const int32_t* sample_cols, int64_t n_sample, float* thresholds, uint8_t* mask,
-                       int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
+                       int64_t mask_ld, uint64_t* bits, int64_t bits_ld, void* workspace, int64_t workspace_bytes,
+                       void* stream);
 
 /* The refresh test of the lagged reuse modes (lagtop2 / lagrefresh{N} /
  * qdrift[maj|head|share|cos|coshead] / pconf{T} before qabs{S}cand{pct},
@@ -547,8 +564,10 @@ int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld,
 
 /* The reuse step's candidates (EV:3988, 4136-4144): qkv_reuse_partial_scores
  * into partial (row stride partial_ld), then mask = partial >= the row's
- * k-th largest (qkv_threshold_mask); thr_out f32 [batch * q_heads]
- * (optional) receives the k-th largest.  One launch per call where the
+ * k-th largest (qkv_threshold_mask), as a byte mask (mask, row stride
+ * mask_ld) or a bitset (bits: bit t % 64 of uint64 word t / 64, row stride
+ * bits_ld words, 8-byte aligned) -- exactly one of the two; thr_out f32
+ * [batch * q_heads] (optional) receives the k-th largest.  One launch per call where the
  * rows fit one workgroup (history <= 40960, head_dim <= 128, a 16-byte
  * aligned copy), the two launches otherwise; workspace as for
  * qkv_threshold_mask (qkv_threshold_mask_workspace_bytes(batch * q_heads,
@@ -557,7 +576,8 @@ int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld,
 int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
                          int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
                          int64_t dim_count, int64_t k, float* partial, int64_t partial_ld, uint8_t* mask,
-                         int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes, void* stream);
+                         int64_t mask_ld, uint64_t* bits, int64_t bits_ld, float* thr_out, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 /* Dim-major copy of K tokens [t_begin, t_end): key_dim_major[b, j, d, t] =
  * key[b, j, t, d] (the reference's incremental transposed copy,

@@ -72,7 +72,8 @@ _PROTOTYPES = {
     "qkv_reuse_select": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
                                 _i64, _f64, _i32, _f32, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "qkv_candidate_mask_workspace_bytes": (_i64, [_i64, _i64, _i32, _i64, _i64]),
-    "qkv_candidate_mask": (_i32, [_vp, _i64, _i64, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "qkv_candidate_mask": (_i32, [_vp, _i64, _i64, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
+                                  _vp]),
     "qkv_reuse_lag_flags": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _P(_i64),
                                    _i64, _vp, _i64, _f32, _f32, _vp, _vp, _i64, _vp]),
     "qkv_reuse_lag_flags_workspace_bytes": (_i64, [_i64, _i64]),
@@ -108,7 +109,9 @@ _PROTOTYPES = {
                                 _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp]),
     "qkv_block_rerank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
     "qkv_reuse_candidates": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
-                                    _vp, _i64, _vp, _vp, _i64, _vp]),
+                                    _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
+    "qkv_reuse_select_bits": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
+                                     _i64, _i64, _f64, _i32, _f32, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
 }
 
 _LIB = None

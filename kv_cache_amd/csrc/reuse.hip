@@ -182,6 +182,46 @@ __global__ __launch_bounds__(kRT) void reuse_mask_kernel(const float* __restrict
   }
 }
 
+// reuse_mask_kernel's mask as a bitset (64 positions per word): each wave
+// writes the ballots of its 64-position words, NW words per wave.
+__global__ __launch_bounds__(kRT) void reuse_mask_bits_kernel(const float* __restrict__ values, int64_t ld, int n,
+                                                              const int32_t* __restrict__ sel, int k,
+                                                              const float* __restrict__ thr_in,
+                                                              uint64_t* __restrict__ bits, int64_t bits_ld,
+                                                              float* __restrict__ thr_out) {
+  constexpr int NW = 4;   // words per wave
+  __shared__ float red[kRT / 64];
+  const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* vrow = values + static_cast<int64_t>(row) * ld;
+  float thr;
+  if (sel) {
+    const int32_t* srow = sel + static_cast<int64_t>(row) * k;
+    thr = __builtin_huge_valf();
+    for (int i = tid; i < k; i += kRT) thr = fminf(thr, vrow[srow[i]]);
+    for (int off = 32; off > 0; off >>= 1) thr = fminf(thr, __shfl_xor(thr, off));
+    if (lane == 0) red[wave] = thr;
+    __syncthreads();
+    thr = fminf(fminf(red[0], red[1]), fminf(red[2], red[3]));
+  } else {
+    thr = thr_in[row];
+  }
+  if (thr_out && blockIdx.x == 0 && tid == 0) thr_out[row] = thr;
+  uint64_t* brow = bits + static_cast<int64_t>(row) * bits_ld;
+  const int w0 = (blockIdx.x * (kRT / 64) + wave) * NW;
+  float v[NW];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int t = (w0 + j) * 64 + lane;
+    v[j] = t < n ? vrow[t] : -__builtin_huge_valf();
+  }
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int t = (w0 + j) * 64 + lane;
+    const uint64_t m = __ballot(t < n && v[j] >= thr);
+    if (lane == 0 && (w0 + j) * 64 < n) brow[w0 + j] = m;
+  }
+}
+
 // The sample_quantile candidate mask (EV:3972-3987) of rows with at most kRT
 // sampled columns, in one launch: every workgroup of a row gathers the row's
 // samples (one per thread, its own tile's values already in flight), counts
@@ -224,7 +264,7 @@ __global__ __launch_bounds__(kRT) void sample_mask_kernel(const float* __restric
   __syncthreads();
   const float thr = thr_s;
   if (thr_out && blockIdx.x == 0 && tid == 0) thr_out[row] = thr;
-  if (t0 >= n) return;
+  if (t0 >= n || !mask) return;   // (mask null: the threshold only)
   uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
   if (full) {
     uint32_t w[4];
@@ -246,8 +286,10 @@ __global__ __launch_bounds__(kRT) void sample_mask_kernel(const float* __restric
 // DFIX = 128 fixes the head size so that a token's 16 row loads issue at once;
 // registers are held to five waves per SIMD so that a row's 33 workgroups
 // times 32 rows are resident together (at three, a second batch waited).
+// BITS: the three masks are bitsets (64 positions per uint64 word, mask_ld
+// in words) instead of byte masks.
 // ---------------------------------------------------------------------------
-template <int DT, int DFIX>
+template <int DT, int DFIX, bool BITS>
 __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void reuse_scores_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ key,
     int q_heads, int group, int history, int head_dim, int64_t sb, int64_t sh, int64_t st, bool kvec,
@@ -267,7 +309,17 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
   const int t0 = tile0 + tid * 4;
   const int64_t moff = static_cast<int64_t>(row) * mask_ld + t0;
   uint32_t bits = 0;
-  if (mvec && t0 + 4 <= history) {
+  if (BITS) {   // positions t0..t0+3 lie in one word; bits past the history are clear
+    if (t0 < history) {
+      const int64_t w = static_cast<int64_t>(row) * mask_ld + (t0 >> 6);
+      const int sh4 = t0 & 63;
+      uint64_t u = reinterpret_cast<const uint64_t*>(cur)[w];
+      if (prev) u |= reinterpret_cast<const uint64_t*>(prev)[w];
+      if (fin) u |= reinterpret_cast<const uint64_t*>(fin)[w];
+      const int n = min(4, history - t0);
+      bits = static_cast<uint32_t>(u >> sh4) & ((1u << n) - 1u);
+    }
+  } else if (mvec && t0 + 4 <= history) {
     uint32_t u = *reinterpret_cast<const uint32_t*>(cur + moff);
     if (prev) u |= *reinterpret_cast<const uint32_t*>(prev + moff);
     if (fin) u |= *reinterpret_cast<const uint32_t*>(fin + moff);
@@ -390,14 +442,28 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
 // invalid), then the sink range, the recent range and the current token.
 // attn_ids (optional) repeats the list with -1 for invalid entries.
 // ---------------------------------------------------------------------------
+// BITS: hf is a bitset (64 positions per uint64 word, hf_ld in words).
+template <bool BITS = false>
 __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
     const float* __restrict__ scores, int64_t scores_ld, const int32_t* __restrict__ sel, int keep,
     int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids,
     int n_out, uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0) {
   const int row = blockIdx.x, tid = threadIdx.x;
-  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
-  for (int t = tid; t < history; t += kRT) hrow[t] = (t < sink_end) || (t >= recent_start);
+  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld * (BITS ? 8 : 1);
+  uint64_t* hw = reinterpret_cast<uint64_t*>(hrow);
+  if constexpr (BITS) {
+    for (int j = tid; j < (history + 63) / 64; j += kRT) {
+      uint64_t w = 0;
+      for (int b = 0; b < 64; ++b) {
+        const int t = 64 * j + b;
+        w |= static_cast<uint64_t>(t < history && ((t < sink_end) || (t >= recent_start))) << b;
+      }
+      hw[j] = w;
+    }
+  } else {
+    for (int t = tid; t < history; t += kRT) hrow[t] = (t < sink_end) || (t >= recent_start);
+  }
   __syncthreads();
   const int32_t* srow = sel + static_cast<int64_t>(row) * keep;
   const float* sc = scores + static_cast<int64_t>(row) * scores_ld;
@@ -406,7 +472,10 @@ __global__ __launch_bounds__(kRT) void reuse_finalize_kernel(
     const int idx = srow[i];
     const float s = sc[idx];
     const bool valid = isfinite(s);
-    if (valid) hrow[idx] = 1;
+    if (valid) {
+      if constexpr (BITS) atomicOr(reinterpret_cast<unsigned long long*>(hw + (idx >> 6)), 1ull << (idx & 63));
+      else hrow[idx] = 1;
+    }
     const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
     final_idx[o + i] = idx;
     final_valid[o + i] = fv;
@@ -457,13 +526,17 @@ constexpr int kWideMax = kWideNT * 40;
 
 // mask[r, t] = values[r, t] >= the row's k-th largest value.
 // thr_out (optional) receives the k-th largest value; with mask null only
-// the threshold is written.
+// the threshold is written.  bits (optional, with mask null): the mask as a
+// bitset instead, 64 positions per word (bit t % 64 of word t / 64; row
+// stride bits_ld words), the words of [0, ceil(n / 64)) written.
 template <int VPL>
 __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* __restrict__ values, int64_t ld, int n,
                                                                   int k, uint8_t* __restrict__ mask, int64_t mask_ld,
                                                                   float* __restrict__ thr_out,
                                                                   const uint8_t* __restrict__ gate = nullptr,
-                                                                  int gate_refresh = 0, int gate_rows = 0) {
+                                                                  int gate_refresh = 0, int gate_rows = 0,
+                                                                  uint64_t* __restrict__ bits = nullptr,
+                                                                  int64_t bits_ld = 0) {
   using WS = WideSelect<VPL, false>;
   __shared__ typename WS::Shared sh;
   WS ws;
@@ -489,6 +562,17 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
       for (int w = 1; w < kWideNT / 64; ++w) m = min(m, wave_min[w]);
       thr_out[row] = sortable_f32(min(m, wave_min[0]));
     }
+  }
+  if (bits) {   // slot i of wave w covers the 64 positions of word w * VPL + i: one ballot each
+    const int lane = tid & 63, wave = tid >> 6;
+    uint64_t* brow = bits + static_cast<int64_t>(row) * bits_ld;
+    const int n_words = (n + 63) / 64;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const uint64_t m = __ballot(ws.on(i) && ws.u[i] >= ws.theta);
+      if (lane == 0 && wave * VPL + i < n_words) brow[wave * VPL + i] = m;
+    }
+    return;
   }
   if (!mask) return;
   // A slot of a wave covers 64 consecutive positions: its flags are one
@@ -538,7 +622,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_candidates_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm, int q_heads,
     int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd, float* __restrict__ out,
     int64_t out_ld, int k, uint8_t* __restrict__ mask, int64_t mask_ld, float* __restrict__ thr_out,
-    const uint8_t* __restrict__ gate, int gate_refresh, int rows) {
+    const uint8_t* __restrict__ gate, int gate_refresh, int rows, uint64_t* __restrict__ bits, int64_t bits_ld) {
   using E = typename Elem<DT>::T;
   constexpr int VPL = 8 * NCH;
   using WS = WideSelect<VPL, false>;
@@ -637,6 +721,22 @@ __global__ __launch_bounds__(kWideNT) void reuse_candidates_kernel(
       thr_out[row] = sortable_f32(min(m, wave_min[0]));
     }
   }
+  if (bits) {   // the 8 flags of a thread's 8 tokens are one byte of the bitset
+    uint8_t* brow = reinterpret_cast<uint8_t*>(bits + static_cast<int64_t>(row) * bits_ld);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int t0 = (c * kWideNT + tid) * 8;
+      uint32_t f = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f |= static_cast<uint32_t>(ws.on(8 * c + i) && ws.u[8 * c + i] >= ws.theta) << i;
+      if (t0 < history) brow[t0 / 8] = static_cast<uint8_t>(f);
+    }
+    if (tid < 7) {   // the rest of the last word
+      const int t = ((history + 7) / 8 + tid) * 8;
+      if (t < (history + 63) / 64 * 64) brow[t / 8] = 0;
+    }
+    return;
+  }
   uint8_t* mrow = mask + static_cast<int64_t>(row) * mask_ld;
   const bool mvec = (reinterpret_cast<uintptr_t>(mrow) & 7) == 0;
 #pragma unroll
@@ -677,7 +777,9 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 constexpr int kMaxTiles = kWideMax / kScoreTile;
 static_assert(kMaxTiles < 64, "the final selection's tile search takes six steps");
 
-template <int VPL, int VPLC>
+// BITS: hf is a bitset (64 positions per uint64 word, hf_ld in words),
+// assembled in LDS and stored once.
+template <int VPL, int VPLC, bool BITS = false>
 __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     const float* __restrict__ scores, int64_t scores_ld, const float* __restrict__ cscore,
     const int32_t* __restrict__ ctok, const int32_t* __restrict__ ccnt, int n_tiles, int64_t c_ld, int keep,
@@ -692,8 +794,10 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   } sh;
   __shared__ int tile_off[kMaxTiles + 1];
   __shared__ int n_fin;
+  __shared__ uint64_t fin_s[BITS ? kWideMax / 64 : 1];
   const int row = blockIdx.x, tid = threadIdx.x;
-  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld * (BITS ? 8 : 1);
+  const int n_words = (history + 63) / 64;
   // the tile lists' lengths first (one load per tile, n_tiles <= 40), in
   // flight while the protected ranges are written
   int len = 0, nf = 0;
@@ -706,6 +810,16 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   // written after the selection's loads are out, and ordered before the
   // scatter below by the barriers of the selection (run) or of place
   auto write_protected = [&]() {
+    if constexpr (BITS) {   // the protected ranges' bits of every word
+      auto range = [](int j, int a, int b) -> uint64_t {   // bits of [a, b) in word j
+        const int lo = max(a, 64 * j) - 64 * j, hi = min(b, 64 * j + 64) - 64 * j;
+        if (hi <= lo) return 0ull;
+        const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+        return upto & ~((1ull << lo) - 1ull);
+      };
+      for (int j = tid; j < n_words; j += kWideNT) fin_s[j] = range(j, 0, sink_end) | range(j, recent_start, history);
+      return;
+    }
     const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
     for (int t0 = 16 * tid; t0 < body; t0 += 16 * kWideNT) {
       uint32_t w[4];
@@ -731,7 +845,10 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   __syncthreads();
   const int64_t o = static_cast<int64_t>(row) * n_out;
   auto emit = [&](int idx, int p, bool valid) {
-    if (valid) hrow[idx] = 1;
+    if (valid) {
+      if constexpr (BITS) atomicOr(&fin_s[idx >> 6], 1ull << (idx & 63));
+      else hrow[idx] = 1;
+    }
     const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
     final_idx[o + p] = idx;
     final_valid[o + p] = fv;
@@ -781,6 +898,11 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     final_idx[o + keep + i] = idx;
     final_valid[o + keep + i] = 1;
     if (attn_ids) attn_ids[o + keep + i] = idx;
+  }
+  if constexpr (BITS) {
+    __syncthreads();   // every emit's bit is in
+    uint64_t* hw = reinterpret_cast<uint64_t*>(hrow);
+    for (int j = tid; j < n_words; j += kWideNT) hw[j] = fin_s[j];
   }
 }
 
@@ -993,7 +1115,7 @@ template <int DT> struct RunReuseScores {
   static int run(const void* q, const void* k, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
                  int64_t D, const uint8_t* cur, const uint8_t* prev, const uint8_t* fin, int64_t mask_ld,
                  float scaling, float* out, int64_t out_ld, float* cscore, int32_t* ctok, int32_t* ccnt,
-                 int64_t c_ld, hipStream_t st) {
+                 int64_t c_ld, hipStream_t st, bool bitsets = false) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;
     const bool kvec = ks[3] == 1 && D % 8 == 0 && aligned(k, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 &&
@@ -1001,14 +1123,19 @@ template <int DT> struct RunReuseScores {
     const bool mvec = mask_ld % 4 == 0 && aligned(cur, 4) && (!prev || aligned(prev, 4)) && (!fin || aligned(fin, 4));
     dim3 grid(static_cast<unsigned>(cdiv(T, kScoreTile)), static_cast<unsigned>(B * Hq));
     if (ks[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "qkv_reuse_select: K channels must be contiguous");
-#define QKV_REUSE_SCORES(DF)                                                                                   \
-  reuse_scores_kernel<DT, DF><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),        \
-                                                    static_cast<int>(Hq), static_cast<int>(Hq / Hkv),          \
-                                                    static_cast<int>(T), static_cast<int>(D), ks[0], ks[1], ks[2], \
-                                                    kvec, cur, prev, fin, mask_ld, mvec, scaling, out, out_ld, \
-                                                    cscore, ctok, ccnt, c_ld)
-    if (kvec && D == 128) QKV_REUSE_SCORES(128);
-    else QKV_REUSE_SCORES(0);
+#define QKV_REUSE_SCORES(DF, BB)                                                                               \
+  reuse_scores_kernel<DT, DF, BB><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),    \
+                                                        static_cast<int>(Hq), static_cast<int>(Hq / Hkv),      \
+                                                        static_cast<int>(T), static_cast<int>(D), ks[0], ks[1], \
+                                                        ks[2], kvec, cur, prev, fin, mask_ld, mvec, scaling, out, \
+                                                        out_ld, cscore, ctok, ccnt, c_ld)
+    if (bitsets) {
+      if (kvec && D == 128) QKV_REUSE_SCORES(128, true);
+      else QKV_REUSE_SCORES(0, true);
+    } else {
+      if (kvec && D == 128) QKV_REUSE_SCORES(128, false);
+      else QKV_REUSE_SCORES(0, false);
+    }
 #undef QKV_REUSE_SCORES
     return check_launch("qkv_reuse_select");
   }
@@ -1034,15 +1161,17 @@ int check_heads(const char* what, int64_t batch, int64_t q_heads, int64_t kv_hea
   return QKV_OK;
 }
 
-// mask = values >= the row's k-th largest (threshold to thr_out when given).
+// mask = values >= the row's k-th largest (threshold to thr_out when given);
+// with bits (mask null) the mask is written as a bitset instead.
 int threshold_mask_impl(const char* what, const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k,
                         uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
-                        hipStream_t st, const uint8_t* gate = nullptr, int gate_refresh = 0) {
+                        hipStream_t st, const uint8_t* gate = nullptr, int gate_refresh = 0,
+                        uint64_t* bits = nullptr, int64_t bits_ld = 0) {
   if (n <= kWideMax) {   // (rows past the one-workgroup length are selected whatever the gate says)
     return with_wide_vpl(n, [&](auto vpl) {
       reuse_mask_wide_kernel<decltype(vpl)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
           values, ld, static_cast<int>(n), static_cast<int>(k), mask, mask_ld, thr_out, gate, gate_refresh,
-          static_cast<int>(rows));
+          static_cast<int>(rows), bits, bits_ld);
       return check_launch(what);
     });
   }
@@ -1050,6 +1179,12 @@ int threshold_mask_impl(const char* what, const float* values, int64_t rows, int
   void* tk_ws = static_cast<char*>(workspace) + align256(rows * k * 4);
   int rc = qkv_topk_ws(values, rows, n, ld, k, sel, tk_ws, workspace_bytes - align256(rows * k * 4), st);
   if (rc) return rc;
+  if (bits) {
+    dim3 grid(static_cast<unsigned>(cdiv(n, kRT * 4)), static_cast<unsigned>(rows));
+    reuse_mask_bits_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sel, static_cast<int>(k), nullptr,
+                                                 bits, bits_ld, thr_out);
+    return check_launch(what);
+  }
   const bool vec = ld % 4 == 0 && aligned(values, 16) && mask_ld % 16 == 0 && aligned(mask, 16);
   dim3 grid(static_cast<unsigned>(cdiv(n, kMaskTile)), static_cast<unsigned>(rows));
   reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sel, static_cast<int>(k), nullptr, mask,
@@ -1066,7 +1201,8 @@ template <int DT> struct RunCandidates {
   static int run(const char* what, const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq,
                  int64_t Hkv, int64_t T, int64_t D, int count, int64_t k, float* partial, int64_t partial_ld,
                  uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
-                 hipStream_t st, const uint8_t* gate, int refresh) {
+                 hipStream_t st, const uint8_t* gate, int refresh, uint64_t* bits = nullptr,
+                 int64_t bits_ld = 0) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
     const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
@@ -1080,7 +1216,7 @@ template <int DT> struct RunCandidates {
         reuse_candidates_kernel<DT, decltype(nch)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
             static_cast<const E*>(q), static_cast<const E*>(kdm), static_cast<int>(Hq), static_cast<int>(Hq / Hkv),
             static_cast<int>(T), static_cast<int>(D), count, ks[0], ks[1], ks[2], partial, partial_ld,
-            static_cast<int>(k), mask, mask_ld, thr_out, gate, refresh, static_cast<int>(rows));
+            static_cast<int>(k), mask, mask_ld, thr_out, gate, refresh, static_cast<int>(rows), bits, bits_ld);
         return check_launch(what);
       };
       const int64_t per = 8 * kWideNT;   // tokens per chunk
@@ -1093,7 +1229,7 @@ template <int DT> struct RunCandidates {
     int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, gate, refresh);
     if (rc) return rc;
     return threshold_mask_impl(what, partial, rows, T, partial_ld, k, mask, mask_ld, thr_out, workspace,
-                               workspace_bytes, st, gate, refresh);
+                               workspace_bytes, st, gate, refresh, bits, bits_ld);
   }
 };
 
@@ -1113,15 +1249,15 @@ QKV_EXPORT int64_t qkv_reuse_select_workspace_bytes(int64_t rows, int64_t histor
   return reuse_ws_bytes(rows, history, reuse_counts(history, 0, 0, top_fraction, 0).keep);
 }
 
-QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_t* k_strides, int dtype,
-                                int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
-                                int64_t head_dim, const uint8_t* current, const uint8_t* previous,
-                                const uint8_t* previous_final, int64_t mask_ld, int64_t protect_sink,
-                                int64_t protect_recent, double top_fraction, int keep_self, float scaling,
-                                void* workspace, int64_t workspace_bytes, int64_t* final_indices,
-                                uint8_t* final_valid, int32_t* attn_ids, int64_t n_out, uint8_t* history_final,
-                                int64_t history_final_ld, void* stream) {
-  const char* what = "qkv_reuse_select";
+namespace {
+
+int reuse_select_impl(const char* what, bool bits, const void* query, const void* key, const int64_t* k_strides,
+                      int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                      int64_t head_dim, const uint8_t* current, const uint8_t* previous,
+                      const uint8_t* previous_final, int64_t mask_ld, int64_t protect_sink, int64_t protect_recent,
+                      double top_fraction, int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
+                      int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                      uint8_t* history_final, int64_t history_final_ld, void* stream) {
   int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
   if (!query || !key || !k_strides || !current || !workspace || !final_indices || !final_valid || !history_final)
@@ -1129,8 +1265,12 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
   const int64_t history = key_count - 1;
   if (history <= 0 || key_count >= (int64_t(1) << 31))
     return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 (history excludes the current token)", what);
-  if (mask_ld < history || history_final_ld < history)
+  const int64_t cover = bits ? cdiv(history, 64) : history;   // words or bytes per row
+  if (mask_ld < cover || history_final_ld < cover)
     return fail(QKV_ERR_INVALID, "%s: mask row strides must cover the history", what);
+  if (bits && (!aligned(current, 8) || !aligned(previous, 8) || !aligned(previous_final, 8) ||
+               !aligned(history_final, 8)))
+    return fail(QKV_ERR_INVALID, "%s: bitsets must be 8-byte aligned", what);
   if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
   const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
   if (n_out != c.n_out)
@@ -1158,29 +1298,68 @@ QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_
 
   rc = dispatch_dtype<RunReuseScores>(dtype, query, key, k_strides, batch, q_heads, kv_heads, history, head_dim,
                                       current, previous, previous_final, mask_ld, scaling, scores, history, cscore,
-                                      ctok, ccnt, c_ld, st);
+                                      ctok, ccnt, c_ld, st, bits);
   if (rc) return rc;
   if (wide) {
     // compacted unions of up to 1/8 of the row's width (at least 2048 entries)
     return with_wide_vpl(history, [&](auto vpl) {
       constexpr int VPL = decltype(vpl)::value;
-      reuse_final_wide_kernel<VPL, (VPL / 8 > 2 ? VPL / 8 : 2)><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
-          scores, history, cscore, ctok, ccnt, static_cast<int>(n_tiles), c_ld, static_cast<int>(c.keep),
-          static_cast<int>(history), static_cast<int>(key_count),
-          static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
-          static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
-          static_cast<int>(n_out), history_final, history_final_ld);
-      return check_launch(what);
+      constexpr int VPLC = VPL / 8 > 2 ? VPL / 8 : 2;
+      auto launch = [&](auto bb) {
+        reuse_final_wide_kernel<VPL, VPLC, decltype(bb)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+            scores, history, cscore, ctok, ccnt, static_cast<int>(n_tiles), c_ld, static_cast<int>(c.keep),
+            static_cast<int>(history), static_cast<int>(key_count),
+            static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+            static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
+            static_cast<int>(n_out), history_final, history_final_ld);
+        return check_launch(what);
+      };
+      return bits ? launch(std::true_type{}) : launch(std::false_type{});
     });
   }
   rc = qkv_topk_ws(scores, rows, history, history, c.keep, sel, tk_ws, tk_bytes, stream);
   if (rc) return rc;
-  reuse_finalize_kernel<<<static_cast<unsigned>(rows), kRT, 0, st>>>(
-      scores, history, sel, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
-      static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
-      static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
-      history_final, history_final_ld);
-  return check_launch(what);
+  auto fin = [&](auto bb) {
+    reuse_finalize_kernel<decltype(bb)::value><<<static_cast<unsigned>(rows), kRT, 0, st>>>(
+        scores, history, sel, static_cast<int>(c.keep), static_cast<int>(history), static_cast<int>(key_count),
+        static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+        static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
+        history_final, history_final_ld);
+    return check_launch(what);
+  };
+  return bits ? fin(std::true_type{}) : fin(std::false_type{});
+}
+
+}  // namespace
+
+QKV_EXPORT int qkv_reuse_select(const void* query, const void* key, const int64_t* k_strides, int dtype,
+                                int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                int64_t head_dim, const uint8_t* current, const uint8_t* previous,
+                                const uint8_t* previous_final, int64_t mask_ld, int64_t protect_sink,
+                                int64_t protect_recent, double top_fraction, int keep_self, float scaling,
+                                void* workspace, int64_t workspace_bytes, int64_t* final_indices,
+                                uint8_t* final_valid, int32_t* attn_ids, int64_t n_out, uint8_t* history_final,
+                                int64_t history_final_ld, void* stream) {
+  return reuse_select_impl("qkv_reuse_select", false, query, key, k_strides, dtype, batch, q_heads, kv_heads,
+                           key_count, head_dim, current, previous, previous_final, mask_ld, protect_sink,
+                           protect_recent, top_fraction, keep_self, scaling, workspace, workspace_bytes,
+                           final_indices, final_valid, attn_ids, n_out, history_final, history_final_ld, stream);
+}
+
+QKV_EXPORT int qkv_reuse_select_bits(const void* query, const void* key, const int64_t* k_strides, int dtype,
+                                     int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                     int64_t head_dim, const uint64_t* current, const uint64_t* previous,
+                                     const uint64_t* previous_final, int64_t words_ld, int64_t protect_sink,
+                                     int64_t protect_recent, double top_fraction, int keep_self, float scaling,
+                                     void* workspace, int64_t workspace_bytes, int64_t* final_indices,
+                                     uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                                     uint64_t* history_final, int64_t history_final_ld, void* stream) {
+  return reuse_select_impl("qkv_reuse_select_bits", true, query, key, k_strides, dtype, batch, q_heads, kv_heads,
+                           key_count, head_dim, reinterpret_cast<const uint8_t*>(current),
+                           reinterpret_cast<const uint8_t*>(previous), reinterpret_cast<const uint8_t*>(previous_final),
+                           words_ld, protect_sink, protect_recent, top_fraction, keep_self, scaling, workspace,
+                           workspace_bytes, final_indices, final_valid, attn_ids, n_out,
+                           reinterpret_cast<uint8_t*>(history_final), history_final_ld, stream);
 }
 
 QKV_EXPORT int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history,
@@ -1370,16 +1549,17 @@ QKV_EXPORT int qkv_reuse_lag_candidates(const void* query, const void* key_dim_m
 QKV_EXPORT int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
                                     int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
                                     int64_t head_dim, int64_t dim_count, int64_t k, float* partial,
-                                    int64_t partial_ld, uint8_t* mask, int64_t mask_ld, float* thr_out,
-                                    void* workspace, int64_t workspace_bytes, void* stream) {
+                                    int64_t partial_ld, uint8_t* mask, int64_t mask_ld, uint64_t* bits,
+                                    int64_t bits_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
+                                    void* stream) {
   const char* what = "qkv_reuse_candidates";
   int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
-  if (!query || !key_dim_major || !kdm_strides || !partial || !mask || !workspace)
-    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
-  if (history <= 0 || history >= (int64_t(1) << 31) || partial_ld < history || mask_ld < history || k < 1 ||
-      k > history)
-    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, partial_ld and mask_ld >= history",
+  if (!query || !key_dim_major || !kdm_strides || !partial || !workspace || !mask == !bits)
+    return fail(QKV_ERR_INVALID, "%s: null pointer (or not exactly one of mask and bits)", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || partial_ld < history || k < 1 || k > history ||
+      (mask && mask_ld < history) || (bits && (bits_ld < cdiv(history, 64) || !aligned(bits, 8))))
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, row strides covering the history",
                 what);
   if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
   const int64_t need = mask_ws_bytes(batch * q_heads, history, k);
@@ -1391,7 +1571,7 @@ QKV_EXPORT int qkv_reuse_candidates(const void* query, const void* key_dim_major
   return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
                                        history, head_dim, count, k, partial, partial_ld, mask, mask_ld, thr_out,
                                        workspace, workspace_bytes, static_cast<hipStream_t>(stream), nullptr,
-                                       QKV_REFRESH_ALL);
+                                       QKV_REFRESH_ALL, bits, bits_ld);
 }
 
 QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k,
@@ -1406,13 +1586,15 @@ QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, i
 
 QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int selection,
                                   int64_t k, const int32_t* sample_cols, int64_t n_sample, float* thresholds,
-                                  uint8_t* mask, int64_t mask_ld, void* workspace, int64_t workspace_bytes,
-                                  void* stream) {
+                                  uint8_t* mask, int64_t mask_ld, uint64_t* bits, int64_t bits_ld, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
   const char* what = "qkv_candidate_mask";
-  if (!values || !mask) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
-  if (rows <= 0 || rows > 65535 || n <= 0 || n >= (int64_t(1) << 31) || ld < n || mask_ld < n)
-    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535, ld and mask_ld >= n", what);
+  if (!values || !mask == !bits) return fail(QKV_ERR_INVALID, "%s: null pointer (or not exactly one of mask and bits)", what);
+  if (rows <= 0 || rows > 65535 || n <= 0 || n >= (int64_t(1) << 31) || ld < n || (mask && mask_ld < n) ||
+      (bits && (bits_ld < cdiv(n, 64) || !aligned(bits, 8))))
+    return fail(QKV_ERR_INVALID, "%s: need 0 < rows <= 65535, ld and the mask's row stride covering n", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 bgrid(static_cast<unsigned>(cdiv(n, kRT * 4)), static_cast<unsigned>(rows));   // bitset launches
   if (selection == QKV_CAND_TOPK) {
     if (k < 1 || k > n) return fail(QKV_ERR_INVALID, "%s: need 1 <= k <= n", what);
     if (!workspace) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
@@ -1421,14 +1603,18 @@ QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, 
       return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                   (long long)workspace_bytes);
     return threshold_mask_impl(what, values, rows, n, ld, k, mask, mask_ld, thresholds, workspace, workspace_bytes,
-                               st);
+                               st, nullptr, 0, bits, bits_ld);
   }
   if (!thresholds) return fail(QKV_ERR_INVALID, "%s: this selection needs the thresholds array", what);
   const bool vec = ld % 4 == 0 && aligned(values, 16) && mask_ld % 16 == 0 && aligned(mask, 16);
   dim3 grid(static_cast<unsigned>(cdiv(n, kMaskTile)), static_cast<unsigned>(rows));
   if (selection == QKV_CAND_PREVIOUS_THRESHOLD) {
-    reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
-                                            vec, nullptr);
+    if (bits)
+      reuse_mask_bits_kernel<<<bgrid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, bits,
+                                                    bits_ld, nullptr);
+    else
+      reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
+                                              vec, nullptr);
     return check_launch(what);
   }
   if (selection != QKV_CAND_SAMPLE_QUANTILE) return fail(QKV_ERR_INVALID, "%s: unknown selection %d", what, selection);
@@ -1440,8 +1626,20 @@ QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, 
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
   if (n_sample <= kRT) {   // gather, k-th of the sample and compare in one launch
-    sample_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sample_cols, static_cast<int>(n_sample),
-                                             static_cast<int>(k), mask, mask_ld, vec, thresholds);
+    if (!bits) {
+      sample_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), sample_cols,
+                                               static_cast<int>(n_sample), static_cast<int>(k), mask, mask_ld, vec,
+                                               thresholds);
+      return check_launch(what);
+    }
+    // the threshold from one tile's launch, then the bitset
+    sample_mask_kernel<<<dim3(1, static_cast<unsigned>(rows)), kRT, 0, st>>>(
+        values, ld, static_cast<int>(n), sample_cols, static_cast<int>(n_sample), static_cast<int>(k), nullptr, 0,
+        false, thresholds);
+    int rc = check_launch(what);
+    if (rc) return rc;
+    reuse_mask_bits_kernel<<<bgrid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, bits,
+                                                  bits_ld, nullptr);
     return check_launch(what);
   }
   float* sampled = static_cast<float*>(workspace);
@@ -1468,8 +1666,12 @@ QKV_EXPORT int qkv_candidate_mask(const float* values, int64_t rows, int64_t n, 
     rc = check_launch(what);
   }
   if (rc) return rc;
-  reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
-                                          vec, nullptr);
+  if (bits)
+    reuse_mask_bits_kernel<<<bgrid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, bits,
+                                                  bits_ld, nullptr);
+  else
+    reuse_mask_kernel<<<grid, kRT, 0, st>>>(values, ld, static_cast<int>(n), nullptr, 0, thresholds, mask, mask_ld,
+                                            vec, nullptr);
   return check_launch(what);
 }
 

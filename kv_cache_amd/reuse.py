@@ -127,14 +127,18 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
     (EV:3958-3989): the k-th largest value (``topk``), the k-th largest of
     the ``n_sample`` columns ``sample_cols`` (``sample_quantile``), or
     ``thresholds`` as given (``previous_threshold``).  The first two write
-    the threshold to ``thresholds`` (f32 [rows]; optional for ``topk``)."""
+    the threshold to ``thresholds`` (f32 [rows]; optional for ``topk``).
+    ``mask`` is a byte mask (uint8 [rows, >= n]) or a bitset (int64 [rows,
+    >= ceil(n / 64)] words, bit t % 64 of word t // 64)."""
     lib = _lib.load()
     code = CANDIDATE_SELECTIONS.get(selection)
     _require(code is not None, f"unknown candidate selection {selection!r}")
     _require(values.is_cuda and values.dtype == torch.float32 and values.dim() == 2 and values.stride(1) == 1
              and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
-    _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
-             and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
+    bits = mask.dtype == torch.int64
+    _require(mask.dim() == 2 and mask.size(0) == values.size(0) and mask.stride(1) == 1
+             and (mask.size(1) >= n if not bits else mask.size(1) * 64 >= n)
+             and mask.dtype in (torch.uint8, torch.int64), "mask must be uint8 [rows, >= n] or int64 bit words")
     _require(thresholds is not None or selection == "topk", f"{selection} needs the thresholds array")
     _require(thresholds is None or (thresholds.dtype == torch.float32 and thresholds.is_contiguous()
                                     and thresholds.is_cuda and thresholds.numel() >= values.size(0)),
@@ -149,9 +153,17 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
     with torch.cuda.device(values.device):
         _lib.check(lib.qkv_candidate_mask(
             values.data_ptr(), values.size(0), int(n), values.stride(0), code, int(k), _lib.ptr(sample_cols),
-            int(n_sample), _lib.ptr(thresholds), mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
+            int(n_sample), _lib.ptr(thresholds), None if bits else mask.data_ptr(), 0 if bits else mask.stride(0),
+            mask.data_ptr() if bits else None, mask.stride(0) if bits else 0, workspace.data_ptr(),
             workspace.numel() * 4, _lib.stream_of(values)))
     return mask
+
+
+def expand_bits(words: torch.Tensor, n: int) -> torch.Tensor:
+    """bool [rows, n] from bitset words (int64 [rows, W], bit t % 64 of word t // 64)."""
+    b = words.contiguous().view(torch.uint8).view(words.size(0), -1)
+    shifts = torch.arange(8, dtype=torch.uint8, device=words.device)
+    return ((b.unsqueeze(-1) >> shifts) & 1).view(words.size(0), -1)[:, :n].bool()
 
 
 def reuse_partial_scores(query: torch.Tensor, key_dim_major: torch.Tensor, history: int, dim_count: int, *,
@@ -266,6 +278,8 @@ def _check_step_dtype(dtype: torch.dtype, query: torch.Tensor, key: torch.Tensor
 
 
 class ReuseDecodeStep:
+    _BITSET = True   # candidate and final state as bitsets (subclasses with byte kernels turn it off)
+
     """One layer's reuse decode step with its state, for K/V caches of up to
     ``capacity`` tokens ([B, Hkv, T, D] as HF stores them, in ``dtype``: bf16
     or fp16, shared by the query and the output).
@@ -302,8 +316,16 @@ class ReuseDecodeStep:
         cap = self.capacity
         self.rows = rows
         self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
-        self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
-        self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
+        # candidate and final masks: bitsets (64 positions per int64 word) for the
+        # plain reuse modes; byte masks where block expansion or a lagged step reads them
+        self.bits = self._BITSET and self.block is None
+        if self.bits:
+            words = -(-cap // 64)
+            self.cand = [torch.zeros((rows, words), dtype=torch.int64, device=device) for _ in range(2)]
+            self.fin = torch.zeros((rows, words), dtype=torch.int64, device=device)
+        else:
+            self.cand = [torch.zeros((rows, cap), dtype=torch.uint8, device=device) for _ in range(2)]
+            self.fin = torch.zeros((rows, cap), dtype=torch.uint8, device=device)
         self.partial = torch.empty((rows, cap), dtype=torch.float32, device=device)
         # the last step's candidate threshold per row (EV:1744-1745), written by the
         # previous_threshold and sample_quantile selections
@@ -396,7 +418,7 @@ class ReuseDecodeStep:
                current: torch.Tensor, previous: torch.Tensor | None, previous_final: torch.Tensor | None, *,
                previous_thresholds: bool = False) -> None:
         """The step's kernels at the history key.size(2) - 1 with explicit
-        mask buffers (rows of ``capacity`` bytes): the current candidates go to
+        mask buffers (the step's byte masks or bitsets): the current candidates go to
         ``current``, the final mask to the final buffer (it may also be the
         ``previous_final`` read).  With ``previous_thresholds`` the
         ``previous_threshold`` selection compares with the thresholds the last
@@ -435,10 +457,13 @@ class ReuseDecodeStep:
             # partial scores, threshold and mask in one launch where a row fits one
             # workgroup; the threshold is kept only where a later step reads it
             with torch.cuda.device(q.device):
+                bits = current.dtype == torch.int64
                 _lib.check(lib.qkv_reuse_candidates(
                     q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), _dtype_code(q), self.batch,
                     self.q_heads, self.kv_heads, history, self.head_dim, self.dims, requested,
-                    self.partial.data_ptr(), self.partial.stride(0), current.data_ptr(), current.stride(0),
+                    self.partial.data_ptr(), self.partial.stride(0), None if bits else current.data_ptr(),
+                    0 if bits else current.stride(0), current.data_ptr() if bits else None,
+                    current.stride(0) if bits else 0,
                     _lib.ptr(self.thresholds) if self.selection != "topk" else None, self.mask_ws.data_ptr(),
                     self.mask_ws.numel() * 4, _lib.stream_of(q)))
 
@@ -455,14 +480,15 @@ class ReuseDecodeStep:
         self.select_ws = self._grow(self.select_ws,
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
         ids = self.attn_ids[: self.rows * n_out]
+        select = lib.qkv_reuse_select_bits if current.dtype == torch.int64 else lib.qkv_reuse_select
         with torch.cuda.device(q.device):
-            _lib.check(lib.qkv_reuse_select(
+            _lib.check(select(
                 q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch, self.q_heads,
                 self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
-                _lib.ptr(previous_final), self.capacity, self.sink, self.recent, self.top_fraction,
+                _lib.ptr(previous_final), current.stride(0), self.sink, self.recent, self.top_fraction,
                 int(self.keep_self), float(scaling), self.select_ws.data_ptr(), self.select_ws.numel() * 4,
                 self.final_idx.data_ptr(), self.final_valid.data_ptr(),
-                ids.data_ptr() if self.block is None else None, n_sel, self.fin.data_ptr(), self.capacity,
+                ids.data_ptr() if self.block is None else None, n_sel, self.fin.data_ptr(), self.fin.stride(0),
                 _lib.stream_of(q)))
             if self.block is not None:   # EV:4314-4316: the final selection grows to whole blocks
                 _lib.check(lib.qkv_reuse_expand_blocks(
@@ -475,11 +501,16 @@ class ReuseDecodeStep:
     # -- state views (tests, tracing) ------------------------------------------
     def candidate_mask(self) -> torch.Tensor:
         """The last step's current candidates, bool [B, Hq, history]."""
+        if self.bits:
+            return expand_bits(self.cand[1 - self.flip], self.last_history).view(self.batch, self.q_heads,
+                                                                                  self.last_history)
         return self.cand[1 - self.flip][:, : self.last_history].view(torch.bool).view(
             self.batch, self.q_heads, self.last_history)
 
     def final_mask(self) -> torch.Tensor:
         """The last step's final selection with the protected ranges, bool [B, Hq, history]."""
+        if self.bits:
+            return expand_bits(self.fin, self.last_history).view(self.batch, self.q_heads, self.last_history)
         return self.fin[:, : self.last_history].view(torch.bool).view(self.batch, self.q_heads, self.last_history)
 
     def final_indices(self) -> tuple[torch.Tensor, torch.Tensor]:
@@ -614,6 +645,8 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
     ``topk`` the step-wide any / majority decisions are taken on the GPU, so a
     step needs no host round trip and can be captured; with the other
     selections those two kinds read the decision on the host."""
+
+    _BITSET = False   # the lagged kernels read and write byte masks
 
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,

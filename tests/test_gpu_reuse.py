@@ -217,14 +217,17 @@ def test_reuse_partial_scores_ties_and_ragged_tails(dtype, d, hist, dims):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("dtype,b,hist,dims,gated", [
-    (torch.bfloat16, 4, 32790, 8, False),    # 128 rows: the one-launch kernel, five 8192-token chunks
-    (torch.float16, 4, 5001, 16, False),     # one chunk, a short last 8-token group
-    (torch.float32, 8, 20003, 8, False),     # 256 rows, three chunks
-    (torch.bfloat16, 4, 9000, 8, True),      # lagged steps: rows whose flag is clear stay untouched
-    (torch.bfloat16, 1, 9000, 8, False),     # 32 rows: the two-launch form
+@pytest.mark.parametrize("dtype,b,hist,dims,gated,bits", [
+    (torch.bfloat16, 4, 32790, 8, False, False),    # 128 rows: the one-launch kernel, five 8192-token chunks
+    (torch.float16, 4, 5001, 16, False, False),     # one chunk, a short last 8-token group
+    (torch.float32, 8, 20003, 8, False, False),     # 256 rows, three chunks
+    (torch.bfloat16, 4, 9000, 8, True, False),      # lagged steps: rows whose flag is clear stay untouched
+    (torch.bfloat16, 1, 9000, 8, False, False),     # 32 rows: the two-launch form
+    (torch.bfloat16, 4, 32790, 8, False, True),     # bitsets: one launch
+    (torch.float16, 1, 5001, 16, False, True),      # bitsets: two launches, a partial last word
+    (torch.bfloat16, 1, 45001, 8, False, True),     # bitsets past the one-workgroup selection
 ])
-def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated):
+def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated, bits):
     # partial scores, the k-th largest and the mask in one call: scores bit-exact
     # to the oracle, mask = score >= the k-th largest (ties all kept), threshold
     from kv_cache_amd import _lib
@@ -242,6 +245,7 @@ def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated):
     kk = -(-hist * 5 // 100)
     part = torch.full((rows, hist + 9), 7.0, device=DEV)
     mask = torch.full((rows, hist + 9), 9, dtype=torch.uint8, device=DEV)
+    words = torch.full((rows, -(-hist // 64) + 3), -1, dtype=torch.int64, device=DEV)
     thr = torch.zeros(rows, device=DEV)
     ws = torch.empty((lib.qkv_threshold_mask_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
     flags = (torch.arange(rows) % 3 == 0).to(torch.uint8).to(DEV)
@@ -254,8 +258,15 @@ def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated):
     else:
         _lib.check(lib.qkv_reuse_candidates(
             qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), _lib.DTYPE_CODES[dtype], b, hq, hkv, hist, d,
-            dims, kk, part.data_ptr(), part.stride(0), mask.data_ptr(), mask.stride(0), thr.data_ptr(),
-            ws.data_ptr(), ws.numel() * 4, _lib.stream_of(qd)))
+            dims, kk, part.data_ptr(), part.stride(0), None if bits else mask.data_ptr(), mask.stride(0),
+            words.data_ptr() if bits else None, words.stride(0), thr.data_ptr(), ws.data_ptr(), ws.numel() * 4,
+            _lib.stream_of(qd)))
+    if bits:   # the words of [0, ceil(hist / 64)) hold the mask, bits past the history clear
+        n_w = -(-hist // 64)
+        exp = RU.expand_bits(words[:, :n_w], n_w * 64).cpu().numpy()
+        mask[:, :hist] = torch.from_numpy(exp[:, :hist].astype(np.uint8)).to(DEV)
+        assert not exp[:, hist:].any()
+        assert (words[:, n_w:] == -1).all()
     want = R.partial_scores(f32(q), np.repeat(f32(k), hq // hkv, axis=1), dims).reshape(rows, hist)
     kth = -np.sort(-want, axis=1)[:, kk - 1 : kk]
     got_p, got_m = part.cpu().numpy(), mask.cpu().numpy()
@@ -267,6 +278,47 @@ def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated):
         assert (got_p[~on] == 7.0).all() and (got_m[~on] == 9).all()
     else:
         assert np.array_equal(thr.cpu().numpy(), kth[:, 0])
+
+
+@pytest.mark.parametrize("hist,sink,recent,frac,prev", [(3000, 4, 8, 0.02, True), (1001, 0, 0, 0.05, False),
+                                                        (45000, 10, 10, 0.02, True)])
+def test_reuse_select_bits_equals_bytes(hist, sink, recent, frac, prev):
+    # the same masks as bytes and as bitsets: the same final list and final mask
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(hist)
+    b, hq, hkv, d = 1, 8, 2, 128
+    rows, t = b * hq, hist + 1
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16).to(DEV)
+    k = torch.randn((b, hkv, t, d), generator=gen).to(torch.bfloat16).to(DEV)
+    masks = [(torch.rand((rows, hist), generator=gen) < 0.03).to(DEV) for _ in range(3)]
+    n_w = -(-hist // 64)
+
+    def to_words(m):
+        pad = torch.zeros((rows, n_w * 64), dtype=torch.bool, device=DEV)
+        pad[:, :hist] = m
+        by = (pad.view(rows, -1, 8).to(torch.uint8) << torch.arange(8, dtype=torch.uint8, device=DEV)).sum(-1)
+        return by.to(torch.uint8).contiguous().view(torch.int64)
+
+    n_out = int(lib.qkv_reuse_final_count(hist, sink, recent, frac, 1))
+    ws = torch.empty((lib.qkv_reuse_select_workspace_bytes(rows, hist, frac) + 3) // 4, device=DEV)
+    outs = []
+    for bits in (False, True):
+        ms = [to_words(m) if bits else m.to(torch.uint8).contiguous() for m in masks]
+        fin = torch.zeros_like(ms[2]) if bits else torch.zeros((rows, hist), dtype=torch.uint8, device=DEV)
+        fi = torch.empty((rows, n_out), dtype=torch.int64, device=DEV)
+        fv = torch.empty((rows, n_out), dtype=torch.uint8, device=DEV)
+        ids = torch.empty((rows, n_out), dtype=torch.int32, device=DEV)
+        select = lib.qkv_reuse_select_bits if bits else lib.qkv_reuse_select
+        _lib.check(select(q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), 0, b, hq, hkv, t, d,
+                          ms[0].data_ptr(), ms[1].data_ptr() if prev else None, ms[2].data_ptr(), ms[0].stride(0),
+                          sink, recent, frac, 1, 0.088, ws.data_ptr(), ws.numel() * 4, fi.data_ptr(), fv.data_ptr(),
+                          ids.data_ptr(), n_out, fin.data_ptr(), fin.stride(0), _lib.stream_of(q)))
+        hf = RU.expand_bits(fin, hist) if bits else fin.bool()
+        outs.append((fi, fv, ids, hf))
+    for a, w in zip(*outs):
+        assert torch.equal(a, w)
 
 
 def test_reuse_select_ties_and_missing_masks():
