@@ -792,12 +792,13 @@ def run_reuse(args) -> dict:
         for layer in range(layers):
             st, kk, _ = fixed(layer)
             select = lib.qkv_reuse_select_bits if st.bits else lib.qkv_reuse_select
+            extra = (None, None, None) if st.bits else ()   # the selection alone (no fused attention)
             RU._lib.check(select(
                 qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv, hist_fixed + 1, d,
                 st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), st.fin.stride(0), c["sink"],
                 c["recent"], c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
                 st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_sel, st.fin.data_ptr(),
-                st.fin.stride(0), RU._lib.stream_of(qs[layer])))
+                st.fin.stride(0), *extra, RU._lib.stream_of(qs[layer])))
 
     def run_expand():
         for layer in range(layers):

@@ -381,14 +381,22 @@ int qkv_reuse_select(const void* query, const void* key, const int64_t* k_stride
  * words_ld / history_final_ld words, 8-byte aligned) instead of byte masks;
  * everything else as qkv_reuse_select.  The compact state the reference
  * names for its reuse step (bitset OR of the masks, no dense per-token byte
- * mask); no reference counterpart as a kernel. */
+ * mask); no reference counterpart as a kernel.  With value and out (may be
+ * NULL): value [B,Hkv,key_count,D] with key's strides, out [B,Hq,D] in the
+ * query's dtype -- the attention of qkv_token_attention over attn_ids is
+ * run by the final selection's own workgroups (the reference's suggested
+ * fusion of rerank and final attention) when the rows allow it (history <=
+ * 40960, n_out <= 4096, D = 128, bf16 / fp16, 16-byte aligned rows);
+ * *attended (host int, may be NULL) says whether it ran, else the caller
+ * runs qkv_token_attention on attn_ids. */
 int qkv_reuse_select_bits(const void* query, const void* key, const int64_t* k_strides, int dtype, int64_t batch,
                           int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
                           const uint64_t* current, const uint64_t* previous, const uint64_t* previous_final,
                           int64_t words_ld, int64_t protect_sink, int64_t protect_recent, double top_fraction,
                           int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
                           int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
-                          uint64_t* history_final, int64_t history_final_ld, void* stream);
+                          uint64_t* history_final, int64_t history_final_ld, const void* value, void* out,
+                          int* attended, void* stream);
 
 /* Workspace bytes of qkv_qabs_candidate_select (0 for histories of at most
  * 40960 positions, which one workgroup per row selects; -1 for bad sizes). */

@@ -777,21 +777,144 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 constexpr int kMaxTiles = kWideMax / kScoreTile;
 static_assert(kMaxTiles < 64, "the final selection's tile search takes six steps");
 
+// The token attention of one row (a query head) over its final list, by the
+// workgroup that selected it (reuse_final_wide_kernel with ATTN): softmax(
+// scaling * q.K[t]) . V[t] over the list's valid entries (-1 skipped), in
+// fp32, the output rounded once to the K/V dtype; a row with no valid entry
+// gives zeros (QK:388, 404).  Lane 16g + c of a wave holds channels
+// 8c..8c+7 of the list entry e = 64 s + 4 w + g at step s (wave w), the
+// dot product a 16-lane sum; the K/V rows of four steps are in flight ahead
+// of the one computed.  Each (wave, lane group) keeps a running maximum and
+// sum; the 64 partials meet in LDS.
+struct ReuseAttn {
+  const uint16_t *q, *k, *v;   // q [rows, 128]; K/V [B, Hkv, T, 128] at (sb, sh, st), channels contiguous
+  int64_t sb, sh, st;
+  int q_heads, group;
+  float scale_log2;            // scaling * log2(e)
+  uint16_t* out;               // [rows, 128]
+};
+constexpr int kAttnList = 4096;   // the longest final list the fused attention holds in LDS
+struct AttnPartials {
+  float acc[64][128];
+  float m[64], l[64];
+};
+
+template <int DT>
+__device__ __forceinline__ void unpack8_16(const uint4& w, float (&x)[8]) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t lo = static_cast<uint16_t>(u[i] & 0xFFFFu), hi = static_cast<uint16_t>(u[i] >> 16);
+    x[2 * i] = Elem<DT>::load(&lo);
+    x[2 * i + 1] = Elem<DT>::load(&hi);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void reuse_attend(const int32_t* ids_s, int n, const ReuseAttn& a, int row,
+                                             AttnPartials& part) {
+  constexpr int DEPTH = 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, c = lane & 15;
+  const int b = row / a.q_heads, h = row - b * a.q_heads;
+  const int64_t kv_off = b * a.sb + (h / a.group) * a.sh + 8 * c;
+  const uint16_t* kb = a.k + kv_off;
+  const uint16_t* vb = a.v + kv_off;
+  float qf[8];
+  unpack8_16<DT>(*reinterpret_cast<const uint4*>(a.q + static_cast<int64_t>(row) * 128 + 8 * c), qf);
+  const float ninf = -__builtin_huge_valf();
+  float m = ninf, l = 0.0f, acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  const int steps = (n + 63) / 64;
+  auto tok_of = [&](int s) -> int {
+    const int e = s * 64 + wave * 4 + g;
+    return (s < steps && e < n) ? ids_s[e] : -1;
+  };
+  int tk[DEPTH];
+  uint4 kx[DEPTH], vx[DEPTH];
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u) {   // invalid entries read token 0 (in bounds) and are skipped
+    tk[u] = tok_of(u);
+    const int64_t at = static_cast<int64_t>(max(tk[u], 0)) * a.st;
+    kx[u] = *reinterpret_cast<const uint4*>(kb + at);
+    vx[u] = *reinterpret_cast<const uint4*>(vb + at);
+  }
+  for (int s0 = 0; s0 < steps; s0 += DEPTH) {
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) {
+      float kf[8], vf[8];
+      unpack8_16<DT>(kx[u], kf);
+      unpack8_16<DT>(vx[u], vf);
+      const int t = tk[u];
+      // the step DEPTH ahead goes out before this one is computed
+      tk[u] = tok_of(s0 + u + DEPTH);
+      if (s0 + u + DEPTH < steps) {
+        const int64_t at = static_cast<int64_t>(max(tk[u], 0)) * a.st;
+        kx[u] = *reinterpret_cast<const uint4*>(kb + at);
+        vx[u] = *reinterpret_cast<const uint4*>(vb + at);
+      }
+      float d = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d = __builtin_fmaf(qf[j], kf[j], d);
+      d += dpp_f<0xB1>(d);    // quad_perm [1,0,3,2]
+      d += dpp_f<0x4E>(d);    // quad_perm [2,3,0,1]
+      d += dpp_f<0x141>(d);   // row_half_mirror
+      d += dpp_f<0x140>(d);   // row_mirror: every lane of the 16 holds the sum
+      if (t >= 0) {           // uniform in the 16 lanes of the entry
+        const float sc = d * a.scale_log2;
+        const float mn = fmaxf(m, sc);
+        const float al = exp2f(m - mn);   // 0 while m = -inf
+        const float p = exp2f(sc - mn);
+        l = __builtin_fmaf(l, al, p);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(acc[j], al, p * vf[j]);
+        m = mn;
+      }
+    }
+  }
+  const int pi = wave * 4 + g;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) part.acc[pi][8 * c + j] = acc[j];
+  if (c == 0) {
+    part.m[pi] = m;
+    part.l[pi] = l;
+  }
+  __syncthreads();
+  if (tid < 128) {
+    float mx = ninf;
+    for (int i = 0; i < 64; ++i) mx = fmaxf(mx, part.m[i]);
+    float num = 0.0f, den = 0.0f;
+    if (mx != ninf) {
+      for (int i = 0; i < 64; ++i) {
+        if (part.m[i] == ninf) continue;
+        const float w = exp2f(part.m[i] - mx);
+        num = __builtin_fmaf(part.acc[i][tid], w, num);
+        den = __builtin_fmaf(part.l[i], w, den);
+      }
+    }
+    a.out[static_cast<int64_t>(row) * 128 + tid] = Elem<DT>::store(mx == ninf ? 0.0f : num / den);
+  }
+}
+
+// ATTN: the workgroup then attends over the row's final list (reuse_attend;
+// DT the K/V dtype, n_out <= kAttnList, head size 128).
 // BITS: hf is a bitset (64 positions per uint64 word, hf_ld in words),
 // assembled in LDS and stored once.
-template <int VPL, int VPLC, bool BITS = false>
+template <int VPL, int VPLC, bool BITS = false, int DT = QKV_DTYPE_BF16, bool ATTN = false>
 __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     const float* __restrict__ scores, int64_t scores_ld, const float* __restrict__ cscore,
     const int32_t* __restrict__ ctok, const int32_t* __restrict__ ccnt, int n_tiles, int64_t c_ld, int keep,
     int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out,
-    uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0) {
+    uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0, ReuseAttn at = {}) {
   using WS = WideSelect<VPL, false>;
   using WC = WideSelect<VPLC, false>;
   __shared__ union {
     typename WS::Shared d;
     typename WC::Shared c;
+    AttnPartials a;
   } sh;
+  __shared__ int32_t ids_s[ATTN ? kAttnList : 1];
   __shared__ int tile_off[kMaxTiles + 1];
   __shared__ int n_fin;
   __shared__ uint64_t fin_s[BITS ? kWideMax / 64 : 1];
@@ -853,6 +976,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     final_idx[o + p] = idx;
     final_valid[o + p] = fv;
     if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
+    if constexpr (ATTN) ids_s[p] = fv ? idx : -1;
   };
   const int total = tile_off[n_tiles];
   if (cscore && n_fin >= keep && total <= VPLC * kWideNT) {   // uniform across the workgroup
@@ -898,12 +1022,14 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     final_idx[o + keep + i] = idx;
     final_valid[o + keep + i] = 1;
     if (attn_ids) attn_ids[o + keep + i] = idx;
+    if constexpr (ATTN) ids_s[keep + i] = idx;
   }
+  if constexpr (BITS || ATTN) __syncthreads();   // every emit is done (the selection's LDS is free)
   if constexpr (BITS) {
-    __syncthreads();   // every emit's bit is in
     uint64_t* hw = reinterpret_cast<uint64_t*>(hrow);
     for (int j = tid; j < n_words; j += kWideNT) hw[j] = fin_s[j];
   }
+  if constexpr (ATTN) reuse_attend<DT>(ids_s, n_out, at, row, sh.a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1257,7 +1383,8 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
                       const uint8_t* previous_final, int64_t mask_ld, int64_t protect_sink, int64_t protect_recent,
                       double top_fraction, int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
                       int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
-                      uint8_t* history_final, int64_t history_final_ld, void* stream) {
+                      uint8_t* history_final, int64_t history_final_ld, void* stream, const void* value = nullptr,
+                      void* out = nullptr, int* attended = nullptr) {
   int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
   if (!query || !key || !k_strides || !current || !workspace || !final_indices || !final_valid || !history_final)
@@ -1300,21 +1427,40 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
                                       current, previous, previous_final, mask_ld, scaling, scores, history, cscore,
                                       ctok, ccnt, c_ld, st, bits);
   if (rc) return rc;
+  // the final selection's workgroup also attends over the row's list (one launch less) where it
+  // holds the list: 16-bit K/V rows of 128 channels, 16-byte aligned, V laid out as K
+  const bool fuse = out && value && bits && wide && n_out <= kAttnList && head_dim == 128 &&
+                    (dtype == QKV_DTYPE_BF16 || dtype == QKV_DTYPE_FP16) && k_strides[3] == 1 &&
+                    aligned(key, 16) && aligned(value, 16) && aligned(query, 16) && aligned(out, 16) &&
+                    (k_strides[0] | k_strides[1] | k_strides[2]) % 8 == 0;
+  if (attended) *attended = fuse ? 1 : 0;
   if (wide) {
     // compacted unions of up to 1/8 of the row's width (at least 2048 entries)
     return with_wide_vpl(history, [&](auto vpl) {
       constexpr int VPL = decltype(vpl)::value;
       constexpr int VPLC = VPL / 8 > 2 ? VPL / 8 : 2;
-      auto launch = [&](auto bb) {
-        reuse_final_wide_kernel<VPL, VPLC, decltype(bb)::value><<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
-            scores, history, cscore, ctok, ccnt, static_cast<int>(n_tiles), c_ld, static_cast<int>(c.keep),
-            static_cast<int>(history), static_cast<int>(key_count),
-            static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
-            static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
-            static_cast<int>(n_out), history_final, history_final_ld);
+      const ReuseAttn at{static_cast<const uint16_t*>(query), static_cast<const uint16_t*>(key),
+                         static_cast<const uint16_t*>(value), k_strides[0], k_strides[1], k_strides[2],
+                         static_cast<int>(q_heads), static_cast<int>(q_heads / kv_heads),
+                         scaling * 1.4426950408889634f, static_cast<uint16_t*>(out)};
+      auto launch = [&](auto bb, auto dt, auto attn) {
+        reuse_final_wide_kernel<VPL, VPLC, decltype(bb)::value, decltype(dt)::value, decltype(attn)::value>
+            <<<static_cast<unsigned>(rows), kWideNT, 0, st>>>(
+                scores, history, cscore, ctok, ccnt, static_cast<int>(n_tiles), c_ld, static_cast<int>(c.keep),
+                static_cast<int>(history), static_cast<int>(key_count),
+                static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
+                static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
+                static_cast<int>(n_out), history_final, history_final_ld, 0, at);
         return check_launch(what);
       };
-      return bits ? launch(std::true_type{}) : launch(std::false_type{});
+      using BF = std::integral_constant<int, QKV_DTYPE_BF16>;
+      using FH = std::integral_constant<int, QKV_DTYPE_FP16>;
+      if (fuse) {
+        if (dtype == QKV_DTYPE_FP16) return launch(std::true_type{}, FH{}, std::true_type{});
+        return launch(std::true_type{}, BF{}, std::true_type{});
+      }
+      return bits ? launch(std::true_type{}, BF{}, std::false_type{})
+                  : launch(std::false_type{}, BF{}, std::false_type{});
     });
   }
   rc = qkv_topk_ws(scores, rows, history, history, c.keep, sel, tk_ws, tk_bytes, stream);
@@ -1353,13 +1499,15 @@ QKV_EXPORT int qkv_reuse_select_bits(const void* query, const void* key, const i
                                      int64_t protect_recent, double top_fraction, int keep_self, float scaling,
                                      void* workspace, int64_t workspace_bytes, int64_t* final_indices,
                                      uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
-                                     uint64_t* history_final, int64_t history_final_ld, void* stream) {
+                                     uint64_t* history_final, int64_t history_final_ld, const void* value, void* out,
+                                     int* attended, void* stream) {
+  if (attended) *attended = 0;
   return reuse_select_impl("qkv_reuse_select_bits", true, query, key, k_strides, dtype, batch, q_heads, kv_heads,
                            key_count, head_dim, reinterpret_cast<const uint8_t*>(current),
                            reinterpret_cast<const uint8_t*>(previous), reinterpret_cast<const uint8_t*>(previous_final),
                            words_ld, protect_sink, protect_recent, top_fraction, keep_self, scaling, workspace,
                            workspace_bytes, final_indices, final_valid, attn_ids, n_out,
-                           reinterpret_cast<uint8_t*>(history_final), history_final_ld, stream);
+                           reinterpret_cast<uint8_t*>(history_final), history_final_ld, stream, value, out, attended);
 }
 
 QKV_EXPORT int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history,

@@ -21,6 +21,8 @@ step once the step is built.
 
 from __future__ import annotations
 
+import ctypes
+
 import math
 import re
 
@@ -294,12 +296,17 @@ class ReuseDecodeStep:
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
                  keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
-                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16):
+                 device: torch.device | str = "cuda", dtype: torch.dtype = torch.bfloat16,
+                 fused_attention: bool = False):
         lib = _lib.load()
         _require(dtype in (torch.bfloat16, torch.float16), f"dtype must be bfloat16 or float16, got {dtype}")
         self.dtype = dtype
         self.device = device
         self.mode = mode
+        # the final selection's workgroups running the attention too (one launch less);
+        # measured slower than the separate attention kernel at batch 1 and 4 and equal at
+        # 8, so off unless asked for
+        self.fused_attention = bool(fused_attention)
         (self.dims, self.cand_fraction, self.use_prev_candidate, self.use_prev_final,
          self.block) = self._parse_mode(mode)
         _require(self.block is None or self.block <= 4096, "reuse blocks hold at most 4096 tokens")
@@ -480,7 +487,14 @@ class ReuseDecodeStep:
         self.select_ws = self._grow(self.select_ws,
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
         ids = self.attn_ids[: self.rows * n_out]
-        select = lib.qkv_reuse_select_bits if current.dtype == torch.int64 else lib.qkv_reuse_select
+        bits = current.dtype == torch.int64
+        # on bitsets the final selection's workgroups can also run the attention
+        attended = ctypes.c_int(0)
+        extra = ((value.data_ptr(), self.out.data_ptr(), ctypes.byref(attended)) if self.fused_attention
+                 else (None, None, None)) if bits else ()
+        select = lib.qkv_reuse_select_bits if bits else lib.qkv_reuse_select
+        _require(not bits or (value.shape == key.shape and value.stride() == key.stride()),
+                 "key/value layout mismatch")
         with torch.cuda.device(q.device):
             _lib.check(select(
                 q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch, self.q_heads,
@@ -489,13 +503,14 @@ class ReuseDecodeStep:
                 int(self.keep_self), float(scaling), self.select_ws.data_ptr(), self.select_ws.numel() * 4,
                 self.final_idx.data_ptr(), self.final_valid.data_ptr(),
                 ids.data_ptr() if self.block is None else None, n_sel, self.fin.data_ptr(), self.fin.stride(0),
-                _lib.stream_of(q)))
+                *extra, _lib.stream_of(q)))
             if self.block is not None:   # EV:4314-4316: the final selection grows to whole blocks
                 _lib.check(lib.qkv_reuse_expand_blocks(
                     self.fin.data_ptr(), self.capacity, self.rows, key_count, self.block, self.sink, self.recent,
                     self.top_fraction, int(self.keep_self), self.final_idx.data_ptr(), self.final_valid.data_ptr(),
                     ids.data_ptr(), n_out, _lib.stream_of(q)))
-        token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+        if not attended.value:
+            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
         self.n_out = n_out
 
     # -- state views (tests, tracing) ------------------------------------------

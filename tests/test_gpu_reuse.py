@@ -311,14 +311,43 @@ def test_reuse_select_bits_equals_bytes(hist, sink, recent, frac, prev):
         fv = torch.empty((rows, n_out), dtype=torch.uint8, device=DEV)
         ids = torch.empty((rows, n_out), dtype=torch.int32, device=DEV)
         select = lib.qkv_reuse_select_bits if bits else lib.qkv_reuse_select
+        extra = (None, None, None) if bits else ()
         _lib.check(select(q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), 0, b, hq, hkv, t, d,
                           ms[0].data_ptr(), ms[1].data_ptr() if prev else None, ms[2].data_ptr(), ms[0].stride(0),
                           sink, recent, frac, 1, 0.088, ws.data_ptr(), ws.numel() * 4, fi.data_ptr(), fv.data_ptr(),
-                          ids.data_ptr(), n_out, fin.data_ptr(), fin.stride(0), _lib.stream_of(q)))
+                          ids.data_ptr(), n_out, fin.data_ptr(), fin.stride(0), *extra, _lib.stream_of(q)))
         hf = RU.expand_bits(fin, hist) if bits else fin.bool()
         outs.append((fi, fv, ids, hf))
     for a, w in zip(*outs):
         assert torch.equal(a, w)
+
+
+@pytest.mark.parametrize("dtype,hist,frac,fused", [(torch.bfloat16, 3000, 0.02, True), (torch.float16, 9000, 0.05, True),
+                                                   (torch.bfloat16, 40000, 0.11, False)])
+def test_step_attention_in_the_final_selection(dtype, hist, frac, fused):
+    # the final selection's workgroups attend over the list they wrote (one launch);
+    # past 4096 list entries the separate token attention runs -- either way the
+    # output equals the token attention over the step's own list
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(hist)
+    hq, hkv = 8, 2
+    k = torch.randn((1, hkv, hist + 1, 128), generator=gen).to(dtype).to(DEV)
+    v = torch.randn((1, hkv, hist + 1, 128), generator=gen).to(dtype).to(DEV)
+    q = torch.randn((1, hq, 128), generator=gen).to(dtype).to(DEV)
+    step = RU.ReuseDecodeStep("qabs8cand5reuse", 1, hq, hkv, 128, hist + 8, top_fraction=frac, protect_sink=4,
+                              protect_recent=8, dtype=dtype, fused_attention=True)
+    out = step(q, k, v, 0.088).clone()
+    n_out = step.n_out
+    assert (n_out <= 4096) == fused
+    ids = step.attn_ids[: hq * n_out].view(hq, n_out)
+    want = RU.token_attention(q, k, v, ids, 0.088, workspace=step.attn_ws)
+    torch.testing.assert_close(out.float(), want.float(), rtol=2e-2, atol=2e-3)
+    fi, fv = (x.cpu().numpy() for x in step.final_indices())
+    o = R.final_attention(f32(q), np.repeat(f32(k), hq // hkv, axis=1), np.repeat(f32(v), hq // hkv, axis=1),
+                          fi, fv, 0.088)
+    np.testing.assert_allclose(f32(out), o[:, 0], rtol=RTOL, atol=ATOL)
 
 
 def test_reuse_select_ties_and_missing_masks():
