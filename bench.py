@@ -767,7 +767,21 @@ def run_reuse(args) -> dict:
             RU.candidate_mask(steps[layer].partial, hist_fixed, "topk", requested, steps[layer].cand[0], None,
                               mask_ws[layer])
 
-    if n_s:   # the sampled columns gathered (index and score), then the mask pass
+    if selection == "topk" and not lagged and st0.bits:
+        # the step's candidates call: the partial scores with their first-digit
+        # counts, then the selection across several workgroups per row
+        mask_name = "reuse_candidates"
+        mask_bytes = rows * hist_fixed * (s_dims * 2 + 4) + rows * hist_fixed * 4 + rows * hist_fixed // 8
+
+        def run_mask():
+            for layer in range(layers):
+                st = steps[layer]
+                RU._lib.check(lib.qkv_reuse_candidates(
+                    qs[layer].data_ptr(), st.kdm.data_ptr(), RU._lib.strides(*st.kdm.stride()), 0, b, hq, hkv,
+                    hist_fixed, d, s_dims, requested, st.partial.data_ptr(), st.partial.stride(0), None, 0,
+                    st.cand[0].data_ptr(), st.cand[0].stride(0), None, st.cand_ws.data_ptr(), st.cand_ws.numel() * 4,
+                    RU._lib.stream_of(qs[layer])))
+    elif n_s:   # the sampled columns gathered (index and score), then the mask pass
         mask_name, mask_bytes = "sample_quantile_mask", n_s * 4 + rows * n_s * 8 + rows * hist_fixed * (4 + 1)
 
         def run_mask():

@@ -570,17 +570,28 @@ int64_t qkv_threshold_mask_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 int qkv_threshold_mask(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, uint8_t* mask,
                        int64_t mask_ld, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes of qkv_reuse_candidates for rows = batch * q_heads (-1
+ * for bad arguments). */
+int64_t qkv_reuse_candidates_workspace_bytes(int64_t rows, int64_t history, int64_t k);
+
 /* The reuse step's candidates (EV:3988, 4136-4144): qkv_reuse_partial_scores
  * into partial (row stride partial_ld), then mask = partial >= the row's
  * k-th largest (qkv_threshold_mask), as a byte mask (mask, row stride
  * mask_ld) or a bitset (bits: bit t % 64 of uint64 word t / 64, row stride
  * bits_ld words, 8-byte aligned) -- exactly one of the two; thr_out f32
- * [batch * q_heads] (optional) receives the k-th largest.  One launch per call where the
- * rows fit one workgroup (history <= 40960, head_dim <= 128, a 16-byte
- * aligned copy), the two launches otherwise; workspace as for
- * qkv_threshold_mask (qkv_threshold_mask_workspace_bytes(batch * q_heads,
- * history, k)).  No reference counterpart as one call: the reference runs
- * the two steps separately (QK:63-96, then torch.topk at EV:3988). */
+ * [batch * q_heads] (optional) receives the k-th largest.  Rows of at most
+ * 40960 history tokens: one launch per call for 128 rows and more
+ * (head_dim <= 128, a 16-byte aligned copy); for fewer rows with a bitset
+ * the partial scores also count each row's leading 12 bits and a second
+ * launch selects with several workgroups per row; otherwise the two
+ * launches of qkv_reuse_partial_scores and qkv_threshold_mask.
+ * workspace: qkv_reuse_candidates_workspace_bytes(batch * q_heads, history,
+ * k) bytes, 16-byte aligned, zero-filled before the first call that uses
+ * it (allocate it zero-filled): it holds per-row counts and tickets that
+ * every completed call leaves zero again.  Calls that share a workspace use
+ * the same batch * q_heads and must not overlap in time.  No reference counterpart as one call: the
+ * reference runs the two steps separately (QK:63-96, then torch.topk at
+ * EV:3988). */
 int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
                          int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history, int64_t head_dim,
                          int64_t dim_count, int64_t k, float* partial, int64_t partial_ld, uint8_t* mask,

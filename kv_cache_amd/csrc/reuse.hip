@@ -37,14 +37,25 @@ constexpr int kMaskTile = 4096;   // tokens per workgroup in reuse_mask_kernel
 // Partial scores: out[r, t] = sum_s q[d_s] * K[d_s, t] over the row's
 // top-|q| dims d_s in selection order (QK:63-96 on the dim-major copy of
 // EV:2018-2042; dims chosen as QK:120-145).  Eight tokens per thread.
+// HIST: each score's top 12 order-preserving bits (the first radix digit of
+// the candidate selection, kCandBins bins) are also counted into
+// hist[row * kCandBins + digit], through a workgroup histogram in LDS and
+// one global atomic per non-empty bin.
 // ---------------------------------------------------------------------------
-template <int DT>
+constexpr int kCandBits = 12, kCandBins = 1 << kCandBits;
+
+template <int DT, bool HIST = false>
 __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm,
     int q_heads, int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd,
     bool vec, float* __restrict__ out, int64_t out_ld, const uint8_t* __restrict__ gate, int gate_refresh,
-    int gate_rows) {
+    int gate_rows, int* __restrict__ hist = nullptr) {
   using E = typename Elem<DT>::T;
+  __shared__ int hist_s[HIST ? kCandBins : 1];
+  if constexpr (HIST) {
+#pragma unroll
+    for (int j = 0; j < kCandBins / kRT; ++j) hist_s[threadIdx.x + kRT * j] = 0;   // (a barrier follows)
+  }
   __shared__ float q_s[512];
   __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
   __shared__ int sel_idx[kMaxDims];
@@ -82,13 +93,16 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     __syncthreads();
   }
   const int t0 = (blockIdx.x * kRT + tid) * 8;
-  if (t0 >= history) return;
-  const E* base = kdm + b * sb + (h / group) * sh + t0;
+  if (!HIST && t0 >= history) return;
+  const int nt = max(min(8, history - t0), 0);   // this thread's tokens
+  const E* base = kdm + b * sb + (h / group) * sh + min(t0, history - 1);
   float* o = out + static_cast<int64_t>(row) * out_ld + t0;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  if (vec && t0 + 8 <= history) {
+  if (nt == 0) {
+    // (HIST: a thread past the row still takes part in the barriers below)
+  } else if (vec && nt == 8) {
     // eight dims' loads in flight at once (clamped, in bounds), then the
     // products added in selection order
     for (int s0 = 0; s0 < count; s0 += 8) {
@@ -132,6 +146,18 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       if (i < n) o[i] = acc[i];
+  }
+  if constexpr (HIST) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < nt) atomicAdd(&hist_s[f32_sortable(acc[i]) >> (32 - kCandBits)], 1);
+    __syncthreads();
+    int* hrow = hist + static_cast<int64_t>(row) * kCandBins;
+#pragma unroll
+    for (int j = 0; j < kCandBins / kRT; ++j) {
+      const int c = hist_s[tid + kRT * j];
+      if (c) __hip_atomic_fetch_add(hrow + tid + kRT * j, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -603,6 +629,225 @@ __global__ __launch_bounds__(kWideNT) void reuse_mask_wide_kernel(const float* _
       for (int j = 0; j < 16 && t0 + j < n; ++j) mrow[t0 + j] = (bits >> j) & 1u;
     }
   }
+}
+
+// The candidate bitset across several workgroups per row (rows of at most
+// kWideMax scores), in one launch after reuse_partial_kernel<DT, true> has
+// counted every row's first digit into hist.  Slice s of a row (kWideNT * J
+// scores; slot i of wave w covers bitset word s * 16 * J + w * J + i) finds
+// the row's boundary bin from the histogram -- the bin holding the k-th
+// largest score, as WideSelect resolves its first digit -- and writes its
+// words with the scores above that bin set.  Its scores inside the bin go,
+// compacted, to its part of the row's list (list_val / list_pos from
+// s * kWideNT * J), their count to state[row * kCandState + s].  The row's
+// last slice to finish (ticket state[row * kCandState + kCandSlices]) then
+// selects the rank-th largest of the list (the k-th largest of the row),
+// sets the bits of the list's scores at or above it, writes it to thr_out
+// (optional), and returns the row's histogram and ticket to zero for the
+// next call.  Slices store coherently and complete their stores before the
+// ticket; the last slice reads coherently.  The ticket is the only atomic
+// that workgroups share (a chain of same-address atomics from many
+// workgroups costs about 0.2 us a link).
+// ---------------------------------------------------------------------------
+constexpr int kCandSlices = kWideMax / kWideNT;   // slices of at least kWideNT scores
+constexpr int kCandState = kCandSlices + 8;       // state ints per row
+
+// Offset in the row's list of its p-th bin score: slice s's scores start at
+// s * slice_len, pre[s] of them before it (pre: slices + 1 prefix counts).
+__device__ __forceinline__ int cand_list_at(const int* pre, int slices, int slice_len, int p) {
+  int lo = 0, hi = slices - 1;   // the last slice with pre[s] <= p
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (pre[mid] <= p) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo * slice_len + (p - pre[lo]);
+}
+
+// The smallest of the taken scores' keys over the workgroup, as the row's
+// threshold (theta may be the lower bound of a boundary bin taken whole).
+__device__ void cand_write_threshold(uint32_t mn, float* __restrict__ thr) {
+  __shared__ uint32_t wave_min[kWideNT / 64];
+  mn = wave_minmax_u32<false>(mn);
+  if ((threadIdx.x & 63) == 0) wave_min[threadIdx.x >> 6] = mn;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWideNT / 64; ++w) mn = min(mn, wave_min[w]);
+    *thr = sortable_f32(mn);
+  }
+}
+
+// The rank-th largest of the m list scores held in registers (m <= kWideNT *
+// VPL), its bits set in brow.
+template <int VPL, typename At>
+__device__ void cand_list_finish(void* raw, const float* __restrict__ lv, const int* __restrict__ lp, int m,
+                                 int rank, int n, uint64_t* __restrict__ brow, float* __restrict__ thr, At&& at) {
+  using WS = WideSelect<VPL, false>;
+  auto& sh = *static_cast<typename WS::Shared*>(raw);
+  WS ws;
+  int off[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int p = WS::pos(i);
+    off[i] = p < m ? at(p) : 0;
+    ws.set(i, p < m ? ld_coherent(lv + off[i]) : 0.0f, p < m);
+  }
+  ws.run(rank, sh);
+  uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (ws.on(i) && ws.u[i] >= ws.theta) {
+      const int pos = ld_coherent(lp + off[i]);
+      if (static_cast<unsigned>(pos) < static_cast<unsigned>(n))   // (a position of this row's scores)
+        atomicOr(reinterpret_cast<unsigned long long*>(brow + (pos >> 6)), 1ull << (pos & 63));
+      mn = min(mn, ws.u[i]);
+    }
+  }
+  if (thr) cand_write_threshold(mn, thr);
+}
+
+// The same for a list too long for registers: radix passes over the bits
+// below the boundary bin's digit, the list read from memory on every pass.
+template <typename At>
+__device__ void cand_list_finish_stream(void* raw, const float* __restrict__ lv, const int* __restrict__ lp, int m,
+                                        int rank, int bin, int n, uint64_t* __restrict__ brow,
+                                        float* __restrict__ thr, At&& at) {
+  using WS = WideSelect<1, false>;
+  auto& sh = *static_cast<typename WS::Shared*>(raw);
+  const int tid = threadIdx.x;
+  WS ws;
+  ws.kr = rank;
+  uint32_t prefix = static_cast<uint32_t>(bin) << (32 - kCandBits), mask = ~((1u << (32 - kCandBits)) - 1u);
+  int remaining = 32 - kCandBits, buf = 0;
+#pragma unroll
+  for (int j = 0; j < WS::NB / kWideNT; ++j) sh.hist[0][tid + kWideNT * j] = 0;
+  __syncthreads();
+  while (remaining > 0) {   // uniform
+    const int shift = remaining > WS::RB ? remaining - WS::RB : 0;
+    const uint32_t dmask = (1u << (remaining - shift)) - 1u;
+    for (int p = tid; p < m; p += kWideNT) {
+      const uint32_t u = f32_sortable(ld_coherent(lv + at(p)));
+      if ((u & mask) == prefix) atomicAdd(&sh.hist[buf][(u >> shift) & dmask], 1);
+    }
+    __syncthreads();
+    int b, krl, whole;
+    ws.boundary(sh, sh.hist[buf], sh.hist[buf ^ 1], b, krl, whole);
+    prefix |= static_cast<uint32_t>(b) << shift;
+    mask |= dmask << shift;
+    ws.kr = krl;
+    remaining = whole ? 0 : shift;
+    buf ^= 1;
+    __syncthreads();   // (the histogram's reads are done before the next pass)
+  }
+  // prefix: the smallest taken key or the lower bound of a bin taken whole
+  uint32_t mn = 0xFFFFFFFFu;
+  for (int p = tid; p < m; p += kWideNT) {
+    const int o = at(p);
+    const uint32_t u = f32_sortable(ld_coherent(lv + o));
+    if (u >= prefix) {
+      const int pos = ld_coherent(lp + o);
+      if (static_cast<unsigned>(pos) < static_cast<unsigned>(n))
+        atomicOr(reinterpret_cast<unsigned long long*>(brow + (pos >> 6)), 1ull << (pos & 63));
+      mn = min(mn, u);
+    }
+  }
+  if (thr) cand_write_threshold(mn, thr);
+}
+
+template <int J>
+__global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
+    const float* __restrict__ values, int64_t ld, int n, int k, int slices, int* __restrict__ hist,
+    int* __restrict__ state, float* __restrict__ list_val, int* __restrict__ list_pos, int64_t list_ld,
+    uint64_t* __restrict__ bits, int64_t bits_ld, float* __restrict__ thr_out) {
+  using WS = WideSelect<1, false>;
+  static_assert(sizeof(typename WideSelect<1, false>::Shared) == sizeof(typename WideSelect<8, false>::Shared),
+                "one shared layout for every list length");
+  __shared__ typename WS::Shared sh;
+  __shared__ int wave_cnt[kWideNT / 64];
+  __shared__ int pre[kCandSlices + 1];
+  __shared__ int last_sh;
+  const int row = blockIdx.x / slices, s = blockIdx.x - row * slices;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int* hrow = hist + static_cast<int64_t>(row) * kCandBins;
+  const float* vrow = values + static_cast<int64_t>(row) * ld;
+  // the histogram (4 bins per thread) and the slice's scores, all loads in flight
+  const int4 hv = *reinterpret_cast<const int4*>(hrow + 4 * tid);
+  const int w0 = s * 16 * J + wave * J;   // the wave's first word
+  float v[J];
+#pragma unroll
+  for (int i = 0; i < J; ++i) v[i] = vrow[min(64 * (w0 + i) + lane, n - 1)];
+  *reinterpret_cast<int4*>(sh.hist[0] + 4 * tid) = hv;
+  __syncthreads();
+  WS ws;
+  ws.kr = k;
+  int bin, rank, whole;
+  ws.boundary(sh, sh.hist[0], sh.hist[1], bin, rank, whole);
+  int* srow = state + static_cast<int64_t>(row) * kCandState;
+  uint64_t* brow = bits + static_cast<int64_t>(row) * bits_ld;
+  const int n_words = (n + 63) / 64;
+  uint32_t inbin = 0;   // bit i: slot i's score is in the boundary bin
+#pragma unroll
+  for (int i = 0; i < J; ++i) {
+    const int p = 64 * (w0 + i) + lane;
+    const uint32_t d = f32_sortable(v[i]) >> (32 - kCandBits);
+    const uint64_t w = __ballot(p < n && d > static_cast<uint32_t>(bin));
+    if (lane == 0 && w0 + i < n_words)
+      __hip_atomic_store(brow + w0 + i, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    inbin |= static_cast<uint32_t>(p < n && d == static_cast<uint32_t>(bin)) << i;
+  }
+  // the slice's bin scores compacted in (wave, slot, lane) = position order
+  const int cnt = __popc(inbin), incl = wave_incl_scan_dpp(cnt);
+  if (lane == 63) wave_cnt[wave] = incl;
+  __syncthreads();
+  int at = incl - cnt, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWideNT / 64; ++w) {
+    at += w < wave ? wave_cnt[w] : 0;
+    total += wave_cnt[w];
+  }
+  if (tid == 0) st_coherent(srow + s, total);
+  if (cnt) {
+    const int64_t base = static_cast<int64_t>(row) * list_ld + static_cast<int64_t>(s) * kWideNT * J;
+#pragma unroll
+    for (int i = 0; i < J; ++i) {
+      if ((inbin >> i) & 1u) {
+        st_coherent(list_val + base + at, v[i]);
+        st_coherent(list_pos + base + at, 64 * (w0 + i) + lane);
+        ++at;
+      }
+    }
+  }
+  // Every word, count and list store of this workgroup has completed before its ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    // compiler-only fences keep memory operations on their side of the ticket
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int t = __hip_atomic_fetch_add(srow + kCandSlices, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const bool last = t == slices - 1;
+    if (last) __hip_atomic_store(srow + kCandSlices, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_sh = last;
+  }
+  __syncthreads();
+  if (!last_sh) return;
+  // The row's last slice: every slice has read the histogram and stored its list.
+  if (tid < 64) {   // prefix counts of the slices' lists (slices <= 40)
+    const int c = tid < slices ? ld_coherent(srow + tid) : 0;
+    const int inc = wave_incl_scan_dpp(c);
+    if (tid <= slices) pre[tid] = inc - c;
+  }
+  *reinterpret_cast<int4*>(hrow + 4 * tid) = make_int4(0, 0, 0, 0);
+  __syncthreads();
+  const int m = min(pre[slices], n);
+  const float* lv = list_val + static_cast<int64_t>(row) * list_ld;
+  const int* lp = list_pos + static_cast<int64_t>(row) * list_ld;
+  float* thr = thr_out ? thr_out + row : nullptr;
+  const int slice_len = kWideNT * J;
+  auto at_fn = [&](int p) { return cand_list_at(pre, slices, slice_len, p); };
+  if (m <= kWideNT) cand_list_finish<1>(&sh, lv, lp, m, rank, n, brow, thr, at_fn);
+  else if (m <= 8 * kWideNT) cand_list_finish<8>(&sh, lv, lp, m, rank, n, brow, thr, at_fn);
+  else cand_list_finish_stream(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
 }
 
 // The step's candidates in one launch (rows of at most kWideMax history
@@ -1220,19 +1465,25 @@ int64_t mask_ws_bytes(int64_t rows, int64_t n, int64_t k) {
   return align256(rows * k * 4) + align256(tk);
 }
 
+// hist (optional, [B * Hq, kCandBins] int, zero): every row's first-digit
+// counts (reuse_partial_kernel's HIST).
 template <int DT> struct RunReusePartial {
   static int run(const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq, int64_t Hkv,
                  int64_t T, int64_t D, int count, float* out, int64_t out_ld, hipStream_t st,
-                 const uint8_t* gate = nullptr, int gate_refresh = 0) {
+                 const uint8_t* gate = nullptr, int gate_refresh = 0, int* hist = nullptr) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
     const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
     dim3 grid(static_cast<unsigned>(cdiv(T, 8 * kRT)), static_cast<unsigned>(B * Hq));
-    reuse_partial_kernel<DT><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),
-                                                   static_cast<int>(Hq), static_cast<int>(Hq / Hkv),
-                                                   static_cast<int>(T), static_cast<int>(D), count, ks[0], ks[1],
-                                                   ks[2], vec, out, out_ld, gate, gate_refresh,
-                                                   static_cast<int>(B * Hq));
+#define QKV_REUSE_PARTIAL(HH)                                                                                  \
+  reuse_partial_kernel<DT, HH><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),     \
+                                                     static_cast<int>(Hq), static_cast<int>(Hq / Hkv),         \
+                                                     static_cast<int>(T), static_cast<int>(D), count, ks[0],   \
+                                                     ks[1], ks[2], vec, out, out_ld, gate, gate_refresh,       \
+                                                     static_cast<int>(B * Hq), hist)
+    if (hist) QKV_REUSE_PARTIAL(true);
+    else QKV_REUSE_PARTIAL(false);
+#undef QKV_REUSE_PARTIAL
     return check_launch("qkv_reuse_partial_scores");
   }
 };
@@ -1320,15 +1571,51 @@ int threshold_mask_impl(const char* what, const float* values, int64_t rows, int
 
 constexpr int64_t kFusedCandRows = 128;
 
-// Partial scores into partial, then mask = partial >= the row's k-th
-// largest (thr_out: the thresholds): one launch (reuse_candidates_kernel)
-// where the row fits it, else reuse_partial_kernel and threshold_mask_impl.
+// The state of the cross-workgroup candidate selection at the start of a
+// candidates workspace: per row the first-digit histogram (kCandBins ints),
+// then per row the slices' list counts and the ticket (kCandState ints);
+// the histograms and tickets are zero between calls.
+int64_t cand_state_bytes(int64_t rows) { return align256(rows * kCandBins * 4) + align256(rows * kCandState * 4); }
+
+// The rest of the workspace: the boundary-bin lists (a score and a position
+// per history token and row) or, on the other paths, qkv_threshold_mask's.
+int64_t cand_scratch_bytes(int64_t rows, int64_t n, int64_t k) {
+  const int64_t m = mask_ws_bytes(rows, n, k);
+  return m < 0 ? -1 : std::max(m, 2 * align256(rows * n * 4));
+}
+
+struct CandSplit {
+  int* hist = nullptr;   // null: the selection runs one workgroup per row
+  int* state = nullptr;
+  float* list_val = nullptr;
+  int* list_pos = nullptr;
+};
+
+// reuse_cand_slices_kernel over rows x slices workgroups: J scores per
+// thread, about 512 workgroups (J 1..8).
+int launch_cand_slices(const char* what, const float* values, int64_t ld, int64_t rows, int64_t n, int64_t k,
+                       const CandSplit& cs, uint64_t* bits, int64_t bits_ld, float* thr_out, hipStream_t st) {
+  auto launch = [&](auto jc) {
+    constexpr int J = decltype(jc)::value;
+    const int64_t slices = cdiv(n, int64_t(kWideNT) * J);
+    reuse_cand_slices_kernel<J><<<static_cast<unsigned>(rows * slices), kWideNT, 0, st>>>(
+        values, ld, static_cast<int>(n), static_cast<int>(k), static_cast<int>(slices), cs.hist, cs.state,
+        cs.list_val, cs.list_pos, n, bits, bits_ld, thr_out);
+    return check_launch(what);
+  };
+  auto wgs = [&](int64_t j) { return rows * cdiv(n, int64_t(kWideNT) * j); };
+  if (wgs(1) <= 512) return launch(std::integral_constant<int, 1>{});
+  if (wgs(2) <= 512) return launch(std::integral_constant<int, 2>{});
+  if (wgs(4) <= 512) return launch(std::integral_constant<int, 4>{});
+  return launch(std::integral_constant<int, 8>{});
+}
+
 template <int DT> struct RunCandidates {
   static int run(const char* what, const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq,
                  int64_t Hkv, int64_t T, int64_t D, int count, int64_t k, float* partial, int64_t partial_ld,
                  uint8_t* mask, int64_t mask_ld, float* thr_out, void* workspace, int64_t workspace_bytes,
                  hipStream_t st, const uint8_t* gate, int refresh, uint64_t* bits = nullptr,
-                 int64_t bits_ld = 0) {
+                 int64_t bits_ld = 0, const CandSplit& split = CandSplit{}) {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
     const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
@@ -1351,6 +1638,13 @@ template <int DT> struct RunCandidates {
       if (T <= 3 * per) return launch(std::integral_constant<int, 3>{});
       if (T <= 4 * per) return launch(std::integral_constant<int, 4>{});
       return launch(std::integral_constant<int, 5>{});
+    }
+    if (split.hist && bits && !gate && T <= kWideMax) {
+      // the partial scores count the first digit; several workgroups per row select
+      int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, nullptr, 0,
+                                        split.hist);
+      if (rc) return rc;
+      return launch_cand_slices(what, partial, partial_ld, rows, T, k, split, bits, bits_ld, thr_out, st);
     }
     int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, gate, refresh);
     if (rc) return rc;
@@ -1710,16 +2004,31 @@ QKV_EXPORT int qkv_reuse_candidates(const void* query, const void* key_dim_major
     return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, row strides covering the history",
                 what);
   if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
-  const int64_t need = mask_ws_bytes(batch * q_heads, history, k);
+  const int64_t rows = batch * q_heads;
+  const int64_t need = qkv_reuse_candidates_workspace_bytes(rows, history, k);
   if (need < 0 || workspace_bytes < need)
     return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
                 (long long)workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(QKV_ERR_INVALID, "%s: the workspace must be 16-byte aligned", what);
   const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
                                                        std::min<int64_t>(head_dim, kMaxDims)));
+  char* ws = static_cast<char*>(workspace);
+  const int64_t state = cand_state_bytes(rows);
+  CandSplit split;
+  split.hist = reinterpret_cast<int*>(ws);
+  split.state = reinterpret_cast<int*>(ws + align256(rows * kCandBins * 4));   // (kCandState ints per row)
+  split.list_val = reinterpret_cast<float*>(ws + state);
+  split.list_pos = reinterpret_cast<int*>(ws + state + align256(rows * history * 4));
   return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
                                        history, head_dim, count, k, partial, partial_ld, mask, mask_ld, thr_out,
-                                       workspace, workspace_bytes, static_cast<hipStream_t>(stream), nullptr,
-                                       QKV_REFRESH_ALL, bits, bits_ld);
+                                       ws + state, workspace_bytes - state, static_cast<hipStream_t>(stream), nullptr,
+                                       QKV_REFRESH_ALL, bits, bits_ld, split);
+}
+
+QKV_EXPORT int64_t qkv_reuse_candidates_workspace_bytes(int64_t rows, int64_t history, int64_t k) {
+  if (rows <= 0 || history <= 0 || history >= (int64_t(1) << 31) || k < 1 || k > history) return -1;
+  const int64_t scratch = cand_scratch_bytes(rows, history, k);
+  return scratch < 0 ? -1 : cand_state_bytes(rows) + scratch;
 }
 
 QKV_EXPORT int64_t qkv_candidate_mask_workspace_bytes(int64_t rows, int64_t n, int selection, int64_t k,

@@ -348,6 +348,11 @@ class ReuseDecodeStep:
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
         self.mask_ws = self._ws(lib.qkv_threshold_mask_workspace_bytes(rows, hist_max, budget_count(hist_max,
                                                                                                     self.cand_fraction)))
+        # qkv_reuse_candidates' own workspace: zero-filled (its selection state
+        # starts at zero and every call leaves it so)
+        need = lib.qkv_reuse_candidates_workspace_bytes(rows, hist_max, budget_count(hist_max, self.cand_fraction))
+        _require(need >= 0, "bad workspace size")
+        self.cand_ws = torch.zeros(max(1, (need + 3) // 4), dtype=torch.float32, device=device)
         n_s_max = self.columns.max_count if self.columns is not None else 0
         if n_s_max:   # sized once for the largest sample, so a captured step never reallocates
             self.mask_ws = self._grow(self.mask_ws, lib.qkv_candidate_mask_workspace_bytes(
@@ -459,8 +464,9 @@ class ReuseDecodeStep:
             candidate_mask(self.partial, history, "sample_quantile", k_s, current, self.thresholds, self.mask_ws,
                            self.columns.row(history), n_s)
         else:                                                                 # EV:3988
-            self.mask_ws = self._grow(self.mask_ws,
-                                      lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+            need = lib.qkv_reuse_candidates_workspace_bytes(self.rows, history, requested)
+            if self.cand_ws.numel() * 4 < need:   # (a fresh workspace starts zero-filled)
+                self.cand_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=self.device)
             # partial scores, threshold and mask in one launch where a row fits one
             # workgroup; the threshold is kept only where a later step reads it
             with torch.cuda.device(q.device):
@@ -471,8 +477,8 @@ class ReuseDecodeStep:
                     self.partial.data_ptr(), self.partial.stride(0), None if bits else current.data_ptr(),
                     0 if bits else current.stride(0), current.data_ptr() if bits else None,
                     current.stride(0) if bits else 0,
-                    _lib.ptr(self.thresholds) if self.selection != "topk" else None, self.mask_ws.data_ptr(),
-                    self.mask_ws.numel() * 4, _lib.stream_of(q)))
+                    _lib.ptr(self.thresholds) if self.selection != "topk" else None, self.cand_ws.data_ptr(),
+                    self.cand_ws.numel() * 4, _lib.stream_of(q)))
 
     def _select_attend(self, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scaling: float,
                        current: torch.Tensor, previous: torch.Tensor | None,

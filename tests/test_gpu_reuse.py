@@ -247,7 +247,10 @@ def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated, bits):
     mask = torch.full((rows, hist + 9), 9, dtype=torch.uint8, device=DEV)
     words = torch.full((rows, -(-hist // 64) + 3), -1, dtype=torch.int64, device=DEV)
     thr = torch.zeros(rows, device=DEV)
-    ws = torch.empty((lib.qkv_threshold_mask_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
+    if gated:
+        ws = torch.empty((lib.qkv_threshold_mask_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
+    else:   # zero-filled: the selection state starts at zero
+        ws = torch.zeros((lib.qkv_reuse_candidates_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
     flags = (torch.arange(rows) % 3 == 0).to(torch.uint8).to(DEV)
     qd = q.to(DEV)
     if gated:
@@ -278,6 +281,122 @@ def test_reuse_candidates_match_oracle(dtype, b, hist, dims, gated, bits):
         assert (got_p[~on] == 7.0).all() and (got_m[~on] == 9).all()
     else:
         assert np.array_equal(thr.cpu().numpy(), kth[:, 0])
+        _assert_cand_state_zero(ws, rows)
+
+
+def _assert_cand_state_zero(ws, rows):
+    # the parts of qkv_reuse_candidates' workspace that are zero between
+    # calls: the 4096 first-digit bins per row at its start, then (after 48
+    # state words per row: 40 list counts, the ticket, padding) each row's ticket
+    assert not ws[: rows * 4096].any()
+    state = ws[rows * 4096 : rows * 4096 + rows * 48].view(torch.int32).view(rows, 48)
+    assert not state[:, 40].any()
+
+
+def _cand_case(b, hist, dims, pattern, seed):
+    # (q, K) whose partial scores follow `pattern`: K[t] = c_t * (a fixed
+    # vector), so the scores are c_t times the row's sum over its dims
+    gen = torch.Generator().manual_seed(seed)
+    hq, hkv, d = 32, 8, 128
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16)
+    if pattern == "normal":
+        k = torch.randn((b, hkv, hist, d), generator=gen)
+    else:
+        if pattern == "equal":          # every score of a row equal: the whole row in one bin
+            c = torch.ones(hist)
+        elif pattern == "narrow":       # 256 values in [1, 2): about an eighth of a row per bin
+            c = 1.0 + torch.randint(0, 256, (hist,), generator=gen).float() / 256.0
+        elif pattern == "coarse":       # 16 values in [1, 1.125): one bin, heavy ties
+            c = 1.0 + torch.randint(0, 16, (hist,), generator=gen).float() / 128.0
+        else:
+            raise ValueError(pattern)
+        k = c.view(1, 1, hist, 1).expand(b, hkv, hist, d).clone()
+    return q, k.to(torch.bfloat16)
+
+
+def _run_candidates(lib, q, kdm, hist, dims, kk, words, thr, ws, part):
+    from kv_cache_amd import _lib
+
+    b, hq, d = q.shape
+    _lib.check(lib.qkv_reuse_candidates(
+        q.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), _lib.DTYPE_CODES[q.dtype], b, hq, kdm.shape[1],
+        hist, d, dims, kk, part.data_ptr(), part.stride(0), None, 0, words.data_ptr(), words.stride(0),
+        thr.data_ptr(), ws.data_ptr(), ws.numel() * 4, _lib.stream_of(q)))
+
+
+def _check_candidates(q, k, hist, dims, kk, words, thr):
+    b, hq, _ = q.shape
+    rows = b * hq
+    want = R.partial_scores(f32(q), np.repeat(f32(k), hq // k.shape[1], axis=1), dims).reshape(rows, hist)
+    kth = -np.sort(-want, axis=1)[:, kk - 1 : kk]
+    n_w = -(-hist // 64)
+    got = RU.expand_bits(words[:, :n_w], n_w * 64).cpu().numpy()
+    assert not got[:, hist:].any()
+    assert np.array_equal(got[:, :hist], want >= kth)
+    assert np.array_equal(thr.cpu().numpy(), kth[:, 0])
+
+
+@pytest.mark.parametrize("b,hist,pattern,frac", [
+    (1, 20000, "equal", 5),      # the boundary bin holds the whole row: the list selected from memory
+    (1, 20000, "narrow", 5),     # a list of a few thousand: eight scores per thread
+    (1, 30011, "coarse", 5),     # one bin and 16 distinct scores: ties at the threshold
+    (2, 40960, "normal", 2),     # 64 rows at the longest one-workgroup row
+    (1, 1000, "normal", 50),     # one slice per row
+    (3, 777, "narrow", 100),     # k = the whole row
+])
+def test_reuse_candidates_slices(b, hist, pattern, frac):
+    # the partial scores' first-digit counts and the selection across several
+    # workgroups per row: the bitset = score >= the k-th largest, the threshold
+    # exact, the workspace's state zero afterwards
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    dims = 8
+    q, k = _cand_case(b, hist, dims, pattern, hist + b)
+    rows = b * 32
+    kdm = torch.zeros((b, 8, 128, hist + 24), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k.to(DEV), kdm, 0, hist)
+    kk = min(hist, -(-hist * frac // 100))
+    part = torch.zeros((rows, hist + 9), device=DEV)
+    words = torch.full((rows, -(-hist // 64) + 3), -1, dtype=torch.int64, device=DEV)
+    thr = torch.zeros(rows, device=DEV)
+    ws = torch.zeros((lib.qkv_reuse_candidates_workspace_bytes(rows, hist, kk) + 3) // 4, device=DEV)
+    qd = q.to(DEV)
+    _run_candidates(lib, qd, kdm, hist, dims, kk, words, thr, ws, part)
+    _check_candidates(q, k, hist, dims, kk, words, thr)
+    assert (words[:, -(-hist // 64):] == -1).all()
+    _assert_cand_state_zero(ws, rows)
+
+
+def test_reuse_candidates_workspace_reused():
+    # one zero-filled workspace through calls of growing and shrinking history
+    # (and a byte-mask call between them): every call exact, the state zero
+    # after each
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    b, cap, dims = 1, 33000, 8
+    rows = b * 32
+    q, k = _cand_case(b, cap, dims, "normal", 11)
+    kdm = torch.zeros((b, 8, 128, cap + 8), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k.to(DEV), kdm, 0, cap)
+    ws = torch.zeros((lib.qkv_reuse_candidates_workspace_bytes(rows, cap, cap) + 3) // 4, device=DEV)
+    part = torch.zeros((rows, cap), device=DEV)
+    words = torch.zeros((rows, -(-cap // 64)), dtype=torch.int64, device=DEV)
+    thr = torch.zeros(rows, device=DEV)
+    qd = q.to(DEV)
+    for hist in (32768, 32769, 4097, 33000, 100):
+        kk = -(-hist * 2 // 100)
+        _run_candidates(lib, qd, kdm, hist, dims, kk, words, thr, ws, part)
+        _check_candidates(q, k[:, :, :hist], hist, dims, kk, words, thr)
+        _assert_cand_state_zero(ws, rows)
+        if hist == 4097:   # the byte mask takes the other path through the same workspace
+            mask = torch.zeros((rows, hist), dtype=torch.uint8, device=DEV)
+            _lib.check(lib.qkv_reuse_candidates(
+                qd.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), _lib.DTYPE_CODES[qd.dtype], b, 32, 8,
+                hist, 128, dims, kk, part.data_ptr(), part.stride(0), mask.data_ptr(), mask.stride(0), None, 0,
+                None, ws.data_ptr(), ws.numel() * 4, _lib.stream_of(qd)))
+            assert np.array_equal(mask.cpu().numpy().astype(bool), RU.expand_bits(words, cap)[:, :hist].cpu().numpy())
 
 
 @pytest.mark.parametrize("hist,sink,recent,frac,prev", [(3000, 4, 8, 0.02, True), (1001, 0, 0, 0.05, False),
