@@ -679,9 +679,12 @@ __device__ void cand_write_threshold(uint32_t mn, float* __restrict__ thr) {
 
 // The rank-th largest of the m list scores held in registers (m <= kWideNT *
 // VPL), its bits set in brow.
+// The list's scores share the boundary bin's digit: the radix passes start
+// below it, in sh.hist[1] (clear: boundary() cleared it).
 template <int VPL, typename At>
 __device__ void cand_list_finish(void* raw, const float* __restrict__ lv, const int* __restrict__ lp, int m,
-                                 int rank, int n, uint64_t* __restrict__ brow, float* __restrict__ thr, At&& at) {
+                                 int rank, int bin, int n, uint64_t* __restrict__ brow, float* __restrict__ thr,
+                                 At&& at) {
   using WS = WideSelect<VPL, false>;
   auto& sh = *static_cast<typename WS::Shared*>(raw);
   WS ws;
@@ -692,7 +695,10 @@ __device__ void cand_list_finish(void* raw, const float* __restrict__ lv, const 
     off[i] = p < m ? at(p) : 0;
     ws.set(i, p < m ? ld_coherent(lv + off[i]) : 0.0f, p < m);
   }
-  ws.run(rank, sh);
+  ws.kr = rank;
+  ws.kk = rank;
+  const uint32_t prefix = static_cast<uint32_t>(bin) << (32 - kCandBits);
+  ws.passes(sh, prefix, ~((1u << (32 - kCandBits)) - 1u), 32 - kCandBits, 1, prefix, false);
   uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -845,8 +851,8 @@ __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
   float* thr = thr_out ? thr_out + row : nullptr;
   const int slice_len = kWideNT * J;
   auto at_fn = [&](int p) { return cand_list_at(pre, slices, slice_len, p); };
-  if (m <= kWideNT) cand_list_finish<1>(&sh, lv, lp, m, rank, n, brow, thr, at_fn);
-  else if (m <= 8 * kWideNT) cand_list_finish<8>(&sh, lv, lp, m, rank, n, brow, thr, at_fn);
+  if (m <= kWideNT) cand_list_finish<1>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
+  else if (m <= 8 * kWideNT) cand_list_finish<8>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
   else cand_list_finish_stream(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
 }
 
@@ -1210,6 +1216,10 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     if (tid <= n_tiles) tile_off[tid] = incl - len;   // tile_off[n_tiles] = the total
     if (tid == 63) n_fin = fin_all;
   }
+  if (cscore) {   // the candidates' first digit is counted as they arrive (cleared before the barrier)
+#pragma unroll
+    for (int j = 0; j < WC::NB / kWideNT; ++j) sh.c.hist[0][tid + kWideNT * j] = 0;
+  }
   __syncthreads();
   const int64_t o = static_cast<int64_t>(row) * n_out;
   auto emit = [&](int idx, int p, bool valid) {
@@ -1245,8 +1255,12 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
       tok[i] = ok ? trow[e] : 0;
       wc.set(i, ok ? crow[e] : 0.0f, ok);
     }
+    int ninf = 0;
+#pragma unroll
+    for (int i = 0; i < VPLC; ++i) wc.count(i, sh.c, ninf);
+    wc.count_done(sh.c, ninf);
     write_protected();
-    wc.run(keep, sh.c);
+    wc.run_counted(keep, sh.c);
     uint64_t fin = 0;
 #pragma unroll
     for (int i = 0; i < VPLC; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(wc.u[i]))) << i;
