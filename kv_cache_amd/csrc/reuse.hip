@@ -329,21 +329,26 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
   __shared__ int n_finite;
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = row / q_heads, h = row - b * q_heads;
-  for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(query + static_cast<int64_t>(row) * head_dim + d);
+  // the query's first kRT values and this thread's mask words are all in
+  // flight before any is used (a load stored to LDS at once, or a load under
+  // a branch, would wait for each in turn)
+  const E* q_row = query + static_cast<int64_t>(row) * head_dim;
+  const float q0 = Elem<DT>::load(q_row + min(tid, head_dim - 1));
 
   const int tile0 = blockIdx.x * kScoreTile;
   const int t0 = tile0 + tid * 4;
   const int64_t moff = static_cast<int64_t>(row) * mask_ld + t0;
   uint32_t bits = 0;
   if (BITS) {   // positions t0..t0+3 lie in one word; bits past the history are clear
+    const int64_t w = static_cast<int64_t>(row) * mask_ld + (min(t0, history - 1) >> 6);
+    const uint64_t* c64 = reinterpret_cast<const uint64_t*>(cur);
+    const uint64_t a = c64[w];
+    const uint64_t p = reinterpret_cast<const uint64_t*>(prev ? prev : cur)[w];
+    const uint64_t f = reinterpret_cast<const uint64_t*>(fin ? fin : cur)[w];
     if (t0 < history) {
-      const int64_t w = static_cast<int64_t>(row) * mask_ld + (t0 >> 6);
-      const int sh4 = t0 & 63;
-      uint64_t u = reinterpret_cast<const uint64_t*>(cur)[w];
-      if (prev) u |= reinterpret_cast<const uint64_t*>(prev)[w];
-      if (fin) u |= reinterpret_cast<const uint64_t*>(fin)[w];
+      const uint64_t u = a | (prev ? p : 0ull) | (fin ? f : 0ull);
       const int n = min(4, history - t0);
-      bits = static_cast<uint32_t>(u >> sh4) & ((1u << n) - 1u);
+      bits = static_cast<uint32_t>(u >> (t0 & 63)) & ((1u << n) - 1u);
     }
   } else if (mvec && t0 + 4 <= history) {
     uint32_t u = *reinterpret_cast<const uint32_t*>(cur + moff);
@@ -367,10 +372,16 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
 #pragma unroll
     for (int i = 0; i < 4; ++i) bits |= static_cast<uint32_t>(i < n && (c[i] | p[i] | f[i]) != 0) << i;
   }
+  if (tid < head_dim) q_s[tid] = q0;
+  for (int d = tid + kRT; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
   float* orow = out + static_cast<int64_t>(row) * out_ld;
   const float ninf = -__builtin_huge_valf();
-  for (int i = 0; i < 4 && t0 + i < history; ++i)
-    if (!((bits >> i) & 1u)) orow[t0 + i] = ninf;
+  if (bits == 0 && t0 + 4 <= history && ((reinterpret_cast<uintptr_t>(orow + t0) & 15) == 0)) {
+    *reinterpret_cast<float4*>(orow + t0) = make_float4(ninf, ninf, ninf, ninf);
+  } else {
+    for (int i = 0; i < 4 && t0 + i < history; ++i)
+      if (!((bits >> i) & 1u)) orow[t0 + i] = ninf;
+  }
 
   // Compaction: the tile's union tokens in index order.
   const int cnt = __popc(bits);
@@ -1165,7 +1176,10 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     typename WC::Shared c;
     AttnPartials a;
   } sh;
-  __shared__ int32_t ids_s[ATTN ? kAttnList : 1];
+  // the final list staged in LDS (n_out <= kAttnList): entry p holds the
+  // index, bitwise negated when the entry is invalid; written out coalesced
+  // after the selection instead of three scattered stores per entry
+  __shared__ int32_t ids_s[kAttnList];
   __shared__ int tile_off[kMaxTiles + 1];
   __shared__ int n_fin;
   __shared__ uint64_t fin_s[BITS ? kWideMax / 64 : 1];
@@ -1222,16 +1236,20 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   }
   __syncthreads();
   const int64_t o = static_cast<int64_t>(row) * n_out;
+  const bool staged = ATTN || n_out <= kAttnList;   // uniform
   auto emit = [&](int idx, int p, bool valid) {
     if (valid) {
       if constexpr (BITS) atomicOr(&fin_s[idx >> 6], 1ull << (idx & 63));
       else hrow[idx] = 1;
     }
     const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
-    final_idx[o + p] = idx;
-    final_valid[o + p] = fv;
-    if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
-    if constexpr (ATTN) ids_s[p] = fv ? idx : -1;
+    if (staged) {
+      ids_s[p] = fv ? idx : ~idx;
+    } else {
+      final_idx[o + p] = idx;
+      final_valid[o + p] = fv;
+      if (attn_ids) attn_ids[o + p] = fv ? idx : -1;
+    }
   };
   const int total = tile_off[n_tiles];
   if (cscore && n_fin >= keep && total <= VPLC * kWideNT) {   // uniform across the workgroup
@@ -1264,7 +1282,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     uint64_t fin = 0;
 #pragma unroll
     for (int i = 0; i < VPLC; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(wc.u[i]))) << i;
-    wc.place(sh.c, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
+    wc.place_uniform(sh.c, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
   } else {
     WS ws;
     ws.load_count(scores + static_cast<int64_t>(row) * scores_ld, history, sh.d);   // first digit counted on load
@@ -1278,12 +1296,23 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   const int extra = sink_end + n_rec + keep_self;
   for (int i = tid; i < extra; i += kWideNT) {
     const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
-    final_idx[o + keep + i] = idx;
-    final_valid[o + keep + i] = 1;
-    if (attn_ids) attn_ids[o + keep + i] = idx;
-    if constexpr (ATTN) ids_s[keep + i] = idx;
+    if (staged) {
+      ids_s[keep + i] = idx;
+    } else {
+      final_idx[o + keep + i] = idx;
+      final_valid[o + keep + i] = 1;
+      if (attn_ids) attn_ids[o + keep + i] = idx;
+    }
   }
-  if constexpr (BITS || ATTN) __syncthreads();   // every emit is done (the selection's LDS is free)
+  if (BITS || staged) __syncthreads();   // every emit is done (the selection's LDS is free)
+  if (staged) {
+    for (int p = tid; p < n_out; p += kWideNT) {
+      const int v = ids_s[p];
+      final_idx[o + p] = v >= 0 ? v : ~v;
+      final_valid[o + p] = v >= 0;
+      if (attn_ids) attn_ids[o + p] = v >= 0 ? v : -1;
+    }
+  }
   if constexpr (BITS) {
     uint64_t* hw = reinterpret_cast<uint64_t*>(hrow);
     for (int j = tid; j < n_words; j += kWideNT) hw[j] = fin_s[j];

@@ -633,6 +633,49 @@ struct WideSelect {
     return kk;
   }
 
+  // place() for few keys per thread: one uniform pass over the slots with a
+  // ballot per slot instead of each thread walking its own candidates
+  // through LDS records (the walk is a chain of dependent LDS reads per
+  // candidate; a slot's taken keys here cost two ballots and two bit
+  // counts).  The same output indices.  Ends with a barrier.
+  template <typename Emit>
+  __device__ void place_uniform(Shared& sh, Emit&& emit) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    refresh();
+    uint64_t bg[VPL], be[VPL];
+    int cg = 0, ce = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      bg[i] = __ballot(on(i) && u[i] > theta);
+      be[i] = __ballot(on(i) && u[i] == theta);
+      cg += __popcll(bg[i]);
+      ce += __popcll(be[i]);
+    }
+    if (lane == 0) {
+      sh.wave_gt[wave] = cg;
+      sh.wave_eq[wave] = ce;
+    }
+    __syncthreads();
+    int g = 0, e = 0;   // keys of the earlier waves
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      g += w < wave ? sh.wave_gt[w] : 0;
+      e += w < wave ? sh.wave_eq[w] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int gl = g + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bg[i] >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bg[i]), 0)));
+      const int el = e + static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(be[i] >> 32),
+                                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(be[i]), 0)));
+      const bool gt = (bg[i] >> lane) & 1ull, eq = (be[i] >> lane) & 1ull;
+      if (gt || (eq && el < kr)) emit(pos(i), gl + min(el, kr), i);
+      g += __popcll(bg[i]);
+      e += __popcll(be[i]);
+    }
+    __syncthreads();
+  }
+
   // Calls emit(position, output index, slot) for every taken key, output
   // indices 0..kk-1 in ascending position order: a taken key's index is the
   // number of keys above theta before it plus min(keys equal to theta before
