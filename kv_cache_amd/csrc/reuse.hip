@@ -1635,7 +1635,13 @@ struct CandSplit {
 };
 
 // reuse_cand_slices_kernel over rows x slices workgroups: J scores per
-// thread, about 512 workgroups (J 1..8).
+// thread, the smallest J that keeps the grid within QKV_CAND_TARGET_WGS
+// workgroups.  Measured at 32 rows x 32792 scores (graph step, us/layer):
+// 288 workgroups of J = 4 51.6, 160 of J = 8 50.3-50.8, 96 of J = 16 52.0,
+// 64 of J = 32 56.0.
+#ifndef QKV_CAND_TARGET_WGS
+#define QKV_CAND_TARGET_WGS 256
+#endif
 int launch_cand_slices(const char* what, const float* values, int64_t ld, int64_t rows, int64_t n, int64_t k,
                        const CandSplit& cs, uint64_t* bits, int64_t bits_ld, float* thr_out, hipStream_t st) {
   auto launch = [&](auto jc) {
@@ -1647,10 +1653,12 @@ int launch_cand_slices(const char* what, const float* values, int64_t ld, int64_
     return check_launch(what);
   };
   auto wgs = [&](int64_t j) { return rows * cdiv(n, int64_t(kWideNT) * j); };
-  if (wgs(1) <= 512) return launch(std::integral_constant<int, 1>{});
-  if (wgs(2) <= 512) return launch(std::integral_constant<int, 2>{});
-  if (wgs(4) <= 512) return launch(std::integral_constant<int, 4>{});
-  return launch(std::integral_constant<int, 8>{});
+  if (wgs(1) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 1>{});
+  if (wgs(2) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 2>{});
+  if (wgs(4) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 4>{});
+  if (wgs(8) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 8>{});
+  if (wgs(16) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 16>{});
+  return launch(std::integral_constant<int, 32>{});
 }
 
 template <int DT> struct RunCandidates {
