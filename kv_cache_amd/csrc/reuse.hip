@@ -30,7 +30,13 @@ namespace qkv {
 namespace {
 
 constexpr int kRT = 256;          // threads per workgroup
-constexpr int kScoreTile = 1024;  // tokens per workgroup in reuse_scores_kernel
+// Measured at 32 rows x 32792 tokens (graph step, us/layer): tiles of 512
+// 50.7, 1024 50.8, 2048 51.7, 4096 58.0 (one thread per union token).
+#ifndef QKV_SCORE_TILE
+#define QKV_SCORE_TILE 1024
+#endif
+constexpr int kScoreTile = QKV_SCORE_TILE;   // tokens per workgroup in reuse_scores_kernel
+constexpr int kScoreNT = kScoreTile / 4;     // its threads (four positions each)
 constexpr int kMaskTile = 4096;   // tokens per workgroup in reuse_mask_kernel
 
 // ---------------------------------------------------------------------------
@@ -43,9 +49,14 @@ constexpr int kMaskTile = 4096;   // tokens per workgroup in reuse_mask_kernel
 // one global atomic per non-empty bin.
 // ---------------------------------------------------------------------------
 constexpr int kCandBits = 12, kCandBins = 1 << kCandBits;
+// (256, 512 and 1024 threads measured within 0.3 us/layer of each other.)
+#ifndef QKV_PARTIAL_NT
+#define QKV_PARTIAL_NT 256
+#endif
+constexpr int kPartNT = QKV_PARTIAL_NT;   // threads per workgroup (8 tokens each)
 
 template <int DT, bool HIST = false>
-__global__ __launch_bounds__(kRT) void reuse_partial_kernel(
+__global__ __launch_bounds__(kPartNT) void reuse_partial_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ kdm,
     int q_heads, int group, int history, int head_dim, int count, int64_t sb, int64_t sh, int64_t sd,
     bool vec, float* __restrict__ out, int64_t out_ld, const uint8_t* __restrict__ gate, int gate_refresh,
@@ -54,7 +65,7 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
   __shared__ int hist_s[HIST ? kCandBins : 1];
   if constexpr (HIST) {
 #pragma unroll
-    for (int j = 0; j < kCandBins / kRT; ++j) hist_s[threadIdx.x + kRT * j] = 0;   // (a barrier follows)
+    for (int j = 0; j < kCandBins / kPartNT; ++j) hist_s[threadIdx.x + kPartNT * j] = 0;   // (a barrier follows)
   }
   __shared__ float q_s[512];
   __shared__ __attribute__((aligned(16))) uint64_t key_s[128];
@@ -62,23 +73,23 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
   __shared__ float sel_q[kMaxDims];
   const int row = blockIdx.y, tid = threadIdx.x;
   if (gate) {   // a lagged step: rows that keep no new candidates are skipped (uniform)
-    __shared__ int gate_cnt[kRT / 64];
+    __shared__ int gate_cnt[kPartNT / 64];
     if (!lag_refreshes(gate, gate_refresh, gate_rows, row, gate_cnt)) return;
   }
   const int b = row / q_heads, h = row - b * q_heads;
   const typename Elem<DT>::T* q_row = query + static_cast<int64_t>(row) * head_dim;
-  for (int d = tid; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
+  for (int d = tid; d < head_dim; d += kPartNT) q_s[d] = Elem<DT>::load(q_row + d);
   __syncthreads();
   if (head_dim <= 128) {   // uniform
     rank_dims128(q_s, key_s, head_dim, count, sel_idx, sel_q);
   } else {
-    for (int s = tid; s < count; s += kRT) {   // valid even for a NaN query
+    for (int s = tid; s < count; s += kPartNT) {   // valid even for a NaN query
       sel_idx[s] = 0;
       sel_q[s] = q_s[0];
     }
     __syncthreads();
     // rank(d) = #{e : |q_e| > |q_d| or (|q_e| == |q_d| and e < d)} (QK:123-145)
-    for (int d = tid; d < head_dim; d += kRT) {
+    for (int d = tid; d < head_dim; d += kPartNT) {
       const float a = fabsf(q_s[d]);
       int rank = 0;
       for (int e = 0; e < head_dim; ++e) {
@@ -92,7 +103,7 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     }
     __syncthreads();
   }
-  const int t0 = (blockIdx.x * kRT + tid) * 8;
+  const int t0 = (blockIdx.x * kPartNT + tid) * 8;
   if (!HIST && t0 >= history) return;
   const int nt = max(min(8, history - t0), 0);   // this thread's tokens
   const E* base = kdm + b * sb + (h / group) * sh + min(t0, history - 1);
@@ -154,9 +165,9 @@ __global__ __launch_bounds__(kRT) void reuse_partial_kernel(
     __syncthreads();
     int* hrow = hist + static_cast<int64_t>(row) * kCandBins;
 #pragma unroll
-    for (int j = 0; j < kCandBins / kRT; ++j) {
-      const int c = hist_s[tid + kRT * j];
-      if (c) __hip_atomic_fetch_add(hrow + tid + kRT * j, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int j = 0; j < kCandBins / kPartNT; ++j) {
+      const int c = hist_s[tid + kPartNT * j];
+      if (c) __hip_atomic_fetch_add(hrow + tid + kPartNT * j, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -316,7 +327,7 @@ __global__ __launch_bounds__(kRT) void sample_mask_kernel(const float* __restric
 // in words) instead of byte masks.
 // ---------------------------------------------------------------------------
 template <int DT, int DFIX, bool BITS>
-__global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void reuse_scores_kernel(
+__global__ __launch_bounds__(kScoreNT) __attribute__((amdgpu_waves_per_eu(5))) void reuse_scores_kernel(
     const typename Elem<DT>::T* __restrict__ query, const typename Elem<DT>::T* __restrict__ key,
     int q_heads, int group, int history, int head_dim, int64_t sb, int64_t sh, int64_t st, bool kvec,
     const uint8_t* __restrict__ cur, const uint8_t* __restrict__ prev, const uint8_t* __restrict__ fin,
@@ -325,11 +336,11 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
   using E = typename Elem<DT>::T;
   __shared__ __attribute__((aligned(16))) float q_s[512];
   __shared__ uint16_t list[kScoreTile];
-  __shared__ int wave_tot[kRT / 64];
+  __shared__ int wave_tot[kScoreNT / 64];
   __shared__ int n_finite;
   const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = row / q_heads, h = row - b * q_heads;
-  // the query's first kRT values and this thread's mask words are all in
+  // the query's first kScoreNT values and this thread's mask words are all in
   // flight before any is used (a load stored to LDS at once, or a load under
   // a branch, would wait for each in turn)
   const E* q_row = query + static_cast<int64_t>(row) * head_dim;
@@ -373,7 +384,7 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
     for (int i = 0; i < 4; ++i) bits |= static_cast<uint32_t>(i < n && (c[i] | p[i] | f[i]) != 0) << i;
   }
   if (tid < head_dim) q_s[tid] = q0;
-  for (int d = tid + kRT; d < head_dim; d += kRT) q_s[d] = Elem<DT>::load(q_row + d);
+  for (int d = tid + kScoreNT; d < head_dim; d += kScoreNT) q_s[d] = Elem<DT>::load(q_row + d);
   float* orow = out + static_cast<int64_t>(row) * out_ld;
   const float ninf = -__builtin_huge_valf();
   if (bits == 0 && t0 + 4 <= history && ((reinterpret_cast<uintptr_t>(orow + t0) & 15) == 0)) {
@@ -394,7 +405,9 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
     if ((bits >> i) & 1u) list[base++] = static_cast<uint16_t>(tid * 4 + i);
   if (tid == 0) n_finite = 0;
   __syncthreads();
-  const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < kScoreNT / 64; ++w) total += wave_tot[w];
 
   // cscore (optional): the tile's union scores again, compacted at the
   // tile's offset, with their tokens and (list length, finite scores) per
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(kRT) __attribute__((amdgpu_waves_per_eu(5))) void r
   int32_t* trow = cscore ? ctok + static_cast<int64_t>(row) * c_ld + tile0 : nullptr;
   int n_fin_own = 0;
   const E* kbase = key + b * sb + (h / group) * sh;
-  for (int i = tid; i < total; i += kRT) {
+  for (int i = tid; i < total; i += kScoreNT) {
     const int t = tile0 + list[i];
     const E* kr = kbase + static_cast<int64_t>(t) * st;
     float acc = 0.0f;
@@ -1037,7 +1050,9 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 // either way, and the lists keep token order, so both paths select and
 // place the same entries (ties to the lower token).
 constexpr int kMaxTiles = kWideMax / kScoreTile;
-static_assert(kMaxTiles < 64, "the final selection's tile search takes six steps");
+constexpr int kTilesPL = (kMaxTiles + 1 + 63) / 64;   // tiles per lane in the offset scan (and the end)
+constexpr int kTileStep0 = kMaxTiles >= 64 ? 64 : 32;   // the tile search's first step
+static_assert(kMaxTiles < 128, "the final selection's tile search takes seven steps");
 
 // The token attention of one row (a query head) over its final list, by the
 // workgroup that selected it (reuse_final_wide_kernel with ATTN): softmax(
@@ -1186,13 +1201,19 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   const int row = blockIdx.x, tid = threadIdx.x;
   uint8_t* hrow = hf + static_cast<int64_t>(row) * hf_ld * (BITS ? 8 : 1);
   const int n_words = (history + 63) / 64;
-  // the tile lists' lengths first (one load per tile, n_tiles <= 40), in
-  // flight while the protected ranges are written
-  int len = 0, nf = 0;
-  if (tid < 64 && cscore && tid < n_tiles) {
+  // the tile lists' lengths first (kTilesPL consecutive tiles per lane of
+  // wave 0), in flight while the protected ranges are written
+  int len[kTilesPL] = {}, nf = 0;
+  if (tid < 64 && cscore) {
     const int32_t* cn = ccnt + static_cast<int64_t>(row) * n_tiles * 2;
-    len = cn[2 * tid];
-    nf = cn[2 * tid + 1];
+#pragma unroll
+    for (int j = 0; j < kTilesPL; ++j) {
+      const int t = tid * kTilesPL + j;
+      if (t < n_tiles) {
+        len[j] = cn[2 * t];
+        nf += cn[2 * t + 1];
+      }
+    }
   }
   // the protected ranges, 16 bytes per store where the row is 16-byte aligned;
   // written after the selection's loads are out, and ordered before the
@@ -1226,8 +1247,17 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     for (int t = body + tid; t < history; t += kWideNT) hrow[t] = (t < sink_end) || (t >= recent_start);
   };
   if (tid < 64) {   // tile list offsets: a wave scan of the lengths
-    const int incl = wave_incl_scan_dpp(len), fin_all = wave_incl_scan_dpp(nf);
-    if (tid <= n_tiles) tile_off[tid] = incl - len;   // tile_off[n_tiles] = the total
+    int own = 0;
+#pragma unroll
+    for (int j = 0; j < kTilesPL; ++j) own += len[j];
+    const int incl = wave_incl_scan_dpp(own), fin_all = wave_incl_scan_dpp(nf);
+    int at = incl - own;
+#pragma unroll
+    for (int j = 0; j < kTilesPL; ++j) {
+      const int t = tid * kTilesPL + j;
+      if (t <= n_tiles) tile_off[t] = at;   // tile_off[n_tiles] = the total
+      at += len[j];
+    }
     if (tid == 63) n_fin = fin_all;
   }
   if (cscore) {   // the candidates' first digit is counted as they arrive (cleared before the barrier)
@@ -1261,11 +1291,11 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     for (int i = 0; i < VPLC; ++i) {
       const int p = WC::pos(i);
       const bool ok = p < total;
-      // the last tile whose list starts at or before p, in six fixed steps
+      // the last tile whose list starts at or before p, in fixed steps
       // (so the VPLC searches interleave instead of running one by one)
       int lo = 0;
 #pragma unroll
-      for (int step = 32; step > 0; step >>= 1) {
+      for (int step = kTileStep0; step > 0; step >>= 1) {
         const int mid = lo + step;
         lo = (mid < n_tiles && tile_off[min(mid, n_tiles)] <= p) ? mid : lo;
       }
@@ -1517,9 +1547,9 @@ template <int DT> struct RunReusePartial {
     using E = typename Elem<DT>::T;
     const int64_t ev = DT == QKV_DTYPE_FP32 ? 4 : 8;   // elements per 16 bytes
     const bool vec = aligned(kdm, 16) && ks[0] % ev == 0 && ks[1] % ev == 0 && ks[2] % ev == 0;
-    dim3 grid(static_cast<unsigned>(cdiv(T, 8 * kRT)), static_cast<unsigned>(B * Hq));
+    dim3 grid(static_cast<unsigned>(cdiv(T, 8 * kPartNT)), static_cast<unsigned>(B * Hq));
 #define QKV_REUSE_PARTIAL(HH)                                                                                  \
-  reuse_partial_kernel<DT, HH><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),     \
+  reuse_partial_kernel<DT, HH><<<grid, kPartNT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(kdm),     \
                                                      static_cast<int>(Hq), static_cast<int>(Hq / Hkv),         \
                                                      static_cast<int>(T), static_cast<int>(D), count, ks[0],   \
                                                      ks[1], ks[2], vec, out, out_ld, gate, gate_refresh,       \
@@ -1544,7 +1574,7 @@ template <int DT> struct RunReuseScores {
     dim3 grid(static_cast<unsigned>(cdiv(T, kScoreTile)), static_cast<unsigned>(B * Hq));
     if (ks[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "qkv_reuse_select: K channels must be contiguous");
 #define QKV_REUSE_SCORES(DF, BB)                                                                               \
-  reuse_scores_kernel<DT, DF, BB><<<grid, kRT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),    \
+  reuse_scores_kernel<DT, DF, BB><<<grid, kScoreNT, 0, st>>>(static_cast<const E*>(q), static_cast<const E*>(k),    \
                                                         static_cast<int>(Hq), static_cast<int>(Hq / Hkv),      \
                                                         static_cast<int>(T), static_cast<int>(D), ks[0], ks[1], \
                                                         ks[2], kvec, cur, prev, fin, mask_ld, mvec, scaling, out, \
