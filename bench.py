@@ -346,6 +346,12 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
         for _ in range(layers):
             K.block_topk(step.bmax, cfg.topk, out=step.sel, workspace=step.topk_ws)
 
+    def run_decode_topk():   # the step's token selection: scoring that also builds the top-k's chunk windows
+        for layer in range(layers):
+            c = caches[layer]
+            K.decode_topk(qs[layer], c.chan_idx, c.slab, c.slab_scales, T, cfg.topk, scores=step.bmax,
+                          out=step.sel, workspace=step.topk_ws)
+
     def run_attn():
         for layer in range(layers):
             K.sparse_attention(qs[layer], ks[layer], vs[layer], step.sel, cfg.block, T, cfg.scaling,
@@ -394,6 +400,9 @@ def run_decode(args, name: str, layers: int | None = None, with_cpu: bool = True
         ("sparse_attention", run_attn, rows * sel_tokens * cfg.head_dim * 2 * 2),
         ("dense_bf16_attention", run_dense, rows * T * cfg.head_dim * 2 * 2),
     ]
+    if not step.fused and cfg.block == 1:   # scores written and read back once more by the top-k
+        plan.insert(2, ("int4_decode_topk", run_decode_topk,
+                        keys_per_layer * cfg.slab_bytes_per_key() + rows * cfg.n_blocks * 4 * 2))
     if step.fused:   # the step's own second launch: selection inside the attention kernel
         plan.insert(3, ("select_sparse_attention", run_select_attn,
                         rows * (cfg.n_blocks * 4 + sel_tokens * cfg.head_dim * 2 * 2)))

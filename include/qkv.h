@@ -220,6 +220,20 @@ int64_t qkv_topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Token-level decode selection in one call: qkv_int4_decode_scores with
+ * block 1 into scores f32 [batch * kv_heads, tokens], then qkv_topk_ws over
+ * those rows into out int32 [rows, k] (the same result as the two calls).
+ * workspace: qkv_topk_workspace_bytes(rows, tokens, k) bytes, 16-byte
+ * aligned, contents irrelevant.  Where qkv_topk_ws takes its
+ * histogram-and-filter path, the scoring launch (one workgroup per
+ * 4096-token chunk) also builds each chunk's histogram window, so the top-k
+ * starts at the row's floor.  Replaces the reference's partial scores plus
+ * torch.topk at EV:5038-5046 for block 1 (no counterpart as one call). */
+int qkv_int4_decode_topk(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                         const int32_t* chan_idx, int64_t selected, const uint8_t* slab,
+                         const uint16_t* slab_scales, int64_t capacity, int64_t tokens, int64_t k, float* scores,
+                         int32_t* out, void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+
 /* No counterpart in the reference; for tests of qkv_topk_ws's one-launch
  * path.  Sets how long (ticks of the 100 MHz real-time clock) a chunk waits
  * for the other chunks of its row before keeping its exact top-k instead of

@@ -15,6 +15,7 @@
 #include "common.h"
 
 #include "score.h"
+#include "window.h"
 
 #ifndef QKV_SCORE_TARGET_WGS
 #define QKV_SCORE_TARGET_WGS 4096
@@ -268,6 +269,39 @@ int launch_scores(int S, dim3 grid, hipStream_t st, const uint16_t* q, int hq, i
   return check_launch("qkv_int4_decode_scores");
 }
 
+// Decode scoring of qkv_int4_decode_topk: token scores (block 1), one
+// workgroup per 4096-key chunk of the long-row top-k, each key also counted
+// in the chunk's 12-bit histogram in LDS, and the chunk's top-k window
+// (chunk_window) written where qkv_topk_ws's histogram pass would write it.
+// win_waves: the chunk's waves, every wave stage one whole slab tile.
+constexpr int win_waves(int s) {
+  return kStageChunk / slab_tile_keys(s) >= 16 ? 16 : static_cast<int>(kStageChunk / slab_tile_keys(s));
+}
+
+template <int S, bool F16>
+__global__ __launch_bounds__(64 * win_waves(S)) void decode_scores_win_kernel(
+    const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
+    const int32_t* __restrict__ chan_idx, const uint8_t* __restrict__ slab,
+    const uint16_t* __restrict__ slab_scales, int64_t capacity, int tokens, int k, float* __restrict__ scores,
+    int n_chunks, int32_t* __restrict__ win, float* __restrict__ qscale_out) {
+  constexpr int NWV = win_waves(S), NT = 64 * NWV;
+  static_assert(kStageChunk % (NWV * slab_tile_keys(S)) == 0, "a chunk is whole workgroup stages");
+  __shared__ uint32_t h[kHistBins];
+  __shared__ int wsum[NWV];
+  __shared__ int t_sh;
+#pragma unroll
+  for (int i = 0; i < kHistBins / NT; ++i) h[threadIdx.x + NT * i] = 0;
+  if (threadIdx.x == 0) t_sh = 0;
+  __syncthreads();
+  score_chunk<S, false, F16, NWV>(query, q_heads, kv_heads, head_dim, chan_idx, slab, slab_scales, capacity, tokens,
+                                  1, kStageChunk, scores, tokens, nullptr, nullptr, qscale_out, blockIdx.y,
+                                  blockIdx.x, h);
+  __syncthreads();
+  const int len = min(kStageChunk, tokens - static_cast<int>(blockIdx.x) * kStageChunk);
+  chunk_window<NT, false>(h, min(k, len), win + (static_cast<int64_t>(blockIdx.y) * n_chunks + blockIdx.x) * kWinWords,
+                          wsum, &t_sh);
+}
+
 bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 }  // namespace
@@ -478,4 +512,69 @@ QKV_EXPORT int qkv_int4_decode_scores(const void* query, int64_t batch, int64_t 
   if (f16) QKV_SC(false, true, nullptr, nullptr);
   QKV_SC(false, false, nullptr, nullptr);
 #undef QKV_SC
+}
+
+namespace qkv {
+int topk_filtered(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
+                  void* workspace, hipStream_t st, bool given);
+bool topk_takes_windows(int64_t n, int64_t k);
+}  // namespace qkv
+
+QKV_EXPORT int qkv_int4_decode_topk(const void* query, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                    int64_t head_dim, const int32_t* chan_idx, int64_t selected,
+                                    const uint8_t* slab, const uint16_t* slab_scales, int64_t capacity,
+                                    int64_t tokens, int64_t k, float* scores, int32_t* out, void* workspace,
+                                    int64_t workspace_bytes, int dtype, void* stream) {
+  static const char* what = "qkv_int4_decode_topk";
+  if (int rc = check_query(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected, what)) return rc;
+  bool f16;
+  if (int rc = half_dtype(dtype, what, &f16)) return rc;
+  if (!slab || !slab_scales || !scores || !out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (tokens <= 0 || tokens > capacity || tokens >= (int64_t(1) << 30))
+    return fail(QKV_ERR_INVALID, "%s: need 1 <= tokens <= capacity", what);
+  if (k < 1 || k > tokens) return fail(QKV_ERR_INVALID, "%s: need 1 <= k <= tokens", what);
+  if (!aligned(slab, 16) || !aligned(slab_scales, 16))
+    return fail(QKV_ERR_INVALID, "%s: slab and scales must be 16-byte aligned", what);
+  if (capacity % slab_tile_keys(static_cast<int>(selected)))
+    return fail(QKV_ERR_INVALID, "%s: capacity must be a multiple of %lld for %lld channels", what,
+                (long long)slab_tile_keys(static_cast<int>(selected)), (long long)selected);
+  const int64_t rows = batch * kv_heads;
+  const int64_t need = qkv_topk_workspace_bytes(rows, tokens, k);
+  if (need < 0 || workspace_bytes < need || (need > 0 && !workspace))
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  if (need > 0 && !aligned(workspace, 16)) return fail(QKV_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
+  if (!topk_takes_windows(tokens, k) || rows > 65535) {   // the scores, then qkv_topk_ws as it stands
+    if (int rc = qkv_int4_decode_scores(query, batch, q_heads, kv_heads, head_dim, chan_idx, selected, slab,
+                                        slab_scales, capacity, tokens, 1, scores, nullptr, nullptr, nullptr, dtype,
+                                        stream))
+      return rc;
+    return qkv_topk_ws(scores, rows, tokens, tokens, k, out, workspace, workspace_bytes, stream);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int n_chunks = static_cast<int>(cdiv(tokens, kStageChunk));
+  dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(rows));
+  const uint16_t* q = static_cast<const uint16_t*>(query);
+  int32_t* win = static_cast<int32_t*>(workspace);   // qkv_topk_ws's window region
+  auto launch = [&](auto sc, auto fc) {
+    constexpr int SS = decltype(sc)::value;
+    constexpr bool FF = decltype(fc)::value;
+    decode_scores_win_kernel<SS, FF><<<grid, 64 * win_waves(SS), 0, st>>>(
+        q, static_cast<int>(q_heads), static_cast<int>(kv_heads), static_cast<int>(head_dim), chan_idx, slab,
+        slab_scales, capacity, static_cast<int>(tokens), static_cast<int>(k), scores, n_chunks, win, nullptr);
+    return check_launch(what);
+  };
+  auto with_f = [&](auto sc) {
+    return f16 ? launch(sc, std::true_type{}) : launch(sc, std::false_type{});
+  };
+  int rc;
+  switch (selected) {
+    case 16: rc = with_f(std::integral_constant<int, 16>{}); break;
+    case 32: rc = with_f(std::integral_constant<int, 32>{}); break;
+    case 64: rc = with_f(std::integral_constant<int, 64>{}); break;
+    case 128: rc = with_f(std::integral_constant<int, 128>{}); break;
+    default: return fail(QKV_ERR_UNSUPPORTED, "%s: selected channel count %lld not built", what, (long long)selected);
+  }
+  if (rc) return rc;
+  return topk_filtered(scores, rows, tokens, tokens, k, out, workspace, st, true);
 }

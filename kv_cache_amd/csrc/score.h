@@ -194,13 +194,15 @@ __device__ __forceinline__ void row_query_finish(const RowQueryLoads<S>& L, cons
 // Scores chunk `bx` of row r (keys [bx*chunk, min(tokens, (bx+1)*chunk)))
 // in one workgroup of kScoreWaves waves, writing its block maxima to bmax
 // and, with DEBUG, every key's int32 sum and fp32 key.
-template <int S, bool DEBUG, bool F16>
+// NWV: the workgroup's waves.  hist (optional, LDS, 4096 bins): every key of
+// the chunk is also counted at its top 12 order-preserving bits.
+template <int S, bool DEBUG, bool F16, int NWV = kScoreWaves>
 __device__ __forceinline__ void score_chunk(
     const uint16_t* __restrict__ query, int q_heads, int kv_heads, int head_dim,
     const int32_t* __restrict__ chan_idx, const uint8_t* __restrict__ slab,
     const uint16_t* __restrict__ slab_scales, int64_t capacity, int tokens, int block,
     int chunk, float* __restrict__ bmax, int nb, int32_t* __restrict__ isum,
-    float* __restrict__ keys_out, float* __restrict__ qscale_out, int r, int bx) {
+    float* __restrict__ keys_out, float* __restrict__ qscale_out, int r, int bx, uint32_t* hist = nullptr) {
   constexpr int KPLN = 128 / S;                        // keys per lane per stage
   constexpr int STAGE = static_cast<int>(slab_tile_keys(S));   // keys per wave stage = 64 * KPLN
   constexpr int DW = S / 8;                            // code dwords per key
@@ -222,8 +224,8 @@ __device__ __forceinline__ void score_chunk(
   const int t_lo = bx * chunk;
   const int t_hi = min(tokens, t_lo + chunk);
 
-  // A wave's stages start at t_lo + wave*STAGE and step by kScoreWaves*STAGE;
-  // t_lo is a multiple of kScoreWaves*STAGE, so every stage is one whole tile.  A stage with
+  // A wave's stages start at t_lo + wave*STAGE and step by NWV*STAGE;
+  // t_lo is a multiple of NWV*STAGE, so every stage is one whole tile.  A stage with
   // tb < t_hi <= tokens <= capacity lies inside the row's slab and scales
   // (capacity is a multiple of STAGE), so its loads need no per-lane guard:
   // lanes past t_hi read padding that score_stage masks to -inf.  Loads
@@ -238,7 +240,7 @@ __device__ __forceinline__ void score_chunk(
 
   int tb = t_lo + wave * STAGE;
   if (tb >= t_hi) return;   // wave-uniform; the chunk's waves share no barrier
-  const int nst = (t_hi - tb + kScoreWaves * STAGE - 1) / (kScoreWaves * STAGE);   // stages of this wave
+  const int nst = (t_hi - tb + NWV * STAGE - 1) / (NWV * STAGE);   // stages of this wave
   uint4 cw[4];
   LS sv;
   load_stage(tb, cw, sv);
@@ -275,6 +277,7 @@ __device__ __forceinline__ void score_chunk(
       // take no part: blocks never straddle chunks, which are whole stages.
       const int t = k0 + e;
       if (t >= t_hi) kf = ninf;
+      else if (hist) atomicAdd(&hist[f32_sortable(kf) >> 20], 1u);
       key[e] = kf;
       if (DEBUG && t < t_hi) {
         isum[static_cast<int64_t>(r) * tokens + t] = isc;
@@ -303,7 +306,7 @@ __device__ __forceinline__ void score_chunk(
 
   // Each wave walks its stages with the next stage's loads in flight.
   for (int i = 1; i < nst; ++i) {
-    const int tn = tb + kScoreWaves * STAGE;
+    const int tn = tb + NWV * STAGE;
     uint4 nw[4];
     LS nsv;
     load_stage(tn, nw, nsv);

@@ -14,6 +14,7 @@
 
 #include "common.h"
 #include "select.h"
+#include "window.h"
 
 namespace qkv {
 namespace {
@@ -528,7 +529,6 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const float* __restrict_
 // take-all path, and a chunk with fewer than k writes -inf after them (below
 // the floor whenever a chunk can run short).
 // ---------------------------------------------------------------------------
-constexpr int kStageChunk = 4096;
 constexpr int kStageMaxK = 1024;
 
 __global__ __launch_bounds__(256) void topk_stage_kernel(const float* __restrict__ in_val,
@@ -634,18 +634,13 @@ __global__ __launch_bounds__(1024) void topk_wide_final_kernel(const float* __re
 constexpr int kFilterMaxChunks = 64;
 constexpr int kFilterMaxLists = 32 * 1024;   // list slots per row (chunks * k): 32 keys per thread
 constexpr int kFilterVPL = kStageChunk / 256;   // keys per thread of a chunk
-constexpr int kHistBits = 12, kHistBins = 1 << kHistBits;
-constexpr int kWin = 64;                     // window bins per chunk
-constexpr int kWinWords = kWin + 2;          // t_c, the count above the window, the window
 
 __global__ __launch_bounds__(256) void topk_hist_kernel(const float* __restrict__ values, int64_t ld, int n, int k,
                                                         int n_chunks, int32_t* __restrict__ win) {
-  constexpr int BPT = kHistBins / 256;   // bins per thread: thread t holds bins [4096 - 16(t+1), 4096 - 16t)
   __shared__ uint32_t h[kHistBins];
   __shared__ int wave_sum[4];
   __shared__ int t_sh;
   const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int i = tid; i < kHistBins; i += 256) h[i] = 0;
   if (tid == 0) t_sh = 0;
   __syncthreads();
@@ -659,46 +654,8 @@ __global__ __launch_bounds__(256) void topk_hist_kernel(const float* __restrict_
   for (int i = 0; i < kFilterVPL; ++i)
     if (tid * kFilterVPL + i < len) atomicAdd(&h[key[i] >> (32 - kHistBits)], 1u);
   __syncthreads();
-  // t_c: where the count from the top reaches min(k, len)
-  const int target = min(k, len);
-  const int b0 = kHistBins - BPT * (tid + 1);
-  int hb[BPT], cnt = 0;
-#pragma unroll
-  for (int i = 0; i < BPT; ++i) {
-    hb[i] = static_cast<int>(h[b0 + i]);
-    cnt += hb[i];
-  }
-  const int incl = wave_incl_scan_dpp(cnt);
-  if (lane == 63) wave_sum[wave] = incl;
-  __syncthreads();
-  int above = incl - cnt;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) above += w < wave ? wave_sum[w] : 0;
-  if (above < target && above + cnt >= target) {   // one thread
-    int t = b0;
-#pragma unroll
-    for (int i = BPT - 1; i >= 0; --i) {
-      if (above < target && above + hb[i] >= target) t = b0 + i;
-      above += hb[i];
-    }
-    t_sh = t;
-  }
-  __syncthreads();
-  const int t = t_sh;
-  int32_t* w = win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords;
-  if (tid < kWin) w[2 + tid] = t + tid < kHistBins ? static_cast<int32_t>(h[t + tid]) : 0;
-  // the keys above the window: this thread's bins from t + kWin up, summed over the workgroup
-  int over = 0;
-#pragma unroll
-  for (int i = 0; i < BPT; ++i) over += b0 + i >= t + kWin ? hb[i] : 0;
-  over = wave_incl_scan_dpp(over);
-  __syncthreads();   // wave_sum is reused
-  if (lane == 63) wave_sum[wave] = over;
-  __syncthreads();
-  if (tid == 0) {
-    w[0] = t;
-    w[1] = wave_sum[0] + wave_sum[1] + wave_sum[2] + wave_sum[3];
-  }
+  chunk_window<256, false>(h, min(k, len), win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords, wave_sum,
+                           &t_sh);
 }
 
 __global__ __launch_bounds__(256) void topk_filter_kernel(const float* __restrict__ values, int64_t ld, int n, int k,
@@ -926,11 +883,14 @@ constexpr int kTicketSlots = 4096;
 constexpr int64_t kSpinTicks = 1 << 17;           // ~1.3 ms of the 100 MHz real-time clock
 int64_t g_spin_ticks = kSpinTicks;                // qkv_topk_set_wait_limit
 
+// given: the windows are in win already (written by an earlier launch, such
+// as the decode scoring of qkv_int4_decode_topk): a and b are skipped.
 __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restrict__ values, int64_t ld, int n,
                                                           int k, int n_chunks, uint64_t spin_ticks,
                                                           uint32_t* __restrict__ tickets, int32_t* __restrict__ win,
                                                           float* __restrict__ lval, int32_t* __restrict__ lidx,
-                                                          int32_t* __restrict__ lcnt, int32_t* __restrict__ out) {
+                                                          int32_t* __restrict__ lcnt, int32_t* __restrict__ out,
+                                                          int given) {
   using WS = WideSelect<kFusedVPL, false>;
   using WB = WideSelect<kFilterMaxLists / 1024, false>;
   constexpr int NW = 16, BPT = kHistBins / 1024;
@@ -955,83 +915,48 @@ __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restric
   uint32_t* tk = tickets + 2 * static_cast<int64_t>(row);
 
   // a. histogram of the keys' top kHistBits bits
-#pragma unroll
-  for (int i = 0; i < BPT; ++i) sh.h[tid + 1024 * i] = 0;
   if (tid == 0) {
     t_sh = 0;
     best_sh = 0x7FFFFFFF;
+    flag_sh = 1;
   }
   WS ws;
   ws.load(vals, len);   // key i of this thread: chunk position WS::pos(i)
-  __syncthreads();
+  if (!given) {   // uniform
 #pragma unroll
-  for (int i = 0; i < kFusedVPL; ++i)
-    if (ws.on(i)) atomicAdd(&sh.h[ws.u[i] >> (32 - kHistBits)], 1u);
-  __syncthreads();
-  const int target = min(k, len);
-  const int b0 = kHistBins - BPT * (tid + 1);   // thread t holds bins [4096 - 4(t+1), 4096 - 4t)
-  int hb[BPT], cnt = 0;
+    for (int i = 0; i < BPT; ++i) sh.h[tid + 1024 * i] = 0;
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < BPT; ++i) {
-    hb[i] = static_cast<int>(sh.h[b0 + i]);
-    cnt += hb[i];
-  }
-  const int incl = wave_incl_scan_dpp(cnt);
-  if (lane == 63) wave_a[wave] = incl;
-  __syncthreads();
-  int above = incl - cnt;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) above += w < wave ? wave_a[w] : 0;
-  if (above < target && above + cnt >= target) {   // one thread
-    int t = b0;
-#pragma unroll
-    for (int i = BPT - 1; i >= 0; --i) {
-      if (above < target && above + hb[i] >= target) t = b0 + i;
-      above += hb[i];
-    }
-    t_sh = t;
-  }
-  __syncthreads();
-  const int t = t_sh;
-  int32_t* w = win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords;
-  if (tid < kWin) st_coherent(w + 2 + tid, t + tid < kHistBins ? static_cast<int32_t>(sh.h[t + tid]) : 0);
-  int over = 0;   // keys above the window
-#pragma unroll
-  for (int i = 0; i < BPT; ++i) over += b0 + i >= t + kWin ? hb[i] : 0;
-  over = wave_incl_scan_dpp(over);
-  if (lane == 63) wave_b[wave] = over;
-  __syncthreads();
-  if (tid == 0) {
-    int sum = 0;
-#pragma unroll
-    for (int v = 0; v < NW; ++v) sum += wave_b[v];
-    st_coherent(w, t);
-    st_coherent(w + 1, sum);
-  }
-  // Every window store of this workgroup has completed before the ticket.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+    for (int i = 0; i < kFusedVPL; ++i)
+      if (ws.on(i)) atomicAdd(&sh.h[ws.u[i] >> (32 - kHistBits)], 1u);
+    __syncthreads();
+    chunk_window<1024, true>(sh.h, min(k, len), win + (static_cast<int64_t>(row) * n_chunks + c) * kWinWords,
+                             wave_a, &t_sh);
+    // Every window store of this workgroup has completed before the ticket.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-  // b. wait for the row's other chunks
-  if (tid == 0) {
-    // The windows went out as coherent (sc1) stores and have completed
-    // (s_waitcnt above) before the ticket; the compiler-only fences keep the
-    // compiler from moving memory operations across the ticket and the wait.
-    // Release/acquire orderings here would add a whole-L2 write-back and
-    // invalidate per workgroup (2.7 us at 8 rows x 32 chunks).
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    int ok = 1;
-    while (__hip_atomic_load(tk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < static_cast<uint32_t>(n_chunks)) {
-      __builtin_amdgcn_s_sleep(2);
-      if (__builtin_amdgcn_s_memrealtime() - t0 >= spin_ticks) {
-        ok = 0;
-        break;
+    // b. wait for the row's other chunks
+    if (tid == 0) {
+      // The windows went out as coherent (sc1) stores and have completed
+      // (s_waitcnt above) before the ticket; the compiler-only fences keep the
+      // compiler from moving memory operations across the ticket and the wait.
+      // Release/acquire orderings here would add a whole-L2 write-back and
+      // invalidate per workgroup (2.7 us at 8 rows x 32 chunks).
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      int ok = 1;
+      while (__hip_atomic_load(tk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < static_cast<uint32_t>(n_chunks)) {
+        __builtin_amdgcn_s_sleep(2);
+        if (__builtin_amdgcn_s_memrealtime() - t0 >= spin_ticks) {
+          ok = 0;
+          break;
+        }
       }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      flag_sh = ok;
     }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    flag_sh = ok;
   }
   __syncthreads();
 
@@ -1350,6 +1275,42 @@ int ticket_slot(hipStream_t stream, uint32_t** out) {
 }
 
 }  // namespace
+
+// The histogram-and-filter path of qkv_topk_ws (filtered(n, k)): the chunk
+// windows at the workspace's start, then the per-chunk lists and counts.
+// given: the windows are there already (chunk_window layout, written by an
+// earlier launch on the stream), so the histogram pass is skipped.
+int topk_filtered(const float* values, int64_t rows, int64_t n, int64_t ld, int64_t k, int32_t* out,
+                  void* workspace, hipStream_t st, bool given) {
+  const int n_bounds = static_cast<int>(cdiv(n, kStageChunk));
+  int32_t* win = static_cast<int32_t*>(workspace);
+  float* lval = reinterpret_cast<float*>(win + rows * n_bounds * kWinWords);
+  int32_t* lidx = reinterpret_cast<int32_t*>(lval + rows * n_bounds * k);
+  int32_t* lcnt = lidx + rows * n_bounds * k;
+  dim3 grid(static_cast<unsigned>(n_bounds), static_cast<unsigned>(rows));
+  if (rows * n_bounds <= kFusedMaxWGs) {
+    uint32_t* tickets = nullptr;
+    if (int rc = ticket_slot(st, &tickets)) return rc;
+    topk_fused_kernel<<<grid, 1024, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds,
+                                             static_cast<uint64_t>(g_spin_ticks), tickets, win, lval, lidx, lcnt,
+                                             out, given ? 1 : 0);
+    return check_launch("qkv_topk_ws");
+  }
+  if (!given) {
+    topk_hist_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds, win);
+    if (int rc = check_launch("qkv_topk_ws")) return rc;
+  }
+  topk_filter_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), win, n_bounds,
+                                           lval, lidx, lcnt);
+  if (int rc = check_launch("qkv_topk_ws")) return rc;
+  topk_lists_final_kernel<kFilterMaxLists / 1024><<<static_cast<unsigned>(rows), 1024, 0, st>>>(
+      lval, lidx, lcnt, n_bounds, static_cast<int>(k), out);
+  return check_launch("qkv_topk_ws");
+}
+
+// Whether qkv_topk_ws takes the histogram-and-filter path for (n, k).
+bool topk_takes_windows(int64_t n, int64_t k) { return filtered(n, k); }
+
 }  // namespace qkv
 
 using namespace qkv;
@@ -1411,30 +1372,7 @@ QKV_EXPORT int qkv_topk_ws(const float* values, int64_t rows, int64_t n, int64_t
   uint32_t* bounds = reinterpret_cast<uint32_t*>(idx_buf[1] + rows * n1);
   const int n_bounds = static_cast<int>(cdiv(n, kStageChunk));
   const int bound_j = static_cast<int>(cdiv(cdiv(k, n_bounds), 4));   // per wave; above 64: no bound
-  if (filtered(n, k)) {
-    // histogram and filter: the chunk windows, then the lists
-    int32_t* win = static_cast<int32_t*>(workspace);
-    float* lval = reinterpret_cast<float*>(win + rows * n_bounds * kWinWords);
-    int32_t* lidx = reinterpret_cast<int32_t*>(lval + rows * n_bounds * k);
-    int32_t* lcnt = lidx + rows * n_bounds * k;
-    dim3 grid(static_cast<unsigned>(n_bounds), static_cast<unsigned>(rows));
-    if (rows * n_bounds <= kFusedMaxWGs) {
-      uint32_t* tickets = nullptr;
-      if (int rc = ticket_slot(st, &tickets)) return rc;
-      topk_fused_kernel<<<grid, 1024, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds,
-                                               static_cast<uint64_t>(g_spin_ticks), tickets, win, lval, lidx,
-                                               lcnt, out);
-      return check_launch("qkv_topk_ws");
-    }
-    topk_hist_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), n_bounds, win);
-    if (int rc = check_launch("qkv_topk_ws")) return rc;
-    topk_filter_kernel<<<grid, 256, 0, st>>>(values, ld, static_cast<int>(n), static_cast<int>(k), win, n_bounds,
-                                             lval, lidx, lcnt);
-    if (int rc = check_launch("qkv_topk_ws")) return rc;
-    topk_lists_final_kernel<kFilterMaxLists / 1024><<<static_cast<unsigned>(rows), 1024, 0, st>>>(
-        lval, lidx, lcnt, n_bounds, static_cast<int>(k), out);
-    return check_launch("qkv_topk_ws");
-  }
+  if (filtered(n, k)) return topk_filtered(values, rows, n, ld, k, out, workspace, st, false);
   const float* cur_val = values;
   const int32_t* cur_idx = nullptr;
   int64_t cur_ld = ld, cur_n = n;

@@ -192,6 +192,42 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
     return bmax
 
 
+def decode_topk(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tensor, slab_scales: torch.Tensor,
+                tokens: int, k: int, *, scores: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """``decode_scores`` with block 1 then ``block_topk`` in one call
+    (qkv_int4_decode_topk): the top-k token indices int32 [B, Hkv, k],
+    ascending, lowest index first among equal scores; the token scores go to
+    ``scores`` f32 [B, Hkv, tokens].  Long rows build the top-k's chunk
+    histograms while they score."""
+    lib = _lib.load()
+    code = _check_query(query)
+    _require(slab.is_cuda and slab.dtype == torch.uint8 and slab.is_contiguous(), "slab must be contiguous CUDA uint8")
+    q = query.contiguous()
+    b, hq, d = q.shape
+    _, hkv, cap, half = slab.shape
+    s = half * 2
+    _require(tuple(chan_idx.shape) == (b, hkv, s) and chan_idx.dtype == torch.int32 and chan_idx.is_contiguous(),
+             "chan_idx must be contiguous int32 [B,Hkv,S]")
+    t = int(tokens)
+    if scores is None:
+        scores = torch.empty((b, hkv, t), dtype=torch.float32, device=q.device)
+    _require(scores.dtype == torch.float32 and scores.is_contiguous() and scores.numel() >= b * hkv * t
+             and scores.size(-1) == t, "scores must be contiguous float32 [B,Hkv,tokens]")
+    if out is None:
+        out = torch.empty((b, hkv, int(k)), dtype=torch.int32, device=q.device)
+    need = lib.qkv_topk_workspace_bytes(b * hkv, t, int(k))
+    _require(need >= 0, f"bad top-k sizes tokens={t} k={k}")
+    if need > 0 and (workspace is None or workspace.numel() * 4 < need):
+        workspace = topk_workspace(b * hkv, t, k, q.device)
+    with torch.cuda.device(q.device):
+        _lib.check(lib.qkv_int4_decode_topk(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s, slab.data_ptr(),
+                                            slab_scales.data_ptr(), cap, t, int(k), scores.data_ptr(), out.data_ptr(),
+                                            _lib.ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
+                                            code, _lib.stream_of(q)))
+    return out
+
+
 def topk_workspace(rows: int, n: int, k: int, device) -> torch.Tensor | None:
     """Workspace for ``block_topk`` on rows of n values (None when not needed)."""
     need = _lib.load().qkv_topk_workspace_bytes(int(rows), int(n), int(k))
@@ -467,11 +503,17 @@ class SparseDecodeStep:
         _require(key.size(2) >= self.tokens, f"K/V hold {key.size(2)} tokens, the step needs {self.tokens}")
         _require(query.dtype == self.out.dtype, f"this step runs on {self.out.dtype}; got a {query.dtype} query")
         prot = dict(protect_sink=self.protect_sink, protect_recent=self.protect_recent, keep_self=self.keep_self)
-        decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.block,
-                      bmax=self.bmax)
         if self.fused:
+            decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.block,
+                          bmax=self.bmax)
             return sparse_attention_select(query, key, value, self.bmax, self.topk, self.block, self.scored,
                                            scaling, workspace=self.workspace, sel_out=self.sel, out=self.out, **prot)
-        block_topk(self.bmax, self.topk, out=self.sel, workspace=self.topk_ws)
+        if self.block == 1:   # token selection: the scoring launch feeds the top-k its chunk histograms
+            decode_topk(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.topk,
+                        scores=self.bmax, out=self.sel, workspace=self.topk_ws)
+        else:
+            decode_scores(query, cache.chan_idx, cache.slab, cache.slab_scales, self.scored, self.block,
+                          bmax=self.bmax)
+            block_topk(self.bmax, self.topk, out=self.sel, workspace=self.topk_ws)
         return sparse_attention(query, key, value, self.sel, self.block, self.scored, scaling,
                                 workspace=self.workspace, out=self.out, **prot)
