@@ -1112,13 +1112,27 @@ def run_qabs_attn(args) -> dict:
         for layer in range(layers):
             RU.reuse_partial_scores(qs[layer], steps[layer].kdm, hf, dims, out=steps[layer].partial)
 
+    lib = RU._lib.load()
+    need = int(lib.qkv_qabs_candidate_select_workspace_bytes(rows, hf, frac))
+    select_ws = torch.empty(max(1, (need + 3) // 4), device="cuda") if need > 0 else None
+
     def run_select():
         for layer in range(layers):
             st = steps[layer]
             out = (st.final_idx[: rows * n_out].view(rows, n_out), st.final_valid[: rows * n_out].view(rows, n_out),
                    st.attn_ids[: rows * n_out].view(rows, n_out), st.hf)
             RU.qabs_candidate_select(st.partial, hf + 1, frac, c["sink"], c["recent"], True, append,
-                                     workspace=st.sel_ws, out=out)
+                                     workspace=select_ws, out=out)
+
+    def run_candidates():   # the step's own call: partial scores and the selection across workgroups
+        for layer in range(layers):
+            st = steps[layer]
+            q = qs[layer]
+            RU._lib.check(lib.qkv_qabs_candidates(
+                q.data_ptr(), st.kdm.data_ptr(), RU._lib.strides(*st.kdm.stride()), 0, b, hq, hkv, hf + 1, d, dims,
+                frac, c["sink"], c["recent"], 1, int(append), st.partial.data_ptr(), st.partial.stride(0),
+                st.sel_ws.data_ptr(), st.sel_ws.numel() * 4, st.final_idx.data_ptr(), st.final_valid.data_ptr(),
+                st.attn_ids.data_ptr(), n_out, st.hf.data_ptr(), st.hf.stride(0), RU._lib.stream_of(q)))
 
     def run_attn():
         for layer in range(layers):
@@ -1131,6 +1145,9 @@ def run_qabs_attn(args) -> dict:
         ("reuse_partial_scores", run_partial, rows * hf * (dims * 2 + 4)),
         # the scores read, the history mask and the index lists written
         ("qabs_candidate_select", run_select, rows * hf * (4 + 1) + rows * n_out * (8 + 1 + 4)),
+        # the partial scores' bytes, the scores read back, the mask and lists written
+        ("qabs_candidates", run_candidates,
+         rows * hf * (dims * 2 + 4) + rows * hf * (4 + 1) + rows * n_out * (8 + 1 + 4)),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
     kernels = {}

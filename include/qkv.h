@@ -437,6 +437,29 @@ int qkv_qabs_candidate_select(const float* scores, int64_t rows, int64_t key_cou
                               int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                               uint8_t* history_final, int64_t history_final_ld, void* stream);
 
+/* Workspace bytes of qkv_qabs_candidates (-1 for bad arguments). */
+int64_t qkv_qabs_candidates_workspace_bytes(int64_t rows, int64_t history, double candidate_fraction);
+
+/* The exact candidate attention's selection in one call (EV:4400-4465):
+ * qkv_reuse_partial_scores into partial over the history key_count - 1,
+ * then qkv_qabs_candidate_select on those scores, the same outputs.  Rows of
+ * at most 40960 history tokens and fewer than 128 rows: the partial scores
+ * also count each row's leading 12 bits, and the selection runs across
+ * several workgroups per row (the row's last workgroup resolves the
+ * boundary and writes the list).  workspace:
+ * qkv_qabs_candidates_workspace_bytes(batch * q_heads, key_count - 1,
+ * candidate_fraction) bytes, 16-byte aligned, zero-filled before the first
+ * call that uses it (allocate it zero-filled): it holds per-row counts and
+ * tickets that every completed call leaves zero again.  Calls that share a
+ * workspace use the same batch * q_heads and must not overlap in time.  No
+ * reference counterpart as one call (QK:63-96, then EV:4448-4465). */
+int qkv_qabs_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
+                        int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count, int64_t head_dim,
+                        int64_t dim_count, double candidate_fraction, int64_t protect_sink, int64_t protect_recent,
+                        int keep_self, int append, float* partial, int64_t partial_ld, void* workspace,
+                        int64_t workspace_bytes, int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                        int64_t n_out, uint8_t* history_final, int64_t history_final_ld, void* stream);
+
 /* The final index list of a given selection (_qabs_final_indices_from_selected
  * EV:2938-2982), as the periodic qabs{S}cand{pct}r{N}attn mode rebuilds it
  * from the indices the last refreshing step kept (EV:4535-4548, 4592-4600):

@@ -109,6 +109,9 @@ _PROTOTYPES = {
                                 _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32, _vp]),
     "qkv_block_rerank_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
     "qkv_reuse_candidates_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "qkv_qabs_candidates_workspace_bytes": (_i64, [_i64, _i64, _f64]),
+    "qkv_qabs_candidates": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f64, _i64, _i64,
+                                   _i32, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "qkv_int4_decode_topk": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
                                     _vp, _i64, _i32, _vp]),
     "qkv_reuse_candidates": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,

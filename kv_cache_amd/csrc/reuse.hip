@@ -784,11 +784,183 @@ __device__ void cand_list_finish_stream(void* raw, const float* __restrict__ lv,
   if (thr) cand_write_threshold(mn, thr);
 }
 
-template <int J>
+// The exact-candidate attention's final list (reuse_final_wide_kernel's
+// outputs for its scores path): where the list, flags and mask go, and the
+// row's protected ranges.
+struct QabsListOut {
+  uint64_t* nf;             // workspace: non-finite scores, one bit per position (row stride bits_ld)
+  int64_t* final_idx;
+  uint8_t* final_valid;
+  int32_t* attn_ids;        // optional
+  int n_out;
+  uint8_t* hf;              // byte mask [rows, hf_ld]
+  int64_t hf_ld;
+  int key_count, sink_end, recent_start, rec_begin, n_rec, keep_self, append;
+};
+
+// The bin's taken scores (above theta, or equal to it among the first kr in
+// position order: WideSelect's rule) as bits of fw, from the list in
+// registers (m <= kWideNT * VPL).  The radix passes start below the bin's
+// digit in sh.hist[1] (clear: boundary() cleared it).
+template <int VPL, typename At>
+__device__ void qabs_bin_taken(void* raw, const float* __restrict__ lv, const int* __restrict__ lp, int m, int rank,
+                               int bin, int n, uint64_t* fw, At&& at) {
+  using WS = WideSelect<VPL, false>;
+  auto& sh = *static_cast<typename WS::Shared*>(raw);
+  WS ws;
+  int off[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int p = WS::pos(i);
+    off[i] = p < m ? at(p) : 0;
+    ws.set(i, p < m ? ld_coherent(lv + off[i]) : 0.0f, p < m);
+  }
+  ws.kr = rank;
+  ws.kk = rank;
+  const uint32_t prefix = static_cast<uint32_t>(bin) << (32 - kCandBits);
+  ws.passes(sh, prefix, ~((1u << (32 - kCandBits)) - 1u), 32 - kCandBits, 1, prefix, false);
+  ws.place_uniform(sh, [&](int, int, int slot) {
+    const int pos = ld_coherent(lp + off[slot]);
+    if (static_cast<unsigned>(pos) < static_cast<unsigned>(n)) atomicOr(&fw[pos >> 6], 1ull << (pos & 63));
+  });
+}
+
+// The same for a list too long for registers: radix passes over the list in
+// memory, then the equal scores ranked in position order 1024 at a time.
+template <typename At>
+__device__ void qabs_bin_taken_stream(void* raw, const float* __restrict__ lv, const int* __restrict__ lp, int m,
+                                      int rank, int bin, int n, uint64_t* fw, At&& at) {
+  using WS = WideSelect<1, false>;
+  auto& sh = *static_cast<typename WS::Shared*>(raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  WS ws;
+  ws.kr = rank;
+  uint32_t prefix = static_cast<uint32_t>(bin) << (32 - kCandBits), mask = ~((1u << (32 - kCandBits)) - 1u);
+  int remaining = 32 - kCandBits, buf = 0;
+#pragma unroll
+  for (int j = 0; j < WS::NB / kWideNT; ++j) sh.hist[0][tid + kWideNT * j] = 0;
+  __syncthreads();
+  while (remaining > 0) {   // uniform
+    const int shift = remaining > WS::RB ? remaining - WS::RB : 0;
+    const uint32_t dmask = (1u << (remaining - shift)) - 1u;
+    for (int p = tid; p < m; p += kWideNT) {
+      const uint32_t u = f32_sortable(ld_coherent(lv + at(p)));
+      if ((u & mask) == prefix) atomicAdd(&sh.hist[buf][(u >> shift) & dmask], 1);
+    }
+    __syncthreads();
+    int b, krl, whole;
+    ws.boundary(sh, sh.hist[buf], sh.hist[buf ^ 1], b, krl, whole);
+    prefix |= static_cast<uint32_t>(b) << shift;
+    mask |= dmask << shift;
+    ws.kr = whole ? 0x7FFFFFFF : krl;
+    remaining = whole ? 0 : shift;
+    buf ^= 1;
+    __syncthreads();   // (the histogram's reads are done before the next pass)
+  }
+  // prefix: theta; equal keys are taken while fewer than kr came before
+  const int kr = ws.kr;
+  int eq_seen = 0;   // equal keys in the earlier rounds (uniform)
+  for (int p0 = 0; p0 < m; p0 += kWideNT) {   // uniform
+    const int p = p0 + tid;
+    const int o = p < m ? at(p) : 0;
+    const uint32_t u = p < m ? f32_sortable(ld_coherent(lv + o)) : 0u;
+    const bool gt = p < m && u > prefix, eq = p < m && u == prefix;
+    const uint64_t be = __ballot(eq);
+    if (lane == 0) sh.wave_eq[wave] = __popcll(be);
+    __syncthreads();
+    int before = eq_seen, round = 0;
+#pragma unroll
+    for (int w = 0; w < WS::NW; ++w) {
+      before += w < wave ? sh.wave_eq[w] : 0;
+      round += sh.wave_eq[w];
+    }
+    before += static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(be >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(be), 0)));
+    if (gt || (eq && before < kr)) {
+      const int pos = ld_coherent(lp + o);
+      if (static_cast<unsigned>(pos) < static_cast<unsigned>(n)) atomicOr(&fw[pos >> 6], 1ull << (pos & 63));
+    }
+    eq_seen += round;
+    __syncthreads();   // (wave_eq is rewritten next round)
+  }
+}
+
+// The row's final list from its taken positions (fw, LDS, one word per
+// thread): ascending positions, an entry valid when its score is finite and
+// (append or) it lies outside the protected ranges; then the sink range,
+// the recent range and the current token; the byte mask = the protected
+// ranges plus the taken positions with finite scores
+// (reuse_final_wide_kernel's emit, EV:2938-2982).  wsum: kWideNT / 64 ints
+// of LDS.
+__device__ void qabs_emit_list(const uint64_t* fw, const uint64_t* __restrict__ nf_row, int history, int keep,
+                               int row, const QabsListOut& qs, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_words = (history + 63) / 64;
+  const uint64_t w = tid < n_words ? fw[tid] : 0ull;
+  const uint64_t nf = tid < n_words ? __hip_atomic_load(nf_row + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0ull;
+  const int c = __popcll(w), incl = wave_incl_scan_dpp(c);
+  __syncthreads();   // (wsum's last readers are done)
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int p = incl - c;
+#pragma unroll
+  for (int v = 0; v < kWideNT / 64; ++v) p += v < wave ? wsum[v] : 0;
+  const int64_t o = static_cast<int64_t>(row) * qs.n_out;
+  for (uint64_t x = w; x; x &= x - 1) {   // this word's taken positions, ascending
+    const int idx = 64 * tid + __builtin_ctzll(x);
+    if (p < keep) {
+      const bool finite = !((nf >> (idx & 63)) & 1ull);
+      const bool fv = finite && (qs.append || (idx >= qs.sink_end && !(idx >= qs.recent_start && idx < history)));
+      qs.final_idx[o + p] = idx;
+      qs.final_valid[o + p] = fv;
+      if (qs.attn_ids) qs.attn_ids[o + p] = fv ? idx : -1;
+    }
+    ++p;
+  }
+  // the byte mask, 64 positions per thread
+  if (tid < n_words) {
+    auto range = [](int j, int a, int b) -> uint64_t {   // bits of [a, b) in word j
+      const int lo = max(a, 64 * j) - 64 * j, hi = min(b, 64 * j + 64) - 64 * j;
+      if (hi <= lo) return 0ull;
+      const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+      return upto & ~((1ull << lo) - 1ull);
+    };
+    const uint64_t bitsm = (w & ~nf) | range(tid, 0, qs.sink_end) | range(tid, qs.recent_start, history);
+    uint8_t* hrow = qs.hf + static_cast<int64_t>(row) * qs.hf_ld + 64 * tid;
+    if (64 * tid + 64 <= history && (reinterpret_cast<uintptr_t>(hrow) & 15) == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t b16 = static_cast<uint32_t>(bitsm >> (16 * q)) & 0xFFFFu;
+        uint32_t x4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x4[j] = (((b16 >> (4 * j)) & 0xFu) * 0x00204081u) & 0x01010101u;
+        *reinterpret_cast<uint4*>(hrow + 16 * q) = make_uint4(x4[0], x4[1], x4[2], x4[3]);
+      }
+    } else {
+      for (int j = 0; j < 64 && 64 * tid + j < history; ++j) hrow[j] = (bitsm >> j) & 1ull;
+    }
+  }
+  const int extra = qs.sink_end + qs.n_rec + qs.keep_self;
+  for (int i = tid; i < extra; i += kWideNT) {
+    const int idx = i < qs.sink_end ? i : (i < qs.sink_end + qs.n_rec ? qs.rec_begin + (i - qs.sink_end)
+                                                                      : qs.key_count - 1);
+    qs.final_idx[o + keep + i] = idx;
+    qs.final_valid[o + keep + i] = 1;
+    if (qs.attn_ids) qs.attn_ids[o + keep + i] = idx;
+  }
+}
+
+// LIST: the row's final selection of the exact-candidate attention instead
+// (reuse_final_wide_kernel's output from the row's scores, qs): k = keep,
+// equal scores at the threshold taken lowest positions first; bits are the
+// workspace's above-bin words, qs.nf its non-finite-score words, and the
+// last slice writes the final list, flags and mask (qabs_emit_list).
+template <int J, bool LIST = false>
 __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
     const float* __restrict__ values, int64_t ld, int n, int k, int slices, int* __restrict__ hist,
     int* __restrict__ state, float* __restrict__ list_val, int* __restrict__ list_pos, int64_t list_ld,
-    uint64_t* __restrict__ bits, int64_t bits_ld, float* __restrict__ thr_out) {
+    uint64_t* __restrict__ bits, int64_t bits_ld, float* __restrict__ thr_out, QabsListOut qs = {}) {
   using WS = WideSelect<1, false>;
   static_assert(sizeof(typename WideSelect<1, false>::Shared) == sizeof(typename WideSelect<8, false>::Shared),
                 "one shared layout for every list length");
@@ -796,6 +968,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
   __shared__ int wave_cnt[kWideNT / 64];
   __shared__ int pre[kCandSlices + 1];
   __shared__ int last_sh;
+  __shared__ uint64_t fw[LIST ? kWideMax / 64 : 1];   // LIST: the row's taken positions
   const int row = blockIdx.x / slices, s = blockIdx.x - row * slices;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int* hrow = hist + static_cast<int64_t>(row) * kCandBins;
@@ -823,28 +996,43 @@ __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
     const uint64_t w = __ballot(p < n && d > static_cast<uint32_t>(bin));
     if (lane == 0 && w0 + i < n_words)
       __hip_atomic_store(brow + w0 + i, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (LIST) {
+      const uint64_t f = __ballot(p < n && !isfinite(v[i]));
+      if (lane == 0 && w0 + i < n_words)
+        __hip_atomic_store(qs.nf + static_cast<int64_t>(row) * bits_ld + w0 + i, f, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
     inbin |= static_cast<uint32_t>(p < n && d == static_cast<uint32_t>(bin)) << i;
   }
   // the slice's bin scores compacted in (wave, slot, lane) = position order
-  const int cnt = __popc(inbin), incl = wave_incl_scan_dpp(cnt);
-  if (lane == 63) wave_cnt[wave] = incl;
+  // (one ballot per slot: a thread's own slots are 64 positions apart)
+  uint64_t bal[J];
+  int wtot = 0;
+#pragma unroll
+  for (int i = 0; i < J; ++i) {
+    bal[i] = __ballot((inbin >> i) & 1u);
+    wtot += __popcll(bal[i]);
+  }
+  if (lane == 0) wave_cnt[wave] = wtot;
   __syncthreads();
-  int at = incl - cnt, total = 0;
+  int at = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kWideNT / 64; ++w) {
     at += w < wave ? wave_cnt[w] : 0;
     total += wave_cnt[w];
   }
   if (tid == 0) st_coherent(srow + s, total);
-  if (cnt) {
+  if (wtot) {   // uniform per wave
     const int64_t base = static_cast<int64_t>(row) * list_ld + static_cast<int64_t>(s) * kWideNT * J;
 #pragma unroll
     for (int i = 0; i < J; ++i) {
       if ((inbin >> i) & 1u) {
-        st_coherent(list_val + base + at, v[i]);
-        st_coherent(list_pos + base + at, 64 * (w0 + i) + lane);
-        ++at;
+        const int e = at + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                               static_cast<uint32_t>(bal[i] >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[i]), 0)));
+        st_coherent(list_val + base + e, v[i]);
+        st_coherent(list_pos + base + e, 64 * (w0 + i) + lane);
       }
+      at += __popcll(bal[i]);
     }
   }
   // Every word, count and list store of this workgroup has completed before its ticket.
@@ -875,9 +1063,20 @@ __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
   float* thr = thr_out ? thr_out + row : nullptr;
   const int slice_len = kWideNT * J;
   auto at_fn = [&](int p) { return cand_list_at(pre, slices, slice_len, p); };
-  if (m <= kWideNT) cand_list_finish<1>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
-  else if (m <= 8 * kWideNT) cand_list_finish<8>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
-  else cand_list_finish_stream(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
+  if constexpr (LIST) {
+    for (int j = tid; j < n_words; j += kWideNT)
+      fw[j] = __hip_atomic_load(brow + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (m <= kWideNT) qabs_bin_taken<1>(&sh, lv, lp, m, rank, bin, n, fw, at_fn);
+    else if (m <= 8 * kWideNT) qabs_bin_taken<8>(&sh, lv, lp, m, rank, bin, n, fw, at_fn);
+    else qabs_bin_taken_stream(&sh, lv, lp, m, rank, bin, n, fw, at_fn);
+    __syncthreads();
+    qabs_emit_list(fw, qs.nf + static_cast<int64_t>(row) * bits_ld, n, k, row, qs, wave_cnt);
+  } else {
+    if (m <= kWideNT) cand_list_finish<1>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
+    else if (m <= 8 * kWideNT) cand_list_finish<8>(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
+    else cand_list_finish_stream(&sh, lv, lp, m, rank, bin, n, brow, thr, at_fn);
+  }
 }
 
 // The step's candidates in one launch (rows of at most kWideMax history
@@ -1691,6 +1890,34 @@ int launch_cand_slices(const char* what, const float* values, int64_t ld, int64_
   return launch(std::integral_constant<int, 32>{});
 }
 
+// reuse_cand_slices_kernel<J, true>: the exact-candidate attention's final
+// list across slices (J as launch_cand_slices picks it); bits / nf: the
+// above-bin and non-finite words, bits_ld words per row.
+int launch_qabs_slices(const char* what, const float* values, int64_t ld, int64_t rows, int64_t n, int64_t keep,
+                       const CandSplit& cs, uint64_t* bits, int64_t bits_ld, const QabsListOut& qs, hipStream_t st) {
+  auto launch = [&](auto jc) {
+    constexpr int J = decltype(jc)::value;
+    const int64_t slices = cdiv(n, int64_t(kWideNT) * J);
+    reuse_cand_slices_kernel<J, true><<<static_cast<unsigned>(rows * slices), kWideNT, 0, st>>>(
+        values, ld, static_cast<int>(n), static_cast<int>(keep), static_cast<int>(slices), cs.hist, cs.state,
+        cs.list_val, cs.list_pos, n, bits, bits_ld, nullptr, qs);
+    return check_launch(what);
+  };
+  auto wgs = [&](int64_t j) { return rows * cdiv(n, int64_t(kWideNT) * j); };
+  if (wgs(1) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 1>{});
+  if (wgs(2) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 2>{});
+  if (wgs(4) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 4>{});
+  if (wgs(8) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 8>{});
+  if (wgs(16) <= QKV_CAND_TARGET_WGS) return launch(std::integral_constant<int, 16>{});
+  return launch(std::integral_constant<int, 32>{});
+}
+
+// The split selection's part of a qkv_qabs_candidates workspace after its
+// state: the boundary-bin lists, then the above-bin and non-finite words.
+int64_t qabs_split_bytes(int64_t rows, int64_t history) {
+  return 2 * align256(rows * history * 4) + 2 * align256(rows * cdiv(history, 64) * 8);
+}
+
 template <int DT> struct RunCandidates {
   static int run(const char* what, const void* q, const void* kdm, const int64_t* ks, int64_t B, int64_t Hq,
                  int64_t Hkv, int64_t T, int64_t D, int count, int64_t k, float* partial, int64_t partial_ld,
@@ -1937,6 +2164,85 @@ QKV_EXPORT int qkv_qabs_candidate_select(const float* scores, int64_t rows, int6
       static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids, static_cast<int>(n_out),
       history_final, history_final_ld, append ? 1 : 0);
   return check_launch(what);
+}
+
+QKV_EXPORT int64_t qkv_qabs_candidates_workspace_bytes(int64_t rows, int64_t history, double candidate_fraction) {
+  const int64_t old = qkv_qabs_candidate_select_workspace_bytes(rows, history, candidate_fraction);
+  if (old < 0) return -1;
+  const int64_t split = history <= kWideMax ? qabs_split_bytes(rows, history) : 0;
+  return cand_state_bytes(rows) + std::max(old, split);
+}
+
+QKV_EXPORT int qkv_qabs_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides, int dtype,
+                                   int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                   int64_t head_dim, int64_t dim_count, double candidate_fraction,
+                                   int64_t protect_sink, int64_t protect_recent, int keep_self, int append,
+                                   float* partial, int64_t partial_ld, void* workspace, int64_t workspace_bytes,
+                                   int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
+                                   uint8_t* history_final, int64_t history_final_ld, void* stream) {
+  const char* what = "qkv_qabs_candidates";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !partial || !workspace || !final_indices || !final_valid ||
+      !history_final)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  const int64_t history = key_count - 1;
+  if (history <= 0 || key_count >= (int64_t(1) << 31) || partial_ld < history || history_final_ld < history)
+    return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 and row strides covering the history", what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
+  if (!(candidate_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: candidate_fraction must be >= 0", what);
+  if (protect_sink < 0 || protect_recent < 0) return fail(QKV_ERR_INVALID, "%s: negative protection", what);
+  const int64_t rows = batch * q_heads;
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, candidate_fraction, keep_self);
+  if (n_out != c.n_out)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the selection needs %lld", what,
+                (long long)n_out, (long long)c.n_out);
+  const int64_t need = qkv_qabs_candidates_workspace_bytes(rows, history, candidate_fraction);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(QKV_ERR_INVALID, "%s: the workspace must be 16-byte aligned", what);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
+                                                       std::min<int64_t>(head_dim, kMaxDims)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t state = cand_state_bytes(rows);
+  if (history > kWideMax || rows >= kFusedCandRows) {   // the partial scores, then qkv_qabs_candidate_select
+    rc = dispatch_dtype<RunReusePartial>(dtype, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
+                                         head_dim, count, partial, partial_ld, st);
+    if (rc) return rc;
+    return qkv_qabs_candidate_select(partial, rows, key_count, partial_ld, candidate_fraction, protect_sink,
+                                     protect_recent, keep_self, append, ws + state, workspace_bytes - state,
+                                     final_indices, final_valid, attn_ids, n_out, history_final, history_final_ld,
+                                     stream);
+  }
+  CandSplit split;
+  split.hist = reinterpret_cast<int*>(ws);
+  split.state = reinterpret_cast<int*>(ws + align256(rows * kCandBins * 4));
+  split.list_val = reinterpret_cast<float*>(ws + state);
+  split.list_pos = reinterpret_cast<int*>(ws + state + align256(rows * history * 4));
+  const int64_t n_words = cdiv(history, 64);
+  uint64_t* words = reinterpret_cast<uint64_t*>(ws + state + 2 * align256(rows * history * 4));
+  uint64_t* nf = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(words) + align256(rows * n_words * 8));
+  rc = dispatch_dtype<RunReusePartial>(dtype, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads, history,
+                                       head_dim, count, partial, partial_ld, st, nullptr, 0, split.hist);
+  if (rc) return rc;
+  QabsListOut qs;
+  qs.nf = nf;
+  qs.final_idx = final_indices;
+  qs.final_valid = final_valid;
+  qs.attn_ids = attn_ids;
+  qs.n_out = static_cast<int>(n_out);
+  qs.hf = history_final;
+  qs.hf_ld = history_final_ld;
+  qs.key_count = static_cast<int>(key_count);
+  qs.sink_end = static_cast<int>(c.sink_end);
+  qs.recent_start = static_cast<int>(c.recent_start);
+  qs.rec_begin = static_cast<int>(c.rec_begin);
+  qs.n_rec = static_cast<int>(c.n_rec);
+  qs.keep_self = keep_self ? 1 : 0;
+  qs.append = append ? 1 : 0;
+  return launch_qabs_slices(what, partial, partial_ld, rows, history, c.keep, split, words, n_words, qs, st);
 }
 
 QKV_EXPORT int qkv_final_indices_from_selected(const int64_t* selected, int64_t selected_ld, int64_t n_sel,

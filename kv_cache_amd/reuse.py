@@ -868,8 +868,11 @@ class QabsCandidateAttentionStep:
         self.final_valid = torch.empty(rows * self.n_out_max, dtype=torch.bool, device=device)
         self.attn_ids = torch.empty(rows * self.n_out_max, dtype=torch.int32, device=device)
         self.hf = torch.zeros((rows, cap), dtype=torch.bool, device=device)
-        need = int(lib.qkv_qabs_candidate_select_workspace_bytes(rows, hist_max, self.cand_fraction))
-        self.sel_ws = torch.empty(max(1, (need + 3) // 4), dtype=torch.float32, device=device)
+        # qkv_qabs_candidates' workspace: zero-filled (its selection state starts
+        # at zero and every call leaves it so)
+        need = int(lib.qkv_qabs_candidates_workspace_bytes(rows, hist_max, self.cand_fraction))
+        _require(need >= 0, "bad candidate selection sizes")
+        self.sel_ws = torch.zeros(max(1, (need + 3) // 4), dtype=torch.float32, device=device)
         need = lib.qkv_sparse_attention_workspace_bytes(batch, q_heads, q_heads, head_dim, self.n_out_max, 1)
         _require(need > 0, "unsupported attention shape (head_dim must be 128)")
         self.attn_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=device)
@@ -935,14 +938,21 @@ class QabsCandidateAttentionStep:
                                         out=out)
         else:
             _require(self.kdm_len >= history, "the dim-major copy does not hold the history")
-            reuse_partial_scores(q, self.kdm, history, self.dims, out=self.partial)
             n_out = int(lib.qkv_reuse_final_count(history, self.sink, self.recent, self.cand_fraction,
                                                   int(self.keep_self)))
             out = (self.final_idx[: rows * n_out].view(rows, n_out),
                    self.final_valid[: rows * n_out].view(rows, n_out), self.attn_ids[: rows * n_out].view(rows, n_out),
                    self.hf)
-            qabs_candidate_select(self.partial, key_count, self.cand_fraction, self.sink, self.recent,
-                                  self.keep_self, self.append, workspace=self.sel_ws, out=out)
+            # partial scores and the selection in one call (across workgroups
+            # where the rows are few and short enough)
+            with torch.cuda.device(q.device):
+                _lib.check(lib.qkv_qabs_candidates(
+                    q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), _dtype_code(q), self.batch,
+                    self.q_heads, self.kv_heads, key_count, self.head_dim, self.dims, self.cand_fraction, self.sink,
+                    self.recent, int(self.keep_self), int(self.append), self.partial.data_ptr(),
+                    self.partial.stride(0), self.sel_ws.data_ptr(), self.sel_ws.numel() * 4, out[0].data_ptr(),
+                    out[1].data_ptr(), out[2].data_ptr(), n_out, self.hf.data_ptr(), self.hf.stride(0),
+                    _lib.stream_of(q)))
             if self.interval is not None:   # the selection the next steps reuse (EV:4574-4580)
                 keep = budget_count(history, self.cand_fraction)
                 self.kept[:, :keep].copy_(out[0][:, :keep])

@@ -188,3 +188,66 @@ def test_final_indices_from_selected_matches_oracle(hist, n_sel, sink, recent, k
     assert np.array_equal(got_v, want_v)
     assert np.array_equal(got_i[got_v], want_i[want_v])   # invalid entries' indices are not read
     assert np.array_equal(ids.cpu().numpy(), np.where(got_v, got_i, -1))
+
+
+def _qabs_case(b, hist, pattern, seed):
+    # (q, K) whose partial scores follow `pattern` (K[t] = c_t * a fixed
+    # vector: the scores are c_t times the row's sum over its dims)
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn((b, 32, 128), generator=gen).to(torch.bfloat16)
+    if pattern == "normal":
+        k = torch.randn((b, 8, hist + 1, 128), generator=gen)
+    else:
+        if pattern == "equal":     # the whole row in one bin: the list selected from memory
+            c = torch.ones(hist + 1)
+        elif pattern == "narrow":  # 128 values in [1, 2): a few thousand scores in the boundary bin
+            c = 1.0 + torch.randint(0, 256, (hist + 1,), generator=gen).float() / 256.0
+        elif pattern == "coarse":  # 16 values in one bin: ties at the threshold
+            c = 1.0 + torch.randint(0, 16, (hist + 1,), generator=gen).float() / 128.0
+        else:
+            raise ValueError(pattern)
+        k = c.view(1, 1, hist + 1, 1).expand(b, 8, hist + 1, 128).clone()
+    return q.to(DEV), k.to(torch.bfloat16).to(DEV)
+
+
+@pytest.mark.parametrize("b,hist,pattern,frac,sink,recent,keep_self,append", [
+    (1, 32768, "normal", 0.03, 10, 10, 1, 0),    # the timed mode's shape: 5 slices per row
+    (1, 32768, "normal", 0.05, 4, 16, 1, 1),     # appendattn: protected picks stay valid
+    (1, 20000, "equal", 0.03, 0, 0, 0, 0),       # every score equal: the lowest positions
+    (1, 20000, "narrow", 0.1, 10, 10, 1, 0),
+    (1, 30011, "coarse", 0.03, 10, 10, 1, 0),    # equal scores at the threshold, lowest positions first
+    (3, 777, "narrow", 1.0, 2, 2, 1, 0),         # every position kept
+    (2, 40960, "normal", 0.02, 10, 10, 1, 0),    # the longest one-workgroup row, 64 rows
+])
+def test_qabs_candidates_equal_two_calls(b, hist, pattern, frac, sink, recent, keep_self, append):
+    # qkv_qabs_candidates (partial scores with first-digit counts, the selection
+    # across workgroups) against qkv_reuse_partial_scores + qkv_qabs_candidate_select
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    q, k = _qabs_case(b, hist, pattern, hist + b)
+    rows, dims, key_count = b * 32, 8, hist + 1
+    kdm = torch.zeros((b, 8, 128, hist + 8), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k, kdm, 0, hist)
+    want_p = RU.reuse_partial_scores(q, kdm, hist, dims)
+    want = RU.qabs_candidate_select(want_p, key_count, frac, sink, recent, bool(keep_self), bool(append))
+    n_out = want[0].size(1)
+    got = (torch.full_like(want[0], -7), torch.zeros_like(want[1]), torch.full_like(want[2], -7),
+           torch.zeros_like(want[3]))
+    part = torch.zeros((rows, hist + 8), device=DEV)
+    ws = torch.zeros((lib.qkv_qabs_candidates_workspace_bytes(rows, hist, frac) + 3) // 4, device=DEV)
+    for _ in range(2):   # the second call on the workspace the first left
+        _lib.check(lib.qkv_qabs_candidates(
+            q.data_ptr(), kdm.data_ptr(), _lib.strides(*kdm.stride()), 0, b, 32, 8, key_count, 128, dims, frac, sink,
+            recent, keep_self, append, part.data_ptr(), part.stride(0), ws.data_ptr(), ws.numel() * 4,
+            got[0].data_ptr(), got[1].data_ptr(), got[2].data_ptr(), n_out, got[3].data_ptr(), got[3].stride(0),
+            _lib.stream_of(q)))
+        assert torch.equal(part[:, :hist], want_p[:, :hist])
+        for g, w in zip(got, want):
+            assert torch.equal(g, w)
+        assert not ws[: rows * 4096].any()   # the first-digit counts are left zero
+        state = ws[rows * 4096 : rows * 4096 + rows * 48].view(torch.int32).view(rows, 48)
+        assert not state[:, 40].any()        # ... and the tickets
+    if pattern == "equal":
+        keep = want[0].size(1) - (sink + recent + keep_self)
+        assert torch.equal(got[0][:, :keep].cpu(), torch.arange(keep).expand(rows, keep))
