@@ -420,25 +420,47 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
   const int b = row / q_heads, h = row - b * q_heads;
   for (int d = tid; d < kHD; d += kRerankNT) q_s[d] = half_to_f32<F16>(query[static_cast<int64_t>(row) * kHD + d]);
   uint8_t* mrow = keep_mask + static_cast<int64_t>(row) * keep_ld;
-  for (int t = tid; t < key_count; t += kRerankNT)
-    mrow[t] = (t < sink_end) || (t >= recent_start && t < history) || (keep_self && t == history);
+  // the protected mask, 16 bytes per store where the row is 16-byte aligned
+  auto prot = [&](int t) -> uint32_t {
+    return (t < sink_end) || (t >= recent_start && t < history) || (keep_self && t == history);
+  };
+  const int body = (reinterpret_cast<uintptr_t>(mrow) & 15) ? 0 : (key_count & ~15);
+  for (int t0 = 16 * tid; t0 < body; t0 += 16 * kRerankNT) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) x |= prot(t0 + 4 * j + bb) << (8 * bb);
+      w[j] = x;
+    }
+    *reinterpret_cast<uint4*>(mrow + t0) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  for (int t = body + tid; t < key_count; t += kRerankNT) mrow[t] = prot(t);
 
-  // 1. candidates
+  // 1. candidates (the first radix digit counted as the scores arrive)
   WS1 ws1;
-  ws1.load(partial + static_cast<int64_t>(row) * partial_ld, n_scan * block);
-  const int kk1 = ws1.run(n_cand, lds.a);
+  ws1.load_count(partial + static_cast<int64_t>(row) * partial_ld, n_scan * block, lds.a);
+  const int kk1 = ws1.run_counted(n_cand, lds.a);
   const int32_t* brow = blocks + static_cast<int64_t>(row) * n_scan;
-  ws1.place(lds.a, [&](int pos, int o, int) {
+  auto emit1 = [&](int pos, int o, int) {
     const int jb = pos / block;
     cand[o] = brow[jb] * block + (pos - jb * block);
     cand_pos[o] = pos;
-  });
+  };
+  if constexpr (VPL1 <= 8) ws1.place_uniform(lds.a, emit1);
+  else ws1.place(lds.a, emit1);
 
   // 2. full scores of the candidates (computed by the scan launch when full
   // is given: then only read back here), 3. the kept ones
   WS2 ws2;
   const uint16_t* kb = key + b * sb + (h / group) * sh;
   const float* frow = full ? full + static_cast<int64_t>(row) * partial_ld : nullptr;
+  // (place ended with a barrier: lds.b's histogram is cleared for the count)
+#pragma unroll
+  for (int j = 0; j < WS2::NB / kRerankNT; ++j) lds.b.hist[0][tid + kRerankNT * j] = 0;
+  __syncthreads();
+  int ninf = 0;
 #pragma unroll
   for (int i = 0; i < VPL2; ++i) {
     const int ci = WS2::pos(i);
@@ -446,15 +468,19 @@ __global__ __launch_bounds__(kRerankNT) void rerank_kernel(
     float acc = 0.0f;
     if (ok) acc = frow ? frow[cand_pos[ci]] : full_score<F16>(kb + static_cast<int64_t>(cand[ci]) * st, q_s, scaling);
     ws2.set(i, acc, ok);
+    ws2.count(i, lds.b, ninf);
   }
-  const int kk2 = ws2.run(n_keep, lds.b);
+  ws2.count_done(lds.b, ninf);
+  const int kk2 = ws2.run_counted(n_keep, lds.b);
   int32_t* ids = attn_ids + static_cast<int64_t>(row) * n_out;
-  ws2.place(lds.b, [&](int ci, int o, int) {
+  auto emit2 = [&](int ci, int o, int) {
     const int tok = cand[ci];
     mrow[tok] = 1;
     const bool fv = tok >= sink_end && !(tok >= recent_start && tok < history);
     ids[o] = fv ? tok : -1;
-  });
+  };
+  if constexpr (VPL2 <= 8) ws2.place_uniform(lds.b, emit2);
+  else ws2.place(lds.b, emit2);
   for (int o = kk2 + tid; o < n_keep; o += kRerankNT) ids[o] = -1;
   const int extra = sink_end + n_rec + keep_self;
   for (int i = tid; i < extra; i += kRerankNT)
