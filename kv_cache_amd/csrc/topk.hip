@@ -835,15 +835,20 @@ __global__ __launch_bounds__(1024) void topk_lists_final_kernel(const float* __r
         cidx[p] = xi[u];
       }
     }
+#pragma unroll
+    for (int j = 0; j < WC::NB / 1024; ++j) sh.c.hist[0][tid + 1024 * j] = 0;   // (counted below)
     __syncthreads();
     WC wc;
+    int ninf = 0;
 #pragma unroll
     for (int i = 0; i < kFinalLds / 1024; ++i) {
       const int p = WC::pos(i);
       wc.set(i, p < total ? cval[p] : 0.0f, p < total);
+      wc.count(i, sh.c, ninf);
     }
-    const int kk = wc.run(k, sh.c);
-    wc.place(sh.c, [&](int p, int o, int) { orow[o] = cidx[p]; });
+    wc.count_done(sh.c, ninf);
+    const int kk = wc.run_counted(k, sh.c);
+    wc.place_uniform(sh.c, [&](int p, int o, int) { orow[o] = cidx[p]; });
     for (int o = kk + tid; o < k; o += 1024) orow[o] = -1;   // not reached: k keys pass the floor
     return;
   }
@@ -1140,15 +1145,20 @@ __global__ __launch_bounds__(1024) void topk_fused_kernel(const float* __restric
         }
       }
     }
+#pragma unroll
+    for (int j = 0; j < WS::NB / 1024; ++j) sh.fin.s.hist[0][tid + 1024 * j] = 0;   // (counted below)
     __syncthreads();
     WS wc;
+    int ninf = 0;
 #pragma unroll
     for (int i = 0; i < kFusedVPL; ++i) {
       const int p = WS::pos(i);
       wc.set(i, p < all ? sh.fin.cval[p] : 0.0f, p < all);
+      wc.count(i, sh.fin.s, ninf);
     }
-    const int kk = wc.run(k, sh.fin.s);
-    wc.place(sh.fin.s, [&](int p, int at, int) { orow[at] = sh.fin.cidx[p]; });
+    wc.count_done(sh.fin.s, ninf);
+    const int kk = wc.run_counted(k, sh.fin.s);
+    wc.place_uniform(sh.fin.s, [&](int p, int at, int) { orow[at] = sh.fin.cidx[p]; });
     for (int at = kk + tid; at < k; at += 1024) orow[at] = -1;   // not reached: k keys pass the floor
     return;
   }
