@@ -399,19 +399,32 @@ def test_reuse_candidates_workspace_reused():
             assert np.array_equal(mask.cpu().numpy().astype(bool), RU.expand_bits(words, cap)[:, :hist].cpu().numpy())
 
 
-@pytest.mark.parametrize("hist,sink,recent,frac,prev", [(3000, 4, 8, 0.02, True), (1001, 0, 0, 0.05, False),
-                                                        (45000, 10, 10, 0.02, True)])
-def test_reuse_select_bits_equals_bytes(hist, sink, recent, frac, prev):
-    # the same masks as bytes and as bitsets: the same final list and final mask
+@pytest.mark.parametrize("hist,sink,recent,frac,prev,dens,ties,dtype", [
+    (3000, 4, 8, 0.02, True, 0.03, False, torch.bfloat16),
+    (1001, 0, 0, 0.05, False, 0.03, False, torch.bfloat16),
+    (45000, 10, 10, 0.02, True, 0.03, False, torch.bfloat16),   # past the one-workgroup rows
+    (32768, 10, 10, 0.02, True, 0.03, False, torch.float16),    # the bench's proportions, fp16
+    (40960, 10, 10, 0.02, True, 0.03, False, torch.bfloat16),   # the longest one-workgroup row
+    (8000, 3, 5, 0.05, True, 0.25, False, torch.bfloat16),      # a union past the compacted keys: the whole row
+    (777, 0, 0, 0.3, True, 0.03, False, torch.bfloat16),        # keep larger than the union: -inf picks
+    (3700, 0, 0, 0.03, True, 0.1, True, torch.bfloat16),        # K rows repeat every 37 tokens: exact ties
+])
+def test_reuse_select_bits_equals_bytes(hist, sink, recent, frac, prev, dens, ties, dtype):
+    # the same masks as bytes and as bitsets (the bitset selection forms and
+    # scores the union in its own workgroup): the same final list and final mask
     from kv_cache_amd import _lib
 
     lib = _lib.load()
     gen = torch.Generator().manual_seed(hist)
     b, hq, hkv, d = 1, 8, 2, 128
     rows, t = b * hq, hist + 1
-    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16).to(DEV)
-    k = torch.randn((b, hkv, t, d), generator=gen).to(torch.bfloat16).to(DEV)
-    masks = [(torch.rand((rows, hist), generator=gen) < 0.03).to(DEV) for _ in range(3)]
+    q = torch.randn((b, hq, d), generator=gen).to(dtype).to(DEV)
+    if ties:
+        k = torch.randn((b, hkv, 37, d), generator=gen).repeat(1, 1, -(-t // 37), 1)[:, :, :t]
+        k = k.contiguous().to(dtype).to(DEV)
+    else:
+        k = torch.randn((b, hkv, t, d), generator=gen).to(dtype).to(DEV)
+    masks = [(torch.rand((rows, hist), generator=gen) < dens).to(DEV) for _ in range(3)]
     n_w = -(-hist // 64)
 
     def to_words(m):
@@ -431,7 +444,8 @@ def test_reuse_select_bits_equals_bytes(hist, sink, recent, frac, prev):
         ids = torch.empty((rows, n_out), dtype=torch.int32, device=DEV)
         select = lib.qkv_reuse_select_bits if bits else lib.qkv_reuse_select
         extra = (None, None, None) if bits else ()
-        _lib.check(select(q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), 0, b, hq, hkv, t, d,
+        _lib.check(select(q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), _lib.DTYPE_CODES[dtype], b, hq,
+                          hkv, t, d,
                           ms[0].data_ptr(), ms[1].data_ptr() if prev else None, ms[2].data_ptr(), ms[0].stride(0),
                           sink, recent, frac, 1, 0.088, ws.data_ptr(), ws.numel() * 4, fi.data_ptr(), fv.data_ptr(),
                           ids.data_ptr(), n_out, fin.data_ptr(), fin.stride(0), *extra, _lib.stream_of(q)))
