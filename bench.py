@@ -811,6 +811,10 @@ def run_reuse(args) -> dict:
     lib = RU._lib.load()
     n_sel = int(lib.qkv_reuse_final_count(hist_fixed, c["sink"], c["recent"], c["top_fraction"], 1))
 
+    # the selection writes its final mask elsewhere, so that every timed launch
+    # reads the previous final (block-expanded in the blk modes) the step reads
+    fin_out = [torch.empty_like(steps[l].fin) for l in range(layers)]
+
     def run_select():
         for layer in range(layers):
             st, kk, _ = fixed(layer)
@@ -820,8 +824,8 @@ def run_reuse(args) -> dict:
                 qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv, hist_fixed + 1, d,
                 st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(), st.fin.stride(0), c["sink"],
                 c["recent"], c["top_fraction"], 1, scaling, st.select_ws.data_ptr(), st.select_ws.numel() * 4,
-                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_sel, st.fin.data_ptr(),
-                st.fin.stride(0), *extra, RU._lib.stream_of(qs[layer])))
+                st.final_idx.data_ptr(), st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_sel,
+                fin_out[layer].data_ptr(), fin_out[layer].stride(0), *extra, RU._lib.stream_of(qs[layer])))
 
     def run_expand():
         for layer in range(layers):

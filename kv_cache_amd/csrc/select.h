@@ -363,7 +363,7 @@ struct WideSelect {
   };
 
   // Position of key i of this thread.
-  __device__ static int pos(int i) {
+  __device__ __forceinline__ static int pos(int i) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     return wave * 64 * VPL + 64 * i + lane;
   }
@@ -371,7 +371,7 @@ struct WideSelect {
   // A raw buffer of exactly the row's n * 4 bytes: positions past the row
   // read 0 from the range check instead of touching memory.  Keys whose
   // order-preserving value is below floor never take part.
-  __device__ void load(const float* __restrict__ vals, int n, uint32_t floor = 0) {
+  __device__ __forceinline__ void load(const float* __restrict__ vals, int n, uint32_t floor = 0) {
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
     const int base = pos(0);
@@ -389,23 +389,23 @@ struct WideSelect {
   }
 
   // Key i from a value computed in place (ok = false: never taken).
-  __device__ void set(int i, float v, bool ok) {
+  __device__ __forceinline__ void set(int i, float v, bool ok) {
     u[i] = f32_sortable(v);
     valid = ok ? (valid | (1ull << i)) : (valid & ~(1ull << i));
   }
 
-  __device__ bool on(int i) const { return (valid >> i) & 1ull; }
+  __device__ __forceinline__ bool on(int i) const { return (valid >> i) & 1ull; }
 
   // Marks the validity bits as changed here, so each phase derives its
   // per-slot lane masks anew instead of keeping VPL scalar-register pairs
   // alive across the whole kernel.
-  __device__ void refresh() { asm volatile("" : "+v"(valid)); }
+  __device__ __forceinline__ void refresh() { asm volatile("" : "+v"(valid)); }
 
   // The row's largest and smallest valid key and the count of valid keys,
   // reduced over the workgroup through sh.red (one barrier); LANE: this
   // thread's extremes are lane_max / lane_min already (load_count).
   template <bool LANE = false>
-  __device__ void reduce_row(Shared& sh, uint32_t& umax, uint32_t& umin, int& nval) {
+  __device__ __forceinline__ void reduce_row(Shared& sh, uint32_t& umax, uint32_t& umin, int& nval) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     umax = lane_max;
     umin = lane_min;
@@ -447,7 +447,7 @@ struct WideSelect {
   // barrier every wave finds the boundary itself -- the wave of bins holding
   // the kr-th key, then the bin among its 256 -- instead of waiting for one
   // thread to publish it.
-  __device__ void boundary(Shared& sh, const int* hist, int* other, int& bin, int& krl, int& whole) {
+  __device__ __forceinline__ void boundary(Shared& sh, const int* hist, int* other, int& bin, int& krl, int& whole) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // (the other histogram was last read before this pass's atomics)
 #pragma unroll
@@ -495,7 +495,7 @@ struct WideSelect {
   // atomics rarely collide; an 8-bit digit of such floats holds a handful of
   // exponents and serializes on them), alternating between sh.hist[buf] and
   // the other, two barriers per digit.  Ends with a barrier when it counted.
-  __device__ void passes(Shared& sh, uint32_t prefix, uint32_t mask, int remaining, int buf, uint32_t umin,
+  __device__ __forceinline__ void passes(Shared& sh, uint32_t prefix, uint32_t mask, int remaining, int buf, uint32_t umin,
                          bool counted) {
     const int lane = threadIdx.x & 63;
     const bool any = counted || remaining > 0;
@@ -538,7 +538,7 @@ struct WideSelect {
   // Every thread calls it; the caller's earlier uses of sh have completed
   // (a barrier since).  The bits the row's largest and smallest keys share
   // are skipped.
-  __device__ int run(int k, Shared& sh) {
+  __device__ __forceinline__ int run(int k, Shared& sh) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < NB / NT; ++j) sh.hist[0][tid + NT * j] = 0;
@@ -569,7 +569,7 @@ struct WideSelect {
   // with run()'s passes.  -inf keys (a flood of unscored positions) are
   // counted by ballot.  Every thread calls both; the caller's earlier uses
   // of sh have completed (a barrier since).
-  __device__ void load_count(const float* __restrict__ vals, int n, Shared& sh) {
+  __device__ __forceinline__ void load_count(const float* __restrict__ vals, int n, Shared& sh) {
     const int tid = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vals), 0, n * 4, 0x00020000);
@@ -596,7 +596,7 @@ struct WideSelect {
   // caller clears sh.hist[0] before a barrier, then calls count(i) after
   // each set(i) (so the atomics follow the keys' loads as they arrive) and
   // count_done() once; run_counted() follows.
-  __device__ void count(int i, Shared& sh, int& ninf) {
+  __device__ __forceinline__ void count(int i, Shared& sh, int& ninf) {
     if (on(i)) {
       lane_max = max(lane_max, u[i]);
       lane_min = min(lane_min, u[i]);
@@ -604,12 +604,12 @@ struct WideSelect {
       else atomicAdd(&sh.hist[0][u[i] >> (32 - RB)], 1);
     }
   }
-  __device__ void count_done(Shared& sh, int ninf) {
+  __device__ __forceinline__ void count_done(Shared& sh, int ninf) {
     ninf = wave_incl_scan_dpp(ninf);
     if ((threadIdx.x & 63) == 63 && ninf) atomicAdd(&sh.hist[0][kNegInfKey >> (32 - RB)], ninf);
   }
 
-  __device__ int run_counted(int k, Shared& sh) {
+  __device__ __forceinline__ int run_counted(int k, Shared& sh) {
     uint32_t umax, umin;
     int nval;
     reduce_row<true>(sh, umax, umin, nval);   // (its barrier also completes load_count's atomics)
@@ -639,7 +639,7 @@ struct WideSelect {
   // candidate; a slot's taken keys here cost two ballots and two bit
   // counts).  The same output indices.  Ends with a barrier.
   template <typename Emit>
-  __device__ void place_uniform(Shared& sh, Emit&& emit) {
+  __device__ __forceinline__ void place_uniform(Shared& sh, Emit&& emit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     refresh();
     uint64_t bg[VPL], be[VPL];
@@ -684,7 +684,7 @@ struct WideSelect {
   // only its own taken keys (a few), instead of the wave stepping through
   // all VPL slots.  Ends with a barrier.
   template <typename Emit>
-  __device__ void place(Shared& sh, Emit&& emit) {
+  __device__ __forceinline__ void place(Shared& sh, Emit&& emit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t below = (1ull << lane) - 1ull;
     refresh();
