@@ -1245,7 +1245,8 @@ __global__ __launch_bounds__(kRT) void gather_cols_kernel(const float* __restric
 // finite scores and at most VPLC * 1024 entries (the usual case: the union
 // is a few percent of the history), the selection ranks the compacted union
 // lists of reuse_scores_kernel (VPLC keys per thread) instead of the whole
-// row (VPL keys per thread).  The keep largest are then finite union scores
+// row (VPL keys per thread); up to 2 VPLC * 1024 entries (the block modes,
+// whose previous final covers whole blocks) in a wider form of the same.  The keep largest are then finite union scores
 // either way, and the lists keep token order, so both paths select and
 // place the same entries (ties to the lower token).
 constexpr int kMaxTiles = kWideMax / kScoreTile;
@@ -1384,7 +1385,7 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out,
     uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0, ReuseAttn at = {}) {
   using WS = WideSelect<VPL, false>;
-  using WC = WideSelect<VPLC, false>;
+  using WC = WideSelect<2 * VPLC, false>;   // (the LDS of both compacted forms)
   __shared__ union {
     typename WS::Shared d;
     typename WC::Shared c;
@@ -1481,17 +1482,21 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     }
   };
   const int total = tile_off[n_tiles];
-  if (cscore && n_fin >= keep && total <= VPLC * kWideNT) {   // uniform across the workgroup
-    WC wc;
-    int tok[VPLC];
+  // the compacted union in registers, C keys per thread
+  auto compacted = [&](auto c) {
+    constexpr int C = decltype(c)::value;
+    using WU = WideSelect<C, false>;
+    auto& shc = *reinterpret_cast<typename WU::Shared*>(&sh.c);
+    WU wc;
+    int tok[C];
     const float* crow = cscore + static_cast<int64_t>(row) * c_ld;
     const int32_t* trow = ctok + static_cast<int64_t>(row) * c_ld;
 #pragma unroll
-    for (int i = 0; i < VPLC; ++i) {
-      const int p = WC::pos(i);
+    for (int i = 0; i < C; ++i) {
+      const int p = WU::pos(i);
       const bool ok = p < total;
       // the last tile whose list starts at or before p, in fixed steps
-      // (so the VPLC searches interleave instead of running one by one)
+      // (so the C searches interleave instead of running one by one)
       int lo = 0;
 #pragma unroll
       for (int step = kTileStep0; step > 0; step >>= 1) {
@@ -1504,14 +1509,21 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     }
     int ninf = 0;
 #pragma unroll
-    for (int i = 0; i < VPLC; ++i) wc.count(i, sh.c, ninf);
-    wc.count_done(sh.c, ninf);
+    for (int i = 0; i < C; ++i) wc.count(i, shc, ninf);
+    wc.count_done(shc, ninf);
     write_protected();
-    wc.run_counted(keep, sh.c);
+    wc.run_counted(keep, shc);
     uint64_t fin = 0;
 #pragma unroll
-    for (int i = 0; i < VPLC; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(wc.u[i]))) << i;
-    wc.place_uniform(sh.c, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
+    for (int i = 0; i < C; ++i) fin |= static_cast<uint64_t>(isfinite(sortable_f32(wc.u[i]))) << i;
+    wc.place_uniform(shc, [&](int, int p, int slot) { emit(tok[slot], p, (fin >> slot) & 1ull); });
+  };
+  // (uniform across the workgroup) a union of up to VPLC keys per thread, or
+  // up to twice that (the block modes' unions) in the wider form
+  if (cscore && n_fin >= keep && total <= VPLC * kWideNT) {
+    compacted(std::integral_constant<int, VPLC>{});
+  } else if (cscore && n_fin >= keep && total <= 2 * VPLC * kWideNT) {
+    compacted(std::integral_constant<int, 2 * VPLC>{});
   } else {
     WS ws;
     ws.load_count(scores + static_cast<int64_t>(row) * scores_ld, history, sh.d);   // first digit counted on load
@@ -2037,7 +2049,7 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
                     (k_strides[0] | k_strides[1] | k_strides[2]) % 8 == 0;
   if (attended) *attended = fuse ? 1 : 0;
   if (wide) {
-    // compacted unions of up to 1/8 of the row's width (at least 2048 entries)
+    // compacted unions of up to 1/8 of the row's width (at least 2048 entries), or twice that
     return with_wide_vpl(history, [&](auto vpl) {
       constexpr int VPL = decltype(vpl)::value;
       constexpr int VPLC = VPL / 8 > 2 ? VPL / 8 : 2;

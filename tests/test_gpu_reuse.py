@@ -120,6 +120,9 @@ def test_reuse_select_matches_oracle(dtype, b, h, t, sink, recent, frac, keep_se
     (8001, (0.4, 0.3, 0.1), 0.05),      # union ~60% of the row: beyond the compacted lists, the whole row is ranked
     (8001, (0.08, 0.0, 0.0), 0.05),     # union just above keep
     (30001, (0.06, 0.05, 0.02), 0.02),  # the bench's proportions
+    (8001, (0.3, 0.1, 0.05), 0.05),     # union ~40%: the wider compacted form (2048-4096 keys at this width)
+    (30001, (0.12, 0.08, 0.04), 0.02),  # union ~22%: the wider form at 32 keys per thread (4096-8192)
+    (40001, (0.15, 0.05, 0.02), 0.02),  # union ~21%: the wider form at 40 keys per thread (5120-10240)
 ])
 def test_reuse_select_union_sizes(t, dens, frac):
     gen = torch.Generator().manual_seed(t + int(100 * dens[0]))
@@ -136,14 +139,15 @@ def test_reuse_select_union_sizes(t, dens, frac):
 
 def test_reuse_select_exact_ties():
     # K rows repeat every 37 tokens, so union scores tie exactly: the lower
-    # token wins, whether the union is ranked compacted or over the whole row
+    # token wins, whether the union is ranked compacted (up to 2048 keys, the
+    # wider form up to 4096 at this width) or over the whole row
     gen = torch.Generator().manual_seed(12)
     q = torch.randn((1, 2, 128), generator=gen).to(torch.bfloat16)
     base = torch.randn((1, 2, 37, 128), generator=gen).to(torch.bfloat16)
-    t = 3701
-    k = base.repeat(1, 1, 101, 1)[:, :, :t].contiguous()
+    t = 5181
+    k = base.repeat(1, 1, 141, 1)[:, :, :t].contiguous()
     hist = t - 1
-    for dens in ((0.1, 0.05, 0.02), (0.7, 0.0, 0.0)):
+    for dens in ((0.1, 0.05, 0.02), (0.5, 0.0, 0.0), (0.9, 0.0, 0.0)):
         masks = [torch.rand((1, 2, hist), generator=gen) < p for p in dens]
         fi, fv, hf = Q.reuse_select(q.to(DEV), k.to(DEV), *(m.to(DEV) for m in masks), 0, 0, 0.03, False, 0.088)
         wi, wv, whf = R.reuse_select(f32(q), f32(k), *(m.numpy() for m in masks), 0, 0, 0.03, False, 0.088)
