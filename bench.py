@@ -815,9 +815,20 @@ def run_reuse(args) -> dict:
     # reads the previous final (block-expanded in the blk modes) the step reads
     fin_out = [torch.empty_like(steps[l].fin) for l in range(layers)]
 
+    fused_expand = block is not None and st0.bits   # the block expansion inside the selection's launch
+
     def run_select():
         for layer in range(layers):
             st, kk, _ = fixed(layer)
+            if fused_expand:
+                RU._lib.check(lib.qkv_reuse_select_bits_blocks(
+                    qs[layer].data_ptr(), kk.data_ptr(), RU._lib.strides(*kk.stride()), 0, b, hq, hkv,
+                    hist_fixed + 1, d, st.cand[0].data_ptr(), st.cand[1].data_ptr(), st.fin.data_ptr(),
+                    st.fin.stride(0), c["sink"], c["recent"], c["top_fraction"], 1, scaling, block,
+                    st.select_ws.data_ptr(), st.select_ws.numel() * 4, st.final_idx.data_ptr(),
+                    st.final_valid.data_ptr(), st.attn_ids.data_ptr(), n_out, fin_out[layer].data_ptr(),
+                    fin_out[layer].stride(0), RU._lib.stream_of(qs[layer])))
+                continue
             select = lib.qkv_reuse_select_bits if st.bits else lib.qkv_reuse_select
             extra = (None, None, None) if st.bits else ()   # the selection alone (no fused attention)
             RU._lib.check(select(
@@ -849,7 +860,10 @@ def run_reuse(args) -> dict:
         ("reuse_select", run_select, rows * hist_fixed * (3 + 4 + 1) + union * d * 2),
         ("token_attention", run_attn, rows * n_out * d * 2 * 2),
     ]
-    if block is not None:   # one byte read and one written per history position
+    if st0.bits:   # mask bits in words (and, with blocks, the expansion in the same launch)
+        plan[2] = ("reuse_select_expand" if fused_expand else "reuse_select", run_select,
+                   rows * hist_fixed * 4 + rows * hist_fixed // 2 + union * d * 2)
+    elif block is not None:   # one byte read and one written per history position
         plan.insert(3, ("reuse_expand_blocks", run_expand, rows * hist_fixed * 2))
     if lagged:
         test = RU.LAGGED_KINDS[st0.kind][0]

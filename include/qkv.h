@@ -412,6 +412,26 @@ int qkv_reuse_select_bits(const void* query, const void* key, const int64_t* k_s
                           uint64_t* history_final, int64_t history_final_ld, const void* value, void* out,
                           int* attended, void* stream);
 
+/* qkv_reuse_select_bits followed by qkv_reuse_expand_blocks in one launch,
+ * for the reuse...blk{bs} modes on bitsets (EV:4270-4316 with the block
+ * expansion of EV:2914-2922): the final selection's bitset is expanded to
+ * aligned blocks of `block` positions (1 <= block <= 4096) before it is
+ * stored in history_final, and final_indices / final_valid / attn_ids
+ * (optional) [rows, n_out] hold the expanded list exactly as
+ * qkv_reuse_expand_blocks writes it (n_out = qkv_reuse_block_final_count).
+ * Histories of at most 40960 positions (else QKV_ERR_UNSUPPORTED: run
+ * qkv_reuse_select on byte masks and qkv_reuse_expand_blocks).  Workspace:
+ * qkv_reuse_select_workspace_bytes.  No reference counterpart as a kernel
+ * (the reference expands in PyTorch after its selection). */
+int qkv_reuse_select_bits_blocks(const void* query, const void* key, const int64_t* k_strides, int dtype,
+                                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                 int64_t head_dim, const uint64_t* current, const uint64_t* previous,
+                                 const uint64_t* previous_final, int64_t words_ld, int64_t protect_sink,
+                                 int64_t protect_recent, double top_fraction, int keep_self, float scaling,
+                                 int64_t block, void* workspace, int64_t workspace_bytes, int64_t* final_indices,
+                                 uint8_t* final_valid, int32_t* attn_ids, int64_t n_out, uint64_t* history_final,
+                                 int64_t history_final_ld, void* stream);
+
 /* Workspace bytes of qkv_qabs_candidate_select (0 for histories of at most
  * 40960 positions, which one workgroup per row selects; -1 for bad sizes). */
 int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history, double candidate_fraction);

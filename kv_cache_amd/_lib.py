@@ -119,6 +119,9 @@ _PROTOTYPES = {
     "qkv_reuse_select_bits": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
                                      _i64, _i64, _f64, _i32, _f32, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
                                      _vp, _P(_i32), _vp]),
+    "qkv_reuse_select_bits_blocks": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
+                                            _i64, _i64, _i64, _f64, _i32, _f32, _i64, _vp, _i64, _vp, _vp, _vp,
+                                            _i64, _vp, _i64, _vp]),
 }
 
 _LIB = None

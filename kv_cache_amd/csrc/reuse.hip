@@ -1373,17 +1373,30 @@ __device__ __forceinline__ void reuse_attend(const int32_t* ids_s, int n, const 
   }
 }
 
+// The bits of positions [a, b) in 64-position word j.
+__device__ __forceinline__ uint64_t word_range_bits(int j, int a, int b) {
+  const int lo = max(a, 64 * j) - 64 * j, hi = min(b, 64 * j + 64) - 64 * j;
+  if (hi <= lo) return 0ull;
+  const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+  return upto & ~((1ull << lo) - 1ull);
+}
+
 // ATTN: the workgroup then attends over the row's final list (reuse_attend;
 // DT the K/V dtype, n_out <= kAttnList, head size 128).
 // BITS: hf is a bitset (64 positions per uint64 word, hf_ld in words),
 // assembled in LDS and stored once.
+// xblock > 0 (BITS only): the block modes' expansion in the same launch --
+// every aligned block of xblock positions holding a final bit is filled in
+// the LDS bitset before it is stored, and the index list is the expanded
+// one of reuse_expand_kernel (body_cap body entries, then the sink range,
+// the recent range and the current token; n_out = body_cap + those).
 template <int VPL, int VPLC, bool BITS = false, int DT = QKV_DTYPE_BF16, bool ATTN = false>
 __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     const float* __restrict__ scores, int64_t scores_ld, const float* __restrict__ cscore,
     const int32_t* __restrict__ ctok, const int32_t* __restrict__ ccnt, int n_tiles, int64_t c_ld, int keep,
     int history, int key_count, int sink_end, int recent_start, int rec_begin, int n_rec, int keep_self,
     int64_t* __restrict__ final_idx, uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out,
-    uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0, ReuseAttn at = {}) {
+    uint8_t* __restrict__ hf, int64_t hf_ld, int append = 0, ReuseAttn at = {}, int xblock = 0, int body_cap = 0) {
   using WS = WideSelect<VPL, false>;
   using WC = WideSelect<2 * VPLC, false>;   // (the LDS of both compacted forms)
   __shared__ union {
@@ -1420,13 +1433,8 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   // scatter below by the barriers of the selection (run) or of place
   auto write_protected = [&]() {
     if constexpr (BITS) {   // the protected ranges' bits of every word
-      auto range = [](int j, int a, int b) -> uint64_t {   // bits of [a, b) in word j
-        const int lo = max(a, 64 * j) - 64 * j, hi = min(b, 64 * j + 64) - 64 * j;
-        if (hi <= lo) return 0ull;
-        const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
-        return upto & ~((1ull << lo) - 1ull);
-      };
-      for (int j = tid; j < n_words; j += kWideNT) fin_s[j] = range(j, 0, sink_end) | range(j, recent_start, history);
+      for (int j = tid; j < n_words; j += kWideNT)
+        fin_s[j] = word_range_bits(j, 0, sink_end) | word_range_bits(j, recent_start, history);
       return;
     }
     const int body = (reinterpret_cast<uintptr_t>(hrow) & 15) ? 0 : (history & ~15);   // bytes in 16-byte stores
@@ -1466,12 +1474,14 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
   }
   __syncthreads();
   const int64_t o = static_cast<int64_t>(row) * n_out;
-  const bool staged = ATTN || n_out <= kAttnList;   // uniform
+  const bool expand = BITS && xblock > 0;                    // uniform
+  const bool staged = !expand && (ATTN || n_out <= kAttnList);   // uniform
   auto emit = [&](int idx, int p, bool valid) {
     if (valid) {
       if constexpr (BITS) atomicOr(&fin_s[idx >> 6], 1ull << (idx & 63));
       else hrow[idx] = 1;
     }
+    if (expand) return;   // the list is the expanded one, written below
     const bool fv = valid && (append || (idx >= sink_end && !(idx >= recent_start && idx < history)));
     if (staged) {
       ids_s[p] = fv ? idx : ~idx;
@@ -1535,17 +1545,78 @@ __global__ __launch_bounds__(kWideNT) void reuse_final_wide_kernel(
     ws.place(sh.d, [&](int idx, int p, int slot) { emit(idx, p, (fin >> slot) & 1ull); });
   }
   const int extra = sink_end + n_rec + keep_self;
+  const int list_at = expand ? body_cap : keep;   // where the protected entries go
   for (int i = tid; i < extra; i += kWideNT) {
     const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
     if (staged) {
       ids_s[keep + i] = idx;
     } else {
-      final_idx[o + keep + i] = idx;
-      final_valid[o + keep + i] = 1;
-      if (attn_ids) attn_ids[o + keep + i] = idx;
+      final_idx[o + list_at + i] = idx;
+      final_valid[o + list_at + i] = 1;
+      if (attn_ids) attn_ids[o + list_at + i] = idx;
     }
   }
   if (BITS || staged) __syncthreads();   // every emit is done (the selection's LDS is free)
+  if constexpr (BITS) {
+    if (expand) {
+      // thread j of a round owns block j0 + j: tests the block's bits, fills
+      // a hit block (LDS atomics: several blocks share a word, and a block's
+      // bits are changed only by its own thread), and lists its positions
+      // outside the protected ranges in ascending order (as reuse_expand_kernel)
+      int* run_off = reinterpret_cast<int*>(&sh);
+      int* run_lo = run_off + kWideNT;
+      int* wave_tot = run_lo + kWideNT;
+      const int lane = tid & 63, wave = tid >> 6;
+      const int nblk = (history + xblock - 1) / xblock;
+      int base = 0;
+      for (int j0 = 0; j0 < nblk; j0 += kWideNT) {
+        const int j = j0 + tid;
+        int lo = 0, hi = 0;
+        if (j < nblk) {
+          const int b_lo = j * xblock, b_hi = min(b_lo + xblock, history);
+          const int w_lo = b_lo >> 6, w_hi = (b_hi - 1) >> 6;
+          uint64_t any = 0;
+          for (int w = w_lo; w <= w_hi; ++w) any |= fin_s[w] & word_range_bits(w, b_lo, b_hi);
+          if (any) {
+            for (int w = w_lo; w <= w_hi; ++w) atomicOr(&fin_s[w], word_range_bits(w, b_lo, b_hi));
+            lo = max(b_lo, sink_end);
+            hi = min(b_hi, recent_start);
+          }
+        }
+        const int cnt = hi > lo ? hi - lo : 0;
+        const int incl = wave_incl_scan_dpp(cnt);
+        run_off[tid] = incl - cnt;
+        run_lo[tid] = lo;
+        if (lane == 63) wave_tot[wave] = incl;
+        __syncthreads();
+        int wave_base = base, total = 0;
+#pragma unroll
+        for (int w = 0; w < kWideNT / 64; ++w) {
+          const int x = wave_tot[w];
+          wave_base += w < wave ? x : 0;
+          total += x;
+        }
+        const int w64 = wave * 64, wave_cnt = wave_tot[wave];
+        for (int q = lane; q < wave_cnt && wave_base + q < body_cap; q += 64) {
+          int k = 0;   // the last lane whose run starts at or before q
+#pragma unroll
+          for (int step = 32; step > 0; step >>= 1) k += run_off[w64 + k + step] <= q ? step : 0;
+          const int t = run_lo[w64 + k] + (q - run_off[w64 + k]);
+          const int64_t e = o + wave_base + q;
+          final_idx[e] = t;
+          final_valid[e] = 1;
+          if (attn_ids) attn_ids[e] = t;
+        }
+        base += total;
+        __syncthreads();   // (run_off, wave_tot and the filled words before the next round and the store)
+      }
+      for (int p = min(base, body_cap) + tid; p < body_cap; p += kWideNT) {
+        final_idx[o + p] = 0;
+        final_valid[o + p] = 0;
+        if (attn_ids) attn_ids[o + p] = -1;
+      }
+    }
+  }
   if (staged) {
     for (int p = tid; p < n_out; p += kWideNT) {
       const int v = ids_s[p];
@@ -1998,7 +2069,7 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
                       double top_fraction, int keep_self, float scaling, void* workspace, int64_t workspace_bytes,
                       int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids, int64_t n_out,
                       uint8_t* history_final, int64_t history_final_ld, void* stream, const void* value = nullptr,
-                      void* out = nullptr, int* attended = nullptr) {
+                      void* out = nullptr, int* attended = nullptr, int64_t xblock = 0) {
   int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
   if (rc) return rc;
   if (!query || !key || !k_strides || !current || !workspace || !final_indices || !final_valid || !history_final)
@@ -2014,9 +2085,22 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
     return fail(QKV_ERR_INVALID, "%s: bitsets must be 8-byte aligned", what);
   if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
   const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
-  if (n_out != c.n_out)
+  int64_t body_cap = 0;
+  if (xblock) {   // the block expansion in the final selection's launch (bitsets of rows up to kWideMax)
+    if (xblock < 1 || xblock > kMaxExpandBlock)
+      return fail(QKV_ERR_INVALID, "%s: block must be in [1, %d]", what, kMaxExpandBlock);
+    if (!bits || history > kWideMax)
+      return fail(QKV_ERR_UNSUPPORTED, "%s: the expansion runs on bitsets of at most %d history tokens", what,
+                  kWideMax);
+    body_cap = block_body_cap(c, xblock);
+    const int64_t need_out = body_cap + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+    if (n_out != need_out)
+      return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the expanded selection needs %lld", what,
+                  (long long)n_out, (long long)need_out);
+  } else if (n_out != c.n_out) {
     return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the selection needs %lld", what,
                 (long long)n_out, (long long)c.n_out);
+  }
   const int64_t rows = batch * q_heads;
   const int64_t need = reuse_ws_bytes(rows, history, c.keep);
   if (need < 0 || workspace_bytes < need)
@@ -2043,7 +2127,7 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
   if (rc) return rc;
   // the final selection's workgroup also attends over the row's list (one launch less) where it
   // holds the list: 16-bit K/V rows of 128 channels, 16-byte aligned, V laid out as K
-  const bool fuse = out && value && bits && wide && n_out <= kAttnList && head_dim == 128 &&
+  const bool fuse = !xblock && out && value && bits && wide && n_out <= kAttnList && head_dim == 128 &&
                     (dtype == QKV_DTYPE_BF16 || dtype == QKV_DTYPE_FP16) && k_strides[3] == 1 &&
                     aligned(key, 16) && aligned(value, 16) && aligned(query, 16) && aligned(out, 16) &&
                     (k_strides[0] | k_strides[1] | k_strides[2]) % 8 == 0;
@@ -2064,7 +2148,8 @@ int reuse_select_impl(const char* what, bool bits, const void* query, const void
                 static_cast<int>(history), static_cast<int>(key_count),
                 static_cast<int>(c.sink_end), static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin),
                 static_cast<int>(c.n_rec), keep_self ? 1 : 0, final_indices, final_valid, attn_ids,
-                static_cast<int>(n_out), history_final, history_final_ld, 0, at);
+                static_cast<int>(n_out), history_final, history_final_ld, 0, at, static_cast<int>(xblock),
+                static_cast<int>(body_cap));
         return check_launch(what);
       };
       using BF = std::integral_constant<int, QKV_DTYPE_BF16>;
@@ -2122,6 +2207,25 @@ QKV_EXPORT int qkv_reuse_select_bits(const void* query, const void* key, const i
                            words_ld, protect_sink, protect_recent, top_fraction, keep_self, scaling, workspace,
                            workspace_bytes, final_indices, final_valid, attn_ids, n_out,
                            reinterpret_cast<uint8_t*>(history_final), history_final_ld, stream, value, out, attended);
+}
+
+QKV_EXPORT int qkv_reuse_select_bits_blocks(const void* query, const void* key, const int64_t* k_strides, int dtype,
+                                            int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t key_count,
+                                            int64_t head_dim, const uint64_t* current, const uint64_t* previous,
+                                            const uint64_t* previous_final, int64_t words_ld, int64_t protect_sink,
+                                            int64_t protect_recent, double top_fraction, int keep_self,
+                                            float scaling, int64_t block, void* workspace, int64_t workspace_bytes,
+                                            int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                                            int64_t n_out, uint64_t* history_final, int64_t history_final_ld,
+                                            void* stream) {
+  if (block < 1) return fail(QKV_ERR_INVALID, "qkv_reuse_select_bits_blocks: block must be >= 1");
+  return reuse_select_impl("qkv_reuse_select_bits_blocks", true, query, key, k_strides, dtype, batch, q_heads,
+                           kv_heads, key_count, head_dim, reinterpret_cast<const uint8_t*>(current),
+                           reinterpret_cast<const uint8_t*>(previous), reinterpret_cast<const uint8_t*>(previous_final),
+                           words_ld, protect_sink, protect_recent, top_fraction, keep_self, scaling, workspace,
+                           workspace_bytes, final_indices, final_valid, attn_ids, n_out,
+                           reinterpret_cast<uint8_t*>(history_final), history_final_ld, stream, nullptr, nullptr,
+                           nullptr, block);
 }
 
 QKV_EXPORT int64_t qkv_qabs_candidate_select_workspace_bytes(int64_t rows, int64_t history,

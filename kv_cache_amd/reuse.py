@@ -64,6 +64,11 @@ def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool, int | None]:
     return int(m.group(1)), frac, not mode.endswith("reusefinal"), not mode.endswith("reuse2set"), block
 
 
+# Rows of at most this many history positions have their block expansion run by
+# the final selection's launch on bitsets (one 1024-thread workgroup per row
+# holds the row's bitset in LDS); longer capacities keep byte masks.
+BLOCK_BITS_MAX_HISTORY = 40960
+
 CANDIDATE_SELECTIONS = {"topk": 0, "sample_quantile": 1, "previous_threshold": 2}   # QKV_CAND_*
 
 
@@ -323,9 +328,10 @@ class ReuseDecodeStep:
         cap = self.capacity
         self.rows = rows
         self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
-        # candidate and final masks: bitsets (64 positions per int64 word) for the
-        # plain reuse modes; byte masks where block expansion or a lagged step reads them
-        self.bits = self._BITSET and self.block is None
+        # candidate and final masks: bitsets (64 positions per int64 word); byte
+        # masks where a lagged step reads them, and for the block modes past the
+        # rows whose expansion runs in the final selection's launch
+        self.bits = self._BITSET and (self.block is None or cap - 1 <= BLOCK_BITS_MAX_HISTORY)
         if self.bits:
             words = -(-cap // 64)
             self.cand = [torch.zeros((rows, words), dtype=torch.int64, device=device) for _ in range(2)]
@@ -494,6 +500,18 @@ class ReuseDecodeStep:
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
         ids = self.attn_ids[: self.rows * n_out]
         bits = current.dtype == torch.int64
+        if bits and self.block is not None:   # the selection and its block expansion in one launch
+            with torch.cuda.device(q.device):
+                _lib.check(lib.qkv_reuse_select_bits_blocks(
+                    q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch,
+                    self.q_heads, self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
+                    _lib.ptr(previous_final), current.stride(0), self.sink, self.recent, self.top_fraction,
+                    int(self.keep_self), float(scaling), self.block, self.select_ws.data_ptr(),
+                    self.select_ws.numel() * 4, self.final_idx.data_ptr(), self.final_valid.data_ptr(),
+                    ids.data_ptr(), n_out, self.fin.data_ptr(), self.fin.stride(0), _lib.stream_of(q)))
+            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+            self.n_out = n_out
+            return
         # on bitsets the final selection's workgroups can also run the attention
         attended = ctypes.c_int(0)
         extra = ((value.data_ptr(), self.out.data_ptr(), ctypes.byref(attended)) if self.fused_attention

@@ -682,6 +682,97 @@ def test_expand_blocks_matches_oracle(rows, history, block, sink, recent, keep_s
         assert np.all(np.diff(idx[r, :body][valid[r, :body]]) > 0), r      # ascending body
 
 
+@pytest.mark.parametrize("hist,sink,recent,frac,prev,dens,block,keep_self,dtype", [
+    (3000, 4, 8, 0.02, True, 0.03, 16, True, torch.bfloat16),
+    (32768, 10, 10, 0.02, True, 0.03, 16, True, torch.bfloat16),   # the bench's blk16 proportions
+    (40960, 10, 10, 0.02, True, 0.03, 100, True, torch.bfloat16),  # the longest row; blocks across words
+    (5000, 0, 0, 0.05, False, 0.1, 1, False, torch.float16),       # blocks of one position: no expansion
+    (9000, 3, 5, 0.02, True, 0.03, 4096, True, torch.bfloat16),    # the largest block
+    (777, 0, 0, 0.3, True, 0.03, 64, True, torch.bfloat16),        # keep above the union
+    (10000, 20, 30, 0.05, True, 0.25, 8, True, torch.bfloat16),    # a union past the compacted forms
+    (12345, 10, 10, 0.02, True, 0.03, 24, False, torch.bfloat16),
+])
+def test_reuse_select_bits_blocks_equals_bytes(hist, sink, recent, frac, prev, dens, block, keep_self, dtype):
+    # the selection and its block expansion in one launch on bitsets against
+    # qkv_reuse_select + qkv_reuse_expand_blocks on the same masks as bytes:
+    # the same expanded list, validity, attention ids and expanded final mask
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(hist + block)
+    b, hq, hkv, d = 1, 8, 2, 128
+    rows, t = b * hq, hist + 1
+    q = torch.randn((b, hq, d), generator=gen).to(dtype).to(DEV)
+    k = torch.randn((b, hkv, t, d), generator=gen).to(dtype).to(DEV)
+    masks = [(torch.rand((rows, hist), generator=gen) < dens).to(DEV) for _ in range(3)]
+    n_w = -(-hist // 64)
+
+    def to_words(m):
+        pad = torch.zeros((rows, n_w * 64), dtype=torch.bool, device=DEV)
+        pad[:, :hist] = m
+        by = (pad.view(rows, -1, 8).to(torch.uint8) << torch.arange(8, dtype=torch.uint8, device=DEV)).sum(-1)
+        return by.to(torch.uint8).contiguous().view(torch.int64)
+
+    n_sel = int(lib.qkv_reuse_final_count(hist, sink, recent, frac, int(keep_self)))
+    n_out = int(lib.qkv_reuse_block_final_count(hist, block, sink, recent, frac, int(keep_self)))
+    ws = torch.empty((lib.qkv_reuse_select_workspace_bytes(rows, hist, frac) + 3) // 4, device=DEV)
+    outs = []
+    for bits in (False, True):
+        ms = [to_words(m) if bits else m.to(torch.uint8).contiguous() for m in masks]
+        fin = torch.zeros_like(ms[2]) if bits else torch.zeros((rows, hist), dtype=torch.uint8, device=DEV)
+        fi = torch.full((rows, n_out), 7, dtype=torch.int64, device=DEV)
+        fv = torch.full((rows, n_out), 7, dtype=torch.uint8, device=DEV)
+        ids = torch.full((rows, n_out), 7, dtype=torch.int32, device=DEV)
+        head = (q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), _lib.DTYPE_CODES[dtype], b, hq, hkv, t, d,
+                ms[0].data_ptr(), ms[1].data_ptr() if prev else None, ms[2].data_ptr(), ms[0].stride(0), sink,
+                recent, frac, int(keep_self), 0.088)
+        if bits:
+            _lib.check(lib.qkv_reuse_select_bits_blocks(
+                *head, block, ws.data_ptr(), ws.numel() * 4, fi.data_ptr(), fv.data_ptr(), ids.data_ptr(), n_out,
+                fin.data_ptr(), fin.stride(0), _lib.stream_of(q)))
+        else:
+            _lib.check(lib.qkv_reuse_select(*head, ws.data_ptr(), ws.numel() * 4, fi.data_ptr(), fv.data_ptr(),
+                                            ids.data_ptr(), n_sel, fin.data_ptr(), fin.stride(0), _lib.stream_of(q)))
+            _lib.check(lib.qkv_reuse_expand_blocks(fin.data_ptr(), fin.stride(0), rows, t, block, sink, recent, frac,
+                                                   int(keep_self), fi.data_ptr(), fv.data_ptr(), ids.data_ptr(),
+                                                   n_out, _lib.stream_of(q)))
+        hf = RU.expand_bits(fin, hist) if bits else fin.bool()
+        outs.append((fi, fv, ids, hf))
+    for a, w in zip(*outs):
+        assert torch.equal(a, w)
+    if bits:   # nothing set past the history in the last word
+        tail = RU.expand_bits(fin, n_w * 64)[:, hist:]
+        assert int(tail.count_nonzero()) == 0
+
+
+def test_reuse_select_bits_blocks_rejects():
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    hist = 40961
+    rows, t = 2, hist + 1
+    q = torch.zeros((1, 2, 128), dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros((1, 1, t, 128), dtype=torch.bfloat16, device=DEV)
+    words = torch.zeros((rows, -(-hist // 64)), dtype=torch.int64, device=DEV)
+    ws = torch.empty((lib.qkv_reuse_select_workspace_bytes(rows, hist, 0.02) + 3) // 4, device=DEV)
+    out = torch.empty(rows * 8192, dtype=torch.int64, device=DEV)
+    n_out = int(lib.qkv_reuse_block_final_count(hist, 16, 0, 0, 0.02, 1))
+
+    def call(block, n, key_count=t):
+        return lib.qkv_reuse_select_bits_blocks(
+            q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), 0, 1, 2, 1, key_count, 128, words.data_ptr(),
+            None, None, words.stride(0), 0, 0, 0.02, 1, 0.088, block, ws.data_ptr(), ws.numel() * 4, out.data_ptr(),
+            out.data_ptr(), None, n, words.data_ptr(), words.stride(0), _lib.stream_of(q))
+
+    unsupported, invalid = -3, -1   # QKV_ERR_UNSUPPORTED, QKV_ERR_INVALID
+    assert call(16, n_out) == unsupported   # past the rows held in one workgroup
+    assert call(5000, n_out) == invalid     # block beyond 4096
+    assert call(0, n_out) == invalid
+    n_small = int(lib.qkv_reuse_block_final_count(4000, 16, 0, 0, 0.02, 1))
+    assert call(16, n_small + 1, 4001) == invalid   # index rows of the wrong width
+    torch.cuda.synchronize()
+
+
 def test_expand_blocks_rejects_bad_arguments():
     m = torch.zeros((2, 100), dtype=torch.uint8, device=DEV)
     with pytest.raises(RuntimeError, match="block must be"):
