@@ -723,7 +723,7 @@ def run_reuse(args) -> dict:
     hist_fixed = hist - 1
     cur, prev, fin = st0.cand[1 - st0.flip], st0.cand[st0.flip], st0.fin
     if lagged:   # the union the lagged step reranked (previous final | candidates | protected ranges)
-        union = int(st0.union[:, :hist_fixed].count_nonzero())
+        union = int((RU.expand_bits(st0.union, hist_fixed) if st0.bits else st0.union[:, :hist_fixed]).count_nonzero())
     elif st0.bits:
         union = int(RU.expand_bits((cur | prev) | fin, hist_fixed).count_nonzero())
     else:
@@ -885,11 +885,13 @@ def run_reuse(args) -> dict:
                 RU.lag_union(st.cand[0], st.fin, st.flags, b, hq, hist_fixed, refresh, share, c["sink"], c["recent"],
                              st.union)
 
-        # candidates and previous final read, union written per position
-        plan.insert(2, ("lag_union", run_union, rows * hist_fixed * 3))
+        # candidates and previous final read, union written per position (bits or bytes)
+        plan.insert(2, ("lag_union", run_union, rows * hist_fixed * 3 // (8 if st0.bits else 1)))
         if test is not None:   # ess: the mask row, then the K row of every previous final token
-            fin_tokens = int(st0.fin[:, :hist_fixed].count_nonzero())
-            plan.insert(0, ("lag_flags", run_flags, rows * hist_fixed + fin_tokens * d * 2 if test == "ess"
+            fin_tokens = int((RU.expand_bits(st0.fin, hist_fixed) if st0.bits else st0.fin[:, :hist_fixed])
+                             .count_nonzero())
+            plan.insert(0, ("lag_flags", run_flags,
+                            rows * hist_fixed // (8 if st0.bits else 1) + fin_tokens * d * 2 if test == "ess"
                             else rows * (d * 2 + s_dims * 16)))
         # partial scores and candidate mask of the rows that refresh only
         flagged = int(st0.flags.count_nonzero())
@@ -900,12 +902,13 @@ def run_reuse(args) -> dict:
             for layer in range(layers):
                 st = steps[layer]
                 RU.lag_candidates(qs[layer], st.kdm, hist_fixed, s_dims, requested, st.flags, refresh, st.partial,
-                                  st.cand[0], mask_ws[layer])
+                                  st.cand[0], st.cand_ws if st.bits else mask_ws[layer])
 
         plan = [p for p in plan if p[0] not in ("reuse_partial_scores", mask_name)]
         if refresh != "none":
             plan.insert(1 if test is not None else 0,
-                        ("lag_candidates", run_cands, n_fresh * hist_fixed * (s_dims * 2 + 4 + 4 + 1)))
+                        ("lag_candidates", run_cands, n_fresh * hist_fixed * (s_dims * 2 + 4 + 4) +
+                         n_fresh * hist_fixed // (8 if st0.bits else 1)))
     kernels = {}
     for name, fn, nbytes in plan:
         gk = graph_of(repeated(fn))

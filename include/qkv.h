@@ -579,6 +579,34 @@ int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_final, int64_t
                         int64_t protect_sink, int64_t protect_recent, uint8_t* union_out, int64_t union_ld,
                         void* stream);
 
+/* The lagged modes' three calls on bitset state (bit t % 64 of uint64 word
+ * t / 64, row strides in words, 8-byte aligned), everything else as the
+ * byte-mask calls above; no reference counterparts as kernels (the
+ * reference keeps these masks as torch bool tensors, EV:4020-4198).
+ * qkv_reuse_lag_flags_bits: QKV_LAG_ESS reads previous_final as a bitset.
+ * qkv_reuse_lag_candidates_bits: the candidate bits of the refreshing rows
+ * (the rows that do not refresh are left as they were), with the workspace
+ * of qkv_reuse_candidates_workspace_bytes(batch * q_heads, history, k)
+ * bytes, zero-filled before the first call and left zero by every call
+ * (rows of up to 40960 positions select across several workgroups).
+ * qkv_reuse_lag_union_bits: the union of qkv_reuse_lag_union into a bitset
+ * (words past the history are not written). */
+int qkv_reuse_lag_flags_bits(const void* query, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             int64_t head_dim, int64_t dim_count, int test, const int32_t* previous_dims,
+                             const float* previous_values, int32_t* dims_out, float* values_out, const void* key,
+                             const int64_t* k_strides, int64_t history, const uint64_t* previous_final,
+                             int64_t words_ld, float scaling, float ess_threshold, uint8_t* flags, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+int qkv_reuse_lag_candidates_bits(const void* query, const void* key_dim_major, const int64_t* kdm_strides,
+                                  int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t history,
+                                  int64_t head_dim, int64_t dim_count, int64_t k, const uint8_t* flags, int refresh,
+                                  float* partial, int64_t partial_ld, uint64_t* bits, int64_t bits_ld,
+                                  void* workspace, int64_t workspace_bytes, void* stream);
+int qkv_reuse_lag_union_bits(uint64_t* current, const uint64_t* previous_final, int64_t words_ld,
+                             const uint8_t* flags, int64_t batch, int64_t q_heads, int64_t history, int refresh,
+                             int share, int64_t protect_sink, int64_t protect_recent, uint64_t* union_out,
+                             int64_t union_ld, void* stream);
+
 /* Entries per row of the final index list of a block-expanded reuse step
  * (the qabs{S}cand{pct}reuse[final|2set]blk{block} modes): body + sink
  * range + recent range (not overlapping the sink) + 1 when keep_self, where

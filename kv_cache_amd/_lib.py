@@ -85,6 +85,12 @@ _PROTOTYPES = {
     "qkv_reuse_lag_candidates": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
                                         _i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
     "qkv_reuse_lag_union": (_i32, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64, _vp]),
+    "qkv_reuse_lag_flags_bits": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
+                                        _P(_i64), _i64, _vp, _i64, _f32, _f32, _vp, _vp, _i64, _vp]),
+    "qkv_reuse_lag_candidates_bits": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                             _vp, _i32, _vp, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "qkv_reuse_lag_union_bits": (_i32, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64,
+                                        _vp]),
     "qkv_reuse_block_final_count": (_i64, [_i64, _i64, _i64, _i64, _f64, _i32]),
     "qkv_reuse_expand_blocks": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _f64, _i32, _vp, _vp, _vp, _i64,
                                        _vp]),

@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kLagNT) void lag_flags_kernel(
 // kLagPass mask bytes in LDS and spreads their dot products over the
 // workgroup.  Each workgroup leaves (max, sum e, sum e^2, count) of its span
 // in part[row * splits + split]; lag_ess_merge_kernel combines them.
-template <int DT>
+// BITS: prev_final is a bitset (mask_ld words per row).
+template <int DT, bool BITS = false>
 __global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
     const typename Elem<DT>::T* __restrict__ query, int q_heads, int group, int head_dim, int count,
     int32_t* __restrict__ dims_out, float* __restrict__ vals_out, const typename Elem<DT>::T* __restrict__ key,
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
   }
   const int bq = row / q_heads, kvh = (row - bq * q_heads) / group;
   const E* krow = key + bq * sb + kvh * sh;
-  const uint8_t* mrow = prev_final + static_cast<int64_t>(row) * mask_ld;
+  const uint8_t* mrow = prev_final + static_cast<int64_t>(row) * mask_ld * (BITS ? 8 : 1);
   float m_t = -INFINITY, z_t = 0.f, z2_t = 0.f;
   int total = 0;
   const int p_begin = split * span, p_end = min(history, p_begin + span);
@@ -164,7 +165,12 @@ __global__ __launch_bounds__(kLagNT) void lag_ess_kernel(
     const int p = p0 + tid * 16;
     const int n = min(16, p_end - p);
     uint32_t bm = 0;
-    if (mvec && n == 16) {
+    if constexpr (BITS) {   // positions p .. p + 15 lie in one word (p is a multiple of 16)
+      if (n > 0) {
+        const uint64_t w = reinterpret_cast<const uint64_t*>(mrow)[p >> 6];
+        bm = static_cast<uint32_t>(w >> (p & 63)) & (n >= 16 ? 0xFFFFu : ((1u << n) - 1u));
+      }
+    } else if (mvec && n == 16) {
       bm = nonzero_bytes(*reinterpret_cast<const uint4*>(mrow + p));
     } else {
       for (int j = 0; j < n; ++j)
@@ -341,6 +347,49 @@ __global__ __launch_bounds__(kLagNT) void lag_union_kernel(
   store16(uni + static_cast<int64_t>(r) * uni_ld, p, n, vec, u);
 }
 
+// lag_union_kernel on bitsets: one thread per 64-position word.
+__global__ __launch_bounds__(kLagNT) void lag_union_bits_kernel(
+    uint64_t* __restrict__ cur, const uint64_t* __restrict__ prev_final, int64_t words_ld,
+    const uint8_t* __restrict__ flags, int rows, int q_heads, int history, int refresh, int share, int sink_end,
+    int recent_start, uint64_t* __restrict__ uni, int64_t uni_ld) {
+  __shared__ int cnt_s[kLagWaves];
+  const int r = blockIdx.y, tid = threadIdx.x;
+  const int b = r / q_heads;
+  bool all = refresh == QKV_REFRESH_ALL;
+  if (refresh == QKV_REFRESH_ANY || refresh == QKV_REFRESH_MAJORITY) {
+    int c = 0;
+    for (int i = tid; i < rows; i += kLagNT) c += flags[i] ? 1 : 0;
+    c = wave_sum_i(c);
+    if ((tid & 63) == 0) cnt_s[tid >> 6] = c;
+    __syncthreads();
+    int t = 0;
+    for (int w = 0; w < kLagWaves; ++w) t += cnt_s[w];
+    all = refresh == QKV_REFRESH_ANY ? t > 0 : 2 * t > rows;   // EV:4057-4066
+  }
+  const bool per_row = refresh == QKV_REFRESH_PER_ROW;
+  const int w = blockIdx.x * kLagNT + tid;
+  if (w >= (history + 63) / 64) return;
+  // the sink and recent ranges (EV:4166-4171)
+  auto range = [&](int a, int e) -> uint64_t {
+    const int lo = max(a, 64 * w) - 64 * w, hi = min(e, 64 * w + 64) - 64 * w;
+    if (hi <= lo) return 0ull;
+    const uint64_t upto = hi >= 64 ? ~0ull : ((1ull << hi) - 1ull);
+    return upto & ~((1ull << lo) - 1ull);
+  };
+  uint64_t u = range(0, sink_end) | range(recent_start, history);
+  if (share) {   // the candidates of every refreshed row of the sequence (EV:4107-4109)
+    for (int h = 0; h < q_heads; ++h) {
+      const int i = b * q_heads + h;
+      if (per_row ? flags[i] != 0 : all) u |= cur[static_cast<int64_t>(i) * words_ld + w];
+    }
+  }
+  uint64_t* crow = cur + static_cast<int64_t>(r) * words_ld;
+  if (per_row ? flags[r] != 0 : all) u |= crow[w];
+  else crow[w] = 0;   // a row that does not refresh has no candidates
+  if (prev_final) u |= prev_final[static_cast<int64_t>(r) * words_ld + w];
+  uni[static_cast<int64_t>(r) * uni_ld + w] = u;
+}
+
 // Spans of the ESS test: about kLagWGs workgroups over the rows, each span a
 // whole number of passes.
 struct EssSplit {
@@ -357,7 +406,7 @@ template <int DT> struct RunLagFlags {
   static int run(const void* q, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int count, int test,
                  const int32_t* pd, const float* pv, int32_t* dims_out, float* vals_out, const void* key,
                  const int64_t* ks, int64_t history, const uint8_t* prev_final, int64_t mask_ld, float scaling,
-                 float ess_threshold, uint8_t* flags, void* workspace, hipStream_t st) {
+                 float ess_threshold, uint8_t* flags, void* workspace, hipStream_t st, bool bits = false) {
     using E = typename Elem<DT>::T;
     const char* what = "qkv_reuse_lag_flags";
     if (test != QKV_LAG_ESS) {
@@ -370,10 +419,17 @@ template <int DT> struct RunLagFlags {
     const bool mvec = aligned(prev_final, 16) && mask_ld % 16 == 0;
     const EssSplit sp = ess_split(B * Hq, history);
     float4* part = static_cast<float4*>(workspace);
-    lag_ess_kernel<DT><<<dim3(static_cast<unsigned>(sp.splits), static_cast<unsigned>(B * Hq)), kLagNT, 0, st>>>(
-        static_cast<const E*>(q), static_cast<int>(Hq), static_cast<int>(Hq / Hkv), static_cast<int>(D), count,
-        dims_out, vals_out, static_cast<const E*>(key), ks[0], ks[1], ks[2], kvec, static_cast<int>(history),
-        sp.span, prev_final, mask_ld, mvec, scaling, part);
+    const dim3 grid(static_cast<unsigned>(sp.splits), static_cast<unsigned>(B * Hq));
+    if (bits)
+      lag_ess_kernel<DT, true><<<grid, kLagNT, 0, st>>>(
+          static_cast<const E*>(q), static_cast<int>(Hq), static_cast<int>(Hq / Hkv), static_cast<int>(D), count,
+          dims_out, vals_out, static_cast<const E*>(key), ks[0], ks[1], ks[2], kvec, static_cast<int>(history),
+          sp.span, prev_final, mask_ld, false, scaling, part);
+    else
+      lag_ess_kernel<DT><<<grid, kLagNT, 0, st>>>(
+          static_cast<const E*>(q), static_cast<int>(Hq), static_cast<int>(Hq / Hkv), static_cast<int>(D), count,
+          dims_out, vals_out, static_cast<const E*>(key), ks[0], ks[1], ks[2], kvec, static_cast<int>(history),
+          sp.span, prev_final, mask_ld, mvec, scaling, part);
     int rc = check_launch(what);
     if (rc) return rc;
     lag_ess_merge_kernel<<<static_cast<unsigned>(cdiv(B * Hq, kLagNT)), kLagNT, 0, st>>>(
@@ -449,5 +505,66 @@ QKV_EXPORT int qkv_reuse_lag_union(uint8_t* current, const uint8_t* previous_fin
   lag_union_kernel<<<grid, kLagNT, 0, static_cast<hipStream_t>(stream)>>>(
       current, previous_final, mask_ld, flags, static_cast<int>(batch * q_heads), static_cast<int>(q_heads),
       static_cast<int>(history), refresh, share ? 1 : 0, sink_end, recent_start, union_out, union_ld, vec);
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_reuse_lag_flags_bits(const void* query, int dtype, int64_t batch, int64_t q_heads,
+                                        int64_t kv_heads, int64_t head_dim, int64_t dim_count, int test,
+                                        const int32_t* previous_dims, const float* previous_values, int32_t* dims_out,
+                                        float* values_out, const void* key, const int64_t* k_strides,
+                                        int64_t history, const uint64_t* previous_final, int64_t words_ld,
+                                        float scaling, float ess_threshold, uint8_t* flags, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  const char* what = "qkv_reuse_lag_flags_bits";
+  if (test == QKV_LAG_ESS) {
+    if (!previous_final || !aligned(previous_final, 8))
+      return fail(QKV_ERR_INVALID, "%s: the ESS test needs the previous final bitset (8-byte aligned)", what);
+    if (history <= 0 || history >= (int64_t(1) << 30) || words_ld < (history + 63) / 64)
+      return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^30 and words_ld covering the history", what);
+  }
+  if (test != QKV_LAG_ESS)   // the other tests read no mask
+    return qkv_reuse_lag_flags(query, dtype, batch, q_heads, kv_heads, head_dim, dim_count, test, previous_dims,
+                               previous_values, dims_out, values_out, key, k_strides, history, nullptr, 0, scaling,
+                               ess_threshold, flags, workspace, workspace_bytes, stream);
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || batch * q_heads > 65535)
+    return fail(QKV_ERR_INVALID, "%s: need batch * q_heads <= 65535, q_heads a positive multiple of kv_heads", what);
+  if (head_dim <= 0 || head_dim > 128) return fail(QKV_ERR_UNSUPPORTED, "%s: head_dim must be in [1, 128]", what);
+  if (!query || !dims_out || !values_out || !flags || !key || !k_strides)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (k_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: K channels must be contiguous", what);
+  const int64_t need = qkv_reuse_lag_flags_workspace_bytes(batch * q_heads, history);
+  if (!workspace || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1), head_dim));
+  return dispatch_dtype<RunLagFlags>(dtype, query, batch, q_heads, kv_heads, head_dim, count, test, previous_dims,
+                                     previous_values, dims_out, values_out, key, k_strides, history,
+                                     reinterpret_cast<const uint8_t*>(previous_final), words_ld, scaling,
+                                     ess_threshold, flags, workspace, static_cast<hipStream_t>(stream), true);
+}
+
+QKV_EXPORT int qkv_reuse_lag_union_bits(uint64_t* current, const uint64_t* previous_final, int64_t words_ld,
+                                        const uint8_t* flags, int64_t batch, int64_t q_heads, int64_t history,
+                                        int refresh, int share, int64_t protect_sink, int64_t protect_recent,
+                                        uint64_t* union_out, int64_t union_ld, void* stream) {
+  const char* what = "qkv_reuse_lag_union_bits";
+  if (!current || !union_out) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (batch <= 0 || q_heads <= 0 || batch * q_heads > 65535)
+    return fail(QKV_ERR_INVALID, "%s: need batch, q_heads > 0 and batch * q_heads <= 65535", what);
+  const int64_t words = (history + 63) / 64;
+  if (history <= 0 || history >= (int64_t(1) << 31) || words_ld < words || union_ld < words)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, words_ld and union_ld covering the history", what);
+  if (!aligned(current, 8) || !aligned(union_out, 8) || !aligned(previous_final, 8))
+    return fail(QKV_ERR_INVALID, "%s: bitsets must be 8-byte aligned", what);
+  if (refresh < QKV_REFRESH_NONE || refresh > QKV_REFRESH_MAJORITY)
+    return fail(QKV_ERR_INVALID, "%s: unknown refresh %d", what, refresh);
+  if (refresh >= QKV_REFRESH_PER_ROW && !flags) return fail(QKV_ERR_INVALID, "%s: null flags", what);
+  if (protect_sink < 0 || protect_recent < 0) return fail(QKV_ERR_INVALID, "%s: negative protection", what);
+  const int sink_end = static_cast<int>(std::min(protect_sink, history));
+  const int recent_start = static_cast<int>(std::max<int64_t>(0, history - protect_recent));
+  dim3 grid(static_cast<unsigned>(cdiv(words, kLagNT)), static_cast<unsigned>(batch * q_heads));
+  lag_union_bits_kernel<<<grid, kLagNT, 0, static_cast<hipStream_t>(stream)>>>(
+      current, previous_final, words_ld, flags, static_cast<int>(batch * q_heads), static_cast<int>(q_heads),
+      static_cast<int>(history), refresh, share ? 1 : 0, sink_end, recent_start, union_out, union_ld);
   return check_launch(what);
 }

@@ -960,7 +960,8 @@ template <int J, bool LIST = false>
 __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
     const float* __restrict__ values, int64_t ld, int n, int k, int slices, int* __restrict__ hist,
     int* __restrict__ state, float* __restrict__ list_val, int* __restrict__ list_pos, int64_t list_ld,
-    uint64_t* __restrict__ bits, int64_t bits_ld, float* __restrict__ thr_out, QabsListOut qs = {}) {
+    uint64_t* __restrict__ bits, int64_t bits_ld, float* __restrict__ thr_out, QabsListOut qs = {},
+    const uint8_t* __restrict__ gate = nullptr, int gate_refresh = 0, int gate_rows = 0) {
   using WS = WideSelect<1, false>;
   static_assert(sizeof(typename WideSelect<1, false>::Shared) == sizeof(typename WideSelect<8, false>::Shared),
                 "one shared layout for every list length");
@@ -971,6 +972,11 @@ __global__ __launch_bounds__(kWideNT) void reuse_cand_slices_kernel(
   __shared__ uint64_t fw[LIST ? kWideMax / 64 : 1];   // LIST: the row's taken positions
   const int row = blockIdx.x / slices, s = blockIdx.x - row * slices;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (gate) {   // a lagged step: rows that keep no new candidates are skipped (uniform; the
+                // partial scores skipped them too, so their histogram and ticket stay zero)
+    if (!lag_refreshes(gate, gate_refresh, gate_rows, row, wave_cnt)) return;
+    __syncthreads();   // (wave_cnt is reused)
+  }
   int* hrow = hist + static_cast<int64_t>(row) * kCandBins;
   const float* vrow = values + static_cast<int64_t>(row) * ld;
   // the histogram (4 bins per thread) and the slice's scores, all loads in flight
@@ -1955,13 +1961,14 @@ struct CandSplit {
 #define QKV_CAND_TARGET_WGS 256
 #endif
 int launch_cand_slices(const char* what, const float* values, int64_t ld, int64_t rows, int64_t n, int64_t k,
-                       const CandSplit& cs, uint64_t* bits, int64_t bits_ld, float* thr_out, hipStream_t st) {
+                       const CandSplit& cs, uint64_t* bits, int64_t bits_ld, float* thr_out, hipStream_t st,
+                       const uint8_t* gate = nullptr, int refresh = 0) {
   auto launch = [&](auto jc) {
     constexpr int J = decltype(jc)::value;
     const int64_t slices = cdiv(n, int64_t(kWideNT) * J);
     reuse_cand_slices_kernel<J><<<static_cast<unsigned>(rows * slices), kWideNT, 0, st>>>(
         values, ld, static_cast<int>(n), static_cast<int>(k), static_cast<int>(slices), cs.hist, cs.state,
-        cs.list_val, cs.list_pos, n, bits, bits_ld, thr_out);
+        cs.list_val, cs.list_pos, n, bits, bits_ld, thr_out, QabsListOut{}, gate, refresh, static_cast<int>(rows));
     return check_launch(what);
   };
   auto wgs = [&](int64_t j) { return rows * cdiv(n, int64_t(kWideNT) * j); };
@@ -2030,12 +2037,14 @@ template <int DT> struct RunCandidates {
       if (T <= 4 * per) return launch(std::integral_constant<int, 4>{});
       return launch(std::integral_constant<int, 5>{});
     }
-    if (split.hist && bits && !gate && T <= kWideMax) {
+    if (split.hist && bits && T <= kWideMax) {
       // the partial scores count the first digit; several workgroups per row select
-      int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, nullptr, 0,
+      // (gate: the rows that keep no new candidates skip both launches)
+      int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, gate, refresh,
                                         split.hist);
       if (rc) return rc;
-      return launch_cand_slices(what, partial, partial_ld, rows, T, k, split, bits, bits_ld, thr_out, st);
+      return launch_cand_slices(what, partial, partial_ld, rows, T, k, split, bits, bits_ld, thr_out, st, gate,
+                                refresh);
     }
     int rc = RunReusePartial<DT>::run(q, kdm, ks, B, Hq, Hkv, T, D, count, partial, partial_ld, st, gate, refresh);
     if (rc) return rc;
@@ -2489,6 +2498,48 @@ QKV_EXPORT int qkv_reuse_lag_candidates(const void* query, const void* key_dim_m
   return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
                                        history, head_dim, count, k, partial, partial_ld, mask, mask_ld, nullptr,
                                        workspace, workspace_bytes, static_cast<hipStream_t>(stream), gate, refresh);
+}
+
+QKV_EXPORT int qkv_reuse_lag_candidates_bits(const void* query, const void* key_dim_major,
+                                             const int64_t* kdm_strides, int dtype, int64_t batch, int64_t q_heads,
+                                             int64_t kv_heads, int64_t history, int64_t head_dim, int64_t dim_count,
+                                             int64_t k, const uint8_t* flags, int refresh, float* partial,
+                                             int64_t partial_ld, uint64_t* bits, int64_t bits_ld, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+  const char* what = "qkv_reuse_lag_candidates_bits";
+  int rc = check_heads(what, batch, q_heads, kv_heads, head_dim);
+  if (rc) return rc;
+  if (!query || !key_dim_major || !kdm_strides || !partial || !bits || !workspace)
+    return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (history <= 0 || history >= (int64_t(1) << 31) || partial_ld < history || bits_ld < cdiv(history, 64) ||
+      !aligned(bits, 8) || k < 1 || k > history)
+    return fail(QKV_ERR_INVALID, "%s: need 0 < history < 2^31, 1 <= k <= history, row strides covering the history",
+                what);
+  if (kdm_strides[3] != 1) return fail(QKV_ERR_UNSUPPORTED, "%s: the token axis of K must be contiguous", what);
+  if (refresh < QKV_REFRESH_NONE || refresh > QKV_REFRESH_MAJORITY)
+    return fail(QKV_ERR_INVALID, "%s: unknown refresh %d", what, refresh);
+  if (refresh >= QKV_REFRESH_PER_ROW && !flags) return fail(QKV_ERR_INVALID, "%s: null flags", what);
+  const int64_t rows = batch * q_heads;
+  const int64_t need = qkv_reuse_candidates_workspace_bytes(rows, history, k);
+  if (need < 0 || workspace_bytes < need)
+    return fail(QKV_ERR_INVALID, "%s: workspace needs %lld bytes, got %lld", what, (long long)need,
+                (long long)workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(QKV_ERR_INVALID, "%s: the workspace must be 16-byte aligned", what);
+  if (refresh == QKV_REFRESH_NONE) return QKV_OK;   // no row takes new candidates
+  const uint8_t* gate = refresh == QKV_REFRESH_ALL ? nullptr : flags;
+  const int count = static_cast<int>(std::min<int64_t>(std::max<int64_t>(dim_count, 1),
+                                                       std::min<int64_t>(head_dim, kMaxDims)));
+  char* ws = static_cast<char*>(workspace);
+  const int64_t state = cand_state_bytes(rows);
+  CandSplit split;
+  split.hist = reinterpret_cast<int*>(ws);
+  split.state = reinterpret_cast<int*>(ws + align256(rows * kCandBins * 4));
+  split.list_val = reinterpret_cast<float*>(ws + state);
+  split.list_pos = reinterpret_cast<int*>(ws + state + align256(rows * history * 4));
+  return dispatch_dtype<RunCandidates>(dtype, what, query, key_dim_major, kdm_strides, batch, q_heads, kv_heads,
+                                       history, head_dim, count, k, partial, partial_ld, nullptr, 0, nullptr,
+                                       ws + state, workspace_bytes - state, static_cast<hipStream_t>(stream), gate,
+                                       refresh, bits, bits_ld, split);
 }
 
 QKV_EXPORT int qkv_reuse_candidates(const void* query, const void* key_dim_major, const int64_t* kdm_strides,

@@ -610,18 +610,19 @@ def lag_flags(query: torch.Tensor, kv_heads: int, test: str, dim_count: int, dim
     query [B, Hq, D]; dims_out int32 / values_out f32 [B*Hq, S] receive the
     row's top-|q| dims and q at them; flags uint8 [B*Hq] the test's result
     (``test`` in ``LAG_TESTS``).  The ``ess`` test reads key [B, Hkv, T, D]
-    and previous_final uint8 rows of the history, and takes a workspace
-    (allocated here when not given)."""
+    and previous_final rows of the history (uint8 masks, or int64 bitset
+    words), and takes a workspace (allocated here when not given)."""
     lib = _lib.load()
     q = query.contiguous()
     b, hq, d = q.shape
     mask_ld = previous_final.stride(0) if previous_final is not None else 0
+    bits = previous_final is not None and previous_final.dtype == torch.int64
     if test == "ess" and workspace is None:
         need = int(lib.qkv_reuse_lag_flags_workspace_bytes(b * hq, history))
         _require(need > 0, "bad ESS sizes")
         workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
-        _lib.check(lib.qkv_reuse_lag_flags(
+        _lib.check((lib.qkv_reuse_lag_flags_bits if bits else lib.qkv_reuse_lag_flags)(
             q.data_ptr(), _dtype_code(q), b, hq, kv_heads, d, dim_count, LAG_TESTS[test], _lib.ptr(previous_dims),
             _lib.ptr(previous_values), dims_out.data_ptr(), values_out.data_ptr(), _lib.ptr(key),
             _lib.strides(*key.stride()) if key is not None else None, history, _lib.ptr(previous_final), mask_ld,
@@ -635,12 +636,14 @@ def lag_candidates(query: torch.Tensor, key_dim_major: torch.Tensor, history: in
     """Partial scores and candidate mask (``partial >= the row's k-th
     largest``) of the rows that refresh (``qkv_reuse_lag_candidates``);
     query [B, Hq, D], key_dim_major [B, Hkv, D, >= history]; partial f32 /
-    mask uint8 rows of >= history."""
+    mask uint8 rows of >= history.  An int64 ``mask`` is a bitset
+    (``qkv_reuse_lag_candidates_bits``), whose workspace is zero-filled."""
     lib = _lib.load()
     q = query.contiguous()
     b, hq, d = q.shape
+    bits = mask.dtype == torch.int64
     with torch.cuda.device(q.device):
-        _lib.check(lib.qkv_reuse_lag_candidates(
+        _lib.check((lib.qkv_reuse_lag_candidates_bits if bits else lib.qkv_reuse_lag_candidates)(
             q.data_ptr(), key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _dtype_code(q), b, hq,
             key_dim_major.size(1), history, d, dim_count, k, _lib.ptr(flags), REFRESH[refresh], partial.data_ptr(),
             partial.stride(0), mask.data_ptr(), mask.stride(0), workspace.data_ptr(), workspace.numel() * 4,
@@ -652,12 +655,16 @@ def lag_union(current: torch.Tensor, previous_final: torch.Tensor | None, flags:
               out: torch.Tensor) -> torch.Tensor:
     """The lagged modes' candidate union (``qkv_reuse_lag_union``) into
     ``out``; ``current`` rows of the rows that do not refresh are cleared.
-    Masks uint8 [B*Hq, >= history] (row strides of their own)."""
+    Masks uint8 [B*Hq, >= history] (row strides of their own), or int64
+    bitset words [B*Hq, >= ceil(history / 64)] (``qkv_reuse_lag_union_bits``)."""
     lib = _lib.load()
     _require(previous_final is None or previous_final.stride(0) == current.stride(0),
              "current and previous_final must share a row stride")
+    bits = current.dtype == torch.int64
+    _require(out.dtype == current.dtype and (previous_final is None or previous_final.dtype == current.dtype),
+             "the masks must all be bytes or all bitsets")
     with torch.cuda.device(current.device):
-        _lib.check(lib.qkv_reuse_lag_union(
+        _lib.check((lib.qkv_reuse_lag_union_bits if bits else lib.qkv_reuse_lag_union)(
             current.data_ptr(), _lib.ptr(previous_final), current.stride(0), _lib.ptr(flags), batch, q_heads, history,
             REFRESH[refresh], int(share), protect_sink, protect_recent, out.data_ptr(), out.stride(0),
             _lib.stream_of(current)))
@@ -685,8 +692,6 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
     step needs no host round trip and can be captured; with the other
     selections those two kinds read the decision on the host."""
 
-    _BITSET = False   # the lagged kernels read and write byte masks
-
     def __init__(self, mode: str, batch: int, q_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  top_fraction: float = 0.02, protect_sink: int = 0, protect_recent: int = 0,
                  keep_self: bool = True, candidate_selection: str = "topk", threshold_sample_size: int = 256,
@@ -703,7 +708,7 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
         self.qdims = [torch.zeros((self.rows, s), dtype=torch.int32, device=device) for _ in range(2)]
         self.qvals = [torch.zeros((self.rows, s), dtype=torch.float32, device=device) for _ in range(2)]
         self.flags = torch.zeros(self.rows, dtype=torch.uint8, device=device)
-        self.union = torch.zeros((self.rows, self.capacity), dtype=torch.uint8, device=device)
+        self.union = torch.zeros_like(self.fin)   # bitset words (or bytes, as the step's masks)
         # the ESS test's per-span sums: at most rows * ceil(1024 / rows) spans
         self.ess_ws = torch.empty(self.rows * -(-1024 // self.rows) * 4 if self.kind == "pconf" else 1,
                                   dtype=torch.float32, device=device)
@@ -762,10 +767,17 @@ class LaggedReuseDecodeStep(ReuseDecodeStep):
             self._candidates(q, history, current, previous_thresholds and self.thr_valid)
         elif refresh != "none":   # the rows that refresh score and threshold (EV:3988-3989, 4089-4106)
             requested = budget_count(history, self.cand_fraction)
-            self.mask_ws = self._grow(self.mask_ws,
-                                      lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+            if self.bits:   # the candidates' zero-filled workspace (grown zero-filled)
+                need = lib.qkv_reuse_candidates_workspace_bytes(self.rows, history, requested)
+                if self.cand_ws.numel() * 4 < need:
+                    self.cand_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=self.device)
+                ws = self.cand_ws
+            else:
+                self.mask_ws = self._grow(self.mask_ws,
+                                          lib.qkv_threshold_mask_workspace_bytes(self.rows, history, requested))
+                ws = self.mask_ws
             lag_candidates(q, self.kdm, history, self.dims, requested, self.flags, refresh, self.partial, current,
-                           self.mask_ws)
+                           ws)
         self.thr_valid = every_row
         lag_union(current, previous_final, self.flags, self.batch, self.q_heads, history, refresh,
                   self.kind == "qdriftshare" and has_prev, self.sink, self.recent, self.union)

@@ -222,6 +222,106 @@ def test_lag_union_matches_numpy(refresh, share, batch, hq, hist, ld):
     assert np.array_equal(out2[:, :hist].cpu().numpy().astype(bool), c)
 
 
+def _to_words(m):
+    # bool [rows, n] -> int64 bitset words [rows, ceil(n / 64)] (bit t % 64 of word t // 64)
+    rows, n = m.shape
+    n_w = -(-n // 64)
+    pad = torch.zeros((rows, n_w * 64), dtype=torch.bool, device=m.device)
+    pad[:, :n] = m
+    by = (pad.view(rows, -1, 8).to(torch.uint8) << torch.arange(8, dtype=torch.uint8, device=m.device)).sum(-1)
+    return by.to(torch.uint8).contiguous().view(torch.int64)
+
+
+@pytest.mark.parametrize("refresh,share", [("none", False), ("all", False), ("per_row", False), ("per_row", True),
+                                           ("any", False), ("majority", False)])
+@pytest.mark.parametrize("batch,hq,hist", [(2, 4, 1000), (1, 3, 37), (3, 2, 4113), (1, 2, 128)])
+def test_lag_union_bits_equals_bytes(refresh, share, batch, hq, hist):
+    # qkv_reuse_lag_union_bits against the byte-mask union on the same masks:
+    # the same union and the same cleared candidates, words past the history untouched
+    gen = torch.Generator().manual_seed(hist * 3 + hq)
+    rows = batch * hq
+    cur = (torch.rand((rows, hist), generator=gen) < 0.05).to(DEV)
+    fin = (torch.rand((rows, hist), generator=gen) < 0.03).to(DEV)
+    flags = (torch.rand(rows, generator=gen) < 0.4).to(torch.uint8).to(DEV)
+    if refresh == "majority":
+        flags[: rows // 2 + 1] = 1
+    cur_b, out_b = cur.to(torch.uint8), torch.zeros((rows, hist), dtype=torch.uint8, device=DEV)
+    RU.lag_union(cur_b, fin.to(torch.uint8), flags, batch, hq, hist, refresh, share, 3, 11, out_b)
+    n_w = -(-hist // 64)
+    cur_w = torch.cat([_to_words(cur), torch.full((rows, 1), 5, dtype=torch.int64, device=DEV)], 1)
+    fin_w = torch.cat([_to_words(fin), torch.zeros((rows, 1), dtype=torch.int64, device=DEV)], 1)
+    out_w = torch.full((rows, n_w + 1), 7, dtype=torch.int64, device=DEV)
+    RU.lag_union(cur_w, fin_w, flags, batch, hq, hist, refresh, share, 3, 11, out_w)
+    assert torch.equal(RU.expand_bits(out_w, hist), out_b.bool())
+    assert torch.equal(RU.expand_bits(cur_w, hist), cur_b.bool())
+    assert bool((out_w[:, n_w] == 7).all()) and bool((cur_w[:, n_w] == 5).all())
+    if hist % 64:   # no bit past the history in the last word
+        assert not RU.expand_bits(out_w[:, :n_w], n_w * 64)[:, hist:].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,hkv,hist,dens", [(8, 2, 3000, 0.03), (4, 4, 70000, 0.2), (6, 3, 37, 0.5)])
+def test_lag_flags_ess_bits_equals_bytes(dtype, rows, hkv, hist, dens):
+    gen = torch.Generator().manual_seed(rows * 11 + hist)
+    q = (torch.randn((1, rows, 128), generator=gen) * 0.5).to(dtype).to(DEV)
+    k = torch.randn((1, hkv, hist + 1, 128), generator=gen).to(dtype).to(DEV)
+    m = (torch.rand((rows, hist), generator=gen) < dens).to(DEV)
+    outs = []
+    for fin in (m.to(torch.uint8), _to_words(m)):
+        flags = torch.full((rows,), 7, dtype=torch.uint8, device=DEV)
+        dims = torch.empty((rows, 8), dtype=torch.int32, device=DEV)
+        vals = torch.empty((rows, 8), dtype=torch.float32, device=DEV)
+        RU.lag_flags(q, hkv, "ess", 8, dims, vals, flags, key=k, history=hist, previous_final=fin,
+                     scaling=128 ** -0.5, ess_threshold=0.3)
+        outs.append((flags, dims, vals))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("refresh", ["all", "per_row", "any", "majority", "none"])
+@pytest.mark.parametrize("hist", [3000, 32790, 50000])
+def test_lag_candidates_bits_equals_bytes(refresh, hist):
+    # the refreshing rows' candidate bits equal the byte path's mask; past
+    # 40960 positions the rows take the one-workgroup path; the workspace
+    # state is left zero
+    gen = torch.Generator().manual_seed(hist + 17)
+    b, hq, hkv, d, s_count = 2, 4, 2, 128, 8
+    rows = b * hq
+    k = torch.randn((b, hkv, hist + 1, d), generator=gen).to(torch.bfloat16).to(DEV)
+    q = torch.randn((b, hq, d), generator=gen).to(torch.bfloat16).to(DEV)
+    kdm = torch.zeros((b, hkv, d, hist + 64), dtype=torch.bfloat16, device=DEV)
+    RU.dim_major_append(k, kdm, 0, hist)
+    flags = torch.tensor([1, 0, 0, 1, 0, 1, 0, 0], dtype=torch.uint8, device=DEV)
+    if refresh == "majority":
+        flags[:5] = 1
+    lib = Q._lib.load()
+    req = R.budget_count(hist, 0.05)
+    ws = torch.empty(lib.qkv_threshold_mask_workspace_bytes(rows, hist, req) // 4 + 1, dtype=torch.float32,
+                     device=DEV)
+    part = torch.full((rows, hist + 64), -7.0, device=DEV)
+    mask = torch.full((rows, hist + 64), 9, dtype=torch.uint8, device=DEV)
+    RU.lag_candidates(q, kdm, hist, s_count, req, flags, refresh, part, mask, ws)
+    n_w = -(-hist // 64)
+    cws = torch.zeros(lib.qkv_reuse_candidates_workspace_bytes(rows, hist, req) // 4 + 1, dtype=torch.float32,
+                      device=DEV)
+    part_b = torch.full((rows, hist + 64), -7.0, device=DEV)
+    words = torch.full((rows, n_w + 1), 3, dtype=torch.int64, device=DEV)
+    for _ in range(2):   # twice through one workspace
+        RU.lag_candidates(q, kdm, hist, s_count, req, flags, refresh, part_b, words, cws)
+    assert not cws[: rows * 4096].any()   # the per-row histograms are clear again
+    fl = flags.cpu().numpy().astype(bool)
+    fresh = {"all": np.ones(rows, bool), "none": np.zeros(rows, bool), "per_row": fl,
+             "any": np.full(rows, fl.any()), "majority": np.full(rows, 2 * fl.sum() > rows)}[refresh]
+    got = RU.expand_bits(words[:, :n_w], hist)
+    for r in range(rows):
+        if fresh[r]:
+            assert torch.equal(part_b[r, :hist], part[r, :hist]), r
+            assert torch.equal(got[r], mask[r, :hist].bool()), r
+        elif hist <= 40960:   # rows that keep are not touched
+            assert bool((part_b[r] == -7.0).all()) and bool((words[r] == 3).all()), r
+    assert bool((words[:, n_w] == 3).all())
+
+
 def test_lag_entry_points_reject_bad_arguments():
     q = torch.zeros((1, 4, 128), dtype=torch.bfloat16, device=DEV)
     d = torch.zeros((4, 8), dtype=torch.int32, device=DEV)
