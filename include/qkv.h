@@ -607,6 +607,14 @@ int qkv_reuse_lag_union_bits(uint64_t* current, const uint64_t* previous_final, 
                              int share, int64_t protect_sink, int64_t protect_recent, uint64_t* union_out,
                              int64_t union_ld, void* stream);
 
+/* qkv_reuse_expand_blocks on a bitset final selection (bit t % 64 of uint64
+ * word t / 64, row stride history_final_ld words, 8-byte aligned), any
+ * history: the same expanded bitset and list. */
+int qkv_reuse_expand_blocks_bits(uint64_t* history_final, int64_t history_final_ld, int64_t rows,
+                                 int64_t key_count, int64_t block, int64_t protect_sink, int64_t protect_recent,
+                                 double top_fraction, int keep_self, int64_t* final_indices, uint8_t* final_valid,
+                                 int32_t* attn_ids, int64_t n_out, void* stream);
+
 /* Entries per row of the final index list of a block-expanded reuse step
  * (the qabs{S}cand{pct}reuse[final|2set]blk{block} modes): body + sink
  * range + recent range (not overlapping the sink) + 1 when keep_self, where

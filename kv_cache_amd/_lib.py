@@ -92,6 +92,8 @@ _PROTOTYPES = {
     "qkv_reuse_lag_union_bits": (_i32, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _i64, _i64, _vp, _i64,
                                         _vp]),
     "qkv_reuse_block_final_count": (_i64, [_i64, _i64, _i64, _i64, _f64, _i32]),
+    "qkv_reuse_expand_blocks_bits": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _f64, _i32, _vp, _vp, _vp,
+                                            _i64, _vp]),
     "qkv_reuse_expand_blocks": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _f64, _i32, _vp, _vp, _vp, _i64,
                                        _vp]),
     "qkv_reuse_partial_scores": (_i32, [_vp, _vp, _P(_i64), _i32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,

@@ -1738,6 +1738,81 @@ __global__ __launch_bounds__(kExpandNT) void reuse_expand_kernel(
   }
 }
 
+// reuse_expand_kernel on a bitset final selection (hf_ld words per row): a
+// block's test reads its own bits, a hit block's bits are set by atomic OR
+// (blocks of fewer than 64 positions, or not a multiple of 64, share words);
+// the list is written as there.
+__global__ __launch_bounds__(kExpandNT) void reuse_expand_bits_kernel(
+    uint64_t* __restrict__ hf, int64_t hf_ld, int history, int block, int body_cap, int key_count, int sink_end,
+    int recent_start, int rec_begin, int n_rec, int keep_self, int64_t* __restrict__ final_idx,
+    uint8_t* __restrict__ final_valid, int32_t* __restrict__ attn_ids, int n_out) {
+  __shared__ int wave_tot[kExpandNT / 64];
+  __shared__ int run_off[kExpandNT], run_lo[kExpandNT];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint64_t* hrow = hf + static_cast<int64_t>(row) * hf_ld;
+  const int64_t o = static_cast<int64_t>(row) * n_out;
+  const int nblk = static_cast<int>((static_cast<int64_t>(history) + block - 1) / block);
+  int base = 0;
+  for (int j0 = 0; j0 < nblk; j0 += kExpandNT) {
+    const int j = j0 + tid;
+    int lo = 0, hi = 0;
+    if (j < nblk) {
+      const int b_lo = j * block, b_hi = min(b_lo + block, history);
+      const int w_lo = b_lo >> 6, w_hi = (b_hi - 1) >> 6;
+      uint64_t any = 0;
+      for (int w = w_lo; w <= w_hi; ++w) any |= hrow[w] & word_range_bits(w, b_lo, b_hi);
+      if (any) {
+        for (int w = w_lo; w <= w_hi; ++w) {
+          const uint64_t m = word_range_bits(w, b_lo, b_hi);
+          if (m == ~0ull) hrow[w] = m;   // a word of this block alone
+          else atomicOr(reinterpret_cast<unsigned long long*>(hrow + w), m);
+        }
+        lo = max(b_lo, sink_end);
+        hi = min(b_hi, recent_start);
+      }
+    }
+    const int cnt = hi > lo ? hi - lo : 0;
+    const int incl = wave_incl_scan_dpp(cnt);
+    run_off[tid] = incl - cnt;
+    run_lo[tid] = lo;
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int wave_base = base, total = 0;
+#pragma unroll
+    for (int w = 0; w < kExpandNT / 64; ++w) {
+      const int x = wave_tot[w];
+      wave_base += w < wave ? x : 0;
+      total += x;
+    }
+    const int w64 = wave * 64, wave_cnt = wave_tot[wave];
+    for (int q = lane; q < wave_cnt && wave_base + q < body_cap; q += 64) {
+      int k = 0;   // the last lane whose run starts at or before q
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1) k += run_off[w64 + k + step] <= q ? step : 0;
+      const int t = run_lo[w64 + k] + (q - run_off[w64 + k]);
+      const int64_t e = o + wave_base + q;
+      final_idx[e] = t;
+      final_valid[e] = 1;
+      if (attn_ids) attn_ids[e] = t;
+    }
+    base += total;
+    __syncthreads();   // wave_tot is rewritten by the next round
+  }
+  for (int p = min(base, body_cap) + tid; p < body_cap; p += kExpandNT) {
+    final_idx[o + p] = 0;
+    final_valid[o + p] = 0;
+    if (attn_ids) attn_ids[o + p] = -1;
+  }
+  const int extra = sink_end + n_rec + keep_self;
+  for (int i = tid; i < extra; i += kExpandNT) {
+    const int idx = i < sink_end ? i : (i < sink_end + n_rec ? rec_begin + (i - sink_end) : key_count - 1);
+    final_idx[o + body_cap + i] = idx;
+    final_valid[o + body_cap + i] = 1;
+    if (attn_ids) attn_ids[o + body_cap + i] = idx;
+  }
+}
+
 // VPL for a row of n values: 16, 32 or 40 (n <= kWideMax).
 template <typename F>
 int with_wide_vpl(int64_t n, F&& f) {
@@ -2424,6 +2499,36 @@ QKV_EXPORT int qkv_reuse_expand_blocks(uint8_t* history_final, int64_t history_f
     return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the expanded selection needs %lld", what,
                 (long long)n_out, (long long)need);
   reuse_expand_kernel<<<static_cast<unsigned>(rows), kExpandNT, 0, static_cast<hipStream_t>(stream)>>>(
+      history_final, history_final_ld, static_cast<int>(history), static_cast<int>(block),
+      static_cast<int>(body), static_cast<int>(key_count), static_cast<int>(c.sink_end),
+      static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin), static_cast<int>(c.n_rec), keep_self ? 1 : 0,
+      final_indices, final_valid, attn_ids, static_cast<int>(n_out));
+  return check_launch(what);
+}
+
+QKV_EXPORT int qkv_reuse_expand_blocks_bits(uint64_t* history_final, int64_t history_final_ld, int64_t rows,
+                                            int64_t key_count, int64_t block, int64_t protect_sink,
+                                            int64_t protect_recent, double top_fraction, int keep_self,
+                                            int64_t* final_indices, uint8_t* final_valid, int32_t* attn_ids,
+                                            int64_t n_out, void* stream) {
+  const char* what = "qkv_reuse_expand_blocks_bits";
+  if (!history_final || !final_indices || !final_valid) return fail(QKV_ERR_INVALID, "%s: null pointer", what);
+  if (rows <= 0 || rows > 65535) return fail(QKV_ERR_INVALID, "%s: need 1 <= rows <= 65535", what);
+  const int64_t history = key_count - 1;
+  if (history <= 0 || key_count >= (int64_t(1) << 31))
+    return fail(QKV_ERR_INVALID, "%s: need 2 <= key_count < 2^31 (history excludes the current token)", what);
+  if (history_final_ld < cdiv(history, 64) || !aligned(history_final, 8))
+    return fail(QKV_ERR_INVALID, "%s: the bitset's row stride must cover the history (8-byte aligned)", what);
+  if (block < 1 || block > kMaxExpandBlock)
+    return fail(QKV_ERR_INVALID, "%s: block must be in [1, %d]", what, kMaxExpandBlock);
+  if (!(top_fraction >= 0.0)) return fail(QKV_ERR_INVALID, "%s: top_fraction must be >= 0", what);
+  const ReuseCounts c = reuse_counts(history, protect_sink, protect_recent, top_fraction, keep_self);
+  const int64_t body = block_body_cap(c, block);
+  const int64_t need = body + c.sink_end + c.n_rec + (keep_self ? 1 : 0);
+  if (n_out != need)
+    return fail(QKV_ERR_INVALID, "%s: index rows hold %lld entries, the expanded selection needs %lld", what,
+                (long long)n_out, (long long)need);
+  reuse_expand_bits_kernel<<<static_cast<unsigned>(rows), kExpandNT, 0, static_cast<hipStream_t>(stream)>>>(
       history_final, history_final_ld, static_cast<int>(history), static_cast<int>(block),
       static_cast<int>(body), static_cast<int>(key_count), static_cast<int>(c.sink_end),
       static_cast<int>(c.recent_start), static_cast<int>(c.rec_begin), static_cast<int>(c.n_rec), keep_self ? 1 : 0,

@@ -65,8 +65,8 @@ def parse_reuse_mode(mode: str) -> tuple[int, float, bool, bool, int | None]:
 
 
 # Rows of at most this many history positions have their block expansion run by
-# the final selection's launch on bitsets (one 1024-thread workgroup per row
-# holds the row's bitset in LDS); longer capacities keep byte masks.
+# the final selection's launch (one 1024-thread workgroup per row holds the
+# row's bitset in LDS); longer rows expand in a launch of their own.
 BLOCK_BITS_MAX_HISTORY = 40960
 
 CANDIDATE_SELECTIONS = {"topk": 0, "sample_quantile": 1, "previous_threshold": 2}   # QKV_CAND_*
@@ -328,10 +328,8 @@ class ReuseDecodeStep:
         cap = self.capacity
         self.rows = rows
         self.kdm = torch.empty((batch, kv_heads, head_dim, cap), dtype=dtype, device=device)
-        # candidate and final masks: bitsets (64 positions per int64 word); byte
-        # masks where a lagged step reads them, and for the block modes past the
-        # rows whose expansion runs in the final selection's launch
-        self.bits = self._BITSET and (self.block is None or cap - 1 <= BLOCK_BITS_MAX_HISTORY)
+        # candidate and final masks: bitsets (64 positions per int64 word)
+        self.bits = self._BITSET
         if self.bits:
             words = -(-cap // 64)
             self.cand = [torch.zeros((rows, words), dtype=torch.int64, device=device) for _ in range(2)]
@@ -500,6 +498,23 @@ class ReuseDecodeStep:
                                     lib.qkv_reuse_select_workspace_bytes(self.rows, history, self.top_fraction))
         ids = self.attn_ids[: self.rows * n_out]
         bits = current.dtype == torch.int64
+        if bits and self.block is not None and history > BLOCK_BITS_MAX_HISTORY:
+            # past one workgroup's row: the selection, then the expansion on the bitset
+            with torch.cuda.device(q.device):
+                _lib.check(lib.qkv_reuse_select_bits(
+                    q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch,
+                    self.q_heads, self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
+                    _lib.ptr(previous_final), current.stride(0), self.sink, self.recent, self.top_fraction,
+                    int(self.keep_self), float(scaling), self.select_ws.data_ptr(), self.select_ws.numel() * 4,
+                    self.final_idx.data_ptr(), self.final_valid.data_ptr(), None, n_sel, self.fin.data_ptr(),
+                    self.fin.stride(0), None, None, None, _lib.stream_of(q)))
+                _lib.check(lib.qkv_reuse_expand_blocks_bits(
+                    self.fin.data_ptr(), self.fin.stride(0), self.rows, key_count, self.block, self.sink,
+                    self.recent, self.top_fraction, int(self.keep_self), self.final_idx.data_ptr(),
+                    self.final_valid.data_ptr(), ids.data_ptr(), n_out, _lib.stream_of(q)))
+            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+            self.n_out = n_out
+            return
         if bits and self.block is not None:   # the selection and its block expansion in one launch
             with torch.cuda.device(q.device):
                 _lib.check(lib.qkv_reuse_select_bits_blocks(

@@ -773,6 +773,46 @@ def test_reuse_select_bits_blocks_rejects():
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("history,block,sink,recent,keep_self,density", [
+    (50000, 16, 10, 10, True, 0.02), (70001, 100, 3, 5, False, 0.01), (3000, 7, 0, 0, True, 0.05),
+    (9000, 64, 4, 8, True, 0.03), (45000, 4096, 10, 10, True, 0.001), (1000, 1, 2, 2, True, 0.1),
+])
+def test_expand_blocks_bits_equals_bytes(history, block, sink, recent, keep_self, density):
+    # qkv_reuse_expand_blocks_bits (any history) against the byte expansion
+    # on the same final mask: the same expanded mask, list, validity and ids
+    from kv_cache_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(history + block)
+    rows = 4
+    mask = torch.rand((rows, history), generator=gen) < density
+    mask[:, :min(sink, history)] = True
+    mask[:, max(0, history - recent):] = True
+    keep = int(mask.sum(dim=1).max())
+    frac = keep / history
+    n_out = int(lib.qkv_reuse_block_final_count(history, block, sink, recent, frac, int(keep_self)))
+    by = mask.to(torch.uint8).to(DEV)
+    n_w = -(-history // 64)
+    pad = torch.zeros((rows, n_w * 64), dtype=torch.bool)
+    pad[:, :history] = mask
+    words = ((pad.view(rows, -1, 8).to(torch.uint8) << torch.arange(8, dtype=torch.uint8)).sum(-1).to(torch.uint8)
+             .contiguous().view(torch.int64)).to(DEV)
+    outs = []
+    for bits in (False, True):
+        buf = words if bits else by
+        fi = torch.full((rows, n_out), 7, dtype=torch.int64, device=DEV)
+        fv = torch.full((rows, n_out), 7, dtype=torch.uint8, device=DEV)
+        ids = torch.full((rows, n_out), 7, dtype=torch.int32, device=DEV)
+        fn = lib.qkv_reuse_expand_blocks_bits if bits else lib.qkv_reuse_expand_blocks
+        _lib.check(fn(buf.data_ptr(), buf.stride(0), rows, history + 1, block, sink, recent, frac, int(keep_self),
+                      fi.data_ptr(), fv.data_ptr(), ids.data_ptr(), n_out, _lib.stream_of(buf)))
+        outs.append((fi, fv, ids, RU.expand_bits(buf, history) if bits else buf.bool()))
+    for a, w in zip(*outs):
+        assert torch.equal(a, w)
+    if history % 64:   # nothing set past the history in the last word
+        assert not RU.expand_bits(words, n_w * 64)[:, history:].any()
+
+
 def test_expand_blocks_rejects_bad_arguments():
     m = torch.zeros((2, 100), dtype=torch.uint8, device=DEV)
     with pytest.raises(RuntimeError, match="block must be"):
