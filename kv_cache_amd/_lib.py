@@ -10,7 +10,9 @@ which makes torch's device pointers and streams valid in it.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import functools
 import os
 import re
 from pathlib import Path
@@ -166,9 +168,27 @@ def check(rc: int) -> None:
         raise RuntimeError(load().qkv_last_error().decode())
 
 
+@functools.lru_cache(maxsize=512)
+def _strides(vals: tuple):
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
 def strides(*vals: int):
-    arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
-    return arr
+    """An int64 array of the values for a C call (read only by the library;
+    the same object for the same values, so a decode step builds none)."""
+    return _strides(tuple(int(v) for v in vals))
+
+
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def on_device(device: torch.device):
+    """torch.cuda.device(device), or a no-op when that device is already
+    current (the per-call guard costs more than the launch it guards)."""
+    idx = device.index
+    if idx is None or torch.cuda.current_device() == idx:
+        return _SAME_DEVICE
+    return torch.cuda.device(device)
 
 
 def ptr(t) -> int | None:

@@ -148,7 +148,7 @@ class BlockSelectDecodeStep:
         if self.meta_len < history and self.meta is None:
             self.meta_len = history
         if self.meta_len < history:
-            with torch.cuda.device(key.device):
+            with _lib.on_device(key.device):
                 _lib.check(lib.qkv_block_meta_update(
                     self.kind, key.data_ptr(), _lib.strides(*key.stride()), self.batch, self.kv_heads, self.head_dim,
                     self.block, self.reps, self.meta_len, history, self.meta.data_ptr(), self.meta_blocks,
@@ -200,7 +200,7 @@ class BlockSelectDecodeStep:
         _require(ws_need >= 0, "bad rerank sizes")
         if ws_need > self.rerank_ws.numel() * 4:
             self.rerank_ws = torch.empty((ws_need + 3) // 4, dtype=torch.float32, device=q.device)
-        with torch.cuda.device(q.device):
+        with _lib.on_device(q.device):
             if self.kind == QBORACLE:
                 _lib.check(lib.qkv_block_max_partial_scores(
                     q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), self.batch, self.q_heads,

@@ -88,7 +88,7 @@ def int4_pack_k(key: torch.Tensor, group: int, *, capacity: int | None = None,
     _require(packed.is_contiguous() and scales.is_contiguous(), "packed/scales must be contiguous")
     _require(tuple(packed.shape) == (b, h, cap, d // 2), "packed shape mismatch")
     _require(tuple(scales.shape) == (b, h, cap, d // group), "scales shape mismatch")
-    with torch.cuda.device(key.device):
+    with _lib.on_device(key.device):
         _lib.check(lib.qkv_int4_pack_k(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
                                        t_end, d, int(group), packed.data_ptr(), scales.data_ptr(), cap, code,
                                        _lib.stream_of(key)))
@@ -107,7 +107,7 @@ def select_channels(packed: torch.Tensor, scales: torch.Tensor, tokens: int, gro
     d = half * 2
     stats = torch.empty((b, h, d), dtype=torch.int64, device=packed.device)
     chan = torch.empty((b, h, int(count)), dtype=torch.int32, device=packed.device)
-    with torch.cuda.device(packed.device):
+    with _lib.on_device(packed.device):
         _lib.check(lib.qkv_int4_select_channels(packed.data_ptr(), scales.data_ptr(), b * h, int(tokens), cap,
                                                 d, int(group), int(count), stats.data_ptr(), chan.data_ptr(),
                                                 _lib.stream_of(packed)))
@@ -130,7 +130,7 @@ def build_slab(key: torch.Tensor, chan_idx: torch.Tensor, *, capacity: int | Non
         slab = torch.empty((b, h, cap, s // 2), dtype=torch.uint8, device=key.device)
         slab_scales = torch.empty((b, h, cap), dtype=torch.float16, device=key.device)
     cap = slab.size(2)
-    with torch.cuda.device(key.device):
+    with _lib.on_device(key.device):
         _lib.check(lib.qkv_int4_build_slab(key.data_ptr(), _lib.strides(*key.stride()[:3]), b, h, int(t_begin),
                                            t_end, d, chan_idx.data_ptr(), s, slab.data_ptr(),
                                            slab_scales.data_ptr(), cap, code, _lib.stream_of(key)))
@@ -151,7 +151,7 @@ def query_words(query: torch.Tensor, chan_idx: torch.Tensor, *, qwords: torch.Te
     _require(chan_idx.size(0) == b, "chan_idx batch mismatch")
     if qwords is None:
         qwords = torch.empty((b, hkv, s // 4), dtype=torch.int32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_int4_query_words(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s,
                                             qwords.data_ptr(), _lib.ptr(qscale), code, _lib.stream_of(q)))
     return qwords, qscale
@@ -182,7 +182,7 @@ def decode_scores(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tenso
         isum = torch.empty((b, hkv, int(tokens)), dtype=torch.int32, device=q.device)
         keys = torch.empty((b, hkv, int(tokens)), dtype=torch.float32, device=q.device)
         qscale = torch.empty((b, hkv), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_int4_decode_scores(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s, slab.data_ptr(),
                                               slab_scales.data_ptr(), cap, int(tokens), int(block),
                                               bmax.data_ptr(), _lib.ptr(isum), _lib.ptr(keys),
@@ -220,7 +220,7 @@ def decode_topk(query: torch.Tensor, chan_idx: torch.Tensor, slab: torch.Tensor,
     _require(need >= 0, f"bad top-k sizes tokens={t} k={k}")
     if need > 0 and (workspace is None or workspace.numel() * 4 < need):
         workspace = topk_workspace(b * hkv, t, k, q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_int4_decode_topk(q.data_ptr(), b, hq, hkv, d, chan_idx.data_ptr(), s, slab.data_ptr(),
                                             slab_scales.data_ptr(), cap, t, int(k), scores.data_ptr(), out.data_ptr(),
                                             _lib.ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
@@ -249,7 +249,7 @@ def block_topk(values: torch.Tensor, k: int, *, out: torch.Tensor | None = None,
     if out is None:
         out = torch.empty((*values.shape[:-1], int(k)), dtype=torch.int32, device=values.device)
     need = lib.qkv_topk_workspace_bytes(rows, n, int(k))
-    with torch.cuda.device(values.device):
+    with _lib.on_device(values.device):
         if need > 0:
             if workspace is None or workspace.numel() * 4 < need:
                 workspace = topk_workspace(rows, n, k, values.device)
@@ -333,7 +333,7 @@ def sparse_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     if workspace is None:
         workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
     out = _output(out, q)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         if prot:
             _lib.check(lib.qkv_sparse_attention_protected(
                 q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,
@@ -382,7 +382,7 @@ def sparse_attention_select(query: torch.Tensor, key: torch.Tensor, value: torch
     if workspace is None:
         workspace = attention_workspace(b, hq, hkv, d, n_ws, block, q.device)
     out = _output(out, q)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         if prot:
             _lib.check(lib.qkv_sparse_attention_protected(
                 q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, hkv,

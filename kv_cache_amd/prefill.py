@@ -37,7 +37,7 @@ def quantize_query(query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     rows = q.size(0)
     q8 = torch.empty((*query.shape[:-1], 128), dtype=torch.int8, device=query.device)
     qscale = torch.empty(query.shape[:-1], dtype=torch.float32, device=query.device)
-    with torch.cuda.device(query.device):
+    with _lib.on_device(query.device):
         _lib.check(lib.qkv_prefill_quantize_query(q.data_ptr(), rows, 128, q.stride(0), q8.data_ptr(),
                                                   qscale.data_ptr(), code, _lib.stream_of(query)))
     return q8, qscale
@@ -60,7 +60,7 @@ def block_scores(q8: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, t
     nb = -(-int(tokens) // BLOCK)
     if bmax is None:
         bmax = torch.empty((b, hq, nq, nb), dtype=torch.float32, device=q8.device)
-    with torch.cuda.device(q8.device):
+    with _lib.on_device(q8.device):
         _lib.check(lib.qkv_prefill_block_scores(q8.data_ptr(), b, hq, hkv, nq, packed.data_ptr(), sc.data_ptr(),
                                                 cap, int(tokens), int(q_pos0), d, BLOCK, bmax.data_ptr(),
                                                 _lib.stream_of(q8)))
@@ -77,7 +77,7 @@ def block_topk(bmax: torch.Tensor, k: int, *, out: torch.Tensor | None = None) -
     _require(v2.stride(1) == 1, "bmax must be contiguous along the last axis")
     if out is None:
         out = torch.empty((*bmax.shape[:-1], int(k)), dtype=torch.int32, device=bmax.device)
-    with torch.cuda.device(bmax.device):
+    with _lib.on_device(bmax.device):
         _lib.check(lib.qkv_prefill_block_topk(v2.data_ptr(), v2.size(0), n, v2.stride(0), int(k), out.data_ptr(),
                                               _lib.stream_of(bmax)))
     return out

@@ -51,7 +51,7 @@ def partial_scores(query: torch.Tensor, key_history: torch.Tensor, dim_count: in
     b, h, d = q.shape
     t = key_history.size(2)
     out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_partial_scores(
             q.data_ptr(), key_history.data_ptr(), out.data_ptr(), _dtype_code(q), b, h, t, d,
             _lib.strides(*key_history.stride()), int(dim_count), _lib.stream_of(q)))
@@ -80,7 +80,7 @@ def partial_scores_dim_major(query: torch.Tensor, key_dim_major: torch.Tensor,
     b, h, d = q.shape
     t = key_dim_major.size(3)
     out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_partial_scores_dim_major(
             q.data_ptr(), key_dim_major.data_ptr(), idx.data_ptr(), out.data_ptr(), _dtype_code(q),
             b, h, t, d, idx.size(2), _lib.strides(*key_dim_major.stride()), _lib.stream_of(q)))
@@ -119,7 +119,7 @@ def candidate_full_scores(query: torch.Tensor, key_history: torch.Tensor,
     b, h, d = q.shape
     t = key_history.size(2)
     out = torch.empty((b, h, t), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_candidate_full_scores(
             q.data_ptr(), key_history.data_ptr(), cur.data_ptr(), _lib.ptr(prev), _lib.ptr(fin),
             out.data_ptr(), _dtype_code(q), b, h, t, d, _lib.strides(*key_history.stride()),
@@ -188,7 +188,7 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         # bf16 / fp16: the list-per-head attention on the matrix cores (qkv_token_attention,
         # G = 1 on these head-expanded K/V), the invalid and out-of-range entries
         # as skipped ids; a row with none valid gives 0, as QK:388, 404 do
-        with torch.cuda.device(q.device):
+        with _lib.on_device(q.device):
             # ids outside [0, t) are skipped (int64 values clamped first so none wraps)
             keep = val if val.dtype == torch.bool else val != 0
             ids = torch.where(keep, idx.clamp(-1, t), -1).to(torch.int32).view(b * h, n)
@@ -201,7 +201,7 @@ def final_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         return out[:, None, :, :]
     out = torch.empty((b, h, d), dtype=q.dtype, device=q.device)
     val = val.to(torch.uint8)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_final_attention(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(),
             _dtype_code(q), b, h, t, n, d, float(scaling), _lib.stream_of(q)))
@@ -246,7 +246,7 @@ def brep_partial_scores(query: torch.Tensor, key_history: torch.Tensor, rep_indi
     k = key_history.contiguous()
     idx = rep_indices.contiguous()
     val = rep_valid.contiguous().view(torch.uint8)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_brep_partial_scores(
             q.data_ptr(), k.data_ptr(), idx.data_ptr(), val.data_ptr(), out.data_ptr(), _dtype_code(k), b, h, t, d,
             _lib.strides(*k.stride()), idx.size(3), int(block_size), int(dim_count), float(scan_fraction),
@@ -296,7 +296,7 @@ def reuse_select(query: torch.Tensor, key_states: torch.Tensor, current_candidat
     final_indices = torch.empty((b, h, n_out), dtype=torch.int64, device=q.device)
     final_valid = torch.empty((b, h, n_out), dtype=torch.bool, device=q.device)
     history_final = torch.empty((b, h, history), dtype=torch.bool, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_reuse_select(
             q.data_ptr(), k.data_ptr(), _lib.strides(*k.stride()), _dtype_code(q), b, h, h, key_count, d,
             cur.data_ptr(), _lib.ptr(masks[0]), _lib.ptr(masks[1]), history, sink, recent, float(top_fraction),

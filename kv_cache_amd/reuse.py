@@ -157,7 +157,7 @@ def candidate_mask(values: torch.Tensor, n: int, selection: str, k: int, mask: t
             _require(bool(((sample_cols[:n_sample] >= 0) & (sample_cols[:n_sample] < n)).all()),
                      "sample_cols must lie in [0, n)")
             sample_cols = sample_cols.to(values.device)
-    with torch.cuda.device(values.device):
+    with _lib.on_device(values.device):
         _lib.check(lib.qkv_candidate_mask(
             values.data_ptr(), values.size(0), int(n), values.stride(0), code, int(k), _lib.ptr(sample_cols),
             int(n_sample), _lib.ptr(thresholds), None if bits else mask.data_ptr(), 0 if bits else mask.stride(0),
@@ -189,7 +189,7 @@ def reuse_partial_scores(query: torch.Tensor, key_dim_major: torch.Tensor, histo
         out = torch.empty((b * hq, history), dtype=torch.float32, device=q.device)
     _require(out.dtype == torch.float32 and out.dim() == 2 and out.size(0) == b * hq and out.size(1) >= history
              and out.stride(1) == 1, "out must be f32 [B*Hq, >= history]")
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_reuse_partial_scores(
             q.data_ptr(), key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _dtype_code(q), b, hq,
             hkv, int(history), d, int(dim_count), out.data_ptr(), out.stride(0), _lib.stream_of(q)))
@@ -203,7 +203,7 @@ def threshold_mask(values: torch.Tensor, n: int, k: int, mask: torch.Tensor, wor
              and values.size(1) >= n, "values must be CUDA f32 [rows, >= n]")
     _require(mask.dtype == torch.uint8 and mask.dim() == 2 and mask.size(0) == values.size(0) and mask.size(1) >= n
              and mask.stride(1) == 1, "mask must be uint8 [rows, >= n]")
-    with torch.cuda.device(values.device):
+    with _lib.on_device(values.device):
         _lib.check(lib.qkv_threshold_mask(values.data_ptr(), values.size(0), int(n), values.stride(0), int(k),
                                           mask.data_ptr(), mask.stride(0), workspace.data_ptr(),
                                           workspace.numel() * 4, _lib.stream_of(values)))
@@ -229,7 +229,7 @@ def expand_blocks(history_final: torch.Tensor, key_count: int, block: int, prote
     idx = torch.empty((rows, n), dtype=torch.int64, device=dev)
     valid = torch.empty((rows, n), dtype=torch.uint8, device=dev)
     ids = torch.empty((rows, n), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.check(lib.qkv_reuse_expand_blocks(
             history_final.data_ptr(), history_final.stride(0), rows, int(key_count), int(block), int(protect_sink),
             int(protect_recent), float(top_fraction), int(keep_self), idx.data_ptr(), valid.data_ptr(),
@@ -246,7 +246,7 @@ def dim_major_append(key: torch.Tensor, key_dim_major: torch.Tensor, t_begin: in
     _require(0 <= t_begin <= t_end <= key.size(2), "token range outside the key cache")
     _require(key_dim_major.dim() == 4 and tuple(key_dim_major.shape[:3]) == (b, hkv, d)
              and key_dim_major.size(3) >= t_end, "key_dim_major must be [B, Hkv, D, >= t_end]")
-    with torch.cuda.device(key.device):
+    with _lib.on_device(key.device):
         _lib.check(lib.qkv_dim_major_append(
             key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(key), b, hkv, d, int(t_begin), int(t_end),
             key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _lib.stream_of(key)))
@@ -271,7 +271,7 @@ def token_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         out = torch.empty((b, hq, d), dtype=q.dtype, device=q.device)
     _require(out.dtype == q.dtype and out.is_contiguous() and out.numel() == b * hq * d,
              f"out must be contiguous {q.dtype} [B, Hq, D]")
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check(lib.qkv_token_attention(
             q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), b, hq, key.size(1),
             key.size(2), d, token_ids.data_ptr(), token_ids.size(-1), float(scaling), workspace.data_ptr(),
@@ -473,7 +473,7 @@ class ReuseDecodeStep:
                 self.cand_ws = torch.zeros((need + 3) // 4, dtype=torch.float32, device=self.device)
             # partial scores, threshold and mask in one launch where a row fits one
             # workgroup; the threshold is kept only where a later step reads it
-            with torch.cuda.device(q.device):
+            with _lib.on_device(q.device):
                 bits = current.dtype == torch.int64
                 _lib.check(lib.qkv_reuse_candidates(
                     q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), _dtype_code(q), self.batch,
@@ -500,7 +500,7 @@ class ReuseDecodeStep:
         bits = current.dtype == torch.int64
         if bits and self.block is not None and history > BLOCK_BITS_MAX_HISTORY:
             # past one workgroup's row: the selection, then the expansion on the bitset
-            with torch.cuda.device(q.device):
+            with _lib.on_device(q.device):
                 _lib.check(lib.qkv_reuse_select_bits(
                     q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch,
                     self.q_heads, self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
@@ -516,7 +516,7 @@ class ReuseDecodeStep:
             self.n_out = n_out
             return
         if bits and self.block is not None:   # the selection and its block expansion in one launch
-            with torch.cuda.device(q.device):
+            with _lib.on_device(q.device):
                 _lib.check(lib.qkv_reuse_select_bits_blocks(
                     q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch,
                     self.q_heads, self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
@@ -534,7 +534,7 @@ class ReuseDecodeStep:
         select = lib.qkv_reuse_select_bits if bits else lib.qkv_reuse_select
         _require(not bits or (value.shape == key.shape and value.stride() == key.stride()),
                  "key/value layout mismatch")
-        with torch.cuda.device(q.device):
+        with _lib.on_device(q.device):
             _lib.check(select(
                 q.data_ptr(), key.data_ptr(), _lib.strides(*key.stride()), _dtype_code(q), self.batch, self.q_heads,
                 self.kv_heads, key_count, self.head_dim, current.data_ptr(), _lib.ptr(previous),
@@ -636,7 +636,7 @@ def lag_flags(query: torch.Tensor, kv_heads: int, test: str, dim_count: int, dim
         need = int(lib.qkv_reuse_lag_flags_workspace_bytes(b * hq, history))
         _require(need > 0, "bad ESS sizes")
         workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check((lib.qkv_reuse_lag_flags_bits if bits else lib.qkv_reuse_lag_flags)(
             q.data_ptr(), _dtype_code(q), b, hq, kv_heads, d, dim_count, LAG_TESTS[test], _lib.ptr(previous_dims),
             _lib.ptr(previous_values), dims_out.data_ptr(), values_out.data_ptr(), _lib.ptr(key),
@@ -657,7 +657,7 @@ def lag_candidates(query: torch.Tensor, key_dim_major: torch.Tensor, history: in
     q = query.contiguous()
     b, hq, d = q.shape
     bits = mask.dtype == torch.int64
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         _lib.check((lib.qkv_reuse_lag_candidates_bits if bits else lib.qkv_reuse_lag_candidates)(
             q.data_ptr(), key_dim_major.data_ptr(), _lib.strides(*key_dim_major.stride()), _dtype_code(q), b, hq,
             key_dim_major.size(1), history, d, dim_count, k, _lib.ptr(flags), REFRESH[refresh], partial.data_ptr(),
@@ -678,7 +678,7 @@ def lag_union(current: torch.Tensor, previous_final: torch.Tensor | None, flags:
     bits = current.dtype == torch.int64
     _require(out.dtype == current.dtype and (previous_final is None or previous_final.dtype == current.dtype),
              "the masks must all be bytes or all bitsets")
-    with torch.cuda.device(current.device):
+    with _lib.on_device(current.device):
         _lib.check((lib.qkv_reuse_lag_union_bits if bits else lib.qkv_reuse_lag_union)(
             current.data_ptr(), _lib.ptr(previous_final), current.stride(0), _lib.ptr(flags), batch, q_heads, history,
             REFRESH[refresh], int(share), protect_sink, protect_recent, out.data_ptr(), out.stride(0),
@@ -833,7 +833,7 @@ def final_indices_from_selected(selected: torch.Tensor, n_sel: int, key_count: i
                torch.empty((rows, n_out), dtype=torch.bool, device=dev),
                torch.empty((rows, n_out), dtype=torch.int32, device=dev))
     fi, fv, ids = out
-    with torch.cuda.device(selected.device):
+    with _lib.on_device(selected.device):
         _lib.check(lib.qkv_final_indices_from_selected(
             selected.data_ptr(), selected.stride(0), n_sel, rows, key_count, protect_sink, protect_recent,
             int(keep_self), fi.data_ptr(), fv.data_ptr(), _lib.ptr(ids), n_out, _lib.stream_of(selected)))
@@ -866,7 +866,7 @@ def qabs_candidate_select(scores: torch.Tensor, key_count: int, candidate_fracti
     _require(need >= 0, "bad candidate selection sizes")
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=scores.device)
-    with torch.cuda.device(scores.device):
+    with _lib.on_device(scores.device):
         _lib.check(lib.qkv_qabs_candidate_select(
             scores.data_ptr(), rows, key_count, scores.stride(0), float(candidate_fraction), protect_sink,
             protect_recent, int(keep_self), int(append), _lib.ptr(workspace) if need else None,
@@ -990,7 +990,7 @@ class QabsCandidateAttentionStep:
                    self.hf)
             # partial scores and the selection in one call (across workgroups
             # where the rows are few and short enough)
-            with torch.cuda.device(q.device):
+            with _lib.on_device(q.device):
                 _lib.check(lib.qkv_qabs_candidates(
                     q.data_ptr(), self.kdm.data_ptr(), _lib.strides(*self.kdm.stride()), _dtype_code(q), self.batch,
                     self.q_heads, self.kv_heads, key_count, self.head_dim, self.dims, self.cand_fraction, self.sink,
