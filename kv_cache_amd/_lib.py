@@ -12,7 +12,6 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
-import functools
 import os
 import re
 from pathlib import Path
@@ -168,15 +167,9 @@ def check(rc: int) -> None:
         raise RuntimeError(load().qkv_last_error().decode())
 
 
-@functools.lru_cache(maxsize=512)
-def _strides(vals: tuple):
-    return (ctypes.c_int64 * len(vals))(*vals)
-
-
 def strides(*vals: int):
-    """An int64 array of the values for a C call (read only by the library;
-    the same object for the same values, so a decode step builds none)."""
-    return _strides(tuple(int(v) for v in vals))
+    arr = (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+    return arr
 
 
 _SAME_DEVICE = contextlib.nullcontext()
@@ -195,7 +188,14 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """The current stream of t's device as a raw handle (without building a
+    torch Stream object where torch offers that)."""
+    if _RAW_STREAM is not None and t.device.type == "cuda":
+        return _RAW_STREAM(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

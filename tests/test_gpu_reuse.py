@@ -875,3 +875,25 @@ def test_dim_major_append_and_token_attention():
     kx, vx = k.repeat_interleave(2, dim=1), v.repeat_interleave(2, dim=1)
     want = R.final_attention(f32(q), f32(kx), f32(vx), idx.clamp(0, 699).numpy(), valid.numpy(), 0.09)
     np.testing.assert_allclose(f32(out), want[:, 0], rtol=RTOL, atol=ATOL)
+
+
+def test_stream_of_follows_the_current_stream():
+    # the raw handle the wrappers launch on is torch's current stream: the
+    # default one, a side stream, and the capture stream of a graph
+    from kv_cache_amd import _lib
+
+    t = torch.zeros(4, device=DEV)
+    assert _lib.stream_of(t) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _lib.stream_of(t) == side.cuda_stream
+    torch.cuda.synchronize()
+    seen = []
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        seen.append((_lib.stream_of(t), torch.cuda.current_stream().cuda_stream))
+        t.add_(1)
+    assert seen[0][0] == seen[0][1]
+    g.replay()
+    torch.cuda.synchronize()
+    assert float(t[0]) == 1.0
