@@ -105,20 +105,30 @@ class SampleColumnTable:
         """Largest column count of any row (0 when every row's sample covers it)."""
         return self.size if self.capacity - 1 > self.size else 0
 
+    FILL = 64   # rows filled per miss: a decode step's next histories come with it
+
     def count(self, history: int) -> int:
         """Columns of ``history``'s sample (0 when the sample covers the row)."""
         h = int(history)
         n = self._counts.get(h)
         if n is None:
             _require(0 <= h < self.capacity, f"history {h} outside the table (capacity {self.capacity})")
-            cols = sample_columns(h, self.size) if h else None
-            n = 0 if cols is None else cols.numel()
-            if n:
-                host = torch.empty(self.size, dtype=torch.int32)
-                host[:n] = cols
-                host[n:] = cols[-1]
-                self.rows[h].copy_(host)
-            self._counts[h] = n
+            # this row and the next ones not yet filled, staged in pinned memory
+            # and copied in one asynchronous transfer (a pageable copy per row
+            # would wait for the stream's earlier work at every decode step)
+            end = h + 1
+            while end < min(h + self.FILL, self.capacity) and end not in self._counts:
+                end += 1
+            host = torch.empty((end - h, self.size), dtype=torch.int32, pin_memory=self.rows.is_cuda)
+            for j in range(h, end):
+                cols = sample_columns(j, self.size) if j else None
+                c = 0 if cols is None else cols.numel()
+                if c:
+                    host[j - h, :c] = cols
+                    host[j - h, c:] = cols[-1]
+                self._counts[j] = c
+            self.rows[h:end].copy_(host, non_blocking=True)
+            n = self._counts[h]
         return n
 
     def row(self, history: int) -> torch.Tensor:

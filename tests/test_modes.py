@@ -130,6 +130,15 @@ def test_sample_column_table_rows_are_the_host_columns():
         assert bool((row[n:] == cols[-1]).all())
     with pytest.raises(RuntimeError):
         table.count(300)
+    # rows are filled in batches from the first missing history: any access
+    # order gives every row its own columns
+    shuffled = RU.SampleColumnTable(300, 40, "cpu")
+    for h in torch.randperm(300, generator=torch.Generator().manual_seed(3)).tolist() + [299, 0, 65, 64]:
+        cols = RU.sample_columns(h, 40) if h else None
+        n = shuffled.count(h)
+        assert n == (0 if cols is None else cols.numel())
+        if n:
+            assert torch.equal(shuffled.row(h)[:n], cols) and bool((shuffled.row(h)[n:] == cols[-1]).all())
 
 
 @pytest.mark.parametrize("mode,want", [
