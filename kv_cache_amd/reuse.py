@@ -522,7 +522,7 @@ class ReuseDecodeStep:
                     self.fin.data_ptr(), self.fin.stride(0), self.rows, key_count, self.block, self.sink,
                     self.recent, self.top_fraction, int(self.keep_self), self.final_idx.data_ptr(),
                     self.final_valid.data_ptr(), ids.data_ptr(), n_out, _lib.stream_of(q)))
-            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+            self._attend(q, key, value, ids, n_out, scaling)
             self.n_out = n_out
             return
         if bits and self.block is not None:   # the selection and its block expansion in one launch
@@ -534,7 +534,7 @@ class ReuseDecodeStep:
                     int(self.keep_self), float(scaling), self.block, self.select_ws.data_ptr(),
                     self.select_ws.numel() * 4, self.final_idx.data_ptr(), self.final_valid.data_ptr(),
                     ids.data_ptr(), n_out, self.fin.data_ptr(), self.fin.stride(0), _lib.stream_of(q)))
-            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+            self._attend(q, key, value, ids, n_out, scaling)
             self.n_out = n_out
             return
         # on bitsets the final selection's workgroups can also run the attention
@@ -559,8 +559,22 @@ class ReuseDecodeStep:
                     self.top_fraction, int(self.keep_self), self.final_idx.data_ptr(), self.final_valid.data_ptr(),
                     ids.data_ptr(), n_out, _lib.stream_of(q)))
         if not attended.value:
-            token_attention(q, key, value, ids.view(self.rows, n_out), scaling, workspace=self.attn_ws, out=self.out)
+            self._attend(q, key, value, ids, n_out, scaling)
         self.n_out = n_out
+
+    def _attend(self, q: torch.Tensor, key: torch.Tensor, value: torch.Tensor, ids: torch.Tensor, n_out: int,
+                scaling: float) -> None:
+        """token_attention over the step's own list into ``self.out`` (the
+        step's buffers need none of that wrapper's checks)."""
+        _require(key.shape == value.shape and key.stride() == value.stride() and key.stride(3) == 1,
+                 "key/value layout mismatch")
+        lib = _lib.load()
+        with _lib.on_device(q.device):
+            _lib.check(lib.qkv_token_attention(
+                q.data_ptr(), key.data_ptr(), value.data_ptr(), _lib.strides(*key.stride()[:3]), self.batch,
+                self.q_heads, key.size(1), key.size(2), self.head_dim, ids.data_ptr(), n_out, float(scaling),
+                self.attn_ws.data_ptr(), self.attn_ws.numel() * 4, self.out.data_ptr(), _dtype_code(q),
+                _lib.stream_of(q)))
 
     # -- state views (tests, tracing) ------------------------------------------
     def candidate_mask(self) -> torch.Tensor:
